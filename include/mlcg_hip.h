@@ -1,0 +1,210 @@
+/*
+ * mlcg_hip.h -- C ABI of libmlcg_hip.so, the gfx950 implementation of the
+ * mlcg SchNet/CFConv hot path (radius graph, Gaussian-RBF filter network,
+ * CFConv gather/scatter with its force backward and force-matching double
+ * backward, bonded and repulsion priors, Langevin BAOAB).
+ *
+ * Conventions (shared by every entry point):
+ *   - all array arguments are device pointers, row-major and contiguous;
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued on it and
+ *     nothing synchronises with the host;
+ *   - nothing allocates device memory: callers pass outputs and workspaces;
+ *   - the return value is an mlcg_status; a non-zero value means nothing
+ *     useful was written.  MLCG_ERR_ARGUMENT is returned before any launch.
+ *   - "pair" = unordered neighbour pair {i, j} with i < j; the pair list is
+ *     the upper triangle of the canonically sorted (i asc, j asc) edge list.
+ *   - functions that take `n_pairs_dev` read the live pair count from device
+ *     memory, so a launch sized by a capacity can be captured in a hipGraph.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the ClementiGroup/mlcg checkout).
+ */
+#ifndef MLCG_HIP_H
+#define MLCG_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MLCG_OK = 0,
+  MLCG_ERR_ARGUMENT = 1,
+  MLCG_ERR_LAUNCH = 2,
+  MLCG_ERR_CAPACITY = 3,
+  MLCG_ERR_UNSUPPORTED = 4
+} mlcg_status;
+
+/* Library identification: returns a static string (build id + arch). */
+const char* mlcg_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Radius graph                                                            */
+/* ---------------------------------------------------------------------- */
+
+/* frame_ptr[b] = first node of frame b, frame_ptr[n_frames] = n_nodes, from a
+ * sorted `batch` vector.  Replaces the torch.bucketize call of
+ * src/opt_radius/mlcg_opt_radius/radius.py:72-75. */
+int mlcg_frame_ptr_from_batch(const int64_t* batch, int64_t n_nodes,
+                              int64_t n_frames, int64_t* frame_ptr,
+                              void* stream);
+
+/* Pass 1 of the radius graph: per-node neighbour counts.
+ * Edge (i, j) exists iff batch[i] == batch[j], (loop || i != j) and
+ * d2 < fl32(r*r), d2 = ((dx*dx + dy*dy) + dz*dz) in fp32 without FMA
+ * contraction, dx = pos[j].x - pos[i].x.  Rows keep their lowest-index
+ * `max_num_neighbors` neighbours; *overflow is set to 1 if any row had more.
+ * deg[i] = kept neighbours, upper_deg[i] = kept neighbours with j > i.
+ * Replaces the counting half of radius_kernel (radius.cu:88-145) and the
+ * torch_cluster.radius_graph call of
+ * src/mlcg/neighbor_list/torch_impl.py:216-224. */
+int mlcg_radius_count(const float* pos, const int64_t* batch,
+                      const int64_t* frame_ptr, int64_t n_nodes, double r,
+                      int loop, int64_t max_num_neighbors, int32_t* deg,
+                      int32_t* upper_deg, int32_t* overflow, void* stream);
+
+/* Exclusive scan of two int32 vectors of length n into out_a/out_b (length
+ * n + 1, the totals at index n).  `workspace` holds
+ * mlcg_scan_workspace_ints(n) int32.  Replaces the block/grid scan of
+ * radius.cu:146-181 (no cooperative launch, no host sync). */
+int64_t mlcg_scan_workspace_ints(int64_t n);
+int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b,
+                             int64_t n, int32_t* out_a, int32_t* out_b,
+                             int32_t* workspace, void* stream);
+
+/* Pass 2: writes the canonical edge list.  edge_index is [2, edge_stride]
+ * int64 (row 0 = centre i, row 1 = neighbour j).  Optional (nullable)
+ * outputs for the CFConv pipeline: col[e] = j (int32), pair_ij [2,
+ * pair_stride] (row 0 = i, row 1 = j, i < j) and eid2pair[e] for upper edges.
+ * Edges at index >= edge_capacity (pairs >= pair_capacity) are dropped and
+ * *overflow is set to 2.  Replaces radius.cu:117-145 and compact_kernel
+ * (radius.cu:60-86). */
+int mlcg_radius_fill(const float* pos, const int64_t* batch,
+                     const int64_t* frame_ptr, int64_t n_nodes, double r,
+                     int loop, int64_t max_num_neighbors,
+                     const int32_t* rowptr, const int32_t* pairptr,
+                     int64_t edge_capacity, int64_t edge_stride,
+                     int64_t* edge_index, int32_t* col,
+                     int64_t pair_capacity, int64_t pair_stride,
+                     int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
+                     void* stream);
+
+/* Pass 3: eid2pair for lower edges (i > j), by binary search of i in row j.
+ * n_pairs_dev points at the live pair count (e.g. pairptr + n_nodes). */
+int mlcg_pair_reverse_map(const int32_t* pair_ij, int64_t pair_stride,
+                          const int32_t* n_pairs_dev, int64_t max_pairs,
+                          const int32_t* rowptr, const int32_t* col,
+                          int32_t* eid2pair, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Filter network (GaussianBasis -> cutoff -> MLP([K, F, F]) -> x cutoff)   */
+/* ---------------------------------------------------------------------- */
+
+/* Per pair p = {i, j}: d = |pos[j] - pos[i]|,
+ *   g_k  = exp(coeff (d - offsets[k])^2) * C_rbf(d)          (gaussian.py:83-102)
+ *   a    = W1 g + b1 ; h = act(a) ; w = W2 h                 (mlp.py:56-58)
+ *   W    = w * C_conv(d)                                     (schnet.py:340-341)
+ *   Wd   = dW/dd (forward-mode tangent of the same chain).
+ * W1 is [F, K] (torch Linear layout), b1 [F], W2 [F, F]; F must be 128 and
+ * 1 <= K <= 128.  W_out/Wd_out are [max_pairs, F]; dist_out [max_pairs] is
+ * optional.  act: 0 = tanh, 1 = shifted softplus.  cut kinds: 0 = identity,
+ * 1 = cosine.  f16 != 0 selects the fp16-operand MFMA path (fp32
+ * accumulate) and fp16 W_out/Wd_out storage.  Replaces CFConv.forward
+ * lines 340-341 plus GaussianBasis/CosineCutoff/MLP (schnet.py:150,340-341). */
+int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
+                    int64_t pair_stride, const int32_t* n_pairs_dev,
+                    int64_t max_pairs, const float* offsets, float coeff,
+                    int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                    int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                    const float* W1, const float* b1, const float* W2,
+                    int num_filters, int f16, void* W_out, void* Wd_out,
+                    float* dist_out, void* stream);
+
+/* Reverse of the filter chain for given pair adjoints Wbar = dL/dW and
+ * Wdbar = dL/dWd ([max_pairs, F] fp32).  Writes the per-pair factors of the
+ * weight gradients: H = [h ; h'] [2, max_pairs, F], T = [wbar ; w'bar]
+ * [2, max_pairs, F], A = [abar ; a'bar] [2, max_pairs, F] and
+ * G = [g ; g'] [2, max_pairs, Kp] with Kp = 4 ceil(K / 4).  Rows past the live
+ * pair count are zero, so dW2 = T^T H, dW1 = A^T G and db1 = sum(A[0]).
+ * Replaces the autograd double backward through mlp.py/gaussian.py. */
+int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij,
+                    int64_t pair_stride, const int32_t* n_pairs_dev,
+                    int64_t max_pairs, const float* offsets, float coeff,
+                    int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                    int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                    const float* W1, const float* b1, const float* W2,
+                    int num_filters, const float* Wbar, const float* Wdbar,
+                    float* H, float* T, float* A, float* G, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* CFConv gather/scatter over the receiver CSR (rowptr, col, eid2pair)      */
+/* ---------------------------------------------------------------------- */
+
+/* out[i] = sum_{e in row i, ascending j} src[col[e]] * W[eid2pair[e]].
+ * F = 128.  w_f16 != 0: W is fp16.  Replaces CFConv.propagate/message
+ * (schnet.py:346,368) with PyG's SumAggregation. */
+int mlcg_cfconv_gather(const float* src, const void* W, int w_f16,
+                       const int32_t* rowptr, const int32_t* col,
+                       const int32_t* eid2pair, int64_t n_nodes,
+                       int num_filters, float* out, void* stream);
+
+/* Force backward of one CFConv: ybar[i] = sum_j gagg[j] * W_ij and, per
+ * pair p = {i < j}, dbar[p] += <Wd_p, gagg[i] * y[j] + gagg[j] * y[i]>.
+ * Replaces the autograd backward of schnet.py:340-346. */
+int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const void* W,
+                           const void* Wd, int w_f16, const int32_t* rowptr,
+                           const int32_t* col, const int32_t* eid2pair,
+                           int64_t n_nodes, int num_filters, float* ybar,
+                           float* dbar, void* stream);
+
+/* Tangent (forward-mode) of the CFConv aggregation along a position
+ * direction: out[i] = sum_j ydot[j] * W_ij + y[j] * Wd_ij * ddot_p.
+ * ydot may be NULL (zero).  Part of the force-matching double backward. */
+int mlcg_cfconv_gather_tangent(const float* ydot, const float* y,
+                               const float* W, const float* Wd,
+                               const float* ddot, const int32_t* rowptr,
+                               const int32_t* col, const int32_t* eid2pair,
+                               int64_t n_nodes, int num_filters, float* out,
+                               void* stream);
+
+/* Reverse over (primal, tangent) of the CFConv aggregation:
+ *   ybar2[i] = sum_j gagg2[j] * W_ij + gagg1[j] * Wd_ij * ddot_p
+ *   Wbar[p]  = gagg2[i] y[j] + gagg2[j] y[i] + gagg1[i] ydot[j] + gagg1[j] ydot[i]
+ *   Wdbar[p] = ddot_p (gagg1[i] y[j] + gagg1[j] y[i])
+ * ydot, gagg1, ddot may be NULL (zero tangent).  Wbar/Wdbar are
+ * [n_pairs, F]. */
+int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1,
+                            const float* y, const float* ydot,
+                            const float* W, const float* Wd,
+                            const float* ddot, const int32_t* rowptr,
+                            const int32_t* col, const int32_t* eid2pair,
+                            int64_t n_nodes, int num_filters, float* ybar2,
+                            float* Wbar, float* Wdbar, void* stream);
+
+/* ddot[p] = rhat_p . (u[j] - u[i]), rhat_p = (pos[j] - pos[i]) / dist[p]. */
+int mlcg_pair_ddot(const float* pos, const float* dist, const int32_t* pair_ij,
+                   int64_t pair_stride, const int32_t* n_pairs_dev,
+                   int64_t max_pairs, const float* u, float* ddot,
+                   void* stream);
+
+/* forces[i] (+)= sum_{j in row i} dbar[p(i,j)] (pos[j] - pos[i]) / dist[p].
+ * Deterministic per-node sum in ascending j.  accumulate != 0 adds to
+ * forces instead of overwriting.  Replaces the autograd position gradient of
+ * compute_distances (internal_coordinates.py:73-100) in GradientsOut. */
+int mlcg_pair_forces(const float* pos, const float* dist, const float* dbar,
+                     const int32_t* rowptr, const int32_t* col,
+                     const int32_t* eid2pair, int64_t n_nodes, int accumulate,
+                     float* forces, void* stream);
+
+/* E[b] = sum_{n in frame b} values[n * stride] (ascending n).  Replaces
+ * torch_geometric.utils.scatter(..., reduce="sum") of schnet.py:158. */
+int mlcg_segment_sum(const float* values, int64_t stride,
+                     const int64_t* frame_ptr, int64_t n_frames, float* out,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLCG_HIP_H */

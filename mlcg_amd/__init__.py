@@ -1,0 +1,9 @@
+"""mlcg_amd -- MI355X-native (gfx950) implementation of mlcg's SchNet CFConv
+hot path: radius graph, Gaussian-RBF filter network, CFConv gather/scatter
+with hand-derived force backward and force-matching double backward, priors
+and the Langevin integrator, behind mlcg's module API."""
+
+from . import ops
+from ._lib import available, version
+
+__all__ = ["ops", "available", "version"]

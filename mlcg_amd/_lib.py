@@ -1,0 +1,136 @@
+"""Loader for ``libmlcg_hip.so``, the gfx950 kernel library.
+
+The library exposes a plain C ABI (``include/mlcg_hip.h``); this module binds
+it with :mod:`ctypes`.  PyTorch is imported first so that the HIP runtime
+already mapped by torch (soname ``libamdhip64.so.7``) is the one the library
+resolves against: the kernels then run on torch's streams and device memory.
+
+There is no fallback: if the shared object is missing or a call returns a
+non-zero status, a :class:`RuntimeError` is raised (the same error class the
+reference's native operator raises, ``radius.cu:7-9``; the reference defers a
+failed build to first use with ``DelayedError``, ``radius.py:35-49`` -- this
+module does the same: importing never fails, calling does).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch  # noqa: F401  (maps the HIP runtime before the library loads)
+
+LIB_NAME = "libmlcg_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+_c = ctypes
+_P = _c.c_void_p
+_I64 = _c.c_int64
+_I32 = _c.c_int
+_F32 = _c.c_float
+_F64 = _c.c_double
+
+# name -> argtypes (all functions return int status unless listed in _RESTYPES)
+_SIGNATURES = {
+    "mlcg_version": [],
+    "mlcg_frame_ptr_from_batch": [_P, _I64, _I64, _P, _P],
+    "mlcg_radius_count": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P],
+    "mlcg_scan_workspace_ints": [_I64],
+    "mlcg_exclusive_scan2_i32": [_P, _P, _I64, _P, _P, _P, _P],
+    "mlcg_radius_fill": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _I64, _I64, _P, _P,
+                         _I64, _I64, _P, _P, _P, _P],
+    "mlcg_pair_reverse_map": [_P, _I64, _P, _I64, _P, _P, _P, _P],
+    "mlcg_filter_fwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
+                        _F32, _F32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],
+    "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
+                        _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P],
+    "mlcg_cfconv_gather": [_P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
+    "mlcg_cfconv_gather_tangent": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_cfconv_gather_rev2": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P,
+                                _P, _P],
+    "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _P, _P],
+    "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
+}
+_RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64}
+
+STATUS = {
+    0: "MLCG_OK",
+    1: "MLCG_ERR_ARGUMENT",
+    2: "MLCG_ERR_LAUNCH",
+    3: "MLCG_ERR_CAPACITY",
+    4: "MLCG_ERR_UNSUPPORTED",
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def exported_symbols():
+    """Names of every entry point this binding expects the library to export."""
+    return list(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise RuntimeError if it is absent."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        _load_error = (
+            f"{LIB_PATH} not found: build it with `make -C mlcg_amd/csrc` or "
+            "`python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+        raise RuntimeError(_load_error)
+    lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, _I32)
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise RuntimeError on a non-zero status."""
+    fn = getattr(load(), name)
+    status = fn(*args)
+    if status != 0:
+        raise RuntimeError(
+            f"{name} failed with {STATUS.get(status, status)}"
+        )
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    """Raw device address of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_handle(device: Optional[torch.device] = None) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    """The kernels only run on a ROCm device: refuse CPU tensors loudly."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "mlcg_amd kernels run on a ROCm GPU only; got a tensor on "
+                f"{t.device}. Move the data and the model to 'cuda'."
+            )
+
+
+def version() -> str:
+    return load().mlcg_version().decode()

@@ -1,0 +1,605 @@
+// Fused Gaussian-RBF -> cutoff -> filter MLP -> cutoff chain (gfx950, MFMA).
+//
+// Reference: GaussianBasis.forward (mlcg/nn/radial_basis/gaussian.py:83-102),
+// CosineCutoff.forward (mlcg/nn/cutoff.py:110-153), MLP([K, F, F],
+// last_bias=False) (mlcg/nn/mlp.py:31-58) and CFConv.forward lines 340-341
+// (mlcg/nn/schnet.py).  The filter depends only on the pair distance, so it
+// is evaluated once per unordered pair (W_ij == W_ji bitwise in the
+// reference too, since d_ij == d_ji).
+//
+// Layout of the work.  One wave owns a tile of 16 pairs and computes the
+// transposed products a^T = W1 g^T ([F x 16]) and w^T = W2 h^T with
+// v_mfma_f32_16x16x4_f32 (fp32 path) or v_mfma_f32_16x16x32_f16 (fp16 path).
+// With pairs on the N axis every lane ends up owning one pair (lane % 16) and
+// a strip of features, so
+//   * the RBF values g are computed directly in the B-operand layout (no LDS),
+//   * the MFMA output of the first product is already the B operand of the
+//     second one (the contraction order over features is permuted to match,
+//     and the matching permutation is baked into the LDS copy of W2),
+//   * the epilogue (x cutoff, d/dd) is per-lane scalar work, and
+//   * W rows are written as float4/half4 strips.
+// W1 and W2 are staged once per workgroup in LDS in the exact per-lane order
+// the MFMA A operand needs (conflict-free ds_read_b32/b128), and workgroups
+// loop persistently over pair tiles.  The forward also produces the distance
+// derivative Wd = dW/dd by pushing the tangent g' = dg/dd through the same
+// chain (a second accumulator set sharing every A fragment).
+#include "common.h"
+
+#include <hip/hip_fp16.h>
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kF = 128;          // number of filters (fixed by the MFMA tiling)
+constexpr int kFT = kF / 16;     // feature tiles of 16
+constexpr int kWaves = 8;        // waves per workgroup
+constexpr int kThreads = kWaves * MLCG_WAVE;
+constexpr int kMaxK = 128;
+
+struct RbfParams {
+  const float* offsets;
+  float coeff;
+  int K;
+  int rbf_kind;
+  float rbf_lo, rbf_hi;
+  int conv_kind;
+  float conv_lo, conv_hi;
+  int act;
+};
+
+// Pair geometry for the lane's pair; out-of-range tiles use a harmless d.
+__device__ __forceinline__ float pair_distance(const float* __restrict__ pos,
+                                               const int32_t* __restrict__ pi,
+                                               const int32_t* __restrict__ pj, int64_t p,
+                                               bool valid) {
+  if (!valid) return 1.0f;
+  const int64_t i = pi[p], j = pj[p];
+  float dx = pos[3 * j + 0] - pos[3 * i + 0];
+  float dy = pos[3 * j + 1] - pos[3 * i + 1];
+  float dz = pos[3 * j + 2] - pos[3 * i + 2];
+  return sqrtf(dx * dx + dy * dy + dz * dz);
+}
+
+// g_k and dg_k/dd for one basis function (zero past K).
+__device__ __forceinline__ void rbf_value(const RbfParams& rp, int k, float d, float crbf,
+                                          float dcrbf, float& g, float& gd) {
+  if (k < rp.K) {
+    float diff = d - rp.offsets[k];
+    float e = expf(rp.coeff * (diff * diff));
+    g = e * crbf;
+    gd = e * (2.0f * rp.coeff * diff * crbf + dcrbf);
+  } else {
+    g = 0.0f;
+    gd = 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS staging.
+//
+// fp32, first product (A = W1, 16x16x4):   w1s[(t*KS + s)*64 + l] =
+//     W1[16t + l%16][4s + l/16]
+// fp32, second product (A = W2, k order kappa(s, q) = 16(s/4) + 4q + s%4):
+//     w2s[((t*8 + u)*64 + l)*4 + i] = W2[16t + l%16][16u + 4(l/16) + i]
+// fp32, reverse product (A = W2^T):
+//     w2ts[((t*8 + u)*64 + l)*4 + i] = W2[16u + 4(l/16) + i][16t + l%16]
+__device__ void stage_w1_f32(float* w1s, const float* __restrict__ W1, int K, int KS) {
+  const int total = kFT * KS * MLCG_WAVE;
+  for (int x = threadIdx.x; x < total; x += blockDim.x) {
+    const int l = x & 63;
+    const int ts = x >> 6;
+    const int s = ts % KS, t = ts / KS;
+    const int k = 4 * s + (l >> 4);
+    w1s[x] = k < K ? W1[(16 * t + (l & 15)) * K + k] : 0.0f;
+  }
+}
+
+__device__ void stage_w2_f32(float* w2s, const float* __restrict__ W2, bool transpose) {
+  const int total = kFT * kFT * MLCG_WAVE;  // float4 slots
+  for (int x = threadIdx.x; x < total; x += blockDim.x) {
+    const int l = x & 63;
+    const int tu = x >> 6;
+    const int u = tu % kFT, t = tu / kFT;
+    const int r = 16 * t + (l & 15);
+    const int c0 = 16 * u + 4 * (l >> 4);
+    float4 v;
+    if (!transpose) {
+      v = *reinterpret_cast<const float4*>(W2 + r * kF + c0);
+    } else {
+      v.x = W2[(c0 + 0) * kF + r];
+      v.y = W2[(c0 + 1) * kF + r];
+      v.z = W2[(c0 + 2) * kF + r];
+      v.w = W2[(c0 + 3) * kF + r];
+    }
+    reinterpret_cast<float4*>(w2s)[x] = v;
+  }
+}
+
+// First product for one 16-pair tile: acc_a = W1 g^T, acc_d = W1 g'^T (fp32).
+// Also returns the lane's g/g' values when `gout` is non-null (reverse pass).
+__device__ __forceinline__ void gemm1_f32(const float* w1s, int KS, const RbfParams& rp,
+                                          float d, float crbf, float dcrbf, floatx4* acc_a,
+                                          floatx4* acc_d, float* gout, float* gdout,
+                                          float gscale) {
+  const int l = mlcg_lane();
+  const int q = l >> 4;
+#pragma unroll
+  for (int t = 0; t < kFT; ++t) {
+    acc_a[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    acc_d[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s = 0; s < KS; ++s) {
+    float g, gd;
+    rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);
+    if (gout) {
+      gout[4 * s + q] = g * gscale;
+      gdout[4 * s + q] = gd * gscale;
+    }
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      const float w = w1s[(t * KS + s) * MLCG_WAVE + l];
+      acc_a[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w, g, acc_a[t], 0, 0, 0);
+      acc_d[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w, gd, acc_d[t], 0, 0, 0);
+    }
+  }
+}
+
+// Second product: out_x = A2 bx^T, out_y = A2 by^T, with A2 staged by
+// stage_w2_f32 and bx/by holding [tile u][i] values of the lane's pair.
+__device__ __forceinline__ void gemm2_f32(const float* w2s, const floatx4* bx,
+                                          const floatx4* by, floatx4* out_x,
+                                          floatx4* out_y) {
+  const int l = mlcg_lane();
+#pragma unroll
+  for (int t = 0; t < kFT; ++t) {
+    out_x[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    out_y[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int u = 0; u < kFT; ++u) {
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      const float4 a = reinterpret_cast<const float4*>(w2s)[(t * kFT + u) * MLCG_WAVE + l];
+      out_x[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bx[u][0], out_x[t], 0, 0, 0);
+      out_y[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, by[u][0], out_y[t], 0, 0, 0);
+      out_x[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bx[u][1], out_x[t], 0, 0, 0);
+      out_y[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, by[u][1], out_y[t], 0, 0, 0);
+      out_x[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bx[u][2], out_x[t], 0, 0, 0);
+      out_y[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, by[u][2], out_y[t], 0, 0, 0);
+      out_x[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bx[u][3], out_x[t], 0, 0, 0);
+      out_y[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, by[u][3], out_y[t], 0, 0, 0);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void filter_fwd_f32_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ pi,
+    const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
+    int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
+    const float* __restrict__ b1, const float* __restrict__ W2, float* __restrict__ Wout,
+    float* __restrict__ Wdout, float* __restrict__ dist_out) {
+  extern __shared__ float lds[];
+  const int KS = (rp.K + 3) / 4;
+  float* w1s = lds;
+  float* w2s = lds + kFT * KS * MLCG_WAVE;
+  stage_w1_f32(w1s, W1, rp.K, KS);
+  stage_w2_f32(w2s, W2, false);
+  __syncthreads();
+
+  int64_t np = *n_pairs_dev;
+  if (np > max_pairs) np = max_pairs;
+  const int64_t tiles = (np + 15) / 16;
+  const int l = mlcg_lane();
+  const int q = l >> 4;
+  float bias[kFT][4];
+#pragma unroll
+  for (int t = 0; t < kFT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[t][i] = b1[16 * t + 4 * q + i];
+
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + threadIdx.x / MLCG_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+  for (int64_t tile = wave; tile < tiles; tile += nwaves) {
+    const int64_t p = tile * 16 + (l & 15);
+    const bool valid = p < np;
+    const float d = pair_distance(pos, pi, pj, p, valid);
+    float crbf, dcrbf, cc, dcc;
+    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+
+    floatx4 a[kFT], ad[kFT];
+    gemm1_f32(w1s, KS, rp, d, crbf, dcrbf, a, ad, nullptr, nullptr, 0.0f);
+    // h = act(a + b1), h' = act'(a + b1) * a'
+#pragma unroll
+    for (int t = 0; t < kFT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s, d1, d2;
+        mlcg_act(rp.act, a[t][i] + bias[t][i], s, d1, d2);
+        a[t][i] = s;
+        ad[t][i] = d1 * ad[t][i];
+      }
+    floatx4 w[kFT], wd[kFT];
+    gemm2_f32(w2s, a, ad, w, wd);
+    if (valid) {
+      float* wr = Wout + p * kF + 4 * q;
+      float* wdr = Wdout + p * kF + 4 * q;
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        float4 o, od;
+        o.x = w[t][0] * cc;
+        o.y = w[t][1] * cc;
+        o.z = w[t][2] * cc;
+        o.w = w[t][3] * cc;
+        od.x = wd[t][0] * cc + w[t][0] * dcc;
+        od.y = wd[t][1] * cc + w[t][1] * dcc;
+        od.z = wd[t][2] * cc + w[t][2] * dcc;
+        od.w = wd[t][3] * cc + w[t][3] * dcc;
+        *reinterpret_cast<float4*>(wr + 16 * t) = o;
+        *reinterpret_cast<float4*>(wdr + 16 * t) = od;
+      }
+      if (dist_out && q == 0) dist_out[p] = d;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp16 operands, fp32 accumulation (v_mfma_f32_16x16x32_f16).
+//
+// First product, k block s (32 basis functions): lane l supplies
+//   A[m = l%16][8q + j] = W1[16t + l%16][32s + 8q + j]      (j = 0..7)
+//   B[8q + j][n = l%16] = g[pair l%16][32s + 8q + j]
+// Second product, k block s covers feature tiles 2s and 2s+1; lane group q
+// supplies features 16(2s + j/4) + 4q + j%4 -- exactly the accumulator
+// values it owns after the first product.
+//   w1h[((t*KS32 + s)*64 + l)*8 + j] = W1[16t + l%16][32s + 8q + j]
+//   w2h[((t*4 + s)*64 + l)*8 + j]    = W2[16t + l%16][16(2s + j/4) + 4q + j%4]
+__device__ void stage_f16(_Float16* w1h, _Float16* w2h, const float* __restrict__ W1,
+                          const float* __restrict__ W2, int K, int KS32) {
+  const int n1 = kFT * KS32 * MLCG_WAVE * 8;
+  for (int x = threadIdx.x; x < n1; x += blockDim.x) {
+    const int j = x & 7;
+    const int l = (x >> 3) & 63;
+    const int ts = x >> 9;
+    const int s = ts % KS32, t = ts / KS32;
+    const int k = 32 * s + 8 * (l >> 4) + j;
+    w1h[x] = (_Float16)(k < K ? W1[(16 * t + (l & 15)) * K + k] : 0.0f);
+  }
+  const int n2 = kFT * (kFT / 2) * MLCG_WAVE * 8;
+  for (int x = threadIdx.x; x < n2; x += blockDim.x) {
+    const int j = x & 7;
+    const int l = (x >> 3) & 63;
+    const int ts = x >> 9;
+    const int s = ts % (kFT / 2), t = ts / (kFT / 2);
+    const int c = 16 * (2 * s + (j >> 2)) + 4 * (l >> 4) + (j & 3);
+    w2h[x] = (_Float16)W2[(16 * t + (l & 15)) * kF + c];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ pi,
+    const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
+    int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
+    const float* __restrict__ b1, const float* __restrict__ W2, __half* __restrict__ Wout,
+    __half* __restrict__ Wdout, float* __restrict__ dist_out) {
+  extern __shared__ float lds[];
+  const int KS32 = (rp.K + 31) / 32;
+  _Float16* w1h = reinterpret_cast<_Float16*>(lds);
+  _Float16* w2h = w1h + kFT * KS32 * MLCG_WAVE * 8;
+  stage_f16(w1h, w2h, W1, W2, rp.K, KS32);
+  __syncthreads();
+
+  int64_t np = *n_pairs_dev;
+  if (np > max_pairs) np = max_pairs;
+  const int64_t tiles = (np + 15) / 16;
+  const int l = mlcg_lane();
+  const int q = l >> 4;
+  float bias[kFT][4];
+#pragma unroll
+  for (int t = 0; t < kFT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[t][i] = b1[16 * t + 4 * q + i];
+
+  const halfx8* w1v = reinterpret_cast<const halfx8*>(w1h);
+  const halfx8* w2v = reinterpret_cast<const halfx8*>(w2h);
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + threadIdx.x / MLCG_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+  for (int64_t tile = wave; tile < tiles; tile += nwaves) {
+    const int64_t p = tile * 16 + (l & 15);
+    const bool valid = p < np;
+    const float d = pair_distance(pos, pi, pj, p, valid);
+    float crbf, dcrbf, cc, dcc;
+    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+
+    floatx4 a[kFT], ad[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      a[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      ad[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s = 0; s < KS32; ++s) {
+      halfx8 g8, gd8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float g, gd;
+        rbf_value(rp, 32 * s + 8 * q + j, d, crbf, dcrbf, g, gd);
+        g8[j] = (_Float16)g;
+        gd8[j] = (_Float16)gd;
+      }
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        const halfx8 w = w1v[(t * KS32 + s) * MLCG_WAVE + l];
+        a[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, g8, a[t], 0, 0, 0);
+        ad[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, gd8, ad[t], 0, 0, 0);
+      }
+    }
+    halfx8 h8[kFT / 2], hd8[kFT / 2];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s, d1, d2;
+        mlcg_act(rp.act, a[t][i] + bias[t][i], s, d1, d2);
+        h8[t >> 1][4 * (t & 1) + i] = (_Float16)s;
+        hd8[t >> 1][4 * (t & 1) + i] = (_Float16)(d1 * ad[t][i]);
+      }
+    floatx4 w[kFT], wd[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      w[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      wd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int s = 0; s < kFT / 2; ++s)
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        const halfx8 a2 = w2v[(t * (kFT / 2) + s) * MLCG_WAVE + l];
+        w[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, h8[s], w[t], 0, 0, 0);
+        wd[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, hd8[s], wd[t], 0, 0, 0);
+      }
+    if (valid) {
+      __half* wr = Wout + p * kF + 4 * q;
+      __half* wdr = Wdout + p * kF + 4 * q;
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        halfx4 o, od;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i] = (_Float16)(w[t][i] * cc);
+          od[i] = (_Float16)(wd[t][i] * cc + w[t][i] * dcc);
+        }
+        *reinterpret_cast<halfx4*>(wr + 16 * t) = o;
+        *reinterpret_cast<halfx4*>(wdr + 16 * t) = od;
+      }
+      if (dist_out && q == 0) dist_out[p] = d;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reverse of the chain for given Wbar, Wdbar (fp32).  Per pair:
+//   wbar  = Wbar C + Wdbar C'       w'bar = Wdbar C
+//   hbar  = W2^T wbar               h'bar = W2^T w'bar
+//   abar  = hbar act'(a) + h'bar act''(a) a'      a'bar = h'bar act'(a)
+// The weight gradients are the pair-reductions dW2 = sum wbar h^T + w'bar h'^T,
+// dW1 = sum abar g^T + a'bar g'^T and db1 = sum abar; this kernel writes the
+// per-pair factors so that they are plain GEMMs.
+__global__ __launch_bounds__(kThreads) void filter_bwd_f32_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ pi,
+    const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
+    int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
+    const float* __restrict__ b1, const float* __restrict__ W2,
+    const float* __restrict__ Wbar, const float* __restrict__ Wdbar, float* __restrict__ H,
+    float* __restrict__ T, float* __restrict__ A, float* __restrict__ G) {
+  extern __shared__ float lds[];
+  const int KS = (rp.K + 3) / 4;
+  const int Kp = 4 * KS;
+  float* w1s = lds;
+  float* w2ts = lds + kFT * KS * MLCG_WAVE;
+  stage_w1_f32(w1s, W1, rp.K, KS);
+  stage_w2_f32(w2ts, W2, true);
+  __syncthreads();
+
+  int64_t np = *n_pairs_dev;
+  if (np > max_pairs) np = max_pairs;
+  const int64_t tiles = (max_pairs + 15) / 16;
+  const int l = mlcg_lane();
+  const int q = l >> 4;
+  float bias[kFT][4];
+#pragma unroll
+  for (int t = 0; t < kFT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[t][i] = b1[16 * t + 4 * q + i];
+
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + threadIdx.x / MLCG_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+  const int64_t slab = max_pairs * kF;  // stride between [0] and [1] halves
+  const int64_t gslab = max_pairs * Kp;
+  for (int64_t tile = wave; tile < tiles; tile += nwaves) {
+    const int64_t p = tile * 16 + (l & 15);
+    const bool inrange = p < max_pairs;
+    const bool valid = p < np;
+    if (tile * 16 >= np) {
+      // whole tile past the live count: zero rows so the GEMMs ignore them
+      if (inrange) {
+        const float4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < kFT; ++t) {
+          const int64_t off = p * kF + 16 * t + 4 * q;
+          *reinterpret_cast<float4*>(H + off) = z;
+          *reinterpret_cast<float4*>(H + slab + off) = z;
+          *reinterpret_cast<float4*>(T + off) = z;
+          *reinterpret_cast<float4*>(T + slab + off) = z;
+          *reinterpret_cast<float4*>(A + off) = z;
+          *reinterpret_cast<float4*>(A + slab + off) = z;
+        }
+        for (int s = 0; s < KS; ++s) {
+          G[p * Kp + 4 * s + q] = 0.f;
+          G[gslab + p * Kp + 4 * s + q] = 0.f;
+        }
+      }
+      continue;
+    }
+    const float d = pair_distance(pos, pi, pj, p, valid);
+    float crbf, dcrbf, cc, dcc;
+    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+
+    floatx4 a[kFT], ad[kFT];
+    // g/g' rows are written straight from the B-operand registers
+    gemm1_f32(w1s, KS, rp, d, crbf, dcrbf, a, ad, inrange ? G + p * Kp : nullptr,
+              inrange ? G + gslab + p * Kp : nullptr, valid ? 1.0f : 0.0f);
+    floatx4 act1[kFT], act2[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s, d1, d2;
+        mlcg_act(rp.act, a[t][i] + bias[t][i], s, d1, d2);
+        a[t][i] = s;                 // h
+        act1[t][i] = d1;
+        act2[t][i] = d2 * ad[t][i];  // act''(a) a'
+        ad[t][i] = d1 * ad[t][i];    // h'
+      }
+    floatx4 tb[kFT], tdb[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      float4 wb = {0.f, 0.f, 0.f, 0.f}, wdb = {0.f, 0.f, 0.f, 0.f};
+      if (valid) {
+        wb = *reinterpret_cast<const float4*>(Wbar + p * kF + 16 * t + 4 * q);
+        wdb = *reinterpret_cast<const float4*>(Wdbar + p * kF + 16 * t + 4 * q);
+      }
+      tb[t][0] = wb.x * cc + wdb.x * dcc;
+      tb[t][1] = wb.y * cc + wdb.y * dcc;
+      tb[t][2] = wb.z * cc + wdb.z * dcc;
+      tb[t][3] = wb.w * cc + wdb.w * dcc;
+      tdb[t][0] = wdb.x * cc;
+      tdb[t][1] = wdb.y * cc;
+      tdb[t][2] = wdb.z * cc;
+      tdb[t][3] = wdb.w * cc;
+    }
+    floatx4 hb[kFT], hdb[kFT];
+    gemm2_f32(w2ts, tb, tdb, hb, hdb);
+    if (inrange) {
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        float4 ab, adb;
+        ab.x = hb[t][0] * act1[t][0] + hdb[t][0] * act2[t][0];
+        ab.y = hb[t][1] * act1[t][1] + hdb[t][1] * act2[t][1];
+        ab.z = hb[t][2] * act1[t][2] + hdb[t][2] * act2[t][2];
+        ab.w = hb[t][3] * act1[t][3] + hdb[t][3] * act2[t][3];
+        adb.x = hdb[t][0] * act1[t][0];
+        adb.y = hdb[t][1] * act1[t][1];
+        adb.z = hdb[t][2] * act1[t][2];
+        adb.w = hdb[t][3] * act1[t][3];
+        const float m = valid ? 1.0f : 0.0f;
+        const int64_t off = p * kF + 16 * t + 4 * q;
+        *reinterpret_cast<float4*>(H + off) =
+            float4{a[t][0] * m, a[t][1] * m, a[t][2] * m, a[t][3] * m};
+        *reinterpret_cast<float4*>(H + slab + off) =
+            float4{ad[t][0] * m, ad[t][1] * m, ad[t][2] * m, ad[t][3] * m};
+        *reinterpret_cast<float4*>(T + off) = float4{tb[t][0], tb[t][1], tb[t][2], tb[t][3]};
+        *reinterpret_cast<float4*>(T + slab + off) =
+            float4{tdb[t][0], tdb[t][1], tdb[t][2], tdb[t][3]};
+        *reinterpret_cast<float4*>(A + off) = ab;
+        *reinterpret_cast<float4*>(A + slab + off) = adb;
+      }
+    }
+  }
+}
+
+// Kernels here use more than 64 KiB of dynamic LDS; raise the per-kernel limit
+// once (gfx950 has 160 KiB per CU).
+template <typename K>
+void allow_lds(K kernel, size_t bytes) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+RbfParams make_params(const float* offsets, float coeff, int K, int rk, float rlo, float rhi,
+                      int ck, float clo, float chi, int act) {
+  RbfParams rp;
+  rp.offsets = offsets;
+  rp.coeff = coeff;
+  rp.K = K;
+  rp.rbf_kind = rk;
+  rp.rbf_lo = rlo;
+  rp.rbf_hi = rhi;
+  rp.conv_kind = ck;
+  rp.conv_lo = clo;
+  rp.conv_hi = chi;
+  rp.act = act;
+  return rp;
+}
+
+bool valid_params(int K, int rk, int ck, int act, int F) {
+  return F == kF && K >= 1 && K <= kMaxK && (rk == 0 || rk == 1) && (ck == 0 || ck == 1) &&
+         (act == 0 || act == 1);
+}
+
+}  // namespace
+
+extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
+                               const int32_t* n_pairs_dev, int64_t max_pairs,
+                               const float* offsets, float coeff, int num_rbf,
+                               int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                               int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                               const float* W1, const float* b1, const float* W2,
+                               int num_filters, int f16, void* W_out, void* Wd_out,
+                               float* dist_out, void* stream) {
+  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
+    return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
+  if (max_pairs == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && pair_ij && n_pairs_dev && offsets && W1 && b1 && W2 && W_out && Wd_out);
+  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
+                             conv_cut_kind, conv_lo, conv_hi, act);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
+  hipStream_t s = mlcg_stream(stream);
+  if (!f16) {
+    const int KS = (num_rbf + 3) / 4;
+    const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
+    allow_lds(filter_fwd_f32_kernel, lds);
+    hipLaunchKernelGGL(filter_fwd_f32_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
+                       pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
+                       static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out);
+  } else {
+    const int KS32 = (num_rbf + 31) / 32;
+    const size_t lds =
+        sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8);
+    allow_lds(filter_fwd_f16_kernel, lds);
+    hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
+                       pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
+                       static_cast<__half*>(W_out), static_cast<__half*>(Wd_out), dist_out);
+  }
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
+                               const int32_t* n_pairs_dev, int64_t max_pairs,
+                               const float* offsets, float coeff, int num_rbf,
+                               int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                               int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                               const float* W1, const float* b1, const float* W2,
+                               int num_filters, const float* Wbar, const float* Wdbar,
+                               float* H, float* T, float* A, float* G, void* stream) {
+  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
+    return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
+  if (max_pairs == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && pair_ij && n_pairs_dev && offsets && W1 && b1 && W2 && Wbar && Wdbar &&
+               H && T && A && G);
+  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
+                             conv_cut_kind, conv_lo, conv_hi, act);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
+  const int KS = (num_rbf + 3) / 4;
+  const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
+  allow_lds(filter_bwd_f32_kernel, lds);
+  hipLaunchKernelGGL(filter_bwd_f32_kernel, dim3(groups), dim3(kThreads), lds,
+                     mlcg_stream(stream), pos, pair_ij, pair_ij + pair_stride, n_pairs_dev,
+                     max_pairs, rp, W1, b1, W2, Wbar, Wdbar, H, T, A, G);
+  return mlcg_launch_status();
+}

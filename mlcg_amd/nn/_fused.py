@@ -1,0 +1,423 @@
+"""Fused SchNet energy / force / force-matching evaluation on the HIP kernels.
+
+This is the hot path of the package.  Edge work (filter network, CFConv
+gather/scatter, their backward, tangent and second-order reverse, the pair ->
+node force scatter) runs in the gfx950 kernels of ``libmlcg_hip.so``; node work
+(the [N, H] x [H, H] linears and elementwise activations) runs as library
+GEMMs and elementwise ops on the same stream.
+
+Math (per interaction block, activation s = act(z)):
+    y = x A1^T ;  agg_i = sum_j y_j * W_ij ;  z = agg A2^T + c2 ;  v = s A3^T + c3 ;
+    x <- x + v ;  o = MLP_out(x) ;  E_b = sum_{n in b} o_n
+with W_ij = filter(d_ij) evaluated per unordered pair, and Wd = dW/dd.
+
+* reverse1 (forces): the usual reverse sweep, plus per pair
+  dbar_p = sum_blocks <Wd_p, gagg_i y_j + gagg_j y_i>, and
+  F_i = sum_j dbar_p (pos_j - pos_i) / d_p.
+* tangent: forward-mode derivative along a position direction u
+  (ddot_p = rhat_p . (u_j - u_i), Wdot = Wd ddot).
+* reverse2: reverse sweep of (primal, tangent) for d/dtheta of
+  sum_n tw_n odot_n + pw_n o_n.  The tangent adjoints equal the reverse1
+  adjoints when reverse1 was seeded with tw, so only the primal adjoints are
+  new.  This is the hand-derived double backward of the force-matching loss
+  L(F): with u = -dL/dF it gives dL/dtheta, replacing the autograd replay of
+  create_graph=True (mlcg/nn/gradients.py:216-222, mlcg/pl/model.py:113-131).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import torch
+
+from .. import ops
+from .activations import act_derivs, act_value
+
+
+@dataclass
+class BlockParams:
+    W1: torch.Tensor  # filter layer 0 weight [F, K]
+    b1: torch.Tensor  # filter layer 0 bias [F]
+    W2: torch.Tensor  # filter layer 2 weight [F, F]
+    A1: torch.Tensor  # conv.lin1.weight [F, H]
+    A2: torch.Tensor  # conv.lin2.weight [H, F]
+    c2: torch.Tensor  # conv.lin2.bias [H]
+    A3: torch.Tensor  # lin.weight [H, H]
+    c3: torch.Tensor  # lin.bias [H]
+
+    def tensors(self) -> List[torch.Tensor]:
+        return [self.W1, self.b1, self.W2, self.A1, self.A2, self.c2, self.A3, self.c3]
+
+
+@dataclass
+class FusedSpec:
+    """Static (non-tensor) description of a fusable SchNet."""
+
+    filt: ops.FilterSpec
+    filter_act: int
+    block_act: int
+    out_act: int
+    num_blocks: int
+    out_has_bias: List[bool]  # per output linear
+    f16: bool = False
+
+
+@dataclass
+class Params:
+    emb: torch.Tensor
+    blocks: List[BlockParams]
+    out_w: List[torch.Tensor]
+    out_b: List[Optional[torch.Tensor]]
+
+    def flat(self) -> List[torch.Tensor]:
+        out = [self.emb]
+        for b in self.blocks:
+            out += b.tensors()
+        for w, b in zip(self.out_w, self.out_b):
+            out.append(w)
+            if b is not None:
+                out.append(b)
+        return out
+
+    @staticmethod
+    def unflat(spec: FusedSpec, flat: List[torch.Tensor]) -> "Params":
+        it = iter(flat)
+        emb = next(it)
+        blocks = [BlockParams(*[next(it) for _ in range(8)]) for _ in range(spec.num_blocks)]
+        out_w, out_b = [], []
+        for has_b in spec.out_has_bias:
+            out_w.append(next(it))
+            out_b.append(next(it) if has_b else None)
+        return Params(emb, blocks, out_w, out_b)
+
+
+@dataclass
+class State:
+    """Activations saved by forward / reverse1 / tangent."""
+
+    pos: torch.Tensor
+    types: torch.Tensor
+    graph: ops.PairGraph
+    dist: Optional[torch.Tensor] = None
+    W: List[torch.Tensor] = field(default_factory=list)
+    Wd: List[torch.Tensor] = field(default_factory=list)
+    x: List[torch.Tensor] = field(default_factory=list)    # block inputs
+    y: List[torch.Tensor] = field(default_factory=list)
+    agg: List[torch.Tensor] = field(default_factory=list)
+    z: List[torch.Tensor] = field(default_factory=list)
+    s: List[torch.Tensor] = field(default_factory=list)
+    xL: Optional[torch.Tensor] = None
+    oh: List[torch.Tensor] = field(default_factory=list)   # output-MLP layer inputs
+    oz: List[torch.Tensor] = field(default_factory=list)   # output-MLP pre-activations
+    os_: List[torch.Tensor] = field(default_factory=list)  # output-MLP activations
+    o: Optional[torch.Tensor] = None
+    # reverse1
+    xbar_out: List[torch.Tensor] = field(default_factory=list)
+    sbar1: List[torch.Tensor] = field(default_factory=list)
+    zbar1: List[torch.Tensor] = field(default_factory=list)
+    gagg1: List[torch.Tensor] = field(default_factory=list)
+    ybar1: List[torch.Tensor] = field(default_factory=list)
+    # tangent
+    ddot: Optional[torch.Tensor] = None
+    xdot_in: List[Optional[torch.Tensor]] = field(default_factory=list)
+    ydot: List[Optional[torch.Tensor]] = field(default_factory=list)
+    aggdot: List[torch.Tensor] = field(default_factory=list)
+    zdot: List[torch.Tensor] = field(default_factory=list)
+    sdot: List[torch.Tensor] = field(default_factory=list)
+    ohdot: List[torch.Tensor] = field(default_factory=list)
+    ozdot: List[torch.Tensor] = field(default_factory=list)
+    odot: Optional[torch.Tensor] = None
+
+
+def _lin(x, w, b=None):
+    return torch.addmm(b, x, w.t()) if b is not None else x.mm(w.t())
+
+
+def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
+            graph: ops.PairGraph, save: bool = True) -> Tuple[torch.Tensor, State]:
+    """Energies [B] and the saved state."""
+    st = State(pos=pos, types=types, graph=graph)
+    x = P.emb.index_select(0, types)
+    for k, bp in enumerate(P.blocks):
+        W, Wd, dist = ops.filter_fwd(pos, graph, spec.filt, bp.W1, bp.b1, bp.W2,
+                                     f16=spec.f16, want_dist=(k == 0))
+        if k == 0:
+            st.dist = dist
+        y = x.mm(bp.A1.t())
+        agg = ops.cfconv_gather(y, W, graph)
+        z = _lin(agg, bp.A2, bp.c2)
+        s = act_value(z, spec.block_act)
+        v = _lin(s, bp.A3, bp.c3)
+        st.W.append(W)
+        st.Wd.append(Wd)
+        if save:
+            st.x.append(x)
+            st.y.append(y)
+            st.agg.append(agg)
+            st.z.append(z)
+            st.s.append(s)
+        x = x + v
+    st.xL = x
+    h = x
+    n_lin = len(P.out_w)
+    for k in range(n_lin):
+        st.oh.append(h)
+        zz = _lin(h, P.out_w[k], P.out_b[k])
+        if k < n_lin - 1:
+            ss = act_value(zz, spec.out_act)
+            st.oz.append(zz)
+            st.os_.append(ss)
+            h = ss
+        else:
+            h = zz
+    st.o = h
+    E = ops.segment_sum(h, graph.frame_ptr)
+    return E, st
+
+
+def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
+             need_forces: bool = True) -> Optional[torch.Tensor]:
+    """First-order reverse seeded with d(objective)/d o_n = seed[n]; returns
+    the forces -d/dpos (sum_n seed_n o_n) and saves the adjoints."""
+    graph = st.graph
+    n_lin = len(P.out_w)
+    hbar = seed.view(-1, 1) * P.out_w[-1]  # [N, n_last_in]
+    for k in range(n_lin - 2, -1, -1):
+        d1, _ = act_derivs(st.oz[k], st.os_[k], spec.out_act)
+        zbar = hbar * d1
+        hbar = zbar.mm(P.out_w[k])
+    xbar = hbar
+    dbar = torch.zeros(graph.pair_capacity, dtype=torch.float32, device=st.pos.device)
+    nb = len(P.blocks)
+    st.xbar_out = [None] * nb
+    st.sbar1 = [None] * nb
+    st.zbar1 = [None] * nb
+    st.gagg1 = [None] * nb
+    st.ybar1 = [None] * nb
+    for k in range(nb - 1, -1, -1):
+        bp = P.blocks[k]
+        sbar = xbar.mm(bp.A3)
+        d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
+        zbar = sbar * d1
+        gagg = zbar.mm(bp.A2)
+        ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar)
+        st.xbar_out[k] = xbar
+        st.sbar1[k] = sbar
+        st.zbar1[k] = zbar
+        st.gagg1[k] = gagg
+        st.ybar1[k] = ybar
+        xbar = xbar + ybar.mm(bp.A1)
+    if not need_forces:
+        return None
+    return ops.pair_forces(st.pos, st.dist, dbar, graph)
+
+
+def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> torch.Tensor:
+    """Forward-mode sweep along position direction u; returns odot [N, 1]."""
+    graph = st.graph
+    st.ddot = ops.pair_ddot(st.pos, st.dist, graph, u)
+    xdot = None
+    st.xdot_in, st.ydot, st.aggdot, st.zdot, st.sdot = [], [], [], [], []
+    for k, bp in enumerate(P.blocks):
+        ydot = None if xdot is None else xdot.mm(bp.A1.t())
+        aggdot = ops.cfconv_gather_tangent(ydot, st.y[k], st.W[k], st.Wd[k], st.ddot, graph)
+        zdot = aggdot.mm(bp.A2.t())
+        d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
+        sdot = d1 * zdot
+        vdot = sdot.mm(bp.A3.t())
+        st.xdot_in.append(xdot)
+        st.ydot.append(ydot)
+        st.aggdot.append(aggdot)
+        st.zdot.append(zdot)
+        st.sdot.append(sdot)
+        xdot = vdot if xdot is None else xdot + vdot
+    hdot = xdot
+    n_lin = len(P.out_w)
+    st.ohdot, st.ozdot = [], []
+    for k in range(n_lin):
+        st.ohdot.append(hdot)
+        zd = hdot.mm(P.out_w[k].t())
+        if k < n_lin - 1:
+            d1, _ = act_derivs(st.oz[k], st.os_[k], spec.out_act)
+            st.ozdot.append(zd)
+            hdot = d1 * zd
+        else:
+            hdot = zd
+    st.odot = hdot
+    return hdot
+
+
+def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
+             pw: Optional[torch.Tensor]) -> List[torch.Tensor]:
+    """Parameter gradients of sum_n tw_n odot_n + pw_n o_n, in Params.flat()
+    order.  tw requires a preceding tangent() and reverse1(seed=tw)."""
+    tangent_on = tw is not None
+    graph = st.graph
+    dev = st.pos.device
+    N = st.pos.shape[0]
+    n_lin = len(P.out_w)
+    g_out_w = [None] * n_lin
+    g_out_b = [None] * n_lin
+    # last output linear: o = h W^T (+ b)
+    WL = P.out_w[-1]
+    gW = torch.zeros_like(WL)
+    if tangent_on:
+        gW = gW + tw.view(1, -1).mm(st.ohdot[-1])
+    if pw is not None:
+        gW = gW + pw.view(1, -1).mm(st.oh[-1])
+    g_out_w[-1] = gW
+    if P.out_b[-1] is not None:
+        g_out_b[-1] = (pw.sum().view(1) if pw is not None
+                       else torch.zeros_like(P.out_b[-1]))
+    hdotbar = tw.view(-1, 1) * WL if tangent_on else None
+    hbar2 = pw.view(-1, 1) * WL if pw is not None else torch.zeros(
+        N, WL.shape[1], dtype=torch.float32, device=dev)
+    for k in range(n_lin - 2, -1, -1):
+        d1, d2 = act_derivs(st.oz[k], st.os_[k], spec.out_act)
+        zbar2 = hbar2 * d1
+        if tangent_on:
+            zdotbar = hdotbar * d1
+            zbar2 = zbar2 + hdotbar * d2 * st.ozdot[k]
+            g_out_w[k] = zdotbar.t().mm(st.ohdot[k]) + zbar2.t().mm(st.oh[k])
+            hdotbar = zdotbar.mm(P.out_w[k])
+        else:
+            g_out_w[k] = zbar2.t().mm(st.oh[k])
+        g_out_b[k] = zbar2.sum(0)
+        hbar2 = zbar2.mm(P.out_w[k])
+    xbar2 = hbar2
+    g_blocks = [None] * len(P.blocks)
+    for k in range(len(P.blocks) - 1, -1, -1):
+        bp = P.blocks[k]
+        sbar2 = xbar2.mm(bp.A3)
+        d1, d2 = act_derivs(st.z[k], st.s[k], spec.block_act)
+        gA3 = xbar2.t().mm(st.s[k])
+        zbar2 = sbar2 * d1
+        if tangent_on:
+            gA3 = gA3 + st.xbar_out[k].t().mm(st.sdot[k])
+            zbar2 = zbar2 + st.sbar1[k] * d2 * st.zdot[k]
+        gc3 = xbar2.sum(0)
+        gagg2 = zbar2.mm(bp.A2)
+        gA2 = zbar2.t().mm(st.agg[k])
+        if tangent_on:
+            gA2 = gA2 + st.zbar1[k].t().mm(st.aggdot[k])
+        gc2 = zbar2.sum(0)
+        ybar2, Wbar, Wdbar = ops.cfconv_gather_rev2(
+            gagg2, st.gagg1[k] if tangent_on else None, st.y[k],
+            st.ydot[k] if tangent_on else None, st.W[k], st.Wd[k],
+            st.ddot if tangent_on else None, graph)
+        gA1 = ybar2.t().mm(st.x[k])
+        if tangent_on and st.xdot_in[k] is not None:
+            gA1 = gA1 + st.ybar1[k].t().mm(st.xdot_in[k])
+        xbar2 = xbar2 + ybar2.mm(bp.A1)
+        gW1, gb1, gW2 = ops.filter_bwd(st.pos, graph, spec.filt, bp.W1, bp.b1, bp.W2, Wbar,
+                                       Wdbar)
+        g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
+    g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
+    out = [g_emb]
+    for gb in g_blocks:
+        out += gb
+    for k in range(n_lin):
+        out.append(g_out_w[k])
+        if P.out_b[k] is not None:
+            out.append(g_out_b[k])
+    return out
+
+
+def node_seed(frame_weights: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
+    return frame_weights.to(torch.float32).index_select(0, batch).contiguous()
+
+
+# --------------------------------------------------------------------------
+# autograd glue
+
+class EnergyForces(torch.autograd.Function):
+    """(E [B], F [N, 3]) = fused SchNet energies and forces.
+
+    backward(Ebar, Fbar) returns parameter gradients of
+    <Ebar, E> + <Fbar, F>, i.e. the force-matching double backward.  Position
+    gradients are not produced (positions enter detached)."""
+
+    @staticmethod
+    def forward(ctx, spec, pos, types, batch, graph, training, *flat):
+        P = Params.unflat(spec, list(flat))
+        E, st = forward(spec, P, pos, types, graph, save=True)
+        ones = torch.ones(pos.shape[0], dtype=torch.float32, device=pos.device)
+        F = reverse1(spec, P, st, ones)
+        if training:
+            ctx.spec, ctx.P, ctx.st, ctx.batch = spec, P, st, batch
+        ctx.set_materialize_grads(False)
+        return E, F
+
+    @staticmethod
+    def backward(ctx, Ebar, Fbar):
+        spec, P, st, batch = ctx.spec, ctx.P, ctx.st, ctx.batch
+        if spec.f16:
+            raise NotImplementedError(
+                "the fp16 filter path provides energies and forces only; "
+                "train with fp32 filters")
+        tw = pw = None
+        if Fbar is not None:
+            # <Fbar, F> = <Fbar, -grad sum E> : tangent along u = -Fbar, seed 1
+            tangent(spec, P, st, -Fbar)
+            tw = torch.ones(st.pos.shape[0], dtype=torch.float32, device=st.pos.device)
+        if Ebar is not None:
+            pw = node_seed(Ebar, batch)
+        if tw is None and pw is None:
+            grads = [None] * len(P.flat())
+        else:
+            grads = reverse2(spec, P, st, tw, pw)
+        ctx.st = None
+        return (None, None, None, None, None, None, *grads)
+
+
+class Energy(torch.autograd.Function):
+    """E [B] with a first-order backward that is itself differentiable
+    (EnergyGrad), for generic autograd.grad(E, pos, create_graph=True) use."""
+
+    @staticmethod
+    def forward(ctx, spec, types, batch, graph, pos, *flat):
+        P = Params.unflat(spec, list(flat))
+        E, st = forward(spec, P, pos.detach(), types, graph, save=True)
+        ctx.spec, ctx.P, ctx.st, ctx.batch = spec, P, st, batch
+        ctx.save_for_backward(pos, *flat)
+        return E
+
+    @staticmethod
+    def backward(ctx, Ebar):
+        pos, *flat = ctx.saved_tensors
+        out = EnergyGrad.apply(ctx.spec, ctx.st, ctx.batch, Ebar, pos, *flat)
+        return (None, None, None, None, *out)
+
+
+class EnergyGrad(torch.autograd.Function):
+    """(dE/dpos, dE/dtheta) weighted by Ebar; its backward implements the
+    second-order term for a loss on dE/dpos (tangent + reverse2)."""
+
+    @staticmethod
+    def forward(ctx, spec, st, batch, Ebar, pos, *flat):
+        P = Params.unflat(spec, list(flat))
+        seed = node_seed(Ebar, batch)
+        F = reverse1(spec, P, st, seed)
+        pgrads = reverse2(spec, P, st, None, seed)
+        ctx.spec, ctx.st, ctx.P, ctx.seed, ctx.batch = spec, st, P, seed, batch
+        ctx.set_materialize_grads(False)
+        return (-F, *pgrads)
+
+    @staticmethod
+    def backward(ctx, gpos_bar, *pgrad_bars):
+        if any(g is not None for g in pgrad_bars):
+            raise NotImplementedError(
+                "differentiating parameter gradients of the fused SchNet is not supported")
+        spec, st, P = ctx.spec, ctx.st, ctx.P
+        nflat = len(P.flat())
+        if gpos_bar is None:
+            return (None,) * (5 + nflat)
+        if spec.f16:
+            raise NotImplementedError("the fp16 filter path has no double backward")
+        # d/dtheta <gpos_bar, grad_pos(sum seed o)> = tangent along gpos_bar
+        odot = tangent(spec, P, st, gpos_bar)
+        grads = reverse2(spec, P, st, ctx.seed, None)
+        # d/dEbar_b <gpos_bar, grad E_b> = per-frame tangent of the energy
+        Ebar_grad = ops.segment_sum(odot, st.graph.frame_ptr)
+        return (None, None, None, Ebar_grad, None, *grads)

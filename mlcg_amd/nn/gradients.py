@@ -1,0 +1,106 @@
+"""Output wrappers: SumOut, EnergyOut, GradientsOut (mlcg/nn/gradients.py:7-233).
+
+GradientsOut around a fusable HIP SchNet computes energies and forces in one
+fused pass (``SchNet.energy_forces``) instead of an autograd replay; in
+training mode the result carries the hand-derived force-matching double
+backward.  Any other model goes through torch.autograd exactly like the
+reference (lines 208-228).
+"""
+
+from __future__ import annotations
+
+from typing import Any, List, Sequence
+
+import torch
+
+from ..data._keys import ENERGY_KEY, FORCE_KEY
+
+
+class SumOut(torch.nn.Module):
+    name: str = "SumOut"
+
+    def __init__(self, models: torch.nn.ModuleDict, targets: List[str] = None):
+        super().__init__()
+        if targets is None:
+            targets = [ENERGY_KEY, FORCE_KEY]
+        self.targets = targets
+        self.models = models
+
+    def forward(self, data):
+        for target in self.targets:
+            data.out[target] = 0.00
+        for name in self.models.keys():
+            data = self.models[name](data)
+            for target in self.targets:
+                data.out[target] += data.out[name][target]
+        return data
+
+    def neighbor_list(self, **kwargs):
+        nl = {}
+        for _, model in self.models.items():
+            nl.update(**model.neighbor_list(**kwargs))
+        return nl
+
+
+class EnergyOut(torch.nn.Module):
+    name: str = "EnergyOut"
+
+    def __init__(self, model: torch.nn.Module, targets: List[str] = None):
+        super().__init__()
+        if targets is None:
+            targets = [ENERGY_KEY]
+        self.targets = targets
+        self.model = model
+        self.name = self.model.name
+
+    def forward(self, data):
+        data = self.model(data)
+        for target in self.targets:
+            data.out[target] = data.out[self.name][target]
+        return data
+
+
+class GradientsOut(torch.nn.Module):
+    _targets = {FORCE_KEY: ENERGY_KEY}
+
+    def __init__(self, model: torch.nn.Module, targets: str = FORCE_KEY):
+        super().__init__()
+        self.model = model
+        self.name = self.model.name
+        self.targets = []
+        if isinstance(targets, str):
+            self.targets = [targets]
+        elif isinstance(targets, Sequence):
+            self.targets = list(targets)
+        assert any(k in GradientsOut._targets for k in self.targets), (
+            f"targets={self.targets} should be any of {GradientsOut._targets}")
+
+    def _fused_model(self):
+        from .schnet import SchNet
+
+        m = self.model
+        if isinstance(m, SchNet) and FORCE_KEY in self.targets and m.fused_spec() is not None:
+            return m
+        return None
+
+    def forward(self, data):
+        fused = self._fused_model()
+        if fused is not None:
+            energy, forces = fused.energy_forces(data, create_graph=self.training)
+            data.out[self.name] = {ENERGY_KEY: energy, FORCE_KEY: forces}
+            data.pos = data.pos.detach()
+            return data
+        data.pos.requires_grad_(True)
+        data = self.model(data)
+        if FORCE_KEY in self.targets:
+            y = data.out[ENERGY_KEY] if self.name == "SumOut" else data.out[self.name][ENERGY_KEY]
+            dy_dr = torch.autograd.grad(y.sum(), data.pos, create_graph=self.training)[0]
+            if self.name == "SumOut":
+                data.out[FORCE_KEY] = -dy_dr
+            else:
+                data.out[self.name][FORCE_KEY] = -dy_dr
+        data.pos = data.pos.detach()
+        return data
+
+    def neighbor_list(self, **kwargs: Any):
+        return self.model.neighbor_list(**kwargs)

@@ -1,0 +1,319 @@
+"""Host-side wrappers around the C ABI of ``libmlcg_hip.so``.
+
+Every function validates shapes, dtypes, devices and contiguity (raising
+``RuntimeError`` like the reference's ``AT_ASSERTM`` checks,
+``src/opt_radius/mlcg_opt_radius/radius.cu:205-228``), allocates outputs with
+torch's caching allocator and launches on torch's current stream.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, require_device, stream_handle
+
+NUM_FILTERS = 128  # F fixed by the MFMA tiling of the filter kernels
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _as_i64(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.int64).contiguous()
+
+
+@dataclass
+class PairGraph:
+    """Canonical radius graph plus the receiver CSR and pair map.
+
+    edge_index : [2, E] int64, rows (centre i, neighbour j), sorted by (i, j)
+    rowptr     : [N + 1] int32, CSR offsets of rows of edge_index
+    col        : [E] int32 = edge_index[1]
+    pair_ij    : [2, P] int32, the upper edges (i < j) in canonical order
+    pairptr    : [N + 1] int32, offsets of each node's upper edges in pair_ij
+    eid2pair   : [E] int32, pair id of every directed edge
+    frame_ptr  : [B + 1] int64
+    """
+
+    edge_index: torch.Tensor
+    rowptr: torch.Tensor
+    col: Optional[torch.Tensor]
+    pair_ij: Optional[torch.Tensor]
+    pairptr: Optional[torch.Tensor]
+    eid2pair: Optional[torch.Tensor]
+    frame_ptr: torch.Tensor
+    num_nodes: int
+    num_edges: int
+    num_pairs: int
+    overflow: int = 0
+
+    @property
+    def n_pairs_dev(self) -> torch.Tensor:
+        """One-element int32 view holding the live pair count on the device."""
+        return self.pairptr[self.num_nodes:]
+
+    @property
+    def pair_capacity(self) -> int:
+        return 0 if self.pair_ij is None else self.pair_ij.shape[1]
+
+
+def frame_ptr_from_batch(batch: torch.Tensor, n_frames: int) -> torch.Tensor:
+    """frame_ptr [B+1] from a sorted batch vector (radius.py:72-75 equivalent)."""
+    require_device(batch)
+    batch = _as_i64(batch)
+    out = torch.empty(n_frames + 1, dtype=torch.int64, device=batch.device)
+    call("mlcg_frame_ptr_from_batch", ptr(batch), batch.numel(), n_frames, ptr(out),
+         stream_handle(batch.device))
+    return out
+
+
+def _validate_pos(pos: torch.Tensor) -> torch.Tensor:
+    require_device(pos)
+    _check(pos.dim() == 2 and pos.shape[1] == 3, f"pos must be [N, 3], got {tuple(pos.shape)}")
+    _check(pos.dtype == torch.float32,
+           f"the HIP radius graph and CFConv kernels take float32 positions, got {pos.dtype}")
+    return pos.contiguous()
+
+
+def radius_graph(
+    pos: torch.Tensor,
+    r: float,
+    batch: Optional[torch.Tensor] = None,
+    loop: bool = False,
+    max_num_neighbors: int = 32,
+    with_pairs: bool = False,
+    n_frames: Optional[int] = None,
+    frame_ptr: Optional[torch.Tensor] = None,
+) -> PairGraph:
+    """All pairs (i, j) of the same frame with |pos[j] - pos[i]| < r.
+
+    Drop-in for ``torch_cluster.radius_graph(pos, r, batch, loop,
+    max_num_neighbors, flow="target_to_source")`` as called at
+    ``mlcg/neighbor_list/torch_impl.py:216-224``, with a deterministic
+    canonical order (i ascending, then j ascending).  The membership test is
+    ``d2 < fl32(r*r)`` with d2 = ((dx*dx + dy*dy) + dz*dz) in fp32.
+
+    with_pairs additionally builds the receiver CSR and pair map used by the
+    CFConv kernels (it requires a symmetric graph, i.e. no binding
+    ``max_num_neighbors`` and ``loop=False``).
+    """
+    pos = _validate_pos(pos)
+    n = pos.shape[0]
+    dev = pos.device
+    if batch is None:
+        batch = torch.zeros(n, dtype=torch.int64, device=dev)
+    require_device(batch)
+    _check(batch.dim() == 1 and batch.numel() == n, "batch must be [N]")
+    batch = _as_i64(batch)
+    _check(r >= 0, "r must be non-negative")
+    _check(max_num_neighbors >= 0, "max_num_neighbors must be non-negative")
+    if with_pairs:
+        _check(not loop, "the pair map is defined for graphs without self loops")
+    if frame_ptr is None:
+        if n_frames is None:
+            n_frames = int(batch[-1].item()) + 1 if n > 0 else 0
+        frame_ptr = frame_ptr_from_batch(batch, n_frames)
+    s = stream_handle(dev)
+
+    deg = torch.empty(n, dtype=torch.int32, device=dev)
+    udeg = torch.empty(n, dtype=torch.int32, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    call("mlcg_radius_count", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
+         int(max_num_neighbors), ptr(deg), ptr(udeg), ptr(flags), s)
+    rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(1, _lib.load().mlcg_scan_workspace_ints(n)), dtype=torch.int32,
+                     device=dev)
+    call("mlcg_exclusive_scan2_i32", ptr(deg), ptr(udeg), n, ptr(rowptr), ptr(pairptr),
+         ptr(ws), s)
+    # one host sync to size the outputs (the reference syncs at radius.cu:288)
+    e_count, p_count, overflow = torch.stack(
+        [rowptr[n], pairptr[n], flags[0]]).tolist()
+    if with_pairs and overflow:
+        raise RuntimeError(
+            f"max_num_neighbors={max_num_neighbors} binds: the truncated graph is not "
+            "symmetric and the pair-based CFConv kernels cannot use it; raise "
+            "max_num_neighbors")
+    edge_index = torch.empty(2, e_count, dtype=torch.int64, device=dev)
+    col = pair_ij = eid2pair = None
+    if with_pairs:
+        col = torch.empty(e_count, dtype=torch.int32, device=dev)
+        pair_ij = torch.empty(2, p_count, dtype=torch.int32, device=dev)
+        eid2pair = torch.empty(e_count, dtype=torch.int32, device=dev)
+    call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
+         int(max_num_neighbors), ptr(rowptr), ptr(pairptr) if with_pairs else None,
+         e_count, e_count, ptr(edge_index), ptr(col), p_count, p_count, ptr(pair_ij),
+         ptr(eid2pair), ptr(flags), s)
+    if with_pairs:
+        call("mlcg_pair_reverse_map", ptr(pair_ij), p_count, ptr(pairptr[n:]), p_count,
+             ptr(rowptr), ptr(col), ptr(eid2pair), s)
+    return PairGraph(edge_index=edge_index, rowptr=rowptr, col=col, pair_ij=pair_ij,
+                     pairptr=pairptr if with_pairs else None, eid2pair=eid2pair,
+                     frame_ptr=frame_ptr, num_nodes=n, num_edges=e_count,
+                     num_pairs=p_count if with_pairs else 0, overflow=int(overflow))
+
+
+# --------------------------------------------------------------------------
+# Filter network
+
+@dataclass
+class FilterSpec:
+    """Static description of one fused RBF -> cutoff -> MLP -> cutoff chain."""
+
+    offsets: torch.Tensor  # [K] float32 device
+    coeff: float
+    num_rbf: int
+    rbf_cut_kind: int
+    rbf_lo: float
+    rbf_hi: float
+    conv_cut_kind: int
+    conv_lo: float
+    conv_hi: float
+    act: int
+
+
+def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
+               b1: torch.Tensor, W2: torch.Tensor, f16: bool = False,
+               want_dist: bool = True) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """W [P, F], dW/dd [P, F] (fp32, or fp16 when f16) and distances [P]."""
+    pos = _validate_pos(pos)
+    F = W1.shape[0]
+    _check(F == NUM_FILTERS, f"num_filters must be {NUM_FILTERS} for the HIP filter kernel")
+    _check(tuple(W1.shape) == (F, spec.num_rbf) and tuple(W2.shape) == (F, F)
+           and tuple(b1.shape) == (F,), "filter weights have unexpected shapes")
+    cap = graph.pair_capacity
+    dt = torch.float16 if f16 else torch.float32
+    W = torch.empty(cap, F, dtype=dt, device=pos.device)
+    Wd = torch.empty(cap, F, dtype=dt, device=pos.device)
+    dist = torch.empty(cap, dtype=torch.float32, device=pos.device) if want_dist else None
+    W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
+    call("mlcg_filter_fwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
+         ptr(spec.offsets), spec.coeff, spec.num_rbf, spec.rbf_cut_kind, spec.rbf_lo,
+         spec.rbf_hi, spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c),
+         ptr(b1c), ptr(W2c), F, int(f16), ptr(W), ptr(Wd), ptr(dist),
+         stream_handle(pos.device))
+    return W, Wd, dist
+
+
+def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
+               b1: torch.Tensor, W2: torch.Tensor, Wbar: torch.Tensor,
+               Wdbar: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients (dW1 [F, K], db1 [F], dW2 [F, F]) of <Wbar, W> + <Wdbar, dW/dd>."""
+    pos = _validate_pos(pos)
+    F = W1.shape[0]
+    K = spec.num_rbf
+    Kp = 4 * ((K + 3) // 4)
+    cap = graph.pair_capacity
+    dev = pos.device
+    H = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
+    T = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
+    A = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
+    G = torch.empty(2, cap, Kp, dtype=torch.float32, device=dev)
+    W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
+    call("mlcg_filter_bwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
+         ptr(spec.offsets), spec.coeff, K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
+         spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
+         ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(H), ptr(T), ptr(A),
+         ptr(G), stream_handle(dev))
+    # pair reductions as library GEMMs: [F, 2P] x [2P, F]
+    dW2 = T.view(2 * cap, F).t().mm(H.view(2 * cap, F))
+    dW1 = A.view(2 * cap, F).t().mm(G.view(2 * cap, Kp))[:, :K]
+    db1 = A[0].sum(0)
+    return dW1.contiguous(), db1, dW2
+
+
+# --------------------------------------------------------------------------
+# CFConv gather/scatter family
+
+def _wptr(W: torch.Tensor) -> Tuple[int, int]:
+    return ptr(W), int(W.dtype == torch.float16)
+
+
+def cfconv_gather(src: torch.Tensor, W: torch.Tensor, graph: PairGraph) -> torch.Tensor:
+    """out[i] = sum_j src[j] * W[p(i, j)]  (schnet.py:346,368)."""
+    require_device(src, W)
+    src = src.contiguous()
+    out = torch.empty_like(src)
+    wp, wf16 = _wptr(W)
+    call("mlcg_cfconv_gather", ptr(src), wp, wf16, ptr(graph.rowptr), ptr(graph.col),
+         ptr(graph.eid2pair), graph.num_nodes, src.shape[1], ptr(out),
+         stream_handle(src.device))
+    return out
+
+
+def cfconv_gather_bwd(gagg: torch.Tensor, y: torch.Tensor, W: torch.Tensor, Wd: torch.Tensor,
+                      graph: PairGraph, dbar: torch.Tensor) -> torch.Tensor:
+    """ybar = gather(gagg, W); dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i> (in place)."""
+    gagg = gagg.contiguous()
+    ybar = torch.empty_like(gagg)
+    wp, wf16 = _wptr(W)
+    call("mlcg_cfconv_gather_bwd", ptr(gagg), ptr(y.contiguous()), wp, ptr(Wd), wf16,
+         ptr(graph.rowptr), ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes,
+         gagg.shape[1], ptr(ybar), ptr(dbar), stream_handle(gagg.device))
+    return ybar
+
+
+def cfconv_gather_tangent(ydot: Optional[torch.Tensor], y: torch.Tensor, W: torch.Tensor,
+                          Wd: torch.Tensor, ddot: torch.Tensor, graph: PairGraph) -> torch.Tensor:
+    y = y.contiguous()
+    out = torch.empty_like(y)
+    call("mlcg_cfconv_gather_tangent", ptr(None if ydot is None else ydot.contiguous()),
+         ptr(y), ptr(W), ptr(Wd), ptr(ddot), ptr(graph.rowptr), ptr(graph.col),
+         ptr(graph.eid2pair), graph.num_nodes, y.shape[1], ptr(out), stream_handle(y.device))
+    return out
+
+
+def cfconv_gather_rev2(gagg2: torch.Tensor, gagg1: Optional[torch.Tensor], y: torch.Tensor,
+                       ydot: Optional[torch.Tensor], W: torch.Tensor, Wd: torch.Tensor,
+                       ddot: Optional[torch.Tensor], graph: PairGraph):
+    gagg2 = gagg2.contiguous()
+    F = gagg2.shape[1]
+    ybar2 = torch.empty_like(gagg2)
+    cap = graph.pair_capacity
+    Wbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
+    Wdbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
+    call("mlcg_cfconv_gather_rev2", ptr(gagg2),
+         ptr(None if gagg1 is None else gagg1.contiguous()), ptr(y.contiguous()),
+         ptr(None if ydot is None else ydot.contiguous()), ptr(W), ptr(Wd), ptr(ddot),
+         ptr(graph.rowptr), ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes, F,
+         ptr(ybar2), ptr(Wbar), ptr(Wdbar), stream_handle(gagg2.device))
+    return ybar2, Wbar, Wdbar
+
+
+def pair_ddot(pos: torch.Tensor, dist: torch.Tensor, graph: PairGraph,
+              u: torch.Tensor) -> torch.Tensor:
+    cap = graph.pair_capacity
+    ddot = torch.empty(cap, dtype=torch.float32, device=pos.device)
+    call("mlcg_pair_ddot", ptr(pos), ptr(dist), ptr(graph.pair_ij), cap,
+         ptr(graph.n_pairs_dev), cap, ptr(u.contiguous()), ptr(ddot),
+         stream_handle(pos.device))
+    return ddot
+
+
+def pair_forces(pos: torch.Tensor, dist: torch.Tensor, dbar: torch.Tensor,
+                graph: PairGraph, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """F_i = sum_j dbar[p(i,j)] (pos_j - pos_i) / d  (= -dE/dpos_i)."""
+    accumulate = out is not None
+    if out is None:
+        out = torch.empty_like(pos)
+    call("mlcg_pair_forces", ptr(pos), ptr(dist), ptr(dbar), ptr(graph.rowptr),
+         ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes, int(accumulate), ptr(out),
+         stream_handle(pos.device))
+    return out
+
+
+def segment_sum(values: torch.Tensor, frame_ptr: torch.Tensor) -> torch.Tensor:
+    """Per-frame sums of a [N] or [N, 1] float32 vector."""
+    require_device(values)
+    v = values.contiguous().view(-1)
+    nb = frame_ptr.numel() - 1
+    out = torch.empty(nb, dtype=torch.float32, device=values.device)
+    call("mlcg_segment_sum", ptr(v), 1, ptr(frame_ptr), nb, ptr(out),
+         stream_handle(values.device))
+    return out

@@ -1,0 +1,193 @@
+"""Fused HIP SchNet against the CPU oracle (oracle/schnet_ref.py).
+
+Tolerances:
+  energies / forces   rtol 1e-5 (relative to the oracle's norm) and atol 1e-6
+  force-matching grads rtol 1e-4
+The oracle runs in fp64 (the mathematically exact target); the HIP path is
+fp32.  Where the reference's own fp32 arithmetic differs from fp64 by more
+than the tolerance (never at these sizes), the test says so.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import radius as oracle_radius
+from oracle import schnet_ref as R
+from tests.helpers import make_cfg, make_model, max_abs, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _small_batch(n_frames=6, n_beads=14, seed=3):
+    from mlcg_amd import synthetic
+
+    rng = np.random.default_rng(seed)
+    pos = synthetic.self_avoiding_walk(n_frames, n_beads, rng)
+    types = rng.integers(1, 21, size=(n_frames, n_beads))
+    forces = rng.standard_normal((n_frames * n_beads, 3)).astype(np.float32)
+    return synthetic._flatten(pos, types, seed, forces)
+
+
+def _oracle_inputs(b, rc, dtype=torch.float64):
+    ei, _ = oracle_radius.radius_graph(b.pos, rc, b.batch, False, 1000)
+    return (torch.from_numpy(b.pos).to(dtype), torch.from_numpy(b.atom_types),
+            torch.from_numpy(b.batch), torch.from_numpy(ei))
+
+
+def test_filter_kernel_matches_torch():
+    from mlcg_amd import ops, synthetic
+
+    cfg = make_cfg(num_blocks=1, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=11)
+    b = synthetic.config2(n_frames=8)
+    pos = torch.from_numpy(b.pos).cuda()
+    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), with_pairs=True)
+    model = make_model(cfg, sd)
+    spec = model.fused_spec()
+    blk = model.fused_params().blocks[0]
+    W, Wd, dist = ops.filter_fwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2)
+    # fp64 torch reference on the same pairs
+    pij = g.pair_ij.long().cpu()
+    p64 = torch.from_numpy(b.pos).double()
+    d = (p64[pij[1]] - p64[pij[0]]).norm(dim=1).requires_grad_(True)
+    sd64 = R.to_dtype(sd, torch.float64)
+    rbf = R.gaussian_rbf(d, sd64["rbf_layer.offset"], sd64["rbf_layer.coeff"],
+                         R.Cutoff("cosine", 0.0, 20.0))
+    layers = R._layers(sd64, "interaction_blocks.0.conv.filter_network")
+    Wr = R.mlp(rbf, layers, torch.tanh) * R.cosine_cutoff(d, 0.0, 20.0).view(-1, 1)
+    Wdr = torch.stack([torch.autograd.grad(Wr[:, f].sum(), d, retain_graph=True)[0]
+                       for f in range(128)], dim=1)
+    print("W rel", rel_err(W, Wr), "Wd rel", rel_err(Wd, Wdr),
+          "dist", max_abs(dist, d.detach()))
+    assert rel_err(W, Wr.detach()) < 1e-5
+    assert rel_err(Wd, Wdr) < 1e-5
+    assert max_abs(dist, d.detach()) < 1e-5
+
+
+def test_gather_matches_index_add():
+    from mlcg_amd import ops, synthetic
+
+    b = synthetic.config2(n_frames=8)
+    pos = torch.from_numpy(b.pos).cuda()
+    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), with_pairs=True)
+    torch.manual_seed(0)
+    y = torch.randn(pos.shape[0], 128, device="cuda")
+    W = torch.randn(g.num_pairs, 128, device="cuda")
+    out = ops.cfconv_gather(y, W, g)
+    ei = g.edge_index
+    We = W[g.eid2pair.long()]
+    ref = torch.zeros_like(y).index_add_(0, ei[1], y[ei[0]] * We)
+    assert rel_err(out, ref) < 1e-6
+
+
+@pytest.mark.parametrize("act", ["tanh", "ssp"])
+def test_energy_forces_small(act):
+    from mlcg_amd import nn
+
+    cfg = make_cfg(num_blocks=3, rc=12.0, act=act)
+    sd = R.random_state_dict(cfg, seed=5)
+    b = _small_batch()
+    pos64, types, batch, ei = _oracle_inputs(b, 12.0)
+    E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
+                                          batch, ei, b.n_frames)
+    model = make_model(cfg, sd)
+    gm = nn.GradientsOut(model).eval()
+    data = b.to_torch("cuda")
+    data = gm(data)
+    E = data.out["SchNet"]["energy"]
+    F = data.out["SchNet"]["forces"]
+    print(act, "E rel", rel_err(E, E_ref), "F rel", rel_err(F, F_ref), "F abs", max_abs(F, F_ref))
+    assert rel_err(E, E_ref) < 1e-5
+    assert rel_err(F, F_ref) < 1e-5
+    assert torch.allclose(E.double().cpu(), E_ref, rtol=1e-5, atol=1e-6 * float(E_ref.abs().max()))
+
+
+def test_energy_plain_forward_and_autograd_forces():
+    """SchNet.forward + torch.autograd.grad (generic GradientsOut path)."""
+    cfg = make_cfg(num_blocks=2, rc=12.0)
+    sd = R.random_state_dict(cfg, seed=9)
+    b = _small_batch()
+    pos64, types, batch, ei = _oracle_inputs(b, 12.0)
+    E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
+                                          batch, ei, b.n_frames)
+    model = make_model(cfg, sd)
+    data = b.to_torch("cuda")
+    data.pos.requires_grad_(True)
+    data = model(data)
+    E = data.out["SchNet"]["energy"]
+    (g,) = torch.autograd.grad(E.sum(), data.pos)
+    assert rel_err(E, E_ref) < 1e-5
+    assert rel_err(-g, F_ref) < 1e-5
+
+
+def _param_grads(model):
+    return {k: p.grad for k, p in model.named_parameters()}
+
+
+@pytest.mark.parametrize("act", ["tanh", "ssp"])
+def test_force_matching_grads_small(act):
+    from mlcg_amd import nn
+
+    cfg = make_cfg(num_blocks=3, rc=12.0, act=act)
+    sd = R.random_state_dict(cfg, seed=13)
+    b = _small_batch()
+    pos64, types, batch, ei = _oracle_inputs(b, 12.0)
+    fref64 = torch.from_numpy(b.forces).double()
+    loss_ref, _, _, g_ref = R.force_matching_grads(R.to_dtype(sd, torch.float64), cfg, pos64,
+                                                   types, batch, ei, b.n_frames, fref64)
+    model = make_model(cfg, sd)
+    gm = nn.GradientsOut(model).train()
+    data = b.to_torch("cuda")
+    data = gm(data)
+    loss = torch.nn.functional.mse_loss(data.out["SchNet"]["forces"], data.forces)
+    loss.backward()
+    assert abs(float(loss) - float(loss_ref)) <= 1e-5 * abs(float(loss_ref))
+    grads = _param_grads(model)
+    worst = 0.0
+    for k, gr in g_ref.items():
+        got = grads[k]
+        assert got is not None, k
+        e = rel_err(got, gr)
+        worst = max(worst, e)
+        assert e < 1e-4, (k, e)
+    print(act, "worst param-grad rel err", worst)
+
+
+def test_generic_double_backward():
+    """autograd.grad(E, pos, create_graph=True) then a force loss backward
+    through the fused Energy/EnergyGrad functions."""
+    cfg = make_cfg(num_blocks=2, rc=12.0)
+    sd = R.random_state_dict(cfg, seed=17)
+    b = _small_batch()
+    pos64, types, batch, ei = _oracle_inputs(b, 12.0)
+    fref64 = torch.from_numpy(b.forces).double()
+    _, _, _, g_ref = R.force_matching_grads(R.to_dtype(sd, torch.float64), cfg, pos64, types,
+                                            batch, ei, b.n_frames, fref64)
+    model = make_model(cfg, sd)
+    data = b.to_torch("cuda")
+    data.pos.requires_grad_(True)
+    data = model(data)
+    E = data.out["SchNet"]["energy"]
+    (g,) = torch.autograd.grad(E.sum(), data.pos, create_graph=True)
+    loss = torch.nn.functional.mse_loss(-g, data.forces)
+    loss.backward()
+    grads = _param_grads(model)
+    for k, gr in g_ref.items():
+        assert rel_err(grads[k], gr) < 1e-4, k
+
+
+def test_config1_cpu_reference_case():
+    """Config 1 (1 block, SSP, 30 A) energies and forces."""
+    from mlcg_amd import nn, synthetic
+
+    cfg = make_cfg(num_blocks=1, rc=30.0, act="ssp")
+    sd = R.random_state_dict(cfg, seed=synthetic.seed_for(1))
+    b = synthetic.config1()
+    pos64, types, batch, ei = _oracle_inputs(b, 30.0)
+    E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
+                                          batch, ei, b.n_frames)
+    model = make_model(cfg, sd)
+    data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
+    assert rel_err(data.out["SchNet"]["energy"], E_ref) < 1e-5
+    assert rel_err(data.out["SchNet"]["forces"], F_ref) < 1e-5
