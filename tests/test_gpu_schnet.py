@@ -42,7 +42,8 @@ def test_filter_kernel_matches_torch():
     sd = R.random_state_dict(cfg, seed=11)
     b = synthetic.config2(n_frames=8)
     pos = torch.from_numpy(b.pos).cuda()
-    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), with_pairs=True)
+    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), max_num_neighbors=1000,
+                         with_pairs=True)
     model = make_model(cfg, sd)
     spec = model.fused_spec()
     blk = model.fused_params().blocks[0]
@@ -70,7 +71,8 @@ def test_gather_matches_index_add():
 
     b = synthetic.config2(n_frames=8)
     pos = torch.from_numpy(b.pos).cuda()
-    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), with_pairs=True)
+    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).cuda(), max_num_neighbors=1000,
+                         with_pairs=True)
     torch.manual_seed(0)
     y = torch.randn(pos.shape[0], 128, device="cuda")
     W = torch.randn(g.num_pairs, 128, device="cuda")
