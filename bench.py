@@ -1,0 +1,373 @@
+#!/usr/bin/env python
+"""Benchmark of the SchNet CFConv hot path on one MI355X.
+
+Workload: full SchNet CG model -- embedding 128, three
+interaction blocks, 50 Gaussian RBF on 0-20 A with a cosine envelope, cosine
+cutoff 20 A, output MLP 128 -> 64 -> 1, Tanh -- on 512 frames of a 35-bead
+self-avoiding chain, synthetic and seeded (``mlcg_amd.synthetic.config2``),
+random-init weights.  One step is the reference's force-matching training
+step (mlcg/pl/model.py:113-131 plus Lightning's backward and AdamW step):
+
+    radius graph -> energies -> forces (create_graph) -> ForceMSE ->
+    double backward to every parameter -> AdamW.step()
+
+Metric: CFConv edges/s := E_directed * n_blocks / t_step (forward + force +
+double backward of every block per step), with the inputs resident in HBM.
+
+Besides the JSON contract fields the line carries
+  roofline      -- the dominant HIP kernel (by device time over the timed
+                   steps, launches bracketed by HIP events on the launch
+                   stream): algorithmic bytes or FLOPs per launch / average
+                   launch time, against the MI355X peak;
+  kernels       -- the same figures for every HIP kernel of the step;
+  radius_graph  -- config 3 (2048 x 100-bead globules, 15 A): edges/s of the
+                   HIP radius graph, inputs resident;
+  cpu_baseline  -- the CPU restatement (oracle/schnet_ref.py) of the same
+                   step on a bounded sample of frames, host threads stated.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix
+
+K_RBF = 50
+F = 128
+H = 128
+N_BLOCKS = 3
+RC = 20.0
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--frames", type=int, default=512, help="config-2 frames per step")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-radius", action="store_true", help="skip the config-3 radius leg")
+    p.add_argument("--cpu-frames", type=int, default=32,
+                   help="frames in the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="approximate CPU time budget of the baseline leg")
+    p.add_argument("--calib-copy-mib", type=int, default=0,
+                   help="run one device-to-device copy of this many MiB first (a "
+                        "known-size reference dispatch for HBM byte counters)")
+    return p.parse_args(argv)
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work per launch of each HIP entry point
+
+def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = False):
+    """(bound, amount, unit) per launch: bytes for HBM-bound kernels, FLOPs
+    for the MFMA filter kernels.  Minimum work only: K is not padded,
+    recomputation is not counted, W is read once per unordered pair."""
+    sw = 2 if f16 else 4
+    kf_ff = K_RBF * F + F * F
+    if name == "mlcg_filter_fwd":
+        # value and distance-tangent through both linears
+        return "mfma", 2 * 2 * kf_ff * P, "flop"
+    if name == "mlcg_filter_bwd":
+        # two reverse products through W2^T (the forward recomputation is
+        # not algorithmic work)
+        return "mfma", 2 * 2 * F * F * P, "flop"
+    if name == "mlcg_cfconv_gather":
+        return "hbm", sw * F * P + 4 * E + 4 * (N + 1) + 2 * 4 * F * N, "byte"
+    if name == "mlcg_cfconv_gather_bwd":
+        # W and Wd read, dbar RMW per pair, gagg and y in, ybar out
+        return "hbm", 2 * sw * F * P + 8 * P + 4 * E + 4 * (N + 1) + 3 * 4 * F * N, "byte"
+    if name == "mlcg_cfconv_gather_tangent":
+        # W, Wd, ddot per pair; ydot, y in, out
+        return "hbm", 2 * sw * F * P + 4 * P + 4 * E + 4 * (N + 1) + 3 * 4 * F * N, "byte"
+    if name == "mlcg_cfconv_gather_rev2":
+        # W, Wd, ddot in, Wbar, Wdbar out per pair; gagg2, gagg1, y, ydot in,
+        # ybar2 out
+        return "hbm", 4 * sw * F * P + 4 * P + 4 * E + 4 * (N + 1) + 5 * 4 * F * N, "byte"
+    if name == "mlcg_radius_count":
+        return "hbm", 12 * N + 8 * N + 8 * (B + 1) + 8 * N, "byte"
+    if name == "mlcg_radius_fill":
+        return "hbm", 12 * N + 8 * N + 8 * (B + 1) + 8 * N + 16 * E + 4 * E + 8 * P + 4 * P, "byte"
+    if name == "mlcg_pair_forces":
+        return "hbm", 12 * N + 8 * P + 8 * E + 4 * (N + 1) + 12 * N, "byte"
+    if name == "mlcg_pair_ddot":
+        return "hbm", 8 * P + 4 * P + 24 * N + 4 * P, "byte"
+    if name == "mlcg_pair_reverse_map":
+        return "hbm", 8 * P + 4 * P + 4 * (N + 1), "byte"
+    return None
+
+
+# entry point -> kernel symbol(s) it launches (as rocprofv3 names them)
+KERNEL_SYMBOL = {
+    "mlcg_filter_fwd": "filter_fwd_f32_kernel",
+    "mlcg_filter_bwd": "filter_bwd_f32_kernel",
+    "mlcg_cfconv_gather": "gather_kernel",
+    "mlcg_cfconv_gather_bwd": "gather_bwd_kernel",
+    "mlcg_cfconv_gather_tangent": "gather_tangent_kernel",
+    "mlcg_cfconv_gather_rev2": "gather_rev2_kernel",
+    "mlcg_radius_count": "radius_count_kernel",
+    "mlcg_radius_fill": "radius_fill_kernel",
+    "mlcg_pair_forces": "pair_forces_kernel",
+    "mlcg_pair_ddot": "pair_ddot_kernel",
+    "mlcg_pair_reverse_map": "pair_reverse_kernel",
+}
+
+
+def kernel_report(summary, E, P, N, B):
+    rows = {}
+    for name, (launches, total_ms) in summary.items():
+        w = algorithmic_work(name, E, P, N, B)
+        avg_ms = total_ms / max(launches, 1)
+        row = {"kernel": KERNEL_SYMBOL.get(name, name), "launches": launches,
+               "avg_us": round(avg_ms * 1e3, 3), "total_ms": round(total_ms, 4)}
+        if w is not None:
+            bound, amount, unit = w
+            if bound == "hbm":
+                ach = amount / (avg_ms * 1e-3) / 1e9
+                row.update(bound="hbm", achieved=round(ach, 2), peak=HBM_PEAK_GBS,
+                           unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
+                           algorithmic_bytes=int(amount))
+            else:
+                ach = amount / (avg_ms * 1e-3) / 1e12
+                row.update(bound="mfma", achieved=round(ach, 3),
+                           peak=FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s",
+                           frac=round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+                           algorithmic_flops=int(amount))
+        rows[name] = row
+    return rows
+
+
+def load_traffic(kernel_symbol: str):
+    """HBM bytes per launch of `kernel_symbol` from the committed rocprofv3
+    counter summary (profiles/traffic_config2.txt: lines
+    `<kernel> <bytes_per_launch>`), or None when absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_config2.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        for line in fh:
+            parts = line.split()
+            if len(parts) >= 2 and parts[0] == kernel_symbol and not line.startswith("#"):
+                try:
+                    return int(float(parts[1]))
+                except ValueError:
+                    return None
+    return None
+
+
+# ---------------------------------------------------------------------------
+
+def build_model(torch, nn, device):
+    act = torch.nn.Tanh()
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, RC), num_rbf=K_RBF)
+    model = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, RC), [64], hidden_channels=H,
+                              embedding_size=100, num_filters=F,
+                              num_interactions=N_BLOCKS, activation=act,
+                              max_num_neighbors=1000)
+    return model.to(device)
+
+
+def gpu_leg(args):
+    import torch
+
+    from mlcg_amd import _lib, nn, ops, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(synthetic.seed_for(2))
+    model = build_model(torch, nn, dev)
+    gm = nn.GradientsOut(model).train()
+    loss_fn = nn.ForceMSE()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0)
+    b = synthetic.config2(n_frames=args.frames)
+    data = b.to_torch(dev)
+    graph = model.build_graph(data)
+    E, P, N, B = graph.num_edges, graph.num_pairs, graph.num_nodes, b.n_frames
+    del graph
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        out = gm(data)
+        out.out.update(**out.out[model.name])
+        loss = loss_fn(out)
+        loss.backward()
+        opt.step()
+        return loss
+
+    # warm-up, with every HIP entry point bracketed to find the dominant one
+    timer = _lib.LaunchTimer(None)
+    _lib.set_timer(timer)
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    _lib.set_timer(None)
+    warm = kernel_report(timer.summary(), E, P, N, B)
+    per_step = {k: v["total_ms"] / max(args.warmup, 1) for k, v in warm.items()}
+    dominant = max(per_step, key=per_step.get)
+
+    # timed region: only the dominant kernel's launches are bracketed
+    timer = _lib.LaunchTimer({dominant})
+    _lib.set_timer(timer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.set_timer(None)
+    ms = (t1 - t0) * 1e3 / args.steps
+    assert math.isfinite(float(loss)), "non-finite loss"
+    dom = kernel_report(timer.summary(), E, P, N, B)[dominant]
+    return {"ms_per_step": ms, "E": E, "P": P, "N": N, "B": B, "dominant": dominant,
+            "dominant_row": dom, "kernels": warm, "loss": float(loss),
+            "step_kernel_ms": round(sum(per_step.values()), 4)}
+
+
+def radius_leg(reps=10):
+    import torch
+
+    from mlcg_amd import ops, synthetic
+
+    b = synthetic.config3()
+    pos = torch.from_numpy(b.pos).cuda()
+    batch = torch.from_numpy(b.batch).cuda()
+    nf = b.n_frames
+    fptr = ops.frame_ptr_from_batch(batch, nf)
+    for _ in range(2):
+        g = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr)
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        g = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr)
+        torch.cuda.synchronize()
+        t.append(time.perf_counter() - t0)
+    s = statistics.median(t)
+    E = g.num_edges
+    return {"workload": "config3: 2048 frames x 100-bead globules, rc 15 A, no loops, "
+                        "int64 [2,E] canonical order",
+            "E": E, "ms": round(s * 1e3, 4), "edges_per_s": E / s,
+            "algorithmic_bytes": 12 * pos.shape[0] + 8 * (nf + 1) + 16 * E}
+
+
+def cpu_leg(args):
+    """The CPU restatement of the same step on a bounded sample of frames."""
+    import torch
+
+    from mlcg_amd import synthetic
+    from oracle import radius as oracle_radius
+    from oracle import schnet_ref as R
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    torch.set_float32_matmul_precision("highest")
+    cfg = R.SchNetConfig(num_rbf=K_RBF, rbf_lo=0.0, rbf_hi=RC, rbf_cut="cosine",
+                         conv_cut="cosine", conv_lo=0.0, conv_hi=RC, act="tanh",
+                         num_blocks=N_BLOCKS)
+    sd = R.random_state_dict(cfg, seed=synthetic.seed_for(2))
+    b = synthetic.config2(n_frames=args.cpu_frames)
+    pos = torch.from_numpy(b.pos)
+    types = torch.from_numpy(b.atom_types)
+    batch = torch.from_numpy(b.batch)
+    fref = torch.from_numpy(b.forces)
+
+    def one():
+        ei, _ = oracle_radius.radius_graph(b.pos, RC, b.batch, False, 1000)
+        ei = torch.from_numpy(ei)
+        R.force_matching_grads(sd, cfg, pos, types, batch, ei, b.n_frames, fref)
+        return ei.shape[1]
+
+    E = one()  # warm-up
+    t = []
+    t_start = time.perf_counter()
+    while len(t) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(t) < 50):
+        t0 = time.perf_counter()
+        one()
+        t.append(time.perf_counter() - t0)
+    s = statistics.median(t)
+    return {"value": E * N_BLOCKS / s, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"{args.cpu_frames} frames of the config-2 workload (E={E}), "
+                      f"oracle/schnet_ref.py fp32 force-matching step incl. brute-force "
+                      f"radius graph, median of {len(t)} reps, torch threads={cores}",
+            "ms_per_step": round(s * 1e3, 3)}
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; frames shard across GPUs with no exchange, see DESIGN.md",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    if args.calib_copy_mib > 0:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    g = gpu_leg(args)
+    print(f"[bench] gpu leg done: {g['ms_per_step']:.3f} ms/step, E={g['E']}", flush=True)
+    rg = None if args.no_radius else radius_leg()
+    if rg:
+        print(f"[bench] radius leg done: {rg['ms']:.3f} ms", flush=True)
+    cpu = None if args.no_cpu else cpu_leg(args)
+    if cpu:
+        print(f"[bench] cpu leg done: {cpu['ms_per_step']:.1f} ms/step", flush=True)
+
+    ms = g["ms_per_step"]
+    value = g["E"] * N_BLOCKS / (ms * 1e-3)
+    dom = g["dominant_row"]
+    sym = dom["kernel"]
+    roofline = {"bound": dom.get("bound"), "achieved": dom.get("achieved"),
+                "peak": dom.get("peak"), "unit": dom.get("unit"), "frac": dom.get("frac"),
+                "traffic": load_traffic(sym), "kernel": sym,
+                "avg_launch_us": dom["avg_us"], "launches": dom["launches"]}
+    line = {
+        "metric": "CFConv fwd+force+double-bwd edges/s",
+        "value": value,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded self-avoiding CG chains, random-init weights)",
+        "config": {"workload": "config2: SchNet force-matching step (radius graph, energy, "
+                               "forces, double backward, AdamW), 512 frames x 35 beads, "
+                               "H=F=128, 3 blocks, 50 RBF, rc 20 A",
+                   "frames": g["B"], "beads_per_frame": g["N"] // max(g["B"], 1),
+                   "edges": g["E"], "pairs": g["P"], "blocks": N_BLOCKS},
+        "frames_per_s": g["B"] / (ms * 1e-3),
+        "roofline": roofline,
+        "kernels": g["kernels"],
+        "step_kernel_ms": g["step_kernel_ms"],
+        "radius_graph": rg,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -100,10 +100,53 @@ def available() -> bool:
         return False
 
 
+class LaunchTimer:
+    """Brackets launches of selected entry points with HIP events recorded on
+    torch's current stream (the stream every wrapper launches on), so the
+    device time of each launch can be read after a synchronisation.
+
+    ``watch`` is a set of entry-point names, or None for every entry point.
+    """
+
+    def __init__(self, watch=None):
+        self.watch = None if watch is None else set(watch)
+        self.events = {}
+
+    def wants(self, name: str) -> bool:
+        return self.watch is None or name in self.watch
+
+    def record(self, name: str):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        self.events.setdefault(name, []).append((start, end))
+        return start, end
+
+    def summary(self):
+        """{name: (launches, total_ms)} -- call after torch.cuda.synchronize()."""
+        return {k: (len(v), sum(s.elapsed_time(e) for s, e in v))
+                for k, v in self.events.items()}
+
+
+_timer: Optional[LaunchTimer] = None
+
+
+def set_timer(timer: Optional[LaunchTimer]) -> Optional[LaunchTimer]:
+    """Install (or with None remove) the launch timer; returns the old one."""
+    global _timer
+    old, _timer = _timer, timer
+    return old
+
+
 def call(name: str, *args) -> None:
     """Call an entry point and raise RuntimeError on a non-zero status."""
     fn = getattr(load(), name)
-    status = fn(*args)
+    if _timer is not None and _timer.wants(name):
+        start, end = _timer.record(name)
+        start.record()
+        status = fn(*args)
+        end.record()
+    else:
+        status = fn(*args)
     if status != 0:
         raise RuntimeError(
             f"{name} failed with {STATUS.get(status, status)}"

@@ -279,10 +279,10 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
         if tangent_on:
             zdotbar = hdotbar * d1
             zbar2 = zbar2 + hdotbar * d2 * st.ozdot[k]
-            g_out_w[k] = zdotbar.t().mm(st.ohdot[k]) + zbar2.t().mm(st.oh[k])
+            g_out_w[k] = ops.tmm(zdotbar, st.ohdot[k]) + ops.tmm(zbar2, st.oh[k])
             hdotbar = zdotbar.mm(P.out_w[k])
         else:
-            g_out_w[k] = zbar2.t().mm(st.oh[k])
+            g_out_w[k] = ops.tmm(zbar2, st.oh[k])
         g_out_b[k] = zbar2.sum(0)
         hbar2 = zbar2.mm(P.out_w[k])
     xbar2 = hbar2
@@ -291,24 +291,24 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
         bp = P.blocks[k]
         sbar2 = xbar2.mm(bp.A3)
         d1, d2 = act_derivs(st.z[k], st.s[k], spec.block_act)
-        gA3 = xbar2.t().mm(st.s[k])
+        gA3 = ops.tmm(xbar2, st.s[k])
         zbar2 = sbar2 * d1
         if tangent_on:
-            gA3 = gA3 + st.xbar_out[k].t().mm(st.sdot[k])
+            gA3 = gA3 + ops.tmm(st.xbar_out[k], st.sdot[k])
             zbar2 = zbar2 + st.sbar1[k] * d2 * st.zdot[k]
         gc3 = xbar2.sum(0)
         gagg2 = zbar2.mm(bp.A2)
-        gA2 = zbar2.t().mm(st.agg[k])
+        gA2 = ops.tmm(zbar2, st.agg[k])
         if tangent_on:
-            gA2 = gA2 + st.zbar1[k].t().mm(st.aggdot[k])
+            gA2 = gA2 + ops.tmm(st.zbar1[k], st.aggdot[k])
         gc2 = zbar2.sum(0)
         ybar2, Wbar, Wdbar = ops.cfconv_gather_rev2(
             gagg2, st.gagg1[k] if tangent_on else None, st.y[k],
             st.ydot[k] if tangent_on else None, st.W[k], st.Wd[k],
             st.ddot if tangent_on else None, graph)
-        gA1 = ybar2.t().mm(st.x[k])
+        gA1 = ops.tmm(ybar2, st.x[k])
         if tangent_on and st.xdot_in[k] is not None:
-            gA1 = gA1 + st.ybar1[k].t().mm(st.xdot_in[k])
+            gA1 = gA1 + ops.tmm(st.ybar1[k], st.xdot_in[k])
         xbar2 = xbar2 + ybar2.mm(bp.A1)
         gW1, gb1, gW2 = ops.filter_bwd(st.pos, graph, spec.filt, bp.W1, bp.b1, bp.W2, Wbar,
                                        Wdbar)

@@ -160,6 +160,31 @@ def radius_graph(
 
 
 # --------------------------------------------------------------------------
+# Reductions over long row dimensions
+
+SPLIT_ROWS = 4096  # rows per slice of the split-K products below
+
+
+def tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T b for a [R, M], b [R, N] with R >> M, N (weight gradients summed
+    over pairs or nodes).  The row dimension is cut into fixed slices whose
+    products run as one batched GEMM and are then summed in slice order, so
+    the result is deterministic and the library GEMM sees a well-shaped
+    problem instead of a single M x N tile with an enormous K."""
+    R = a.shape[0]
+    S = R // SPLIT_ROWS
+    if S < 2:
+        return a.t().mm(b)
+    m = S * SPLIT_ROWS
+    av = a[:m].reshape(S, SPLIT_ROWS, a.shape[1])
+    bv = b[:m].reshape(S, SPLIT_ROWS, b.shape[1])
+    out = torch.bmm(av.transpose(1, 2), bv).sum(0)
+    if m < R:
+        out = out + a[m:].t().mm(b[m:])
+    return out
+
+
+# --------------------------------------------------------------------------
 # Filter network
 
 @dataclass
@@ -222,8 +247,8 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
          ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(H), ptr(T), ptr(A),
          ptr(G), stream_handle(dev))
     # pair reductions as library GEMMs: [F, 2P] x [2P, F]
-    dW2 = T.view(2 * cap, F).t().mm(H.view(2 * cap, F))
-    dW1 = A.view(2 * cap, F).t().mm(G.view(2 * cap, Kp))[:, :K]
+    dW2 = tmm(T.view(2 * cap, F), H.view(2 * cap, F))
+    dW1 = tmm(A.view(2 * cap, F), G.view(2 * cap, Kp))[:, :K]
     db1 = A[0].sum(0)
     return dW1.contiguous(), db1, dW2
 

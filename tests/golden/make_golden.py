@@ -1,0 +1,89 @@
+"""Writes the small golden fixtures under tests/golden/ (run from the repo
+root: ``python tests/golden/make_golden.py``).
+
+radius_small.npz  8 frames x 100-bead compact globules (config-3 generator,
+                  Rg ~ 12 A), cutoff 15 A, no loops: positions, batch and the
+                  canonical edge_index of the C oracle.  Before writing, the
+                  edge set is checked against per-frame scipy cKDTree
+                  queries (the reference's radius oracle,
+                  src/opt_radius/mlcg_opt_radius/utils.py:32-47) away from the
+                  cutoff boundary.
+schnet_small.pt   3 frames x 9-bead self-avoiding chains, SchNet with 2
+                  blocks, hidden 16, 128 filters, 16 RBF on 0-9 A, cosine
+                  envelopes, tanh, output MLP 16 -> 8 -> 1: the fp64
+                  oracle's energies, forces, force-matching loss and every
+                  parameter gradient, plus the state_dict and edge list.  Saved
+                  with torch.save of plain tensors (loadable with
+                  weights_only=True).
+"""
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from mlcg_amd import synthetic  # noqa: E402
+from oracle import radius as oracle_radius  # noqa: E402
+from oracle import schnet_ref as R  # noqa: E402
+
+
+def radius_small():
+    rng = np.random.default_rng(20263)
+    pos3 = synthetic.globule(8, 100, 26.0, rng)
+    b = synthetic._flatten(pos3, np.ones((8, 100), np.int64), 20263)
+    ei, ovf = oracle_radius.radius_graph(b.pos, 15.0, b.batch, False, 1000)
+    assert ovf == 0
+    from scipy.spatial import cKDTree
+
+    got = set(map(tuple, ei.T.tolist()))
+    for f in range(8):
+        idx = np.arange(100 * f, 100 * f + 100)
+        p = b.pos[idx].astype(np.float64)
+        tree = cKDTree(p)
+        for a, hits in enumerate(tree.query_ball_point(p, 15.0 + 1e-4)):
+            for h in hits:
+                if h == a:
+                    continue
+                d = np.linalg.norm(p[h] - p[a])
+                if abs(d - 15.0) > 1e-4:
+                    assert ((idx[a], idx[h]) in got) == (d < 15.0)
+    np.savez_compressed(os.path.join(HERE, "radius_small.npz"), pos=b.pos, batch=b.batch,
+                        r=np.float64(15.0), edge_index=ei)
+    print("radius_small.npz: E =", ei.shape[1])
+
+
+def schnet_small():
+    rng = np.random.default_rng(20262)
+    pos3 = synthetic.self_avoiding_walk(3, 9, rng)
+    types = rng.integers(1, 21, size=(3, 9))
+    b = synthetic._flatten(pos3, types, 20262)
+    cfg = dict(num_rbf=16, rbf_lo=0.0, rbf_hi=9.0, rbf_cut="cosine", conv_cut="cosine",
+               conv_lo=0.0, conv_hi=9.0, act="tanh", num_blocks=2)
+    c = R.SchNetConfig(**cfg)
+    sd = R.to_dtype(R.random_state_dict(c, hidden=16, embedding_size=24, out_widths=(8,),
+                                        seed=20262, bias_scale=0.2),
+                    torch.float64)
+    ei, _ = oracle_radius.radius_graph(b.pos, 9.0, b.batch, False, 1000)
+    ei = torch.from_numpy(ei)
+    pos = torch.from_numpy(b.pos).double()
+    tt = torch.from_numpy(b.atom_types)
+    bb = torch.from_numpy(b.batch)
+    fref = torch.from_numpy(rng.standard_normal((27, 3)))
+    E, F = R.schnet_energy_forces(sd, c, pos, tt, bb, ei, 3)
+    loss, _, _, grads = R.force_matching_grads(sd, c, pos, tt, bb, ei, 3, fref)
+    torch.save({"cfg": cfg, "state_dict": sd, "pos": pos, "types": tt, "batch": bb,
+                "edge_index": ei, "n_frames": torch.tensor(3), "energy": E.detach(),
+                "forces": F.detach(), "forces_ref": fref, "loss": loss,
+                "grads": {k: v.detach() for k, v in grads.items()}},
+               os.path.join(HERE, "schnet_small.pt"))
+    print("schnet_small.pt: E =", ei.shape[1], "loss", float(loss))
+
+
+if __name__ == "__main__":
+    radius_small()
+    schnet_small()

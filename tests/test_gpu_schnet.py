@@ -193,3 +193,41 @@ def test_config1_cpu_reference_case():
     data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
     assert rel_err(data.out["SchNet"]["energy"], E_ref) < 1e-5
     assert rel_err(data.out["SchNet"]["forces"], F_ref) < 1e-5
+
+
+def test_golden_fixture_hip():
+    """HIP path against the committed fp64 oracle fixture (hidden 16, 16 RBF,
+    2 blocks; tests/golden/make_golden.py): energies, forces and every
+    force-matching parameter gradient."""
+    import os
+
+    from mlcg_amd import nn
+
+    g = torch.load(os.path.join(os.path.dirname(__file__), "golden", "schnet_small.pt"),
+                   weights_only=True)
+    cfg = R.SchNetConfig(**g["cfg"])
+    sd = {k: v.float() for k, v in g["state_dict"].items()}
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, cfg.rbf_hi), num_rbf=cfg.num_rbf)
+    model = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, cfg.conv_hi), [8], hidden_channels=16,
+                              embedding_size=sd["embedding_layer.weight"].shape[0],
+                              num_filters=128, num_interactions=cfg.num_blocks,
+                              activation=torch.nn.Tanh())
+    model.load_state_dict(sd)
+    model = model.cuda()
+    from mlcg_amd.data import AtomicData
+
+    n_frames = int(g["n_frames"])
+    data = AtomicData(pos=g["pos"].float().cuda(), atom_types=g["types"].cuda(),
+                      batch=g["batch"].cuda(),
+                      n_atoms=torch.bincount(g["batch"], minlength=n_frames).cuda(),
+                      forces=g["forces_ref"].float().cuda())
+    gm = nn.GradientsOut(model).train()
+    data = gm(data)
+    E, F = data.out["SchNet"]["energy"], data.out["SchNet"]["forces"]
+    assert rel_err(E, g["energy"]) < 1e-5
+    assert rel_err(F, g["forces"]) < 1e-5
+    loss = torch.nn.functional.mse_loss(F, data.forces)
+    loss.backward()
+    assert abs(float(loss) - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
+    for k, p in model.named_parameters():
+        assert rel_err(p.grad, g["grads"][k]) < 1e-4, k

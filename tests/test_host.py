@@ -1,0 +1,183 @@
+"""Host-side logic that needs no GPU: the C-ABI library loads and exports
+every entry point declared in include/mlcg_hip.h, the Python wrappers refuse
+CPU tensors loudly, the module API keeps the reference's constructor
+behaviour and state_dict layout, and AtomicData collation follows the
+reference's increment rules."""
+
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    names = []
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[\w\*\s]+?\b(mlcg_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    from mlcg_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), name
+    # and the Python binding binds exactly the declared set
+    assert sorted(_lib.exported_symbols()) == declared
+    assert "gfx950" in _lib.version()
+
+
+def test_library_symbols_in_dynamic_table():
+    so = os.path.join(ROOT, "mlcg_amd", "libmlcg_hip.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (mlcg_\w+)", out))
+    assert set(_declared_symbols()) <= exported
+
+
+def test_wrappers_refuse_cpu_tensors():
+    from mlcg_amd import ops
+
+    pos = torch.zeros(4, 3)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.radius_graph(pos, 1.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.frame_ptr_from_batch(torch.zeros(4, dtype=torch.long), 1)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.segment_sum(torch.zeros(4), torch.tensor([0, 4]))
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from mlcg_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    assert not _lib.available()
+    with pytest.raises(RuntimeError, match="not found"):
+        _lib.call("mlcg_version")
+
+
+def test_model_forward_refuses_cpu():
+    from mlcg_amd import nn, synthetic
+
+    m = _config2_model(nn)
+    data = synthetic.config2(n_frames=2).to_torch("cpu")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nn.GradientsOut(m)(data)
+
+
+def _config2_model(nn, act=None):
+    act = act or torch.nn.Tanh()
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0, 20), num_rbf=50)
+    return nn.StandardSchNet(rbf, nn.CosineCutoff(0, 20), [64], 128, 100, 128, 3, act)
+
+
+def test_state_dict_contract():
+    """Keys and shapes of StandardSchNet (config 2) follow the reference's
+    module tree (schnet.py:86-105,219-221,295-298, mlp.py:49)."""
+    from mlcg_amd import nn
+
+    sd = _config2_model(nn).state_dict()
+    want = {"embedding_layer.weight": (100, 128), "rbf_layer.offset": (50,),
+            "rbf_layer.coeff": (), "output_network.layers.0.weight": (64, 128),
+            "output_network.layers.0.bias": (64,), "output_network.layers.2.weight": (1, 64)}
+    for b in range(3):
+        p = f"interaction_blocks.{b}"
+        want.update({f"{p}.conv.lin1.weight": (128, 128), f"{p}.conv.lin2.weight": (128, 128),
+                     f"{p}.conv.lin2.bias": (128,),
+                     f"{p}.conv.filter_network.layers.0.weight": (128, 50),
+                     f"{p}.conv.filter_network.layers.0.bias": (128,),
+                     f"{p}.conv.filter_network.layers.2.weight": (128, 128),
+                     f"{p}.lin.weight": (128, 128), f"{p}.lin.bias": (128,)})
+    assert {k: tuple(v.shape) for k, v in sd.items()} == want
+    m = _config2_model(nn)
+    assert sum(p.numel() for p in m.parameters()) == 238_080
+    g = nn.GradientsOut(m)
+    assert all(k.startswith("model.") for k in g.state_dict())
+
+
+def test_standard_schnet_checks():
+    from mlcg_amd import nn
+
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0, 20), num_rbf=50)
+    with pytest.raises(ValueError):
+        nn.StandardSchNet(rbf, nn.CosineCutoff(0, 20), [64], num_interactions=0)
+    with pytest.warns(UserWarning):
+        nn.StandardSchNet(rbf, nn.CosineCutoff(0, 15), [64], num_interactions=1)
+    with pytest.raises(NotImplementedError):
+        nn.SchNet(torch.nn.Embedding(10, 128), [], rbf, nn.MLP([128, 1]),
+                  self_interaction=True)
+
+
+@pytest.mark.parametrize("cls", ["IdentityCutoff", "CosineCutoff"])
+def test_cutoff_bounds_raise(cls):
+    from mlcg_amd import nn
+
+    with pytest.raises(ValueError):
+        getattr(nn, cls)(cutoff_lower=10, cutoff_upper=0)
+
+
+def test_gaussian_float_cutoff_defaults_to_identity():
+    """tests/unit/nn/radial_basis/test_radial_basis.py:30-44."""
+    from mlcg_amd import nn
+
+    basis = nn.GaussianBasis(cutoff=10)
+    assert isinstance(basis.cutoff, nn.IdentityCutoff)
+    assert basis.cutoff.cutoff_lower == 0 and basis.cutoff.cutoff_upper == 10
+
+
+def test_fused_spec_recognises_config2():
+    from mlcg_amd import nn
+
+    m = _config2_model(nn)
+    spec = m.fused_spec()
+    assert spec is not None and spec.num_blocks == 3 and spec.filt.num_rbf == 50
+    m2 = _config2_model(nn, act=torch.nn.ReLU())
+    assert m2.fused_spec() is None  # no kernel for ReLU: module-by-module path
+
+
+def test_collate_increments_index_keys():
+    from mlcg_amd.data import AtomicData
+    from mlcg_amd.data.atomic_data import collate
+
+    frames = []
+    for n in (3, 4):
+        nl = {"bonds": {"index_mapping": torch.tensor([[0, 1], [1, 2]]), "order": 2}}
+        frames.append(AtomicData.from_points(torch.zeros(n, 3), torch.arange(n),
+                                             neighborlist=nl))
+    b = collate(frames)
+    assert b.batch.tolist() == [0, 0, 0, 1, 1, 1, 1]
+    assert b.neighbor_list["bonds"]["index_mapping"].tolist() == [[0, 1, 3, 4], [1, 2, 4, 5]]
+    assert b.neighbor_list["bonds"]["mapping_batch"].tolist() == [0, 0, 1, 1]
+    assert b.n_atoms.tolist() == [3, 4]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+
+
+def test_bench_algorithmic_work_formulas():
+    """Per-launch algorithmic figures used by bench.py's roofline."""
+    sys.path.insert(0, ROOT)
+    import bench
+
+    E, P, N, B = 1000, 500, 100, 4
+    bound, flops, _ = bench.algorithmic_work("mlcg_filter_fwd", E, P, N, B)
+    assert bound == "mfma" and flops == 2 * 2 * (50 * 128 + 128 * 128) * P
+    bound, byts, _ = bench.algorithmic_work("mlcg_cfconv_gather", E, P, N, B)
+    assert bound == "hbm" and byts == 4 * 128 * P + 4 * E + 4 * (N + 1) + 8 * 128 * N

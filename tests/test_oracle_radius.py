@@ -1,0 +1,149 @@
+"""Pins the C radius-graph oracle (oracle/radius_ref.c) without a GPU.
+
+What pins it:
+  * the reference's own radius test sweep (src/opt_radius/mlcg_opt_radius/
+    test_radius.py:31-104: N in {0, 10, 100}, two coordinate ranges,
+    r in {0, 1, 10}, 1-3 frames, loop on/off) against
+    scipy.spatial.cKDTree.query_ball_point -- the reference's kd-tree oracle
+    (utils.py:32-47) -- as set equality, with pairs within 1e-4 A of the
+    cutoff excluded from the comparison (the kd-tree works in float64);
+  * exact boundary cases: d2 == fl32(r^2) is outside (strict `<`,
+    radius.cu:134), one float ulp closer is inside, and an off-axis pair whose
+    fp32 d2 rounds onto the boundary;
+  * the max_num_neighbors cap keeps the lowest-index neighbours
+    (radius.cu:125-141), checked against a sort of the kd-tree hits;
+  * the canonical order (rows ascending, neighbours ascending), frames never
+    mixed, no self loops unless asked.
+"""
+
+import math
+from itertools import product
+
+import numpy as np
+import pytest
+from scipy.spatial import cKDTree
+
+from oracle import radius as oracle_radius
+
+X = [0, 10, 100]
+X_RANGE = [(-1.0, 1.0), (-10.0, -20.0)]
+R = [0.0, 1.0, 10.0]
+BATCH_SIZES = [(100,), (50, 100), (10, 20, 100)]
+LOOP = [True, False]
+
+
+def _batch(n, split):
+    out, p = [], 0
+    for i, b in enumerate(split):
+        k = math.ceil(n * (b / 100)) - p
+        out.append(np.full(k, i, dtype=np.int64))
+        p += k
+    return np.concatenate(out) if out else np.zeros(0, np.int64)
+
+
+def _kdtree_pairs(pos, r, batch, loop):
+    """Set of (i, j) from per-frame kd-trees, plus the set of pairs whose
+    float64 distance is within 1e-4 of r (ambiguous for the fp32 test)."""
+    pairs, near = set(), set()
+    pos64 = pos.astype(np.float64)
+    for b in np.unique(batch):
+        idx = np.nonzero(batch == b)[0]
+        tree = cKDTree(pos64[idx])
+        for a, hits in enumerate(tree.query_ball_point(pos64[idx], r + 1e-4)):
+            for h in hits:
+                i, j = int(idx[a]), int(idx[h])
+                if i == j and not loop:
+                    continue
+                d = np.linalg.norm(pos64[j] - pos64[i])
+                if abs(d - r) <= 1e-4:
+                    near.add((i, j))
+                elif d < r:
+                    pairs.add((i, j))
+    return pairs, near
+
+
+@pytest.mark.parametrize("n,x_range,r,split,loop",
+                         list(product(X, X_RANGE, R, BATCH_SIZES, LOOP)))
+def test_oracle_vs_kdtree_sweep(n, x_range, r, split, loop):
+    rng = np.random.default_rng(1000 + n)
+    lo, hi = x_range
+    pos = ((hi - lo) * rng.random((n, 3)) + lo).astype(np.float32)
+    batch = _batch(n, split)
+    ei, ovf = oracle_radius.radius_graph(pos, r, batch, loop, 1000)
+    assert ovf == 0
+    got = set(map(tuple, ei.T.tolist()))
+    want, near = _kdtree_pairs(pos, r, batch, loop)
+    assert got - near == want - near
+    # canonical order, frames not mixed, self loops only with loop=True
+    if ei.shape[1]:
+        key = ei[0] * (n + 1) + ei[1]
+        assert np.all(np.diff(key) > 0)
+        assert np.array_equal(batch[ei[0]], batch[ei[1]])
+        assert loop or np.all(ei[0] != ei[1])
+
+
+def test_oracle_boundary_exact():
+    r = 15.0
+    x_in = float(np.nextafter(np.float32(15.0), np.float32(0.0)))
+    pos = np.array([[0, 0, 0], [15.0, 0, 0],
+                    [0, 0, 0], [x_in, 0, 0],
+                    [0, 0, 0], [9.0, 12.0, 0.0],
+                    [1, 2, 3], [10.0, 14.0, 5.0]], dtype=np.float32)
+    batch = np.array([0, 0, 1, 1, 2, 2, 3, 3], dtype=np.int64)
+    ei, _ = oracle_radius.radius_graph(pos, r, batch, False, 32)
+    assert ei.tolist() == [[2, 3], [3, 2]]
+    # with the cutoff a hair larger the boundary pairs join
+    ei2, _ = oracle_radius.radius_graph(pos, 15.0001, batch, False, 32)
+    assert sorted(map(tuple, ei2.T.tolist())) == [(0, 1), (1, 0), (2, 3), (3, 2), (4, 5),
+                                                  (5, 4)]
+
+
+def test_oracle_r2_rounding_of_cutoff():
+    """r^2 is formed in double and rounded once to fp32 (radius.cu:250): a
+    pair with fp32 d2 equal to fl32(r*r) stays outside even when r*r is not
+    representable."""
+    r = 0.1
+    r2 = np.float32(r * r)
+    # construct dx with fl32(dx*dx) == r2 exactly if possible, else closest below
+    dx = np.float32(np.sqrt(np.float64(r2)))
+    while np.float32(dx * dx) > r2:
+        dx = np.nextafter(dx, np.float32(0))
+    pos = np.array([[0, 0, 0], [dx, 0, 0]], dtype=np.float32)
+    ei, _ = oracle_radius.radius_graph(pos, r, None, False, 8)
+    inside = np.float32(dx * dx) < r2
+    assert (ei.shape[1] == 2) == bool(inside)
+
+
+@pytest.mark.parametrize("mnn", [1, 3, 7])
+def test_oracle_max_num_neighbors(mnn):
+    rng = np.random.default_rng(7)
+    pos = (rng.random((150, 3)) * 4).astype(np.float32)
+    batch = _batch(150, (40, 100))
+    ei, ovf = oracle_radius.radius_graph(pos, 2.0, batch, False, mnn)
+    assert ovf == 1
+    full, _ = oracle_radius.radius_graph(pos, 2.0, batch, False, 10_000)
+    # every row keeps exactly its min(mnn, deg) lowest-index neighbours
+    for i in range(150):
+        row_full = full[1][full[0] == i]
+        row = ei[1][ei[0] == i]
+        assert np.array_equal(row, np.sort(row_full)[:mnn])
+
+
+def test_oracle_empty_and_single():
+    ei, _ = oracle_radius.radius_graph(np.zeros((0, 3), np.float32), 1.0, None, False, 8)
+    assert ei.shape == (2, 0)
+    ei, _ = oracle_radius.radius_graph(np.zeros((1, 3), np.float32), 1.0, None, False, 8)
+    assert ei.shape == (2, 0)
+    ei, _ = oracle_radius.radius_graph(np.zeros((1, 3), np.float32), 1.0, None, True, 8)
+    assert ei.tolist() == [[0], [0]]
+
+
+def test_oracle_golden_fixture():
+    """Committed fixture (tests/golden/make_golden.py) of a small config-3-like
+    batch: the oracle must keep producing exactly these edges."""
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "golden", "radius_small.npz")
+    g = np.load(path)
+    ei, _ = oracle_radius.radius_graph(g["pos"], float(g["r"]), g["batch"], False, 1000)
+    assert np.array_equal(ei, g["edge_index"])
