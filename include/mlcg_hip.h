@@ -203,6 +203,73 @@ int mlcg_segment_sum(const float* values, int64_t stride,
                      const int64_t* frame_ptr, int64_t n_frames, float* out,
                      void* stream);
 
+/* ---------------------------------------------------------------------- */
+/* Priors: harmonic bonds and angles, Fourier dihedrals, repulsion          */
+/* ---------------------------------------------------------------------- */
+
+typedef enum {
+  MLCG_PRIOR_BOND = 0,      /* order 2, params [x0, k, V0]                  */
+  MLCG_PRIOR_ANGLE = 1,     /* order 3, params [x0, k, V0] on cos(theta)    */
+  MLCG_PRIOR_DIHEDRAL = 2,  /* order 4, params [v0, k1_1..k1_n, k2_1..k2_n] */
+  MLCG_PRIOR_REPULSION = 3  /* order 2, params [sigma]                      */
+} mlcg_prior_kind;
+
+/* Interaction order and number of per-interaction parameters of a kind
+ * (n_degs is the Fourier order of MLCG_PRIOR_DIHEDRAL, ignored otherwise);
+ * 0 / -1 for an unknown kind. */
+int mlcg_prior_order(int kind);
+int mlcg_prior_num_params(int kind, int n_degs);
+
+/* Per interaction m (index_mapping [order, mapping_stride] int64, bead
+ * index_mapping[s][m] in slot s; params [M, n_params] float32):
+ *   energy[m]            the interaction energy,
+ *   slot_forces[m, s, :] the force -dU_m/dpos on the bead of slot s.
+ * Replaces the forward of HarmonicBonds / HarmonicAngles
+ * (src/mlcg/nn/prior/harmonic.py:90-120,199-298), Dihedral / FourierSeries
+ * (src/mlcg/nn/prior/fourier_series.py:120-198,446-483) and Repulsion
+ * (src/mlcg/nn/prior/repulsion.py:111-140) together with the autograd
+ * position gradient GradientsOut takes of them (src/mlcg/nn/gradients.py:
+ * 208-226); the static pre-gathered parameter layout is the one of
+ * src/mlcg/simulation/specialize_prior.py:49-72,175-206. */
+int mlcg_prior_terms(int kind, int n_degs, const float* pos,
+                     const int64_t* index_mapping, int64_t mapping_stride,
+                     int64_t n_interactions, const float* params, int n_params,
+                     float* energy, float* slot_forces, void* stream);
+
+/* forces[a] (+)= sum of slot_forces over the slots of bead a: CSR bead_ptr
+ * [N + 1] int32 over bead_slots (flat slot ids m * order + s, ascending within
+ * a bead).  accumulate != 0 adds to forces.  Deterministic, atomic-free
+ * replacement of the per-prior autograd scatter into pos.grad. */
+int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
+                             const int32_t* bead_slots, int64_t n_nodes,
+                             int accumulate, float* forces, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Langevin BAOAB                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* B, A, O, A sub-steps of LangevinSimulation.timestep
+ * (src/mlcg/simulation/langevin.py:100-137) for [N, 3] float32 pos / vel
+ * and the forces at the current positions; beta_mass_ratio [N] =
+ * sqrt(1 / (beta m)) (langevin.py:176-180).  Noise is `noise` [N, 3] when
+ * non-NULL, else Philox4x32-10 normals keyed by `seed` at counter (bead,
+ * *step_dev) (step 0 when step_dev is NULL). */
+int mlcg_langevin_baoa(float* pos, float* vel, const float* forces,
+                       const float* masses, const float* beta_mass_ratio,
+                       int64_t n_nodes, float dt, float vscale, float noisescale,
+                       uint64_t seed, const int64_t* step_dev, const float* noise,
+                       void* stream);
+
+/* Final B sub-step (langevin.py:141) with the forces at the new positions;
+ * advances *step_dev by one when step_dev is non-NULL. */
+int mlcg_langevin_b(float* vel, const float* forces, const float* masses,
+                    int64_t n_nodes, float dt, int64_t* step_dev, void* stream);
+
+/* The normals mlcg_langevin_baoa draws at `step`: out [N, 3].  Replaces the
+ * torch.randn draw of langevin.py:129-134 (used by the statistics tests). */
+int mlcg_philox_normals(uint64_t seed, int64_t step, int64_t n_nodes, float* out,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,7 @@ _I64 = _c.c_int64
 _I32 = _c.c_int
 _F32 = _c.c_float
 _F64 = _c.c_double
+_U64 = _c.c_uint64
 
 # name -> argtypes (all functions return int status unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -52,6 +53,13 @@ _SIGNATURES = {
     "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _P, _P],
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
+    "mlcg_prior_order": [_I32],
+    "mlcg_prior_num_params": [_I32, _I32],
+    "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
+    "mlcg_prior_gather_forces": [_P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_langevin_baoa": [_P, _P, _P, _P, _P, _I64, _F32, _F32, _F32, _U64, _P, _P, _P],
+    "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
+    "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64}
 

@@ -268,14 +268,32 @@ __global__ void pair_forces_kernel(const float* __restrict__ pos, const float* _
   }
 }
 
-__global__ void segment_sum_kernel(const float* __restrict__ v, int64_t stride,
-                                   const int64_t* __restrict__ ptr, int64_t nb,
-                                   float* __restrict__ out) {
-  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb;
-       b += (int64_t)gridDim.x * blockDim.x) {
-    float acc = 0.f;
-    for (int64_t k = ptr[b]; k < ptr[b + 1]; ++k) acc += v[k * stride];
-    out[b] = acc;
+// One workgroup per segment: every thread keeps a compensated (Kahan) sum of
+// a strided subset, then the partial sums are combined in a fixed tree order
+// in LDS.  Deterministic for a given launch shape, and accurate to a few ulp
+// even for the ~10^5-term per-frame sums of a pair prior.
+constexpr int kSegThreads = 256;
+
+__global__ __launch_bounds__(kSegThreads) void segment_sum_kernel(
+    const float* __restrict__ v, int64_t stride, const int64_t* __restrict__ ptr, int64_t nb,
+    float* __restrict__ out) {
+  __shared__ float part[kSegThreads];
+  for (int64_t b = blockIdx.x; b < nb; b += gridDim.x) {
+    float s = 0.f, c = 0.f;
+    for (int64_t k = ptr[b] + threadIdx.x; k < ptr[b + 1]; k += kSegThreads) {
+      const float y = v[k * stride] - c;
+      const float t = s + y;
+      c = (t - s) - y;
+      s = t;
+    }
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kSegThreads / 2; w > 0; w >>= 1) {
+      if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) out[b] = part[0];
+    __syncthreads();
   }
 }
 
@@ -373,7 +391,8 @@ extern "C" int mlcg_segment_sum(const float* values, int64_t stride, const int64
   MLCG_REQUIRE(n_frames >= 0 && stride >= 1);
   if (n_frames == 0) return MLCG_OK;
   MLCG_REQUIRE(values && frame_ptr && out);
-  hipLaunchKernelGGL(segment_sum_kernel, dim3(mlcg_div_up(n_frames, 256)), dim3(256), 0,
-                     mlcg_stream(stream), values, stride, frame_ptr, n_frames, out);
+  hipLaunchKernelGGL(segment_sum_kernel, dim3(mlcg_persistent_groups(n_frames, 8)),
+                     dim3(kSegThreads), 0, mlcg_stream(stream), values, stride, frame_ptr,
+                     n_frames, out);
   return mlcg_launch_status();
 }

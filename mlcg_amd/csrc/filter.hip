@@ -511,12 +511,21 @@ __global__ __launch_bounds__(kThreads) void filter_bwd_f32_kernel(
   }
 }
 
-// Kernels here use more than 64 KiB of dynamic LDS; raise the per-kernel limit
-// once (gfx950 has 160 KiB per CU).
-template <typename K>
-void allow_lds(K kernel, size_t bytes) {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+// Kernels here use more than 64 KiB of dynamic LDS; raise their limit to the
+// 160 KiB of a gfx950 CU once per device (not per launch, so launches inside
+// a stream capture make no extra runtime calls).
+void allow_lds_once() {
+  static bool done[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
+  const int bytes = 160 * 1024;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f32_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_f32_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  done[dev] = true;
 }
 
 RbfParams make_params(const float* offsets, float coeff, int K, int rk, float rlo, float rhi,
@@ -562,7 +571,7 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
   if (!f16) {
     const int KS = (num_rbf + 3) / 4;
     const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
-    allow_lds(filter_fwd_f32_kernel, lds);
+    allow_lds_once();
     hipLaunchKernelGGL(filter_fwd_f32_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
                        pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
                        static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out);
@@ -570,7 +579,7 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
     const int KS32 = (num_rbf + 31) / 32;
     const size_t lds =
         sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8);
-    allow_lds(filter_fwd_f16_kernel, lds);
+    allow_lds_once();
     hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
                        pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
                        static_cast<__half*>(W_out), static_cast<__half*>(Wd_out), dist_out);
@@ -597,7 +606,7 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
   const int KS = (num_rbf + 3) / 4;
   const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
-  allow_lds(filter_bwd_f32_kernel, lds);
+  allow_lds_once();
   hipLaunchKernelGGL(filter_bwd_f32_kernel, dim3(groups), dim3(kThreads), lds,
                      mlcg_stream(stream), pos, pair_ij, pair_ij + pair_stride, n_pairs_dev,
                      max_pairs, rp, W1, b1, W2, Wbar, Wdbar, H, T, A, G);

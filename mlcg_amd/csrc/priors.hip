@@ -1,0 +1,235 @@
+// Bonded and repulsion prior energies with analytic forces (gfx950).
+//
+// Reference forms (ClementiGroup/mlcg):
+//   bonds      U = k (r - x0)^2 + V0, r = |p1 - p0|
+//              (Harmonic.compute, nn/prior/harmonic.py:119-120; features from
+//              compute_distances, geometry/internal_coordinates.py:73-100)
+//   angles     U = k (cos t - x0)^2 + V0, cos t = (dr1.dr2)/|dr1|/|dr2|,
+//              dr1 = p0 - p1, dr2 = p2 - p1 (internal_coordinates.py:146-183)
+//   dihedrals  V = sum_n k1_n sin(n t) + k2_n cos(n t) + v0
+//              (FourierSeries.compute, nn/prior/fourier_series.py:160-198) with
+//              the mdtraj-convention torsion of internal_coordinates.py:187-252
+//   repulsion  U = (sigma / r)^6 (Repulsion.compute, nn/prior/repulsion.py:136-140)
+// The reference obtains forces by autograd; here each interaction writes its
+// energy and the analytic force on each of its beads ("slot forces"), and a
+// second kernel sums the slot forces of every bead over a bead -> slot CSR in
+// ascending slot order, so the force reduction is deterministic and needs no
+// atomics.  Per-frame energies use the segmented sum of cfconv.hip.
+//
+// Torsion: with rij = pi - pj, rkj = pk - pj, rkl = pk - pl, m = rij x rkj,
+// n = rkj x rkl, the reference's atan2(-y, x) equals
+//   t = atan2(|rkj| (rij . n), m . n),
+// and dt/dp follows the Bekker/Blondel-Karplus form:
+//   dt/dpi = -|rkj|/|m|^2 m,  dt/dpl = |rkj|/|n|^2 n, and the two inner
+//   beads from p = (rij.rkj)/|rkj|^2, q = (rkl.rkj)/|rkj|^2.
+#include "common.h"
+
+namespace {
+
+struct V3 {
+  float x, y, z;
+};
+__device__ __forceinline__ V3 ld3(const float* __restrict__ p, int64_t i) {
+  return V3{p[3 * i], p[3 * i + 1], p[3 * i + 2]};
+}
+__device__ __forceinline__ V3 sub(V3 a, V3 b) { return V3{a.x - b.x, a.y - b.y, a.z - b.z}; }
+__device__ __forceinline__ V3 add(V3 a, V3 b) { return V3{a.x + b.x, a.y + b.y, a.z + b.z}; }
+__device__ __forceinline__ V3 scl(float s, V3 a) { return V3{s * a.x, s * a.y, s * a.z}; }
+__device__ __forceinline__ float dot(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ V3 cross(V3 a, V3 b) {
+  return V3{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+__device__ __forceinline__ void st3(float* __restrict__ f, int64_t slot, V3 v) {
+  f[3 * slot] = v.x;
+  f[3 * slot + 1] = v.y;
+  f[3 * slot + 2] = v.z;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void prior_terms_kernel(
+    int n_degs, const float* __restrict__ pos, const int64_t* __restrict__ map,
+    int64_t stride, int64_t M, const float* __restrict__ params, int n_params,
+    float* __restrict__ energy, float* __restrict__ slot_f) {
+  for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M;
+       m += (int64_t)gridDim.x * blockDim.x) {
+    const float* pr = params + m * n_params;
+    if (KIND == MLCG_PRIOR_BOND || KIND == MLCG_PRIOR_REPULSION) {
+      const V3 pi = ld3(pos, map[m]);
+      const V3 pj = ld3(pos, map[stride + m]);
+      const V3 d = sub(pj, pi);
+      const float r = sqrtf(dot(d, d));
+      float e, dUdr;
+      if (KIND == MLCG_PRIOR_BOND) {
+        const float x0 = pr[0], k = pr[1], v0 = pr[2];
+        const float dr = r - x0;
+        e = k * (dr * dr) + v0;
+        dUdr = 2.0f * k * dr;
+      } else {
+        const float s = pr[0] / r;
+        const float rr = s * s;
+        e = rr * rr * rr;
+        dUdr = -6.0f * e / r;
+      }
+      const V3 fi = scl(dUdr / r, d);  // force on bead 0; bead 1 gets -fi
+      energy[m] = e;
+      st3(slot_f, 2 * m, fi);
+      st3(slot_f, 2 * m + 1, scl(-1.0f, fi));
+    } else if (KIND == MLCG_PRIOR_ANGLE) {
+      const V3 p0 = ld3(pos, map[m]);
+      const V3 p1 = ld3(pos, map[stride + m]);
+      const V3 p2 = ld3(pos, map[2 * stride + m]);
+      const V3 a = sub(p0, p1), b = sub(p2, p1);
+      const float na = sqrtf(dot(a, a)), nb = sqrtf(dot(b, b));
+      const float c = dot(a, b) / na / nb;
+      const float x0 = pr[0], k = pr[1], v0 = pr[2];
+      const float dc = c - x0;
+      energy[m] = k * (dc * dc) + v0;
+      const float g = 2.0f * k * dc;  // dU/dcos
+      const float inv = 1.0f / (na * nb);
+      const V3 dca = sub(scl(inv, b), scl(c / (na * na), a));
+      const V3 dcb = sub(scl(inv, a), scl(c / (nb * nb), b));
+      const V3 f0 = scl(-g, dca), f2 = scl(-g, dcb);
+      st3(slot_f, 3 * m, f0);
+      st3(slot_f, 3 * m + 1, scl(-1.0f, add(f0, f2)));
+      st3(slot_f, 3 * m + 2, f2);
+    } else {  // MLCG_PRIOR_DIHEDRAL
+      const V3 pi = ld3(pos, map[m]);
+      const V3 pj = ld3(pos, map[stride + m]);
+      const V3 pk = ld3(pos, map[2 * stride + m]);
+      const V3 pl = ld3(pos, map[3 * stride + m]);
+      const V3 rij = sub(pi, pj), rkj = sub(pk, pj), rkl = sub(pk, pl);
+      const V3 mv = cross(rij, rkj), nv = cross(rkj, rkl);
+      const float rkj2 = dot(rkj, rkj);
+      const float nrkj = sqrtf(rkj2);
+      const float t = atan2f(nrkj * dot(rij, nv), dot(mv, nv));
+      float V = pr[0], dV = 0.0f;
+      for (int d = 1; d <= n_degs; ++d) {
+        float s, co;
+        sincosf((float)d * t, &s, &co);
+        const float k1 = pr[d], k2 = pr[n_degs + d];
+        V += k1 * s + k2 * co;
+        dV += (float)d * (k1 * co - k2 * s);
+      }
+      energy[m] = V;
+      const V3 fi = scl(-dV * nrkj / dot(mv, mv), mv);
+      const V3 fl = scl(dV * nrkj / dot(nv, nv), nv);
+      const float p = dot(rij, rkj) / rkj2, q = dot(rkl, rkj) / rkj2;
+      const V3 sv = sub(scl(p, fi), scl(q, fl));
+      const V3 fj = sub(fi, sv), fk = add(fl, sv);
+      st3(slot_f, 4 * m, fi);
+      st3(slot_f, 4 * m + 1, scl(-1.0f, fj));
+      st3(slot_f, 4 * m + 2, scl(-1.0f, fk));
+      st3(slot_f, 4 * m + 3, fl);
+    }
+  }
+}
+
+// forces[a] (+)= sum over the slots of bead a, ascending slot id.
+__global__ __launch_bounds__(256) void prior_gather_kernel(
+    const float* __restrict__ slot_f, const int32_t* __restrict__ bead_ptr,
+    const int32_t* __restrict__ bead_slots, int64_t n, int accumulate,
+    float* __restrict__ forces) {
+  for (int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; a < n;
+       a += (int64_t)gridDim.x * blockDim.x) {
+    float fx = 0.f, fy = 0.f, fz = 0.f;
+    for (int32_t s = bead_ptr[a]; s < bead_ptr[a + 1]; ++s) {
+      const int64_t slot = bead_slots[s];
+      fx += slot_f[3 * slot];
+      fy += slot_f[3 * slot + 1];
+      fz += slot_f[3 * slot + 2];
+    }
+    if (accumulate) {
+      forces[3 * a] += fx;
+      forces[3 * a + 1] += fy;
+      forces[3 * a + 2] += fz;
+    } else {
+      forces[3 * a] = fx;
+      forces[3 * a + 1] = fy;
+      forces[3 * a + 2] = fz;
+    }
+  }
+}
+
+int order_of(int kind) {
+  switch (kind) {
+    case MLCG_PRIOR_BOND:
+    case MLCG_PRIOR_REPULSION:
+      return 2;
+    case MLCG_PRIOR_ANGLE:
+      return 3;
+    case MLCG_PRIOR_DIHEDRAL:
+      return 4;
+    default:
+      return 0;
+  }
+}
+
+int params_of(int kind, int n_degs) {
+  switch (kind) {
+    case MLCG_PRIOR_BOND:
+    case MLCG_PRIOR_ANGLE:
+      return 3;
+    case MLCG_PRIOR_REPULSION:
+      return 1;
+    case MLCG_PRIOR_DIHEDRAL:
+      return 1 + 2 * n_degs;
+    default:
+      return -1;
+  }
+}
+
+}  // namespace
+
+extern "C" int mlcg_prior_order(int kind) { return order_of(kind); }
+
+extern "C" int mlcg_prior_num_params(int kind, int n_degs) { return params_of(kind, n_degs); }
+
+extern "C" int mlcg_prior_terms(int kind, int n_degs, const float* pos,
+                                const int64_t* index_mapping, int64_t mapping_stride,
+                                int64_t n_interactions, const float* params, int n_params,
+                                float* energy, float* slot_forces, void* stream) {
+  if (order_of(kind) == 0) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(n_interactions >= 0 && mapping_stride >= n_interactions);
+  MLCG_REQUIRE(kind != MLCG_PRIOR_DIHEDRAL || (n_degs >= 1 && n_degs <= 64));
+  MLCG_REQUIRE(n_params == params_of(kind, n_degs));
+  if (n_interactions == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && index_mapping && params && energy && slot_forces);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_interactions, 256), 8);
+  hipStream_t s = mlcg_stream(stream);
+  switch (kind) {
+    case MLCG_PRIOR_BOND:
+      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_BOND>, dim3(groups), dim3(256), 0, s,
+                         n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
+                         n_params, energy, slot_forces);
+      break;
+    case MLCG_PRIOR_ANGLE:
+      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_ANGLE>, dim3(groups), dim3(256), 0, s,
+                         n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
+                         n_params, energy, slot_forces);
+      break;
+    case MLCG_PRIOR_DIHEDRAL:
+      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_DIHEDRAL>, dim3(groups), dim3(256), 0,
+                         s, n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
+                         n_params, energy, slot_forces);
+      break;
+    default:
+      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_REPULSION>, dim3(groups), dim3(256), 0,
+                         s, n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
+                         n_params, energy, slot_forces);
+      break;
+  }
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
+                                        const int32_t* bead_slots, int64_t n_nodes,
+                                        int accumulate, float* forces, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0);
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(bead_ptr && forces);
+  MLCG_REQUIRE(slot_forces || bead_slots == nullptr);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, 256), 8);
+  hipLaunchKernelGGL(prior_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
+                     slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces);
+  return mlcg_launch_status();
+}

@@ -3,7 +3,7 @@
 GradientsOut around a fusable HIP SchNet computes energies and forces in one
 fused pass (``SchNet.energy_forces``) instead of an autograd replay; in
 training mode the result carries the hand-derived force-matching double
-backward.  Any other model goes through torch.autograd exactly like the
+backward.  Around a prior it takes the prior kernel's analytic forces.  Any other model goes through torch.autograd exactly like the
 reference (lines 208-228).
 """
 
@@ -75,18 +75,25 @@ class GradientsOut(torch.nn.Module):
         assert any(k in GradientsOut._targets for k in self.targets), (
             f"targets={self.targets} should be any of {GradientsOut._targets}")
 
-    def _fused_model(self):
+    def _direct_model(self):
+        """The wrapped model when it computes energies and forces in one pass
+        on the HIP kernels (a fusable SchNet or a prior), else None."""
+        from .prior import _Prior
         from .schnet import SchNet
 
         m = self.model
-        if isinstance(m, SchNet) and FORCE_KEY in self.targets and m.fused_spec() is not None:
+        if FORCE_KEY not in self.targets:
+            return None
+        if isinstance(m, SchNet) and m.fused_spec() is not None:
+            return m
+        if isinstance(m, _Prior):
             return m
         return None
 
     def forward(self, data):
-        fused = self._fused_model()
-        if fused is not None:
-            energy, forces = fused.energy_forces(data, create_graph=self.training)
+        direct = self._direct_model()
+        if direct is not None:
+            energy, forces = direct.energy_forces(data, create_graph=self.training)
             data.out[self.name] = {ENERGY_KEY: energy, FORCE_KEY: forces}
             data.pos = data.pos.detach()
             return data

@@ -160,6 +160,11 @@ class SchNet(torch.nn.Module):
         self.output_network = output_network
         # fp16 operands (fp32 accumulation) for the filter-network matmuls
         self.fp16_filters = False
+        # fixed edge capacity of the radius graph (None: sized exactly with
+        # one host sync per call; an int: no sync, as needed inside a captured
+        # graph -- the caller then checks last_graph.flags)
+        self.graph_capacity: Optional[int] = None
+        self.last_graph: Optional[ops.PairGraph] = None
         self.reset_parameters()
 
     def reset_parameters(self):
@@ -185,7 +190,21 @@ class SchNet(torch.nn.Module):
     # ------------------------------------------------------------------
     def fused_spec(self) -> Optional[_fused.FusedSpec]:
         """The kernel description of this model, or None if some piece has no
-        kernel (then forward runs module by module)."""
+        kernel (then forward runs module by module).  Cached: building it reads
+        the basis coefficient back to the host once, and a cached spec lets the
+        fused path run inside a stream capture."""
+        rbf = self.rbf_layer
+        key = (bool(self.fp16_filters), rbf.offset.data_ptr(), rbf.offset._version,
+               rbf.coeff.data_ptr(), rbf.coeff._version, bool(getattr(rbf, "trainable", False)),
+               len(self.interaction_blocks))
+        cached = self.__dict__.get("_spec_cache")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        spec = self._build_fused_spec()
+        self.__dict__["_spec_cache"] = (key, spec)
+        return spec
+
+    def _build_fused_spec(self) -> Optional[_fused.FusedSpec]:
         rbf = self.rbf_layer
         if not isinstance(rbf, GaussianBasis) or rbf.trainable:
             return None
@@ -266,10 +285,12 @@ class SchNet(torch.nn.Module):
         batch = data.batch if "batch" in data else torch.zeros(
             n, dtype=torch.long, device=data.pos.device)
         n_frames = int(data.n_atoms.numel()) if "n_atoms" in data else None
-        return ops.radius_graph(data.pos.detach(), float(self.rbf_layer.cutoff.cutoff_upper),
-                                batch=batch, loop=False,
-                                max_num_neighbors=self.max_num_neighbors, with_pairs=True,
-                                n_frames=n_frames)
+        g = ops.radius_graph(data.pos.detach(), float(self.rbf_layer.cutoff.cutoff_upper),
+                             batch=batch, loop=False, max_num_neighbors=self.max_num_neighbors,
+                             with_pairs=True, n_frames=n_frames,
+                             capacity=self.graph_capacity)
+        self.last_graph = g
+        return g
 
     # ------------------------------------------------------------------
     def forward(self, data):

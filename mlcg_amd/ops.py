@@ -52,6 +52,7 @@ class PairGraph:
     num_edges: int
     num_pairs: int
     overflow: int = 0
+    flags: Optional[torch.Tensor] = None  # device int32 [1]: overflow bits
 
     @property
     def n_pairs_dev(self) -> torch.Tensor:
@@ -90,6 +91,7 @@ def radius_graph(
     with_pairs: bool = False,
     n_frames: Optional[int] = None,
     frame_ptr: Optional[torch.Tensor] = None,
+    capacity: Optional[int] = None,
 ) -> PairGraph:
     """All pairs (i, j) of the same frame with |pos[j] - pos[i]| < r.
 
@@ -102,6 +104,15 @@ def radius_graph(
     with_pairs additionally builds the receiver CSR and pair map used by the
     CFConv kernels (it requires a symmetric graph, i.e. no binding
     ``max_num_neighbors`` and ``loop=False``).
+
+    Without ``capacity`` the edge count is read back to size the outputs
+    exactly (one host synchronisation, as the reference's radius.cu:288).
+    With ``capacity`` nothing synchronises: buffers hold ``capacity`` edges
+    (``capacity // 2`` pairs), the live counts stay on the device
+    (``rowptr[N]``, ``n_pairs_dev``), rows are clamped to the capacity so
+    every later kernel stays in bounds, and ``graph.flags`` (bit 0: a row
+    exceeded max_num_neighbors, bit 1: the capacity was exceeded) must be
+    checked by the caller -- this is the form a captured graph replays.
     """
     pos = _validate_pos(pos)
     n = pos.shape[0]
@@ -115,6 +126,8 @@ def radius_graph(
     _check(max_num_neighbors >= 0, "max_num_neighbors must be non-negative")
     if with_pairs:
         _check(not loop, "the pair map is defined for graphs without self loops")
+    if capacity is not None:
+        _check(capacity >= 0 and capacity < 2 ** 31, "capacity must fit int32 edge ids")
     if frame_ptr is None:
         if n_frames is None:
             n_frames = int(batch[-1].item()) + 1 if n > 0 else 0
@@ -132,31 +145,44 @@ def radius_graph(
                      device=dev)
     call("mlcg_exclusive_scan2_i32", ptr(deg), ptr(udeg), n, ptr(rowptr), ptr(pairptr),
          ptr(ws), s)
-    # one host sync to size the outputs (the reference syncs at radius.cu:288)
-    e_count, p_count, overflow = torch.stack(
-        [rowptr[n], pairptr[n], flags[0]]).tolist()
-    if with_pairs and overflow:
-        raise RuntimeError(
-            f"max_num_neighbors={max_num_neighbors} binds: the truncated graph is not "
-            "symmetric and the pair-based CFConv kernels cannot use it; raise "
-            "max_num_neighbors")
-    edge_index = torch.empty(2, e_count, dtype=torch.int64, device=dev)
+    if capacity is None:
+        # one host sync to size the outputs (the reference syncs at radius.cu:288)
+        e_count, p_count, overflow = torch.stack(
+            [rowptr[n], pairptr[n], flags[0]]).tolist()
+        if with_pairs and overflow:
+            raise RuntimeError(
+                f"max_num_neighbors={max_num_neighbors} binds: the truncated graph is not "
+                "symmetric and the pair-based CFConv kernels cannot use it; raise "
+                "max_num_neighbors")
+        e_cap, p_cap = e_count, p_count
+    else:
+        e_cap, p_cap = capacity, capacity // 2
+        e_count = p_count = -1  # live counts stay on the device
+        overflow = -1
+    edge_index = torch.empty(2, e_cap, dtype=torch.int64, device=dev)
     col = pair_ij = eid2pair = None
     if with_pairs:
-        col = torch.empty(e_count, dtype=torch.int32, device=dev)
-        pair_ij = torch.empty(2, p_count, dtype=torch.int32, device=dev)
-        eid2pair = torch.empty(e_count, dtype=torch.int32, device=dev)
+        col = torch.empty(e_cap, dtype=torch.int32, device=dev)
+        pair_ij = torch.empty(2, p_cap, dtype=torch.int32, device=dev)
+        eid2pair = (torch.empty if capacity is None else torch.zeros)(
+            e_cap, dtype=torch.int32, device=dev)
     call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
          int(max_num_neighbors), ptr(rowptr), ptr(pairptr) if with_pairs else None,
-         e_count, e_count, ptr(edge_index), ptr(col), p_count, p_count, ptr(pair_ij),
+         e_cap, e_cap, ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij),
          ptr(eid2pair), ptr(flags), s)
+    if capacity is not None:
+        # rows past the capacity were dropped by the fill: clamp the CSR (and
+        # the pair count) so that every consumer stays inside the buffers
+        rowptr.clamp_(max=e_cap)
+        pairptr.clamp_(max=p_cap)
     if with_pairs:
-        call("mlcg_pair_reverse_map", ptr(pair_ij), p_count, ptr(pairptr[n:]), p_count,
+        call("mlcg_pair_reverse_map", ptr(pair_ij), p_cap, ptr(pairptr[n:]), p_cap,
              ptr(rowptr), ptr(col), ptr(eid2pair), s)
     return PairGraph(edge_index=edge_index, rowptr=rowptr, col=col, pair_ij=pair_ij,
                      pairptr=pairptr if with_pairs else None, eid2pair=eid2pair,
                      frame_ptr=frame_ptr, num_nodes=n, num_edges=e_count,
-                     num_pairs=p_count if with_pairs else 0, overflow=int(overflow))
+                     num_pairs=p_count if with_pairs else 0, overflow=int(overflow),
+                     flags=flags)
 
 
 # --------------------------------------------------------------------------
@@ -341,4 +367,142 @@ def segment_sum(values: torch.Tensor, frame_ptr: torch.Tensor) -> torch.Tensor:
     out = torch.empty(nb, dtype=torch.float32, device=values.device)
     call("mlcg_segment_sum", ptr(v), 1, ptr(frame_ptr), nb, ptr(out),
          stream_handle(values.device))
+    return out
+
+
+# --------------------------------------------------------------------------
+# Priors
+
+PRIOR_KIND = {"bonds": 0, "angles": 1, "dihedrals": 2, "repulsion": 3}
+PRIOR_ORDER = {0: 2, 1: 3, 2: 4, 3: 2}
+
+
+@dataclass
+class PriorGraph:
+    """Interaction list of one prior plus the index structures its kernels use.
+
+    index_mapping : [order, M] int64 (bead of slot s of interaction m)
+    bead_ptr      : [N + 1] int32 CSR over bead_slots
+    bead_slots    : [M * order] int32 flat slot ids m * order + s, grouped by
+                    bead and ascending within a bead
+    seg_ptr       : [B + 1] int64, interactions of frame b are
+                    seg_ptr[b] : seg_ptr[b + 1] (mapping_batch is sorted)
+    """
+
+    index_mapping: torch.Tensor
+    bead_ptr: torch.Tensor
+    bead_slots: torch.Tensor
+    seg_ptr: torch.Tensor
+    num_nodes: int
+    num_frames: int
+
+    @property
+    def num_interactions(self) -> int:
+        return self.index_mapping.shape[1]
+
+
+def prior_graph(index_mapping: torch.Tensor, mapping_batch: Optional[torch.Tensor],
+                num_nodes: int, num_frames: int) -> PriorGraph:
+    """Builds the bead -> slot CSR and the frame segments of an interaction
+    list (once per topology; the MD loop reuses it every step)."""
+    require_device(index_mapping)
+    _check(index_mapping.dim() == 2 and index_mapping.shape[0] in (2, 3, 4),
+           f"index_mapping must be [order, M], got {tuple(index_mapping.shape)}")
+    im = _as_i64(index_mapping)
+    order, M = im.shape
+    dev = im.device
+    if M > 0:
+        _check(int(im.min()) >= 0 and int(im.max()) < num_nodes,
+               "index_mapping refers to beads outside [0, num_nodes)")
+    flat = im.t().reshape(-1)  # slot id m * order + s -> bead
+    srt = torch.sort(flat, stable=True)
+    bead_slots = srt.indices.to(torch.int32).contiguous()
+    counts = torch.bincount(flat, minlength=num_nodes)
+    bead_ptr = torch.zeros(num_nodes + 1, dtype=torch.int32, device=dev)
+    bead_ptr[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    if mapping_batch is None:
+        mapping_batch = torch.zeros(M, dtype=torch.int64, device=dev)
+    mb = _as_i64(mapping_batch)
+    _check(mb.numel() == M, "mapping_batch must have one entry per interaction")
+    if M > 1:
+        _check(bool((mb[1:] >= mb[:-1]).all()),
+               "mapping_batch must be sorted by frame (collated neighbour lists are)")
+    seg_ptr = frame_ptr_from_batch(mb, num_frames)
+    return PriorGraph(index_mapping=im, bead_ptr=bead_ptr, bead_slots=bead_slots,
+                      seg_ptr=seg_ptr, num_nodes=num_nodes, num_frames=num_frames)
+
+
+def prior_terms(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
+                params: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(energy [M], slot forces [M, order, 3]) of every interaction."""
+    pos = _validate_pos(pos)
+    M = graph.num_interactions
+    order = PRIOR_ORDER[kind]
+    n_params = int(_lib.load().mlcg_prior_num_params(kind, n_degs))
+    params = params.to(torch.float32).contiguous()
+    _check(tuple(params.shape) == (M, n_params),
+           f"params must be [{M}, {n_params}], got {tuple(params.shape)}")
+    energy = torch.empty(M, dtype=torch.float32, device=pos.device)
+    slot_f = torch.empty(M, order, 3, dtype=torch.float32, device=pos.device)
+    call("mlcg_prior_terms", kind, n_degs, ptr(pos), ptr(graph.index_mapping), M, M,
+         ptr(params), n_params, ptr(energy), ptr(slot_f), stream_handle(pos.device))
+    return energy, slot_f
+
+
+def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
+                        params: torch.Tensor, forces: Optional[torch.Tensor] = None):
+    """Per-frame energies [B] and forces [N, 3] of one prior; with `forces`
+    given the forces are added to it in place."""
+    energy, slot_f = prior_terms(kind, n_degs, pos, graph, params)
+    E = segment_sum(energy, graph.seg_ptr)
+    accumulate = forces is not None
+    if forces is None:
+        forces = torch.empty(graph.num_nodes, 3, dtype=torch.float32, device=pos.device)
+    call("mlcg_prior_gather_forces", ptr(slot_f), ptr(graph.bead_ptr), ptr(graph.bead_slots),
+         graph.num_nodes, int(accumulate), ptr(forces), stream_handle(pos.device))
+    return E, forces
+
+
+# --------------------------------------------------------------------------
+# Langevin BAOAB
+
+def langevin_baoa(pos: torch.Tensor, vel: torch.Tensor, forces: torch.Tensor,
+                  masses: torch.Tensor, beta_mass_ratio: torch.Tensor, dt: float,
+                  vscale: float, noisescale: float, seed: int,
+                  step: Optional[torch.Tensor] = None,
+                  noise: Optional[torch.Tensor] = None) -> None:
+    """B, A, O, A sub-steps in place on pos and vel ([N, 3] float32)."""
+    require_device(pos, vel, forces, masses, beta_mass_ratio)
+    for t in (pos, vel, forces):
+        _check(t.dtype == torch.float32 and t.is_contiguous() and t.shape == pos.shape,
+               "pos, vel and forces must be contiguous float32 [N, 3]")
+    n = pos.shape[0]
+    _check(masses.numel() == n and beta_mass_ratio.numel() == n,
+           "masses and beta_mass_ratio must have one entry per bead")
+    if noise is not None:
+        _check(noise.shape == pos.shape and noise.dtype == torch.float32,
+               "noise must be float32 [N, 3]")
+        noise = noise.contiguous()
+    if step is not None:
+        _check(step.dtype == torch.int64 and step.numel() == 1, "step must be one int64")
+    call("mlcg_langevin_baoa", ptr(pos), ptr(vel), ptr(forces),
+         ptr(masses.to(torch.float32).contiguous()),
+         ptr(beta_mass_ratio.to(torch.float32).contiguous()), n, float(dt), float(vscale),
+         float(noisescale), int(seed) & ((1 << 64) - 1), ptr(step), ptr(noise),
+         stream_handle(pos.device))
+
+
+def langevin_b(vel: torch.Tensor, forces: torch.Tensor, masses: torch.Tensor, dt: float,
+               step: Optional[torch.Tensor] = None) -> None:
+    """Final B sub-step in place on vel; advances `step` by one."""
+    require_device(vel, forces, masses)
+    call("mlcg_langevin_b", ptr(vel), ptr(forces), ptr(masses.to(torch.float32).contiguous()),
+         vel.shape[0], float(dt), ptr(step), stream_handle(vel.device))
+
+
+def philox_normals(seed: int, step: int, n: int, device) -> torch.Tensor:
+    """The [n, 3] normals langevin_baoa draws at `step` (for statistics tests)."""
+    out = torch.empty(n, 3, dtype=torch.float32, device=device)
+    call("mlcg_philox_normals", int(seed) & ((1 << 64) - 1), int(step), n, ptr(out),
+         stream_handle(torch.device(device)))
     return out

@@ -1,0 +1,220 @@
+"""BAOAB Langevin dynamics (mlcg/simulation/langevin.py, base.py).
+
+``LangevinSimulation`` keeps the reference's constructor arguments that shape
+the dynamics (``friction``, ``dt``, ``n_timesteps``, ``save_interval``,
+``random_seed``, ``save_forces``, ``save_energies``, ``dtype``) and its
+``attach_model_and_configurations(model, configurations, beta)`` /
+``simulate()`` entry points.  One timestep is
+
+    BAOA kernel (mlcg_langevin_baoa)  ->  model forces  ->  B kernel
+
+with the noise drawn in the kernel from a counter-based generator whose step
+counter lives on the device, so the whole step -- including the radius-graph
+rebuild at a fixed edge capacity -- can be captured once as a HIP graph and
+replayed (``capture=True``).  The model is called exactly as the reference
+calls it (``calculate_potential_and_forces``, base.py:517-539): a module whose
+``forward(data)`` fills ``data.out["energy"]`` and ``data.out["forces"]``
+(e.g. SumOut of GradientsOut models).
+
+File I/O, checkpoints, logging and parallel tempering of the reference
+(base.py:653-1040, parallel_tempering.py) are not part of this module; the
+trajectory is returned as an array.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Union
+
+import numpy as np
+import torch
+
+from .. import ops
+from ..data import AtomicData
+from ..data._keys import ENERGY_KEY, FORCE_KEY, MASS_KEY, POSITIONS_KEY, VELOCITY_KEY
+from ..data.atomic_data import collate
+
+
+def sample_maxwell_boltzmann(betas: torch.Tensor, masses: torch.Tensor,
+                             generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """[N, 3] velocities with per-component variance 1/(beta m)
+    (langevin.py:79-98)."""
+    assert bool((masses > 0).all())
+    scale = torch.sqrt(1.0 / (betas * masses))
+    z = torch.randn(masses.shape[0], 3, generator=generator, dtype=masses.dtype)
+    return z * scale[:, None]
+
+
+class LangevinSimulation:
+    def __init__(self, friction: float = 1e-3, dt: float = 5e-4, n_timesteps: int = 100,
+                 save_interval: int = 10, random_seed: Optional[int] = None,
+                 device: str = "cuda", dtype: str = "single", save_forces: bool = False,
+                 save_energies: bool = False, capture: bool = False,
+                 edge_capacity_factor: float = 1.5, check_interval: int = 100):
+        assert friction > 0
+        if dtype != "single":
+            raise NotImplementedError("the HIP kernels integrate in single precision")
+        if n_timesteps % save_interval != 0:
+            raise ValueError("n_timesteps must be a multiple of save_interval")
+        self.friction = friction
+        self.dt = dt
+        self.n_timesteps = n_timesteps
+        self.save_interval = save_interval
+        self.random_seed = 0 if random_seed is None else int(random_seed)
+        self.device = torch.device(device)
+        self.dtype = torch.float32
+        self.save_forces = save_forces
+        self.save_energies = save_energies
+        self.capture = capture
+        self.edge_capacity_factor = edge_capacity_factor
+        self.check_interval = check_interval
+        self.vscale = float(np.exp(-self.dt * self.friction))
+        self.noisescale = float(np.sqrt(1 - self.vscale * self.vscale))
+        self.model = None
+        self.initial_data = None
+
+    # ------------------------------------------------------------------
+    def attach_model_and_configurations(self, model: torch.nn.Module,
+                                        configurations: List[AtomicData],
+                                        beta: Union[float, List[float]]):
+        self.model = model.eval().to(self.device)
+        for p in self.model.parameters():
+            p.requires_grad = False
+        self._attach_configurations(configurations, beta)
+
+    def _attach_configurations(self, configurations, beta):
+        if len(configurations) == 0:
+            raise ValueError("no configurations")
+        n0 = configurations[0].pos.shape[0]
+        for k, d in enumerate(configurations):
+            if MASS_KEY not in d:
+                raise ValueError(f"configuration {k} has no masses")
+            if d.pos.shape != (n0, 3) or d.masses.shape != (n0,):
+                raise ValueError(f"configuration {k} differs in shape from the first one")
+        data = collate(configurations).to(self.device)
+        data.pos = data.pos.to(self.dtype).contiguous()
+        data.masses = data.masses.to(self.dtype).contiguous()
+        self.n_sims = len(configurations)
+        self.n_atoms = n0
+        if isinstance(beta, (float, int)):
+            if beta <= 0:
+                raise ValueError(f"Beta must be positive, but {beta} was supplied")
+            self.beta = torch.full((self.n_sims,), float(beta), dtype=self.dtype)
+        else:
+            self.beta = torch.tensor(beta, dtype=self.dtype)
+            if not bool((self.beta > 0).all()):
+                raise ValueError(f"All betas must be positive, but {beta} contains an "
+                                 "illegal value.")
+        assert len(self.beta) == self.n_sims
+        betas = self.beta.repeat_interleave(self.n_atoms)
+        if VELOCITY_KEY not in data:
+            g = torch.Generator().manual_seed(self.random_seed)
+            data[VELOCITY_KEY] = sample_maxwell_boltzmann(
+                betas, data.masses.cpu(), generator=g).to(self.device, self.dtype)
+        self.beta_mass_ratio = torch.sqrt(1.0 / betas.to(self.device) / data.masses).contiguous()
+        self.initial_data = data
+
+    # ------------------------------------------------------------------
+    def calculate_potential_and_forces(self, data):
+        data = self.model(data)
+        return data.out[ENERGY_KEY].detach(), data.out[FORCE_KEY].detach()
+
+    def _set_capacity(self, data):
+        """Fixed radius-graph capacities for every SchNet in the model (from
+        the initial structure's edge count), so that no step synchronises."""
+        from ..nn.schnet import SchNet
+
+        for m in self.model.modules():
+            if isinstance(m, SchNet) and m.graph_capacity is None:
+                g = m.build_graph(data)
+                cap = int(math.ceil(g.num_edges * self.edge_capacity_factor)) + 64
+                m.graph_capacity = cap + (cap % 2)
+
+    def _graph_flags(self):
+        from ..nn.schnet import SchNet
+
+        return [m.last_graph.flags for m in self.model.modules()
+                if isinstance(m, SchNet) and m.last_graph is not None
+                and m.graph_capacity is not None]
+
+    def _check_flags(self, flags):
+        for f in flags:
+            v = int(f.item())
+            if v:
+                raise RuntimeError(
+                    f"radius graph overflow (flags={v}): raise edge_capacity_factor or "
+                    "max_num_neighbors")
+
+    def simulate(self) -> np.ndarray:
+        """Runs n_timesteps BAOAB steps; returns the saved positions
+        [n_sims, n_saves, n_atoms, 3] (and stores energies/forces if asked)."""
+        if self.model is None or self.initial_data is None:
+            raise RuntimeError("attach a model and configurations first")
+        data = self.initial_data.clone()
+        x, v, m = data.pos, data.velocities.contiguous(), data.masses
+        data.velocities = v
+        self._set_capacity(data)
+        step_ctr = torch.zeros(1, dtype=torch.int64, device=self.device)
+        epot = torch.zeros(self.n_sims, dtype=self.dtype, device=self.device)
+        F = torch.zeros_like(x)
+        with torch.no_grad():
+            e0, f0 = self.calculate_potential_and_forces(data)
+        F.copy_(f0)
+        epot.copy_(e0)
+        n_saves = self.n_timesteps // self.save_interval
+        traj = torch.empty(n_saves, *x.shape, dtype=self.dtype, device=self.device)
+        saved_e = (torch.empty(n_saves, self.n_sims, dtype=self.dtype, device=self.device)
+                   if self.save_energies else None)
+        saved_f = (torch.empty(n_saves, *x.shape, dtype=self.dtype, device=self.device)
+                   if self.save_forces else None)
+
+        def one_step():
+            ops.langevin_baoa(x, v, F, m, self.beta_mass_ratio, self.dt, self.vscale,
+                              self.noisescale, self.random_seed, step=step_ctr)
+            data.pos = x
+            e, f = self.calculate_potential_and_forces(data)
+            F.copy_(f)
+            epot.copy_(e)
+            ops.langevin_b(v, F, m, self.dt, step=step_ctr)
+
+        graph = None
+        flags = []
+        with torch.no_grad():
+            for t in range(self.n_timesteps):
+                if graph is None and self.capture and t >= 2:
+                    torch.cuda.synchronize()
+                    self._check_flags(self._graph_flags())
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        one_step()
+                    flags = self._graph_flags()
+                    graph.replay()  # the captured step is step t
+                elif graph is not None:
+                    graph.replay()
+                else:
+                    one_step()
+                    flags = self._graph_flags()
+                if (t + 1) % self.save_interval == 0:
+                    k = (t + 1) // self.save_interval - 1
+                    traj[k].copy_(x)
+                    if saved_e is not None:
+                        saved_e[k].copy_(epot)
+                    if saved_f is not None:
+                        saved_f[k].copy_(F)
+                if (t + 1) % self.check_interval == 0:
+                    self._check_flags(flags)
+                    if not bool(torch.isfinite(x).all()):
+                        raise RuntimeError(f"non-finite positions at step {t + 1}")
+        torch.cuda.synchronize()
+        self._check_flags(flags)
+        self.final_data = data
+        self.potential = epot
+        self.forces = F
+        shape = (n_saves, self.n_sims, self.n_atoms, 3)
+        out = traj.view(shape).permute(1, 0, 2, 3).cpu().numpy()
+        self.simulated_coords = out
+        if saved_e is not None:
+            self.simulated_potential = saved_e.t().cpu().numpy()
+        if saved_f is not None:
+            self.simulated_forces = saved_f.view(shape).permute(1, 0, 2, 3).cpu().numpy()
+        return out

@@ -1,0 +1,304 @@
+"""HIP priors, BAOAB integrator and the captured MD step against the CPU
+oracles (oracle/priors_ref.py, oracle/langevin_ref.py).
+
+Tolerances: fp32 energies and forces within 1e-5
+relative (to the oracle's norm) of the fp64 oracle.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import langevin_ref as L
+from oracle import priors_ref as P
+from tests.helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+KINDS = ["bonds", "angles", "dihedrals", "repulsion"]
+
+
+def _chain_batch(n_frames, n_beads, seed=5):
+    from mlcg_amd import synthetic
+
+    rng = np.random.default_rng(seed)
+    pos = synthetic.self_avoiding_walk(n_frames, n_beads, rng)
+    return torch.from_numpy(pos.reshape(-1, 3))
+
+
+def _param_matrix(kind, params):
+    if kind in ("bonds", "angles"):
+        return torch.stack([params["x0"], params["k"], params["V0"]], 1)
+    if kind == "dihedrals":
+        return torch.cat([params["v_0"][:, None], params["k1s"], params["k2s"]], 1)
+    return params["sigma"][:, None]
+
+
+def _params(kind, M, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bonds":
+        return {"x0": 3.8 + 0.1 * torch.randn(M, generator=g), "k": torch.full((M,), 100.0),
+                "V0": torch.zeros(M)}
+    if kind == "angles":
+        return {"x0": torch.full((M,), math.cos(math.radians(100.0))),
+                "k": 5.0 + torch.rand(M, generator=g), "V0": 0.1 * torch.rand(M, generator=g)}
+    if kind == "dihedrals":
+        return {"v_0": torch.rand(M, generator=g), "k1s": 0.5 * torch.randn(M, 3, generator=g),
+                "k2s": 0.5 * torch.randn(M, 3, generator=g)}
+    return {"sigma": torch.full((M,), 4.0)}
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_prior_kernel_vs_oracle(kind):
+    from mlcg_amd import ops
+
+    n_frames, n = 6, 268
+    pos = _chain_batch(n_frames, n)
+    mapping, mb = P.chain_topology(n_frames, n)[kind]
+    params = _params(kind, mapping.shape[1])
+    E_ref, F_ref = P.prior_energy_forces(kind, pos.double(), mapping, mb, n_frames,
+                                         {k: v.double() for k, v in params.items()})
+    g = ops.prior_graph(mapping.cuda(), mb.cuda(), pos.shape[0], n_frames)
+    E, F = ops.prior_energy_forces(ops.PRIOR_KIND[kind], 3, pos.cuda(), g,
+                                   _param_matrix(kind, params).cuda())
+    print(kind, "E rel", rel_err(E, E_ref), "F rel", rel_err(F, F_ref))
+    assert rel_err(E, E_ref) < 1e-5
+    assert rel_err(F, F_ref) < 1e-5
+    # accumulate mode adds onto an existing force array
+    F0 = torch.ones_like(F)
+    _, F2 = ops.prior_energy_forces(ops.PRIOR_KIND[kind], 3, pos.cuda(), g,
+                                    _param_matrix(kind, params).cuda(), forces=F0)
+    assert torch.allclose(F2, F + 1.0, rtol=1e-6, atol=1e-6)
+
+
+def _stats_tables():
+    bonds = {(a, b): {"x_0": 3.8 + 0.01 * (a + b), "k": 100.0 - a} for a in range(1, 6)
+             for b in range(1, 6)}
+    angles = {(a, b, c): {"x_0": math.cos(math.radians(95 + a + c)), "k": 4.0 + 0.1 * b}
+              for a in range(1, 6) for b in range(1, 6) for c in range(1, 6)}
+    dih = {}
+    for a in range(1, 3):
+        for b in range(1, 6):
+            for c in range(1, 6):
+                for d in range(1, 3):
+                    dih[(a, b, c, d)] = {
+                        "k1s": {f"k1_{i}": 0.1 * i * (a - d + 0.5) for i in (1, 2, 3)},
+                        "k2s": {f"k2_{i}": 0.2 / i * (b - c + 0.3) for i in (1, 2, 3)},
+                        "v_0": 0.05 * (a + b)}
+    rep = {(a, b): {"sigma": 3.5 + 0.1 * (a + b)} for a in range(1, 6) for b in range(1, 6)}
+    return bonds, angles, dih, rep
+
+
+def _md_config(n_frames=4, n_beads=20, seed=9, with_rep=True):
+    from mlcg_amd.data import AtomicData
+
+    rng = np.random.default_rng(seed)
+    from mlcg_amd import synthetic
+
+    pos3 = synthetic.self_avoiding_walk(n_frames, n_beads, rng)
+    confs = []
+    for f in range(n_frames):
+        types = torch.from_numpy(rng.integers(1, 6, n_beads))
+        types[::7] = 1  # dihedral table covers end types 1..2
+        types[0] = types[-1] = 1
+        topo = P.chain_topology(1, n_beads)
+        nl = {}
+        for name in ("bonds", "angles", "dihedrals") + (("repulsion",) if with_rep else ()):
+            nl[name] = {"index_mapping": topo[name][0], "order": topo[name][0].shape[0]}
+        confs.append(AtomicData(pos=torch.from_numpy(pos3[f]), atom_types=types,
+                                masses=torch.full((n_beads,), 12.0 / 418.4),
+                                n_atoms=torch.tensor([n_beads]), neighbor_list=nl))
+    return confs
+
+
+def _dihedral_types_ok(data):
+    m = data.neighbor_list["dihedrals"]["index_mapping"]
+    t = data.atom_types
+    return bool(((t[m[0]] <= 2) & (t[m[3]] <= 2)).all())
+
+
+def test_prior_modules_sumout_and_static():
+    """Module API: every prior through GradientsOut equals the oracle; SumOut
+    total equals the sum of its parts (tests/unit/nn/test_outs.py:134-166);
+    the condensed static priors give the same energies and forces."""
+    from mlcg_amd import nn
+    from mlcg_amd.data.atomic_data import collate
+    from mlcg_amd.simulation import condense_all_priors_for_simulation
+
+    bonds, angles, dih, rep = _stats_tables()
+    confs = _md_config()
+    # keep only dihedrals whose end types are in the table's range
+    for c in confs:
+        m = c.neighbor_list["dihedrals"]["index_mapping"]
+        keep = (c.atom_types[m[0]] <= 2) & (c.atom_types[m[3]] <= 2)
+        c.neighbor_list["dihedrals"]["index_mapping"] = m[:, keep]
+    priors = torch.nn.ModuleDict({
+        "bonds": nn.GradientsOut(nn.HarmonicBonds(bonds)),
+        "angles": nn.GradientsOut(nn.HarmonicAngles(angles)),
+        "dihedrals": nn.GradientsOut(nn.Dihedral(dih, n_degs=3)),
+        "repulsion": nn.GradientsOut(nn.Repulsion(rep))})
+    model = nn.SumOut(priors).cuda()
+    data = collate(confs).to("cuda")
+    out = model(data)
+    total_E = torch.zeros_like(out.out["energy"])
+    total_F = torch.zeros_like(out.out["forces"])
+    for name, gm in priors.items():
+        e = out.out[name]["energy"]
+        f = out.out[name]["forces"]
+        total_E += e
+        total_F += f
+        # against the oracle with the reference's type-table gather
+        prior = gm.model
+        pp = {k: v.double().cpu() for k, v in prior.data2parameters(data).items()}
+        if name == "repulsion":
+            pp = {"sigma": pp["sigma"]}
+        nlm = data.neighbor_list[name]
+        E_ref, F_ref = P.prior_energy_forces(name, data.pos.double().cpu(),
+                                             nlm["index_mapping"].cpu(),
+                                             nlm["mapping_batch"].cpu(), 4, pp)
+        assert rel_err(e, E_ref) < 1e-5, name
+        assert rel_err(f, F_ref) < 1e-5, name
+    assert torch.allclose(out.out["energy"], total_E, atol=1e-5)
+    assert torch.allclose(out.out["forces"], total_F, atol=1e-5)
+    # generic autograd route: forward energy, then grad wrt pos
+    d2 = collate(confs).to("cuda")
+    d2.pos.requires_grad_(True)
+    d2 = priors["dihedrals"].model(d2)
+    (gpos,) = torch.autograd.grad(d2.out["dihedrals"]["energy"].sum(), d2.pos)
+    assert rel_err(-gpos, out.out["dihedrals"]["forces"]) < 1e-6
+    # static specialisation
+    sp, sconfs = condense_all_priors_for_simulation(model.cpu(), confs)
+    sp = sp.cuda()
+    sdata = collate(sconfs).to("cuda")
+    sout = sp(sdata)
+    assert torch.allclose(sout.out["energy"], out.out["energy"], rtol=1e-6, atol=1e-5)
+    assert torch.allclose(sout.out["forces"], out.out["forces"], rtol=1e-6, atol=1e-5)
+
+
+def test_baoab_kernel_vs_oracle():
+    from mlcg_amd import ops
+
+    rng = np.random.default_rng(11)
+    n = 1000
+    x = torch.from_numpy(rng.normal(size=(n, 3)).astype(np.float32))
+    v = torch.from_numpy(rng.normal(size=(n, 3)).astype(np.float32))
+    F = torch.from_numpy(rng.normal(size=(n, 3)).astype(np.float32))
+    Fn = torch.from_numpy(rng.normal(size=(n, 3)).astype(np.float32))
+    m = torch.from_numpy(rng.uniform(0.02, 0.04, n).astype(np.float32))
+    bmr = torch.sqrt(1.0 / (L.beta_of(300.0) * m))
+    xi = torch.from_numpy(rng.normal(size=(n, 3)).astype(np.float32))
+    vs, ns = L.constants(0.004, 1.0)
+    xr, vr = L.baoa(x.double(), v.double(), F.double(), m.double(), bmr.double(), 0.004, vs,
+                    ns, xi.double())
+    vr = L.b(vr, Fn.double(), m.double(), 0.004)
+    xg, vg = x.cuda(), v.cuda()
+    step = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ops.langevin_baoa(xg, vg, F.cuda(), m.cuda(), bmr.cuda(), 0.004, vs, ns, 7, step=step,
+                      noise=xi.cuda())
+    ops.langevin_b(vg, Fn.cuda(), m.cuda(), 0.004, step=step)
+    assert rel_err(xg, xr) < 1e-6
+    assert rel_err(vg, vr) < 1e-6
+    assert int(step.item()) == 1
+
+
+def test_philox_normals_moments_and_streams():
+    from mlcg_amd import ops
+
+    z = ops.philox_normals(1234, 0, 400_000, "cuda").double()
+    assert abs(float(z.mean())) < 5e-3
+    assert abs(float(z.var()) - 1.0) < 1e-2
+    assert abs(float((z ** 3).mean())) < 1e-2
+    assert abs(float((z ** 4).mean()) - 3.0) < 3e-2
+    # components uncorrelated, steps and seeds give different streams
+    c = torch.corrcoef(z[:, :3].t().float())
+    assert float((c - torch.eye(3, device="cuda")).abs().max()) < 1e-2
+    z1 = ops.philox_normals(1234, 1, 1000, "cuda")
+    z2 = ops.philox_normals(1235, 0, 1000, "cuda")
+    assert not torch.equal(z1, z[:1000].float()) and not torch.equal(z2, z[:1000].float())
+    assert torch.equal(ops.philox_normals(1234, 0, 1000, "cuda"), z[:1000].float())
+
+
+def test_langevin_thermostat_equipartition():
+    """Soft harmonic bonds only, 256 chains of 12 beads at 300 K: after
+    equilibration the kinetic energy per degree of freedom is 1/(2 beta)
+    (the Maxwell-Boltzmann check of tests/unit/simulation/
+    test_simulation.py:451-472, here through the dynamics)."""
+    from mlcg_amd import nn
+    from mlcg_amd.simulation import LangevinSimulation
+
+    bonds = {(a, b): {"x_0": 3.8, "k": 5.0} for a in range(1, 6) for b in range(1, 6)}
+    confs = _md_config(n_frames=256, n_beads=12, with_rep=False)
+    for c in confs:
+        for k in ("angles", "dihedrals"):
+            c.neighbor_list.pop(k)
+    model = nn.SumOut(torch.nn.ModuleDict({"bonds": nn.GradientsOut(nn.HarmonicBonds(bonds))}))
+    beta = L.beta_of(300.0)
+    sim = LangevinSimulation(friction=10.0, dt=0.004, n_timesteps=3000, save_interval=1000,
+                             random_seed=3, capture=True)
+    sim.attach_model_and_configurations(model, confs, beta)
+    sim.simulate()
+    v = sim.final_data.velocities.double()
+    m = sim.final_data.masses.double()
+    ke_per_dof = float((0.5 * m[:, None] * v * v).mean())
+    assert ke_per_dof == pytest.approx(0.5 / beta, rel=0.08)
+
+
+def test_radius_graph_capacity_mode():
+    from mlcg_amd import ops, synthetic
+
+    b = synthetic.config2(n_frames=32)
+    pos = torch.from_numpy(b.pos).cuda()
+    batch = torch.from_numpy(b.batch).cuda()
+    g = ops.radius_graph(pos, 20.0, batch, False, 1000, with_pairs=True, n_frames=32)
+    gc = ops.radius_graph(pos, 20.0, batch, False, 1000, with_pairs=True, n_frames=32,
+                          capacity=g.num_edges + 100)
+    E, P_ = g.num_edges, g.num_pairs
+    assert int(gc.flags.item()) == 0
+    assert torch.equal(gc.edge_index[:, :E], g.edge_index)
+    assert torch.equal(gc.rowptr, g.rowptr)
+    assert torch.equal(gc.pair_ij[:, :P_], g.pair_ij)
+    assert torch.equal(gc.eid2pair[:E], g.eid2pair)
+    assert int(gc.n_pairs_dev.item()) == P_
+    small = ops.radius_graph(pos, 20.0, batch, False, 1000, with_pairs=True, n_frames=32,
+                             capacity=E // 2)
+    assert int(small.flags.item()) & 2
+    assert int(small.rowptr[-1].item()) <= E // 2
+    assert int(small.eid2pair.max().item()) < E // 4 + 1
+
+
+def test_md_step_captured_matches_eager():
+    """SchNet (config-2 architecture, rc 20) + priors on 268-bead chains: the
+    hipGraph-captured BAOAB step replays give the same trajectory as the eager
+    loop (every replay checked through the saved frames)."""
+    from mlcg_amd import nn
+    from mlcg_amd.simulation import LangevinSimulation
+
+    bonds, angles, dih, rep = _stats_tables()
+
+    def build():
+        torch.manual_seed(0)
+        rbf = nn.GaussianBasis(nn.CosineCutoff(0, 20.0), num_rbf=50)
+        schnet = nn.StandardSchNet(rbf, nn.CosineCutoff(0, 20.0), [64], 128, 100, 128, 3,
+                                   torch.nn.Tanh())
+        return nn.SumOut(torch.nn.ModuleDict({
+            "SchNet": nn.GradientsOut(schnet),
+            "bonds": nn.GradientsOut(nn.HarmonicBonds(bonds)),
+            "angles": nn.GradientsOut(nn.HarmonicAngles(angles)),
+            "repulsion": nn.GradientsOut(nn.Repulsion(rep))}))
+
+    confs = _md_config(n_frames=3, n_beads=60)
+    for c in confs:
+        c.neighbor_list.pop("dihedrals")
+    trajs = []
+    for capture in (False, True):
+        sim = LangevinSimulation(friction=1.0, dt=0.004, n_timesteps=12, save_interval=1,
+                                 random_seed=21, capture=capture, save_energies=True)
+        sim.attach_model_and_configurations(build(), [c.clone() for c in confs],
+                                            L.beta_of(300.0))
+        trajs.append((sim.simulate(), sim.simulated_potential))
+    (x0, e0), (x1, e1) = trajs
+    assert np.isfinite(x0).all()
+    np.testing.assert_allclose(x1, x0, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(e1, e0, rtol=1e-5, atol=1e-4)
