@@ -22,7 +22,7 @@ def radius_graph(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None
 
     With flow="target_to_source" row 0 is the centre (as mlcg calls it,
     torch_impl.py:216-224); "source_to_target" swaps the rows."""
-    g = ops.radius_graph(x.detach(), r, batch=batch, loop=loop,
+    g = ops.radius_graph(x.detach().float(), r, batch=batch, loop=loop,
                          max_num_neighbors=max_num_neighbors)
     ei = g.edge_index
     if flow == "source_to_target":
@@ -36,7 +36,9 @@ def radius_distance_fn(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] 
                        loop: bool = False, max_num_neighbors: int = 32,
                        batch_size: Optional[int] = None):
     """(edge_index [2, E], distance [E]) like radius.py:52-88."""
-    g = ops.radius_graph(x.detach(), r, batch=batch, loop=loop,
+    # membership is decided in fp32 (the kernel's arithmetic); the distances
+    # themselves are computed in x's dtype so fp64 gradchecks stay exact
+    g = ops.radius_graph(x.detach().float(), r, batch=batch, loop=loop,
                          max_num_neighbors=max_num_neighbors, n_frames=batch_size)
     ei = g.edge_index
     d = (x.detach()[ei[0]] - x.detach()[ei[1]]).norm(dim=1)
