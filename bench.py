@@ -22,6 +22,10 @@ Besides the JSON contract fields the line carries
   kernels       -- the same figures for every HIP kernel of the step;
   radius_graph  -- config 3 (2048 x 100-bead globules, 15 A): edges/s of the
                    HIP radius graph, inputs resident;
+  fp16_config4  -- config 4 (256 x 500 beads, fp16 filter linears): energy +
+                   forces per call, and the fp16 filter kernel's MFMA fraction;
+  md_config5    -- config 5 (100 x 268-bead Langevin replicas, SchNet +
+                   priors, captured step): MD steps/s;
   cpu_baseline  -- the CPU restatement (oracle/schnet_ref.py) of the same
                    step on a bounded sample of frames, host threads stated.
 """
@@ -59,6 +63,9 @@ def parse_args(argv=None):
     p.add_argument("--frames", type=int, default=512, help="config-2 frames per step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-radius", action="store_true", help="skip the config-3 radius leg")
+    p.add_argument("--no-fp16", action="store_true", help="skip the config-4 fp16 leg")
+    p.add_argument("--no-md", action="store_true", help="skip the config-5 MD leg")
+    p.add_argument("--md-steps", type=int, default=200, help="MD steps of the config-5 leg")
     p.add_argument("--cpu-frames", type=int, default=32,
                    help="frames in the CPU baseline sample")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -113,7 +120,7 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
 # entry point -> kernel symbol(s) it launches (as rocprofv3 names them)
 KERNEL_SYMBOL = {
     "mlcg_filter_fwd": "filter_fwd_f32_kernel",
-    "mlcg_filter_bwd": "filter_bwd_f32_kernel",
+    "mlcg_filter_bwd": "filter_bwd_fused_kernel",
     "mlcg_cfconv_gather": "gather_kernel",
     "mlcg_cfconv_gather_bwd": "gather_bwd_kernel",
     "mlcg_cfconv_gather_tangent": "gather_tangent_kernel",
@@ -262,6 +269,85 @@ def radius_leg(reps=10):
             "algorithmic_bytes": 12 * pos.shape[0] + 8 * (nf + 1) + 16 * E}
 
 
+def fp16_leg(reps=5):
+    """Config 4: 256 frames x 500-bead globules, rc 15 A, fp16 filter linears
+    with fp32 accumulation; energy + forces (inference) per call."""
+    import torch
+
+    from mlcg_amd import _lib, nn, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(synthetic.seed_for(4))
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, 15.0), num_rbf=K_RBF)
+    model = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, 15.0), [64], H, 100, F, N_BLOCKS,
+                              torch.nn.Tanh()).to(dev)
+    model.fp16_filters = True
+    gm = nn.GradientsOut(model).eval()
+    b = synthetic.config4()
+    data = b.to_torch(dev)
+    with torch.no_grad():
+        gm(data)
+        torch.cuda.synchronize()
+        E, P = model.last_graph.num_edges, model.last_graph.num_pairs
+        t = []
+        timer = _lib.LaunchTimer({"mlcg_filter_fwd"})
+        for _ in range(reps):
+            _lib.set_timer(timer)
+            t0 = time.perf_counter()
+            gm(data)
+            torch.cuda.synchronize()
+            t.append(time.perf_counter() - t0)
+            _lib.set_timer(None)
+    s = statistics.median(t)
+    n_l, tot = timer.summary()["mlcg_filter_fwd"]
+    avg = tot / n_l
+    flops = 2 * 2 * (K_RBF * F + F * F) * P
+    ach = flops / (avg * 1e-3) / 1e12
+    return {"workload": "config4: 256 frames x 500-bead globules, rc 15 A, fp16 filter "
+                        "linears (fp32 accumulate), energy + forces",
+            "edges": E, "ms_per_call": round(s * 1e3, 3),
+            "cfconv_edges_per_s": E * N_BLOCKS / s, "frames_per_s": b.n_frames / s,
+            "filter_roofline": {"kernel": "filter_fwd_f16_kernel", "bound": "mfma",
+                                "achieved": round(ach, 2), "peak": FP16_MFMA_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(ach / FP16_MFMA_PEAK_TFLOPS, 4),
+                                "avg_launch_us": round(avg * 1e3, 2)}}
+
+
+def md_leg(steps):
+    """Config 5: 100 replicas x 268-bead chains, config-2 SchNet (rc 20 A) +
+    bonds, angles, 3-term dihedrals and (sigma/r)^6 repulsion, BAOAB at 300 K,
+    dt 4 fs, friction 1/ps; radius graph rebuilt every step; the step is
+    captured once as a HIP graph and replayed."""
+    import torch
+
+    from mlcg_amd import nn, synthetic
+    from mlcg_amd.simulation import LangevinSimulation
+
+    c = synthetic.CONFIG5_PRIORS
+    torch.manual_seed(synthetic.seed_for(5))
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, RC), num_rbf=K_RBF)
+    schnet = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, RC), [64], H, 100, F, N_BLOCKS,
+                               torch.nn.Tanh())
+    models = {"SchNet": nn.GradientsOut(schnet)}
+    for k, v in synthetic.config5_prior_models().items():
+        models[k] = nn.GradientsOut(v)
+    model = nn.SumOut(torch.nn.ModuleDict(models))
+    confs = synthetic.config5_configurations()
+    beta = 1.0 / (0.0019872041 * c["temperature_K"])
+    n = steps + 3
+    sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"], n_timesteps=n,
+                             save_interval=n, random_seed=synthetic.seed_for(5), capture=True,
+                             check_interval=n)
+    sim.attach_model_and_configurations(model, confs, beta)
+    sim.simulate()
+    sps = sim.timed_steps / sim.timed_seconds
+    return {"workload": "config5: 100 x 268-bead chains, SchNet (3 blocks, rc 20 A) + "
+                        "bonds/angles/dihedrals/repulsion priors, BAOAB, HIP-graph step",
+            "steps_timed": sim.timed_steps, "ms_per_step": round(1e3 / sps, 4),
+            "steps_per_s": sps, "replica_steps_per_s": sps * sim.n_sims,
+            "edge_capacity": schnet.graph_capacity, "prior_constants": c}
+
+
 def cpu_leg(args):
     """The CPU restatement of the same step on a bounded sample of frames."""
     import torch
@@ -328,6 +414,12 @@ def main(argv=None):
     rg = None if args.no_radius else radius_leg()
     if rg:
         print(f"[bench] radius leg done: {rg['ms']:.3f} ms", flush=True)
+    f16 = None if args.no_fp16 else fp16_leg()
+    if f16:
+        print(f"[bench] fp16 leg done: {f16['ms_per_call']:.3f} ms/call", flush=True)
+    md = None if args.no_md else md_leg(args.md_steps)
+    if md:
+        print(f"[bench] md leg done: {md['ms_per_step']:.3f} ms/step", flush=True)
     cpu = None if args.no_cpu else cpu_leg(args)
     if cpu:
         print(f"[bench] cpu leg done: {cpu['ms_per_step']:.1f} ms/step", flush=True)
@@ -363,6 +455,8 @@ def main(argv=None):
         "kernels": g["kernels"],
         "step_kernel_ms": g["step_kernel_ms"],
         "radius_graph": rg,
+        "fp16_config4": f16,
+        "md_config5": md,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

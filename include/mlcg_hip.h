@@ -121,13 +121,18 @@ int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
                     int num_filters, int f16, void* W_out, void* Wd_out,
                     float* dist_out, void* stream);
 
-/* Reverse of the filter chain for given pair adjoints Wbar = dL/dW and
- * Wdbar = dL/dWd ([max_pairs, F] fp32).  Writes the per-pair factors of the
- * weight gradients: H = [h ; h'] [2, max_pairs, F], T = [wbar ; w'bar]
- * [2, max_pairs, F], A = [abar ; a'bar] [2, max_pairs, F] and
- * G = [g ; g'] [2, max_pairs, Kp] with Kp = 4 ceil(K / 4).  Rows past the live
- * pair count are zero, so dW2 = T^T H, dW1 = A^T G and db1 = sum(A[0]).
- * Replaces the autograd double backward through mlp.py/gaussian.py. */
+/* Parameter gradients of the filter chain for given pair adjoints
+ * Wbar = dL/dW and Wdbar = dL/dWd ([max_pairs, F] fp32, rows past the live
+ * pair count ignored):
+ *   dW1 [F, K] = d/dW1, db1 [F] = d/db1, dW2 [F, F] = d/dW2
+ * of <Wbar, W> + <Wdbar, dW/dd>.  The per-pair reverse products and the pair
+ * reductions run in one kernel (per-workgroup partial sums in `workspace`,
+ * then a fixed-order reduction), so nothing per pair is written to memory.
+ * `workspace` holds mlcg_filter_bwd_workspace_floats(max_pairs, num_rbf)
+ * floats.  Replaces the autograd double backward through mlp.py:56-58 and
+ * gaussian.py:98-102 (the parameter half of the create_graph=True backward
+ * of gradients.py:216-222). */
+int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_rbf);
 int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij,
                     int64_t pair_stride, const int32_t* n_pairs_dev,
                     int64_t max_pairs, const float* offsets, float coeff,
@@ -135,7 +140,8 @@ int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij,
                     int conv_cut_kind, float conv_lo, float conv_hi, int act,
                     const float* W1, const float* b1, const float* W2,
                     int num_filters, const float* Wbar, const float* Wdbar,
-                    float* H, float* T, float* A, float* G, void* stream);
+                    float* dW1, float* db1, float* dW2, float* workspace,
+                    int64_t workspace_floats, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* CFConv gather/scatter over the receiver CSR (rowptr, col, eid2pair)      */

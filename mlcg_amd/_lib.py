@@ -43,8 +43,10 @@ _SIGNATURES = {
     "mlcg_pair_reverse_map": [_P, _I64, _P, _I64, _P, _P, _P, _P],
     "mlcg_filter_fwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
                         _F32, _F32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],
+    "mlcg_filter_bwd_workspace_floats": [_I64, _I32],
     "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
-                        _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P],
+                        _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64,
+                        _P],
     "mlcg_cfconv_gather": [_P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
     "mlcg_cfconv_gather_tangent": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
@@ -61,7 +63,8 @@ _SIGNATURES = {
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
 }
-_RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64}
+_RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
+             "mlcg_filter_bwd_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

@@ -278,7 +278,13 @@ __device__ void stage_f16(_Float16* w1h, _Float16* w2h, const float* __restrict_
   }
 }
 
-__global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
+// 4 waves per workgroup (one per SIMD): the fp16 tile keeps more operand
+// fragments live than the fp32 one, and one wave per SIMD gets the full
+// register file, so nothing spills.
+constexpr int kWaves16 = 4;
+constexpr int kThreads16 = kWaves16 * MLCG_WAVE;
+
+__global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
     int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
@@ -288,7 +294,11 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
   const int KS32 = (rp.K + 31) / 32;
   _Float16* w1h = reinterpret_cast<_Float16*>(lds);
   _Float16* w2h = w1h + kFT * KS32 * MLCG_WAVE * 8;
+  // the bias lives in LDS here (not registers): the fp16 path keeps more
+  // operand fragments live and would otherwise spill
+  float* b1s = reinterpret_cast<float*>(w2h + kFT * (kFT / 2) * MLCG_WAVE * 8);
   stage_f16(w1h, w2h, W1, W2, rp.K, KS32);
+  for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
   __syncthreads();
 
   int64_t np = *n_pairs_dev;
@@ -296,16 +306,11 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
   const int64_t tiles = (np + 15) / 16;
   const int l = mlcg_lane();
   const int q = l >> 4;
-  float bias[kFT][4];
-#pragma unroll
-  for (int t = 0; t < kFT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bias[t][i] = b1[16 * t + 4 * q + i];
 
   const halfx8* w1v = reinterpret_cast<const halfx8*>(w1h);
   const halfx8* w2v = reinterpret_cast<const halfx8*>(w2h);
-  const int64_t wave = (int64_t)blockIdx.x * kWaves + threadIdx.x / MLCG_WAVE;
-  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+  const int64_t wave = (int64_t)blockIdx.x * kWaves16 + threadIdx.x / MLCG_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves16;
   for (int64_t tile = wave; tile < tiles; tile += nwaves) {
     const int64_t p = tile * 16 + (l & 15);
     const bool valid = p < np;
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float s, d1, d2;
-        mlcg_act(rp.act, a[t][i] + bias[t][i], s, d1, d2);
+        mlcg_act(rp.act, a[t][i] + b1s[16 * t + 4 * q + i], s, d1, d2);
         h8[t >> 1][4 * (t & 1) + i] = (_Float16)s;
         hd8[t >> 1][4 * (t & 1) + i] = (_Float16)(d1 * ad[t][i]);
       }
@@ -380,135 +385,272 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f16_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Reverse of the chain for given Wbar, Wdbar (fp32).  Per pair:
-//   wbar  = Wbar C + Wdbar C'       w'bar = Wdbar C
-//   hbar  = W2^T wbar               h'bar = W2^T w'bar
-//   abar  = hbar act'(a) + h'bar act''(a) a'      a'bar = h'bar act'(a)
-// The weight gradients are the pair-reductions dW2 = sum wbar h^T + w'bar h'^T,
-// dW1 = sum abar g^T + a'bar g'^T and db1 = sum abar; this kernel writes the
-// per-pair factors so that they are plain GEMMs.
-__global__ __launch_bounds__(kThreads) void filter_bwd_f32_kernel(
+// Reverse of the chain with the weight-gradient reductions fused in (fp32).
+//
+// For given pair adjoints Wbar = dL/dW and Wdbar = dL/dWd, per pair:
+//   t   = Wbar C + Wdbar C'            t'  = Wdbar C
+//   hb  = W2^T t                       hb' = W2^T t'
+//   ab  = hb act'(a) + hb' act''(a) a' ab' = hb' act'(a)
+// and the parameter gradients are pair sums
+//   dW2 = sum_p t h^T + t' h'^T,  dW1 = sum_p ab g^T + ab' g'^T,  db1 = sum_p ab.
+//
+// Work split: a workgroup of 8 waves walks 16-pair tiles; wave w owns feature
+// tile w (features 16w..16w+15) in every product, so it needs only its slice
+// of W1 (one A fragment per k step) and of W2^T (8 float4 fragments), both
+// kept in registers for the whole kernel.  Per tile:
+//   1. every wave recomputes g, g' for the 16 pairs (B operand layout) and
+//      a, a' of its feature tile (v_mfma_f32_16x16x4f32);
+//   2. it forms t, t', h, h' of its features and publishes them in LDS as
+//      [pair][feature] rows;
+//   3. hb, hb' of its tile: B operands read from LDS (all 128 features);
+//   4. dW2 rows of its tile += t^T h over the 16 pairs (the pair index is the
+//      MFMA reduction axis; operands read from the LDS rows);
+//   5. ab, ab' replace t, t' in LDS; dW1 rows of its tile += ab^T g.
+// The accumulators stay in registers across all tiles of the workgroup; at
+// the end each workgroup writes its partial sums, and filter_bwd_reduce adds
+// the partials in workgroup order, so the result is deterministic.  Nothing
+// per pair is written to HBM.
+constexpr int kBwdWaves = 8;
+constexpr int kBwdThreads = kBwdWaves * MLCG_WAVE;
+constexpr int kRowPad = 4;
+constexpr int kXRow = kF + kRowPad;  // LDS row of one pair's 128 features
+
+__host__ __device__ constexpr int bwd_kp16(int K) { return 16 * ((K + 15) / 16); }
+__host__ __device__ constexpr int bwd_partial_floats(int K) {
+  return kF * kF + kF * bwd_kp16(K) + kF;
+}
+__host__ __device__ constexpr int bwd_lds_floats(int K) {
+  return 2 * 16 * kXRow * 2 + 2 * 16 * (bwd_kp16(K) + 4);
+}
+
+template <int KSMAX>
+__global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
     int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
     const float* __restrict__ b1, const float* __restrict__ W2,
-    const float* __restrict__ Wbar, const float* __restrict__ Wdbar, float* __restrict__ H,
-    float* __restrict__ T, float* __restrict__ A, float* __restrict__ G) {
+    const float* __restrict__ Wbar, const float* __restrict__ Wdbar,
+    float* __restrict__ partial) {
+  constexpr int KTMAX = (4 * KSMAX + 15) / 16;
   extern __shared__ float lds[];
-  const int KS = (rp.K + 3) / 4;
-  const int Kp = 4 * KS;
-  float* w1s = lds;
-  float* w2ts = lds + kFT * KS * MLCG_WAVE;
-  stage_w1_f32(w1s, W1, rp.K, KS);
-  stage_w2_f32(w2ts, W2, true);
+  const int K = rp.K;
+  const int KS = (K + 3) / 4;
+  const int Kp16 = bwd_kp16(K);
+  const int KT = Kp16 / 16;
+  const int gRow = Kp16 + 4;
+  float* TB = lds;                   // [2][16][kXRow]  t, t'  (later ab, ab')
+  float* HH = TB + 2 * 16 * kXRow;   // [2][16][kXRow]  h, h'
+  float* GG = HH + 2 * 16 * kXRow;   // [2][16][gRow]   g, g'
+  const int w = threadIdx.x / MLCG_WAVE;
+  const int l = mlcg_lane();
+  const int q = l >> 4, n = l & 15;
+
+  for (int x = threadIdx.x; x < 2 * 16 * gRow; x += blockDim.x) GG[x] = 0.0f;
+
+  // register-resident weight fragments of feature tile w
+  float w1f[KSMAX];
+#pragma unroll
+  for (int s = 0; s < KSMAX; ++s) {
+    const int k = 4 * s + q;
+    w1f[s] = (s < KS && k < K) ? W1[(16 * w + n) * K + k] : 0.0f;
+  }
+  float4 a2[kFT];  // A fragments of W2^T: a2[u].i = W2[16u + 4q + i][16w + n]
+#pragma unroll
+  for (int u = 0; u < kFT; ++u) {
+    const int c0 = 16 * u + 4 * q;
+    a2[u].x = W2[(c0 + 0) * kF + 16 * w + n];
+    a2[u].y = W2[(c0 + 1) * kF + 16 * w + n];
+    a2[u].z = W2[(c0 + 2) * kF + 16 * w + n];
+    a2[u].w = W2[(c0 + 3) * kF + 16 * w + n];
+  }
+  float bias[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bias[i] = b1[16 * w + 4 * q + i];
+
+  floatx4 acc2[kFT];
+#pragma unroll
+  for (int u = 0; u < kFT; ++u) acc2[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 acc1[KTMAX];
+#pragma unroll
+  for (int kt = 0; kt < KTMAX; ++kt) acc1[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
   __syncthreads();
 
-  int64_t np = *n_pairs_dev;
+  int64_t np = max_pairs > 0 ? *n_pairs_dev : 0;
   if (np > max_pairs) np = max_pairs;
-  const int64_t tiles = (max_pairs + 15) / 16;
-  const int l = mlcg_lane();
-  const int q = l >> 4;
-  float bias[kFT][4];
-#pragma unroll
-  for (int t = 0; t < kFT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bias[t][i] = b1[16 * t + 4 * q + i];
+  const int64_t tiles = (np + 15) / 16;
+  const int fcol = 16 * w + 4 * q;  // first of the lane's 4 features in row layout
 
-  const int64_t wave = (int64_t)blockIdx.x * kWaves + threadIdx.x / MLCG_WAVE;
-  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
-  const int64_t slab = max_pairs * kF;  // stride between [0] and [1] halves
-  const int64_t gslab = max_pairs * Kp;
-  for (int64_t tile = wave; tile < tiles; tile += nwaves) {
-    const int64_t p = tile * 16 + (l & 15);
-    const bool inrange = p < max_pairs;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t p = tile * 16 + n;
     const bool valid = p < np;
-    if (tile * 16 >= np) {
-      // whole tile past the live count: zero rows so the GEMMs ignore them
-      if (inrange) {
-        const float4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < kFT; ++t) {
-          const int64_t off = p * kF + 16 * t + 4 * q;
-          *reinterpret_cast<float4*>(H + off) = z;
-          *reinterpret_cast<float4*>(H + slab + off) = z;
-          *reinterpret_cast<float4*>(T + off) = z;
-          *reinterpret_cast<float4*>(T + slab + off) = z;
-          *reinterpret_cast<float4*>(A + off) = z;
-          *reinterpret_cast<float4*>(A + slab + off) = z;
-        }
-        for (int s = 0; s < KS; ++s) {
-          G[p * Kp + 4 * s + q] = 0.f;
-          G[gslab + p * Kp + 4 * s + q] = 0.f;
-        }
-      }
-      continue;
-    }
     const float d = pair_distance(pos, pi, pj, p, valid);
     float crbf, dcrbf, cc, dcc;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
     mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
 
-    floatx4 a[kFT], ad[kFT];
-    // g/g' rows are written straight from the B-operand registers
-    gemm1_f32(w1s, KS, rp, d, crbf, dcrbf, a, ad, inrange ? G + p * Kp : nullptr,
-              inrange ? G + gslab + p * Kp : nullptr, valid ? 1.0f : 0.0f);
-    floatx4 act1[kFT], act2[kFT];
+    // 1. a, a' of feature tile w; wave w publishes the g columns of its k steps
+    floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < kFT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float s, d1, d2;
-        mlcg_act(rp.act, a[t][i] + bias[t][i], s, d1, d2);
-        a[t][i] = s;                 // h
-        act1[t][i] = d1;
-        act2[t][i] = d2 * ad[t][i];  // act''(a) a'
-        ad[t][i] = d1 * ad[t][i];    // h'
-      }
-    floatx4 tb[kFT], tdb[kFT];
-#pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      float4 wb = {0.f, 0.f, 0.f, 0.f}, wdb = {0.f, 0.f, 0.f, 0.f};
-      if (valid) {
-        wb = *reinterpret_cast<const float4*>(Wbar + p * kF + 16 * t + 4 * q);
-        wdb = *reinterpret_cast<const float4*>(Wdbar + p * kF + 16 * t + 4 * q);
-      }
-      tb[t][0] = wb.x * cc + wdb.x * dcc;
-      tb[t][1] = wb.y * cc + wdb.y * dcc;
-      tb[t][2] = wb.z * cc + wdb.z * dcc;
-      tb[t][3] = wb.w * cc + wdb.w * dcc;
-      tdb[t][0] = wdb.x * cc;
-      tdb[t][1] = wdb.y * cc;
-      tdb[t][2] = wdb.z * cc;
-      tdb[t][3] = wdb.w * cc;
-    }
-    floatx4 hb[kFT], hdb[kFT];
-    gemm2_f32(w2ts, tb, tdb, hb, hdb);
-    if (inrange) {
-#pragma unroll
-      for (int t = 0; t < kFT; ++t) {
-        float4 ab, adb;
-        ab.x = hb[t][0] * act1[t][0] + hdb[t][0] * act2[t][0];
-        ab.y = hb[t][1] * act1[t][1] + hdb[t][1] * act2[t][1];
-        ab.z = hb[t][2] * act1[t][2] + hdb[t][2] * act2[t][2];
-        ab.w = hb[t][3] * act1[t][3] + hdb[t][3] * act2[t][3];
-        adb.x = hdb[t][0] * act1[t][0];
-        adb.y = hdb[t][1] * act1[t][1];
-        adb.z = hdb[t][2] * act1[t][2];
-        adb.w = hdb[t][3] * act1[t][3];
-        const float m = valid ? 1.0f : 0.0f;
-        const int64_t off = p * kF + 16 * t + 4 * q;
-        *reinterpret_cast<float4*>(H + off) =
-            float4{a[t][0] * m, a[t][1] * m, a[t][2] * m, a[t][3] * m};
-        *reinterpret_cast<float4*>(H + slab + off) =
-            float4{ad[t][0] * m, ad[t][1] * m, ad[t][2] * m, ad[t][3] * m};
-        *reinterpret_cast<float4*>(T + off) = float4{tb[t][0], tb[t][1], tb[t][2], tb[t][3]};
-        *reinterpret_cast<float4*>(T + slab + off) =
-            float4{tdb[t][0], tdb[t][1], tdb[t][2], tdb[t][3]};
-        *reinterpret_cast<float4*>(A + off) = ab;
-        *reinterpret_cast<float4*>(A + slab + off) = adb;
+    for (int s = 0; s < KSMAX; ++s) {
+      if (s < KS) {
+        float g, gd;
+        rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);
+        if ((s & (kBwdWaves - 1)) == w) {
+          GG[n * gRow + 4 * s + q] = valid ? g : 0.0f;
+          GG[16 * gRow + n * gRow + 4 * s + q] = valid ? gd : 0.0f;
+        }
+        a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
+        ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
       }
     }
+    // 2. h, h', activation derivatives and t, t' of the lane's 4 features
+    float h[4], hd[4], act1[4], act2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv, d1, d2;
+      mlcg_act(rp.act, a[i] + bias[i], sv, d1, d2);
+      h[i] = valid ? sv : 0.0f;
+      act1[i] = d1;
+      act2[i] = d2 * ad[i];
+      hd[i] = valid ? d1 * ad[i] : 0.0f;
+    }
+    float4 wb = {0.f, 0.f, 0.f, 0.f}, wdb = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+      wb = *reinterpret_cast<const float4*>(Wbar + p * kF + fcol);
+      wdb = *reinterpret_cast<const float4*>(Wdbar + p * kF + fcol);
+    }
+    const float4 tb = {wb.x * cc + wdb.x * dcc, wb.y * cc + wdb.y * dcc,
+                       wb.z * cc + wdb.z * dcc, wb.w * cc + wdb.w * dcc};
+    const float4 tdb = {wdb.x * cc, wdb.y * cc, wdb.z * cc, wdb.w * cc};
+    *reinterpret_cast<float4*>(TB + n * kXRow + fcol) = tb;
+    *reinterpret_cast<float4*>(TB + 16 * kXRow + n * kXRow + fcol) = tdb;
+    *reinterpret_cast<float4*>(HH + n * kXRow + fcol) = float4{h[0], h[1], h[2], h[3]};
+    *reinterpret_cast<float4*>(HH + 16 * kXRow + n * kXRow + fcol) =
+        float4{hd[0], hd[1], hd[2], hd[3]};
+    __syncthreads();
+
+    // 3. hb, hb' of feature tile w (all 128 t features from LDS)
+    floatx4 hb = {0.f, 0.f, 0.f, 0.f}, hdb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kFT; ++u) {
+      const float4 bx = *reinterpret_cast<const float4*>(TB + n * kXRow + 16 * u + 4 * q);
+      const float4 by =
+          *reinterpret_cast<const float4*>(TB + 16 * kXRow + n * kXRow + 16 * u + 4 * q);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].x, bx.x, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].x, by.x, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].y, bx.y, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].y, by.y, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].z, bx.z, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].z, by.z, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].w, bx.w, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].w, by.w, hdb, 0, 0, 0);
+    }
+    float ab[4], adb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ab[i] = hb[i] * act1[i] + hdb[i] * act2[i];
+      adb[i] = hdb[i] * act1[i];
+      db[i] += ab[i];
+    }
+    // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c]
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const float* T = TB + st * 16 * kXRow;
+      const float* Hs = HH + st * 16 * kXRow;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float av = T[(4 * kk + q) * kXRow + 16 * w + n];
+#pragma unroll
+        for (int u = 0; u < kFT; ++u) {
+          const float bv = Hs[(4 * kk + q) * kXRow + 16 * u + n];
+          acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc2[u], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+    // 5. ab, ab' replace t, t'; dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
+    *reinterpret_cast<float4*>(TB + n * kXRow + fcol) = float4{ab[0], ab[1], ab[2], ab[3]};
+    *reinterpret_cast<float4*>(TB + 16 * kXRow + n * kXRow + fcol) =
+        float4{adb[0], adb[1], adb[2], adb[3]};
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const float* A = TB + st * 16 * kXRow;
+      const float* G = GG + st * 16 * gRow;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float av = A[(4 * kk + q) * kXRow + 16 * w + n];
+#pragma unroll
+        for (int kt = 0; kt < KTMAX; ++kt) {
+          if (kt < KT) {
+            const float bv = G[(4 * kk + q) * gRow + 16 * kt + n];
+            acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc1[kt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    __syncthreads();
   }
+
+  // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
+  float* out = partial + (int64_t)blockIdx.x * bwd_partial_floats(K);
+#pragma unroll
+  for (int u = 0; u < kFT; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[(16 * w + 4 * q + r) * kF + 16 * u + n] = acc2[u][r];
+  float* o1 = out + kF * kF;
+#pragma unroll
+  for (int kt = 0; kt < KTMAX; ++kt)
+    if (kt < KT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o1[(16 * w + 4 * q + r) * Kp16 + 16 * kt + n] = acc1[kt][r];
+  // db1: sum the 16 pair lanes that share q (fixed butterfly order)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = db[i];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, MLCG_WAVE);
+    db[i] = v;
+  }
+  if (n == 0) {
+    float* o2 = o1 + kF * Kp16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o2[16 * w + 4 * q + i] = db[i];
+  }
+}
+
+// dW2 [F, F], dW1 [F, K], db1 [F] = sum over workgroup partials (in order).
+__global__ __launch_bounds__(256) void filter_bwd_reduce_kernel(
+    const float* __restrict__ partial, int groups, int K, float* __restrict__ dW1,
+    float* __restrict__ db1, float* __restrict__ dW2) {
+  const int Kp16 = bwd_kp16(K);
+  const int stride = bwd_partial_floats(K);
+  const int total = kF * kF + kF * K + kF;
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < total; j += gridDim.x * blockDim.x) {
+    int src;
+    float* dst;
+    if (j < kF * kF) {
+      src = j;
+      dst = dW2 + j;
+    } else if (j < kF * kF + kF * K) {
+      const int r = j - kF * kF;
+      src = kF * kF + (r / K) * Kp16 + (r % K);
+      dst = dW1 + r;
+    } else {
+      const int r = j - kF * kF - kF * K;
+      src = kF * kF + kF * Kp16 + r;
+      dst = db1 + r;
+    }
+    float acc = 0.f;
+    for (int g = 0; g < groups; ++g) acc += partial[(int64_t)g * stride + src];
+    *dst = acc;
+  }
+}
+
+int bwd_groups(int64_t max_pairs) {
+  const int64_t tiles = (max_pairs + 15) / 16;
+  return (int)(tiles < 256 ? (tiles < 1 ? 1 : tiles) : 256);
 }
 
 // Kernels here use more than 64 KiB of dynamic LDS; raise their limit to the
@@ -522,8 +664,6 @@ void allow_lds_once() {
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f32_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_f32_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   done[dev] = true;
 }
@@ -578,13 +718,20 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
   } else {
     const int KS32 = (num_rbf + 31) / 32;
     const size_t lds =
-        sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8);
+        sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
+        sizeof(float) * kF;
     allow_lds_once();
-    hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
+    const unsigned groups16 = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves16), 1);
+    hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups16), dim3(kThreads16), lds, s, pos,
                        pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
                        static_cast<__half*>(W_out), static_cast<__half*>(Wd_out), dist_out);
   }
   return mlcg_launch_status();
+}
+
+extern "C" int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_rbf) {
+  if (max_pairs < 0 || num_rbf < 1 || num_rbf > kMaxK) return -1;
+  return (int64_t)bwd_groups(max_pairs) * bwd_partial_floats(num_rbf);
 }
 
 extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
@@ -594,21 +741,35 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
                                int conv_cut_kind, float conv_lo, float conv_hi, int act,
                                const float* W1, const float* b1, const float* W2,
                                int num_filters, const float* Wbar, const float* Wdbar,
-                               float* H, float* T, float* A, float* G, void* stream) {
+                               float* dW1, float* db1, float* dW2, float* workspace,
+                               int64_t workspace_floats, void* stream) {
   if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
     return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
-  if (max_pairs == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && pair_ij && n_pairs_dev && offsets && W1 && b1 && W2 && Wbar && Wdbar &&
-               H && T && A && G);
+  MLCG_REQUIRE(offsets && W1 && b1 && W2 && dW1 && db1 && dW2 && workspace);
+  MLCG_REQUIRE(max_pairs == 0 || (pos && pair_ij && n_pairs_dev && Wbar && Wdbar));
+  const int groups = bwd_groups(max_pairs);
+  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * bwd_partial_floats(num_rbf));
   RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
                              conv_cut_kind, conv_lo, conv_hi, act);
-  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
-  const int KS = (num_rbf + 3) / 4;
-  const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
-  allow_lds_once();
-  hipLaunchKernelGGL(filter_bwd_f32_kernel, dim3(groups), dim3(kThreads), lds,
-                     mlcg_stream(stream), pos, pair_ij, pair_ij + pair_stride, n_pairs_dev,
-                     max_pairs, rp, W1, b1, W2, Wbar, Wdbar, H, T, A, G);
+  hipStream_t s = mlcg_stream(stream);
+  const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
+  if (max_pairs == 0) {
+    // no pairs: every gradient is zero (the reduce of one zero partial)
+    hipLaunchKernelGGL(filter_bwd_fused_kernel<16>, dim3(1), dim3(kBwdThreads), lds, s, pos,
+                       pair_ij, pair_ij + pair_stride, n_pairs_dev, (int64_t)0, rp, W1, b1,
+                       W2, Wbar, Wdbar, workspace);
+  } else if (num_rbf <= 64) {
+    hipLaunchKernelGGL(filter_bwd_fused_kernel<16>, dim3(groups), dim3(kBwdThreads), lds, s,
+                       pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1,
+                       b1, W2, Wbar, Wdbar, workspace);
+  } else {
+    hipLaunchKernelGGL(filter_bwd_fused_kernel<32>, dim3(groups), dim3(kBwdThreads), lds, s,
+                       pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1,
+                       b1, W2, Wbar, Wdbar, workspace);
+  }
+  const int total = kF * kF + kF * num_rbf + kF;
+  hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + 255) / 256), dim3(256), 0, s,
+                     workspace, groups, num_rbf, dW1, db1, dW2);
   return mlcg_launch_status();
 }

@@ -259,24 +259,23 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     pos = _validate_pos(pos)
     F = W1.shape[0]
     K = spec.num_rbf
-    Kp = 4 * ((K + 3) // 4)
     cap = graph.pair_capacity
     dev = pos.device
-    H = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
-    T = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
-    A = torch.empty(2, cap, F, dtype=torch.float32, device=dev)
-    G = torch.empty(2, cap, Kp, dtype=torch.float32, device=dev)
+    _check(tuple(Wbar.shape) == (cap, F) and tuple(Wdbar.shape) == (cap, F),
+           "Wbar / Wdbar must be [pair_capacity, F]")
+    nws = int(_lib.load().mlcg_filter_bwd_workspace_floats(cap, K))
+    _check(nws > 0, f"num_rbf={K} is not supported by the filter backward")
+    ws = torch.empty(nws, dtype=torch.float32, device=dev)
+    dW1 = torch.empty(F, K, dtype=torch.float32, device=dev)
+    db1 = torch.empty(F, dtype=torch.float32, device=dev)
+    dW2 = torch.empty(F, F, dtype=torch.float32, device=dev)
     W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
     call("mlcg_filter_bwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
          ptr(spec.offsets), spec.coeff, K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
          spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
-         ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(H), ptr(T), ptr(A),
-         ptr(G), stream_handle(dev))
-    # pair reductions as library GEMMs: [F, 2P] x [2P, F]
-    dW2 = tmm(T.view(2 * cap, F), H.view(2 * cap, F))
-    dW1 = tmm(A.view(2 * cap, F), G.view(2 * cap, Kp))[:, :K]
-    db1 = A[0].sum(0)
-    return dW1.contiguous(), db1, dW2
+         ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(dW1), ptr(db1),
+         ptr(dW2), ptr(ws), nws, stream_handle(dev))
+    return dW1, db1, dW2
 
 
 # --------------------------------------------------------------------------

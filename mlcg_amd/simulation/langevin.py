@@ -179,8 +179,17 @@ class LangevinSimulation:
 
         graph = None
         flags = []
+        # steady-state timing: steps after the capture (or after step 2)
+        import time
+
+        self.timed_steps = 0
+        self.timed_seconds = 0.0
+        t_start = None
         with torch.no_grad():
             for t in range(self.n_timesteps):
+                if t == 3:
+                    torch.cuda.synchronize()
+                    t_start = time.perf_counter()
                 if graph is None and self.capture and t >= 2:
                     torch.cuda.synchronize()
                     self._check_flags(self._graph_flags())
@@ -206,6 +215,9 @@ class LangevinSimulation:
                     if not bool(torch.isfinite(x).all()):
                         raise RuntimeError(f"non-finite positions at step {t + 1}")
         torch.cuda.synchronize()
+        if t_start is not None:
+            self.timed_seconds = time.perf_counter() - t_start
+            self.timed_steps = self.n_timesteps - 3
         self._check_flags(flags)
         self.final_data = data
         self.potential = epot

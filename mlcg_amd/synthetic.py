@@ -90,25 +90,46 @@ def self_avoiding_walk(n_frames: int, n_beads: int, rng: np.random.Generator,
 
 
 def globule(n_frames: int, n_beads: int, radius: float, rng: np.random.Generator,
-            max_tries: int = 1000, exclusion: float = 0.0) -> np.ndarray:
+            max_tries: int = 64, exclusion: float = 0.0, candidates: int = 16) -> np.ndarray:
+    """Random walk of 3.8 A steps confined to a sphere of `radius` (and, with
+    `exclusion` > 0, keeping every bead at least that far from all earlier
+    non-adjacent beads).  The first round draws one trial step per frame,
+    later rounds `candidates` per unfinished frame, keeping the first
+    acceptable one; a frame that finds none after `max_tries` rounds keeps a
+    trial that satisfies the sphere only (rare dead ends)."""
     pos = np.zeros((n_frames, n_beads, 3))
     pos[:, 0] = _unit(rng.standard_normal((n_frames, 3))) * radius * 0.5 * rng.uniform(
         0, 1, (n_frames, 1))
     for k in range(1, n_beads):
         todo = np.arange(n_frames)
         new = np.zeros((n_frames, 3))
-        for _ in range(max_tries):
-            cand = pos[todo, k - 1] + _unit(rng.standard_normal((todo.size, 3))) * BOND
+        last = None
+        for attempt in range(max_tries):
+            m = todo.size
+            c = 1 if attempt == 0 else candidates
+            cand = pos[todo, k - 1][:, None, :] + _unit(
+                rng.standard_normal((m, c, 3))) * BOND
             ok = np.linalg.norm(cand, axis=-1) <= radius
+            last = (todo, cand, ok)
             if exclusion > 0 and k >= 2:
-                dd = np.linalg.norm(pos[todo, : k - 1] - cand[:, None, :], axis=-1)
-                ok &= (dd >= exclusion).all(axis=1)
-            new[todo[ok]] = cand[ok]
-            todo = todo[~ok]
+                # squared distances to all earlier non-adjacent beads through
+                # one batched product: |p|^2 + |c|^2 - 2 p.c
+                prev = pos[todo, : k - 1]
+                d2 = ((prev * prev).sum(-1)[:, None, :] + (cand * cand).sum(-1)[:, :, None]
+                      - 2.0 * np.matmul(cand, prev.transpose(0, 2, 1)))
+                ok &= (d2 >= exclusion * exclusion).all(axis=2)
+            anyok = ok.any(axis=1)
+            first = ok.argmax(axis=1)
+            sel = np.nonzero(anyok)[0]
+            new[todo[sel]] = cand[sel, first[sel]]
+            todo = todo[~anyok]
             if todo.size == 0:
                 break
-        if todo.size:  # dead end: keep the bond length, drop the other tests
-            new[todo] = cand[~ok]
+        if todo.size:  # dead end: keep the bond length and the sphere
+            t0, cand, ok_sphere = last
+            idx = np.searchsorted(t0, todo)
+            pick = np.where(ok_sphere[idx].any(axis=1), ok_sphere[idx].argmax(axis=1), 0)
+            new[todo] = cand[idx, pick]
         pos[:, k] = new
     return pos.astype(np.float32)
 
@@ -196,3 +217,89 @@ def config5(n_frames: int = 100, n_beads: int = 268) -> Batch:
 def radius_of_gyration(pos3: np.ndarray) -> np.ndarray:
     c = pos3 - pos3.mean(axis=1, keepdims=True)
     return np.sqrt((c ** 2).sum(-1).mean(-1))
+
+
+# ---------------------------------------------------------------------------
+# Config 5: priors and topology of the CG Langevin workload
+
+#: builder-chosen prior constants for config 5 (the configuration fixes only
+#: the bond and repulsion constants; the angle, dihedral and pair-set choices
+#: are recorded here)
+CONFIG5_PRIORS = {
+    "bonds": {"k": 100.0, "x_0": 3.8},
+    "angles": {"k": 10.0, "theta_0_deg": 100.0},
+    "dihedrals": {"k1s": (0.2, 0.1, 0.05), "k2s": (0.3, -0.1, 0.05), "v_0": 0.0},
+    "repulsion": {"sigma": 4.0, "min_separation": 3},
+    "masses_amu": 12.0,
+    "temperature_K": 300.0,
+    "dt_ps": 0.004,
+    "friction_per_ps": 1.0,
+}
+
+
+def chain_neighbor_lists(n_beads: int, min_separation: int = 3):
+    """Index maps of one linear chain: bonds (i, i+1), angles (i..i+2),
+    dihedrals (i..i+3) and the repulsion pairs |i - j| >= min_separation
+    (ordered, both directions, as the reference's fully connected list)."""
+    import torch
+
+    def stack(order):
+        base = torch.arange(n_beads - order + 1)
+        return torch.stack([base + s for s in range(order)])
+
+    ii, jj = torch.meshgrid(torch.arange(n_beads), torch.arange(n_beads), indexing="ij")
+    keep = (ii - jj).abs() >= min_separation
+    nl = {"bonds": stack(2), "angles": stack(3), "dihedrals": stack(4),
+          "repulsion": torch.stack([ii[keep], jj[keep]])}
+    return {k: {"index_mapping": v, "order": v.shape[0]} for k, v in nl.items()}
+
+
+def config5_prior_models(n_types: int = 21):
+    """HarmonicBonds, HarmonicAngles, Dihedral (3 terms) and Repulsion with the
+    CONFIG5_PRIORS constants for every type combination (types < n_types).
+    The modules are built from one statistics key and their type tables then
+    filled whole, which avoids a Python loop over n_types**4 dihedral keys."""
+    import math
+
+    from . import nn
+
+    c = CONFIG5_PRIORS
+    top = n_types - 1
+    bonds = nn.HarmonicBonds({(top, top): {"x_0": c["bonds"]["x_0"], "k": c["bonds"]["k"]}})
+    bonds.x_0.fill_(c["bonds"]["x_0"])
+    bonds.k.fill_(c["bonds"]["k"])
+    cos0 = math.cos(math.radians(c["angles"]["theta_0_deg"]))
+    angles = nn.HarmonicAngles({(top,) * 3: {"x_0": cos0, "k": c["angles"]["k"]}})
+    angles.x_0.fill_(cos0)
+    angles.k.fill_(c["angles"]["k"])
+    d = c["dihedrals"]
+    dih = nn.Dihedral({(top,) * 4: {"k1s": {f"k1_{i + 1}": v for i, v in enumerate(d["k1s"])},
+                                     "k2s": {f"k2_{i + 1}": v for i, v in enumerate(d["k2s"])},
+                                     "v_0": d["v_0"]}}, n_degs=3)
+    for i in range(3):
+        dih.k1s[i].fill_(d["k1s"][i])
+        dih.k2s[i].fill_(d["k2s"][i])
+    dih.v_0.fill_(d["v_0"])
+    rep = nn.Repulsion({(top, top): {"sigma": c["repulsion"]["sigma"]}})
+    rep.sigma.fill_(c["repulsion"]["sigma"])
+    return {"bonds": bonds, "angles": angles, "dihedrals": dih, "repulsion": rep}
+
+
+def config5_configurations(n_frames: int = 100, n_beads: int = 268):
+    """AtomicData frames of config 5 with masses and the chain neighbour lists."""
+    import torch
+
+    from .data import AtomicData
+
+    b = config5(n_frames, n_beads)
+    nls = chain_neighbor_lists(n_beads, CONFIG5_PRIORS["repulsion"]["min_separation"])
+    m = CONFIG5_PRIORS["masses_amu"] / 418.4
+    out = []
+    for f in range(n_frames):
+        sl = slice(f * n_beads, (f + 1) * n_beads)
+        out.append(AtomicData(pos=torch.from_numpy(b.pos[sl].copy()),
+                              atom_types=torch.from_numpy(b.atom_types[sl].copy()),
+                              masses=torch.full((n_beads,), m),
+                              n_atoms=torch.tensor([n_beads]),
+                              neighbor_list={k: dict(v) for k, v in nls.items()}))
+    return out

@@ -231,3 +231,52 @@ def test_golden_fixture_hip():
     assert abs(float(loss) - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
     for k, p in model.named_parameters():
         assert rel_err(p.grad, g["grads"][k]) < 1e-4, k
+
+
+def _config4_model(sd=None, seed=4):
+    from mlcg_amd import nn
+
+    cfg = make_cfg(num_blocks=3, rc=15.0)
+    if sd is None:
+        sd = R.random_state_dict(cfg, seed=seed)
+    return cfg, sd, make_model(cfg, sd)
+
+
+def test_fp16_filters_config4_vs_oracle():
+    """Config 4 (globular 500-bead frames, rc 15 A, fp16 filter linears with
+    fp32 accumulation): energies and forces within 2e-3 relative of the fp64
+    oracle on 3 frames."""
+    from mlcg_amd import nn, synthetic
+
+    b = synthetic.config4(n_frames=3)
+    cfg, sd, model = _config4_model()
+    pos64, types, batch, ei = _oracle_inputs(b, 15.0)
+    E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
+                                          batch, ei, b.n_frames)
+    model.fp16_filters = True
+    data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
+    e = rel_err(data.out["SchNet"]["energy"], E_ref)
+    f = rel_err(data.out["SchNet"]["forces"], F_ref)
+    print("fp16 config4: E rel", e, "F rel", f, "E", ei.shape[1])
+    assert f < 2e-3 and e < 2e-3
+    # and the fp32 path on the same frames meets the fp32 tolerance
+    model.fp16_filters = False
+    d32 = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
+    assert rel_err(d32.out["SchNet"]["forces"], F_ref) < 1e-5
+
+
+def test_fp16_filters_config4_full_size_vs_fp32():
+    """Full config 4 (256 x 500 beads, ~6M edges): fp16-filter forces within
+    2e-3 of the fp32 HIP path (the fp32 path is pinned to the oracle above)."""
+    from mlcg_amd import nn, synthetic
+
+    b = synthetic.config4()
+    _, _, model = _config4_model()
+    data = b.to_torch("cuda")
+    gm = nn.GradientsOut(model).eval()
+    F32 = gm(data).out["SchNet"]["forces"].clone()
+    model.fp16_filters = True
+    F16 = gm(data).out["SchNet"]["forces"]
+    err = rel_err(F16, F32)
+    print("fp16 vs fp32 forces at full config 4:", err, "edges", model.last_graph.num_edges)
+    assert err < 2e-3
