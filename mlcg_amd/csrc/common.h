@@ -81,7 +81,8 @@ __device__ __forceinline__ float mlcg_act_value(int act, float x) {
 // Cutoff envelope and its derivative with respect to the distance.
 // Cosine with lower == 0:  0.5 (cos(pi d / hi) + 1) [d < hi]
 // Cosine with lower  > 0:  0.5 (cos(pi (2 (d - lo)/(hi - lo) + 1)) + 1) [lo < d < hi]
-// (mlcg/nn/cutoff.py:110-153)
+// (mlcg/nn/cutoff.py:110-153).  cos(pi u) and sin(pi u) come from sincospif,
+// whose argument reduction is exact and cheap (no large-argument path).
 __device__ __forceinline__ void mlcg_cutoff(int kind, float lo, float hi, float d,
                                             float& c, float& dc) {
   const float pi = 3.14159265358979323846f;
@@ -90,14 +91,16 @@ __device__ __forceinline__ void mlcg_cutoff(int kind, float lo, float hi, float 
     dc = 0.0f;
   } else if (lo > 0.0f) {
     float w = hi - lo;
-    float arg = pi * (2.0f * (d - lo) / w + 1.0f);
+    float sn, cs;
+    sincospif(2.0f * (d - lo) / w + 1.0f, &sn, &cs);
     float m = (d < hi && d > lo) ? 1.0f : 0.0f;
-    c = 0.5f * (cosf(arg) + 1.0f) * m;
-    dc = -0.5f * sinf(arg) * (2.0f * pi / w) * m;
+    c = 0.5f * (cs + 1.0f) * m;
+    dc = -0.5f * sn * (2.0f * pi / w) * m;
   } else {
-    float arg = d * pi / hi;
+    float sn, cs;
+    sincospif(d / hi, &sn, &cs);
     float m = d < hi ? 1.0f : 0.0f;
-    c = 0.5f * (cosf(arg) + 1.0f) * m;
-    dc = -0.5f * sinf(arg) * (pi / hi) * m;
+    c = 0.5f * (cs + 1.0f) * m;
+    dc = -0.5f * sn * (pi / hi) * m;
   }
 }

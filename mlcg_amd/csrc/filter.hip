@@ -68,7 +68,7 @@ __device__ __forceinline__ void rbf_value(const RbfParams& rp, int k, float d, f
                                           float dcrbf, float& g, float& gd) {
   if (k < rp.K) {
     float diff = d - rp.offsets[k];
-    float e = expf(rp.coeff * (diff * diff));
+    float e = __expf(rp.coeff * (diff * diff));  // argument <= 0: no overflow
     g = e * crbf;
     gd = e * (2.0f * rp.coeff * diff * crbf + dcrbf);
   } else {
@@ -395,21 +395,25 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
 //   dW2 = sum_p t h^T + t' h'^T,  dW1 = sum_p ab g^T + ab' g'^T,  db1 = sum_p ab.
 //
 // Work split: a workgroup of 8 waves walks 16-pair tiles; wave w owns feature
-// tile w (features 16w..16w+15) in every product, so it needs only its slice
-// of W1 (one A fragment per k step) and of W2^T (8 float4 fragments), both
-// kept in registers for the whole kernel.  Per tile:
-//   1. every wave recomputes g, g' for the 16 pairs (B operand layout) and
-//      a, a' of its feature tile (v_mfma_f32_16x16x4f32);
-//   2. it forms t, t', h, h' of its features and publishes them in LDS as
-//      [pair][feature] rows;
-//   3. hb, hb' of its tile: B operands read from LDS (all 128 features);
+// tile w (features 16w..16w+15) in every product.  Its slice of W1 (one A
+// fragment per k step) stays in registers; the W2^T A fragments of all eight
+// tiles are staged once in LDS.  Per tile:
+//   0. the waves share the per-pair scalar work: wave w evaluates the basis
+//      columns of k steps w and w + 8 for the 16 pairs (g, g' into LDS), and
+//      wave 0 the filter envelope C, C';                        -- barrier --
+//   1. a, a' of feature tile w (v_mfma_f32_16x16x4f32, B operand from LDS);
+//   2. t, t', h, h' of its features, published in LDS as [pair][feature]
+//      rows;                                                     -- barrier --
+//   3. hb, hb' of its tile (B operands = all 128 t features from LDS);
 //   4. dW2 rows of its tile += t^T h over the 16 pairs (the pair index is the
-//      MFMA reduction axis; operands read from the LDS rows);
-//   5. ab, ab' replace t, t' in LDS; dW1 rows of its tile += ab^T g.
-// The accumulators stay in registers across all tiles of the workgroup; at
-// the end each workgroup writes its partial sums, and filter_bwd_reduce adds
-// the partials in workgroup order, so the result is deterministic.  Nothing
-// per pair is written to HBM.
+//      MFMA reduction axis; both operands read from the LDS rows);
+//   5. ab, ab' published in their own buffer;                   -- barrier --
+//   6. dW1 rows of its tile += ab^T g.
+// The g and envelope buffers are double-buffered across tiles, which makes
+// three barriers per tile sufficient.  The accumulators stay in registers
+// across all tiles of the workgroup; at the end each workgroup writes its
+// partial sums, and filter_bwd_reduce adds the partials in workgroup order,
+// so the result is deterministic.  Nothing per pair is written to HBM.
 constexpr int kBwdWaves = 8;
 constexpr int kBwdThreads = kBwdWaves * MLCG_WAVE;
 constexpr int kRowPad = 4;
@@ -419,8 +423,12 @@ __host__ __device__ constexpr int bwd_kp16(int K) { return 16 * ((K + 15) / 16);
 __host__ __device__ constexpr int bwd_partial_floats(int K) {
   return kF * kF + kF * bwd_kp16(K) + kF;
 }
+__host__ __device__ constexpr int bwd_grow(int K) { return (K <= 64 ? 64 : 128) + 4; }
+// LDS: W2^T fragments [8][8][64] float4 | TB, HH, AB [2][16][kXRow] |
+//      GG [2 buffers][2][16][grow] | PS [2 buffers][16][2] (C, C')
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
-  return 2 * 16 * kXRow * 2 + 2 * 16 * (bwd_kp16(K) + 4);
+  return kFT * kFT * MLCG_WAVE * 4 + 3 * 2 * 16 * kXRow + 2 * 2 * 16 * bwd_grow(K) +
+         2 * 16 * 2;
 }
 
 template <int KSMAX>
@@ -432,36 +440,33 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const float* __restrict__ Wbar, const float* __restrict__ Wdbar,
     float* __restrict__ partial) {
   constexpr int KTMAX = (4 * KSMAX + 15) / 16;
+  // g rows span the compile-time maximum width and the unused columns stay
+  // zero, so the k loops below run without data-dependent branches (which
+  // would otherwise make the compiler copy the accumulators at every merge)
+  constexpr int gRow = 16 * KTMAX + 4;
   extern __shared__ float lds[];
   const int K = rp.K;
-  const int KS = (K + 3) / 4;
   const int Kp16 = bwd_kp16(K);
   const int KT = Kp16 / 16;
-  const int gRow = Kp16 + 4;
-  float* TB = lds;                   // [2][16][kXRow]  t, t'  (later ab, ab')
-  float* HH = TB + 2 * 16 * kXRow;   // [2][16][kXRow]  h, h'
-  float* GG = HH + 2 * 16 * kXRow;   // [2][16][gRow]   g, g'
+  float* w2ts = lds;                                  // [8 t][8 u][64 l] float4
+  float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;       // [2][16][kXRow]  t, t'
+  float* HH = TB + 2 * 16 * kXRow;                    // [2][16][kXRow]  h, h'
+  float* AB = HH + 2 * 16 * kXRow;                    // [2][16][kXRow]  ab, ab'
+  float* GG0 = AB + 2 * 16 * kXRow;                   // [2 bufs][2][16][gRow] g, g'
+  float* PS0 = GG0 + 2 * 2 * 16 * gRow;               // [2 bufs][16][2] C, C'
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
 
-  for (int x = threadIdx.x; x < 2 * 16 * gRow; x += blockDim.x) GG[x] = 0.0f;
+  stage_w2_f32(w2ts, W2, true);
+  for (int x = threadIdx.x; x < 2 * 2 * 16 * gRow; x += blockDim.x) GG0[x] = 0.0f;
 
-  // register-resident weight fragments of feature tile w
+  // W1 fragment of feature tile w stays in registers: W1[16w + n][4s + q]
   float w1f[KSMAX];
 #pragma unroll
   for (int s = 0; s < KSMAX; ++s) {
     const int k = 4 * s + q;
-    w1f[s] = (s < KS && k < K) ? W1[(16 * w + n) * K + k] : 0.0f;
-  }
-  float4 a2[kFT];  // A fragments of W2^T: a2[u].i = W2[16u + 4q + i][16w + n]
-#pragma unroll
-  for (int u = 0; u < kFT; ++u) {
-    const int c0 = 16 * u + 4 * q;
-    a2[u].x = W2[(c0 + 0) * kF + 16 * w + n];
-    a2[u].y = W2[(c0 + 1) * kF + 16 * w + n];
-    a2[u].z = W2[(c0 + 2) * kF + 16 * w + n];
-    a2[u].w = W2[(c0 + 3) * kF + 16 * w + n];
+    w1f[s] = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
   }
   float bias[4];
 #pragma unroll
@@ -480,78 +485,101 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   if (np > max_pairs) np = max_pairs;
   const int64_t tiles = (np + 15) / 16;
   const int fcol = 16 * w + 4 * q;  // first of the lane's 4 features in row layout
+  const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
 
-  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+  int buf = 0;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
+    float* GG = GG0 + buf * 2 * 16 * gRow;
+    float* PS = PS0 + buf * 16 * 2;
     const int64_t p = tile * 16 + n;
     const bool valid = p < np;
-    const float d = pair_distance(pos, pi, pj, p, valid);
-    float crbf, dcrbf, cc, dcc;
-    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
-
-    // 1. a, a' of feature tile w; wave w publishes the g columns of its k steps
-    floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSMAX; ++s) {
-      if (s < KS) {
-        float g, gd;
-        rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);
-        if ((s & (kBwdWaves - 1)) == w) {
-          GG[n * gRow + 4 * s + q] = valid ? g : 0.0f;
-          GG[16 * gRow + n * gRow + 4 * s + q] = valid ? gd : 0.0f;
-        }
-        a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
-        ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
-      }
-    }
-    // 2. h, h', activation derivatives and t, t' of the lane's 4 features
-    float h[4], hd[4], act1[4], act2[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float sv, d1, d2;
-      mlcg_act(rp.act, a[i] + bias[i], sv, d1, d2);
-      h[i] = valid ? sv : 0.0f;
-      act1[i] = d1;
-      act2[i] = d2 * ad[i];
-      hd[i] = valid ? d1 * ad[i] : 0.0f;
-    }
+    const float vmask = valid ? 1.0f : 0.0f;
+    // the pair adjoints are loaded first so their latency overlaps phase 0
     float4 wb = {0.f, 0.f, 0.f, 0.f}, wdb = {0.f, 0.f, 0.f, 0.f};
     if (valid) {
       wb = *reinterpret_cast<const float4*>(Wbar + p * kF + fcol);
       wdb = *reinterpret_cast<const float4*>(Wdbar + p * kF + fcol);
+    }
+
+    // 0. shared per-pair work: basis columns of k steps w and w + 8, envelope
+    {
+      const float d = pair_distance(pos, pi, pj, p, valid);
+      float crbf, dcrbf;
+      mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+#pragma unroll
+      for (int s0 = 0; s0 < KSMAX; s0 += kBwdWaves) {
+        const int s = s0 + w;
+        if (s < KSMAX) {
+          float g, gd;
+          rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);  // zero for k >= K
+          GG[n * gRow + 4 * s + q] = g * vmask;
+          GG[16 * gRow + n * gRow + 4 * s + q] = gd * vmask;
+        }
+      }
+      if (w == 0 && q == 0) {
+        float cc, dcc;
+        mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+        PS[2 * n] = cc;
+        PS[2 * n + 1] = dcc;
+      }
+    }
+    __syncthreads();
+
+    // 1. a, a' of feature tile w
+    floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSMAX; ++s) {
+      const float g = GG[n * gRow + 4 * s + q];
+      const float gd = GG[16 * gRow + n * gRow + 4 * s + q];
+      a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
+      ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
+    }
+    // 2. h, h', activation derivatives and t, t' of the lane's 4 features
+    const float cc = PS[2 * n], dcc = PS[2 * n + 1];
+    float act1[4], act2[4];
+    float4 hv, hdv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv, d1, d2;
+      mlcg_act(rp.act, a[i] + bias[i], sv, d1, d2);
+      act1[i] = d1;
+      act2[i] = d2 * ad[i];
+      reinterpret_cast<float*>(&hv)[i] = sv * vmask;
+      reinterpret_cast<float*>(&hdv)[i] = d1 * ad[i] * vmask;
     }
     const float4 tb = {wb.x * cc + wdb.x * dcc, wb.y * cc + wdb.y * dcc,
                        wb.z * cc + wdb.z * dcc, wb.w * cc + wdb.w * dcc};
     const float4 tdb = {wdb.x * cc, wdb.y * cc, wdb.z * cc, wdb.w * cc};
     *reinterpret_cast<float4*>(TB + n * kXRow + fcol) = tb;
     *reinterpret_cast<float4*>(TB + 16 * kXRow + n * kXRow + fcol) = tdb;
-    *reinterpret_cast<float4*>(HH + n * kXRow + fcol) = float4{h[0], h[1], h[2], h[3]};
-    *reinterpret_cast<float4*>(HH + 16 * kXRow + n * kXRow + fcol) =
-        float4{hd[0], hd[1], hd[2], hd[3]};
+    *reinterpret_cast<float4*>(HH + n * kXRow + fcol) = hv;
+    *reinterpret_cast<float4*>(HH + 16 * kXRow + n * kXRow + fcol) = hdv;
     __syncthreads();
 
     // 3. hb, hb' of feature tile w (all 128 t features from LDS)
     floatx4 hb = {0.f, 0.f, 0.f, 0.f}, hdb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < kFT; ++u) {
+      const float4 a2 = w2v[u * MLCG_WAVE];
       const float4 bx = *reinterpret_cast<const float4*>(TB + n * kXRow + 16 * u + 4 * q);
       const float4 by =
           *reinterpret_cast<const float4*>(TB + 16 * kXRow + n * kXRow + 16 * u + 4 * q);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].x, bx.x, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].x, by.x, hdb, 0, 0, 0);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].y, bx.y, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].y, by.y, hdb, 0, 0, 0);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].z, bx.z, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].z, by.z, hdb, 0, 0, 0);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].w, bx.w, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[u].w, by.w, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, bx.x, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, by.x, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, bx.y, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, by.y, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.z, bx.z, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.z, by.z, hdb, 0, 0, 0);
+      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, bx.w, hb, 0, 0, 0);
+      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, by.w, hdb, 0, 0, 0);
     }
-    float ab[4], adb[4];
+    float4 abv, adbv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      ab[i] = hb[i] * act1[i] + hdb[i] * act2[i];
-      adb[i] = hdb[i] * act1[i];
-      db[i] += ab[i];
+      const float ab = hb[i] * act1[i] + hdb[i] * act2[i];
+      reinterpret_cast<float*>(&abv)[i] = ab;
+      reinterpret_cast<float*>(&adbv)[i] = hdb[i] * act1[i];
+      db[i] += ab;
     }
     // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c]
 #pragma unroll
@@ -561,36 +589,34 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const float av = T[(4 * kk + q) * kXRow + 16 * w + n];
+        float bv[kFT];
 #pragma unroll
-        for (int u = 0; u < kFT; ++u) {
-          const float bv = Hs[(4 * kk + q) * kXRow + 16 * u + n];
-          acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc2[u], 0, 0, 0);
-        }
+        for (int u = 0; u < kFT; ++u) bv[u] = Hs[(4 * kk + q) * kXRow + 16 * u + n];
+#pragma unroll
+        for (int u = 0; u < kFT; ++u)
+          acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc2[u], 0, 0, 0);
       }
     }
+    // 5. publish ab, ab'
+    *reinterpret_cast<float4*>(AB + n * kXRow + fcol) = abv;
+    *reinterpret_cast<float4*>(AB + 16 * kXRow + n * kXRow + fcol) = adbv;
     __syncthreads();
-    // 5. ab, ab' replace t, t'; dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
-    *reinterpret_cast<float4*>(TB + n * kXRow + fcol) = float4{ab[0], ab[1], ab[2], ab[3]};
-    *reinterpret_cast<float4*>(TB + 16 * kXRow + n * kXRow + fcol) =
-        float4{adb[0], adb[1], adb[2], adb[3]};
-    __syncthreads();
+    // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const float* A = TB + st * 16 * kXRow;
+      const float* A = AB + st * 16 * kXRow;
       const float* G = GG + st * 16 * gRow;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const float av = A[(4 * kk + q) * kXRow + 16 * w + n];
+        float bv[KTMAX];
 #pragma unroll
-        for (int kt = 0; kt < KTMAX; ++kt) {
-          if (kt < KT) {
-            const float bv = G[(4 * kk + q) * gRow + 16 * kt + n];
-            acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc1[kt], 0, 0, 0);
-          }
-        }
+        for (int kt = 0; kt < KTMAX; ++kt) bv[kt] = G[(4 * kk + q) * gRow + 16 * kt + n];
+#pragma unroll
+        for (int kt = 0; kt < KTMAX; ++kt)
+          acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[kt], acc1[kt], 0, 0, 0);
       }
     }
-    __syncthreads();
   }
 
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
@@ -620,32 +646,48 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   }
 }
 
-// dW2 [F, F], dW1 [F, K], db1 [F] = sum over workgroup partials (in order).
+// dW2 [F, F], dW1 [F, K], db1 [F] = sum over the workgroup partials.  A block
+// handles 64 outputs; its 4 waves take the groups g = slice (mod 4), each lane
+// keeping 4 interleaved accumulators, and the partial sums are combined in a
+// fixed order, so the result does not depend on timing.
+constexpr int kRedOut = 64;
+
 __global__ __launch_bounds__(256) void filter_bwd_reduce_kernel(
     const float* __restrict__ partial, int groups, int K, float* __restrict__ dW1,
     float* __restrict__ db1, float* __restrict__ dW2) {
+  __shared__ float part[4][kRedOut];
   const int Kp16 = bwd_kp16(K);
   const int stride = bwd_partial_floats(K);
   const int total = kF * kF + kF * K + kF;
-  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < total; j += gridDim.x * blockDim.x) {
-    int src;
-    float* dst;
-    if (j < kF * kF) {
-      src = j;
-      dst = dW2 + j;
-    } else if (j < kF * kF + kF * K) {
-      const int r = j - kF * kF;
-      src = kF * kF + (r / K) * Kp16 + (r % K);
-      dst = dW1 + r;
-    } else {
-      const int r = j - kF * kF - kF * K;
-      src = kF * kF + kF * Kp16 + r;
-      dst = db1 + r;
-    }
-    float acc = 0.f;
-    for (int g = 0; g < groups; ++g) acc += partial[(int64_t)g * stride + src];
-    *dst = acc;
+  const int o = threadIdx.x & (kRedOut - 1);
+  const int slice = threadIdx.x / kRedOut;
+  const int j = blockIdx.x * kRedOut + o;
+  int src = 0;
+  float* dst = nullptr;
+  if (j < kF * kF) {
+    src = j;
+    dst = dW2 + j;
+  } else if (j < kF * kF + kF * K) {
+    const int r = j - kF * kF;
+    src = kF * kF + (r / K) * Kp16 + (r % K);
+    dst = dW1 + r;
+  } else if (j < total) {
+    const int r = j - kF * kF - kF * K;
+    src = kF * kF + kF * Kp16 + r;
+    dst = db1 + r;
   }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (dst) {
+    int g = slice;
+    for (; g + 12 < groups; g += 16) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += partial[(int64_t)(g + 4 * u) * stride + src];
+    }
+    for (int u = 0; g < groups; g += 4, ++u) acc[u & 3] += partial[(int64_t)g * stride + src];
+  }
+  part[slice][o] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (slice == 0 && dst) *dst = (part[0][o] + part[1][o]) + (part[2][o] + part[3][o]);
 }
 
 int bwd_groups(int64_t max_pairs) {
@@ -664,6 +706,10 @@ void allow_lds_once() {
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f32_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   done[dev] = true;
 }
@@ -754,6 +800,7 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
                              conv_cut_kind, conv_lo, conv_hi, act);
   hipStream_t s = mlcg_stream(stream);
   const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
+  allow_lds_once();
   if (max_pairs == 0) {
     // no pairs: every gradient is zero (the reduce of one zero partial)
     hipLaunchKernelGGL(filter_bwd_fused_kernel<16>, dim3(1), dim3(kBwdThreads), lds, s, pos,
@@ -769,7 +816,8 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
                        b1, W2, Wbar, Wdbar, workspace);
   }
   const int total = kF * kF + kF * num_rbf + kF;
-  hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + 255) / 256), dim3(256), 0, s,
+  hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + kRedOut - 1) / kRedOut), dim3(256),
+                     0, s,
                      workspace, groups, num_rbf, dW1, db1, dW2);
   return mlcg_launch_status();
 }
