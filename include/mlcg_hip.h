@@ -179,7 +179,8 @@ int mlcg_cfconv_gather_tangent(const float* ydot, const float* y,
  *   Wbar[p]  = gagg2[i] y[j] + gagg2[j] y[i] + gagg1[i] ydot[j] + gagg1[j] ydot[i]
  *   Wdbar[p] = ddot_p (gagg1[i] y[j] + gagg1[j] y[i])
  * ydot, gagg1, ddot may be NULL (zero tangent).  Wbar/Wdbar are
- * [n_pairs, F]. */
+ * [n_pairs, F]; both may be NULL, then only ybar2 is computed (the pair
+ * adjoints are then formed inside mlcg_filter_bwd_cfconv instead). */
 int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1,
                             const float* y, const float* ydot,
                             const float* W, const float* Wd,
@@ -187,6 +188,26 @@ int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1,
                             const int32_t* col, const int32_t* eid2pair,
                             int64_t n_nodes, int num_filters, float* ybar2,
                             float* Wbar, float* Wdbar, void* stream);
+
+/* mlcg_filter_bwd with the pair adjoints formed from node vectors of the
+ * CFConv reverse instead of read from [P, F] arrays:
+ *   Wbar_p  = gagg2_i y_j + gagg2_j y_i + gagg1_i ydot_j + gagg1_j ydot_i
+ *   Wdbar_p = ddot_p (gagg1_i y_j + gagg1_j y_i)
+ * (node arrays [N, F] fp32; gagg1, ydot, ddot may be NULL for a zero
+ * tangent, ddot is [max_pairs]).  Same outputs and workspace as
+ * mlcg_filter_bwd; the two [P, F] adjoint arrays are never materialised. */
+int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
+                           int64_t pair_stride, const int32_t* n_pairs_dev,
+                           int64_t max_pairs, const float* offsets, float coeff,
+                           int num_rbf, int rbf_cut_kind, float rbf_lo,
+                           float rbf_hi, int conv_cut_kind, float conv_lo,
+                           float conv_hi, int act, const float* W1,
+                           const float* b1, const float* W2, int num_filters,
+                           const float* gagg2, const float* y,
+                           const float* gagg1, const float* ydot,
+                           const float* ddot, float* dW1, float* db1,
+                           float* dW2, float* workspace,
+                           int64_t workspace_floats, void* stream);
 
 /* ddot[p] = rhat_p . (u[j] - u[i]), rhat_p = (pos[j] - pos[i]) / dist[p]. */
 int mlcg_pair_ddot(const float* pos, const float* dist, const int32_t* pair_ij,
@@ -208,6 +229,21 @@ int mlcg_pair_forces(const float* pos, const float* dist, const float* dbar,
 int mlcg_segment_sum(const float* values, int64_t stride,
                      const int64_t* frame_ptr, int64_t n_frames, float* out,
                      void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Weight gradients of the node-level linears (F = 128)                    */
+/* ---------------------------------------------------------------------- */
+
+/* out [128, 128] (+)= a1^T b1 (+ a2^T b2) for [rows, 128] inputs (a2/b2 may
+ * be NULL), deterministic split over 64-row slices; `workspace` holds
+ * mlcg_node_tmm_workspace_floats(rows) floats.  accumulate != 0 adds to out.
+ * Replaces the weight-gradient products of the same linears (the autograd
+ * backward of schnet.py:259-261,343,347 through the double backward). */
+int64_t mlcg_node_tmm_workspace_floats(int64_t rows);
+int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
+                  const float* b2, int64_t rows, int features, int accumulate,
+                  float* out, float* workspace, int64_t workspace_floats,
+                  void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Priors: harmonic bonds and angles, Fourier dihedrals, repulsion          */

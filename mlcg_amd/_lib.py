@@ -47,6 +47,9 @@ _SIGNATURES = {
     "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
                         _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64,
                         _P],
+    "mlcg_filter_bwd_cfconv": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32,
+                               _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
+                               _P, _P, _P, _P, _I64, _P],
     "mlcg_cfconv_gather": [_P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
     "mlcg_cfconv_gather_tangent": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
@@ -55,6 +58,8 @@ _SIGNATURES = {
     "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _P, _P],
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
+    "mlcg_node_tmm_workspace_floats": [_I64],
+    "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
     "mlcg_prior_order": [_I32],
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
@@ -64,7 +69,7 @@ _SIGNATURES = {
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
-             "mlcg_filter_bwd_workspace_floats": _I64}
+             "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

@@ -431,13 +431,114 @@ __host__ __device__ constexpr int bwd_lds_floats(int K) {
          2 * 16 * 2;
 }
 
-template <int KSMAX>
+// Where the pair adjoints (Wbar, Wdbar) come from: explicit [P, F] arrays, or
+// formed on the fly from node vectors of the CFConv aggregation (the reverse
+// of agg_i = sum_j y_j W_ij with a tangent stream, see mlcg_hip.h):
+//   Wbar_p  = g2_i y_j + g2_j y_i + g1_i yd_j + g1_j yd_i
+//   Wdbar_p = dd_p (g1_i y_j + g1_j y_i)
+// which saves writing and re-reading two [P, F] arrays.
+struct PairAdjoint {
+  const float* Wbar;
+  const float* Wdbar;
+  const float* g2;    // node mode: gagg2 [N, F]
+  const float* y;     //            y [N, F]
+  const float* g1;    //            gagg1 [N, F] or null (no tangent)
+  const float* yd;    //            ydot [N, F] or null
+  const float* dd;    //            ddot [P] (with g1)
+};
+
+__device__ __forceinline__ float4 ld4(const float* __restrict__ p, int64_t row, int col) {
+  return *reinterpret_cast<const float4*>(p + row * kF + col);
+}
+__device__ __forceinline__ float4 f4(float a, float b, float c, float d) {
+  return float4{a, b, c, d};
+}
+
+// Global inputs of one lane's pair for one tile, loaded one tile ahead so that
+// their latency overlaps the previous tile's MFMA work.
+struct TileIn {
+  float xi, yi, zi, xj, yj, zj;  // positions of the pair's beads
+  float4 v[8];                   // adjoint sources (explicit: v[0..1])
+  float dd;
+  bool valid;
+};
+
+template <bool kNodes>
+__device__ __forceinline__ TileIn fetch_tile(const float* __restrict__ pos,
+                                             const int32_t* __restrict__ pi,
+                                             const int32_t* __restrict__ pj,
+                                             const PairAdjoint& adj, int64_t p, int64_t np,
+                                             int fcol) {
+  TileIn t;
+  t.valid = p < np;
+  t.dd = 0.f;
+  const float4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) t.v[k] = z;
+  t.xi = t.yi = t.zi = 0.f;
+  t.xj = 1.f;  // harmless distance for padding lanes
+  t.yj = t.zj = 0.f;
+  if (t.valid) {
+    const int64_t i = pi[p], j = pj[p];
+    t.xi = pos[3 * i];
+    t.yi = pos[3 * i + 1];
+    t.zi = pos[3 * i + 2];
+    t.xj = pos[3 * j];
+    t.yj = pos[3 * j + 1];
+    t.zj = pos[3 * j + 2];
+    if (!kNodes) {
+      t.v[0] = ld4(adj.Wbar, p, fcol);
+      t.v[1] = ld4(adj.Wdbar, p, fcol);
+    } else {
+      t.v[0] = ld4(adj.g2, i, fcol);
+      t.v[1] = ld4(adj.g2, j, fcol);
+      t.v[2] = ld4(adj.y, i, fcol);
+      t.v[3] = ld4(adj.y, j, fcol);
+      if (adj.g1) {
+        t.v[4] = ld4(adj.g1, i, fcol);
+        t.v[5] = ld4(adj.g1, j, fcol);
+        if (adj.yd) {
+          t.v[6] = ld4(adj.yd, i, fcol);
+          t.v[7] = ld4(adj.yd, j, fcol);
+        }
+        t.dd = adj.dd[p];
+      }
+    }
+  }
+  return t;
+}
+
+// Wbar, Wdbar of the lane's 4 features from the prefetched sources.
+template <bool kNodes>
+__device__ __forceinline__ void tile_adjoint(const TileIn& t, bool tangent, float4& wb,
+                                             float4& wdb) {
+  if (!kNodes) {
+    wb = t.v[0];
+    wdb = t.v[1];
+    return;
+  }
+  const float4 g2i = t.v[0], g2j = t.v[1], yi = t.v[2], yj = t.v[3];
+  const float4 g1i = t.v[4], g1j = t.v[5], ydi = t.v[6], ydj = t.v[7];
+  wb = f4(g2i.x * yj.x + g2j.x * yi.x, g2i.y * yj.y + g2j.y * yi.y,
+          g2i.z * yj.z + g2j.z * yi.z, g2i.w * yj.w + g2j.w * yi.w);
+  wdb = f4(0.f, 0.f, 0.f, 0.f);
+  if (tangent) {
+    // ydot terms are zero when ydot is absent (v[6], v[7] stay zero)
+    wb.x += g1i.x * ydj.x + g1j.x * ydi.x;
+    wb.y += g1i.y * ydj.y + g1j.y * ydi.y;
+    wb.z += g1i.z * ydj.z + g1j.z * ydi.z;
+    wb.w += g1i.w * ydj.w + g1j.w * ydi.w;
+    wdb = f4(t.dd * (g1i.x * yj.x + g1j.x * yi.x), t.dd * (g1i.y * yj.y + g1j.y * yi.y),
+             t.dd * (g1i.z * yj.z + g1j.z * yi.z), t.dd * (g1i.w * yj.w + g1j.w * yi.w));
+  }
+}
+
+template <int KSMAX, bool kNodes>
 __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
     int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
-    const float* __restrict__ b1, const float* __restrict__ W2,
-    const float* __restrict__ Wbar, const float* __restrict__ Wdbar,
+    const float* __restrict__ b1, const float* __restrict__ W2, PairAdjoint adj,
     float* __restrict__ partial) {
   constexpr int KTMAX = (4 * KSMAX + 15) / 16;
   // g rows span the compile-time maximum width and the unused columns stay
@@ -487,23 +588,24 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   const int fcol = 16 * w + 4 * q;  // first of the lane's 4 features in row layout
   const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
 
+  const bool tangent = kNodes && adj.g1 != nullptr;
   int buf = 0;
+  TileIn cur = fetch_tile<kNodes>(pos, pi, pj, adj, (int64_t)blockIdx.x * 16 + n, np, fcol);
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
     float* GG = GG0 + buf * 2 * 16 * gRow;
     float* PS = PS0 + buf * 16 * 2;
-    const int64_t p = tile * 16 + n;
-    const bool valid = p < np;
+    const bool valid = cur.valid;
     const float vmask = valid ? 1.0f : 0.0f;
-    // the pair adjoints are loaded first so their latency overlaps phase 0
-    float4 wb = {0.f, 0.f, 0.f, 0.f}, wdb = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
-      wb = *reinterpret_cast<const float4*>(Wbar + p * kF + fcol);
-      wdb = *reinterpret_cast<const float4*>(Wdbar + p * kF + fcol);
-    }
+    // the next tile's inputs are requested now; they are consumed one tile later
+    const TileIn nxt =
+        fetch_tile<kNodes>(pos, pi, pj, adj, (tile + gridDim.x) * 16 + n, np, fcol);
+    float4 wb, wdb;
+    tile_adjoint<kNodes>(cur, tangent, wb, wdb);
 
     // 0. shared per-pair work: basis columns of k steps w and w + 8, envelope
     {
-      const float d = pair_distance(pos, pi, pj, p, valid);
+      const float dx = cur.xj - cur.xi, dy = cur.yj - cur.yi, dz = cur.zj - cur.zi;
+      const float d = sqrtf(dx * dx + dy * dy + dz * dz);
       float crbf, dcrbf;
       mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
 #pragma unroll
@@ -617,6 +719,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[kt], acc1[kt], 0, 0, 0);
       }
     }
+    cur = nxt;
   }
 
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
@@ -707,9 +810,13 @@ void allow_lds_once() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16>),
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32>),
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   done[dev] = true;
 }
@@ -780,6 +887,46 @@ extern "C" int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_r
   return (int64_t)bwd_groups(max_pairs) * bwd_partial_floats(num_rbf);
 }
 
+namespace {
+
+int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
+                      const int32_t* n_pairs_dev, int64_t max_pairs, const float* offsets,
+                      float coeff, int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                      int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                      const float* W1, const float* b1, const float* W2, int num_filters,
+                      const PairAdjoint& adj, bool nodes, float* dW1, float* db1, float* dW2,
+                      float* workspace, int64_t workspace_floats, void* stream) {
+  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
+    return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
+  MLCG_REQUIRE(offsets && W1 && b1 && W2 && dW1 && db1 && dW2 && workspace);
+  MLCG_REQUIRE(max_pairs == 0 || (pos && pair_ij && n_pairs_dev));
+  const int groups = bwd_groups(max_pairs);
+  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * bwd_partial_floats(num_rbf));
+  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
+                             conv_cut_kind, conv_lo, conv_hi, act);
+  hipStream_t s = mlcg_stream(stream);
+  const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
+  allow_lds_once();
+  const int grid = max_pairs == 0 ? 1 : groups;
+  const bool small_k = num_rbf <= 64;
+#define MLCG_BWD_LAUNCH(KS, NODES)                                                         \
+  hipLaunchKernelGGL((filter_bwd_fused_kernel<KS, NODES>), dim3(grid), dim3(kBwdThreads), \
+                     lds, s, pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs,  \
+                     rp, W1, b1, W2, adj, workspace)
+  if (small_k && !nodes) MLCG_BWD_LAUNCH(16, false);
+  else if (small_k) MLCG_BWD_LAUNCH(16, true);
+  else if (!nodes) MLCG_BWD_LAUNCH(32, false);
+  else MLCG_BWD_LAUNCH(32, true);
+#undef MLCG_BWD_LAUNCH
+  const int total = kF * kF + kF * num_rbf + kF;
+  hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + kRedOut - 1) / kRedOut), dim3(256),
+                     0, s, workspace, groups, num_rbf, dW1, db1, dW2);
+  return mlcg_launch_status();
+}
+
+}  // namespace
+
 extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
                                const int32_t* n_pairs_dev, int64_t max_pairs,
                                const float* offsets, float coeff, int num_rbf,
@@ -789,35 +936,30 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
                                int num_filters, const float* Wbar, const float* Wdbar,
                                float* dW1, float* db1, float* dW2, float* workspace,
                                int64_t workspace_floats, void* stream) {
-  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
-    return MLCG_ERR_UNSUPPORTED;
-  MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
-  MLCG_REQUIRE(offsets && W1 && b1 && W2 && dW1 && db1 && dW2 && workspace);
-  MLCG_REQUIRE(max_pairs == 0 || (pos && pair_ij && n_pairs_dev && Wbar && Wdbar));
-  const int groups = bwd_groups(max_pairs);
-  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * bwd_partial_floats(num_rbf));
-  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
-                             conv_cut_kind, conv_lo, conv_hi, act);
-  hipStream_t s = mlcg_stream(stream);
-  const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
-  allow_lds_once();
-  if (max_pairs == 0) {
-    // no pairs: every gradient is zero (the reduce of one zero partial)
-    hipLaunchKernelGGL(filter_bwd_fused_kernel<16>, dim3(1), dim3(kBwdThreads), lds, s, pos,
-                       pair_ij, pair_ij + pair_stride, n_pairs_dev, (int64_t)0, rp, W1, b1,
-                       W2, Wbar, Wdbar, workspace);
-  } else if (num_rbf <= 64) {
-    hipLaunchKernelGGL(filter_bwd_fused_kernel<16>, dim3(groups), dim3(kBwdThreads), lds, s,
-                       pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1,
-                       b1, W2, Wbar, Wdbar, workspace);
-  } else {
-    hipLaunchKernelGGL(filter_bwd_fused_kernel<32>, dim3(groups), dim3(kBwdThreads), lds, s,
-                       pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1,
-                       b1, W2, Wbar, Wdbar, workspace);
-  }
-  const int total = kF * kF + kF * num_rbf + kF;
-  hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + kRedOut - 1) / kRedOut), dim3(256),
-                     0, s,
-                     workspace, groups, num_rbf, dW1, db1, dW2);
-  return mlcg_launch_status();
+  MLCG_REQUIRE(max_pairs == 0 || (Wbar && Wdbar));
+  PairAdjoint adj{Wbar, Wdbar, nullptr, nullptr, nullptr, nullptr, nullptr};
+  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, offsets, coeff,
+                           num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind, conv_lo,
+                           conv_hi, act, W1, b1, W2, num_filters, adj, false, dW1, db1, dW2,
+                           workspace, workspace_floats, stream);
+}
+
+extern "C" int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
+                                      int64_t pair_stride, const int32_t* n_pairs_dev,
+                                      int64_t max_pairs, const float* offsets, float coeff,
+                                      int num_rbf, int rbf_cut_kind, float rbf_lo,
+                                      float rbf_hi, int conv_cut_kind, float conv_lo,
+                                      float conv_hi, int act, const float* W1, const float* b1,
+                                      const float* W2, int num_filters, const float* gagg2,
+                                      const float* y, const float* gagg1, const float* ydot,
+                                      const float* ddot, float* dW1, float* db1, float* dW2,
+                                      float* workspace, int64_t workspace_floats,
+                                      void* stream) {
+  MLCG_REQUIRE(max_pairs == 0 || (gagg2 && y));
+  MLCG_REQUIRE(!gagg1 || ddot);
+  PairAdjoint adj{nullptr, nullptr, gagg2, y, gagg1, gagg1 ? ydot : nullptr, ddot};
+  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, offsets, coeff,
+                           num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind, conv_lo,
+                           conv_hi, act, W1, b1, W2, num_filters, adj, true, dW1, db1, dW2,
+                           workspace, workspace_floats, stream);
 }

@@ -144,11 +144,10 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
                                      f16=spec.f16, want_dist=(k == 0))
         if k == 0:
             st.dist = dist
-        y = x.mm(bp.A1.t())
+        y = ops.node_linear(x, bp.A1)
         agg = ops.cfconv_gather(y, W, graph)
-        z = _lin(agg, bp.A2, bp.c2)
+        z = ops.node_linear(agg, bp.A2, bias=bp.c2)
         s = act_value(z, spec.block_act)
-        v = _lin(s, bp.A3, bp.c3)
         st.W.append(W)
         st.Wd.append(Wd)
         if save:
@@ -157,7 +156,7 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             st.agg.append(agg)
             st.z.append(z)
             st.s.append(s)
-        x = x + v
+        x = ops.node_linear(s, bp.A3, bias=bp.c3, residual=x)  # x + lin(act(z))
     st.xL = x
     h = x
     n_lin = len(P.out_w)
@@ -197,17 +196,17 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     st.ybar1 = [None] * nb
     for k in range(nb - 1, -1, -1):
         bp = P.blocks[k]
-        sbar = xbar.mm(bp.A3)
+        sbar = ops.node_linear(xbar, bp.A3, transpose=True)
         d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
         zbar = sbar * d1
-        gagg = zbar.mm(bp.A2)
+        gagg = ops.node_linear(zbar, bp.A2, transpose=True)
         ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar)
         st.xbar_out[k] = xbar
         st.sbar1[k] = sbar
         st.zbar1[k] = zbar
         st.gagg1[k] = gagg
         st.ybar1[k] = ybar
-        xbar = xbar + ybar.mm(bp.A1)
+        xbar = ops.node_linear(ybar, bp.A1, transpose=True, residual=xbar)
     if not need_forces:
         return None
     return ops.pair_forces(st.pos, st.dist, dbar, graph)
@@ -220,18 +219,17 @@ def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> torch.Ten
     xdot = None
     st.xdot_in, st.ydot, st.aggdot, st.zdot, st.sdot = [], [], [], [], []
     for k, bp in enumerate(P.blocks):
-        ydot = None if xdot is None else xdot.mm(bp.A1.t())
+        ydot = None if xdot is None else ops.node_linear(xdot, bp.A1)
         aggdot = ops.cfconv_gather_tangent(ydot, st.y[k], st.W[k], st.Wd[k], st.ddot, graph)
-        zdot = aggdot.mm(bp.A2.t())
+        zdot = ops.node_linear(aggdot, bp.A2)
         d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
         sdot = d1 * zdot
-        vdot = sdot.mm(bp.A3.t())
         st.xdot_in.append(xdot)
         st.ydot.append(ydot)
         st.aggdot.append(aggdot)
         st.zdot.append(zdot)
         st.sdot.append(sdot)
-        xdot = vdot if xdot is None else xdot + vdot
+        xdot = ops.node_linear(sdot, bp.A3, residual=xdot)
     hdot = xdot
     n_lin = len(P.out_w)
     st.ohdot, st.ozdot = [], []
@@ -289,29 +287,33 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
     g_blocks = [None] * len(P.blocks)
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
-        sbar2 = xbar2.mm(bp.A3)
+        sbar2 = ops.node_linear(xbar2, bp.A3, transpose=True)
         d1, d2 = act_derivs(st.z[k], st.s[k], spec.block_act)
-        gA3 = ops.tmm(xbar2, st.s[k])
         zbar2 = sbar2 * d1
         if tangent_on:
-            gA3 = gA3 + ops.tmm(st.xbar_out[k], st.sdot[k])
+            gA3 = ops.node_tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k])
             zbar2 = zbar2 + st.sbar1[k] * d2 * st.zdot[k]
+        else:
+            gA3 = ops.node_tmm(xbar2, st.s[k])
         gc3 = xbar2.sum(0)
-        gagg2 = zbar2.mm(bp.A2)
-        gA2 = ops.tmm(zbar2, st.agg[k])
+        gagg2 = ops.node_linear(zbar2, bp.A2, transpose=True)
         if tangent_on:
-            gA2 = gA2 + ops.tmm(st.zbar1[k], st.aggdot[k])
+            gA2 = ops.node_tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k])
+        else:
+            gA2 = ops.node_tmm(zbar2, st.agg[k])
         gc2 = zbar2.sum(0)
-        ybar2, Wbar, Wdbar = ops.cfconv_gather_rev2(
-            gagg2, st.gagg1[k] if tangent_on else None, st.y[k],
-            st.ydot[k] if tangent_on else None, st.W[k], st.Wd[k],
-            st.ddot if tangent_on else None, graph)
-        gA1 = ops.tmm(ybar2, st.x[k])
+        g1 = st.gagg1[k] if tangent_on else None
+        yd = st.ydot[k] if tangent_on else None
+        dd = st.ddot if tangent_on else None
+        ybar2, _, _ = ops.cfconv_gather_rev2(gagg2, g1, st.y[k], yd, st.W[k], st.Wd[k], dd,
+                                             graph, pair_adjoints=False)
         if tangent_on and st.xdot_in[k] is not None:
-            gA1 = gA1 + ops.tmm(st.ybar1[k], st.xdot_in[k])
-        xbar2 = xbar2 + ybar2.mm(bp.A1)
-        gW1, gb1, gW2 = ops.filter_bwd(st.pos, graph, spec.filt, bp.W1, bp.b1, bp.W2, Wbar,
-                                       Wdbar)
+            gA1 = ops.node_tmm(ybar2, st.x[k], st.ybar1[k], st.xdot_in[k])
+        else:
+            gA1 = ops.node_tmm(ybar2, st.x[k])
+        xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
+        gW1, gb1, gW2 = ops.filter_bwd_cfconv(st.pos, graph, spec.filt, bp.W1, bp.b1, bp.W2,
+                                              gagg2, st.y[k], g1, yd, dd)
         g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
     g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
     out = [g_emb]

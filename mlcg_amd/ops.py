@@ -211,6 +211,46 @@ def tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------
+# Node-level linears (products on hipBLASLt, weight gradients on the MFMA
+# reduction kernel for F = 128)
+
+def node_linear(x: torch.Tensor, W: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                residual: Optional[torch.Tensor] = None, transpose: bool = False) -> torch.Tensor:
+    """x W^T (or x W with transpose=True) [+ bias] [+ residual] as one library
+    GEMM (hipBLASLt): the [N, 128] x [128, 128] products are left to the
+    library, which times at or below a hand-written MFMA tile for this shape
+    on MI355X; the epilogue terms ride in addmm's beta input."""
+    Wm = W if transpose else W.t()
+    if residual is not None and bias is not None:
+        return torch.addmm(residual + bias, x, Wm)
+    if residual is not None:
+        return torch.addmm(residual, x, Wm)
+    if bias is not None:
+        return torch.addmm(bias, x, Wm)
+    return x.mm(Wm)
+
+
+def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = None,
+             b2: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a1^T b1 (+ a2^T b2) reduced over the rows."""
+    shapes_ok = all(t is None or (t.dim() == 2 and t.shape[1] == NUM_FILTERS)
+                    for t in (a1, b1, a2, b2))
+    if shapes_ok and a1.is_cuda and a1.dtype == torch.float32:
+        rows = a1.shape[0]
+        out = torch.empty(NUM_FILTERS, NUM_FILTERS, dtype=torch.float32, device=a1.device)
+        nws = int(_lib.load().mlcg_node_tmm_workspace_floats(rows))
+        ws = torch.empty(nws, dtype=torch.float32, device=a1.device)
+        c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+        call("mlcg_node_tmm", ptr(c(a1)), ptr(c(b1)), ptr(c(a2)), ptr(c(b2)), rows,
+             NUM_FILTERS, 0, ptr(out), ptr(ws), nws, stream_handle(a1.device))
+        return out
+    out = tmm(a1, b1)
+    if a2 is not None:
+        out = out + tmm(a2, b2)
+    return out
+
+
+# --------------------------------------------------------------------------
 # Filter network
 
 @dataclass
@@ -278,6 +318,35 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     return dW1, db1, dW2
 
 
+def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
+                      W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor,
+                      gagg2: torch.Tensor, y: torch.Tensor, gagg1: Optional[torch.Tensor],
+                      ydot: Optional[torch.Tensor],
+                      ddot: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor,
+                                                             torch.Tensor]:
+    """filter_bwd with Wbar_p = g2_i y_j + g2_j y_i + g1_i yd_j + g1_j yd_i and
+    Wdbar_p = dd_p (g1_i y_j + g1_j y_i) formed in the kernel from node arrays."""
+    pos = _validate_pos(pos)
+    F = W1.shape[0]
+    K = spec.num_rbf
+    cap = graph.pair_capacity
+    dev = pos.device
+    nws = int(_lib.load().mlcg_filter_bwd_workspace_floats(cap, K))
+    _check(nws > 0, f"num_rbf={K} is not supported by the filter backward")
+    ws = torch.empty(nws, dtype=torch.float32, device=dev)
+    dW1 = torch.empty(F, K, dtype=torch.float32, device=dev)
+    db1 = torch.empty(F, dtype=torch.float32, device=dev)
+    dW2 = torch.empty(F, F, dtype=torch.float32, device=dev)
+    W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    call("mlcg_filter_bwd_cfconv", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev),
+         cap, ptr(spec.offsets), spec.coeff, K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
+         spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
+         ptr(W2c), F, ptr(c(gagg2)), ptr(c(y)), ptr(c(gagg1)), ptr(c(ydot)), ptr(ddot),
+         ptr(dW1), ptr(db1), ptr(dW2), ptr(ws), nws, stream_handle(dev))
+    return dW1, db1, dW2
+
+
 # --------------------------------------------------------------------------
 # CFConv gather/scatter family
 
@@ -321,13 +390,17 @@ def cfconv_gather_tangent(ydot: Optional[torch.Tensor], y: torch.Tensor, W: torc
 
 def cfconv_gather_rev2(gagg2: torch.Tensor, gagg1: Optional[torch.Tensor], y: torch.Tensor,
                        ydot: Optional[torch.Tensor], W: torch.Tensor, Wd: torch.Tensor,
-                       ddot: Optional[torch.Tensor], graph: PairGraph):
+                       ddot: Optional[torch.Tensor], graph: PairGraph,
+                       pair_adjoints: bool = True):
+    """ybar2 and (with pair_adjoints) the [P, F] adjoints Wbar, Wdbar."""
     gagg2 = gagg2.contiguous()
     F = gagg2.shape[1]
     ybar2 = torch.empty_like(gagg2)
     cap = graph.pair_capacity
-    Wbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
-    Wdbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
+    Wbar = Wdbar = None
+    if pair_adjoints:
+        Wbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
+        Wdbar = torch.empty(cap, F, dtype=torch.float32, device=gagg2.device)
     call("mlcg_cfconv_gather_rev2", ptr(gagg2),
          ptr(None if gagg1 is None else gagg1.contiguous()), ptr(y.contiguous()),
          ptr(None if ydot is None else ydot.contiguous()), ptr(W), ptr(Wd), ptr(ddot),
