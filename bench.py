@@ -402,7 +402,8 @@ def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; frames shard across GPUs with no exchange, see DESIGN.md",
+              "multi-GPU path (frames would shard across GPUs with no exchange; only the "
+              "parameter-gradient all-reduce of a training step would cross GPUs)",
               file=sys.stderr)
         return 2
     import torch

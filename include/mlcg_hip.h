@@ -51,17 +51,26 @@ int mlcg_frame_ptr_from_batch(const int64_t* batch, int64_t n_nodes,
                               void* stream);
 
 /* Pass 1 of the radius graph: per-node neighbour counts.
- * Edge (i, j) exists iff batch[i] == batch[j], (loop || i != j) and
+ * Edge (i, j) exists iff batch[i] == batch[j], (loop || i != j),
  * d2 < fl32(r*r), d2 = ((dx*dx + dy*dy) + dz*dz) in fp32 without FMA
- * contraction, dx = pos[j].x - pos[i].x.  Rows keep their lowest-index
- * `max_num_neighbors` neighbours; *overflow is set to 1 if any row had more.
- * deg[i] = kept neighbours, upper_deg[i] = kept neighbours with j > i.
- * Replaces the counting half of radius_kernel (radius.cu:88-145) and the
+ * contraction, dx = pos[j].x - pos[i].x, and j is not excluded from row i.
+ * Exclusions (both pointers null, or both set) use the reference's CSR:
+ * row i excludes exclude_pair_xs[ptr_exclude_pair_xs[i] ..
+ * ptr_exclude_pair_xs[i+1]), each segment sorted ascending, ptr of length
+ * n_nodes + 1 (mlcg_exclusion_pair_to_ptr builds it).  Rows keep their
+ * lowest-index `max_num_neighbors` non-excluded neighbours; *overflow gets
+ * bit 0 (1) if any row had more, and bit 2 (4) if a kept edge (i, j) has its
+ * reverse (j, i) excluded (an asymmetric graph, which the pair-based CFConv
+ * kernels cannot use).  deg[i] = kept neighbours, upper_deg[i] = kept
+ * neighbours with j > i.  Replaces the counting half of radius_kernel
+ * (radius.cu:88-145, exclusion test 113-133) and the
  * torch_cluster.radius_graph call of
  * src/mlcg/neighbor_list/torch_impl.py:216-224. */
 int mlcg_radius_count(const float* pos, const int64_t* batch,
                       const int64_t* frame_ptr, int64_t n_nodes, double r,
-                      int loop, int64_t max_num_neighbors, int32_t* deg,
+                      int loop, int64_t max_num_neighbors,
+                      const int64_t* exclude_pair_xs,
+                      const int64_t* ptr_exclude_pair_xs, int32_t* deg,
                       int32_t* upper_deg, int32_t* overflow, void* stream);
 
 /* Exclusive scan of two int32 vectors of length n into out_a/out_b (length
@@ -73,7 +82,8 @@ int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b,
                              int64_t n, int32_t* out_a, int32_t* out_b,
                              int32_t* workspace, void* stream);
 
-/* Pass 2: writes the canonical edge list.  edge_index is [2, edge_stride]
+/* Pass 2: writes the canonical edge list (same membership and exclusion
+ * arguments as pass 1).  edge_index is [2, edge_stride]
  * int64 (row 0 = centre i, row 1 = neighbour j).  Optional (nullable)
  * outputs for the CFConv pipeline: col[e] = j (int32), pair_ij [2,
  * pair_stride] (row 0 = i, row 1 = j, i < j) and eid2pair[e] for upper edges.
@@ -83,12 +93,26 @@ int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b,
 int mlcg_radius_fill(const float* pos, const int64_t* batch,
                      const int64_t* frame_ptr, int64_t n_nodes, double r,
                      int loop, int64_t max_num_neighbors,
+                     const int64_t* exclude_pair_xs,
+                     const int64_t* ptr_exclude_pair_xs,
                      const int32_t* rowptr, const int32_t* pairptr,
                      int64_t edge_capacity, int64_t edge_stride,
                      int64_t* edge_index, int32_t* col,
                      int64_t pair_capacity, int64_t pair_stride,
                      int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                      void* stream);
+
+/* HOST function (host pointers, no stream): the reference's
+ * exclusion_pair_to_ptr (exclusion_pairs.cpp:7-62).  exc_pair_index is
+ * [2, num_pairs] int64, row 0 = x (the excluded neighbour), row 1 = y (the
+ * centre).  Pairs are ordered by y, then x; pair_xs[num_pairs] receives the x
+ * of every pair in that order, y_ptr[num_nodes + 1] the row offsets (y_ptr[n]
+ * = pairs with y < n).  Pairs with y >= num_nodes stay at the end of pair_xs,
+ * outside every row; a negative y is an argument error when num_nodes > 0
+ * (the reference's TORCH_CHECK at line 47). */
+int mlcg_exclusion_pair_to_ptr(const int64_t* exc_pair_index,
+                               int64_t num_pairs, int64_t num_nodes,
+                               int64_t* pair_xs, int64_t* y_ptr);
 
 /* Pass 3: eid2pair for lower edges (i > j), by binary search of i in row j.
  * n_pairs_dev points at the live pair count (e.g. pairptr + n_nodes). */

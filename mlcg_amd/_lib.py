@@ -35,11 +35,12 @@ _U64 = _c.c_uint64
 _SIGNATURES = {
     "mlcg_version": [],
     "mlcg_frame_ptr_from_batch": [_P, _I64, _I64, _P, _P],
-    "mlcg_radius_count": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P],
+    "mlcg_radius_count": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
+    "mlcg_exclusion_pair_to_ptr": [_P, _I64, _I64, _P, _P],
     "mlcg_scan_workspace_ints": [_I64],
     "mlcg_exclusive_scan2_i32": [_P, _P, _I64, _P, _P, _P, _P],
-    "mlcg_radius_fill": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _I64, _I64, _P, _P,
-                         _I64, _I64, _P, _P, _P, _P],
+    "mlcg_radius_fill": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _I64, _I64, _P,
+                         _P, _I64, _I64, _P, _P, _P, _P],
     "mlcg_pair_reverse_map": [_P, _I64, _P, _I64, _P, _P, _P, _P],
     "mlcg_filter_fwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
                         _F32, _F32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],

@@ -14,6 +14,17 @@
 // coalesced runs.  Two passes (count, then fill at scanned offsets) give an
 // exact, deterministic layout without atomics, cooperative launches or host
 // synchronisation inside the library.
+//
+// Optional pair exclusion follows the reference kernel's CSR form
+// (radius.cu:113-133, built by exclusion_pair_to_ptr in exclusion_pairs.cpp:
+// 7-62): neighbour j is dropped from row i when j appears in
+// xs[ptr[i] .. ptr[i+1]), a segment sorted ascending.  Excluded neighbours do
+// not count towards max_num_neighbors, as in the reference.  Each lane looks
+// its candidate up by binary search in the row's segment.
+#include <algorithm>
+#include <utility>
+#include <vector>
+
 #include "common.h"
 
 namespace {
@@ -46,6 +57,20 @@ __device__ __forceinline__ float sqdist_exact(Vec3 a, Vec3 b) {
   return s;
 }
 
+// True when j occurs in the sorted segment xs[lo, hi).
+__device__ __forceinline__ bool in_sorted(const int64_t* __restrict__ xs, int64_t lo,
+                                          int64_t hi, int64_t j) {
+  const int64_t end = hi;
+  while (lo < hi) {
+    const int64_t mid = lo + ((hi - lo) >> 1);
+    if (xs[mid] < j)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo < end && xs[lo] == j;
+}
+
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
   // number of set bits of `mask` strictly below this lane
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
@@ -68,27 +93,39 @@ __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
     for (int64_t k = b + 1; k <= n_frames; ++k) ptr[k] = n;
 }
 
-// Shared sweep over row i: calls `emit(j, rank, is_upper, upper_rank)` for
-// every kept neighbour on the lanes that hold it; returns (kept, upper kept)
-// through the references and whether the row overflowed max_nn.
-template <bool kFill>
+// Shared sweep over row i: writes (fill pass) every kept neighbour from the
+// lane that holds it, returns (kept, upper kept) through the references and
+// whether the row overflowed max_nn.  With exclusions, `asym` is set when a
+// kept edge (i, j) has its reverse (j, i) excluded.
+template <bool kFill, bool kExcl>
 __device__ __forceinline__ bool sweep_row(
     const float* __restrict__ pos, int64_t i, int64_t start, int64_t end,
-    float r2, int loop, int64_t max_nn, int& kept, int& ukept,
+    float r2, int loop, int64_t max_nn, const int64_t* __restrict__ exs,
+    const int64_t* __restrict__ eptr, int& kept, int& ukept,
     int64_t* __restrict__ ei0, int64_t* __restrict__ ei1, int32_t* __restrict__ col,
     int64_t e_base, int64_t e_cap, int32_t* __restrict__ pi, int32_t* __restrict__ pj,
-    int32_t* __restrict__ eid2pair, int64_t p_base, int64_t p_cap, bool& dropped) {
+    int32_t* __restrict__ eid2pair, int64_t p_base, int64_t p_cap, bool& dropped,
+    bool& asym) {
   const int lane = mlcg_lane();
   const Vec3 a = load_pos(pos, i);
   int64_t total = 0;
   kept = 0;
   ukept = 0;
+  int64_t x_lo = 0, x_hi = 0;
+  if (kExcl) {
+    x_lo = eptr[i];
+    x_hi = eptr[i + 1];
+  }
   for (int64_t j0 = start; j0 < end; j0 += MLCG_WAVE) {
     const int64_t j = j0 + lane;
     bool hit = false;
     if (j < end) {
       float d2 = sqdist_exact(a, load_pos(pos, j));
       hit = (d2 < r2) && (loop || j != i);
+      if (kExcl && hit) {
+        hit = !in_sorted(exs, x_lo, x_hi, j);
+        if (!kFill && hit && in_sorted(exs, eptr[j], eptr[j + 1], i)) asym = true;
+      }
     }
     const uint64_t m = __ballot(hit);
     if (m == 0) continue;
@@ -126,47 +163,52 @@ __device__ __forceinline__ bool sweep_row(
   return total > max_nn;
 }
 
+template <bool kExcl>
 __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_count_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ batch,
     const int64_t* __restrict__ frame_ptr, int64_t n, float r2, int loop,
-    int64_t max_nn, int32_t* __restrict__ deg, int32_t* __restrict__ udeg,
-    int32_t* __restrict__ overflow) {
+    int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
+    int32_t* __restrict__ deg, int32_t* __restrict__ udeg, int32_t* __restrict__ overflow) {
   const int64_t waves = (int64_t)gridDim.x * kRowWaves;
-  bool dropped = false;
+  bool dropped = false, asym = false;
   for (int64_t i = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x / MLCG_WAVE); i < n;
        i += waves) {
     const int64_t b = batch[i];
     int kept, ukept;
-    bool over = sweep_row<false>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop, max_nn,
-                                 kept, ukept, nullptr, nullptr, nullptr, 0, 0, nullptr,
-                                 nullptr, nullptr, 0, 0, dropped);
+    bool over = sweep_row<false, kExcl>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop,
+                                        max_nn, exs, eptr, kept, ukept, nullptr, nullptr,
+                                        nullptr, 0, 0, nullptr, nullptr, nullptr, 0, 0,
+                                        dropped, asym);
     if (mlcg_lane() == 0) {
       deg[i] = kept;
       udeg[i] = ukept;
       if (over && overflow) atomicOr(overflow, 1);
     }
   }
+  if (kExcl && asym && overflow) atomicOr(overflow, 4);
 }
 
+template <bool kExcl>
 __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ batch,
     const int64_t* __restrict__ frame_ptr, int64_t n, float r2, int loop,
-    int64_t max_nn, const int32_t* __restrict__ rowptr,
-    const int32_t* __restrict__ pairptr, int64_t e_cap, int64_t e_stride,
-    int64_t* __restrict__ edge_index, int32_t* __restrict__ col, int64_t p_cap,
-    int64_t p_stride, int32_t* __restrict__ pair_ij, int32_t* __restrict__ eid2pair,
-    int32_t* __restrict__ overflow) {
+    int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ pairptr, int64_t e_cap,
+    int64_t e_stride, int64_t* __restrict__ edge_index, int32_t* __restrict__ col,
+    int64_t p_cap, int64_t p_stride, int32_t* __restrict__ pair_ij,
+    int32_t* __restrict__ eid2pair, int32_t* __restrict__ overflow) {
   const int64_t waves = (int64_t)gridDim.x * kRowWaves;
   int32_t* pi = pair_ij;
   int32_t* pj = pair_ij ? pair_ij + p_stride : nullptr;
-  bool dropped = false;
+  bool dropped = false, asym = false;
   for (int64_t i = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x / MLCG_WAVE); i < n;
        i += waves) {
     const int64_t b = batch[i];
     int kept, ukept;
-    sweep_row<true>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop, max_nn, kept, ukept,
-                    edge_index, edge_index + e_stride, col, rowptr[i], e_cap, pi, pj,
-                    eid2pair, pairptr ? pairptr[i] : 0, p_cap, dropped);
+    sweep_row<true, kExcl>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop, max_nn, exs,
+                           eptr, kept, ukept, edge_index, edge_index + e_stride, col,
+                           rowptr[i], e_cap, pi, pj, eid2pair, pairptr ? pairptr[i] : 0,
+                           p_cap, dropped, asym);
   }
   if (dropped && overflow) atomicOr(overflow, 2);
 }
@@ -330,16 +372,26 @@ extern "C" int mlcg_frame_ptr_from_batch(const int64_t* batch, int64_t n_nodes,
 
 extern "C" int mlcg_radius_count(const float* pos, const int64_t* batch,
                                  const int64_t* frame_ptr, int64_t n_nodes, double r,
-                                 int loop, int64_t max_num_neighbors, int32_t* deg,
+                                 int loop, int64_t max_num_neighbors,
+                                 const int64_t* exclude_pair_xs,
+                                 const int64_t* ptr_exclude_pair_xs, int32_t* deg,
                                  int32_t* upper_deg, int32_t* overflow, void* stream) {
   MLCG_REQUIRE(n_nodes >= 0 && r >= 0.0 && max_num_neighbors >= 0);
+  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && batch && frame_ptr && deg && upper_deg);
   const float r2 = (float)(r * r);
   unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, kRowWaves), 16);
-  hipLaunchKernelGGL(radius_count_kernel, dim3(groups), dim3(kRowWaves * MLCG_WAVE), 0,
-                     mlcg_stream(stream), pos, batch, frame_ptr, n_nodes, r2, loop,
-                     max_num_neighbors, deg, upper_deg, overflow);
+  dim3 grid(groups), block(kRowWaves * MLCG_WAVE);
+  hipStream_t s = mlcg_stream(stream);
+  if (exclude_pair_xs)
+    hipLaunchKernelGGL(radius_count_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
+                       n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
+                       ptr_exclude_pair_xs, deg, upper_deg, overflow);
+  else
+    hipLaunchKernelGGL(radius_count_kernel<false>, grid, block, 0, s, pos, batch, frame_ptr,
+                       n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, deg,
+                       upper_deg, overflow);
   return mlcg_launch_status();
 }
 
@@ -370,7 +422,9 @@ extern "C" int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b
 
 extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
                                 const int64_t* frame_ptr, int64_t n_nodes, double r,
-                                int loop, int64_t max_num_neighbors, const int32_t* rowptr,
+                                int loop, int64_t max_num_neighbors,
+                                const int64_t* exclude_pair_xs,
+                                const int64_t* ptr_exclude_pair_xs, const int32_t* rowptr,
                                 const int32_t* pairptr, int64_t edge_capacity,
                                 int64_t edge_stride, int64_t* edge_index, int32_t* col,
                                 int64_t pair_capacity, int64_t pair_stride,
@@ -378,18 +432,53 @@ extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
                                 void* stream) {
   MLCG_REQUIRE(n_nodes >= 0 && r >= 0.0 && max_num_neighbors >= 0);
   MLCG_REQUIRE(edge_capacity >= 0 && edge_stride >= edge_capacity);
+  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
   if (n_nodes == 0 || edge_capacity == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && batch && frame_ptr && rowptr && edge_index);
   MLCG_REQUIRE(!pair_ij || (pairptr && pair_stride >= pair_capacity));
   MLCG_REQUIRE(!eid2pair || pair_ij);
   const float r2 = (float)(r * r);
   unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, kRowWaves), 16);
-  hipLaunchKernelGGL(radius_fill_kernel, dim3(groups), dim3(kRowWaves * MLCG_WAVE), 0,
-                     mlcg_stream(stream), pos, batch, frame_ptr, n_nodes, r2, loop,
-                     max_num_neighbors, rowptr, pairptr, edge_capacity, edge_stride,
-                     edge_index, col, pair_capacity, pair_stride, pair_ij, eid2pair,
-                     overflow);
+  dim3 grid(groups), block(kRowWaves * MLCG_WAVE);
+  hipStream_t s = mlcg_stream(stream);
+  if (exclude_pair_xs)
+    hipLaunchKernelGGL(radius_fill_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
+                       n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
+                       ptr_exclude_pair_xs, rowptr, pairptr, edge_capacity, edge_stride,
+                       edge_index, col, pair_capacity, pair_stride, pair_ij, eid2pair,
+                       overflow);
+  else
+    hipLaunchKernelGGL(radius_fill_kernel<false>, grid, block, 0, s, pos, batch, frame_ptr,
+                       n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, rowptr,
+                       pairptr, edge_capacity, edge_stride, edge_index, col, pair_capacity,
+                       pair_stride, pair_ij, eid2pair, overflow);
   return mlcg_launch_status();
+}
+
+// Host-side conversion of an exclusion pair list to the per-row CSR the
+// kernels read (exclusion_pair_to_ptr, exclusion_pairs.cpp:7-62): pairs
+// (x, y) are ordered by y, then x; pair_xs lists the x of every pair in that
+// order and y_ptr[n] counts the pairs with y < n.  A pair with y < 0 is an
+// error once num_nodes > 0 (the reference's check at line 47); pairs with
+// y >= num_nodes stay at the end of pair_xs, outside every row.
+extern "C" int mlcg_exclusion_pair_to_ptr(const int64_t* exc_pair_index, int64_t num_pairs,
+                                          int64_t num_nodes, int64_t* pair_xs,
+                                          int64_t* y_ptr) {
+  MLCG_REQUIRE(num_pairs >= 0 && num_nodes >= 0 && y_ptr);
+  MLCG_REQUIRE(num_pairs == 0 || (exc_pair_index && pair_xs));
+  std::vector<std::pair<int64_t, int64_t>> yx((size_t)num_pairs);
+  for (int64_t k = 0; k < num_pairs; ++k)
+    yx[(size_t)k] = {exc_pair_index[num_pairs + k], exc_pair_index[k]};
+  std::sort(yx.begin(), yx.end());
+  for (int64_t k = 0; k < num_pairs; ++k) pair_xs[k] = yx[(size_t)k].second;
+  if (num_nodes > 0 && num_pairs > 0 && yx[0].first < 0) return MLCG_ERR_ARGUMENT;
+  int64_t k = 0;
+  y_ptr[0] = 0;
+  for (int64_t node = 0; node < num_nodes; ++node) {
+    while (k < num_pairs && yx[(size_t)k].first == node) ++k;
+    y_ptr[node + 1] = k;
+  }
+  return MLCG_OK;
 }
 
 extern "C" int mlcg_pair_reverse_map(const int32_t* pair_ij, int64_t pair_stride,

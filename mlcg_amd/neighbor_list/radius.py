@@ -13,6 +13,7 @@ from typing import Optional, Tuple
 import torch
 
 from .. import ops
+from .._lib import require_device
 
 
 def radius_graph(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None,
@@ -32,14 +33,60 @@ def radius_graph(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None
     return ei
 
 
+exclusion_pair_to_ptr = ops.exclusion_pair_to_ptr
+
+
+def radius_cuda(x: torch.Tensor, ptr_x: Optional[torch.Tensor], r: float,
+                max_num_neighbors: int, ignore_same_index: bool,
+                exclude_pair_xs: Optional[torch.Tensor] = None,
+                ptr_exclude_pair_xs: Optional[torch.Tensor] = None):
+    """(edge_index [2, E] int64, distance [E]) with the arguments of the
+    reference's native operator ``mlcg::radius_cuda`` (radius.cu:197-307):
+    frames given by ``ptr_x`` [B+1] (None = one frame), optional exclusion CSR.
+    Edges come out in canonical (centre, neighbour) order; x must be float32
+    (the reference also accepts f16/bf16/f64)."""
+    require_device(x)
+    _check_2d(x)
+    n = x.shape[0]
+    if ptr_x is None:
+        ptr_x = torch.tensor([0, n], dtype=torch.int64, device=x.device)
+    require_device(ptr_x)
+    ptr_x = ptr_x.to(torch.int64).contiguous()
+    if ptr_x.dim() != 1:
+        raise RuntimeError("ptr_x must be 1-D")
+    nodes = torch.arange(n, device=x.device)
+    batch = torch.searchsorted(ptr_x, nodes, right=True) - 1
+    g = ops.radius_graph(x.detach(), r, batch=batch, loop=not ignore_same_index,
+                         max_num_neighbors=max_num_neighbors, frame_ptr=ptr_x,
+                         exclude_pair_xs=exclude_pair_xs,
+                         ptr_exclude_pair_xs=ptr_exclude_pair_xs)
+    ei = g.edge_index
+    return ei, (x.detach()[ei[0]] - x.detach()[ei[1]]).norm(dim=1)
+
+
+def _check_2d(x: torch.Tensor) -> None:
+    if x.dim() != 2:
+        raise RuntimeError(f"x must be [N, D], got {tuple(x.shape)}")
+
+
 def radius_distance_fn(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None,
                        loop: bool = False, max_num_neighbors: int = 32,
-                       batch_size: Optional[int] = None):
-    """(edge_index [2, E], distance [E]) like radius.py:52-88."""
+                       batch_size: Optional[int] = None,
+                       exclude_pair_indices: Optional[torch.Tensor] = None):
+    """(edge_index [2, E], distance [E]) like radius.py:52-88, including the
+    optional exclusion pair list [2, M] (converted by exclusion_pair_to_ptr,
+    radius.py:77-84)."""
+    if x.numel() == 0:
+        return (torch.empty(2, 0, dtype=torch.long, device=x.device),
+                torch.empty(0, dtype=x.dtype, device=x.device))
+    exs = eptr = None
+    if exclude_pair_indices is not None:
+        exs, eptr = ops.exclusion_pair_to_ptr(exclude_pair_indices, x.size(0))
     # membership is decided in fp32 (the kernel's arithmetic); the distances
     # themselves are computed in x's dtype so fp64 gradchecks stay exact
     g = ops.radius_graph(x.detach().float(), r, batch=batch, loop=loop,
-                         max_num_neighbors=max_num_neighbors, n_frames=batch_size)
+                         max_num_neighbors=max_num_neighbors, n_frames=batch_size,
+                         exclude_pair_xs=exs, ptr_exclude_pair_xs=eptr)
     ei = g.edge_index
     d = (x.detach()[ei[0]] - x.detach()[ei[1]]).norm(dim=1)
     return ei, d
@@ -47,9 +94,10 @@ def radius_distance_fn(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] 
 
 class RadiusDistanceAGF(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, r, batch, loop, max_num_neighbors, batch_size):
+    def forward(ctx, x, r, batch, loop, max_num_neighbors, batch_size,
+                exclude_pair_indices=None):
         edge_index, distance = radius_distance_fn(x, r, batch, loop, max_num_neighbors,
-                                                  batch_size)
+                                                  batch_size, exclude_pair_indices)
         ctx.save_for_backward(x, distance, edge_index)
         ctx.mark_non_differentiable(edge_index)
         return distance, edge_index
@@ -57,7 +105,7 @@ class RadiusDistanceAGF(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_d, grad_ei):
         x, distance, edge_index = ctx.saved_tensors
-        return (RadiusDistanceAGB.apply(x, distance, grad_d, edge_index),) + (None,) * 5
+        return (RadiusDistanceAGB.apply(x, distance, grad_d, edge_index),) + (None,) * 6
 
 
 class RadiusDistanceAGB(torch.autograd.Function):
@@ -89,6 +137,10 @@ class RadiusDistanceAGB(torch.autograd.Function):
 
 def radius_distance(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None,
                     loop: bool = False, max_num_neighbors: int = 32,
-                    batch_size: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(distance [E], edge_index [2, E]) with autograd on the distances."""
-    return RadiusDistanceAGF.apply(x, r, batch, loop, max_num_neighbors, batch_size)
+                    batch_size: Optional[int] = None,
+                    exclude_pair_indices: Optional[torch.Tensor] = None,
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(distance [E], edge_index [2, E]) with autograd on the distances
+    (radius.py:187-199)."""
+    return RadiusDistanceAGF.apply(x, r, batch, loop, max_num_neighbors, batch_size,
+                                   exclude_pair_indices)

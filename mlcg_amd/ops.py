@@ -74,6 +74,55 @@ def frame_ptr_from_batch(batch: torch.Tensor, n_frames: int) -> torch.Tensor:
     return out
 
 
+def exclusion_pair_to_ptr(exc_pair_index: torch.Tensor,
+                          num_nodes: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(pair_xs [M] int64, y_ptr [num_nodes + 1] int64): the per-centre CSR of
+    an exclusion pair list [2, M] (row 0 = excluded neighbour x, row 1 =
+    centre y), ordered by y then x, on the input's device.
+
+    Same contract as the reference's ``mlcg::exclusion_pair_to_ptr``
+    (exclusion_pairs.cpp:7-62): int64 input of shape [2, M], conversion on
+    the host, a RuntimeError for a negative centre index."""
+    _check(exc_pair_index.dtype == torch.int64, "exc_pair_index must be int64")
+    _check(exc_pair_index.dim() == 2 and exc_pair_index.shape[0] == 2,
+           f"exc_pair_index must be [2, M], got {tuple(exc_pair_index.shape)}")
+    _check(num_nodes >= 0, "num_nodes must be non-negative")
+    host = exc_pair_index.detach().cpu().contiguous()
+    m = host.shape[1]
+    pair_xs = torch.empty(m, dtype=torch.int64)
+    y_ptr = torch.empty(num_nodes + 1, dtype=torch.int64)
+    call("mlcg_exclusion_pair_to_ptr", ptr(host) if m else None, m, int(num_nodes),
+         ptr(pair_xs) if m else None, ptr(y_ptr))
+    dev = exc_pair_index.device
+    return pair_xs.to(dev), y_ptr.to(dev)
+
+
+def _validate_exclusions(exclude_pair_xs, ptr_exclude_pair_xs, n: int, dev):
+    if exclude_pair_xs is None and ptr_exclude_pair_xs is None:
+        return None, None
+    _check(exclude_pair_xs is not None and ptr_exclude_pair_xs is not None,
+           "exclude_pair_xs and ptr_exclude_pair_xs go together")
+    for t, name in ((exclude_pair_xs, "exclude_pair_xs"),
+                    (ptr_exclude_pair_xs, "ptr_exclude_pair_xs")):
+        require_device(t)
+        _check(t.device == dev, f"{name} must be on {dev}")
+        _check(t.dtype == torch.int64 and t.dim() == 1, f"{name} must be 1-D int64")
+    _check(ptr_exclude_pair_xs.numel() == n + 1,
+           f"ptr_exclude_pair_xs must have N + 1 = {n + 1} entries")
+    xs = exclude_pair_xs.contiguous()
+    eptr = ptr_exclude_pair_xs.contiguous()
+    if not torch.cuda.is_current_stream_capturing():
+        # the kernels read xs[eptr[i] .. eptr[i+1]) unchecked: make sure every
+        # segment lies inside xs (one host synchronisation, outside capture)
+        ok = torch.stack([(eptr[1:] >= eptr[:-1]).all(), eptr[0] >= 0,
+                          eptr[-1] <= xs.numel()]).all()
+        _check(bool(ok), "ptr_exclude_pair_xs must be non-decreasing, start at >= 0 and end "
+               "at <= len(exclude_pair_xs)")
+    if xs.numel() == 0:  # keep a valid address for the kernels
+        xs = torch.zeros(1, dtype=torch.int64, device=dev)
+    return xs, eptr
+
+
 def _validate_pos(pos: torch.Tensor) -> torch.Tensor:
     require_device(pos)
     _check(pos.dim() == 2 and pos.shape[1] == 3, f"pos must be [N, 3], got {tuple(pos.shape)}")
@@ -92,6 +141,8 @@ def radius_graph(
     n_frames: Optional[int] = None,
     frame_ptr: Optional[torch.Tensor] = None,
     capacity: Optional[int] = None,
+    exclude_pair_xs: Optional[torch.Tensor] = None,
+    ptr_exclude_pair_xs: Optional[torch.Tensor] = None,
 ) -> PairGraph:
     """All pairs (i, j) of the same frame with |pos[j] - pos[i]| < r.
 
@@ -113,6 +164,12 @@ def radius_graph(
     every later kernel stays in bounds, and ``graph.flags`` (bit 0: a row
     exceeded max_num_neighbors, bit 1: the capacity was exceeded) must be
     checked by the caller -- this is the form a captured graph replays.
+
+    ``exclude_pair_xs`` / ``ptr_exclude_pair_xs`` (int64, the CSR of
+    ``exclusion_pair_to_ptr``) drop listed neighbours from each row as the
+    reference's native kernel does (radius.cu:113-133); excluded neighbours
+    do not count towards ``max_num_neighbors``.  With ``with_pairs`` the
+    exclusions must be symmetric (flag bit 2 otherwise).
     """
     pos = _validate_pos(pos)
     n = pos.shape[0]
@@ -132,13 +189,14 @@ def radius_graph(
         if n_frames is None:
             n_frames = int(batch[-1].item()) + 1 if n > 0 else 0
         frame_ptr = frame_ptr_from_batch(batch, n_frames)
+    exs, eptr = _validate_exclusions(exclude_pair_xs, ptr_exclude_pair_xs, n, dev)
     s = stream_handle(dev)
 
     deg = torch.empty(n, dtype=torch.int32, device=dev)
     udeg = torch.empty(n, dtype=torch.int32, device=dev)
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
     call("mlcg_radius_count", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
-         int(max_num_neighbors), ptr(deg), ptr(udeg), ptr(flags), s)
+         int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(deg), ptr(udeg), ptr(flags), s)
     rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, _lib.load().mlcg_scan_workspace_ints(n)), dtype=torch.int32,
@@ -149,11 +207,15 @@ def radius_graph(
         # one host sync to size the outputs (the reference syncs at radius.cu:288)
         e_count, p_count, overflow = torch.stack(
             [rowptr[n], pairptr[n], flags[0]]).tolist()
-        if with_pairs and overflow:
+        if with_pairs and overflow & 1:
             raise RuntimeError(
                 f"max_num_neighbors={max_num_neighbors} binds: the truncated graph is not "
                 "symmetric and the pair-based CFConv kernels cannot use it; raise "
                 "max_num_neighbors")
+        if with_pairs and overflow & 4:
+            raise RuntimeError(
+                "the exclusion list is not symmetric: an edge (i, j) is kept while (j, i) is "
+                "excluded, and the pair-based CFConv kernels need a symmetric graph")
         e_cap, p_cap = e_count, p_count
     else:
         e_cap, p_cap = capacity, capacity // 2
@@ -167,7 +229,8 @@ def radius_graph(
         eid2pair = (torch.empty if capacity is None else torch.zeros)(
             e_cap, dtype=torch.int32, device=dev)
     call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
-         int(max_num_neighbors), ptr(rowptr), ptr(pairptr) if with_pairs else None,
+         int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr),
+         ptr(pairptr) if with_pairs else None,
          e_cap, e_cap, ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij),
          ptr(eid2pair), ptr(flags), s)
     if capacity is not None:

@@ -35,10 +35,10 @@ def _load():
         lib = ctypes.CDLL(_SO)
         P = ctypes.c_void_p
         lib.oracle_radius_count.argtypes = [P, P, ctypes.c_int64, ctypes.c_double,
-                                            ctypes.c_int, ctypes.c_int64, P, P]
+                                            ctypes.c_int, ctypes.c_int64, P, P, P, P]
         lib.oracle_radius_count.restype = ctypes.c_int64
         lib.oracle_radius_fill.argtypes = [P, P, ctypes.c_int64, ctypes.c_double,
-                                           ctypes.c_int, ctypes.c_int64, P, P]
+                                           ctypes.c_int, ctypes.c_int64, P, P, P, P]
         lib.oracle_radius_fill.restype = None
         _lib = lib
     return _lib
@@ -51,9 +51,27 @@ def frame_ptr_from_batch(batch: np.ndarray, n_frames: int | None = None) -> np.n
     return np.searchsorted(batch, np.arange(n_frames + 1), side="left").astype(np.int64)
 
 
+def exclusion_pair_to_ptr(exc_pair_index, num_nodes: int):
+    """(pair_xs [M], y_ptr [num_nodes + 1]) restating exclusion_pairs.cpp:30-58:
+    a stable lexsort by centre y (row 1), then neighbour x (row 0), and
+    y_ptr[n] = number of pairs with y < n.  Raises ValueError for a negative
+    y when num_nodes > 0 (the TORCH_CHECK at line 47)."""
+    exc = np.asarray(exc_pair_index, dtype=np.int64).reshape(2, -1)
+    x, y = exc[0], exc[1]
+    order = np.lexsort((x, y))
+    pair_xs = x[order]
+    ys = y[order]
+    if num_nodes > 0 and ys.size and ys[0] < 0:
+        raise ValueError("negative centre index in the exclusion list")
+    y_ptr = np.searchsorted(ys, np.arange(num_nodes + 1), side="left").astype(np.int64)
+    y_ptr[0] = 0  # set unconditionally at line 42
+    return pair_xs.astype(np.int64), y_ptr
+
+
 def radius_graph(pos, r: float, batch=None, loop: bool = False, max_num_neighbors: int = 32,
-                 n_frames: int | None = None):
-    """Returns (edge_index [2, E] int64, overflow flag)."""
+                 n_frames: int | None = None, exclude_pair_xs=None, ptr_exclude_pair_xs=None):
+    """Returns (edge_index [2, E] int64, overflow flag).  The optional
+    exclusion CSR is the one exclusion_pair_to_ptr returns."""
     pos = np.ascontiguousarray(np.asarray(pos, dtype=np.float32))
     n = pos.shape[0]
     if batch is None:
@@ -61,12 +79,22 @@ def radius_graph(pos, r: float, batch=None, loop: bool = False, max_num_neighbor
     ptr = frame_ptr_from_batch(batch, n_frames)
     nb = ptr.shape[0] - 1
     lib = _load()
+    exs = eptr = None
+    if exclude_pair_xs is not None:
+        exs = np.ascontiguousarray(np.asarray(exclude_pair_xs, dtype=np.int64))
+        if exs.size == 0:
+            exs = np.zeros(1, dtype=np.int64)
+        eptr = np.ascontiguousarray(np.asarray(ptr_exclude_pair_xs, dtype=np.int64))
+        assert eptr.shape == (n + 1,)
+    ex_p = None if exs is None else exs.ctypes.data
+    ep_p = None if eptr is None else eptr.ctypes.data
     deg = np.zeros(max(n, 1), dtype=np.int64)
     ovf = ctypes.c_int(0)
     total = lib.oracle_radius_count(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
-                                    int(max_num_neighbors), deg.ctypes.data,
+                                    int(max_num_neighbors), ex_p, ep_p, deg.ctypes.data,
                                     ctypes.addressof(ovf))
     ei = np.zeros((2, max(total, 1)), dtype=np.int64)
     lib.oracle_radius_fill(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
-                           int(max_num_neighbors), ei[0].ctypes.data, ei[1].ctypes.data)
+                           int(max_num_neighbors), ex_p, ep_p, ei[0].ctypes.data,
+                           ei[1].ctypes.data)
     return ei[:, :total].copy(), int(ovf.value)

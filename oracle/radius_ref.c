@@ -11,10 +11,28 @@
  * hits).  Output is the canonical edge list: rows (centre i) ascending,
  * neighbours j ascending.
  *
+ * Optional exclusions restate the reference's merge walk over the centre's
+ * sorted exclusion segment (radius.cu:30-58 is_in_sorted_array, called for
+ * every candidate at 113-133): the cursor advances past smaller values and a
+ * candidate is excluded when the cursor value equals it.  Excluded candidates
+ * do not count towards max_num_neighbors.
+ *
  * Built with -ffp-contract=off so that every product and sum is rounded to
  * float separately (no FMA), which is the arithmetic the HIP kernel uses.
  */
 #include <stdint.h>
+
+/* radius.cu:30-58: advances *cur over xs[*cur, end) while below q. */
+static int merge_member(int64_t q, const int64_t* xs, int64_t* cur, int64_t end) {
+  while (*cur < end) {
+    int64_t v = xs[*cur];
+    if (v < q)
+      ++*cur;
+    else
+      return v == q;
+  }
+  return 0;
+}
 
 static float sqdist(const float* pos, int64_t i, int64_t j) {
   float dx = pos[3 * j + 0] - pos[3 * i + 0];
@@ -29,16 +47,18 @@ static float sqdist(const float* pos, int64_t i, int64_t j) {
 /* deg[i] for every node; returns the total edge count, -1 on bad input.
  * *overflow is set when some row had more than max_nn hits. */
 int64_t oracle_radius_count(const float* pos, const int64_t* frame_ptr, int64_t n_frames,
-                            double r, int loop, int64_t max_nn, int64_t* deg,
-                            int* overflow) {
+                            double r, int loop, int64_t max_nn, const int64_t* exs,
+                            const int64_t* eptr, int64_t* deg, int* overflow) {
   const float r2 = (float)(r * r);
   int64_t total = 0;
   *overflow = 0;
   for (int64_t b = 0; b < n_frames; ++b) {
     for (int64_t i = frame_ptr[b]; i < frame_ptr[b + 1]; ++i) {
       int64_t c = 0, hits = 0;
+      int64_t cur = exs ? eptr[i] : 0, end = exs ? eptr[i + 1] : 0;
       for (int64_t j = frame_ptr[b]; j < frame_ptr[b + 1]; ++j) {
-        if (!loop && j == i) continue;
+        int excluded = exs ? merge_member(j, exs, &cur, end) : 0;
+        if (excluded || (!loop && j == i)) continue;
         if (sqdist(pos, i, j) < r2) {
           ++hits;
           if (c < max_nn) ++c;
@@ -55,14 +75,17 @@ int64_t oracle_radius_count(const float* pos, const int64_t* frame_ptr, int64_t 
 /* Writes edges into ei0 (centre) / ei1 (neighbour), each of length
  * sum(deg). */
 void oracle_radius_fill(const float* pos, const int64_t* frame_ptr, int64_t n_frames,
-                        double r, int loop, int64_t max_nn, int64_t* ei0, int64_t* ei1) {
+                        double r, int loop, int64_t max_nn, const int64_t* exs,
+                        const int64_t* eptr, int64_t* ei0, int64_t* ei1) {
   const float r2 = (float)(r * r);
   int64_t e = 0;
   for (int64_t b = 0; b < n_frames; ++b) {
     for (int64_t i = frame_ptr[b]; i < frame_ptr[b + 1]; ++i) {
       int64_t c = 0;
+      int64_t cur = exs ? eptr[i] : 0, end = exs ? eptr[i + 1] : 0;
       for (int64_t j = frame_ptr[b]; j < frame_ptr[b + 1] && c < max_nn; ++j) {
-        if (!loop && j == i) continue;
+        int excluded = exs ? merge_member(j, exs, &cur, end) : 0;
+        if (excluded || (!loop && j == i)) continue;
         if (sqdist(pos, i, j) < r2) {
           ei0[e] = i;
           ei1[e] = j;

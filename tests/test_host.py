@@ -181,3 +181,31 @@ def test_bench_algorithmic_work_formulas():
     assert bound == "mfma" and flops == 2 * 2 * (50 * 128 + 128 * 128) * P
     bound, byts, _ = bench.algorithmic_work("mlcg_cfconv_gather", E, P, N, B)
     assert bound == "hbm" and byts == 4 * 128 * P + 4 * E + 4 * (N + 1) + 8 * 128 * N
+
+
+def test_exclusion_pair_to_ptr_host_abi():
+    """mlcg_exclusion_pair_to_ptr is a host function of the C ABI (the
+    reference converts on the host too, exclusion_pairs.cpp:7-62): checked
+    against the oracle's restatement, including duplicates, centres past the
+    last node, an empty list and the negative-centre error."""
+    import numpy as np
+
+    from mlcg_amd import ops
+    from oracle import radius as oracle_radius
+
+    rng = np.random.default_rng(2)
+    for n, m in [(1, 3), (17, 0), (50, 400), (200, 5000)]:
+        x = rng.integers(-3, n + 3, m)
+        y = rng.integers(0, n + 2, m)
+        exc = np.stack([x, y]).astype(np.int64)
+        xs, yp = ops.exclusion_pair_to_ptr(torch.from_numpy(exc), n)
+        want_xs, want_yp = oracle_radius.exclusion_pair_to_ptr(exc, n)
+        assert xs.dtype == torch.int64 and yp.dtype == torch.int64
+        assert np.array_equal(xs.numpy(), want_xs)
+        assert np.array_equal(yp.numpy(), want_yp)
+    with pytest.raises(RuntimeError):
+        ops.exclusion_pair_to_ptr(torch.tensor([[0, 1], [-1, 0]]), 3)
+    xs, yp = ops.exclusion_pair_to_ptr(torch.tensor([[0, 1], [-1, 0]]), 0)
+    assert yp.tolist() == [0] and xs.tolist() == [0, 1]
+    with pytest.raises(RuntimeError):
+        ops.exclusion_pair_to_ptr(torch.tensor([[0, 1], [1, 0]], dtype=torch.int32), 3)

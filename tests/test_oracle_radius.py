@@ -147,3 +147,106 @@ def test_oracle_golden_fixture():
     g = np.load(path)
     ei, _ = oracle_radius.radius_graph(g["pos"], float(g["r"]), g["batch"], False, 1000)
     assert np.array_equal(ei, g["edge_index"])
+
+
+# ---------------------------------------------------------------------------
+# Pair exclusion (radius.cu:113-133, exclusion_pairs.cpp:7-62)
+
+def test_exclusion_to_ptr_worked_example():
+    """Pairs (x, y) = (2,1), (1,2), (3,2), (2,2), (2,3), num_nodes = 4.
+    Following the code of exclusion_pairs.cpp:30-58 by hand (stable argsort
+    by x, then stable argsort by y; y_ptr[n+1] = pairs with y <= n): the
+    y = 1 row holds x = 2, the y = 2 row x = 1, 2, 3, the y = 3 row x = 2.
+    (The comment example at exclusion_pairs.cpp:15-19 lists other values;
+    the code is what the kernel consumes.)"""
+    exc = np.array([[2, 1, 3, 2, 2], [1, 2, 2, 2, 3]], dtype=np.int64)
+    xs, yp = oracle_radius.exclusion_pair_to_ptr(exc, 4)
+    assert xs.tolist() == [2, 1, 2, 3, 2]
+    assert yp.tolist() == [0, 0, 1, 4, 5]
+
+
+def _random_exclusions(rng, n, m, n_out=0):
+    x = rng.integers(0, max(n, 1), m)
+    y = rng.integers(0, max(n, 1), m)
+    if n_out:  # centres past the last node stay outside every row
+        x = np.concatenate([x, rng.integers(0, n, n_out)])
+        y = np.concatenate([y, rng.integers(n, n + 5, n_out)])
+    return np.stack([x, y]).astype(np.int64)
+
+
+def test_exclusion_to_ptr_rows_brute_force():
+    rng = np.random.default_rng(11)
+    n = 40
+    exc = _random_exclusions(rng, n, 300, n_out=7)  # includes duplicates
+    xs, yp = oracle_radius.exclusion_pair_to_ptr(exc, n)
+    assert yp.shape == (n + 1,) and yp[0] == 0 and yp[-1] == 300
+    assert xs.shape == (307,)
+    for y in range(n):
+        seg = xs[yp[y]:yp[y + 1]]
+        want = np.sort(exc[0][exc[1] == y])
+        assert np.array_equal(seg, want)
+    # the 7 out-of-range centres come last, ordered by (y, x)
+    tail = sorted(zip(exc[1][300:], exc[0][300:]))
+    assert xs[300:].tolist() == [x for _, x in tail]
+
+
+def test_exclusion_to_ptr_negative_centre():
+    exc = np.array([[0, 1], [-1, 0]], dtype=np.int64)
+    with pytest.raises(ValueError):
+        oracle_radius.exclusion_pair_to_ptr(exc, 3)
+    xs, yp = oracle_radius.exclusion_pair_to_ptr(exc, 0)  # no rows: nothing checked
+    assert yp.tolist() == [0] and xs.tolist() == [0, 1]
+
+
+def _brute_rows(pos, r, batch, loop, mnn, excluded):
+    """Independent numpy float32 restatement: per row, candidates ascending,
+    drop excluded (i, j), keep the first mnn hits."""
+    r2 = np.float32(r * r)
+    out = []
+    for i in range(pos.shape[0]):
+        kept = 0
+        for j in np.nonzero(batch == batch[i])[0]:
+            if (j == i and not loop) or (i, int(j)) in excluded:
+                continue
+            d = pos[j] - pos[i]
+            s = np.float32(d[0] * d[0])
+            s = np.float32(s + np.float32(d[1] * d[1]))
+            s = np.float32(s + np.float32(d[2] * d[2]))
+            if s < r2 and kept < mnn:
+                out.append((i, int(j)))
+                kept += 1
+    return np.array(out, dtype=np.int64).reshape(-1, 2).T
+
+
+@pytest.mark.parametrize("loop,mnn", [(False, 1000), (True, 1000), (False, 3)])
+def test_oracle_exclusions_brute_force(loop, mnn):
+    """Exclusion = set difference on the edge (y, x) of every pair (x, y),
+    self pairs included, cross-frame pairs and duplicates harmless, and
+    excluded neighbours not counted towards max_num_neighbors."""
+    rng = np.random.default_rng(5 + mnn + int(loop))
+    n = 90
+    pos = (rng.random((n, 3)) * 5).astype(np.float32)
+    batch = _batch(n, (30, 70, 100))
+    exc = _random_exclusions(rng, n, 600)
+    exc = np.concatenate([exc, np.stack([np.arange(0, n, 7)] * 2)], axis=1)  # self pairs
+    xs, yp = oracle_radius.exclusion_pair_to_ptr(exc, n)
+    ei, _ = oracle_radius.radius_graph(pos, 2.5, batch, loop, mnn, exclude_pair_xs=xs,
+                                       ptr_exclude_pair_xs=yp)
+    excluded = set(zip(exc[1].tolist(), exc[0].tolist()))
+    want = _brute_rows(pos, 2.5, batch, loop, mnn, excluded)
+    assert np.array_equal(ei, want)
+    full, _ = oracle_radius.radius_graph(pos, 2.5, batch, loop, mnn)
+    if mnn >= n:
+        diff = {e for e in zip(*full.tolist())} - excluded
+        assert set(zip(*ei.tolist())) == diff
+        assert ei.shape[1] < full.shape[1]
+
+
+def test_oracle_exclusions_empty_list():
+    rng = np.random.default_rng(3)
+    pos = (rng.random((30, 3)) * 3).astype(np.float32)
+    xs, yp = oracle_radius.exclusion_pair_to_ptr(np.zeros((2, 0), np.int64), 30)
+    ei, _ = oracle_radius.radius_graph(pos, 1.5, None, False, 100, exclude_pair_xs=xs,
+                                       ptr_exclude_pair_xs=yp)
+    full, _ = oracle_radius.radius_graph(pos, 1.5, None, False, 100)
+    assert np.array_equal(ei, full)
