@@ -93,6 +93,10 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
         # weight gradients dW2 (two streams) and dW1 (two streams); the
         # forward recomputation of a, a' is not algorithmic work
         return "mfma", (2 * 2 * F * F + 2 * 2 * F * F + 2 * 2 * K_RBF * F) * P, "flop"
+    if name == "mlcg_node_gemm":
+        # one [N, 128] x [128, 128] product (its epilogue streams 2-6 [N, 128]
+        # tensors depending on the mode)
+        return "mfma", 2 * N * F * F, "flop"
     if name == "mlcg_cfconv_gather":
         return "hbm", sw * F * P + 4 * E + 4 * (N + 1) + 2 * 4 * F * N, "byte"
     if name == "mlcg_cfconv_gather_bwd":
@@ -124,6 +128,7 @@ KERNEL_SYMBOL = {
     "mlcg_filter_bwd": "filter_bwd_fused_kernel",
     "mlcg_filter_bwd_cfconv": "filter_bwd_fused_kernel",
     "mlcg_node_tmm": "node_tmm_kernel",
+    "mlcg_node_gemm": "node_gemm_kernel",
     "mlcg_cfconv_gather": "gather_kernel",
     "mlcg_cfconv_gather_bwd": "gather_bwd_kernel",
     "mlcg_cfconv_gather_tangent": "gather_tangent_kernel",

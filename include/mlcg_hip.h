@@ -255,8 +255,35 @@ int mlcg_segment_sum(const float* values, int64_t stride,
                      void* stream);
 
 /* ---------------------------------------------------------------------- */
-/* Weight gradients of the node-level linears (F = 128)                    */
+/* Node-level linears (F = H = 128) and their weight gradients             */
 /* ---------------------------------------------------------------------- */
+
+/* Epilogues of mlcg_node_gemm (y = x W^T, or x W when transpose_w != 0,
+ * then + bias[128] and + residual[rows, 128] when those are non-NULL):
+ *   PLAIN  out0 = y
+ *   ACT    out0 = y (optional), out1 = act(y)
+ *   DACT   out0 = y (optional), out1 = y * act'(z)
+ *   DACT2  out0 = y * act'(z) + e * act''(z) * f   (e, f optional, together)
+ * act'/act'' are evaluated from z and s = act(z) (tanh uses s only, and z
+ * may then be NULL; shifted softplus uses z). */
+typedef enum {
+  MLCG_NODE_PLAIN = 0,
+  MLCG_NODE_ACT = 1,
+  MLCG_NODE_DACT = 2,
+  MLCG_NODE_DACT2 = 3
+} mlcg_node_epilogue;
+
+/* [rows, 128] x [128, 128] product with a fused elementwise epilogue, all
+ * [rows, 128] tensors row-major fp32.  Replaces the Linear calls of the
+ * interaction block and CFConv (schnet.py:259-261 lin + activation,
+ * 343 lin1, 347 lin2 + bias) and their transposes in the force backward and
+ * the force-matching double backward, together with the activation and
+ * derivative elementwise kernels around them. */
+int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
+                   int transpose_w, const float* bias, const float* residual,
+                   int epilogue, int act, const float* z, const float* s,
+                   const float* e, const float* f, float* out0, float* out1,
+                   void* stream);
 
 /* out [128, 128] (+)= a1^T b1 (+ a2^T b2) for [rows, 128] inputs (a2/b2 may
  * be NULL), deterministic split over 64-row slices; `workspace` holds
@@ -268,6 +295,45 @@ int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
                   const float* b2, int64_t rows, int features, int accumulate,
                   float* out, float* workspace, int64_t workspace_floats,
                   void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Output network MLP([128, HH, 1]) with its reverse and tangent sweeps    */
+/* ---------------------------------------------------------------------- */
+
+/* Per node n (x [rows, 128], W0 [HH, 128], b0 [HH] or NULL, w1 [HH] = the
+ * final Linear's weight row, b1 [1] or NULL, HH in {32, 64, 128}):
+ *   oz = x W0^T + b0 ; os = act(oz) ; o = os . w1 + b1
+ * writes o [rows] (nullable), oz/os [rows, HH] (nullable, saved for the
+ * sweeps below) and, when reverse != 0, the adjoint entering the interaction
+ * blocks for the objective sum_n seed_n o_n (seed NULL = all ones):
+ *   xbar = ((seed w1) * act'(oz)) W0   [rows, 128].
+ * Replaces the output_network MLP of schnet.py:156,462-467 (mlp.py:56-58)
+ * and the first step of its autograd backward (gradients.py:216-222). */
+int mlcg_out_forward(const float* x, int64_t rows, int in_features, int hidden,
+                     const float* W0, const float* b0, const float* w1,
+                     const float* b1, int act, int reverse, const float* seed,
+                     float* o, float* oz, float* os, float* xbar, void* stream);
+
+/* Second-order sweep of the same network for sum_n tw_n odot_n + pw_n o_n
+ * (tw, pw nullable), with odot the tangent of o along xdot (xdot NULL = no
+ * tangent):
+ *   ozdot = xdot W0^T ; hdot = act'(oz) ozdot ; odot = hdot . w1
+ *   zbar2 = pw w1 act'(oz) + tw w1 act''(oz) ozdot ; xbar2 = zbar2 W0
+ *   gW0 = sum_n (tw w1 act'(oz))^T xdot + zbar2^T x ; gb0 = sum_n zbar2
+ *   gW1 = sum_n tw hdot + pw os ; gb1 = sum_n pw.
+ * oz may be NULL for tanh.  Outputs odot [rows] (nullable), xbar2 [rows, 128],
+ * gW0 [HH, 128], gb0 [HH] (nullable), gW1 [HH], gb1 [1] (nullable).
+ * `workspace` holds mlcg_out_rev2_workspace_floats(rows, HH) floats; the
+ * reductions are in a fixed order.  Replaces the output-network part of the
+ * force-matching double backward (losses.py:167-181 through
+ * gradients.py:216-222 with create_graph=True, pl/model.py:113-131). */
+int64_t mlcg_out_rev2_workspace_floats(int64_t rows, int hidden);
+int mlcg_out_rev2(const float* x, const float* xdot, int64_t rows,
+                  int in_features, int hidden, const float* W0, const float* w1,
+                  const float* oz, const float* os, int act, const float* tw,
+                  const float* pw, float* odot, float* xbar2, float* gW0,
+                  float* gb0, float* gW1, float* gb1, float* workspace,
+                  int64_t workspace_floats, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Priors: harmonic bonds and angles, Fourier dihedrals, repulsion          */

@@ -59,6 +59,13 @@ _SIGNATURES = {
     "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _P, _P],
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
+    "mlcg_node_gemm": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
+                       _P],
+    "mlcg_out_forward": [_P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P,
+                         _P],
+    "mlcg_out_rev2_workspace_floats": [_I64, _I32],
+    "mlcg_out_rev2": [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P,
+                      _P, _P, _P, _I64, _P],
     "mlcg_node_tmm_workspace_floats": [_I64],
     "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
     "mlcg_prior_order": [_I32],
@@ -70,7 +77,8 @@ _SIGNATURES = {
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
-             "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64}
+             "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,
+             "mlcg_out_rev2_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

@@ -1,19 +1,26 @@
-// Weight gradients of the node-level linears of the interaction blocks
-// (gfx950, MFMA fp32).
+// Node-level linears of the interaction blocks (gfx950, MFMA fp32).
 //
 // The CFConv and interaction-block linears of SchNet (conv.lin1, conv.lin2,
 // lin: mlcg/nn/schnet.py:259-261,343,347) act on [N, 128] node features with
-// 128 x 128 weights; their weight gradients are transposed products a^T b
-// with the reduction over the N ~ 10^4-10^5 rows, a shape (M = N = 128,
-// huge K) that a general GEMM library tiles poorly.  They run here on
-// v_mfma_f32_16x16x4f32:
+// 128 x 128 weights.  Both their products and their weight gradients run here
+// on v_mfma_f32_16x16x4f32:
 //
-//   node_tmm      out = a1^T b1 [+ a2^T b2] ([128, 128]): up to 128 workgroups
-//                 each reduce a fixed set of 64-row chunks (staged in LDS)
-//                 with the row index as the MFMA reduction axis (wave w owns
-//                 output rows 16w..16w+15) and write their partial; a second
-//                 kernel adds the partials in a fixed order -- deterministic
-//                 for a given row count.
+//   node_gemm     y = x W^T or x W ([N, 128]) with the elementwise work around
+//                 it fused into the store: bias, residual, the activation, or
+//                 the activation's first / second derivative factors of the
+//                 force and force-matching sweeps.  Persistent workgroups of
+//                 4 waves keep their 32-column slice of W in registers (as
+//                 MFMA B fragments, loaded once) and stream 16-row tiles of x
+//                 through LDS, double-buffered; each tile's result passes
+//                 through LDS once more so that the epilogue reads and writes
+//                 whole rows with float4 accesses.
+//   node_tmm      out = a1^T b1 [+ a2^T b2] ([128, 128]): the weight
+//                 gradients, a reduction over N ~ 10^4-10^5 rows.  Up to 128
+//                 workgroups each reduce a fixed set of 64-row chunks (staged
+//                 in LDS) with the row index as the MFMA reduction axis (wave w
+//                 owns output rows 16w..16w+15) and write their partial; a
+//                 second kernel adds the partials in a fixed order --
+//                 deterministic for a given row count.
 #include "common.h"
 
 namespace {
@@ -125,12 +132,260 @@ __global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// node_gemm
+#ifndef MLCG_NODE_GEMM_ROWS
+#define MLCG_NODE_GEMM_ROWS 16
+#endif
+#ifndef MLCG_NODE_GEMM_PER_CU
+#define MLCG_NODE_GEMM_PER_CU 3
+#endif
+constexpr int kGemmRows = MLCG_NODE_GEMM_ROWS;   // rows per tile
+constexpr int kGemmRT = kGemmRows / 16;          // 16-row MFMA tiles per tile
+constexpr int kGemmThreads = 256;                // wave w owns columns 32w..32w+31
+constexpr int kGemmXPer = kGemmRows * (kF / 4) / kGemmThreads;  // float4 per thread
+
+// Activation derivatives from the pre-activation z and the value s = act(z)
+// (the same expressions as the host-side act_derivs).
+__device__ __forceinline__ void act_d1d2(int act, float z, float s, float& d1, float& d2) {
+  if (act == MLCG_ACT_TANH) {
+    d1 = 1.0f - s * s;
+    d2 = -2.0f * s * d1;
+  } else {
+    const float sg = 1.0f / (1.0f + expf(-z));
+    d1 = sg;
+    d2 = sg * (1.0f - sg);
+  }
+}
+
+__device__ __forceinline__ float4 ld4(const float* __restrict__ p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ void st4(float* __restrict__ p, float4 v) {
+  *reinterpret_cast<float4*>(p) = v;
+}
+
+// Loads tile t (zero past `rows`) as kGemmXPer float4 per thread.
+__device__ __forceinline__ void gemm_load_x(float4 (&v)[kGemmXPer], const float* __restrict__ x,
+                                            int64_t t, int64_t rows) {
+#pragma unroll
+  for (int m = 0; m < kGemmXPer; ++m) {
+    const int c = threadIdx.x + m * kGemmThreads;
+    const int64_t r = t * kGemmRows + (c >> 5);
+    v[m] = r < rows ? ld4(x + r * kF + 4 * (c & 31)) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+__device__ __forceinline__ void gemm_store_x(float* xs, const float4 (&v)[kGemmXPer]) {
+#pragma unroll
+  for (int m = 0; m < kGemmXPer; ++m) {
+    const int c = threadIdx.x + m * kGemmThreads;
+    st4(xs + (c >> 5) * kTRow + 4 * (c & 31), v[m]);
+  }
+}
+
+// Epilogue on one float4 of the product (row r, columns col..col+3).
+template <int MODE>
+__device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col,
+                                              const float* __restrict__ bias,
+                                              const float* __restrict__ residual, int act,
+                                              const float* __restrict__ zin,
+                                              const float* __restrict__ sin_,
+                                              const float* __restrict__ ein,
+                                              const float* __restrict__ fin,
+                                              float* __restrict__ out0,
+                                              float* __restrict__ out1) {
+  const int64_t o = r * kF + col;
+  if (bias) {
+    const float4 b = ld4(bias + col);
+    y.x += b.x; y.y += b.y; y.z += b.z; y.w += b.w;
+  }
+  if (residual) {
+    const float4 b = ld4(residual + o);
+    y.x += b.x; y.y += b.y; y.z += b.z; y.w += b.w;
+  }
+  if (MODE == MLCG_NODE_PLAIN) {
+    st4(out0 + o, y);
+  } else if (MODE == MLCG_NODE_ACT) {
+    if (out0) st4(out0 + o, y);
+    st4(out1 + o, float4{mlcg_act_value(act, y.x), mlcg_act_value(act, y.y),
+                         mlcg_act_value(act, y.z), mlcg_act_value(act, y.w)});
+  } else {
+    const float4 s = ld4(sin_ + o);
+    const float4 z = act == MLCG_ACT_TANH ? s : ld4(zin + o);  // tanh needs s only
+    float4 d1, d2;
+    act_d1d2(act, z.x, s.x, d1.x, d2.x);
+    act_d1d2(act, z.y, s.y, d1.y, d2.y);
+    act_d1d2(act, z.z, s.z, d1.z, d2.z);
+    act_d1d2(act, z.w, s.w, d1.w, d2.w);
+    if (MODE == MLCG_NODE_DACT) {
+      if (out0) st4(out0 + o, y);
+      st4(out1 + o, float4{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w});
+    } else {  // MLCG_NODE_DACT2
+      float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
+      if (ein) {
+        const float4 e = ld4(ein + o), f = ld4(fin + o);
+        v.x += e.x * d2.x * f.x;
+        v.y += e.y * d2.y * f.y;
+        v.z += e.z * d2.z * f.z;
+        v.w += e.w * d2.w * f.w;
+      }
+      st4(out0 + o, v);
+    }
+  }
+}
+
+// y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true).
+// MFMA step kk of lane group q = l/16 covers k = 16(kk/4) + 4q + kk%4, so a
+// lane's four consecutive steps read one float4 of its x row.
+template <int MODE, bool kXW>
+__global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
+    const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
+    const float* __restrict__ bias, const float* __restrict__ residual, int act,
+    const float* __restrict__ zin, const float* __restrict__ sin_,
+    const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
+    float* __restrict__ out1) {
+  __shared__ float xs[2][kGemmRows * kTRow];
+  __shared__ float ys[kGemmRows * kTRow];
+  const int w = threadIdx.x / MLCG_WAVE;
+  const int l = mlcg_lane();
+  const int q = l >> 4, n = l & 15;
+  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  float b[2][32];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int col = 32 * w + 16 * c + n;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (kXW) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[c][4 * m + j] = W[(16 * m + 4 * q + j) * kF + col];
+      } else {  // the four k of one group are contiguous in row `col` of W
+        const float4 v = ld4(W + col * kF + 16 * m + 4 * q);
+        b[c][4 * m + 0] = v.x;
+        b[c][4 * m + 1] = v.y;
+        b[c][4 * m + 2] = v.z;
+        b[c][4 * m + 3] = v.w;
+      }
+    }
+  }
+  int64_t t = blockIdx.x;
+  float4 pf[kGemmXPer];
+  gemm_load_x(pf, x, t, rows);
+  gemm_store_x(xs[0], pf);
+  __syncthreads();
+  int buf = 0;
+  for (; t < tiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < tiles;
+    if (has_next) gemm_load_x(pf, x, tn, rows);
+    floatx4 acc[kGemmRT][2];
+#pragma unroll
+    for (int r = 0; r < kGemmRT; ++r)
+      acc[r][0] = acc[r][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const float* xa = xs[buf] + n * kTRow + 4 * q;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      float av[kGemmRT][4];
+#pragma unroll
+      for (int r = 0; r < kGemmRT; ++r) {
+        const float4 a = ld4(xa + 16 * r * kTRow + 16 * m);
+        av[r][0] = a.x; av[r][1] = a.y; av[r][2] = a.z; av[r][3] = a.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < kGemmRT; ++r) {
+          acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r][j], b[0][4 * m + j], acc[r][0],
+                                                           0, 0, 0);
+          acc[r][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r][j], b[1][4 * m + j], acc[r][1],
+                                                           0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kGemmRT; ++r)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          ys[(16 * r + 4 * q + i) * kTRow + 32 * w + 16 * c + n] = acc[r][c][i];
+    if (has_next) gemm_store_x(xs[buf ^ 1], pf);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kGemmXPer; ++m) {
+      const int c = threadIdx.x + m * kGemmThreads;
+      const int rr = c >> 5, col = 4 * (c & 31);
+      const int64_t r = t * kGemmRows + rr;
+      if (r < rows)
+        gemm_epilogue<MODE>(ld4(ys + rr * kTRow + col), r, col, bias, residual, act, zin, sin_,
+                            ein, fin, out0, out1);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+}
+
 int tmm_groups(int64_t rows) {
   const int64_t chunks = rows == 0 ? 1 : (rows + kTmmRows - 1) / kTmmRows;
   return (int)(chunks < 128 ? chunks : 128);
 }
 
+template <int MODE>
+void launch_node_gemm(bool xw, dim3 grid, hipStream_t s, const float* x, int64_t rows,
+                      const float* W, const float* bias, const float* residual, int act,
+                      const float* z, const float* sv, const float* e, const float* f,
+                      float* out0, float* out1) {
+  if (xw)
+    hipLaunchKernelGGL((node_gemm_kernel<MODE, true>), grid, dim3(kGemmThreads), 0, s, x, rows,
+                       W, bias, residual, act, z, sv, e, f, out0, out1);
+  else
+    hipLaunchKernelGGL((node_gemm_kernel<MODE, false>), grid, dim3(kGemmThreads), 0, s, x,
+                       rows, W, bias, residual, act, z, sv, e, f, out0, out1);
+}
+
 }  // namespace
+
+extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
+                              int transpose_w, const float* bias, const float* residual,
+                              int epilogue, int act, const float* z, const float* s,
+                              const float* e, const float* f, float* out0, float* out1,
+                              void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(rows >= 0 && (act == MLCG_ACT_TANH || act == MLCG_ACT_SSP));
+  MLCG_REQUIRE((e == nullptr) == (f == nullptr));
+  MLCG_REQUIRE(epilogue >= MLCG_NODE_PLAIN && epilogue <= MLCG_NODE_DACT2);
+  if (rows == 0) return MLCG_OK;
+  switch (epilogue) {
+    case MLCG_NODE_PLAIN: MLCG_REQUIRE(out0 != nullptr); break;
+    case MLCG_NODE_ACT: MLCG_REQUIRE(out1 != nullptr); break;
+    case MLCG_NODE_DACT: MLCG_REQUIRE(out1 && s && (z || act == MLCG_ACT_TANH)); break;
+    case MLCG_NODE_DACT2: MLCG_REQUIRE(out0 && s && (z || act == MLCG_ACT_TANH)); break;
+    default: break;
+  }
+  MLCG_REQUIRE(x && W);
+  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  const dim3 grid(mlcg_persistent_groups(tiles, MLCG_NODE_GEMM_PER_CU));
+  hipStream_t st = mlcg_stream(stream);
+  const bool xw = transpose_w != 0;
+  switch (epilogue) {
+    case MLCG_NODE_PLAIN:
+      launch_node_gemm<MLCG_NODE_PLAIN>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+                                        f, out0, out1);
+      break;
+    case MLCG_NODE_ACT:
+      launch_node_gemm<MLCG_NODE_ACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e, f,
+                                      out0, out1);
+      break;
+    case MLCG_NODE_DACT:
+      launch_node_gemm<MLCG_NODE_DACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+                                       f, out0, out1);
+      break;
+    default:
+      launch_node_gemm<MLCG_NODE_DACT2>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+                                        f, out0, out1);
+      break;
+  }
+  return mlcg_launch_status();
+}
 
 extern "C" int64_t mlcg_node_tmm_workspace_floats(int64_t rows) {
   if (rows < 0) return -1;

@@ -32,7 +32,7 @@ from typing import List, Optional, Tuple
 import torch
 
 from .. import ops
-from .activations import act_derivs, act_value
+from .activations import ACT_TANH, act_derivs, act_value
 
 
 @dataclass
@@ -128,15 +128,63 @@ class State:
     ohdot: List[torch.Tensor] = field(default_factory=list)
     ozdot: List[torch.Tensor] = field(default_factory=list)
     odot: Optional[torch.Tensor] = None
+    # fused output network
+    xdotL: Optional[torch.Tensor] = None      # tangent of the last block output
+    out_seed: Optional[torch.Tensor] = None   # reverse seed the forward already applied
+    out_xbar: Optional[torch.Tensor] = None   # ... and the adjoint it produced
+
+
+def _out_fused(P: "Params") -> bool:
+    """True when the output network is MLP([128, HH, 1]) with HH in the
+    kernel's set (StandardSchNet's [64] default shape)."""
+    return (len(P.out_w) == 2 and P.out_w[1].shape[0] == 1
+            and P.out_w[0].shape[1] == ops.NUM_FILTERS
+            and P.out_w[0].shape[0] in ops.OUT_HIDDEN
+            and P.out_w[1].shape[1] == P.out_w[0].shape[0])
 
 
 def _lin(x, w, b=None):
     return torch.addmm(b, x, w.t()) if b is not None else x.mm(w.t())
 
 
+# Node linears with their elementwise neighbours fused (mlcg_node_gemm); the
+# unfused forms serve hidden widths the kernel does not tile.
+
+def _lin_act(x, A, c, act, want_z):
+    """(z, s) = (x A^T + c, act(z)); z is None when not wanted."""
+    if ops._node_gemm_ok(x, A):
+        return ops.node_gemm(x, A, bias=c, epilogue=ops.NODE_ACT, act=act, want_out0=want_z)
+    z = ops.node_linear(x, A, bias=c)
+    return z, act_value(z, act)
+
+
+def _lin_dact(x, A, z, s, act, transpose):
+    """(y, y * act'(z)) with y = x A^T (x A with transpose)."""
+    if ops._node_gemm_ok(x, A):
+        return ops.node_gemm(x, A, transpose=transpose, epilogue=ops.NODE_DACT, act=act, z=z,
+                             s=s)
+    y = ops.node_linear(x, A, transpose=transpose)
+    d1, _ = act_derivs(z, s, act)
+    return y, y * d1
+
+
+def _lin_dact2(x, A, z, s, act, e, f):
+    """(x A) * act'(z) [+ e * act''(z) * f]."""
+    if ops._node_gemm_ok(x, A):
+        return ops.node_gemm(x, A, transpose=True, epilogue=ops.NODE_DACT2, act=act, z=z, s=s,
+                             e=e, f=f)[0]
+    y = ops.node_linear(x, A, transpose=True)
+    d1, d2 = act_derivs(z, s, act)
+    v = y * d1
+    return v if e is None else v + e * d2 * f
+
+
 def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
-            graph: ops.PairGraph, save: bool = True) -> Tuple[torch.Tensor, State]:
-    """Energies [B] and the saved state."""
+            graph: ops.PairGraph, save: bool = True,
+            rev_seed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, State]:
+    """Energies [B] and the saved state.  With rev_seed, the output network's
+    kernel also forms the adjoint a following reverse1(seed=rev_seed) starts
+    from."""
     st = State(pos=pos, types=types, graph=graph)
     x = P.emb.index_select(0, types)
     for k, bp in enumerate(P.blocks):
@@ -146,8 +194,9 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             st.dist = dist
         y = ops.node_linear(x, bp.A1)
         agg = ops.cfconv_gather(y, W, graph)
-        z = ops.node_linear(agg, bp.A2, bias=bp.c2)
-        s = act_value(z, spec.block_act)
+        # z itself is only read back by the shifted-softplus derivatives
+        z, s = _lin_act(agg, bp.A2, bp.c2, spec.block_act,
+                        want_z=save and spec.block_act != ACT_TANH)
         st.W.append(W)
         st.Wd.append(Wd)
         if save:
@@ -158,6 +207,14 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             st.s.append(s)
         x = ops.node_linear(s, bp.A3, bias=bp.c3, residual=x)  # x + lin(act(z))
     st.xL = x
+    if _out_fused(P):
+        o, oz, os_, xbar = ops.out_forward(x, P.out_w[0], P.out_b[0], P.out_w[1], P.out_b[1],
+                                           spec.out_act, seed=rev_seed,
+                                           reverse=rev_seed is not None, save=save)
+        st.oz, st.os_, st.o = [oz], [os_], o
+        if rev_seed is not None:
+            st.out_seed, st.out_xbar = rev_seed, xbar
+        return ops.segment_sum(o, graph.frame_ptr), st
     h = x
     n_lin = len(P.out_w)
     for k in range(n_lin):
@@ -181,12 +238,21 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     the forces -d/dpos (sum_n seed_n o_n) and saves the adjoints."""
     graph = st.graph
     n_lin = len(P.out_w)
-    hbar = seed.view(-1, 1) * P.out_w[-1]  # [N, n_last_in]
-    for k in range(n_lin - 2, -1, -1):
-        d1, _ = act_derivs(st.oz[k], st.os_[k], spec.out_act)
-        zbar = hbar * d1
-        hbar = zbar.mm(P.out_w[k])
-    xbar = hbar
+    if _out_fused(P):
+        if st.out_seed is seed:
+            xbar = st.out_xbar
+        else:
+            xbar = ops.out_forward(st.xL, P.out_w[0], P.out_b[0], P.out_w[1], P.out_b[1],
+                                   spec.out_act, seed=seed, reverse=True, want_o=False,
+                                   save=False)[3]
+        st.out_seed = st.out_xbar = None
+    else:
+        hbar = seed.view(-1, 1) * P.out_w[-1]  # [N, n_last_in]
+        for k in range(n_lin - 2, -1, -1):
+            d1, _ = act_derivs(st.oz[k], st.os_[k], spec.out_act)
+            zbar = hbar * d1
+            hbar = zbar.mm(P.out_w[k])
+        xbar = hbar
     dbar = torch.zeros(graph.pair_capacity, dtype=torch.float32, device=st.pos.device)
     nb = len(P.blocks)
     st.xbar_out = [None] * nb
@@ -196,9 +262,7 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     st.ybar1 = [None] * nb
     for k in range(nb - 1, -1, -1):
         bp = P.blocks[k]
-        sbar = ops.node_linear(xbar, bp.A3, transpose=True)
-        d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
-        zbar = sbar * d1
+        sbar, zbar = _lin_dact(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True)
         gagg = ops.node_linear(zbar, bp.A2, transpose=True)
         ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar)
         st.xbar_out[k] = xbar
@@ -212,8 +276,10 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     return ops.pair_forces(st.pos, st.dist, dbar, graph)
 
 
-def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> torch.Tensor:
-    """Forward-mode sweep along position direction u; returns odot [N, 1]."""
+def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> None:
+    """Forward-mode sweep along position direction u.  The output network's
+    tangent odot lands in st.odot here, or -- with the fused output network
+    -- in the following reverse2(want_odot=True)."""
     graph = st.graph
     st.ddot = ops.pair_ddot(st.pos, st.dist, graph, u)
     xdot = None
@@ -221,15 +287,17 @@ def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> torch.Ten
     for k, bp in enumerate(P.blocks):
         ydot = None if xdot is None else ops.node_linear(xdot, bp.A1)
         aggdot = ops.cfconv_gather_tangent(ydot, st.y[k], st.W[k], st.Wd[k], st.ddot, graph)
-        zdot = ops.node_linear(aggdot, bp.A2)
-        d1, _ = act_derivs(st.z[k], st.s[k], spec.block_act)
-        sdot = d1 * zdot
+        zdot, sdot = _lin_dact(aggdot, bp.A2, st.z[k], st.s[k], spec.block_act, False)
         st.xdot_in.append(xdot)
         st.ydot.append(ydot)
         st.aggdot.append(aggdot)
         st.zdot.append(zdot)
         st.sdot.append(sdot)
         xdot = ops.node_linear(sdot, bp.A3, residual=xdot)
+    st.xdotL = xdot
+    st.odot = None
+    if _out_fused(P):
+        return
     hdot = xdot
     n_lin = len(P.out_w)
     st.ohdot, st.ozdot = [], []
@@ -243,18 +311,34 @@ def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> torch.Ten
         else:
             hdot = zd
     st.odot = hdot
-    return hdot
+
+
+def _out_reverse2(spec, P, st, tw, pw, want_odot):
+    """Output-network part of reverse2 as one kernel: (xbar2, g_out_w,
+    g_out_b); also sets st.odot when asked."""
+    tangent_on = tw is not None
+    odot, xbar2, gW0, gb0, gW1, gb1 = ops.out_rev2(
+        st.xL, st.xdotL if (tangent_on or want_odot) else None, P.out_w[0], P.out_w[1],
+        st.oz[0], st.os_[0], spec.out_act, tw, pw, P.out_b[0] is not None,
+        P.out_b[1] is not None, want_odot=want_odot)
+    if want_odot:
+        st.odot = odot
+    return xbar2, [gW0, gW1], [gb0, gb1]
 
 
 def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
-             pw: Optional[torch.Tensor]) -> List[torch.Tensor]:
+             pw: Optional[torch.Tensor], want_odot: bool = False) -> List[torch.Tensor]:
     """Parameter gradients of sum_n tw_n odot_n + pw_n o_n, in Params.flat()
-    order.  tw requires a preceding tangent() and reverse1(seed=tw)."""
+    order.  tw requires a preceding tangent() and reverse1(seed=tw).
+    want_odot makes sure st.odot holds the output tangent afterwards."""
     tangent_on = tw is not None
     graph = st.graph
     dev = st.pos.device
     N = st.pos.shape[0]
     n_lin = len(P.out_w)
+    if _out_fused(P):
+        xbar2, g_out_w, g_out_b = _out_reverse2(spec, P, st, tw, pw, want_odot)
+        return _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b)
     g_out_w = [None] * n_lin
     g_out_b = [None] * n_lin
     # last output linear: o = h W^T (+ b)
@@ -283,17 +367,24 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
             g_out_w[k] = ops.tmm(zbar2, st.oh[k])
         g_out_b[k] = zbar2.sum(0)
         hbar2 = zbar2.mm(P.out_w[k])
-    xbar2 = hbar2
+    return _blocks_reverse2(spec, P, st, tw, hbar2, g_out_w, g_out_b)
+
+
+def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
+    """reverse2 through the interaction blocks from the output network's
+    adjoint xbar2; assembles the gradients in Params.flat() order."""
+    tangent_on = tw is not None
+    graph = st.graph
+    n_lin = len(P.out_w)
     g_blocks = [None] * len(P.blocks)
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
-        sbar2 = ops.node_linear(xbar2, bp.A3, transpose=True)
-        d1, d2 = act_derivs(st.z[k], st.s[k], spec.block_act)
-        zbar2 = sbar2 * d1
         if tangent_on:
+            zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, st.sbar1[k],
+                               st.zdot[k])
             gA3 = ops.node_tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k])
-            zbar2 = zbar2 + st.sbar1[k] * d2 * st.zdot[k]
         else:
+            zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, None, None)
             gA3 = ops.node_tmm(xbar2, st.s[k])
         gc3 = xbar2.sum(0)
         gagg2 = ops.node_linear(zbar2, bp.A2, transpose=True)
@@ -343,8 +434,8 @@ class EnergyForces(torch.autograd.Function):
     @staticmethod
     def forward(ctx, spec, pos, types, batch, graph, training, *flat):
         P = Params.unflat(spec, list(flat))
-        E, st = forward(spec, P, pos, types, graph, save=True)
         ones = torch.ones(pos.shape[0], dtype=torch.float32, device=pos.device)
+        E, st = forward(spec, P, pos, types, graph, save=True, rev_seed=ones)
         F = reverse1(spec, P, st, ones)
         if training:
             ctx.spec, ctx.P, ctx.st, ctx.batch = spec, P, st, batch
@@ -418,8 +509,8 @@ class EnergyGrad(torch.autograd.Function):
         if spec.f16:
             raise NotImplementedError("the fp16 filter path has no double backward")
         # d/dtheta <gpos_bar, grad_pos(sum seed o)> = tangent along gpos_bar
-        odot = tangent(spec, P, st, gpos_bar)
-        grads = reverse2(spec, P, st, ctx.seed, None)
+        tangent(spec, P, st, gpos_bar)
+        grads = reverse2(spec, P, st, ctx.seed, None, want_odot=True)
         # d/dEbar_b <gpos_bar, grad E_b> = per-frame tangent of the energy
-        Ebar_grad = ops.segment_sum(odot, st.graph.frame_ptr)
+        Ebar_grad = ops.segment_sum(st.odot, st.graph.frame_ptr)
         return (None, None, None, Ebar_grad, None, *grads)

@@ -279,10 +279,12 @@ def tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 def node_linear(x: torch.Tensor, W: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 residual: Optional[torch.Tensor] = None, transpose: bool = False) -> torch.Tensor:
-    """x W^T (or x W with transpose=True) [+ bias] [+ residual] as one library
-    GEMM (hipBLASLt): the [N, 128] x [128, 128] products are left to the
-    library, which times at or below a hand-written MFMA tile for this shape
-    on MI355X; the epilogue terms ride in addmm's beta input."""
+    """x W^T (or x W with transpose=True) [+ bias] [+ residual]: the fused
+    node GEMM kernel for [N, 128] x [128, 128]; other shapes (the output
+    network) go to one library GEMM with the epilogue terms in addmm's beta
+    input."""
+    if _node_gemm_ok(x, W):
+        return node_gemm(x, W, transpose=transpose, bias=bias, residual=residual)[0]
     Wm = W if transpose else W.t()
     if residual is not None and bias is not None:
         return torch.addmm(residual + bias, x, Wm)
@@ -291,6 +293,53 @@ def node_linear(x: torch.Tensor, W: torch.Tensor, bias: Optional[torch.Tensor] =
     if bias is not None:
         return torch.addmm(bias, x, Wm)
     return x.mm(Wm)
+
+
+NODE_PLAIN, NODE_ACT, NODE_DACT, NODE_DACT2 = 0, 1, 2, 3
+
+
+def _node_gemm_ok(x: torch.Tensor, W: torch.Tensor) -> bool:
+    return (x.is_cuda and x.dtype == torch.float32 and x.dim() == 2
+            and x.shape[1] == NUM_FILTERS and tuple(W.shape) == (NUM_FILTERS, NUM_FILTERS))
+
+
+def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
+              bias: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+              epilogue: int = NODE_PLAIN, act: int = 0, z: Optional[torch.Tensor] = None,
+              s: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
+              f: Optional[torch.Tensor] = None, want_out0: bool = True,
+              ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """(out0, out1) of the fused node GEMM (mlcg_node_gemm) on [N, 128] fp32
+    rows and a [128, 128] weight: y = x W^T (x W with transpose) [+ bias]
+    [+ residual], then the epilogue
+
+        NODE_PLAIN  out0 = y
+        NODE_ACT    out0 = y, out1 = act(y)
+        NODE_DACT   out0 = y, out1 = y * act'(z)
+        NODE_DACT2  out0 = y * act'(z) [+ e * act''(z) * f]
+
+    (act' and act'' from z and s = act(z)).  out0 is skipped for ACT/DACT
+    when want_out0 is False."""
+    require_device(x)
+    _check(_node_gemm_ok(x, W), f"node_gemm takes [N, {NUM_FILTERS}] float32 rows and a "
+           f"[{NUM_FILTERS}, {NUM_FILTERS}] weight, got {tuple(x.shape)} / {tuple(W.shape)}")
+    n = x.shape[0]
+    dev = x.device
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    x, W, bias, residual, z, s, e, f = map(c, (x, W, bias, residual, z, s, e, f))
+    for t in (residual, z, s, e, f):
+        _check(t is None or (t.shape == x.shape and t.dtype == torch.float32
+                             and t.device == dev), "epilogue tensors must match x")
+    _check(bias is None or bias.numel() == NUM_FILTERS, "bias must have 128 entries")
+    out0 = out1 = None
+    if epilogue == NODE_PLAIN or epilogue == NODE_DACT2 or want_out0:
+        out0 = torch.empty_like(x)
+    if epilogue in (NODE_ACT, NODE_DACT):
+        out1 = torch.empty_like(x)
+    call("mlcg_node_gemm", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
+         ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
+         ptr(out1), stream_handle(dev))
+    return out0, out1
 
 
 def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = None,
@@ -311,6 +360,73 @@ def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = No
     if a2 is not None:
         out = out + tmm(a2, b2)
     return out
+
+
+# --------------------------------------------------------------------------
+# Output network MLP([128, HH, 1])
+
+OUT_HIDDEN = (32, 64, 128)
+
+
+def out_forward(x: torch.Tensor, W0: torch.Tensor, b0: Optional[torch.Tensor],
+                w1: torch.Tensor, b1: Optional[torch.Tensor], act: int,
+                seed: Optional[torch.Tensor] = None, reverse: bool = False,
+                want_o: bool = True, save: bool = True):
+    """(o [N], oz [N, HH] | None, os [N, HH] | None, xbar [N, 128] | None) of
+    the output network o = act(x W0^T + b0) . w1 + b1 (mlcg_out_forward).
+    With reverse, xbar = ((seed w1) * act'(oz)) W0 (seed None = ones).  oz
+    is kept only for the shifted softplus (tanh derivatives need os only)."""
+    require_device(x)
+    hh = W0.shape[0]
+    _check(x.dim() == 2 and x.shape[1] == NUM_FILTERS and x.dtype == torch.float32,
+           "out_forward takes [N, 128] float32 rows")
+    _check(hh in OUT_HIDDEN and tuple(W0.shape) == (hh, NUM_FILTERS) and w1.numel() == hh,
+           f"unsupported output network shape {tuple(W0.shape)}")
+    n = x.shape[0]
+    dev = x.device
+    x = x.contiguous()
+    o = torch.empty(n, dtype=torch.float32, device=dev) if want_o else None
+    os_ = torch.empty(n, hh, dtype=torch.float32, device=dev) if save else None
+    oz = torch.empty(n, hh, dtype=torch.float32, device=dev) if save and act != 0 else None
+    xbar = torch.empty_like(x) if reverse else None
+    if seed is not None:
+        seed = seed.contiguous().to(torch.float32)
+        _check(seed.numel() == n, "seed must have one entry per node")
+    call("mlcg_out_forward", ptr(x), n, NUM_FILTERS, hh, ptr(W0.contiguous()),
+         ptr(None if b0 is None else b0.contiguous()), ptr(w1.contiguous().view(-1)),
+         ptr(None if b1 is None else b1.contiguous()), int(act), int(reverse), ptr(seed),
+         ptr(o), ptr(oz), ptr(os_), ptr(xbar), stream_handle(dev))
+    return o, oz, os_, xbar
+
+
+def out_rev2(x: torch.Tensor, xdot: Optional[torch.Tensor], W0: torch.Tensor,
+             w1: torch.Tensor, oz: Optional[torch.Tensor], os_: torch.Tensor, act: int,
+             tw: Optional[torch.Tensor], pw: Optional[torch.Tensor], has_b0: bool,
+             has_b1: bool, want_odot: bool = False):
+    """(odot | None, xbar2, gW0, gb0 | None, gW1 [1, HH], gb1 | None): the
+    tangent and second reverse sweep of the output network (mlcg_out_rev2)."""
+    require_device(x)
+    hh = W0.shape[0]
+    n = x.shape[0]
+    dev = x.device
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    x, xdot, oz, os_, tw, pw = map(c, (x, xdot, oz, os_, tw, pw))
+    _check(os_ is not None and tuple(os_.shape) == (n, hh), "os must be [N, HH]")
+    _check(xdot is None or xdot.shape == x.shape, "xdot must match x")
+    _check(not want_odot or xdot is not None, "odot needs a tangent direction")
+    odot = torch.empty(n, dtype=torch.float32, device=dev) if want_odot else None
+    xbar2 = torch.empty_like(x)
+    gW0 = torch.empty(hh, NUM_FILTERS, dtype=torch.float32, device=dev)
+    gb0 = torch.empty(hh, dtype=torch.float32, device=dev) if has_b0 else None
+    gW1 = torch.empty(1, hh, dtype=torch.float32, device=dev)
+    gb1 = torch.empty(1, dtype=torch.float32, device=dev) if has_b1 else None
+    nws = int(_lib.load().mlcg_out_rev2_workspace_floats(n, hh))
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
+    call("mlcg_out_rev2", ptr(x), ptr(xdot), n, NUM_FILTERS, hh, ptr(W0.contiguous()),
+         ptr(w1.contiguous().view(-1)), ptr(oz), ptr(os_), int(act), ptr(tw), ptr(pw),
+         ptr(odot), ptr(xbar2), ptr(gW0), ptr(gb0), ptr(gW1), ptr(gb1), ptr(ws), nws,
+         stream_handle(dev))
+    return odot, xbar2, gW0, gb0, gW1, gb1
 
 
 # --------------------------------------------------------------------------

@@ -41,3 +41,75 @@ def test_node_tmm(rows):
     assert rel_err(ops.node_tmm(a1, b1, a2, b2), ref2) < 1e-6
     # deterministic: bitwise identical on a second call
     assert torch.equal(ops.node_tmm(a1, b1, a2, b2), ops.node_tmm(a1, b1, a2, b2))
+
+
+def _act64(z, act):
+    if act == 0:
+        return torch.tanh(z)
+    return torch.nn.functional.softplus(z) - torch.log(torch.tensor(2.0, dtype=z.dtype))
+
+
+def _derivs64(z, act):
+    if act == 0:
+        s = torch.tanh(z)
+        d1 = 1 - s * s
+        return d1, -2 * s * d1
+    sg = torch.sigmoid(z)
+    return sg, sg * (1 - sg)
+
+
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 1000, 17920])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("act", [0, 1])
+def test_node_gemm_epilogues(rows, transpose, act):
+    """Every epilogue of mlcg_node_gemm against fp64 torch at ragged row
+    counts (tiles of 16 rows) and both weight orientations."""
+    from mlcg_amd import ops
+
+    print(f"node_gemm rows={rows} transpose={transpose} act={act}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows * 4 + 2 * int(transpose) + act)
+    rnd = lambda *s: torch.randn(*s, device="cuda", generator=g)  # noqa: E731
+    x, r, z, e, f = (rnd(rows, 128) for _ in range(5))
+    W = rnd(128, 128) / 11
+    b = rnd(128)
+    s = _act64(z.double(), act).float()
+    Wd = W.double()
+    y = x.double().mm(Wd if transpose else Wd.t())
+    d1, d2 = _derivs64(z.double(), act)
+    if act == 0:  # the tanh derivative factors are formed from s as stored
+        sd = s.double()
+        d1 = 1 - sd * sd
+        d2 = -2 * sd * d1
+
+    out0, _ = ops.node_gemm(x, W, transpose=transpose)
+    assert rel_err(out0, y) < 1e-6
+    out0, _ = ops.node_gemm(x, W, transpose=transpose, bias=b, residual=r)
+    assert rel_err(out0, y + b.double() + r.double()) < 1e-6
+    zz, ss = ops.node_gemm(x, W, transpose=transpose, bias=b, epilogue=ops.NODE_ACT, act=act)
+    assert rel_err(zz, y + b.double()) < 1e-6
+    assert rel_err(ss, _act64(y + b.double(), act)) < 2e-6
+    _, only = ops.node_gemm(x, W, transpose=transpose, bias=b, epilogue=ops.NODE_ACT, act=act,
+                            want_out0=False)
+    assert torch.equal(only, ss)
+    yy, yd = ops.node_gemm(x, W, transpose=transpose, epilogue=ops.NODE_DACT, act=act, z=z, s=s)
+    assert rel_err(yy, y) < 1e-6
+    assert rel_err(yd, y * d1) < 2e-6
+    v, _ = ops.node_gemm(x, W, transpose=transpose, epilogue=ops.NODE_DACT2, act=act, z=z, s=s)
+    assert rel_err(v, y * d1) < 2e-6
+    v, _ = ops.node_gemm(x, W, transpose=transpose, epilogue=ops.NODE_DACT2, act=act, z=z, s=s,
+                         e=e, f=f)
+    assert rel_err(v, y * d1 + e.double() * d2 * f.double()) < 2e-6
+
+
+def test_node_gemm_deterministic_and_checks():
+    from mlcg_amd import ops
+
+    x = torch.randn(3000, 128, device="cuda")
+    W = torch.randn(128, 128, device="cuda")
+    assert torch.equal(ops.node_gemm(x, W)[0], ops.node_gemm(x, W)[0])
+    empty = ops.node_gemm(x[:0], W)[0]
+    assert empty.shape == (0, 128)
+    with pytest.raises(RuntimeError):
+        ops.node_gemm(x[:, :64], W[:, :64])
+    with pytest.raises(RuntimeError):
+        ops.node_gemm(x, W, epilogue=ops.NODE_DACT, act=0)  # z, s missing
