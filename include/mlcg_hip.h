@@ -286,15 +286,18 @@ int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
                    void* stream);
 
 /* out [128, 128] (+)= a1^T b1 (+ a2^T b2) for [rows, 128] inputs (a2/b2 may
- * be NULL), deterministic split over 64-row slices; `workspace` holds
- * mlcg_node_tmm_workspace_floats(rows) floats.  accumulate != 0 adds to out.
- * Replaces the weight-gradient products of the same linears (the autograd
- * backward of schnet.py:259-261,343,347 through the double backward). */
+ * be NULL) and, when colsum_a1 is non-NULL, colsum_a1 [128] (+)= the column
+ * sums of a1 (a bias gradient); deterministic split over contiguous row
+ * ranges, one per workgroup; `workspace` holds
+ * mlcg_node_tmm_workspace_floats(rows) floats.  accumulate != 0 adds to the
+ * outputs.  Replaces the weight- and bias-gradient reductions of the same
+ * linears (the autograd backward of schnet.py:259-261,343,347 through the
+ * double backward). */
 int64_t mlcg_node_tmm_workspace_floats(int64_t rows);
 int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
                   const float* b2, int64_t rows, int features, int accumulate,
-                  float* out, float* workspace, int64_t workspace_floats,
-                  void* stream);
+                  float* out, float* colsum_a1, float* workspace,
+                  int64_t workspace_floats, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Output network MLP([128, HH, 1]) with its reverse and tangent sweeps    */

@@ -67,7 +67,7 @@ _SIGNATURES = {
     "mlcg_out_rev2": [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P,
                       _P, _P, _P, _I64, _P],
     "mlcg_node_tmm_workspace_floats": [_I64],
-    "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
+    "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _I64, _P],
     "mlcg_prior_order": [_I32],
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],

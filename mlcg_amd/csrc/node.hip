@@ -30,40 +30,59 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kF = 128;
 constexpr int kFT = kF / 16;
 // ---------------------------------------------------------------------------
+// node_tmm
 constexpr int kTmmWaves = 8;
 constexpr int kTmmThreads = kTmmWaves * MLCG_WAVE;
-constexpr int kTmmRows = 64;                     // rows per workgroup slice
+constexpr int kTmmRows = 16;                     // rows per staged chunk
 constexpr int kTRow = kF + 4;                    // padded LDS row
+constexpr int kTmmMaxGroups = 256;               // one workgroup per CU
+constexpr int kTmmPer = kTmmRows * kF / 4 / kTmmThreads;  // float4 per thread per matrix
+constexpr int kTmmPart = kF * kF + kF;           // partial: out [128, 128] + column sums
 
-// Loads rows r0..r0+63 of a and b into LDS (zero past `rows`): 8 float4 per
-// thread, all issued before the stores.
-__device__ __forceinline__ void tmm_stage(float* la, float* lb, const float* __restrict__ a,
-                                          const float* __restrict__ b, int64_t r0,
-                                          int64_t rows) {
-  constexpr int kChunks = kTmmRows * kF / 4;       // float4 chunks per matrix
-  constexpr int kPer = kChunks / kTmmThreads;      // 4
-  float4 va[kPer], vb[kPer];
+// One 16-row chunk of up to four matrices, held in registers between its
+// global load and its LDS store.  Thread i always covers columns
+// 4 (i % 32) .. 4 (i % 32) + 3, which the column sum relies on.
+struct TmmChunk {
+  float4 v[4][kTmmPer];
+};
+
+__device__ __forceinline__ void tmm_load(TmmChunk& ch, const float* __restrict__ a1,
+                                         const float* __restrict__ b1,
+                                         const float* __restrict__ a2,
+                                         const float* __restrict__ b2, int64_t r0,
+                                         int64_t r_end) {
+  const float* src[4] = {a1, b1, a2, b2};
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int c = threadIdx.x + k * kTmmThreads;
-    const int64_t r = r0 + c / (kF / 4);
-    const int col = 4 * (c % (kF / 4));
-    const bool ok = r < rows;
-    va[k] = ok ? *reinterpret_cast<const float4*>(a + r * kF + col) : float4{0.f, 0.f, 0.f, 0.f};
-    vb[k] = ok ? *reinterpret_cast<const float4*>(b + r * kF + col) : float4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int m = 0; m < 4; ++m) {
+    if (m >= 2 && !a2) break;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int c = threadIdx.x + k * kTmmThreads;
-    const int rr = c / (kF / 4), col = 4 * (c % (kF / 4));
-    *reinterpret_cast<float4*>(la + rr * kTRow + col) = va[k];
-    *reinterpret_cast<float4*>(lb + rr * kTRow + col) = vb[k];
+    for (int k = 0; k < kTmmPer; ++k) {
+      const int c = threadIdx.x + k * kTmmThreads;
+      const int64_t r = r0 + c / (kF / 4);
+      ch.v[m][k] = r < r_end ? *reinterpret_cast<const float4*>(src[m] + r * kF + 4 * (c % (kF / 4)))
+                             : float4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 }
 
+__device__ __forceinline__ void tmm_store(float* buf, const TmmChunk& ch, bool two) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (m >= 2 && !two) break;
+#pragma unroll
+    for (int k = 0; k < kTmmPer; ++k) {
+      const int c = threadIdx.x + k * kTmmThreads;
+      *reinterpret_cast<float4*>(buf + m * kTmmRows * kTRow + (c / (kF / 4)) * kTRow +
+                                 4 * (c % (kF / 4))) = ch.v[m][k];
+    }
+  }
+}
+
+// acc[u] += la^T lb over the 16 staged rows, for output rows 16w..16w+15
+// (columns of a) and output columns 16u..16u+15 (columns of b).
 __device__ __forceinline__ void tmm_accumulate(const float* la, const float* lb, int w, int q,
                                                int n, floatx4* acc) {
-#pragma unroll 4
+#pragma unroll
   for (int kk = 0; kk < kTmmRows / 4; ++kk) {
     const float av = la[(4 * kk + q) * kTRow + 16 * w + n];
     float bv[kFT];
@@ -75,60 +94,94 @@ __device__ __forceinline__ void tmm_accumulate(const float* la, const float* lb,
   }
 }
 
+// Workgroup g reduces the contiguous rows [g R / G, (g+1) R / G) in 16-row
+// chunks, the next chunk's loads in flight while the current one feeds the
+// MFMAs, and writes its partial [128, 128] (+ the column sums of a1).
 __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     const float* __restrict__ a1, const float* __restrict__ b1,
     const float* __restrict__ a2, const float* __restrict__ b2, int64_t rows,
-    float* __restrict__ partial) {
-  __shared__ float lds[4 * kTmmRows * kTRow];
-  float* la1 = lds;
-  float* lb1 = la1 + kTmmRows * kTRow;
-  float* la2 = lb1 + kTmmRows * kTRow;
-  float* lb2 = la2 + kTmmRows * kTRow;
+    int want_colsum, float* __restrict__ partial) {
+  __shared__ float lds[2][4 * kTmmRows * kTRow];
+  __shared__ float4 csum[kTmmThreads];
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
+  const bool two = a2 != nullptr;
+  const int64_t G = gridDim.x;
+  const int64_t r_beg = rows * blockIdx.x / G;
+  const int64_t r_end = rows * (blockIdx.x + 1) / G;
   floatx4 acc[kFT];
 #pragma unroll
   for (int u = 0; u < kFT; ++u) acc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int64_t chunks = (rows + kTmmRows - 1) / kTmmRows;
-  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
-    const int64_t r0 = c * kTmmRows;
-    tmm_stage(la1, lb1, a1, b1, r0, rows);
-    if (a2) tmm_stage(la2, lb2, a2, b2, r0, rows);
+  float4 cs{0.f, 0.f, 0.f, 0.f};
+  TmmChunk ch;
+  tmm_load(ch, a1, b1, a2, b2, r_beg, r_end);
+  int buf = 0;
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += kTmmRows) {
+    tmm_store(lds[buf], ch, two);
+    if (want_colsum) {
+#pragma unroll
+      for (int k = 0; k < kTmmPer; ++k) {
+        cs.x += ch.v[0][k].x;
+        cs.y += ch.v[0][k].y;
+        cs.z += ch.v[0][k].z;
+        cs.w += ch.v[0][k].w;
+      }
+    }
     __syncthreads();
-    tmm_accumulate(la1, lb1, w, q, n, acc);
-    if (a2) tmm_accumulate(la2, lb2, w, q, n, acc);
-    __syncthreads();
+    if (r0 + kTmmRows < r_end) tmm_load(ch, a1, b1, a2, b2, r0 + kTmmRows, r_end);
+    const float* base = lds[buf];
+    tmm_accumulate(base, base + kTmmRows * kTRow, w, q, n, acc);
+    if (two) tmm_accumulate(base + 2 * kTmmRows * kTRow, base + 3 * kTmmRows * kTRow, w, q, n, acc);
+    buf ^= 1;
   }
-  float* o = partial + (int64_t)blockIdx.x * kF * kF;
+  float* o = partial + (int64_t)blockIdx.x * kTmmPart;
 #pragma unroll
   for (int u = 0; u < kFT; ++u)
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[(16 * w + 4 * q + i) * kF + 16 * u + n] = acc[u][i];
+  if (want_colsum) {
+    // threads t, t + 32, ..., t + 480 share columns 4 (t % 32) .. + 3
+    csum[threadIdx.x] = cs;
+    __syncthreads();
+    if (threadIdx.x < kF / 4) {
+      float4 t{0.f, 0.f, 0.f, 0.f};
+      for (int j = threadIdx.x; j < kTmmThreads; j += kF / 4) {
+        t.x += csum[j].x;
+        t.y += csum[j].y;
+        t.z += csum[j].z;
+        t.w += csum[j].w;
+      }
+      *reinterpret_cast<float4*>(o + kF * kF + 4 * threadIdx.x) = t;
+    }
+  }
 }
 
-// out (+)= sum of the `slices` partials.  A block covers 64 outputs with 8
-// waves, wave g summing the partials s = g (mod 8) (two interleaved
-// accumulators); the 8 wave sums are combined in a fixed order.
+// out (+)= sum of the `slices` partials (and colsum likewise).  A block
+// covers 64 outputs with 8 waves, wave g summing the partials s = g (mod 8)
+// (two interleaved accumulators); the 8 wave sums are combined in a fixed
+// order.
 __global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __restrict__ partial,
                                                               int slices, int accumulate,
-                                                              float* __restrict__ out) {
+                                                              float* __restrict__ out,
+                                                              float* __restrict__ colsum) {
   __shared__ float part[8][64];
   const int o = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int j = blockIdx.x * 64 + o;
   float a0 = 0.f, a1 = 0.f;
   int s = g;
   for (; s + 8 < slices; s += 16) {
-    a0 += partial[(int64_t)s * kF * kF + j];
-    a1 += partial[(int64_t)(s + 8) * kF * kF + j];
+    a0 += partial[(int64_t)s * kTmmPart + j];
+    a1 += partial[(int64_t)(s + 8) * kTmmPart + j];
   }
-  if (s < slices) a0 += partial[(int64_t)s * kF * kF + j];
+  if (s < slices) a0 += partial[(int64_t)s * kTmmPart + j];
   part[g][o] = a0 + a1;
   __syncthreads();
   if (g == 0) {
     const float v = ((part[0][o] + part[1][o]) + (part[2][o] + part[3][o])) +
                     ((part[4][o] + part[5][o]) + (part[6][o] + part[7][o]));
-    out[j] = accumulate ? out[j] + v : v;
+    float* dst = j < kF * kF ? out + j : colsum + (j - kF * kF);
+    *dst = accumulate ? *dst + v : v;
   }
 }
 
@@ -326,7 +379,7 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
 
 int tmm_groups(int64_t rows) {
   const int64_t chunks = rows == 0 ? 1 : (rows + kTmmRows - 1) / kTmmRows;
-  return (int)(chunks < 128 ? chunks : 128);
+  return (int)(chunks < kTmmMaxGroups ? chunks : kTmmMaxGroups);
 }
 
 template <int MODE>
@@ -389,23 +442,25 @@ extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const 
 
 extern "C" int64_t mlcg_node_tmm_workspace_floats(int64_t rows) {
   if (rows < 0) return -1;
-  return (int64_t)tmm_groups(rows) * kF * kF;
+  return (int64_t)tmm_groups(rows) * kTmmPart;
 }
 
 extern "C" int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
                              const float* b2, int64_t rows, int features, int accumulate,
-                             float* out, float* workspace, int64_t workspace_floats,
-                             void* stream) {
+                             float* out, float* colsum_a1, float* workspace,
+                             int64_t workspace_floats, void* stream) {
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(rows >= 0 && out && workspace);
   MLCG_REQUIRE(rows == 0 || (a1 && b1));
   MLCG_REQUIRE((a2 == nullptr) == (b2 == nullptr));
   const int groups = tmm_groups(rows);
-  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * kF * kF);
+  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * kTmmPart);
   hipStream_t s = mlcg_stream(stream);
   hipLaunchKernelGGL(node_tmm_kernel, dim3((unsigned)groups), dim3(kTmmThreads), 0, s, a1, b1,
-                     rows == 0 ? nullptr : a2, b2, rows, workspace);
-  hipLaunchKernelGGL(node_tmm_reduce_kernel, dim3(kF * kF / 64), dim3(512), 0, s, workspace,
-                     groups, accumulate, out);
+                     rows == 0 ? nullptr : a2, b2, rows, colsum_a1 != nullptr ? 1 : 0,
+                     workspace);
+  const int outs = kF * kF + (colsum_a1 ? kF : 0);
+  hipLaunchKernelGGL(node_tmm_reduce_kernel, dim3(outs / 64), dim3(512), 0, s, workspace, groups,
+                     accumulate, out, colsum_a1);
   return mlcg_launch_status();
 }

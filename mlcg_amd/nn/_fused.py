@@ -382,17 +382,15 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
         if tangent_on:
             zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, st.sbar1[k],
                                st.zdot[k])
-            gA3 = ops.node_tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k])
+            gA3, gc3 = ops.node_tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k], colsum=True)
         else:
             zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, None, None)
-            gA3 = ops.node_tmm(xbar2, st.s[k])
-        gc3 = xbar2.sum(0)
+            gA3, gc3 = ops.node_tmm(xbar2, st.s[k], colsum=True)
         gagg2 = ops.node_linear(zbar2, bp.A2, transpose=True)
         if tangent_on:
-            gA2 = ops.node_tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k])
+            gA2, gc2 = ops.node_tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], colsum=True)
         else:
-            gA2 = ops.node_tmm(zbar2, st.agg[k])
-        gc2 = zbar2.sum(0)
+            gA2, gc2 = ops.node_tmm(zbar2, st.agg[k], colsum=True)
         g1 = st.gagg1[k] if tangent_on else None
         yd = st.ydot[k] if tangent_on else None
         dd = st.ddot if tangent_on else None

@@ -343,23 +343,25 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
 
 
 def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = None,
-             b2: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """a1^T b1 (+ a2^T b2) reduced over the rows."""
+             b2: Optional[torch.Tensor] = None, colsum: bool = False):
+    """a1^T b1 (+ a2^T b2) reduced over the rows; with colsum, returns
+    (product, a1.sum(0)) from the same pass."""
     shapes_ok = all(t is None or (t.dim() == 2 and t.shape[1] == NUM_FILTERS)
                     for t in (a1, b1, a2, b2))
     if shapes_ok and a1.is_cuda and a1.dtype == torch.float32:
         rows = a1.shape[0]
         out = torch.empty(NUM_FILTERS, NUM_FILTERS, dtype=torch.float32, device=a1.device)
+        cs = torch.empty(NUM_FILTERS, dtype=torch.float32, device=a1.device) if colsum else None
         nws = int(_lib.load().mlcg_node_tmm_workspace_floats(rows))
         ws = torch.empty(nws, dtype=torch.float32, device=a1.device)
         c = lambda t: None if t is None else t.contiguous()  # noqa: E731
         call("mlcg_node_tmm", ptr(c(a1)), ptr(c(b1)), ptr(c(a2)), ptr(c(b2)), rows,
-             NUM_FILTERS, 0, ptr(out), ptr(ws), nws, stream_handle(a1.device))
-        return out
+             NUM_FILTERS, 0, ptr(out), ptr(cs), ptr(ws), nws, stream_handle(a1.device))
+        return (out, cs) if colsum else out
     out = tmm(a1, b1)
     if a2 is not None:
         out = out + tmm(a2, b2)
-    return out
+    return (out, a1.sum(0)) if colsum else out
 
 
 # --------------------------------------------------------------------------

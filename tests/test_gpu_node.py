@@ -25,7 +25,8 @@ def test_node_linear_helper(transpose):
     assert rel_err(out, ref + b.double() + r.double()) < 1e-6
 
 
-@pytest.mark.parametrize("rows", [0, 1, 127, 128, 129, 5000, 17920])
+@pytest.mark.parametrize("rows", [0, 1, 15, 16, 17, 127, 128, 129, 4095, 4097, 5000, 17920,
+                                  128000])
 def test_node_tmm(rows):
     from mlcg_amd import ops
 
@@ -41,6 +42,12 @@ def test_node_tmm(rows):
     assert rel_err(ops.node_tmm(a1, b1, a2, b2), ref2) < 1e-6
     # deterministic: bitwise identical on a second call
     assert torch.equal(ops.node_tmm(a1, b1, a2, b2), ops.node_tmm(a1, b1, a2, b2))
+    # fused column sums of a1 (bias gradients)
+    got, cs = ops.node_tmm(a1, b1, a2, b2, colsum=True)
+    assert rel_err(got, ref2) < 1e-6
+    assert rel_err(cs, a1.double().sum(0)) < 1e-6
+    got, cs = ops.node_tmm(a1, b1, colsum=True)
+    assert rel_err(cs, a1.double().sum(0)) < 1e-6
 
 
 def _act64(z, act):
