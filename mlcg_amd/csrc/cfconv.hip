@@ -9,11 +9,15 @@
 // reproduces the CPU reference's accumulation order (ascending sender) and
 // needs no atomics.
 //
-// Mapping: one wave per receiver row; every lane owns 2 of the 128 features
-// (float2), so one W row (512 B) or node row is one coalesced wave load.  The
-// row's (col, pair) indices are fetched 64 at a time by the lanes and
-// broadcast with readlane, and loads for several edges are issued before
-// their products are accumulated (in order) to keep HBM busy.
+// Mapping: one wave per receiver row.  The two half-waves take consecutive
+// edges of the row (edges 2t and 2t + 1), and every lane of a half owns 4 of
+// the 128 features (float4), so one step moves two W rows and two node rows
+// (2 x 512 B each) with one 16-byte load per lane and tensor.  The row's
+// (col, pair) indices are fetched 64 at a time by the lanes and broadcast
+// with readlane; the loads of several steps are issued before their
+// products are accumulated.  Each half accumulates its edges in ascending
+// order and the two halves are added at the end, so the result does not
+// depend on timing.
 #include "common.h"
 
 #include <hip/hip_fp16.h>
@@ -23,35 +27,66 @@ namespace {
 constexpr int kF = 128;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * MLCG_WAVE;
-constexpr int kUnroll = 4;
+#ifndef MLCG_GATHER_STEPS
+#define MLCG_GATHER_STEPS 4
+#endif
+constexpr int kSteps = MLCG_GATHER_STEPS;  // steps (2 edges each) with loads in flight together
 
-struct F2 {
-  float x, y;
-};
+__device__ __forceinline__ float4 f4zero() { return float4{0.f, 0.f, 0.f, 0.f}; }
 
-__device__ __forceinline__ F2 ld2(const float* __restrict__ p, int64_t row, int lane) {
-  float2 v = *reinterpret_cast<const float2*>(p + row * kF + 2 * lane);
-  return F2{v.x, v.y};
+// Row `row` of a [*, 128] fp32 tensor, features 4m .. 4m + 3.
+__device__ __forceinline__ float4 ld4(const float* __restrict__ p, int64_t row, int m) {
+  return *reinterpret_cast<const float4*>(p + row * kF + 4 * m);
 }
 
-__device__ __forceinline__ F2 ldw(const void* __restrict__ W, bool f16, int64_t row, int lane) {
+__device__ __forceinline__ float4 ldw4(const void* __restrict__ W, bool f16, int64_t row, int m) {
   if (f16) {
-    __half2 h = *reinterpret_cast<const __half2*>(static_cast<const __half*>(W) + row * kF +
-                                                  2 * lane);
-    float2 v = __half22float2(h);
-    return F2{v.x, v.y};
+    const __half2* h = reinterpret_cast<const __half2*>(static_cast<const __half*>(W) + row * kF +
+                                                        4 * m);
+    const float2 a = __half22float2(h[0]), b = __half22float2(h[1]);
+    return float4{a.x, a.y, b.x, b.y};
   }
-  return ld2(static_cast<const float*>(W), row, lane);
+  return ld4(static_cast<const float*>(W), row, m);
 }
 
-__device__ __forceinline__ void st2(float* __restrict__ p, int64_t row, int lane, F2 v) {
-  *reinterpret_cast<float2*>(p + row * kF + 2 * lane) = float2{v.x, v.y};
+__device__ __forceinline__ void st4(float* __restrict__ p, int64_t row, int m, float4 v) {
+  *reinterpret_cast<float4*>(p + row * kF + 4 * m) = v;
+}
+
+__device__ __forceinline__ void fma4(float4& acc, float4 a, float4 b) {
+  acc.x += a.x * b.x;
+  acc.y += a.y * b.y;
+  acc.z += a.z * b.z;
+  acc.w += a.w * b.w;
+}
+
+__device__ __forceinline__ float dot4(float4 a, float4 b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ float lanef(float v, int k) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
+// Sum over the 32 lanes of a half-wave, returned to all of them.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, MLCG_WAVE);
+  return v;
+}
+
+// Adds the other half-wave's accumulator (lanes l and l ^ 32 hold the same
+// features): lower half first, then upper half, on both.
+__device__ __forceinline__ float4 combine_halves(float4 a, int h) {
+  float4 o;
+  o.x = __shfl_xor(a.x, 32, MLCG_WAVE);
+  o.y = __shfl_xor(a.y, 32, MLCG_WAVE);
+  o.z = __shfl_xor(a.z, 32, MLCG_WAVE);
+  o.w = __shfl_xor(a.w, 32, MLCG_WAVE);
+  return h == 0 ? float4{a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w}
+                : float4{o.x + a.x, o.y + a.y, o.z + a.z, o.w + a.w};
 }
 
 // XCD-aware receiver row of this wave.  Workgroups are dispatched round-robin
@@ -85,125 +120,131 @@ __device__ __forceinline__ int64_t xcd_row() {
 
 #define MLCG_ROW_LOOP_END }
 
+// Edge of half h at step base k (k even, so k + 1 <= 63): its neighbour,
+// pair, the per-edge scalar `sv` (lane k / k + 1 of v) and whether it exists.
+struct Edge {
+  int j, p;
+  float sv;
+  bool ok;
+};
+
+__device__ __forceinline__ Edge edge_at(int k, int h, int cn, int my_col, int my_pair,
+                                        float v) {
+  const int ja = __builtin_amdgcn_readlane(my_col, k);
+  const int jb = __builtin_amdgcn_readlane(my_col, k + 1);
+  const int pa = __builtin_amdgcn_readlane(my_pair, k);
+  const int pb = __builtin_amdgcn_readlane(my_pair, k + 1);
+  const float va = lanef(v, k), vb = lanef(v, k + 1);
+  Edge e;
+  e.j = h ? jb : ja;
+  e.p = h ? pb : pa;
+  e.sv = h ? vb : va;
+  e.ok = k + h < cn;
+  return e;
+}
+
 __global__ __launch_bounds__(kThreads) void gather_kernel(
     const float* __restrict__ src, const void* __restrict__ W, int w_f16,
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
     const int32_t* __restrict__ eid2pair, int64_t n, float* __restrict__ out) {
   const int lane = mlcg_lane();
+  const int h = lane >> 5, m = lane & 31;
   const bool f16 = w_f16 != 0;
   const int64_t i = xcd_row();
   if (i >= n) return;
-  F2 acc{0.f, 0.f};
+  float4 acc = f4zero();
   MLCG_ROW_LOOP_BEGIN(i)
   (void)split;
   int k = 0;
-  for (; k + kUnroll <= cn; k += kUnroll) {
-    F2 s[kUnroll], w[kUnroll];
+  for (; k + 2 * kSteps <= cn; k += 2 * kSteps) {
+    float4 sv[kSteps], wv[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = __builtin_amdgcn_readlane(my_col, k + u);
-      const int p = __builtin_amdgcn_readlane(my_pair, k + u);
-      s[u] = ld2(src, j, lane);
-      w[u] = ldw(W, f16, p, lane);
+    for (int u = 0; u < kSteps; ++u) {
+      const Edge e = edge_at(k + 2 * u, h, cn, my_col, my_pair, 0.f);
+      sv[u] = ld4(src, e.j, m);
+      wv[u] = ldw4(W, f16, e.p, m);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc.x += s[u].x * w[u].x;
-      acc.y += s[u].y * w[u].y;
-    }
+    for (int u = 0; u < kSteps; ++u) fma4(acc, sv[u], wv[u]);
   }
-  for (; k < cn; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    F2 s = ld2(src, j, lane), w = ldw(W, f16, p, lane);
-    acc.x += s.x * w.x;
-    acc.y += s.y * w.y;
+  for (; k < cn; k += 2) {
+    const Edge e = edge_at(k, h, cn, my_col, my_pair, 0.f);
+    if (e.ok) fma4(acc, ld4(src, e.j, m), ldw4(W, f16, e.p, m));
   }
   MLCG_ROW_LOOP_END
-  st2(out, i, lane, acc);
+  acc = combine_halves(acc, h);
+  if (h == 0) st4(out, i, m, acc);
 }
 
-// ybar[i] = sum_j gagg[j] W_ij (all edges, ascending j) and, on the upper
-// edges (i < j) that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i>.
+// ybar[i] = sum_j gagg[j] W_ij (all edges) and, on the upper edges (i < j)
+// that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i>.
 __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     const float* __restrict__ gagg, const float* __restrict__ y, const void* __restrict__ W,
     const void* __restrict__ Wd, int w_f16, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ col, const int32_t* __restrict__ eid2pair, int64_t n,
     float* __restrict__ ybar, float* __restrict__ dbar) {
   const int lane = mlcg_lane();
+  const int h = lane >> 5, m = lane & 31;
   const bool f16 = w_f16 != 0;
   const int64_t i = xcd_row();
   if (i >= n) return;
-  const F2 gi = ld2(gagg, i, lane);
-  const F2 yi = ld2(y, i, lane);
-  F2 acc{0.f, 0.f};
+  const float4 gi = ld4(gagg, i, m);
+  const float4 yi = ld4(y, i, m);
+  float4 acc = f4zero();
   MLCG_ROW_LOOP_BEGIN(i)
+  // steps before the first step that holds an upper edge: gather only
+  const int lo_steps_end = split & ~1;
   int k = 0;
-  // lower edges: gather only
-  for (; k + kUnroll <= split; k += kUnroll) {
-    F2 g[kUnroll], w[kUnroll];
+  for (; k + 2 * kSteps <= lo_steps_end; k += 2 * kSteps) {
+    float4 g[kSteps], w[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = __builtin_amdgcn_readlane(my_col, k + u);
-      const int p = __builtin_amdgcn_readlane(my_pair, k + u);
-      g[u] = ld2(gagg, j, lane);
-      w[u] = ldw(W, f16, p, lane);
+    for (int u = 0; u < kSteps; ++u) {
+      const Edge e = edge_at(k + 2 * u, h, cn, my_col, my_pair, 0.f);
+      g[u] = ld4(gagg, e.j, m);
+      w[u] = ldw4(W, f16, e.p, m);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc.x += g[u].x * w[u].x;
-      acc.y += g[u].y * w[u].y;
-    }
+    for (int u = 0; u < kSteps; ++u) fma4(acc, g[u], w[u]);
   }
-  for (; k < split; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    const F2 g = ld2(gagg, j, lane), w = ldw(W, f16, p, lane);
-    acc.x += g.x * w.x;
-    acc.y += g.y * w.y;
+  for (; k < lo_steps_end; k += 2) {
+    const Edge e = edge_at(k, h, cn, my_col, my_pair, 0.f);
+    fma4(acc, ld4(gagg, e.j, m), ldw4(W, f16, e.p, m));
   }
-  // upper edges: gather plus the pair's distance adjoint
-  for (; k + kUnroll <= cn; k += kUnroll) {
-    F2 g[kUnroll], w[kUnroll], yj[kUnroll], wd[kUnroll];
-    int p[kUnroll];
+  // remaining steps: gather, plus the distance adjoint on upper edges
+  for (; k < cn; k += 2 * kSteps) {
+    float4 g[kSteps], w[kSteps], yj[kSteps], wd[kSteps];
+    int p[kSteps];
+    bool ok[kSteps], up[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = __builtin_amdgcn_readlane(my_col, k + u);
-      p[u] = __builtin_amdgcn_readlane(my_pair, k + u);
-      g[u] = ld2(gagg, j, lane);
-      w[u] = ldw(W, f16, p[u], lane);
-      yj[u] = ld2(y, j, lane);
-      wd[u] = ldw(Wd, f16, p[u], lane);
+    for (int u = 0; u < kSteps; ++u) {
+      const Edge e = edge_at(k + 2 * u < 62 ? k + 2 * u : 62, h, cn, my_col, my_pair, 0.f);
+      const int ke = k + 2 * u + h;
+      ok[u] = k + 2 * u < cn && ke < cn;
+      up[u] = ok[u] && ke >= split;
+      p[u] = e.p;
+      g[u] = ok[u] ? ld4(gagg, e.j, m) : f4zero();
+      w[u] = ok[u] ? ldw4(W, f16, e.p, m) : f4zero();
+      yj[u] = up[u] ? ld4(y, e.j, m) : f4zero();
+      wd[u] = up[u] ? ldw4(Wd, f16, e.p, m) : f4zero();
     }
-    float part[kUnroll];
+    float part[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc.x += g[u].x * w[u].x;
-      acc.y += g[u].y * w[u].y;
-      part[u] = wd[u].x * (gi.x * yj[u].x + g[u].x * yi.x) +
-                wd[u].y * (gi.y * yj[u].y + g[u].y * yi.y);
+    for (int u = 0; u < kSteps; ++u) {
+      fma4(acc, g[u], w[u]);
+      const float4 t{gi.x * yj[u].x + g[u].x * yi.x, gi.y * yj[u].y + g[u].y * yi.y,
+                     gi.z * yj[u].z + g[u].z * yi.z, gi.w * yj[u].w + g[u].w * yi.w};
+      part[u] = dot4(wd[u], t);
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
+    for (int u = 0; u < kSteps; ++u) part[u] = half_sum(part[u]);
+    if (m == 0)
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) part[u] += __shfl_xor(part[u], o, MLCG_WAVE);
-    if (lane == 0)
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) dbar[p[u]] += part[u];
-  }
-  for (; k < cn; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    const F2 g = ld2(gagg, j, lane), w = ldw(W, f16, p, lane);
-    const F2 yj = ld2(y, j, lane), wd = ldw(Wd, f16, p, lane);
-    acc.x += g.x * w.x;
-    acc.y += g.y * w.y;
-    float part = wd.x * (gi.x * yj.x + g.x * yi.x) + wd.y * (gi.y * yj.y + g.y * yi.y);
-    part = mlcg_wave_sum(part);
-    if (lane == 0) dbar[p] += part;
+      for (int u = 0; u < kSteps; ++u)
+        if (up[u]) dbar[p[u]] += part[u];
   }
   MLCG_ROW_LOOP_END
-  st2(ybar, i, lane, acc);
+  acc = combine_halves(acc, h);
+  if (h == 0) st4(ybar, i, m, acc);
 }
 
 // out[i] = sum_j ydot[j] W_ij + y[j] Wd_ij ddot_p (ydot may be null).
@@ -213,72 +254,46 @@ __global__ __launch_bounds__(kThreads) void gather_tangent_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
     const int32_t* __restrict__ eid2pair, int64_t n, float* __restrict__ out) {
   const int lane = mlcg_lane();
+  const int h = lane >> 5, m = lane & 31;
   const int64_t i = xcd_row();
   if (i >= n) return;
   const bool has_ydot = ydot != nullptr;
-  F2 acc{0.f, 0.f};
+  float4 acc = f4zero();
   MLCG_ROW_LOOP_BEGIN(i)
   (void)split;
   const float my_dd = lane < cn ? ddot[my_pair] : 0.f;
-  int k = 0;
-  for (; k + kUnroll <= cn; k += kUnroll) {
-    F2 yj[kUnroll], wd[kUnroll], yd[kUnroll], w[kUnroll];
-    float dd[kUnroll];
+  for (int k = 0; k < cn; k += 2 * kSteps) {
+    float4 yj[kSteps], wd[kSteps], yd[kSteps], w[kSteps];
+    float dd[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = __builtin_amdgcn_readlane(my_col, k + u);
-      const int p = __builtin_amdgcn_readlane(my_pair, k + u);
-      dd[u] = lanef(my_dd, k + u);
-      yj[u] = ld2(y, j, lane);
-      wd[u] = ld2(Wd, p, lane);
-      if (has_ydot) {
-        yd[u] = ld2(ydot, j, lane);
-        w[u] = ld2(W, p, lane);
-      } else {
-        yd[u] = F2{0.f, 0.f};
-        w[u] = F2{0.f, 0.f};
-      }
+    for (int u = 0; u < kSteps; ++u) {
+      const int kb = k + 2 * u < 62 ? k + 2 * u : 62;
+      const Edge e = edge_at(kb, h, cn, my_col, my_pair, my_dd);
+      const bool ok = k + 2 * u + h < cn;
+      dd[u] = ok ? e.sv : 0.f;
+      yj[u] = ok ? ld4(y, e.j, m) : f4zero();
+      wd[u] = ok ? ld4(Wd, e.p, m) : f4zero();
+      yd[u] = (ok && has_ydot) ? ld4(ydot, e.j, m) : f4zero();
+      w[u] = (ok && has_ydot) ? ld4(W, e.p, m) : f4zero();
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kSteps; ++u) {
       acc.x += yd[u].x * w[u].x + yj[u].x * (wd[u].x * dd[u]);
       acc.y += yd[u].y * w[u].y + yj[u].y * (wd[u].y * dd[u]);
+      acc.z += yd[u].z * w[u].z + yj[u].z * (wd[u].z * dd[u]);
+      acc.w += yd[u].w * w[u].w + yj[u].w * (wd[u].w * dd[u]);
     }
-  }
-  for (; k < cn; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    const float dd = lanef(my_dd, k);
-    const F2 yj = ld2(y, j, lane), wd = ld2(Wd, p, lane);
-    F2 yd{0.f, 0.f}, w{0.f, 0.f};
-    if (has_ydot) {
-      yd = ld2(ydot, j, lane);
-      w = ld2(W, p, lane);
-    }
-    acc.x += yd.x * w.x + yj.x * (wd.x * dd);
-    acc.y += yd.y * w.y + yj.y * (wd.y * dd);
   }
   MLCG_ROW_LOOP_END
-  st2(out, i, lane, acc);
+  acc = combine_halves(acc, h);
+  if (h == 0) st4(out, i, m, acc);
 }
 
 // Reverse over (primal, tangent) of the aggregation (see mlcg_hip.h):
 //   ybar2[i] = sum_j gagg2[j] W_ij + gagg1[j] Wd_ij ddot_p
-// and on the upper edges of pair p:
+// and on the upper edges of pair p (when Wbar is given):
 //   Wbar[p]  = gagg2_i y_j + gagg2_j y_i + gagg1_i ydot_j + gagg1_j ydot_i
 //   Wdbar[p] = ddot_p (gagg1_i y_j + gagg1_j y_i)
-template <bool kTangent>
-__device__ __forceinline__ void rev2_edge(int lane, int64_t p, float dd, F2 g2j, F2 w, F2 g1j,
-                                          F2 wd, F2& acc) {
-  if (kTangent) {
-    acc.x += g2j.x * w.x + g1j.x * (wd.x * dd);
-    acc.y += g2j.y * w.y + g1j.y * (wd.y * dd);
-  } else {
-    acc.x += g2j.x * w.x;
-    acc.y += g2j.y * w.y;
-  }
-}
-
 template <bool kTangent>
 __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
     const float* __restrict__ gagg2, const float* __restrict__ gagg1,
@@ -288,71 +303,70 @@ __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
     const int32_t* __restrict__ eid2pair, int64_t n, float* __restrict__ ybar2,
     float* __restrict__ Wbar, float* __restrict__ Wdbar) {
   const int lane = mlcg_lane();
+  const int h = lane >> 5, m = lane & 31;
   const int64_t i = xcd_row();
   if (i >= n) return;
   const bool has_ydot = ydot != nullptr;
-  const F2 g2i = ld2(gagg2, i, lane);
-  const F2 yi = ld2(y, i, lane);
-  const F2 g1i = kTangent ? ld2(gagg1, i, lane) : F2{0.f, 0.f};
-  const F2 ydi = (kTangent && has_ydot) ? ld2(ydot, i, lane) : F2{0.f, 0.f};
-  F2 acc{0.f, 0.f};
   const bool want_adj = Wbar != nullptr;
+  const float4 g2i = want_adj ? ld4(gagg2, i, m) : f4zero();
+  const float4 yi = want_adj ? ld4(y, i, m) : f4zero();
+  const float4 g1i = (kTangent && want_adj) ? ld4(gagg1, i, m) : f4zero();
+  const float4 ydi = (kTangent && want_adj && has_ydot) ? ld4(ydot, i, m) : f4zero();
+  float4 acc = f4zero();
   MLCG_ROW_LOOP_BEGIN(i)
   const float my_dd = (kTangent && lane < cn) ? ddot[my_pair] : 0.f;
-  // without pair-adjoint outputs every edge is a plain gather edge
-  const int lo_end = want_adj ? split : cn;
-  int k = 0;
-  // lower edges: only the gather into ybar2
-  for (; k + kUnroll <= lo_end; k += kUnroll) {
-    F2 g2j[kUnroll], w[kUnroll], g1j[kUnroll], wd[kUnroll];
-    float dd[kUnroll];
+  for (int k = 0; k < cn; k += 2 * kSteps) {
+    float4 g2j[kSteps], w[kSteps], g1j[kSteps], wd[kSteps];
+    float dd[kSteps];
+    bool ok[kSteps];
+    Edge ed[kSteps];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = __builtin_amdgcn_readlane(my_col, k + u);
-      const int p = __builtin_amdgcn_readlane(my_pair, k + u);
-      dd[u] = lanef(my_dd, k + u);
-      g2j[u] = ld2(gagg2, j, lane);
-      w[u] = ld2(W, p, lane);
-      g1j[u] = kTangent ? ld2(gagg1, j, lane) : F2{0.f, 0.f};
-      wd[u] = kTangent ? ld2(Wd, p, lane) : F2{0.f, 0.f};
+    for (int u = 0; u < kSteps; ++u) {
+      const int kb = k + 2 * u < 62 ? k + 2 * u : 62;
+      ed[u] = edge_at(kb, h, cn, my_col, my_pair, my_dd);
+      ok[u] = k + 2 * u + h < cn;
+      dd[u] = ok[u] ? ed[u].sv : 0.f;
+      g2j[u] = ok[u] ? ld4(gagg2, ed[u].j, m) : f4zero();
+      w[u] = ok[u] ? ld4(W, ed[u].p, m) : f4zero();
+      g1j[u] = (kTangent && ok[u]) ? ld4(gagg1, ed[u].j, m) : f4zero();
+      wd[u] = (kTangent && ok[u]) ? ld4(Wd, ed[u].p, m) : f4zero();
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      rev2_edge<kTangent>(lane, 0, dd[u], g2j[u], w[u], g1j[u], wd[u], acc);
-  }
-  for (; k < lo_end; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    const F2 g2j = ld2(gagg2, j, lane), w = ld2(W, p, lane);
-    const F2 g1j = kTangent ? ld2(gagg1, j, lane) : F2{0.f, 0.f};
-    const F2 wd = kTangent ? ld2(Wd, p, lane) : F2{0.f, 0.f};
-    rev2_edge<kTangent>(lane, 0, lanef(my_dd, k), g2j, w, g1j, wd, acc);
-  }
-  // upper edges: gather plus the pair adjoints of W and Wd
-  for (; k < cn; ++k) {
-    const int j = __builtin_amdgcn_readlane(my_col, k);
-    const int p = __builtin_amdgcn_readlane(my_pair, k);
-    const float dd = lanef(my_dd, k);
-    const F2 g2j = ld2(gagg2, j, lane), w = ld2(W, p, lane);
-    const F2 g1j = kTangent ? ld2(gagg1, j, lane) : F2{0.f, 0.f};
-    const F2 wd = kTangent ? ld2(Wd, p, lane) : F2{0.f, 0.f};
-    const F2 yj = ld2(y, j, lane);
-    const F2 ydj = (kTangent && has_ydot) ? ld2(ydot, j, lane) : F2{0.f, 0.f};
-    rev2_edge<kTangent>(lane, p, dd, g2j, w, g1j, wd, acc);
-    F2 wb, wdb{0.f, 0.f};
-    wb.x = g2i.x * yj.x + g2j.x * yi.x;
-    wb.y = g2i.y * yj.y + g2j.y * yi.y;
-    if (kTangent) {
-      wb.x += g1i.x * ydj.x + g1j.x * ydi.x;
-      wb.y += g1i.y * ydj.y + g1j.y * ydi.y;
-      wdb.x = dd * (g1i.x * yj.x + g1j.x * yi.x);
-      wdb.y = dd * (g1i.y * yj.y + g1j.y * yi.y);
+    for (int u = 0; u < kSteps; ++u) {
+      fma4(acc, g2j[u], w[u]);
+      if (kTangent) {
+        acc.x += g1j[u].x * (wd[u].x * dd[u]);
+        acc.y += g1j[u].y * (wd[u].y * dd[u]);
+        acc.z += g1j[u].z * (wd[u].z * dd[u]);
+        acc.w += g1j[u].w * (wd[u].w * dd[u]);
+      }
     }
-    st2(Wbar, p, lane, wb);
-    st2(Wdbar, p, lane, wdb);
+    if (want_adj) {
+#pragma unroll
+      for (int u = 0; u < kSteps; ++u) {
+        if (!(ok[u] && k + 2 * u + h >= split)) continue;
+        const float4 yj = ld4(y, ed[u].j, m);
+        const float4 ydj = (kTangent && has_ydot) ? ld4(ydot, ed[u].j, m) : f4zero();
+        float4 wb{g2i.x * yj.x + g2j[u].x * yi.x, g2i.y * yj.y + g2j[u].y * yi.y,
+                  g2i.z * yj.z + g2j[u].z * yi.z, g2i.w * yj.w + g2j[u].w * yi.w};
+        float4 wdb = f4zero();
+        if (kTangent) {
+          wb.x += g1i.x * ydj.x + g1j[u].x * ydi.x;
+          wb.y += g1i.y * ydj.y + g1j[u].y * ydi.y;
+          wb.z += g1i.z * ydj.z + g1j[u].z * ydi.z;
+          wb.w += g1i.w * ydj.w + g1j[u].w * ydi.w;
+          const float d = dd[u];
+          wdb = float4{d * (g1i.x * yj.x + g1j[u].x * yi.x), d * (g1i.y * yj.y + g1j[u].y * yi.y),
+                       d * (g1i.z * yj.z + g1j[u].z * yi.z), d * (g1i.w * yj.w + g1j[u].w * yi.w)};
+        }
+        st4(Wbar, ed[u].p, m, wb);
+        st4(Wdbar, ed[u].p, m, wdb);
+      }
+    }
   }
   MLCG_ROW_LOOP_END
-  st2(ybar2, i, lane, acc);
+  acc = combine_halves(acc, h);
+  if (h == 0) st4(ybar2, i, m, acc);
 }
 
 __global__ void pair_ddot_kernel(const float* __restrict__ pos, const float* __restrict__ dist,
@@ -433,6 +447,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_sum_kernel(
 
 // one wave per receiver row, kWaves rows per workgroup (see xcd_row)
 unsigned row_groups(int64_t n) { return mlcg_div_up(n, kWaves); }
+
 
 }  // namespace
 
