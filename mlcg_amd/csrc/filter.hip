@@ -589,53 +589,63 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
 
   const bool tangent = kNodes && adj.g1 != nullptr;
+  // Phase 0 of a tile: basis columns of k steps w and w + 8, and envelope.
+  // It runs for tile t + 1 in the same barrier interval as the last exchange
+  // of tile t, so a tile costs two workgroup barriers.
+  auto basis = [&](const TileIn& t, float* GGb, float* PSb) {
+    const float vm = t.valid ? 1.0f : 0.0f;
+    const float dx = t.xj - t.xi, dy = t.yj - t.yi, dz = t.zj - t.zi;
+    const float d = sqrtf(dx * dx + dy * dy + dz * dz);
+    float crbf, dcrbf;
+    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+#pragma unroll
+    for (int s0 = 0; s0 < KSMAX; s0 += kBwdWaves) {
+      const int s = s0 + w;
+      if (s < KSMAX) {
+        float g, gd;
+        rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);  // zero for k >= K
+        GGb[n * gRow + 4 * s + q] = g * vm;
+        GGb[16 * gRow + n * gRow + 4 * s + q] = gd * vm;
+      }
+    }
+    if (w == 0 && q == 0) {
+      float cc, dcc;
+      mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+      PSb[2 * n] = cc;
+      PSb[2 * n + 1] = dcc;
+    }
+  };
   int buf = 0;
   TileIn cur = fetch_tile<kNodes>(pos, pi, pj, adj, (int64_t)blockIdx.x * 16 + n, np, fcol);
+  basis(cur, GG0, PS0);
+  __syncthreads();
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
     float* GG = GG0 + buf * 2 * 16 * gRow;
     float* PS = PS0 + buf * 16 * 2;
-    const bool valid = cur.valid;
-    const float vmask = valid ? 1.0f : 0.0f;
+    const float vmask = cur.valid ? 1.0f : 0.0f;
     // the next tile's inputs are requested now; they are consumed one tile later
     const TileIn nxt =
         fetch_tile<kNodes>(pos, pi, pj, adj, (tile + gridDim.x) * 16 + n, np, fcol);
     float4 wb, wdb;
     tile_adjoint<kNodes>(cur, tangent, wb, wdb);
 
-    // 0. shared per-pair work: basis columns of k steps w and w + 8, envelope
-    {
-      const float dx = cur.xj - cur.xi, dy = cur.yj - cur.yi, dz = cur.zj - cur.zi;
-      const float d = sqrtf(dx * dx + dy * dy + dz * dz);
-      float crbf, dcrbf;
-      mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-#pragma unroll
-      for (int s0 = 0; s0 < KSMAX; s0 += kBwdWaves) {
-        const int s = s0 + w;
-        if (s < KSMAX) {
-          float g, gd;
-          rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);  // zero for k >= K
-          GG[n * gRow + 4 * s + q] = g * vmask;
-          GG[16 * gRow + n * gRow + 4 * s + q] = gd * vmask;
-        }
-      }
-      if (w == 0 && q == 0) {
-        float cc, dcc;
-        mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
-        PS[2 * n] = cc;
-        PS[2 * n + 1] = dcc;
-      }
-    }
-    __syncthreads();
-
-    // 1. a, a' of feature tile w
+    // 1. a, a' of feature tile w (two accumulators each: shorter MFMA chains)
     floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
+    floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSMAX; ++s) {
       const float g = GG[n * gRow + 4 * s + q];
       const float gd = GG[16 * gRow + n * gRow + 4 * s + q];
-      a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
-      ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
+      if (s & 1) {
+        a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
+        ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
+      } else {
+        a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
+        ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
+      }
     }
+    a += a_o;
+    ad += ad_o;
     // 2. h, h', activation derivatives and t, t' of the lane's 4 features
     const float cc = PS[2 * n], dcc = PS[2 * n + 1];
     float act1[4], act2[4];
@@ -658,8 +668,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     *reinterpret_cast<float4*>(HH + 16 * kXRow + n * kXRow + fcol) = hdv;
     __syncthreads();
 
-    // 3. hb, hb' of feature tile w (all 128 t features from LDS)
+    // 3. hb, hb' of feature tile w (all 128 t features from LDS), four chains
     floatx4 hb = {0.f, 0.f, 0.f, 0.f}, hdb = {0.f, 0.f, 0.f, 0.f};
+    floatx4 hb_o = {0.f, 0.f, 0.f, 0.f}, hdb_o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < kFT; ++u) {
       const float4 a2 = w2v[u * MLCG_WAVE];
@@ -668,13 +679,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           *reinterpret_cast<const float4*>(TB + 16 * kXRow + n * kXRow + 16 * u + 4 * q);
       hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, bx.x, hb, 0, 0, 0);
       hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, by.x, hdb, 0, 0, 0);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, bx.y, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, by.y, hdb, 0, 0, 0);
+      hb_o = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, bx.y, hb_o, 0, 0, 0);
+      hdb_o = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, by.y, hdb_o, 0, 0, 0);
       hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.z, bx.z, hb, 0, 0, 0);
       hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.z, by.z, hdb, 0, 0, 0);
-      hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, bx.w, hb, 0, 0, 0);
-      hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, by.w, hdb, 0, 0, 0);
+      hb_o = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, bx.w, hb_o, 0, 0, 0);
+      hdb_o = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.w, by.w, hdb_o, 0, 0, 0);
     }
+    hb += hb_o;
+    hdb += hdb_o;
     float4 abv, adbv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -699,9 +712,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc2[u], 0, 0, 0);
       }
     }
-    // 5. publish ab, ab'
+    // 5. publish ab, ab' and the next tile's basis
     *reinterpret_cast<float4*>(AB + n * kXRow + fcol) = abv;
     *reinterpret_cast<float4*>(AB + 16 * kXRow + n * kXRow + fcol) = adbv;
+    basis(nxt, GG0 + (buf ^ 1) * 2 * 16 * gRow, PS0 + (buf ^ 1) * 16 * 2);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
 #pragma unroll
