@@ -122,11 +122,17 @@ int mlcg_pair_reverse_map(const int32_t* pair_ij, int64_t pair_stride,
                           int32_t* eid2pair, void* stream);
 
 /* ---------------------------------------------------------------------- */
-/* Filter network (GaussianBasis -> cutoff -> MLP([K, F, F]) -> x cutoff)   */
+/* Filter network (radial basis -> cutoff -> MLP([K, F, F]) -> x cutoff)  */
 /* ---------------------------------------------------------------------- */
 
-/* Per pair p = {i, j}: d = |pos[j] - pos[i]|,
- *   g_k  = exp(coeff (d - offsets[k])^2) * C_rbf(d)          (gaussian.py:83-102)
+/* Per pair p = {i, j}: d = |pos[j] - pos[i]|, radial basis
+ *   basis 0: g_k = exp(c (d - centers[k])^2) * C_rbf(d), c = widths[0]
+ *            (GaussianBasis, gaussian.py:83-102: centers = offset,
+ *            widths = the 0-dim coeff)
+ *   basis 1: g_k = exp(-widths[k] (exp(alpha (rbf_lo - d)) - centers[k])^2)
+ *            * C_rbf(d) (ExpNormalBasis, exp_normal.py:104-124: centers =
+ *            means, widths = betas, alpha = 5 / (upper - lower))
+ * all read on the device (no host copy of the basis parameters), then
  *   a    = W1 g + b1 ; h = act(a) ; w = W2 h                 (mlp.py:56-58)
  *   W    = w * C_conv(d)                                     (schnet.py:340-341)
  *   Wd   = dW/dd (forward-mode tangent of the same chain).
@@ -135,11 +141,11 @@ int mlcg_pair_reverse_map(const int32_t* pair_ij, int64_t pair_stride,
  * optional.  act: 0 = tanh, 1 = shifted softplus.  cut kinds: 0 = identity,
  * 1 = cosine.  f16 != 0 selects the fp16-operand MFMA path (fp32
  * accumulate) and fp16 W_out/Wd_out storage.  Replaces CFConv.forward
- * lines 340-341 plus GaussianBasis/CosineCutoff/MLP (schnet.py:150,340-341). */
+ * lines 340-341 plus the basis/CosineCutoff/MLP (schnet.py:150,340-341). */
 int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
                     int64_t pair_stride, const int32_t* n_pairs_dev,
-                    int64_t max_pairs, const float* offsets, float coeff,
-                    int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                    int64_t max_pairs, int basis, const float* centers,
+                    const float* widths, float alpha, int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
                     int conv_cut_kind, float conv_lo, float conv_hi, int act,
                     const float* W1, const float* b1, const float* W2,
                     int num_filters, int f16, void* W_out, void* Wd_out,
@@ -159,12 +165,14 @@ int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
 int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_rbf);
 int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij,
                     int64_t pair_stride, const int32_t* n_pairs_dev,
-                    int64_t max_pairs, const float* offsets, float coeff,
-                    int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                    int64_t max_pairs, int basis, const float* centers,
+                    const float* widths, float alpha, int num_rbf,
+                    int rbf_cut_kind, float rbf_lo, float rbf_hi,
                     int conv_cut_kind, float conv_lo, float conv_hi, int act,
                     const float* W1, const float* b1, const float* W2,
                     int num_filters, const float* Wbar, const float* Wdbar,
-                    float* dW1, float* db1, float* dW2, float* workspace,
+                    float* dW1, float* db1, float* dW2, float* abar_out,
+                    float* adbar_out, float* workspace,
                     int64_t workspace_floats, void* stream);
 
 /* ---------------------------------------------------------------------- */
@@ -222,16 +230,42 @@ int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1,
  * mlcg_filter_bwd; the two [P, F] adjoint arrays are never materialised. */
 int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
                            int64_t pair_stride, const int32_t* n_pairs_dev,
-                           int64_t max_pairs, const float* offsets, float coeff,
-                           int num_rbf, int rbf_cut_kind, float rbf_lo,
-                           float rbf_hi, int conv_cut_kind, float conv_lo,
-                           float conv_hi, int act, const float* W1,
-                           const float* b1, const float* W2, int num_filters,
+                           int64_t max_pairs, int basis, const float* centers,
+                           const float* widths, float alpha, int num_rbf,
+                           int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                           int conv_cut_kind, float conv_lo, float conv_hi,
+                           int act, const float* W1, const float* b1,
+                           const float* W2, int num_filters,
                            const float* gagg2, const float* y,
                            const float* gagg1, const float* ydot,
                            const float* ddot, float* dW1, float* db1,
-                           float* dW2, float* workspace,
-                           int64_t workspace_floats, void* stream);
+                           float* dW2, float* abar_out, float* adbar_out,
+                           float* workspace, int64_t workspace_floats,
+                           void* stream);
+
+/* Gradients of trainable basis parameters from the first-layer pair
+ * adjoints abar = dL/da, adbar = dL/da' [max_pairs, F] (a = W1 g + b1,
+ * a' = W1 dg/dd), which mlcg_filter_bwd / mlcg_filter_bwd_cfconv write to
+ * abar_out / adbar_out when those are non-NULL.  With gbar = W1^T abar and
+ * gdbar = W1^T adbar per pair:
+ *   dcenters[k] (+)= sum_p gbar_pk dg_pk/dcenters[k] + gdbar_pk dg'_pk/dcenters[k]
+ *   dwidths[k]  (+)= the same with d/dwidths[k]; for the Gaussian basis
+ *                   (one shared coeff) sum_k dwidths[k] is d/dcoeff.
+ * dist holds the pair distances (mlcg_filter_fwd's dist_out); `workspace`
+ * holds mlcg_rbf_param_grad_workspace_floats(max_pairs, num_rbf) floats;
+ * accumulate != 0 adds to the outputs (the blocks share one basis).
+ * Replaces the autograd of GaussianBasis/ExpNormalBasis with
+ * trainable=True (gaussian.py:46-52, exp_normal.py:72-78) through the
+ * force-matching double backward. */
+int64_t mlcg_rbf_param_grad_workspace_floats(int64_t max_pairs, int num_rbf);
+int mlcg_rbf_param_grad(const float* dist, const int32_t* n_pairs_dev,
+                        int64_t max_pairs, int basis, const float* centers,
+                        const float* widths, float alpha, int num_rbf,
+                        int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                        const float* W1, int num_filters, const float* abar,
+                        const float* adbar, int accumulate, float* dcenters,
+                        float* dwidths, float* workspace,
+                        int64_t workspace_floats, void* stream);
 
 /* ddot[p] = rhat_p . (u[j] - u[i]), rhat_p = (pos[j] - pos[i]) / dist[p]. */
 int mlcg_pair_ddot(const float* pos, const float* dist, const int32_t* pair_ij,

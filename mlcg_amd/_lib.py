@@ -42,15 +42,18 @@ _SIGNATURES = {
     "mlcg_radius_fill": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _I64, _I64, _P,
                          _P, _I64, _I64, _P, _P, _P, _P],
     "mlcg_pair_reverse_map": [_P, _I64, _P, _I64, _P, _P, _P, _P],
-    "mlcg_filter_fwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
-                        _F32, _F32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],
+    "mlcg_filter_fwd": [_P, _P, _I64, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32,
+                        _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],
     "mlcg_filter_bwd_workspace_floats": [_I64, _I32],
-    "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32, _I32,
-                        _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64,
-                        _P],
-    "mlcg_filter_bwd_cfconv": [_P, _P, _I64, _P, _I64, _P, _F32, _I32, _I32, _F32, _F32,
-                               _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
-                               _P, _P, _P, _P, _I64, _P],
+    "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32,
+                        _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P,
+                        _P, _I64, _P],
+    "mlcg_filter_bwd_cfconv": [_P, _P, _I64, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32,
+                               _F32, _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P,
+                               _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+    "mlcg_rbf_param_grad_workspace_floats": [_I64, _I32],
+    "mlcg_rbf_param_grad": [_P, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32, _P, _I32,
+                            _P, _P, _I32, _P, _P, _P, _I64, _P],
     "mlcg_cfconv_gather": [_P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
     "mlcg_cfconv_gather_tangent": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
@@ -78,7 +81,8 @@ _SIGNATURES = {
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,
-             "mlcg_out_rev2_workspace_floats": _I64}
+             "mlcg_out_rev2_workspace_floats": _I64,
+             "mlcg_rbf_param_grad_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

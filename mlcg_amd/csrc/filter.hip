@@ -39,9 +39,17 @@ constexpr int kWaves = 8;        // waves per workgroup
 constexpr int kThreads = kWaves * MLCG_WAVE;
 constexpr int kMaxK = 128;
 
+// Radial basis (per basis function k, distance d, envelope C(d)):
+//   basis 0, Gaussian (gaussian.py:83-102): g_k = C exp(c (d - centers[k])^2),
+//            c = widths[0] (the module's 0-dim `coeff`)
+//   basis 1, ExpNormal (exp_normal.py:116-130):
+//            g_k = C exp(-widths[k] (exp(alpha (lo - d)) - centers[k])^2)
+//            with widths = betas, centers = means, lo = the basis' lower cutoff.
 struct RbfParams {
-  const float* offsets;
-  float coeff;
+  const float* centers;
+  const float* widths;
+  float alpha;
+  int basis;
   int K;
   int rbf_kind;
   float rbf_lo, rbf_hi;
@@ -66,14 +74,22 @@ __device__ __forceinline__ float pair_distance(const float* __restrict__ pos,
 // g_k and dg_k/dd for one basis function (zero past K).
 __device__ __forceinline__ void rbf_value(const RbfParams& rp, int k, float d, float crbf,
                                           float dcrbf, float& g, float& gd) {
-  if (k < rp.K) {
-    float diff = d - rp.offsets[k];
-    float e = __expf(rp.coeff * (diff * diff));  // argument <= 0: no overflow
-    g = e * crbf;
-    gd = e * (2.0f * rp.coeff * diff * crbf + dcrbf);
-  } else {
+  if (k >= rp.K) {
     g = 0.0f;
     gd = 0.0f;
+  } else if (rp.basis == 0) {
+    const float c = rp.widths[0];
+    const float diff = d - rp.centers[k];
+    const float e = __expf(c * (diff * diff));  // argument <= 0: no overflow
+    g = e * crbf;
+    gd = e * (2.0f * c * diff * crbf + dcrbf);
+  } else {
+    const float ex = __expf(rp.alpha * (rp.rbf_lo - d));
+    const float u = ex - rp.centers[k];
+    const float b = rp.widths[k];
+    const float e = __expf(-b * (u * u));
+    g = e * crbf;
+    gd = e * (dcrbf + 2.0f * rp.alpha * b * u * ex * crbf);
   }
 }
 
@@ -539,7 +555,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
     int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
     const float* __restrict__ b1, const float* __restrict__ W2, PairAdjoint adj,
-    float* __restrict__ partial) {
+    float* __restrict__ abar_out, float* __restrict__ adbar_out, float* __restrict__ partial) {
   constexpr int KTMAX = (4 * KSMAX + 15) / 16;
   // g rows span the compile-time maximum width and the unused columns stay
   // zero, so the k loops below run without data-dependent branches (which
@@ -712,9 +728,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc2[u], 0, 0, 0);
       }
     }
-    // 5. publish ab, ab' and the next tile's basis
+    // 5. publish ab, ab' (and store them per pair when the basis parameters
+    //    need gradients) and the next tile's basis
     *reinterpret_cast<float4*>(AB + n * kXRow + fcol) = abv;
     *reinterpret_cast<float4*>(AB + 16 * kXRow + n * kXRow + fcol) = adbv;
+    if (abar_out && cur.valid) {
+      const int64_t p = tile * 16 + n;
+      *reinterpret_cast<float4*>(abar_out + p * kF + fcol) = abv;
+      *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) = adbv;
+    }
     basis(nxt, GG0 + (buf ^ 1) * 2 * 16 * gRow, PS0 + (buf ^ 1) * 16 * 2);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
@@ -835,11 +857,13 @@ void allow_lds_once() {
   done[dev] = true;
 }
 
-RbfParams make_params(const float* offsets, float coeff, int K, int rk, float rlo, float rhi,
-                      int ck, float clo, float chi, int act) {
+RbfParams make_params(int basis, const float* centers, const float* widths, float alpha, int K,
+                      int rk, float rlo, float rhi, int ck, float clo, float chi, int act) {
   RbfParams rp;
-  rp.offsets = offsets;
-  rp.coeff = coeff;
+  rp.basis = basis;
+  rp.centers = centers;
+  rp.widths = widths;
+  rp.alpha = alpha;
   rp.K = K;
   rp.rbf_kind = rk;
   rp.rbf_lo = rlo;
@@ -851,28 +875,29 @@ RbfParams make_params(const float* offsets, float coeff, int K, int rk, float rl
   return rp;
 }
 
-bool valid_params(int K, int rk, int ck, int act, int F) {
-  return F == kF && K >= 1 && K <= kMaxK && (rk == 0 || rk == 1) && (ck == 0 || ck == 1) &&
-         (act == 0 || act == 1);
+bool valid_params(int basis, int K, int rk, int ck, int act, int F) {
+  return F == kF && K >= 1 && K <= kMaxK && (basis == 0 || basis == 1) && (rk == 0 || rk == 1) &&
+         (ck == 0 || ck == 1) && (act == 0 || act == 1);
 }
 
 }  // namespace
 
 extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
-                               const int32_t* n_pairs_dev, int64_t max_pairs,
-                               const float* offsets, float coeff, int num_rbf,
-                               int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                               const int32_t* n_pairs_dev, int64_t max_pairs, int basis,
+                               const float* centers, const float* widths, float alpha,
+                               int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
                                int conv_cut_kind, float conv_lo, float conv_hi, int act,
                                const float* W1, const float* b1, const float* W2,
                                int num_filters, int f16, void* W_out, void* Wd_out,
                                float* dist_out, void* stream) {
-  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
+  if (!valid_params(basis, num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
     return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
   if (max_pairs == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && pair_ij && n_pairs_dev && offsets && W1 && b1 && W2 && W_out && Wd_out);
-  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
-                             conv_cut_kind, conv_lo, conv_hi, act);
+  MLCG_REQUIRE(pos && pair_ij && n_pairs_dev && centers && widths && W1 && b1 && W2 && W_out &&
+               Wd_out);
+  RbfParams rp = make_params(basis, centers, widths, alpha, num_rbf, rbf_cut_kind, rbf_lo,
+                             rbf_hi, conv_cut_kind, conv_lo, conv_hi, act);
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
   hipStream_t s = mlcg_stream(stream);
   if (!f16) {
@@ -904,21 +929,23 @@ extern "C" int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_r
 namespace {
 
 int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
-                      const int32_t* n_pairs_dev, int64_t max_pairs, const float* offsets,
-                      float coeff, int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
-                      int conv_cut_kind, float conv_lo, float conv_hi, int act,
-                      const float* W1, const float* b1, const float* W2, int num_filters,
-                      const PairAdjoint& adj, bool nodes, float* dW1, float* db1, float* dW2,
+                      const int32_t* n_pairs_dev, int64_t max_pairs, int basis,
+                      const float* centers, const float* widths, float alpha, int num_rbf,
+                      int rbf_cut_kind, float rbf_lo, float rbf_hi, int conv_cut_kind,
+                      float conv_lo, float conv_hi, int act, const float* W1, const float* b1,
+                      const float* W2, int num_filters, const PairAdjoint& adj, bool nodes,
+                      float* dW1, float* db1, float* dW2, float* abar_out, float* adbar_out,
                       float* workspace, int64_t workspace_floats, void* stream) {
-  if (!valid_params(num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
+  if (!valid_params(basis, num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
     return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
-  MLCG_REQUIRE(offsets && W1 && b1 && W2 && dW1 && db1 && dW2 && workspace);
+  MLCG_REQUIRE(centers && widths && W1 && b1 && W2 && dW1 && db1 && dW2 && workspace);
   MLCG_REQUIRE(max_pairs == 0 || (pos && pair_ij && n_pairs_dev));
+  MLCG_REQUIRE((abar_out == nullptr) == (adbar_out == nullptr));
   const int groups = bwd_groups(max_pairs);
   MLCG_REQUIRE(workspace_floats >= (int64_t)groups * bwd_partial_floats(num_rbf));
-  RbfParams rp = make_params(offsets, coeff, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi,
-                             conv_cut_kind, conv_lo, conv_hi, act);
+  RbfParams rp = make_params(basis, centers, widths, alpha, num_rbf, rbf_cut_kind, rbf_lo,
+                             rbf_hi, conv_cut_kind, conv_lo, conv_hi, act);
   hipStream_t s = mlcg_stream(stream);
   const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
   allow_lds_once();
@@ -927,7 +954,7 @@ int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_str
 #define MLCG_BWD_LAUNCH(KS, NODES)                                                         \
   hipLaunchKernelGGL((filter_bwd_fused_kernel<KS, NODES>), dim3(grid), dim3(kBwdThreads), \
                      lds, s, pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs,  \
-                     rp, W1, b1, W2, adj, workspace)
+                     rp, W1, b1, W2, adj, abar_out, adbar_out, workspace)
   if (small_k && !nodes) MLCG_BWD_LAUNCH(16, false);
   else if (small_k) MLCG_BWD_LAUNCH(16, true);
   else if (!nodes) MLCG_BWD_LAUNCH(32, false);
@@ -942,38 +969,240 @@ int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_str
 }  // namespace
 
 extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
-                               const int32_t* n_pairs_dev, int64_t max_pairs,
-                               const float* offsets, float coeff, int num_rbf,
-                               int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                               const int32_t* n_pairs_dev, int64_t max_pairs, int basis,
+                               const float* centers, const float* widths, float alpha,
+                               int num_rbf, int rbf_cut_kind, float rbf_lo, float rbf_hi,
                                int conv_cut_kind, float conv_lo, float conv_hi, int act,
                                const float* W1, const float* b1, const float* W2,
                                int num_filters, const float* Wbar, const float* Wdbar,
-                               float* dW1, float* db1, float* dW2, float* workspace,
-                               int64_t workspace_floats, void* stream) {
+                               float* dW1, float* db1, float* dW2, float* abar_out,
+                               float* adbar_out, float* workspace, int64_t workspace_floats,
+                               void* stream) {
   MLCG_REQUIRE(max_pairs == 0 || (Wbar && Wdbar));
   PairAdjoint adj{Wbar, Wdbar, nullptr, nullptr, nullptr, nullptr, nullptr};
-  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, offsets, coeff,
-                           num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind, conv_lo,
-                           conv_hi, act, W1, b1, W2, num_filters, adj, false, dW1, db1, dW2,
-                           workspace, workspace_floats, stream);
+  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, basis, centers,
+                           widths, alpha, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind,
+                           conv_lo, conv_hi, act, W1, b1, W2, num_filters, adj, false, dW1, db1,
+                           dW2, abar_out, adbar_out, workspace, workspace_floats, stream);
 }
 
 extern "C" int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
                                       int64_t pair_stride, const int32_t* n_pairs_dev,
-                                      int64_t max_pairs, const float* offsets, float coeff,
-                                      int num_rbf, int rbf_cut_kind, float rbf_lo,
-                                      float rbf_hi, int conv_cut_kind, float conv_lo,
-                                      float conv_hi, int act, const float* W1, const float* b1,
-                                      const float* W2, int num_filters, const float* gagg2,
-                                      const float* y, const float* gagg1, const float* ydot,
+                                      int64_t max_pairs, int basis, const float* centers,
+                                      const float* widths, float alpha, int num_rbf,
+                                      int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                                      int conv_cut_kind, float conv_lo, float conv_hi, int act,
+                                      const float* W1, const float* b1, const float* W2,
+                                      int num_filters, const float* gagg2, const float* y,
+                                      const float* gagg1, const float* ydot,
                                       const float* ddot, float* dW1, float* db1, float* dW2,
-                                      float* workspace, int64_t workspace_floats,
-                                      void* stream) {
+                                      float* abar_out, float* adbar_out, float* workspace,
+                                      int64_t workspace_floats, void* stream) {
   MLCG_REQUIRE(max_pairs == 0 || (gagg2 && y));
   MLCG_REQUIRE(!gagg1 || ddot);
   PairAdjoint adj{nullptr, nullptr, gagg2, y, gagg1, gagg1 ? ydot : nullptr, ddot};
-  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, offsets, coeff,
-                           num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind, conv_lo,
-                           conv_hi, act, W1, b1, W2, num_filters, adj, true, dW1, db1, dW2,
-                           workspace, workspace_floats, stream);
+  return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, basis, centers,
+                           widths, alpha, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind,
+                           conv_lo, conv_hi, act, W1, b1, W2, num_filters, adj, true, dW1, db1,
+                           dW2, abar_out, adbar_out, workspace, workspace_floats, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Gradients of trainable basis parameters.
+//
+// With the pair adjoints of the first filter layer, abar = dL/da and
+// adbar = dL/da' (a = W1 g + b1, a' = W1 g'), the basis adjoints are
+// gbar = W1^T abar and gdbar = W1^T adbar, and per basis function k
+//   dcenters[k] += sum_p gbar_pk dg_pk/dcenter_k + gdbar_pk dg'_pk/dcenter_k
+//   dwidths[k]  += sum_p gbar_pk dg_pk/dwidth_k  + gdbar_pk dg'_pk/dwidth_k
+// (for the Gaussian basis dwidths[k] is the share of basis function k in
+// d/dcoeff).  One wave per 16-pair tile computes gbar, gdbar with
+// v_mfma_f32_16x16x4f32 (A = the pair adjoints, B = W1 from LDS), the
+// derivative factors per (pair, k), and keeps per-lane sums; the
+// workgroup partials are added in a fixed order by rbf_grad_reduce_kernel.
+namespace {
+
+constexpr int kRgWaves = 4;
+constexpr int kRgThreads = kRgWaves * MLCG_WAVE;
+constexpr int kRgMaxGroups = 512;
+
+__device__ __forceinline__ void basis_param_derivs(const RbfParams& rp, int k, float d,
+                                                   float C, float dC, float& g_c, float& g_w,
+                                                   float& gd_c, float& gd_w) {
+  if (rp.basis == 0) {
+    const float c = rp.widths[0];
+    const float x = d - rp.centers[k];
+    const float e = __expf(c * x * x);
+    const float q = 2.0f * c * x * C + dC;            // g' = e q
+    g_c = -2.0f * c * x * C * e;                       // dg/dcenter
+    g_w = x * x * C * e;                               // dg/dc
+    gd_c = -e * (2.0f * c * x * q + 2.0f * c * C);     // dg'/dcenter
+    gd_w = e * (x * x * q + 2.0f * x * C);             // dg'/dc
+  } else {
+    const float ex = __expf(rp.alpha * (rp.rbf_lo - d));
+    const float u = ex - rp.centers[k];
+    const float b = rp.widths[k];
+    const float e = __expf(-b * u * u);
+    const float r = dC + 2.0f * rp.alpha * b * u * ex * C;  // g' = e r
+    g_c = 2.0f * b * u * C * e;
+    g_w = -u * u * C * e;
+    gd_c = e * (2.0f * b * u * r - 2.0f * rp.alpha * b * ex * C);
+    gd_w = e * (-u * u * r + 2.0f * rp.alpha * u * ex * C);
+  }
+}
+
+template <int KT>
+__global__ __launch_bounds__(kRgThreads) void rbf_grad_kernel(
+    const float* __restrict__ dist, const int32_t* __restrict__ n_pairs_dev, int64_t max_pairs,
+    RbfParams rp, const float* __restrict__ W1, const float* __restrict__ abar,
+    const float* __restrict__ adbar, float* __restrict__ partial) {
+  __shared__ float w1s[kF * (16 * KT + 1)];  // W1 as [f][k], zero past K
+  const int K = rp.K;
+  const int kr = 16 * KT + 1;
+  for (int x = threadIdx.x; x < kF * 16 * KT; x += blockDim.x) {
+    const int f = x / (16 * KT), k = x % (16 * KT);
+    w1s[f * kr + k] = k < K ? W1[f * K + k] : 0.0f;
+  }
+  __syncthreads();
+  const int w = threadIdx.x / MLCG_WAVE, l = mlcg_lane(), q = l >> 4, n = l & 15;
+  int64_t np = max_pairs > 0 ? *n_pairs_dev : 0;
+  if (np > max_pairs) np = max_pairs;
+  const int64_t tiles = (np + 15) / 16;
+  float sc[KT], sw[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) sc[kt] = sw[kt] = 0.f;
+  for (int64_t tile = (int64_t)blockIdx.x * kRgWaves + w; tile < tiles;
+       tile += (int64_t)gridDim.x * kRgWaves) {
+    const int64_t pa = tile * 16 + n;  // the pair this lane feeds into the A operand
+    const bool va = pa < np;
+    floatx4 gb[KT], gdb[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) gb[kt] = gdb[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (int m = 0; m < kF / 16; ++m) {
+      // MFMA step s = 4m + j covers feature f = 16m + 4q + j of pair pa
+      const float4 av = va ? *reinterpret_cast<const float4*>(abar + pa * kF + 16 * m + 4 * q)
+                           : float4{0.f, 0.f, 0.f, 0.f};
+      const float4 ad = va ? *reinterpret_cast<const float4*>(adbar + pa * kF + 16 * m + 4 * q)
+                           : float4{0.f, 0.f, 0.f, 0.f};
+      const float a4[4] = {av.x, av.y, av.z, av.w};
+      const float d4[4] = {ad.x, ad.y, ad.z, ad.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = 16 * m + 4 * q + j;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const float bw = w1s[f * kr + 16 * kt + n];
+          gb[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[j], bw, gb[kt], 0, 0, 0);
+          gdb[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(d4[j], bw, gdb[kt], 0, 0, 0);
+        }
+      }
+    }
+    // gb[kt][i]: pair tile*16 + 4q + i, basis function 16kt + n
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t p = tile * 16 + 4 * q + i;
+      if (p >= np) continue;
+      const float d = dist[p];
+      float C, dC;
+      mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, C, dC);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int k = 16 * kt + n;
+        if (k >= K) continue;
+        float g_c, g_w, gd_c, gd_w;
+        basis_param_derivs(rp, k, d, C, dC, g_c, g_w, gd_c, gd_w);
+        sc[kt] += gb[kt][i] * g_c + gdb[kt][i] * gd_c;
+        sw[kt] += gb[kt][i] * g_w + gdb[kt][i] * gd_w;
+      }
+    }
+  }
+  // sum the 4 lane groups, then the waves (fixed order through LDS)
+  __shared__ float red[kRgWaves][2][16 * KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    float c = sc[kt], v = sw[kt];
+    c += __shfl_xor(c, 16, MLCG_WAVE);
+    c += __shfl_xor(c, 32, MLCG_WAVE);
+    v += __shfl_xor(v, 16, MLCG_WAVE);
+    v += __shfl_xor(v, 32, MLCG_WAVE);
+    if (q == 0) {
+      red[w][0][16 * kt + n] = c;
+      red[w][1][16 * kt + n] = v;
+    }
+  }
+  __syncthreads();
+  for (int x = threadIdx.x; x < 2 * 16 * KT; x += blockDim.x) {
+    const int which = x / (16 * KT), k = x % (16 * KT);
+    partial[(int64_t)blockIdx.x * 2 * 16 * KT + x] =
+        (red[0][which][k] + red[1][which][k]) + (red[2][which][k] + red[3][which][k]);
+  }
+}
+
+// out[x] (+)= sum over the groups' partials, in group order.
+__global__ void rbf_grad_reduce_kernel(const float* __restrict__ partial, int groups, int kp,
+                                       int K, int accumulate, float* __restrict__ dcenters,
+                                       float* __restrict__ dwidths) {
+  const int x = threadIdx.x;
+  if (x >= 2 * kp) return;
+  const int which = x / kp, k = x % kp;
+  if (k >= K) return;
+  float v = 0.f;
+  for (int g = 0; g < groups; ++g) v += partial[(int64_t)g * 2 * kp + x];
+  float* dst = which == 0 ? dcenters + k : dwidths + k;
+  *dst = accumulate ? *dst + v : v;
+}
+
+int rg_groups(int64_t max_pairs) {
+  const int64_t tiles = (max_pairs + 15) / 16;
+  const int64_t g = (tiles + kRgWaves - 1) / kRgWaves;
+  return (int)(g < 1 ? 1 : (g < kRgMaxGroups ? g : kRgMaxGroups));
+}
+
+}  // namespace
+
+extern "C" int64_t mlcg_rbf_param_grad_workspace_floats(int64_t max_pairs, int num_rbf) {
+  if (max_pairs < 0 || num_rbf < 1 || num_rbf > kMaxK) return -1;
+  return (int64_t)rg_groups(max_pairs) * 2 * 16 * ((num_rbf + 15) / 16);
+}
+
+extern "C" int mlcg_rbf_param_grad(const float* dist, const int32_t* n_pairs_dev,
+                                   int64_t max_pairs, int basis, const float* centers,
+                                   const float* widths, float alpha, int num_rbf,
+                                   int rbf_cut_kind, float rbf_lo, float rbf_hi,
+                                   const float* W1, int num_filters, const float* abar,
+                                   const float* adbar, int accumulate, float* dcenters,
+                                   float* dwidths, float* workspace, int64_t workspace_floats,
+                                   void* stream) {
+  if (!valid_params(basis, num_rbf, rbf_cut_kind, 0, 0, num_filters))
+    return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(max_pairs >= 0 && centers && widths && W1 && dcenters && dwidths && workspace);
+  MLCG_REQUIRE(max_pairs == 0 || (dist && n_pairs_dev && abar && adbar));
+  const int groups = rg_groups(max_pairs);
+  const int KT = (num_rbf + 15) / 16;
+  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * 2 * 16 * KT);
+  RbfParams rp = make_params(basis, centers, widths, alpha, num_rbf, rbf_cut_kind, rbf_lo,
+                             rbf_hi, 0, 0.f, 1.f, 0);
+  hipStream_t s = mlcg_stream(stream);
+  switch (KT) {
+#define MLCG_RG(KTV)                                                                        \
+  case KTV:                                                                                 \
+    hipLaunchKernelGGL(rbf_grad_kernel<KTV>, dim3(groups), dim3(kRgThreads), 0, s, dist,   \
+                       n_pairs_dev, max_pairs, rp, W1, abar, adbar, workspace);             \
+    break;
+    MLCG_RG(1)
+    MLCG_RG(2)
+    MLCG_RG(3)
+    MLCG_RG(4)
+    MLCG_RG(5)
+    MLCG_RG(6)
+    MLCG_RG(7)
+    MLCG_RG(8)
+#undef MLCG_RG
+    default:
+      return MLCG_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(rbf_grad_reduce_kernel, dim3(1), dim3(256), 0, s, workspace, groups,
+                     16 * KT, num_rbf, accumulate, dcenters, dwidths);
+  return mlcg_launch_status();
 }

@@ -6,12 +6,12 @@ from .mlp import MLP, init_xavier_uniform
 from .prior import (Dihedral, FourierSeries, Harmonic, HarmonicAngles, HarmonicBonds,
                     Repulsion, StaticDihedral, StaticHarmonicAngles, StaticHarmonicBonds,
                     StaticRepulsion)
-from .radial_basis import GaussianBasis
+from .radial_basis import ExpNormalBasis, GaussianBasis
 from .schnet import CFConv, InteractionBlock, SchNet, StandardSchNet
 
 __all__ = ["ShiftedSoftplus", "CosineCutoff", "IdentityCutoff", "EnergyOut", "GradientsOut",
            "SumOut", "EnergyMSE", "ForceMSE", "ForceRMSE", "Loss", "MLP",
-           "init_xavier_uniform", "GaussianBasis", "CFConv", "InteractionBlock", "SchNet",
-           "StandardSchNet", "Harmonic", "HarmonicBonds", "HarmonicAngles", "FourierSeries",
-           "Dihedral", "Repulsion", "StaticHarmonicBonds", "StaticHarmonicAngles",
-           "StaticDihedral", "StaticRepulsion"]
+           "init_xavier_uniform", "GaussianBasis", "ExpNormalBasis", "CFConv",
+           "InteractionBlock", "SchNet", "StandardSchNet", "Harmonic", "HarmonicBonds",
+           "HarmonicAngles", "FourierSeries", "Dihedral", "Repulsion", "StaticHarmonicBonds",
+           "StaticHarmonicAngles", "StaticDihedral", "StaticRepulsion"]

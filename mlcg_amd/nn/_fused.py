@@ -2,9 +2,9 @@
 
 This is the hot path of the package.  Edge work (filter network, CFConv
 gather/scatter, their backward, tangent and second-order reverse, the pair ->
-node force scatter) runs in the gfx950 kernels of ``libmlcg_hip.so``; node work
-(the [N, H] x [H, H] linears and elementwise activations) runs as library
-GEMMs and elementwise ops on the same stream.
+node force scatter) and node work (the [N, H] x [H, H] linears with their
+bias / residual / activation epilogues, the output network) run in the gfx950
+kernels of ``libmlcg_hip.so``, all on torch's current stream.
 
 Math (per interaction block, activation s = act(z)):
     y = x A1^T ;  agg_i = sum_j y_j * W_ij ;  z = agg A2^T + c2 ;  v = s A3^T + c3 ;
@@ -22,11 +22,15 @@ with W_ij = filter(d_ij) evaluated per unordered pair, and Wd = dW/dd.
   new.  This is the hand-derived double backward of the force-matching loss
   L(F): with u = -dL/dF it gives dL/dtheta, replacing the autograd replay of
   create_graph=True (mlcg/nn/gradients.py:216-222, mlcg/pl/model.py:113-131).
+* trainable basis parameters theta_b: the filter backward also emits the
+  first-layer pair adjoints abar = dL/da and adbar = dL/da' (a = W1 g + b1,
+  a' = W1 g'), and dL/dtheta_b = sum_p (W1^T abar_p) . dg/dtheta_b
+  + (W1^T adbar_p) . dg'/dtheta_b, summed over blocks.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from typing import List, Optional, Tuple
 
 import torch
@@ -61,6 +65,7 @@ class FusedSpec:
     num_blocks: int
     out_has_bias: List[bool]  # per output linear
     f16: bool = False
+    basis_trainable: bool = False  # Params.basis carries (centers, widths)
 
 
 @dataclass
@@ -69,6 +74,7 @@ class Params:
     blocks: List[BlockParams]
     out_w: List[torch.Tensor]
     out_b: List[Optional[torch.Tensor]]
+    basis: List[torch.Tensor] = field(default_factory=list)  # trainable (centers, widths)
 
     def flat(self) -> List[torch.Tensor]:
         out = [self.emb]
@@ -78,7 +84,7 @@ class Params:
             out.append(w)
             if b is not None:
                 out.append(b)
-        return out
+        return out + list(self.basis)
 
     @staticmethod
     def unflat(spec: FusedSpec, flat: List[torch.Tensor]) -> "Params":
@@ -89,7 +95,17 @@ class Params:
         for has_b in spec.out_has_bias:
             out_w.append(next(it))
             out_b.append(next(it) if has_b else None)
-        return Params(emb, blocks, out_w, out_b)
+        basis = [next(it), next(it)] if spec.basis_trainable else []
+        return Params(emb, blocks, out_w, out_b, basis)
+
+
+def filter_spec(spec: FusedSpec, P: Params) -> ops.FilterSpec:
+    """The filter description with the basis tensors of this call (the
+    trainable parameters when the basis is trained)."""
+    if not spec.basis_trainable:
+        return spec.filt
+    c, w = (t.detach().float().reshape(-1).contiguous() for t in P.basis)
+    return replace(spec.filt, centers=c, widths=w)
 
 
 @dataclass
@@ -99,6 +115,7 @@ class State:
     pos: torch.Tensor
     types: torch.Tensor
     graph: ops.PairGraph
+    filt: Optional[ops.FilterSpec] = None
     dist: Optional[torch.Tensor] = None
     W: List[torch.Tensor] = field(default_factory=list)
     Wd: List[torch.Tensor] = field(default_factory=list)
@@ -185,10 +202,10 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     """Energies [B] and the saved state.  With rev_seed, the output network's
     kernel also forms the adjoint a following reverse1(seed=rev_seed) starts
     from."""
-    st = State(pos=pos, types=types, graph=graph)
+    st = State(pos=pos, types=types, graph=graph, filt=filter_spec(spec, P))
     x = P.emb.index_select(0, types)
     for k, bp in enumerate(P.blocks):
-        W, Wd, dist = ops.filter_fwd(pos, graph, spec.filt, bp.W1, bp.b1, bp.W2,
+        W, Wd, dist = ops.filter_fwd(pos, graph, st.filt, bp.W1, bp.b1, bp.W2,
                                      f16=spec.f16, want_dist=(k == 0))
         if k == 0:
             st.dist = dist
@@ -377,6 +394,7 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     graph = st.graph
     n_lin = len(P.out_w)
     g_blocks = [None] * len(P.blocks)
+    g_basis = None
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
         if tangent_on:
@@ -401,8 +419,13 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
         else:
             gA1 = ops.node_tmm(ybar2, st.x[k])
         xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
-        gW1, gb1, gW2 = ops.filter_bwd_cfconv(st.pos, graph, spec.filt, bp.W1, bp.b1, bp.W2,
-                                              gagg2, st.y[k], g1, yd, dd)
+        res = ops.filter_bwd_cfconv(st.pos, graph, st.filt, bp.W1, bp.b1, bp.W2, gagg2,
+                                    st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable)
+        gW1, gb1, gW2 = res[:3]
+        if spec.basis_trainable:
+            # basis parameters are shared by all blocks: accumulate
+            g_basis = ops.rbf_param_grad(st.dist, graph, st.filt, bp.W1, res[3], res[4],
+                                         out=g_basis)
         g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
     g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
     out = [g_emb]
@@ -412,6 +435,12 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
         out.append(g_out_w[k])
         if P.out_b[k] is not None:
             out.append(g_out_b[k])
+    if spec.basis_trainable:
+        gc, gw = g_basis
+        if P.basis[1].numel() != gw.numel():  # one shared Gaussian coefficient
+            gw = gw.sum()
+        out += [gc.reshape(P.basis[0].shape).to(P.basis[0].dtype),
+                gw.reshape(P.basis[1].shape).to(P.basis[1].dtype)]
     return out
 
 

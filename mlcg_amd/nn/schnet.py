@@ -2,9 +2,9 @@
 constructor signatures and state_dict keys (mlcg/nn/schnet.py:32-475).
 
 ``SchNet.forward`` runs the fused HIP path (``_fused``) whenever the model is
-made of the pieces the kernels implement (Gaussian basis with identity/cosine
-envelope, MLP filters [K, 128, 128] without last bias, Tanh or shifted
-softplus).  Other compositions run module by module, still on the HIP radius
+made of the pieces the kernels implement (Gaussian or exp-normal basis,
+trainable or not, with identity/cosine envelope, MLP filters [K, 128, 128]
+without last bias, Tanh or shifted softplus).  Other compositions run module by module, still on the HIP radius
 graph and the HIP CFConv gather.  Tensors on the CPU are rejected: there is
 no CPU implementation in this package.
 """
@@ -24,7 +24,7 @@ from . import _fused
 from .activations import activation_id
 from .cutoff import CosineCutoff, IdentityCutoff
 from .mlp import MLP, init_xavier_uniform
-from .radial_basis import GaussianBasis
+from .radial_basis import ExpNormalBasis, GaussianBasis
 
 
 class _EdgeGather(torch.autograd.Function):
@@ -127,6 +127,16 @@ class InteractionBlock(torch.nn.Module):
 _NL_METHODS = ("torch", "custom_kernel", "hip")
 
 
+def _basis_tensors(rbf):
+    """(centers, widths) of a basis the filter kernels evaluate -- Gaussian
+    (offset [K], coeff []) or exp-normal (means [K], betas [K]) -- else None."""
+    if isinstance(rbf, GaussianBasis):
+        return rbf.offset, rbf.coeff
+    if isinstance(rbf, ExpNormalBasis):
+        return rbf.means, rbf.betas
+    return None
+
+
 class SchNet(torch.nn.Module):
     """SchNet energy model (schnet.py:32-192)."""
 
@@ -190,13 +200,20 @@ class SchNet(torch.nn.Module):
     # ------------------------------------------------------------------
     def fused_spec(self) -> Optional[_fused.FusedSpec]:
         """The kernel description of this model, or None if some piece has no
-        kernel (then forward runs module by module).  Cached: building it reads
-        the basis coefficient back to the host once, and a cached spec lets the
-        fused path run inside a stream capture."""
+        kernel (then forward runs module by module).  Cached, so that the
+        fused path can run inside a stream capture: the spec holds the basis
+        tensors themselves (float32 views of the module's own parameters or
+        buffers), so in-place updates reach the kernels without a rebuild."""
         rbf = self.rbf_layer
-        key = (bool(self.fp16_filters), rbf.offset.data_ptr(), rbf.offset._version,
-               rbf.coeff.data_ptr(), rbf.coeff._version, bool(getattr(rbf, "trainable", False)),
-               len(self.interaction_blocks))
+        bt = _basis_tensors(rbf)
+        key = (bool(self.fp16_filters), type(rbf), len(self.interaction_blocks),
+               bool(getattr(rbf, "trainable", False)))
+        if bt is not None:
+            # a float32 contiguous tensor is used in place; anything else is
+            # converted, and the conversion is redone when the source changes
+            key += tuple((t.data_ptr(), t.dtype, t.is_contiguous(),
+                          None if t.dtype == torch.float32 and t.is_contiguous() else t._version)
+                         for t in bt)
         cached = self.__dict__.get("_spec_cache")
         if cached is not None and cached[0] == key:
             return cached[1]
@@ -206,7 +223,9 @@ class SchNet(torch.nn.Module):
 
     def _build_fused_spec(self) -> Optional[_fused.FusedSpec]:
         rbf = self.rbf_layer
-        if not isinstance(rbf, GaussianBasis) or rbf.trainable:
+        bt = _basis_tensors(rbf)
+        if bt is None or bt[1].numel() != (bt[0].numel() if isinstance(rbf, ExpNormalBasis)
+                                           else 1):
             return None
         if not isinstance(self.embedding_layer, torch.nn.Embedding):
             return None
@@ -226,7 +245,7 @@ class SchNet(torch.nn.Module):
             if (len(lins) != 2 or len(acts) != 1 or lins[1].bias is not None
                     or lins[0].bias is None or lins[0].out_features != ops.NUM_FILTERS
                     or lins[1].out_features != ops.NUM_FILTERS
-                    or lins[0].in_features != rbf.num_rbf):
+                    or lins[0].in_features != bt[0].numel()):
                 return None
             c = blk.conv.cutoff
             if not isinstance(c, (IdentityCutoff, CosineCutoff)):
@@ -252,9 +271,11 @@ class SchNet(torch.nn.Module):
             return None
         out_act = oa.pop() if oa else 0
         c0 = self.interaction_blocks[0].conv.cutoff
+        centers, widths = (t.detach().float().reshape(-1).contiguous() for t in bt)
         filt = ops.FilterSpec(
-            offsets=rbf.offset.detach().float().contiguous(),
-            coeff=float(rbf.coeff), num_rbf=rbf.num_rbf,
+            centers=centers, widths=widths, num_rbf=centers.numel(),
+            basis=ops.BASIS_EXPNORMAL if isinstance(rbf, ExpNormalBasis) else ops.BASIS_GAUSSIAN,
+            alpha=float(getattr(rbf, "alpha", 0.0)),
             rbf_cut_kind=rc.kind_id, rbf_lo=float(rc.cutoff_lower),
             rbf_hi=float(min(rc.cutoff_upper, 3.0e38)),
             conv_cut_kind=c0.kind_id, conv_lo=float(c0.cutoff_lower),
@@ -263,7 +284,7 @@ class SchNet(torch.nn.Module):
             filt=filt, filter_act=filt_act, block_act=block_act, out_act=out_act,
             num_blocks=len(self.interaction_blocks),
             out_has_bias=[lin.bias is not None for lin in self.output_network.linears()],
-            f16=bool(self.fp16_filters))
+            f16=bool(self.fp16_filters), basis_trainable=bool(rbf.trainable))
 
     def fused_params(self) -> _fused.Params:
         blocks = []
@@ -274,9 +295,11 @@ class SchNet(torch.nn.Module):
                 A2=blk.conv.lin2.weight, c2=blk.conv.lin2.bias, A3=blk.lin.weight,
                 c3=blk.lin.bias))
         lins = self.output_network.linears()
+        rbf = self.rbf_layer
+        basis = list(_basis_tensors(rbf)) if getattr(rbf, "trainable", False) else []
         return _fused.Params(emb=self.embedding_layer.weight, blocks=blocks,
                              out_w=[lin.weight for lin in lins],
-                             out_b=[lin.bias for lin in lins])
+                             out_b=[lin.bias for lin in lins], basis=basis)
 
     def build_graph(self, data) -> ops.PairGraph:
         """Radius graph with the receiver CSR and pair map (HIP kernels)."""

@@ -436,10 +436,15 @@ def out_rev2(x: torch.Tensor, xdot: Optional[torch.Tensor], W0: torch.Tensor,
 
 @dataclass
 class FilterSpec:
-    """Static description of one fused RBF -> cutoff -> MLP -> cutoff chain."""
+    """Description of one fused RBF -> cutoff -> MLP -> cutoff chain.
 
-    offsets: torch.Tensor  # [K] float32 device
-    coeff: float
+    basis 0 (Gaussian): centers = offset [K], widths = coeff [1];
+    basis 1 (ExpNormal): centers = means [K], widths = betas [K], alpha.
+    centers/widths are float32 device tensors the kernels read at launch
+    (they may be the module's own parameters)."""
+
+    centers: torch.Tensor
+    widths: torch.Tensor
     num_rbf: int
     rbf_cut_kind: int
     rbf_lo: float
@@ -448,6 +453,14 @@ class FilterSpec:
     conv_lo: float
     conv_hi: float
     act: int
+    basis: int = 0
+    alpha: float = 0.0
+
+    def basis_args(self):
+        return (int(self.basis), ptr(self.centers), ptr(self.widths), float(self.alpha))
+
+
+BASIS_GAUSSIAN, BASIS_EXPNORMAL = 0, 1
 
 
 def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
@@ -466,17 +479,26 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     dist = torch.empty(cap, dtype=torch.float32, device=pos.device) if want_dist else None
     W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
     call("mlcg_filter_fwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
-         ptr(spec.offsets), spec.coeff, spec.num_rbf, spec.rbf_cut_kind, spec.rbf_lo,
+         *spec.basis_args(), spec.num_rbf, spec.rbf_cut_kind, spec.rbf_lo,
          spec.rbf_hi, spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c),
          ptr(b1c), ptr(W2c), F, int(f16), ptr(W), ptr(Wd), ptr(dist),
          stream_handle(pos.device))
     return W, Wd, dist
 
 
+def _pair_adjoint_outputs(want: bool, cap: int, F: int, dev):
+    if not want:
+        return None, None
+    return (torch.empty(cap, F, dtype=torch.float32, device=dev),
+            torch.empty(cap, F, dtype=torch.float32, device=dev))
+
+
 def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
                b1: torch.Tensor, W2: torch.Tensor, Wbar: torch.Tensor,
-               Wdbar: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gradients (dW1 [F, K], db1 [F], dW2 [F, F]) of <Wbar, W> + <Wdbar, dW/dd>."""
+               Wdbar: torch.Tensor, pair_adjoints: bool = False):
+    """Gradients (dW1 [F, K], db1 [F], dW2 [F, F]) of <Wbar, W> + <Wdbar, dW/dd>;
+    with pair_adjoints also the first-layer pair adjoints (abar, adbar)
+    [P, F] that rbf_param_grad consumes."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     K = spec.num_rbf
@@ -491,11 +513,14 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     db1 = torch.empty(F, dtype=torch.float32, device=dev)
     dW2 = torch.empty(F, F, dtype=torch.float32, device=dev)
     W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
+    ab, adb = _pair_adjoint_outputs(pair_adjoints, cap, F, dev)
     call("mlcg_filter_bwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
-         ptr(spec.offsets), spec.coeff, K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
+         *spec.basis_args(), K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
          spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
          ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(dW1), ptr(db1),
-         ptr(dW2), ptr(ws), nws, stream_handle(dev))
+         ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, stream_handle(dev))
+    if pair_adjoints:
+        return dW1, db1, dW2, ab, adb
     return dW1, db1, dW2
 
 
@@ -503,10 +528,10 @@ def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
                       W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor,
                       gagg2: torch.Tensor, y: torch.Tensor, gagg1: Optional[torch.Tensor],
                       ydot: Optional[torch.Tensor],
-                      ddot: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor,
-                                                             torch.Tensor]:
+                      ddot: Optional[torch.Tensor], pair_adjoints: bool = False):
     """filter_bwd with Wbar_p = g2_i y_j + g2_j y_i + g1_i yd_j + g1_j yd_i and
-    Wdbar_p = dd_p (g1_i y_j + g1_j y_i) formed in the kernel from node arrays."""
+    Wdbar_p = dd_p (g1_i y_j + g1_j y_i) formed in the kernel from node arrays
+    (pair_adjoints as in filter_bwd)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     K = spec.num_rbf
@@ -520,12 +545,41 @@ def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
     dW2 = torch.empty(F, F, dtype=torch.float32, device=dev)
     W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
     c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    ab, adb = _pair_adjoint_outputs(pair_adjoints, cap, F, dev)
     call("mlcg_filter_bwd_cfconv", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev),
-         cap, ptr(spec.offsets), spec.coeff, K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
+         cap, *spec.basis_args(), K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
          spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
          ptr(W2c), F, ptr(c(gagg2)), ptr(c(y)), ptr(c(gagg1)), ptr(c(ydot)), ptr(ddot),
-         ptr(dW1), ptr(db1), ptr(dW2), ptr(ws), nws, stream_handle(dev))
+         ptr(dW1), ptr(db1), ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, stream_handle(dev))
+    if pair_adjoints:
+        return dW1, db1, dW2, ab, adb
     return dW1, db1, dW2
+
+
+def rbf_param_grad(dist: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
+                   abar: torch.Tensor, adbar: torch.Tensor,
+                   out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
+    """(dcenters [K], dwidths [K]) of the basis from the first-layer pair
+    adjoints (mlcg_rbf_param_grad); added into `out` when given."""
+    require_device(dist, abar, adbar)
+    K = spec.num_rbf
+    cap = graph.pair_capacity
+    dev = dist.device
+    _check(tuple(abar.shape) == (cap, NUM_FILTERS) and abar.shape == adbar.shape,
+           "abar / adbar must be [pair_capacity, F]")
+    nws = int(_lib.load().mlcg_rbf_param_grad_workspace_floats(cap, K))
+    _check(nws > 0, f"num_rbf={K} is not supported")
+    ws = torch.empty(nws, dtype=torch.float32, device=dev)
+    accumulate = out is not None
+    if out is None:
+        out = (torch.empty(K, dtype=torch.float32, device=dev),
+               torch.empty(K, dtype=torch.float32, device=dev))
+    W1c = W1.detach().float().contiguous()
+    call("mlcg_rbf_param_grad", ptr(dist), ptr(graph.n_pairs_dev), cap, *spec.basis_args(), K,
+         spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi, ptr(W1c), NUM_FILTERS,
+         ptr(abar.contiguous()), ptr(adbar.contiguous()), int(accumulate), ptr(out[0]),
+         ptr(out[1]), ptr(ws), nws, stream_handle(dev))
+    return out
 
 
 # --------------------------------------------------------------------------

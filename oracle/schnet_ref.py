@@ -12,6 +12,11 @@ oracle and the HIP model can be loaded from the same dict.
 Parity pins (besides the restatement itself):
   cosine_cutoff   -- endpoint values of tests/unit/nn/test_cutoff.py:27-42
   gaussian_rbf    -- e_k(mu_k) == C(mu_k); offsets/coeff closed forms
+  expnormal_rbf   -- equals gaussian_rbf of u = exp(alpha (lo - d)) with
+                     offsets = means, coeff = -beta; e_k == C where u == mu_k;
+                     means/betas closed forms (exp_normal.py:80-94)
+  basis gradients -- central finite differences in fp64 of the energy and of
+                     the force loss with respect to the basis parameters
   schnet_energy   -- two-bead closed form; translation/rotation/permutation
                      invariance; sum_i F_i == 0 per frame
   forces          -- central finite differences in fp64
@@ -73,6 +78,28 @@ def gaussian_rbf(d: torch.Tensor, offset: torch.Tensor, coeff: torch.Tensor,
     return torch.exp(coeff * torch.pow(d - offset, 2)) * cut(d)
 
 
+def expnormal_params(lo: float, hi: float, num_rbf: int, dtype=torch.float32):
+    """ExpNormalBasis._initial_params (mlcg/nn/radial_basis/exp_normal.py:80-94):
+    means = linspace(exp(lo - hi), 1, K), betas = (2 / K (1 - exp(lo - hi)))^-2."""
+    start = torch.exp(torch.scalar_tensor(-hi + lo))
+    means = torch.linspace(start, 1, num_rbf)
+    betas = torch.tensor([(2 / num_rbf * (1 - start)) ** -2] * num_rbf)
+    return means.to(dtype), betas.to(dtype)
+
+
+def expnormal_alpha(lo: float, hi: float) -> float:
+    """alpha = 5 / (hi - lo) (exp_normal.py:70)."""
+    return 5.0 / (hi - lo)
+
+
+def expnormal_rbf(d: torch.Tensor, means: torch.Tensor, betas: torch.Tensor, alpha: float,
+                  lo: float, cut: Cutoff) -> torch.Tensor:
+    """ExpNormalBasis.forward (exp_normal.py:104-124):
+    C(d) exp(-beta_k (exp(alpha (lo - d)) - mu_k)^2)."""
+    d = d.unsqueeze(-1)
+    return cut(d) * torch.exp(-betas * (torch.exp(alpha * (-d + lo)) - means) ** 2)
+
+
 def shifted_softplus(x: torch.Tensor) -> torch.Tensor:
     """softplus(x) - ln 2 (the reference defines no SSP; this build's choice)."""
     return torch.nn.functional.softplus(x) - math.log(2.0)
@@ -120,6 +147,19 @@ class SchNetConfig:
     conv_hi: float = 20.0
     act: str = "tanh"
     num_blocks: int = 3
+    basis: str = "gaussian"        # "gaussian" | "expnormal"
+
+
+BASIS_KEYS = {"gaussian": ("rbf_layer.offset", "rbf_layer.coeff"),
+              "expnormal": ("rbf_layer.means", "rbf_layer.betas")}
+
+
+def rbf_expand(sd, cfg: SchNetConfig, distances: torch.Tensor) -> torch.Tensor:
+    rbf_cut = Cutoff(cfg.rbf_cut, cfg.rbf_lo, cfg.rbf_hi)
+    if cfg.basis == "gaussian":
+        return gaussian_rbf(distances, sd["rbf_layer.offset"], sd["rbf_layer.coeff"], rbf_cut)
+    return expnormal_rbf(distances, sd["rbf_layer.means"], sd["rbf_layer.betas"],
+                         expnormal_alpha(cfg.rbf_lo, cfg.rbf_hi), cfg.rbf_lo, rbf_cut)
 
 
 def _layers(sd, prefix: str) -> List[Dict[str, torch.Tensor]]:
@@ -140,11 +180,10 @@ def schnet_energy(sd: Dict[str, torch.Tensor], cfg: SchNetConfig, pos: torch.Ten
     """SchNet.forward (mlcg/nn/schnet.py:116-162) with the blocks of
     InteractionBlock.forward (229-262) and CFConv.forward/message (312-368)."""
     act = activation(cfg.act)
-    rbf_cut = Cutoff(cfg.rbf_cut, cfg.rbf_lo, cfg.rbf_hi)
     conv_cut = Cutoff(cfg.conv_cut, cfg.conv_lo, cfg.conv_hi)
     x = sd["embedding_layer.weight"][atom_types]
     distances = compute_distances(pos, edge_index)
-    rbf = gaussian_rbf(distances, sd["rbf_layer.offset"], sd["rbf_layer.coeff"], rbf_cut)
+    rbf = rbf_expand(sd, cfg, distances)
     for b in range(cfg.num_blocks):
         p = f"interaction_blocks.{b}"
         # CFConv.forward (schnet.py:340-347)
@@ -177,11 +216,14 @@ def force_mse(forces: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
 
 
 def force_matching_grads(sd, cfg, pos, atom_types, batch, edge_index, n_frames,
-                         f_ref: torch.Tensor, param_names: Optional[List[str]] = None):
+                         f_ref: torch.Tensor, param_names: Optional[List[str]] = None,
+                         trainable_basis: bool = False):
     """PLModel.step (mlcg/pl/model.py:113-131) + loss.backward(): the loss
-    mean((F - F_ref)^2) and d loss / d theta through the create_graph graph."""
+    mean((F - F_ref)^2) and d loss / d theta through the create_graph graph.
+    The basis parameters are among theta only when trainable_basis."""
+    fixed = () if trainable_basis else BASIS_KEYS[cfg.basis]
     params = {k: v.detach().clone().requires_grad_(True) for k, v in sd.items()
-              if k not in ("rbf_layer.offset", "rbf_layer.coeff")}
+              if k not in fixed}
     sd2 = dict(sd)
     sd2.update(params)
     E, F = schnet_energy_forces(sd2, cfg, pos, atom_types, batch, edge_index, n_frames,
@@ -214,9 +256,14 @@ def random_state_dict(cfg: SchNetConfig, hidden: int = 128, filters: int = 128,
         return ((torch.rand(n, generator=g) * 2 - 1) * bias_scale).to(dtype)
 
     sd = {"embedding_layer.weight": torch.randn(embedding_size, hidden, generator=g).to(dtype)}
-    off, coeff = gaussian_params(cfg.rbf_lo, cfg.rbf_hi, cfg.num_rbf, dtype)
-    sd["rbf_layer.offset"] = off
-    sd["rbf_layer.coeff"] = coeff
+    if cfg.basis == "gaussian":
+        off, coeff = gaussian_params(cfg.rbf_lo, cfg.rbf_hi, cfg.num_rbf, dtype)
+        sd["rbf_layer.offset"] = off
+        sd["rbf_layer.coeff"] = coeff
+    else:
+        means, betas = expnormal_params(cfg.rbf_lo, cfg.rbf_hi, cfg.num_rbf, dtype)
+        sd["rbf_layer.means"] = means
+        sd["rbf_layer.betas"] = betas
     for b in range(cfg.num_blocks):
         p = f"interaction_blocks.{b}"
         sd[f"{p}.conv.lin1.weight"] = xavier(filters, hidden)

@@ -7,13 +7,13 @@ from oracle import schnet_ref as R
 
 
 def make_cfg(num_blocks=3, num_rbf=50, rc=20.0, act="tanh", rbf_cut="cosine",
-             conv_cut="cosine", conv_lo=0.0):
+             conv_cut="cosine", conv_lo=0.0, basis="gaussian"):
     return R.SchNetConfig(num_rbf=num_rbf, rbf_lo=0.0, rbf_hi=rc, rbf_cut=rbf_cut,
                           conv_cut=conv_cut, conv_lo=conv_lo, conv_hi=rc, act=act,
-                          num_blocks=num_blocks)
+                          num_blocks=num_blocks, basis=basis)
 
 
-def make_model(cfg, sd, out_widths=(64,), device="cuda"):
+def make_model(cfg, sd, out_widths=(64,), device="cuda", trainable_basis=False):
     from mlcg_amd import nn
 
     act = torch.nn.Tanh() if cfg.act == "tanh" else nn.ShiftedSoftplus()
@@ -21,7 +21,10 @@ def make_model(cfg, sd, out_widths=(64,), device="cuda"):
                else nn.IdentityCutoff(0.0, cfg.rbf_hi))
     conv_cut = (nn.CosineCutoff(cfg.conv_lo, cfg.conv_hi) if cfg.conv_cut == "cosine"
                 else nn.IdentityCutoff(cfg.conv_lo, cfg.conv_hi))
-    rbf = nn.GaussianBasis(rbf_cut, num_rbf=cfg.num_rbf)
+    if cfg.basis == "gaussian":
+        rbf = nn.GaussianBasis(rbf_cut, num_rbf=cfg.num_rbf, trainable=trainable_basis)
+    else:
+        rbf = nn.ExpNormalBasis(rbf_cut, num_rbf=cfg.num_rbf, trainable=trainable_basis)
     m = nn.StandardSchNet(rbf, conv_cut, list(out_widths), hidden_channels=128,
                           embedding_size=sd["embedding_layer.weight"].shape[0],
                           num_filters=128, num_interactions=cfg.num_blocks, activation=act)

@@ -129,13 +129,59 @@ def test_cutoff_bounds_raise(cls):
         getattr(nn, cls)(cutoff_lower=10, cutoff_upper=0)
 
 
-def test_gaussian_float_cutoff_defaults_to_identity():
-    """tests/unit/nn/radial_basis/test_radial_basis.py:30-44."""
+@pytest.mark.parametrize("basis,default_cutoff", [("GaussianBasis", "IdentityCutoff"),
+                                                   ("ExpNormalBasis", "CosineCutoff")])
+def test_basis_float_cutoff_defaults(basis, default_cutoff):
+    """tests/unit/nn/radial_basis/test_radial_basis.py:12-44."""
     from mlcg_amd import nn
 
-    basis = nn.GaussianBasis(cutoff=10)
-    assert isinstance(basis.cutoff, nn.IdentityCutoff)
-    assert basis.cutoff.cutoff_lower == 0 and basis.cutoff.cutoff_upper == 10
+    b = getattr(nn, basis)(cutoff=10)
+    assert isinstance(b.cutoff, getattr(nn, default_cutoff))
+    assert b.cutoff.cutoff_lower == 0 and b.cutoff.cutoff_upper == 10
+    with pytest.raises(ValueError):
+        getattr(nn, basis)(cutoff=nn.IdentityCutoff(cutoff_lower=10, cutoff_upper=0))
+
+
+def test_expnormal_module_matches_oracle():
+    """ExpNormalBasis: parameter/buffer registration and state_dict keys
+    (exp_normal.py:72-78), initial values and forward against the oracle."""
+    from mlcg_amd import nn
+    from oracle import schnet_ref as R
+
+    b = nn.ExpNormalBasis(nn.CosineCutoff(0.0, 12.0), num_rbf=16)
+    assert b.trainable and b.alpha == pytest.approx(5.0 / 12.0)
+    assert {k for k, _ in b.named_parameters()} == {"means", "betas"}
+    fixed = nn.ExpNormalBasis(12.0, num_rbf=16, trainable=False)
+    assert not list(fixed.parameters()) and set(fixed.state_dict()) == {"means", "betas"}
+    means, betas = R.expnormal_params(0.0, 12.0, 16)
+    assert torch.equal(b.means.data, means) and torch.equal(b.betas.data, betas)
+    d = torch.linspace(0.0, 13.0, 40)
+    ref = R.expnormal_rbf(d.double(), means.double(), betas.double(), 5.0 / 12.0, 0.0,
+                          R.Cutoff("cosine", 0.0, 12.0))
+    assert torch.allclose(b(d).double(), ref, rtol=1e-5, atol=1e-7)
+    with torch.no_grad():
+        b.means.mul_(2.0)
+    b.reset_parameters()
+    assert torch.equal(b.means.data, means)
+
+
+@pytest.mark.parametrize("basis,key", [("GaussianBasis", "offset"), ("ExpNormalBasis", "means")])
+@pytest.mark.parametrize("trainable", [False, True])
+def test_pruned_basis(basis, key, trainable):
+    """build_pruned_from_mask (gaussian.py:104-153, exp_normal.py:126-178)."""
+    from mlcg_amd import nn
+
+    mask = torch.tensor([True, False, True, True, False, False, True, False])
+    full = getattr(nn, basis)(nn.CosineCutoff(0.0, 8.0), num_rbf=8, trainable=trainable)
+    pr = getattr(nn, basis).build_pruned_from_mask(nn.CosineCutoff(0.0, 8.0), mask,
+                                                    num_rbf=8, trainable=trainable)
+    assert torch.equal(getattr(pr, key).data, getattr(full, key).data[mask])
+    assert pr.num_rbf == 8  # the reference keeps the unpruned count
+    assert (key in dict(pr.named_parameters())) == trainable
+    d = torch.linspace(0.1, 7.9, 9)
+    assert torch.allclose(pr(d), full(d)[:, mask])
+    with pytest.raises(ValueError):
+        getattr(nn, basis).build_pruned_from_mask(8.0, mask[:5], num_rbf=8)
 
 
 def test_fused_spec_recognises_config2():
@@ -146,6 +192,28 @@ def test_fused_spec_recognises_config2():
     assert spec is not None and spec.num_blocks == 3 and spec.filt.num_rbf == 50
     m2 = _config2_model(nn, act=torch.nn.ReLU())
     assert m2.fused_spec() is None  # no kernel for ReLU: module-by-module path
+
+
+@pytest.mark.parametrize("trainable", [False, True])
+def test_fused_spec_basis_kinds(trainable):
+    """Both bases, trainable or fixed, have a fused spec; its basis tensors
+    alias the module's own float32 parameters."""
+    from mlcg_amd import nn, ops
+
+    for cls, kind in ((nn.GaussianBasis, ops.BASIS_GAUSSIAN),
+                      (nn.ExpNormalBasis, ops.BASIS_EXPNORMAL)):
+        rbf = cls(nn.CosineCutoff(0, 20), num_rbf=50, trainable=trainable)
+        m = nn.StandardSchNet(rbf, nn.CosineCutoff(0, 20), [64], 128, 100, 128, 2,
+                              torch.nn.Tanh())
+        spec = m.fused_spec()
+        assert spec is not None and spec.filt.basis == kind
+        assert spec.basis_trainable == trainable
+        c = rbf.offset if cls is nn.GaussianBasis else rbf.means
+        assert spec.filt.centers.data_ptr() == c.data_ptr()
+        P = m.fused_params()
+        assert len(P.flat()) == 1 + 8 * 2 + 3 + (2 if trainable else 0)
+        if kind == ops.BASIS_EXPNORMAL:
+            assert spec.filt.alpha == pytest.approx(0.25)
 
 
 def test_collate_increments_index_keys():

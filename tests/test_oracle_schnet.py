@@ -13,10 +13,15 @@ Each check is chosen so that a plausible slip in the restatement fails it:
                     rotation and in-frame permutation invariance; frames are
                     independent; continuity when a pair crosses the cutoff
                     (catches a dropped filter envelope)
+  expnormal_rbf     means/betas closed forms (exp_normal.py:80-94); equal to
+                    the (pinned) Gaussian of u = exp(alpha (lo - d)) with
+                    offsets = means, coeff = -beta; e_k == C where u == mu_k
   forces            central finite differences in fp64; sum_i F_i == 0
   force_matching    the parameter gradient of mean((F - F_ref)^2) against
                     central finite differences along random parameter
-                    directions (pins the double backward)
+                    directions (pins the double backward), with the basis
+                    parameters (Gaussian offset/coeff, exp-normal means/betas)
+                    trained or fixed
 """
 
 import math
@@ -31,10 +36,10 @@ from oracle import schnet_ref as R
 D64 = torch.float64
 
 
-def _cfg(blocks=2, rc=8.0, act="tanh", rbf_cut="cosine", num_rbf=12):
+def _cfg(blocks=2, rc=8.0, act="tanh", rbf_cut="cosine", num_rbf=12, basis="gaussian"):
     return R.SchNetConfig(num_rbf=num_rbf, rbf_lo=0.0, rbf_hi=rc, rbf_cut=rbf_cut,
                           conv_cut="cosine", conv_lo=0.0, conv_hi=rc, act=act,
-                          num_blocks=blocks)
+                          num_blocks=blocks, basis=basis)
 
 
 def _sd(cfg, seed=0, hidden=128, filters=128):
@@ -88,6 +93,33 @@ def test_gaussian_params_and_values():
     assert torch.allclose(e1[ks, ks], torch.full((49,), math.exp(-0.5), dtype=D64), rtol=1e-6)
 
 
+@pytest.mark.parametrize("lo,hi,K", [(0.0, 5.0, 8), (0.5, 12.0, 50)])
+def test_expnormal_params_and_values(lo, hi, K):
+    means, betas = R.expnormal_params(lo, hi, K, D64)
+    start = math.exp(lo - hi)
+    assert float(means[0]) == pytest.approx(start, rel=1e-6)
+    assert float(means[-1]) == pytest.approx(1.0, rel=1e-7)
+    assert torch.allclose(means[1:] - means[:-1],
+                          torch.full((K - 1,), (1 - start) / (K - 1), dtype=D64), rtol=1e-5)
+    assert torch.allclose(betas, torch.full((K,), (2.0 / K * (1 - start)) ** -2, dtype=D64),
+                          rtol=1e-6)
+    alpha = R.expnormal_alpha(lo, hi)
+    assert alpha == pytest.approx(5.0 / (hi - lo))
+    cut = R.Cutoff("cosine", lo, hi)
+    gen = torch.Generator().manual_seed(0)
+    d = lo + (hi - lo) * torch.rand(40, dtype=D64, generator=gen)
+    b = 3.0 + torch.rand(1, dtype=D64, generator=gen)
+    e = R.expnormal_rbf(d, means, b.expand(K), alpha, lo, cut)
+    # a Gaussian in u = exp(alpha (lo - d)) with the means as offsets
+    u = torch.exp(alpha * (lo - d))
+    g = R.gaussian_rbf(u, means, -b, R.Cutoff("identity", 0.0, 1.0))
+    assert torch.allclose(e, g * cut(d).unsqueeze(-1), rtol=1e-12, atol=0)
+    # e_k == C(d_k) where u(d_k) == mu_k, i.e. d_k = lo - ln(mu_k) / alpha
+    dk = lo - torch.log(means) / alpha
+    ek = R.expnormal_rbf(dk, means, betas, alpha, lo, cut)
+    assert torch.allclose(torch.diagonal(ek), cut(dk), rtol=1e-12, atol=1e-15)
+
+
 # --------------------------------------------------------------------------
 # per-node numpy restatement of the math (no index_add, no edge lists)
 
@@ -104,8 +136,18 @@ def _np_energy(sd, cfg, pos, types):
     pos = pos.numpy()
     types = types.numpy()
     n = pos.shape[0]
-    off, coeff = s["rbf_layer.offset"], float(s["rbf_layer.coeff"])
     rc = cfg.conv_hi
+    if cfg.basis == "gaussian":
+        off, coeff = s["rbf_layer.offset"], float(s["rbf_layer.coeff"])
+
+        def basis(d):
+            return np.exp(coeff * (d - off) ** 2)
+    else:
+        means, betas = s["rbf_layer.means"], s["rbf_layer.betas"]
+        alpha = 5.0 / (cfg.rbf_hi - cfg.rbf_lo)
+
+        def basis(d):
+            return np.exp(-betas * (math.exp(-alpha * (d - cfg.rbf_lo)) - means) ** 2)
 
     def cosc(d):
         return 0.5 * (math.cos(d * math.pi / rc) + 1.0) if d < rc else 0.0
@@ -126,7 +168,7 @@ def _np_energy(sd, cfg, pos, types):
                 if not np.float32(d) < np.float32(rc):
                     continue
                 crbf = cosc(d) if cfg.rbf_cut == "cosine" else 1.0
-                g = np.exp(coeff * (d - off) ** 2) * crbf
+                g = basis(d) * crbf
                 w = W2 @ act(W1 @ g + b1) * cosc(d)
                 agg[i] += y[j] * w
         z = agg @ s[f"{p}.conv.lin2.weight"].T + s[f"{p}.conv.lin2.bias"]
@@ -136,10 +178,11 @@ def _np_energy(sd, cfg, pos, types):
     return float(o.sum())
 
 
+@pytest.mark.parametrize("basis", ["gaussian", "expnormal"])
 @pytest.mark.parametrize("act", ["tanh", "ssp"])
 @pytest.mark.parametrize("n_beads", [2, 3, 5])
-def test_energy_matches_per_node_restatement(act, n_beads):
-    cfg = _cfg(blocks=2, rc=6.0, act=act)
+def test_energy_matches_per_node_restatement(act, n_beads, basis):
+    cfg = _cfg(blocks=2, rc=6.0, act=act, basis=basis)
     sd = _sd(cfg, seed=n_beads)
     rng = np.random.default_rng(n_beads)
     pos = torch.from_numpy(rng.normal(0, 2.0, (n_beads, 3)))
@@ -210,14 +253,18 @@ def test_forces_finite_differences(act):
         assert torch.allclose(F[batch == b].sum(0), torch.zeros(3, dtype=D64), atol=1e-10)
 
 
-@pytest.mark.parametrize("act", ["tanh", "ssp"])
-def test_force_matching_grads_finite_differences(act):
-    cfg = _cfg(blocks=2, rc=7.0, act=act)
+@pytest.mark.parametrize("act,basis,trainable", [
+    ("tanh", "gaussian", False), ("ssp", "gaussian", False), ("tanh", "gaussian", True),
+    ("tanh", "expnormal", True), ("ssp", "expnormal", True), ("tanh", "expnormal", False)])
+def test_force_matching_grads_finite_differences(act, basis, trainable):
+    cfg = _cfg(blocks=2, rc=7.0, act=act, basis=basis)
     sd = _sd(cfg, seed=7)
     pos, types, batch = _frames(2, 6, seed=8, spread=2.5)
     ei = _edges(pos, 7.0, batch)
     fref = torch.randn(pos.shape, dtype=D64, generator=torch.Generator().manual_seed(9))
-    loss, _, _, grads = R.force_matching_grads(sd, cfg, pos, types, batch, ei, 2, fref)
+    loss, _, _, grads = R.force_matching_grads(sd, cfg, pos, types, batch, ei, 2, fref,
+                                               trainable_basis=trainable)
+    assert all(k in grads for k in R.BASIS_KEYS[basis]) == trainable
     gen = torch.Generator().manual_seed(10)
     names = list(grads)
     for trial in range(3):
@@ -239,6 +286,36 @@ def test_force_matching_grads_finite_differences(act):
     for k in names:
         if k != "embedding_layer.weight":
             assert float(grads[k].abs().max()) > 0, k
+
+
+@pytest.mark.parametrize("basis", ["gaussian", "expnormal"])
+def test_energy_basis_gradients_finite_differences(basis):
+    """dE/d(basis parameters) by autograd through the oracle against central
+    differences (the first-order path a trainable basis takes)."""
+    cfg = _cfg(blocks=2, rc=7.0, basis=basis)
+    sd = _sd(cfg, seed=11)
+    pos, types, batch = _frames(2, 6, seed=12, spread=2.5)
+    ei = _edges(pos, 7.0, batch)
+    keys = R.BASIS_KEYS[basis]
+    w = torch.tensor([0.7, -1.3], dtype=D64)
+    sd2 = dict(sd)
+    for k in keys:
+        sd2[k] = sd[k].clone().requires_grad_(True)
+    E = R.schnet_energy(sd2, cfg, pos, types, batch, ei, 2)
+    grads = torch.autograd.grad((E * w).sum(), [sd2[k] for k in keys])
+    gen = torch.Generator().manual_seed(13)
+    for k, g in zip(keys, grads):
+        assert float(g.abs().max()) > 0, k
+        v = torch.randn(sd[k].shape, dtype=D64, generator=gen)
+        h = 1e-6 * max(1.0, float(sd[k].abs().max()))
+
+        def e_at(sign):
+            sd3 = dict(sd)
+            sd3[k] = sd[k] + sign * h * v
+            return float((R.schnet_energy(sd3, cfg, pos, types, batch, ei, 2) * w).sum())
+
+        fd = (e_at(1.0) - e_at(-1.0)) / (2 * h)
+        assert float((g * v).sum()) == pytest.approx(fd, rel=1e-6, abs=1e-9), k
 
 
 def test_golden_fixture_reproduced():
