@@ -72,25 +72,41 @@ __device__ __forceinline__ float pair_distance(const float* __restrict__ pos,
 }
 
 // g_k and dg_k/dd for one basis function (zero past K).
-__device__ __forceinline__ void rbf_value(const RbfParams& rp, int k, float d, float crbf,
-                                          float dcrbf, float& g, float& gd) {
-  if (k >= rp.K) {
+// g_k and g_k' of one basis function from its centre `cen` and width `wid`
+// (the Gaussian's shared coeff, or the exp-normal beta_k); zero when !on.
+__device__ __forceinline__ void rbf_eval(const RbfParams& rp, bool on, float cen, float wid,
+                                         float d, float crbf, float dcrbf, float& g,
+                                         float& gd) {
+  if (!on) {
     g = 0.0f;
     gd = 0.0f;
   } else if (rp.basis == 0) {
-    const float c = rp.widths[0];
-    const float diff = d - rp.centers[k];
-    const float e = __expf(c * (diff * diff));  // argument <= 0: no overflow
+    const float diff = d - cen;
+    const float e = __expf(wid * (diff * diff));  // argument <= 0: no overflow
     g = e * crbf;
-    gd = e * (2.0f * c * diff * crbf + dcrbf);
+    gd = e * (2.0f * wid * diff * crbf + dcrbf);
   } else {
     const float ex = __expf(rp.alpha * (rp.rbf_lo - d));
-    const float u = ex - rp.centers[k];
-    const float b = rp.widths[k];
-    const float e = __expf(-b * (u * u));
+    const float u = ex - cen;
+    const float e = __expf(-wid * (u * u));
     g = e * crbf;
-    gd = e * (dcrbf + 2.0f * rp.alpha * b * u * ex * crbf);
+    gd = e * (dcrbf + 2.0f * rp.alpha * wid * u * ex * crbf);
   }
+}
+
+// Centre and width of basis function k read from global memory (zero past K).
+__device__ __forceinline__ void basis_params(const RbfParams& rp, int k, float& cen,
+                                             float& wid) {
+  const bool on = k < rp.K;
+  cen = on ? rp.centers[k] : 0.0f;
+  wid = on ? (rp.basis == 0 ? rp.widths[0] : rp.widths[k]) : 0.0f;
+}
+
+// The basis parameters staged in LDS once per workgroup, so that the
+// per-tile basis evaluation reads them with LDS latency instead of a global
+// load: bc[k], bw[k] for k < kMaxK (zero past K).
+__device__ void stage_basis(float* bc, float* bw, const RbfParams& rp) {
+  for (int k = threadIdx.x; k < kMaxK; k += blockDim.x) basis_params(rp, k, bc[k], bw[k]);
 }
 
 // ---------------------------------------------------------------------------
@@ -137,7 +153,8 @@ __device__ void stage_w2_f32(float* w2s, const float* __restrict__ W2, bool tran
 // First product for one 16-pair tile: acc_a = W1 g^T, acc_d = W1 g'^T (fp32).
 // Also returns the lane's g/g' values when `gout` is non-null (reverse pass).
 __device__ __forceinline__ void gemm1_f32(const float* w1s, int KS, const RbfParams& rp,
-                                          float d, float crbf, float dcrbf, floatx4* acc_a,
+                                          const float* bc, const float* bw, float d,
+                                          float crbf, float dcrbf, floatx4* acc_a,
                                           floatx4* acc_d, float* gout, float* gdout,
                                           float gscale) {
   const int l = mlcg_lane();
@@ -149,7 +166,8 @@ __device__ __forceinline__ void gemm1_f32(const float* w1s, int KS, const RbfPar
   }
   for (int s = 0; s < KS; ++s) {
     float g, gd;
-    rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);
+    const int k = 4 * s + q;
+    rbf_eval(rp, k < rp.K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
     if (gout) {
       gout[4 * s + q] = g * gscale;
       gdout[4 * s + q] = gd * gscale;
@@ -200,8 +218,11 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f32_kernel(
   const int KS = (rp.K + 3) / 4;
   float* w1s = lds;
   float* w2s = lds + kFT * KS * MLCG_WAVE;
+  float* bc = w2s + kFT * kFT * MLCG_WAVE * 4;
+  float* bw = bc + kMaxK;
   stage_w1_f32(w1s, W1, rp.K, KS);
   stage_w2_f32(w2s, W2, false);
+  stage_basis(bc, bw, rp);
   __syncthreads();
 
   int64_t np = *n_pairs_dev;
@@ -226,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f32_kernel(
     mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
 
     floatx4 a[kFT], ad[kFT];
-    gemm1_f32(w1s, KS, rp, d, crbf, dcrbf, a, ad, nullptr, nullptr, 0.0f);
+    gemm1_f32(w1s, KS, rp, bc, bw, d, crbf, dcrbf, a, ad, nullptr, nullptr, 0.0f);
     // h = act(a + b1), h' = act'(a + b1) * a'
 #pragma unroll
     for (int t = 0; t < kFT; ++t)
@@ -313,8 +334,11 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
   // the bias lives in LDS here (not registers): the fp16 path keeps more
   // operand fragments live and would otherwise spill
   float* b1s = reinterpret_cast<float*>(w2h + kFT * (kFT / 2) * MLCG_WAVE * 8);
+  float* bc = b1s + kF;
+  float* bw = bc + kMaxK;
   stage_f16(w1h, w2h, W1, W2, rp.K, KS32);
   for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
+  stage_basis(bc, bw, rp);
   __syncthreads();
 
   int64_t np = *n_pairs_dev;
@@ -346,7 +370,8 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float g, gd;
-        rbf_value(rp, 32 * s + 8 * q + j, d, crbf, dcrbf, g, gd);
+        const int k = 32 * s + 8 * q + j;
+        rbf_eval(rp, k < rp.K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
         g8[j] = (_Float16)g;
         gd8[j] = (_Float16)gd;
       }
@@ -414,37 +439,55 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
 // tile w (features 16w..16w+15) in every product.  Its slice of W1 (one A
 // fragment per k step) stays in registers; the W2^T A fragments of all eight
 // tiles are staged once in LDS.  Per tile:
-//   0. the waves share the per-pair scalar work: wave w evaluates the basis
-//      columns of k steps w and w + 8 for the 16 pairs (g, g' into LDS), and
-//      wave 0 the filter envelope C, C';                        -- barrier --
-//   1. a, a' of feature tile w (v_mfma_f32_16x16x4f32, B operand from LDS);
-//   2. t, t', h, h' of its features, published in LDS as [pair][feature]
-//      rows;                                                     -- barrier --
+//   1. a, a' of feature tile w (v_mfma_f32_16x16x4f32, B operand g, g' from
+//      LDS);
+//   2. t, t', h, h' of its features, published in LDS;         -- barrier --
 //   3. hb, hb' of its tile (B operands = all 128 t features from LDS);
 //   4. dW2 rows of its tile += t^T h over the 16 pairs (the pair index is the
-//      MFMA reduction axis; both operands read from the LDS rows);
-//   5. ab, ab' published in their own buffer;                   -- barrier --
+//      MFMA reduction axis);
+//   5. ab, ab' published, and the basis g, g' and envelope C, C' of the next
+//      tile evaluated (wave w: k steps w, w + 8, ...);        -- barrier --
 //   6. dW1 rows of its tile += ab^T g.
-// The g and envelope buffers are double-buffered across tiles, which makes
-// three barriers per tile sufficient.  The accumulators stay in registers
-// across all tiles of the workgroup; at the end each workgroup writes its
-// partial sums, and filter_bwd_reduce adds the partials in workgroup order,
-// so the result is deterministic.  Nothing per pair is written to HBM.
+// g, g' are double-buffered across tiles, so a tile costs two barriers.  The
+// accumulators stay in registers across all tiles of the workgroup; at the
+// end each workgroup writes its partial sums, and filter_bwd_reduce adds the
+// partials in workgroup order, so the result is deterministic.  Nothing per
+// pair is written to HBM (unless the first-layer pair adjoints are asked for).
+//
+// The global inputs of a tile (bead positions, node vectors) are requested
+// one tile ahead and the pair indices two tiles ahead, so no load latency is
+// waited for inside a tile.
+//
+// LDS layouts.  The LDS has 32 four-byte banks; a float4 access serves the
+// lane groups {0-3, 20-23}, {4-7, 16-19}, {8-11, 28-31}, {12-15, 24-27} (and
+// the same +32) in one cycle each, a scalar access one half-wave per cycle.
+//   TB  [pair][feature]: t, t' as the B operand of step 3 (float4 of four
+//       features of one pair); rows of 128 floats, float4 group g of pair n
+//       stored at g ^ (n & 7).
+//   TT, HT, AT, GT  [row][pair] (row = feature, or basis index k for GT): the
+//       operands of the pair reductions, steps 4 and 6 (float4 of four pairs
+//       of one row), and the B operand of step 1 (scalar); rows of 16 floats,
+//       float4 pair group c of row r stored at c ^ ((r >> 1) & 3).
+// All reads are free of bank conflicts; the scalar [row][pair] writes of TT,
+// HT and AT are 2-way.
 constexpr int kBwdWaves = 8;
 constexpr int kBwdThreads = kBwdWaves * MLCG_WAVE;
-constexpr int kRowPad = 4;
-constexpr int kXRow = kF + kRowPad;  // LDS row of one pair's 128 features
+
+__device__ __forceinline__ int tb_at(int pair, int g) { return pair * kF + ((g ^ (pair & 7)) << 2); }
+__device__ __forceinline__ int rp_at(int r, int pair) {
+  return r * 16 + ((((pair >> 2) ^ ((r >> 1) & 3)) << 2) | (pair & 3));
+}
 
 __host__ __device__ constexpr int bwd_kp16(int K) { return 16 * ((K + 15) / 16); }
 __host__ __device__ constexpr int bwd_partial_floats(int K) {
   return kF * kF + kF * bwd_kp16(K) + kF;
 }
-__host__ __device__ constexpr int bwd_grow(int K) { return (K <= 64 ? 64 : 128) + 4; }
-// LDS: W2^T fragments [8][8][64] float4 | TB, HH, AB [2][16][kXRow] |
-//      GG [2 buffers][2][16][grow] | PS [2 buffers][16][2] (C, C')
+__host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
+// LDS: W2^T fragments [8][8][64] float4 | TB [2][16][128] | TT, HT, AT
+//      [2][128][16] | GT [2 buffers][2][krows][16]; 147,456 bytes for K <= 64
+//      and exactly the 160 KiB of a gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
-  return kFT * kFT * MLCG_WAVE * 4 + 3 * 2 * 16 * kXRow + 2 * 2 * 16 * bwd_grow(K) +
-         2 * 16 * 2;
+  return kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 3 * 2 * kF * 16 + 2 * 2 * bwd_krows(K) * 16;
 }
 
 // Where the pair adjoints (Wbar, Wdbar) come from: explicit [P, F] arrays, or
@@ -470,67 +513,56 @@ __device__ __forceinline__ float4 f4(float a, float b, float c, float d) {
   return float4{a, b, c, d};
 }
 
-// Global inputs of one lane's pair for one tile, loaded one tile ahead so that
-// their latency overlaps the previous tile's MFMA work.
+// Global inputs of one lane's pair for one tile.  Every load is issued
+// unconditionally (lanes past the last pair read the last pair, and absent
+// tangent arrays are replaced by present ones whose values are not used), so
+// that no branch joins force a wait for the loads before they are needed.
 struct TileIn {
   float xi, yi, zi, xj, yj, zj;  // positions of the pair's beads
   float4 v[8];                   // adjoint sources (explicit: v[0..1])
   float dd;
-  bool valid;
 };
 
 template <bool kNodes>
 __device__ __forceinline__ TileIn fetch_tile(const float* __restrict__ pos,
-                                             const int32_t* __restrict__ pi,
-                                             const int32_t* __restrict__ pj,
-                                             const PairAdjoint& adj, int64_t p, int64_t np,
-                                             int fcol) {
+                                             const PairAdjoint& adj, const float* ddp,
+                                             const float* g1p, const float* ydp, int64_t p,
+                                             int64_t i, int64_t j, int fcol) {
   TileIn t;
-  t.valid = p < np;
-  t.dd = 0.f;
-  const float4 z = {0.f, 0.f, 0.f, 0.f};
+  t.xi = pos[3 * i];
+  t.yi = pos[3 * i + 1];
+  t.zi = pos[3 * i + 2];
+  t.xj = pos[3 * j];
+  t.yj = pos[3 * j + 1];
+  t.zj = pos[3 * j + 2];
+  if (!kNodes) {
+    t.v[0] = ld4(adj.Wbar, p, fcol);
+    t.v[1] = ld4(adj.Wdbar, p, fcol);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) t.v[k] = z;
-  t.xi = t.yi = t.zi = 0.f;
-  t.xj = 1.f;  // harmless distance for padding lanes
-  t.yj = t.zj = 0.f;
-  if (t.valid) {
-    const int64_t i = pi[p], j = pj[p];
-    t.xi = pos[3 * i];
-    t.yi = pos[3 * i + 1];
-    t.zi = pos[3 * i + 2];
-    t.xj = pos[3 * j];
-    t.yj = pos[3 * j + 1];
-    t.zj = pos[3 * j + 2];
-    if (!kNodes) {
-      t.v[0] = ld4(adj.Wbar, p, fcol);
-      t.v[1] = ld4(adj.Wdbar, p, fcol);
-    } else {
-      t.v[0] = ld4(adj.g2, i, fcol);
-      t.v[1] = ld4(adj.g2, j, fcol);
-      t.v[2] = ld4(adj.y, i, fcol);
-      t.v[3] = ld4(adj.y, j, fcol);
-      if (adj.g1) {
-        t.v[4] = ld4(adj.g1, i, fcol);
-        t.v[5] = ld4(adj.g1, j, fcol);
-        if (adj.yd) {
-          t.v[6] = ld4(adj.yd, i, fcol);
-          t.v[7] = ld4(adj.yd, j, fcol);
-        }
-        t.dd = adj.dd[p];
-      }
-    }
+    for (int k = 2; k < 8; ++k) t.v[k] = float4{0.f, 0.f, 0.f, 0.f};
+    t.dd = 0.f;
+  } else {
+    t.v[0] = ld4(adj.g2, i, fcol);
+    t.v[1] = ld4(adj.g2, j, fcol);
+    t.v[2] = ld4(adj.y, i, fcol);
+    t.v[3] = ld4(adj.y, j, fcol);
+    t.v[4] = ld4(g1p, i, fcol);
+    t.v[5] = ld4(g1p, j, fcol);
+    t.v[6] = ld4(ydp, i, fcol);
+    t.v[7] = ld4(ydp, j, fcol);
+    t.dd = ddp[p];
   }
   return t;
 }
 
-// Wbar, Wdbar of the lane's 4 features from the prefetched sources.
+// Wbar, Wdbar of the lane's 4 features from the prefetched sources (zero for
+// a lane past the last pair: vm = 0).
 template <bool kNodes>
-__device__ __forceinline__ void tile_adjoint(const TileIn& t, bool tangent, float4& wb,
-                                             float4& wdb) {
+__device__ __forceinline__ void tile_adjoint(const TileIn& t, bool tangent, bool has_yd,
+                                             float vm, float4& wb, float4& wdb) {
   if (!kNodes) {
-    wb = t.v[0];
-    wdb = t.v[1];
+    wb = f4(t.v[0].x * vm, t.v[0].y * vm, t.v[0].z * vm, t.v[0].w * vm);
+    wdb = f4(t.v[1].x * vm, t.v[1].y * vm, t.v[1].z * vm, t.v[1].w * vm);
     return;
   }
   const float4 g2i = t.v[0], g2j = t.v[1], yi = t.v[2], yj = t.v[3];
@@ -539,14 +571,17 @@ __device__ __forceinline__ void tile_adjoint(const TileIn& t, bool tangent, floa
           g2i.z * yj.z + g2j.z * yi.z, g2i.w * yj.w + g2j.w * yi.w);
   wdb = f4(0.f, 0.f, 0.f, 0.f);
   if (tangent) {
-    // ydot terms are zero when ydot is absent (v[6], v[7] stay zero)
-    wb.x += g1i.x * ydj.x + g1j.x * ydi.x;
-    wb.y += g1i.y * ydj.y + g1j.y * ydi.y;
-    wb.z += g1i.z * ydj.z + g1j.z * ydi.z;
-    wb.w += g1i.w * ydj.w + g1j.w * ydi.w;
-    wdb = f4(t.dd * (g1i.x * yj.x + g1j.x * yi.x), t.dd * (g1i.y * yj.y + g1j.y * yi.y),
-             t.dd * (g1i.z * yj.z + g1j.z * yi.z), t.dd * (g1i.w * yj.w + g1j.w * yi.w));
+    if (has_yd) {
+      wb.x += g1i.x * ydj.x + g1j.x * ydi.x;
+      wb.y += g1i.y * ydj.y + g1j.y * ydi.y;
+      wb.z += g1i.z * ydj.z + g1j.z * ydi.z;
+      wb.w += g1i.w * ydj.w + g1j.w * ydi.w;
+    }
+    const float s = t.dd * vm;
+    wdb = f4(s * (g1i.x * yj.x + g1j.x * yi.x), s * (g1i.y * yj.y + g1j.y * yi.y),
+             s * (g1i.z * yj.z + g1j.z * yi.z), s * (g1i.w * yj.w + g1j.w * yi.w));
   }
+  wb = f4(wb.x * vm, wb.y * vm, wb.z * vm, wb.w * vm);
 }
 
 template <int KSMAX, bool kNodes>
@@ -557,26 +592,25 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const float* __restrict__ b1, const float* __restrict__ W2, PairAdjoint adj,
     float* __restrict__ abar_out, float* __restrict__ adbar_out, float* __restrict__ partial) {
   constexpr int KTMAX = (4 * KSMAX + 15) / 16;
-  // g rows span the compile-time maximum width and the unused columns stay
-  // zero, so the k loops below run without data-dependent branches (which
-  // would otherwise make the compiler copy the accumulators at every merge)
-  constexpr int gRow = 16 * KTMAX + 4;
+  // basis rows span the compile-time maximum width (rows k >= K hold zeros),
+  // so the k loops below run without data-dependent branches
+  constexpr int kRows = 16 * KTMAX;
+  static_assert(4 * KSMAX == kRows, "every basis row is written for every tile");
   extern __shared__ float lds[];
   const int K = rp.K;
   const int Kp16 = bwd_kp16(K);
   const int KT = Kp16 / 16;
   float* w2ts = lds;                                  // [8 t][8 u][64 l] float4
-  float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;       // [2][16][kXRow]  t, t'
-  float* HH = TB + 2 * 16 * kXRow;                    // [2][16][kXRow]  h, h'
-  float* AB = HH + 2 * 16 * kXRow;                    // [2][16][kXRow]  ab, ab'
-  float* GG0 = AB + 2 * 16 * kXRow;                   // [2 bufs][2][16][gRow] g, g'
-  float* PS0 = GG0 + 2 * 2 * 16 * gRow;               // [2 bufs][16][2] C, C'
+  float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;       // [2][16 pairs][128]  t, t'
+  float* TT = TB + 2 * 16 * kF;                       // [2][128][16 pairs]  t, t'
+  float* HT = TT + 2 * kF * 16;                       // [2][128][16 pairs]  h, h'
+  float* AT = HT + 2 * kF * 16;                       // [2][128][16 pairs]  ab, ab'
+  float* GT0 = AT + 2 * kF * 16;                      // [2 bufs][2][kRows][16]  g, g'
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
 
   stage_w2_f32(w2ts, W2, true);
-  for (int x = threadIdx.x; x < 2 * 2 * 16 * gRow; x += blockDim.x) GG0[x] = 0.0f;
 
   // W1 fragment of feature tile w stays in registers: W1[16w + n][4s + q]
   float w1f[KSMAX];
@@ -588,6 +622,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float bias[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) bias[i] = b1[16 * w + 4 * q + i];
+  // parameters of the basis functions this lane evaluates (k = 4 (8e + w) + q),
+  // kept in registers when K <= 64 (the wide variant has no registers to
+  // spare and reads them per tile)
+  constexpr int kBasisSteps = (KSMAX + kBwdWaves - 1) / kBwdWaves;
+  constexpr bool kBasisRegs = KSMAX <= 16;
+  float bcen[kBasisSteps], bwid[kBasisSteps];
+#pragma unroll
+  for (int e = 0; e < kBasisSteps; ++e)
+    if (kBasisRegs) basis_params(rp, 4 * (kBwdWaves * e + w) + q, bcen[e], bwid[e]);
 
   floatx4 acc2[kFT];
 #pragma unroll
@@ -596,62 +639,95 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
   for (int kt = 0; kt < KTMAX; ++kt) acc1[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float db[4] = {0.f, 0.f, 0.f, 0.f};
-  __syncthreads();
 
   int64_t np = max_pairs > 0 ? *n_pairs_dev : 0;
   if (np > max_pairs) np = max_pairs;
   const int64_t tiles = (np + 15) / 16;
-  const int fcol = 16 * w + 4 * q;  // first of the lane's 4 features in row layout
+  const int fcol = 16 * w + 4 * q;  // first of the lane's 4 features
+  // LDS offsets: a per-lane base plus a compile-time offset per unrolled step
+  const int oTBw = tb_at(n, 4 * w + q);  // step 2: t, t' of (pair n, features fcol..)
+  int oTB3[2];                           // step 3: tb_at(n, 4u + q) = oTB3[u & 1] + 32 (u >> 1)
+#pragma unroll
+  for (int e = 0; e < 2; ++e) oTB3[e] = n * kF + 16 * (e ^ ((n >> 2) & 1)) + 4 * (q ^ (n & 3));
+  // steps 4, 6: rp_at(16x + n, 4q) = oR + 256 x (float4 of pairs 4q..4q+3)
+  const int oR = n * 16 + 4 * (q ^ ((n >> 1) & 3));
+  const int oRw = oR + 256 * w;
+  int oG1[2];  // step 1: rp_at(4s + q, n) = oG1[s & 1] + 64 s
+#pragma unroll
+  for (int e = 0; e < 2; ++e) oG1[e] = 16 * q + 4 * ((n >> 2) ^ ((2 * e) | (q >> 1))) + (n & 3);
+  int oW[4];  // steps 2, 5: rp_at(16w + 4q + i, n)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) oW[i] = rp_at(fcol + i, n);
   const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
 
   const bool tangent = kNodes && adj.g1 != nullptr;
-  // Phase 0 of a tile: basis columns of k steps w and w + 8, and envelope.
-  // It runs for tile t + 1 in the same barrier interval as the last exchange
-  // of tile t, so a tile costs two workgroup barriers.
-  auto basis = [&](const TileIn& t, float* GGb, float* PSb) {
-    const float vm = t.valid ? 1.0f : 0.0f;
+  const bool has_yd = tangent && adj.yd != nullptr;
+  // stand-ins for absent tangent arrays: valid memory, values never used
+  const float* g1p = tangent ? adj.g1 : adj.g2;
+  const float* ydp = has_yd ? adj.yd : adj.y;
+  const float* ddp = tangent ? adj.dd : reinterpret_cast<const float*>(pi);
+  auto clamp_pair = [&](int64_t t_) -> int64_t {
+    const int64_t p = t_ * 16 + n;
+    return p < np ? p : np - 1;
+  };
+  // Basis of a tile: wave w evaluates k steps w, w + 8, ... for the 16 pairs
+  // (into GT), every lane the envelope of its own pair (returned).
+  auto basis = [&](const TileIn& t, float vm, float* GTb, float& cc, float& dcc) {
     const float dx = t.xj - t.xi, dy = t.yj - t.yi, dz = t.zj - t.zi;
     const float d = sqrtf(dx * dx + dy * dy + dz * dz);
     float crbf, dcrbf;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
 #pragma unroll
-    for (int s0 = 0; s0 < KSMAX; s0 += kBwdWaves) {
-      const int s = s0 + w;
+    for (int e = 0; e < kBasisSteps; ++e) {
+      const int s = kBwdWaves * e + w;
       if (s < KSMAX) {
-        float g, gd;
-        rbf_value(rp, 4 * s + q, d, crbf, dcrbf, g, gd);  // zero for k >= K
-        GGb[n * gRow + 4 * s + q] = g * vm;
-        GGb[16 * gRow + n * gRow + 4 * s + q] = gd * vm;
+        float g, gd, cen = bcen[e], wid = bwid[e];
+        if (!kBasisRegs) basis_params(rp, 4 * s + q, cen, wid);
+        rbf_eval(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
+        const int o = rp_at(4 * s + q, n);
+        GTb[o] = g * vm;
+        GTb[kRows * 16 + o] = gd * vm;
       }
     }
-    if (w == 0 && q == 0) {
-      float cc, dcc;
-      mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
-      PSb[2 * n] = cc;
-      PSb[2 * n + 1] = dcc;
-    }
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
   };
+
   int buf = 0;
-  TileIn cur = fetch_tile<kNodes>(pos, pi, pj, adj, (int64_t)blockIdx.x * 16 + n, np, fcol);
-  basis(cur, GG0, PS0);
+  TileIn cur;
+  float cc_cur = 0.f, dcc_cur = 0.f;
+  int64_t ni = 0, nj = 0;  // bead indices of the next tile's pair
+  if (np > 0) {  // uniform across the workgroup
+    const int64_t p0 = clamp_pair(blockIdx.x);
+    cur = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, p0, pi[p0], pj[p0], fcol);
+    const int64_t p1 = clamp_pair((int64_t)blockIdx.x + gridDim.x);
+    ni = pi[p1];
+    nj = pj[p1];
+    basis(cur, (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f, GT0, cc_cur, dcc_cur);
+  }
   __syncthreads();
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
-    float* GG = GG0 + buf * 2 * 16 * gRow;
-    float* PS = PS0 + buf * 16 * 2;
-    const float vmask = cur.valid ? 1.0f : 0.0f;
-    // the next tile's inputs are requested now; they are consumed one tile later
-    const TileIn nxt =
-        fetch_tile<kNodes>(pos, pi, pj, adj, (tile + gridDim.x) * 16 + n, np, fcol);
+    float* GT = GT0 + buf * 2 * kRows * 16;
+    const float vmask = tile * 16 + n < np ? 1.0f : 0.0f;
+    // inputs of the next tile and indices of the one after it: consumed one
+    // tile later
+    const int64_t pn = clamp_pair(tile + gridDim.x);
+    const TileIn nxt = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, pn, ni, nj, fcol);
+    {
+      const int64_t pnn = clamp_pair(tile + 2 * (int64_t)gridDim.x);
+      ni = pi[pnn];
+      nj = pj[pnn];
+    }
     float4 wb, wdb;
-    tile_adjoint<kNodes>(cur, tangent, wb, wdb);
+    tile_adjoint<kNodes>(cur, tangent, has_yd, vmask, wb, wdb);
 
     // 1. a, a' of feature tile w (two accumulators each: shorter MFMA chains)
     floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
     floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSMAX; ++s) {
-      const float g = GG[n * gRow + 4 * s + q];
-      const float gd = GG[16 * gRow + n * gRow + 4 * s + q];
+      const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
+      const float g = GT[o];
+      const float gd = GT[kRows * 16 + o];
       if (s & 1) {
         a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
         ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
@@ -663,25 +739,31 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     a += a_o;
     ad += ad_o;
     // 2. h, h', activation derivatives and t, t' of the lane's 4 features
-    const float cc = PS[2 * n], dcc = PS[2 * n + 1];
+    const float cc = cc_cur, dcc = dcc_cur;
     float act1[4], act2[4];
-    float4 hv, hdv;
+    float hv[4], hdv[4], tb[4], tdb[4];
+    const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
+    const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float sv, d1, d2;
       mlcg_act(rp.act, a[i] + bias[i], sv, d1, d2);
       act1[i] = d1;
       act2[i] = d2 * ad[i];
-      reinterpret_cast<float*>(&hv)[i] = sv * vmask;
-      reinterpret_cast<float*>(&hdv)[i] = d1 * ad[i] * vmask;
+      hv[i] = sv * vmask;
+      hdv[i] = d1 * ad[i] * vmask;
+      tb[i] = wbv[i] * cc + wdbv[i] * dcc;
+      tdb[i] = wdbv[i] * cc;
     }
-    const float4 tb = {wb.x * cc + wdb.x * dcc, wb.y * cc + wdb.y * dcc,
-                       wb.z * cc + wdb.z * dcc, wb.w * cc + wdb.w * dcc};
-    const float4 tdb = {wdb.x * cc, wdb.y * cc, wdb.z * cc, wdb.w * cc};
-    *reinterpret_cast<float4*>(TB + n * kXRow + fcol) = tb;
-    *reinterpret_cast<float4*>(TB + 16 * kXRow + n * kXRow + fcol) = tdb;
-    *reinterpret_cast<float4*>(HH + n * kXRow + fcol) = hv;
-    *reinterpret_cast<float4*>(HH + 16 * kXRow + n * kXRow + fcol) = hdv;
+    *reinterpret_cast<float4*>(TB + oTBw) = f4(tb[0], tb[1], tb[2], tb[3]);
+    *reinterpret_cast<float4*>(TB + 16 * kF + oTBw) = f4(tdb[0], tdb[1], tdb[2], tdb[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      TT[oW[i]] = tb[i];
+      TT[kF * 16 + oW[i]] = tdb[i];
+      HT[oW[i]] = hv[i];
+      HT[kF * 16 + oW[i]] = hdv[i];
+    }
     __syncthreads();
 
     // 3. hb, hb' of feature tile w (all 128 t features from LDS), four chains
@@ -690,9 +772,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
     for (int u = 0; u < kFT; ++u) {
       const float4 a2 = w2v[u * MLCG_WAVE];
-      const float4 bx = *reinterpret_cast<const float4*>(TB + n * kXRow + 16 * u + 4 * q);
-      const float4 by =
-          *reinterpret_cast<const float4*>(TB + 16 * kXRow + n * kXRow + 16 * u + 4 * q);
+      const int o = oTB3[u & 1] + 32 * (u >> 1);  // tb_at(n, 4u + q)
+      const float4 bx = *reinterpret_cast<const float4*>(TB + o);
+      const float4 by = *reinterpret_cast<const float4*>(TB + 16 * kF + o);
       hb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, bx.x, hb, 0, 0, 0);
       hdb = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.x, by.x, hdb, 0, 0, 0);
       hb_o = __builtin_amdgcn_mfma_f32_16x16x4f32(a2.y, bx.y, hb_o, 0, 0, 0);
@@ -704,58 +786,64 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     hb += hb_o;
     hdb += hdb_o;
-    float4 abv, adbv;
+    float abv[4], adbv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float ab = hb[i] * act1[i] + hdb[i] * act2[i];
-      reinterpret_cast<float*>(&abv)[i] = ab;
-      reinterpret_cast<float*>(&adbv)[i] = hdb[i] * act1[i];
-      db[i] += ab;
+      abv[i] = hb[i] * act1[i] + hdb[i] * act2[i];
+      adbv[i] = hdb[i] * act1[i];
+      db[i] += abv[i];
     }
-    // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c]
+    // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c];
+    //    MFMA step kk of lane group q reduces over pair 4q + kk
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const float* T = TB + st * 16 * kXRow;
-      const float* Hs = HH + st * 16 * kXRow;
+      const float* T = TT + st * kF * 16;
+      const float* H = HT + st * kF * 16;
+      const float4 av = *reinterpret_cast<const float4*>(T + oRw);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const float av = T[(4 * kk + q) * kXRow + 16 * w + n];
-        float bv[kFT];
-#pragma unroll
-        for (int u = 0; u < kFT; ++u) bv[u] = Hs[(4 * kk + q) * kXRow + 16 * u + n];
-#pragma unroll
-        for (int u = 0; u < kFT; ++u)
-          acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc2[u], 0, 0, 0);
+      for (int u = 0; u < kFT; ++u) {
+        const float4 bv = *reinterpret_cast<const float4*>(H + oR + 256 * u);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc2[u], 0, 0, 0);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc2[u], 0, 0, 0);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc2[u], 0, 0, 0);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc2[u], 0, 0, 0);
       }
     }
     // 5. publish ab, ab' (and store them per pair when the basis parameters
     //    need gradients) and the next tile's basis
-    *reinterpret_cast<float4*>(AB + n * kXRow + fcol) = abv;
-    *reinterpret_cast<float4*>(AB + 16 * kXRow + n * kXRow + fcol) = adbv;
-    if (abar_out && cur.valid) {
-      const int64_t p = tile * 16 + n;
-      *reinterpret_cast<float4*>(abar_out + p * kF + fcol) = abv;
-      *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) = adbv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      AT[oW[i]] = abv[i];
+      AT[kF * 16 + oW[i]] = adbv[i];
     }
-    basis(nxt, GG0 + (buf ^ 1) * 2 * 16 * gRow, PS0 + (buf ^ 1) * 16 * 2);
+    if (abar_out && vmask != 0.0f) {
+      const int64_t p = tile * 16 + n;
+      *reinterpret_cast<float4*>(abar_out + p * kF + fcol) = f4(abv[0], abv[1], abv[2], abv[3]);
+      *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) =
+          f4(adbv[0], adbv[1], adbv[2], adbv[3]);
+    }
+    float cc_nxt, dcc_nxt;
+    basis(nxt, (tile + gridDim.x) * 16 + n < np ? 1.0f : 0.0f,
+          GT0 + (buf ^ 1) * 2 * kRows * 16, cc_nxt, dcc_nxt);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const float* A = AB + st * 16 * kXRow;
-      const float* G = GG + st * 16 * gRow;
+      const float* A = AT + st * kF * 16;
+      const float* G = GT + st * kRows * 16;
+      const float4 av = *reinterpret_cast<const float4*>(A + oRw);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const float av = A[(4 * kk + q) * kXRow + 16 * w + n];
-        float bv[KTMAX];
-#pragma unroll
-        for (int kt = 0; kt < KTMAX; ++kt) bv[kt] = G[(4 * kk + q) * gRow + 16 * kt + n];
-#pragma unroll
-        for (int kt = 0; kt < KTMAX; ++kt)
-          acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[kt], acc1[kt], 0, 0, 0);
+      for (int kt = 0; kt < KTMAX; ++kt) {
+        const float4 bv = *reinterpret_cast<const float4*>(G + oR + 256 * kt);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc1[kt], 0, 0, 0);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc1[kt], 0, 0, 0);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc1[kt], 0, 0, 0);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc1[kt], 0, 0, 0);
       }
     }
     cur = nxt;
+    cc_cur = cc_nxt;
+    dcc_cur = dcc_nxt;
   }
 
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
@@ -902,7 +990,8 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
   hipStream_t s = mlcg_stream(stream);
   if (!f16) {
     const int KS = (num_rbf + 3) / 4;
-    const size_t lds = sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4);
+    const size_t lds =
+        sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4 + 2 * kMaxK);
     allow_lds_once();
     hipLaunchKernelGGL(filter_fwd_f32_kernel, dim3(groups), dim3(kThreads), lds, s, pos,
                        pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
@@ -911,7 +1000,7 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
     const int KS32 = (num_rbf + 31) / 32;
     const size_t lds =
         sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
-        sizeof(float) * kF;
+        sizeof(float) * (kF + 2 * kMaxK);
     allow_lds_once();
     const unsigned groups16 = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves16), 1);
     hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups16), dim3(kThreads16), lds, s, pos,
@@ -1026,12 +1115,12 @@ constexpr int kRgWaves = 4;
 constexpr int kRgThreads = kRgWaves * MLCG_WAVE;
 constexpr int kRgMaxGroups = 512;
 
-__device__ __forceinline__ void basis_param_derivs(const RbfParams& rp, int k, float d,
-                                                   float C, float dC, float& g_c, float& g_w,
-                                                   float& gd_c, float& gd_w) {
+__device__ __forceinline__ void basis_param_derivs(const RbfParams& rp, float cen, float wid,
+                                                   float d, float C, float dC, float& g_c,
+                                                   float& g_w, float& gd_c, float& gd_w) {
   if (rp.basis == 0) {
-    const float c = rp.widths[0];
-    const float x = d - rp.centers[k];
+    const float c = wid;
+    const float x = d - cen;
     const float e = __expf(c * x * x);
     const float q = 2.0f * c * x * C + dC;            // g' = e q
     g_c = -2.0f * c * x * C * e;                       // dg/dcenter
@@ -1040,8 +1129,8 @@ __device__ __forceinline__ void basis_param_derivs(const RbfParams& rp, int k, f
     gd_w = e * (x * x * q + 2.0f * x * C);             // dg'/dc
   } else {
     const float ex = __expf(rp.alpha * (rp.rbf_lo - d));
-    const float u = ex - rp.centers[k];
-    const float b = rp.widths[k];
+    const float u = ex - cen;
+    const float b = wid;
     const float e = __expf(-b * u * u);
     const float r = dC + 2.0f * rp.alpha * b * u * ex * C;  // g' = e r
     g_c = 2.0f * b * u * C * e;
@@ -1068,6 +1157,9 @@ __global__ __launch_bounds__(kRgThreads) void rbf_grad_kernel(
   int64_t np = max_pairs > 0 ? *n_pairs_dev : 0;
   if (np > max_pairs) np = max_pairs;
   const int64_t tiles = (np + 15) / 16;
+  float cen[KT], wid[KT];  // basis function 16kt + n of this lane
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) basis_params(rp, 16 * kt + n, cen[kt], wid[kt]);
   float sc[KT], sw[KT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) sc[kt] = sw[kt] = 0.f;
@@ -1111,7 +1203,7 @@ __global__ __launch_bounds__(kRgThreads) void rbf_grad_kernel(
         const int k = 16 * kt + n;
         if (k >= K) continue;
         float g_c, g_w, gd_c, gd_w;
-        basis_param_derivs(rp, k, d, C, dC, g_c, g_w, gd_c, gd_w);
+        basis_param_derivs(rp, cen[kt], wid[kt], d, C, dC, g_c, g_w, gd_c, gd_w);
         sc[kt] += gb[kt][i] * g_c + gdb[kt][i] * gd_c;
         sw[kt] += gb[kt][i] * g_w + gdb[kt][i] * gd_w;
       }

@@ -282,10 +282,10 @@ def test_fp16_filters_config4_full_size_vs_fp32():
     assert err < 2e-3
 
 
-def _filter_setup(n_frames=8, seed=11):
+def _filter_setup(n_frames=8, seed=11, num_rbf=50):
     from mlcg_amd import ops, synthetic
 
-    cfg = make_cfg(num_blocks=1, rc=20.0)
+    cfg = make_cfg(num_blocks=1, rc=20.0, num_rbf=num_rbf)
     sd = R.random_state_dict(cfg, seed=seed)
     b = synthetic.config2(n_frames=n_frames)
     pos = torch.from_numpy(b.pos).cuda()
@@ -295,12 +295,14 @@ def _filter_setup(n_frames=8, seed=11):
     return cfg, sd, b, pos, g, model.fused_spec(), model.fused_params().blocks[0]
 
 
-def test_filter_bwd_matches_autograd():
+@pytest.mark.parametrize("num_rbf", [50, 100])
+def test_filter_bwd_matches_autograd(num_rbf):
     """Parameter gradients of <Wbar, W> + <Wdbar, dW/dd> from the fused
-    backward kernel against fp64 autograd of the restated filter chain."""
+    backward kernel against fp64 autograd of the restated filter chain
+    (K <= 64 and the wide K <= 128 kernel variant)."""
     from mlcg_amd import ops
 
-    cfg, sd, b, pos, g, spec, blk = _filter_setup()
+    cfg, sd, b, pos, g, spec, blk = _filter_setup(num_rbf=num_rbf)
     P = g.num_pairs
     gen = torch.Generator(device="cuda").manual_seed(3)
     Wbar = torch.randn(P, 128, device="cuda", generator=gen)
@@ -326,12 +328,13 @@ def test_filter_bwd_matches_autograd():
     assert rel_err(dW2, gW2) < 1e-4
 
 
-def test_filter_bwd_cfconv_matches_explicit():
+@pytest.mark.parametrize("num_rbf", [50, 100])
+def test_filter_bwd_cfconv_matches_explicit(num_rbf):
     """The node-adjoint backward equals the explicit one with the adjoints
     formed in torch."""
     from mlcg_amd import ops
 
-    cfg, sd, b, pos, g, spec, blk = _filter_setup(n_frames=16, seed=12)
+    cfg, sd, b, pos, g, spec, blk = _filter_setup(n_frames=16, seed=12, num_rbf=num_rbf)
     N = pos.shape[0]
     gen = torch.Generator(device="cuda").manual_seed(5)
     g2, y, g1, yd = (torch.randn(N, 128, device="cuda", generator=gen) for _ in range(4))
@@ -350,4 +353,10 @@ def test_filter_bwd_cfconv_matches_explicit():
     got0 = ops.filter_bwd_cfconv(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, g2, y, None, None,
                                  None)
     for a, r in zip(got0, ref0):
+        assert rel_err(a, r) < 1e-5
+    # tangent stream without ydot (the first block, whose input has no tangent)
+    ref1 = ops.filter_bwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, Wbar0, Wdbar)
+    got1 = ops.filter_bwd_cfconv(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, g2, y, g1, None,
+                                 dd)
+    for a, r in zip(got1, ref1):
         assert rel_err(a, r) < 1e-5
