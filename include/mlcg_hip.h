@@ -139,9 +139,18 @@ int mlcg_pair_reverse_map(const int32_t* pair_ij, int64_t pair_stride,
  * W1 is [F, K] (torch Linear layout), b1 [F], W2 [F, F]; F must be 128 and
  * 1 <= K <= 128.  W_out/Wd_out are [max_pairs, F]; dist_out [max_pairs] is
  * optional.  act: 0 = tanh, 1 = shifted softplus.  cut kinds: 0 = identity,
- * 1 = cosine.  f16 != 0 selects the fp16-operand MFMA path (fp32
- * accumulate) and fp16 W_out/Wd_out storage.  Replaces CFConv.forward
- * lines 340-341 plus the basis/CosineCutoff/MLP (schnet.py:150,340-341). */
+ * 1 = cosine.  `f16` selects the arithmetic:
+ *   MLCG_FILTER_FP32 (0)        fp32 results; for K <= 64 the products run
+ *                               on the fp16 MFMA with every operand split
+ *                               into two fp16 parts (about 22 significant
+ *                               bits, fp32 accumulation), wider bases on the
+ *                               fp32 MFMA;
+ *   MLCG_FILTER_FP16 (1)        fp16 operands, fp32 accumulation, fp16
+ *                               W_out/Wd_out storage (the fp16 filter path);
+ *   MLCG_FILTER_FP32_STRICT (2) fp32 results from the fp32 MFMA throughout.
+ * Replaces CFConv.forward lines 340-341 plus the basis/CosineCutoff/MLP
+ * (schnet.py:150,340-341). */
+enum { MLCG_FILTER_FP32 = 0, MLCG_FILTER_FP16 = 1, MLCG_FILTER_FP32_STRICT = 2 };
 int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
                     int64_t pair_stride, const int32_t* n_pairs_dev,
                     int64_t max_pairs, int basis, const float* centers,

@@ -33,6 +33,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 
+#ifndef MLCG_FILTER_FWD_X3
+#define MLCG_FILTER_FWD_X3 1  // fp32-accurate forward on the fp16 MFMA (see filter_fwd_x3)
+#endif
 constexpr int kF = 128;          // number of filters (fixed by the MFMA tiling)
 constexpr int kFT = kF / 16;     // feature tiles of 16
 constexpr int kWaves = 8;        // waves per workgroup
@@ -423,6 +426,219 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
       if (dist_out && q == 0) dist_out[p] = d;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// fp32-accurate products on the fp16 MFMA (v_mfma_f32_16x16x32_f16).
+//
+// An fp32 operand x is carried as two fp16 parts, hi = fp16(x) and
+// lo = fp16((x - hi) S) with S = 2^e, which together hold about 22
+// significant bits.  A product A B (A = a weight matrix, B = per-pair data)
+// is accumulated in fp32 as
+//     S A B ~ (hi_A S) hi_B + hi_A lo_B + lo_A hi_B       (three MFMAs)
+// dropping only lo_A lo_B / S (2^-22 relative), and the accumulator is
+// divided by S afterwards.  The weights' three planes (hi, hi S, lo) are
+// staged in LDS once per workgroup, with e <= 11 chosen per workgroup and
+// per matrix from its largest entry so that hi S stays inside the fp16
+// range.  The per-pair operands (basis values, activations, their distance
+// derivatives) are required to stay below 2^15 in magnitude -- basis values
+// are at most 1 and the activations and derivatives of a trained filter are
+// of order one -- and a lane whose operand overflows yields a non-finite
+// filter value rather than a silently wrong one.  On this part the fp16 MFMA
+// issues at about 14 times the fp32 rate, so the three products cost about a
+// fifth of the fp32 ones.
+constexpr int kWavesX3 = 8;
+constexpr int kThreadsX3 = kWavesX3 * MLCG_WAVE;
+
+// Largest |v| over the workgroup (every thread must call; two barriers).
+__device__ float block_absmax(float v, float* red) {
+  v = fabsf(v);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MLCG_WAVE));
+  if (mlcg_lane() == 0) red[threadIdx.x / MLCG_WAVE] = v;
+  __syncthreads();
+  float m = 0.f;
+  for (int i = 0; i < (int)(blockDim.x / MLCG_WAVE); ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+// S = 2^e with e <= 11 and maxabs S < 2^14.
+__device__ __forceinline__ float x3_scale(float maxabs) {
+  int ex = 0;
+  (void)frexpf(maxabs, &ex);  // maxabs < 2^ex (ex = 0 for 0)
+  const int e = ex > 3 ? 14 - ex : 11;
+  return ldexpf(1.0f, e);
+}
+
+__device__ __forceinline__ void x3_store(_Float16* plane, int plane_stride, int idx, float v,
+                                         float S) {
+  const _Float16 h = (_Float16)v;
+  plane[idx] = h;
+  plane[plane_stride + idx] = (_Float16)((float)h * S);
+  plane[2 * plane_stride + idx] = (_Float16)((v - (float)h) * S);
+}
+
+__device__ __forceinline__ _Float16 x3_hi(float v) { return (_Float16)v; }
+__device__ __forceinline__ _Float16 x3_lo(float v, _Float16 hi, float S) {
+  return (_Float16)((v - (float)hi) * S);
+}
+
+// acc += S A B over one 32-wide k block from A's planes and B's parts.
+__device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, halfx8 bh,
+                                           halfx8 bl, floatx4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+  return acc;
+}
+
+// Filter forward, fp32-accurate, on the fp16 MFMA.  The operand layouts are
+// those of filter_fwd_f16_kernel (see stage_f16); W1 and W2 are staged as
+// three planes each.  One wave per 16-pair tile, 8 waves per workgroup.
+__global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ pi,
+    const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
+    int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
+    const float* __restrict__ b1, const float* __restrict__ W2, float* __restrict__ Wout,
+    float* __restrict__ Wdout, float* __restrict__ dist_out) {
+  extern __shared__ float lds[];
+  const int K = rp.K;
+  const int KS32 = (K + 31) / 32;
+  const int n1 = kFT * KS32 * MLCG_WAVE * 8;       // halfs per W1 plane
+  const int n2 = kFT * (kFT / 2) * MLCG_WAVE * 8;  // halfs per W2 plane
+  _Float16* w1p = reinterpret_cast<_Float16*>(lds);
+  _Float16* w2p = w1p + 3 * n1;
+  float* b1s = reinterpret_cast<float*>(w2p + 3 * n2);
+  float* bc = b1s + kF;
+  float* bw = bc + kMaxK;
+  float* red = bw + kMaxK;
+  // per-matrix scales from the largest weights
+  float m1 = 0.f, m2 = 0.f;
+  for (int x = threadIdx.x; x < kF * K; x += blockDim.x) m1 = fmaxf(m1, fabsf(W1[x]));
+  for (int x = threadIdx.x; x < kF * kF; x += blockDim.x) m2 = fmaxf(m2, fabsf(W2[x]));
+  const float S1 = x3_scale(block_absmax(m1, red));
+  const float S2 = x3_scale(block_absmax(m2, red));
+  for (int x = threadIdx.x; x < n1; x += blockDim.x) {
+    const int j = x & 7, l = (x >> 3) & 63, ts = x >> 9;
+    const int s = ts % KS32, t = ts / KS32;
+    const int k = 32 * s + 8 * (l >> 4) + j;
+    x3_store(w1p, n1, x, k < K ? W1[(16 * t + (l & 15)) * K + k] : 0.0f, S1);
+  }
+  for (int x = threadIdx.x; x < n2; x += blockDim.x) {
+    const int j = x & 7, l = (x >> 3) & 63, ts = x >> 9;
+    const int s = ts % (kFT / 2), t = ts / (kFT / 2);
+    const int c = 16 * (2 * s + (j >> 2)) + 4 * (l >> 4) + (j & 3);
+    x3_store(w2p, n2, x, W2[(16 * t + (l & 15)) * kF + c], S2);
+  }
+  for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
+  stage_basis(bc, bw, rp);
+  __syncthreads();
+
+  int64_t np = *n_pairs_dev;
+  if (np > max_pairs) np = max_pairs;
+  const int64_t tiles = (np + 15) / 16;
+  const int l = mlcg_lane();
+  const int q = l >> 4;
+  const float inv1 = 1.0f / S1, inv2 = 1.0f / S2;  // powers of two: exact
+
+  const halfx8* w1v = reinterpret_cast<const halfx8*>(w1p);
+  const halfx8* w2v = reinterpret_cast<const halfx8*>(w2p);
+  const int n1v = n1 / 8, n2v = n2 / 8;
+  const int64_t wave = (int64_t)blockIdx.x * kWavesX3 + threadIdx.x / MLCG_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesX3;
+  for (int64_t tile = wave; tile < tiles; tile += nwaves) {
+    const int64_t p = tile * 16 + (l & 15);
+    const bool valid = p < np;
+    const float d = pair_distance(pos, pi, pj, p, valid);
+    float crbf, dcrbf, cc, dcc;
+    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+
+    // 1. a = W1 g, a' = W1 g' (times S1)
+    floatx4 a[kFT], ad[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      a[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      ad[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s = 0; s < KS32; ++s) {
+      halfx8 gh, gl, gdh, gdl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float g, gd;
+        const int k = 32 * s + 8 * q + j;
+        rbf_eval(rp, k < K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
+        gh[j] = x3_hi(g);
+        gl[j] = x3_lo(g, gh[j], S1);
+        gdh[j] = x3_hi(gd);
+        gdl[j] = x3_lo(gd, gdh[j], S1);
+      }
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        const int o = (t * KS32 + s) * MLCG_WAVE + l;
+        const halfx8 ah = w1v[o], ahs = w1v[n1v + o], al = w1v[2 * n1v + o];
+        a[t] = mfma_x3(ah, ahs, al, gh, gl, a[t]);
+        ad[t] = mfma_x3(ah, ahs, al, gdh, gdl, ad[t]);
+      }
+    }
+    // 2. h = act(a + b1), h' = act'(a + b1) a', split for the second product
+    halfx8 hh[kFT / 2], hl[kFT / 2], hdh[kFT / 2], hdl[kFT / 2];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float sv, d1, d2;
+        mlcg_act(rp.act, a[t][i] * inv1 + b1s[16 * t + 4 * q + i], sv, d1, d2);
+        const int e = 4 * (t & 1) + i;
+        const float hd = d1 * (ad[t][i] * inv1);
+        hh[t >> 1][e] = x3_hi(sv);
+        hl[t >> 1][e] = x3_lo(sv, hh[t >> 1][e], S2);
+        hdh[t >> 1][e] = x3_hi(hd);
+        hdl[t >> 1][e] = x3_lo(hd, hdh[t >> 1][e], S2);
+      }
+    // 3. w = W2 h, w' = W2 h' (times S2)
+    floatx4 w[kFT], wd[kFT];
+#pragma unroll
+    for (int t = 0; t < kFT; ++t) {
+      w[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      wd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int s = 0; s < kFT / 2; ++s)
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        const int o = (t * (kFT / 2) + s) * MLCG_WAVE + l;
+        const halfx8 ah = w2v[o], ahs = w2v[n2v + o], al = w2v[2 * n2v + o];
+        w[t] = mfma_x3(ah, ahs, al, hh[s], hl[s], w[t]);
+        wd[t] = mfma_x3(ah, ahs, al, hdh[s], hdl[s], wd[t]);
+      }
+    if (valid) {
+      float* wr = Wout + p * kF + 4 * q;
+      float* wdr = Wdout + p * kF + 4 * q;
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        float4 o, od;
+        float* op = reinterpret_cast<float*>(&o);
+        float* odp = reinterpret_cast<float*>(&od);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float wv = w[t][i] * inv2, wdv = wd[t][i] * inv2;
+          op[i] = wv * cc;
+          odp[i] = wdv * cc + wv * dcc;
+        }
+        *reinterpret_cast<float4*>(wr + 16 * t) = o;
+        *reinterpret_cast<float4*>(wdr + 16 * t) = od;
+      }
+      if (dist_out && q == 0) dist_out[p] = d;
+    }
+  }
+}
+
+size_t fwd_x3_lds_bytes(int K) {
+  const int KS32 = (K + 31) / 32;
+  return sizeof(_Float16) * 3 * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
+         sizeof(float) * (kF + 2 * kMaxK + kWavesX3);
 }
 
 // ---------------------------------------------------------------------------
@@ -934,6 +1150,8 @@ void allow_lds_once() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, false>),
@@ -988,7 +1206,17 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
                              rbf_hi, conv_cut_kind, conv_lo, conv_hi, act);
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves), 1);
   hipStream_t s = mlcg_stream(stream);
-  if (!f16) {
+  MLCG_REQUIRE(f16 == MLCG_FILTER_FP32 || f16 == MLCG_FILTER_FP16 ||
+               f16 == MLCG_FILTER_FP32_STRICT);
+  if (f16 == MLCG_FILTER_FP32 && MLCG_FILTER_FWD_X3 &&
+      fwd_x3_lds_bytes(num_rbf) <= 160 * 1024) {  // K <= 64
+    const size_t lds = fwd_x3_lds_bytes(num_rbf);
+    allow_lds_once();
+    const unsigned gx = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWavesX3), 1);
+    hipLaunchKernelGGL(filter_fwd_x3_kernel, dim3(gx), dim3(kThreadsX3), lds, s, pos, pair_ij,
+                       pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
+                       static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out);
+  } else if (f16 != MLCG_FILTER_FP16) {
     const int KS = (num_rbf + 3) / 4;
     const size_t lds =
         sizeof(float) * (kFT * KS * MLCG_WAVE + kFT * kFT * MLCG_WAVE * 4 + 2 * kMaxK);

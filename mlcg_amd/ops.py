@@ -463,10 +463,17 @@ class FilterSpec:
 BASIS_GAUSSIAN, BASIS_EXPNORMAL = 0, 1
 
 
+FILTER_FP32, FILTER_FP16, FILTER_FP32_STRICT = 0, 1, 2
+
+
 def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
                b1: torch.Tensor, W2: torch.Tensor, f16: bool = False,
-               want_dist: bool = True) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """W [P, F], dW/dd [P, F] (fp32, or fp16 when f16) and distances [P]."""
+               want_dist: bool = True, strict_fp32: bool = False,
+               ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """W [P, F], dW/dd [P, F] (fp32, or fp16 when f16) and distances [P].
+    fp32 results come from split-fp16 products (about 22 significant bits
+    per operand, fp32 accumulation) unless strict_fp32 asks for the fp32
+    MFMA throughout (mlcg_filter_fwd's FP32_STRICT mode)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     _check(F == NUM_FILTERS, f"num_filters must be {NUM_FILTERS} for the HIP filter kernel")
@@ -481,8 +488,9 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     call("mlcg_filter_fwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
          *spec.basis_args(), spec.num_rbf, spec.rbf_cut_kind, spec.rbf_lo,
          spec.rbf_hi, spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c),
-         ptr(b1c), ptr(W2c), F, int(f16), ptr(W), ptr(Wd), ptr(dist),
-         stream_handle(pos.device))
+         ptr(b1c), ptr(W2c), F,
+         FILTER_FP16 if f16 else (FILTER_FP32_STRICT if strict_fp32 else FILTER_FP32),
+         ptr(W), ptr(Wd), ptr(dist), stream_handle(pos.device))
     return W, Wd, dist
 
 

@@ -35,10 +35,13 @@ def _oracle_inputs(b, rc, dtype=torch.float64):
             torch.from_numpy(b.batch), torch.from_numpy(ei))
 
 
-def test_filter_kernel_matches_torch():
+@pytest.mark.parametrize("num_rbf", [50, 100])
+def test_filter_kernel_matches_torch(num_rbf):
+    """The filter forward (K <= 64: products on the fp16 MFMA with split
+    operands; wider bases: fp32 MFMA) against fp64 torch."""
     from mlcg_amd import ops, synthetic
 
-    cfg = make_cfg(num_blocks=1, rc=20.0)
+    cfg = make_cfg(num_blocks=1, rc=20.0, num_rbf=num_rbf)
     sd = R.random_state_dict(cfg, seed=11)
     b = synthetic.config2(n_frames=8)
     pos = torch.from_numpy(b.pos).cuda()
@@ -48,6 +51,7 @@ def test_filter_kernel_matches_torch():
     spec = model.fused_spec()
     blk = model.fused_params().blocks[0]
     W, Wd, dist = ops.filter_fwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2)
+    Ws, Wds, _ = ops.filter_fwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, strict_fp32=True)
     # fp64 torch reference on the same pairs
     pij = g.pair_ij.long().cpu()
     p64 = torch.from_numpy(b.pos).double()
@@ -61,8 +65,11 @@ def test_filter_kernel_matches_torch():
                        for f in range(128)], dim=1)
     print("W rel", rel_err(W, Wr), "Wd rel", rel_err(Wd, Wdr),
           "dist", max_abs(dist, d.detach()))
+    print("strict fp32: W rel", rel_err(Ws, Wr), "Wd rel", rel_err(Wds, Wdr))
     assert rel_err(W, Wr.detach()) < 1e-5
     assert rel_err(Wd, Wdr) < 1e-5
+    assert rel_err(Ws, Wr.detach()) < 1e-5
+    assert rel_err(Wds, Wdr) < 1e-5
     assert max_abs(dist, d.detach()) < 1e-5
 
 
