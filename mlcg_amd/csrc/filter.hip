@@ -471,6 +471,14 @@ __device__ __forceinline__ float x3_scale(float maxabs) {
   return ldexpf(1.0f, e);
 }
 
+// sigma = 2^k with m sigma < 4: brings values of magnitude <= m into the
+// range the split planes of an adjoint operand expect.
+__device__ __forceinline__ float x3_norm(float m) {
+  int ex = 0;
+  (void)frexpf(m, &ex);  // m < 2^ex (ex = 0 for 0)
+  return ldexpf(1.0f, 2 - ex);
+}
+
 __device__ __forceinline__ void x3_store(_Float16* plane, int plane_stride, int idx, float v,
                                          float S) {
   const _Float16 h = (_Float16)v;
@@ -699,11 +707,15 @@ __host__ __device__ constexpr int bwd_partial_floats(int K) {
   return kF * kF + kF * bwd_kp16(K) + kF;
 }
 __host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
-// LDS: W2^T fragments [8][8][64] float4 | TB [2][16][128] | TT, HT, AT
-//      [2][128][16] | GT [2 buffers][2][krows][16]; 147,456 bytes for K <= 64
-//      and exactly the 160 KiB of a gfx950 CU for K <= 128
+// LDS: W2^T fragments [8][8][64] float4 (or two fp16 planes) | TB [2][16][128]
+//      (or three fp16 planes) | TT, HT, AT [2][128][16] | GT [2 buffers][2]
+//      [krows][16] | per-pair maxima [2][8][16] (split path); 156,672 bytes for
+//      K <= 64 and exactly the 160 KiB of a gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
-  return kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 3 * 2 * kF * 16 + 2 * 2 * bwd_krows(K) * 16;
+  return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 3 * 2 * kF * 16 +
+                       2 * 2 * bwd_krows(K) * 16 + 2 * kBwdWaves * 16
+                 : kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 3 * 2 * kF * 16 +
+                       2 * 2 * bwd_krows(K) * 16;
 }
 
 // Where the pair adjoints (Wbar, Wdbar) come from: explicit [P, F] arrays, or
@@ -816,17 +828,43 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   const int K = rp.K;
   const int Kp16 = bwd_kp16(K);
   const int KT = Kp16 / 16;
-  float* w2ts = lds;                                  // [8 t][8 u][64 l] float4
-  float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;       // [2][16 pairs][128]  t, t'
-  float* TT = TB + 2 * 16 * kF;                       // [2][128][16 pairs]  t, t'
+  // step 3 on the fp16 MFMA with split operands (see filter_fwd_x3_kernel)
+  // when the LDS allows it (K <= 64); the wide variant keeps it on fp32
+  constexpr bool kX3 = KSMAX <= 16;
+  // fp32: W2^T A fragments [8 t][8 u][64 l] float4; x3: W2^T as two fp16
+  // planes (hi, lo S) of [8 t][4 s][64 l][8]
+  float* w2ts = lds;
+  // fp32: [2][16 pairs][128] t, t'; x3: three fp16 planes (hi, hi S, lo S)
+  // of [2][16 pairs][128], each t scaled per pair (sigma) into [-4, 4]
+  float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;
+  float* TT = TB + (kX3 ? 3 * 16 * kF : 2 * 16 * kF);  // [2][128][16 pairs]  t, t'
   float* HT = TT + 2 * kF * 16;                       // [2][128][16 pairs]  h, h'
   float* AT = HT + 2 * kF * 16;                       // [2][128][16 pairs]  ab, ab'
   float* GT0 = AT + 2 * kF * 16;                      // [2 bufs][2][kRows][16]  g, g'
+  float* PMAX = GT0 + 2 * 2 * kRows * 16;             // x3: [2][8 waves][16 pairs] max |t|
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
 
-  stage_w2_f32(w2ts, W2, true);
+  float S = 1.0f;  // x3: the split scale of W2 and t
+  if constexpr (kX3) {
+    float m2 = 0.f;
+    for (int x = threadIdx.x; x < kF * kF; x += blockDim.x) m2 = fmaxf(m2, fabsf(W2[x]));
+    S = x3_scale(block_absmax(m2, PMAX));
+    _Float16* w2h = reinterpret_cast<_Float16*>(w2ts);
+    constexpr int kPlane = kF * kF;
+    for (int x = threadIdx.x; x < kPlane; x += blockDim.x) {
+      // A[m][8 kq + j] of block s for tile t = W2[32 s + 8 kq + j][16 t + m]
+      const int j = x & 7, ll = (x >> 3) & 63, ts = x >> 9;
+      const int sb = ts & 3, t = ts >> 2;
+      const float v = W2[(32 * sb + 8 * (ll >> 4) + j) * kF + 16 * t + (ll & 15)];
+      const _Float16 h = (_Float16)v;
+      w2h[x] = h;
+      w2h[kPlane + x] = (_Float16)((v - (float)h) * S);
+    }
+  } else {
+    stage_w2_f32(w2ts, W2, true);
+  }
 
   // W1 fragment of feature tile w stays in registers: W1[16w + n][4s + q]
   float w1f[KSMAX];
@@ -908,24 +946,55 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
   };
 
+  // t, t' of the lane's 4 features of a tile (formed one tile ahead, in the
+  // barrier interval of step 5) and, on the split path, the per-pair maxima
+  // of |t|, |t'| over the wave's 16 features, published for step 2
+  float tbv[4], tdbv[4];
+  auto pair_adjoints = [&](float4 wb, float4 wdb, float cc, float dcc) {
+    const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
+    const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
+    float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tbv[i] = wbv[i] * cc + wdbv[i] * dcc;
+      tdbv[i] = wdbv[i] * cc;
+      m0 = fmaxf(m0, fabsf(tbv[i]));
+      m1 = fmaxf(m1, fabsf(tdbv[i]));
+    }
+    if constexpr (kX3) {
+      m0 = fmaxf(m0, __shfl_xor(m0, 16, MLCG_WAVE));
+      m0 = fmaxf(m0, __shfl_xor(m0, 32, MLCG_WAVE));
+      m1 = fmaxf(m1, __shfl_xor(m1, 16, MLCG_WAVE));
+      m1 = fmaxf(m1, __shfl_xor(m1, 32, MLCG_WAVE));
+      if (q == 0) {
+        PMAX[w * 16 + n] = m0;
+        PMAX[(kBwdWaves + w) * 16 + n] = m1;
+      }
+    }
+  };
+
   int buf = 0;
-  TileIn cur;
   float cc_cur = 0.f, dcc_cur = 0.f;
   int64_t ni = 0, nj = 0;  // bead indices of the next tile's pair
+  __syncthreads();  // PMAX served as scratch of the W2 scale
   if (np > 0) {  // uniform across the workgroup
     const int64_t p0 = clamp_pair(blockIdx.x);
-    cur = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, p0, pi[p0], pj[p0], fcol);
+    const TileIn first = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, p0, pi[p0], pj[p0], fcol);
     const int64_t p1 = clamp_pair((int64_t)blockIdx.x + gridDim.x);
     ni = pi[p1];
     nj = pj[p1];
-    basis(cur, (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f, GT0, cc_cur, dcc_cur);
+    const float vm0 = (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f;
+    basis(first, vm0, GT0, cc_cur, dcc_cur);
+    float4 wb0, wdb0;
+    tile_adjoint<kNodes>(first, tangent, has_yd, vm0, wb0, wdb0);
+    pair_adjoints(wb0, wdb0, cc_cur, dcc_cur);
   }
   __syncthreads();
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
     float* GT = GT0 + buf * 2 * kRows * 16;
     const float vmask = tile * 16 + n < np ? 1.0f : 0.0f;
-    // inputs of the next tile and indices of the one after it: consumed one
-    // tile later
+    // inputs of the next tile and indices of the one after it: consumed in
+    // step 5 and one tile later
     const int64_t pn = clamp_pair(tile + gridDim.x);
     const TileIn nxt = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, pn, ni, nj, fcol);
     {
@@ -933,8 +1002,6 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       ni = pi[pnn];
       nj = pj[pnn];
     }
-    float4 wb, wdb;
-    tile_adjoint<kNodes>(cur, tangent, has_yd, vmask, wb, wdb);
 
     // 1. a, a' of feature tile w (two accumulators each: shorter MFMA chains)
     floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
@@ -954,12 +1021,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     a += a_o;
     ad += ad_o;
-    // 2. h, h', activation derivatives and t, t' of the lane's 4 features
-    const float cc = cc_cur, dcc = dcc_cur;
+    // 2. h, h', activation derivatives; publish t, t', h, h'
     float act1[4], act2[4];
-    float hv[4], hdv[4], tb[4], tdb[4];
-    const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
-    const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
+    float hv[4], hdv[4];
+    const float* tb = tbv;
+    const float* tdb = tdbv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float sv, d1, d2;
@@ -968,11 +1034,43 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       act2[i] = d2 * ad[i];
       hv[i] = sv * vmask;
       hdv[i] = d1 * ad[i] * vmask;
-      tb[i] = wbv[i] * cc + wdbv[i] * dcc;
-      tdb[i] = wdbv[i] * cc;
     }
-    *reinterpret_cast<float4*>(TB + oTBw) = f4(tb[0], tb[1], tb[2], tb[3]);
-    *reinterpret_cast<float4*>(TB + 16 * kF + oTBw) = f4(tdb[0], tdb[1], tdb[2], tdb[3]);
+    float inv_t = 1.0f, inv_td = 1.0f;  // x3: 1 / (S sigma) of the lane's pair
+    if constexpr (kX3) {
+      float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+      for (int v = 0; v < kBwdWaves; ++v) {
+        m0 = fmaxf(m0, PMAX[v * 16 + n]);
+        m1 = fmaxf(m1, PMAX[(kBwdWaves + v) * 16 + n]);
+      }
+      const float sg0 = x3_norm(m0), sg1 = x3_norm(m1);
+      inv_t = 1.0f / (S * sg0);
+      inv_td = 1.0f / (S * sg1);
+      // three planes (hi, hi S, lo S) of t sigma; float4 group g of pair n's
+      // row (8 halfs) at g ^ (n & 7)
+      _Float16* TBh = reinterpret_cast<_Float16*>(TB);
+      const int o = n * kF + 8 * ((2 * w + (q >> 1)) ^ (n & 7)) + 4 * (q & 1);
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const float sg = st ? sg1 : sg0;
+        const float* src = st ? tdb : tb;
+        halfx4 ph, phs, pl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = src[i] * sg;
+          const _Float16 h = (_Float16)v;
+          ph[i] = h;
+          phs[i] = (_Float16)((float)h * S);
+          pl[i] = (_Float16)((v - (float)h) * S);
+        }
+        *reinterpret_cast<halfx4*>(TBh + (0 * 2 + st) * 16 * kF + o) = ph;
+        *reinterpret_cast<halfx4*>(TBh + (1 * 2 + st) * 16 * kF + o) = phs;
+        *reinterpret_cast<halfx4*>(TBh + (2 * 2 + st) * 16 * kF + o) = pl;
+      }
+    } else {
+      *reinterpret_cast<float4*>(TB + oTBw) = f4(tb[0], tb[1], tb[2], tb[3]);
+      *reinterpret_cast<float4*>(TB + 16 * kF + oTBw) = f4(tdb[0], tdb[1], tdb[2], tdb[3]);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       TT[oW[i]] = tb[i];
@@ -982,9 +1080,36 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     __syncthreads();
 
-    // 3. hb, hb' of feature tile w (all 128 t features from LDS), four chains
+    // 3. hb, hb' of feature tile w (all 128 t features from LDS)
     floatx4 hb = {0.f, 0.f, 0.f, 0.f}, hdb = {0.f, 0.f, 0.f, 0.f};
     floatx4 hb_o = {0.f, 0.f, 0.f, 0.f}, hdb_o = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kX3) {
+      // S sigma W2^T t in 4 k blocks of 32 features, three fp16 MFMAs each
+      const halfx8* w2hv = reinterpret_cast<const halfx8*>(w2ts);
+      const halfx8* tbh = reinterpret_cast<const halfx8*>(TB);
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        const int oa = (w * 4 + sb) * MLCG_WAVE + l;
+        const halfx8 ah = w2hv[oa], al = w2hv[kF * kF / 8 + oa];
+        const int ob = (n * kF + 8 * ((4 * sb + q) ^ (n & 7))) / 8;
+        constexpr int kP = 16 * kF / 8;  // halfx8 per (plane, stream)
+        // planes of t: (hi, hi S, lo S) at (0, 2, 4) kP, of t' at (1, 3, 5) kP;
+        // S sigma A t ~ hi_A (hi_t S) + hi_A (lo_t S) + (lo_A S) hi_t
+        const halfx8 t0h = tbh[ob], t0s = tbh[2 * kP + ob], t0l = tbh[4 * kP + ob];
+        const halfx8 t1h = tbh[kP + ob], t1s = tbh[3 * kP + ob], t1l = tbh[5 * kP + ob];
+        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t0s, hb, 0, 0, 0);
+        hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t1s, hdb, 0, 0, 0);
+        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t0l, hb, 0, 0, 0);
+        hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t1l, hdb, 0, 0, 0);
+        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, t0h, hb, 0, 0, 0);
+        hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, t1h, hdb, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hb[i] *= inv_t;
+        hdb[i] *= inv_td;
+      }
+    } else {
 #pragma unroll
     for (int u = 0; u < kFT; ++u) {
       const float4 a2 = w2v[u * MLCG_WAVE];
@@ -1002,6 +1127,12 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     hb += hb_o;
     hdb += hdb_o;
+    }
+    // the next tile's pair adjoints from its node vectors (requested at the
+    // start of this tile), early so that their registers are free for step 4
+    const float vm_nxt = (tile + gridDim.x) * 16 + n < np ? 1.0f : 0.0f;
+    float4 wb_nxt, wdb_nxt;
+    tile_adjoint<kNodes>(nxt, tangent, has_yd, vm_nxt, wb_nxt, wdb_nxt);
     float abv[4], adbv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1038,9 +1169,8 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) =
           f4(adbv[0], adbv[1], adbv[2], adbv[3]);
     }
-    float cc_nxt, dcc_nxt;
-    basis(nxt, (tile + gridDim.x) * 16 + n < np ? 1.0f : 0.0f,
-          GT0 + (buf ^ 1) * 2 * kRows * 16, cc_nxt, dcc_nxt);
+    basis(nxt, vm_nxt, GT0 + (buf ^ 1) * 2 * kRows * 16, cc_cur, dcc_cur);
+    pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
 #pragma unroll
@@ -1057,9 +1187,6 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc1[kt], 0, 0, 0);
       }
     }
-    cur = nxt;
-    cc_cur = cc_nxt;
-    dcc_cur = dcc_nxt;
   }
 
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
