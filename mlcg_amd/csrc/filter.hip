@@ -913,6 +913,13 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) oW[i] = rp_at(fcol + i, n);
   const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
+  // step 4 on the split path: A = TT row 16w + n, stream q >> 1, pairs
+  // 8 (q & 1) .. + 7 (two float4, the second at offset ^ 4); B = halfx8 of HT
+  // plane rows 16u + (n ^ (n >> 2)), same stream and pairs
+  // split scales of step 4: t rw (rw = 2^k, with |t| rw < 4 over every tile
+  // seen so far), h beta; the accumulators hold S4 rw beta dW2
+  constexpr float kS4 = 2048.0f, kBetaH = 0.0625f;
+  float rw = 1.0f, trun = 0.0f;
 
   const bool tangent = kNodes && adj.g1 != nullptr;
   const bool has_yd = tangent && adj.yd != nullptr;
@@ -950,6 +957,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // barrier interval of step 5) and, on the split path, the per-pair maxima
   // of |t|, |t'| over the wave's 16 features, published for step 2
   float tbv[4], tdbv[4];
+  float tmax_tile = 0.f;  // split path: max |t|, |t'| over the wave's features and pairs
   auto pair_adjoints = [&](float4 wb, float4 wdb, float cc, float dcc) {
     const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
     const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
@@ -970,6 +978,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         PMAX[w * 16 + n] = m0;
         PMAX[(kBwdWaves + w) * 16 + n] = m1;
       }
+      float mx = fmaxf(m0, m1);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, MLCG_WAVE));
+      tmax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
     }
   };
 
@@ -1035,6 +1047,27 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       hv[i] = sv * vmask;
       hdv[i] = d1 * ad[i] * vmask;
     }
+    if constexpr (kX3) {
+      // h beta, h' beta as two fp16 planes (hi, lo S4) of [2][128 rows][16
+      // pairs]; row 4q + i of a 16-row block stored at 4q + (i ^ q)
+      _Float16* HTh = reinterpret_cast<_Float16*>(HT);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int o = (16 * w + 4 * q + (i ^ q)) * 16 + n;
+        const float v0 = hv[i] * kBetaH, v1 = hdv[i] * kBetaH;
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        HTh[o] = h0;
+        HTh[kF * 16 + o] = h1;
+        HTh[2 * kF * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
+        HTh[3 * kF * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        HT[oW[i]] = hv[i];
+        HT[kF * 16 + oW[i]] = hdv[i];
+      }
+    }
     float inv_t = 1.0f, inv_td = 1.0f;  // x3: 1 / (S sigma) of the lane's pair
     if constexpr (kX3) {
       float m0 = 0.f, m1 = 0.f;
@@ -1075,8 +1108,6 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     for (int i = 0; i < 4; ++i) {
       TT[oW[i]] = tb[i];
       TT[kF * 16 + oW[i]] = tdb[i];
-      HT[oW[i]] = hv[i];
-      HT[kF * 16 + oW[i]] = hdv[i];
     }
     __syncthreads();
 
@@ -1140,7 +1171,42 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       adbv[i] = hdb[i] * act1[i];
       db[i] += abv[i];
     }
-    // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c];
+    // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c]
+    if constexpr (kX3) {
+      // fp16 MFMA, k = 32 = (stream, pair): lane group q holds stream q >> 1,
+      // pairs 8 (q & 1) .. + 7.  A = t rw split when read, B = h beta
+      if (tmax_tile > trun) {  // wave-uniform; the running scale only shrinks
+        const float rn =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x3_norm(tmax_tile))));
+        const float f = rn / rw;
+#pragma unroll
+        for (int u = 0; u < kFT; ++u) acc2[u] *= f;
+        rw = rn;
+        trun = tmax_tile;
+      }
+      const int oA4 = (q >> 1) * kF * 16 + rp_at(16 * w + n, 8 * (q & 1));
+      const int oB4 = (q >> 1) * 2 * kF + 2 * (n ^ (n >> 2)) + (q & 1);
+      const float4 x0 = *reinterpret_cast<const float4*>(TT + oA4);
+      const float4 x1 = *reinterpret_cast<const float4*>(TT + (oA4 ^ 4));
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      halfx8 ah, ahs, al;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float s = xv[j] * rw;
+        const _Float16 h = (_Float16)s;
+        ah[j] = h;
+        ahs[j] = (_Float16)((float)h * kS4);
+        al[j] = (_Float16)((s - (float)h) * kS4);
+      }
+      const halfx8* hth = reinterpret_cast<const halfx8*>(HT);
+#pragma unroll
+      for (int u = 0; u < kFT; ++u) {
+        const halfx8 bh = hth[oB4 + 32 * u], bl = hth[oB4 + 2 * kF * 16 / 8 + 32 * u];
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh, acc2[u], 0, 0, 0);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc2[u], 0, 0, 0);
+        acc2[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc2[u], 0, 0, 0);
+      }
+    } else {
     //    MFMA step kk of lane group q reduces over pair 4q + kk
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -1155,6 +1221,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc2[u], 0, 0, 0);
         acc2[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc2[u], 0, 0, 0);
       }
+    }
     }
     // 5. publish ab, ab' (and store them per pair when the basis parameters
     //    need gradients) and the next tile's basis
@@ -1189,6 +1256,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
   }
 
+  if constexpr (kX3) {
+    const float f = 1.0f / (kS4 * rw * kBetaH);
+#pragma unroll
+    for (int u = 0; u < kFT; ++u) acc2[u] *= f;
+  }
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
   float* out = partial + (int64_t)blockIdx.x * bwd_partial_floats(K);
 #pragma unroll

@@ -315,6 +315,16 @@ def test_filter_bwd_matches_autograd(num_rbf):
     Wbar = torch.randn(P, 128, device="cuda", generator=gen)
     Wdbar = torch.randn(P, 128, device="cuda", generator=gen)
     dW1, db1, dW2 = ops.filter_bwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, Wbar, Wdbar)
+    gW1, gb1, gW2 = _filter_bwd_ref(sd, b, g, Wbar, Wdbar)
+    print("dW1", rel_err(dW1, gW1), "db1", rel_err(db1, gb1), "dW2", rel_err(dW2, gW2))
+    assert rel_err(dW1, gW1) < 1e-4
+    assert rel_err(db1, gb1) < 1e-4
+    assert rel_err(dW2, gW2) < 1e-4
+
+
+def _filter_bwd_ref(sd, b, g, Wbar, Wdbar):
+    """fp64 autograd of <Wbar, W> + <Wdbar, dW/dd> through the restated
+    filter chain (Gaussian basis, tanh, cosine cutoffs at 20)."""
     pij = g.pair_ij.long().cpu()
     p64 = torch.from_numpy(b.pos).double()
     d = (p64[pij[1]] - p64[pij[0]]).norm(dim=1).requires_grad_(True)
@@ -329,7 +339,26 @@ def test_filter_bwd_matches_autograd(num_rbf):
     # dW/dd contracted with Wdbar: d/dd of <Wdbar, W> per pair
     wd_term, = torch.autograd.grad((Wr * Wdbar.double().cpu()).sum(), d, create_graph=True)
     obj = (Wr * Wbar.double().cpu()).sum() + wd_term.sum()
-    gW1, gb1, gW2 = torch.autograd.grad(obj, [lay[0]["weight"], lay[0]["bias"], lay[1]["weight"]])
+    return torch.autograd.grad(obj, [lay[0]["weight"], lay[0]["bias"], lay[1]["weight"]])
+
+
+def test_filter_bwd_adjoint_dynamic_range():
+    """Adjoints whose size grows by 10^6 along the pair list, after a run of
+    all-zero tiles: every workgroup meets a larger maximum on most of its
+    tiles, so the split-operand pair reductions rescale their accumulators
+    many times; the gradients still match fp64 autograd."""
+    from mlcg_amd import ops
+
+    cfg, sd, b, pos, g, spec, blk = _filter_setup(n_frames=64, seed=13)
+    P = g.num_pairs
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    ramp = torch.pow(10.0, torch.linspace(-4.0, 2.0, P, device="cuda"))
+    ramp[: 16 * 300] = 0.0
+    Wbar = torch.randn(P, 128, device="cuda", generator=gen) * ramp[:, None]
+    Wdbar = torch.randn(P, 128, device="cuda", generator=gen) * ramp[:, None]
+    dW1, db1, dW2 = ops.filter_bwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, Wbar, Wdbar)
+    gW1, gb1, gW2 = _filter_bwd_ref(sd, b, g, Wbar, Wdbar)
+    print("P", P, "dW1", rel_err(dW1, gW1), "db1", rel_err(db1, gb1), "dW2", rel_err(dW2, gW2))
     assert rel_err(dW1, gW1) < 1e-4
     assert rel_err(db1, gb1) < 1e-4
     assert rel_err(dW2, gW2) < 1e-4
