@@ -24,14 +24,11 @@
 // derivative Wd = dW/dd by pushing the tangent g' = dg/dd through the same
 // chain (a second accumulator set sharing every A fragment).
 #include "common.h"
+#include "split16.h"
 
 #include <hip/hip_fp16.h>
 
 namespace {
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
-typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 
 #ifndef MLCG_FILTER_FWD_X3
 #define MLCG_FILTER_FWD_X3 1  // fp32-accurate forward on the fp16 MFMA (see filter_fwd_x3)
@@ -471,14 +468,6 @@ __device__ __forceinline__ float x3_scale(float maxabs) {
   return ldexpf(1.0f, e);
 }
 
-// sigma = 2^k with m sigma < 4: brings values of magnitude <= m into the
-// range the split planes of an adjoint operand expect.
-__device__ __forceinline__ float x3_norm(float m) {
-  int ex = 0;
-  (void)frexpf(m, &ex);  // m < 2^ex (ex = 0 for 0)
-  return ldexpf(1.0f, 2 - ex);
-}
-
 __device__ __forceinline__ void x3_store(_Float16* plane, int plane_stride, int idx, float v,
                                          float S) {
   const _Float16 h = (_Float16)v;
@@ -846,11 +835,12 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
 
-  float S = 1.0f;  // x3: the split scale of W2 and t
+  float S = 1.0f, inv_S = 1.0f;  // x3: the split scale of W2 and t
   if constexpr (kX3) {
     float m2 = 0.f;
     for (int x = threadIdx.x; x < kF * kF; x += blockDim.x) m2 = fmaxf(m2, fabsf(W2[x]));
     S = x3_scale(block_absmax(m2, PMAX));
+    inv_S = 1.0f / S;
     _Float16* w2h = reinterpret_cast<_Float16*>(w2ts);
     constexpr int kPlane = kF * kF;
     for (int x = threadIdx.x; x < kPlane; x += blockDim.x) {
@@ -920,6 +910,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // seen so far), h beta; the accumulators hold S4 rw beta dW2
   constexpr float kS4 = 2048.0f, kBetaH = 0.0625f;
   float rw = 1.0f, trun = 0.0f;
+  float ra = 1.0f, arun = 0.0f;  // the same for ab in step 6 (no beta: |g| <= 1)
 
   const bool tangent = kNodes && adj.g1 != nullptr;
   const bool has_yd = tangent && adj.yd != nullptr;
@@ -945,9 +936,21 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         float g, gd, cen = bcen[e], wid = bwid[e];
         if (!kBasisRegs) basis_params(rp, 4 * s + q, cen, wid);
         rbf_eval(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
-        const int o = rp_at(4 * s + q, n);
-        GTb[o] = g * vm;
-        GTb[kRows * 16 + o] = gd * vm;
+        if constexpr (kX3) {
+          // two fp16 planes (hi, lo S4) of [2][kRows][16 pairs]
+          _Float16* GTh = reinterpret_cast<_Float16*>(GTb);
+          const int o = (4 * s + q) * 16 + n;
+          const float v0 = g * vm, v1 = gd * vm;
+          const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+          GTh[o] = h0;
+          GTh[kRows * 16 + o] = h1;
+          GTh[2 * kRows * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
+          GTh[3 * kRows * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
+        } else {
+          const int o = rp_at(4 * s + q, n);
+          GTb[o] = g * vm;
+          GTb[kRows * 16 + o] = gd * vm;
+        }
       }
     }
     mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
@@ -970,17 +973,13 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       m1 = fmaxf(m1, fabsf(tdbv[i]));
     }
     if constexpr (kX3) {
-      m0 = fmaxf(m0, __shfl_xor(m0, 16, MLCG_WAVE));
-      m0 = fmaxf(m0, __shfl_xor(m0, 32, MLCG_WAVE));
-      m1 = fmaxf(m1, __shfl_xor(m1, 16, MLCG_WAVE));
-      m1 = fmaxf(m1, __shfl_xor(m1, 32, MLCG_WAVE));
+      m0 = cross_row_max(m0);
+      m1 = cross_row_max(m1);
       if (q == 0) {
         PMAX[w * 16 + n] = m0;
         PMAX[(kBwdWaves + w) * 16 + n] = m1;
       }
-      float mx = fmaxf(m0, m1);
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, MLCG_WAVE));
+      const float mx = row16_max(fmaxf(m0, m1));
       tmax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
     }
   };
@@ -1020,9 +1019,17 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSMAX; ++s) {
-      const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
-      const float g = GT[o];
-      const float gd = GT[kRows * 16 + o];
+      float g, gd;
+      if constexpr (kX3) {  // hi + lo / S4 of the two planes
+        const _Float16* GTh = reinterpret_cast<const _Float16*>(GT);
+        const int o = 16 * q + n + 64 * s;  // (4s + q) * 16 + n
+        g = (float)GTh[2 * kRows * 16 + o] * (1.0f / kS4) + (float)GTh[o];
+        gd = (float)GTh[3 * kRows * 16 + o] * (1.0f / kS4) + (float)GTh[kRows * 16 + o];
+      } else {
+        const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
+        g = GT[o];
+        gd = GT[kRows * 16 + o];
+      }
       if (s & 1) {
         a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
         ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
@@ -1077,8 +1084,8 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         m1 = fmaxf(m1, PMAX[(kBwdWaves + v) * 16 + n]);
       }
       const float sg0 = x3_norm(m0), sg1 = x3_norm(m1);
-      inv_t = 1.0f / (S * sg0);
-      inv_td = 1.0f / (S * sg1);
+      inv_t = x3_norm_inv(m0) * inv_S;
+      inv_td = x3_norm_inv(m1) * inv_S;
       // three planes (hi, hi S, lo S) of t sigma; float4 group g of pair n's
       // row (8 halfs) at g ^ (n & 7)
       _Float16* TBh = reinterpret_cast<_Float16*>(TB);
@@ -1171,6 +1178,14 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       adbv[i] = hdb[i] * act1[i];
       db[i] += abv[i];
     }
+    float amax_tile = 0.f;  // split path: max |ab|, |ab'| over the wave
+    if constexpr (kX3) {
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fmaxf(fabsf(abv[i]), fabsf(adbv[i])));
+      mx = cross_row_max(row16_max(mx));
+      amax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
+    }
     // 4. dW2[16w + m][16u + c] += sum_pairs t[pair][16w + m] h[pair][16u + c]
     if constexpr (kX3) {
       // fp16 MFMA, k = 32 = (stream, pair): lane group q holds stream q >> 1,
@@ -1240,6 +1255,42 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
+    if constexpr (kX3) {
+      // as step 4: A = ab ra split when read (ra = 2^k, |ab| ra < 4 over every
+      // tile seen so far), B = the two planes of g
+      if (amax_tile > arun) {  // wave-uniform; the running scale only shrinks
+        const float rn =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x3_norm(amax_tile))));
+        const float f = rn / ra;
+#pragma unroll
+        for (int kt = 0; kt < KTMAX; ++kt) acc1[kt] *= f;
+        ra = rn;
+        arun = amax_tile;
+      }
+      const int oA6 = (q >> 1) * kF * 16 + rp_at(16 * w + n, 8 * (q & 1));
+      const float4 x0 = *reinterpret_cast<const float4*>(AT + oA6);
+      const float4 x1 = *reinterpret_cast<const float4*>(AT + (oA6 ^ 4));
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      halfx8 ah, ahs, al;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float s = xv[j] * ra;
+        const _Float16 h = (_Float16)s;
+        ah[j] = h;
+        ahs[j] = (_Float16)((float)h * kS4);
+        al[j] = (_Float16)((s - (float)h) * kS4);
+      }
+      // B: halfx8 of plane rows 16kt + n, stream q >> 1, pairs 8 (q & 1) .. + 7
+      const halfx8* gth = reinterpret_cast<const halfx8*>(GT);
+      const int oB6 = (q >> 1) * 2 * kRows + 2 * n + (q & 1);
+#pragma unroll
+      for (int kt = 0; kt < KTMAX; ++kt) {
+        const halfx8 bh = gth[oB6 + 32 * kt], bl = gth[oB6 + 2 * kRows * 16 / 8 + 32 * kt];
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh, acc1[kt], 0, 0, 0);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc1[kt], 0, 0, 0);
+        acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc1[kt], 0, 0, 0);
+      }
+    } else {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const float* A = AT + st * kF * 16;
@@ -1254,12 +1305,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         acc1[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc1[kt], 0, 0, 0);
       }
     }
+    }
   }
 
   if constexpr (kX3) {
     const float f = 1.0f / (kS4 * rw * kBetaH);
 #pragma unroll
     for (int u = 0; u < kFT; ++u) acc2[u] *= f;
+    const float f1 = 1.0f / (kS4 * ra);
+#pragma unroll
+    for (int kt = 0; kt < KTMAX; ++kt) acc1[kt] *= f1;
   }
   // partial sums of this workgroup: [dW2 (F x F) | dW1 (F x Kp16) | db1 (F)]
   float* out = partial + (int64_t)blockIdx.x * bwd_partial_floats(K);

@@ -1,31 +1,33 @@
-// Node-level linears of the interaction blocks (gfx950, MFMA fp32).
+// Node-level linears of the interaction blocks (gfx950, MFMA).
 //
 // The CFConv and interaction-block linears of SchNet (conv.lin1, conv.lin2,
 // lin: mlcg/nn/schnet.py:259-261,343,347) act on [N, 128] node features with
-// 128 x 128 weights.  Both their products and their weight gradients run here
-// on v_mfma_f32_16x16x4f32:
+// 128 x 128 weights.  Their products and their weight gradients run here:
 //
 //   node_gemm     y = x W^T or x W ([N, 128]) with the elementwise work around
 //                 it fused into the store: bias, residual, the activation, or
 //                 the activation's first / second derivative factors of the
-//                 force and force-matching sweeps.  Persistent workgroups of
-//                 4 waves keep their 32-column slice of W in registers (as
-//                 MFMA B fragments, loaded once) and stream 16-row tiles of x
-//                 through LDS, double-buffered; each tile's result passes
-//                 through LDS once more so that the epilogue reads and writes
-//                 whole rows with float4 accesses.
+//                 force and force-matching sweeps.  Products on
+//                 v_mfma_f32_16x16x32_f16 with split fp32 operands (three
+//                 fp16 products, fp32 accumulation; split16.h).  Persistent
+//                 workgroups of 4 waves keep their 32-column slice of W in
+//                 registers as two fp16 planes and stream 16-row tiles of x
+//                 through LDS as three planes, each row scaled by a power of
+//                 two; the tile's result passes through LDS once more so that
+//                 the epilogue reads and writes whole rows with float4
+//                 accesses, its inputs requested before the products.
 //   node_tmm      out = a1^T b1 [+ a2^T b2] ([128, 128]): the weight
-//                 gradients, a reduction over N ~ 10^4-10^5 rows.  Up to 128
-//                 workgroups each reduce a fixed set of 64-row chunks (staged
-//                 in LDS) with the row index as the MFMA reduction axis (wave w
-//                 owns output rows 16w..16w+15) and write their partial; a
-//                 second kernel adds the partials in a fixed order --
-//                 deterministic for a given row count.
+//                 gradients, a reduction over N ~ 10^4-10^5 rows on
+//                 v_mfma_f32_16x16x4f32.  Up to 256 workgroups each reduce a
+//                 contiguous range of rows in 16-row chunks (staged in LDS)
+//                 with the row index as the MFMA reduction axis (wave w owns
+//                 output rows 16w..16w+15) and write their partial; a second
+//                 kernel adds the partials in a fixed order -- deterministic
+//                 for a given row count.
 #include "common.h"
+#include "split16.h"
 
 namespace {
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kF = 128;
 constexpr int kFT = kF / 16;
@@ -228,34 +230,80 @@ __device__ __forceinline__ void gemm_load_x(float4 (&v)[kGemmXPer], const float*
     v[m] = r < rows ? ld4(x + r * kF + 4 * (c & 31)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 }
-__device__ __forceinline__ void gemm_store_x(float* xs, const float4 (&v)[kGemmXPer]) {
+// Split scale of the node products: x is brought into [-4, 4) per row, so
+// hi S stays below 2^13; W needs |W| < 2^15.
+constexpr float kNodeS = 2048.0f;
+constexpr int kXPlane = kGemmRows * kF;  // halfs per plane of a staged tile
+
+// Stages a loaded tile: per row r, sigma_r = 2^k with max_c |x[r][c]| sigma_r
+// < 4; the three planes (hi, hi S, lo S) of x sigma go to LDS as [row][128]
+// halfs with 16-byte chunk j of row r stored at j ^ (r & 15), and
+// 1 / (S sigma_r) to rinv[r].  The 32 lanes of a wave half hold one row.
+__device__ __forceinline__ void gemm_stage_x3(_Float16* xp, float* rinv,
+                                              const float4 (&v)[kGemmXPer]) {
 #pragma unroll
   for (int m = 0; m < kGemmXPer; ++m) {
     const int c = threadIdx.x + m * kGemmThreads;
-    st4(xs + (c >> 5) * kTRow + 4 * (c & 31), v[m]);
+    const int row = c >> 5, c4 = c & 31;
+    const float4 x = v[m];
+    float mx = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    mx = pair_row_max(row16_max(mx));
+    const float sg = x3_norm(mx);
+    if (c4 == 0) rinv[row] = x3_norm_inv(mx) * (1.0f / kNodeS);
+    const float xv[4] = {x.x, x.y, x.z, x.w};
+    halfx4 ph, phs, pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t = xv[i] * sg;
+      const _Float16 h = (_Float16)t;
+      ph[i] = h;
+      phs[i] = (_Float16)((float)h * kNodeS);
+      pl[i] = (_Float16)((t - (float)h) * kNodeS);
+    }
+    const int o = row * kF + 8 * ((c4 >> 1) ^ (row & 15)) + 4 * (c4 & 1);
+    *reinterpret_cast<halfx4*>(xp + o) = ph;
+    *reinterpret_cast<halfx4*>(xp + kXPlane + o) = phs;
+    *reinterpret_cast<halfx4*>(xp + 2 * kXPlane + o) = pl;
+  }
+}
+
+// Epilogue inputs of one float4 of the product, requested ahead of it.
+struct EpiIn {
+  float4 res, s, z, e, f;
+};
+
+template <int MODE>
+__device__ __forceinline__ void gemm_epilogue_load(EpiIn& in, int64_t r, int col,
+                                                   const float* __restrict__ residual, int act,
+                                                   const float* __restrict__ zin,
+                                                   const float* __restrict__ sin_,
+                                                   const float* __restrict__ ein,
+                                                   const float* __restrict__ fin) {
+  const int64_t o = r * kF + col;
+  const float4 zero{0.f, 0.f, 0.f, 0.f};
+  in.res = residual ? ld4(residual + o) : zero;
+  if (MODE >= MLCG_NODE_DACT) {
+    in.s = ld4(sin_ + o);
+    in.z = act == MLCG_ACT_TANH ? in.s : ld4(zin + o);  // tanh needs s only
+    if (MODE == MLCG_NODE_DACT2 && ein) {
+      in.e = ld4(ein + o);
+      in.f = ld4(fin + o);
+    }
   }
 }
 
 // Epilogue on one float4 of the product (row r, columns col..col+3).
 template <int MODE>
-__device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col,
-                                              const float* __restrict__ bias,
-                                              const float* __restrict__ residual, int act,
-                                              const float* __restrict__ zin,
-                                              const float* __restrict__ sin_,
-                                              const float* __restrict__ ein,
-                                              const float* __restrict__ fin,
-                                              float* __restrict__ out0,
+__device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col, const EpiIn& in,
+                                              const float* __restrict__ bias, int act,
+                                              bool has_ef, float* __restrict__ out0,
                                               float* __restrict__ out1) {
   const int64_t o = r * kF + col;
   if (bias) {
     const float4 b = ld4(bias + col);
     y.x += b.x; y.y += b.y; y.z += b.z; y.w += b.w;
   }
-  if (residual) {
-    const float4 b = ld4(residual + o);
-    y.x += b.x; y.y += b.y; y.z += b.z; y.w += b.w;
-  }
+  y.x += in.res.x; y.y += in.res.y; y.z += in.res.z; y.w += in.res.w;
   if (MODE == MLCG_NODE_PLAIN) {
     st4(out0 + o, y);
   } else if (MODE == MLCG_NODE_ACT) {
@@ -263,8 +311,7 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col,
     st4(out1 + o, float4{mlcg_act_value(act, y.x), mlcg_act_value(act, y.y),
                          mlcg_act_value(act, y.z), mlcg_act_value(act, y.w)});
   } else {
-    const float4 s = ld4(sin_ + o);
-    const float4 z = act == MLCG_ACT_TANH ? s : ld4(zin + o);  // tanh needs s only
+    const float4 s = in.s, z = in.z;
     float4 d1, d2;
     act_d1d2(act, z.x, s.x, d1.x, d2.x);
     act_d1d2(act, z.y, s.y, d1.y, d2.y);
@@ -275,8 +322,8 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col,
       st4(out1 + o, float4{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w});
     } else {  // MLCG_NODE_DACT2
       float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
-      if (ein) {
-        const float4 e = ld4(ein + o), f = ld4(fin + o);
+      if (has_ef) {
+        const float4 e = in.e, f = in.f;
         v.x += e.x * d2.x * f.x;
         v.y += e.y * d2.y * f.y;
         v.z += e.z * d2.z * f.z;
@@ -287,9 +334,10 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col,
   }
 }
 
-// y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true).
-// MFMA step kk of lane group q = l/16 covers k = 16(kk/4) + 4q + kk%4, so a
-// lane's four consecutive steps read one float4 of its x row.
+// y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true), on
+// v_mfma_f32_16x16x32_f16 with split operands: x as three planes (staged
+// per tile, scaled per row), B as two planes (hi, lo S) held in registers.
+// MFMA k block kb of lane group q = l/16 covers k = 32 kb + 8q .. + 7.
 template <int MODE, bool kXW>
 __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
     const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
@@ -297,71 +345,85 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
     const float* __restrict__ zin, const float* __restrict__ sin_,
     const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
     float* __restrict__ out1) {
-  __shared__ float xs[2][kGemmRows * kTRow];
+  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
+  __shared__ float rinv[2][kGemmRows];
   __shared__ float ys[kGemmRows * kTRow];
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
   const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  float b[2][32];
+  halfx8 bh[2][kF / 32], bl[2][kF / 32];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int col = 32 * w + 16 * c + n;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int kb = 0; kb < kF / 32; ++kb) {
+      float wv[8];
       if (kXW) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[c][4 * m + j] = W[(16 * m + 4 * q + j) * kF + col];
-      } else {  // the four k of one group are contiguous in row `col` of W
-        const float4 v = ld4(W + col * kF + 16 * m + 4 * q);
-        b[c][4 * m + 0] = v.x;
-        b[c][4 * m + 1] = v.y;
-        b[c][4 * m + 2] = v.z;
-        b[c][4 * m + 3] = v.w;
+        for (int j = 0; j < 8; ++j) wv[j] = W[(32 * kb + 8 * q + j) * kF + col];
+      } else {  // the eight k of a lane are contiguous in row `col` of W
+        const float4 v0 = ld4(W + col * kF + 32 * kb + 8 * q);
+        const float4 v1 = ld4(W + col * kF + 32 * kb + 8 * q + 4);
+        wv[0] = v0.x; wv[1] = v0.y; wv[2] = v0.z; wv[3] = v0.w;
+        wv[4] = v1.x; wv[5] = v1.y; wv[6] = v1.z; wv[7] = v1.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const _Float16 h = (_Float16)wv[j];
+        bh[c][kb][j] = h;
+        bl[c][kb][j] = (_Float16)((wv[j] - (float)h) * kNodeS);
       }
     }
   }
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
   gemm_load_x(pf, x, t, rows);
-  gemm_store_x(xs[0], pf);
+  gemm_stage_x3(xs[0], rinv[0], pf);
   __syncthreads();
   int buf = 0;
   for (; t < tiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < tiles;
     if (has_next) gemm_load_x(pf, x, tn, rows);
+    // this tile's epilogue inputs, requested before the products
+    EpiIn ein_[kGemmXPer];
+#pragma unroll
+    for (int m = 0; m < kGemmXPer; ++m) {
+      const int c = threadIdx.x + m * kGemmThreads;
+      const int64_t r = t * kGemmRows + (c >> 5);
+      gemm_epilogue_load<MODE>(ein_[m], r < rows ? r : 0, 4 * (c & 31), residual, act, zin,
+                               sin_, ein, fin);
+    }
     floatx4 acc[kGemmRT][2];
 #pragma unroll
     for (int r = 0; r < kGemmRT; ++r)
       acc[r][0] = acc[r][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const float* xa = xs[buf] + n * kTRow + 4 * q;
+    const halfx8* xv = reinterpret_cast<const halfx8*>(xs[buf]);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      float av[kGemmRT][4];
+    for (int kb = 0; kb < kF / 32; ++kb) {
 #pragma unroll
       for (int r = 0; r < kGemmRT; ++r) {
-        const float4 a = ld4(xa + 16 * r * kTRow + 16 * m);
-        av[r][0] = a.x; av[r][1] = a.y; av[r][2] = a.z; av[r][3] = a.w;
-      }
+        const int o = (16 * r + n) * (kF / 8) + ((4 * kb + q) ^ n);
+        const halfx8 ah = xv[o], ahs = xv[kXPlane / 8 + o], al = xv[2 * kXPlane / 8 + o];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < kGemmRT; ++r) {
-          acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r][j], b[0][4 * m + j], acc[r][0],
-                                                           0, 0, 0);
-          acc[r][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r][j], b[1][4 * m + j], acc[r][1],
-                                                           0, 0, 0);
+        for (int c = 0; c < 2; ++c) {
+          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh[c][kb], acc[r][c], 0, 0, 0);
+          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[c][kb], acc[r][c], 0, 0, 0);
+          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[c][kb], acc[r][c], 0, 0, 0);
         }
+      }
     }
 #pragma unroll
     for (int r = 0; r < kGemmRT; ++r)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * r + 4 * q + i;
+        const float u = rinv[buf][row];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          ys[(16 * r + 4 * q + i) * kTRow + 32 * w + 16 * c + n] = acc[r][c][i];
-    if (has_next) gemm_store_x(xs[buf ^ 1], pf);
+        for (int c = 0; c < 2; ++c) ys[row * kTRow + 32 * w + 16 * c + n] = acc[r][c][i] * u;
+      }
+    if (has_next) gemm_stage_x3(xs[buf ^ 1], rinv[buf ^ 1], pf);
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
@@ -369,8 +431,8 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
       const int rr = c >> 5, col = 4 * (c & 31);
       const int64_t r = t * kGemmRows + rr;
       if (r < rows)
-        gemm_epilogue<MODE>(ld4(ys + rr * kTRow + col), r, col, bias, residual, act, zin, sin_,
-                            ein, fin, out0, out1);
+        gemm_epilogue<MODE>(ld4(ys + rr * kTRow + col), r, col, ein_[m], bias, act,
+                            ein != nullptr, out0, out1);
     }
     __syncthreads();
     buf ^= 1;

@@ -387,6 +387,38 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
     return _blocks_reverse2(spec, P, st, tw, hbar2, g_out_w, g_out_b)
 
 
+_SIDE_STREAMS = {}
+
+
+class _SideStream:
+    """A second stream (default priority) for the weight-gradient reductions
+    of reverse2: their results feed only the optimizer, so they run beside
+    the adjoint chain instead of between its kernels.  Each launch waits for
+    the work already queued on the main stream; the inputs are marked as used
+    by the side stream, so the caching allocator does not hand their memory
+    out again before the side stream is done; join() makes the main stream
+    wait for every side launch."""
+
+    def __init__(self, device: torch.device):
+        self.main = torch.cuda.current_stream(device)
+        key = (device.index, self.main.cuda_stream)
+        if key not in _SIDE_STREAMS:
+            _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+        self.side = _SIDE_STREAMS[key]
+
+    def run(self, fn, *inputs):
+        self.side.wait_stream(self.main)
+        with torch.cuda.stream(self.side):
+            out = fn()
+        for t in inputs:
+            if t is not None:
+                t.record_stream(self.side)
+        return out
+
+    def join(self):
+        self.main.wait_stream(self.side)
+
+
 def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     """reverse2 through the interaction blocks from the output network's
     adjoint xbar2; assembles the gradients in Params.flat() order."""
@@ -395,29 +427,34 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     n_lin = len(P.out_w)
     g_blocks = [None] * len(P.blocks)
     g_basis = None
+    side = _SideStream(st.pos.device)
+
+    def tmm(a1, b1, a2=None, b2=None, colsum=False):
+        return side.run(lambda: ops.node_tmm(a1, b1, a2, b2, colsum=colsum), a1, b1, a2, b2)
+
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
         if tangent_on:
             zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, st.sbar1[k],
                                st.zdot[k])
-            gA3, gc3 = ops.node_tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k], colsum=True)
+            gA3, gc3 = tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k], colsum=True)
         else:
             zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, None, None)
-            gA3, gc3 = ops.node_tmm(xbar2, st.s[k], colsum=True)
+            gA3, gc3 = tmm(xbar2, st.s[k], colsum=True)
         gagg2 = ops.node_linear(zbar2, bp.A2, transpose=True)
         if tangent_on:
-            gA2, gc2 = ops.node_tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], colsum=True)
+            gA2, gc2 = tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], colsum=True)
         else:
-            gA2, gc2 = ops.node_tmm(zbar2, st.agg[k], colsum=True)
+            gA2, gc2 = tmm(zbar2, st.agg[k], colsum=True)
         g1 = st.gagg1[k] if tangent_on else None
         yd = st.ydot[k] if tangent_on else None
         dd = st.ddot if tangent_on else None
         ybar2, _, _ = ops.cfconv_gather_rev2(gagg2, g1, st.y[k], yd, st.W[k], st.Wd[k], dd,
                                              graph, pair_adjoints=False)
         if tangent_on and st.xdot_in[k] is not None:
-            gA1 = ops.node_tmm(ybar2, st.x[k], st.ybar1[k], st.xdot_in[k])
+            gA1 = tmm(ybar2, st.x[k], st.ybar1[k], st.xdot_in[k])
         else:
-            gA1 = ops.node_tmm(ybar2, st.x[k])
+            gA1 = tmm(ybar2, st.x[k])
         xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
         res = ops.filter_bwd_cfconv(st.pos, graph, st.filt, bp.W1, bp.b1, bp.W2, gagg2,
                                     st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable)
@@ -428,6 +465,7 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
                                          out=g_basis)
         g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
     g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
+    side.join()
     out = [g_emb]
     for gb in g_blocks:
         out += gb

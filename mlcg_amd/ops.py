@@ -283,6 +283,7 @@ def node_linear(x: torch.Tensor, W: torch.Tensor, bias: Optional[torch.Tensor] =
     node GEMM kernel for [N, 128] x [128, 128]; other shapes (the output
     network) go to one library GEMM with the epilogue terms in addmm's beta
     input."""
+    require_device(x)
     if _node_gemm_ok(x, W):
         return node_gemm(x, W, transpose=transpose, bias=bias, residual=residual)[0]
     Wm = W if transpose else W.t()
@@ -346,6 +347,7 @@ def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = No
              b2: Optional[torch.Tensor] = None, colsum: bool = False):
     """a1^T b1 (+ a2^T b2) reduced over the rows; with colsum, returns
     (product, a1.sum(0)) from the same pass."""
+    require_device(a1, b1, a2, b2)
     shapes_ok = all(t is None or (t.dim() == 2 and t.shape[1] == NUM_FILTERS)
                     for t in (a1, b1, a2, b2))
     if shapes_ok and a1.is_cuda and a1.dtype == torch.float32:
