@@ -544,10 +544,37 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
   const int n1v = n1 / 8, n2v = n2 / 8;
   const int64_t wave = (int64_t)blockIdx.x * kWavesX3 + threadIdx.x / MLCG_WAVE;
   const int64_t nwaves = (int64_t)gridDim.x * kWavesX3;
+  // the pair indices are requested two tiles ahead and the bead positions one
+  // tile ahead (clamped to the last pair: valid memory, values unused)
+  auto pair_at = [&](int64_t t_) -> int64_t {
+    const int64_t p_ = (t_ < tiles ? t_ : tiles - 1) * 16 + (l & 15);
+    return p_ < np ? p_ : np - 1;
+  };
+  float3 ri{0.f, 0.f, 0.f}, rj{0.f, 0.f, 0.f};
+  int64_t ni = 0, nj = 0;
+  if (wave < tiles) {
+    const int64_t p0 = pair_at(wave), p1 = pair_at(wave + nwaves);
+    const int64_t i0 = pi[p0], j0 = pj[p0];
+    ri = float3{pos[3 * i0], pos[3 * i0 + 1], pos[3 * i0 + 2]};
+    rj = float3{pos[3 * j0], pos[3 * j0 + 1], pos[3 * j0 + 2]};
+    ni = pi[p1];
+    nj = pj[p1];
+  }
   for (int64_t tile = wave; tile < tiles; tile += nwaves) {
     const int64_t p = tile * 16 + (l & 15);
     const bool valid = p < np;
-    const float d = pair_distance(pos, pi, pj, p, valid);
+    float d = 1.0f;
+    if (valid) {
+      const float dx = rj.x - ri.x, dy = rj.y - ri.y, dz = rj.z - ri.z;
+      d = sqrtf(dx * dx + dy * dy + dz * dz);
+    }
+    ri = float3{pos[3 * ni], pos[3 * ni + 1], pos[3 * ni + 2]};
+    rj = float3{pos[3 * nj], pos[3 * nj + 1], pos[3 * nj + 2]};
+    {
+      const int64_t p2 = pair_at(tile + 2 * nwaves);
+      ni = pi[p2];
+      nj = pj[p2];
+    }
     float crbf, dcrbf, cc, dcc;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
     mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);

@@ -207,7 +207,7 @@ __device__ __forceinline__ void act_d1d2(int act, float z, float s, float& d1, f
     d1 = 1.0f - s * s;
     d2 = -2.0f * s * d1;
   } else {
-    const float sg = 1.0f / (1.0f + expf(-z));
+    const float sg = mlcg_sigmoid(z);
     d1 = sg;
     d2 = sg * (1.0f - sg);
   }
