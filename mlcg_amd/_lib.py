@@ -71,6 +71,8 @@ _SIGNATURES = {
                       _P, _P, _P, _I64, _P],
     "mlcg_node_tmm_workspace_floats": [_I64],
     "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _I64, _P],
+    "mlcg_type_sum_workspace_floats": [_I64, _I32],
+    "mlcg_type_sum": [_P, _P, _I64, _I32, _I32, _P, _P, _P, _I64, _P],
     "mlcg_prior_order": [_I32],
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
@@ -82,7 +84,8 @@ _SIGNATURES = {
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
-             "mlcg_rbf_param_grad_workspace_floats": _I64}
+             "mlcg_rbf_param_grad_workspace_floats": _I64,
+             "mlcg_type_sum_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

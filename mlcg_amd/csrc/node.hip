@@ -439,6 +439,72 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// type_sum: out[t][:] = sum of the rows x[n][:] with types[n] == t, for
+// t < T <= 128 -- the gradient of an embedding table.  Workgroup g sums its
+// contiguous row range into an LDS table, thread c owning column c and
+// walking the rows in ascending order, and writes that partial table; a
+// second kernel adds the partials in workgroup order.  No atomics: the
+// result is the same on every run.
+constexpr int kTypeMax = 128;
+constexpr int kTypeGroups = 1024;
+constexpr int kTypeBatch = 32;  // rows whose loads are in flight together
+
+__global__ __launch_bounds__(kF) void type_sum_kernel(const float* __restrict__ x,
+                                                       const int64_t* __restrict__ types,
+                                                       int64_t rows, int T,
+                                                       float* __restrict__ partial,
+                                                       int* __restrict__ bad) {
+  extern __shared__ float acc[];  // [T][128]
+  const int c = threadIdx.x;
+  for (int t = 0; t < T; ++t) acc[t * kF + c] = 0.0f;
+  const int64_t G = gridDim.x;
+  const int64_t r0 = rows * blockIdx.x / G, r1 = rows * (blockIdx.x + 1) / G;
+  constexpr int kBatch = kTypeBatch;
+  for (int64_t r = r0; r < r1; r += kBatch) {
+    int64_t tt[kBatch];
+    float xv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool in = r + u < r1;
+      tt[u] = in ? types[r + u] : 0;
+      xv[u] = in ? x[(r + u) * kF + c] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (r + u >= r1) break;
+      const int64_t t = tt[u];
+      if (t < 0 || t >= T) {  // out-of-table type: flagged, not summed
+        if (c == 0) bad[0] = 1;
+        continue;
+      }
+      acc[t * kF + c] += xv[u];
+    }
+  }
+  float* o = partial + (int64_t)blockIdx.x * T * kF;
+  for (int t = 0; t < T; ++t) o[t * kF + c] = acc[t * kF + c];
+}
+
+__global__ __launch_bounds__(256) void type_sum_reduce_kernel(const float* __restrict__ partial,
+                                                              int groups, int T,
+                                                              float* __restrict__ out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= T * kF) return;
+  float a0 = 0.f, a1 = 0.f;
+  int g = 0;
+  for (; g + 1 < groups; g += 2) {
+    a0 += partial[(int64_t)g * T * kF + j];
+    a1 += partial[(int64_t)(g + 1) * T * kF + j];
+  }
+  if (g < groups) a0 += partial[(int64_t)g * T * kF + j];
+  out[j] = a0 + a1;
+}
+
+int type_groups(int64_t rows) {
+  const int64_t g = (rows + kTypeBatch - 1) / kTypeBatch;
+  return (int)(g < 1 ? 1 : (g < kTypeGroups ? g : kTypeGroups));
+}
+
 int tmm_groups(int64_t rows) {
   const int64_t chunks = rows == 0 ? 1 : (rows + kTmmRows - 1) / kTmmRows;
   return (int)(chunks < kTmmMaxGroups ? chunks : kTmmMaxGroups);
@@ -524,5 +590,28 @@ extern "C" int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
   const int outs = kF * kF + (colsum_a1 ? kF : 0);
   hipLaunchKernelGGL(node_tmm_reduce_kernel, dim3(outs / 64), dim3(512), 0, s, workspace, groups,
                      accumulate, out, colsum_a1);
+  return mlcg_launch_status();
+}
+
+extern "C" int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types) {
+  if (rows < 0 || num_types < 1 || num_types > kTypeMax) return -1;
+  return (int64_t)type_groups(rows) * num_types * kF;
+}
+
+extern "C" int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
+                             int num_types, float* out, int* bad, float* workspace,
+                             int64_t workspace_floats, void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  if (num_types > kTypeMax) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out && bad && workspace);
+  MLCG_REQUIRE(rows == 0 || (x && types));
+  const int groups = type_groups(rows);
+  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * num_types * kF);
+  hipStream_t s = mlcg_stream(stream);
+  hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)groups), dim3(kF),
+                     sizeof(float) * num_types * kF, s, x, types, rows, num_types, workspace, bad);
+  const int outs = num_types * kF;
+  hipLaunchKernelGGL(type_sum_reduce_kernel, dim3((outs + 255) / 256), dim3(256), 0, s,
+                     workspace, groups, num_types, out);
   return mlcg_launch_status();
 }

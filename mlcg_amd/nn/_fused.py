@@ -464,7 +464,10 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
             g_basis = ops.rbf_param_grad(st.dist, graph, st.filt, bp.W1, res[3], res[4],
                                          out=g_basis)
         g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
-    g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
+    if P.emb.shape[0] <= 128 and P.emb.shape[1] == 128 and st.types.dtype == torch.int64:
+        g_emb = ops.type_sum(xbar2, st.types, P.emb.shape[0])[0]  # fixed summation order
+    else:
+        g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
     side.join()
     out = [g_emb]
     for gb in g_blocks:

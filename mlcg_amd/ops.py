@@ -366,6 +366,27 @@ def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = No
     return (out, a1.sum(0)) if colsum else out
 
 
+def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
+             ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(out [num_types, 128], bad [1] int32): out[t] = sum of the rows of x
+    whose type is t (the embedding-table gradient), summed in a fixed order
+    (mlcg_type_sum); bad[0] = 1 when a type lies outside [0, num_types)."""
+    require_device(x, types)
+    _check(x.dim() == 2 and x.shape[1] == NUM_FILTERS and x.dtype == torch.float32,
+           f"type_sum takes [N, {NUM_FILTERS}] float32 rows")
+    _check(types.dtype == torch.int64 and types.shape == (x.shape[0],)
+           and types.device == x.device, "types must be int64 [N] on the rows' device")
+    _check(1 <= num_types <= 128, "type_sum supports 1..128 types")
+    x, types = x.contiguous(), types.contiguous()
+    out = torch.empty(num_types, NUM_FILTERS, dtype=torch.float32, device=x.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=x.device)
+    nws = int(_lib.load().mlcg_type_sum_workspace_floats(x.shape[0], num_types))
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=x.device)
+    call("mlcg_type_sum", ptr(x), ptr(types), x.shape[0], NUM_FILTERS, num_types, ptr(out),
+         ptr(bad), ptr(ws), nws, stream_handle(x.device))
+    return out, bad
+
+
 # --------------------------------------------------------------------------
 # Output network MLP([128, HH, 1])
 

@@ -120,3 +120,38 @@ def test_node_gemm_deterministic_and_checks():
         ops.node_gemm(x[:, :64], W[:, :64])
     with pytest.raises(RuntimeError):
         ops.node_gemm(x, W, epilogue=ops.NODE_DACT, act=0)  # z, s missing
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,num_types", [(0, 5), (1, 1), (17920, 35), (5000, 128), (300, 7)])
+def test_type_sum_matches_index_add(rows, num_types):
+    """The embedding-table gradient against fp64 index_add, identical on
+    repeated calls (fixed summation order)."""
+    from mlcg_amd import ops
+
+    print(f"type_sum rows={rows} num_types={num_types}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + num_types)
+    x = torch.randn(rows, 128, device="cuda", generator=g)
+    types = torch.randint(0, num_types, (rows,), device="cuda", generator=g)
+    out, bad = ops.type_sum(x, types, num_types)
+    ref = torch.zeros(num_types, 128, dtype=torch.float64).index_add_(
+        0, types.cpu(), x.double().cpu())
+    assert int(bad.item()) == 0
+    if rows == 0:
+        assert torch.equal(out.cpu(), torch.zeros(num_types, 128))
+    else:
+        assert rel_err(out, ref) < 1e-6
+    assert torch.equal(ops.type_sum(x, types, num_types)[0], out)
+
+
+@pytest.mark.gpu
+def test_type_sum_flags_out_of_table_types():
+    from mlcg_amd import ops
+
+    x = torch.ones(10, 128, device="cuda")
+    types = torch.tensor([0, 1, 2, 3, 9, 1, 1, 0, 2, 3], device="cuda")
+    out, bad = ops.type_sum(x, types, 4)
+    assert int(bad.item()) == 1
+    assert out[:, 0].tolist() == [2.0, 3.0, 2.0, 2.0]  # the type-9 row is skipped
+    with pytest.raises(RuntimeError):
+        ops.type_sum(x, types, 129)
