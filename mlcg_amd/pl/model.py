@@ -107,7 +107,9 @@ class PLModel(torch.nn.Module):
 
     def configure_optimizers(self, lr: float = 1e-4,
                              weight_decay: float = 0.0) -> torch.optim.Optimizer:
-        return torch.optim.AdamW(self.model.parameters(), lr=lr, weight_decay=weight_decay)
+        fused = next(self.model.parameters()).is_cuda  # one fused kernel per step on the GPU
+        return torch.optim.AdamW(self.model.parameters(), lr=lr, weight_decay=weight_decay,
+                                 fused=fused)
 
 
 def train_epoch(plmodel: PLModel, batches: Iterable, optimizer: torch.optim.Optimizer

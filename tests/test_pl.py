@@ -109,7 +109,7 @@ def test_plmodel_step_matches_the_plain_training_step():
     pl = PLModel(GradientsOut(models[0]), Loss([ForceMSE()])).to("cuda")  # as Lightning does
     opt_pl = pl.configure_optimizers(lr=1e-3)
     plain = GradientsOut(models[1])
-    opt = torch.optim.AdamW(models[1].parameters(), lr=1e-3, weight_decay=0.0)
+    opt = torch.optim.AdamW(models[1].parameters(), lr=1e-3, weight_decay=0.0, fused=True)
     for it in range(2):
         train_epoch(pl, [b.to_torch("cuda")], opt_pl)
         opt.zero_grad(set_to_none=True)
