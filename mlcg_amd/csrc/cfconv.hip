@@ -386,17 +386,23 @@ __global__ void pair_ddot_kernel(const float* __restrict__ pos, const float* __r
   }
 }
 
-__global__ void pair_forces_kernel(const float* __restrict__ pos, const float* __restrict__ dist,
-                                   const float* __restrict__ dbar,
-                                   const int32_t* __restrict__ rowptr,
-                                   const int32_t* __restrict__ col,
-                                   const int32_t* __restrict__ eid2pair, int64_t n,
-                                   int accumulate, float* __restrict__ forces) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
+// 16 lanes per node: lane `sub` takes the node's edges sub, sub + 16, ...,
+// and the 16 partial forces are added by a fixed xor butterfly, so the
+// result does not depend on timing.
+constexpr int kForceLanes = 16;
+
+__global__ __launch_bounds__(256) void pair_forces_kernel(
+    const float* __restrict__ pos, const float* __restrict__ dist,
+    const float* __restrict__ dbar, const int32_t* __restrict__ rowptr,
+    const int32_t* __restrict__ col, const int32_t* __restrict__ eid2pair, int64_t n,
+    int accumulate, float* __restrict__ forces) {
+  const int sub = threadIdx.x % kForceLanes;
+  const int64_t i = (int64_t)blockIdx.x * (256 / kForceLanes) + threadIdx.x / kForceLanes;
+  float fx = 0.f, fy = 0.f, fz = 0.f;
+  if (i < n) {
     const float xi = pos[3 * i], yi = pos[3 * i + 1], zi = pos[3 * i + 2];
-    float fx = 0.f, fy = 0.f, fz = 0.f;
-    for (int e = rowptr[i]; e < rowptr[i + 1]; ++e) {
+    const int e1 = rowptr[i + 1];
+    for (int e = rowptr[i] + sub; e < e1; e += kForceLanes) {
       const int64_t j = col[e];
       const int p = eid2pair[e];
       const float s = dbar[p] / dist[p];
@@ -404,6 +410,14 @@ __global__ void pair_forces_kernel(const float* __restrict__ pos, const float* _
       fy += s * (pos[3 * j + 1] - yi);
       fz += s * (pos[3 * j + 2] - zi);
     }
+  }
+#pragma unroll
+  for (int o = kForceLanes / 2; o > 0; o >>= 1) {
+    fx += __shfl_xor(fx, o, kForceLanes);
+    fy += __shfl_xor(fy, o, kForceLanes);
+    fz += __shfl_xor(fz, o, kForceLanes);
+  }
+  if (i < n && sub == 0) {
     if (accumulate) {
       forces[3 * i] += fx;
       forces[3 * i + 1] += fy;
@@ -536,7 +550,7 @@ extern "C" int mlcg_pair_forces(const float* pos, const float* dist, const float
   MLCG_REQUIRE(n_nodes >= 0);
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && dist && dbar && rowptr && col && eid2pair && forces);
-  hipLaunchKernelGGL(pair_forces_kernel, dim3(mlcg_div_up(n_nodes, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(pair_forces_kernel, dim3(mlcg_div_up(n_nodes, 256 / kForceLanes)), dim3(256), 0,
                      mlcg_stream(stream), pos, dist, dbar, rowptr, col, eid2pair, n_nodes,
                      accumulate, forces);
   return mlcg_launch_status();

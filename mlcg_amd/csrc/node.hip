@@ -447,7 +447,7 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
 // second kernel adds the partials in workgroup order.  No atomics: the
 // result is the same on every run.
 constexpr int kTypeMax = 128;
-constexpr int kTypeGroups = 1024;
+constexpr int kTypeGroups = 256;
 constexpr int kTypeBatch = 32;  // rows whose loads are in flight together
 
 __global__ __launch_bounds__(kF) void type_sum_kernel(const float* __restrict__ x,
@@ -485,19 +485,19 @@ __global__ __launch_bounds__(kF) void type_sum_kernel(const float* __restrict__ 
   for (int t = 0; t < T; ++t) o[t * kF + c] = acc[t * kF + c];
 }
 
+// One wave per output: lane l adds the partials l, l + 64, ... in order, then
+// the 64 lane sums are combined by a fixed xor butterfly.
 __global__ __launch_bounds__(256) void type_sum_reduce_kernel(const float* __restrict__ partial,
                                                               int groups, int T,
                                                               float* __restrict__ out) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= T * kF) return;
-  float a0 = 0.f, a1 = 0.f;
-  int g = 0;
-  for (; g + 1 < groups; g += 2) {
-    a0 += partial[(int64_t)g * T * kF + j];
-    a1 += partial[(int64_t)(g + 1) * T * kF + j];
-  }
-  if (g < groups) a0 += partial[(int64_t)g * T * kF + j];
-  out[j] = a0 + a1;
+  const int64_t j = (int64_t)blockIdx.x * (256 / MLCG_WAVE) + threadIdx.x / MLCG_WAVE;
+  const int l = mlcg_lane();
+  float a = 0.f;
+  if (j < (int64_t)T * kF)
+    for (int g = l; g < groups; g += MLCG_WAVE) a += partial[(int64_t)g * T * kF + j];
+#pragma unroll
+  for (int o = MLCG_WAVE / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, MLCG_WAVE);
+  if (j < (int64_t)T * kF && l == 0) out[j] = a;
 }
 
 int type_groups(int64_t rows) {
@@ -611,7 +611,7 @@ extern "C" int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows,
   hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)groups), dim3(kF),
                      sizeof(float) * num_types * kF, s, x, types, rows, num_types, workspace, bad);
   const int outs = num_types * kF;
-  hipLaunchKernelGGL(type_sum_reduce_kernel, dim3((outs + 255) / 256), dim3(256), 0, s,
-                     workspace, groups, num_types, out);
+  hipLaunchKernelGGL(type_sum_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, s, workspace,
+                     groups, num_types, out);
   return mlcg_launch_status();
 }
