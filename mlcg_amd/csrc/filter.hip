@@ -56,7 +56,19 @@ struct RbfParams {
   int conv_kind;
   float conv_lo, conv_hi;
   int act;
+  int same_cut;  // the CFConv envelope is the RBF envelope: evaluated once
 };
+
+// CFConv envelope of a pair whose RBF envelope (crbf, dcrbf) is known.
+__device__ __forceinline__ void conv_cutoff(const RbfParams& rp, float d, float crbf, float dcrbf,
+                                            float& cc, float& dcc) {
+  if (rp.same_cut) {
+    cc = crbf;
+    dcc = dcrbf;
+  } else {
+    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+  }
+}
 
 // Pair geometry for the lane's pair; out-of-range tiles use a harmless d.
 __device__ __forceinline__ float pair_distance(const float* __restrict__ pos,
@@ -244,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f32_kernel(
     const float d = pair_distance(pos, pi, pj, p, valid);
     float crbf, dcrbf, cc, dcc;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
 
     floatx4 a[kFT], ad[kFT];
     gemm1_f32(w1s, KS, rp, bc, bw, d, crbf, dcrbf, a, ad, nullptr, nullptr, 0.0f);
@@ -357,7 +369,7 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
     const float d = pair_distance(pos, pi, pj, p, valid);
     float crbf, dcrbf, cc, dcc;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
 
     floatx4 a[kFT], ad[kFT];
 #pragma unroll
@@ -577,7 +589,7 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     }
     float crbf, dcrbf, cc, dcc;
     mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
 
     // 1. a = W1 g, a' = W1 g' (times S1)
     floatx4 a[kFT], ad[kFT];
@@ -725,7 +737,8 @@ __host__ __device__ constexpr int bwd_partial_floats(int K) {
 __host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
 // LDS: W2^T fragments [8][8][64] float4 (or two fp16 planes) | TB [2][16][128]
 //      (or three fp16 planes) | TT, HT, AT [2][128][16] | GT [2 buffers][2]
-//      [krows][16] | per-pair maxima [2][8][16] (split path); 156,672 bytes for
+//      [krows][16] | per-pair maxima (split path: [2 buffers][2][16] atomic-max
+//      bits; 256 floats reserved, the W2 scale's reduction scratch); 156,672 bytes for
 //      K <= 64 and exactly the 160 KiB of a gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
   return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 3 * 2 * kF * 16 +
@@ -857,7 +870,8 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float* HT = TT + 2 * kF * 16;                       // [2][128][16 pairs]  h, h'
   float* AT = HT + 2 * kF * 16;                       // [2][128][16 pairs]  ab, ab'
   float* GT0 = AT + 2 * kF * 16;                      // [2 bufs][2][kRows][16]  g, g'
-  float* PMAX = GT0 + 2 * 2 * kRows * 16;             // x3: [2][8 waves][16 pairs] max |t|
+  float* PMAX = GT0 + 2 * 2 * kRows * 16;  // x3: [2 bufs][2 streams][16 pairs] max |t| (bits)
+  unsigned* PMAXu = reinterpret_cast<unsigned*>(PMAX);
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
@@ -980,7 +994,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         }
       }
     }
-    mlcg_cutoff(rp.conv_kind, rp.conv_lo, rp.conv_hi, d, cc, dcc);
+    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
   };
 
   // t, t' of the lane's 4 features of a tile (formed one tile ahead, in the
@@ -988,7 +1002,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // of |t|, |t'| over the wave's 16 features, published for step 2
   float tbv[4], tdbv[4];
   float tmax_tile = 0.f;  // split path: max |t|, |t'| over the wave's features and pairs
-  auto pair_adjoints = [&](float4 wb, float4 wdb, float cc, float dcc) {
+  auto pair_adjoints = [&](float4 wb, float4 wdb, float cc, float dcc, int pb) {
     const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
     const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
     float m0 = 0.f, m1 = 0.f;
@@ -1002,9 +1016,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     if constexpr (kX3) {
       m0 = cross_row_max(m0);
       m1 = cross_row_max(m1);
-      if (q == 0) {
-        PMAX[w * 16 + n] = m0;
-        PMAX[(kBwdWaves + w) * 16 + n] = m1;
+      if (q == 0) {  // non-negative floats order as their bit patterns
+        atomicMax(PMAXu + pb * 32 + n, __float_as_uint(m0));
+        atomicMax(PMAXu + pb * 32 + 16 + n, __float_as_uint(m1));
       }
       const float mx = row16_max(fmaxf(m0, m1));
       tmax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
@@ -1015,6 +1029,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float cc_cur = 0.f, dcc_cur = 0.f;
   int64_t ni = 0, nj = 0;  // bead indices of the next tile's pair
   __syncthreads();  // PMAX served as scratch of the W2 scale
+  if constexpr (kX3) {
+    if (threadIdx.x < 64) PMAXu[threadIdx.x] = 0u;
+    __syncthreads();
+  }
   if (np > 0) {  // uniform across the workgroup
     const int64_t p0 = clamp_pair(blockIdx.x);
     const TileIn first = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, p0, pi[p0], pj[p0], fcol);
@@ -1025,7 +1043,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     basis(first, vm0, GT0, cc_cur, dcc_cur);
     float4 wb0, wdb0;
     tile_adjoint<kNodes>(first, tangent, has_yd, vm0, wb0, wdb0);
-    pair_adjoints(wb0, wdb0, cc_cur, dcc_cur);
+    pair_adjoints(wb0, wdb0, cc_cur, dcc_cur, 0);
   }
   __syncthreads();
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
@@ -1104,12 +1122,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     float inv_t = 1.0f, inv_td = 1.0f;  // x3: 1 / (S sigma) of the lane's pair
     if constexpr (kX3) {
-      float m0 = 0.f, m1 = 0.f;
-#pragma unroll
-      for (int v = 0; v < kBwdWaves; ++v) {
-        m0 = fmaxf(m0, PMAX[v * 16 + n]);
-        m1 = fmaxf(m1, PMAX[(kBwdWaves + v) * 16 + n]);
-      }
+      const float m0 = __uint_as_float(PMAXu[buf * 32 + n]);
+      const float m1 = __uint_as_float(PMAXu[buf * 32 + 16 + n]);
+      // the other buffer collects the next tile's maxima (phase 5, after the
+      // barrier below); its last reader was phase 2 of the previous tile
+      if (w == 0 && l < 32) PMAXu[(buf ^ 1) * 32 + l] = 0u;
       const float sg0 = x3_norm(m0), sg1 = x3_norm(m1);
       inv_t = x3_norm_inv(m0) * inv_S;
       inv_td = x3_norm_inv(m1) * inv_S;
@@ -1279,7 +1296,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           f4(adbv[0], adbv[1], adbv[2], adbv[3]);
     }
     basis(nxt, vm_nxt, GT0 + (buf ^ 1) * 2 * kRows * 16, cc_cur, dcc_cur);
-    pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur);
+    pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur, buf ^ 1);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
     if constexpr (kX3) {
@@ -1459,6 +1476,7 @@ RbfParams make_params(int basis, const float* centers, const float* widths, floa
   rp.conv_lo = clo;
   rp.conv_hi = chi;
   rp.act = act;
+  rp.same_cut = rk == ck && rlo == clo && rhi == chi;
   return rp;
 }
 
