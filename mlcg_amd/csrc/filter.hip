@@ -736,9 +736,11 @@ __host__ __device__ constexpr int bwd_partial_floats(int K) {
 }
 __host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
 // LDS: W2^T fragments [8][8][64] float4 (or two fp16 planes) | TB [2][16][128]
-//      (or three fp16 planes) | TT, HT, AT [2][128][16] | GT [2 buffers][2]
-//      [krows][16] | per-pair maxima (split path: [2 buffers][2][16] atomic-max
-//      bits; 256 floats reserved, the W2 scale's reduction scratch); 156,672 bytes for
+//      (or three fp16 planes) | TT, HT, AT [2][128][16] (split path: AT in
+//      TT's memory, and in its place an fp32 copy of g, g' [2 buffers][2][64]
+//      [16] beside their fp16 planes) | GT [2 buffers][2][krows][16] |
+//      per-pair maxima (split path: [2 buffers][2][16] atomic-max bits; 256
+//      floats reserved, the W2 scale's reduction scratch); 156,672 bytes for
 //      K <= 64 and exactly the 160 KiB of a gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
   return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 3 * 2 * kF * 16 +
@@ -868,9 +870,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;
   float* TT = TB + (kX3 ? 3 * 16 * kF : 2 * 16 * kF);  // [2][128][16 pairs]  t, t'
   float* HT = TT + 2 * kF * 16;                       // [2][128][16 pairs]  h, h'
-  float* AT = HT + 2 * kF * 16;                       // [2][128][16 pairs]  ab, ab'
-  float* GT0 = AT + 2 * kF * 16;                      // [2 bufs][2][kRows][16]  g, g'
-  float* PMAX = GT0 + 2 * 2 * kRows * 16;  // x3: [2 bufs][2 streams][16 pairs] max |t| (bits)
+  // [2][128][16 pairs] ab, ab'.  On the split path AT shares TT's memory: both
+  // hold rows of the wave's own features only, and a wave reads TT (step 4)
+  // before it writes AT (step 5) and reads AT (step 6) before it writes the
+  // next tile's TT (step 2), all in program order.
+  float* AT = kX3 ? TT : HT + 2 * kF * 16;
+  float* GT0 = kX3 ? HT + 2 * kF * 16 : AT + 2 * kF * 16;  // [2 bufs][2][kRows][16] g, g'
+  // split path: GT0 holds the fp16 planes of g, g' (step 6), GT32 an fp32
+  // copy in the [row][pair] layout for step 1
+  float* GT32 = GT0 + 2 * 2 * kRows * 16;
+  float* PMAX = GT32 + (kX3 ? 2 * 2 * kRows * 16 : 0);  // x3: [2 bufs][2][16] max |t| (bits)
   unsigned* PMAXu = reinterpret_cast<unsigned*>(PMAX);
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
@@ -965,7 +974,8 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   };
   // Basis of a tile: wave w evaluates k steps w, w + 8, ... for the 16 pairs
   // (into GT), every lane the envelope of its own pair (returned).
-  auto basis = [&](const TileIn& t, float vm, float* GTb, float& cc, float& dcc) {
+  auto basis = [&](const TileIn& t, float vm, int bsel, float& cc, float& dcc) {
+    float* GTb = GT0 + bsel * 2 * kRows * 16;
     const float dx = t.xj - t.xi, dy = t.yj - t.yi, dz = t.zj - t.zi;
     const float d = sqrtf(dx * dx + dy * dy + dz * dz);
     float crbf, dcrbf;
@@ -987,6 +997,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           GTh[kRows * 16 + o] = h1;
           GTh[2 * kRows * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
           GTh[3 * kRows * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
+          float* G32 = GT32 + bsel * 2 * kRows * 16;
+          const int o32 = rp_at(4 * s + q, n);
+          G32[o32] = v0;
+          G32[kRows * 16 + o32] = v1;
         } else {
           const int o = rp_at(4 * s + q, n);
           GTb[o] = g * vm;
@@ -1040,7 +1054,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     ni = pi[p1];
     nj = pj[p1];
     const float vm0 = (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f;
-    basis(first, vm0, GT0, cc_cur, dcc_cur);
+    basis(first, vm0, 0, cc_cur, dcc_cur);
     float4 wb0, wdb0;
     tile_adjoint<kNodes>(first, tangent, has_yd, vm0, wb0, wdb0);
     pair_adjoints(wb0, wdb0, cc_cur, dcc_cur, 0);
@@ -1064,17 +1078,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSMAX; ++s) {
-      float g, gd;
-      if constexpr (kX3) {  // hi + lo / S4 of the two planes
-        const _Float16* GTh = reinterpret_cast<const _Float16*>(GT);
-        const int o = 16 * q + n + 64 * s;  // (4s + q) * 16 + n
-        g = (float)GTh[2 * kRows * 16 + o] * (1.0f / kS4) + (float)GTh[o];
-        gd = (float)GTh[3 * kRows * 16 + o] * (1.0f / kS4) + (float)GTh[kRows * 16 + o];
-      } else {
-        const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
-        g = GT[o];
-        gd = GT[kRows * 16 + o];
-      }
+      const float* G1 = kX3 ? GT32 + buf * 2 * kRows * 16 : GT;
+      const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
+      const float g = G1[o];
+      const float gd = G1[kRows * 16 + o];
       if (s & 1) {
         a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
         ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
@@ -1295,7 +1302,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) =
           f4(adbv[0], adbv[1], adbv[2], adbv[3]);
     }
-    basis(nxt, vm_nxt, GT0 + (buf ^ 1) * 2 * kRows * 16, cc_cur, dcc_cur);
+    basis(nxt, vm_nxt, buf ^ 1, cc_cur, dcc_cur);
     pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur, buf ^ 1);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
