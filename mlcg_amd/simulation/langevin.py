@@ -16,14 +16,26 @@ calls it (``calculate_potential_and_forces``, base.py:517-539): a module whose
 ``forward(data)`` fills ``data.out["energy"]`` and ``data.out["forces"]``
 (e.g. SumOut of GradientsOut models).
 
-File I/O, checkpoints, logging and parallel tempering of the reference
-(base.py:653-1040, parallel_tempering.py) are not part of this module; the
-trajectory is returned as an array.
+With ``filename`` set, the run is written as the reference writes it
+(base.py:799-1040): every ``export_interval`` steps the saved frames go to
+``{filename}_coords_{kkkk}.npy`` ([n_sims, export_interval / save_interval,
+n_atoms, 3]; ``_forces_``/``_potential_`` likewise when asked), with
+``create_checkpoints`` the current positions and velocities and the number
+of files written go to ``{filename}_checkpoint.pt``, and ``log_interval``
+logs progress by ``print`` or to ``{filename}_log.txt``.  A run started with
+``read_checkpoint_file`` (True for ``{filename}_checkpoint.pt``, or a path)
+continues from the checkpointed state and file index up to n_timesteps;
+because the noise is a function of the step counter, the continued
+trajectory is bit-identical to an uninterrupted run.  Parallel tempering
+(parallel_tempering.py) is not part of this module.
 """
 
 from __future__ import annotations
 
 import math
+import os
+import time
+import warnings
 from typing import List, Optional, Union
 
 import numpy as np
@@ -50,7 +62,11 @@ class LangevinSimulation:
                  save_interval: int = 10, random_seed: Optional[int] = None,
                  device: str = "cuda", dtype: str = "single", save_forces: bool = False,
                  save_energies: bool = False, capture: bool = False,
-                 edge_capacity_factor: float = 1.5, check_interval: int = 100):
+                 edge_capacity_factor: float = 1.5, check_interval: int = 100,
+                 filename: Optional[str] = None, export_interval: Optional[int] = None,
+                 log_interval: Optional[int] = None, log_type: str = "write",
+                 create_checkpoints: bool = False,
+                 read_checkpoint_file: Union[str, bool, None] = None):
         assert friction > 0
         if dtype != "single":
             raise NotImplementedError("the HIP kernels integrate in single precision")
@@ -72,6 +88,23 @@ class LangevinSimulation:
         self.noisescale = float(np.sqrt(1 - self.vscale * self.vscale))
         self.model = None
         self.initial_data = None
+        # export / log / checkpoint options (base.py:147-240, 629-720)
+        self.filename = filename
+        self.export_interval = n_timesteps if export_interval is None else int(export_interval)
+        if self.export_interval % save_interval != 0:
+            raise ValueError("export_interval must be a multiple of save_interval")
+        if n_timesteps % self.export_interval != 0:
+            raise ValueError("n_timesteps must be a multiple of export_interval")
+        if log_type not in ("print", "write"):
+            raise ValueError("log_type must be 'print' or 'write'")
+        if filename is None and (export_interval is not None or create_checkpoints
+                                 or (log_interval is not None and log_type == "write")):
+            raise ValueError("filename is required for exports, checkpoints and written logs")
+        self.log_interval = log_interval
+        self.log_type = log_type
+        self.create_checkpoints = create_checkpoints
+        self.read_checkpoint_file = None if read_checkpoint_file is False else read_checkpoint_file
+        self.current_timestep = 0  # files already written (restored from a checkpoint)
 
     # ------------------------------------------------------------------
     def attach_model_and_configurations(self, model: torch.nn.Module,
@@ -112,7 +145,62 @@ class LangevinSimulation:
             data[VELOCITY_KEY] = sample_maxwell_boltzmann(
                 betas, data.masses.cpu(), generator=g).to(self.device, self.dtype)
         self.beta_mass_ratio = torch.sqrt(1.0 / betas.to(self.device) / data.masses).contiguous()
+        if self.read_checkpoint_file is not None:
+            self._read_checkpoint(data)
         self.initial_data = data
+
+    def _checkpoint_path(self) -> str:
+        if isinstance(self.read_checkpoint_file, str):
+            return self.read_checkpoint_file
+        if self.filename is None:
+            raise ValueError("read_checkpoint_file=True needs a filename")
+        return f"{self.filename}_checkpoint.pt"
+
+    def _read_checkpoint(self, data):
+        """Positions, velocities and the number of files written by an earlier
+        run; its intervals win over the ones given here (base.py:653-695)."""
+        path = self._checkpoint_path()
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} does not exist")
+        ck = torch.load(path, map_location="cpu", weights_only=True)
+        for key in ("export_interval", "save_interval", "log_interval"):
+            if key in ck and ck[key] != getattr(self, key):
+                warnings.warn(f"specified {key} doesn't match the checkpoint, using "
+                              f"the checkpointed {key} instead", UserWarning)
+                setattr(self, key, ck[key])
+        if ck[POSITIONS_KEY].shape != data.pos.shape:
+            raise ValueError("checkpoint positions do not match the configurations")
+        data.pos = ck[POSITIONS_KEY].to(self.device, self.dtype).contiguous()
+        data[VELOCITY_KEY] = ck[VELOCITY_KEY].to(self.device, self.dtype).contiguous()
+        self.current_timestep = int(ck["current_timestep"])
+
+    def _log(self, msg: str):
+        if self.log_type == "print":
+            print(msg, flush=True)
+        else:
+            with open(f"{self.filename}_log.txt", "a") as fh:
+                fh.write(msg + "\n")
+
+    def _export(self, index: int, coords, potential, forces, x, v):
+        """Writes one export chunk ([n_sims, frames, n_atoms, 3] arrays) and,
+        when asked, the checkpoint (base.py:930-990)."""
+        key = f"{index:04d}"
+        shape = (coords.shape[0], self.n_sims, self.n_atoms, 3)
+        np.save(f"{self.filename}_coords_{key}.npy",
+                coords.view(shape).permute(1, 0, 2, 3).cpu().numpy())
+        if forces is not None:
+            np.save(f"{self.filename}_forces_{key}.npy",
+                    forces.view(shape).permute(1, 0, 2, 3).cpu().numpy())
+        if potential is not None:
+            np.save(f"{self.filename}_potential_{key}.npy", potential.t().cpu().numpy())
+        if self.create_checkpoints:
+            torch.save({POSITIONS_KEY: x.detach().cpu().clone(),
+                        VELOCITY_KEY: v.detach().cpu().clone(),
+                        "current_timestep": index + 1,
+                        "export_interval": self.export_interval,
+                        "save_interval": self.save_interval,
+                        "log_interval": self.log_interval},
+                       f"{self.filename}_checkpoint.pt")
 
     # ------------------------------------------------------------------
     def calculate_potential_and_forces(self, data):
@@ -146,22 +234,29 @@ class LangevinSimulation:
                     "max_num_neighbors")
 
     def simulate(self) -> np.ndarray:
-        """Runs n_timesteps BAOAB steps; returns the saved positions
-        [n_sims, n_saves, n_atoms, 3] (and stores energies/forces if asked)."""
+        """Runs the BAOAB steps up to n_timesteps (from the checkpointed step
+        when resuming); returns the saved positions [n_sims, n_saves, n_atoms,
+        3] -- with a filename, those of the last export chunk -- and stores
+        energies/forces if asked."""
         if self.model is None or self.initial_data is None:
             raise RuntimeError("attach a model and configurations first")
         data = self.initial_data.clone()
         x, v, m = data.pos, data.velocities.contiguous(), data.masses
         data.velocities = v
         self._set_capacity(data)
-        step_ctr = torch.zeros(1, dtype=torch.int64, device=self.device)
+        # resumed runs continue the step counter, hence the noise stream
+        t_init = self.current_timestep * self.export_interval
+        step_ctr = torch.full((1,), t_init, dtype=torch.int64, device=self.device)
         epot = torch.zeros(self.n_sims, dtype=self.dtype, device=self.device)
         F = torch.zeros_like(x)
         with torch.no_grad():
             e0, f0 = self.calculate_potential_and_forces(data)
         F.copy_(f0)
         epot.copy_(e0)
-        n_saves = self.n_timesteps // self.save_interval
+        # frames held on the device: one export chunk when writing files, the
+        # whole run otherwise
+        n_saves = (self.export_interval if self.filename is not None
+                   else self.n_timesteps) // self.save_interval
         traj = torch.empty(n_saves, *x.shape, dtype=self.dtype, device=self.device)
         saved_e = (torch.empty(n_saves, self.n_sims, dtype=self.dtype, device=self.device)
                    if self.save_energies else None)
@@ -179,18 +274,19 @@ class LangevinSimulation:
 
         graph = None
         flags = []
+        if self.log_interval is not None:
+            self._log(f"Generating {self.n_sims} simulations of n_timesteps {self.n_timesteps} "
+                      f"saved at {self.save_interval}-step intervals ({time.asctime()})")
         # steady-state timing: steps after the capture (or after step 2)
-        import time
-
         self.timed_steps = 0
         self.timed_seconds = 0.0
         t_start = None
         with torch.no_grad():
-            for t in range(self.n_timesteps):
-                if t == 3:
+            for t in range(t_init, self.n_timesteps):
+                if t == t_init + 3:
                     torch.cuda.synchronize()
                     t_start = time.perf_counter()
-                if graph is None and self.capture and t >= 2:
+                if graph is None and self.capture and t >= t_init + 2:
                     torch.cuda.synchronize()
                     self._check_flags(self._graph_flags())
                     graph = torch.cuda.CUDAGraph()
@@ -204,7 +300,7 @@ class LangevinSimulation:
                     one_step()
                     flags = self._graph_flags()
                 if (t + 1) % self.save_interval == 0:
-                    k = (t + 1) // self.save_interval - 1
+                    k = ((t + 1) // self.save_interval - 1) % n_saves
                     traj[k].copy_(x)
                     if saved_e is not None:
                         saved_e[k].copy_(epot)
@@ -214,10 +310,18 @@ class LangevinSimulation:
                     self._check_flags(flags)
                     if not bool(torch.isfinite(x).all()):
                         raise RuntimeError(f"non-finite positions at step {t + 1}")
+                if self.filename is not None and (t + 1) % self.export_interval == 0:
+                    self._check_flags(flags)
+                    self._export((t + 1) // self.export_interval - 1, traj, saved_e, saved_f,
+                                 x, v)
+                if self.log_interval is not None and (t + 1) % self.log_interval == 0:
+                    self._log(f"{(t + 1) // self.save_interval} / "
+                              f"{self.n_timesteps // self.save_interval} time points saved "
+                              f"({time.asctime()})")
         torch.cuda.synchronize()
         if t_start is not None:
             self.timed_seconds = time.perf_counter() - t_start
-            self.timed_steps = self.n_timesteps - 3
+            self.timed_steps = self.n_timesteps - t_init - 3
         self._check_flags(flags)
         self.final_data = data
         self.potential = epot

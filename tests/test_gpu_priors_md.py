@@ -302,3 +302,47 @@ def test_md_step_captured_matches_eager():
     assert np.isfinite(x0).all()
     np.testing.assert_allclose(x1, x0, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(e1, e0, rtol=1e-5, atol=1e-4)
+
+
+def test_md_export_checkpoint_and_resume(tmp_path):
+    """Exports, checkpoints and logs as base.py:799-1040 writes them; a run
+    resumed from the checkpoint after the first export chunk writes the same
+    second chunk, bit for bit, as the uninterrupted run (the noise is a
+    function of the step counter, which the checkpoint restores)."""
+    from mlcg_amd import nn
+    from mlcg_amd.simulation import LangevinSimulation
+
+    bonds = {(a, b): {"x_0": 3.8, "k": 5.0} for a in range(1, 6) for b in range(1, 6)}
+    confs = _md_config(n_frames=3, n_beads=10, with_rep=False)
+    for c in confs:
+        for k in ("angles", "dihedrals"):
+            c.neighbor_list.pop(k)
+
+    def run(name, n_timesteps, capture, **kw):
+        model = nn.SumOut(torch.nn.ModuleDict({"bonds": nn.GradientsOut(nn.HarmonicBonds(bonds))}))
+        sim = LangevinSimulation(friction=1.0, dt=0.004, n_timesteps=n_timesteps,
+                                 save_interval=5, export_interval=20, random_seed=11,
+                                 capture=capture, save_energies=True, save_forces=True,
+                                 filename=str(tmp_path / name), create_checkpoints=True,
+                                 log_interval=20, **kw)
+        sim.attach_model_and_configurations(model, [c.clone() for c in confs], L.beta_of(300.0))
+        return sim, sim.simulate()
+
+    _, last = run("a", 40, capture=False)
+    a0 = np.load(tmp_path / "a_coords_0000.npy")
+    a1 = np.load(tmp_path / "a_coords_0001.npy")
+    assert a0.shape == (3, 4, 10, 3) and a1.shape == (3, 4, 10, 3)
+    assert np.array_equal(last, a1)
+    assert np.load(tmp_path / "a_potential_0001.npy").shape == (3, 4)
+    assert np.load(tmp_path / "a_forces_0001.npy").shape == (3, 4, 10, 3)
+    ck = torch.load(tmp_path / "a_checkpoint.pt", weights_only=True)
+    assert ck["current_timestep"] == 2 and ck["export_interval"] == 20
+    assert len(open(tmp_path / "a_log.txt").read().splitlines()) == 3  # header + 2 lines
+
+    run("b", 20, capture=False)
+    assert np.array_equal(np.load(tmp_path / "b_coords_0000.npy"), a0)
+    sim, _ = run("b", 40, capture=False, read_checkpoint_file=True)
+    assert sim.current_timestep == 1
+    assert np.array_equal(np.load(tmp_path / "b_coords_0001.npy"), a1)
+    assert np.array_equal(np.load(tmp_path / "b_potential_0001.npy"),
+                          np.load(tmp_path / "a_potential_0001.npy"))

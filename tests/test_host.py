@@ -277,3 +277,21 @@ def test_exclusion_pair_to_ptr_host_abi():
     assert yp.tolist() == [0] and xs.tolist() == [0, 1]
     with pytest.raises(RuntimeError):
         ops.exclusion_pair_to_ptr(torch.tensor([[0, 1], [1, 0]], dtype=torch.int32), 3)
+
+
+def test_langevin_export_options_are_checked():
+    from mlcg_amd.simulation import LangevinSimulation
+
+    with pytest.raises(ValueError, match="filename"):
+        LangevinSimulation(n_timesteps=100, save_interval=10, export_interval=50)
+    with pytest.raises(ValueError, match="filename"):
+        LangevinSimulation(n_timesteps=100, save_interval=10, create_checkpoints=True)
+    with pytest.raises(ValueError, match="multiple of save_interval"):
+        LangevinSimulation(n_timesteps=100, save_interval=10, export_interval=25, filename="x")
+    with pytest.raises(ValueError, match="multiple of export_interval"):
+        LangevinSimulation(n_timesteps=100, save_interval=10, export_interval=30, filename="x")
+    with pytest.raises(ValueError, match="log_type"):
+        LangevinSimulation(n_timesteps=100, save_interval=10, log_interval=10, log_type="x")
+    sim = LangevinSimulation(n_timesteps=100, save_interval=10, log_interval=10,
+                             log_type="print", device="cpu")
+    assert sim.export_interval == 100 and sim.filename is None
