@@ -105,6 +105,9 @@ class LangevinSimulation:
         self.create_checkpoints = create_checkpoints
         self.read_checkpoint_file = None if read_checkpoint_file is False else read_checkpoint_file
         self.current_timestep = 0  # files already written (restored from a checkpoint)
+        # hook run eagerly every `_hook_interval` steps on (x, v, F, potential)
+        self._hook = None
+        self._hook_interval = 0
 
     # ------------------------------------------------------------------
     def attach_model_and_configurations(self, model: torch.nn.Module,
@@ -299,6 +302,8 @@ class LangevinSimulation:
                 else:
                     one_step()
                     flags = self._graph_flags()
+                if self._hook is not None and (t + 1) % self._hook_interval == 0:
+                    self._hook(x, v, F, epot)
                 if (t + 1) % self.save_interval == 0:
                     k = ((t + 1) // self.save_interval - 1) % n_saves
                     traj[k].copy_(x)

@@ -1,0 +1,126 @@
+"""Parallel tempering (mlcg/simulation/parallel_tempering.py): the exchange
+rules on synthetic energies (CPU) and a short replica-exchange run on the
+HIP driver (GPU)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from mlcg_amd.simulation import PTSimulation
+
+
+def _sim(betas, n_indep=2, n_atoms=3, seed=0):
+    """A PTSimulation with its slot layout and pairs set up, without a model."""
+    sim = PTSimulation(exchange_interval=10, n_timesteps=10, save_interval=10, device="cpu",
+                       random_seed=seed)
+    sim.n_indep_sims, sim.n_replicas = n_indep, len(betas)
+    sim.n_sims, sim.n_atoms = n_indep * len(betas), n_atoms
+    sim.beta = torch.tensor([b for b in betas for _ in range(n_indep)], dtype=torch.float32)
+    n = n_indep
+    ea = torch.cat([torch.arange(n) + r * n for r in range(0, len(betas) - 1, 2)])
+    oa = (torch.cat([torch.arange(n) + r * n for r in range(1, len(betas) - 1, 2)])
+          if len(betas) > 2 else ea)
+    sim._even_pairs, sim._odd_pairs = (ea, ea + n), (oa, oa + n)
+    sim._propose_even_pairs = True
+    sim.pair_to_beta_idx = torch.arange(len(betas)).repeat_interleave(n)
+    sim.acceptance_matrix = torch.zeros(len(betas), len(betas))
+    sim.exchange_attempts = sim.exchange_approved = 0
+    return sim
+
+
+def _state(sim, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(sim.n_sims * sim.n_atoms, 3, generator=g)
+    v = torch.randn(sim.n_sims * sim.n_atoms, 3, generator=g)
+    f = torch.randn(sim.n_sims * sim.n_atoms, 3, generator=g)
+    return x, v, f
+
+
+def test_equal_temperatures_always_exchange_and_alternate_pairs():
+    sim = _sim([1.0, 1.0, 1.0], n_indep=2)
+    x, v, f = _state(sim)
+    u = torch.arange(6, dtype=torch.float32)
+    x0, v0, f0, u0 = x.clone(), v.clone(), f.clone(), u.clone()
+    sim.detect_and_exchange_replicas(x, v, f, u)  # even pairs: slots (0,2), (1,3)
+    perm = [2, 3, 0, 1, 4, 5]
+    X0 = x0.view(6, 3, 3)
+    assert torch.equal(x.view(6, 3, 3), X0[perm])
+    assert torch.equal(v.view(6, 3, 3), v0.view(6, 3, 3)[perm])  # beta ratio 1
+    assert torch.equal(f.view(6, 3, 3), f0.view(6, 3, 3)[perm])
+    assert u.tolist() == u0[perm].tolist()
+    assert sim.acceptance_matrix[0, 1] == 2 and sim.acceptance_matrix[1, 0] == 0
+    sim.detect_and_exchange_replicas(x, v, f, u)  # odd pairs: slots (2,4), (3,5)
+    assert sim.acceptance_matrix[1, 2] == 2
+    assert sim.exchange_attempts == 4 and sim.exchange_approved == 4
+
+
+def test_metropolis_rule_and_velocity_rescaling():
+    # slot 0 colder (beta 2), slot 1 hotter (beta 1); one independent sim
+    sim = _sim([2.0, 1.0], n_indep=1)
+    x, v, f = _state(sim)
+    v0 = v.clone()
+    # (U_a - U_b)(beta_a - beta_b) = (5 - 1)(1) > 0: always accepted
+    u = torch.tensor([5.0, 1.0])
+    sim.detect_and_exchange_replicas(x, v, f, u)
+    assert sim.acceptance_matrix[0, 1] == 1
+    # the hot configuration entering the cold slot slows by sqrt(1/2)
+    torch.testing.assert_close(v.view(2, 3, 3)[0], v0.view(2, 3, 3)[1] * math.sqrt(0.5))
+    torch.testing.assert_close(v.view(2, 3, 3)[1], v0.view(2, 3, 3)[0] * math.sqrt(2.0))
+    # a huge penalty: never accepted
+    u = torch.tensor([0.0, 1e4])
+    before = x.clone()
+    for _ in range(20):
+        sim.detect_and_exchange_replicas(x, v, f, u)
+    assert torch.equal(x, before)
+    assert sim.acceptance_matrix[1, 0] == 20
+
+
+def test_acceptance_rate_matches_metropolis():
+    sim = _sim([1.5, 1.0], n_indep=4000, n_atoms=1, seed=5)
+    x, v, f = _state(sim)
+    d = 0.7  # (U_a - U_b)(beta_a - beta_b) = -0.35 for every pair
+    u = torch.cat([torch.zeros(4000), torch.full((4000,), d)])
+    sim.detect_and_exchange_replicas(x, v, f, u)
+    rate = sim.exchange_approved / sim.exchange_attempts
+    assert rate == pytest.approx(math.exp(-0.35), abs=0.03)
+
+
+def test_betas_are_checked():
+    sim = PTSimulation(n_timesteps=10, save_interval=10, device="cpu")
+    with pytest.raises(ValueError, match="multiple temperatures"):
+        sim.attach_model_and_configurations(None, [], [1.0])
+    with pytest.raises(ValueError, match="increasing temperature"):
+        sim.attach_model_and_configurations(None, [], [1.0, 2.0])
+
+
+@pytest.mark.gpu
+def test_pt_run_on_the_gpu():
+    """Harmonic chains at three temperatures: the run completes with finite
+    positions, every attempt is counted once in the acceptance matrix, and
+    each temperature slot ends at its own kinetic temperature (the thermostat
+    and the rescaled exchanges keep equipartition per slot)."""
+    from mlcg_amd import nn
+    from oracle import langevin_ref as L
+    from tests.test_gpu_priors_md import _md_config
+
+    bonds = {(a, b): {"x_0": 3.8, "k": 5.0} for a in range(1, 6) for b in range(1, 6)}
+    confs = _md_config(n_frames=64, n_beads=12, with_rep=False)
+    for c in confs:
+        for k in ("angles", "dihedrals"):
+            c.neighbor_list.pop(k)
+    model = nn.SumOut(torch.nn.ModuleDict({"bonds": nn.GradientsOut(nn.HarmonicBonds(bonds))}))
+    betas = [L.beta_of(300.0), L.beta_of(350.0), L.beta_of(400.0)]
+    sim = PTSimulation(exchange_interval=50, friction=10.0, dt=0.004, n_timesteps=3000,
+                       save_interval=1000, random_seed=4, capture=True)
+    sim.attach_model_and_configurations(model, confs, betas)
+    out = sim.simulate()
+    assert np.isfinite(out).all()
+    assert int(sim.acceptance_matrix.sum()) == sim.exchange_attempts
+    assert 0 < sim.exchange_approved < sim.exchange_attempts
+    v = sim.final_data.velocities.double().view(3, 64, 12, 3)
+    m = sim.final_data.masses.double().view(3, 64, 12, 1)
+    for r, b in enumerate(betas):
+        ke = float((0.5 * m[r] * v[r] * v[r]).mean())
+        assert ke == pytest.approx(0.5 / b, rel=0.1), r
