@@ -263,7 +263,8 @@ def gpu_leg(args):
     per_step = {k: v["total_ms"] / n_prof for k, v in warm.items()}
     dominant = max((k for k in per_step if k not in SIDE_STREAM), key=per_step.get)
 
-    # timed region: only the dominant kernel's launches are bracketed
+    # timed region: only the dominant kernel's launches are bracketed (HIP
+    # events on the stream it runs on)
     timer = _lib.LaunchTimer({dominant})
     _lib.set_timer(timer)
     torch.cuda.synchronize()
@@ -274,14 +275,14 @@ def gpu_leg(args):
     t1 = time.perf_counter()
     _lib.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
-    assert math.isfinite(float(loss)), "non-finite loss"
+    assert math.isfinite(float(loss.detach())), "non-finite loss"
     if model.graph_capacity is not None:
         flags = int(model.last_graph.flags.item())
         assert flags == 0, f"radius graph overflowed its capacity (flags {flags})"
         assert int(model.last_graph.rowptr[-1]) == E, "edge count changed"
     dom = kernel_report(timer.summary(), E, P, N, B)[dominant]
     return {"ms_per_step": ms, "E": E, "P": P, "N": N, "B": B, "dominant": dominant,
-            "dominant_row": dom, "kernels": warm, "loss": float(loss),
+            "dominant_row": dom, "kernels": warm, "loss": float(loss.detach()),
             "step_kernel_ms": round(sum(per_step.values()), 4)}
 
 

@@ -394,10 +394,11 @@ class _SideStream:
     """A second stream (default priority) for the weight-gradient reductions
     of reverse2: their results feed only the optimizer, so they run beside
     the adjoint chain instead of between its kernels.  Each launch waits for
-    the work already queued on the main stream; the inputs are marked as used
-    by the side stream, so the caching allocator does not hand their memory
-    out again before the side stream is done; join() makes the main stream
-    wait for every side launch."""
+    the work already queued on the main stream; the inputs are held until
+    join(), which makes the main stream wait for every side launch, so the
+    caching allocator cannot hand their memory to main-stream work the side
+    stream has not finished with (this also holds inside a HIP-graph
+    capture, where the fork and join become graph edges)."""
 
     def __init__(self, device: torch.device):
         self.main = torch.cuda.current_stream(device)
@@ -405,18 +406,18 @@ class _SideStream:
         if key not in _SIDE_STREAMS:
             _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
         self.side = _SIDE_STREAMS[key]
+        self.held = []
 
     def run(self, fn, *inputs):
         self.side.wait_stream(self.main)
         with torch.cuda.stream(self.side):
             out = fn()
-        for t in inputs:
-            if t is not None:
-                t.record_stream(self.side)
+        self.held.extend(t for t in inputs if t is not None)
         return out
 
     def join(self):
         self.main.wait_stream(self.side)
+        self.held.clear()
 
 
 def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
