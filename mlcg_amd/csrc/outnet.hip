@@ -416,7 +416,7 @@ __global__ __launch_bounds__(512) void out_rev2_reduce_kernel(const float* __res
   }
 }
 
-constexpr int kRev2MaxGroups = 256;
+constexpr int kRev2MaxGroups = 512;  // two per CU: about two 16-row tiles each
 
 int rev2_groups(int64_t rows) {
   const int64_t tiles = rows == 0 ? 1 : (rows + kRowsT - 1) / kRowsT;
