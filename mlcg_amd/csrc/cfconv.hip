@@ -19,6 +19,7 @@
 // order and the two halves are added at the end, so the result does not
 // depend on timing.
 #include "common.h"
+#include "split16.h"
 
 #include <hip/hip_fp16.h>
 
@@ -70,12 +71,9 @@ __device__ __forceinline__ float lanef(float v, int k) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
 }
 
-// Sum over the 32 lanes of a half-wave, returned to all of them.
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, MLCG_WAVE);
-  return v;
-}
+// Sum over the 32 lanes of a half-wave, returned to all of them (DPP and
+// v_permlane16_swap: no LDS round trips).
+__device__ __forceinline__ float half_sum(float v) { return half32_sum(v); }
 
 // Adds the other half-wave's accumulator (lanes l and l ^ 32 hold the same
 // features): lower half first, then upper half, on both.

@@ -652,6 +652,7 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     if (valid) {
       float* wr = Wout + p * kF + 4 * q;
       float* wdr = Wdout + p * kF + 4 * q;
+      const float c2 = cc * inv2, dc2 = dcc * inv2;  // 1 / S2 is a power of two
 #pragma unroll
       for (int t = 0; t < kFT; ++t) {
         float4 o, od;
@@ -659,9 +660,8 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
         float* odp = reinterpret_cast<float*>(&od);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float wv = w[t][i] * inv2, wdv = wd[t][i] * inv2;
-          op[i] = wv * cc;
-          odp[i] = wdv * cc + wv * dcc;
+          op[i] = w[t][i] * c2;
+          odp[i] = wd[t][i] * c2 + w[t][i] * dc2;
         }
         *reinterpret_cast<float4*>(wr + 16 * t) = o;
         *reinterpret_cast<float4*>(wdr + 16 * t) = od;

@@ -58,3 +58,25 @@ __device__ __forceinline__ float cross_row_max(float v) {
       __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+
+// Sums across lanes in the same fixed patterns (the result is the same on
+// every run).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_fadd(float v) {
+  return v + __int_as_float(
+                 __builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+// sum over the 16 lanes of each row, in every lane of the row
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_fadd<0xB1>(v);      // quad_perm [1, 0, 3, 2]
+  v = dpp_fadd<0x4E>(v);      // quad_perm [2, 3, 0, 1]
+  v = dpp_fadd<0x141>(v);     // row_half_mirror
+  return dpp_fadd<0x140>(v);  // row_mirror
+}
+// sum over the 32 lanes of each half-wave, in every lane of the half
+__device__ __forceinline__ float half32_sum(float v) {
+  v = row16_sum(v);
+  const auto a =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
