@@ -35,7 +35,7 @@ def _oracle_inputs(b, rc, dtype=torch.float64):
             torch.from_numpy(b.batch), torch.from_numpy(ei))
 
 
-@pytest.mark.parametrize("num_rbf", [50, 100])
+@pytest.mark.parametrize("num_rbf", [10, 50, 64, 65, 100])
 def test_filter_kernel_matches_torch(num_rbf):
     """The filter forward (K <= 64: products on the fp16 MFMA with split
     operands; wider bases: fp32 MFMA) against fp64 torch."""
@@ -302,7 +302,7 @@ def _filter_setup(n_frames=8, seed=11, num_rbf=50):
     return cfg, sd, b, pos, g, model.fused_spec(), model.fused_params().blocks[0]
 
 
-@pytest.mark.parametrize("num_rbf", [50, 100])
+@pytest.mark.parametrize("num_rbf", [10, 50, 64, 65, 100])
 def test_filter_bwd_matches_autograd(num_rbf):
     """Parameter gradients of <Wbar, W> + <Wdbar, dW/dd> from the fused
     backward kernel against fp64 autograd of the restated filter chain
@@ -364,7 +364,7 @@ def test_filter_bwd_adjoint_dynamic_range():
     assert rel_err(dW2, gW2) < 1e-4
 
 
-@pytest.mark.parametrize("num_rbf", [50, 100])
+@pytest.mark.parametrize("num_rbf", [10, 50, 64, 65, 100])
 def test_filter_bwd_cfconv_matches_explicit(num_rbf):
     """The node-adjoint backward equals the explicit one with the adjoints
     formed in torch."""
