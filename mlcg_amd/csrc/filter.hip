@@ -692,7 +692,8 @@ size_t fwd_x3_lds_bytes(int K) {
 // fragment per k step) stays in registers; the W2^T A fragments of all eight
 // tiles are staged once in LDS.  Per tile:
 //   1. a, a' of feature tile w (v_mfma_f32_16x16x4f32, B operand g, g' from
-//      LDS);
+//      LDS; for K <= 64 three v_mfma_f32_16x16x16f16 per 16-wide k block of
+//      split operands, W1's two planes in registers);
 //   2. t, t', h, h' of its features, published in LDS;         -- barrier --
 //   3. hb, hb' of its tile (B operands = all 128 t features from LDS);
 //   4. dW2 rows of its tile += t^T h over the 16 pairs (the pair index is the
@@ -737,14 +738,15 @@ __host__ __device__ constexpr int bwd_partial_floats(int K) {
 __host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
 // LDS: W2^T fragments [8][8][64] float4 (or two fp16 planes) | TB [2][16][128]
 //      (or three fp16 planes) | TT, HT, AT [2][128][16] (split path: AT in
-//      TT's memory, and in its place an fp32 copy of g, g' [2 buffers][2][64]
-//      [16] beside their fp16 planes) | GT [2 buffers][2][krows][16] |
-//      per-pair maxima (split path: [2 buffers][2][16] atomic-max bits; 256
-//      floats reserved, the W2 scale's reduction scratch); 156,672 bytes for
-//      K <= 64 and exactly the 160 KiB of a gfx950 CU for K <= 128
+//      TT's memory) | GT [2 buffers][2][krows][16] (split path: two fp16
+//      planes, followed by the pair-major three-plane copy of g, g' for step
+//      1, [3][2][16][64] halfs) | per-pair maxima (split path: [2 buffers][2]
+//      [16] atomic-max bits; 256 floats reserved, the W2 scale's reduction
+//      scratch); 152,576 bytes for K <= 64 and exactly the 160 KiB of a
+//      gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
-  return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 3 * 2 * kF * 16 +
-                       2 * 2 * bwd_krows(K) * 16 + 2 * kBwdWaves * 16
+  return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 2 * 2 * kF * 16 +
+                       2 * 2 * bwd_krows(K) * 16 + 3 * 2 * 16 * 64 / 2 + 2 * kBwdWaves * 16
                  : kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 3 * 2 * kF * 16 +
                        2 * 2 * bwd_krows(K) * 16;
 }
@@ -862,6 +864,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // step 3 on the fp16 MFMA with split operands (see filter_fwd_x3_kernel)
   // when the LDS allows it (K <= 64); the wide variant keeps it on fp32
   constexpr bool kX3 = KSMAX <= 16;
+  // split scales: S4 of every split product; h enters step 4 as h beta_h, and
+  // g, g' enter step 1 as g beta_0, g' beta_1 (so hi S4 stays in the fp16
+  // range for |h| < 2^20, |g| < 512 and |g'| < 2047)
+  constexpr float kS4 = 2048.0f, kBetaH = 0.0625f, kBetaG0 = 0.0625f, kBetaG1 = 0.015625f;
   // fp32: W2^T A fragments [8 t][8 u][64 l] float4; x3: W2^T as two fp16
   // planes (hi, lo S) of [8 t][4 s][64 l][8]
   float* w2ts = lds;
@@ -876,10 +882,12 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // next tile's TT (step 2), all in program order.
   float* AT = kX3 ? TT : HT + 2 * kF * 16;
   float* GT0 = kX3 ? HT + 2 * kF * 16 : AT + 2 * kF * 16;  // [2 bufs][2][kRows][16] g, g'
-  // split path: GT0 holds the fp16 planes of g, g' (step 6), GT32 an fp32
-  // copy in the [row][pair] layout for step 1
-  float* GT32 = GT0 + 2 * 2 * kRows * 16;
-  float* PMAX = GT32 + (kX3 ? 2 * 2 * kRows * 16 : 0);  // x3: [2 bufs][2][16] max |t| (bits)
+  // split path: GT0 holds the [row][pair] fp16 planes of g, g' (step 6); G1h
+  // the pair-major planes (hi, hi S4, lo S4) of g beta_0, g' beta_1 for step
+  // 1, [3][2][16 pairs][64 k], 8-byte chunk c of pair n's row stored at c ^ n
+  // (one buffer: written in step 5 after the barrier that follows step 1)
+  _Float16* G1h = reinterpret_cast<_Float16*>(GT0 + 2 * 2 * kRows * 16);
+  float* PMAX = GT0 + 2 * 2 * kRows * 16 + (kX3 ? 3 * 2 * 16 * 64 / 2 : 0);  // x3: [2][2][16] bits
   unsigned* PMAXu = reinterpret_cast<unsigned*>(PMAX);
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
@@ -907,11 +915,27 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   }
 
   // W1 fragment of feature tile w stays in registers: W1[16w + n][4s + q]
+  // (fp32 path) or, on the split path, the two planes (hi, lo S4) of the
+  // v_mfma_f32_16x16x16f16 A fragments W1[16w + n][16b + 4q + j]
   float w1f[KSMAX];
+  halfx4 w1h[KSMAX / 4], w1l[KSMAX / 4];
+  if constexpr (kX3) {
 #pragma unroll
-  for (int s = 0; s < KSMAX; ++s) {
-    const int k = 4 * s + q;
-    w1f[s] = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
+    for (int b = 0; b < KSMAX / 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 16 * b + 4 * q + j;
+        const float v = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
+        const _Float16 hv1 = (_Float16)v;
+        w1h[b][j] = hv1;
+        w1l[b][j] = (_Float16)((v - (float)hv1) * kS4);
+      }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KSMAX; ++s) {
+      const int k = 4 * s + q;
+      w1f[s] = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
+    }
   }
   float bias[4];
 #pragma unroll
@@ -958,7 +982,6 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // plane rows 16u + (n ^ (n >> 2)), same stream and pairs
   // split scales of step 4: t rw (rw = 2^k, with |t| rw < 4 over every tile
   // seen so far), h beta; the accumulators hold S4 rw beta dW2
-  constexpr float kS4 = 2048.0f, kBetaH = 0.0625f;
   float rw = 1.0f, trun = 0.0f;
   float ra = 1.0f, arun = 0.0f;  // the same for ab in step 6 (no beta: |g| <= 1)
 
@@ -997,10 +1020,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           GTh[kRows * 16 + o] = h1;
           GTh[2 * kRows * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
           GTh[3 * kRows * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
-          float* G32 = GT32 + bsel * 2 * kRows * 16;
-          const int o32 = rp_at(4 * s + q, n);
-          G32[o32] = v0;
-          G32[kRows * 16 + o32] = v1;
+          // step 1's copy (k = 4s + q: chunk s, element q)
+          const int o1 = n * 64 + 4 * (s ^ n) + q;
+          const float u0 = v0 * kBetaG0, u1 = v1 * kBetaG1;
+          const _Float16 c0 = (_Float16)u0, c1 = (_Float16)u1;
+          G1h[o1] = c0;
+          G1h[1024 + o1] = c1;
+          G1h[2048 + o1] = (_Float16)((float)c0 * kS4);
+          G1h[3072 + o1] = (_Float16)((float)c1 * kS4);
+          G1h[4096 + o1] = (_Float16)((u0 - (float)c0) * kS4);
+          G1h[5120 + o1] = (_Float16)((u1 - (float)c1) * kS4);
         } else {
           const int o = rp_at(4 * s + q, n);
           GTb[o] = g * vm;
@@ -1076,22 +1105,43 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     // 1. a, a' of feature tile w (two accumulators each: shorter MFMA chains)
     floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
     floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kX3) {
+      // 16-wide k blocks; B fragment = halfx4 of pair n, k = 16b + 4q .. + 3;
+      // slabs (plane, stream) of 256 halfx4: hi (0, 1), hi S (2, 3), lo S (4, 5)
+      const halfx4* g1v = reinterpret_cast<const halfx4*>(G1h);
 #pragma unroll
-    for (int s = 0; s < KSMAX; ++s) {
-      const float* G1 = kX3 ? GT32 + buf * 2 * kRows * 16 : GT;
-      const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
-      const float g = G1[o];
-      const float gd = G1[kRows * 16 + o];
-      if (s & 1) {
-        a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
-        ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
-      } else {
-        a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
-        ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
+      for (int b = 0; b < KSMAX / 4; ++b) {
+        const int c = n * 16 + ((4 * b + q) ^ n);
+        const halfx4 h0 = g1v[c], s0 = g1v[512 + c], l0 = g1v[1024 + c];
+        const halfx4 h1 = g1v[256 + c], s1 = g1v[768 + c], l1 = g1v[1280 + c];
+        floatx4& A0 = (b & 1) ? a_o : a;
+        floatx4& A1 = (b & 1) ? ad_o : ad;
+        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], s0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], s1, A1, 0, 0, 0);
+        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], l0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], l1, A1, 0, 0, 0);
+        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1l[b], h0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1l[b], h1, A1, 0, 0, 0);
       }
+      a = (a + a_o) * (1.0f / (kS4 * kBetaG0));
+      ad = (ad + ad_o) * (1.0f / (kS4 * kBetaG1));
+    } else {
+#pragma unroll
+      for (int s = 0; s < KSMAX; ++s) {
+        const int o = oG1[s & 1] + 64 * s;  // rp_at(4s + q, n)
+        const float g = GT[o];
+        const float gd = GT[kRows * 16 + o];
+        if (s & 1) {
+          a_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a_o, 0, 0, 0);
+          ad_o = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad_o, 0, 0, 0);
+        } else {
+          a = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], g, a, 0, 0, 0);
+          ad = __builtin_amdgcn_mfma_f32_16x16x4f32(w1f[s], gd, ad, 0, 0, 0);
+        }
+      }
+      a += a_o;
+      ad += ad_o;
     }
-    a += a_o;
-    ad += ad_o;
     // 2. h, h', activation derivatives; publish t, t', h, h'
     float act1[4], act2[4];
     float hv[4], hdv[4];
