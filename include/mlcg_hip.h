@@ -328,6 +328,22 @@ int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
                    const float* e, const float* f, float* out0, float* out1,
                    void* stream);
 
+/* Two consecutive linears of the interaction block in one pass over the
+ * rows: mlcg_node_gemm(x, W, ..., epilogue) as above (ACT, DACT or DACT2),
+ * then out2 = v W2^T (v W2 when transpose_w != 0) [+ bias2] [+ residual2],
+ * v being the first call's principal output (out1 for ACT and DACT, out0 for
+ * DACT2), which is still stored.  The results equal those of the two
+ * separate mlcg_node_gemm calls bit for bit.  Replaces the pairs
+ * schnet.py:347 lin2 -> 259-261 act + lin (+ the residual of schnet.py:153)
+ * and their transposes in the backward, tangent and double backward sweeps;
+ * the x -> v -> out2 chain reads x once and v never back. */
+int mlcg_node_gemm2(const float* x, int64_t rows, int features, const float* W,
+                    int transpose_w, const float* bias, const float* residual,
+                    int epilogue, int act, const float* z, const float* s,
+                    const float* e, const float* f, float* out0, float* out1,
+                    const float* W2, const float* bias2, const float* residual2,
+                    float* out2, void* stream);
+
 /* out [128, 128] (+)= a1^T b1 (+ a2^T b2) for [rows, 128] inputs (a2/b2 may
  * be NULL) and, when colsum_a1 is non-NULL, colsum_a1 [128] (+)= the column
  * sums of a1 (a bias gradient); deterministic split over contiguous row

@@ -64,6 +64,8 @@ _SIGNATURES = {
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
     "mlcg_node_gemm": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
                        _P],
+    "mlcg_node_gemm2": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
+                        _P, _P, _P, _P, _P],
     "mlcg_out_forward": [_P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P,
                          _P],
     "mlcg_out_rev2_workspace_floats": [_I64, _I32],

@@ -195,6 +195,9 @@ __global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __res
 #ifndef MLCG_NODE_GEMM_PER_CU
 #define MLCG_NODE_GEMM_PER_CU 3
 #endif
+#ifndef MLCG_NODE_GEMM2_PER_CU
+#define MLCG_NODE_GEMM2_PER_CU 2
+#endif
 constexpr int kGemmRows = MLCG_NODE_GEMM_ROWS;   // rows per tile
 constexpr int kGemmRT = kGemmRows / 16;          // 16-row MFMA tiles per tile
 constexpr int kGemmThreads = 256;                // wave w owns columns 32w..32w+31
@@ -292,9 +295,11 @@ __device__ __forceinline__ void gemm_epilogue_load(EpiIn& in, int64_t r, int col
   }
 }
 
-// Epilogue on one float4 of the product (row r, columns col..col+3).
+// Epilogue on one float4 of the product (row r, columns col..col+3); returns
+// the value a following product takes as its input (out0 for PLAIN and DACT2,
+// out1 for ACT and DACT).
 template <int MODE>
-__device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col, const EpiIn& in,
+__device__ __forceinline__ float4 gemm_epilogue(float4 y, int64_t r, int col, const EpiIn& in,
                                               const float* __restrict__ bias, int act,
                                               bool has_ef, float* __restrict__ out0,
                                               float* __restrict__ out1) {
@@ -306,10 +311,13 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col, cons
   y.x += in.res.x; y.y += in.res.y; y.z += in.res.z; y.w += in.res.w;
   if (MODE == MLCG_NODE_PLAIN) {
     st4(out0 + o, y);
+    return y;
   } else if (MODE == MLCG_NODE_ACT) {
     if (out0) st4(out0 + o, y);
-    st4(out1 + o, float4{mlcg_act_value(act, y.x), mlcg_act_value(act, y.y),
-                         mlcg_act_value(act, y.z), mlcg_act_value(act, y.w)});
+    const float4 a{mlcg_act_value(act, y.x), mlcg_act_value(act, y.y),
+                   mlcg_act_value(act, y.z), mlcg_act_value(act, y.w)};
+    st4(out1 + o, a);
+    return a;
   } else {
     const float4 s = in.s, z = in.z;
     float4 d1, d2;
@@ -319,7 +327,9 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col, cons
     act_d1d2(act, z.w, s.w, d1.w, d2.w);
     if (MODE == MLCG_NODE_DACT) {
       if (out0) st4(out0 + o, y);
-      st4(out1 + o, float4{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w});
+      const float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
+      st4(out1 + o, v);
+      return v;
     } else {  // MLCG_NODE_DACT2
       float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
       if (has_ef) {
@@ -330,29 +340,18 @@ __device__ __forceinline__ void gemm_epilogue(float4 y, int64_t r, int col, cons
         v.w += e.w * d2.w * f.w;
       }
       st4(out0 + o, v);
+      return v;
     }
   }
 }
 
-// y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true), on
-// v_mfma_f32_16x16x32_f16 with split operands: x as three planes (staged
-// per tile, scaled per row), B as two planes (hi, lo S) held in registers.
-// MFMA k block kb of lane group q = l/16 covers k = 32 kb + 8q .. + 7.
-template <int MODE, bool kXW>
-__global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
-    const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
-    const float* __restrict__ bias, const float* __restrict__ residual, int act,
-    const float* __restrict__ zin, const float* __restrict__ sin_,
-    const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
-    float* __restrict__ out1) {
-  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
-  __shared__ float rinv[2][kGemmRows];
-  __shared__ float ys[kGemmRows * kTRow];
-  const int w = threadIdx.x / MLCG_WAVE;
-  const int l = mlcg_lane();
-  const int q = l >> 4, n = l & 15;
-  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  halfx8 bh[2][kF / 32], bl[2][kF / 32];
+// B = W^T (kXW = false, torch Linear) or B = W (kXW = true) as two fp16
+// planes (hi, lo S) in registers: plane[c][kb] of lane (q, n) in wave w holds
+// B[32 kb + 8q + j][32 w + 16 c + n], j = 0..7 (the B operand layout of
+// v_mfma_f32_16x16x32_f16).
+template <bool kXW>
+__device__ __forceinline__ void gemm_load_w(halfx8 (&bh)[2][kF / 32], halfx8 (&bl)[2][kF / 32],
+                                            const float* __restrict__ W, int w, int q, int n) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int col = 32 * w + 16 * c + n;
@@ -376,6 +375,65 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
       }
     }
   }
+}
+
+// The product of a staged tile (three planes in xs, row scales in rinv) and
+// the B planes: wave w's 32 columns of all kGemmRows rows go to ys, with the
+// row scales undone.
+__device__ __forceinline__ void gemm_tile(const _Float16* xs, const float* rinv,
+                                          const halfx8 (&bh)[2][kF / 32],
+                                          const halfx8 (&bl)[2][kF / 32], float* ys, int w,
+                                          int q, int n) {
+  floatx4 acc[kGemmRT][2];
+#pragma unroll
+  for (int r = 0; r < kGemmRT; ++r)
+    acc[r][0] = acc[r][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const halfx8* xv = reinterpret_cast<const halfx8*>(xs);
+#pragma unroll
+  for (int kb = 0; kb < kF / 32; ++kb) {
+#pragma unroll
+    for (int r = 0; r < kGemmRT; ++r) {
+      const int o = (16 * r + n) * (kF / 8) + ((4 * kb + q) ^ n);
+      const halfx8 ah = xv[o], ahs = xv[kXPlane / 8 + o], al = xv[2 * kXPlane / 8 + o];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh[c][kb], acc[r][c], 0, 0, 0);
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[c][kb], acc[r][c], 0, 0, 0);
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[c][kb], acc[r][c], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kGemmRT; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * r + 4 * q + i;
+      const float u = rinv[row];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) ys[row * kTRow + 32 * w + 16 * c + n] = acc[r][c][i] * u;
+    }
+}
+
+// y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true), on
+// v_mfma_f32_16x16x32_f16 with split operands: x as three planes (staged
+// per tile, scaled per row), B as two planes (hi, lo S) held in registers.
+// MFMA k block kb of lane group q = l/16 covers k = 32 kb + 8q .. + 7.
+template <int MODE, bool kXW>
+__global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
+    const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
+    const float* __restrict__ bias, const float* __restrict__ residual, int act,
+    const float* __restrict__ zin, const float* __restrict__ sin_,
+    const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
+    float* __restrict__ out1) {
+  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
+  __shared__ float rinv[2][kGemmRows];
+  __shared__ float ys[kGemmRows * kTRow];
+  const int w = threadIdx.x / MLCG_WAVE;
+  const int l = mlcg_lane();
+  const int q = l >> 4, n = l & 15;
+  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  halfx8 bh[2][kF / 32], bl[2][kF / 32];
+  gemm_load_w<kXW>(bh, bl, W, w, q, n);
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
   gemm_load_x(pf, x, t, rows);
@@ -395,34 +453,7 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
       gemm_epilogue_load<MODE>(ein_[m], r < rows ? r : 0, 4 * (c & 31), residual, act, zin,
                                sin_, ein, fin);
     }
-    floatx4 acc[kGemmRT][2];
-#pragma unroll
-    for (int r = 0; r < kGemmRT; ++r)
-      acc[r][0] = acc[r][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const halfx8* xv = reinterpret_cast<const halfx8*>(xs[buf]);
-#pragma unroll
-    for (int kb = 0; kb < kF / 32; ++kb) {
-#pragma unroll
-      for (int r = 0; r < kGemmRT; ++r) {
-        const int o = (16 * r + n) * (kF / 8) + ((4 * kb + q) ^ n);
-        const halfx8 ah = xv[o], ahs = xv[kXPlane / 8 + o], al = xv[2 * kXPlane / 8 + o];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh[c][kb], acc[r][c], 0, 0, 0);
-          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[c][kb], acc[r][c], 0, 0, 0);
-          acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[c][kb], acc[r][c], 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < kGemmRT; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * r + 4 * q + i;
-        const float u = rinv[buf][row];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) ys[row * kTRow + 32 * w + 16 * c + n] = acc[r][c][i] * u;
-      }
+    gemm_tile(xs[buf], rinv[buf], bh, bl, ys, w, q, n);
     if (has_next) gemm_stage_x3(xs[buf ^ 1], rinv[buf ^ 1], pf);
     __syncthreads();
 #pragma unroll
@@ -435,6 +466,92 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
                             ein != nullptr, out0, out1);
     }
     __syncthreads();
+    buf ^= 1;
+  }
+}
+
+// Two consecutive node linears in one pass over the rows:
+//     (out0, out1) = epilogue_MODE(x B + bias [+ residual])      as node_gemm
+//     out2 = v B2 [+ bias2] [+ residual2]
+// where v is the first product's principal output (out1 for ACT / DACT,
+// out0 for DACT2) and B, B2 are both W^T or both W (kXW).  v is stored and
+// staged from registers into a second set of planes, so each tile reads x
+// once and never reads v back.  The products, scalings and epilogue
+// arithmetic are those of two node_gemm_kernel launches, so the results are
+// the same bit for bit.  Both B operands stay in registers (about 128 VGPRs).
+template <int MODE, bool kXW>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void node_gemm2_kernel(
+    const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
+    const float* __restrict__ bias, const float* __restrict__ residual, int act,
+    const float* __restrict__ zin, const float* __restrict__ sin_,
+    const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
+    float* __restrict__ out1, const float* __restrict__ W2, const float* __restrict__ bias2,
+    const float* __restrict__ residual2, float* __restrict__ out2) {
+  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
+  __shared__ __align__(16) _Float16 vs[3 * kXPlane];
+  __shared__ float rinv[3][kGemmRows];
+  __shared__ float ys[2][kGemmRows * kTRow];
+  const int w = threadIdx.x / MLCG_WAVE;
+  const int l = mlcg_lane();
+  const int q = l >> 4, n = l & 15;
+  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  halfx8 bh[2][kF / 32], bl[2][kF / 32], ch[2][kF / 32], cl[2][kF / 32];
+  gemm_load_w<kXW>(bh, bl, W, w, q, n);
+  gemm_load_w<kXW>(ch, cl, W2, w, q, n);
+  int64_t t = blockIdx.x;
+  float4 pf[kGemmXPer];
+  gemm_load_x(pf, x, t, rows);
+  gemm_stage_x3(xs[0], rinv[0], pf);
+  __syncthreads();
+  int buf = 0;
+  // LDS reuse across iterations: xs[buf] and ys[0] are last read before the
+  // second barrier of an iteration, vs and ys[1] before the third, and each
+  // is next written after at least one further barrier.
+  for (; t < tiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < tiles;
+    if (has_next) gemm_load_x(pf, x, tn, rows);
+    EpiIn ein_[kGemmXPer];
+    float4 res2[kGemmXPer];
+#pragma unroll
+    for (int m = 0; m < kGemmXPer; ++m) {
+      const int c = threadIdx.x + m * kGemmThreads;
+      const int64_t r = t * kGemmRows + (c >> 5);
+      const int64_t rr = r < rows ? r : 0;
+      gemm_epilogue_load<MODE>(ein_[m], rr, 4 * (c & 31), residual, act, zin, sin_, ein, fin);
+      res2[m] = residual2 ? ld4(residual2 + rr * kF + 4 * (c & 31)) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    gemm_tile(xs[buf], rinv[buf], bh, bl, ys[0], w, q, n);
+    if (has_next) gemm_stage_x3(xs[buf ^ 1], rinv[buf ^ 1], pf);
+    __syncthreads();
+    float4 v[kGemmXPer];
+#pragma unroll
+    for (int m = 0; m < kGemmXPer; ++m) {
+      const int c = threadIdx.x + m * kGemmThreads;
+      const int rr = c >> 5, col = 4 * (c & 31);
+      const int64_t r = t * kGemmRows + rr;
+      v[m] = float4{0.f, 0.f, 0.f, 0.f};  // rows past the end enter the product as zeros
+      if (r < rows)
+        v[m] = gemm_epilogue<MODE>(ld4(ys[0] + rr * kTRow + col), r, col, ein_[m], bias, act,
+                                   ein != nullptr, out0, out1);
+    }
+    gemm_stage_x3(vs, rinv[2], v);
+    __syncthreads();
+    gemm_tile(vs, rinv[2], ch, cl, ys[1], w, q, n);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kGemmXPer; ++m) {
+      const int c = threadIdx.x + m * kGemmThreads;
+      const int rr = c >> 5, col = 4 * (c & 31);
+      const int64_t r = t * kGemmRows + rr;
+      if (r < rows) {
+        EpiIn e2;
+        e2.res = res2[m];
+        gemm_epilogue<MLCG_NODE_PLAIN>(ld4(ys[1] + rr * kTRow + col), r, col, e2, bias2, act,
+                                       false, out2, nullptr);
+      }
+    }
     buf ^= 1;
   }
 }
@@ -523,14 +640,26 @@ void launch_node_gemm(bool xw, dim3 grid, hipStream_t s, const float* x, int64_t
                        rows, W, bias, residual, act, z, sv, e, f, out0, out1);
 }
 
-}  // namespace
+template <int MODE>
+void launch_node_gemm2(bool xw, dim3 grid, hipStream_t s, const float* x, int64_t rows,
+                       const float* W, const float* bias, const float* residual, int act,
+                       const float* z, const float* sv, const float* e, const float* f,
+                       float* out0, float* out1, const float* W2, const float* bias2,
+                       const float* residual2, float* out2) {
+  if (xw)
+    hipLaunchKernelGGL((node_gemm2_kernel<MODE, true>), grid, dim3(kGemmThreads), 0, s, x,
+                       rows, W, bias, residual, act, z, sv, e, f, out0, out1, W2, bias2,
+                       residual2, out2);
+  else
+    hipLaunchKernelGGL((node_gemm2_kernel<MODE, false>), grid, dim3(kGemmThreads), 0, s, x,
+                       rows, W, bias, residual, act, z, sv, e, f, out0, out1, W2, bias2,
+                       residual2, out2);
+}
 
-extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
-                              int transpose_w, const float* bias, const float* residual,
-                              int epilogue, int act, const float* z, const float* s,
-                              const float* e, const float* f, float* out0, float* out1,
-                              void* stream) {
-  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+// Argument checks shared by mlcg_node_gemm and mlcg_node_gemm2.
+int check_node_gemm(const float* x, int64_t rows, const float* W, int epilogue, int act,
+                    const float* z, const float* s, const float* e, const float* f,
+                    const float* out0, const float* out1) {
   MLCG_REQUIRE(rows >= 0 && (act == MLCG_ACT_TANH || act == MLCG_ACT_SSP));
   MLCG_REQUIRE((e == nullptr) == (f == nullptr));
   MLCG_REQUIRE(epilogue >= MLCG_NODE_PLAIN && epilogue <= MLCG_NODE_DACT2);
@@ -543,6 +672,19 @@ extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const 
     default: break;
   }
   MLCG_REQUIRE(x && W);
+  return MLCG_OK;
+}
+
+}  // namespace
+
+extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
+                              int transpose_w, const float* bias, const float* residual,
+                              int epilogue, int act, const float* z, const float* s,
+                              const float* e, const float* f, float* out0, float* out1,
+                              void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
+  if (rc != MLCG_OK || rows == 0) return rc;
   const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
   const dim3 grid(mlcg_persistent_groups(tiles, MLCG_NODE_GEMM_PER_CU));
   hipStream_t st = mlcg_stream(stream);
@@ -563,6 +705,38 @@ extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const 
     default:
       launch_node_gemm<MLCG_NODE_DACT2>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
                                         f, out0, out1);
+      break;
+  }
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_node_gemm2(const float* x, int64_t rows, int features, const float* W,
+                               int transpose_w, const float* bias, const float* residual,
+                               int epilogue, int act, const float* z, const float* s,
+                               const float* e, const float* f, float* out0, float* out1,
+                               const float* W2, const float* bias2, const float* residual2,
+                               float* out2, void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(epilogue != MLCG_NODE_PLAIN);
+  const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
+  if (rc != MLCG_OK || rows == 0) return rc;
+  MLCG_REQUIRE(W2 && out2);
+  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  const dim3 grid(mlcg_persistent_groups(tiles, MLCG_NODE_GEMM2_PER_CU));
+  hipStream_t st = mlcg_stream(stream);
+  const bool xw = transpose_w != 0;
+  switch (epilogue) {
+    case MLCG_NODE_ACT:
+      launch_node_gemm2<MLCG_NODE_ACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+                                       f, out0, out1, W2, bias2, residual2, out2);
+      break;
+    case MLCG_NODE_DACT:
+      launch_node_gemm2<MLCG_NODE_DACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+                                        f, out0, out1, W2, bias2, residual2, out2);
+      break;
+    default:
+      launch_node_gemm2<MLCG_NODE_DACT2>(xw, grid, st, x, rows, W, bias, residual, act, z, s,
+                                         e, f, out0, out1, W2, bias2, residual2, out2);
       break;
   }
   return mlcg_launch_status();

@@ -196,6 +196,42 @@ def _lin_dact2(x, A, z, s, act, e, f):
     return v if e is None else v + e * d2 * f
 
 
+# Consecutive node linears in one kernel (mlcg_node_gemm2): the first
+# product's activation output feeds the second without a round trip through
+# memory; results are bit-identical to the two separate calls.
+
+def _gemm2_ok(x, A, B):
+    return ops._node_gemm_ok(x, A) and ops._node_gemm_ok(x, B)
+
+
+def _lin_act_lin(x, A, c, act, want_z, B, cb, residual):
+    """(z, s, s B^T + cb + residual) with (z, s) = _lin_act(x, A, c, act)."""
+    if _gemm2_ok(x, A, B):
+        return ops.node_gemm2(x, A, B, bias=c, epilogue=ops.NODE_ACT, act=act,
+                              want_out0=want_z, bias2=cb, residual2=residual)
+    z, s = _lin_act(x, A, c, act, want_z)
+    return z, s, ops.node_linear(s, B, bias=cb, residual=residual)
+
+
+def _lin_dact_lin(x, A, z, s, act, transpose, B, residual=None):
+    """(y, v, v B^T [+ residual]) (v B with transpose), (y, v) = _lin_dact(...)."""
+    if _gemm2_ok(x, A, B):
+        return ops.node_gemm2(x, A, B, transpose=transpose, epilogue=ops.NODE_DACT, act=act,
+                              z=z, s=s, residual2=residual)
+    y, v = _lin_dact(x, A, z, s, act, transpose)
+    return y, v, ops.node_linear(v, B, transpose=transpose, residual=residual)
+
+
+def _lin_dact2_lin(x, A, z, s, act, e, f, B):
+    """(v, v B) with v = _lin_dact2(x, A, z, s, act, e, f)."""
+    if _gemm2_ok(x, A, B):
+        v, _, out = ops.node_gemm2(x, A, B, transpose=True, epilogue=ops.NODE_DACT2, act=act,
+                                   z=z, s=s, e=e, f=f)
+        return v, out
+    v = _lin_dact2(x, A, z, s, act, e, f)
+    return v, ops.node_linear(v, B, transpose=True)
+
+
 def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             graph: ops.PairGraph, save: bool = True,
             rev_seed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, State]:
@@ -211,9 +247,10 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             st.dist = dist
         y = ops.node_linear(x, bp.A1)
         agg = ops.cfconv_gather(y, W, graph)
-        # z itself is only read back by the shifted-softplus derivatives
-        z, s = _lin_act(agg, bp.A2, bp.c2, spec.block_act,
-                        want_z=save and spec.block_act != ACT_TANH)
+        # z itself is only read back by the shifted-softplus derivatives;
+        # x_next = x + lin(act(z))
+        z, s, x_next = _lin_act_lin(agg, bp.A2, bp.c2, spec.block_act,
+                                    save and spec.block_act != ACT_TANH, bp.A3, bp.c3, x)
         st.W.append(W)
         st.Wd.append(Wd)
         if save:
@@ -222,7 +259,7 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             st.agg.append(agg)
             st.z.append(z)
             st.s.append(s)
-        x = ops.node_linear(s, bp.A3, bias=bp.c3, residual=x)  # x + lin(act(z))
+        x = x_next
     st.xL = x
     if _out_fused(P):
         o, oz, os_, xbar = ops.out_forward(x, P.out_w[0], P.out_b[0], P.out_w[1], P.out_b[1],
@@ -279,8 +316,8 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     st.ybar1 = [None] * nb
     for k in range(nb - 1, -1, -1):
         bp = P.blocks[k]
-        sbar, zbar = _lin_dact(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True)
-        gagg = ops.node_linear(zbar, bp.A2, transpose=True)
+        sbar, zbar, gagg = _lin_dact_lin(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True,
+                                         bp.A2)
         ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar)
         st.xbar_out[k] = xbar
         st.sbar1[k] = sbar
@@ -304,13 +341,14 @@ def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> None:
     for k, bp in enumerate(P.blocks):
         ydot = None if xdot is None else ops.node_linear(xdot, bp.A1)
         aggdot = ops.cfconv_gather_tangent(ydot, st.y[k], st.W[k], st.Wd[k], st.ddot, graph)
-        zdot, sdot = _lin_dact(aggdot, bp.A2, st.z[k], st.s[k], spec.block_act, False)
+        zdot, sdot, xdot_next = _lin_dact_lin(aggdot, bp.A2, st.z[k], st.s[k], spec.block_act,
+                                              False, bp.A3, residual=xdot)
         st.xdot_in.append(xdot)
         st.ydot.append(ydot)
         st.aggdot.append(aggdot)
         st.zdot.append(zdot)
         st.sdot.append(sdot)
-        xdot = ops.node_linear(sdot, bp.A3, residual=xdot)
+        xdot = xdot_next
     st.xdotL = xdot
     st.odot = None
     if _out_fused(P):
@@ -436,13 +474,13 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
         if tangent_on:
-            zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, st.sbar1[k],
-                               st.zdot[k])
             gA3, gc3 = tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k], colsum=True)
+            zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
+                                          st.sbar1[k], st.zdot[k], bp.A2)
         else:
-            zbar2 = _lin_dact2(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act, None, None)
             gA3, gc3 = tmm(xbar2, st.s[k], colsum=True)
-        gagg2 = ops.node_linear(zbar2, bp.A2, transpose=True)
+            zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
+                                          None, None, bp.A2)
         if tangent_on:
             gA2, gc2 = tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], colsum=True)
         else:

@@ -343,6 +343,46 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
     return out0, out1
 
 
+def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bool = False,
+               bias: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+               epilogue: int = NODE_ACT, act: int = 0, z: Optional[torch.Tensor] = None,
+               s: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
+               f: Optional[torch.Tensor] = None, want_out0: bool = True,
+               bias2: Optional[torch.Tensor] = None, residual2: Optional[torch.Tensor] = None,
+               ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor], torch.Tensor]:
+    """(out0, out1, out2): node_gemm(x, W, ...) with an ACT, DACT or DACT2
+    epilogue followed, in the same kernel (mlcg_node_gemm2), by
+    out2 = v W2^T (v W2 with transpose) [+ bias2] [+ residual2], v being out1
+    (ACT, DACT) or out0 (DACT2).  Bit-identical to the two node_gemm calls."""
+    require_device(x)
+    _check(epilogue in (NODE_ACT, NODE_DACT, NODE_DACT2),
+           "node_gemm2 takes an ACT, DACT or DACT2 first epilogue")
+    _check(_node_gemm_ok(x, W) and _node_gemm_ok(x, W2),
+           f"node_gemm2 takes [N, {NUM_FILTERS}] float32 rows and two "
+           f"[{NUM_FILTERS}, {NUM_FILTERS}] weights, got {tuple(x.shape)} / "
+           f"{tuple(W.shape)} / {tuple(W2.shape)}")
+    n = x.shape[0]
+    dev = x.device
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    x, W, W2, bias, bias2, residual, residual2, z, s, e, f = map(
+        c, (x, W, W2, bias, bias2, residual, residual2, z, s, e, f))
+    for t in (residual, residual2, z, s, e, f):
+        _check(t is None or (t.shape == x.shape and t.dtype == torch.float32
+                             and t.device == dev), "epilogue tensors must match x")
+    for b in (bias, bias2):
+        _check(b is None or b.numel() == NUM_FILTERS, "bias must have 128 entries")
+    out0 = out1 = None
+    if epilogue == NODE_DACT2 or want_out0:
+        out0 = torch.empty_like(x)
+    if epilogue in (NODE_ACT, NODE_DACT):
+        out1 = torch.empty_like(x)
+    out2 = torch.empty_like(x)
+    call("mlcg_node_gemm2", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
+         ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
+         ptr(out1), ptr(W2), ptr(bias2), ptr(residual2), ptr(out2), stream_handle(dev))
+    return out0, out1, out2
+
+
 def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = None,
              b2: Optional[torch.Tensor] = None, colsum: bool = False):
     """a1^T b1 (+ a2^T b2) reduced over the rows; with colsum, returns

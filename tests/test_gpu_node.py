@@ -122,6 +122,71 @@ def test_node_gemm_deterministic_and_checks():
         ops.node_gemm(x, W, epilogue=ops.NODE_DACT, act=0)  # z, s missing
 
 
+@pytest.mark.parametrize("rows", [1, 17, 1000, 17920, 30001])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("act", [0, 1])
+def test_node_gemm2_matches_two_calls(rows, transpose, act):
+    """mlcg_node_gemm2 (two consecutive linears in one kernel) is bitwise the
+    pair of mlcg_node_gemm calls it replaces, for every first epilogue, with
+    and without the second bias and residual, and checked once against fp64
+    torch so that a shared mistake in both paths cannot pass."""
+    from mlcg_amd import ops
+
+    print(f"node_gemm2 rows={rows} transpose={transpose} act={act}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows * 4 + 2 * int(transpose) + act + 99)
+    rnd = lambda *s: torch.randn(*s, device="cuda", generator=g)  # noqa: E731
+    x, r, r2, z, e, f = (rnd(rows, 128) for _ in range(6))
+    W, W2 = rnd(128, 128) / 11, rnd(128, 128) / 11
+    b, b2 = rnd(128), rnd(128)
+    s = _act64(z.double(), act).float()
+    kw = dict(transpose=transpose, act=act)
+
+    # ACT then a linear with bias and residual (the interaction block's forward)
+    z0, s0 = ops.node_gemm(x, W, bias=b, residual=r, epilogue=ops.NODE_ACT, **kw)
+    ref2 = ops.node_gemm(s0, W2, transpose=transpose, bias=b2, residual=r2)[0]
+    g0, g1, g2 = ops.node_gemm2(x, W, W2, bias=b, residual=r, epilogue=ops.NODE_ACT,
+                                bias2=b2, residual2=r2, **kw)
+    assert torch.equal(g0, z0) and torch.equal(g1, s0) and torch.equal(g2, ref2)
+    W2d = W2.double()
+    y2 = s0.double().mm(W2d if transpose else W2d.t()) + b2.double() + r2.double()
+    assert rel_err(g2, y2) < 1e-6
+    g0, g1, g2 = ops.node_gemm2(x, W, W2, bias=b, epilogue=ops.NODE_ACT, want_out0=False, **kw)
+    z0, s0 = ops.node_gemm(x, W, bias=b, epilogue=ops.NODE_ACT, **kw)
+    assert g0 is None and torch.equal(g1, s0)
+    assert torch.equal(g2, ops.node_gemm(s0, W2, transpose=transpose)[0])
+
+    # DACT then a linear (reverse and tangent sweeps), with and without residual
+    y0, v0 = ops.node_gemm(x, W, epilogue=ops.NODE_DACT, z=z, s=s, **kw)
+    for res2 in (None, r2):
+        g0, g1, g2 = ops.node_gemm2(x, W, W2, epilogue=ops.NODE_DACT, z=z, s=s, residual2=res2,
+                                    **kw)
+        assert torch.equal(g0, y0) and torch.equal(g1, v0)
+        assert torch.equal(g2, ops.node_gemm(v0, W2, transpose=transpose, residual=res2)[0])
+
+    # DACT2 (with and without the e, f term) then a linear (double backward)
+    for ef in ((None, None), (e, f)):
+        v0, _ = ops.node_gemm(x, W, epilogue=ops.NODE_DACT2, z=z, s=s, e=ef[0], f=ef[1], **kw)
+        g0, g1, g2 = ops.node_gemm2(x, W, W2, epilogue=ops.NODE_DACT2, z=z, s=s, e=ef[0],
+                                    f=ef[1], **kw)
+        assert g1 is None and torch.equal(g0, v0)
+        assert torch.equal(g2, ops.node_gemm(v0, W2, transpose=transpose)[0])
+
+
+def test_node_gemm2_checks():
+    from mlcg_amd import ops
+
+    x = torch.randn(100, 128, device="cuda")
+    W = torch.randn(128, 128, device="cuda")
+    out = ops.node_gemm2(x[:0], W, W, epilogue=ops.NODE_ACT)
+    assert out[2].shape == (0, 128)
+    with pytest.raises(RuntimeError):
+        ops.node_gemm2(x, W, W, epilogue=ops.NODE_PLAIN)
+    with pytest.raises(RuntimeError):
+        ops.node_gemm2(x, W, W[:, :64], epilogue=ops.NODE_ACT)
+    with pytest.raises(RuntimeError):
+        ops.node_gemm2(x, W, W, epilogue=ops.NODE_DACT, act=0)  # z, s missing
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,num_types", [(0, 5), (1, 1), (17920, 35), (5000, 128), (300, 7)])
 def test_type_sum_matches_index_add(rows, num_types):
