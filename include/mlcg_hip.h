@@ -352,24 +352,25 @@ int mlcg_node_gemm2(const float* x, int64_t rows, int features, const float* W,
  * outputs.  Replaces the weight- and bias-gradient reductions of the same
  * linears (the autograd backward of schnet.py:259-261,343,347 through the
  * double backward). */
-/* out [num_types, 128] = for each type t the sum of the rows of x [rows, 128]
- * whose types[row] == t: the gradient of the bead-type embedding table
- * (schnet.py:132, `x = self.embedding_layer(data.atom_types)`, whose
- * autograd backward scatters the adjoint of x into the table).  One
- * workgroup per contiguous row range sums in a fixed order and the partials
- * are added in workgroup order, so the result is run-to-run identical.
- * num_types <= 128 (MLCG_ERR_UNSUPPORTED beyond); a type outside
- * [0, num_types) is skipped and sets *bad = 1 (bad is not cleared here).
- * `workspace` holds mlcg_type_sum_workspace_floats(rows, num_types) floats. */
-int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types);
-int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
-                  int num_types, float* out, int* bad, float* workspace,
-                  int64_t workspace_floats, void* stream);
-
 int64_t mlcg_node_tmm_workspace_floats(int64_t rows);
 int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
                   const float* b2, int64_t rows, int features, int accumulate,
                   float* out, float* colsum_a1, float* workspace,
+                  int64_t workspace_floats, void* stream);
+
+/* out [num_types, 128] = for each type t the sum of the rows of x [rows, 128]
+ * whose types[row] == t: the gradient of the bead-type embedding table
+ * (schnet.py:132, `x = self.embedding_layer(data.atom_types)`, whose
+ * autograd backward scatters the adjoint of x into the table).  One
+ * workgroup per type lists its rows in ascending order and sums them in a
+ * fixed order, so the result is run-to-run identical.
+ * num_types <= 128 (MLCG_ERR_UNSUPPORTED beyond); a type outside
+ * [0, num_types) is skipped and sets *bad = 1 (bad is not cleared here).
+ * mlcg_type_sum_workspace_floats returns 0 (no workspace is used; the
+ * workspace arguments are accepted and ignored, and may be NULL / 0). */
+int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types);
+int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
+                  int num_types, float* out, int* bad, float* workspace,
                   int64_t workspace_floats, void* stream);
 
 /* ---------------------------------------------------------------------- */

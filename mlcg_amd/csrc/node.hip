@@ -558,68 +558,101 @@ void node_gemm2_kernel(
 
 // ---------------------------------------------------------------------------
 // type_sum: out[t][:] = sum of the rows x[n][:] with types[n] == t, for
-// t < T <= 128 -- the gradient of an embedding table.  Workgroup g sums its
-// contiguous row range into an LDS table, thread c owning column c and
-// walking the rows in ascending order, and writes that partial table; a
-// second kernel adds the partials in workgroup order.  No atomics: the
-// result is the same on every run.
+// t < T <= 128 -- the gradient of an embedding table.  One workgroup per
+// type t walks the rows in chunks: its waves find the rows of type t
+// (ballot, in ascending row order) and list them in LDS, then the rows are
+// summed column by column, slot h of the eight slots per column taking the
+// listed rows h, h + 8, ... in order with a compensated (Kahan) sum, and the
+// slots are added in order at the end.  No atomics and no partial tables: the
+// result is the same on every run, and each row of x is read once in total.
 constexpr int kTypeMax = 128;
-constexpr int kTypeGroups = 256;
-constexpr int kTypeBatch = 32;  // rows whose loads are in flight together
+constexpr int kTypeThreads = 1024;
+constexpr int kTypeWaves = kTypeThreads / MLCG_WAVE;
+constexpr int kTypeSteps = 24;  // 64-row steps per wave and chunk
+constexpr int kTypeWaveRows = kTypeSteps * MLCG_WAVE;
+constexpr int kTypeChunk = kTypeWaves * kTypeWaveRows;  // 24576 rows
+constexpr int kTypeSlots = kTypeThreads / kF;           // partial sums per column
+constexpr int kTypeBatch = 24;                          // row loads in flight per thread
 
-__global__ __launch_bounds__(kF) void type_sum_kernel(const float* __restrict__ x,
-                                                       const int64_t* __restrict__ types,
-                                                       int64_t rows, int T,
-                                                       float* __restrict__ partial,
-                                                       int* __restrict__ bad) {
-  extern __shared__ float acc[];  // [T][128]
-  const int c = threadIdx.x;
-  for (int t = 0; t < T; ++t) acc[t * kF + c] = 0.0f;
-  const int64_t G = gridDim.x;
-  const int64_t r0 = rows * blockIdx.x / G, r1 = rows * (blockIdx.x + 1) / G;
-  constexpr int kBatch = kTypeBatch;
-  for (int64_t r = r0; r < r1; r += kBatch) {
-    int64_t tt[kBatch];
-    float xv[kBatch];
+__global__ __launch_bounds__(kTypeThreads) void type_sum_kernel(const float* __restrict__ x,
+                                                                 const int64_t* __restrict__ types,
+                                                                 int64_t rows, int T,
+                                                                 float* __restrict__ out,
+                                                                 int* __restrict__ bad) {
+  __shared__ int list[kTypeChunk];  // the chunk's matches in ascending row order
+  __shared__ int cnt[kTypeWaves];
+  __shared__ float red[kTypeSlots][kF], red2[kTypeSlots][kF];
+  const int t = blockIdx.x;
+  const int w = threadIdx.x / MLCG_WAVE, l = mlcg_lane();
+  const int c = threadIdx.x % kF, h = threadIdx.x / kF;
+  const uint64_t below = (l == 0) ? 0ull : (~0ull >> (MLCG_WAVE - l));  // lanes < l
+  float acc = 0.f, comp = 0.f;  // running sum and its lost low-order part
+  for (int64_t r0 = 0; r0 < rows; r0 += kTypeChunk) {
+    const int64_t base = r0 + (int64_t)w * kTypeWaveRows;
+    int64_t tt[kTypeSteps];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const bool in = r + u < r1;
-      tt[u] = in ? types[r + u] : 0;
-      xv[u] = in ? x[(r + u) * kF + c] : 0.0f;
+    for (int i = 0; i < kTypeSteps; ++i) {
+      const int64_t r = base + MLCG_WAVE * i + l;
+      tt[i] = r < rows ? types[r] : -1;
+    }
+    // count this wave's matches, then (with every wave's count known) list
+    // them at the wave's offset; rows past the end have tt = -1, never t
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < kTypeSteps; ++i) {
+      // an out-of-table type is flagged (by workgroup 0) and summed nowhere
+      if (t == 0 && base + MLCG_WAVE * i + l < rows && (tt[i] < 0 || tt[i] >= T)) bad[0] = 1;
+      n += __popcll(__ballot(tt[i] == t));
+    }
+    if (l == 0) cnt[w] = n;
+    __syncthreads();
+    int off = 0, total = 0;
+#pragma unroll
+    for (int v = 0; v < kTypeWaves; ++v) {
+      const int cv = cnt[v];
+      off += v < w ? cv : 0;
+      total += cv;
     }
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      if (r + u >= r1) break;
-      const int64_t t = tt[u];
-      if (t < 0 || t >= T) {  // out-of-table type: flagged, not summed
-        if (c == 0) bad[0] = 1;
-        continue;
+    for (int i = 0; i < kTypeSteps; ++i) {
+      const bool m = tt[i] == t;
+      const uint64_t bal = __ballot(m);
+      if (m) list[off + __popcll(bal & below)] = (int)(base + MLCG_WAVE * i + l - r0);
+      off += __popcll(bal);
+    }
+    __syncthreads();
+    for (int m0 = h; m0 < total; m0 += kTypeSlots * kTypeBatch) {
+      float xv[kTypeBatch];
+#pragma unroll
+      for (int u = 0; u < kTypeBatch; ++u) {
+        const int m = m0 + u * kTypeSlots;
+        xv[u] = m < total ? x[(r0 + list[m]) * kF + c] : 0.f;
       }
-      acc[t * kF + c] += xv[u];
-    }
-  }
-  float* o = partial + (int64_t)blockIdx.x * T * kF;
-  for (int t = 0; t < T; ++t) o[t * kF + c] = acc[t * kF + c];
-}
-
-// One wave per output: lane l adds the partials l, l + 64, ... in order, then
-// the 64 lane sums are combined by a fixed xor butterfly.
-__global__ __launch_bounds__(256) void type_sum_reduce_kernel(const float* __restrict__ partial,
-                                                              int groups, int T,
-                                                              float* __restrict__ out) {
-  const int64_t j = (int64_t)blockIdx.x * (256 / MLCG_WAVE) + threadIdx.x / MLCG_WAVE;
-  const int l = mlcg_lane();
-  float a = 0.f;
-  if (j < (int64_t)T * kF)
-    for (int g = l; g < groups; g += MLCG_WAVE) a += partial[(int64_t)g * T * kF + j];
 #pragma unroll
-  for (int o = MLCG_WAVE / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, MLCG_WAVE);
-  if (j < (int64_t)T * kF && l == 0) out[j] = a;
-}
-
-int type_groups(int64_t rows) {
-  const int64_t g = (rows + kTypeBatch - 1) / kTypeBatch;
-  return (int)(g < 1 ? 1 : (g < kTypeGroups ? g : kTypeGroups));
+      for (int u = 0; u < kTypeBatch; ++u)
+        if (m0 + u * kTypeSlots < total) {
+          const float yv = xv[u] - comp;
+          const float tv = acc + yv;
+          comp = (tv - acc) - yv;
+          acc = tv;
+        }
+    }
+    __syncthreads();  // list and cnt are rewritten by the next chunk
+  }
+  red[h][c] = acc;
+  red2[h][c] = comp;
+  __syncthreads();
+  if (h == 0) {
+    float sum = 0.f, cs = 0.f;
+#pragma unroll
+    for (int v = 0; v < kTypeSlots; ++v) {
+      const float yv = red[v][c] - (cs + red2[v][c]);
+      const float tv = sum + yv;
+      cs = (tv - sum) - yv;
+      sum = tv;
+    }
+    out[(int64_t)t * kF + c] = sum;
+  }
 }
 
 int tmm_groups(int64_t rows) {
@@ -769,23 +802,19 @@ extern "C" int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
 
 extern "C" int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types) {
   if (rows < 0 || num_types < 1 || num_types > kTypeMax) return -1;
-  return (int64_t)type_groups(rows) * num_types * kF;
+  return 0;  // no workspace: one pass, no partial tables
 }
 
 extern "C" int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
                              int num_types, float* out, int* bad, float* workspace,
                              int64_t workspace_floats, void* stream) {
+  (void)workspace;
+  (void)workspace_floats;
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   if (num_types > kTypeMax) return MLCG_ERR_UNSUPPORTED;
-  MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out && bad && workspace);
+  MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out && bad);
   MLCG_REQUIRE(rows == 0 || (x && types));
-  const int groups = type_groups(rows);
-  MLCG_REQUIRE(workspace_floats >= (int64_t)groups * num_types * kF);
-  hipStream_t s = mlcg_stream(stream);
-  hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)groups), dim3(kF),
-                     sizeof(float) * num_types * kF, s, x, types, rows, num_types, workspace, bad);
-  const int outs = num_types * kF;
-  hipLaunchKernelGGL(type_sum_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, s, workspace,
-                     groups, num_types, out);
+  hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)num_types), dim3(kTypeThreads), 0,
+                     mlcg_stream(stream), x, types, rows, num_types, out, bad);
   return mlcg_launch_status();
 }

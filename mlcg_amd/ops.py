@@ -421,7 +421,7 @@ def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
     out = torch.empty(num_types, NUM_FILTERS, dtype=torch.float32, device=x.device)
     bad = torch.zeros(1, dtype=torch.int32, device=x.device)
     nws = int(_lib.load().mlcg_type_sum_workspace_floats(x.shape[0], num_types))
-    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=x.device)
+    ws = torch.empty(nws, dtype=torch.float32, device=x.device) if nws > 0 else None
     call("mlcg_type_sum", ptr(x), ptr(types), x.shape[0], NUM_FILTERS, num_types, ptr(out),
          ptr(bad), ptr(ws), nws, stream_handle(x.device))
     return out, bad

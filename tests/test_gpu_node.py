@@ -188,7 +188,9 @@ def test_node_gemm2_checks():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,num_types", [(0, 5), (1, 1), (17920, 35), (5000, 128), (300, 7)])
+@pytest.mark.parametrize("rows,num_types", [(0, 5), (1, 1), (17920, 35), (17920, 100),
+                                            (5000, 128), (300, 7), (24576, 3), (24577, 3),
+                                            (50000, 1)])
 def test_type_sum_matches_index_add(rows, num_types):
     """The embedding-table gradient against fp64 index_add, identical on
     repeated calls (fixed summation order)."""
@@ -207,6 +209,25 @@ def test_type_sum_matches_index_add(rows, num_types):
     else:
         assert rel_err(out, ref) < 1e-6
     assert torch.equal(ops.type_sum(x, types, num_types)[0], out)
+
+
+@pytest.mark.gpu
+def test_type_sum_sorted_and_skewed_types():
+    """Row lists that cross the 24,576-row chunks unevenly: all rows of one
+    type in a block at the end, and types sorted ascending (frames of a
+    batch), against fp64 index_add."""
+    from mlcg_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(40000, 128, device="cuda", generator=g)
+    types = torch.zeros(40000, dtype=torch.int64, device="cuda")
+    types[-20000:] = 2
+    for tt in (types, torch.sort(torch.randint(0, 50, (40000,), device="cuda",
+                                               generator=g))[0]):
+        out, bad = ops.type_sum(x, tt, 50)
+        ref = torch.zeros(50, 128, dtype=torch.float64).index_add_(0, tt.cpu(), x.double().cpu())
+        assert int(bad.item()) == 0
+        assert rel_err(out, ref) < 1e-6
 
 
 @pytest.mark.gpu
