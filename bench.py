@@ -100,6 +100,12 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
         # one [N, 128] x [128, 128] product (its epilogue streams 2-6 [N, 128]
         # tensors depending on the mode)
         return "mfma", 2 * N * F * F, "flop"
+    if name == "mlcg_node_gemm2":
+        # two consecutive [N, 128] x [128, 128] products in one kernel
+        return "mfma", 2 * 2 * N * F * F, "flop"
+    if name == "mlcg_type_sum":
+        # the rows of x and their types read once
+        return "hbm", 4 * F * N + 8 * N, "byte"
     if name == "mlcg_cfconv_gather":
         return "hbm", sw * F * P + 4 * E + 4 * (N + 1) + 2 * 4 * F * N, "byte"
     if name == "mlcg_cfconv_gather_bwd":
@@ -129,7 +135,8 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
 # products of split operands: their MFMA ceiling, in fp32-equivalent FLOP/s,
 # is a third of the fp16 peak.  (The filter backward's recomputation of the
 # first layer stays on the fp32 MFMA but is not counted as algorithmic work.)
-SPLIT_FP16 = {"mlcg_filter_fwd", "mlcg_filter_bwd", "mlcg_filter_bwd_cfconv", "mlcg_node_gemm"}
+SPLIT_FP16 = {"mlcg_filter_fwd", "mlcg_filter_bwd", "mlcg_filter_bwd_cfconv", "mlcg_node_gemm",
+              "mlcg_node_gemm2"}
 # Entry points the training step launches on its second stream, beside the
 # main one: their bracketing events also count time spent sharing the GPU or
 # waiting for CUs, so they are reported but never taken as the dominant kernel.
@@ -143,6 +150,8 @@ KERNEL_SYMBOL = {
     "mlcg_filter_bwd_cfconv": "filter_bwd_fused_kernel",
     "mlcg_node_tmm": "node_tmm_kernel",
     "mlcg_node_gemm": "node_gemm_kernel",
+    "mlcg_node_gemm2": "node_gemm2_kernel",
+    "mlcg_type_sum": "type_sum_kernel",
     "mlcg_cfconv_gather": "gather_kernel",
     "mlcg_cfconv_gather_bwd": "gather_bwd_kernel",
     "mlcg_cfconv_gather_tangent": "gather_tangent_kernel",
