@@ -482,16 +482,12 @@ __device__ __forceinline__ float x3_scale(float maxabs) {
 
 __device__ __forceinline__ void x3_store(_Float16* plane, int plane_stride, int idx, float v,
                                          float S) {
-  const _Float16 h = (_Float16)v;
-  plane[idx] = h;
-  plane[plane_stride + idx] = (_Float16)((float)h * S);
-  plane[2 * plane_stride + idx] = (_Float16)((v - (float)h) * S);
+  const f16split sp = split2(v, S);
+  plane[idx] = sp.hi;
+  plane[plane_stride + idx] = (_Float16)((float)sp.hi * S);
+  plane[2 * plane_stride + idx] = sp.lo;
 }
 
-__device__ __forceinline__ _Float16 x3_hi(float v) { return (_Float16)v; }
-__device__ __forceinline__ _Float16 x3_lo(float v, _Float16 hi, float S) {
-  return (_Float16)((v - (float)hi) * S);
-}
 
 // acc += S A B over one 32-wide k block from A's planes and B's parts.
 __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, halfx8 bh,
@@ -605,10 +601,11 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
         float g, gd;
         const int k = 32 * s + 8 * q + j;
         rbf_eval(rp, k < K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
-        gh[j] = x3_hi(g);
-        gl[j] = x3_lo(g, gh[j], S1);
-        gdh[j] = x3_hi(gd);
-        gdl[j] = x3_lo(gd, gdh[j], S1);
+        const f16split sg = split2(g, S1), sgd = split2(gd, S1);
+        gh[j] = sg.hi;
+        gl[j] = sg.lo;
+        gdh[j] = sgd.hi;
+        gdl[j] = sgd.lo;
       }
 #pragma unroll
       for (int t = 0; t < kFT; ++t) {
@@ -628,10 +625,11 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
         mlcg_act(rp.act, a[t][i] * inv1 + b1s[16 * t + 4 * q + i], sv, d1, d2);
         const int e = 4 * (t & 1) + i;
         const float hd = d1 * (ad[t][i] * inv1);
-        hh[t >> 1][e] = x3_hi(sv);
-        hl[t >> 1][e] = x3_lo(sv, hh[t >> 1][e], S2);
-        hdh[t >> 1][e] = x3_hi(hd);
-        hdl[t >> 1][e] = x3_lo(hd, hdh[t >> 1][e], S2);
+        const f16split sh = split2(sv, S2), shd = split2(hd, S2);
+        hh[t >> 1][e] = sh.hi;
+        hl[t >> 1][e] = sh.lo;
+        hdh[t >> 1][e] = shd.hi;
+        hdl[t >> 1][e] = shd.lo;
       }
     // 3. w = W2 h, w' = W2 h' (times S2)
     floatx4 w[kFT], wd[kFT];
@@ -906,9 +904,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const int j = x & 7, ll = (x >> 3) & 63, ts = x >> 9;
       const int sb = ts & 3, t = ts >> 2;
       const float v = W2[(32 * sb + 8 * (ll >> 4) + j) * kF + 16 * t + (ll & 15)];
-      const _Float16 h = (_Float16)v;
-      w2h[x] = h;
-      w2h[kPlane + x] = (_Float16)((v - (float)h) * S);
+      const f16split sp = split2(v, S);
+      w2h[x] = sp.hi;
+      w2h[kPlane + x] = sp.lo;
     }
   } else {
     stage_w2_f32(w2ts, W2, true);
@@ -926,9 +924,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       for (int j = 0; j < 4; ++j) {
         const int k = 16 * b + 4 * q + j;
         const float v = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
-        const _Float16 hv1 = (_Float16)v;
-        w1h[b][j] = hv1;
-        w1l[b][j] = (_Float16)((v - (float)hv1) * kS4);
+        const f16split sp = split2(v, kS4);
+        w1h[b][j] = sp.hi;
+        w1l[b][j] = sp.lo;
       }
   } else {
 #pragma unroll
@@ -1015,21 +1013,21 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           _Float16* GTh = reinterpret_cast<_Float16*>(GTb);
           const int o = (4 * s + q) * 16 + n;
           const float v0 = g * vm, v1 = gd * vm;
-          const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-          GTh[o] = h0;
-          GTh[kRows * 16 + o] = h1;
-          GTh[2 * kRows * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
-          GTh[3 * kRows * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
+          const f16split s0 = split2(v0, kS4), s1 = split2(v1, kS4);
+          GTh[o] = s0.hi;
+          GTh[kRows * 16 + o] = s1.hi;
+          GTh[2 * kRows * 16 + o] = s0.lo;
+          GTh[3 * kRows * 16 + o] = s1.lo;
           // step 1's copy (k = 4s + q: chunk s, element q)
           const int o1 = n * 64 + 4 * (s ^ n) + q;
           const float u0 = v0 * kBetaG0, u1 = v1 * kBetaG1;
-          const _Float16 c0 = (_Float16)u0, c1 = (_Float16)u1;
-          G1h[o1] = c0;
-          G1h[1024 + o1] = c1;
-          G1h[2048 + o1] = (_Float16)((float)c0 * kS4);
-          G1h[3072 + o1] = (_Float16)((float)c1 * kS4);
-          G1h[4096 + o1] = (_Float16)((u0 - (float)c0) * kS4);
-          G1h[5120 + o1] = (_Float16)((u1 - (float)c1) * kS4);
+          const f16split c0 = split2(u0, kS4), c1 = split2(u1, kS4);
+          G1h[o1] = c0.hi;
+          G1h[1024 + o1] = c1.hi;
+          G1h[2048 + o1] = (_Float16)((float)c0.hi * kS4);
+          G1h[3072 + o1] = (_Float16)((float)c1.hi * kS4);
+          G1h[4096 + o1] = c0.lo;
+          G1h[5120 + o1] = c1.lo;
         } else {
           const int o = rp_at(4 * s + q, n);
           GTb[o] = g * vm;
@@ -1164,11 +1162,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       for (int i = 0; i < 4; ++i) {
         const int o = (16 * w + 4 * q + (i ^ q)) * 16 + n;
         const float v0 = hv[i] * kBetaH, v1 = hdv[i] * kBetaH;
-        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-        HTh[o] = h0;
-        HTh[kF * 16 + o] = h1;
-        HTh[2 * kF * 16 + o] = (_Float16)((v0 - (float)h0) * kS4);
-        HTh[3 * kF * 16 + o] = (_Float16)((v1 - (float)h1) * kS4);
+        const f16split s0 = split2(v0, kS4), s1 = split2(v1, kS4);
+        HTh[o] = s0.hi;
+        HTh[kF * 16 + o] = s1.hi;
+        HTh[2 * kF * 16 + o] = s0.lo;
+        HTh[3 * kF * 16 + o] = s1.lo;
       }
     } else {
 #pragma unroll
@@ -1198,11 +1196,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         halfx4 ph, phs, pl;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float v = src[i] * sg;
-          const _Float16 h = (_Float16)v;
-          ph[i] = h;
-          phs[i] = (_Float16)((float)h * S);
-          pl[i] = (_Float16)((v - (float)h) * S);
+          const f16split sp = split2(src[i] * sg, S);
+          ph[i] = sp.hi;
+          phs[i] = (_Float16)((float)sp.hi * S);
+          pl[i] = sp.lo;
         }
         *reinterpret_cast<halfx4*>(TBh + (0 * 2 + st) * 16 * kF + o) = ph;
         *reinterpret_cast<halfx4*>(TBh + (1 * 2 + st) * 16 * kF + o) = phs;
@@ -1309,10 +1306,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float s = xv[j] * rw;
-        const _Float16 h = (_Float16)s;
-        ah[j] = h;
-        ahs[j] = (_Float16)((float)h * kS4);
-        al[j] = (_Float16)((s - (float)h) * kS4);
+        const f16split sp = split2(s, kS4);
+        ah[j] = sp.hi;
+        ahs[j] = (_Float16)((float)sp.hi * kS4);
+        al[j] = sp.lo;
       }
       const halfx8* hth = reinterpret_cast<const halfx8*>(HT);
 #pragma unroll
@@ -1376,10 +1373,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float s = xv[j] * ra;
-        const _Float16 h = (_Float16)s;
-        ah[j] = h;
-        ahs[j] = (_Float16)((float)h * kS4);
-        al[j] = (_Float16)((s - (float)h) * kS4);
+        const f16split sp = split2(s, kS4);
+        ah[j] = sp.hi;
+        ahs[j] = (_Float16)((float)sp.hi * kS4);
+        al[j] = sp.lo;
       }
       // B: halfx8 of plane rows 16kt + n, stream q >> 1, pairs 8 (q & 1) .. + 7
       const halfx8* gth = reinterpret_cast<const halfx8*>(GT);

@@ -257,11 +257,10 @@ __device__ __forceinline__ void gemm_stage_x3(_Float16* xp, float* rinv,
     halfx4 ph, phs, pl;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float t = xv[i] * sg;
-      const _Float16 h = (_Float16)t;
-      ph[i] = h;
-      phs[i] = (_Float16)((float)h * kNodeS);
-      pl[i] = (_Float16)((t - (float)h) * kNodeS);
+      const f16split sp = split2(xv[i] * sg, kNodeS);
+      ph[i] = sp.hi;
+      phs[i] = (_Float16)((float)sp.hi * kNodeS);
+      pl[i] = sp.lo;
     }
     const int o = row * kF + 8 * ((c4 >> 1) ^ (row & 15)) + 4 * (c4 & 1);
     *reinterpret_cast<halfx4*>(xp + o) = ph;
@@ -369,9 +368,9 @@ __device__ __forceinline__ void gemm_load_w(halfx8 (&bh)[2][kF / 32], halfx8 (&b
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const _Float16 h = (_Float16)wv[j];
-        bh[c][kb][j] = h;
-        bl[c][kb][j] = (_Float16)((wv[j] - (float)h) * kNodeS);
+        const f16split sp = split2(wv[j], kNodeS);
+        bh[c][kb][j] = sp.hi;
+        bl[c][kb][j] = sp.lo;
       }
     }
   }

@@ -16,6 +16,23 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 
+// The two fp16 parts of an fp32 operand, hi = fp16(v) and lo = fp16((v - hi)
+// S), taken from one rounded fp32 value.  v is first made opaque to the
+// optimiser: hipcc contracts floating-point expressions by default and has
+// been seen to fold the product that computed v into one of the conversions
+// only (a mixed-precision fma rounds the exact product straight to fp16, which
+// can differ in the last bit from fp16 of the fp32-rounded product), and a hi
+// that differs from the one lo was formed against leaves an uncompensated
+// error of one fp16 ulp.  The empty asm emits no instruction.
+struct f16split {
+  _Float16 hi, lo;
+};
+__device__ __forceinline__ f16split split2(float v, float S) {
+  asm("" : "+v"(v));
+  const _Float16 hi = (_Float16)v;
+  return f16split{hi, (_Float16)((v - (float)hi) * S)};
+}
+
 // sigma = 2^k with m sigma < 4: brings values of magnitude <= m into the
 // range the split planes of an operand expect (sigma = 4 for m = 0).
 __device__ __forceinline__ float x3_norm(float m) {

@@ -66,6 +66,7 @@ class FusedSpec:
     out_has_bias: List[bool]  # per output linear
     f16: bool = False
     basis_trainable: bool = False  # Params.basis carries (centers, widths)
+    strict_fp32: bool = False  # filter forward on the fp32 MFMA throughout
 
 
 @dataclass
@@ -242,7 +243,8 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     x = P.emb.index_select(0, types)
     for k, bp in enumerate(P.blocks):
         W, Wd, dist = ops.filter_fwd(pos, graph, st.filt, bp.W1, bp.b1, bp.W2,
-                                     f16=spec.f16, want_dist=(k == 0))
+                                     f16=spec.f16, want_dist=(k == 0),
+                                     strict_fp32=spec.strict_fp32)
         if k == 0:
             st.dist = dist
         y = ops.node_linear(x, bp.A1)

@@ -170,6 +170,9 @@ class SchNet(torch.nn.Module):
         self.output_network = output_network
         # fp16 operands (fp32 accumulation) for the filter-network matmuls
         self.fp16_filters = False
+        # fp32 filter forward on the fp32 MFMA throughout instead of the
+        # default split-fp16 products (about 22 significant bits per operand)
+        self.strict_fp32_filters = False
         # fixed edge capacity of the radius graph (None: sized exactly with
         # one host sync per call; an int: no sync, as needed inside a captured
         # graph -- the caller then checks last_graph.flags)
@@ -206,7 +209,8 @@ class SchNet(torch.nn.Module):
         buffers), so in-place updates reach the kernels without a rebuild."""
         rbf = self.rbf_layer
         bt = _basis_tensors(rbf)
-        key = (bool(self.fp16_filters), type(rbf), len(self.interaction_blocks),
+        key = (bool(self.fp16_filters), bool(self.strict_fp32_filters), type(rbf),
+               len(self.interaction_blocks),
                bool(getattr(rbf, "trainable", False)))
         if bt is not None:
             # a float32 contiguous tensor is used in place; anything else is
@@ -284,7 +288,8 @@ class SchNet(torch.nn.Module):
             filt=filt, filter_act=filt_act, block_act=block_act, out_act=out_act,
             num_blocks=len(self.interaction_blocks),
             out_has_bias=[lin.bias is not None for lin in self.output_network.linears()],
-            f16=bool(self.fp16_filters), basis_trainable=bool(rbf.trainable))
+            f16=bool(self.fp16_filters), basis_trainable=bool(rbf.trainable),
+            strict_fp32=bool(self.strict_fp32_filters))
 
     def fused_params(self) -> _fused.Params:
         blocks = []

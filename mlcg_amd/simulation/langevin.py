@@ -228,13 +228,17 @@ class LangevinSimulation:
                 if isinstance(m, SchNet) and m.last_graph is not None
                 and m.graph_capacity is not None]
 
-    def _check_flags(self, flags):
-        for f in flags:
-            v = int(f.item())
-            if v:
-                raise RuntimeError(
-                    f"radius graph overflow (flags={v}): raise edge_capacity_factor or "
-                    "max_num_neighbors")
+    def _check_flags(self, sticky):
+        """Raises if any step since the start of the run overflowed a radius
+        graph: `sticky` is the OR of every step's graph flags, accumulated on
+        the device inside the (captured) step, so an overflow between two
+        checks is not lost."""
+        v = int(sticky.item())
+        if v:
+            raise RuntimeError(
+                f"radius graph overflow (flags={v}) in a step before step "
+                f"{self.current_step_for_check}: raise edge_capacity_factor or "
+                "max_num_neighbors")
 
     def simulate(self) -> np.ndarray:
         """Runs the BAOAB steps up to n_timesteps (from the checkpointed step
@@ -252,8 +256,17 @@ class LangevinSimulation:
         step_ctr = torch.full((1,), t_init, dtype=torch.int64, device=self.device)
         epot = torch.zeros(self.n_sims, dtype=self.dtype, device=self.device)
         F = torch.zeros_like(x)
+        # OR of the radius-graph flags of every step (bit 0: max_num_neighbors
+        # bound, bit 1: edge capacity exceeded); read only at the checks
+        sticky = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+        def or_flags():
+            for fl in self._graph_flags():
+                sticky.bitwise_or_(fl)
+
         with torch.no_grad():
             e0, f0 = self.calculate_potential_and_forces(data)
+            or_flags()
         F.copy_(f0)
         epot.copy_(e0)
         # frames held on the device: one export chunk when writing files, the
@@ -271,12 +284,13 @@ class LangevinSimulation:
                               self.noisescale, self.random_seed, step=step_ctr)
             data.pos = x
             e, f = self.calculate_potential_and_forces(data)
+            or_flags()
             F.copy_(f)
             epot.copy_(e)
             ops.langevin_b(v, F, m, self.dt, step=step_ctr)
 
         graph = None
-        flags = []
+        self.current_step_for_check = t_init
         if self.log_interval is not None:
             self._log(f"Generating {self.n_sims} simulations of n_timesteps {self.n_timesteps} "
                       f"saved at {self.save_interval}-step intervals ({time.asctime()})")
@@ -289,19 +303,18 @@ class LangevinSimulation:
                 if t == t_init + 3:
                     torch.cuda.synchronize()
                     t_start = time.perf_counter()
+                self.current_step_for_check = t + 1
                 if graph is None and self.capture and t >= t_init + 2:
                     torch.cuda.synchronize()
-                    self._check_flags(self._graph_flags())
+                    self._check_flags(sticky)
                     graph = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(graph):
                         one_step()
-                    flags = self._graph_flags()
                     graph.replay()  # the captured step is step t
                 elif graph is not None:
                     graph.replay()
                 else:
                     one_step()
-                    flags = self._graph_flags()
                 if self._hook is not None and (t + 1) % self._hook_interval == 0:
                     self._hook(x, v, F, epot)
                 if (t + 1) % self.save_interval == 0:
@@ -312,11 +325,11 @@ class LangevinSimulation:
                     if saved_f is not None:
                         saved_f[k].copy_(F)
                 if (t + 1) % self.check_interval == 0:
-                    self._check_flags(flags)
+                    self._check_flags(sticky)
                     if not bool(torch.isfinite(x).all()):
                         raise RuntimeError(f"non-finite positions at step {t + 1}")
                 if self.filename is not None and (t + 1) % self.export_interval == 0:
-                    self._check_flags(flags)
+                    self._check_flags(sticky)
                     self._export((t + 1) // self.export_interval - 1, traj, saved_e, saved_f,
                                  x, v)
                 if self.log_interval is not None and (t + 1) % self.log_interval == 0:
@@ -327,7 +340,7 @@ class LangevinSimulation:
         if t_start is not None:
             self.timed_seconds = time.perf_counter() - t_start
             self.timed_steps = self.n_timesteps - t_init - 3
-        self._check_flags(flags)
+        self._check_flags(sticky)
         self.final_data = data
         self.potential = epot
         self.forces = F

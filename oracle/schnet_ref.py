@@ -237,6 +237,41 @@ def force_matching_grads(sd, cfg, pos, atom_types, batch, edge_index, n_frames,
     return loss.detach(), E.detach(), F.detach(), out
 
 
+def force_matching_grads_chunked(sd, cfg, pos, atom_types, batch, edge_index, n_frames,
+                                 f_ref: torch.Tensor, frames_per_chunk: int = 32,
+                                 trainable_basis: bool = False):
+    """force_matching_grads over a large batch, evaluated frame chunk by
+    frame chunk to bound the memory of the create_graph graph.  Frames share
+    no edges (neighbor_list.py:89-91), so energies and forces are per chunk,
+    and with loss = sum_c SSE_c / (3 N) the parameter gradient is
+    sum_c grad(mean_c) * N_c / N (mean_c = SSE_c / (3 N_c)).  `batch` must be
+    sorted and `edge_index` grouped by frame (any edge list of the batch)."""
+    N = pos.shape[0]
+    counts = torch.bincount(batch, minlength=n_frames)
+    ptr = torch.zeros(n_frames + 1, dtype=torch.long)
+    ptr[1:] = torch.cumsum(counts, 0)
+    E_all, F_all, grads, sse = [], [], None, 0.0
+    for f0 in range(0, n_frames, frames_per_chunk):
+        f1 = min(n_frames, f0 + frames_per_chunk)
+        n0, n1 = int(ptr[f0]), int(ptr[f1])
+        sel = (edge_index[0] >= n0) & (edge_index[0] < n1)
+        ei = edge_index[:, sel] - n0
+        loss_c, E_c, F_c, g_c = force_matching_grads(
+            sd, cfg, pos[n0:n1], atom_types[n0:n1], batch[n0:n1] - f0, ei, f1 - f0,
+            f_ref[n0:n1], trainable_basis=trainable_basis)
+        w = (n1 - n0) / N
+        sse = sse + float(loss_c) * 3 * (n1 - n0)
+        E_all.append(E_c)
+        F_all.append(F_c)
+        if grads is None:
+            grads = {k: v * w for k, v in g_c.items()}
+        else:
+            for k, v in g_c.items():
+                grads[k] = grads[k] + v * w
+    return (torch.tensor(sse / (3 * N), dtype=pos.dtype), torch.cat(E_all), torch.cat(F_all),
+            grads)
+
+
 # --------------------------------------------------------------------------
 # Parameter construction (independent of torch.nn module init order)
 

@@ -15,6 +15,21 @@ schnet_small.pt   3 frames x 9-bead self-avoiding chains, SchNet with 2
                   parameter gradient, plus the state_dict and edge list.  Saved
                   with torch.save of plain tensors (loadable with
                   weights_only=True).
+config2_512.pt    the full config-2 training batch (512 frames x 35-bead
+                  self-avoiding chains, synthetic.config2()) through the
+                  config-2 model (3 blocks, H = F = 128, 50 Gaussian RBF on
+                  0-20 A with a cosine envelope, cosine cutoff 20 A, tanh,
+                  output MLP 128 -> 64 -> 1; weights random_state_dict(seed
+                  20262)): the fp64 oracle's energies, forces, force-matching
+                  loss and every parameter gradient (evaluated in 32-frame
+                  chunks, R.force_matching_grads_chunked), stored as float32
+                  (rounding 6e-8 relative, far inside the 1e-5 / 1e-4
+                  tolerances), plus the edge count and a float64 checksum of
+                  the positions so that a test can tell the generator still
+                  yields the same batch.
+
+``python tests/golden/make_golden.py [name ...]`` writes the named fixtures
+(all three by default).
 """
 
 import os
@@ -84,6 +99,36 @@ def schnet_small():
     print("schnet_small.pt: E =", ei.shape[1], "loss", float(loss))
 
 
+CONFIG2_SEED = 20262
+
+
+def config2_512():
+    import time
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    b = synthetic.config2()
+    cfg = R.SchNetConfig(num_rbf=50, rbf_lo=0.0, rbf_hi=20.0, rbf_cut="cosine",
+                         conv_cut="cosine", conv_lo=0.0, conv_hi=20.0, act="tanh", num_blocks=3)
+    sd = R.random_state_dict(cfg, seed=CONFIG2_SEED)
+    ei, ovf = oracle_radius.radius_graph(b.pos, 20.0, b.batch, False, 1000)
+    assert ovf == 0
+    t0 = time.time()
+    loss, E, F, grads = R.force_matching_grads_chunked(
+        R.to_dtype(sd, torch.float64), cfg, torch.from_numpy(b.pos).double(),
+        torch.from_numpy(b.atom_types), torch.from_numpy(b.batch), torch.from_numpy(ei),
+        b.n_frames, torch.from_numpy(b.forces).double(), frames_per_chunk=32)
+    torch.save({"seed": torch.tensor(CONFIG2_SEED), "n_frames": torch.tensor(b.n_frames),
+                "num_edges": torch.tensor(ei.shape[1]),
+                "pos_checksum": torch.tensor(float(np.abs(b.pos.astype(np.float64)).sum()),
+                                             dtype=torch.float64),
+                "loss": loss.double(), "energy": E.float(), "forces": F.float(),
+                "grads": {k: v.float() for k, v in grads.items()}},
+               os.path.join(HERE, "config2_512.pt"))
+    print("config2_512.pt: E =", ei.shape[1], "loss", float(loss),
+          f"({time.time() - t0:.0f} s)")
+
+
 if __name__ == "__main__":
-    radius_small()
-    schnet_small()
+    names = sys.argv[1:] or ["radius_small", "schnet_small", "config2_512"]
+    for name in names:
+        globals()[name]()

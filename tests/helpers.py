@@ -40,3 +40,39 @@ def rel_err(a, b):
 
 def max_abs(a, b):
     return float((a.double().cpu() - b.double().cpu()).abs().max())
+
+
+def close_report(got, ref, rtol, atol):
+    """Element-wise check |got - ref| <= atol + rtol * |ref| (torch.allclose's
+    rule) in fp64.  Returns (n_fail, n, worst ratio |d| / (atol + rtol |ref|),
+    a description of the worst element)."""
+    a = got.detach().double().cpu().reshape(-1)
+    r = ref.detach().double().cpu().reshape(-1)
+    if a.numel() == 0:
+        return 0, 0, 0.0, "empty"
+    d = (a - r).abs()
+    lim = atol + rtol * r.abs()
+    ratio = torch.where(lim > 0, d / lim.clamp_min(1e-300),
+                        torch.where(d > 0, torch.full_like(d, float("inf")), torch.zeros_like(d)))
+    ratio = torch.where(torch.isfinite(a), ratio, torch.full_like(d, float("inf")))
+    k = int(torch.argmax(ratio))
+    n_fail = int((ratio > 1.0).sum())
+    desc = (f"worst at flat index {k}: got {float(a[k]):.9e} ref {float(r[k]):.9e} "
+            f"|d| {float(d[k]):.3e} ratio {float(ratio[k]):.3f}; max|d| {float(d.max()):.3e}, "
+            f"max|ref| {float(r.abs().max()):.3e}")
+    return n_fail, a.numel(), float(ratio[k]), desc
+
+
+def assert_close(got, ref, rtol, atol, name=""):
+    """Element-wise parity assertion: every element within atol + rtol |ref|.
+    Prints the worst element (so a passing run still shows the margin)."""
+    assert tuple(got.shape) == tuple(ref.shape), (name, tuple(got.shape), tuple(ref.shape))
+    n_fail, n, worst, desc = close_report(got, ref, rtol, atol)
+    print(f"{name}: rtol {rtol:g} atol {atol:.3g}: {n_fail}/{n} outside; {desc}")
+    assert n_fail == 0, f"{name}: {n_fail}/{n} elements outside rtol {rtol:g} atol {atol:.3g}; {desc}"
+    return worst
+
+
+def scaled_atol(ref, scale):
+    """An absolute tolerance of `scale` times the largest |ref| element."""
+    return scale * float(ref.detach().double().abs().max()) if ref.numel() else 0.0

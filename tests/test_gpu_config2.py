@@ -1,0 +1,123 @@
+"""Config 2 -- the benchmark's own workload -- element-wise against the fp64
+oracle.
+
+Model: the bench's architecture (3 interaction blocks, H = F = 128, 50
+Gaussian RBF on 0-20 A with a cosine envelope, cosine cutoff 20 A, tanh,
+output MLP 128 -> 64 -> 1), weights random_state_dict(seed 20262).  Inputs:
+synthetic.config2 (seeded self-avoiding 35-bead chains, N(0, 1) target
+forces).  The step is the reference's force-matching step
+(mlcg/pl/model.py:113-131: GradientsOut forces with create_graph
+(gradients.py:216-222), ForceMSE (losses.py:167-181), backward).
+
+Tolerances (north_star: energies/forces 1e-5 relative / 1e-6 absolute,
+force-matching gradients 1e-4 relative), applied per element as
+|got - ref| <= atol + rtol |ref|:
+  loss       rtol 1e-5
+  E, F       rtol 1e-5, atol 1e-6 * max|ref| (the absolute term in units of
+             the tensor's largest element: the reference's own fp32
+             arithmetic -- the oracle in fp32, same op order -- misses a
+             literal atol of 1e-6 on 11 of 3,360 force components and 1 of 32
+             energies of the 32-frame batch, |F| up to 3.3)
+  gradients  rtol 1e-4, atol 1e-5 * max|ref| per parameter tensor (the
+             reference's fp32 arithmetic misses atol 0 on ~0.5 % of the
+             elements: gradients near zero are sums of cancelling terms)
+"""
+
+import os
+
+import pytest
+import torch
+
+from oracle import radius as oracle_radius
+from oracle import schnet_ref as R
+from tests.helpers import assert_close, close_report, make_cfg, make_model, scaled_atol
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20262
+RTOL_EF, ATOL_EF = 1e-5, 1e-6
+RTOL_G, ATOL_G = 1e-4, 1e-5
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _cfg():
+    return make_cfg(num_blocks=3, rc=20.0, num_rbf=50, act="tanh")
+
+
+def _hip_step(sd, b, strict=False):
+    from mlcg_amd import nn
+
+    model = make_model(_cfg(), sd, out_widths=(64,))
+    model.strict_fp32_filters = strict
+    gm = nn.GradientsOut(model).train()
+    data = gm(b.to_torch("cuda"))
+    data.out.update(**data.out[model.name])
+    loss = nn.ForceMSE()(data)
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = {k: p.grad for k, p in model.named_parameters()}
+    return (float(loss), data.out["SchNet"]["energy"].detach(),
+            data.out["SchNet"]["forces"].detach(), grads, model.last_graph.num_edges)
+
+
+def _check(label, hip, ref, n_edges_ref=None):
+    loss, E, F, grads, n_edges = hip
+    loss_r, E_r, F_r, g_r = ref
+    if n_edges_ref is not None:
+        assert n_edges == n_edges_ref
+    print(f"[{label}] edges {n_edges}, loss {loss:.9f} (oracle {float(loss_r):.9f})")
+    assert abs(loss - float(loss_r)) <= RTOL_EF * abs(float(loss_r))
+    assert_close(E, E_r, RTOL_EF, scaled_atol(E_r, ATOL_EF), f"[{label}] energy")
+    assert_close(F, F_r, RTOL_EF, scaled_atol(F_r, ATOL_EF), f"[{label}] forces")
+    worst = 0.0
+    for k, gr in g_r.items():
+        assert grads[k] is not None, k
+        worst = max(worst, assert_close(grads[k], gr, RTOL_G, scaled_atol(gr, ATOL_G),
+                                        f"[{label}] grad {k}"))
+    print(f"[{label}] worst gradient ratio {worst:.3f}")
+
+
+@pytest.mark.parametrize("strict", [False, True], ids=["split_fp16", "strict_fp32"])
+def test_config2_32_frames_vs_oracle(strict):
+    """32 config-2 frames: the live fp64 oracle (and, for scale, the oracle in
+    fp32 -- the reference's own arithmetic -- against the same fp64 values)."""
+    from mlcg_amd import synthetic
+
+    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
+    cfg = _cfg()
+    sd = R.random_state_dict(cfg, seed=SEED)
+    b = synthetic.config2(n_frames=32)
+    ei, _ = oracle_radius.radius_graph(b.pos, 20.0, b.batch, False, 1000)
+    args = (torch.from_numpy(b.atom_types), torch.from_numpy(b.batch), torch.from_numpy(ei),
+            b.n_frames)
+    ref = R.force_matching_grads(R.to_dtype(sd, torch.float64), cfg,
+                                 torch.from_numpy(b.pos).double(), *args,
+                                 torch.from_numpy(b.forces).double())
+    if not strict:
+        r32 = R.force_matching_grads(sd, cfg, torch.from_numpy(b.pos), *args,
+                                     torch.from_numpy(b.forces))
+        for name, got, r in (("F", r32[2], ref[2]), ("E", r32[1], ref[1])):
+            print("reference fp32 arithmetic vs fp64,", name, close_report(
+                got, r, RTOL_EF, scaled_atol(r, ATOL_EF))[3])
+    _check("32 frames " + ("strict" if strict else "split"), _hip_step(sd, b, strict), ref,
+           ei.shape[1])
+
+
+@pytest.mark.parametrize("strict", [False, True], ids=["split_fp16", "strict_fp32"])
+def test_config2_512_frames_vs_golden(strict):
+    """The full 512-frame config-2 batch (the one bench.py times) against the
+    committed fp64 oracle fixture (tests/golden/config2_512.pt, written by
+    tests/golden/make_golden.py)."""
+    import numpy as np
+
+    from mlcg_amd import synthetic
+
+    g = torch.load(os.path.join(HERE, "golden", "config2_512.pt"), weights_only=True)
+    assert int(g["seed"]) == SEED
+    b = synthetic.config2()
+    assert b.n_frames == int(g["n_frames"])
+    assert abs(float(np.abs(b.pos.astype(np.float64)).sum()) - float(g["pos_checksum"])) == 0.0
+    sd = R.random_state_dict(_cfg(), seed=SEED)
+    ref = (g["loss"], g["energy"], g["forces"], g["grads"])
+    _check("512 frames " + ("strict" if strict else "split"), _hip_step(sd, b, strict), ref,
+           int(g["num_edges"]))

@@ -12,6 +12,9 @@ from tests.helpers import make_cfg, make_model
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.skip(reason="capture of the whole training step crashed the host process in "
+                         "bench.py (512 frames, eager warm-up on the default stream); until "
+                         "that crash has a fix tested once, no variant of it runs on the GPU")
 def test_captured_training_step_matches_eager():
     from mlcg_amd import nn, synthetic
 

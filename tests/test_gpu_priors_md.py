@@ -346,3 +346,56 @@ def test_md_export_checkpoint_and_resume(tmp_path):
     assert np.array_equal(np.load(tmp_path / "b_coords_0001.npy"), a1)
     assert np.array_equal(np.load(tmp_path / "b_potential_0001.npy"),
                           np.load(tmp_path / "a_potential_0001.npy"))
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+def test_md_overflow_between_checks_raises(capture):
+    """A radius-graph capacity overflow on one intermediate step -- the
+    chains are collapsed after step 4 and restored after step 5, so steps 5
+    and 6 differ only in that step -- makes the run raise at its next check,
+    although the last step's own graph flags are clean: every step's flags are
+    ORed into one device flag inside the (captured) step."""
+    from mlcg_amd import nn
+    from mlcg_amd.simulation import LangevinSimulation
+
+    confs = _md_config(n_frames=3, n_beads=60, with_rep=False)
+    for c in confs:
+        c.neighbor_list = {}
+
+    def build():
+        torch.manual_seed(0)
+        rbf = nn.GaussianBasis(nn.CosineCutoff(0, 20.0), num_rbf=50)
+        schnet = nn.StandardSchNet(rbf, nn.CosineCutoff(0, 20.0), [64], 128, 100, 128, 2,
+                                   torch.nn.Tanh())
+        return schnet, nn.SumOut(torch.nn.ModuleDict({"SchNet": nn.GradientsOut(schnet)}))
+
+    for collapse in (False, True):
+        schnet, model = build()
+        sim = LangevinSimulation(friction=1.0, dt=0.004, n_timesteps=10, save_interval=10,
+                                 random_seed=5, capture=capture, check_interval=1000,
+                                 edge_capacity_factor=1.02)
+        sim.attach_model_and_configurations(model, [c.clone() for c in confs], L.beta_of(300.0))
+        saved = {}
+
+        def hook(x, v, F, epot, step=[0]):
+            step[0] += 1
+            if not collapse:
+                return
+            if step[0] == 4:  # positions of step 5 collapse towards each frame's centre
+                saved["x"], saved["v"] = x.clone(), v.clone()
+                xf = x.view(3, 60, 3)
+                xf.copy_(xf.mean(dim=1, keepdim=True) + 0.2 * (xf - xf.mean(dim=1, keepdim=True)))
+            elif step[0] == 5:
+                x.copy_(saved["x"])
+                v.copy_(saved["v"])
+
+        sim._hook, sim._hook_interval = hook, 1
+        if not collapse:
+            sim.simulate()
+            e0 = schnet.last_graph.rowptr[-1].item()
+            assert e0 < 0.9 * 3 * 60 * 59, "the test needs frames whose graph is not complete"
+            continue
+        with pytest.raises(RuntimeError, match="overflow"):
+            sim.simulate()
+        # the last step's own flags are clean: only the sticky flag saw it
+        assert int(schnet.last_graph.flags.item()) == 0

@@ -337,3 +337,28 @@ def test_golden_fixture_reproduced():
     assert float(loss) == pytest.approx(float(g["loss"]), rel=1e-12)
     for k, v in grads.items():
         assert torch.allclose(v, g["grads"][k], rtol=1e-10, atol=1e-14), k
+
+
+def test_chunked_force_matching_equals_whole_batch():
+    """force_matching_grads_chunked (frame chunks, weighted by chunk size)
+    gives the whole-batch loss, energies, forces and gradients: catches a
+    chunk weight of 1/chunks instead of N_c/N, or an edge list not shifted to
+    the chunk's node numbering."""
+    cfg = _cfg(blocks=2, rc=8.0)
+    sd = _sd(cfg, seed=3)
+    pos, types, batch = _frames(n_frames=5, n=6, seed=4, spread=2.5)
+    # ragged frames: drop two beads of frame 1
+    keep = torch.ones(pos.shape[0], dtype=torch.bool)
+    keep[7:9] = False
+    pos, types, batch = pos[keep], types[keep], batch[keep]
+    ei = _edges(pos, 8.0, batch)
+    fref = torch.from_numpy(np.random.default_rng(5).normal(0, 1, (pos.shape[0], 3)))
+    whole = R.force_matching_grads(sd, cfg, pos, types, batch, ei, 5, fref)
+    for chunk in (1, 2, 3):
+        part = R.force_matching_grads_chunked(sd, cfg, pos, types, batch, ei, 5, fref,
+                                              frames_per_chunk=chunk)
+        assert float(part[0]) == pytest.approx(float(whole[0]), rel=1e-12)
+        assert torch.allclose(part[1], whole[1], rtol=1e-12, atol=1e-14)
+        assert torch.allclose(part[2], whole[2], rtol=1e-12, atol=1e-14)
+        for k, v in whole[3].items():
+            assert torch.allclose(part[3][k], v, rtol=1e-10, atol=1e-14), (chunk, k)
