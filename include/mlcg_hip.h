@@ -82,6 +82,23 @@ int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b,
                              int64_t n, int32_t* out_a, int32_t* out_b,
                              int32_t* workspace, void* stream);
 
+/* mlcg_exclusive_scan2_i32 without the workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * or MD loops, harnesses that forbid hipMalloc); it has no counterpart in the
+ * reference.  Same inputs, outputs and results, bit for bit.  The per-tile
+ * sums live in a file-scope device array of the library sized for at most
+ * MLCG_SCAN_NOALLOC_MAX_N elements (128 KiB per device, held until the
+ * process ends); a larger n returns MLCG_ERR_CAPACITY before any launch.
+ * Nothing in the array needs to start at zero.  Every call on one device
+ * shares that device's array: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller.  The first
+ * call on a device looks the array's address up (no allocation, no stream
+ * work): make that first call outside a stream capture. */
+#define MLCG_SCAN_NOALLOC_MAX_N (1LL << 24)
+int mlcg_exclusive_scan2_i32_noalloc(const int32_t* in_a, const int32_t* in_b,
+                                     int64_t n, int32_t* out_a, int32_t* out_b,
+                                     void* stream);
+
 /* Pass 2: writes the canonical edge list (same membership and exclusion
  * arguments as pass 1).  edge_index is [2, edge_stride]
  * int64 (row 0 = centre i, row 1 = neighbour j).  Optional (nullable)

@@ -39,6 +39,7 @@ _SIGNATURES = {
     "mlcg_exclusion_pair_to_ptr": [_P, _I64, _I64, _P, _P],
     "mlcg_scan_workspace_ints": [_I64],
     "mlcg_exclusive_scan2_i32": [_P, _P, _I64, _P, _P, _P, _P],
+    "mlcg_exclusive_scan2_i32_noalloc": [_P, _P, _I64, _P, _P, _P],
     "mlcg_radius_fill": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _I64, _I64, _P,
                          _P, _I64, _I64, _P, _P, _P, _P],
     "mlcg_pair_reverse_map": [_P, _I64, _P, _I64, _P, _P, _P, _P],

@@ -22,6 +22,7 @@
 // not count towards max_num_neighbors, as in the reference.  Each lane looks
 // its candidate up by binary search in the row's segment.
 #include <algorithm>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -399,12 +400,12 @@ extern "C" int64_t mlcg_scan_workspace_ints(int64_t n) {
   return 2 * ((n + kScanTile - 1) / kScanTile + 1);
 }
 
-extern "C" int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b, int64_t n,
-                                        int32_t* out_a, int32_t* out_b, int32_t* workspace,
-                                        void* stream) {
-  MLCG_REQUIRE(n >= 0 && out_a && out_b && workspace);
-  MLCG_REQUIRE(n == 0 || (in_a && in_b));
-  hipStream_t s = mlcg_stream(stream);
+namespace {
+
+// The scan proper; `workspace` holds mlcg_scan_workspace_ints(n) int32 (the
+// per-tile sums, every one written before it is read: nothing needs clearing).
+int launch_scan2(const int32_t* in_a, const int32_t* in_b, int64_t n, int32_t* out_a,
+                 int32_t* out_b, int32_t* workspace, hipStream_t s) {
   if (n == 0) {
     hipLaunchKernelGGL(zero_totals, dim3(1), dim3(1), 0, s, out_a, out_b);
     return mlcg_launch_status();
@@ -418,6 +419,53 @@ extern "C" int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b
   hipLaunchKernelGGL(scan_tile_apply, dim3((unsigned)tiles), dim3(kScanThreads), 0, s, in_a,
                      in_b, n, sa, sb, out_a, out_b);
   return mlcg_launch_status();
+}
+
+// Workspace of mlcg_exclusive_scan2_i32_noalloc: a file-scope device array
+// sized for MLCG_SCAN_NOALLOC_MAX_N elements (2 x 16,385 int32 = 128 KiB per
+// device, held until the process ends).  Host code never passes `scratch`
+// itself to a kernel (in host code the name is only a stand-in): its device
+// address is looked up once per device with hipGetSymbolAddress and cached.
+constexpr int64_t kScanNoAllocInts = 2 * ((MLCG_SCAN_NOALLOC_MAX_N + kScanTile - 1) / kScanTile + 1);
+__device__ __align__(256) int32_t scratch[kScanNoAllocInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr on failure).
+int32_t* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int mlcg_exclusive_scan2_i32(const int32_t* in_a, const int32_t* in_b, int64_t n,
+                                        int32_t* out_a, int32_t* out_b, int32_t* workspace,
+                                        void* stream) {
+  MLCG_REQUIRE(n >= 0 && out_a && out_b && workspace);
+  MLCG_REQUIRE(n == 0 || (in_a && in_b));
+  return launch_scan2(in_a, in_b, n, out_a, out_b, workspace, mlcg_stream(stream));
+}
+
+extern "C" int mlcg_exclusive_scan2_i32_noalloc(const int32_t* in_a, const int32_t* in_b,
+                                                int64_t n, int32_t* out_a, int32_t* out_b,
+                                                void* stream) {
+  MLCG_REQUIRE(n >= 0 && out_a && out_b);
+  MLCG_REQUIRE(n == 0 || (in_a && in_b));
+  if (n > MLCG_SCAN_NOALLOC_MAX_N) return MLCG_ERR_CAPACITY;
+  int32_t* ws = scratch_for_current_device();
+  if (ws == nullptr) return MLCG_ERR_LAUNCH;
+  return launch_scan2(in_a, in_b, n, out_a, out_b, ws, mlcg_stream(stream));
 }
 
 extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
