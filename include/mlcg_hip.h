@@ -496,6 +496,20 @@ int mlcg_langevin_b(float* vel, const float* forces, const float* masses,
 int mlcg_philox_normals(uint64_t seed, int64_t step, int64_t n_nodes, float* out,
                         void* stream);
 
+/* ---------------------------------------------------------------------- */
+/* Elementary functions (accuracy checks)                                  */
+/* ---------------------------------------------------------------------- */
+
+/* y[i] = f(x[i]) for the library's own fp32 elementary functions, the ones
+ * the filter, node and output kernels evaluate inline: tanh (the reference's
+ * default activation, schnet.py:419), the sigmoid and softplus of the
+ * shifted-softplus activation, and sin(pi u) / cos(pi u) of the cosine
+ * cutoff (cutoff.py:145-153).  Exposed so that their accuracy can be
+ * measured against fp64; no reference interface is replaced. */
+enum { MLCG_MATH_TANH = 0, MLCG_MATH_SIGMOID = 1, MLCG_MATH_SOFTPLUS = 2,
+       MLCG_MATH_SINPI = 3, MLCG_MATH_COSPI = 4 };
+int mlcg_math_eval(int fn, const float* x, int64_t n, float* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

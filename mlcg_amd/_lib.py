@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mlcg_langevin_baoa": [_P, _P, _P, _P, _P, _I64, _F32, _F32, _F32, _U64, _P, _P, _P],
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
+    "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,

@@ -26,23 +26,41 @@
 
 namespace {
 
-struct V3 {
-  float x, y, z;
+template <typename T>
+struct V3T {
+  T x, y, z;
 };
-__device__ __forceinline__ V3 ld3(const float* __restrict__ p, int64_t i) {
-  return V3{p[3 * i], p[3 * i + 1], p[3 * i + 2]};
+using V3 = V3T<float>;
+using D3 = V3T<double>;
+template <typename T = float>
+__device__ __forceinline__ V3T<T> ld3(const float* __restrict__ p, int64_t i) {
+  return V3T<T>{(T)p[3 * i], (T)p[3 * i + 1], (T)p[3 * i + 2]};
 }
-__device__ __forceinline__ V3 sub(V3 a, V3 b) { return V3{a.x - b.x, a.y - b.y, a.z - b.z}; }
-__device__ __forceinline__ V3 add(V3 a, V3 b) { return V3{a.x + b.x, a.y + b.y, a.z + b.z}; }
-__device__ __forceinline__ V3 scl(float s, V3 a) { return V3{s * a.x, s * a.y, s * a.z}; }
-__device__ __forceinline__ float dot(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
-__device__ __forceinline__ V3 cross(V3 a, V3 b) {
-  return V3{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+template <typename T>
+__device__ __forceinline__ V3T<T> sub(V3T<T> a, V3T<T> b) {
+  return V3T<T>{a.x - b.x, a.y - b.y, a.z - b.z};
 }
-__device__ __forceinline__ void st3(float* __restrict__ f, int64_t slot, V3 v) {
-  f[3 * slot] = v.x;
-  f[3 * slot + 1] = v.y;
-  f[3 * slot + 2] = v.z;
+template <typename T>
+__device__ __forceinline__ V3T<T> add(V3T<T> a, V3T<T> b) {
+  return V3T<T>{a.x + b.x, a.y + b.y, a.z + b.z};
+}
+template <typename T>
+__device__ __forceinline__ V3T<T> scl(T s, V3T<T> a) {
+  return V3T<T>{s * a.x, s * a.y, s * a.z};
+}
+template <typename T>
+__device__ __forceinline__ T dot(V3T<T> a, V3T<T> b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z;
+}
+template <typename T>
+__device__ __forceinline__ V3T<T> cross(V3T<T> a, V3T<T> b) {
+  return V3T<T>{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+template <typename T>
+__device__ __forceinline__ void st3(float* __restrict__ f, int64_t slot, V3T<T> v) {
+  f[3 * slot] = (float)v.x;
+  f[3 * slot + 1] = (float)v.y;
+  f[3 * slot + 2] = (float)v.z;
 }
 
 template <int KIND>
@@ -53,44 +71,54 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
   for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M;
        m += (int64_t)gridDim.x * blockDim.x) {
     const float* pr = params + m * n_params;
-    if (KIND == MLCG_PRIOR_BOND || KIND == MLCG_PRIOR_REPULSION) {
+    if (KIND == MLCG_PRIOR_BOND) {
+      // Harmonic terms are evaluated in fp64 from the fp32 positions: the
+      // force 2 k (r - x0) of a stiff bond (k = 100 at config 5) amplifies the
+      // fp32 rounding of r (a few 1e-7 A) into force errors of ~6e-5, which the
+      // reference's fp32 arithmetic carries; in fp64 only the final rounding
+      // of the force remains.
+      const D3 pi = ld3<double>(pos, map[m]);
+      const D3 pj = ld3<double>(pos, map[stride + m]);
+      const D3 d = sub(pj, pi);
+      const double r = sqrt(dot(d, d));
+      const double x0 = pr[0], k = pr[1], v0 = pr[2];
+      const double dr = r - x0;
+      const double dUdr = 2.0 * k * dr;
+      const D3 fi = scl(dUdr / r, d);  // force on bead 0; bead 1 gets -fi
+      energy[m] = (float)(k * (dr * dr) + v0);
+      st3(slot_f, 2 * m, fi);
+      st3(slot_f, 2 * m + 1, scl(-1.0, fi));
+    } else if (KIND == MLCG_PRIOR_REPULSION) {
       const V3 pi = ld3(pos, map[m]);
       const V3 pj = ld3(pos, map[stride + m]);
       const V3 d = sub(pj, pi);
       const float r = sqrtf(dot(d, d));
-      float e, dUdr;
-      if (KIND == MLCG_PRIOR_BOND) {
-        const float x0 = pr[0], k = pr[1], v0 = pr[2];
-        const float dr = r - x0;
-        e = k * (dr * dr) + v0;
-        dUdr = 2.0f * k * dr;
-      } else {
-        const float s = pr[0] / r;
-        const float rr = s * s;
-        e = rr * rr * rr;
-        dUdr = -6.0f * e / r;
-      }
-      const V3 fi = scl(dUdr / r, d);  // force on bead 0; bead 1 gets -fi
+      const float s = pr[0] / r;
+      const float rr = s * s;
+      const float e = rr * rr * rr;
+      const float dUdr = -6.0f * e / r;
+      const V3 fi = scl(dUdr / r, d);
       energy[m] = e;
       st3(slot_f, 2 * m, fi);
       st3(slot_f, 2 * m + 1, scl(-1.0f, fi));
     } else if (KIND == MLCG_PRIOR_ANGLE) {
-      const V3 p0 = ld3(pos, map[m]);
-      const V3 p1 = ld3(pos, map[stride + m]);
-      const V3 p2 = ld3(pos, map[2 * stride + m]);
-      const V3 a = sub(p0, p1), b = sub(p2, p1);
-      const float na = sqrtf(dot(a, a)), nb = sqrtf(dot(b, b));
-      const float c = dot(a, b) / na / nb;
-      const float x0 = pr[0], k = pr[1], v0 = pr[2];
-      const float dc = c - x0;
-      energy[m] = k * (dc * dc) + v0;
-      const float g = 2.0f * k * dc;  // dU/dcos
-      const float inv = 1.0f / (na * nb);
-      const V3 dca = sub(scl(inv, b), scl(c / (na * na), a));
-      const V3 dcb = sub(scl(inv, a), scl(c / (nb * nb), b));
-      const V3 f0 = scl(-g, dca), f2 = scl(-g, dcb);
+      // fp64 for the same reason as the bonds (k (cos t - x0)^2)
+      const D3 p0 = ld3<double>(pos, map[m]);
+      const D3 p1 = ld3<double>(pos, map[stride + m]);
+      const D3 p2 = ld3<double>(pos, map[2 * stride + m]);
+      const D3 a = sub(p0, p1), b = sub(p2, p1);
+      const double na = sqrt(dot(a, a)), nb = sqrt(dot(b, b));
+      const double c = dot(a, b) / na / nb;
+      const double x0 = pr[0], k = pr[1], v0 = pr[2];
+      const double dc = c - x0;
+      energy[m] = (float)(k * (dc * dc) + v0);
+      const double g = 2.0 * k * dc;  // dU/dcos
+      const double inv = 1.0 / (na * nb);
+      const D3 dca = sub(scl(inv, b), scl(c / (na * na), a));
+      const D3 dcb = sub(scl(inv, a), scl(c / (nb * nb), b));
+      const D3 f0 = scl(-g, dca), f2 = scl(-g, dcb);
       st3(slot_f, 3 * m, f0);
-      st3(slot_f, 3 * m + 1, scl(-1.0f, add(f0, f2)));
+      st3(slot_f, 3 * m + 1, scl(-1.0, add(f0, f2)));
       st3(slot_f, 3 * m + 2, f2);
     } else {  // MLCG_PRIOR_DIHEDRAL
       const V3 pi = ld3(pos, map[m]);

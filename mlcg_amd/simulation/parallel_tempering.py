@@ -14,7 +14,9 @@ configurations, rescaling the velocities by sqrt(beta_old / beta_new)
 beta_new keeps its kinetic temperature consistent with the new slot.  (The
 reference's code multiplies by sqrt(beta_new / beta_old) instead, lines
 484-497, which heats configurations moving to a colder slot; this module
-follows the docstring and equipartition.)  The forces travel with the configurations
+follows the docstring and equipartition; ``reference_velocity_scaling=True``
+applies the reference code's factor instead, for reproducing a reference run's
+ensemble.)  The forces travel with the configurations
 (a force depends on the configuration only), so the next half-kick uses the
 force of the configuration it moves.  `acceptance_matrix[a, b]` counts the
 accepted (a < b) and rejected (a > b) exchanges between temperatures a and b.
@@ -33,11 +35,17 @@ from .langevin import LangevinSimulation
 
 
 class PTSimulation(LangevinSimulation):
-    def __init__(self, exchange_interval: int = 100, **kwargs):
+    def __init__(self, exchange_interval: int = 100, reference_velocity_scaling: bool = False,
+                 **kwargs):
         super().__init__(**kwargs)
         if exchange_interval < 1:
             raise ValueError("exchange_interval must be positive")
         self.exchange_interval = int(exchange_interval)
+        # False: a configuration moving from beta_old to beta_new has its
+        # velocities scaled by sqrt(beta_old / beta_new) (the reference's
+        # docstring, parallel_tempering.py:433-435); True: by
+        # sqrt(beta_new / beta_old), as the reference's code does (484-497)
+        self.reference_velocity_scaling = bool(reference_velocity_scaling)
         self._hook = self.detect_and_exchange_replicas
         self._hook_interval = self.exchange_interval
         self._rng = torch.Generator().manual_seed(self.random_seed + 1)
@@ -91,8 +99,9 @@ class PTSimulation(LangevinSimulation):
 
     def _perform_exchange(self, x, v, F, potential, pair_a, pair_b) -> None:
         """Swaps the configurations of the approved slot pairs in place,
-        velocities rescaled by sqrt(beta_old / beta_new) (parallel_tempering.py:
-        442-520)."""
+        velocities rescaled by sqrt(beta_old / beta_new), or by the reference
+        code's sqrt(beta_new / beta_old) with reference_velocity_scaling
+        (parallel_tempering.py:442-520)."""
         if len(pair_a) == 0:
             return
         dev = x.device
@@ -102,7 +111,9 @@ class PTSimulation(LangevinSimulation):
         x3, v3, f3 = (t.view(s, self.n_atoms, 3) for t in (x, v, F))
         beta = self.beta.to(dev)
         # b's configuration moves into slot a: v sqrt(beta_b / beta_a), and back
-        scale_ba = torch.sqrt(beta[b] / beta[a]).view(-1, 1, 1).to(v.dtype)
+        # (the reference code's inverse factor when asked for)
+        ratio = beta[a] / beta[b] if self.reference_velocity_scaling else beta[b] / beta[a]
+        scale_ba = torch.sqrt(ratio).view(-1, 1, 1).to(v.dtype)
         xa, va, fa, ua = x3[a].clone(), v3[a].clone(), f3[a].clone(), potential[a].clone()
         x3[a] = x3[b]
         x3[b] = xa

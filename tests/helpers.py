@@ -76,3 +76,14 @@ def assert_close(got, ref, rtol, atol, name=""):
 def scaled_atol(ref, scale):
     """An absolute tolerance of `scale` times the largest |ref| element."""
     return scale * float(ref.detach().double().abs().max()) if ref.numel() else 0.0
+
+
+def check(got, ref, rtol, name="", atol_frac=0.1):
+    """assert_close with the absolute term atol_frac * rtol times the largest
+    |ref| element: every element within rtol of itself, or within
+    atol_frac * rtol of the tensor's scale (elements near zero are sums of
+    cancelling terms, whose fp32 rounding error scales with the terms, not with
+    the sum).  atol_frac = 0.1 for model outputs (energies, forces, parameter
+    gradients); 1.0 -- every element within rtol of the tensor's largest, a
+    max-norm relative bound -- where a test says why."""
+    return assert_close(got, ref, rtol, scaled_atol(ref, atol_frac * rtol), name)

@@ -12,7 +12,7 @@ import torch
 
 from oracle import radius as oracle_radius
 from oracle import schnet_ref as R
-from tests.helpers import make_cfg, make_model, rel_err
+from tests.helpers import check, make_cfg, make_model, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -81,8 +81,8 @@ def test_expnormal_filter_fwd_matches_torch(rbf_cut):
                        for f in range(128)], dim=1)
     P = g.num_pairs
     print("expnormal W rel", rel_err(W[:P], Wr), "Wd rel", rel_err(Wd[:P], Wdr))
-    assert rel_err(W[:P], Wr.detach()) < 1e-5
-    assert rel_err(Wd[:P], Wdr) < 1e-5
+    check(W[:P], Wr.detach(), 1e-5, 'W[:P]')
+    check(Wd[:P], Wdr, 1e-5, 'Wd[:P]')
 
 
 @pytest.mark.parametrize("basis", ["gaussian", "expnormal"])
@@ -119,10 +119,10 @@ def test_rbf_param_grad_matches_autograd(basis):
     else:
         dw_total, dw2_total = dw, dw2
     print(basis, "dcenters rel", rel_err(dc, gc), "dwidths rel", rel_err(dw_total, gw))
-    assert rel_err(dc, gc) < 1e-4
-    assert rel_err(dw_total, gw) < 1e-4
-    assert rel_err(dc2, 2 * gc) < 1e-4
-    assert rel_err(dw2_total, 2 * gw) < 1e-4
+    check(dc, gc, 1e-4, 'dc')
+    check(dw_total, gw, 1e-4, 'dw_total')
+    check(dc2, 2 * gc, 1e-4, 'dc2')
+    check(dw2_total, 2 * gw, 1e-4, 'dw2_total')
     # the W1 gradient is unchanged by asking for the pair adjoints
     ref = ops.filter_bwd(pos, g, spec.filt, blk.W1, blk.b1, blk.W2, Wbar, Wdbar)
     assert torch.equal(ref[0], dW1) and torch.equal(ref[1], db1) and torch.equal(ref[2], dW2)
@@ -146,8 +146,8 @@ def test_expnormal_energy_forces(trainable):
     F = data.out["SchNet"]["forces"]
     print("expnormal trainable", trainable, "E rel", rel_err(E, E_ref), "F rel",
           rel_err(F, F_ref))
-    assert rel_err(E, E_ref) < 1e-5
-    assert rel_err(F, F_ref) < 1e-5
+    check(E, E_ref, 1e-5, 'E')
+    check(F, F_ref, 1e-5, 'F')
 
 
 @pytest.mark.parametrize("basis,act", [("gaussian", "tanh"), ("expnormal", "tanh"),
@@ -178,10 +178,8 @@ def test_force_matching_grads_trainable_basis(basis, act):
         assert grads[k].shape == sd[k].shape
     worst = 0.0
     for k, gr in g_ref.items():
-        e = rel_err(grads[k], gr)
-        worst = max(worst, e)
-        assert e < 1e-4, (k, e)
-    print(basis, act, "worst param-grad rel err", worst,
+        worst = max(worst, check(grads[k], gr, 1e-4, k))
+    print(basis, act, "worst param-grad ratio", worst,
           {k: rel_err(grads[k], g_ref[k]) for k in R.BASIS_KEYS[basis]})
 
 
@@ -203,11 +201,9 @@ def test_energy_backward_trainable_basis(basis):
     E = data.out["SchNet"]["energy"]
     (E * w.float().cuda()).sum().backward()
     params = dict(model.named_parameters())
-    assert rel_err(E, E_ref.detach()) < 1e-5
+    check(E, E_ref.detach(), 1e-5, 'E')
     for k, gr in zip(R.BASIS_KEYS[basis], g_ref):
-        e = rel_err(params[k].grad, gr)
-        print(basis, k, "rel", e)
-        assert e < 1e-4, (k, e)
+        check(params[k].grad, gr, 1e-4, f"{basis} {k}")
 
 
 def test_pruned_expnormal_basis():
@@ -241,5 +237,5 @@ def test_pruned_expnormal_basis():
     E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
                                           batch, ei, b.n_frames)
     data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
-    assert rel_err(data.out["SchNet"]["energy"], E_ref) < 1e-5
-    assert rel_err(data.out["SchNet"]["forces"], F_ref) < 1e-5
+    check(data.out["SchNet"]["energy"], E_ref, 1e-5, 'data.out["SchNet"]["energy"]')
+    check(data.out["SchNet"]["forces"], F_ref, 1e-5, 'data.out["SchNet"]["forces"]')

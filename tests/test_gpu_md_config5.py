@@ -1,0 +1,168 @@
+"""Config 5's composite MD step -- SchNet (the config-2 architecture, rc 20 A)
+plus harmonic bonds and angles, 3-term Fourier dihedrals and the (sigma/r)^6
+repulsion, integrated by BAOAB with the radius graph rebuilt every step --
+against the CPU oracles chained together:
+  forces  oracle/schnet_ref.py (fp64 SchNet, oracle radius graph at rc 20)
+          + oracle/priors_ref.py (the four priors with the config-5 constants)
+  step    oracle/langevin_ref.py (LangevinSimulation.timestep,
+          mlcg/simulation/langevin.py:100-144), fed the normals the HIP step
+          draws (ops.philox_normals at the same step counter).
+Every step of the HIP run (eager and captured) is checked from the state the
+HIP run itself reached, so the oracle never drifts along a chaotic trajectory:
+the forces and potential energies at the step's positions, and the positions
+and velocities of the next step.
+
+Tolerances, per element (tests.helpers.check): forces rtol 1e-5 (the
+energy/force bar of north_star); positions rtol 1e-6 (one fp32 rounding of a
+coordinate of up to ~40 A on a displacement of ~0.02 A per step); velocities
+rtol 1e-5 (they carry the force error through 0.5 dt F / m).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import langevin_ref as L
+from oracle import priors_ref as P
+from oracle import radius as oracle_radius
+from oracle import schnet_ref as R
+from tests.helpers import check
+
+pytestmark = pytest.mark.gpu
+
+N_BEADS = 268
+SEED = 20265
+
+
+def _model():
+    from mlcg_amd import nn, synthetic
+
+    torch.manual_seed(synthetic.seed_for(5))
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, 20.0), num_rbf=50)
+    schnet = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, 20.0), [64], 128, 100, 128, 3,
+                               torch.nn.Tanh())
+    models = {"SchNet": nn.GradientsOut(schnet)}
+    for k, v in synthetic.config5_prior_models().items():
+        models[k] = nn.GradientsOut(v)
+    return schnet, nn.SumOut(torch.nn.ModuleDict(models))
+
+
+def _oracle_force_fn(schnet, n_frames, types):
+    """Total force of the composite model at given positions, in fp64."""
+    import math
+
+    from mlcg_amd import synthetic
+
+    c = synthetic.CONFIG5_PRIORS
+    sd = {k: v.detach().double().cpu() for k, v in schnet.state_dict().items()}
+    cfg = R.SchNetConfig(num_rbf=50, rbf_lo=0.0, rbf_hi=20.0, rbf_cut="cosine",
+                         conv_cut="cosine", conv_lo=0.0, conv_hi=20.0, act="tanh",
+                         num_blocks=3)
+    topo = P.chain_topology(n_frames, N_BEADS, min_sep=c["repulsion"]["min_separation"])
+    batch = torch.arange(n_frames).repeat_interleave(N_BEADS)
+
+    def full(M, v):
+        return torch.full((M,), float(v), dtype=torch.float64)
+
+    params = {}
+    M = topo["bonds"][0].shape[1]
+    params["bonds"] = {"x0": full(M, c["bonds"]["x_0"]), "k": full(M, c["bonds"]["k"])}
+    M = topo["angles"][0].shape[1]
+    params["angles"] = {"x0": full(M, math.cos(math.radians(c["angles"]["theta_0_deg"]))),
+                        "k": full(M, c["angles"]["k"])}
+    M = topo["dihedrals"][0].shape[1]
+    d = c["dihedrals"]
+    params["dihedrals"] = {"v_0": full(M, d["v_0"]),
+                           "k1s": torch.tensor(d["k1s"], dtype=torch.float64).repeat(M, 1),
+                           "k2s": torch.tensor(d["k2s"], dtype=torch.float64).repeat(M, 1)}
+    M = topo["repulsion"][0].shape[1]
+    params["repulsion"] = {"sigma": full(M, c["repulsion"]["sigma"])}
+
+    def forces(x64):
+        ei, ovf = oracle_radius.radius_graph(x64.float().numpy(), 20.0, batch.numpy(), False,
+                                             1000)
+        assert ovf == 0
+        E, F = R.schnet_energy_forces(sd, cfg, x64, types, batch, torch.from_numpy(ei),
+                                      n_frames)
+        for kind, (mapping, mb) in topo.items():
+            Ek, Fk = P.prior_energy_forces(kind, x64, mapping, mb, n_frames, params[kind])
+            E = E + Ek
+            F = F + Fk
+        return E.detach(), F.detach()
+
+    return forces
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+def test_config5_composite_steps_vs_oracle(capture):
+    from mlcg_amd import ops, synthetic
+    from mlcg_amd.simulation import LangevinSimulation
+
+    n_frames, n_steps = 4, 6
+    print(f"config-5 composite step, {n_frames} x {N_BEADS} beads, capture={capture}",
+          flush=True)
+    c = synthetic.CONFIG5_PRIORS
+    schnet, model = _model()
+    confs = synthetic.config5_configurations(n_frames=n_frames, n_beads=N_BEADS)
+    beta = L.beta_of(c["temperature_K"])
+    sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"],
+                             n_timesteps=n_steps, save_interval=1, random_seed=SEED,
+                             capture=capture)
+    sim.attach_model_and_configurations(model, confs, beta)
+    states = []
+    sim._hook = lambda x, v, F, e: states.append(
+        tuple(t.detach().double().cpu().clone() for t in (x, v, F, e)))
+    sim._hook_interval = 1
+    sim.simulate()
+    assert len(states) == n_steps
+    types = torch.cat([d.atom_types for d in confs])
+    forces = _oracle_force_fn(schnet, n_frames, types)
+    m = sim.initial_data.masses.double().cpu()
+    bmr = torch.sqrt(1.0 / (beta * m))
+    vscale, noisescale = L.constants(c["dt_ps"], c["friction_per_ps"])
+    N = m.numel()
+    oracle = [forces(s[0]) for s in states]  # (E, F) at every state's positions
+    for k in range(n_steps):
+        _, _, F, epot = states[k]
+        check(F, oracle[k][1], 1e-5, f"step {k} forces")
+        check(epot, oracle[k][0], 1e-5, f"step {k} potential energies")
+    for k in range(n_steps - 1):
+        x, v, _, _ = states[k]
+        xn, vn, _, _ = states[k + 1]
+        # the next step from this state, with the normals the kernel drew at
+        # step counter k + 1; the closing half-kick takes the force at the
+        # positions the HIP step reached (with stiff bonds, 2k = 200
+        # kcal/mol/A^2, a position difference of one fp32 rounding would
+        # already move that force by ~1e-3)
+        xi = ops.philox_normals(SEED, k + 1, N, "cuda").double().cpu()
+        x1, v1 = L.baoa(x, v, oracle[k][1], m, bmr, c["dt_ps"], vscale, noisescale, xi)
+        v1 = L.b(v1, oracle[k + 1][1], m, c["dt_ps"])
+        check(xn, x1, 1e-6, f"step {k + 1} positions")
+        check(vn, v1, 1e-5, f"step {k + 1} velocities")
+
+
+def test_config5_full_size_captured_run():
+    """The full config-5 system (100 x 268 beads): a captured run stays
+    finite, never overflows its radius-graph capacity (the simulation raises
+    otherwise), and its steps after the capture equal those of the eager run."""
+    from mlcg_amd import synthetic
+    from mlcg_amd.simulation import LangevinSimulation
+
+    c = synthetic.CONFIG5_PRIORS
+    trajs = []
+    for capture in (False, True):
+        print(f"config-5 full size, capture={capture}", flush=True)
+        _, model = _model()
+        sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"], n_timesteps=6,
+                                 save_interval=1, random_seed=SEED, capture=capture,
+                                 save_energies=True, check_interval=1)
+        sim.attach_model_and_configurations(model, synthetic.config5_configurations(),
+                                            L.beta_of(c["temperature_K"]))
+        x = sim.simulate()
+        assert np.isfinite(x).all() and np.isfinite(sim.simulated_potential).all()
+        trajs.append((x, sim.simulated_potential))
+    (xe, ee), (xc, ec) = trajs
+    assert xe.shape == (100, 6, N_BEADS, 3)
+    # the capture happens at step 3; steps 3..6 are replays
+    np.testing.assert_allclose(xc[:, 2:], xe[:, 2:], rtol=1e-6, atol=1e-5)
+    np.testing.assert_allclose(ec[:, 2:], ee[:, 2:], rtol=1e-5, atol=1e-4)

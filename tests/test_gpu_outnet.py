@@ -1,14 +1,18 @@
 """Output network kernels (mlcg_out_forward, mlcg_out_rev2) against float64
 torch: values against the module's own arithmetic, the reverse seed adjoint
 and the second-order sweep against torch.autograd (jvp for the tangent, then
-reverse mode for the force-matching gradients) at ragged row counts."""
+reverse mode for the force-matching gradients) at ragged row counts.
+
+Every element is held to rtol of the tensor's largest element (check with
+atol_frac=1.0): the first layer is a split-operand product on the fp16 MFMA
+(about 22 significant bits), whose error scales with the sum of its terms."""
 
 import math
 
 import pytest
 import torch
 
-from tests.helpers import rel_err
+from tests.helpers import check
 
 pytestmark = pytest.mark.gpu
 
@@ -51,21 +55,21 @@ def test_out_forward(rows, hh, act, b0, b1):
     d = lambda t: None if t is None else t.double()  # noqa: E731
     x64 = x.double().requires_grad_(True)
     o_ref = _o64(x64, d(W0), d(bb0), d(w1), d(bb1), act)
-    assert rel_err(o, o_ref.detach()) < 2e-6
+    check(o, o_ref.detach(), 2e-6, 'o', atol_frac=1.0)
     z_ref = x64.detach().mm(d(W0).t()) + (0 if bb0 is None else d(bb0))
-    assert rel_err(os_, _act(z_ref, act)) < 2e-6
+    check(os_, _act(z_ref, act), 2e-6, 'os_', atol_frac=1.0)
     if act == 1:
-        assert rel_err(oz, z_ref) < 1e-6
+        check(oz, z_ref, 1e-6, 'oz', atol_frac=1.0)
     else:
         assert oz is None
     (xbar_ref,) = torch.autograd.grad((o_ref * seed.double()).sum(), x64, retain_graph=True)
-    assert rel_err(xbar, xbar_ref) < 2e-6
+    check(xbar, xbar_ref, 2e-6, 'xbar', atol_frac=1.0)
     # all-ones seed when none is given; no o / no saves on request
     o2, _, _, xbar1 = ops.out_forward(x, W0, bb0, w1, bb1, act, reverse=True, want_o=False,
                                       save=False)
     assert o2 is None
     (xbar1_ref,) = torch.autograd.grad(o_ref.sum(), x64)
-    assert rel_err(xbar1, xbar1_ref) < 2e-6
+    check(xbar1, xbar1_ref, 2e-6, 'xbar1', atol_frac=1.0)
 
 
 @pytest.mark.parametrize("rows", [1, 17, 1000, 17920])
@@ -104,12 +108,12 @@ def test_out_rev2_matches_autograd(rows, hh, act, b0, b1, terms):
     ref = dict(zip([id(t) for t in wrt], grads))
     z = lambda t: torch.zeros_like(t) if ref[id(t)] is None else ref[id(t)]  # noqa: E731
     if use_xdot:
-        assert rel_err(odot, odot_ref) < 2e-6
-    assert rel_err(xbar2, z(x64)) < 5e-6
-    assert rel_err(gW0, z(W064)) < 5e-6
-    assert rel_err(gW1, z(w164)) < 5e-6
+        check(odot, odot_ref, 2e-6, 'odot', atol_frac=1.0)
+    check(xbar2, z(x64), 5e-6, 'xbar2', atol_frac=1.0)
+    check(gW0, z(W064), 5e-6, 'gW0', atol_frac=1.0)
+    check(gW1, z(w164), 5e-6, 'gW1', atol_frac=1.0)
     if b0:
-        assert rel_err(gb0, z(b064)) < 5e-6
+        check(gb0, z(b064), 5e-6, 'gb0', atol_frac=1.0)
     else:
         assert gb0 is None
     if b1:

@@ -2,7 +2,8 @@
 oracles (oracle/priors_ref.py, oracle/langevin_ref.py).
 
 Tolerances: fp32 energies and forces within 1e-5
-relative (to the oracle's norm) of the fp64 oracle.
+of the fp64 oracle per element (tests.helpers.check: rtol 1e-5 of the element,
+or 1e-6 of the tensor's largest element).
 """
 
 import math
@@ -13,7 +14,7 @@ import torch
 
 from oracle import langevin_ref as L
 from oracle import priors_ref as P
-from tests.helpers import rel_err
+from tests.helpers import check, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -64,8 +65,8 @@ def test_prior_kernel_vs_oracle(kind):
     E, F = ops.prior_energy_forces(ops.PRIOR_KIND[kind], 3, pos.cuda(), g,
                                    _param_matrix(kind, params).cuda())
     print(kind, "E rel", rel_err(E, E_ref), "F rel", rel_err(F, F_ref))
-    assert rel_err(E, E_ref) < 1e-5
-    assert rel_err(F, F_ref) < 1e-5
+    check(E, E_ref, 1e-5, 'E')
+    check(F, F_ref, 1e-5, 'F')
     # accumulate mode adds onto an existing force array
     F0 = torch.ones_like(F)
     _, F2 = ops.prior_energy_forces(ops.PRIOR_KIND[kind], 3, pos.cuda(), g,
@@ -158,8 +159,8 @@ def test_prior_modules_sumout_and_static():
         E_ref, F_ref = P.prior_energy_forces(name, data.pos.double().cpu(),
                                              nlm["index_mapping"].cpu(),
                                              nlm["mapping_batch"].cpu(), 4, pp)
-        assert rel_err(e, E_ref) < 1e-5, name
-        assert rel_err(f, F_ref) < 1e-5, name
+        check(e, E_ref, 1e-5, name)
+        check(f, F_ref, 1e-5, name)
     assert torch.allclose(out.out["energy"], total_E, atol=1e-5)
     assert torch.allclose(out.out["forces"], total_F, atol=1e-5)
     # generic autograd route: forward energy, then grad wrt pos
@@ -167,7 +168,7 @@ def test_prior_modules_sumout_and_static():
     d2.pos.requires_grad_(True)
     d2 = priors["dihedrals"].model(d2)
     (gpos,) = torch.autograd.grad(d2.out["dihedrals"]["energy"].sum(), d2.pos)
-    assert rel_err(-gpos, out.out["dihedrals"]["forces"]) < 1e-6
+    check(-gpos, out.out["dihedrals"]["forces"], 1e-6, '-gpos')
     # static specialisation
     sp, sconfs = condense_all_priors_for_simulation(model.cpu(), confs)
     sp = sp.cuda()
@@ -198,8 +199,8 @@ def test_baoab_kernel_vs_oracle():
     ops.langevin_baoa(xg, vg, F.cuda(), m.cuda(), bmr.cuda(), 0.004, vs, ns, 7, step=step,
                       noise=xi.cuda())
     ops.langevin_b(vg, Fn.cuda(), m.cuda(), 0.004, step=step)
-    assert rel_err(xg, xr) < 1e-6
-    assert rel_err(vg, vr) < 1e-6
+    check(xg, xr, 1e-6, 'xg')
+    check(vg, vr, 1e-6, 'vg')
     assert int(step.item()) == 1
 
 

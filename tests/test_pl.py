@@ -123,3 +123,50 @@ def test_plmodel_step_matches_the_plain_training_step():
                                       models[1].named_parameters()):
             assert n0 == n1
             assert torch.equal(p0, p1), (it, n0)  # every reduction has a fixed order
+
+
+@pytest.mark.gpu
+def test_plmodel_step_against_oracle_gradients_and_cpu_adamw():
+    """Two PLModel training steps (pl/model.py:113-131 + AdamW) on the fused
+    SchNet: at each step the loss and every parameter gradient match the fp64
+    oracle's force_matching_grads evaluated at the step's parameters (rtol
+    1e-4 per element), and the AdamW update equals torch's CPU AdamW in fp64
+    applied to the same gradients (rtol 1e-6)."""
+    from mlcg_amd import synthetic
+    from oracle import radius as oracle_radius
+    from oracle import schnet_ref as R
+    from tests.helpers import check, make_cfg, make_model
+
+    cfg = make_cfg(num_blocks=2, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=22)
+    b = synthetic.config2(n_frames=8)
+    model = make_model(cfg, sd).train()
+    pl = PLModel(GradientsOut(model), Loss([ForceMSE()])).to("cuda")
+    opt = pl.configure_optimizers(lr=1e-3, weight_decay=0.01)
+    group = opt.param_groups[0]
+    names = [n for n, _ in model.named_parameters()]
+    cpu_params = [p.detach().double().cpu().clone().requires_grad_(False)
+                  for p in model.parameters()]
+    cpu_opt = torch.optim.AdamW(cpu_params, lr=group["lr"], betas=group["betas"],
+                                eps=group["eps"], weight_decay=group["weight_decay"])
+    ei, _ = oracle_radius.radius_graph(b.pos, 20.0, b.batch, False, 1000)
+    args = (torch.from_numpy(b.pos).double(), torch.from_numpy(b.atom_types),
+            torch.from_numpy(b.batch), torch.from_numpy(ei), b.n_frames,
+            torch.from_numpy(b.forces).double())
+    for step in range(2):
+        # the oracle at the parameters this step starts from
+        sd_now = {k: v.detach().double().cpu() for k, v in model.state_dict().items()}
+        loss_ref, _, _, g_ref = R.force_matching_grads(sd_now, cfg, *args)
+        train_epoch(pl, [b.to_torch("cuda")], opt)
+        got_loss = float(pl.logged["train_loss"])
+        assert abs(got_loss - float(loss_ref)) <= 1e-5 * abs(float(loss_ref)), step
+        grads = {n: p.grad.detach().double().cpu() for n, p in model.named_parameters()}
+        for n in names:
+            check(grads[n], g_ref[n], 1e-4, f"step {step} grad {n}")
+        # CPU AdamW (fp64) fed the same gradients the GPU step used
+        for n, p in zip(names, cpu_params):
+            p.grad = grads[n].clone()
+        cpu_opt.step()
+        for n, p_gpu, p_cpu in zip(names, model.parameters(), cpu_params):
+            check(p_gpu.detach(), p_cpu, 1e-6, f"step {step} AdamW update {n}")
+            p_cpu.copy_(p_gpu.detach().double().cpu())  # continue from the GPU state

@@ -77,6 +77,27 @@ def test_metropolis_rule_and_velocity_rescaling():
     assert sim.acceptance_matrix[1, 0] == 20
 
 
+def test_reference_velocity_scaling_option():
+    """reference_velocity_scaling=True applies the factor of the reference's
+    code (parallel_tempering.py:484-497): the configuration entering slot a
+    from slot b is scaled by sqrt(beta_a / beta_b); the default follows the
+    reference's docstring, sqrt(beta_b / beta_a).  Positions and forces move
+    the same way in both."""
+    for ref_scaling, factor_into_cold in ((False, math.sqrt(0.5)), (True, math.sqrt(2.0))):
+        sim = _sim([2.0, 1.0], n_indep=1)
+        sim.reference_velocity_scaling = ref_scaling
+        x, v, f = _state(sim)
+        x0, v0, f0 = x.clone(), v.clone(), f.clone()
+        sim.detect_and_exchange_replicas(x, v, f, torch.tensor([5.0, 1.0]))  # accepted
+        torch.testing.assert_close(v.view(2, 3, 3)[0], v0.view(2, 3, 3)[1] * factor_into_cold)
+        torch.testing.assert_close(v.view(2, 3, 3)[1], v0.view(2, 3, 3)[0] / factor_into_cold)
+        assert torch.equal(x.view(2, 3, 3)[0], x0.view(2, 3, 3)[1])
+        assert torch.equal(f.view(2, 3, 3)[1], f0.view(2, 3, 3)[0])
+    sim = PTSimulation(exchange_interval=5, reference_velocity_scaling=True, n_timesteps=10,
+                       save_interval=10, device="cpu")
+    assert sim.reference_velocity_scaling
+
+
 def test_acceptance_rate_matches_metropolis():
     sim = _sim([1.5, 1.0], n_indep=4000, n_atoms=1, seed=5)
     x, v, f = _state(sim)
