@@ -290,15 +290,33 @@ def gpu_leg(args):
         assert flags == 0, f"radius graph overflowed its capacity (flags {flags})"
         assert int(model.last_graph.rowptr[-1]) == E, "edge count changed"
     dom = kernel_report(timer.summary(), E, P, N, B)[dominant]
+    # the same step with the filter forward on the fp32 MFMA throughout
+    # (MLCG_FILTER_FP32_STRICT) instead of split-fp16 products, for comparison
+    model.strict_fp32_filters = True
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    strict_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    model.strict_fp32_filters = False
     return {"ms_per_step": ms, "E": E, "P": P, "N": N, "B": B, "dominant": dominant,
+            "strict_fp32_ms_per_step": strict_ms,
             "dominant_row": dom, "kernels": warm, "loss": float(loss.detach()),
             "step_kernel_ms": round(sum(per_step.values()), 4)}
 
 
 def radius_leg(reps=10):
+    """Config 3 radius graph, inputs resident in HBM.  Three figures: the
+    kernels' device time (HIP events around count, scan and fill), the
+    exactly-sized call end to end (one host synchronisation to size the
+    output, as the reference's radius.cu:288), and the fixed-capacity call
+    (no synchronisation, the form a captured step uses)."""
     import torch
 
-    from mlcg_amd import ops, synthetic
+    from mlcg_amd import _lib, ops, synthetic
 
     b = synthetic.config3()
     pos = torch.from_numpy(b.pos).cuda()
@@ -308,18 +326,47 @@ def radius_leg(reps=10):
     for _ in range(2):
         g = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr)
     torch.cuda.synchronize()
-    t = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        g = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr)
-        torch.cuda.synchronize()
-        t.append(time.perf_counter() - t0)
-    s = statistics.median(t)
     E = g.num_edges
+    cap = E + 1024
+
+    def timed(fn):
+        t = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            t.append(time.perf_counter() - t0)
+        return statistics.median(t)
+
+    s_exact = timed(lambda: ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr))
+    gc = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, capacity=cap)
+    s_cap = timed(lambda: ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr,
+                                           capacity=cap))
+    gc = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, capacity=cap)
+    torch.cuda.synchronize()
+    assert int(gc.flags.item()) == 0 and int(gc.rowptr[-1].item()) == E
+    names = ("mlcg_radius_count", "mlcg_exclusive_scan2_i32", "mlcg_radius_fill")
+    timer = _lib.LaunchTimer(set(names))
+    _lib.set_timer(timer)
+    for _ in range(reps):
+        ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, capacity=cap)
+    torch.cuda.synchronize()
+    _lib.set_timer(None)
+    summ = timer.summary()
+    dev_ms = sum(summ[k][1] / summ[k][0] for k in names)
+    nbytes = 12 * pos.shape[0] + 8 * (nf + 1) + 16 * E
+    ach = nbytes / (dev_ms * 1e-3) / 1e9
     return {"workload": "config3: 2048 frames x 100-bead globules, rc 15 A, no loops, "
                         "int64 [2,E] canonical order",
-            "E": E, "ms": round(s * 1e3, 4), "edges_per_s": E / s,
-            "algorithmic_bytes": 12 * pos.shape[0] + 8 * (nf + 1) + 16 * E}
+            "E": E, "ms": round(s_exact * 1e3, 4), "edges_per_s": E / s_exact,
+            "ms_capacity_form": round(s_cap * 1e3, 4), "edges_per_s_capacity_form": E / s_cap,
+            "kernels_device_ms": round(dev_ms, 4),
+            "kernels_avg_us": {k: round(summ[k][1] / summ[k][0] * 1e3, 2) for k in names},
+            "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                         "time": "device time of count + scan + fill"}}
 
 
 def fp16_leg(reps=5):
@@ -370,10 +417,12 @@ def md_leg(steps):
     """Config 5: 100 replicas x 268-bead chains, config-2 SchNet (rc 20 A) +
     bonds, angles, 3-term dihedrals and (sigma/r)^6 repulsion, BAOAB at 300 K,
     dt 4 fs, friction 1/ps; radius graph rebuilt every step; the step is
-    captured once as a HIP graph and replayed."""
+    captured once as a HIP graph and replayed.  The per-kernel report comes
+    from a few eager force evaluations on the final state (HIP events cannot
+    bracket launches inside a replayed graph)."""
     import torch
 
-    from mlcg_amd import nn, synthetic
+    from mlcg_amd import _lib, nn, synthetic
     from mlcg_amd.simulation import LangevinSimulation
 
     c = synthetic.CONFIG5_PRIORS
@@ -394,15 +443,75 @@ def md_leg(steps):
     sim.attach_model_and_configurations(model, confs, beta)
     sim.simulate()
     sps = sim.timed_steps / sim.timed_seconds
+    # per-kernel device times of the force evaluation, eagerly, on the final state
+    data = sim.final_data
+    with torch.no_grad():
+        model(data)
+        torch.cuda.synchronize()
+        timer = _lib.LaunchTimer(None)
+        _lib.set_timer(timer)
+        reps = 3
+        for _ in range(reps):
+            model(data)
+        torch.cuda.synchronize()
+        _lib.set_timer(None)
+    g = schnet.last_graph
+    N = data.pos.shape[0]
+    E = int(g.rowptr[-1].item())
+    P = int(g.pairptr[-1].item())
+    summ = {k: (v[0] // reps, v[1] / reps) for k, v in timer.summary().items()}
+    rows = kernel_report(summ, E, P, N, sim.n_sims)
+    dom = max(rows, key=lambda k: rows[k]["total_ms"])
+    d = rows[dom]
+    roof = {k: d.get(k) for k in ("bound", "achieved", "peak", "unit", "frac")}
+    roof.update(kernel=d["kernel"], avg_launch_us=d["avg_us"], launches_per_step=d["launches"])
     return {"workload": "config5: 100 x 268-bead chains, SchNet (3 blocks, rc 20 A) + "
                         "bonds/angles/dihedrals/repulsion priors, BAOAB, HIP-graph step",
             "steps_timed": sim.timed_steps, "ms_per_step": round(1e3 / sps, 4),
             "steps_per_s": sps, "replica_steps_per_s": sps * sim.n_sims,
-            "edge_capacity": schnet.graph_capacity, "prior_constants": c}
+            "edges": E, "pairs": P, "edge_capacity": schnet.graph_capacity,
+            "roofline": roof,
+            "kernels": {k: {kk: v[kk] for kk in ("kernel", "launches", "avg_us", "frac")
+                            if kk in v} for k, v in rows.items()},
+            "prior_constants": c}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, warmups=2, reps=5):
+    for _ in range(warmups):
+        fn()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+    return statistics.median(t), len(t)
 
 
 def cpu_leg(args):
-    """The CPU restatement of the same step on a bounded sample of frames."""
+    """The CPU restatement (oracle/, this repository's op-by-op restatement of
+    the reference, run in fp32) of the config-2 step on a bounded sample of
+    frames: 2 warm-ups, then the median of at least 5 runs."""
     import torch
 
     from mlcg_amd import synthetic
@@ -431,16 +540,139 @@ def cpu_leg(args):
     E = one()  # warm-up
     t = []
     t_start = time.perf_counter()
-    while len(t) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(t) < 50):
+    while len(t) < 5 or (time.perf_counter() - t_start < args.cpu_seconds and len(t) < 50):
         t0 = time.perf_counter()
         one()
         t.append(time.perf_counter() - t0)
     s = statistics.median(t)
     return {"value": E * N_BLOCKS / s, "unit": "edges/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{args.cpu_frames} frames of the config-2 workload (E={E}), "
                       f"oracle/schnet_ref.py fp32 force-matching step incl. brute-force "
                       f"radius graph, median of {len(t)} reps, torch threads={cores}",
             "ms_per_step": round(s * 1e3, 3)}
+
+
+def cpu_configs_leg():
+    """CPU baselines of configs 1, 3, 4 and 5: the
+    oracle restatements in fp32 on the host cores, 2 warm-ups then the median
+    of 5 (configs 1, 3, 4), and 20 steps reported per step (config 5).
+    Configs 4 and 5 run on bounded samples (stated in each record)."""
+    import math as _m
+
+    import numpy as np
+    import torch
+
+    from mlcg_amd import synthetic
+    from oracle import langevin_ref as L
+    from oracle import priors_ref as P
+    from oracle import radius as oracle_radius
+    from oracle import schnet_ref as R
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    torch.set_float32_matmul_precision("highest")
+    out = {"cores": cores, "cpu_model": cpu_model(), "kind": "port"}
+
+    def nl(bt, rc):
+        ei, _ = oracle_radius.radius_graph(bt.pos, rc, bt.batch, False, 1000)
+        return torch.from_numpy(ei)
+
+    def schnet_cfg(blocks, rc, act):
+        return R.SchNetConfig(num_rbf=K_RBF, rbf_lo=0.0, rbf_hi=rc, rbf_cut="cosine",
+                              conv_cut="cosine", conv_lo=0.0, conv_hi=rc, act=act,
+                              num_blocks=blocks)
+
+    # config 1: 1 block, SSP, rc 30, 32 x 10 beads, energy + forces (whole config)
+    b1 = synthetic.config1()
+    c1 = schnet_cfg(1, 30.0, "ssp")
+    sd1 = R.random_state_dict(c1, seed=synthetic.seed_for(1))
+    t1 = [torch.from_numpy(x) for x in (b1.pos, b1.atom_types, b1.batch)]
+    s, n = _median_time(lambda: R.schnet_energy_forces(sd1, c1, t1[0], t1[1], t1[2],
+                                                       nl(b1, 30.0), b1.n_frames))
+    E1 = nl(b1, 30.0).shape[1]
+    out["config1"] = {"value": E1 / s, "unit": "CFConv edges/s (1 block)",
+                      "ms_per_call": round(s * 1e3, 3), "reps": n,
+                      "sample": "whole config 1 (32 x 10 beads), energy + forces incl. "
+                                "the brute-force radius graph"}
+    # config 3: radius graph, whole config, the C brute force (one thread)
+    b3 = synthetic.config3()
+    s, n = _median_time(lambda: oracle_radius.radius_graph(b3.pos, 15.0, b3.batch, False, 1000))
+    E3 = oracle_radius.radius_graph(b3.pos, 15.0, b3.batch, False, 1000)[0].shape[1]
+    out["config3"] = {"value": E3 / s, "unit": "radius-graph edges/s",
+                      "ms_per_call": round(s * 1e3, 3), "reps": n, "threads": 1,
+                      "sample": "whole config 3 (2048 x 100 beads); oracle/radius_ref.c per-frame "
+                                "brute force standing in for torch_cluster's kd-tree"}
+    # config 4: fp32 energy + forces (the reference's fp32 path; the fp16
+    # filter variant is a GPU option) on 8 of the 500-bead globules
+    b4 = synthetic.config4(n_frames=8)
+    c4 = schnet_cfg(N_BLOCKS, 15.0, "tanh")
+    sd4 = R.random_state_dict(c4, seed=synthetic.seed_for(4))
+    t4 = [torch.from_numpy(x) for x in (b4.pos, b4.atom_types, b4.batch)]
+    ei4 = nl(b4, 15.0)
+    s, n = _median_time(lambda: R.schnet_energy_forces(sd4, c4, t4[0], t4[1], t4[2], nl(b4, 15.0),
+                                                       b4.n_frames), warmups=1)
+    out["config4"] = {"value": ei4.shape[1] * N_BLOCKS / s, "unit": "CFConv edges/s",
+                      "ms_per_call": round(s * 1e3, 3), "reps": n,
+                      "sample": f"8 of the 256 frames (E={ei4.shape[1]}), fp32 energy + "
+                                "forces incl. the radius graph"}
+    # config 5: the composite BAOAB step on 2 of the 100 replicas, 20 steps
+    c = synthetic.CONFIG5_PRIORS
+    nrep, nb = 2, 268
+    b5 = synthetic.config5(n_frames=nrep, n_beads=nb)
+    c5 = schnet_cfg(N_BLOCKS, RC, "tanh")
+    sd5 = R.random_state_dict(c5, seed=synthetic.seed_for(5))
+    topo = P.chain_topology(nrep, nb, min_sep=c["repulsion"]["min_separation"])
+
+    def full(M, v):
+        return torch.full((M,), float(v))
+
+    prm = {"bonds": {"x0": full(topo["bonds"][0].shape[1], c["bonds"]["x_0"]),
+                     "k": full(topo["bonds"][0].shape[1], c["bonds"]["k"])},
+           "angles": {"x0": full(topo["angles"][0].shape[1],
+                                 _m.cos(_m.radians(c["angles"]["theta_0_deg"]))),
+                      "k": full(topo["angles"][0].shape[1], c["angles"]["k"])},
+           "dihedrals": {"v_0": full(topo["dihedrals"][0].shape[1], c["dihedrals"]["v_0"]),
+                         "k1s": torch.tensor(c["dihedrals"]["k1s"]).repeat(
+                             topo["dihedrals"][0].shape[1], 1),
+                         "k2s": torch.tensor(c["dihedrals"]["k2s"]).repeat(
+                             topo["dihedrals"][0].shape[1], 1)},
+           "repulsion": {"sigma": full(topo["repulsion"][0].shape[1], c["repulsion"]["sigma"])}}
+    types5 = torch.from_numpy(b5.atom_types)
+    batch5 = torch.from_numpy(b5.batch)
+    m = torch.full((nrep * nb,), c["masses_amu"] / 418.4)
+    beta = 1.0 / (L.KB_KCAL * c["temperature_K"])
+    bmr = torch.sqrt(1.0 / (beta * m))
+    vs, ns = L.constants(c["dt_ps"], c["friction_per_ps"])
+    gen = torch.Generator().manual_seed(5)
+
+    def forces(x):
+        ei = torch.from_numpy(oracle_radius.radius_graph(
+            x.numpy(), RC, b5.batch, False, 1000)[0])
+        _, F = R.schnet_energy_forces(sd5, c5, x, types5, batch5, ei, nrep)
+        for kind, (mp, mb) in topo.items():
+            F = F + P.prior_energy_forces(kind, x, mp, mb, nrep, prm[kind])[1]
+        return F
+
+    x = torch.from_numpy(b5.pos).clone()
+    v = torch.randn(x.shape, generator=gen) * bmr[:, None]
+    F = forces(x)
+    n_steps = 20
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        xi = torch.randn(x.shape, generator=gen)
+        x, v = L.baoa(x, v, F, m, bmr, c["dt_ps"], vs, ns, xi)
+        F = forces(x)
+        v = L.b(v, F, m, c["dt_ps"])
+    s5 = (time.perf_counter() - t0) / n_steps
+    assert bool(np.isfinite(x.numpy()).all())
+    out["config5"] = {"value": nrep / s5, "unit": "replica-steps/s",
+                      "ms_per_step": round(s5 * 1e3, 3),
+                      "ms_per_1000_steps_100_replicas_extrapolated":
+                          round(s5 * 1e3 * 1000 * 100 / nrep, 1),
+                      "sample": f"{nrep} of the 100 replicas x {nb} beads, {n_steps} BAOAB "
+                                "steps, fp32 SchNet + 4 priors + radius graph each step"}
+    return out
 
 
 def main(argv=None):
@@ -477,6 +709,9 @@ def main(argv=None):
     cpu = None if args.no_cpu else cpu_leg(args)
     if cpu:
         print(f"[bench] cpu leg done: {cpu['ms_per_step']:.1f} ms/step", flush=True)
+    cpu_cfg = None if args.no_cpu else cpu_configs_leg()
+    if cpu_cfg:
+        print("[bench] cpu configs 1, 3, 4, 5 done", flush=True)
 
     ms = g["ms_per_step"]
     value = g["E"] * N_BLOCKS / (ms * 1e-3)
@@ -505,6 +740,11 @@ def main(argv=None):
                    "frames": g["B"], "beads_per_frame": g["N"] // max(g["B"], 1),
                    "edges": g["E"], "pairs": g["P"], "blocks": N_BLOCKS},
         "frames_per_s": g["B"] / (ms * 1e-3),
+        "strict_fp32_filter_step": {
+            "ms_per_step": round(g["strict_fp32_ms_per_step"], 4),
+            "edges_per_s": g["E"] * N_BLOCKS / (g["strict_fp32_ms_per_step"] * 1e-3),
+            "note": "same step, filter forward on the fp32 MFMA (MLCG_FILTER_FP32_STRICT) "
+                    "instead of split-fp16 products; both meet the element-wise parity bar"},
         "roofline": roofline,
         "kernels": g["kernels"],
         "step_kernel_ms": g["step_kernel_ms"],
@@ -512,6 +752,7 @@ def main(argv=None):
         "fp16_config4": f16,
         "md_config5": md,
         "cpu_baseline": cpu,
+        "cpu_baselines_other_configs": cpu_cfg,
     }
     print(json.dumps(line))
     return 0
