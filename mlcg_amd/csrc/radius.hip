@@ -8,12 +8,14 @@
 // 125-141).  Output order is canonical: rows by centre i ascending, and
 // within a row neighbours j ascending.
 //
-// Design: one wave per row.  The wave sweeps the row's frame 64 candidates at
-// a time; each lane tests one candidate, a ballot gives the hit mask and
-// mbcnt the rank of each hit, so every row's edges are written as contiguous,
-// coalesced runs.  Two passes (count, then fill at scanned offsets) give an
-// exact, deterministic layout without atomics, cooperative launches or host
-// synchronisation inside the library.
+// Design: two passes (count, then fill at scanned offsets) give an exact,
+// deterministic layout without atomics, cooperative launches or host
+// synchronisation inside the library.  The count runs one thread per row
+// over its frame; the fill one wave per row: the wave sweeps the row's frame
+// 64 candidates at a time, each lane testing one candidate, a ballot gives the
+// hit mask and mbcnt the rank of each hit, so every row's edges are written as
+// contiguous, coalesced runs.  Both stage the positions of a workgroup's
+// frames in LDS.
 //
 // Optional pair exclusion follows the reference kernel's CSR form
 // (radius.cu:113-133, built by exclusion_pair_to_ptr in exclusion_pairs.cpp:
@@ -98,9 +100,12 @@ __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
 // lane that holds it, returns (kept, upper kept) through the references and
 // whether the row overflowed max_nn.  With exclusions, `asym` is set when a
 // kept edge (i, j) has its reverse (j, i) excluded.
-template <bool kFill, bool kExcl>
+// Positions come from `pos` (global memory, node n at pos[3 n]) or, with
+// kStaged, from a workgroup's LDS copy of nodes [base, ...) (node n at
+// pos[3 (n - base)]).
+template <bool kFill, bool kExcl, bool kStaged = false>
 __device__ __forceinline__ bool sweep_row(
-    const float* __restrict__ pos, int64_t i, int64_t start, int64_t end,
+    const float* __restrict__ pos, int64_t base, int64_t i, int64_t start, int64_t end,
     float r2, int loop, int64_t max_nn, const int64_t* __restrict__ exs,
     const int64_t* __restrict__ eptr, int& kept, int& ukept,
     int64_t* __restrict__ ei0, int64_t* __restrict__ ei1, int32_t* __restrict__ col,
@@ -108,7 +113,7 @@ __device__ __forceinline__ bool sweep_row(
     int32_t* __restrict__ eid2pair, int64_t p_base, int64_t p_cap, bool& dropped,
     bool& asym) {
   const int lane = mlcg_lane();
-  const Vec3 a = load_pos(pos, i);
+  const Vec3 a = load_pos(pos, kStaged ? i - base : i);
   int64_t total = 0;
   kept = 0;
   ukept = 0;
@@ -121,7 +126,7 @@ __device__ __forceinline__ bool sweep_row(
     const int64_t j = j0 + lane;
     bool hit = false;
     if (j < end) {
-      float d2 = sqdist_exact(a, load_pos(pos, j));
+      float d2 = sqdist_exact(a, load_pos(pos, kStaged ? j - base : j));
       hit = (d2 < r2) && (loop || j != i);
       if (kExcl && hit) {
         hit = !in_sorted(exs, x_lo, x_hi, j);
@@ -164,28 +169,126 @@ __device__ __forceinline__ bool sweep_row(
   return total > max_nn;
 }
 
+// Work split of the count and fill kernels: a workgroup of kRowWaves waves
+// takes a block of kBlockRows consecutive rows (wave w: rows w, w + 4, ...).
+// The nodes of the frames those rows belong to -- a contiguous node range,
+// as frames are -- are staged once in LDS when they fit (kStage nodes), so
+// every distance test reads LDS instead of L2 and the rows' loads are shared;
+// a block whose frames are larger reads positions from global memory.
+constexpr int kBlockRows = 64;
+constexpr int kStage = 2048;  // nodes staged per workgroup (24 KiB of LDS)
+
+struct BlockNodes {
+  int64_t r0, r1;      // rows of the block
+  int64_t c_lo, c_hi;  // nodes of its frames
+  bool staged;
+};
+
+// Stages the block's nodes (every thread must call; one barrier when staged).
+__device__ __forceinline__ BlockNodes stage_block(const float* __restrict__ pos,
+                                                  const int64_t* __restrict__ batch,
+                                                  const int64_t* __restrict__ frame_ptr,
+                                                  int64_t n, float* sp) {
+  BlockNodes bn;
+  bn.r0 = (int64_t)blockIdx.x * kBlockRows;
+  bn.r1 = bn.r0 + kBlockRows < n ? bn.r0 + kBlockRows : n;
+  bn.c_lo = frame_ptr[batch[bn.r0]];
+  bn.c_hi = frame_ptr[batch[bn.r1 - 1] + 1];
+  bn.staged = bn.c_hi >= bn.c_lo && bn.c_hi - bn.c_lo <= kStage;
+  if (bn.staged) {
+    const int64_t cnt = 3 * (bn.c_hi - bn.c_lo);
+    for (int64_t t = threadIdx.x; t < cnt; t += blockDim.x) sp[t] = pos[3 * bn.c_lo + t];
+    __syncthreads();
+  }
+  return bn;
+}
+
+// The per-row scalars of a wave's rows (row k of wave w: r0 + w + 4 k) are
+// loaded once, lane k holding row k's, so that no row waits on a chain of
+// dependent loads (batch -> frame_ptr -> rowptr) before its sweep; the row
+// loop takes them with readlane.  Offsets are below 2^31 (int32 CSR).
+constexpr int kRowsPerWave = kBlockRows / kRowWaves;
+struct RowBounds {
+  int start, end, e_base, p_base;
+};
+__device__ __forceinline__ RowBounds row_bounds(const BlockNodes& bn,
+                                                const int64_t* __restrict__ batch,
+                                                const int64_t* __restrict__ frame_ptr,
+                                                const int32_t* __restrict__ rowptr,
+                                                const int32_t* __restrict__ pairptr) {
+  RowBounds rb{0, 0, 0, 0};
+  const int lane = mlcg_lane();
+  const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) + kRowWaves * lane;
+  if (lane < kRowsPerWave && i < bn.r1) {
+    const int64_t b = batch[i];
+    rb.start = (int)frame_ptr[b];
+    rb.end = (int)frame_ptr[b + 1];
+    if (rowptr) rb.e_base = rowptr[i];
+    if (pairptr) rb.p_base = pairptr[i];
+  }
+  return rb;
+}
+
+// Pass 1 runs one thread per row (a counting sweep needs no ballots or ranks,
+// and per candidate a thread spends a handful of instructions where a wave
+// per row spends a few dozen on masks): kCountRows rows per workgroup, the
+// positions of their frames staged in LDS as in the fill pass.  Candidates
+// are visited in ascending j, so with a binding max_num_neighbors the kept
+// neighbours are the lowest-index ones: kept = min(hits, max_nn) and the
+// kept upper neighbours (j > i) are what remains after the lower ones and the
+// self loop.
+constexpr int kCountThreads = 256;
+
 template <bool kExcl>
-__global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_count_kernel(
+__global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ batch,
     const int64_t* __restrict__ frame_ptr, int64_t n, float r2, int loop,
     int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
     int32_t* __restrict__ deg, int32_t* __restrict__ udeg, int32_t* __restrict__ overflow) {
-  const int64_t waves = (int64_t)gridDim.x * kRowWaves;
-  bool dropped = false, asym = false;
-  for (int64_t i = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x / MLCG_WAVE); i < n;
-       i += waves) {
-    const int64_t b = batch[i];
-    int kept, ukept;
-    bool over = sweep_row<false, kExcl>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop,
-                                        max_nn, exs, eptr, kept, ukept, nullptr, nullptr,
-                                        nullptr, 0, 0, nullptr, nullptr, nullptr, 0, 0,
-                                        dropped, asym);
-    if (mlcg_lane() == 0) {
-      deg[i] = kept;
-      udeg[i] = ukept;
-      if (over && overflow) atomicOr(overflow, 1);
+  __shared__ float sp[3 * kStage];
+  const int64_t r0 = (int64_t)blockIdx.x * kCountThreads;
+  const int64_t r1 = r0 + kCountThreads < n ? r0 + kCountThreads : n;
+  const int64_t c_lo = frame_ptr[batch[r0]];
+  const int64_t c_hi = frame_ptr[batch[r1 - 1] + 1];
+  const bool staged = c_hi >= c_lo && c_hi - c_lo <= kStage;  // uniform
+  if (staged) {
+    for (int64_t t = threadIdx.x; t < 3 * (c_hi - c_lo); t += blockDim.x)
+      sp[t] = pos[3 * c_lo + t];
+    __syncthreads();
+  }
+  const int64_t i = r0 + threadIdx.x;
+  if (i >= r1) return;
+  const int64_t b = batch[i];
+  const int64_t start = frame_ptr[b], end = frame_ptr[b + 1];
+  const bool local = staged && start >= c_lo && end <= c_hi;
+  const Vec3 a = local ? load_pos(sp, i - c_lo) : load_pos(pos, i);
+  int64_t x_lo = 0, x_hi = 0;
+  if (kExcl) {
+    x_lo = eptr[i];
+    x_hi = eptr[i + 1];
+  }
+  int lower = 0, self = 0, upper = 0;
+  bool asym = false;
+  for (int64_t j = start; j < end; ++j) {
+    const float d2 = sqdist_exact(a, local ? load_pos(sp, j - c_lo) : load_pos(pos, j));
+    bool hit = (d2 < r2) && (loop || j != i);
+    if (kExcl && hit) {
+      hit = !in_sorted(exs, x_lo, x_hi, j);
+      if (hit && in_sorted(exs, eptr[j], eptr[j + 1], i)) asym = true;
+    }
+    if (hit) {
+      lower += j < i;
+      self += j == i;
+      upper += j > i;
     }
   }
+  const int64_t total = (int64_t)lower + self + upper;
+  const int64_t kept = total < max_nn ? total : max_nn;
+  const int64_t room = max_nn - lower - self;
+  const int64_t ukept = room <= 0 ? 0 : (upper < room ? upper : room);
+  deg[i] = (int32_t)kept;
+  udeg[i] = (int32_t)ukept;
+  if (total > max_nn && overflow) atomicOr(overflow, 1);
   if (kExcl && asym && overflow) atomicOr(overflow, 4);
 }
 
@@ -198,18 +301,28 @@ __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
     int64_t e_stride, int64_t* __restrict__ edge_index, int32_t* __restrict__ col,
     int64_t p_cap, int64_t p_stride, int32_t* __restrict__ pair_ij,
     int32_t* __restrict__ eid2pair, int32_t* __restrict__ overflow) {
-  const int64_t waves = (int64_t)gridDim.x * kRowWaves;
+  __shared__ float sp[3 * kStage];
+  const BlockNodes bn = stage_block(pos, batch, frame_ptr, n, sp);
+  const RowBounds rb = row_bounds(bn, batch, frame_ptr, rowptr, pairptr);
   int32_t* pi = pair_ij;
   int32_t* pj = pair_ij ? pair_ij + p_stride : nullptr;
   bool dropped = false, asym = false;
-  for (int64_t i = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x / MLCG_WAVE); i < n;
-       i += waves) {
-    const int64_t b = batch[i];
+  for (int k = 0; k < kRowsPerWave; ++k) {
+    const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) + kRowWaves * k;
+    if (i >= bn.r1) break;
+    const int64_t start = __builtin_amdgcn_readlane(rb.start, k);
+    const int64_t end = __builtin_amdgcn_readlane(rb.end, k);
+    const int64_t e_base = __builtin_amdgcn_readlane(rb.e_base, k);
+    const int64_t p_base = __builtin_amdgcn_readlane(rb.p_base, k);
     int kept, ukept;
-    sweep_row<true, kExcl>(pos, i, frame_ptr[b], frame_ptr[b + 1], r2, loop, max_nn, exs,
-                           eptr, kept, ukept, edge_index, edge_index + e_stride, col,
-                           rowptr[i], e_cap, pi, pj, eid2pair, pairptr ? pairptr[i] : 0,
-                           p_cap, dropped, asym);
+    if (bn.staged && start >= bn.c_lo && end <= bn.c_hi)  // wave-uniform
+      sweep_row<true, kExcl, true>(sp, bn.c_lo, i, start, end, r2, loop, max_nn, exs, eptr,
+                                   kept, ukept, edge_index, edge_index + e_stride, col, e_base,
+                                   e_cap, pi, pj, eid2pair, p_base, p_cap, dropped, asym);
+    else
+      sweep_row<true, kExcl>(pos, 0, i, start, end, r2, loop, max_nn, exs, eptr, kept, ukept,
+                             edge_index, edge_index + e_stride, col, e_base, e_cap, pi, pj,
+                             eid2pair, p_base, p_cap, dropped, asym);
   }
   if (dropped && overflow) atomicOr(overflow, 2);
 }
@@ -377,13 +490,13 @@ extern "C" int mlcg_radius_count(const float* pos, const int64_t* batch,
                                  const int64_t* exclude_pair_xs,
                                  const int64_t* ptr_exclude_pair_xs, int32_t* deg,
                                  int32_t* upper_deg, int32_t* overflow, void* stream) {
-  MLCG_REQUIRE(n_nodes >= 0 && r >= 0.0 && max_num_neighbors >= 0);
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
+               max_num_neighbors >= 0);
   MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && batch && frame_ptr && deg && upper_deg);
   const float r2 = (float)(r * r);
-  unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, kRowWaves), 16);
-  dim3 grid(groups), block(kRowWaves * MLCG_WAVE);
+  dim3 grid(mlcg_div_up(n_nodes, kCountThreads)), block(kCountThreads);
   hipStream_t s = mlcg_stream(stream);
   if (exclude_pair_xs)
     hipLaunchKernelGGL(radius_count_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
@@ -478,7 +591,8 @@ extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
                                 int64_t pair_capacity, int64_t pair_stride,
                                 int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                                 void* stream) {
-  MLCG_REQUIRE(n_nodes >= 0 && r >= 0.0 && max_num_neighbors >= 0);
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
+               max_num_neighbors >= 0);
   MLCG_REQUIRE(edge_capacity >= 0 && edge_stride >= edge_capacity);
   MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
   if (n_nodes == 0 || edge_capacity == 0) return MLCG_OK;
@@ -486,8 +600,7 @@ extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
   MLCG_REQUIRE(!pair_ij || (pairptr && pair_stride >= pair_capacity));
   MLCG_REQUIRE(!eid2pair || pair_ij);
   const float r2 = (float)(r * r);
-  unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, kRowWaves), 16);
-  dim3 grid(groups), block(kRowWaves * MLCG_WAVE);
+  dim3 grid(mlcg_div_up(n_nodes, kBlockRows)), block(kRowWaves * MLCG_WAVE);
   hipStream_t s = mlcg_stream(stream);
   if (exclude_pair_xs)
     hipLaunchKernelGGL(radius_fill_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
