@@ -73,6 +73,17 @@ int mlcg_radius_count(const float* pos, const int64_t* batch,
                       const int64_t* ptr_exclude_pair_xs, int32_t* deg,
                       int32_t* upper_deg, int32_t* overflow, void* stream);
 
+/* mlcg_radius_count for float64 positions: the same membership test in
+ * double arithmetic, d2 < r*r (r*r rounded once, in double), as the
+ * reference's kernel runs it for double inputs (the AT_DISPATCH over the
+ * scalar type and `scalar_t r_squared = r*r` of radius.cu:243-250). */
+int mlcg_radius_count_f64(const double* pos, const int64_t* batch,
+                          const int64_t* frame_ptr, int64_t n_nodes, double r,
+                          int loop, int64_t max_num_neighbors,
+                          const int64_t* exclude_pair_xs,
+                          const int64_t* ptr_exclude_pair_xs, int32_t* deg,
+                          int32_t* upper_deg, int32_t* overflow, void* stream);
+
 /* Exclusive scan of two int32 vectors of length n into out_a/out_b (length
  * n + 1, the totals at index n).  `workspace` holds
  * mlcg_scan_workspace_ints(n) int32.  Replaces the block/grid scan of
@@ -118,6 +129,19 @@ int mlcg_radius_fill(const float* pos, const int64_t* batch,
                      int64_t pair_capacity, int64_t pair_stride,
                      int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                      void* stream);
+
+/* mlcg_radius_fill for float64 positions (membership as in
+ * mlcg_radius_count_f64); writes the edge list only (the pair structures of
+ * the CFConv pipeline take float32 positions).  Replaces radius.cu:117-145
+ * for double inputs. */
+int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
+                         const int64_t* frame_ptr, int64_t n_nodes, double r,
+                         int loop, int64_t max_num_neighbors,
+                         const int64_t* exclude_pair_xs,
+                         const int64_t* ptr_exclude_pair_xs,
+                         const int32_t* rowptr, int64_t edge_capacity,
+                         int64_t edge_stride, int64_t* edge_index,
+                         int32_t* overflow, void* stream);
 
 /* HOST function (host pointers, no stream): the reference's
  * exclusion_pair_to_ptr (exclusion_pairs.cpp:7-62).  exc_pair_index is

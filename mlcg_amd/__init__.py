@@ -3,7 +3,11 @@ hot path: radius graph, Gaussian-RBF filter network, CFConv gather/scatter
 with hand-derived force backward and force-matching double backward, priors
 and the Langevin integrator, behind mlcg's module API."""
 
-from . import ops
+from . import library, ops
 from ._lib import available, version
+
+# torch.ops.mlcg.radius_cuda / exclusion_pair_to_ptr, as the reference's
+# extension registers them
+library.register()
 
 __all__ = ["ops", "available", "version"]

@@ -36,6 +36,9 @@ _SIGNATURES = {
     "mlcg_version": [],
     "mlcg_frame_ptr_from_batch": [_P, _I64, _I64, _P, _P],
     "mlcg_radius_count": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
+    "mlcg_radius_count_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
+    "mlcg_radius_fill_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
+                             _P, _P],
     "mlcg_exclusion_pair_to_ptr": [_P, _I64, _I64, _P, _P],
     "mlcg_scan_workspace_ints": [_I64],
     "mlcg_exclusive_scan2_i32": [_P, _P, _I64, _P, _P, _P, _P],

@@ -34,12 +34,16 @@ namespace {
 
 constexpr int kRowWaves = 4;  // waves per workgroup (256 threads)
 
-struct Vec3 {
-  float x, y, z;
+// Positions are float32 or float64 (T); the membership test runs in T, as
+// the reference's kernel runs it in its scalar type (radius.cu:243-250).
+template <typename T>
+struct Vec3T {
+  T x, y, z;
 };
 
-__device__ __forceinline__ Vec3 load_pos(const float* __restrict__ pos, int64_t n) {
-  Vec3 v;
+template <typename T>
+__device__ __forceinline__ Vec3T<T> load_pos(const T* __restrict__ pos, int64_t n) {
+  Vec3T<T> v;
   v.x = pos[3 * n + 0];
   v.y = pos[3 * n + 1];
   v.z = pos[3 * n + 2];
@@ -49,12 +53,13 @@ __device__ __forceinline__ Vec3 load_pos(const float* __restrict__ pos, int64_t 
 // Squared distance exactly as ((dx*dx + dy*dy) + dz*dz) with round-to-nearest
 // on every operation: contraction into FMA is disabled so that membership at
 // the cutoff boundary is reproducible bit for bit by a plain C restatement.
-__device__ __forceinline__ float sqdist_exact(Vec3 a, Vec3 b) {
+template <typename T>
+__device__ __forceinline__ T sqdist_exact(Vec3T<T> a, Vec3T<T> b) {
 #pragma clang fp contract(off)
-  float dx = b.x - a.x;
-  float dy = b.y - a.y;
-  float dz = b.z - a.z;
-  float s = dx * dx;
+  T dx = b.x - a.x;
+  T dy = b.y - a.y;
+  T dz = b.z - a.z;
+  T s = dx * dx;
   s = s + dy * dy;
   s = s + dz * dz;
   return s;
@@ -103,17 +108,17 @@ __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
 // Positions come from `pos` (global memory, node n at pos[3 n]) or, with
 // kStaged, from a workgroup's LDS copy of nodes [base, ...) (node n at
 // pos[3 (n - base)]).
-template <bool kFill, bool kExcl, bool kStaged = false>
+template <bool kFill, bool kExcl, bool kStaged, typename T>
 __device__ __forceinline__ bool sweep_row(
-    const float* __restrict__ pos, int64_t base, int64_t i, int64_t start, int64_t end,
-    float r2, int loop, int64_t max_nn, const int64_t* __restrict__ exs,
+    const T* __restrict__ pos, int64_t base, int64_t i, int64_t start, int64_t end,
+    T r2, int loop, int64_t max_nn, const int64_t* __restrict__ exs,
     const int64_t* __restrict__ eptr, int& kept, int& ukept,
     int64_t* __restrict__ ei0, int64_t* __restrict__ ei1, int32_t* __restrict__ col,
     int64_t e_base, int64_t e_cap, int32_t* __restrict__ pi, int32_t* __restrict__ pj,
     int32_t* __restrict__ eid2pair, int64_t p_base, int64_t p_cap, bool& dropped,
     bool& asym) {
   const int lane = mlcg_lane();
-  const Vec3 a = load_pos(pos, kStaged ? i - base : i);
+  const Vec3T<T> a = load_pos(pos, kStaged ? i - base : i);
   int64_t total = 0;
   kept = 0;
   ukept = 0;
@@ -126,7 +131,7 @@ __device__ __forceinline__ bool sweep_row(
     const int64_t j = j0 + lane;
     bool hit = false;
     if (j < end) {
-      float d2 = sqdist_exact(a, load_pos(pos, kStaged ? j - base : j));
+      const T d2 = sqdist_exact(a, load_pos(pos, kStaged ? j - base : j));
       hit = (d2 < r2) && (loop || j != i);
       if (kExcl && hit) {
         hit = !in_sorted(exs, x_lo, x_hi, j);
@@ -185,10 +190,11 @@ struct BlockNodes {
 };
 
 // Stages the block's nodes (every thread must call; one barrier when staged).
-__device__ __forceinline__ BlockNodes stage_block(const float* __restrict__ pos,
+template <typename T>
+__device__ __forceinline__ BlockNodes stage_block(const T* __restrict__ pos,
                                                   const int64_t* __restrict__ batch,
                                                   const int64_t* __restrict__ frame_ptr,
-                                                  int64_t n, float* sp) {
+                                                  int64_t n, T* sp) {
   BlockNodes bn;
   bn.r0 = (int64_t)blockIdx.x * kBlockRows;
   bn.r1 = bn.r0 + kBlockRows < n ? bn.r0 + kBlockRows : n;
@@ -239,13 +245,13 @@ __device__ __forceinline__ RowBounds row_bounds(const BlockNodes& bn,
 // self loop.
 constexpr int kCountThreads = 256;
 
-template <bool kExcl>
+template <bool kExcl, typename T>
 __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
-    const float* __restrict__ pos, const int64_t* __restrict__ batch,
-    const int64_t* __restrict__ frame_ptr, int64_t n, float r2, int loop,
+    const T* __restrict__ pos, const int64_t* __restrict__ batch,
+    const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop,
     int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
     int32_t* __restrict__ deg, int32_t* __restrict__ udeg, int32_t* __restrict__ overflow) {
-  __shared__ float sp[3 * kStage];
+  __shared__ T sp[3 * kStage];
   const int64_t r0 = (int64_t)blockIdx.x * kCountThreads;
   const int64_t r1 = r0 + kCountThreads < n ? r0 + kCountThreads : n;
   const int64_t c_lo = frame_ptr[batch[r0]];
@@ -261,7 +267,7 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
   const int64_t b = batch[i];
   const int64_t start = frame_ptr[b], end = frame_ptr[b + 1];
   const bool local = staged && start >= c_lo && end <= c_hi;
-  const Vec3 a = local ? load_pos(sp, i - c_lo) : load_pos(pos, i);
+  const Vec3T<T> a = local ? load_pos(sp, i - c_lo) : load_pos(pos, i);
   int64_t x_lo = 0, x_hi = 0;
   if (kExcl) {
     x_lo = eptr[i];
@@ -270,7 +276,7 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
   int lower = 0, self = 0, upper = 0;
   bool asym = false;
   for (int64_t j = start; j < end; ++j) {
-    const float d2 = sqdist_exact(a, local ? load_pos(sp, j - c_lo) : load_pos(pos, j));
+    const T d2 = sqdist_exact(a, local ? load_pos(sp, j - c_lo) : load_pos(pos, j));
     bool hit = (d2 < r2) && (loop || j != i);
     if (kExcl && hit) {
       hit = !in_sorted(exs, x_lo, x_hi, j);
@@ -292,16 +298,16 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
   if (kExcl && asym && overflow) atomicOr(overflow, 4);
 }
 
-template <bool kExcl>
+template <bool kExcl, typename T>
 __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
-    const float* __restrict__ pos, const int64_t* __restrict__ batch,
-    const int64_t* __restrict__ frame_ptr, int64_t n, float r2, int loop,
+    const T* __restrict__ pos, const int64_t* __restrict__ batch,
+    const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop,
     int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ pairptr, int64_t e_cap,
     int64_t e_stride, int64_t* __restrict__ edge_index, int32_t* __restrict__ col,
     int64_t p_cap, int64_t p_stride, int32_t* __restrict__ pair_ij,
     int32_t* __restrict__ eid2pair, int32_t* __restrict__ overflow) {
-  __shared__ float sp[3 * kStage];
+  __shared__ T sp[3 * kStage];
   const BlockNodes bn = stage_block(pos, batch, frame_ptr, n, sp);
   const RowBounds rb = row_bounds(bn, batch, frame_ptr, rowptr, pairptr);
   int32_t* pi = pair_ij;
@@ -320,7 +326,7 @@ __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
                                    kept, ukept, edge_index, edge_index + e_stride, col, e_base,
                                    e_cap, pi, pj, eid2pair, p_base, p_cap, dropped, asym);
     else
-      sweep_row<true, kExcl>(pos, 0, i, start, end, r2, loop, max_nn, exs, eptr, kept, ukept,
+      sweep_row<true, kExcl, false>(pos, 0, i, start, end, r2, loop, max_nn, exs, eptr, kept, ukept,
                              edge_index, edge_index + e_stride, col, e_base, e_cap, pi, pj,
                              eid2pair, p_base, p_cap, dropped, asym);
   }
@@ -484,29 +490,87 @@ extern "C" int mlcg_frame_ptr_from_batch(const int64_t* batch, int64_t n_nodes,
   return mlcg_launch_status();
 }
 
+namespace {
+
+template <typename T>
+int launch_radius_count(const T* pos, const int64_t* batch, const int64_t* frame_ptr,
+                        int64_t n_nodes, double r, int loop, int64_t max_num_neighbors,
+                        const int64_t* exclude_pair_xs, const int64_t* ptr_exclude_pair_xs,
+                        int32_t* deg, int32_t* upper_deg, int32_t* overflow, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
+               max_num_neighbors >= 0);
+  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && batch && frame_ptr && deg && upper_deg);
+  const T r2 = (T)(r * r);  // r*r in double, then the scalar type (radius.cu:250)
+  dim3 grid(mlcg_div_up(n_nodes, kCountThreads)), block(kCountThreads);
+  hipStream_t s = mlcg_stream(stream);
+  if (exclude_pair_xs)
+    hipLaunchKernelGGL((radius_count_kernel<true, T>), grid, block, 0, s, pos, batch,
+                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
+                       ptr_exclude_pair_xs, deg, upper_deg, overflow);
+  else
+    hipLaunchKernelGGL((radius_count_kernel<false, T>), grid, block, 0, s, pos, batch,
+                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, deg,
+                       upper_deg, overflow);
+  return mlcg_launch_status();
+}
+
+template <typename T>
+int launch_radius_fill(const T* pos, const int64_t* batch, const int64_t* frame_ptr,
+                       int64_t n_nodes, double r, int loop, int64_t max_num_neighbors,
+                       const int64_t* exclude_pair_xs, const int64_t* ptr_exclude_pair_xs,
+                       const int32_t* rowptr, const int32_t* pairptr, int64_t edge_capacity,
+                       int64_t edge_stride, int64_t* edge_index, int32_t* col,
+                       int64_t pair_capacity, int64_t pair_stride, int32_t* pair_ij,
+                       int32_t* eid2pair, int32_t* overflow, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
+               max_num_neighbors >= 0);
+  MLCG_REQUIRE(edge_capacity >= 0 && edge_stride >= edge_capacity);
+  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
+  if (n_nodes == 0 || edge_capacity == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && batch && frame_ptr && rowptr && edge_index);
+  MLCG_REQUIRE(!pair_ij || (pairptr && pair_stride >= pair_capacity));
+  MLCG_REQUIRE(!eid2pair || pair_ij);
+  const T r2 = (T)(r * r);
+  dim3 grid(mlcg_div_up(n_nodes, kBlockRows)), block(kRowWaves * MLCG_WAVE);
+  hipStream_t s = mlcg_stream(stream);
+  if (exclude_pair_xs)
+    hipLaunchKernelGGL((radius_fill_kernel<true, T>), grid, block, 0, s, pos, batch,
+                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
+                       ptr_exclude_pair_xs, rowptr, pairptr, edge_capacity, edge_stride,
+                       edge_index, col, pair_capacity, pair_stride, pair_ij, eid2pair,
+                       overflow);
+  else
+    hipLaunchKernelGGL((radius_fill_kernel<false, T>), grid, block, 0, s, pos, batch,
+                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr,
+                       rowptr, pairptr, edge_capacity, edge_stride, edge_index, col,
+                       pair_capacity, pair_stride, pair_ij, eid2pair, overflow);
+  return mlcg_launch_status();
+}
+
+}  // namespace
+
 extern "C" int mlcg_radius_count(const float* pos, const int64_t* batch,
                                  const int64_t* frame_ptr, int64_t n_nodes, double r,
                                  int loop, int64_t max_num_neighbors,
                                  const int64_t* exclude_pair_xs,
                                  const int64_t* ptr_exclude_pair_xs, int32_t* deg,
                                  int32_t* upper_deg, int32_t* overflow, void* stream) {
-  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
-               max_num_neighbors >= 0);
-  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
-  if (n_nodes == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && batch && frame_ptr && deg && upper_deg);
-  const float r2 = (float)(r * r);
-  dim3 grid(mlcg_div_up(n_nodes, kCountThreads)), block(kCountThreads);
-  hipStream_t s = mlcg_stream(stream);
-  if (exclude_pair_xs)
-    hipLaunchKernelGGL(radius_count_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
-                       n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
-                       ptr_exclude_pair_xs, deg, upper_deg, overflow);
-  else
-    hipLaunchKernelGGL(radius_count_kernel<false>, grid, block, 0, s, pos, batch, frame_ptr,
-                       n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, deg,
-                       upper_deg, overflow);
-  return mlcg_launch_status();
+  return launch_radius_count(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
+                             exclude_pair_xs, ptr_exclude_pair_xs, deg, upper_deg, overflow,
+                             stream);
+}
+
+extern "C" int mlcg_radius_count_f64(const double* pos, const int64_t* batch,
+                                     const int64_t* frame_ptr, int64_t n_nodes, double r,
+                                     int loop, int64_t max_num_neighbors,
+                                     const int64_t* exclude_pair_xs,
+                                     const int64_t* ptr_exclude_pair_xs, int32_t* deg,
+                                     int32_t* upper_deg, int32_t* overflow, void* stream) {
+  return launch_radius_count(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
+                             exclude_pair_xs, ptr_exclude_pair_xs, deg, upper_deg, overflow,
+                             stream);
 }
 
 extern "C" int64_t mlcg_scan_workspace_ints(int64_t n) {
@@ -591,29 +655,25 @@ extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
                                 int64_t pair_capacity, int64_t pair_stride,
                                 int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                                 void* stream) {
-  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
-               max_num_neighbors >= 0);
-  MLCG_REQUIRE(edge_capacity >= 0 && edge_stride >= edge_capacity);
-  MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
-  if (n_nodes == 0 || edge_capacity == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && batch && frame_ptr && rowptr && edge_index);
-  MLCG_REQUIRE(!pair_ij || (pairptr && pair_stride >= pair_capacity));
-  MLCG_REQUIRE(!eid2pair || pair_ij);
-  const float r2 = (float)(r * r);
-  dim3 grid(mlcg_div_up(n_nodes, kBlockRows)), block(kRowWaves * MLCG_WAVE);
-  hipStream_t s = mlcg_stream(stream);
-  if (exclude_pair_xs)
-    hipLaunchKernelGGL(radius_fill_kernel<true>, grid, block, 0, s, pos, batch, frame_ptr,
-                       n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
-                       ptr_exclude_pair_xs, rowptr, pairptr, edge_capacity, edge_stride,
-                       edge_index, col, pair_capacity, pair_stride, pair_ij, eid2pair,
-                       overflow);
-  else
-    hipLaunchKernelGGL(radius_fill_kernel<false>, grid, block, 0, s, pos, batch, frame_ptr,
-                       n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, rowptr,
-                       pairptr, edge_capacity, edge_stride, edge_index, col, pair_capacity,
-                       pair_stride, pair_ij, eid2pair, overflow);
-  return mlcg_launch_status();
+  return launch_radius_fill(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
+                            exclude_pair_xs, ptr_exclude_pair_xs, rowptr, pairptr,
+                            edge_capacity, edge_stride, edge_index, col, pair_capacity,
+                            pair_stride, pair_ij, eid2pair, overflow, stream);
+}
+
+extern "C" int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
+                                    const int64_t* frame_ptr, int64_t n_nodes, double r,
+                                    int loop, int64_t max_num_neighbors,
+                                    const int64_t* exclude_pair_xs,
+                                    const int64_t* ptr_exclude_pair_xs,
+                                    const int32_t* rowptr, int64_t edge_capacity,
+                                    int64_t edge_stride, int64_t* edge_index,
+                                    int32_t* overflow, void* stream) {
+  return launch_radius_fill(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
+                            exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
+                            (const int32_t*)nullptr, edge_capacity, edge_stride, edge_index,
+                            (int32_t*)nullptr, 0, 0, (int32_t*)nullptr, (int32_t*)nullptr,
+                            overflow, stream);
 }
 
 // Host-side conversion of an exclusion pair list to the per-row CSR the

@@ -23,8 +23,8 @@ def radius_graph(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] = None
 
     With flow="target_to_source" row 0 is the centre (as mlcg calls it,
     torch_impl.py:216-224); "source_to_target" swaps the rows."""
-    g = ops.radius_graph(x.detach().float(), r, batch=batch, loop=loop,
-                         max_num_neighbors=max_num_neighbors)
+    xm = x.detach() if x.dtype == torch.float64 else x.detach().float()
+    g = ops.radius_graph(xm, r, batch=batch, loop=loop, max_num_neighbors=max_num_neighbors)
     ei = g.edge_index
     if flow == "source_to_target":
         ei = ei.flip(0)
@@ -43,10 +43,14 @@ def radius_cuda(x: torch.Tensor, ptr_x: Optional[torch.Tensor], r: float,
     """(edge_index [2, E] int64, distance [E]) with the arguments of the
     reference's native operator ``mlcg::radius_cuda`` (radius.cu:197-307):
     frames given by ``ptr_x`` [B+1] (None = one frame), optional exclusion CSR.
-    Edges come out in canonical (centre, neighbour) order; x must be float32
-    (the reference also accepts f16/bf16/f64)."""
+    Edges come out in canonical (centre, neighbour) order.  x is float32 or
+    float64, the membership test running in x's type as in the reference's
+    dispatch (radius.cu:243-250); float16/bfloat16 raise (the reference also
+    takes them)."""
     require_device(x)
     _check_2d(x)
+    if x.dtype not in (torch.float32, torch.float64):
+        raise RuntimeError(f"radius_cuda takes float32 or float64 positions, got {x.dtype}")
     n = x.shape[0]
     if ptr_x is None:
         ptr_x = torch.tensor([0, n], dtype=torch.int64, device=x.device)
@@ -82,9 +86,11 @@ def radius_distance_fn(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] 
     exs = eptr = None
     if exclude_pair_indices is not None:
         exs, eptr = ops.exclusion_pair_to_ptr(exclude_pair_indices, x.size(0))
-    # membership is decided in fp32 (the kernel's arithmetic); the distances
-    # themselves are computed in x's dtype so fp64 gradchecks stay exact
-    g = ops.radius_graph(x.detach().float(), r, batch=batch, loop=loop,
+    # membership is decided in x's precision for float64 (the reference's
+    # scalar-type dispatch), in fp32 otherwise; the distances are computed in
+    # x's dtype so fp64 gradchecks stay exact
+    xm = x.detach() if x.dtype == torch.float64 else x.detach().float()
+    g = ops.radius_graph(xm, r, batch=batch, loop=loop,
                          max_num_neighbors=max_num_neighbors, n_frames=batch_size,
                          exclude_pair_xs=exs, ptr_exclude_pair_xs=eptr)
     ei = g.edge_index

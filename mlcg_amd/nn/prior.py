@@ -89,6 +89,7 @@ class _Prior(torch.nn.Module):
             return data.batch
         return torch.zeros(data.pos.shape[0], dtype=torch.long, device=data.pos.device)
 
+    @torch.compiler.disable  # kernel launches: opaque to torch.compile
     def forward(self, data):
         require_device(data.pos)
         g = self.prior_graph(data)
@@ -97,6 +98,7 @@ class _Prior(torch.nn.Module):
         data.out[self.name] = {ENERGY_KEY: E}
         return data
 
+    @torch.compiler.disable
     def energy_forces(self, data, create_graph: bool = False,
                       forces: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         """(E [B], F [N, 3]); F is added into `forces` when given."""

@@ -321,6 +321,10 @@ class SchNet(torch.nn.Module):
         return g
 
     # ------------------------------------------------------------------
+    # The fused path launches HIP kernels through ctypes: torch.compile runs
+    # it as an opaque call (a graph break), the compiled code around it
+    # unchanged.
+    @torch.compiler.disable
     def forward(self, data):
         spec = self.fused_spec()
         if spec is None:
@@ -335,6 +339,7 @@ class SchNet(torch.nn.Module):
         data.out[self.name] = {ENERGY_KEY: E}
         return data
 
+    @torch.compiler.disable
     def energy_forces(self, data, create_graph: bool):
         """Fused energy and forces (used by GradientsOut)."""
         spec = self.fused_spec()

@@ -150,7 +150,8 @@ def radius_graph(
     max_num_neighbors, flow="target_to_source")`` as called at
     ``mlcg/neighbor_list/torch_impl.py:216-224``, with a deterministic
     canonical order (i ascending, then j ascending).  The membership test is
-    ``d2 < fl32(r*r)`` with d2 = ((dx*dx + dy*dy) + dz*dz) in fp32.
+    ``d2 < fl32(r*r)`` with d2 = ((dx*dx + dy*dy) + dz*dz) in fp32, or in fp64
+    (``d2 < r*r``) for float64 positions (edge list only, no pair structures).
 
     with_pairs additionally builds the receiver CSR and pair map used by the
     CFConv kernels (it requires a symmetric graph, i.e. no binding
@@ -171,7 +172,17 @@ def radius_graph(
     do not count towards ``max_num_neighbors``.  With ``with_pairs`` the
     exclusions must be symmetric (flag bit 2 otherwise).
     """
-    pos = _validate_pos(pos)
+    f64 = pos.dtype == torch.float64
+    if f64:
+        # the membership test in double arithmetic (the reference dispatches
+        # on the scalar type, radius.cu:243-250); edge list only
+        require_device(pos)
+        _check(pos.dim() == 2 and pos.shape[1] == 3,
+               f"pos must be [N, 3], got {tuple(pos.shape)}")
+        _check(not with_pairs, "the CFConv pair structures take float32 positions")
+        pos = pos.contiguous()
+    else:
+        pos = _validate_pos(pos)
     n = pos.shape[0]
     dev = pos.device
     if batch is None:
@@ -195,8 +206,9 @@ def radius_graph(
     deg = torch.empty(n, dtype=torch.int32, device=dev)
     udeg = torch.empty(n, dtype=torch.int32, device=dev)
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
-    call("mlcg_radius_count", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
-         int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(deg), ptr(udeg), ptr(flags), s)
+    call("mlcg_radius_count_f64" if f64 else "mlcg_radius_count", ptr(pos), ptr(batch),
+         ptr(frame_ptr), n, float(r), int(loop), int(max_num_neighbors), ptr(exs), ptr(eptr),
+         ptr(deg), ptr(udeg), ptr(flags), s)
     rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, _lib.load().mlcg_scan_workspace_ints(n)), dtype=torch.int32,
@@ -228,11 +240,16 @@ def radius_graph(
         pair_ij = torch.empty(2, p_cap, dtype=torch.int32, device=dev)
         eid2pair = (torch.empty if capacity is None else torch.zeros)(
             e_cap, dtype=torch.int32, device=dev)
-    call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
-         int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr),
-         ptr(pairptr) if with_pairs else None,
-         e_cap, e_cap, ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij),
-         ptr(eid2pair), ptr(flags), s)
+    if f64:
+        call("mlcg_radius_fill_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+             int(loop), int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr), e_cap, e_cap,
+             ptr(edge_index), ptr(flags), s)
+    else:
+        call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
+             int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr),
+             ptr(pairptr) if with_pairs else None,
+             e_cap, e_cap, ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij),
+             ptr(eid2pair), ptr(flags), s)
     if capacity is not None:
         # rows past the capacity were dropped by the fill: clamp the CSR (and
         # the pair count) so that every consumer stays inside the buffers

@@ -40,6 +40,10 @@ def _load():
         lib.oracle_radius_fill.argtypes = [P, P, ctypes.c_int64, ctypes.c_double,
                                            ctypes.c_int, ctypes.c_int64, P, P, P, P]
         lib.oracle_radius_fill.restype = None
+        lib.oracle_radius_count_f64.argtypes = lib.oracle_radius_count.argtypes
+        lib.oracle_radius_count_f64.restype = ctypes.c_int64
+        lib.oracle_radius_fill_f64.argtypes = lib.oracle_radius_fill.argtypes
+        lib.oracle_radius_fill_f64.restype = None
         _lib = lib
     return _lib
 
@@ -71,8 +75,10 @@ def exclusion_pair_to_ptr(exc_pair_index, num_nodes: int):
 def radius_graph(pos, r: float, batch=None, loop: bool = False, max_num_neighbors: int = 32,
                  n_frames: int | None = None, exclude_pair_xs=None, ptr_exclude_pair_xs=None):
     """Returns (edge_index [2, E] int64, overflow flag).  The optional
-    exclusion CSR is the one exclusion_pair_to_ptr returns."""
-    pos = np.ascontiguousarray(np.asarray(pos, dtype=np.float32))
+    exclusion CSR is the one exclusion_pair_to_ptr returns.  float64 positions
+    are searched in double arithmetic (d2 < r*r), anything else in float32."""
+    f64 = np.asarray(pos).dtype == np.float64
+    pos = np.ascontiguousarray(np.asarray(pos, dtype=np.float64 if f64 else np.float32))
     n = pos.shape[0]
     if batch is None:
         batch = np.zeros(n, dtype=np.int64)
@@ -90,11 +96,13 @@ def radius_graph(pos, r: float, batch=None, loop: bool = False, max_num_neighbor
     ep_p = None if eptr is None else eptr.ctypes.data
     deg = np.zeros(max(n, 1), dtype=np.int64)
     ovf = ctypes.c_int(0)
-    total = lib.oracle_radius_count(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
+    count = lib.oracle_radius_count_f64 if f64 else lib.oracle_radius_count
+    fill = lib.oracle_radius_fill_f64 if f64 else lib.oracle_radius_fill
+    total = count(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
                                     int(max_num_neighbors), ex_p, ep_p, deg.ctypes.data,
                                     ctypes.addressof(ovf))
     ei = np.zeros((2, max(total, 1)), dtype=np.int64)
-    lib.oracle_radius_fill(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
+    fill(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
                            int(max_num_neighbors), ex_p, ep_p, ei[0].ctypes.data,
                            ei[1].ctypes.data)
     return ei[:, :total].copy(), int(ovf.value)

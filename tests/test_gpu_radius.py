@@ -291,3 +291,89 @@ def test_atomic_data2neighbor_list_dict(method):
                        nl["index_mapping"])
     with pytest.raises(ValueError, match="not supported"):
         atomic_data2neighbor_list(data, 20.0, nls_distance_method="nvalchemi")
+
+
+@pytest.mark.parametrize("n,x_range,r,split,loop", list(product(X, X_RANGE, R, BATCH_SIZES, LOOP)))
+def test_radius_f64_sweep_bit_exact(n, x_range, r, split, loop):
+    """float64 positions (the reference's own test sweep runs its kernel in
+    float64, test_radius.py:66-104): the HIP double search equals the C
+    oracle's double search bit for bit."""
+    rng = np.random.default_rng(3000 + n)
+    lo, hi = x_range
+    pos = (hi - lo) * rng.random((n, 3)) + lo
+    batch = _batch(n, split)
+    ei_ref, _ = oracle_radius.radius_graph(pos, r, batch, loop, 1000)
+    g = _hip(pos, r, batch, loop, 1000)
+    assert np.array_equal(g.edge_index.cpu().numpy(), ei_ref)
+
+
+def test_radius_cuda_float64_boundary():
+    """radius_cuda on float64 positions decides membership in double: a pair
+    one double ulp inside the cutoff is kept, although float32 rounding would
+    put it on the cutoff; the distances come back in float64."""
+    from mlcg_amd.neighbor_list.radius import radius_cuda
+
+    x = float(np.nextafter(1.0, 0.0))
+    pos = torch.tensor([[0.0, 0, 0], [x, 0, 0], [0.0, 0, 0], [1.0, 0, 0]],
+                       dtype=torch.float64, device="cuda")
+    ptr = torch.tensor([0, 2, 4], device="cuda")
+    ei, d = radius_cuda(pos, ptr, 1.0, 8, True)
+    assert ei.cpu().tolist() == [[0, 1], [1, 0]] and d.dtype == torch.float64
+    ei32, _ = radius_cuda(pos.float(), ptr, 1.0, 8, True)
+    assert ei32.shape[1] == 0
+    with pytest.raises(RuntimeError, match="float32 or float64"):
+        radius_cuda(pos.half(), ptr, 1.0, 8, True)
+
+
+def test_registered_operators_and_torch_compile():
+    """torch.ops.mlcg.radius_cuda and exclusion_pair_to_ptr (the reference's
+    registered operator names, radius.cu:313-314, exclusion_pairs.cpp:64-65)
+    give the wrappers' results, also inside torch.compile(fullgraph=True) --
+    traced through the fake kernels -- as the reference's simulation compiles
+    its model (simulation/base.py:447-490)."""
+    import mlcg_amd  # noqa: F401
+    from mlcg_amd import ops
+    from mlcg_amd.neighbor_list.radius import radius_cuda
+
+    rng = np.random.default_rng(5)
+    pos = torch.from_numpy(rng.random((300, 3)) * 8.0).float().cuda()
+    ptr = torch.tensor([0, 100, 300], device="cuda")
+    ei, d = torch.ops.mlcg.radius_cuda(pos, ptr, 2.5, 64, True)
+    ei2, d2 = radius_cuda(pos, ptr, 2.5, 64, True)
+    assert torch.equal(ei, ei2) and torch.equal(d, d2)
+    exc = torch.tensor([[1, 2, 2, 5], [0, 0, 3, 4]], device="cuda")
+    xs, p = torch.ops.mlcg.exclusion_pair_to_ptr(exc, 6)
+    xs2, p2 = ops.exclusion_pair_to_ptr(exc, 6)
+    assert torch.equal(xs, xs2) and torch.equal(p, p2)
+
+    def per_frame_sum(x, ptr_x):
+        e, dist = torch.ops.mlcg.radius_cuda(x, ptr_x, 2.5, 64, True)
+        frame = torch.searchsorted(ptr_x, e[0], right=True) - 1
+        return torch.zeros(2, device=x.device, dtype=x.dtype).index_add(0, frame, dist)
+
+    torch._dynamo.reset()
+    compiled = torch.compile(per_frame_sum, backend="aot_eager", fullgraph=True)
+    assert torch.allclose(compiled(pos, ptr), per_frame_sum(pos, ptr), rtol=1e-6, atol=0)
+
+
+def test_compiled_schnet_matches_eager():
+    """torch.compile of the module (the reference's simulation path,
+    simulation/base.py:447-490; its differential test is eager against
+    compiled, tests/unit/simulation/test_compilation.py:229-270, rtol = atol =
+    1e-5): the fused HIP forward and forces run under the compiler (which
+    treats the kernel launches as opaque calls) and give the eager energies
+    and forces."""
+    from mlcg_amd import nn, synthetic
+
+    torch.manual_seed(3)
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, 20.0), num_rbf=50)
+    model = nn.GradientsOut(nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, 20.0), [64])).cuda()
+    model.eval()
+    data = synthetic.config2(n_frames=8).to_torch("cuda")
+    ref = model(data.clone())
+    E0, F0 = ref.out["SchNet"]["energy"].clone(), ref.out["SchNet"]["forces"].clone()
+    torch._dynamo.reset()
+    compiled = torch.compile(model, backend="aot_eager")
+    out = compiled(data.clone())
+    assert torch.allclose(out.out["SchNet"]["energy"], E0, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(out.out["SchNet"]["forces"], F0, rtol=1e-5, atol=1e-5)

@@ -295,3 +295,23 @@ def test_langevin_export_options_are_checked():
     sim = LangevinSimulation(n_timesteps=100, save_interval=10, log_interval=10,
                              log_type="print", device="cpu")
     assert sim.export_interval == 100 and sim.filename is None
+
+
+def test_reference_operators_registered_with_fake_kernels():
+    """Importing the package registers the reference's operator names
+    (radius.cu:313-314, exclusion_pairs.cpp:64-65) as torch.library custom
+    ops; their fake kernels give torch.compile the output shapes (an unbacked
+    edge count for the radius graph) without running anything."""
+    import mlcg_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.fx.experimental.symbolic_shapes import ShapeEnv
+
+    assert torch.ops.mlcg.radius_cuda is not None
+    assert torch.ops.mlcg.exclusion_pair_to_ptr is not None
+    with FakeTensorMode(shape_env=ShapeEnv()):
+        x = torch.empty(10, 3, dtype=torch.float64)
+        ei, d = torch.ops.mlcg.radius_cuda(x, None, 1.0, 8, True)
+        assert ei.dim() == 2 and ei.shape[0] == 2 and ei.dtype == torch.int64
+        assert d.dtype == torch.float64 and d.shape[0] == ei.shape[1]
+        xs, ptr = torch.ops.mlcg.exclusion_pair_to_ptr(torch.empty(2, 5, dtype=torch.int64), 7)
+        assert tuple(xs.shape) == (5,) and tuple(ptr.shape) == (8,)

@@ -250,3 +250,55 @@ def test_oracle_exclusions_empty_list():
                                        ptr_exclude_pair_xs=yp)
     full, _ = oracle_radius.radius_graph(pos, 1.5, None, False, 100)
     assert np.array_equal(ei, full)
+
+
+@pytest.mark.parametrize("n,x_range,r,split,loop",
+                         list(product(X, X_RANGE, R, BATCH_SIZES, LOOP)))
+def test_oracle_f64_vs_kdtree_sweep(n, x_range, r, split, loop):
+    """float64 positions: the double-arithmetic search against scipy's kd-tree
+    away from the boundary (the sweep of test_radius.py:66-104, which runs the
+    reference's kernel in float64)."""
+    rng = np.random.default_rng(2000 + n)
+    lo, hi = x_range
+    pos = (hi - lo) * rng.random((n, 3)) + lo
+    batch = _batch(n, split)
+    ei, ovf = oracle_radius.radius_graph(pos, r, batch, loop, 1000)
+    assert ovf == 0
+    got = set(map(tuple, ei.T.tolist()))
+    want, near = _kdtree_pairs(pos, r, batch, loop)
+    assert got - near == want - near
+
+
+def test_oracle_f64_boundary_is_decided_in_double():
+    """A pair whose float64 d2 lies one double ulp below r*r is inside in
+    double arithmetic although its float32 rounding sits on the cutoff: the
+    float64 search does not round positions to float32 first.  Also: a pair at
+    exactly d2 == r*r stays outside (strict <)."""
+    r = 1.0
+    x = float(np.nextafter(1.0, 0.0))  # x*x < 1 in double; float32(x) == 1.0
+    assert np.float32(x) == np.float32(1.0) and x * x < 1.0
+    pos = np.array([[0.0, 0, 0], [x, 0, 0], [0.0, 0, 0], [1.0, 0, 0]])
+    batch = np.array([0, 0, 1, 1])
+    ei, _ = oracle_radius.radius_graph(pos, r, batch, False, 8)
+    assert ei.tolist() == [[0, 1], [1, 0]]
+    ei32, _ = oracle_radius.radius_graph(pos.astype(np.float32), r, batch, False, 8)
+    assert ei32.shape[1] == 0
+
+
+def test_oracle_f64_numpy_restatement():
+    """The double search equals a plain numpy double restatement (d2 summed
+    as ((dx^2 + dy^2) + dz^2), strict < r*r) on random frames."""
+    rng = np.random.default_rng(17)
+    pos = rng.random((90, 3)) * 3.0
+    batch = np.repeat(np.arange(3), 30)
+    r = 0.9
+    ei, _ = oracle_radius.radius_graph(pos, r, batch, False, 1000)
+    want = []
+    for i in range(90):
+        for j in range(90):
+            if i == j or batch[i] != batch[j]:
+                continue
+            d = pos[j] - pos[i]
+            if (d[0] * d[0] + d[1] * d[1]) + d[2] * d[2] < r * r:
+                want.append((i, j))
+    assert list(map(tuple, ei.T.tolist())) == want
