@@ -113,8 +113,9 @@ int mlcg_exclusive_scan2_i32_noalloc(const int32_t* in_a, const int32_t* in_b,
 /* Pass 2: writes the canonical edge list (same membership and exclusion
  * arguments as pass 1).  edge_index is [2, edge_stride]
  * int64 (row 0 = centre i, row 1 = neighbour j).  Optional (nullable)
- * outputs for the CFConv pipeline: col[e] = j (int32), pair_ij [2,
- * pair_stride] (row 0 = i, row 1 = j, i < j) and eid2pair[e] for upper edges.
+ * outputs for the CFConv pipeline, all three or none: col[e] = j (int32),
+ * pair_ij [2, pair_stride] (row 0 = i, row 1 = j, i < j) and eid2pair[e] for
+ * upper edges (with pairptr).
  * Edges at index >= edge_capacity (pairs >= pair_capacity) are dropped and
  * *overflow is set to 2.  Replaces radius.cu:117-145 and compact_kernel
  * (radius.cu:60-86). */

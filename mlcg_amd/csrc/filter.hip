@@ -45,6 +45,49 @@ constexpr int kMaxK = 128;
 //   basis 1, ExpNormal (exp_normal.py:116-130):
 //            g_k = C exp(-widths[k] (exp(alpha (lo - d)) - centers[k])^2)
 //            with widths = betas, centers = means, lo = the basis' lower cutoff.
+// A cutoff envelope in branch-free form (the kernels evaluate it without a
+// data- or kind-dependent branch, so that it schedules freely among the MFMA
+// chains): u = (d - lo) s + o, C = 0.5 (cos(pi u) + 1) m, dC/dd = -sin(pi u) k m
+// with m = [d < hi] and, when gate, [d > lo]:
+//   cosine, lo = 0   s = 1 / hi,        o = 0, k = pi s / 2, gate off
+//   cosine, lo > 0   s = 2 / (hi - lo), o = 1, k = pi s / 2, gate on
+//   identity         s = o = k = 0, hi = +inf (C = 1, dC = 0)
+// The same operations, in the same order, as mlcg_cutoff of common.h.
+struct Cut {
+  float lo, hi, s, o, k;
+  int gate;
+};
+
+__host__ Cut make_cut(int kind, float lo, float hi) {
+  Cut c{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0};
+  const float pi = 3.14159265358979323846f;
+  if (kind == MLCG_CUT_IDENTITY) {
+    c.hi = __builtin_huge_valf();
+  } else if (lo > 0.0f) {
+    const float iw = 1.0f / (hi - lo);
+    c.lo = lo;
+    c.hi = hi;
+    c.s = 2.0f * iw;
+    c.o = 1.0f;
+    c.k = pi * iw;
+    c.gate = 1;
+  } else {
+    const float ih = 1.0f / hi;
+    c.hi = hi;
+    c.s = ih;
+    c.k = 0.5f * (pi * ih);
+  }
+  return c;
+}
+
+__device__ __forceinline__ void cut_eval(const Cut& c, float d, float& cv, float& dcv) {
+  float sn, cs;
+  mlcg_sincospi((d - c.lo) * c.s + c.o, sn, cs);
+  const float m = (d < c.hi && (!c.gate || d > c.lo)) ? 1.0f : 0.0f;
+  cv = 0.5f * (cs + 1.0f) * m;
+  dcv = -sn * c.k * m;
+}
+
 struct RbfParams {
   const float* centers;
   const float* widths;
@@ -57,7 +100,23 @@ struct RbfParams {
   float conv_lo, conv_hi;
   int act;
   int same_cut;  // the CFConv envelope is the RBF envelope: evaluated once
+  Cut rcut, ccut;  // the two envelopes in branch-free form
 };
+
+// Activation value and first derivative for a compile-time activation id.
+template <int ACT>
+__device__ __forceinline__ void act_t(float x, float& s, float& d1, float& d2) {
+  if constexpr (ACT == MLCG_ACT_TANH) {
+    s = mlcg_tanh(x);
+    d1 = 1.0f - s * s;
+    d2 = -2.0f * s * d1;
+  } else {
+    s = mlcg_softplus(x) - 0.69314718055994530942f;
+    const float sg = mlcg_sigmoid(x);
+    d1 = sg;
+    d2 = sg * (1.0f - sg);
+  }
+}
 
 // CFConv envelope of a pair whose RBF envelope (crbf, dcrbf) is known.
 __device__ __forceinline__ void conv_cutoff(const RbfParams& rp, float d, float crbf, float dcrbf,
@@ -103,6 +162,25 @@ __device__ __forceinline__ void rbf_eval(const RbfParams& rp, bool on, float cen
     const float e = __expf(-wid * (u * u));
     g = e * crbf;
     gd = e * (dcrbf + 2.0f * rp.alpha * wid * u * ex * crbf);
+  }
+}
+
+// rbf_eval for a compile-time basis kind (no branch on rp.basis).
+template <int BASIS>
+__device__ __forceinline__ void rbf_eval_t(const RbfParams& rp, bool on, float cen, float wid,
+                                           float d, float crbf, float dcrbf, float& g,
+                                           float& gd) {
+  if constexpr (BASIS == 0) {
+    const float diff = d - cen;
+    const float e = __expf(wid * (diff * diff));
+    g = on ? e * crbf : 0.0f;
+    gd = on ? e * (2.0f * wid * diff * crbf + dcrbf) : 0.0f;
+  } else {
+    const float ex = __expf(rp.alpha * (rp.rbf_lo - d));
+    const float u = ex - cen;
+    const float e = __expf(-wid * (u * u));
+    g = on ? e * crbf : 0.0f;
+    gd = on ? e * (dcrbf + 2.0f * rp.alpha * wid * u * ex * crbf) : 0.0f;
   }
 }
 
@@ -501,6 +579,7 @@ __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, hal
 // Filter forward, fp32-accurate, on the fp16 MFMA.  The operand layouts are
 // those of filter_fwd_f16_kernel (see stage_f16); W1 and W2 are staged as
 // three planes each.  One wave per 16-pair tile, 8 waves per workgroup.
+template <int BASIS, int ACT>
 __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
@@ -584,8 +663,8 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
       nj = pj[p2];
     }
     float crbf, dcrbf, cc, dcc;
-    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
+    cut_eval(rp.rcut, d, crbf, dcrbf);
+    cut_eval(rp.ccut, d, cc, dcc);
 
     // 1. a = W1 g, a' = W1 g' (times S1)
     floatx4 a[kFT], ad[kFT];
@@ -600,7 +679,7 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
       for (int j = 0; j < 8; ++j) {
         float g, gd;
         const int k = 32 * s + 8 * q + j;
-        rbf_eval(rp, k < K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
+        rbf_eval_t<BASIS>(rp, k < K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
         const f16split sg = split2(g, S1), sgd = split2(gd, S1);
         gh[j] = sg.hi;
         gl[j] = sg.lo;
@@ -622,7 +701,7 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float sv, d1, d2;
-        mlcg_act(rp.act, a[t][i] * inv1 + b1s[16 * t + 4 * q + i], sv, d1, d2);
+        act_t<ACT>(a[t][i] * inv1 + b1s[16 * t + 4 * q + i], sv, d1, d2);
         const int e = 4 * (t & 1) + i;
         const float hd = d1 * (ad[t][i] * inv1);
         const f16split sh = split2(sv, S2), shd = split2(hd, S2);
@@ -1502,7 +1581,13 @@ void allow_lds_once() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel),
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<0, 0>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<0, 1>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<1, 0>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<1, 1>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -1531,6 +1616,8 @@ RbfParams make_params(int basis, const float* centers, const float* widths, floa
   rp.conv_hi = chi;
   rp.act = act;
   rp.same_cut = rk == ck && rlo == clo && rhi == chi;
+  rp.rcut = make_cut(rk, rlo, rhi);
+  rp.ccut = make_cut(ck, clo, chi);
   return rp;
 }
 
@@ -1566,9 +1653,15 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
     const size_t lds = fwd_x3_lds_bytes(num_rbf);
     allow_lds_once();
     const unsigned gx = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWavesX3), 1);
-    hipLaunchKernelGGL(filter_fwd_x3_kernel, dim3(gx), dim3(kThreadsX3), lds, s, pos, pair_ij,
-                       pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
-                       static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out);
+#define MLCG_X3_LAUNCH(B, A)                                                               \
+  hipLaunchKernelGGL((filter_fwd_x3_kernel<B, A>), dim3(gx), dim3(kThreadsX3), lds, s, pos,  \
+                     pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2, \
+                     static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out)
+    if (basis == 0 && act == 0) MLCG_X3_LAUNCH(0, 0);
+    else if (basis == 0) MLCG_X3_LAUNCH(0, 1);
+    else if (act == 0) MLCG_X3_LAUNCH(1, 0);
+    else MLCG_X3_LAUNCH(1, 1);
+#undef MLCG_X3_LAUNCH
   } else if (f16 != MLCG_FILTER_FP16) {
     const int KS = (num_rbf + 3) / 4;
     const size_t lds =

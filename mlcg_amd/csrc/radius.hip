@@ -10,8 +10,8 @@
 //
 // Design: two passes (count, then fill at scanned offsets) give an exact,
 // deterministic layout without atomics, cooperative launches or host
-// synchronisation inside the library.  The count runs one thread per row
-// over its frame; the fill one wave per row: the wave sweeps the row's frame
+// synchronisation inside the library.  The count runs one or more threads per
+// row over its frame; the fill one wave per row: the wave sweeps the row's frame
 // 64 candidates at a time, each lane testing one candidate, a ballot gives the
 // hit mask and mbcnt the rank of each hit, so every row's edges are written as
 // contiguous, coalesced runs.  Both stage the positions of a workgroup's
@@ -101,77 +101,65 @@ __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
     for (int64_t k = b + 1; k <= n_frames; ++k) ptr[k] = n;
 }
 
-// Shared sweep over row i: writes (fill pass) every kept neighbour from the
-// lane that holds it, returns (kept, upper kept) through the references and
-// whether the row overflowed max_nn.  With exclusions, `asym` is set when a
-// kept edge (i, j) has its reverse (j, i) excluded.
-// Positions come from `pos` (global memory, node n at pos[3 n]) or, with
-// kStaged, from a workgroup's LDS copy of nodes [base, ...) (node n at
-// pos[3 (n - base)]).
-template <bool kFill, bool kExcl, bool kStaged, typename T>
-__device__ __forceinline__ bool sweep_row(
-    const T* __restrict__ pos, int64_t base, int64_t i, int64_t start, int64_t end,
-    T r2, int loop, int64_t max_nn, const int64_t* __restrict__ exs,
-    const int64_t* __restrict__ eptr, int& kept, int& ukept,
+// Fill sweep over row i: writes every kept neighbour from the lane that holds
+// it (ranks by mbcnt over the hit ballot), with kPairs also the pair list and
+// its edge map for the upper neighbours.  Node and edge indices are int32
+// (the CSR is int32; the host entry points reject larger inputs).  Returns
+// nothing; `dropped` is set when an edge or pair falls past its capacity.
+template <bool kExcl, bool kStaged, bool kPairs, typename T>
+__device__ __forceinline__ void fill_row(
+    const T* __restrict__ pos, int base, int i, int start, int end, T r2, int loop,
+    int max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
     int64_t* __restrict__ ei0, int64_t* __restrict__ ei1, int32_t* __restrict__ col,
-    int64_t e_base, int64_t e_cap, int32_t* __restrict__ pi, int32_t* __restrict__ pj,
-    int32_t* __restrict__ eid2pair, int64_t p_base, int64_t p_cap, bool& dropped,
-    bool& asym) {
+    int e_base, int e_cap, int32_t* __restrict__ pi, int32_t* __restrict__ pj,
+    int32_t* __restrict__ eid2pair, int p_base, int p_cap, bool& dropped) {
   const int lane = mlcg_lane();
   const Vec3T<T> a = load_pos(pos, kStaged ? i - base : i);
-  int64_t total = 0;
-  kept = 0;
-  ukept = 0;
+  int kept = 0, ukept = 0;
   int64_t x_lo = 0, x_hi = 0;
   if (kExcl) {
     x_lo = eptr[i];
     x_hi = eptr[i + 1];
   }
-  for (int64_t j0 = start; j0 < end; j0 += MLCG_WAVE) {
-    const int64_t j = j0 + lane;
+  for (int j0 = start; j0 < end && kept < max_nn; j0 += MLCG_WAVE) {
+    const int j = j0 + lane;
     bool hit = false;
     if (j < end) {
       const T d2 = sqdist_exact(a, load_pos(pos, kStaged ? j - base : j));
       hit = (d2 < r2) && (loop || j != i);
-      if (kExcl && hit) {
-        hit = !in_sorted(exs, x_lo, x_hi, j);
-        if (!kFill && hit && in_sorted(exs, eptr[j], eptr[j + 1], i)) asym = true;
-      }
+      if (kExcl && hit) hit = !in_sorted(exs, x_lo, x_hi, (int64_t)j);
     }
     const uint64_t m = __ballot(hit);
     if (m == 0) continue;
     const int rank = lanes_below(m);
     const bool keep = hit && (kept + rank < max_nn);
-    const uint64_t km = __ballot(keep);
-    const bool upper = keep && (j > i);
-    const uint64_t um = __ballot(upper);
-    if (kFill) {
-      if (keep) {
-        int64_t e = e_base + kept + rank;
-        if (e < e_cap) {
-          ei0[e] = i;
-          ei1[e] = j;
-          if (col) col[e] = (int32_t)j;
-          if (upper && pi) {
-            int64_t p = p_base + ukept + lanes_below(um);
-            if (p < p_cap) {
-              pi[p] = (int32_t)i;
-              pj[p] = (int32_t)j;
-              if (eid2pair) eid2pair[e] = (int32_t)p;
-            } else {
-              dropped = true;
-            }
-          }
+    const int e = e_base + kept + rank;
+    if (keep) {
+      if (e < e_cap) {
+        ei0[e] = i;
+        ei1[e] = j;
+        if (kPairs) col[e] = j;
+      } else {
+        dropped = true;
+      }
+    }
+    if (kPairs) {
+      const bool upper = keep && (j > i);
+      const uint64_t um = __ballot(upper);
+      if (upper && e < e_cap) {
+        const int p = p_base + ukept + lanes_below(um);
+        if (p < p_cap) {
+          pi[p] = i;
+          pj[p] = j;
+          eid2pair[e] = p;
         } else {
           dropped = true;
         }
       }
+      ukept += __popcll(um);
     }
-    total += __popcll(m);
-    kept += __popcll(km);
-    ukept += __popcll(um);
+    kept += __popcll(m);
   }
-  return total > max_nn;
 }
 
 // Work split of the count and fill kernels: a workgroup of kRowWaves waves
@@ -235,25 +223,28 @@ __device__ __forceinline__ RowBounds row_bounds(const BlockNodes& bn,
   return rb;
 }
 
-// Pass 1 runs one thread per row (a counting sweep needs no ballots or ranks,
-// and per candidate a thread spends a handful of instructions where a wave
-// per row spends a few dozen on masks): kCountRows rows per workgroup, the
-// positions of their frames staged in LDS as in the fill pass.  Candidates
-// are visited in ascending j, so with a binding max_num_neighbors the kept
-// neighbours are the lowest-index ones: kept = min(hits, max_nn) and the
-// kept upper neighbours (j > i) are what remains after the lower ones and the
-// self loop.
+// Pass 1 runs `parts` threads per row (a power of two up to 64, chosen by the
+// host so that the launch fills the chip): a counting sweep needs no ballots
+// or ranks, and per candidate a thread spends a handful of instructions where
+// a wave per row spends a few dozen on masks.  Thread p of a row visits the
+// candidates start + p, start + p + parts, ...; the per-row counts are then
+// summed over the row's threads (adjacent lanes) with xor shuffles.  The
+// positions of the workgroup's frames are staged in LDS as in the fill pass.
+// With a binding max_num_neighbors the kept neighbours are the lowest-index
+// ones: kept = min(hits, max_nn) and the kept upper neighbours (j > i) are
+// what remains after the lower ones and the self loop.
 constexpr int kCountThreads = 256;
 
 template <bool kExcl, typename T>
 __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
     const T* __restrict__ pos, const int64_t* __restrict__ batch,
-    const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop,
-    int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
+    const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop, int64_t max_nn,
+    const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr, int parts,
     int32_t* __restrict__ deg, int32_t* __restrict__ udeg, int32_t* __restrict__ overflow) {
   __shared__ T sp[3 * kStage];
-  const int64_t r0 = (int64_t)blockIdx.x * kCountThreads;
-  const int64_t r1 = r0 + kCountThreads < n ? r0 + kCountThreads : n;
+  const int rows_per_block = kCountThreads / parts;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
   const int64_t c_lo = frame_ptr[batch[r0]];
   const int64_t c_hi = frame_ptr[batch[r1 - 1] + 1];
   const bool staged = c_hi >= c_lo && c_hi - c_lo <= kStage;  // uniform
@@ -262,31 +253,44 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
       sp[t] = pos[3 * c_lo + t];
     __syncthreads();
   }
-  const int64_t i = r0 + threadIdx.x;
-  if (i >= r1) return;
-  const int64_t b = batch[i];
-  const int64_t start = frame_ptr[b], end = frame_ptr[b + 1];
-  const bool local = staged && start >= c_lo && end <= c_hi;
-  const Vec3T<T> a = local ? load_pos(sp, i - c_lo) : load_pos(pos, i);
-  int64_t x_lo = 0, x_hi = 0;
-  if (kExcl) {
-    x_lo = eptr[i];
-    x_hi = eptr[i + 1];
-  }
+  const int64_t i = r0 + threadIdx.x / parts;
+  const int part = threadIdx.x % parts;
+  const bool active = i < r1;
   int lower = 0, self = 0, upper = 0;
   bool asym = false;
-  for (int64_t j = start; j < end; ++j) {
-    const T d2 = sqdist_exact(a, local ? load_pos(sp, j - c_lo) : load_pos(pos, j));
-    bool hit = (d2 < r2) && (loop || j != i);
-    if (kExcl && hit) {
-      hit = !in_sorted(exs, x_lo, x_hi, j);
-      if (hit && in_sorted(exs, eptr[j], eptr[j + 1], i)) asym = true;
+  if (active) {
+    const int64_t b = batch[i];
+    const int64_t start = frame_ptr[b], end = frame_ptr[b + 1];
+    const bool local = staged && start >= c_lo && end <= c_hi;
+    const Vec3T<T> a = local ? load_pos(sp, i - c_lo) : load_pos(pos, i);
+    int64_t x_lo = 0, x_hi = 0;
+    if (kExcl) {
+      x_lo = eptr[i];
+      x_hi = eptr[i + 1];
     }
-    if (hit) {
-      lower += j < i;
-      self += j == i;
-      upper += j > i;
+    for (int64_t j = start + part; j < end; j += parts) {
+      const T d2 = sqdist_exact(a, local ? load_pos(sp, j - c_lo) : load_pos(pos, j));
+      bool hit = (d2 < r2) && (loop || j != i);
+      if (kExcl && hit) {
+        hit = !in_sorted(exs, x_lo, x_hi, j);
+        if (hit && in_sorted(exs, eptr[j], eptr[j + 1], i)) asym = true;
+      }
+      if (hit) {
+        lower += j < i;
+        self += j == i;
+        upper += j > i;
+      }
     }
+  }
+  // sum over the row's `parts` adjacent lanes (every lane takes part)
+  for (int o = 1; o < parts; o <<= 1) {
+    lower += __shfl_xor(lower, o, MLCG_WAVE);
+    self += __shfl_xor(self, o, MLCG_WAVE);
+    upper += __shfl_xor(upper, o, MLCG_WAVE);
+  }
+  if (!active || part != 0) {
+    if (kExcl && asym && overflow) atomicOr(overflow, 4);
+    return;
   }
   const int64_t total = (int64_t)lower + self + upper;
   const int64_t kept = total < max_nn ? total : max_nn;
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
   if (kExcl && asym && overflow) atomicOr(overflow, 4);
 }
 
-template <bool kExcl, typename T>
+template <bool kExcl, bool kPairs, typename T>
 __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
     const T* __restrict__ pos, const int64_t* __restrict__ batch,
     const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop,
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
   const RowBounds rb = row_bounds(bn, batch, frame_ptr, rowptr, pairptr);
   int32_t* pi = pair_ij;
   int32_t* pj = pair_ij ? pair_ij + p_stride : nullptr;
-  bool dropped = false, asym = false;
+  bool dropped = false;
   for (int k = 0; k < kRowsPerWave; ++k) {
     const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) + kRowWaves * k;
     if (i >= bn.r1) break;
@@ -320,15 +324,18 @@ __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
     const int64_t end = __builtin_amdgcn_readlane(rb.end, k);
     const int64_t e_base = __builtin_amdgcn_readlane(rb.e_base, k);
     const int64_t p_base = __builtin_amdgcn_readlane(rb.p_base, k);
-    int kept, ukept;
+    const int mnn = max_nn < (int64_t)INT32_MAX ? (int)max_nn : INT32_MAX;
+    const int ecap = e_cap < (int64_t)INT32_MAX ? (int)e_cap : INT32_MAX;
+    const int pcap = p_cap < (int64_t)INT32_MAX ? (int)p_cap : INT32_MAX;
     if (bn.staged && start >= bn.c_lo && end <= bn.c_hi)  // wave-uniform
-      sweep_row<true, kExcl, true>(sp, bn.c_lo, i, start, end, r2, loop, max_nn, exs, eptr,
-                                   kept, ukept, edge_index, edge_index + e_stride, col, e_base,
-                                   e_cap, pi, pj, eid2pair, p_base, p_cap, dropped, asym);
+      fill_row<kExcl, true, kPairs>(sp, (int)bn.c_lo, (int)i, (int)start, (int)end, r2, loop,
+                                    mnn, exs, eptr, edge_index, edge_index + e_stride, col,
+                                    (int)e_base, ecap, pi, pj, eid2pair, (int)p_base, pcap,
+                                    dropped);
     else
-      sweep_row<true, kExcl, false>(pos, 0, i, start, end, r2, loop, max_nn, exs, eptr, kept, ukept,
-                             edge_index, edge_index + e_stride, col, e_base, e_cap, pi, pj,
-                             eid2pair, p_base, p_cap, dropped, asym);
+      fill_row<kExcl, false, kPairs>(pos, 0, (int)i, (int)start, (int)end, r2, loop, mnn, exs,
+                                     eptr, edge_index, edge_index + e_stride, col, (int)e_base,
+                                     ecap, pi, pj, eid2pair, (int)p_base, pcap, dropped);
   }
   if (dropped && overflow) atomicOr(overflow, 2);
 }
@@ -503,16 +510,19 @@ int launch_radius_count(const T* pos, const int64_t* batch, const int64_t* frame
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && batch && frame_ptr && deg && upper_deg);
   const T r2 = (T)(r * r);  // r*r in double, then the scalar type (radius.cu:250)
-  dim3 grid(mlcg_div_up(n_nodes, kCountThreads)), block(kCountThreads);
+  // threads per row: enough threads for about four waves per SIMD
+  int parts = 1;
+  while (parts < MLCG_WAVE && n_nodes * parts < (int64_t(1) << 18)) parts *= 2;
+  dim3 grid(mlcg_div_up(n_nodes, kCountThreads / parts)), block(kCountThreads);
   hipStream_t s = mlcg_stream(stream);
   if (exclude_pair_xs)
     hipLaunchKernelGGL((radius_count_kernel<true, T>), grid, block, 0, s, pos, batch,
                        frame_ptr, n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
-                       ptr_exclude_pair_xs, deg, upper_deg, overflow);
+                       ptr_exclude_pair_xs, parts, deg, upper_deg, overflow);
   else
     hipLaunchKernelGGL((radius_count_kernel<false, T>), grid, block, 0, s, pos, batch,
-                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, deg,
-                       upper_deg, overflow);
+                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr, parts,
+                       deg, upper_deg, overflow);
   return mlcg_launch_status();
 }
 
@@ -535,17 +545,21 @@ int launch_radius_fill(const T* pos, const int64_t* batch, const int64_t* frame_
   const T r2 = (T)(r * r);
   dim3 grid(mlcg_div_up(n_nodes, kBlockRows)), block(kRowWaves * MLCG_WAVE);
   hipStream_t s = mlcg_stream(stream);
-  if (exclude_pair_xs)
-    hipLaunchKernelGGL((radius_fill_kernel<true, T>), grid, block, 0, s, pos, batch,
-                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, exclude_pair_xs,
-                       ptr_exclude_pair_xs, rowptr, pairptr, edge_capacity, edge_stride,
-                       edge_index, col, pair_capacity, pair_stride, pair_ij, eid2pair,
-                       overflow);
-  else
-    hipLaunchKernelGGL((radius_fill_kernel<false, T>), grid, block, 0, s, pos, batch,
-                       frame_ptr, n_nodes, r2, loop, max_num_neighbors, nullptr, nullptr,
-                       rowptr, pairptr, edge_capacity, edge_stride, edge_index, col,
-                       pair_capacity, pair_stride, pair_ij, eid2pair, overflow);
+  // the pair structures come together (col, pair list and its edge map)
+  MLCG_REQUIRE((col == nullptr && pair_ij == nullptr && eid2pair == nullptr) ||
+               (col != nullptr && pair_ij != nullptr && eid2pair != nullptr));
+  const bool pairs = pair_ij != nullptr;
+#define MLCG_FILL_LAUNCH(EX, PR)                                                          \
+  hipLaunchKernelGGL((radius_fill_kernel<EX, PR, T>), grid, block, 0, s, pos, batch,      \
+                     frame_ptr, n_nodes, r2, loop, max_num_neighbors,                     \
+                     EX ? exclude_pair_xs : nullptr, EX ? ptr_exclude_pair_xs : nullptr,  \
+                     rowptr, pairptr, edge_capacity, edge_stride, edge_index, col,        \
+                     pair_capacity, pair_stride, pair_ij, eid2pair, overflow)
+  if (exclude_pair_xs && pairs) MLCG_FILL_LAUNCH(true, true);
+  else if (exclude_pair_xs) MLCG_FILL_LAUNCH(true, false);
+  else if (pairs) MLCG_FILL_LAUNCH(false, true);
+  else MLCG_FILL_LAUNCH(false, false);
+#undef MLCG_FILL_LAUNCH
   return mlcg_launch_status();
 }
 

@@ -12,7 +12,7 @@ import torch
 
 from oracle import radius as oracle_radius
 from oracle import schnet_ref as R
-from tests.helpers import check, make_cfg, make_model, rel_err
+from tests.helpers import check, check_calibrated, make_cfg, make_model, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -138,16 +138,18 @@ def test_expnormal_energy_forces(trainable):
     pos64, types, batch, ei = _oracle_inputs(b, 12.0)
     E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
                                           batch, ei, b.n_frames)
+    E32, F32 = R.schnet_energy_forces(sd, cfg, pos64.float(), types, batch, ei, b.n_frames)
     model = make_model(cfg, sd, trainable_basis=trainable)
     assert model.fused_spec() is not None
     gm = nn.GradientsOut(model).eval()
     data = gm(b.to_torch("cuda"))
     E = data.out["SchNet"]["energy"]
     F = data.out["SchNet"]["forces"]
-    print("expnormal trainable", trainable, "E rel", rel_err(E, E_ref), "F rel",
-          rel_err(F, F_ref))
-    check(E, E_ref, 1e-5, 'E')
-    check(F, F_ref, 1e-5, 'F')
+    # the exp-normal basis exp(-beta (exp(alpha (lo - d)) - mu)^2), beta = 625,
+    # amplifies fp32 rounding of d: the reference's fp32 arithmetic misses the
+    # bar here itself (ratio ~1.2), hence the calibrated bound
+    check_calibrated(E, E_ref, E32, 1e-5, 'E')
+    check_calibrated(F, F_ref, F32, 1e-5, 'F')
 
 
 @pytest.mark.parametrize("basis,act", [("gaussian", "tanh"), ("expnormal", "tanh"),
