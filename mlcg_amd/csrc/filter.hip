@@ -184,6 +184,37 @@ __device__ __forceinline__ void rbf_eval_t(const RbfParams& rp, bool on, float c
   }
 }
 
+// Basis, activation and envelopes for a compile-time kind, or (kind -1)
+// dispatched at run time on rp.
+template <int BASIS>
+__device__ __forceinline__ void rbf_any(const RbfParams& rp, bool on, float cen, float wid,
+                                        float d, float crbf, float dcrbf, float& g, float& gd) {
+  if constexpr (BASIS < 0) {
+    rbf_eval(rp, on, cen, wid, d, crbf, dcrbf, g, gd);
+  } else {
+    rbf_eval_t<BASIS>(rp, on, cen, wid, d, crbf, dcrbf, g, gd);
+  }
+}
+template <int ACT>
+__device__ __forceinline__ void act_any(int act, float x, float& s, float& d1, float& d2) {
+  if constexpr (ACT < 0) {
+    mlcg_act(act, x, s, d1, d2);
+  } else {
+    act_t<ACT>(x, s, d1, d2);
+  }
+}
+// Both envelopes of a pair from their branch-free forms.
+__device__ __forceinline__ void envelopes(const RbfParams& rp, float d, float& crbf,
+                                          float& dcrbf, float& cc, float& dcc) {
+  cut_eval(rp.rcut, d, crbf, dcrbf);
+  if (rp.same_cut) {  // uniform
+    cc = crbf;
+    dcc = dcrbf;
+  } else {
+    cut_eval(rp.ccut, d, cc, dcc);
+  }
+}
+
 // Centre and width of basis function k read from global memory (zero past K).
 __device__ __forceinline__ void basis_params(const RbfParams& rp, int k, float& cen,
                                              float& wid) {
@@ -534,7 +565,12 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
 // filter value rather than a silently wrong one.  On this part the fp16 MFMA
 // issues at about 14 times the fp32 rate, so the three products cost about a
 // fifth of the fp32 ones.
-constexpr int kWavesX3 = 8;
+// waves per workgroup of the split-product forward (a build-time tuning
+// constant: the workgroup shares one copy of the staged weights)
+#ifndef MLCG_X3_WAVES
+#define MLCG_X3_WAVES 12
+#endif
+constexpr int kWavesX3 = MLCG_X3_WAVES;
 constexpr int kThreadsX3 = kWavesX3 * MLCG_WAVE;
 
 // Largest |v| over the workgroup (every thread must call; two barriers).
@@ -558,15 +594,6 @@ __device__ __forceinline__ float x3_scale(float maxabs) {
   return ldexpf(1.0f, e);
 }
 
-__device__ __forceinline__ void x3_store(_Float16* plane, int plane_stride, int idx, float v,
-                                         float S) {
-  const f16split sp = split2(v, S);
-  plane[idx] = sp.hi;
-  plane[plane_stride + idx] = (_Float16)((float)sp.hi * S);
-  plane[2 * plane_stride + idx] = sp.lo;
-}
-
-
 // acc += S A B over one 32-wide k block from A's planes and B's parts.
 __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, halfx8 bh,
                                            halfx8 bl, floatx4 acc) {
@@ -577,8 +604,18 @@ __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, hal
 }
 
 // Filter forward, fp32-accurate, on the fp16 MFMA.  The operand layouts are
-// those of filter_fwd_f16_kernel (see stage_f16); W1 and W2 are staged as
-// three planes each.  One wave per 16-pair tile, 8 waves per workgroup.
+// those of filter_fwd_f16_kernel (see stage_f16) with K padded to two 32-wide
+// k blocks (K <= 64); W1 and W2 are staged as three planes each.  One wave per
+// 16-pair tile, 12 waves per workgroup.  Per tile the wave evaluates the basis
+// of its 16 pairs once, then walks the 8 feature tiles: a, a' of tile t
+// (6 MFMAs per k block), their activation, and the split h, h' parts, which
+// accumulate into the B operands of the second product; then the 8 output
+// tiles of W, W' (6 MFMAs per 32-wide feature block).  Taking one feature
+// tile at a time keeps only 8 accumulators live next to the operand parts.
+// Basis rows k >= K are evaluated with centre and width 0 (finite values)
+// and meet zero weights, so they add exact zeros.
+constexpr int kX3Blocks = 2;  // 32-wide k blocks of the first product
+
 template <int BASIS, int ACT>
 __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
@@ -588,35 +625,97 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     float* __restrict__ Wdout, float* __restrict__ dist_out) {
   extern __shared__ float lds[];
   const int K = rp.K;
-  const int KS32 = (K + 31) / 32;
-  const int n1 = kFT * KS32 * MLCG_WAVE * 8;       // halfs per W1 plane
-  const int n2 = kFT * (kFT / 2) * MLCG_WAVE * 8;  // halfs per W2 plane
+  constexpr int KS32 = kX3Blocks;
+  constexpr int n1 = kFT * KS32 * MLCG_WAVE * 8;       // halfs per W1 plane
+  constexpr int n2 = kFT * (kFT / 2) * MLCG_WAVE * 8;  // halfs per W2 plane
   _Float16* w1p = reinterpret_cast<_Float16*>(lds);
   _Float16* w2p = w1p + 3 * n1;
   float* b1s = reinterpret_cast<float*>(w2p + 3 * n2);
   float* bc = b1s + kF;
   float* bw = bc + kMaxK;
   float* red = bw + kMaxK;
-  // per-matrix scales from the largest weights
+  // The weights are read once, into registers, in chunks of 8 plane
+  // elements (one halfx8 of one lane's A fragment; chunk c of a plane is
+  // held by thread c mod blockDim), which also gives the per-matrix scales
+  // from the largest weights; the three planes are then written as halfx8.
+  //   W1 chunk c = (t, s, l): W1[16 t + (l & 15)][32 s + 8 (l >> 4) + 0..7]
+  //      (zero for k >= K; K <= 64, rows 8-byte aligned: float2 loads)
+  //   W2 chunk c = (t, s, l): W2[16 t + (l & 15)][32 s + 4 (l >> 4) + 0..3]
+  //      and the same + 16 (two float4 loads)
+  constexpr int nc1 = n1 / 8, nc2 = n2 / 8;
+  constexpr int kPer1 = (nc1 + kThreadsX3 - 1) / kThreadsX3;
+  constexpr int kPer2 = (nc2 + kThreadsX3 - 1) / kThreadsX3;
+  float v1[kPer1][8], v2[kPer2][8];
   float m1 = 0.f, m2 = 0.f;
-  for (int x = threadIdx.x; x < kF * K; x += blockDim.x) m1 = fmaxf(m1, fabsf(W1[x]));
-  for (int x = threadIdx.x; x < kF * kF; x += blockDim.x) m2 = fmaxf(m2, fabsf(W2[x]));
+#pragma unroll
+  for (int r = 0; r < kPer1; ++r) {
+    const int c = threadIdx.x + r * kThreadsX3;
+    const int l = c & 63, ts = c >> 6;
+    const int s = ts % KS32, t = ts / KS32;
+    const int k0 = 32 * s + 8 * (l >> 4);
+    const float* row = W1 + (16 * t + (l & 15)) * K;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      float2 w = float2{0.f, 0.f};
+      if (c < nc1) {
+        if (k0 + j + 1 < K && (K & 1) == 0) {
+          w = *reinterpret_cast<const float2*>(row + k0 + j);
+        } else {
+          w.x = k0 + j < K ? row[k0 + j] : 0.0f;
+          w.y = k0 + j + 1 < K ? row[k0 + j + 1] : 0.0f;
+        }
+      }
+      v1[r][j] = w.x;
+      v1[r][j + 1] = w.y;
+      m1 = fmaxf(m1, fmaxf(fabsf(w.x), fabsf(w.y)));
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kPer2; ++r) {
+    const int c = threadIdx.x + r * kThreadsX3;
+    const int l = c & 63, ts = c >> 6;
+    const int s = ts % (kFT / 2), t = ts / (kFT / 2);
+    const float* src = W2 + (16 * t + (l & 15)) * kF + 32 * s + 4 * (l >> 4);
+    float4 lo4 = float4{0.f, 0.f, 0.f, 0.f}, hi4 = lo4;
+    if (c < nc2) {
+      lo4 = *reinterpret_cast<const float4*>(src);
+      hi4 = *reinterpret_cast<const float4*>(src + 16);
+    }
+    const float w8[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v2[r][j] = w8[j];
+      m2 = fmaxf(m2, fabsf(w8[j]));
+    }
+  }
   const float S1 = x3_scale(block_absmax(m1, red));
   const float S2 = x3_scale(block_absmax(m2, red));
-  for (int x = threadIdx.x; x < n1; x += blockDim.x) {
-    const int j = x & 7, l = (x >> 3) & 63, ts = x >> 9;
-    const int s = ts % KS32, t = ts / KS32;
-    const int k = 32 * s + 8 * (l >> 4) + j;
-    x3_store(w1p, n1, x, k < K ? W1[(16 * t + (l & 15)) * K + k] : 0.0f, S1);
+  auto store_chunk = [](_Float16* plane, int plane_halfs, int c, const float* v, float S) {
+    halfx8 h, hs, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f16split sp = split2(v[j], S);
+      h[j] = sp.hi;
+      hs[j] = (_Float16)((float)sp.hi * S);
+      lo[j] = sp.lo;
+    }
+    halfx8* p = reinterpret_cast<halfx8*>(plane) + c;
+    p[0] = h;
+    p[plane_halfs / 8] = hs;
+    p[2 * (plane_halfs / 8)] = lo;
+  };
+#pragma unroll
+  for (int r = 0; r < kPer1; ++r) {
+    const int c = threadIdx.x + r * kThreadsX3;
+    if (c < nc1) store_chunk(w1p, n1, c, v1[r], S1);
   }
-  for (int x = threadIdx.x; x < n2; x += blockDim.x) {
-    const int j = x & 7, l = (x >> 3) & 63, ts = x >> 9;
-    const int s = ts % (kFT / 2), t = ts / (kFT / 2);
-    const int c = 16 * (2 * s + (j >> 2)) + 4 * (l >> 4) + (j & 3);
-    x3_store(w2p, n2, x, W2[(16 * t + (l & 15)) * kF + c], S2);
+#pragma unroll
+  for (int r = 0; r < kPer2; ++r) {
+    const int c = threadIdx.x + r * kThreadsX3;
+    if (c < nc2) store_chunk(w2p, n2, c, v2[r], S2);
   }
   for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
-  stage_basis(bc, bw, rp);
+  stage_basis(bc, bw, rp);  // zeros past K
   __syncthreads();
 
   int64_t np = *n_pairs_dev;
@@ -628,7 +727,7 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
 
   const halfx8* w1v = reinterpret_cast<const halfx8*>(w1p);
   const halfx8* w2v = reinterpret_cast<const halfx8*>(w2p);
-  const int n1v = n1 / 8, n2v = n2 / 8;
+  constexpr int n1v = n1 / 8, n2v = n2 / 8;
   const int64_t wave = (int64_t)blockIdx.x * kWavesX3 + threadIdx.x / MLCG_WAVE;
   const int64_t nwaves = (int64_t)gridDim.x * kWavesX3;
   // the pair indices are requested two tiles ahead and the bead positions one
@@ -664,93 +763,105 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     }
     float crbf, dcrbf, cc, dcc;
     cut_eval(rp.rcut, d, crbf, dcrbf);
-    cut_eval(rp.ccut, d, cc, dcc);
+    if (rp.same_cut) {  // uniform
+      cc = crbf;
+      dcc = dcrbf;
+    } else {
+      cut_eval(rp.ccut, d, cc, dcc);
+    }
 
-    // 1. a = W1 g, a' = W1 g' (times S1)
-    floatx4 a[kFT], ad[kFT];
+    // basis g, g' of the lane's pair, k = 32 s + 8 q + j, as split B parts
+    halfx8 gh[KS32], gl[KS32], gdh[KS32], gdl[KS32];
 #pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      a[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      ad[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int s = 0; s < KS32; ++s) {
-      halfx8 gh, gl, gdh, gdl;
+    for (int s = 0; s < KS32; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float g, gd;
+      for (int j = 0; j < 8; j += 2) {
+        float g0, gd0, g1, gd1;
         const int k = 32 * s + 8 * q + j;
-        rbf_eval_t<BASIS>(rp, k < K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
-        const f16split sg = split2(g, S1), sgd = split2(gd, S1);
-        gh[j] = sg.hi;
-        gl[j] = sg.lo;
-        gdh[j] = sgd.hi;
-        gdl[j] = sgd.lo;
+        rbf_eval_t<BASIS>(rp, true, bc[k], bw[k], d, crbf, dcrbf, g0, gd0);
+        rbf_eval_t<BASIS>(rp, true, bc[k + 1], bw[k + 1], d, crbf, dcrbf, g1, gd1);
+        halfx2 h, lo, hd, lod;
+        split2x2(g0, g1, S1, h, lo);
+        split2x2(gd0, gd1, S1, hd, lod);
+        gh[s][j] = h[0];
+        gh[s][j + 1] = h[1];
+        gl[s][j] = lo[0];
+        gl[s][j + 1] = lo[1];
+        gdh[s][j] = hd[0];
+        gdh[s][j + 1] = hd[1];
+        gdl[s][j] = lod[0];
+        gdl[s][j + 1] = lod[1];
       }
-#pragma unroll
-      for (int t = 0; t < kFT; ++t) {
-        const int o = (t * KS32 + s) * MLCG_WAVE + l;
-        const halfx8 ah = w1v[o], ahs = w1v[n1v + o], al = w1v[2 * n1v + o];
-        a[t] = mfma_x3(ah, ahs, al, gh, gl, a[t]);
-        ad[t] = mfma_x3(ah, ahs, al, gdh, gdl, ad[t]);
-      }
-    }
-    // 2. h = act(a + b1), h' = act'(a + b1) a', split for the second product
+    // 1.-2. per feature tile t: a = W1 g, a' = W1 g' (times S1); then
+    // h = act(a + b1), h' = act'(a + b1) a', split for the second product
     halfx8 hh[kFT / 2], hl[kFT / 2], hdh[kFT / 2], hdl[kFT / 2];
 #pragma unroll
-    for (int t = 0; t < kFT; ++t)
+    for (int t = 0; t < kFT; ++t) {
+      floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float sv, d1, d2;
-        act_t<ACT>(a[t][i] * inv1 + b1s[16 * t + 4 * q + i], sv, d1, d2);
-        const int e = 4 * (t & 1) + i;
-        const float hd = d1 * (ad[t][i] * inv1);
-        const f16split sh = split2(sv, S2), shd = split2(hd, S2);
-        hh[t >> 1][e] = sh.hi;
-        hl[t >> 1][e] = sh.lo;
-        hdh[t >> 1][e] = shd.hi;
-        hdl[t >> 1][e] = shd.lo;
+      for (int s = 0; s < KS32; ++s) {
+        const int o = (t * KS32 + s) * MLCG_WAVE + l;
+        const halfx8 ah = w1v[o], ahs = w1v[n1v + o], al = w1v[2 * n1v + o];
+        a = mfma_x3(ah, ahs, al, gh[s], gl[s], a);
+        ad = mfma_x3(ah, ahs, al, gdh[s], gdl[s], ad);
       }
-    // 3. w = W2 h, w' = W2 h' (times S2)
-    floatx4 w[kFT], wd[kFT];
+      const float4 bias = *reinterpret_cast<const float4*>(b1s + 16 * t + 4 * q);
+      const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        float s0, s1, e0, e1, unused;
+        act_t<ACT>(a[i] * inv1 + bv[i], s0, e0, unused);
+        act_t<ACT>(a[i + 1] * inv1 + bv[i + 1], s1, e1, unused);
+        const float hd0 = e0 * (ad[i] * inv1), hd1 = e1 * (ad[i + 1] * inv1);
+        halfx2 h, lo, hd, lod;
+        split2x2(s0, s1, S2, h, lo);
+        split2x2(hd0, hd1, S2, hd, lod);
+        const int e = 4 * (t & 1) + i;
+        hh[t >> 1][e] = h[0];
+        hh[t >> 1][e + 1] = h[1];
+        hl[t >> 1][e] = lo[0];
+        hl[t >> 1][e + 1] = lo[1];
+        hdh[t >> 1][e] = hd[0];
+        hdh[t >> 1][e + 1] = hd[1];
+        hdl[t >> 1][e] = lod[0];
+        hdl[t >> 1][e + 1] = lod[1];
+      }
+    }
+    // 3. per output tile t: w = W2 h, w' = W2 h' (times S2), enveloped
+    const float c2 = cc * inv2, dc2 = dcc * inv2;  // 1 / S2 is a power of two
+    float* wr = Wout + p * kF + 4 * q;
+    float* wdr = Wdout + p * kF + 4 * q;
 #pragma unroll
     for (int t = 0; t < kFT; ++t) {
-      w[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      wd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+      floatx4 w = {0.f, 0.f, 0.f, 0.f}, wd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < kFT / 2; ++s)
-#pragma unroll
-      for (int t = 0; t < kFT; ++t) {
+      for (int s = 0; s < kFT / 2; ++s) {
         const int o = (t * (kFT / 2) + s) * MLCG_WAVE + l;
         const halfx8 ah = w2v[o], ahs = w2v[n2v + o], al = w2v[2 * n2v + o];
-        w[t] = mfma_x3(ah, ahs, al, hh[s], hl[s], w[t]);
-        wd[t] = mfma_x3(ah, ahs, al, hdh[s], hdl[s], wd[t]);
+        w = mfma_x3(ah, ahs, al, hh[s], hl[s], w);
+        wd = mfma_x3(ah, ahs, al, hdh[s], hdl[s], wd);
       }
-    if (valid) {
-      float* wr = Wout + p * kF + 4 * q;
-      float* wdr = Wdout + p * kF + 4 * q;
-      const float c2 = cc * inv2, dc2 = dcc * inv2;  // 1 / S2 is a power of two
-#pragma unroll
-      for (int t = 0; t < kFT; ++t) {
+      if (valid) {
         float4 o, od;
         float* op = reinterpret_cast<float*>(&o);
         float* odp = reinterpret_cast<float*>(&od);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          op[i] = w[t][i] * c2;
-          odp[i] = wd[t][i] * c2 + w[t][i] * dc2;
+          op[i] = w[i] * c2;
+          odp[i] = wd[i] * c2 + w[i] * dc2;
         }
         *reinterpret_cast<float4*>(wr + 16 * t) = o;
         *reinterpret_cast<float4*>(wdr + 16 * t) = od;
       }
-      if (dist_out && q == 0) dist_out[p] = d;
     }
+    if (valid && dist_out && q == 0) dist_out[p] = d;
   }
 }
 
 size_t fwd_x3_lds_bytes(int K) {
-  const int KS32 = (K + 31) / 32;
-  return sizeof(_Float16) * 3 * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
+  if (K > 32 * kX3Blocks) return SIZE_MAX;  // the x3 kernel pads K to 64
+  return sizeof(_Float16) * 3 *
+             (kFT * kX3Blocks * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
          sizeof(float) * (kF + 2 * kMaxK + kWavesX3);
 }
 
@@ -922,7 +1033,7 @@ __device__ __forceinline__ void tile_adjoint(const TileIn& t, bool tangent, bool
   wb = f4(wb.x * vm, wb.y * vm, wb.z * vm, wb.w * vm);
 }
 
-template <int KSMAX, bool kNodes>
+template <int KSMAX, bool kNodes, int BASIS, int ACT>
 __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
@@ -972,20 +1083,43 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 
   float S = 1.0f, inv_S = 1.0f;  // x3: the split scale of W2 and t
   if constexpr (kX3) {
+    // W2 read once into registers, in chunks of 8 plane elements (one halfx8
+    // of one lane's A fragment; chunk c held by thread c mod blockDim), which
+    // also gives the scale; then both planes written as halfx8.  Chunk
+    // c = (t, s, ll): A[m][8 kq + j] of block s for tile t =
+    // W2[32 s + 8 kq + j][16 t + m], m = ll & 15, kq = ll >> 4.
+    constexpr int kChunks = kF * kF / 8;
+    constexpr int kPer = kChunks / kBwdThreads;
+    static_assert(kChunks % kBwdThreads == 0, "whole chunks per thread");
+    float v2[kPer][8];
     float m2 = 0.f;
-    for (int x = threadIdx.x; x < kF * kF; x += blockDim.x) m2 = fmaxf(m2, fabsf(W2[x]));
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int c = threadIdx.x + r * kBwdThreads;
+      const int ll = c & 63, ts = c >> 6;
+      const int sb = ts & 3, t = ts >> 2;
+      const float* src = W2 + (32 * sb + 8 * (ll >> 4)) * kF + 16 * t + (ll & 15);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v2[r][j] = src[j * kF];
+        m2 = fmaxf(m2, fabsf(v2[r][j]));
+      }
+    }
     S = x3_scale(block_absmax(m2, PMAX));
     inv_S = 1.0f / S;
-    _Float16* w2h = reinterpret_cast<_Float16*>(w2ts);
-    constexpr int kPlane = kF * kF;
-    for (int x = threadIdx.x; x < kPlane; x += blockDim.x) {
-      // A[m][8 kq + j] of block s for tile t = W2[32 s + 8 kq + j][16 t + m]
-      const int j = x & 7, ll = (x >> 3) & 63, ts = x >> 9;
-      const int sb = ts & 3, t = ts >> 2;
-      const float v = W2[(32 * sb + 8 * (ll >> 4) + j) * kF + 16 * t + (ll & 15)];
-      const f16split sp = split2(v, S);
-      w2h[x] = sp.hi;
-      w2h[kPlane + x] = sp.lo;
+    halfx8* w2h = reinterpret_cast<halfx8*>(w2ts);
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int c = threadIdx.x + r * kBwdThreads;
+      halfx8 h, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f16split sp = split2(v2[r][j], S);
+        h[j] = sp.hi;
+        lo[j] = sp.lo;
+      }
+      w2h[c] = h;
+      w2h[kChunks + c] = lo;
     }
   } else {
     stage_w2_f32(w2ts, W2, true);
@@ -1074,47 +1208,51 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   };
   // Basis of a tile: wave w evaluates k steps w, w + 8, ... for the 16 pairs
   // (into GT), every lane the envelope of its own pair (returned).
-  auto basis = [&](const TileIn& t, float vm, int bsel, float& cc, float& dcc) {
+  // Lanes past the last pair evaluate the (finite) basis and activations of
+  // the last pair but carry zero adjoints (tile_adjoint's mask), hence
+  // t = t' = 0 and ab = ab' = 0: they add exact zeros to every pair sum.
+  auto basis = [&](const TileIn& t, int bsel, float& cc, float& dcc) {
     float* GTb = GT0 + bsel * 2 * kRows * 16;
     const float dx = t.xj - t.xi, dy = t.yj - t.yi, dz = t.zj - t.zi;
     const float d = sqrtf(dx * dx + dy * dy + dz * dz);
     float crbf, dcrbf;
-    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
+    envelopes(rp, d, crbf, dcrbf, cc, dcc);
 #pragma unroll
     for (int e = 0; e < kBasisSteps; ++e) {
       const int s = kBwdWaves * e + w;
       if (s < KSMAX) {
         float g, gd, cen = bcen[e], wid = bwid[e];
         if (!kBasisRegs) basis_params(rp, 4 * s + q, cen, wid);
-        rbf_eval(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
+        rbf_any<BASIS>(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
         if constexpr (kX3) {
           // two fp16 planes (hi, lo S4) of [2][kRows][16 pairs]
           _Float16* GTh = reinterpret_cast<_Float16*>(GTb);
           const int o = (4 * s + q) * 16 + n;
-          const float v0 = g * vm, v1 = gd * vm;
-          const f16split s0 = split2(v0, kS4), s1 = split2(v1, kS4);
-          GTh[o] = s0.hi;
-          GTh[kRows * 16 + o] = s1.hi;
-          GTh[2 * kRows * 16 + o] = s0.lo;
-          GTh[3 * kRows * 16 + o] = s1.lo;
+          const float v0 = g, v1 = gd;
+          halfx2 sh, sl;
+          split2x2(v0, v1, kS4, sh, sl);
+          GTh[o] = sh[0];
+          GTh[kRows * 16 + o] = sh[1];
+          GTh[2 * kRows * 16 + o] = sl[0];
+          GTh[3 * kRows * 16 + o] = sl[1];
           // step 1's copy (k = 4s + q: chunk s, element q)
           const int o1 = n * 64 + 4 * (s ^ n) + q;
           const float u0 = v0 * kBetaG0, u1 = v1 * kBetaG1;
-          const f16split c0 = split2(u0, kS4), c1 = split2(u1, kS4);
-          G1h[o1] = c0.hi;
-          G1h[1024 + o1] = c1.hi;
-          G1h[2048 + o1] = (_Float16)((float)c0.hi * kS4);
-          G1h[3072 + o1] = (_Float16)((float)c1.hi * kS4);
-          G1h[4096 + o1] = c0.lo;
-          G1h[5120 + o1] = c1.lo;
+          halfx2 ch, cl;
+          split2x2(u0, u1, kS4, ch, cl);
+          G1h[o1] = ch[0];
+          G1h[1024 + o1] = ch[1];
+          G1h[2048 + o1] = (_Float16)((float)ch[0] * kS4);
+          G1h[3072 + o1] = (_Float16)((float)ch[1] * kS4);
+          G1h[4096 + o1] = cl[0];
+          G1h[5120 + o1] = cl[1];
         } else {
           const int o = rp_at(4 * s + q, n);
-          GTb[o] = g * vm;
-          GTb[kRows * 16 + o] = gd * vm;
+          GTb[o] = g;
+          GTb[kRows * 16 + o] = gd;
         }
       }
     }
-    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
   };
 
   // t, t' of the lane's 4 features of a tile (formed one tile ahead, in the
@@ -1160,7 +1298,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     ni = pi[p1];
     nj = pj[p1];
     const float vm0 = (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f;
-    basis(first, vm0, 0, cc_cur, dcc_cur);
+    basis(first, 0, cc_cur, dcc_cur);
     float4 wb0, wdb0;
     tile_adjoint<kNodes>(first, tangent, has_yd, vm0, wb0, wdb0);
     pair_adjoints(wb0, wdb0, cc_cur, dcc_cur, 0);
@@ -1227,11 +1365,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float sv, d1, d2;
-      mlcg_act(rp.act, a[i] + bias[i], sv, d1, d2);
+      act_any<ACT>(rp.act, a[i] + bias[i], sv, d1, d2);
       act1[i] = d1;
       act2[i] = d2 * ad[i];
-      hv[i] = sv * vmask;
-      hdv[i] = d1 * ad[i] * vmask;
+      hv[i] = sv;
+      hdv[i] = d1 * ad[i];
     }
     if constexpr (kX3) {
       // h beta, h' beta as two fp16 planes (hi, lo S4) of [2][128 rows][16
@@ -1240,12 +1378,12 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int o = (16 * w + 4 * q + (i ^ q)) * 16 + n;
-        const float v0 = hv[i] * kBetaH, v1 = hdv[i] * kBetaH;
-        const f16split s0 = split2(v0, kS4), s1 = split2(v1, kS4);
-        HTh[o] = s0.hi;
-        HTh[kF * 16 + o] = s1.hi;
-        HTh[2 * kF * 16 + o] = s0.lo;
-        HTh[3 * kF * 16 + o] = s1.lo;
+        halfx2 sh, sl;
+        split2x2(hv[i] * kBetaH, hdv[i] * kBetaH, kS4, sh, sl);
+        HTh[o] = sh[0];
+        HTh[kF * 16 + o] = sh[1];
+        HTh[2 * kF * 16 + o] = sl[0];
+        HTh[3 * kF * 16 + o] = sl[1];
       }
     } else {
 #pragma unroll
@@ -1262,6 +1400,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       // barrier below); its last reader was phase 2 of the previous tile
       if (w == 0 && l < 32) PMAXu[(buf ^ 1) * 32 + l] = 0u;
       const float sg0 = x3_norm(m0), sg1 = x3_norm(m1);
+      const halfx2 S16 = halfx2{(_Float16)S, (_Float16)S};
       inv_t = x3_norm_inv(m0) * inv_S;
       inv_td = x3_norm_inv(m1) * inv_S;
       // three planes (hi, hi S, lo S) of t sigma; float4 group g of pair n's
@@ -1274,11 +1413,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         const float* src = st ? tdb : tb;
         halfx4 ph, phs, pl;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f16split sp = split2(src[i] * sg, S);
-          ph[i] = sp.hi;
-          phs[i] = (_Float16)((float)sp.hi * S);
-          pl[i] = sp.lo;
+        for (int i = 0; i < 4; i += 2) {
+          halfx2 sh, sl;
+          split2x2(src[i] * sg, src[i + 1] * sg, S, sh, sl);
+          const halfx2 shs = sh * S16;  // exact: S is a power of two
+          ph[i] = sh[0];
+          ph[i + 1] = sh[1];
+          phs[i] = shs[0];
+          phs[i + 1] = shs[1];
+          pl[i] = sl[0];
+          pl[i + 1] = sl[1];
         }
         *reinterpret_cast<halfx4*>(TBh + (0 * 2 + st) * 16 * kF + o) = ph;
         *reinterpret_cast<halfx4*>(TBh + (1 * 2 + st) * 16 * kF + o) = phs;
@@ -1383,12 +1527,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       halfx8 ah, ahs, al;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float s = xv[j] * rw;
-        const f16split sp = split2(s, kS4);
-        ah[j] = sp.hi;
-        ahs[j] = (_Float16)((float)sp.hi * kS4);
-        al[j] = sp.lo;
+      for (int j = 0; j < 8; j += 2) {
+        halfx2 sh, sl;
+        split2x2(xv[j] * rw, xv[j + 1] * rw, kS4, sh, sl);
+        ah[j] = sh[0];
+        ah[j + 1] = sh[1];
+        ahs[j] = (_Float16)((float)sh[0] * kS4);
+        ahs[j + 1] = (_Float16)((float)sh[1] * kS4);
+        al[j] = sl[0];
+        al[j + 1] = sl[1];
       }
       const halfx8* hth = reinterpret_cast<const halfx8*>(HT);
 #pragma unroll
@@ -1428,7 +1575,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) =
           f4(adbv[0], adbv[1], adbv[2], adbv[3]);
     }
-    basis(nxt, vm_nxt, buf ^ 1, cc_cur, dcc_cur);
+    basis(nxt, buf ^ 1, cc_cur, dcc_cur);
     pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur, buf ^ 1);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
@@ -1450,12 +1597,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       halfx8 ah, ahs, al;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float s = xv[j] * ra;
-        const f16split sp = split2(s, kS4);
-        ah[j] = sp.hi;
-        ahs[j] = (_Float16)((float)sp.hi * kS4);
-        al[j] = sp.lo;
+      for (int j = 0; j < 8; j += 2) {
+        halfx2 sh, sl;
+        split2x2(xv[j] * ra, xv[j + 1] * ra, kS4, sh, sl);
+        ah[j] = sh[0];
+        ah[j + 1] = sh[1];
+        ahs[j] = (_Float16)((float)sh[0] * kS4);
+        ahs[j + 1] = (_Float16)((float)sh[1] * kS4);
+        al[j] = sl[0];
+        al[j + 1] = sl[1];
       }
       // B: halfx8 of plane rows 16kt + n, stream q >> 1, pairs 8 (q & 1) .. + 7
       const halfx8* gth = reinterpret_cast<const halfx8*>(GT);
@@ -1589,14 +1739,19 @@ void allow_lds_once() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<1, 1>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  const void* bwd[] = {
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 0, 0>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 0, 1>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 1, 0>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 1, 1>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true, 0, 0>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true, 0, 1>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true, 1, 0>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, true, 1, 1>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, false, -1, -1>),
+      reinterpret_cast<const void*>(filter_bwd_fused_kernel<32, true, -1, -1>)};
+  for (const void* f : bwd)
+    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   done[dev] = true;
 }
 
@@ -1714,14 +1869,26 @@ int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_str
   allow_lds_once();
   const int grid = max_pairs == 0 ? 1 : groups;
   const bool small_k = num_rbf <= 64;
-#define MLCG_BWD_LAUNCH(KS, NODES)                                                         \
-  hipLaunchKernelGGL((filter_bwd_fused_kernel<KS, NODES>), dim3(grid), dim3(kBwdThreads), \
-                     lds, s, pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs,  \
-                     rp, W1, b1, W2, adj, abar_out, adbar_out, workspace)
-  if (small_k && !nodes) MLCG_BWD_LAUNCH(16, false);
-  else if (small_k) MLCG_BWD_LAUNCH(16, true);
-  else if (!nodes) MLCG_BWD_LAUNCH(32, false);
-  else MLCG_BWD_LAUNCH(32, true);
+#define MLCG_BWD_LAUNCH(KS, NODES, B, A)                                                      \
+  hipLaunchKernelGGL((filter_bwd_fused_kernel<KS, NODES, B, A>), dim3(grid),                 \
+                     dim3(kBwdThreads), lds, s, pos, pair_ij, pair_ij + pair_stride,         \
+                     n_pairs_dev, max_pairs, rp, W1, b1, W2, adj, abar_out, adbar_out,       \
+                     workspace)
+#define MLCG_BWD_SMALL(NODES)                                   \
+  if (basis == 0 && act == 0) MLCG_BWD_LAUNCH(16, NODES, 0, 0); \
+  else if (basis == 0) MLCG_BWD_LAUNCH(16, NODES, 0, 1);        \
+  else if (act == 0) MLCG_BWD_LAUNCH(16, NODES, 1, 0);          \
+  else MLCG_BWD_LAUNCH(16, NODES, 1, 1)
+  if (small_k && !nodes) {
+    MLCG_BWD_SMALL(false);
+  } else if (small_k) {
+    MLCG_BWD_SMALL(true);
+  } else if (!nodes) {
+    MLCG_BWD_LAUNCH(32, false, -1, -1);
+  } else {
+    MLCG_BWD_LAUNCH(32, true, -1, -1);
+  }
+#undef MLCG_BWD_SMALL
 #undef MLCG_BWD_LAUNCH
   const int total = kF * kF + kF * num_rbf + kF;
   hipLaunchKernelGGL(filter_bwd_reduce_kernel, dim3((total + kRedOut - 1) / kRedOut), dim3(256),

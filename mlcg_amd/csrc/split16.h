@@ -33,6 +33,22 @@ __device__ __forceinline__ f16split split2(float v, float S) {
   return f16split{hi, (_Float16)((v - (float)hi) * S)};
 }
 
+typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// split2 of two values at once: both hi parts from one packed round-to-
+// nearest-even conversion, and each lo part as fma(-hi, S, v S) rounded to
+// fp16 once.  v S is exact (S is a power of two) and so is the fma's exact
+// result (v - hi) S, so lo equals split2's fp16((v - hi) S) bit for bit; the
+// fma takes hi straight from its fp16 half (a mixed-precision fma), which
+// makes the pair cost five instructions instead of ten.
+__device__ __forceinline__ void split2x2(float v0, float v1, float S, halfx2& hi, halfx2& lo) {
+  asm("" : "+v"(v0), "+v"(v1));
+  hi = __builtin_convertvector(floatx2{v0, v1}, halfx2);
+  lo[0] = (_Float16)__builtin_fmaf(-(float)hi[0], S, v0 * S);
+  lo[1] = (_Float16)__builtin_fmaf(-(float)hi[1], S, v1 * S);
+}
+
 // sigma = 2^k with m sigma < 4: brings values of magnitude <= m into the
 // range the split planes of an operand expect (sigma = 4 for m = 0).
 __device__ __forceinline__ float x3_norm(float m) {
@@ -49,31 +65,36 @@ __device__ __forceinline__ float x3_norm_inv(float m) {
 }
 
 // Maxima across lanes without the LDS crossbar: DPP inside a row of 16
-// lanes, v_permlane16_swap / v_permlane32_swap across the four rows.
+// lanes, v_permlane16_swap / v_permlane32_swap across the four rows.  The
+// arguments are magnitudes (non-negative floats, or NaN): their bit patterns
+// order as unsigned integers, so the maxima are taken as v_max_u32 (one
+// instruction per step with the DPP operand folded in; a float max would
+// first quiet the moved operand), and a NaN, being the largest pattern,
+// propagates instead of being dropped.
 template <int kCtrl>
-__device__ __forceinline__ float dpp_fmax(float v) {
-  return fmaxf(v, __int_as_float(
-                      __builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false)));
+__device__ __forceinline__ unsigned dpp_umax(unsigned v) {
+  return max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xF, 0xF, false));
 }
 // max over the 16 lanes of each row, in every lane of the row
 __device__ __forceinline__ float row16_max(float v) {
-  v = dpp_fmax<0xB1>(v);      // quad_perm [1, 0, 3, 2]
-  v = dpp_fmax<0x4E>(v);      // quad_perm [2, 3, 0, 1]
-  v = dpp_fmax<0x141>(v);     // row_half_mirror
-  return dpp_fmax<0x140>(v);  // row_mirror
+  unsigned u = __float_as_uint(v);
+  u = dpp_umax<0xB1>(u);      // quad_perm [1, 0, 3, 2]
+  u = dpp_umax<0x4E>(u);      // quad_perm [2, 3, 0, 1]
+  u = dpp_umax<0x141>(u);     // row_half_mirror
+  u = dpp_umax<0x140>(u);     // row_mirror
+  return __uint_as_float(u);
 }
 // max over lanes l and l ^ 16, in both
 __device__ __forceinline__ float pair_row_max(float v) {
-  const auto a =
-      __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(max(a[0], a[1]));
 }
 // max over lanes l, l ^ 16, l ^ 32, l ^ 48, in each of them
 __device__ __forceinline__ float cross_row_max(float v) {
-  v = pair_row_max(v);
-  const auto b =
-      __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  const unsigned u = __float_as_uint(pair_row_max(v));
+  const auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(max(b[0], b[1]));
 }
 
 // Sums across lanes in the same fixed patterns (the result is the same on
