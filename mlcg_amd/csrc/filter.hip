@@ -436,30 +436,45 @@ __device__ void stage_f16(_Float16* w1h, _Float16* w2h, const float* __restrict_
   }
 }
 
-// 4 waves per workgroup (one per SIMD): the fp16 tile keeps more operand
-// fragments live than the fp32 one, and one wave per SIMD gets the full
-// register file, so nothing spills.
-constexpr int kWaves16 = 4;
+// tanh for the fp16 filter: 1 - 2 / (e^2x + 1) in fp32 (two hardware
+// transcendentals; saturates to exactly +-1).  Its absolute error is a few
+// 1e-7 -- relative accuracy is lost only where |tanh x| < 1e-3, and the value
+// is rounded to fp16 (relative step 2^-11) right after.
+__device__ __forceinline__ float tanh_f16path(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);  // e^2x
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+}
+
+// 8 waves per workgroup and two workgroups per CU: one wave per 16-pair
+// tile, feature tile at a time (as filter_fwd_x3_kernel), so only two
+// accumulators are live next to the fp16 operands.
+#ifndef MLCG_F16_WAVES
+#define MLCG_F16_WAVES 8
+#endif
+#ifndef MLCG_F16_GROUPS_PER_CU
+#define MLCG_F16_GROUPS_PER_CU 2
+#endif
+constexpr int kWaves16 = MLCG_F16_WAVES;  // the second launch bound is waves per SIMD
 constexpr int kThreads16 = kWaves16 * MLCG_WAVE;
 
-__global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
+template <int KS32, int BASIS, int ACT>
+__global__ __launch_bounds__(kThreads16, kWaves16 * MLCG_F16_GROUPS_PER_CU / 4) void filter_fwd_f16_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ pi,
     const int32_t* __restrict__ pj, const int32_t* __restrict__ n_pairs_dev,
     int64_t max_pairs, RbfParams rp, const float* __restrict__ W1,
     const float* __restrict__ b1, const float* __restrict__ W2, __half* __restrict__ Wout,
     __half* __restrict__ Wdout, float* __restrict__ dist_out) {
   extern __shared__ float lds[];
-  const int KS32 = (rp.K + 31) / 32;
   _Float16* w1h = reinterpret_cast<_Float16*>(lds);
   _Float16* w2h = w1h + kFT * KS32 * MLCG_WAVE * 8;
-  // the bias lives in LDS here (not registers): the fp16 path keeps more
-  // operand fragments live and would otherwise spill
   float* b1s = reinterpret_cast<float*>(w2h + kFT * (kFT / 2) * MLCG_WAVE * 8);
   float* bc = b1s + kF;
   float* bw = bc + kMaxK;
+  // per-wave output staging buffer, 1024 halfs
+  _Float16* obuf = reinterpret_cast<_Float16*>(bw + kMaxK) + (threadIdx.x / MLCG_WAVE) * 1024;
   stage_f16(w1h, w2h, W1, W2, rp.K, KS32);
   for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
-  stage_basis(bc, bw, rp);
+  stage_basis(bc, bw, rp);  // zeros past K: finite basis values that meet zero weights
   __syncthreads();
 
   int64_t np = *n_pairs_dev;
@@ -472,77 +487,126 @@ __global__ __launch_bounds__(kThreads16) void filter_fwd_f16_kernel(
   const halfx8* w2v = reinterpret_cast<const halfx8*>(w2h);
   const int64_t wave = (int64_t)blockIdx.x * kWaves16 + threadIdx.x / MLCG_WAVE;
   const int64_t nwaves = (int64_t)gridDim.x * kWaves16;
+  auto pair_at = [&](int64_t t_) -> int64_t {
+    const int64_t p_ = (t_ < tiles ? t_ : tiles - 1) * 16 + (l & 15);
+    return p_ < np ? p_ : np - 1;
+  };
+  float3 ri{0.f, 0.f, 0.f}, rj{0.f, 0.f, 0.f};
+  int64_t ni = 0, nj = 0;
+  if (wave < tiles) {
+    const int64_t p0 = pair_at(wave), p1 = pair_at(wave + nwaves);
+    const int64_t i0 = pi[p0], j0 = pj[p0];
+    ri = float3{pos[3 * i0], pos[3 * i0 + 1], pos[3 * i0 + 2]};
+    rj = float3{pos[3 * j0], pos[3 * j0 + 1], pos[3 * j0 + 2]};
+    ni = pi[p1];
+    nj = pj[p1];
+  }
   for (int64_t tile = wave; tile < tiles; tile += nwaves) {
+    // the weight fragments are re-read from LDS every tile: without this
+    // barrier the compiler hoists all 48 of them into registers and spills
+    asm volatile("" ::: "memory");
     const int64_t p = tile * 16 + (l & 15);
     const bool valid = p < np;
-    const float d = pair_distance(pos, pi, pj, p, valid);
-    float crbf, dcrbf, cc, dcc;
-    mlcg_cutoff(rp.rbf_kind, rp.rbf_lo, rp.rbf_hi, d, crbf, dcrbf);
-    conv_cutoff(rp, d, crbf, dcrbf, cc, dcc);
-
-    floatx4 a[kFT], ad[kFT];
-#pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      a[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      ad[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float d = 1.0f;
+    if (valid) {
+      const float dx = rj.x - ri.x, dy = rj.y - ri.y, dz = rj.z - ri.z;
+      d = sqrtf(dx * dx + dy * dy + dz * dz);
     }
-    for (int s = 0; s < KS32; ++s) {
-      halfx8 g8, gd8;
+    ri = float3{pos[3 * ni], pos[3 * ni + 1], pos[3 * ni + 2]};
+    rj = float3{pos[3 * nj], pos[3 * nj + 1], pos[3 * nj + 2]};
+    {
+      const int64_t p2 = pair_at(tile + 2 * nwaves);
+      ni = pi[p2];
+      nj = pj[p2];
+    }
+    float crbf, dcrbf, cc, dcc;
+    envelopes(rp, d, crbf, dcrbf, cc, dcc);
+
+    halfx8 g8[KS32], gd8[KS32];
+#pragma unroll
+    for (int s = 0; s < KS32; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float g, gd;
         const int k = 32 * s + 8 * q + j;
-        rbf_eval(rp, k < rp.K, bc[k], bw[k], d, crbf, dcrbf, g, gd);
-        g8[j] = (_Float16)g;
-        gd8[j] = (_Float16)gd;
+        rbf_eval_t<BASIS>(rp, true, bc[k], bw[k], d, crbf, dcrbf, g, gd);
+        g8[s][j] = (_Float16)g;
+        gd8[s][j] = (_Float16)gd;
       }
-#pragma unroll
-      for (int t = 0; t < kFT; ++t) {
-        const halfx8 w = w1v[(t * KS32 + s) * MLCG_WAVE + l];
-        a[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, g8, a[t], 0, 0, 0);
-        ad[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, gd8, ad[t], 0, 0, 0);
-      }
-    }
     halfx8 h8[kFT / 2], hd8[kFT / 2];
 #pragma unroll
-    for (int t = 0; t < kFT; ++t)
+    for (int t = 0; t < kFT; ++t) {
+      floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS32; ++s) {
+        const halfx8 w = w1v[(t * KS32 + s) * MLCG_WAVE + l];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, g8[s], a, 0, 0, 0);
+        ad = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, gd8[s], ad, 0, 0, 0);
+      }
+      const float4 bias = *reinterpret_cast<const float4*>(b1s + 16 * t + 4 * q);
+      const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float s, d1, d2;
-        mlcg_act(rp.act, a[t][i] + b1s[16 * t + 4 * q + i], s, d1, d2);
-        h8[t >> 1][4 * (t & 1) + i] = (_Float16)s;
-        hd8[t >> 1][4 * (t & 1) + i] = (_Float16)(d1 * ad[t][i]);
+        float sv, d1;
+        if constexpr (ACT == MLCG_ACT_TANH) {
+          sv = tanh_f16path(a[i] + bv[i]);
+          d1 = fmaf(-sv, sv, 1.0f);
+        } else {
+          float d2;
+          act_t<ACT>(a[i] + bv[i], sv, d1, d2);
+        }
+        h8[t >> 1][4 * (t & 1) + i] = (_Float16)sv;
+        hd8[t >> 1][4 * (t & 1) + i] = (_Float16)(d1 * ad[i]);
       }
-    floatx4 w[kFT], wd[kFT];
-#pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      w[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      wd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
+    // Output in two halves of the features: W then W' of the 16 pairs go
+    // through the wave's own 2 KB LDS buffer ([16 pairs][64 halfs], 16-byte
+    // chunk c of row n stored at c ^ (n & 7)), so that every global store
+    // writes 8 whole 128-byte row halves.  Only this wave touches its buffer
+    // and a wave's LDS operations complete in issue order, so the compiler
+    // barriers (which keep the accesses in program order) are the only
+    // synchronisation needed.
+    const int64_t row0 = tile * 16;
 #pragma unroll
-    for (int s = 0; s < kFT / 2; ++s)
+    for (int hf = 0; hf < 2; ++hf) {
+      halfx4 ow[4], owd[4];
 #pragma unroll
-      for (int t = 0; t < kFT; ++t) {
-        const halfx8 a2 = w2v[(t * (kFT / 2) + s) * MLCG_WAVE + l];
-        w[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, h8[s], w[t], 0, 0, 0);
-        wd[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, hd8[s], wd[t], 0, 0, 0);
-      }
-    if (valid) {
-      __half* wr = Wout + p * kF + 4 * q;
-      __half* wdr = Wdout + p * kF + 4 * q;
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t = 4 * hf + tt;
+        floatx4 w = {0.f, 0.f, 0.f, 0.f}, wd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < kFT; ++t) {
-        halfx4 o, od;
+        for (int s = 0; s < kFT / 2; ++s) {
+          const halfx8 a2 = w2v[(t * (kFT / 2) + s) * MLCG_WAVE + l];
+          w = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, h8[s], w, 0, 0, 0);
+          wd = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, hd8[s], wd, 0, 0, 0);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          o[i] = (_Float16)(w[t][i] * cc);
-          od[i] = (_Float16)(wd[t][i] * cc + w[t][i] * dcc);
+          ow[tt][i] = (_Float16)(w[i] * cc);
+          owd[tt][i] = (_Float16)(wd[i] * cc + w[i] * dcc);
         }
-        *reinterpret_cast<halfx4*>(wr + 16 * t) = o;
-        *reinterpret_cast<halfx4*>(wdr + 16 * t) = od;
       }
-      if (dist_out && q == 0) dist_out[p] = d;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int c = 2 * tt + (q >> 1);
+          *reinterpret_cast<halfx4*>(obuf + (l & 15) * 64 + ((c ^ (l & 7)) << 3) + 4 * (q & 1)) =
+              m ? owd[tt] : ow[tt];
+        }
+        asm volatile("" ::: "memory");
+        __half* dst = m ? Wdout : Wout;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int r = 8 * i + (l >> 3), c = l & 7;
+          const halfx8 v = *reinterpret_cast<const halfx8*>(obuf + r * 64 + ((c ^ (r & 7)) << 3));
+          if (row0 + r < np)
+            *reinterpret_cast<halfx8*>(dst + (row0 + r) * kF + 64 * hf + 8 * c) = v;
+        }
+      }
     }
+    if (valid && dist_out && q == 0) dist_out[p] = d;
   }
 }
 
@@ -1729,8 +1793,6 @@ void allow_lds_once() {
   const int bytes = 160 * 1024;
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f32_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_f16_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<0, 0>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<0, 1>),
@@ -1739,6 +1801,17 @@ void allow_lds_once() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(filter_fwd_x3_kernel<1, 1>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  const void* f16[] = {
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<2, 0, 0>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<2, 0, 1>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<2, 1, 0>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<2, 1, 1>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<4, 0, 0>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<4, 0, 1>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<4, 1, 0>),
+      reinterpret_cast<const void*>(filter_fwd_f16_kernel<4, 1, 1>)};
+  for (const void* f : f16)
+    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   const void* bwd[] = {
       reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 0, 0>),
       reinterpret_cast<const void*>(filter_bwd_fused_kernel<16, false, 0, 1>),
@@ -1826,15 +1899,31 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
                        pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
                        static_cast<float*>(W_out), static_cast<float*>(Wd_out), dist_out);
   } else {
-    const int KS32 = (num_rbf + 31) / 32;
+    // K padded to 64 or 128 (two or four 32-wide k blocks)
+    const int KS32 = num_rbf <= 64 ? 2 : 4;
     const size_t lds =
         sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
-        sizeof(float) * (kF + 2 * kMaxK);
+        sizeof(float) * (kF + 2 * kMaxK) + sizeof(_Float16) * 1024 * kWaves16;
     allow_lds_once();
-    const unsigned groups16 = mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves16), 1);
-    hipLaunchKernelGGL(filter_fwd_f16_kernel, dim3(groups16), dim3(kThreads16), lds, s, pos,
-                       pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1, b1, W2,
-                       static_cast<__half*>(W_out), static_cast<__half*>(Wd_out), dist_out);
+    const unsigned groups16 =
+        mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves16), MLCG_F16_GROUPS_PER_CU);
+#define MLCG_F16_LAUNCH(KB, B, A)                                                             \
+  hipLaunchKernelGGL((filter_fwd_f16_kernel<KB, B, A>), dim3(groups16), dim3(kThreads16), lds, \
+                     s, pos, pair_ij, pair_ij + pair_stride, n_pairs_dev, max_pairs, rp, W1,   \
+                     b1, W2, static_cast<__half*>(W_out), static_cast<__half*>(Wd_out),       \
+                     dist_out)
+#define MLCG_F16_KB(KB)                                       \
+  if (basis == 0 && act == 0) MLCG_F16_LAUNCH(KB, 0, 0);      \
+  else if (basis == 0) MLCG_F16_LAUNCH(KB, 0, 1);             \
+  else if (act == 0) MLCG_F16_LAUNCH(KB, 1, 0);               \
+  else MLCG_F16_LAUNCH(KB, 1, 1)
+    if (KS32 == 2) {
+      MLCG_F16_KB(2);
+    } else {
+      MLCG_F16_KB(4);
+    }
+#undef MLCG_F16_KB
+#undef MLCG_F16_LAUNCH
   }
   return mlcg_launch_status();
 }
