@@ -152,28 +152,47 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
   }
 }
 
-// forces[a] (+)= sum over the slots of bead a, ascending slot id.
+// forces[a] (+)= sum over the slots of bead a.  A group of kGatherLanes
+// lanes serves one bead: lane k sums the bead's slots k, k + kGatherLanes,
+// ... in ascending order, and the group then adds its partial sums in a fixed
+// butterfly, so the result does not depend on timing (a bead of the
+// repulsion prior has hundreds of slots; a lane per bead would walk them one
+// dependent load at a time).
+constexpr int kGatherLanes = 16;
+
 __global__ __launch_bounds__(256) void prior_gather_kernel(
     const float* __restrict__ slot_f, const int32_t* __restrict__ bead_ptr,
     const int32_t* __restrict__ bead_slots, int64_t n, int accumulate,
     float* __restrict__ forces) {
-  for (int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; a < n;
-       a += (int64_t)gridDim.x * blockDim.x) {
+  const int sub = threadIdx.x % kGatherLanes;
+  const int64_t ngroups = (int64_t)gridDim.x * blockDim.x / kGatherLanes;
+  for (int64_t a = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kGatherLanes; a < n;
+       a += ngroups) {
     float fx = 0.f, fy = 0.f, fz = 0.f;
-    for (int32_t s = bead_ptr[a]; s < bead_ptr[a + 1]; ++s) {
+    const int32_t s1 = bead_ptr[a + 1];
+    for (int32_t s = bead_ptr[a] + sub; s < s1; s += kGatherLanes) {
       const int64_t slot = bead_slots[s];
       fx += slot_f[3 * slot];
       fy += slot_f[3 * slot + 1];
       fz += slot_f[3 * slot + 2];
     }
-    if (accumulate) {
-      forces[3 * a] += fx;
-      forces[3 * a + 1] += fy;
-      forces[3 * a + 2] += fz;
-    } else {
-      forces[3 * a] = fx;
-      forces[3 * a + 1] = fy;
-      forces[3 * a + 2] = fz;
+    // every lane of the group shares a, so the group is active together
+#pragma unroll
+    for (int o = kGatherLanes / 2; o > 0; o >>= 1) {
+      fx += __shfl_xor(fx, o, kGatherLanes);
+      fy += __shfl_xor(fy, o, kGatherLanes);
+      fz += __shfl_xor(fz, o, kGatherLanes);
+    }
+    if (sub == 0) {
+      if (accumulate) {
+        forces[3 * a] += fx;
+        forces[3 * a + 1] += fy;
+        forces[3 * a + 2] += fz;
+      } else {
+        forces[3 * a] = fx;
+        forces[3 * a + 1] = fy;
+        forces[3 * a + 2] = fz;
+      }
     }
   }
 }
@@ -256,7 +275,7 @@ extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t*
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(bead_ptr && forces);
   MLCG_REQUIRE(slot_forces || bead_slots == nullptr);
-  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes, 256), 8);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes * kGatherLanes, 256), 8);
   hipLaunchKernelGGL(prior_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
                      slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces);
   return mlcg_launch_status();
