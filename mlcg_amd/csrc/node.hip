@@ -431,11 +431,13 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
   const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  halfx8 bh[2][kF / 32], bl[2][kF / 32];
-  gemm_load_w<kXW>(bh, bl, W, w, q, n);
+  // the first tile's rows are requested before the weights, so that the two
+  // loads' latencies overlap
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
   gemm_load_x(pf, x, t, rows);
+  halfx8 bh[2][kF / 32], bl[2][kF / 32];
+  gemm_load_w<kXW>(bh, bl, W, w, q, n);
   gemm_stage_x3(xs[0], rinv[0], pf);
   __syncthreads();
   int buf = 0;
@@ -495,12 +497,12 @@ void node_gemm2_kernel(
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
   const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  halfx8 bh[2][kF / 32], bl[2][kF / 32], ch[2][kF / 32], cl[2][kF / 32];
-  gemm_load_w<kXW>(bh, bl, W, w, q, n);
-  gemm_load_w<kXW>(ch, cl, W2, w, q, n);
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
   gemm_load_x(pf, x, t, rows);
+  halfx8 bh[2][kF / 32], bl[2][kF / 32], ch[2][kF / 32], cl[2][kF / 32];
+  gemm_load_w<kXW>(bh, bl, W, w, q, n);
+  gemm_load_w<kXW>(ch, cl, W2, w, q, n);
   gemm_stage_x3(xs[0], rinv[0], pf);
   __syncthreads();
   int buf = 0;

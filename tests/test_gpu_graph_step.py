@@ -1,7 +1,9 @@
-"""The force-matching training step captured as one HIP graph (what bench.py
-times) against the same step run eagerly: every replay, with eager work and
-synchronisations between the replays, gives the eager loss and parameters
-bit for bit."""
+"""The force-matching training step captured as one HIP graph (bench.py's
+captured_step) against the same step run eagerly: every replay, with eager
+work and synchronisations between the replays, gives the eager loss and
+parameters bit for bit.  The capture follows torch's rules: a capturable
+optimizer (a non-capturable one raises inside the capture region), warm-up
+and capture on one side stream, no timing events inside the capture."""
 
 import pytest
 import torch
@@ -12,9 +14,6 @@ from tests.helpers import make_cfg, make_model
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.skip(reason="capture of the whole training step crashed the host process in "
-                         "bench.py (512 frames, eager warm-up on the default stream); until "
-                         "that crash has a fix tested once, no variant of it runs on the GPU")
 def test_captured_training_step_matches_eager():
     from mlcg_amd import nn, synthetic
 
@@ -53,7 +52,7 @@ def test_captured_training_step_matches_eager():
                 params.append([p.detach().clone() for p in model.parameters()])
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
+            with torch.cuda.graph(graph, stream=side):
                 static_loss = step()
             for _ in range(4):  # steps 3..6 by replay, eager work in between
                 graph.replay()
