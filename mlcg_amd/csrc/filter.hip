@@ -963,9 +963,8 @@ size_t fwd_x3_lds_bytes(int K) {
 // one tile ahead and the pair indices two tiles ahead, so no load latency is
 // waited for inside a tile.
 //
-// LDS layouts.  The LDS has 32 four-byte banks; a float4 access serves the
-// lane groups {0-3, 20-23}, {4-7, 16-19}, {8-11, 28-31}, {12-15, 24-27} (and
-// the same +32) in one cycle each, a scalar access one half-wave per cycle.
+// LDS layouts (fp32 path; the split path's TB, TT and AT layouts and the
+// measured lane groups of the LDS are given at tb_swz and tt_at).
 //   TB  [pair][feature]: t, t' as the B operand of step 3 (float4 of four
 //       features of one pair); rows of 128 floats, float4 group g of pair n
 //       stored at g ^ (n & 7).
@@ -973,12 +972,28 @@ size_t fwd_x3_lds_bytes(int K) {
 //       operands of the pair reductions, steps 4 and 6 (float4 of four pairs
 //       of one row), and the B operand of step 1 (scalar); rows of 16 floats,
 //       float4 pair group c of row r stored at c ^ ((r >> 1) & 3).
-// All reads are free of bank conflicts; the scalar [row][pair] writes of TT,
-// HT and AT are 2-way.
 constexpr int kBwdWaves = 8;
 constexpr int kBwdThreads = kBwdWaves * MLCG_WAVE;
 
 __device__ __forceinline__ int tb_at(int pair, int g) { return pair * kF + ((g ^ (pair & 7)) << 2); }
+// Split path: chunk g (16 bytes) of pair n's fp16 row at g ^ tb_swz(n).
+// Measured on gfx950 (LDS bank-conflict counter, one wave): a 16-byte-per-lane
+// access is served for the lane groups {0-3, 12-15, 20-23, 24-27} and
+// {4-11, 16-19, 28-31} (and the same + 32) in one cycle each over 64
+// four-byte banks, an 8-byte access for lanes 0-31 and 32-63 over 64 banks,
+// a 4-byte access for lanes 0-31 and 32-63 over 32 banks.  The pair row of
+// 256 bytes covers the 64 banks once; with this permutation both the step-3
+// reads (chunk 4 sb + q of pair n) and the step-2 writes (chunk 2 w + q / 2,
+// half q % 2) reach distinct banks in every group.
+__device__ __forceinline__ int tb_swz(int n) { return n ^ (n >> 2); }
+// Split path: TT and AT [row][pair] (rows of 16 floats): row r at position
+// r ^ ((r >> 2) & 3) and pair p at p ^ 4 ((r >> 2) & 1).  The scalar writes
+// (lane (n, q) -> row 16 w + 4 q + i, pair n) and the float4 reads (lane
+// (n, q) -> row 16 w + n, pairs 8 (q & 1) + 0..3 and + 4..7) are then free of
+// bank conflicts under the lane groups above.
+__device__ __forceinline__ int tt_at(int r, int pair) {
+  return 16 * (r ^ ((r >> 2) & 3)) + (pair ^ (((r >> 2) & 1) << 2));
+}
 __device__ __forceinline__ int rp_at(int r, int pair) {
   return r * 16 + ((((pair >> 2) ^ ((r >> 1) & 3)) << 2) | (pair & 3));
 }
@@ -1250,7 +1265,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   for (int e = 0; e < 2; ++e) oG1[e] = 16 * q + 4 * ((n >> 2) ^ ((2 * e) | (q >> 1))) + (n & 3);
   int oW[4];  // steps 2, 5: rp_at(16w + 4q + i, n)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) oW[i] = rp_at(fcol + i, n);
+  for (int i = 0; i < 4; ++i) oW[i] = kX3 ? tt_at(fcol + i, n) : rp_at(fcol + i, n);
   const float4* w2v = reinterpret_cast<const float4*>(w2ts) + (w * kFT) * MLCG_WAVE + l;
   // step 4 on the split path: A = TT row 16w + n, stream q >> 1, pairs
   // 8 (q & 1) .. + 7 (two float4, the second at offset ^ 4); B = halfx8 of HT
@@ -1467,10 +1482,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const halfx2 S16 = halfx2{(_Float16)S, (_Float16)S};
       inv_t = x3_norm_inv(m0) * inv_S;
       inv_td = x3_norm_inv(m1) * inv_S;
-      // three planes (hi, hi S, lo S) of t sigma; float4 group g of pair n's
-      // row (8 halfs) at g ^ (n & 7)
+      // three planes (hi, hi S, lo S) of t sigma; 16-byte chunk g of pair n's
+      // row (8 halfs) at g ^ tb_swz(n)
       _Float16* TBh = reinterpret_cast<_Float16*>(TB);
-      const int o = n * kF + 8 * ((2 * w + (q >> 1)) ^ (n & 7)) + 4 * (q & 1);
+      const int o = n * kF + 8 * ((2 * w + (q >> 1)) ^ tb_swz(n)) + 4 * (q & 1);
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const float sg = st ? sg1 : sg0;
@@ -1514,7 +1529,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       for (int sb = 0; sb < 4; ++sb) {
         const int oa = (w * 4 + sb) * MLCG_WAVE + l;
         const halfx8 ah = w2hv[oa], al = w2hv[kF * kF / 8 + oa];
-        const int ob = (n * kF + 8 * ((4 * sb + q) ^ (n & 7))) / 8;
+        const int ob = (n * kF + 8 * ((4 * sb + q) ^ tb_swz(n))) / 8;
         constexpr int kP = 16 * kF / 8;  // halfx8 per (plane, stream)
         // planes of t: (hi, hi S, lo S) at (0, 2, 4) kP, of t' at (1, 3, 5) kP;
         // S sigma A t ~ hi_A (hi_t S) + hi_A (lo_t S) + (lo_A S) hi_t
@@ -1584,10 +1599,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         rw = rn;
         trun = tmax_tile;
       }
-      const int oA4 = (q >> 1) * kF * 16 + rp_at(16 * w + n, 8 * (q & 1));
+      const int oA4 = (q >> 1) * kF * 16;
       const int oB4 = (q >> 1) * 2 * kF + 2 * (n ^ (n >> 2)) + (q & 1);
-      const float4 x0 = *reinterpret_cast<const float4*>(TT + oA4);
-      const float4 x1 = *reinterpret_cast<const float4*>(TT + (oA4 ^ 4));
+      const float4 x0 = *reinterpret_cast<const float4*>(TT + oA4 + tt_at(16 * w + n, 8 * (q & 1)));
+      const float4 x1 =
+          *reinterpret_cast<const float4*>(TT + oA4 + tt_at(16 * w + n, 8 * (q & 1) + 4));
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       halfx8 ah, ahs, al;
 #pragma unroll
@@ -1655,9 +1671,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         ra = rn;
         arun = amax_tile;
       }
-      const int oA6 = (q >> 1) * kF * 16 + rp_at(16 * w + n, 8 * (q & 1));
-      const float4 x0 = *reinterpret_cast<const float4*>(AT + oA6);
-      const float4 x1 = *reinterpret_cast<const float4*>(AT + (oA6 ^ 4));
+      const int oA6 = (q >> 1) * kF * 16;
+      const float4 x0 = *reinterpret_cast<const float4*>(AT + oA6 + tt_at(16 * w + n, 8 * (q & 1)));
+      const float4 x1 =
+          *reinterpret_cast<const float4*>(AT + oA6 + tt_at(16 * w + n, 8 * (q & 1) + 4));
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       halfx8 ah, ahs, al;
 #pragma unroll
