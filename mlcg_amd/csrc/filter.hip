@@ -413,7 +413,8 @@ __global__ __launch_bounds__(kThreads) void filter_fwd_f32_kernel(
 // supplies features 16(2s + j/4) + 4q + j%4 -- exactly the accumulator
 // values it owns after the first product.
 //   w1h[((t*KS32 + s)*64 + l)*8 + j] = W1[16t + l%16][32s + 8q + j]
-//   w2h[((t*4 + s)*64 + l)*8 + j]    = W2[16t + l%16][16(2s + j/4) + 4q + j%4]
+//   w2h[((t*4 + s)*64 + l)*8 + j]    = W2[f(t, l%16)][16(2s + j/4) + 4q + j%4]
+// with the output-row permutation f(t, m) = 32(t/2) + 8(m/4) + 4(t%2) + m%4.
 __device__ void stage_f16(_Float16* w1h, _Float16* w2h, const float* __restrict__ W1,
                           const float* __restrict__ W2, int K, int KS32) {
   const int n1 = kFT * KS32 * MLCG_WAVE * 8;
@@ -432,7 +433,12 @@ __device__ void stage_f16(_Float16* w1h, _Float16* w2h, const float* __restrict_
     const int ts = x >> 9;
     const int s = ts % (kFT / 2), t = ts / (kFT / 2);
     const int c = 16 * (2 * s + (j >> 2)) + 4 * (l >> 4) + (j & 3);
-    w2h[x] = (_Float16)W2[(16 * t + (l & 15)) * kF + c];
+    // A row m of output tile t is output feature 32 (t / 2) + 8 (m / 4) +
+    // 4 (t % 2) + m % 4, so that after tiles 2u and 2u + 1 lane (n, q) holds
+    // the eight consecutive features 32 u + 8 q .. + 7 of its pair
+    const int m = l & 15;
+    const int f = 32 * (t >> 1) + 8 * (m >> 2) + 4 * (t & 1) + (m & 3);
+    w2h[x] = (_Float16)W2[f * kF + c];
   }
 }
 
@@ -447,7 +453,9 @@ __device__ __forceinline__ float tanh_f16path(float x) {
 
 // 8 waves per workgroup and two workgroups per CU: one wave per 16-pair
 // tile, feature tile at a time (as filter_fwd_x3_kernel), so only two
-// accumulators are live next to the fp16 operands.
+// accumulators are live next to the fp16 operands.  The second linear's
+// output rows are permuted at staging (stage_f16) so that each lane ends up
+// with eight consecutive features of its pair and stores them as 16 bytes.
 #ifndef MLCG_F16_WAVES
 #define MLCG_F16_WAVES 8
 #endif
@@ -470,8 +478,6 @@ __global__ __launch_bounds__(kThreads16, kWaves16 * MLCG_F16_GROUPS_PER_CU / 4) 
   float* b1s = reinterpret_cast<float*>(w2h + kFT * (kFT / 2) * MLCG_WAVE * 8);
   float* bc = b1s + kF;
   float* bw = bc + kMaxK;
-  // per-wave output staging buffer, 1024 halfs
-  _Float16* obuf = reinterpret_cast<_Float16*>(bw + kMaxK) + (threadIdx.x / MLCG_WAVE) * 1024;
   stage_f16(w1h, w2h, W1, W2, rp.K, KS32);
   for (int x = threadIdx.x; x < kF; x += blockDim.x) b1s[x] = b1[x];
   stage_basis(bc, bw, rp);  // zeros past K: finite basis values that meet zero weights
@@ -559,20 +565,14 @@ __global__ __launch_bounds__(kThreads16, kWaves16 * MLCG_F16_GROUPS_PER_CU / 4) 
         hd8[t >> 1][4 * (t & 1) + i] = (_Float16)(d1 * ad[i]);
       }
     }
-    // Output in two halves of the features: W then W' of the 16 pairs go
-    // through the wave's own 2 KB LDS buffer ([16 pairs][64 halfs], 16-byte
-    // chunk c of row n stored at c ^ (n & 7)), so that every global store
-    // writes 8 whole 128-byte row halves.  Only this wave touches its buffer
-    // and a wave's LDS operations complete in issue order, so the compiler
-    // barriers (which keep the accesses in program order) are the only
-    // synchronisation needed.
-    const int64_t row0 = tile * 16;
+    __half* wr = Wout + p * kF + 8 * q;
+    __half* wdr = Wdout + p * kF + 8 * q;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      halfx4 ow[4], owd[4];
+    for (int u = 0; u < kFT / 2; ++u) {
+      halfx8 o, od;
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int t = 4 * hf + tt;
+      for (int v = 0; v < 2; ++v) {
+        const int t = 2 * u + v;
         floatx4 w = {0.f, 0.f, 0.f, 0.f}, wd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < kFT / 2; ++s) {
@@ -582,28 +582,13 @@ __global__ __launch_bounds__(kThreads16, kWaves16 * MLCG_F16_GROUPS_PER_CU / 4) 
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          ow[tt][i] = (_Float16)(w[i] * cc);
-          owd[tt][i] = (_Float16)(wd[i] * cc + w[i] * dcc);
+          o[4 * v + i] = (_Float16)(w[i] * cc);
+          od[4 * v + i] = (_Float16)(wd[i] * cc + w[i] * dcc);
         }
       }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const int c = 2 * tt + (q >> 1);
-          *reinterpret_cast<halfx4*>(obuf + (l & 15) * 64 + ((c ^ (l & 7)) << 3) + 4 * (q & 1)) =
-              m ? owd[tt] : ow[tt];
-        }
-        asm volatile("" ::: "memory");
-        __half* dst = m ? Wdout : Wout;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int r = 8 * i + (l >> 3), c = l & 7;
-          const halfx8 v = *reinterpret_cast<const halfx8*>(obuf + r * 64 + ((c ^ (r & 7)) << 3));
-          if (row0 + r < np)
-            *reinterpret_cast<halfx8*>(dst + (row0 + r) * kF + 64 * hf + 8 * c) = v;
-        }
+      if (valid) {
+        *reinterpret_cast<halfx8*>(wr + 32 * u) = o;
+        *reinterpret_cast<halfx8*>(wdr + 32 * u) = od;
       }
     }
     if (valid && dist_out && q == 0) dist_out[p] = d;
@@ -1920,7 +1905,7 @@ extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t
     const int KS32 = num_rbf <= 64 ? 2 : 4;
     const size_t lds =
         sizeof(_Float16) * (kFT * KS32 * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
-        sizeof(float) * (kF + 2 * kMaxK) + sizeof(_Float16) * 1024 * kWaves16;
+        sizeof(float) * (kF + 2 * kMaxK);
     allow_lds_once();
     const unsigned groups16 =
         mlcg_persistent_groups(mlcg_div_up(max_pairs, 16 * kWaves16), MLCG_F16_GROUPS_PER_CU);

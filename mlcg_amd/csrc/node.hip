@@ -36,7 +36,11 @@ constexpr int kFT = kF / 16;
 constexpr int kTmmWaves = 8;
 constexpr int kTmmThreads = kTmmWaves * MLCG_WAVE;
 constexpr int kTmmRows = 16;                     // rows per staged chunk
-constexpr int kTRow = kF + 4;                    // padded LDS row
+constexpr int kTRow = kF + 4;                    // padded LDS row (node GEMM epilogue)
+// node_tmm's staged rows: a stride of 16 (mod 32) floats puts the two lane
+// halves of a scalar read (rows 4 kk + q, q = 0, 1 in lanes 0-31) on disjoint
+// banks of the 32 that a 4-byte LDS access sees
+constexpr int kTmmRow = kF + 16;
 constexpr int kTmmMaxGroups = 256;               // one workgroup per CU
 constexpr int kTmmPer = kTmmRows * kF / 4 / kTmmThreads;  // float4 per thread per matrix
 constexpr int kTmmPart = kF * kF + kF;           // partial: out [128, 128] + column sums
@@ -74,7 +78,7 @@ __device__ __forceinline__ void tmm_store(float* buf, const TmmChunk& ch, bool t
 #pragma unroll
     for (int k = 0; k < kTmmPer; ++k) {
       const int c = threadIdx.x + k * kTmmThreads;
-      *reinterpret_cast<float4*>(buf + m * kTmmRows * kTRow + (c / (kF / 4)) * kTRow +
+      *reinterpret_cast<float4*>(buf + m * kTmmRows * kTmmRow + (c / (kF / 4)) * kTmmRow +
                                  4 * (c % (kF / 4))) = ch.v[m][k];
     }
   }
@@ -86,10 +90,10 @@ __device__ __forceinline__ void tmm_accumulate(const float* la, const float* lb,
                                                int n, floatx4* acc) {
 #pragma unroll
   for (int kk = 0; kk < kTmmRows / 4; ++kk) {
-    const float av = la[(4 * kk + q) * kTRow + 16 * w + n];
+    const float av = la[(4 * kk + q) * kTmmRow + 16 * w + n];
     float bv[kFT];
 #pragma unroll
-    for (int u = 0; u < kFT; ++u) bv[u] = lb[(4 * kk + q) * kTRow + 16 * u + n];
+    for (int u = 0; u < kFT; ++u) bv[u] = lb[(4 * kk + q) * kTmmRow + 16 * u + n];
 #pragma unroll
     for (int u = 0; u < kFT; ++u)
       acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc[u], 0, 0, 0);
@@ -103,7 +107,7 @@ __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     const float* __restrict__ a1, const float* __restrict__ b1,
     const float* __restrict__ a2, const float* __restrict__ b2, int64_t rows,
     int want_colsum, float* __restrict__ partial) {
-  __shared__ float lds[2][4 * kTmmRows * kTRow];
+  __shared__ float lds[2][4 * kTmmRows * kTmmRow];
   __shared__ float4 csum[kTmmThreads];
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
@@ -133,8 +137,9 @@ __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     __syncthreads();
     if (r0 + kTmmRows < r_end) tmm_load(ch, a1, b1, a2, b2, r0 + kTmmRows, r_end);
     const float* base = lds[buf];
-    tmm_accumulate(base, base + kTmmRows * kTRow, w, q, n, acc);
-    if (two) tmm_accumulate(base + 2 * kTmmRows * kTRow, base + 3 * kTmmRows * kTRow, w, q, n, acc);
+    tmm_accumulate(base, base + kTmmRows * kTmmRow, w, q, n, acc);
+    if (two)
+      tmm_accumulate(base + 2 * kTmmRows * kTmmRow, base + 3 * kTmmRows * kTmmRow, w, q, n, acc);
     buf ^= 1;
   }
   float* o = partial + (int64_t)blockIdx.x * kTmmPart;
