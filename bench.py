@@ -67,6 +67,8 @@ def parse_args(argv=None):
     p.add_argument("--no-radius", action="store_true", help="skip the config-3 radius leg")
     p.add_argument("--no-fp16", action="store_true", help="skip the config-4 fp16 leg")
     p.add_argument("--no-md", action="store_true", help="skip the config-5 MD leg")
+    p.add_argument("--gather-probe", action="store_true",
+                   help="run the gather access-pattern probe (cold caches)")
     p.add_argument("--no-capture", action="store_true",
                    help="skip the captured (HIP graph) config-2 step")
     p.add_argument("--md-steps", type=int, default=200, help="MD steps of the config-5 leg")
@@ -373,6 +375,93 @@ def captured_leg(args, E):
             "note": "same step as the headline (radius graph, energy, forces, double backward, "
                     "AdamW), captured once as a HIP graph and replayed; the headline value is "
                     "the eager step"}
+
+
+def gather_ceiling_leg(reps=10):
+    """What the CFConv gather kernel (mlcg_cfconv_gather: one wave per
+    receiver row, each half-wave reading one 512-byte filter row and one node
+    row per edge as float4 lanes) reaches on synthetic CSR graphs whose
+    access pattern is controlled, all with the caches flushed (a 1 GiB read)
+    before every timed launch, beside torch's streaming reads of the same
+    filter bytes:
+      config2     the config-2 radius graph (each pair's filter row read from
+                  both of its rows, node rows of the frame); also after a
+                  1 GiB write (dirty caches, as in the training step)
+      seq_unique  24 edges per row, every edge its own filter row, rows in
+                  address order, node row = the receiver's own (cached)
+      rand_unique the same with the filter rows in a random order
+    Bytes are the algorithmic ones (filter rows read once, node rows once,
+    output once)."""
+    import torch
+
+    from mlcg_amd import ops, synthetic
+
+    dev = torch.device("cuda:0")
+    F = 128
+    flush = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    flush.fill_(1.0)
+    torch.cuda.synchronize()
+
+    def timed(fn, dirty=False):
+        ts = []
+        for _ in range(reps):
+            # a 1 GiB read evicts the caches and leaves them clean; a 1 GiB
+            # write (dirty=True) leaves them full of dirty lines whose write-back
+            # competes with the timed reads -- the state after the filter
+            # forward, which writes W and W' just before the gathers
+            if dirty:
+                flush.fill_(1.0)
+            else:
+                flush.sum()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(ts)
+
+    out = {}
+    b = synthetic.config2(n_frames=512)
+    pos = torch.from_numpy(b.pos).to(dev)
+    g = ops.radius_graph(pos, 20.0, torch.from_numpy(b.batch).to(dev), max_num_neighbors=1000,
+                         with_pairs=True)
+    N, P, E = g.num_nodes, g.num_pairs, g.num_edges
+    y = torch.randn(N, F, device=dev, generator=gen)
+    W = torch.randn(g.pair_capacity, F, device=dev, generator=gen)
+    byt = 4 * F * (P + 2 * N) + 4 * (N + 1) + 8 * E
+    for dirty in (False, True):
+        t = timed(lambda: ops.cfconv_gather(y, W, g), dirty)
+        out["config2" + ("_dirty_caches" if dirty else "")] = {
+            "us": round(t * 1e6, 2), "TB_per_s": round(byt / t / 1e12, 3), "bytes": byt,
+            "edges": E}
+    deg = 24
+    Eu = N * deg
+    rowptr = torch.arange(0, Eu + 1, deg, dtype=torch.int32, device=dev)
+    col = torch.arange(N, dtype=torch.int32, device=dev).repeat_interleave(deg)
+    Wu = torch.randn(Eu, F, device=dev, generator=gen)
+    for name, e2p in (("seq_unique", torch.arange(Eu, dtype=torch.int32, device=dev)),
+                      ("rand_unique", torch.randperm(Eu, generator=gen, device=dev)
+                       .to(torch.int32))):
+        gu = ops.PairGraph(edge_index=None, rowptr=rowptr, col=col, pair_ij=None, pairptr=None,
+                           eid2pair=e2p, frame_ptr=None, num_nodes=N, num_edges=Eu,
+                           num_pairs=Eu)
+        t = timed(lambda: ops.cfconv_gather(y, Wu, gu))
+        byt = 4 * F * (Eu + 2 * N) + 4 * (N + 1) + 8 * Eu
+        out[name] = {"us": round(t * 1e6, 2), "TB_per_s": round(byt / t / 1e12, 3),
+                     "bytes": byt, "edges": Eu}
+    t = timed(lambda: Wu.sum(dtype=torch.float32))
+    out["torch_sum_same_bytes"] = {"us": round(t * 1e6, 2),
+                                   "TB_per_s": round(4 * F * Eu / t / 1e12, 3)}
+    dst = torch.empty_like(Wu)
+    t = timed(lambda: dst.copy_(Wu))
+    out["torch_copy_same_bytes"] = {"us": round(t * 1e6, 2),
+                                    "TB_per_s_read_plus_write": round(8 * F * Eu / t / 1e12, 3)}
+    del flush
+    return out
 
 
 def radius_leg(reps=10):
@@ -767,6 +856,9 @@ def main(argv=None):
     cg = None if args.no_capture else captured_leg(args, g["E"])
     if cg:
         print(f"[bench] captured leg done: {cg['ms_per_step']:.3f} ms/step", flush=True)
+    gc = gather_ceiling_leg() if args.gather_probe else None
+    if gc:
+        print(f"[bench] gather probe done: {gc}", flush=True)
     rg = None if args.no_radius else radius_leg()
     if rg:
         print(f"[bench] radius leg done: {rg['ms']:.3f} ms", flush=True)
@@ -816,6 +908,7 @@ def main(argv=None):
             "note": "same step, filter forward on the fp32 MFMA (MLCG_FILTER_FP32_STRICT) "
                     "instead of split-fp16 products; both meet the element-wise parity bar"},
         "captured_step": cg,
+        "gather_ceiling": gc,
         "roofline": roofline,
         "kernels": g["kernels"],
         "step_kernel_ms": g["step_kernel_ms"],
