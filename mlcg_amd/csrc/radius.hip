@@ -162,8 +162,10 @@ __device__ __forceinline__ void fill_row(
   }
 }
 
-// Work split of the count and fill kernels: a workgroup of kRowWaves waves
-// takes a block of kBlockRows consecutive rows (wave w: rows w, w + 4, ...).
+// Work split of the fill kernel: a workgroup of kRowWaves waves takes a block
+// of kBlockRows consecutive rows, wave w the consecutive rows w R .. w R + R - 1
+// (R = kRowsPerWave), so that each wave writes one contiguous run of the
+// edge list and completes the cache lines its rows share.
 // The nodes of the frames those rows belong to -- a contiguous node range,
 // as frames are -- are staged once in LDS when they fit (kStage nodes), so
 // every distance test reads LDS instead of L2 and the rows' loads are shared;
@@ -197,7 +199,7 @@ __device__ __forceinline__ BlockNodes stage_block(const T* __restrict__ pos,
   return bn;
 }
 
-// The per-row scalars of a wave's rows (row k of wave w: r0 + w + 4 k) are
+// The per-row scalars of a wave's rows (row k of wave w: r0 + w R + k) are
 // loaded once, lane k holding row k's, so that no row waits on a chain of
 // dependent loads (batch -> frame_ptr -> rowptr) before its sweep; the row
 // loop takes them with readlane.  Offsets are below 2^31 (int32 CSR).
@@ -212,7 +214,7 @@ __device__ __forceinline__ RowBounds row_bounds(const BlockNodes& bn,
                                                 const int32_t* __restrict__ pairptr) {
   RowBounds rb{0, 0, 0, 0};
   const int lane = mlcg_lane();
-  const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) + kRowWaves * lane;
+  const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) * kRowsPerWave + lane;
   if (lane < kRowsPerWave && i < bn.r1) {
     const int64_t b = batch[i];
     rb.start = (int)frame_ptr[b];
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
   int32_t* pj = pair_ij ? pair_ij + p_stride : nullptr;
   bool dropped = false;
   for (int k = 0; k < kRowsPerWave; ++k) {
-    const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) + kRowWaves * k;
+    const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) * kRowsPerWave + k;
     if (i >= bn.r1) break;
     const int64_t start = __builtin_amdgcn_readlane(rb.start, k);
     const int64_t end = __builtin_amdgcn_readlane(rb.end, k);
