@@ -64,6 +64,28 @@ class _Prior(torch.nn.Module):
         super().__init__()
         self._graph_key = None
         self._graph: Optional[ops.PriorGraph] = None
+        self._pcache = None
+
+    def _params(self, data) -> torch.Tensor:
+        """param_matrix(data), reused while the interaction list, the atom
+        types and the parameter tables are the same tensors at the same
+        versions: a simulation evaluates the per-interaction lookup once
+        instead of every step (and a captured step holds no lookup kernels).
+        The cache keeps references to the tensors it was built from, so their
+        memory cannot be reused by other tensors while it is valid."""
+        mapping = data.neighbor_list[self.name]["index_mapping"]
+        types = data.atom_types
+        bufs = tuple(self.buffers())
+        if any(b.requires_grad for b in bufs):
+            return self.param_matrix(data)
+        key = (mapping._version, types._version, tuple(b._version for b in bufs),
+               tuple(b.data_ptr() for b in bufs))
+        c = getattr(self, "_pcache", None)
+        if c is not None and c[0] is mapping and c[1] is types and c[2] == key:
+            return c[3]
+        m = self.param_matrix(data).contiguous()
+        self._pcache = (mapping, types, key, m)
+        return m
 
     def data2parameters(self, data) -> Dict[str, torch.Tensor]:
         raise NotImplementedError
@@ -94,7 +116,7 @@ class _Prior(torch.nn.Module):
         require_device(data.pos)
         g = self.prior_graph(data)
         E = _PriorEnergy.apply(data.pos.float(), self.kind, self.n_degs, g,
-                               self.param_matrix(data), self._batch(data))
+                               self._params(data), self._batch(data))
         data.out[self.name] = {ENERGY_KEY: E}
         return data
 
@@ -105,7 +127,7 @@ class _Prior(torch.nn.Module):
         require_device(data.pos)
         g = self.prior_graph(data)
         return ops.prior_energy_forces(self.kind, self.n_degs, data.pos.detach().float(), g,
-                                       self.param_matrix(data), forces=forces)
+                                       self._params(data), forces=forces)
 
     def _types(self, data, order):
         mapping = data.neighbor_list[self.name]["index_mapping"]
