@@ -124,10 +124,17 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
         # the fused step calls it without pair-adjoint outputs: W, Wd, ddot
         # per pair; gagg2, gagg1 in, ybar2 out
         return "hbm", 2 * sw * F * P + 4 * P + 4 * E + 4 * (N + 1) + 3 * 4 * F * N, "byte"
+    # radius graph: positions, batch and frame_ptr in; CSR (rowptr, and
+    # pairptr when the pair structures are built, P > 0) and the int64 edge
+    # list out, with col, the pair list and its edge map when P > 0
+    csr = 4 * (N + 1) * (2 if P else 1)
+    pair_out = 4 * E + 12 * P if P else 0
     if name == "mlcg_radius_count":
         return "hbm", 12 * N + 8 * N + 8 * (B + 1) + 8 * N, "byte"
-    if name == "mlcg_radius_fill":
-        return "hbm", 12 * N + 8 * N + 8 * (B + 1) + 8 * N + 16 * E + 4 * E + 8 * P + 4 * P, "byte"
+    if name == "mlcg_radius_rowptr":
+        return "hbm", 12 * N + 8 * N + 8 * (B + 1) + csr, "byte"
+    if name in ("mlcg_radius_fill", "mlcg_radius_graph"):
+        return "hbm", 12 * N + 8 * N + 8 * (B + 1) + csr + 16 * E + pair_out, "byte"
     if name == "mlcg_pair_forces":
         return "hbm", 12 * N + 8 * P + 8 * E + 4 * (N + 1) + 12 * N, "byte"
     if name == "mlcg_pair_ddot":
@@ -163,7 +170,9 @@ KERNEL_SYMBOL = {
     "mlcg_cfconv_gather_tangent": "gather_tangent_kernel",
     "mlcg_cfconv_gather_rev2": "gather_rev2_kernel",
     "mlcg_radius_count": "radius_count_kernel",
-    "mlcg_radius_fill": "radius_fill_kernel",
+    "mlcg_radius_rowptr": "radius_rows_kernel<0, ...>",
+    "mlcg_radius_fill": "radius_rows_kernel<1, ...>",
+    "mlcg_radius_graph": "radius_rows_kernel<2, ...>",
     "mlcg_pair_forces": "pair_forces_kernel",
     "mlcg_pair_ddot": "pair_ddot_kernel",
     "mlcg_pair_reverse_map": "pair_reverse_kernel",
@@ -465,11 +474,12 @@ def gather_ceiling_leg(reps=10):
 
 
 def radius_leg(reps=10):
-    """Config 3 radius graph, inputs resident in HBM.  Three figures: the
-    kernels' device time (HIP events around count, scan and fill), the
-    exactly-sized call end to end (one host synchronisation to size the
-    output, as the reference's radius.cu:288), and the fixed-capacity call
-    (no synchronisation, the form a captured step uses)."""
+    """Config 3 radius graph, inputs resident in HBM.  Figures: the exactly
+    sized call end to end (sizing pass, one host synchronisation to size the
+    output as the reference's radius.cu:288, write pass), the fixed-capacity
+    call (one launch plus its clearing kernel, no synchronisation: the form a
+    captured step uses), and the device time of each entry point (HIP events
+    around the call); the roofline takes the fixed-capacity form's."""
     import torch
 
     from mlcg_amd import _lib, ops, synthetic
@@ -502,15 +512,20 @@ def radius_leg(reps=10):
     gc = ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, capacity=cap)
     torch.cuda.synchronize()
     assert int(gc.flags.item()) == 0 and int(gc.rowptr[-1].item()) == E
-    names = ("mlcg_radius_count", "mlcg_exclusive_scan2_i32", "mlcg_radius_fill")
-    timer = _lib.LaunchTimer(set(names))
-    _lib.set_timer(timer)
-    for _ in range(reps):
-        ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, capacity=cap)
-    torch.cuda.synchronize()
-    _lib.set_timer(None)
-    summ = timer.summary()
-    dev_ms = sum(summ[k][1] / summ[k][0] for k in names)
+
+    def device_ms(names, **kw):
+        timer = _lib.LaunchTimer(set(names))
+        _lib.set_timer(timer)
+        for _ in range(reps):
+            ops.radius_graph(pos, 15.0, batch, False, 1000, frame_ptr=fptr, **kw)
+        torch.cuda.synchronize()
+        _lib.set_timer(None)
+        summ = timer.summary()
+        return {k: summ[k][1] / summ[k][0] for k in names}
+
+    fused = device_ms(("mlcg_radius_graph",), capacity=cap)
+    exact = device_ms(("mlcg_radius_rowptr", "mlcg_radius_fill"))
+    dev_ms = fused["mlcg_radius_graph"]
     nbytes = 12 * pos.shape[0] + 8 * (nf + 1) + 16 * E
     ach = nbytes / (dev_ms * 1e-3) / 1e9
     return {"workload": "config3: 2048 frames x 100-bead globules, rc 15 A, no loops, "
@@ -518,11 +533,13 @@ def radius_leg(reps=10):
             "E": E, "ms": round(s_exact * 1e3, 4), "edges_per_s": E / s_exact,
             "ms_capacity_form": round(s_cap * 1e3, 4), "edges_per_s_capacity_form": E / s_cap,
             "kernels_device_ms": round(dev_ms, 4),
-            "kernels_avg_us": {k: round(summ[k][1] / summ[k][0] * 1e3, 2) for k in names},
+            "kernels_avg_us": {k: round(v * 1e3, 2) for k, v in {**fused, **exact}.items()},
+            "exact_form_device_ms": round(sum(exact.values()), 4),
             "algorithmic_bytes": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                         "time": "device time of count + scan + fill"}}
+                         "time": "device time of mlcg_radius_graph (clearing kernel + "
+                                 "one-launch sweep, look-back and write)"}}
 
 
 def fp16_leg(reps=5):

@@ -131,6 +131,70 @@ int mlcg_radius_fill(const float* pos, const int64_t* batch,
                      int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                      void* stream);
 
+/* Bytes of the workspace of mlcg_radius_rowptr / mlcg_radius_graph for
+ * n_nodes rows (a ticket counter and one status word per 64-row block); the
+ * calls clear it themselves, on their stream. */
+int64_t mlcg_radius_workspace_bytes(int64_t n_nodes);
+
+/* Sizing pass in one launch (plus a clearing kernel): per-row kept counts
+ * (membership, exclusion and max_num_neighbors rules of mlcg_radius_count)
+ * scanned within 64-row blocks and across blocks by a decoupled look-back,
+ * written as the CSR: rowptr[n_nodes + 1] (edges) and, when non-NULL,
+ * pairptr[n_nodes + 1] (upper edges j > i).  *overflow is cleared, then gets
+ * bit value 1 when a row exceeded max_num_neighbors, 4 for an asymmetric
+ * exclusion, 16 when the totals exceed 2^31 - 1 (offsets saturate) and 8 if a
+ * look-back wait hit its bound (never expected; the output is then invalid).
+ * Replaces the count, block scan and grid scan of radius_kernel
+ * (radius.cu:88-181) up to the host read of the total (radius.cu:288). */
+int mlcg_radius_rowptr(const float* pos, const int64_t* batch,
+                       const int64_t* frame_ptr, int64_t n_nodes, double r,
+                       int loop, int64_t max_num_neighbors,
+                       const int64_t* exclude_pair_xs,
+                       const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                       int32_t* pairptr, void* workspace, int32_t* overflow,
+                       void* stream);
+
+/* mlcg_radius_rowptr for float64 positions (membership as in
+ * mlcg_radius_count_f64, radius.cu:243-250). */
+int mlcg_radius_rowptr_f64(const double* pos, const int64_t* batch,
+                           const int64_t* frame_ptr, int64_t n_nodes, double r,
+                           int loop, int64_t max_num_neighbors,
+                           const int64_t* exclude_pair_xs,
+                           const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                           int32_t* pairptr, void* workspace, int32_t* overflow,
+                           void* stream);
+
+/* The whole radius graph in one launch (plus a clearing kernel), for callers
+ * that give a capacity instead of reading the edge count back: the sweep,
+ * the look-back of mlcg_radius_rowptr and the writes of mlcg_radius_fill,
+ * with each row's distances tested once.  rowptr / pairptr come out clamped
+ * to edge_capacity / pair_capacity, so every consumer stays inside the
+ * buffers; rowptr[n_nodes] is the number of edges written.  *overflow is
+ * cleared, then gets the bits of mlcg_radius_rowptr and 2 when edges or
+ * pairs fell past their capacity.  Pair outputs as in mlcg_radius_fill
+ * (pairptr required with them).  Replaces radius_kernel and compact_kernel
+ * (radius.cu:60-181) with the output sized by the caller. */
+int mlcg_radius_graph(const float* pos, const int64_t* batch,
+                      const int64_t* frame_ptr, int64_t n_nodes, double r,
+                      int loop, int64_t max_num_neighbors,
+                      const int64_t* exclude_pair_xs,
+                      const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                      int32_t* pairptr, int64_t edge_capacity,
+                      int64_t edge_stride, int64_t* edge_index, int32_t* col,
+                      int64_t pair_capacity, int64_t pair_stride,
+                      int32_t* pair_ij, int32_t* eid2pair, void* workspace,
+                      int32_t* overflow, void* stream);
+
+/* mlcg_radius_graph for float64 positions, edge list only. */
+int mlcg_radius_graph_f64(const double* pos, const int64_t* batch,
+                          const int64_t* frame_ptr, int64_t n_nodes, double r,
+                          int loop, int64_t max_num_neighbors,
+                          const int64_t* exclude_pair_xs,
+                          const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                          int64_t edge_capacity, int64_t edge_stride,
+                          int64_t* edge_index, void* workspace,
+                          int32_t* overflow, void* stream);
+
 /* mlcg_radius_fill for float64 positions (membership as in
  * mlcg_radius_count_f64); writes the edge list only (the pair structures of
  * the CFConv pipeline take float32 positions).  Replaces radius.cu:117-145

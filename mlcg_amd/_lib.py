@@ -40,6 +40,14 @@ _SIGNATURES = {
     "mlcg_radius_fill_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
                              _P, _P],
     "mlcg_exclusion_pair_to_ptr": [_P, _I64, _I64, _P, _P],
+    "mlcg_radius_workspace_bytes": [_I64],
+    "mlcg_radius_rowptr": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "mlcg_radius_rowptr_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P,
+                               _P],
+    "mlcg_radius_graph": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _I64, _I64, _P,
+                          _P, _I64, _I64, _P, _P, _P, _P, _P],
+    "mlcg_radius_graph_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
+                              _P, _P, _P],
     "mlcg_scan_workspace_ints": [_I64],
     "mlcg_exclusive_scan2_i32": [_P, _P, _I64, _P, _P, _P, _P],
     "mlcg_exclusive_scan2_i32_noalloc": [_P, _P, _I64, _P, _P, _P],
@@ -89,6 +97,7 @@ _SIGNATURES = {
     "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
+             "mlcg_radius_workspace_bytes": _I64,
              "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,

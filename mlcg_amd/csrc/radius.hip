@@ -32,8 +32,6 @@
 
 namespace {
 
-constexpr int kRowWaves = 4;  // waves per workgroup (256 threads)
-
 // Positions are float32 or float64 (T); the membership test runs in T, as
 // the reference's kernel runs it in its scalar type (radius.cu:243-250).
 template <typename T>
@@ -85,6 +83,27 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// Inclusive scan over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = mlcg_lane();
+#pragma unroll
+  for (int o = 1; o < MLCG_WAVE; o <<= 1) {
+    int t = __shfl_up(v, o, MLCG_WAVE);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t v) {
+  const int lane = mlcg_lane();
+#pragma unroll
+  for (int o = 1; o < MLCG_WAVE; o <<= 1) {
+    int64_t t = __shfl_up(v, o, MLCG_WAVE);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
 __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
                                  int64_t n_frames, int64_t* __restrict__ ptr) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -101,129 +120,7 @@ __global__ void frame_ptr_kernel(const int64_t* __restrict__ batch, int64_t n,
     for (int64_t k = b + 1; k <= n_frames; ++k) ptr[k] = n;
 }
 
-// Fill sweep over row i: writes every kept neighbour from the lane that holds
-// it (ranks by mbcnt over the hit ballot), with kPairs also the pair list and
-// its edge map for the upper neighbours.  Node and edge indices are int32
-// (the CSR is int32; the host entry points reject larger inputs).  Returns
-// nothing; `dropped` is set when an edge or pair falls past its capacity.
-template <bool kExcl, bool kStaged, bool kPairs, typename T>
-__device__ __forceinline__ void fill_row(
-    const T* __restrict__ pos, int base, int i, int start, int end, T r2, int loop,
-    int max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
-    int64_t* __restrict__ ei0, int64_t* __restrict__ ei1, int32_t* __restrict__ col,
-    int e_base, int e_cap, int32_t* __restrict__ pi, int32_t* __restrict__ pj,
-    int32_t* __restrict__ eid2pair, int p_base, int p_cap, bool& dropped) {
-  const int lane = mlcg_lane();
-  const Vec3T<T> a = load_pos(pos, kStaged ? i - base : i);
-  int kept = 0, ukept = 0;
-  int64_t x_lo = 0, x_hi = 0;
-  if (kExcl) {
-    x_lo = eptr[i];
-    x_hi = eptr[i + 1];
-  }
-  for (int j0 = start; j0 < end && kept < max_nn; j0 += MLCG_WAVE) {
-    const int j = j0 + lane;
-    bool hit = false;
-    if (j < end) {
-      const T d2 = sqdist_exact(a, load_pos(pos, kStaged ? j - base : j));
-      hit = (d2 < r2) && (loop || j != i);
-      if (kExcl && hit) hit = !in_sorted(exs, x_lo, x_hi, (int64_t)j);
-    }
-    const uint64_t m = __ballot(hit);
-    if (m == 0) continue;
-    const int rank = lanes_below(m);
-    const bool keep = hit && (kept + rank < max_nn);
-    const int e = e_base + kept + rank;
-    if (keep) {
-      if (e < e_cap) {
-        ei0[e] = i;
-        ei1[e] = j;
-        if (kPairs) col[e] = j;
-      } else {
-        dropped = true;
-      }
-    }
-    if (kPairs) {
-      const bool upper = keep && (j > i);
-      const uint64_t um = __ballot(upper);
-      if (upper && e < e_cap) {
-        const int p = p_base + ukept + lanes_below(um);
-        if (p < p_cap) {
-          pi[p] = i;
-          pj[p] = j;
-          eid2pair[e] = p;
-        } else {
-          dropped = true;
-        }
-      }
-      ukept += __popcll(um);
-    }
-    kept += __popcll(m);
-  }
-}
-
-// Work split of the fill kernel: a workgroup of kRowWaves waves takes a block
-// of kBlockRows consecutive rows, wave w the consecutive rows w R .. w R + R - 1
-// (R = kRowsPerWave), so that each wave writes one contiguous run of the
-// edge list and completes the cache lines its rows share.
-// The nodes of the frames those rows belong to -- a contiguous node range,
-// as frames are -- are staged once in LDS when they fit (kStage nodes), so
-// every distance test reads LDS instead of L2 and the rows' loads are shared;
-// a block whose frames are larger reads positions from global memory.
-constexpr int kBlockRows = 64;
-constexpr int kStage = 2048;  // nodes staged per workgroup (24 KiB of LDS)
-
-struct BlockNodes {
-  int64_t r0, r1;      // rows of the block
-  int64_t c_lo, c_hi;  // nodes of its frames
-  bool staged;
-};
-
-// Stages the block's nodes (every thread must call; one barrier when staged).
-template <typename T>
-__device__ __forceinline__ BlockNodes stage_block(const T* __restrict__ pos,
-                                                  const int64_t* __restrict__ batch,
-                                                  const int64_t* __restrict__ frame_ptr,
-                                                  int64_t n, T* sp) {
-  BlockNodes bn;
-  bn.r0 = (int64_t)blockIdx.x * kBlockRows;
-  bn.r1 = bn.r0 + kBlockRows < n ? bn.r0 + kBlockRows : n;
-  bn.c_lo = frame_ptr[batch[bn.r0]];
-  bn.c_hi = frame_ptr[batch[bn.r1 - 1] + 1];
-  bn.staged = bn.c_hi >= bn.c_lo && bn.c_hi - bn.c_lo <= kStage;
-  if (bn.staged) {
-    const int64_t cnt = 3 * (bn.c_hi - bn.c_lo);
-    for (int64_t t = threadIdx.x; t < cnt; t += blockDim.x) sp[t] = pos[3 * bn.c_lo + t];
-    __syncthreads();
-  }
-  return bn;
-}
-
-// The per-row scalars of a wave's rows (row k of wave w: r0 + w R + k) are
-// loaded once, lane k holding row k's, so that no row waits on a chain of
-// dependent loads (batch -> frame_ptr -> rowptr) before its sweep; the row
-// loop takes them with readlane.  Offsets are below 2^31 (int32 CSR).
-constexpr int kRowsPerWave = kBlockRows / kRowWaves;
-struct RowBounds {
-  int start, end, e_base, p_base;
-};
-__device__ __forceinline__ RowBounds row_bounds(const BlockNodes& bn,
-                                                const int64_t* __restrict__ batch,
-                                                const int64_t* __restrict__ frame_ptr,
-                                                const int32_t* __restrict__ rowptr,
-                                                const int32_t* __restrict__ pairptr) {
-  RowBounds rb{0, 0, 0, 0};
-  const int lane = mlcg_lane();
-  const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) * kRowsPerWave + lane;
-  if (lane < kRowsPerWave && i < bn.r1) {
-    const int64_t b = batch[i];
-    rb.start = (int)frame_ptr[b];
-    rb.end = (int)frame_ptr[b + 1];
-    if (rowptr) rb.e_base = rowptr[i];
-    if (pairptr) rb.p_base = pairptr[i];
-  }
-  return rb;
-}
+constexpr int kStage = 2048;  // nodes staged per workgroup by the count kernel (24 KiB)
 
 // Pass 1 runs `parts` threads per row (a power of two up to 64, chosen by the
 // host so that the launch fills the chip): a counting sweep needs no ballots
@@ -304,42 +201,678 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
   if (kExcl && asym && overflow) atomicOr(overflow, 4);
 }
 
-template <bool kExcl, bool kPairs, typename T>
-__global__ __launch_bounds__(kRowWaves * MLCG_WAVE) void radius_fill_kernel(
+// ---------------------------------------------------------------------------
+// Row-block kernel of the radius graph.  A workgroup of kRBWaves waves takes a
+// block of kRB consecutive rows, wave w the rows w R .. w R + R - 1
+// (R = kRowsPerWave), so that each wave writes one contiguous run of the edge
+// list.  The nodes of the block's frames -- a contiguous node range, as frames
+// are -- are staged in LDS as 4-component records when they fit
+// (StageNodes<T>); a block whose frames are larger reads positions from
+// global memory.
+//
+// The kernel is instruction-bound, not memory-bound (a 64-wide VALU or SALU
+// instruction retires at about one per cycle per CU), so the sweep is built to
+// spend few instructions per 64 candidates:
+// - a wave takes its rows kGroup at a time; when the kGroup rows share one
+//   staged frame (the common case) every lane loads its candidate once
+//   (ds_read_b128) and tests it against the kGroup centres; the compare writes
+//   the row's hit mask straight into scalar registers, cut to the frame by one
+//   scalar mask on the last chunk;
+// - the self pair (j = i) is taken out once per row, not per candidate: the
+//   count from the same distance test (d(i, i) < r^2 is what the sweep saw),
+//   the mask bit when the write pass reads the row's masks;
+// - the masks of a row's first kMaskWords chunks go to LDS (one write per
+//   chunk for the kGroup rows); rows with pair exclusions and groups that
+//   straddle frames or are not staged take a general path that tests every
+//   condition per lane, and rows longer than kMaskWords chunks are tested
+//   again in the write pass.
+// Rows keep their lowest-index neighbours when max_num_neighbors binds
+// (radius.cu:125-141): kept = min(hits, max_nn), and the kept upper neighbours
+// (j > i) are what remains after the lower ones and the self loop.
+//
+// Modes:
+//   kModeRowptr  kept counts scanned within the block (one wave) and across
+//                blocks (decoupled look-back); rowptr / pairptr written (the
+//                sizing pass of the exactly-sized graph);
+//   kModeFill    rowptr / pairptr given; a write pass emits every kept
+//                neighbour from the lane that holds it (rank by mbcnt over the
+//                row's mask; rows past 64 chunks are tested again);
+//   kModeFused   both in one launch (the fixed-capacity form).
+// Look-back: each block publishes its totals (edges, pairs) in a status word
+// of the workspace, first as an aggregate, then as an inclusive prefix; a
+// block sums the aggregates of its predecessors back to the first inclusive
+// prefix, reading kLookLanes x 64 predecessors per round.  Block indices come
+// from a ticket counter, so a block only waits for blocks that are already
+// running, and every wait is bounded (kSpinLimit polls): a block that gives
+// up sets overflow bit 8 and carries on, so the kernel always finishes.  The
+// workspace is cleared by radius_ws_init on the same stream before every such
+// launch.
+constexpr int kRBWaves = 4;
+enum { kModeRowptr = 0, kModeFill = 1, kModeFused = 2 };
+// Rows per wave: 64 (one per lane) in the look-back modes, where a larger
+// block amortises the staging, the block scan and the look-back over more
+// rows; 16 in kModeFill, which has no look-back and gains more from four
+// times as many waves hiding each other's latencies.
+template <int kMode>
+struct RowsPerWave {
+  static constexpr int value = kMode == kModeFill ? 16 : 64;
+};
+constexpr int kRBScan = kRBWaves * 64;  // rows per block of the look-back modes
+constexpr int kGroup = 4;                      // rows swept together
+constexpr int kMaskWords = 8;                  // mask words kept per row (512 candidates)
+constexpr int kLookLanes = 4;                  // statuses per lane and look-back round
+constexpr int kSpinLimit = 1 << 14;
+enum {
+  kOvTruncated = 1,   // a row had more than max_num_neighbors neighbours
+  kOvCapacity = 2,    // edges or pairs fell past their capacity
+  kOvAsymmetric = 4,  // (i, j) kept while (j, i) is excluded
+  kOvLookback = 8,    // a look-back wait hit its bound (never expected)
+  kOvInt32 = 16       // more than 2^31 - 1 edges or pairs
+};
+
+// Staged position record (x, y, z, unused), one 16-byte (fp32) or two
+// (fp64) LDS reads.
+template <typename T>
+struct alignas(4 * sizeof(T)) Pos4 {
+  T x, y, z, w;
+};
+// 16 KiB of positions per workgroup (1024 fp32 or 512 fp64 nodes).
+template <typename T>
+struct StageNodes {
+  static constexpr int value = 16384 / (4 * (int)sizeof(T));
+};
+
+template <typename T>
+__device__ __forceinline__ Vec3T<T> load_pos(const Pos4<T>* __restrict__ sp, int64_t n) {
+  const Pos4<T> p = sp[n];
+  return Vec3T<T>{p.x, p.y, p.z};
+}
+
+// Status word: flag (bits 62-63: 0 none, 1 aggregate, 2 inclusive prefix),
+// pairs (bits 31-61), edges (bits 0-30).  Totals saturate at 2^31 - 1.
+constexpr uint64_t kVal31 = 0x7fffffffull;
+constexpr uint64_t kFlagAgg = 1ull << 62;
+constexpr uint64_t kFlagPre = 2ull << 62;
+
+__device__ __forceinline__ uint64_t pack_status(uint64_t flag, uint64_t e, uint64_t p) {
+  return flag | ((p < kVal31 ? p : kVal31) << 31) | (e < kVal31 ? e : kVal31);
+}
+__device__ __forceinline__ uint64_t ld_status(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_status(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, MLCG_WAVE);
+  return v;
+}
+
+// Decoupled look-back of block t (one full wave): publishes the aggregate,
+// sums the predecessors' aggregates back to the first inclusive prefix,
+// publishes the inclusive prefix and returns the exclusive one.  A round reads
+// kLookLanes x 64 statuses, entry o = kLookLanes l + q (lane l, slot q) being
+// block k - o; it waits only while a status before the nearest inclusive
+// prefix is still missing.
+__device__ __forceinline__ void lookback(uint64_t* __restrict__ st, int t, uint64_t agg_e,
+                                         uint64_t agg_p, uint64_t& pre_e, uint64_t& pre_p,
+                                         int& ov) {
+  const int lane = mlcg_lane();
+  pre_e = 0;
+  pre_p = 0;
+  if (t > 0) {
+    if (lane == 0) st_status(st + t, pack_status(kFlagAgg, agg_e, agg_p));
+    for (int k = t - 1;; k -= kLookLanes * MLCG_WAVE) {
+      uint64_t w[kLookLanes];
+#pragma unroll
+      for (int q = 0; q < kLookLanes; ++q) {
+        const int idx = k - kLookLanes * lane - q;
+        w[q] = idx >= 0 ? ld_status(st + idx) : kFlagPre;
+      }
+      int first_pre = 0, first_missing = 0;  // in entry order, 1 << 30 when absent
+      for (int spins = 0;; ++spins) {
+        int fp = kLookLanes, fm = kLookLanes;  // first slot of this lane
+#pragma unroll
+        for (int q = kLookLanes - 1; q >= 0; --q) {
+          if ((w[q] >> 62) == 2) fp = q;
+          if ((w[q] >> 62) == 0) fm = q;
+        }
+        const uint64_t pl = __ballot(fp < kLookLanes), ml = __ballot(fm < kLookLanes);
+        const int lp = pl ? __builtin_ctzll(pl) : MLCG_WAVE;
+        const int lm = ml ? __builtin_ctzll(ml) : MLCG_WAVE;
+        first_pre = lp < MLCG_WAVE ? kLookLanes * lp + __builtin_amdgcn_readlane(fp, lp)
+                                   : (1 << 30);
+        first_missing = lm < MLCG_WAVE ? kLookLanes * lm + __builtin_amdgcn_readlane(fm, lm)
+                                       : (1 << 30);
+        if (first_missing > first_pre || (first_missing == (1 << 30))) break;
+        if (spins == kSpinLimit) {  // give up: count what is missing as zero
+          ov |= kOvLookback;
+#pragma unroll
+          for (int q = 0; q < kLookLanes; ++q)
+            if ((w[q] >> 62) == 0) w[q] = kFlagPre;
+          first_missing = 1 << 30;
+          first_pre = lm < MLCG_WAVE ? kLookLanes * lm + __builtin_amdgcn_readlane(fm, lm) : 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int q = 0; q < kLookLanes; ++q) {
+          const int idx = k - kLookLanes * lane - q;
+          if ((w[q] >> 62) == 0) w[q] = ld_status(st + idx);
+        }
+      }
+      // sum the entries up to and including the nearest inclusive prefix
+      uint64_t se = 0, sp = 0;
+#pragma unroll
+      for (int q = 0; q < kLookLanes; ++q) {
+        const bool in = kLookLanes * lane + q <= first_pre;
+        se += in ? (w[q] & kVal31) : 0;
+        sp += in ? ((w[q] >> 31) & kVal31) : 0;
+      }
+      pre_e += wave_sum_u64(se);
+      pre_p += wave_sum_u64(sp);
+      if (first_pre < (1 << 30)) break;
+    }
+  }
+  const uint64_t inc_e = pre_e + agg_e, inc_p = pre_p + agg_p;
+  if (inc_e > kVal31 || inc_p > kVal31) ov |= kOvInt32;
+  if (lane == 0) st_status(st + t, pack_status(kFlagPre, inc_e, inc_p));
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int k) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, k);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), k);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Lanes 0 .. n - 1 (n in 0 .. 64).
+__device__ __forceinline__ uint64_t low_lanes(int n) {
+  return n >= MLCG_WAVE ? ~0ull : (n <= 0 ? 0ull : (1ull << n) - 1);
+}
+
+// Candidate test of lane's j against row i (centre a), every condition per
+// lane: inside the row's frame, within the cutoff, not the self pair unless
+// loop, not excluded.
+template <bool kExcl, typename PosT, typename T>
+__device__ __forceinline__ bool test_candidate(const PosT* __restrict__ P, int base, Vec3T<T> a,
+                                               int i, int j, int end, T r2, int loop,
+                                               const int64_t* __restrict__ exs, int64_t x_lo,
+                                               int64_t x_hi) {
+  const bool valid = j < end;
+  const T d2 = sqdist_exact(a, load_pos(P, (valid ? j : i) - base));
+  bool hit = valid && (d2 < r2) && (loop || j != i);
+  if (kExcl && hit) hit = !in_sorted(exs, x_lo, x_hi, (int64_t)j);
+  return hit;
+}
+
+// Per-row results of the sweep of a group.
+struct GroupCounts {
+  uint32_t tot[kGroup];  // kept-eligible hits (self excluded unless loop)
+  uint32_t low[kGroup];  // hits with j < i
+  uint32_t slf[kGroup];  // the self hit (loop only)
+};
+
+// Fast sweep: kGroup rows ii[] of one staged frame [st, en), no exclusions.
+// Lanes past the frame read the sentinel record sp[kStage] (+inf), whose
+// distance never passes the test, so no lane mask is needed.  Masks of the
+// first kMaskWords chunks go to smask_g (row u at u * kMaskWords) when kMasks,
+// the self bit included; the caller takes the self pair out of the counts.
+// kLow accumulates the hits below the diagonal.
+template <bool kMasks, bool kLow, int kStage, typename T>
+__device__ __forceinline__ void sweep_fast(const Pos4<T>* __restrict__ sp, int base,
+                                           const int (&ii)[kGroup], int st, int en, int nch,
+                                           T r2, uint64_t* __restrict__ smask_g,
+                                           GroupCounts& gc) {
+  const int lane = mlcg_lane();
+  Vec3T<T> a[kGroup];
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) a[u] = load_pos(sp, ii[u] - base);
+  const int jend = en - base;
+  int idx = st - base + lane;
+  for (int c = 0; c < nch; ++c, idx += MLCG_WAVE) {
+    const Vec3T<T> p = load_pos(sp, idx < jend ? idx : kStage);
+    uint64_t mv = 0;  // lane u: row u's mask
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const uint64_t m = __ballot(sqdist_exact(a[u], p) < r2);
+      gc.tot[u] += (uint32_t)__popcll(m);
+      if (kLow) gc.low[u] += (uint32_t)__popcll(m & low_lanes(ii[u] - st - MLCG_WAVE * c));
+      if (kMasks && __builtin_amdgcn_inverse_ballot_w64(1ull << u)) mv = m;  // lane u only
+    }
+    if (kMasks && c < kMaskWords && lane < kGroup) smask_g[lane * kMaskWords + c] = mv;
+  }
+}
+
+// General sweep: any kGroup rows (candidates st[u] .. en[u]), every condition
+// tested per lane; counts accumulate in scalars, masks of the first
+// kMaskWords chunks go to smask_g as in sweep_fast.  With kAsym a kept (i, j)
+// whose (j, i) is excluded sets asym.
+template <bool kExcl, bool kMasks, bool kAsym, typename PosT, typename T>
+__device__ __forceinline__ void sweep_general(
+    const PosT* __restrict__ P, int base, const int (&ii)[kGroup], const int (&st)[kGroup],
+    const int (&en)[kGroup], int nch, T r2, int loop, const int64_t* __restrict__ exs,
+    const int64_t* __restrict__ eptr, uint64_t* __restrict__ smask_g, GroupCounts& gc,
+    bool& asym) {
+  const int lane = mlcg_lane();
+  Vec3T<T> a[kGroup];
+  int64_t x_lo[kGroup], x_hi[kGroup];
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {
+    a[u] = load_pos(P, ii[u] - base);
+    x_lo[u] = x_hi[u] = 0;
+    if (kExcl) {
+      x_lo[u] = eptr[ii[u]];
+      x_hi[u] = eptr[ii[u] + 1];
+    }
+  }
+  for (int c = 0; c < nch; ++c) {
+    uint64_t mv = 0;  // lane u: row u's mask
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int jb = st[u] + MLCG_WAVE * c;
+      const int j = jb + lane;
+      const bool hit =
+          test_candidate<kExcl>(P, base, a[u], ii[u], j, en[u], r2, loop, exs, x_lo[u], x_hi[u]);
+      if (kAsym && hit && in_sorted(exs, eptr[j], eptr[j + 1], (int64_t)ii[u])) asym = true;
+      const uint64_t m = __ballot(hit);
+      if (kMasks) mv = lane == u ? m : mv;
+      gc.tot[u] += (uint32_t)__popcll(m);
+      const int d = ii[u] - jb;  // lanes below d hold j < i
+      gc.low[u] += (uint32_t)__popcll(m & low_lanes(d));
+      if (d >= 0 && d < MLCG_WAVE) gc.slf[u] += (uint32_t)((m >> d) & 1);
+    }
+    if (kMasks && c < kMaskWords && lane < kGroup) smask_g[lane * kMaskWords + c] = mv;
+  }
+}
+
+// Write pass of a row whose kept neighbours all fit (no truncation, inside
+// the capacities): mask w holds chunk c in lane c, self bit already cleared;
+// every hit lane stores at e_base + (hits before it), and with kPairs the upper
+// ones (j > i) also to the pair list.  No per-lane tests beyond the mask bit.
+template <bool kPairs>
+__device__ __forceinline__ void emit_row_fast(uint64_t w, int nch, int st, int i,
+                                              int64_t e_base, int64_t p_base,
+                                              int64_t* __restrict__ ei0,
+                                              int64_t* __restrict__ ei1,
+                                              int32_t* __restrict__ col,
+                                              int32_t* __restrict__ pi,
+                                              int32_t* __restrict__ pj,
+                                              int32_t* __restrict__ eid2pair) {
+  const int lane = mlcg_lane();
+  const int64_t vi = (int64_t)(uint32_t)i;
+  // the row's scalar bases; chunk c stores at 32-bit offsets from them
+  char* const b0 = (char*)(ei0 + e_base);
+  char* const b1 = (char*)(ei1 + e_base);
+  char* const bc = kPairs ? (char*)(col + e_base) : nullptr;
+  char* const be = kPairs ? (char*)(eid2pair + e_base) : nullptr;
+  char* const bpi = kPairs ? (char*)(pi + p_base) : nullptr;
+  char* const bpj = kPairs ? (char*)(pj + p_base) : nullptr;
+  uint32_t e = 0, p = 0;  // edges / pairs of the row written so far
+  for (int c = 0; c < nch; ++c) {
+    const uint64_t m = readlane64(w, c);
+    const int jb = st + MLCG_WAVE * c;
+    const uint64_t um = kPairs ? m & ~low_lanes(i - jb + 1) : 0ull;  // lanes with j > i
+    if (__builtin_amdgcn_inverse_ballot_w64(m)) {  // exec = the lanes of m
+      const uint32_t r = e + (uint32_t)lanes_below(m);
+      const uint32_t j = (uint32_t)(jb + lane);
+      *(int64_t*)(b0 + r * 8u) = vi;
+      *(int64_t*)(b1 + r * 8u) = (int64_t)j;
+      if (kPairs) {
+        *(int32_t*)(bc + r * 4u) = (int32_t)j;
+        if (__builtin_amdgcn_inverse_ballot_w64(um)) {
+          const uint32_t rp = p + (uint32_t)lanes_below(um);
+          *(int32_t*)(bpi + rp * 4u) = i;
+          *(int32_t*)(bpj + rp * 4u) = (int32_t)j;
+          *(int32_t*)(be + r * 4u) = (int32_t)(p_base + rp);
+        }
+      }
+    }
+    e += (uint32_t)__popcll(m);
+    if (kPairs) p += (uint32_t)__popcll(um);
+  }
+}
+
+// Write pass of one chunk of row i with every lane tested (rows truncated by
+// max_num_neighbors or running past a capacity): kept neighbours go to edges
+// e_base + kept + rank, with kPairs the upper ones also to pair
+// p_base + ukept + rank among upper; a lane that falls past a capacity sets
+// dropped.
+template <bool kPairs>
+__device__ __forceinline__ void emit_chunk(uint64_t m, int jb, int i, int mnn, int64_t e_base,
+                                           int& kept, int64_t p_base, int& ukept,
+                                           int64_t e_cap, int64_t* __restrict__ ei0,
+                                           int64_t* __restrict__ ei1, int32_t* __restrict__ col,
+                                           int64_t p_cap, int32_t* __restrict__ pi,
+                                           int32_t* __restrict__ pj,
+                                           int32_t* __restrict__ eid2pair, bool& dropped) {
+  const int lane = mlcg_lane();
+  const int j = jb + lane;
+  const bool hit = (m >> lane) & 1;
+  const int rank = lanes_below(m);
+  const bool keep = hit && (kept + rank < mnn);
+  const int64_t e = e_base + kept + rank;
+  if (keep) {
+    if (e >= 0 && e < e_cap) {
+      ei0[e] = i;
+      ei1[e] = j;
+      if (kPairs) col[e] = j;
+    } else {
+      dropped = true;
+    }
+  }
+  if (kPairs) {
+    const bool upper = keep && (j > i);
+    const uint64_t kum = __ballot(upper);
+    if (upper && e >= 0 && e < e_cap) {
+      const int64_t p = p_base + ukept + lanes_below(kum);
+      if (p >= 0 && p < p_cap) {
+        pi[p] = i;
+        pj[p] = j;
+        eid2pair[e] = (int32_t)p;
+      } else {
+        dropped = true;
+      }
+    }
+    ukept += __popcll(kum);
+  }
+  kept += __popcll(m);
+}
+
+template <int kMode, bool kExcl, bool kPairs, typename T>
+__global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     const T* __restrict__ pos, const int64_t* __restrict__ batch,
-    const int64_t* __restrict__ frame_ptr, int64_t n, T r2, int loop,
-    int64_t max_nn, const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
-    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ pairptr, int64_t e_cap,
+    const int64_t* __restrict__ frame_ptr, int n, T r2, int loop, int mnn,
+    const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
+    int32_t* __restrict__ rowptr, int32_t* __restrict__ pairptr, int64_t e_cap,
     int64_t e_stride, int64_t* __restrict__ edge_index, int32_t* __restrict__ col,
     int64_t p_cap, int64_t p_stride, int32_t* __restrict__ pair_ij,
-    int32_t* __restrict__ eid2pair, int32_t* __restrict__ overflow) {
-  __shared__ T sp[3 * kStage];
-  const BlockNodes bn = stage_block(pos, batch, frame_ptr, n, sp);
-  const RowBounds rb = row_bounds(bn, batch, frame_ptr, rowptr, pairptr);
-  int32_t* pi = pair_ij;
-  int32_t* pj = pair_ij ? pair_ij + p_stride : nullptr;
-  bool dropped = false;
-  for (int k = 0; k < kRowsPerWave; ++k) {
-    const int64_t i = bn.r0 + (threadIdx.x / MLCG_WAVE) * kRowsPerWave + k;
-    if (i >= bn.r1) break;
-    const int64_t start = __builtin_amdgcn_readlane(rb.start, k);
-    const int64_t end = __builtin_amdgcn_readlane(rb.end, k);
-    const int64_t e_base = __builtin_amdgcn_readlane(rb.e_base, k);
-    const int64_t p_base = __builtin_amdgcn_readlane(rb.p_base, k);
-    const int mnn = max_nn < (int64_t)INT32_MAX ? (int)max_nn : INT32_MAX;
-    const int ecap = e_cap < (int64_t)INT32_MAX ? (int)e_cap : INT32_MAX;
-    const int pcap = p_cap < (int64_t)INT32_MAX ? (int)p_cap : INT32_MAX;
-    if (bn.staged && start >= bn.c_lo && end <= bn.c_hi)  // wave-uniform
-      fill_row<kExcl, true, kPairs>(sp, (int)bn.c_lo, (int)i, (int)start, (int)end, r2, loop,
-                                    mnn, exs, eptr, edge_index, edge_index + e_stride, col,
-                                    (int)e_base, ecap, pi, pj, eid2pair, (int)p_base, pcap,
-                                    dropped);
-    else
-      fill_row<kExcl, false, kPairs>(pos, 0, (int)i, (int)start, (int)end, r2, loop, mnn, exs,
-                                     eptr, edge_index, edge_index + e_stride, col, (int)e_base,
-                                     ecap, pi, pj, eid2pair, (int)p_base, pcap, dropped);
+    int32_t* __restrict__ eid2pair, uint64_t* __restrict__ ws, int32_t* __restrict__ overflow) {
+  constexpr bool kScan = kMode != kModeFill;
+  constexpr bool kWrite = kMode != kModeRowptr;
+  constexpr int kRowsPerWave = RowsPerWave<kMode>::value;
+  constexpr int kRB = kRBWaves * kRowsPerWave;
+  constexpr bool kMasks = kWrite || kPairs;  // kPairs needs the lower counts from the sweep
+  constexpr bool kLow = kPairs;
+  constexpr int kStage = StageNodes<T>::value;
+  __shared__ Pos4<T> sp[kStage + 1];  // + the sentinel record
+  __shared__ uint64_t smask[kMasks ? kRB * kMaskWords : 1];
+  __shared__ int64_t swt[2 * kRBWaves];  // per-wave totals (edges, pairs), then offsets
+  __shared__ uint64_t spre[2];
+
+  // Blocks take their rows in launch order: a block only waits (look-back)
+  // for blocks with a lower index, which the dispatcher started before it.
+  // The wave index as a scalar (the compiler cannot prove it uniform).
+  const int lane = mlcg_lane();
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / MLCG_WAVE);
+  const int t = blockIdx.x;
+  const int nblocks = (n + kRB - 1) / kRB;
+  const int r0 = t * kRB;
+  const int r1 = r0 + kRB < n ? r0 + kRB : n;
+  // the block's node window (node indices are below 2^31: int32 CSR)
+  const int c_lo = (int)frame_ptr[batch[r0]];
+  const int c_hi = (int)frame_ptr[batch[r1 - 1] + 1];
+  const bool staged = c_hi >= c_lo && c_hi - c_lo <= kStage;  // block-uniform
+  if (staged) {
+    const int cnt = c_hi - c_lo;
+    for (int k = threadIdx.x; k < cnt; k += blockDim.x) {
+      const T* q = pos + 3 * (int64_t)(c_lo + k);
+      sp[k] = Pos4<T>{q[0], q[1], q[2], T(0)};
+    }
+    if (threadIdx.x == 0) {
+      const T inf = __builtin_huge_val();
+      sp[kStage] = Pos4<T>{inf, inf, inf, T(0)};
+    }
   }
-  if (dropped && overflow) atomicOr(overflow, 2);
+  // lane k of wave wv holds the scalars of row rw0 + k
+  const int rw0 = r0 + wv * kRowsPerWave;
+  int rs_start = 0, rs_end = 0, rs_e = 0, rs_p = 0;
+  if (lane < kRowsPerWave && rw0 + lane < r1) {
+    const int64_t b = batch[rw0 + lane];
+    rs_start = (int)frame_ptr[b];
+    rs_end = (int)frame_ptr[b + 1];
+    if (kMode == kModeFill) {
+      rs_e = rowptr[rw0 + lane];
+      if (kPairs) rs_p = pairptr[rw0 + lane];
+    }
+  }
+  if (staged) __syncthreads();
+  const int base = c_lo;
+
+  // the self pair of each row, one row per lane: the sweep's own test of j = i
+  const int my_i = rw0 + lane;
+  const bool my_row = lane < kRowsPerWave && my_i < r1;
+  uint64_t selfm;
+  {
+    bool sh = false;
+    if (my_row) {
+      const Vec3T<T> a = (staged && my_i >= c_lo && my_i < c_hi) ? load_pos(sp, my_i - base)
+                                                                 : load_pos(pos, my_i);
+      sh = sqdist_exact(a, a) < r2;
+    }
+    selfm = __ballot(sh);
+  }
+
+  // sweep: masks of row k at smask_w[k * kMaskWords]; per-row counts to lane k
+  uint64_t* smask_w = smask + (kMasks ? wv * kRowsPerWave * kMaskWords : 0);
+  int my_tot = 0, my_low = 0, my_slf = 0;
+  uint64_t fastm = 0;  // rows swept by the fast path
+  bool asym = false;
+  for (int g = 0; g < kRowsPerWave && rw0 + g < r1; g += kGroup) {
+    int ii[kGroup], st[kGroup], en[kGroup];
+    const bool full = rw0 + g + kGroup <= r1;
+    const int st0 = __builtin_amdgcn_readlane(rs_start, g);
+    const int en0 = __builtin_amdgcn_readlane(rs_end, g);
+    bool fast = false;
+    if (!kExcl && full) {  // rows of one frame: the first and the last share it
+      const int st3 = __builtin_amdgcn_readlane(rs_start, g + kGroup - 1);
+      const int en3 = __builtin_amdgcn_readlane(rs_end, g + kGroup - 1);
+      fast = staged && st0 == st3 && en0 == en3 && st0 >= c_lo && en0 <= c_hi;
+    }
+    GroupCounts gc;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) gc.tot[u] = gc.low[u] = gc.slf[u] = 0;
+    uint64_t* smask_g = smask_w + g * kMaskWords;
+    if (fast) {  // wave-uniform
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) ii[u] = rw0 + g + u;
+      sweep_fast<kMasks, kLow, kStage>(sp, base, ii, st0, en0,
+                                       (en0 - st0 + MLCG_WAVE - 1) / MLCG_WAVE, r2, smask_g, gc);
+      fastm |= (uint64_t)((1u << kGroup) - 1) << g;
+    } else {
+      int nch = 0;
+      bool local = staged;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        ii[u] = rw0 + g + u;
+        st[u] = __builtin_amdgcn_readlane(rs_start, g + u);
+        en[u] = __builtin_amdgcn_readlane(rs_end, g + u);
+        if (ii[u] >= r1) {  // past the last row: the group's first row again, ignored
+          ii[u] = rw0 + g;
+          st[u] = st0;
+          en[u] = en0;
+        }
+        const int ch = (en[u] - st[u] + MLCG_WAVE - 1) / MLCG_WAVE;
+        nch = ch > nch ? ch : nch;
+        local = local && st[u] >= c_lo && en[u] <= c_hi && ii[u] >= c_lo && ii[u] < c_hi;
+      }
+      if (local)
+        sweep_general<kExcl, kMasks, kExcl && kScan>(sp, base, ii, st, en, nch, r2, loop, exs,
+                                                     eptr, smask_g, gc, asym);
+      else
+        sweep_general<kExcl, kMasks, kExcl && kScan>(pos, 0, ii, st, en, nch, r2, loop, exs,
+                                                     eptr, smask_g, gc, asym);
+    }
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const bool mine = lane == g + u;
+      my_tot = mine ? (int)gc.tot[u] : my_tot;
+      if (kLow) my_low = mine ? (int)gc.low[u] : my_low;
+      my_slf = mine ? (int)gc.slf[u] : my_slf;
+    }
+  }
+
+  // per-row counts, one row per lane: the fast sweep counted the self pair
+  // (and kept its mask bit); take it out of the count, and out of the mask
+  // unless loop, so that the write pass sees only kept candidates
+  const int my_st = rs_start, my_en = rs_end;
+  const int my_nch = (my_en - my_st + MLCG_WAVE - 1) / MLCG_WAVE;
+  if (my_row && (((selfm & fastm) >> lane) & 1)) {
+    if (loop) {
+      my_slf = 1;
+    } else {
+      my_tot -= 1;
+      if (kMasks && my_nch <= kMaskWords) {
+        const int off = my_i - my_st;
+        uint64_t* wd = smask_w + lane * kMaskWords + (off >> 6);
+        *wd &= ~(1ull << (off & 63));
+      }
+    }
+  }
+  const int my_kept = my_tot < mnn ? my_tot : mnn;
+  const int my_up = my_tot - my_low - my_slf;
+  int my_ukept = 0;
+  if (kPairs) {
+    const int64_t room = (int64_t)mnn - my_low - my_slf;
+    my_ukept = room <= 0 ? 0 : (int)(my_up < room ? my_up : room);
+  }
+  const bool trunc = __ballot(my_row && my_tot > mnn) != 0;
+
+  // offsets: the lane's row within its wave (wave scan), the wave within the
+  // block, the block within the graph (look-back)
+  uint64_t pre_e = 0, pre_p = 0;  // the wave's first edge / pair
+  int64_t my_off_e = 0, my_off_p = 0;
+  if (kScan) {
+    int ov = 0;
+    const int64_t ve = my_row ? my_kept : 0, vp = my_row ? my_ukept : 0;
+    const int64_t ie = wave_incl_scan64(ve), ip = wave_incl_scan64(vp);
+    my_off_e = ie - ve;
+    my_off_p = ip - vp;
+    if (lane == MLCG_WAVE - 1) {
+      swt[wv] = ie;
+      swt[kRBWaves + wv] = ip;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      const int64_t we = lane < kRBWaves ? swt[lane] : 0;
+      const int64_t wp = lane < kRBWaves ? swt[kRBWaves + lane] : 0;
+      const int64_t iwe = wave_incl_scan64(we), iwp = wave_incl_scan64(wp);
+      const uint64_t agg_e = readlane64((uint64_t)iwe, kRBWaves - 1);
+      const uint64_t agg_p = readlane64((uint64_t)iwp, kRBWaves - 1);
+      uint64_t le, lp;
+      lookback(ws + 1, t, agg_e, agg_p, le, lp, ov);
+      if (lane < kRBWaves) {  // every lane read its swt entry before these writes
+        swt[lane] = (int64_t)le + iwe - we;
+        swt[kRBWaves + lane] = (int64_t)lp + iwp - wp;
+      }
+      if (lane == 0) {
+        spre[0] = le + agg_e;
+        spre[1] = lp + agg_p;
+      }
+    }
+    if (trunc) ov |= kOvTruncated;
+    if (__ballot(asym)) ov |= kOvAsymmetric;
+    if (ov && lane == 0 && overflow) atomicOr(overflow, ov);
+    __syncthreads();
+    pre_e = (uint64_t)swt[wv];
+    pre_p = (uint64_t)swt[kRBWaves + wv];
+    // the CSR, clamped to the capacities in the fused form
+    const uint64_t ecl = kMode == kModeFused ? (uint64_t)e_cap : kVal31;
+    const uint64_t pcl = kMode == kModeFused ? (uint64_t)p_cap : kVal31;
+    if (my_row) {
+      const uint64_t oe = pre_e + my_off_e, op = pre_p + my_off_p;
+      rowptr[my_i] = (int32_t)(oe < ecl ? oe : ecl);
+      if (kPairs) pairptr[my_i] = (int32_t)(op < pcl ? op : pcl);
+    }
+    if (t == nblocks - 1 && threadIdx.x == 0) {
+      rowptr[n] = (int32_t)(spre[0] < ecl ? spre[0] : ecl);
+      if (kPairs) pairptr[n] = (int32_t)(spre[1] < pcl ? spre[1] : pcl);
+    }
+  }
+
+  if (kWrite) {
+    int64_t* ei0 = edge_index;
+    int64_t* ei1 = edge_index + e_stride;
+    int32_t* pi = pair_ij;
+    int32_t* pj = kPairs ? pair_ij + p_stride : nullptr;
+    // per-row offsets, and whether the row takes the untested path (all of it
+    // kept, inside the capacities, masks kept), one row per lane
+    int64_t my_e = 0, my_p = 0;
+    if (kMode == kModeFill) {
+      my_e = rs_e;
+      my_p = rs_p;
+    } else {
+      my_e = (int64_t)pre_e + my_off_e;
+      my_p = (int64_t)pre_p + my_off_p;
+    }
+    const bool my_fast = my_row && my_nch <= kMaskWords && my_tot <= mnn && my_e >= 0 &&
+                         my_e + my_tot <= e_cap &&
+                         (!kPairs || (my_p >= 0 && my_p + my_up <= p_cap));
+    const uint64_t fastw = __ballot(my_fast);
+    for (int k = 0; k < kRowsPerWave && rw0 + k < r1; ++k) {
+      const int i = rw0 + k;
+      const int st = __builtin_amdgcn_readlane(my_st, k);
+      const int nch = __builtin_amdgcn_readlane(my_nch, k);
+      const int64_t e_base = (int64_t)readlane64((uint64_t)my_e, k);
+      const int64_t p_base = kPairs ? (int64_t)readlane64((uint64_t)my_p, k) : 0;
+      if ((fastw >> k) & 1) {  // wave-uniform
+        const uint64_t w = lane < nch ? smask_w[k * kMaskWords + lane] : 0ull;
+        emit_row_fast<kPairs>(w, nch, st, i, e_base, p_base, ei0, ei1, col, pi, pj, eid2pair);
+        continue;
+      }
+      // truncated, past a capacity, or longer than the kept masks
+      bool dropped = false;
+      int kept = 0, ukept = 0;
+      if (nch <= kMaskWords) {
+        const uint64_t w = lane < nch ? smask_w[k * kMaskWords + lane] : 0ull;
+        for (int c = 0; c < nch && kept < mnn; ++c) {
+          const uint64_t m = readlane64(w, c);
+          if (m)
+            emit_chunk<kPairs>(m, st + MLCG_WAVE * c, i, mnn, e_base, kept, p_base, ukept,
+                               e_cap, ei0, ei1, col, p_cap, pi, pj, eid2pair, dropped);
+        }
+      } else {  // long row: test again, chunk by chunk
+        const int en = __builtin_amdgcn_readlane(my_en, k);
+        const bool loc = staged && st >= c_lo && en <= c_hi && i >= c_lo && i < c_hi;
+        const Vec3T<T> a = loc ? load_pos(sp, i - base) : load_pos(pos, i);
+        int64_t x_lo = 0, x_hi = 0;
+        if (kExcl) {
+          x_lo = eptr[i];
+          x_hi = eptr[i + 1];
+        }
+        for (int c = 0; c < nch && kept < mnn; ++c) {
+          const int jb = st + MLCG_WAVE * c;
+          const bool hit =
+              loc ? test_candidate<kExcl>(sp, base, a, i, jb + lane, en, r2, loop, exs, x_lo,
+                                          x_hi)
+                  : test_candidate<kExcl>(pos, 0, a, i, jb + lane, en, r2, loop, exs, x_lo,
+                                          x_hi);
+          const uint64_t m = __ballot(hit);
+          if (m)
+            emit_chunk<kPairs>(m, jb, i, mnn, e_base, kept, p_base, ukept, e_cap, ei0, ei1, col,
+                               p_cap, pi, pj, eid2pair, dropped);
+        }
+      }
+      if (__ballot(dropped) && lane == 0 && overflow) atomicOr(overflow, (int)kOvCapacity);
+    }
+  }
+}
+
+// Clears the look-back workspace (ticket + status words) and the overflow
+// word before a kModeRowptr / kModeFused launch (a kernel rather than a
+// memset node, so the sequence stays safe inside captured graphs).
+__global__ void radius_ws_init(uint64_t* __restrict__ ws, int64_t words,
+                               int32_t* __restrict__ overflow) {
+  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < words;
+       k += (int64_t)gridDim.x * blockDim.x)
+    ws[k] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0 && overflow) *overflow = 0;
+}
+
+// n == 0: the CSR is the single offset 0.
+__global__ void radius_empty(int32_t* rowptr, int32_t* pairptr, int32_t* overflow) {
+  rowptr[0] = 0;
+  if (pairptr) pairptr[0] = 0;
+  if (overflow) *overflow = 0;
 }
 
 // eid2pair for the lower copy (j, i) of every pair (i < j): binary search of i
@@ -373,16 +906,6 @@ __global__ void pair_reverse_kernel(const int32_t* __restrict__ pi,
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 4;
 constexpr int kScanTile = kScanThreads * kScanItems;
-
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = mlcg_lane();
-#pragma unroll
-  for (int o = 1; o < MLCG_WAVE; o <<= 1) {
-    int t = __shfl_up(v, o, MLCG_WAVE);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
 
 // Block-wide exclusive scan of one value per thread; returns the exclusive
 // prefix and writes the block total to *total.
@@ -528,40 +1051,82 @@ int launch_radius_count(const T* pos, const int64_t* batch, const int64_t* frame
   return mlcg_launch_status();
 }
 
+// Launches radius_rows_kernel in `mode` (argument checks of every form).  The
+// pair structures (col, pair list, its edge map) come together, with pairptr;
+// they are built for float32 positions only.
 template <typename T>
-int launch_radius_fill(const T* pos, const int64_t* batch, const int64_t* frame_ptr,
+int launch_radius_rows(int mode, const T* pos, const int64_t* batch, const int64_t* frame_ptr,
                        int64_t n_nodes, double r, int loop, int64_t max_num_neighbors,
                        const int64_t* exclude_pair_xs, const int64_t* ptr_exclude_pair_xs,
-                       const int32_t* rowptr, const int32_t* pairptr, int64_t edge_capacity,
+                       int32_t* rowptr, int32_t* pairptr, int64_t edge_capacity,
                        int64_t edge_stride, int64_t* edge_index, int32_t* col,
                        int64_t pair_capacity, int64_t pair_stride, int32_t* pair_ij,
-                       int32_t* eid2pair, int32_t* overflow, void* stream) {
+                       int32_t* eid2pair, void* workspace, int32_t* overflow, void* stream) {
   MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && r >= 0.0 &&
                max_num_neighbors >= 0);
-  MLCG_REQUIRE(edge_capacity >= 0 && edge_stride >= edge_capacity);
   MLCG_REQUIRE((exclude_pair_xs == nullptr) == (ptr_exclude_pair_xs == nullptr));
-  if (n_nodes == 0 || edge_capacity == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && batch && frame_ptr && rowptr && edge_index);
-  MLCG_REQUIRE(!pair_ij || (pairptr && pair_stride >= pair_capacity));
-  MLCG_REQUIRE(!eid2pair || pair_ij);
-  const T r2 = (T)(r * r);
-  dim3 grid(mlcg_div_up(n_nodes, kBlockRows)), block(kRowWaves * MLCG_WAVE);
-  hipStream_t s = mlcg_stream(stream);
-  // the pair structures come together (col, pair list and its edge map)
   MLCG_REQUIRE((col == nullptr && pair_ij == nullptr && eid2pair == nullptr) ||
                (col != nullptr && pair_ij != nullptr && eid2pair != nullptr));
   const bool pairs = pair_ij != nullptr;
-#define MLCG_FILL_LAUNCH(EX, PR)                                                          \
-  hipLaunchKernelGGL((radius_fill_kernel<EX, PR, T>), grid, block, 0, s, pos, batch,      \
-                     frame_ptr, n_nodes, r2, loop, max_num_neighbors,                     \
-                     EX ? exclude_pair_xs : nullptr, EX ? ptr_exclude_pair_xs : nullptr,  \
-                     rowptr, pairptr, edge_capacity, edge_stride, edge_index, col,        \
-                     pair_capacity, pair_stride, pair_ij, eid2pair, overflow)
-  if (exclude_pair_xs && pairs) MLCG_FILL_LAUNCH(true, true);
-  else if (exclude_pair_xs) MLCG_FILL_LAUNCH(true, false);
-  else if (pairs) MLCG_FILL_LAUNCH(false, true);
-  else MLCG_FILL_LAUNCH(false, false);
-#undef MLCG_FILL_LAUNCH
+  MLCG_REQUIRE(!pairs || sizeof(T) == sizeof(float));
+  MLCG_REQUIRE(rowptr);
+  if (mode != kModeRowptr) {
+    MLCG_REQUIRE(edge_capacity >= 0 && edge_capacity < (int64_t(1) << 31) &&
+                 edge_stride >= edge_capacity);
+    MLCG_REQUIRE(edge_capacity == 0 || edge_index);
+    MLCG_REQUIRE(!pairs || (pairptr && pair_capacity >= 0 &&
+                            pair_capacity < (int64_t(1) << 31) && pair_stride >= pair_capacity));
+  }
+  if (mode != kModeFill) MLCG_REQUIRE(workspace);
+  hipStream_t s = mlcg_stream(stream);
+  if (n_nodes == 0) {
+    if (mode != kModeFill) hipLaunchKernelGGL(radius_empty, dim3(1), dim3(1), 0, s, rowptr,
+                                              pairptr, overflow);
+    return mlcg_launch_status();
+  }
+  if (mode == kModeFill && edge_capacity == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && batch && frame_ptr);
+  const T r2 = (T)(r * r);  // r*r in double, then the scalar type (radius.cu:250)
+  const int mnn = max_num_neighbors < (int64_t)INT32_MAX ? (int)max_num_neighbors : INT32_MAX;
+  const int n = (int)n_nodes;
+  const int64_t rb =
+      kRBWaves * (mode == kModeFill ? RowsPerWave<kModeFill>::value : RowsPerWave<kModeFused>::value);
+  const int64_t nblocks = (n_nodes + rb - 1) / rb;
+  uint64_t* ws = static_cast<uint64_t*>(workspace);
+  if (mode != kModeFill)
+    hipLaunchKernelGGL(radius_ws_init, dim3(mlcg_persistent_groups(mlcg_div_up(nblocks + 1, 256), 4)),
+                       dim3(256), 0, s, ws, nblocks + 1, overflow);
+  const dim3 grid((unsigned)nblocks), block(kRBWaves * MLCG_WAVE);
+  const bool ex = exclude_pair_xs != nullptr;
+#define MLCG_ROWS_LAUNCH(MODE, EX, PR)                                                      \
+  hipLaunchKernelGGL((radius_rows_kernel<MODE, EX, PR, T>), grid, block, 0, s, pos, batch,  \
+                     frame_ptr, n, r2, loop, mnn, EX ? exclude_pair_xs : nullptr,           \
+                     EX ? ptr_exclude_pair_xs : nullptr, rowptr, pairptr, edge_capacity,    \
+                     edge_stride, edge_index, col, pair_capacity, pair_stride, pair_ij,     \
+                     eid2pair, ws, overflow)
+  if (mode == kModeRowptr) {  // pair counts with pairptr
+    if (ex && pairptr) MLCG_ROWS_LAUNCH(kModeRowptr, true, true);
+    else if (ex) MLCG_ROWS_LAUNCH(kModeRowptr, true, false);
+    else if (pairptr) MLCG_ROWS_LAUNCH(kModeRowptr, false, true);
+    else MLCG_ROWS_LAUNCH(kModeRowptr, false, false);
+  } else if (mode == kModeFill) {
+    if (sizeof(T) == sizeof(float) && pairs) {
+      if (ex) MLCG_ROWS_LAUNCH(kModeFill, true, (sizeof(T) == sizeof(float)));
+      else MLCG_ROWS_LAUNCH(kModeFill, false, (sizeof(T) == sizeof(float)));
+    } else {
+      if (ex) MLCG_ROWS_LAUNCH(kModeFill, true, false);
+      else MLCG_ROWS_LAUNCH(kModeFill, false, false);
+    }
+  } else {
+    if (sizeof(T) == sizeof(float) && pairs) {
+      if (ex) MLCG_ROWS_LAUNCH(kModeFused, true, (sizeof(T) == sizeof(float)));
+      else MLCG_ROWS_LAUNCH(kModeFused, false, (sizeof(T) == sizeof(float)));
+    } else {
+      if (ex) MLCG_ROWS_LAUNCH(kModeFused, true, false);
+      else MLCG_ROWS_LAUNCH(kModeFused, false, false);
+    }
+  }
+#undef MLCG_ROWS_LAUNCH
   return mlcg_launch_status();
 }
 
@@ -671,10 +1236,11 @@ extern "C" int mlcg_radius_fill(const float* pos, const int64_t* batch,
                                 int64_t pair_capacity, int64_t pair_stride,
                                 int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                                 void* stream) {
-  return launch_radius_fill(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
-                            exclude_pair_xs, ptr_exclude_pair_xs, rowptr, pairptr,
+  return launch_radius_rows(kModeFill, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs,
+                            const_cast<int32_t*>(rowptr), const_cast<int32_t*>(pairptr),
                             edge_capacity, edge_stride, edge_index, col, pair_capacity,
-                            pair_stride, pair_ij, eid2pair, overflow, stream);
+                            pair_stride, pair_ij, eid2pair, nullptr, overflow, stream);
 }
 
 extern "C" int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
@@ -685,11 +1251,70 @@ extern "C" int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
                                     const int32_t* rowptr, int64_t edge_capacity,
                                     int64_t edge_stride, int64_t* edge_index,
                                     int32_t* overflow, void* stream) {
-  return launch_radius_fill(pos, batch, frame_ptr, n_nodes, r, loop, max_num_neighbors,
-                            exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
-                            (const int32_t*)nullptr, edge_capacity, edge_stride, edge_index,
+  return launch_radius_rows(kModeFill, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs,
+                            const_cast<int32_t*>(rowptr), (int32_t*)nullptr, edge_capacity,
+                            edge_stride, edge_index, (int32_t*)nullptr, 0, 0,
+                            (int32_t*)nullptr, (int32_t*)nullptr, nullptr, overflow, stream);
+}
+
+extern "C" int64_t mlcg_radius_workspace_bytes(int64_t n_nodes) {
+  if (n_nodes < 0) return 0;
+  return 8 * ((n_nodes + kRBScan - 1) / kRBScan + 1);
+}
+
+extern "C" int mlcg_radius_rowptr(const float* pos, const int64_t* batch,
+                                  const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                                  int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                                  const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                                  int32_t* pairptr, void* workspace, int32_t* overflow,
+                                  void* stream) {
+  return launch_radius_rows(kModeRowptr, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
+                            pairptr, 0, 0, (int64_t*)nullptr, (int32_t*)nullptr, 0, 0,
+                            (int32_t*)nullptr, (int32_t*)nullptr, workspace, overflow, stream);
+}
+
+extern "C" int mlcg_radius_rowptr_f64(const double* pos, const int64_t* batch,
+                                      const int64_t* frame_ptr, int64_t n_nodes, double r,
+                                      int loop, int64_t max_num_neighbors,
+                                      const int64_t* exclude_pair_xs,
+                                      const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                                      int32_t* pairptr, void* workspace, int32_t* overflow,
+                                      void* stream) {
+  return launch_radius_rows(kModeRowptr, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
+                            pairptr, 0, 0, (int64_t*)nullptr, (int32_t*)nullptr, 0, 0,
+                            (int32_t*)nullptr, (int32_t*)nullptr, workspace, overflow, stream);
+}
+
+extern "C" int mlcg_radius_graph(const float* pos, const int64_t* batch,
+                                 const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                                 int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                                 const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                                 int32_t* pairptr, int64_t edge_capacity, int64_t edge_stride,
+                                 int64_t* edge_index, int32_t* col, int64_t pair_capacity,
+                                 int64_t pair_stride, int32_t* pair_ij, int32_t* eid2pair,
+                                 void* workspace, int32_t* overflow, void* stream) {
+  return launch_radius_rows(kModeFused, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
+                            pairptr, edge_capacity, edge_stride, edge_index, col, pair_capacity,
+                            pair_stride, pair_ij, eid2pair, workspace, overflow, stream);
+}
+
+extern "C" int mlcg_radius_graph_f64(const double* pos, const int64_t* batch,
+                                     const int64_t* frame_ptr, int64_t n_nodes, double r,
+                                     int loop, int64_t max_num_neighbors,
+                                     const int64_t* exclude_pair_xs,
+                                     const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                                     int64_t edge_capacity, int64_t edge_stride,
+                                     int64_t* edge_index, void* workspace, int32_t* overflow,
+                                     void* stream) {
+  return launch_radius_rows(kModeFused, pos, batch, frame_ptr, n_nodes, r, loop,
+                            max_num_neighbors, exclude_pair_xs, ptr_exclude_pair_xs, rowptr,
+                            (int32_t*)nullptr, edge_capacity, edge_stride, edge_index,
                             (int32_t*)nullptr, 0, 0, (int32_t*)nullptr, (int32_t*)nullptr,
-                            overflow, stream);
+                            workspace, overflow, stream);
 }
 
 // Host-side conversion of an exclusion pair list to the per-row CSR the

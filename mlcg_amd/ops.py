@@ -131,6 +131,17 @@ def _validate_pos(pos: torch.Tensor) -> torch.Tensor:
     return pos.contiguous()
 
 
+def _check_radius_flags(overflow: int) -> None:
+    """Raise for the radius graph's internal failure bits (8: a look-back wait
+    hit its bound, 16: more than 2^31 - 1 edges for the int32 CSR)."""
+    if overflow & 16:
+        raise RuntimeError("radius graph: more than 2^31 - 1 edges; the int32 CSR cannot "
+                           "hold them")
+    if overflow & 8:
+        raise RuntimeError("radius graph: a block of the sizing pass timed out waiting for "
+                           "its predecessors")
+
+
 def radius_graph(
     pos: torch.Tensor,
     r: float,
@@ -203,22 +214,23 @@ def radius_graph(
     exs, eptr = _validate_exclusions(exclude_pair_xs, ptr_exclude_pair_xs, n, dev)
     s = stream_handle(dev)
 
-    deg = torch.empty(n, dtype=torch.int32, device=dev)
-    udeg = torch.empty(n, dtype=torch.int32, device=dev)
-    flags = torch.zeros(1, dtype=torch.int32, device=dev)
-    call("mlcg_radius_count_f64" if f64 else "mlcg_radius_count", ptr(pos), ptr(batch),
-         ptr(frame_ptr), n, float(r), int(loop), int(max_num_neighbors), ptr(exs), ptr(eptr),
-         ptr(deg), ptr(udeg), ptr(flags), s)
+    mnn = int(max_num_neighbors)
     rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
-    pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
-    ws = torch.empty(max(1, _lib.load().mlcg_scan_workspace_ints(n)), dtype=torch.int32,
+    pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev) if with_pairs else None
+    flags = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the kernels
+    ws = torch.empty(max(1, _lib.load().mlcg_radius_workspace_bytes(n) // 8), dtype=torch.int64,
                      device=dev)
-    call("mlcg_exclusive_scan2_i32", ptr(deg), ptr(udeg), n, ptr(rowptr), ptr(pairptr),
-         ptr(ws), s)
     if capacity is None:
+        # sizing pass (counts, block scan, look-back) -> rowptr / pairptr, then
         # one host sync to size the outputs (the reference syncs at radius.cu:288)
-        e_count, p_count, overflow = torch.stack(
-            [rowptr[n], pairptr[n], flags[0]]).tolist()
+        call("mlcg_radius_rowptr_f64" if f64 else "mlcg_radius_rowptr", ptr(pos), ptr(batch),
+             ptr(frame_ptr), n, float(r), int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr),
+             ptr(pairptr), ptr(ws), ptr(flags), s)
+        if with_pairs:
+            e_count, p_count, overflow = torch.cat([rowptr[n:], pairptr[n:], flags]).tolist()
+        else:
+            (e_count, overflow), p_count = torch.cat([rowptr[n:], flags]).tolist(), 0
+        _check_radius_flags(overflow)
         if with_pairs and overflow & 1:
             raise RuntimeError(
                 f"max_num_neighbors={max_num_neighbors} binds: the truncated graph is not "
@@ -240,26 +252,32 @@ def radius_graph(
         pair_ij = torch.empty(2, p_cap, dtype=torch.int32, device=dev)
         eid2pair = (torch.empty if capacity is None else torch.zeros)(
             e_cap, dtype=torch.int32, device=dev)
-    if f64:
-        call("mlcg_radius_fill_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
-             int(loop), int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr), e_cap, e_cap,
-             ptr(edge_index), ptr(flags), s)
+    if capacity is None:
+        if f64:
+            call("mlcg_radius_fill_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+                 int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), e_cap, e_cap,
+                 ptr(edge_index), ptr(flags), s)
+        else:
+            call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+                 int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), ptr(pairptr), e_cap, e_cap,
+                 ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij), ptr(eid2pair),
+                 ptr(flags), s)
+    elif f64:
+        # one launch: sweep, look-back and write; the CSR comes out clamped to
+        # the capacity, so every consumer stays inside the buffers
+        call("mlcg_radius_graph_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+             int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), e_cap, e_cap, ptr(edge_index),
+             ptr(ws), ptr(flags), s)
     else:
-        call("mlcg_radius_fill", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
-             int(max_num_neighbors), ptr(exs), ptr(eptr), ptr(rowptr),
-             ptr(pairptr) if with_pairs else None,
-             e_cap, e_cap, ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij),
-             ptr(eid2pair), ptr(flags), s)
-    if capacity is not None:
-        # rows past the capacity were dropped by the fill: clamp the CSR (and
-        # the pair count) so that every consumer stays inside the buffers
-        rowptr.clamp_(max=e_cap)
-        pairptr.clamp_(max=p_cap)
+        call("mlcg_radius_graph", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r), int(loop),
+             mnn, ptr(exs), ptr(eptr), ptr(rowptr), ptr(pairptr), e_cap, e_cap,
+             ptr(edge_index), ptr(col), p_cap, p_cap, ptr(pair_ij), ptr(eid2pair), ptr(ws),
+             ptr(flags), s)
     if with_pairs:
         call("mlcg_pair_reverse_map", ptr(pair_ij), p_cap, ptr(pairptr[n:]), p_cap,
              ptr(rowptr), ptr(col), ptr(eid2pair), s)
     return PairGraph(edge_index=edge_index, rowptr=rowptr, col=col, pair_ij=pair_ij,
-                     pairptr=pairptr if with_pairs else None, eid2pair=eid2pair,
+                     pairptr=pairptr, eid2pair=eid2pair,
                      frame_ptr=frame_ptr, num_nodes=n, num_edges=e_count,
                      num_pairs=p_count if with_pairs else 0, overflow=int(overflow),
                      flags=flags)
