@@ -8,14 +8,16 @@
 // 125-141).  Output order is canonical: rows by centre i ascending, and
 // within a row neighbours j ascending.
 //
-// Design: two passes (count, then fill at scanned offsets) give an exact,
-// deterministic layout without atomics, cooperative launches or host
-// synchronisation inside the library.  The count runs one or more threads per
-// row over its frame; the fill one wave per row: the wave sweeps the row's frame
-// 64 candidates at a time, each lane testing one candidate, a ballot gives the
-// hit mask and mbcnt the rank of each hit, so every row's edges are written as
-// contiguous, coalesced runs.  Both stage the positions of a workgroup's
-// frames in LDS.
+// Design: one row-block kernel (radius_rows_kernel) gives an exact,
+// deterministic layout without atomics on the output, cooperative launches or
+// host synchronisation inside the library.  A wave sweeps a row's frame 64
+// candidates at a time, each lane testing one candidate; the ballot is the
+// row's hit mask and mbcnt the rank of each hit, so every row's edges are
+// written as contiguous runs.  Row offsets come from a block scan plus a
+// decoupled look-back across blocks (the sizing pass and the one-launch
+// form), or from a CSR the caller passes (the write pass).  The positions of a
+// workgroup's frames are staged in LDS.  radius_count_kernel and the
+// three-kernel int32 scan remain for the per-node degree entry points.
 //
 // Optional pair exclusion follows the reference kernel's CSR form
 // (radius.cu:113-133, built by exclusion_pair_to_ptr in exclusion_pairs.cpp:
@@ -241,10 +243,11 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 // Look-back: each block publishes its totals (edges, pairs) in a status word
 // of the workspace, first as an aggregate, then as an inclusive prefix; a
 // block sums the aggregates of its predecessors back to the first inclusive
-// prefix, reading kLookLanes x 64 predecessors per round.  Block indices come
-// from a ticket counter, so a block only waits for blocks that are already
-// running, and every wait is bounded (kSpinLimit polls): a block that gives
-// up sets overflow bit 8 and carries on, so the kernel always finishes.  The
+// prefix, reading kLookLanes x 64 predecessors per round.  A block waits
+// only for blocks of lower index, which the dispatcher started before it (it
+// dispatches workgroups in index order), and every wait is bounded
+// (kSpinLimit polls): a block that gives up sets overflow bit 8 and carries
+// on, so the kernel always finishes and the host reports the error.  The
 // workspace is cleared by radius_ws_init on the same stream before every such
 // launch.
 constexpr int kRBWaves = 4;
@@ -857,7 +860,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
   }
 }
 
-// Clears the look-back workspace (ticket + status words) and the overflow
+// Clears the look-back workspace (one unused word + the status words) and the overflow
 // word before a kModeRowptr / kModeFused launch (a kernel rather than a
 // memset node, so the sequence stays safe inside captured graphs).
 __global__ void radius_ws_init(uint64_t* __restrict__ ws, int64_t words,
