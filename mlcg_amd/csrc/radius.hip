@@ -205,8 +205,8 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 
 // ---------------------------------------------------------------------------
 // Row-block kernel of the radius graph.  A workgroup of kRBWaves waves takes a
-// block of kRB consecutive rows, wave w the rows w R .. w R + R - 1
-// (R = kRowsPerWave), so that each wave writes one contiguous run of the edge
+// block of kRBWaves R consecutive rows, wave w the rows w R .. w R + R - 1
+// (R rows per wave, see RowsPerWave), so that each wave writes one contiguous run of the edge
 // list.  The nodes of the block's frames -- a contiguous node range, as frames
 // are -- are staged in LDS as 4-component records when they fit
 // (StageNodes<T>); a block whose frames are larger reads positions from
@@ -252,15 +252,16 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 // launch.
 constexpr int kRBWaves = 4;
 enum { kModeRowptr = 0, kModeFill = 1, kModeFused = 2 };
-// Rows per wave: 64 (one per lane) in the look-back modes, where a larger
-// block amortises the staging, the block scan and the look-back over more
-// rows; 16 in kModeFill, which has no look-back and gains more from four
-// times as many waves hiding each other's latencies.
+// Rows per wave: 16 in kModeFill, which has no look-back and gains from many
+// waves hiding each other's latencies; 32 to 64 (at most one per lane) in the
+// look-back modes, where larger blocks amortise the staging, the block scan
+// and the look-back, chosen per launch so that the waves spread evenly over
+// the chip's SIMDs (scan_rows_per_wave).  RowsPerWave is the maximum.
 template <int kMode>
 struct RowsPerWave {
   static constexpr int value = kMode == kModeFill ? 16 : 64;
 };
-constexpr int kRBScan = kRBWaves * 64;  // rows per block of the look-back modes
+constexpr int kMinScanRows = 32;  // fewest rows per wave of the look-back modes
 constexpr int kGroup = 4;                      // rows swept together
 constexpr int kMaskWords = 8;                  // mask words kept per row (512 candidates)
 constexpr int kLookLanes = 4;                  // statuses per lane and look-back round
@@ -589,16 +590,16 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     int32_t* __restrict__ rowptr, int32_t* __restrict__ pairptr, int64_t e_cap,
     int64_t e_stride, int64_t* __restrict__ edge_index, int32_t* __restrict__ col,
     int64_t p_cap, int64_t p_stride, int32_t* __restrict__ pair_ij,
-    int32_t* __restrict__ eid2pair, uint64_t* __restrict__ ws, int32_t* __restrict__ overflow) {
+    int32_t* __restrict__ eid2pair, uint64_t* __restrict__ ws, int32_t* __restrict__ overflow,
+    int rpw) {
   constexpr bool kScan = kMode != kModeFill;
   constexpr bool kWrite = kMode != kModeRowptr;
-  constexpr int kRowsPerWave = RowsPerWave<kMode>::value;
-  constexpr int kRB = kRBWaves * kRowsPerWave;
+  constexpr int kMaxRows = RowsPerWave<kMode>::value;  // rows per wave at most
   constexpr bool kMasks = kWrite || kPairs;  // kPairs needs the lower counts from the sweep
   constexpr bool kLow = kPairs;
   constexpr int kStage = StageNodes<T>::value;
   __shared__ Pos4<T> sp[kStage + 1];  // + the sentinel record
-  __shared__ uint64_t smask[kMasks ? kRB * kMaskWords : 1];
+  __shared__ uint64_t smask[kMasks ? kRBWaves * kMaxRows * kMaskWords : 1];
   __shared__ int64_t swt[2 * kRBWaves];  // per-wave totals (edges, pairs), then offsets
   __shared__ uint64_t spre[2];
 
@@ -608,9 +609,10 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
   const int lane = mlcg_lane();
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / MLCG_WAVE);
   const int t = blockIdx.x;
-  const int nblocks = (n + kRB - 1) / kRB;
-  const int r0 = t * kRB;
-  const int r1 = r0 + kRB < n ? r0 + kRB : n;
+  const int rb = kRBWaves * rpw;  // rows per block
+  const int nblocks = (n + rb - 1) / rb;
+  const int r0 = t * rb;
+  const int r1 = r0 + rb < n ? r0 + rb : n;
   // the block's node window (node indices are below 2^31: int32 CSR)
   const int c_lo = (int)frame_ptr[batch[r0]];
   const int c_hi = (int)frame_ptr[batch[r1 - 1] + 1];
@@ -627,9 +629,10 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     }
   }
   // lane k of wave wv holds the scalars of row rw0 + k
-  const int rw0 = r0 + wv * kRowsPerWave;
+  const int rw0 = r0 + wv * rpw;
+  const int rwe = rw0 + rpw < r1 ? rw0 + rpw : r1;  // past the wave's last row
   int rs_start = 0, rs_end = 0, rs_e = 0, rs_p = 0;
-  if (lane < kRowsPerWave && rw0 + lane < r1) {
+  if (rw0 + lane < rwe) {
     const int64_t b = batch[rw0 + lane];
     rs_start = (int)frame_ptr[b];
     rs_end = (int)frame_ptr[b + 1];
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
 
   // the self pair of each row, one row per lane: the sweep's own test of j = i
   const int my_i = rw0 + lane;
-  const bool my_row = lane < kRowsPerWave && my_i < r1;
+  const bool my_row = my_i < rwe;
   uint64_t selfm;
   {
     bool sh = false;
@@ -656,13 +659,13 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
   }
 
   // sweep: masks of row k at smask_w[k * kMaskWords]; per-row counts to lane k
-  uint64_t* smask_w = smask + (kMasks ? wv * kRowsPerWave * kMaskWords : 0);
+  uint64_t* smask_w = smask + (kMasks ? wv * kMaxRows * kMaskWords : 0);
   int my_tot = 0, my_low = 0, my_slf = 0;
   uint64_t fastm = 0;  // rows swept by the fast path
   bool asym = false;
-  for (int g = 0; g < kRowsPerWave && rw0 + g < r1; g += kGroup) {
+  for (int g = 0; rw0 + g < rwe; g += kGroup) {
     int ii[kGroup], st[kGroup], en[kGroup];
-    const bool full = rw0 + g + kGroup <= r1;
+    const bool full = rw0 + g + kGroup <= rwe;
     const int st0 = __builtin_amdgcn_readlane(rs_start, g);
     const int en0 = __builtin_amdgcn_readlane(rs_end, g);
     bool fast = false;
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
         ii[u] = rw0 + g + u;
         st[u] = __builtin_amdgcn_readlane(rs_start, g + u);
         en[u] = __builtin_amdgcn_readlane(rs_end, g + u);
-        if (ii[u] >= r1) {  // past the last row: the group's first row again, ignored
+        if (ii[u] >= rwe) {  // past the wave's last row: its first row again, ignored
           ii[u] = rw0 + g;
           st[u] = st0;
           en[u] = en0;
@@ -811,7 +814,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
                          my_e + my_tot <= e_cap &&
                          (!kPairs || (my_p >= 0 && my_p + my_up <= p_cap));
     const uint64_t fastw = __ballot(my_fast);
-    for (int k = 0; k < kRowsPerWave && rw0 + k < r1; ++k) {
+    for (int k = 0; rw0 + k < rwe; ++k) {
       const int i = rw0 + k;
       const int st = __builtin_amdgcn_readlane(my_st, k);
       const int nch = __builtin_amdgcn_readlane(my_nch, k);
@@ -1054,6 +1057,41 @@ int launch_radius_count(const T* pos, const int64_t* batch, const int64_t* frame
   return mlcg_launch_status();
 }
 
+// SIMDs of the current device (4 per CU), looked up once per device.
+int device_simds() {
+  static std::mutex mu;
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = -1;
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= 0 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                     hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev >= 0) cached[dev] = 4 * cus;
+  return 4 * cus;
+}
+
+// Rows per wave of the look-back modes: of 32 .. 64, the count that spreads
+// the waves most evenly over the SIMDs (the largest per-SIMD load of rows is
+// smallest; ties go to more rows per wave).  n = 204,800 takes 50 rows: 4,096
+// waves, four per SIMD on 256 CUs.
+int scan_rows_per_wave(int64_t n) {
+  const int64_t simds = device_simds();
+  int best = RowsPerWave<kModeFused>::value;
+  int64_t best_load = INT64_MAX;
+  for (int r = RowsPerWave<kModeFused>::value; r >= kMinScanRows; --r) {
+    const int64_t waves = (n + r - 1) / r;
+    const int64_t load = (waves + simds - 1) / simds * r;
+    if (load < best_load) {
+      best_load = load;
+      best = r;
+    }
+  }
+  return best;
+}
+
 // Launches radius_rows_kernel in `mode` (argument checks of every form).  The
 // pair structures (col, pair list, its edge map) come together, with pairptr;
 // they are built for float32 positions only.
@@ -1092,8 +1130,8 @@ int launch_radius_rows(int mode, const T* pos, const int64_t* batch, const int64
   const T r2 = (T)(r * r);  // r*r in double, then the scalar type (radius.cu:250)
   const int mnn = max_num_neighbors < (int64_t)INT32_MAX ? (int)max_num_neighbors : INT32_MAX;
   const int n = (int)n_nodes;
-  const int64_t rb =
-      kRBWaves * (mode == kModeFill ? RowsPerWave<kModeFill>::value : RowsPerWave<kModeFused>::value);
+  const int rpw = mode == kModeFill ? RowsPerWave<kModeFill>::value : scan_rows_per_wave(n_nodes);
+  const int64_t rb = (int64_t)kRBWaves * rpw;
   const int64_t nblocks = (n_nodes + rb - 1) / rb;
   uint64_t* ws = static_cast<uint64_t*>(workspace);
   if (mode != kModeFill)
@@ -1106,7 +1144,7 @@ int launch_radius_rows(int mode, const T* pos, const int64_t* batch, const int64
                      frame_ptr, n, r2, loop, mnn, EX ? exclude_pair_xs : nullptr,           \
                      EX ? ptr_exclude_pair_xs : nullptr, rowptr, pairptr, edge_capacity,    \
                      edge_stride, edge_index, col, pair_capacity, pair_stride, pair_ij,     \
-                     eid2pair, ws, overflow)
+                     eid2pair, ws, overflow, rpw)
   if (mode == kModeRowptr) {  // pair counts with pairptr
     if (ex && pairptr) MLCG_ROWS_LAUNCH(kModeRowptr, true, true);
     else if (ex) MLCG_ROWS_LAUNCH(kModeRowptr, true, false);
@@ -1263,7 +1301,8 @@ extern "C" int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
 
 extern "C" int64_t mlcg_radius_workspace_bytes(int64_t n_nodes) {
   if (n_nodes < 0) return 0;
-  return 8 * ((n_nodes + kRBScan - 1) / kRBScan + 1);
+  const int64_t rb = (int64_t)kRBWaves * kMinScanRows;
+  return 8 * ((n_nodes + rb - 1) / rb + 1);
 }
 
 extern "C" int mlcg_radius_rowptr(const float* pos, const int64_t* batch,
