@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 constexpr int kRBWaves = 4;
 enum { kModeRowptr = 0, kModeFill = 1, kModeFused = 2 };
 // Rows per wave: 16 in kModeFill, which has no look-back and gains from many
-// waves hiding each other's latencies; 32 to 64 (at most one per lane) in the
+// waves hiding each other's latencies; 8 to 64 (at most one per lane) in the
 // look-back modes, where larger blocks amortise the staging, the block scan
 // and the look-back, chosen per launch so that the waves spread evenly over
 // the chip's SIMDs (scan_rows_per_wave).  RowsPerWave is the maximum.
@@ -261,7 +261,7 @@ template <int kMode>
 struct RowsPerWave {
   static constexpr int value = kMode == kModeFill ? 16 : 64;
 };
-constexpr int kMinScanRows = 32;  // fewest rows per wave of the look-back modes
+constexpr int kMinScanRows = 8;  // fewest rows per wave of the look-back modes
 constexpr int kGroup = 4;                      // rows swept together
 constexpr int kMaskWords = 8;                  // mask words kept per row (512 candidates)
 constexpr int kLookLanes = 4;                  // statuses per lane and look-back round
@@ -1073,10 +1073,10 @@ int device_simds() {
   return 4 * cus;
 }
 
-// Rows per wave of the look-back modes: of 32 .. 64, the count that spreads
+// Rows per wave of the look-back modes: of 8 .. 64, the count that spreads
 // the waves most evenly over the SIMDs (the largest per-SIMD load of rows is
-// smallest; ties go to more rows per wave).  n = 204,800 takes 50 rows: 4,096
-// waves, four per SIMD on 256 CUs.
+// smallest; ties go to more rows per wave).  On 256 CUs n = 204,800 takes 50
+// rows (4,096 waves, four per SIMD) and n = 17,920 takes 18 (996 waves).
 int scan_rows_per_wave(int64_t n) {
   const int64_t simds = device_simds();
   int best = RowsPerWave<kModeFused>::value;
