@@ -989,15 +989,15 @@ __host__ __device__ constexpr int bwd_partial_floats(int K) {
 }
 __host__ __device__ constexpr int bwd_krows(int K) { return K <= 64 ? 64 : 128; }
 // LDS: W2^T fragments [8][8][64] float4 (or two fp16 planes) | TB [2][16][128]
-//      (or three fp16 planes) | TT, HT, AT [2][128][16] (split path: AT in
+//      (or two fp16 planes) | TT, HT, AT [2][128][16] (split path: AT in
 //      TT's memory) | GT [2 buffers][2][krows][16] (split path: two fp16
 //      planes, followed by the pair-major three-plane copy of g, g' for step
 //      1, [3][2][16][64] halfs) | per-pair maxima (split path: [2 buffers][2]
 //      [16] atomic-max bits; 256 floats reserved, the W2 scale's reduction
-//      scratch); 152,576 bytes for K <= 64 and exactly the 160 KiB of a
+//      scratch); 144,384 bytes for K <= 64 and exactly the 160 KiB of a
 //      gfx950 CU for K <= 128
 __host__ __device__ constexpr int bwd_lds_floats(int K) {
-  return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 3 * 16 * kF + 2 * 2 * kF * 16 +
+  return K <= 64 ? kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 2 * 2 * kF * 16 +
                        2 * 2 * bwd_krows(K) * 16 + 3 * 2 * 16 * 64 / 2 + 2 * kBwdWaves * 16
                  : kFT * kFT * MLCG_WAVE * 4 + 2 * 16 * kF + 3 * 2 * kF * 16 +
                        2 * 2 * bwd_krows(K) * 16;
@@ -1123,11 +1123,11 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // fp32: W2^T A fragments [8 t][8 u][64 l] float4; x3: W2^T as two fp16
   // planes (hi, lo S) of [8 t][4 s][64 l][8]
   float* w2ts = lds;
-  // fp32: [2][16 pairs][128] t, t'; x3: three fp16 planes (hi, hi S, lo S)
-  // of [2][16 pairs][128], each t scaled per pair (sigma) into [-4, 4]
+  // fp32: [2][16 pairs][128] t, t'; x3: two fp16 planes (hi, lo S) of
+  // [2][16 pairs][128], each t scaled per pair (sigma) into [-4, 4]
   float* TB = w2ts + kFT * kFT * MLCG_WAVE * 4;
-  float* TT = TB + (kX3 ? 3 * 16 * kF : 2 * 16 * kF);  // [2][128][16 pairs]  t, t'
-  float* HT = TT + 2 * kF * 16;                       // [2][128][16 pairs]  h, h'
+  float* TT = TB + 2 * 16 * kF;  // [2][128][16 pairs]  t, t'
+  float* HT = TT + 2 * kF * 16;  // [2][128][16 pairs]  h, h'
   // [2][128][16 pairs] ab, ab'.  On the split path AT shares TT's memory: both
   // hold rows of the wave's own features only, and a wave reads TT (step 4)
   // before it writes AT (step 5) and reads AT (step 6) before it writes the
@@ -1271,49 +1271,70 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     return p < np ? p : np - 1;
   };
   // Basis of a tile: wave w evaluates k steps w, w + 8, ... for the 16 pairs
-  // (into GT), every lane the envelope of its own pair (returned).
+  // (into GT), every lane the envelope of its own pair.  In two parts, so that
+  // the arithmetic (basis_eval) can be scheduled among the MFMAs of step 4
+  // and only the LDS writes (basis_store) come after them.
   // Lanes past the last pair evaluate the (finite) basis and activations of
   // the last pair but carry zero adjoints (tile_adjoint's mask), hence
   // t = t' = 0 and ab = ab' = 0: they add exact zeros to every pair sum.
-  auto basis = [&](const TileIn& t, int bsel, float& cc, float& dcc) {
-    float* GTb = GT0 + bsel * 2 * kRows * 16;
+  struct BasisV {
+    float cc, dcc;                        // envelope of the lane's pair
+    float g[kBasisSteps], gd[kBasisSteps];  // fp32 path
+    halfx2 sh[kBasisSteps], sl[kBasisSteps];  // split path: GT planes (hi, lo S4)
+    halfx2 ch[kBasisSteps], chs[kBasisSteps], cl[kBasisSteps];  // step 1's planes
+  };
+  auto basis_eval = [&](const TileIn& t) -> BasisV {
+    BasisV bv;
     const float dx = t.xj - t.xi, dy = t.yj - t.yi, dz = t.zj - t.zi;
     const float d = sqrtf(dx * dx + dy * dy + dz * dz);
     float crbf, dcrbf;
-    envelopes(rp, d, crbf, dcrbf, cc, dcc);
+    envelopes(rp, d, crbf, dcrbf, bv.cc, bv.dcc);
+#pragma unroll
+    for (int e = 0; e < kBasisSteps; ++e) {
+      const int s = kBwdWaves * e + w;
+      float g = 0.f, gd = 0.f;
+      if (s < KSMAX) {
+        float cen = bcen[e], wid = bwid[e];
+        if (!kBasisRegs) basis_params(rp, 4 * s + q, cen, wid);
+        rbf_any<BASIS>(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
+      }
+      bv.g[e] = g;
+      bv.gd[e] = gd;
+      if constexpr (kX3) {
+        split2x2(g, gd, kS4, bv.sh[e], bv.sl[e]);
+        split2x2(g * kBetaG0, gd * kBetaG1, kS4, bv.ch[e], bv.cl[e]);
+        // hi S4 in fp16: exact (a power of two), one packed multiply
+        bv.chs[e] = bv.ch[e] * halfx2{(_Float16)kS4, (_Float16)kS4};
+      }
+    }
+    return bv;
+  };
+  auto basis_store = [&](const BasisV& bv, int bsel) {
+    float* GTb = GT0 + bsel * 2 * kRows * 16;
 #pragma unroll
     for (int e = 0; e < kBasisSteps; ++e) {
       const int s = kBwdWaves * e + w;
       if (s < KSMAX) {
-        float g, gd, cen = bcen[e], wid = bwid[e];
-        if (!kBasisRegs) basis_params(rp, 4 * s + q, cen, wid);
-        rbf_any<BASIS>(rp, 4 * s + q < K, cen, wid, d, crbf, dcrbf, g, gd);  // zero for k >= K
         if constexpr (kX3) {
           // two fp16 planes (hi, lo S4) of [2][kRows][16 pairs]
           _Float16* GTh = reinterpret_cast<_Float16*>(GTb);
           const int o = (4 * s + q) * 16 + n;
-          const float v0 = g, v1 = gd;
-          halfx2 sh, sl;
-          split2x2(v0, v1, kS4, sh, sl);
-          GTh[o] = sh[0];
-          GTh[kRows * 16 + o] = sh[1];
-          GTh[2 * kRows * 16 + o] = sl[0];
-          GTh[3 * kRows * 16 + o] = sl[1];
+          GTh[o] = bv.sh[e][0];
+          GTh[kRows * 16 + o] = bv.sh[e][1];
+          GTh[2 * kRows * 16 + o] = bv.sl[e][0];
+          GTh[3 * kRows * 16 + o] = bv.sl[e][1];
           // step 1's copy (k = 4s + q: chunk s, element q)
           const int o1 = n * 64 + 4 * (s ^ n) + q;
-          const float u0 = v0 * kBetaG0, u1 = v1 * kBetaG1;
-          halfx2 ch, cl;
-          split2x2(u0, u1, kS4, ch, cl);
-          G1h[o1] = ch[0];
-          G1h[1024 + o1] = ch[1];
-          G1h[2048 + o1] = (_Float16)((float)ch[0] * kS4);
-          G1h[3072 + o1] = (_Float16)((float)ch[1] * kS4);
-          G1h[4096 + o1] = cl[0];
-          G1h[5120 + o1] = cl[1];
+          G1h[o1] = bv.ch[e][0];
+          G1h[1024 + o1] = bv.ch[e][1];
+          G1h[2048 + o1] = bv.chs[e][0];
+          G1h[3072 + o1] = bv.chs[e][1];
+          G1h[4096 + o1] = bv.cl[e][0];
+          G1h[5120 + o1] = bv.cl[e][1];
         } else {
           const int o = rp_at(4 * s + q, n);
-          GTb[o] = g;
-          GTb[kRows * 16 + o] = gd;
+          GTb[o] = bv.g[e];
+          GTb[kRows * 16 + o] = bv.gd[e];
         }
       }
     }
@@ -1324,10 +1345,13 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   // of |t|, |t'| over the wave's 16 features, published for step 2
   float tbv[4], tdbv[4];
   float tmax_tile = 0.f;  // split path: max |t|, |t'| over the wave's features and pairs
-  auto pair_adjoints = [&](float4 wb, float4 wdb, float cc, float dcc, int pb) {
+  // in two parts like the basis: the arithmetic, then the LDS atomics
+  auto pair_adjoints_eval = [&](float4 wb, float4 wdb, float cc, float dcc, float& m0,
+                                float& m1) {
     const float wbv[4] = {wb.x, wb.y, wb.z, wb.w};
     const float wdbv[4] = {wdb.x, wdb.y, wdb.z, wdb.w};
-    float m0 = 0.f, m1 = 0.f;
+    m0 = 0.f;
+    m1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       tbv[i] = wbv[i] * cc + wdbv[i] * dcc;
@@ -1338,12 +1362,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     if constexpr (kX3) {
       m0 = cross_row_max(m0);
       m1 = cross_row_max(m1);
+      const float mx = row16_max(fmaxf(m0, m1));
+      tmax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
+    }
+  };
+  auto pair_adjoints_store = [&](float m0, float m1, int pb) {
+    if constexpr (kX3) {
       if (q == 0) {  // non-negative floats order as their bit patterns
         atomicMax(PMAXu + pb * 32 + n, __float_as_uint(m0));
         atomicMax(PMAXu + pb * 32 + 16 + n, __float_as_uint(m1));
       }
-      const float mx = row16_max(fmaxf(m0, m1));
-      tmax_tile = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
     }
   };
 
@@ -1362,10 +1390,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     ni = pi[p1];
     nj = pj[p1];
     const float vm0 = (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f;
-    basis(first, 0, cc_cur, dcc_cur);
+    const BasisV bv0 = basis_eval(first);
+    basis_store(bv0, 0);
+    cc_cur = bv0.cc;
+    dcc_cur = bv0.dcc;
     float4 wb0, wdb0;
     tile_adjoint<kNodes>(first, tangent, has_yd, vm0, wb0, wdb0);
-    pair_adjoints(wb0, wdb0, cc_cur, dcc_cur, 0);
+    float pm0, pm1;
+    pair_adjoints_eval(wb0, wdb0, cc_cur, dcc_cur, pm0, pm1);
+    pair_adjoints_store(pm0, pm1, 0);
   }
   __syncthreads();
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
@@ -1464,10 +1497,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       // barrier below); its last reader was phase 2 of the previous tile
       if (w == 0 && l < 32) PMAXu[(buf ^ 1) * 32 + l] = 0u;
       const float sg0 = x3_norm(m0), sg1 = x3_norm(m1);
-      const halfx2 S16 = halfx2{(_Float16)S, (_Float16)S};
       inv_t = x3_norm_inv(m0) * inv_S;
       inv_td = x3_norm_inv(m1) * inv_S;
-      // three planes (hi, hi S, lo S) of t sigma; 16-byte chunk g of pair n's
+      // two planes (hi, lo S) of t sigma (step 3 scales W2's hi plane by S
+      // instead of reading a third, hi S plane); 16-byte chunk g of pair n's
       // row (8 halfs) at g ^ tb_swz(n)
       _Float16* TBh = reinterpret_cast<_Float16*>(TB);
       const int o = n * kF + 8 * ((2 * w + (q >> 1)) ^ tb_swz(n)) + 4 * (q & 1);
@@ -1475,22 +1508,18 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       for (int st = 0; st < 2; ++st) {
         const float sg = st ? sg1 : sg0;
         const float* src = st ? tdb : tb;
-        halfx4 ph, phs, pl;
+        halfx4 ph, pl;
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
           halfx2 sh, sl;
           split2x2(src[i] * sg, src[i + 1] * sg, S, sh, sl);
-          const halfx2 shs = sh * S16;  // exact: S is a power of two
           ph[i] = sh[0];
           ph[i + 1] = sh[1];
-          phs[i] = shs[0];
-          phs[i + 1] = shs[1];
           pl[i] = sl[0];
           pl[i + 1] = sl[1];
         }
         *reinterpret_cast<halfx4*>(TBh + (0 * 2 + st) * 16 * kF + o) = ph;
-        *reinterpret_cast<halfx4*>(TBh + (1 * 2 + st) * 16 * kF + o) = phs;
-        *reinterpret_cast<halfx4*>(TBh + (2 * 2 + st) * 16 * kF + o) = pl;
+        *reinterpret_cast<halfx4*>(TBh + (1 * 2 + st) * 16 * kF + o) = pl;
       }
     } else {
       *reinterpret_cast<float4*>(TB + oTBw) = f4(tb[0], tb[1], tb[2], tb[3]);
@@ -1514,14 +1543,17 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       for (int sb = 0; sb < 4; ++sb) {
         const int oa = (w * 4 + sb) * MLCG_WAVE + l;
         const halfx8 ah = w2hv[oa], al = w2hv[kF * kF / 8 + oa];
+        // hi_A S in fp16: exact (S a power of two, |W2| S < 2^14)
+        const halfx8 ahs = ah * (_Float16)S;
         const int ob = (n * kF + 8 * ((4 * sb + q) ^ tb_swz(n))) / 8;
         constexpr int kP = 16 * kF / 8;  // halfx8 per (plane, stream)
-        // planes of t: (hi, hi S, lo S) at (0, 2, 4) kP, of t' at (1, 3, 5) kP;
-        // S sigma A t ~ hi_A (hi_t S) + hi_A (lo_t S) + (lo_A S) hi_t
-        const halfx8 t0h = tbh[ob], t0s = tbh[2 * kP + ob], t0l = tbh[4 * kP + ob];
-        const halfx8 t1h = tbh[kP + ob], t1s = tbh[3 * kP + ob], t1l = tbh[5 * kP + ob];
-        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t0s, hb, 0, 0, 0);
-        hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t1s, hdb, 0, 0, 0);
+        // planes of t: (hi, lo S) at (0, 2) kP, of t' at (1, 3) kP;
+        // S sigma A t ~ (hi_A S) hi_t + hi_A (lo_t S) + (lo_A S) hi_t, the
+        // first product equal to hi_A (hi_t S) bit for bit
+        const halfx8 t0h = tbh[ob], t0l = tbh[2 * kP + ob];
+        const halfx8 t1h = tbh[kP + ob], t1l = tbh[3 * kP + ob];
+        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, t0h, hb, 0, 0, 0);
+        hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, t1h, hdb, 0, 0, 0);
         hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t0l, hb, 0, 0, 0);
         hdb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, t1l, hdb, 0, 0, 0);
         hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, t0h, hb, 0, 0, 0);
@@ -1590,18 +1622,18 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const float4 x1 =
           *reinterpret_cast<const float4*>(TT + oA4 + tt_at(16 * w + n, 8 * (q & 1) + 4));
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      halfx8 ah, ahs, al;
+      halfx8 ah, al;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         halfx2 sh, sl;
         split2x2(xv[j] * rw, xv[j + 1] * rw, kS4, sh, sl);
         ah[j] = sh[0];
         ah[j + 1] = sh[1];
-        ahs[j] = (_Float16)((float)sh[0] * kS4);
-        ahs[j + 1] = (_Float16)((float)sh[1] * kS4);
         al[j] = sl[0];
         al[j + 1] = sl[1];
       }
+      // hi S4 in fp16: exact (a power of two; |hi| < 4), packed multiplies
+      const halfx8 ahs = ah * (_Float16)kS4;
       const halfx8* hth = reinterpret_cast<const halfx8*>(HT);
 #pragma unroll
       for (int u = 0; u < kFT; ++u) {
@@ -1627,6 +1659,25 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       }
     }
     }
+    // the next tile's basis, envelope and pair adjoints t, t': independent of
+    // step 4, so their arithmetic can issue among its MFMAs
+    const BasisV bv = basis_eval(nxt);
+    cc_cur = bv.cc;
+    dcc_cur = bv.dcc;
+    float pm0, pm1;
+    pair_adjoints_eval(wb_nxt, wdb_nxt, cc_cur, dcc_cur, pm0, pm1);
+    if constexpr (kX3) {
+      // scheduling hint for the region above: the operand loads and splits
+      // first, then each MFMA of step 4 followed by a few of the independent
+      // VALU instructions of the next tile's basis
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+      __builtin_amdgcn_sched_group_barrier(0x002, 24, 0);  // VALU
+#pragma unroll
+      for (int i = 0; i < 3 * kFT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      }
+    }
     // 5. publish ab, ab' (and store them per pair when the basis parameters
     //    need gradients) and the next tile's basis
 #pragma unroll
@@ -1640,8 +1691,8 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       *reinterpret_cast<float4*>(adbar_out + p * kF + fcol) =
           f4(adbv[0], adbv[1], adbv[2], adbv[3]);
     }
-    basis(nxt, buf ^ 1, cc_cur, dcc_cur);
-    pair_adjoints(wb_nxt, wdb_nxt, cc_cur, dcc_cur, buf ^ 1);
+    basis_store(bv, buf ^ 1);
+    pair_adjoints_store(pm0, pm1, buf ^ 1);
     __syncthreads();
     // 6. dW1[16w + m][k] += sum_pairs ab[pair][16w + m] g[pair][k]
     if constexpr (kX3) {
@@ -1661,18 +1712,18 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       const float4 x1 =
           *reinterpret_cast<const float4*>(AT + oA6 + tt_at(16 * w + n, 8 * (q & 1) + 4));
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      halfx8 ah, ahs, al;
+      halfx8 ah, al;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         halfx2 sh, sl;
         split2x2(xv[j] * ra, xv[j + 1] * ra, kS4, sh, sl);
         ah[j] = sh[0];
         ah[j + 1] = sh[1];
-        ahs[j] = (_Float16)((float)sh[0] * kS4);
-        ahs[j + 1] = (_Float16)((float)sh[1] * kS4);
         al[j] = sl[0];
         al[j + 1] = sl[1];
       }
+      // hi S4 in fp16: exact (a power of two; |hi| < 4), packed multiplies
+      const halfx8 ahs = ah * (_Float16)kS4;
       // B: halfx8 of plane rows 16kt + n, stream q >> 1, pairs 8 (q & 1) .. + 7
       const halfx8* gth = reinterpret_cast<const halfx8*>(GT);
       const int oB6 = (q >> 1) * 2 * kRows + 2 * n + (q & 1);
