@@ -477,9 +477,9 @@ def radius_leg(reps=10):
     """Config 3 radius graph, inputs resident in HBM.  Figures: the exactly
     sized call end to end (sizing pass, one host synchronisation to size the
     output as the reference's radius.cu:288, write pass), the fixed-capacity
-    call (one launch plus its clearing kernel, no synchronisation: the form a
-    captured step uses), and the device time of each entry point (HIP events
-    around the call); the roofline takes the fixed-capacity form's."""
+    call (one launch, no synchronisation: the form a captured step uses),
+    and the device time of each entry point (HIP events around the call);
+    the roofline takes the fixed-capacity form's."""
     import torch
 
     from mlcg_amd import _lib, ops, synthetic
@@ -538,8 +538,8 @@ def radius_leg(reps=10):
             "algorithmic_bytes": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                         "time": "device time of mlcg_radius_graph (clearing kernel + "
-                                 "one-launch sweep, look-back and write)"}}
+                         "time": "device time of mlcg_radius_graph (one launch: sweep, "
+                                 "look-back and write)"}}
 
 
 def fp16_leg(reps=5):

@@ -131,14 +131,19 @@ int mlcg_radius_fill(const float* pos, const int64_t* batch,
                      int32_t* pair_ij, int32_t* eid2pair, int32_t* overflow,
                      void* stream);
 
-/* Bytes of the workspace of mlcg_radius_rowptr / mlcg_radius_graph for
- * n_nodes rows (a ticket counter and one status word per 64-row block); the
- * calls clear it themselves, on their stream. */
+/* Bytes of the workspace of mlcg_radius_rowptr / mlcg_radius_graph for up
+ * to n_nodes rows: a two-word header (a call counter, the most blocks a call
+ * has used) and two status words per block of at least 32 rows.  The caller
+ * zero-fills it once, before its first use; every call then leaves it ready
+ * for the next call (no clearing between calls), so one workspace serves a
+ * sequence of calls on one stream, of any sizes up to n_nodes.  Calls that
+ * may overlap (other streams) need workspaces of their own.  After a call
+ * that reports overflow bit 8 the workspace must be zero-filled again. */
 int64_t mlcg_radius_workspace_bytes(int64_t n_nodes);
 
-/* Sizing pass in one launch (plus a clearing kernel): per-row kept counts
- * (membership, exclusion and max_num_neighbors rules of mlcg_radius_count)
- * scanned within 64-row blocks and across blocks by a decoupled look-back,
+/* Sizing pass in one launch: per-row kept counts (membership, exclusion and
+ * max_num_neighbors rules of mlcg_radius_count) scanned within blocks of 32
+ * to 256 rows and across blocks by a decoupled look-back,
  * written as the CSR: rowptr[n_nodes + 1] (edges) and, when non-NULL,
  * pairptr[n_nodes + 1] (upper edges j > i).  *overflow is cleared, then gets
  * bit value 1 when a row exceeded max_num_neighbors, 4 for an asymmetric
@@ -164,8 +169,8 @@ int mlcg_radius_rowptr_f64(const double* pos, const int64_t* batch,
                            int32_t* pairptr, void* workspace, int32_t* overflow,
                            void* stream);
 
-/* The whole radius graph in one launch (plus a clearing kernel), for callers
- * that give a capacity instead of reading the edge count back: the sweep,
+/* The whole radius graph in one launch, for callers that give a capacity
+ * instead of reading the edge count back: the sweep,
  * the look-back of mlcg_radius_rowptr and the writes of mlcg_radius_fill,
  * with each row's distances tested once.  rowptr / pairptr come out clamped
  * to edge_capacity / pair_capacity, so every consumer stays inside the

@@ -204,10 +204,10 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Row-block kernel of the radius graph.  A workgroup of kRBWaves waves takes a
-// block of kRBWaves R consecutive rows, wave w the rows w R .. w R + R - 1
-// (R rows per wave, see RowsPerWave), so that each wave writes one contiguous run of the edge
-// list.  The nodes of the block's frames -- a contiguous node range, as frames
+// Row-block kernel of the radius graph.  A workgroup of W waves (BlockWaves)
+// takes a block of W R consecutive rows, wave w the rows w R .. w R + R - 1
+// (R rows per wave, see RowsPerWave), so that each wave writes one contiguous
+// run of the edge list.  The nodes of the block's frames -- a contiguous node range, as frames
 // are -- are staged in LDS as 4-component records when they fit
 // (StageNodes<T>); a block whose frames are larger reads positions from
 // global memory.
@@ -223,11 +223,12 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 // - the self pair (j = i) is taken out once per row, not per candidate: the
 //   count from the same distance test (d(i, i) < r^2 is what the sweep saw),
 //   the mask bit when the write pass reads the row's masks;
-// - the masks of a row's first kMaskWords chunks go to LDS (one write per
-//   chunk for the kGroup rows); rows with pair exclusions and groups that
-//   straddle frames or are not staged take a general path that tests every
-//   condition per lane, and rows longer than kMaskWords chunks are tested
-//   again in the write pass.
+// - the masks of a row's first kMaskWords chunks go to LDS, laid out
+//   [chunk][row] so that lane 0 stores a group's kGroup masks of a chunk as
+//   one 32-byte record straight from the ballots; rows with pair exclusions
+//   and groups that straddle frames or are not staged take a general path
+//   that tests every condition per lane, and rows longer than kMaskWords
+//   chunks are tested again in the write pass.
 // Rows keep their lowest-index neighbours when max_num_neighbors binds
 // (radius.cu:125-141): kept = min(hits, max_nn), and the kept upper neighbours
 // (j > i) are what remains after the lower ones and the self loop.
@@ -247,11 +248,26 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 // only for blocks of lower index, which the dispatcher started before it (it
 // dispatches workgroups in index order), and every wait is bounded
 // (kSpinLimit polls): a block that gives up sets overflow bit 8 and carries
-// on, so the kernel always finishes and the host reports the error.  The
-// workspace is cleared by radius_ws_init on the same stream before every such
-// launch.
-constexpr int kRBWaves = 4;
+// on, so the kernel always finishes and the host reports the error.
+// Workspace (zero-filled by the caller before its first use, then reused):
+// word 0 the launch epoch, word 1 the most blocks any launch has used, then
+// two interleaved status arrays -- block b's status of a launch with epoch e
+// at word 2 + 2b + (e & 1).  Every block reads the two header words first;
+// each launch clears the other array's words up to the larger of the two
+// block counts, and its last block advances the header after its look-back
+// (by then every block has published, so every block has read the header).
+// The next launch's array is therefore zero wherever it reads, with no
+// clearing launch in between.  The caller's overflow word is cleared by
+// block 0 before it publishes its prefix, and every block raises its bits
+// only after its own look-back has reached that prefix.
 enum { kModeRowptr = 0, kModeFill = 1, kModeFused = 2 };
+// Waves per workgroup: 4 in kModeFill; 8 in the look-back modes, whose
+// larger blocks halve the look-back chain (512 blocks of 400 rows on 204,800
+// rows) -- the chain the last blocks wait for before they write.
+template <int kMode>
+struct BlockWaves {
+  static constexpr int value = kMode == kModeFill ? 4 : 8;
+};
 // Rows per wave: 16 in kModeFill, which has no look-back and gains from many
 // waves hiding each other's latencies; 8 to 64 (at most one per lane) in the
 // look-back modes, where larger blocks amortise the staging, the block scan
@@ -297,6 +313,7 @@ __device__ __forceinline__ Vec3T<T> load_pos(const Pos4<T>* __restrict__ sp, int
 constexpr uint64_t kVal31 = 0x7fffffffull;
 constexpr uint64_t kFlagAgg = 1ull << 62;
 constexpr uint64_t kFlagPre = 2ull << 62;
+constexpr int kStatStride = 2;  // the workspace's two status arrays interleave
 
 __device__ __forceinline__ uint64_t pack_status(uint64_t flag, uint64_t e, uint64_t p) {
   return flag | ((p < kVal31 ? p : kVal31) << 31) | (e < kVal31 ? e : kVal31);
@@ -313,7 +330,8 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
   return v;
 }
 
-// Decoupled look-back of block t (one full wave): publishes the aggregate,
+// Decoupled look-back of block t (one full wave; statuses kStatStride words
+// apart from st): publishes the aggregate,
 // sums the predecessors' aggregates back to the first inclusive prefix,
 // publishes the inclusive prefix and returns the exclusive one.  A round reads
 // kLookLanes x 64 statuses, entry o = kLookLanes l + q (lane l, slot q) being
@@ -326,13 +344,13 @@ __device__ __forceinline__ void lookback(uint64_t* __restrict__ st, int t, uint6
   pre_e = 0;
   pre_p = 0;
   if (t > 0) {
-    if (lane == 0) st_status(st + t, pack_status(kFlagAgg, agg_e, agg_p));
+    if (lane == 0) st_status(st + kStatStride * t, pack_status(kFlagAgg, agg_e, agg_p));
     for (int k = t - 1;; k -= kLookLanes * MLCG_WAVE) {
       uint64_t w[kLookLanes];
 #pragma unroll
       for (int q = 0; q < kLookLanes; ++q) {
         const int idx = k - kLookLanes * lane - q;
-        w[q] = idx >= 0 ? ld_status(st + idx) : kFlagPre;
+        w[q] = idx >= 0 ? ld_status(st + kStatStride * idx) : kFlagPre;
       }
       int first_pre = 0, first_missing = 0;  // in entry order, 1 << 30 when absent
       for (int spins = 0;; ++spins) {
@@ -363,7 +381,7 @@ __device__ __forceinline__ void lookback(uint64_t* __restrict__ st, int t, uint6
 #pragma unroll
         for (int q = 0; q < kLookLanes; ++q) {
           const int idx = k - kLookLanes * lane - q;
-          if ((w[q] >> 62) == 0) w[q] = ld_status(st + idx);
+          if ((w[q] >> 62) == 0) w[q] = ld_status(st + kStatStride * idx);
         }
       }
       // sum the entries up to and including the nearest inclusive prefix
@@ -379,9 +397,10 @@ __device__ __forceinline__ void lookback(uint64_t* __restrict__ st, int t, uint6
       if (first_pre < (1 << 30)) break;
     }
   }
+  // (the inclusive prefix is stored after the loads it sums have returned)
   const uint64_t inc_e = pre_e + agg_e, inc_p = pre_p + agg_p;
   if (inc_e > kVal31 || inc_p > kVal31) ov |= kOvInt32;
-  if (lane == 0) st_status(st + t, pack_status(kFlagPre, inc_e, inc_p));
+  if (lane == 0) st_status(st + kStatStride * t, pack_status(kFlagPre, inc_e, inc_p));
 }
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int k) {
@@ -416,13 +435,28 @@ struct GroupCounts {
   uint32_t slf[kGroup];  // the self hit (loop only)
 };
 
+// A group's masks of one chunk: the kGroup rows are consecutive in the
+// [chunk][row] mask layout, so lane 0 stores them as one 32-byte record
+// straight from the ballots.
+typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+static_assert(kGroup == 4, "two 16-byte stores per group");
+__device__ __forceinline__ void store_group_masks(uint64_t* __restrict__ d,
+                                                  const uint64_t (&m)[kGroup]) {
+  if (mlcg_lane() == 0) {
+    u64x2* q = reinterpret_cast<u64x2*>(d);
+    q[0] = u64x2{m[0], m[1]};
+    q[1] = u64x2{m[2], m[3]};
+  }
+}
+
 // Fast sweep: kGroup rows ii[] of one staged frame [st, en), no exclusions.
 // Lanes past the frame read the sentinel record sp[kStage] (+inf), whose
-// distance never passes the test, so no lane mask is needed.  Masks of the
-// first kMaskWords chunks go to smask_g (row u at u * kMaskWords) when kMasks,
-// the self bit included; the caller takes the self pair out of the counts.
-// kLow accumulates the hits below the diagonal.
-template <bool kMasks, bool kLow, int kStage, typename T>
+// distance never passes the test, so no lane mask is needed; each chunk's
+// candidates are read from LDS one chunk ahead.  Masks of the first
+// kMaskWords chunks go to smask_g (chunk c of row u at c * kRS + u) when
+// kMasks, the self bit included; the caller takes the self pair out of the
+// counts.  kLow accumulates the hits below the diagonal.
+template <bool kMasks, bool kLow, int kStage, int kRS, typename T>
 __device__ __forceinline__ void sweep_fast(const Pos4<T>* __restrict__ sp, int base,
                                            const int (&ii)[kGroup], int st, int en, int nch,
                                            T r2, uint64_t* __restrict__ smask_g,
@@ -433,17 +467,19 @@ __device__ __forceinline__ void sweep_fast(const Pos4<T>* __restrict__ sp, int b
   for (int u = 0; u < kGroup; ++u) a[u] = load_pos(sp, ii[u] - base);
   const int jend = en - base;
   int idx = st - base + lane;
-  for (int c = 0; c < nch; ++c, idx += MLCG_WAVE) {
-    const Vec3T<T> p = load_pos(sp, idx < jend ? idx : kStage);
-    uint64_t mv = 0;  // lane u: row u's mask
+  Vec3T<T> p = load_pos(sp, idx < jend ? idx : kStage);
+  for (int c = 0; c < nch; ++c) {
+    idx += MLCG_WAVE;
+    const Vec3T<T> pn = load_pos(sp, idx < jend ? idx : kStage);  // the next chunk's
+    uint64_t m[kGroup];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
-      const uint64_t m = __ballot(sqdist_exact(a[u], p) < r2);
-      gc.tot[u] += (uint32_t)__popcll(m);
-      if (kLow) gc.low[u] += (uint32_t)__popcll(m & low_lanes(ii[u] - st - MLCG_WAVE * c));
-      if (kMasks && __builtin_amdgcn_inverse_ballot_w64(1ull << u)) mv = m;  // lane u only
+      m[u] = __ballot(sqdist_exact(a[u], p) < r2);
+      gc.tot[u] += (uint32_t)__popcll(m[u]);
+      if (kLow) gc.low[u] += (uint32_t)__popcll(m[u] & low_lanes(ii[u] - st - MLCG_WAVE * c));
     }
-    if (kMasks && c < kMaskWords && lane < kGroup) smask_g[lane * kMaskWords + c] = mv;
+    if (kMasks && c < kMaskWords) store_group_masks(smask_g + c * kRS, m);
+    p = pn;
   }
 }
 
@@ -451,7 +487,7 @@ __device__ __forceinline__ void sweep_fast(const Pos4<T>* __restrict__ sp, int b
 // tested per lane; counts accumulate in scalars, masks of the first
 // kMaskWords chunks go to smask_g as in sweep_fast.  With kAsym a kept (i, j)
 // whose (j, i) is excluded sets asym.
-template <bool kExcl, bool kMasks, bool kAsym, typename PosT, typename T>
+template <bool kExcl, bool kMasks, bool kAsym, int kRS, typename PosT, typename T>
 __device__ __forceinline__ void sweep_general(
     const PosT* __restrict__ P, int base, const int (&ii)[kGroup], const int (&st)[kGroup],
     const int (&en)[kGroup], int nch, T r2, int loop, const int64_t* __restrict__ exs,
@@ -470,7 +506,7 @@ __device__ __forceinline__ void sweep_general(
     }
   }
   for (int c = 0; c < nch; ++c) {
-    uint64_t mv = 0;  // lane u: row u's mask
+    uint64_t mm[kGroup];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
       const int jb = st[u] + MLCG_WAVE * c;
@@ -479,13 +515,13 @@ __device__ __forceinline__ void sweep_general(
           test_candidate<kExcl>(P, base, a[u], ii[u], j, en[u], r2, loop, exs, x_lo[u], x_hi[u]);
       if (kAsym && hit && in_sorted(exs, eptr[j], eptr[j + 1], (int64_t)ii[u])) asym = true;
       const uint64_t m = __ballot(hit);
-      if (kMasks) mv = lane == u ? m : mv;
+      mm[u] = m;
       gc.tot[u] += (uint32_t)__popcll(m);
       const int d = ii[u] - jb;  // lanes below d hold j < i
       gc.low[u] += (uint32_t)__popcll(m & low_lanes(d));
       if (d >= 0 && d < MLCG_WAVE) gc.slf[u] += (uint32_t)((m >> d) & 1);
     }
-    if (kMasks && c < kMaskWords && lane < kGroup) smask_g[lane * kMaskWords + c] = mv;
+    if (kMasks && c < kMaskWords) store_group_masks(smask_g + c * kRS, mm);
   }
 }
 
@@ -583,7 +619,7 @@ __device__ __forceinline__ void emit_chunk(uint64_t m, int jb, int i, int mnn, i
 }
 
 template <int kMode, bool kExcl, bool kPairs, typename T>
-__global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
+__global__ __launch_bounds__(BlockWaves<kMode>::value * MLCG_WAVE) void radius_rows_kernel(
     const T* __restrict__ pos, const int64_t* __restrict__ batch,
     const int64_t* __restrict__ frame_ptr, int n, T r2, int loop, int mnn,
     const int64_t* __restrict__ exs, const int64_t* __restrict__ eptr,
@@ -595,11 +631,13 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
   constexpr bool kScan = kMode != kModeFill;
   constexpr bool kWrite = kMode != kModeRowptr;
   constexpr int kMaxRows = RowsPerWave<kMode>::value;  // rows per wave at most
+  constexpr int kRBWaves = BlockWaves<kMode>::value;
   constexpr bool kMasks = kWrite || kPairs;  // kPairs needs the lower counts from the sweep
   constexpr bool kLow = kPairs;
   constexpr int kStage = StageNodes<T>::value;
   __shared__ Pos4<T> sp[kStage + 1];  // + the sentinel record
-  __shared__ uint64_t smask[kMasks ? kRBWaves * kMaxRows * kMaskWords : 1];
+  __shared__ __attribute__((aligned(16))) uint64_t
+      smask[kMasks ? kRBWaves * kMaxRows * kMaskWords : 2];
   __shared__ int64_t swt[2 * kRBWaves];  // per-wave totals (edges, pairs), then offsets
   __shared__ uint64_t spre[2];
 
@@ -613,6 +651,18 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
   const int nblocks = (n + rb - 1) / rb;
   const int r0 = t * rb;
   const int r1 = r0 + rb < n ? r0 + rb : n;
+  // look-back modes: the workspace header, then this launch's share of the
+  // clearing of the other status array (the next launch's)
+  uint64_t ws_epoch = 0, ws_mark = 0;
+  if (kScan) {
+    ws_epoch = ld_status(ws);
+    ws_mark = ld_status(ws + 1);
+    const int64_t clear = (int64_t)ws_mark > nblocks ? (int64_t)ws_mark : nblocks;
+    uint64_t* other = ws + 2 + (int)((ws_epoch + 1) & 1);
+    for (int64_t b = (int64_t)t * blockDim.x + threadIdx.x; b < clear;
+         b += (int64_t)nblocks * blockDim.x)
+      st_status(other + kStatStride * b, 0);
+  }
   // the block's node window (node indices are below 2^31: int32 CSR)
   const int c_lo = (int)frame_ptr[batch[r0]];
   const int c_hi = (int)frame_ptr[batch[r1 - 1] + 1];
@@ -658,7 +708,8 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     selfm = __ballot(sh);
   }
 
-  // sweep: masks of row k at smask_w[k * kMaskWords]; per-row counts to lane k
+  // sweep: chunk c of row k's mask at smask_w[c * kMaxRows + k]; per-row
+  // counts to lane k
   uint64_t* smask_w = smask + (kMasks ? wv * kMaxRows * kMaskWords : 0);
   int my_tot = 0, my_low = 0, my_slf = 0;
   uint64_t fastm = 0;  // rows swept by the fast path
@@ -677,11 +728,11 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     GroupCounts gc;
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) gc.tot[u] = gc.low[u] = gc.slf[u] = 0;
-    uint64_t* smask_g = smask_w + g * kMaskWords;
+    uint64_t* smask_g = smask_w + g;
     if (fast) {  // wave-uniform
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) ii[u] = rw0 + g + u;
-      sweep_fast<kMasks, kLow, kStage>(sp, base, ii, st0, en0,
+      sweep_fast<kMasks, kLow, kStage, kMaxRows>(sp, base, ii, st0, en0,
                                        (en0 - st0 + MLCG_WAVE - 1) / MLCG_WAVE, r2, smask_g, gc);
       fastm |= (uint64_t)((1u << kGroup) - 1) << g;
     } else {
@@ -702,11 +753,11 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
         local = local && st[u] >= c_lo && en[u] <= c_hi && ii[u] >= c_lo && ii[u] < c_hi;
       }
       if (local)
-        sweep_general<kExcl, kMasks, kExcl && kScan>(sp, base, ii, st, en, nch, r2, loop, exs,
-                                                     eptr, smask_g, gc, asym);
+        sweep_general<kExcl, kMasks, kExcl && kScan, kMaxRows>(
+            sp, base, ii, st, en, nch, r2, loop, exs, eptr, smask_g, gc, asym);
       else
-        sweep_general<kExcl, kMasks, kExcl && kScan>(pos, 0, ii, st, en, nch, r2, loop, exs,
-                                                     eptr, smask_g, gc, asym);
+        sweep_general<kExcl, kMasks, kExcl && kScan, kMaxRows>(
+            pos, 0, ii, st, en, nch, r2, loop, exs, eptr, smask_g, gc, asym);
     }
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
@@ -729,7 +780,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
       my_tot -= 1;
       if (kMasks && my_nch <= kMaskWords) {
         const int off = my_i - my_st;
-        uint64_t* wd = smask_w + lane * kMaskWords + (off >> 6);
+        uint64_t* wd = smask_w + (off >> 6) * kMaxRows + lane;
         *wd &= ~(1ull << (off & 63));
       }
     }
@@ -765,7 +816,17 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
       const uint64_t agg_e = readlane64((uint64_t)iwe, kRBWaves - 1);
       const uint64_t agg_p = readlane64((uint64_t)iwp, kRBWaves - 1);
       uint64_t le, lp;
-      lookback(ws + 1, t, agg_e, agg_p, le, lp, ov);
+      if (t == 0 && lane == 0 && overflow) {  // done before the first prefix is published
+        __hip_atomic_store(overflow, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // wait for the store itself (an agent-scope release fence would also
+        // write back this XCD's L2, which the status words do not need)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      lookback(ws + 2 + (int)(ws_epoch & 1), t, agg_e, agg_p, le, lp, ov);
+      if (t == nblocks - 1 && lane == 0) {  // every block has read the header
+        st_status(ws + 1, (int64_t)ws_mark > nblocks ? ws_mark : (uint64_t)nblocks);
+        st_status(ws, ws_epoch + 1);
+      }
       if (lane < kRBWaves) {  // every lane read its swt entry before these writes
         swt[lane] = (int64_t)le + iwe - we;
         swt[kRBWaves + lane] = (int64_t)lp + iwp - wp;
@@ -777,8 +838,9 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
     }
     if (trunc) ov |= kOvTruncated;
     if (__ballot(asym)) ov |= kOvAsymmetric;
-    if (ov && lane == 0 && overflow) atomicOr(overflow, ov);
     __syncthreads();
+    // after wave 0's look-back, hence after block 0 cleared the overflow word
+    if (ov && lane == 0 && overflow) atomicOr(overflow, ov);
     pre_e = (uint64_t)swt[wv];
     pre_p = (uint64_t)swt[kRBWaves + wv];
     // the CSR, clamped to the capacities in the fused form
@@ -821,7 +883,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
       const int64_t e_base = (int64_t)readlane64((uint64_t)my_e, k);
       const int64_t p_base = kPairs ? (int64_t)readlane64((uint64_t)my_p, k) : 0;
       if ((fastw >> k) & 1) {  // wave-uniform
-        const uint64_t w = lane < nch ? smask_w[k * kMaskWords + lane] : 0ull;
+        const uint64_t w = lane < nch ? smask_w[lane * kMaxRows + k] : 0ull;
         emit_row_fast<kPairs>(w, nch, st, i, e_base, p_base, ei0, ei1, col, pi, pj, eid2pair);
         continue;
       }
@@ -829,7 +891,7 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
       bool dropped = false;
       int kept = 0, ukept = 0;
       if (nch <= kMaskWords) {
-        const uint64_t w = lane < nch ? smask_w[k * kMaskWords + lane] : 0ull;
+        const uint64_t w = lane < nch ? smask_w[lane * kMaxRows + k] : 0ull;
         for (int c = 0; c < nch && kept < mnn; ++c) {
           const uint64_t m = readlane64(w, c);
           if (m)
@@ -861,17 +923,6 @@ __global__ __launch_bounds__(kRBWaves * MLCG_WAVE) void radius_rows_kernel(
       if (__ballot(dropped) && lane == 0 && overflow) atomicOr(overflow, (int)kOvCapacity);
     }
   }
-}
-
-// Clears the look-back workspace (one unused word + the status words) and the overflow
-// word before a kModeRowptr / kModeFused launch (a kernel rather than a
-// memset node, so the sequence stays safe inside captured graphs).
-__global__ void radius_ws_init(uint64_t* __restrict__ ws, int64_t words,
-                               int32_t* __restrict__ overflow) {
-  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < words;
-       k += (int64_t)gridDim.x * blockDim.x)
-    ws[k] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0 && overflow) *overflow = 0;
 }
 
 // n == 0: the CSR is the single offset 0.
@@ -1131,13 +1182,11 @@ int launch_radius_rows(int mode, const T* pos, const int64_t* batch, const int64
   const int mnn = max_num_neighbors < (int64_t)INT32_MAX ? (int)max_num_neighbors : INT32_MAX;
   const int n = (int)n_nodes;
   const int rpw = mode == kModeFill ? RowsPerWave<kModeFill>::value : scan_rows_per_wave(n_nodes);
-  const int64_t rb = (int64_t)kRBWaves * rpw;
+  const int bw = mode == kModeFill ? BlockWaves<kModeFill>::value : BlockWaves<kModeFused>::value;
+  const int64_t rb = (int64_t)bw * rpw;
   const int64_t nblocks = (n_nodes + rb - 1) / rb;
   uint64_t* ws = static_cast<uint64_t*>(workspace);
-  if (mode != kModeFill)
-    hipLaunchKernelGGL(radius_ws_init, dim3(mlcg_persistent_groups(mlcg_div_up(nblocks + 1, 256), 4)),
-                       dim3(256), 0, s, ws, nblocks + 1, overflow);
-  const dim3 grid((unsigned)nblocks), block(kRBWaves * MLCG_WAVE);
+  const dim3 grid((unsigned)nblocks), block(bw * MLCG_WAVE);
   const bool ex = exclude_pair_xs != nullptr;
 #define MLCG_ROWS_LAUNCH(MODE, EX, PR)                                                      \
   hipLaunchKernelGGL((radius_rows_kernel<MODE, EX, PR, T>), grid, block, 0, s, pos, batch,  \
@@ -1301,8 +1350,8 @@ extern "C" int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
 
 extern "C" int64_t mlcg_radius_workspace_bytes(int64_t n_nodes) {
   if (n_nodes < 0) return 0;
-  const int64_t rb = (int64_t)kRBWaves * kMinScanRows;
-  return 8 * ((n_nodes + rb - 1) / rb + 1);
+  const int64_t rb = (int64_t)BlockWaves<kModeFused>::value * kMinScanRows;
+  return 8 * (2 + kStatStride * ((n_nodes + rb - 1) / rb));
 }
 
 extern "C" int mlcg_radius_rowptr(const float* pos, const int64_t* batch,

@@ -142,6 +142,28 @@ def _check_radius_flags(overflow: int) -> None:
                            "its predecessors")
 
 
+# Look-back workspaces of the radius graph, one per (device, stream): zero-filled
+# once, and every call leaves its workspace ready for the next call on that
+# stream (mlcg_radius_workspace_bytes).
+_RADIUS_WS: dict = {}
+
+
+def _radius_workspace(n: int, dev: torch.device) -> Tuple[torch.Tensor, Optional[tuple]]:
+    """The workspace for n rows on the current stream, and its cache key
+    (None for a fresh one).  Inside a stream capture the graph gets a
+    zero-filled workspace of its own (its replays may run on any stream)."""
+    words = max(1, _lib.load().mlcg_radius_workspace_bytes(n) // 8)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(words, dtype=torch.int64, device=dev), None
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _RADIUS_WS.get(key)
+    if ws is None or ws.numel() < words:
+        ws = torch.zeros(words, dtype=torch.int64, device=dev)
+        _RADIUS_WS[key] = ws
+    return ws, key
+
+
 def radius_graph(
     pos: torch.Tensor,
     r: float,
@@ -218,8 +240,7 @@ def radius_graph(
     rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     pairptr = torch.empty(n + 1, dtype=torch.int32, device=dev) if with_pairs else None
     flags = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the kernels
-    ws = torch.empty(max(1, _lib.load().mlcg_radius_workspace_bytes(n) // 8), dtype=torch.int64,
-                     device=dev)
+    ws, ws_key = _radius_workspace(n, dev)
     if capacity is None:
         # sizing pass (counts, block scan, look-back) -> rowptr / pairptr, then
         # one host sync to size the outputs (the reference syncs at radius.cu:288)
@@ -230,6 +251,9 @@ def radius_graph(
             e_count, p_count, overflow = torch.cat([rowptr[n:], pairptr[n:], flags]).tolist()
         else:
             (e_count, overflow), p_count = torch.cat([rowptr[n:], flags]).tolist(), 0
+        if overflow & 8 and ws_key is not None:
+            # a block gave up waiting: the workspace's state is no longer known
+            _RADIUS_WS.pop(ws_key, None)
         _check_radius_flags(overflow)
         if with_pairs and overflow & 1:
             raise RuntimeError(

@@ -7,10 +7,12 @@ The cases reach every path of the kernel: frames staged in LDS and frames too
 large to stage, rows whose hit masks are kept (up to 512 candidates) and
 longer rows that are tested again in the write pass, from LDS or from global
 memory, blocks that span many small frames, more than 256 predecessors in the
-look-back (config 3 has 800 blocks of 256 rows), a binding max_num_neighbors, self loops, pair exclusions, float64
-positions, a capacity that is too small and an empty input.  The reference's
-own sweep (test_radius.py:31-104) stops at 100 nodes; the larger cases here
-follow its construction (uniform positions, frames by percentage split)."""
+look-back (config 3 has 1,024 blocks of 200 rows), a binding
+max_num_neighbors, self loops, pair exclusions, float64 positions, a
+capacity that is too small, an empty input and one workspace reused by calls
+of different sizes.  The reference's own sweep (test_radius.py:31-104) stops
+at 100 nodes; the larger cases here follow its construction (uniform
+positions, frames by percentage split)."""
 
 import numpy as np
 import pytest
@@ -166,28 +168,51 @@ def test_empty_input():
         assert g.rowptr.cpu().tolist() == [0] and int(g.flags.item()) == 0
 
 
-def test_rowptr_entry_point_repeated():
-    """mlcg_radius_rowptr through the C ABI, three calls in a row on one
-    workspace (the call clears it): the CSR equals the oracle's each time."""
+def test_workspace_reused_across_sizes_and_forms():
+    """One zero-filled workspace through a sequence of calls of both look-back
+    entry points (mlcg_radius_rowptr, mlcg_radius_graph) whose row counts, and
+    so block counts, rise, fall and rise again: every CSR and edge list equals
+    the oracle's, the overflow word comes back cleared from garbage, and after
+    each call the header counts the calls and the status words the next call
+    will read are zero (no clearing launch between calls)."""
     from mlcg_amd import _lib, ops
 
-    pos, batch, r = _case("config3")
-    n = pos.shape[0]
-    ref, _ = oracle_radius.radius_graph(pos, r, batch, False, 1000)
-    want = _rowptr_ref(ref, n)
-    p = torch.from_numpy(pos).cuda()
-    b = torch.from_numpy(batch).cuda()
-    fptr = ops.frame_ptr_from_batch(b, int(batch.max()) + 1)
     lib = _lib.load()
-    ws = torch.full((lib.mlcg_radius_workspace_bytes(n) // 8,), -1, dtype=torch.int64,
-                    device="cuda")
-    for _ in range(3):
+    seq = [("config3", "rowptr"), ("ragged", "graph"), ("long_rows", "rowptr"),
+           ("config3", "graph"), ("mid_rows", "graph"), ("huge_frame", "rowptr"),
+           ("config3", "rowptr")]
+    cases = {name: _case(name) for name, _ in seq}
+    n_max = max(c[0].shape[0] for c in cases.values())
+    ws = torch.zeros(lib.mlcg_radius_workspace_bytes(n_max) // 8, dtype=torch.int64,
+                     device="cuda")
+    P = _lib.ptr
+    for k, (name, form) in enumerate(seq):
+        pos, batch, r = cases[name]
+        n = pos.shape[0]
+        print(f"call {k}: {name} n={n} {form}", flush=True)
+        ref, _ = oracle_radius.radius_graph(pos, r, batch, False, 1000)
+        E = ref.shape[1]
+        p = torch.from_numpy(pos).cuda()
+        b = torch.from_numpy(batch).cuda()
+        fptr = ops.frame_ptr_from_batch(b, int(batch.max()) + 1)
         rowptr = torch.full((n + 1,), -7, dtype=torch.int32, device="cuda")
         flags = torch.full((1,), 99, dtype=torch.int32, device="cuda")
-        st = lib.mlcg_radius_rowptr(_lib.ptr(p), _lib.ptr(b), _lib.ptr(fptr), n, r, 0, 1000,
-                                    None, None, _lib.ptr(rowptr), None, _lib.ptr(ws),
-                                    _lib.ptr(flags), _lib.stream_handle())
+        if form == "rowptr":
+            st = lib.mlcg_radius_rowptr(P(p), P(b), P(fptr), n, r, 0, 1000, None, None,
+                                        P(rowptr), None, P(ws), P(flags), _lib.stream_handle())
+        else:
+            cap = E + 16
+            ei = torch.full((2, cap), -1, dtype=torch.int64, device="cuda")
+            st = lib.mlcg_radius_graph(P(p), P(b), P(fptr), n, r, 0, 1000, None, None,
+                                       P(rowptr), None, cap, cap, P(ei), None, 0, 0, None, None,
+                                       P(ws), P(flags), _lib.stream_handle())
         assert st == 0
         torch.cuda.synchronize()
         assert int(flags.item()) == 0
-        assert np.array_equal(rowptr.cpu().numpy(), want)
+        assert np.array_equal(rowptr.cpu().numpy(), _rowptr_ref(ref, n))
+        if form == "graph":
+            assert np.array_equal(ei[:, :E].cpu().numpy(), ref)
+        epoch, mark = ws[:2].cpu().tolist()
+        assert epoch == k + 1 and mark > 0
+        nxt = ws[2 + ((k + 1) & 1)::2][:mark]
+        assert int(nxt.abs().max().item()) == 0
