@@ -235,10 +235,13 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kSteps; ++u) part[u] = half_sum(part[u]);
+    // each pair has exactly one upper edge, so one add per address and launch:
+    // a returnless float atomic (performed in the L2) adds it without the
+    // dependent load of a read-modify-write holding up the next step
     if (m == 0)
 #pragma unroll
       for (int u = 0; u < kSteps; ++u)
-        if (up[u]) dbar[p[u]] += part[u];
+        if (up[u]) unsafeAtomicAdd(dbar + p[u], part[u]);
   }
   MLCG_ROW_LOOP_END
   acc = combine_halves(acc, h);
