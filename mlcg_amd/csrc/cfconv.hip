@@ -175,7 +175,10 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
 }
 
 // ybar[i] = sum_j gagg[j] W_ij (all edges) and, on the upper edges (i < j)
-// that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i>.
+// that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i>.  The steps of
+// upper edges keep kUp steps (four loads per edge) in flight: its registers
+// set the kernel's occupancy, lower-edge steps included.
+template <int kUp>
 __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     const float* __restrict__ gagg, const float* __restrict__ y, const void* __restrict__ W,
     const void* __restrict__ Wd, int w_f16, const int32_t* __restrict__ rowptr,
@@ -209,12 +212,12 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     fma4(acc, ld4(gagg, e.j, m), ldw4(W, f16, e.p, m));
   }
   // remaining steps: gather, plus the distance adjoint on upper edges
-  for (; k < cn; k += 2 * kSteps) {
-    float4 g[kSteps], w[kSteps], yj[kSteps], wd[kSteps];
-    int p[kSteps];
-    bool ok[kSteps], up[kSteps];
+  for (; k < cn; k += 2 * kUp) {
+    float4 g[kUp], w[kUp], yj[kUp], wd[kUp];
+    int p[kUp];
+    bool ok[kUp], up[kUp];
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) {
+    for (int u = 0; u < kUp; ++u) {
       const Edge e = edge_at(k + 2 * u < 62 ? k + 2 * u : 62, h, cn, my_col, my_pair, 0.f);
       const int ke = k + 2 * u + h;
       ok[u] = k + 2 * u < cn && ke < cn;
@@ -225,22 +228,22 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
       yj[u] = up[u] ? ld4(y, e.j, m) : f4zero();
       wd[u] = up[u] ? ldw4(Wd, f16, e.p, m) : f4zero();
     }
-    float part[kSteps];
+    float part[kUp];
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) {
+    for (int u = 0; u < kUp; ++u) {
       fma4(acc, g[u], w[u]);
       const float4 t{gi.x * yj[u].x + g[u].x * yi.x, gi.y * yj[u].y + g[u].y * yi.y,
                      gi.z * yj[u].z + g[u].z * yi.z, gi.w * yj[u].w + g[u].w * yi.w};
       part[u] = dot4(wd[u], t);
     }
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) part[u] = half_sum(part[u]);
+    for (int u = 0; u < kUp; ++u) part[u] = half_sum(part[u]);
     // each pair has exactly one upper edge, so one add per address and launch:
     // a returnless float atomic (performed in the L2) adds it without the
     // dependent load of a read-modify-write holding up the next step
     if (m == 0)
 #pragma unroll
-      for (int u = 0; u < kSteps; ++u)
+      for (int u = 0; u < kUp; ++u)
         if (up[u]) unsafeAtomicAdd(dbar + p[u], part[u]);
   }
   MLCG_ROW_LOOP_END
@@ -488,9 +491,18 @@ extern "C" int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const v
   MLCG_REQUIRE(n_nodes >= 0);
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(gagg && y && W && Wd && rowptr && col && eid2pair && ybar && dbar);
-  hipLaunchKernelGGL(gather_bwd_kernel, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
-                     mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
-                     n_nodes, ybar, dbar);
+  // upper steps in flight: 4 with fp32 filter rows (104 VGPRs, 4 waves per
+  // SIMD; config 2, 24 edges a row: 48 us against 54 with 2), 2 with fp16
+  // rows (68 VGPRs, 7 waves per SIMD; config 4, 47 edges a row: 0.61 ms
+  // against 0.89 with 4)
+  if (w_f16)
+    hipLaunchKernelGGL(gather_bwd_kernel<2>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
+                       mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
+                       n_nodes, ybar, dbar);
+  else
+    hipLaunchKernelGGL(gather_bwd_kernel<kSteps>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
+                       mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
+                       n_nodes, ybar, dbar);
   return mlcg_launch_status();
 }
 
