@@ -133,7 +133,7 @@ int mlcg_radius_fill(const float* pos, const int64_t* batch,
 
 /* Bytes of the workspace of mlcg_radius_rowptr / mlcg_radius_graph for up
  * to n_nodes rows: a two-word header (a call counter, the most blocks a call
- * has used) and two status words per block of at least 32 rows.  The caller
+ * has used) and two status words per block of at least 64 rows.  The caller
  * zero-fills it once, before its first use; every call then leaves it ready
  * for the next call (no clearing between calls), so one workspace serves a
  * sequence of calls on one stream, of any sizes up to n_nodes.  Calls that
