@@ -438,27 +438,78 @@ __global__ __launch_bounds__(256) void pair_forces_kernel(
 // a strided subset, then the partial sums are combined in a fixed tree order
 // in LDS.  Deterministic for a given launch shape, and accurate to a few ulp
 // even for the ~10^5-term per-frame sums of a pair prior.
-constexpr int kSegThreads = 256;
+constexpr int kSegThreads = 1024;
+constexpr int kSegWaves = kSegThreads / MLCG_WAVE;
+constexpr int kSegLoads = 4;  // 16-byte loads in flight per thread
 
+// Compensated (Kahan) accumulation of y into (s, c).
+__device__ __forceinline__ void kahan_add(float& s, float& c, float y) {
+  const float yy = y - c;
+  const float t = s + yy;
+  c = (t - s) - yy;
+  s = t;
+}
+
+// out[b] = sum of v[k * stride] over the frame's k in [ptr[b], ptr[b+1]).  One
+// workgroup per frame (grid-stride over frames); with stride 1 its 1024
+// threads read the frame as 16-byte vectors, kSegLoads in flight per thread,
+// after a scalar head up to 16-byte alignment and before a scalar tail (a
+// prior's per-interaction energies run to 71,556 values a frame).  Each
+// thread keeps a compensated sum over a fixed set of elements; the threads'
+// sums are added by a fixed butterfly within each wave and the wave sums in
+// wave order, so the result does not depend on timing.
 __global__ __launch_bounds__(kSegThreads) void segment_sum_kernel(
     const float* __restrict__ v, int64_t stride, const int64_t* __restrict__ ptr, int64_t nb,
     float* __restrict__ out) {
-  __shared__ float part[kSegThreads];
+  __shared__ float part[kSegWaves];
+  const int tid = threadIdx.x;
+  const int lane = mlcg_lane(), wv = tid / MLCG_WAVE;
   for (int64_t b = blockIdx.x; b < nb; b += gridDim.x) {
+    const int64_t k0 = ptr[b], k1 = ptr[b + 1];
     float s = 0.f, c = 0.f;
-    for (int64_t k = ptr[b] + threadIdx.x; k < ptr[b + 1]; k += kSegThreads) {
-      const float y = v[k * stride] - c;
-      const float t = s + y;
-      c = (t - s) - y;
-      s = t;
+    if (stride == 1) {
+      // aligned body [a0, a1) as float4, head [k0, a0) and tail [a1, k1) scalar
+      const int64_t a0 = k0 + ((4 - ((reinterpret_cast<uintptr_t>(v + k0) >> 2) & 3)) & 3);
+      const int64_t a1 = a0 < k1 ? a0 + ((k1 - a0) & ~int64_t(3)) : a0;
+      if (a0 >= k1) {  // no aligned body
+        for (int64_t k = k0 + tid; k < k1; k += kSegThreads) kahan_add(s, c, v[k]);
+      } else {
+        if (k0 + tid < a0) kahan_add(s, c, v[k0 + tid]);
+        const float4* v4 = reinterpret_cast<const float4*>(v + a0);
+        const int64_t n4 = (a1 - a0) / 4;
+        int64_t q = tid;
+        for (; q + (kSegLoads - 1) * kSegThreads < n4; q += kSegLoads * kSegThreads) {
+          float4 x[kSegLoads];
+#pragma unroll
+          for (int u = 0; u < kSegLoads; ++u) x[u] = v4[q + u * kSegThreads];
+#pragma unroll
+          for (int u = 0; u < kSegLoads; ++u) {
+            kahan_add(s, c, x[u].x);
+            kahan_add(s, c, x[u].y);
+            kahan_add(s, c, x[u].z);
+            kahan_add(s, c, x[u].w);
+          }
+        }
+        for (; q < n4; q += kSegThreads) {
+          const float4 x = v4[q];
+          kahan_add(s, c, x.x);
+          kahan_add(s, c, x.y);
+          kahan_add(s, c, x.z);
+          kahan_add(s, c, x.w);
+        }
+        if (a1 + tid < k1) kahan_add(s, c, v[a1 + tid]);
+      }
+    } else {
+      for (int64_t k = k0 + tid; k < k1; k += kSegThreads) kahan_add(s, c, v[k * stride]);
     }
-    part[threadIdx.x] = s;
+    const float ws = mlcg_wave_sum(s);
+    if (lane == 0) part[wv] = ws;
     __syncthreads();
-    for (int w = kSegThreads / 2; w > 0; w >>= 1) {
-      if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
-      __syncthreads();
+    if (tid == 0) {
+      float t = 0.f;
+      for (int w = 0; w < kSegWaves; ++w) t += part[w];
+      out[b] = t;
     }
-    if (threadIdx.x == 0) out[b] = part[0];
     __syncthreads();
   }
 }
