@@ -268,14 +268,15 @@ template <int kMode>
 struct BlockWaves {
   static constexpr int value = kMode == kModeFill ? 4 : 8;
 };
-// Rows per wave: 16 in kModeFill, which has no look-back and gains from many
-// waves hiding each other's latencies; 8 to 64 (at most one per lane) in the
+// Rows per wave: 8 in kModeFill, which has no look-back and gains from many
+// waves hiding each other's latencies (config 3: 44 us against 48 with 16
+// and 49 with 4); 8 to 64 (at most one per lane) in the
 // look-back modes, where larger blocks amortise the staging, the block scan
 // and the look-back, chosen per launch so that the waves spread evenly over
 // the chip's SIMDs (scan_rows_per_wave).  RowsPerWave is the maximum.
 template <int kMode>
 struct RowsPerWave {
-  static constexpr int value = kMode == kModeFill ? 16 : 64;
+  static constexpr int value = kMode == kModeFill ? 8 : 64;
 };
 constexpr int kMinScanRows = 8;  // fewest rows per wave of the look-back modes
 constexpr int kGroup = 4;                      // rows swept together
