@@ -472,13 +472,15 @@ int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
 /* out [num_types, 128] = for each type t the sum of the rows of x [rows, 128]
  * whose types[row] == t: the gradient of the bead-type embedding table
  * (schnet.py:132, `x = self.embedding_layer(data.atom_types)`, whose
- * autograd backward scatters the adjoint of x into the table).  One
- * workgroup per type lists its rows in ascending order and sums them in a
- * fixed order, so the result is run-to-run identical.
+ * autograd backward scatters the adjoint of x into the table).  Workgroups
+ * per type list their rows in ascending order and sum them in a fixed order
+ * (with many rows, G groups of row chunks per type whose partial sums are
+ * added in group order), so the result is run-to-run identical.
  * num_types <= 128 (MLCG_ERR_UNSUPPORTED beyond); a type outside
  * [0, num_types) is skipped and sets *bad = 1 (bad is not cleared here).
- * mlcg_type_sum_workspace_floats returns 0 (no workspace is used; the
- * workspace arguments are accepted and ignored, and may be NULL / 0). */
+ * mlcg_type_sum_workspace_floats gives the workspace the call needs: 0 up to
+ * 24,576 rows or when one group per type fills the chip (workspace may then
+ * be NULL), else 2 G num_types 128 floats. */
 int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types);
 int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
                   int num_types, float* out, int* bad, float* workspace,

@@ -569,8 +569,12 @@ void node_gemm2_kernel(
 // (ballot, in ascending row order) and list them in LDS, then the rows are
 // summed column by column, slot h of the eight slots per column taking the
 // listed rows h, h + 8, ... in order with a compensated (Kahan) sum, and the
-// slots are added in order at the end.  No atomics and no partial tables: the
-// result is the same on every run, and each row of x is read once in total.
+// slots are added in order at the end.  With many rows the chunks are shared
+// among G workgroups per type (blockIdx.y = g takes the chunks g, g + G, ...),
+// each writing its compensated column sums to a partial table that
+// type_sum_combine_kernel adds in group order; with one chunk G = 1 and the
+// workgroup writes the result itself.  No atomics: the result is the same on
+// every run, and each row of x is read once in total.
 constexpr int kTypeMax = 128;
 constexpr int kTypeThreads = 1024;
 constexpr int kTypeWaves = kTypeThreads / MLCG_WAVE;
@@ -584,16 +588,18 @@ __global__ __launch_bounds__(kTypeThreads) void type_sum_kernel(const float* __r
                                                                  const int64_t* __restrict__ types,
                                                                  int64_t rows, int T,
                                                                  float* __restrict__ out,
-                                                                 int* __restrict__ bad) {
+                                                                 int* __restrict__ bad,
+                                                                 float* __restrict__ partial) {
   __shared__ int list[kTypeChunk];  // the chunk's matches in ascending row order
   __shared__ int cnt[kTypeWaves];
   __shared__ float red[kTypeSlots][kF], red2[kTypeSlots][kF];
   const int t = blockIdx.x;
+  const int g = blockIdx.y, G = gridDim.y;
   const int w = threadIdx.x / MLCG_WAVE, l = mlcg_lane();
   const int c = threadIdx.x % kF, h = threadIdx.x / kF;
   const uint64_t below = (l == 0) ? 0ull : (~0ull >> (MLCG_WAVE - l));  // lanes < l
   float acc = 0.f, comp = 0.f;  // running sum and its lost low-order part
-  for (int64_t r0 = 0; r0 < rows; r0 += kTypeChunk) {
+  for (int64_t r0 = (int64_t)g * kTypeChunk; r0 < rows; r0 += (int64_t)G * kTypeChunk) {
     const int64_t base = r0 + (int64_t)w * kTypeWaveRows;
     int64_t tt[kTypeSteps];
 #pragma unroll
@@ -657,8 +663,40 @@ __global__ __launch_bounds__(kTypeThreads) void type_sum_kernel(const float* __r
       cs = (tv - sum) - yv;
       sum = tv;
     }
-    out[(int64_t)t * kF + c] = sum;
+    if (G == 1) {
+      out[(int64_t)t * kF + c] = sum;
+    } else {  // the group's sum and its lost low-order part
+      float* pg = partial + ((int64_t)g * T + t) * 2 * kF;
+      pg[c] = sum;
+      pg[kF + c] = cs;
+    }
   }
+}
+
+// out[t][c] = the G groups' partial sums of type t, added in group order with
+// their low-order parts (compensated).
+__global__ __launch_bounds__(kF) void type_sum_combine_kernel(const float* __restrict__ partial,
+                                                              int G, int T,
+                                                              float* __restrict__ out) {
+  const int t = blockIdx.x, c = threadIdx.x;
+  float sum = 0.f, cs = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const float* pg = partial + ((int64_t)g * T + t) * 2 * kF;
+    const float yv = pg[c] - (cs + pg[kF + c]);
+    const float tv = sum + yv;
+    cs = (tv - sum) - yv;
+    sum = tv;
+  }
+  out[(int64_t)t * kF + c] = sum;
+}
+
+// Workgroups per type: enough to give the chip about 256 workgroups, at most
+// one per chunk of rows.
+int type_groups(int64_t rows, int T) {
+  const int64_t chunks = rows <= 0 ? 1 : (rows + kTypeChunk - 1) / kTypeChunk;
+  const int64_t want = (256 + T - 1) / T;
+  const int64_t g = chunks < want ? chunks : want;
+  return (int)(g < 1 ? 1 : (g > 64 ? 64 : g));
 }
 
 int tmm_groups(int64_t rows) {
@@ -808,19 +846,24 @@ extern "C" int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
 
 extern "C" int64_t mlcg_type_sum_workspace_floats(int64_t rows, int num_types) {
   if (rows < 0 || num_types < 1 || num_types > kTypeMax) return -1;
-  return 0;  // no workspace: one pass, no partial tables
+  const int G = type_groups(rows, num_types);
+  return G == 1 ? 0 : (int64_t)2 * G * num_types * kF;  // the groups' partial sums
 }
 
 extern "C" int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows, int features,
                              int num_types, float* out, int* bad, float* workspace,
                              int64_t workspace_floats, void* stream) {
-  (void)workspace;
-  (void)workspace_floats;
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   if (num_types > kTypeMax) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out && bad);
   MLCG_REQUIRE(rows == 0 || (x && types));
-  hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)num_types), dim3(kTypeThreads), 0,
-                     mlcg_stream(stream), x, types, rows, num_types, out, bad);
+  const int G = type_groups(rows, num_types);
+  const int64_t need = G == 1 ? 0 : (int64_t)2 * G * num_types * kF;
+  MLCG_REQUIRE(workspace_floats >= need && (need == 0 || workspace));
+  hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)num_types, (unsigned)G), dim3(kTypeThreads),
+                     0, mlcg_stream(stream), x, types, rows, num_types, out, bad, workspace);
+  if (G > 1)
+    hipLaunchKernelGGL(type_sum_combine_kernel, dim3((unsigned)num_types), dim3(kF), 0,
+                       mlcg_stream(stream), workspace, G, num_types, out);
   return mlcg_launch_status();
 }

@@ -195,7 +195,7 @@ def test_node_gemm2_checks():
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,num_types", [(0, 5), (1, 1), (17920, 35), (17920, 100),
                                             (5000, 128), (300, 7), (24576, 3), (24577, 3),
-                                            (50000, 1)])
+                                            (50000, 1), (200000, 3), (128000, 20)])
 def test_type_sum_matches_index_add(rows, num_types):
     """The embedding-table gradient against fp64 index_add, identical on
     repeated calls (fixed summation order)."""
