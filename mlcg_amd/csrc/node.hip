@@ -18,146 +18,202 @@
 //                 accesses, its inputs requested before the products.
 //   node_tmm      out = a1^T b1 [+ a2^T b2] ([128, 128]): the weight
 //                 gradients, a reduction over N ~ 10^4-10^5 rows on
-//                 v_mfma_f32_16x16x4f32.  Up to 256 workgroups each reduce a
-//                 contiguous range of rows in 16-row chunks (staged in LDS)
-//                 with the row index as the MFMA reduction axis (wave w owns
-//                 output rows 16w..16w+15) and write their partial; a second
-//                 kernel adds the partials in a fixed order -- deterministic
-//                 for a given row count.
+//                 v_mfma_f32_16x16x32_bf16 with each fp32 operand split
+//                 exactly into three bf16 pieces (six products).  Up to 256
+//                 workgroups each reduce a contiguous range of 32-row blocks
+//                 (staged in LDS column-major, the row index being the MFMA
+//                 reduction axis) and write their partial; a second kernel
+//                 adds the partials in a fixed order -- deterministic for a
+//                 given row count.
 #include "common.h"
 #include "split16.h"
 
 namespace {
 
 constexpr int kF = 128;
-constexpr int kFT = kF / 16;
 // ---------------------------------------------------------------------------
 // node_tmm
+//
+// Products on v_mfma_f32_16x16x32_bf16.  Every fp32 operand x is split
+// exactly into three bf16 pieces x = hi + mid + lo, each rounded to nearest
+// from the remainder of the previous one (|mid| <= 2^-8 |x|, |lo| <= 2^-16
+// |x|: the remainders carry at most 16 and 8 significant bits, so every
+// piece is exact).  A product x y is taken as the six terms hi hi, hi mid,
+// mid hi, hi lo, lo hi, mid mid; the three left out are below 2^-23 |x y|.
+// bf16 x bf16 products are exact and the MFMA accumulates them in fp32.
+// bf16 has fp32's exponent range, so the operands need no scaling.
 constexpr int kTmmWaves = 8;
 constexpr int kTmmThreads = kTmmWaves * MLCG_WAVE;
-constexpr int kTmmRows = 16;                     // rows per staged chunk
-constexpr int kTRow = kF + 4;                    // padded LDS row (node GEMM epilogue)
-// node_tmm's staged rows: a stride of 16 (mod 32) floats puts the two lane
-// halves of a scalar read (rows 4 kk + q, q = 0, 1 in lanes 0-31) on disjoint
-// banks of the 32 that a 4-byte LDS access sees
-constexpr int kTmmRow = kF + 16;
-constexpr int kTmmMaxGroups = 256;               // one workgroup per CU
-constexpr int kTmmPer = kTmmRows * kF / 4 / kTmmThreads;  // float4 per thread per matrix
-constexpr int kTmmPart = kF * kF + kF;           // partial: out [128, 128] + column sums
+constexpr int kTmmK = 32;                   // rows per staged block (the MFMA's K)
+// bf16 per staged column: an 80-byte stride puts the 16-byte reads of the 16
+// lanes of a lane group (16 consecutive columns) on disjoint banks
+constexpr int kTmmCol = kTmmK + 8;
+constexpr int kTmmPlane = kF * kTmmCol;     // bf16 per plane
+constexpr int kTmmMat = 3 * kTmmPlane;      // hi, mid, lo planes of one matrix
+constexpr int kTRow = kF + 4;               // padded LDS row (node GEMM epilogue)
+constexpr int kTmmMaxGroups = 256;          // one workgroup per CU
+constexpr int kTmmPart = kF * kF + kF;      // partial: out [128, 128] + column sums
 
-// One 16-row chunk of up to four matrices, held in registers between its
-// global load and its LDS store.  Thread i always covers columns
-// 4 (i % 32) .. 4 (i % 32) + 3, which the column sum relies on.
-struct TmmChunk {
-  float4 v[4][kTmmPer];
-};
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void tmm_load(TmmChunk& ch, const float* __restrict__ a1,
-                                         const float* __restrict__ b1,
-                                         const float* __restrict__ a2,
-                                         const float* __restrict__ b2, int64_t r0,
-                                         int64_t r_end) {
-  const float* src[4] = {a1, b1, a2, b2};
+// Splits eight values (consecutive rows of one column) into their hi, mid
+// and lo bf16 pieces, two at a time.
+__device__ __forceinline__ void tmm_split8(const float (&x)[8], bf16x8& hi, bf16x8& mid,
+                                           bf16x8& lo) {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m >= 2 && !a2) break;
+  for (int j = 0; j < 8; j += 2) {
+    const floatx2 v = {x[j], x[j + 1]};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    const floatx2 r1 = v - __builtin_convertvector(h, floatx2);
+    const bf16x2 m = __builtin_convertvector(r1, bf16x2);
+    const bf16x2 o = __builtin_convertvector(r1 - __builtin_convertvector(m, floatx2), bf16x2);
+    hi[j] = h[0];
+    hi[j + 1] = h[1];
+    mid[j] = m[0];
+    mid[j + 1] = m[1];
+    lo[j] = o[0];
+    lo[j + 1] = o[1];
+  }
+}
+
+// Thread i loads rows 8 g .. 8 g + 7 (g = (i / 32) % 4) of a block, columns
+// 4 (i % 32) .. + 3, of matrix i / 128 (a1, b1, a2, b2); zero past r_end.
+__device__ __forceinline__ void tmm_load(float4 (&v)[8], const float* __restrict__ src,
+                                         int64_t r0, int64_t r_end) {
+  const int g = (threadIdx.x >> 5) & 3, c = threadIdx.x & 31;
+  const float* p = src + (r0 + 8 * g) * kF + 4 * c;
+  if (r0 + kTmmK <= r_end) {  // a whole block (every block but a range's last)
 #pragma unroll
-    for (int k = 0; k < kTmmPer; ++k) {
-      const int c = threadIdx.x + k * kTmmThreads;
-      const int64_t r = r0 + c / (kF / 4);
-      ch.v[m][k] = r < r_end ? *reinterpret_cast<const float4*>(src[m] + r * kF + 4 * (c % (kF / 4)))
-                             : float4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(p + j * kF);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = r0 + 8 * g + j < r_end ? *reinterpret_cast<const float4*>(p + j * kF)
+                                    : float4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// Stores a loaded 8 x 4 piece as three planes, each column's eight rows as
+// one 16-byte write at [column][8 g].
+__device__ __forceinline__ void tmm_stage(__bf16* mat, const float4 (&v)[8]) {
+  const int g = (threadIdx.x >> 5) & 3, c = threadIdx.x & 31;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = k == 0 ? v[j].x : k == 1 ? v[j].y : k == 2 ? v[j].z : v[j].w;
+    bf16x8 hi, mid, lo;
+    tmm_split8(x, hi, mid, lo);
+    const int o = (4 * c + k) * kTmmCol + 8 * g;
+    *reinterpret_cast<bf16x8*>(mat + o) = hi;
+    *reinterpret_cast<bf16x8*>(mat + kTmmPlane + o) = mid;
+    *reinterpret_cast<bf16x8*>(mat + 2 * kTmmPlane + o) = lo;
+  }
+}
+
+// acc[rt][ct] += a^T b over one staged block for output rows 16 (4 rg + rt)
+// + .. and columns 16 (2 cg + ct) + ..: lane (q, n) supplies a's column
+// 16 (4 rg + rt) + n and b's column 16 (2 cg + ct) + n, rows 8q .. 8q + 7.
+__device__ __forceinline__ void tmm_accumulate(const __bf16* ma, const __bf16* mb, int rg,
+                                               int cg, int q, int n, floatx4 (&acc)[4][2]) {
+  bf16x8 b[2][3];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      b[ct][p] = *reinterpret_cast<const bf16x8*>(mb + p * kTmmPlane +
+                                                  (16 * (2 * cg + ct) + n) * kTmmCol + 8 * q);
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    bf16x8 a[3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      a[p] = *reinterpret_cast<const bf16x8*>(ma + p * kTmmPlane +
+                                              (16 * (4 * rg + rt) + n) * kTmmCol + 8 * q);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      floatx4 c = acc[rt][ct];
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[ct][0], c, 0, 0, 0);  // lo hi
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[ct][2], c, 0, 0, 0);  // hi lo
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[ct][1], c, 0, 0, 0);  // mid mid
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[ct][0], c, 0, 0, 0);  // mid hi
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[ct][1], c, 0, 0, 0);  // hi mid
+      acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[ct][0], c, 0, 0, 0);
     }
   }
 }
 
-__device__ __forceinline__ void tmm_store(float* buf, const TmmChunk& ch, bool two) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m >= 2 && !two) break;
-#pragma unroll
-    for (int k = 0; k < kTmmPer; ++k) {
-      const int c = threadIdx.x + k * kTmmThreads;
-      *reinterpret_cast<float4*>(buf + m * kTmmRows * kTmmRow + (c / (kF / 4)) * kTmmRow +
-                                 4 * (c % (kF / 4))) = ch.v[m][k];
-    }
-  }
-}
-
-// acc[u] += la^T lb over the 16 staged rows, for output rows 16w..16w+15
-// (columns of a) and output columns 16u..16u+15 (columns of b).
-__device__ __forceinline__ void tmm_accumulate(const float* la, const float* lb, int w, int q,
-                                               int n, floatx4* acc) {
-#pragma unroll
-  for (int kk = 0; kk < kTmmRows / 4; ++kk) {
-    const float av = la[(4 * kk + q) * kTmmRow + 16 * w + n];
-    float bv[kFT];
-#pragma unroll
-    for (int u = 0; u < kFT; ++u) bv[u] = lb[(4 * kk + q) * kTmmRow + 16 * u + n];
-#pragma unroll
-    for (int u = 0; u < kFT; ++u)
-      acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc[u], 0, 0, 0);
-  }
-}
-
-// Workgroup g reduces the contiguous rows [g R / G, (g+1) R / G) in 16-row
-// chunks, the next chunk's loads in flight while the current one feeds the
-// MFMAs, and writes its partial [128, 128] (+ the column sums of a1).
+// Workgroup g reduces the 32-row blocks [g B / G, (g+1) B / G) of the
+// B = ceil(rows / 32) blocks: per block, each thread loads (the next block's
+// loads in flight during the products) and splits one 8 x 4 piece of one
+// matrix, and wave (rg, cg) = (w / 4, w % 4) accumulates output rows
+// 64 rg .. + 63 and columns 32 cg .. + 31.  Writes its partial [128, 128]
+// (+ the column sums of a1, added per thread in row order and over the four
+// row groups in order).
 __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     const float* __restrict__ a1, const float* __restrict__ b1,
     const float* __restrict__ a2, const float* __restrict__ b2, int64_t rows,
     int want_colsum, float* __restrict__ partial) {
-  __shared__ float lds[2][4 * kTmmRows * kTmmRow];
-  __shared__ float4 csum[kTmmThreads];
+  __shared__ __align__(16) __bf16 lds[4 * kTmmMat];
+  __shared__ float4 csum[4][kF / 4];
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
+  const int rg = w >> 2, cg = w & 3;
   const bool two = a2 != nullptr;
+  const int mat = threadIdx.x >> 7;  // the matrix this thread loads
+  const float* src = mat == 0 ? a1 : mat == 1 ? b1 : mat == 2 ? a2 : b2;
+  const bool loads = mat < 2 || two;
   const int64_t G = gridDim.x;
-  const int64_t r_beg = rows * blockIdx.x / G;
-  const int64_t r_end = rows * (blockIdx.x + 1) / G;
-  floatx4 acc[kFT];
+  const int64_t nb = (rows + kTmmK - 1) / kTmmK;
+  const int64_t r_beg = kTmmK * (nb * blockIdx.x / G);
+  const int64_t r_stop = kTmmK * (nb * (blockIdx.x + 1) / G);
+  const int64_t r_end = r_stop < rows ? r_stop : rows;
+  floatx4 acc[4][2];
 #pragma unroll
-  for (int u = 0; u < kFT; ++u) acc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int rt = 0; rt < 4; ++rt) acc[rt][0] = acc[rt][1] = floatx4{0.f, 0.f, 0.f, 0.f};
   float4 cs{0.f, 0.f, 0.f, 0.f};
-  TmmChunk ch;
-  tmm_load(ch, a1, b1, a2, b2, r_beg, r_end);
-  int buf = 0;
-  for (int64_t r0 = r_beg; r0 < r_end; r0 += kTmmRows) {
-    tmm_store(lds[buf], ch, two);
-    if (want_colsum) {
+  float4 v[8];
+  if (loads) tmm_load(v, src, r_beg, r_end);
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += kTmmK) {
+    if (loads) {
+      tmm_stage(lds + mat * kTmmMat, v);
+      if (want_colsum && mat == 0) {
 #pragma unroll
-      for (int k = 0; k < kTmmPer; ++k) {
-        cs.x += ch.v[0][k].x;
-        cs.y += ch.v[0][k].y;
-        cs.z += ch.v[0][k].z;
-        cs.w += ch.v[0][k].w;
+        for (int j = 0; j < 8; ++j) {
+          cs.x += v[j].x;
+          cs.y += v[j].y;
+          cs.z += v[j].z;
+          cs.w += v[j].w;
+        }
       }
     }
     __syncthreads();
-    if (r0 + kTmmRows < r_end) tmm_load(ch, a1, b1, a2, b2, r0 + kTmmRows, r_end);
-    const float* base = lds[buf];
-    tmm_accumulate(base, base + kTmmRows * kTmmRow, w, q, n, acc);
-    if (two)
-      tmm_accumulate(base + 2 * kTmmRows * kTmmRow, base + 3 * kTmmRows * kTmmRow, w, q, n, acc);
-    buf ^= 1;
+    if (loads && r0 + kTmmK < r_end) tmm_load(v, src, r0 + kTmmK, r_end);
+    tmm_accumulate(lds, lds + kTmmMat, rg, cg, q, n, acc);
+    if (two) tmm_accumulate(lds + 2 * kTmmMat, lds + 3 * kTmmMat, rg, cg, q, n, acc);
+    __syncthreads();
   }
   float* o = partial + (int64_t)blockIdx.x * kTmmPart;
 #pragma unroll
-  for (int u = 0; u < kFT; ++u)
+  for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[(16 * w + 4 * q + i) * kF + 16 * u + n] = acc[u][i];
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[(16 * (4 * rg + rt) + 4 * q + i) * kF + 16 * (2 * cg + ct) + n] = acc[rt][ct][i];
   if (want_colsum) {
-    // threads t, t + 32, ..., t + 480 share columns 4 (t % 32) .. + 3
-    csum[threadIdx.x] = cs;
+    if (mat == 0) csum[(threadIdx.x >> 5) & 3][threadIdx.x & 31] = cs;
     __syncthreads();
     if (threadIdx.x < kF / 4) {
-      float4 t{0.f, 0.f, 0.f, 0.f};
-      for (int j = threadIdx.x; j < kTmmThreads; j += kF / 4) {
-        t.x += csum[j].x;
-        t.y += csum[j].y;
-        t.z += csum[j].z;
-        t.w += csum[j].w;
+      float4 t = csum[0][threadIdx.x];
+#pragma unroll
+      for (int g = 1; g < 4; ++g) {
+        t.x += csum[g][threadIdx.x].x;
+        t.y += csum[g][threadIdx.x].y;
+        t.z += csum[g][threadIdx.x].z;
+        t.w += csum[g][threadIdx.x].w;
       }
       *reinterpret_cast<float4*>(o + kF * kF + 4 * threadIdx.x) = t;
     }
@@ -700,8 +756,8 @@ int type_groups(int64_t rows, int T) {
 }
 
 int tmm_groups(int64_t rows) {
-  const int64_t chunks = rows == 0 ? 1 : (rows + kTmmRows - 1) / kTmmRows;
-  return (int)(chunks < kTmmMaxGroups ? chunks : kTmmMaxGroups);
+  const int64_t blocks = rows == 0 ? 1 : (rows + kTmmK - 1) / kTmmK;
+  return (int)(blocks < kTmmMaxGroups ? blocks : kTmmMaxGroups);
 }
 
 template <int MODE>

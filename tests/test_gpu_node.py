@@ -2,9 +2,10 @@
 products at ragged row counts, and the node_linear helper's epilogues.
 
 Every element is held to rtol of the tensor's largest element (check with
-atol_frac=1.0): the products run on the fp16 MFMA with split operands, about
-22 significant bits each, so an element's error scales with the row of terms
-it sums, not with the element."""
+atol_frac=1.0): node_linear's products run on the fp16 MFMA with split
+operands (about 22 significant bits) and node_tmm's on the bf16 MFMA with
+three-way splits (each product within 2^-23 of exact, summed in fp32), so an
+element's error scales with the terms it sums, not with the element."""
 
 import pytest
 import torch
