@@ -250,19 +250,16 @@ __global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __res
 
 // ---------------------------------------------------------------------------
 // node_gemm
-#ifndef MLCG_NODE_GEMM_ROWS
-#define MLCG_NODE_GEMM_ROWS 16
-#endif
-#ifndef MLCG_NODE_GEMM_PER_CU
-#define MLCG_NODE_GEMM_PER_CU 3
-#endif
-#ifndef MLCG_NODE_GEMM2_PER_CU
-#define MLCG_NODE_GEMM2_PER_CU 2
-#endif
-constexpr int kGemmRows = MLCG_NODE_GEMM_ROWS;   // rows per tile
-constexpr int kGemmRT = kGemmRows / 16;          // 16-row MFMA tiles per tile
-constexpr int kGemmThreads = 256;                // wave w owns columns 32w..32w+31
-constexpr int kGemmXPer = kGemmRows * (kF / 4) / kGemmThreads;  // float4 per thread
+// A workgroup of 4 kRT waves computes tiles of 16 kRT rows: wave w owns the
+// 32 columns 32 (w % 4) .. + 31 of the rows 16 (w / 4) .. + 15 of a tile.
+// One workgroup per CU; its waves share one split copy of each weight.
+template <int kRT>
+struct GemmShape {
+  static constexpr int kThreads = 4 * kRT * MLCG_WAVE;
+  static constexpr int kRows = 16 * kRT;
+  static constexpr int kPlane = kRows * kF;  // halfs per plane of a staged tile
+};
+constexpr int kGemmXPer = 2;  // float4 per thread of a tile: 32 per row, 16 rows per 4 waves
 
 // Activation derivatives from the pre-activation z and the value s = act(z)
 // (the same expressions as the host-side act_derivs).
@@ -285,29 +282,31 @@ __device__ __forceinline__ void st4(float* __restrict__ p, float4 v) {
 }
 
 // Loads tile t (zero past `rows`) as kGemmXPer float4 per thread.
+template <int kRT>
 __device__ __forceinline__ void gemm_load_x(float4 (&v)[kGemmXPer], const float* __restrict__ x,
                                             int64_t t, int64_t rows) {
 #pragma unroll
   for (int m = 0; m < kGemmXPer; ++m) {
-    const int c = threadIdx.x + m * kGemmThreads;
-    const int64_t r = t * kGemmRows + (c >> 5);
+    const int c = threadIdx.x + m * GemmShape<kRT>::kThreads;
+    const int64_t r = t * GemmShape<kRT>::kRows + (c >> 5);
     v[m] = r < rows ? ld4(x + r * kF + 4 * (c & 31)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 }
 // Split scale of the node products: x is brought into [-4, 4) per row, so
 // hi S stays below 2^13; W needs |W| < 2^15.
 constexpr float kNodeS = 2048.0f;
-constexpr int kXPlane = kGemmRows * kF;  // halfs per plane of a staged tile
 
 // Stages a loaded tile: per row r, sigma_r = 2^k with max_c |x[r][c]| sigma_r
 // < 4; the three planes (hi, hi S, lo S) of x sigma go to LDS as [row][128]
 // halfs with 16-byte chunk j of row r stored at j ^ (r & 15), and
 // 1 / (S sigma_r) to rinv[r].  The 32 lanes of a wave half hold one row.
+template <int kRT>
 __device__ __forceinline__ void gemm_stage_x3(_Float16* xp, float* rinv,
                                               const float4 (&v)[kGemmXPer]) {
+  constexpr int kXPlane = GemmShape<kRT>::kPlane;
 #pragma unroll
   for (int m = 0; m < kGemmXPer; ++m) {
-    const int c = threadIdx.x + m * kGemmThreads;
+    const int c = threadIdx.x + m * GemmShape<kRT>::kThreads;
     const int row = c >> 5, c4 = c & 31;
     const float4 x = v[m];
     float mx = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
@@ -406,24 +405,73 @@ __device__ __forceinline__ float4 gemm_epilogue(float4 y, int64_t r, int col, co
 }
 
 // B = W^T (kXW = false, torch Linear) or B = W (kXW = true) as two fp16
-// planes (hi, lo S) in registers: plane[c][kb] of lane (q, n) in wave w holds
-// B[32 kb + 8q + j][32 w + 16 c + n], j = 0..7 (the B operand layout of
-// v_mfma_f32_16x16x32_f16).
+// planes (hi, lo S), held in registers by each wave: plane[c][kb] of lane
+// (q, n) in a wave of column slice cw holds B[32 kb + 8q + j][32 cw + 16 c + n],
+// j = 0..7 (the B operand layout of v_mfma_f32_16x16x32_f16).  The workgroup
+// splits W once into an LDS image in exactly that order -- entry
+// e = ((cw 2 + c) 4 + kb) 64 + lane holds the lane's eight halfs, hi plane
+// at e, lo plane at kWImg + e -- and each wave reads its 16 entries back.
+constexpr int kWImg = 4 * 2 * (kF / 32) * MLCG_WAVE;  // halfx8 entries per plane
+constexpr int kWImgBytes = 2 * kWImg * 16;             // 64 KiB
+
+template <int kRT, bool kXW>
+__device__ __forceinline__ void gemm_stage_w(halfx8* img, const float* __restrict__ W) {
+  constexpr int kT = GemmShape<kRT>::kThreads;
+  constexpr int kIt = (kWImg + kT - 1) / kT;
+  constexpr int kBatch = 2;  // entries whose loads are in flight together
+#pragma unroll
+  for (int i0 = 0; i0 < kIt; i0 += kBatch) {
+    float wv[kBatch][8];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int e = threadIdx.x + (i0 + b) * kT;
+      if (i0 + b >= kIt || (kWImg % kT != 0 && e >= kWImg)) break;
+      const int l = e & 63, kb = (e >> 6) & 3, c = (e >> 8) & 1, cw = e >> 9;
+      const int q = l >> 4, col = 32 * cw + 16 * c + (l & 15);
+      if (kXW) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[b][j] = W[(32 * kb + 8 * q + j) * kF + col];
+      } else {  // the eight k of an entry are contiguous in row `col` of W
+        const float4 v0 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q);
+        const float4 v1 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q + 4);
+        wv[b][0] = v0.x; wv[b][1] = v0.y; wv[b][2] = v0.z; wv[b][3] = v0.w;
+        wv[b][4] = v1.x; wv[b][5] = v1.y; wv[b][6] = v1.z; wv[b][7] = v1.w;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int e = threadIdx.x + (i0 + b) * kT;
+      if (i0 + b >= kIt || (kWImg % kT != 0 && e >= kWImg)) break;
+      halfx8 h, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f16split sp = split2(wv[b][j], kNodeS);
+        h[j] = sp.hi;
+        lo[j] = sp.lo;
+      }
+      img[e] = h;
+      img[kWImg + e] = lo;
+    }
+  }
+}
+
+// The same 16 entries loaded and split by one wave directly from W (for
+// node_gemm2, whose second weight leaves no registers for a staged copy).
 template <bool kXW>
 __device__ __forceinline__ void gemm_load_w(halfx8 (&bh)[2][kF / 32], halfx8 (&bl)[2][kF / 32],
-                                            const float* __restrict__ W, int w, int q, int n) {
+                                            const float* __restrict__ W, int cw, int q, int n) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const int col = 32 * w + 16 * c + n;
+    const int col = 32 * cw + 16 * c + n;
 #pragma unroll
     for (int kb = 0; kb < kF / 32; ++kb) {
       float wv[8];
       if (kXW) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) wv[j] = W[(32 * kb + 8 * q + j) * kF + col];
-      } else {  // the eight k of a lane are contiguous in row `col` of W
-        const float4 v0 = ld4(W + col * kF + 32 * kb + 8 * q);
-        const float4 v1 = ld4(W + col * kF + 32 * kb + 8 * q + 4);
+      } else {
+        const float4 v0 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q);
+        const float4 v1 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q + 4);
         wv[0] = v0.x; wv[1] = v0.y; wv[2] = v0.z; wv[3] = v0.w;
         wv[4] = v1.x; wv[5] = v1.y; wv[6] = v1.z; wv[7] = v1.w;
       }
@@ -437,92 +485,110 @@ __device__ __forceinline__ void gemm_load_w(halfx8 (&bh)[2][kF / 32], halfx8 (&b
   }
 }
 
+__device__ __forceinline__ void gemm_read_w(halfx8 (&bh)[2][kF / 32], halfx8 (&bl)[2][kF / 32],
+                                            const halfx8* img, int cw, int l) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int kb = 0; kb < kF / 32; ++kb) {
+      const int e = ((cw * 2 + c) * (kF / 32) + kb) * MLCG_WAVE + l;
+      bh[c][kb] = img[e];
+      bl[c][kb] = img[kWImg + e];
+    }
+}
+
 // The product of a staged tile (three planes in xs, row scales in rinv) and
-// the B planes: wave w's 32 columns of all kGemmRows rows go to ys, with the
-// row scales undone.
+// the B planes: the 32 columns 32 cw .. of the 16 rows 16 rs .. go to ys,
+// with the row scales undone.
+template <int kRT>
 __device__ __forceinline__ void gemm_tile(const _Float16* xs, const float* rinv,
                                           const halfx8 (&bh)[2][kF / 32],
-                                          const halfx8 (&bl)[2][kF / 32], float* ys, int w,
-                                          int q, int n) {
-  floatx4 acc[kGemmRT][2];
-#pragma unroll
-  for (int r = 0; r < kGemmRT; ++r)
-    acc[r][0] = acc[r][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+                                          const halfx8 (&bl)[2][kF / 32], float* ys, int cw,
+                                          int rs, int q, int n) {
+  constexpr int kP8 = GemmShape<kRT>::kPlane / 8;
+  floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
   const halfx8* xv = reinterpret_cast<const halfx8*>(xs);
 #pragma unroll
   for (int kb = 0; kb < kF / 32; ++kb) {
+    const int o = (16 * rs + n) * (kF / 8) + ((4 * kb + q) ^ n);
+    const halfx8 ah = xv[o], ahs = xv[kP8 + o], al = xv[2 * kP8 + o];
 #pragma unroll
-    for (int r = 0; r < kGemmRT; ++r) {
-      const int o = (16 * r + n) * (kF / 8) + ((4 * kb + q) ^ n);
-      const halfx8 ah = xv[o], ahs = xv[kXPlane / 8 + o], al = xv[2 * kXPlane / 8 + o];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh[c][kb], acc[r][c], 0, 0, 0);
-        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[c][kb], acc[r][c], 0, 0, 0);
-        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[c][kb], acc[r][c], 0, 0, 0);
-      }
+    for (int c = 0; c < 2; ++c) {
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahs, bh[c][kb], acc[c], 0, 0, 0);
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[c][kb], acc[c], 0, 0, 0);
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[c][kb], acc[c], 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int r = 0; r < kGemmRT; ++r)
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * rs + 4 * q + i;
+    const float u = rinv[row];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * r + 4 * q + i;
-      const float u = rinv[row];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) ys[row * kTRow + 32 * w + 16 * c + n] = acc[r][c][i] * u;
-    }
+    for (int c = 0; c < 2; ++c) ys[row * kTRow + 32 * cw + 16 * c + n] = acc[c][i] * u;
+  }
 }
 
 // y = x B with B = W^T (kXW = false, torch Linear) or B = W (kXW = true), on
 // v_mfma_f32_16x16x32_f16 with split operands: x as three planes (staged
 // per tile, scaled per row), B as two planes (hi, lo S) held in registers.
 // MFMA k block kb of lane group q = l/16 covers k = 32 kb + 8q .. + 7.
-template <int MODE, bool kXW>
-__global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
+// LDS: the weight image first, then (over the same bytes) the tile buffers.
+template <int MODE, bool kXW, int kRT>
+__global__ __launch_bounds__(GemmShape<kRT>::kThreads) void node_gemm_kernel(
     const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
     const float* __restrict__ bias, const float* __restrict__ residual, int act,
     const float* __restrict__ zin, const float* __restrict__ sin_,
     const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
     float* __restrict__ out1) {
-  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
-  __shared__ float rinv[2][kGemmRows];
-  __shared__ float ys[kGemmRows * kTRow];
+  using S = GemmShape<kRT>;
+  constexpr int kXs = 2 * 3 * S::kPlane * 2, kRinv = 2 * S::kRows * 4;
+  constexpr int kBytes = kXs + kRinv + S::kRows * kTRow * 4;
+  static_assert(kBytes >= kWImgBytes, "the weight image overlays the tile buffers");
+  __shared__ __align__(16) unsigned char smem[kBytes];
+  _Float16* const xs0 = reinterpret_cast<_Float16*>(smem);
+  _Float16* const xs1 = xs0 + 3 * S::kPlane;
+  float* const rinv0 = reinterpret_cast<float*>(smem + kXs);
+  float* const rinv1 = rinv0 + S::kRows;
+  float* const ys = reinterpret_cast<float*>(smem + kXs + kRinv);
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
-  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  const int cw = w & 3, rs = w >> 2;
+  const int64_t tiles = (rows + S::kRows - 1) / S::kRows;
   // the first tile's rows are requested before the weights, so that the two
   // loads' latencies overlap
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
-  gemm_load_x(pf, x, t, rows);
+  gemm_load_x<kRT>(pf, x, t, rows);
   halfx8 bh[2][kF / 32], bl[2][kF / 32];
-  gemm_load_w<kXW>(bh, bl, W, w, q, n);
-  gemm_stage_x3(xs[0], rinv[0], pf);
+  gemm_stage_w<kRT, kXW>(reinterpret_cast<halfx8*>(smem), W);
+  __syncthreads();
+  gemm_read_w(bh, bl, reinterpret_cast<const halfx8*>(smem), cw, l);
+  __syncthreads();
+  gemm_stage_x3<kRT>(xs0, rinv0, pf);
   __syncthreads();
   int buf = 0;
   for (; t < tiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < tiles;
-    if (has_next) gemm_load_x(pf, x, tn, rows);
+    if (has_next) gemm_load_x<kRT>(pf, x, tn, rows);
     // this tile's epilogue inputs, requested before the products
     EpiIn ein_[kGemmXPer];
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
-      const int c = threadIdx.x + m * kGemmThreads;
-      const int64_t r = t * kGemmRows + (c >> 5);
+      const int c = threadIdx.x + m * S::kThreads;
+      const int64_t r = t * S::kRows + (c >> 5);
       gemm_epilogue_load<MODE>(ein_[m], r < rows ? r : 0, 4 * (c & 31), residual, act, zin,
                                sin_, ein, fin);
     }
-    gemm_tile(xs[buf], rinv[buf], bh, bl, ys, w, q, n);
-    if (has_next) gemm_stage_x3(xs[buf ^ 1], rinv[buf ^ 1], pf);
+    gemm_tile<kRT>(buf ? xs1 : xs0, buf ? rinv1 : rinv0, bh, bl, ys, cw, rs, q, n);
+    if (has_next) gemm_stage_x3<kRT>(buf ? xs0 : xs1, buf ? rinv0 : rinv1, pf);
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
-      const int c = threadIdx.x + m * kGemmThreads;
+      const int c = threadIdx.x + m * S::kThreads;
       const int rr = c >> 5, col = 4 * (c & 31);
-      const int64_t r = t * kGemmRows + rr;
+      const int64_t r = t * S::kRows + rr;
       if (r < rows)
         gemm_epilogue<MODE>(ld4(ys + rr * kTRow + col), r, col, ein_[m], bias, act,
                             ein != nullptr, out0, out1);
@@ -540,9 +606,12 @@ __global__ __launch_bounds__(kGemmThreads) void node_gemm_kernel(
 // staged from registers into a second set of planes, so each tile reads x
 // once and never reads v back.  The products, scalings and epilogue
 // arithmetic are those of two node_gemm_kernel launches, so the results are
-// the same bit for bit.  Both B operands stay in registers (about 128 VGPRs).
-template <int MODE, bool kXW>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+// the same bit for bit.  Both B operands stay in registers (about 128 VGPRs),
+// each wave loading its own slices (kRT = 1: four waves, two workgroups per
+// CU; an 8-wave workgroup sharing staged weights measured slower, its
+// registers spilling).
+template <int MODE, bool kXW, int kRT>
+__global__ __launch_bounds__(GemmShape<kRT>::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void node_gemm2_kernel(
     const float* __restrict__ x, int64_t rows, const float* __restrict__ W,
     const float* __restrict__ bias, const float* __restrict__ residual, int act,
@@ -550,67 +619,75 @@ void node_gemm2_kernel(
     const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
     float* __restrict__ out1, const float* __restrict__ W2, const float* __restrict__ bias2,
     const float* __restrict__ residual2, float* __restrict__ out2) {
-  __shared__ __align__(16) _Float16 xs[2][3 * kXPlane];
-  __shared__ __align__(16) _Float16 vs[3 * kXPlane];
-  __shared__ float rinv[3][kGemmRows];
-  __shared__ float ys[2][kGemmRows * kTRow];
+  using S = GemmShape<kRT>;
+  constexpr int kXs = 3 * 3 * S::kPlane * 2, kRinv = 3 * S::kRows * 4;
+  __shared__ __align__(16) unsigned char smem[kXs + kRinv + 2 * S::kRows * kTRow * 4];
+  _Float16* const xs0 = reinterpret_cast<_Float16*>(smem);
+  _Float16* const xs1 = xs0 + 3 * S::kPlane;
+  _Float16* const vs = xs1 + 3 * S::kPlane;
+  float* const rinv0 = reinterpret_cast<float*>(smem + kXs);
+  float* const rinv1 = rinv0 + S::kRows;
+  float* const rinv2 = rinv1 + S::kRows;
+  float* const ys0 = reinterpret_cast<float*>(smem + kXs + kRinv);
+  float* const ys1 = ys0 + S::kRows * kTRow;
   const int w = threadIdx.x / MLCG_WAVE;
   const int l = mlcg_lane();
   const int q = l >> 4, n = l & 15;
-  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
+  const int cw = w & 3, rs = w >> 2;
+  const int64_t tiles = (rows + S::kRows - 1) / S::kRows;
   int64_t t = blockIdx.x;
   float4 pf[kGemmXPer];
-  gemm_load_x(pf, x, t, rows);
+  gemm_load_x<kRT>(pf, x, t, rows);
   halfx8 bh[2][kF / 32], bl[2][kF / 32], ch[2][kF / 32], cl[2][kF / 32];
-  gemm_load_w<kXW>(bh, bl, W, w, q, n);
-  gemm_load_w<kXW>(ch, cl, W2, w, q, n);
-  gemm_stage_x3(xs[0], rinv[0], pf);
+  gemm_load_w<kXW>(bh, bl, W, cw, q, n);
+  gemm_load_w<kXW>(ch, cl, W2, cw, q, n);
+  gemm_stage_x3<kRT>(xs0, rinv0, pf);
   __syncthreads();
   int buf = 0;
-  // LDS reuse across iterations: xs[buf] and ys[0] are last read before the
-  // second barrier of an iteration, vs and ys[1] before the third, and each
+  // LDS reuse across iterations: xs[buf] and ys0 are last read before the
+  // second barrier of an iteration, vs and ys1 before the third, and each
   // is next written after at least one further barrier.
   for (; t < tiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < tiles;
-    if (has_next) gemm_load_x(pf, x, tn, rows);
+    if (has_next) gemm_load_x<kRT>(pf, x, tn, rows);
     EpiIn ein_[kGemmXPer];
     float4 res2[kGemmXPer];
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
-      const int c = threadIdx.x + m * kGemmThreads;
-      const int64_t r = t * kGemmRows + (c >> 5);
+      const int c = threadIdx.x + m * S::kThreads;
+      const int64_t r = t * S::kRows + (c >> 5);
       const int64_t rr = r < rows ? r : 0;
       gemm_epilogue_load<MODE>(ein_[m], rr, 4 * (c & 31), residual, act, zin, sin_, ein, fin);
       res2[m] = residual2 ? ld4(residual2 + rr * kF + 4 * (c & 31)) : float4{0.f, 0.f, 0.f, 0.f};
     }
-    gemm_tile(xs[buf], rinv[buf], bh, bl, ys[0], w, q, n);
-    if (has_next) gemm_stage_x3(xs[buf ^ 1], rinv[buf ^ 1], pf);
+    gemm_tile<kRT>(buf ? xs1 : xs0, buf ? rinv1 : rinv0, bh, bl, ys0, cw, rs, q, n);
+    if (has_next) gemm_stage_x3<kRT>(buf ? xs0 : xs1, buf ? rinv0 : rinv1, pf);
     __syncthreads();
     float4 v[kGemmXPer];
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
-      const int c = threadIdx.x + m * kGemmThreads;
+      const int c = threadIdx.x + m * S::kThreads;
       const int rr = c >> 5, col = 4 * (c & 31);
-      const int64_t r = t * kGemmRows + rr;
+      const int64_t r = t * S::kRows + rr;
       v[m] = float4{0.f, 0.f, 0.f, 0.f};  // rows past the end enter the product as zeros
       if (r < rows)
-        v[m] = gemm_epilogue<MODE>(ld4(ys[0] + rr * kTRow + col), r, col, ein_[m], bias, act,
+        v[m] = gemm_epilogue<MODE>(ld4(ys0 + rr * kTRow + col), r, col, ein_[m], bias, act,
                                    ein != nullptr, out0, out1);
     }
-    gemm_stage_x3(vs, rinv[2], v);
+    gemm_stage_x3<kRT>(vs, rinv2, v);
     __syncthreads();
-    gemm_tile(vs, rinv[2], ch, cl, ys[1], w, q, n);
+    gemm_tile<kRT>(vs, rinv2, ch, cl, ys1, cw, rs, q, n);
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < kGemmXPer; ++m) {
-      const int c = threadIdx.x + m * kGemmThreads;
+      const int c = threadIdx.x + m * S::kThreads;
       const int rr = c >> 5, col = 4 * (c & 31);
-      const int64_t r = t * kGemmRows + rr;
+      const int64_t r = t * S::kRows + rr;
       if (r < rows) {
         EpiIn e2;
         e2.res = res2[m];
-        gemm_epilogue<MLCG_NODE_PLAIN>(ld4(ys[1] + rr * kTRow + col), r, col, e2, bias2, act,
+        gemm_epilogue<MLCG_NODE_PLAIN>(ld4(ys1 + rr * kTRow + col), r, col, e2, bias2, act,
                                        false, out2, nullptr);
       }
     }
@@ -760,33 +837,48 @@ int tmm_groups(int64_t rows) {
   return (int)(blocks < kTmmMaxGroups ? blocks : kTmmMaxGroups);
 }
 
+// Row subtiles per node_gemm workgroup: 12 waves (3 per SIMD, at most 168
+// VGPRs) where the epilogue fits, else 8.
 template <int MODE>
-void launch_node_gemm(bool xw, dim3 grid, hipStream_t s, const float* x, int64_t rows,
-                      const float* W, const float* bias, const float* residual, int act,
-                      const float* z, const float* sv, const float* e, const float* f,
-                      float* out0, float* out1) {
-  if (xw)
-    hipLaunchKernelGGL((node_gemm_kernel<MODE, true>), grid, dim3(kGemmThreads), 0, s, x, rows,
-                       W, bias, residual, act, z, sv, e, f, out0, out1);
-  else
-    hipLaunchKernelGGL((node_gemm_kernel<MODE, false>), grid, dim3(kGemmThreads), 0, s, x,
-                       rows, W, bias, residual, act, z, sv, e, f, out0, out1);
+struct GemmRT {
+  static constexpr int value = MODE == MLCG_NODE_DACT2 ? 2 : 3;
+};
+template <int kRT>
+int64_t gemm_tiles(int64_t rows) {
+  return (rows + GemmShape<kRT>::kRows - 1) / GemmShape<kRT>::kRows;
 }
 
 template <int MODE>
-void launch_node_gemm2(bool xw, dim3 grid, hipStream_t s, const float* x, int64_t rows,
+void launch_node_gemm(bool xw, hipStream_t s, const float* x, int64_t rows,
+                      const float* W, const float* bias, const float* residual, int act,
+                      const float* z, const float* sv, const float* e, const float* f,
+                      float* out0, float* out1) {
+  constexpr int kRT = GemmRT<MODE>::value;
+  const dim3 grid(mlcg_persistent_groups(gemm_tiles<kRT>(rows), 1));
+  const dim3 block(GemmShape<kRT>::kThreads);
+  if (xw)
+    hipLaunchKernelGGL((node_gemm_kernel<MODE, true, kRT>), grid, block, 0, s, x, rows, W, bias,
+                       residual, act, z, sv, e, f, out0, out1);
+  else
+    hipLaunchKernelGGL((node_gemm_kernel<MODE, false, kRT>), grid, block, 0, s, x, rows, W, bias,
+                       residual, act, z, sv, e, f, out0, out1);
+}
+
+template <int MODE>
+void launch_node_gemm2(bool xw, hipStream_t s, const float* x, int64_t rows,
                        const float* W, const float* bias, const float* residual, int act,
                        const float* z, const float* sv, const float* e, const float* f,
                        float* out0, float* out1, const float* W2, const float* bias2,
                        const float* residual2, float* out2) {
+  constexpr int kRT = 1;  // both weights in registers: ~240 VGPRs, two workgroups per CU
+  const dim3 grid(mlcg_persistent_groups(gemm_tiles<kRT>(rows), 2));
+  const dim3 block(GemmShape<kRT>::kThreads);
   if (xw)
-    hipLaunchKernelGGL((node_gemm2_kernel<MODE, true>), grid, dim3(kGemmThreads), 0, s, x,
-                       rows, W, bias, residual, act, z, sv, e, f, out0, out1, W2, bias2,
-                       residual2, out2);
+    hipLaunchKernelGGL((node_gemm2_kernel<MODE, true, kRT>), grid, block, 0, s, x, rows, W,
+                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2);
   else
-    hipLaunchKernelGGL((node_gemm2_kernel<MODE, false>), grid, dim3(kGemmThreads), 0, s, x,
-                       rows, W, bias, residual, act, z, sv, e, f, out0, out1, W2, bias2,
-                       residual2, out2);
+    hipLaunchKernelGGL((node_gemm2_kernel<MODE, false, kRT>), grid, block, 0, s, x, rows, W,
+                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2);
 }
 
 // Argument checks shared by mlcg_node_gemm and mlcg_node_gemm2.
@@ -818,25 +910,23 @@ extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const 
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
   if (rc != MLCG_OK || rows == 0) return rc;
-  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  const dim3 grid(mlcg_persistent_groups(tiles, MLCG_NODE_GEMM_PER_CU));
   hipStream_t st = mlcg_stream(stream);
   const bool xw = transpose_w != 0;
   switch (epilogue) {
     case MLCG_NODE_PLAIN:
-      launch_node_gemm<MLCG_NODE_PLAIN>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+      launch_node_gemm<MLCG_NODE_PLAIN>(xw, st, x, rows, W, bias, residual, act, z, s, e,
                                         f, out0, out1);
       break;
     case MLCG_NODE_ACT:
-      launch_node_gemm<MLCG_NODE_ACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e, f,
+      launch_node_gemm<MLCG_NODE_ACT>(xw, st, x, rows, W, bias, residual, act, z, s, e, f,
                                       out0, out1);
       break;
     case MLCG_NODE_DACT:
-      launch_node_gemm<MLCG_NODE_DACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+      launch_node_gemm<MLCG_NODE_DACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
                                        f, out0, out1);
       break;
     default:
-      launch_node_gemm<MLCG_NODE_DACT2>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+      launch_node_gemm<MLCG_NODE_DACT2>(xw, st, x, rows, W, bias, residual, act, z, s, e,
                                         f, out0, out1);
       break;
   }
@@ -854,21 +944,19 @@ extern "C" int mlcg_node_gemm2(const float* x, int64_t rows, int features, const
   const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
   if (rc != MLCG_OK || rows == 0) return rc;
   MLCG_REQUIRE(W2 && out2);
-  const int64_t tiles = (rows + kGemmRows - 1) / kGemmRows;
-  const dim3 grid(mlcg_persistent_groups(tiles, MLCG_NODE_GEMM2_PER_CU));
   hipStream_t st = mlcg_stream(stream);
   const bool xw = transpose_w != 0;
   switch (epilogue) {
     case MLCG_NODE_ACT:
-      launch_node_gemm2<MLCG_NODE_ACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+      launch_node_gemm2<MLCG_NODE_ACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
                                        f, out0, out1, W2, bias2, residual2, out2);
       break;
     case MLCG_NODE_DACT:
-      launch_node_gemm2<MLCG_NODE_DACT>(xw, grid, st, x, rows, W, bias, residual, act, z, s, e,
+      launch_node_gemm2<MLCG_NODE_DACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
                                         f, out0, out1, W2, bias2, residual2, out2);
       break;
     default:
-      launch_node_gemm2<MLCG_NODE_DACT2>(xw, grid, st, x, rows, W, bias, residual, act, z, s,
+      launch_node_gemm2<MLCG_NODE_DACT2>(xw, st, x, rows, W, bias, residual, act, z, s,
                                          e, f, out0, out1, W2, bias2, residual2, out2);
       break;
   }
