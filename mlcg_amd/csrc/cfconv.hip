@@ -298,7 +298,10 @@ __global__ __launch_bounds__(kThreads) void gather_tangent_kernel(
 // and on the upper edges of pair p (when Wbar is given):
 //   Wbar[p]  = gagg2_i y_j + gagg2_j y_i + gagg1_i ydot_j + gagg1_j ydot_i
 //   Wdbar[p] = ddot_p (gagg1_i y_j + gagg1_j y_i)
-template <bool kTangent>
+// The pair-adjoint path is a template parameter: compiled in, its node rows of
+// i and edge state hold 140 VGPRs (3 waves per SIMD); without it the kernel
+// needs about 90 (5 waves per SIMD), as the tangent gather does.
+template <bool kTangent, bool kAdj>
 __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
     const float* __restrict__ gagg2, const float* __restrict__ gagg1,
     const float* __restrict__ y, const float* __restrict__ ydot, const float* __restrict__ W,
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
   const int64_t i = xcd_row();
   if (i >= n) return;
   const bool has_ydot = ydot != nullptr;
-  const bool want_adj = Wbar != nullptr;
+  constexpr bool want_adj = kAdj;
   const float4 g2i = want_adj ? ld4(gagg2, i, m) : f4zero();
   const float4 yi = want_adj ? ld4(y, i, m) : f4zero();
   const float4 g1i = (kTangent && want_adj) ? ld4(gagg1, i, m) : f4zero();
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
         acc.w += g1j[u].w * (wd[u].w * dd[u]);
       }
     }
-    if (want_adj) {
+    if constexpr (want_adj) {
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {
         if (!(ok[u] && k + 2 * u + h >= split)) continue;
@@ -584,14 +587,11 @@ extern "C" int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1, c
   MLCG_REQUIRE(gagg2 && y && W && rowptr && col && eid2pair && ybar2);
   MLCG_REQUIRE((Wbar == nullptr) == (Wdbar == nullptr));
   MLCG_REQUIRE(!gagg1 || (Wd && ddot));
-  if (gagg1)
-    hipLaunchKernelGGL(gather_rev2_kernel<true>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
-                       mlcg_stream(stream), gagg2, gagg1, y, ydot, W, Wd, ddot, rowptr, col,
-                       eid2pair, n_nodes, ybar2, Wbar, Wdbar);
-  else
-    hipLaunchKernelGGL(gather_rev2_kernel<false>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
-                       mlcg_stream(stream), gagg2, gagg1, y, ydot, W, Wd, ddot, rowptr, col,
-                       eid2pair, n_nodes, ybar2, Wbar, Wdbar);
+  auto kern = gagg1 ? (Wbar ? gather_rev2_kernel<true, true> : gather_rev2_kernel<true, false>)
+                    : (Wbar ? gather_rev2_kernel<false, true> : gather_rev2_kernel<false, false>);
+  hipLaunchKernelGGL(kern, dim3(row_groups(n_nodes)), dim3(kThreads), 0, mlcg_stream(stream),
+                     gagg2, gagg1, y, ydot, W, Wd, ddot, rowptr, col, eid2pair, n_nodes, ybar2,
+                     Wbar, Wdbar);
   return mlcg_launch_status();
 }
 
