@@ -33,6 +33,8 @@ from __future__ import annotations
 from dataclasses import dataclass, field, replace
 from typing import List, Optional, Tuple
 
+import os
+
 import torch
 
 from .. import ops
@@ -233,6 +235,46 @@ def _lin_dact2_lin(x, A, z, s, act, e, f, B):
     return v, ops.node_linear(v, B, transpose=True)
 
 
+# Filter forwards of blocks 1.. on the side stream (MLCG_FILTER_AHEAD=0 keeps
+# them in block order on the caller's stream).
+_FILTER_AHEAD = os.environ.get("MLCG_FILTER_AHEAD", "1") != "0"
+
+
+def _filters_ahead(spec: FusedSpec, P: Params, pos: torch.Tensor, graph: ops.PairGraph,
+                   filt) -> dict:
+    """Issues the filter forwards of blocks 1.. on the side stream at the start
+    of the forward: they depend only on the pair distances and the block's
+    filter weights, not on node features, so they run beside block 0's node
+    linears and gathers (memory-bound work that leaves VGPRs and LDS free on
+    each CU).  Returns {k: (W, Wd, event)}; the caller's stream waits on the
+    event before block k's gather.  The outputs are allocated on the caller's
+    stream, which alone uses them afterwards."""
+    if not (_FILTER_AHEAD and pos.is_cuda and len(P.blocks) > 1):
+        return {}
+    main = torch.cuda.current_stream(pos.device)
+    key = (pos.device.index, main.cuda_stream)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=pos.device)
+    side = _SIDE_STREAMS[key]
+    cap = graph.pair_capacity
+    dt = torch.float16 if spec.f16 else torch.float32
+    outs = {k: (torch.empty(cap, ops.NUM_FILTERS, dtype=dt, device=pos.device),
+                torch.empty(cap, ops.NUM_FILTERS, dtype=dt, device=pos.device))
+            for k in range(1, len(P.blocks))}
+    side.wait_stream(main)
+    ahead = {}
+    with torch.cuda.stream(side):
+        for k in range(1, len(P.blocks)):
+            bp = P.blocks[k]
+            W, Wd, _ = ops.filter_fwd(pos, graph, filt, bp.W1, bp.b1, bp.W2, f16=spec.f16,
+                                      want_dist=False, strict_fp32=spec.strict_fp32,
+                                      out=outs[k])
+            ev = torch.cuda.Event()
+            ev.record(side)
+            ahead[k] = (W, Wd, ev)
+    return ahead
+
+
 def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             graph: ops.PairGraph, save: bool = True,
             rev_seed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, State]:
@@ -240,14 +282,22 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     kernel also forms the adjoint a following reverse1(seed=rev_seed) starts
     from."""
     st = State(pos=pos, types=types, graph=graph, filt=filter_spec(spec, P))
+    ahead = _filters_ahead(spec, P, pos, graph, st.filt)
     x = P.emb.index_select(0, types)
     for k, bp in enumerate(P.blocks):
-        W, Wd, dist = ops.filter_fwd(pos, graph, st.filt, bp.W1, bp.b1, bp.W2,
-                                     f16=spec.f16, want_dist=(k == 0),
-                                     strict_fp32=spec.strict_fp32)
+        if k in ahead:
+            W, Wd, done = ahead[k]
+            dist = None
+        else:
+            W, Wd, dist = ops.filter_fwd(pos, graph, st.filt, bp.W1, bp.b1, bp.W2,
+                                         f16=spec.f16, want_dist=(k == 0),
+                                         strict_fp32=spec.strict_fp32)
+            done = None
         if k == 0:
             st.dist = dist
         y = ops.node_linear(x, bp.A1)
+        if done is not None:
+            torch.cuda.current_stream(pos.device).wait_event(done)
         agg = ops.cfconv_gather(y, W, graph)
         # z itself is only read back by the shifted-softplus derivatives;
         # x_next = x + lin(act(z))

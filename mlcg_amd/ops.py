@@ -591,11 +591,14 @@ FILTER_FP32, FILTER_FP16, FILTER_FP32_STRICT = 0, 1, 2
 def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
                b1: torch.Tensor, W2: torch.Tensor, f16: bool = False,
                want_dist: bool = True, strict_fp32: bool = False,
+               out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
                ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """W [P, F], dW/dd [P, F] (fp32, or fp16 when f16) and distances [P].
     fp32 results come from split-fp16 products (about 22 significant bits
     per operand, fp32 accumulation) unless strict_fp32 asks for the fp32
-    MFMA throughout (mlcg_filter_fwd's FP32_STRICT mode)."""
+    MFMA throughout (mlcg_filter_fwd's FP32_STRICT mode).  `out` = (W, Wd)
+    written in place of new tensors (a caller that launches on another
+    stream allocates them on the stream that consumes them)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     _check(F == NUM_FILTERS, f"num_filters must be {NUM_FILTERS} for the HIP filter kernel")
@@ -603,8 +606,14 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
            and tuple(b1.shape) == (F,), "filter weights have unexpected shapes")
     cap = graph.pair_capacity
     dt = torch.float16 if f16 else torch.float32
-    W = torch.empty(cap, F, dtype=dt, device=pos.device)
-    Wd = torch.empty(cap, F, dtype=dt, device=pos.device)
+    if out is None:
+        W = torch.empty(cap, F, dtype=dt, device=pos.device)
+        Wd = torch.empty(cap, F, dtype=dt, device=pos.device)
+    else:
+        W, Wd = out
+        _check(all(t.dtype == dt and tuple(t.shape) == (cap, F) and t.is_contiguous()
+                   and t.device == pos.device for t in (W, Wd)),
+               "filter_fwd out tensors must be contiguous [pair_capacity, 128] of the result dtype")
     dist = torch.empty(cap, dtype=torch.float32, device=pos.device) if want_dist else None
     W1c, b1c, W2c = (t.detach().float().contiguous() for t in (W1, b1, W2))
     call("mlcg_filter_fwd", ptr(pos), ptr(graph.pair_ij), cap, ptr(graph.n_pairs_dev), cap,
