@@ -69,6 +69,11 @@ def parse_args(argv=None):
     p.add_argument("--no-md", action="store_true", help="skip the config-5 MD leg")
     p.add_argument("--gather-probe", action="store_true",
                    help="run the gather access-pattern probe (cold caches)")
+    p.add_argument("--stream-probe", action="store_true",
+                   help="measure the HBM read / copy ceiling with the library's streaming "
+                        "kernels")
+    p.add_argument("--only-probes", action="store_true",
+                   help="run only the requested probes (no config legs)")
     p.add_argument("--no-capture", action="store_true",
                    help="skip the captured (HIP graph) config-2 step")
     p.add_argument("--md-steps", type=int, default=200, help="MD steps of the config-5 leg")
@@ -103,12 +108,15 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
         # forward recomputation of a, a' is not algorithmic work
         return "mfma", (2 * 2 * F * F + 2 * 2 * F * F + 2 * 2 * K_RBF * F) * P, "flop"
     if name == "mlcg_node_gemm":
-        # one [N, 128] x [128, 128] product (its epilogue streams 2-6 [N, 128]
-        # tensors depending on the mode)
-        return "mfma", 2 * N * F * F, "flop"
+        # one [N, 128] x [128, 128] product whose epilogue streams 2-6 [N, 128]
+        # tensors: HBM-bound (at most ~32 FLOP/B against the ~104 FLOP/B
+        # ridge of the split-fp16 MFMA); the wrapper reports each launch's
+        # bytes, this is the plain form's
+        return "hbm", 2 * 4 * F * N + 4 * (F + 1) * F, "byte"
     if name == "mlcg_node_gemm2":
-        # two consecutive [N, 128] x [128, 128] products in one kernel
-        return "mfma", 2 * 2 * N * F * F, "flop"
+        # two consecutive products in one kernel (bytes reported per launch
+        # by the wrapper; this is the smallest form's: x in, two outputs)
+        return "hbm", 3 * 4 * F * N + 2 * 4 * (F + 1) * F, "byte"
     if name == "mlcg_type_sum":
         # the rows of x and their types read once
         return "hbm", 4 * F * N + 8 * N, "byte"
@@ -148,12 +156,7 @@ def algorithmic_work(name: str, E: int, P: int, N: int, B: int, f16: bool = Fals
 # products of split operands: their MFMA ceiling, in fp32-equivalent FLOP/s,
 # is a third of the fp16 peak.  (The filter backward's recomputation of the
 # first layer stays on the fp32 MFMA but is not counted as algorithmic work.)
-SPLIT_FP16 = {"mlcg_filter_fwd", "mlcg_filter_bwd", "mlcg_filter_bwd_cfconv", "mlcg_node_gemm",
-              "mlcg_node_gemm2"}
-# Entry points the training step launches on its second stream, beside the
-# main one: their bracketing events also count time spent sharing the GPU or
-# waiting for CUs, so they are reported but never taken as the dominant kernel.
-SIDE_STREAM = {"mlcg_node_tmm"}
+SPLIT_FP16 = {"mlcg_filter_fwd", "mlcg_filter_bwd", "mlcg_filter_bwd_cfconv"}
 SPLIT_FP16_PEAK_TFLOPS = FP16_MFMA_PEAK_TFLOPS / 3
 
 # entry point -> kernel symbol(s) it launches (as rocprofv3 names them)
@@ -179,15 +182,20 @@ KERNEL_SYMBOL = {
 }
 
 
-def kernel_report(summary, E, P, N, B):
+def kernel_report(summary, E, P, N, B, work=None):
+    """Per entry point: launches, average device time and the roofline
+    fraction of its algorithmic work.  `work` holds the summed work of the
+    launches whose wrapper reported it (the node GEMMs' bytes, which depend
+    on the epilogue); the other entry points use algorithmic_work."""
+    work = work or {}
     rows = {}
     for name, (launches, total_ms) in summary.items():
         w = algorithmic_work(name, E, P, N, B)
+        if w is not None and name in work:
+            w = (w[0], work[name] / max(launches, 1), w[2])
         avg_ms = total_ms / max(launches, 1)
         row = {"kernel": KERNEL_SYMBOL.get(name, name), "launches": launches,
                "avg_us": round(avg_ms * 1e3, 3), "total_ms": round(total_ms, 4)}
-        if name in SIDE_STREAM:
-            row["stream"] = "side (times include sharing the GPU with the main stream)"
         if w is not None:
             bound, amount, unit = w
             if bound == "hbm":
@@ -237,101 +245,9 @@ def build_model(torch, nn, device):
     return model.to(device)
 
 
-def gpu_leg(args):
-    import torch
-
-    from mlcg_amd import _lib, nn, ops, synthetic
-
-    dev = torch.device("cuda:0")
-    torch.manual_seed(synthetic.seed_for(2))
-    model = build_model(torch, nn, dev)
-    gm = nn.GradientsOut(model).train()
-    loss_fn = nn.ForceMSE()
-    # torch's fused AdamW: the same update in one multi-tensor kernel launch per
-    # chunk instead of one per elementwise stage (about 25 us less per step)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0, fused=True)
-    b = synthetic.config2(n_frames=args.frames)
-    data = b.to_torch(dev)
-    graph = model.build_graph(data)
-    E, P, N, B = graph.num_edges, graph.num_pairs, graph.num_nodes, b.n_frames
-    del graph
-    if not args.exact_graph:
-        # fixed-capacity radius graph: no host synchronisation inside the step
-        # (the edge count stays on the device); overflow is checked after the
-        # timed region, so the graph used is exactly the one sized above
-        cap = int(E * 1.02) + 64
-        model.graph_capacity = cap + (cap % 2)
-
-    def step():
-        opt.zero_grad(set_to_none=True)
-        out = gm(data)
-        out.out.update(**out.out[model.name])
-        loss = loss_fn(out)
-        loss.backward()
-        opt.step()
-        return loss
-
-    for _ in range(max(args.warmup, 1)):
-        step()
-    torch.cuda.synchronize()
-    # a short profiling pass (outside the timed region) with every HIP entry
-    # point bracketed, to find the dominant kernel and report all of them
-    n_prof = 3
-    timer = _lib.LaunchTimer(None)
-    _lib.set_timer(timer)
-    for _ in range(n_prof):
-        step()
-    torch.cuda.synchronize()
-    _lib.set_timer(None)
-    warm = kernel_report(timer.summary(), E, P, N, B)
-    per_step = {k: v["total_ms"] / n_prof for k, v in warm.items()}
-    dominant = max((k for k in per_step if k not in SIDE_STREAM), key=per_step.get)
-
-    # timed region: only the dominant kernel's launches are bracketed (HIP
-    # events on the stream it runs on)
-    timer = _lib.LaunchTimer({dominant})
-    _lib.set_timer(timer)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        loss = step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    _lib.set_timer(None)
-    ms = (t1 - t0) * 1e3 / args.steps
-    assert math.isfinite(float(loss.detach())), "non-finite loss"
-    if model.graph_capacity is not None:
-        flags = int(model.last_graph.flags.item())
-        assert flags == 0, f"radius graph overflowed its capacity (flags {flags})"
-        assert int(model.last_graph.rowptr[-1]) == E, "edge count changed"
-    dom = kernel_report(timer.summary(), E, P, N, B)[dominant]
-    # the same step with the filter forward on the fp32 MFMA throughout
-    # (MLCG_FILTER_FP32_STRICT) instead of split-fp16 products, for comparison
-    model.strict_fp32_filters = True
-    for _ in range(2):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    strict_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    model.strict_fp32_filters = False
-    return {"ms_per_step": ms, "E": E, "P": P, "N": N, "B": B, "dominant": dominant,
-            "strict_fp32_ms_per_step": strict_ms,
-            "dominant_row": dom, "kernels": warm, "loss": float(loss.detach()),
-            "step_kernel_ms": round(sum(per_step.values()), 4)}
-
-
-def captured_leg(args, E):
-    """The same config-2 training step captured once as a HIP graph and
-    replayed: the host issues one graph launch per step instead of ~140 kernel
-    launches.  Built as torch's capture rules require: AdamW with
-    capturable=True (a non-capturable optimizer raises inside the capture
-    region, after which ending the capture is undefined), the warm-up steps
-    and the capture on one side stream (never on the default stream), and no
-    event timing inside the capture.  Fresh model and optimizer from the same
-    seed as the eager leg."""
+def _config2(args, capturable=False):
+    """The config-2 model, its force-matching step function, the AdamW and
+    the resident batch (fresh model from the benchmark seed)."""
     import torch
 
     from mlcg_amd import nn, synthetic
@@ -341,49 +257,180 @@ def captured_leg(args, E):
     model = build_model(torch, nn, dev)
     gm = nn.GradientsOut(model).train()
     loss_fn = nn.ForceMSE()
+    # torch's fused AdamW: the update in one multi-tensor kernel launch per
+    # chunk instead of one per elementwise stage
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.0, fused=True,
-                            capturable=True)
+                            capturable=capturable)
     data = synthetic.config2(n_frames=args.frames).to_torch(dev)
-    cap = int(E * 1.02) + 64
-    model.graph_capacity = cap + (cap % 2)
 
-    def step():
+    def step(d=data):
         opt.zero_grad(set_to_none=True)
-        out = gm(data)
+        out = gm(d)
         out.out.update(**out.out[model.name])
         loss = loss_fn(out)
         loss.backward()
         opt.step()
         return loss
 
-    side = torch.cuda.Stream(device=dev)
-    side.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(side):
-        for _ in range(3):
-            step()
-    torch.cuda.current_stream(dev).wait_stream(side)
+    return model, step, opt, data
+
+
+def _device_ms_per_step(step, k=5):
+    """Device time of k steps with the host issue kept off the critical
+    path: a spin kernel holds the stream while the host queues the k steps,
+    and HIP events bracket the steps behind it."""
+    import torch
+
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
-        static_loss = step()
-    for _ in range(max(args.warmup, 1)):
-        graph.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(1_000_000)
+    e1.record()
+    torch.cuda.synchronize()
+    cyc_per_ms = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    # enough spin for the host to queue every step (generously: 10 ms each)
+    torch.cuda._sleep(int(cyc_per_ms * 10.0 * k))
+    e0.record()
+    for _ in range(k):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / k
+
+
+def _host_issue_ms(step, reps=7):
+    """Host time for step() to return (no synchronisation inside), each
+    repetition starting from an idle, drained stream."""
+    import torch
+
+    t = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        t.append((time.perf_counter() - t0) * 1e3)
+    torch.cuda.synchronize()
+    return statistics.median(t)
+
+
+def _timed_steps(step, steps):
+    import torch
+
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
+    for _ in range(steps):
+        loss = step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    loss = float(static_loss.detach())
+    return (time.perf_counter() - t0) * 1e3 / steps, loss
+
+
+def gpu_leg(args):
+    import torch
+
+    from mlcg_amd import _lib
+    from mlcg_amd.nn import _fused
+
+    model, step, opt, data = _config2(args)
+    graph = model.build_graph(data)
+    E, P, N, B = graph.num_edges, graph.num_pairs, graph.num_nodes, int(data.n_atoms.numel())
+    del graph
+    if not args.exact_graph:
+        # fixed-capacity radius graph: no host synchronisation inside the step
+        # (the edge count stays on the device); overflow is checked after the
+        # timed region, so the graph used is exactly the one sized above
+        cap = int(E * 1.02) + 64
+        model.graph_capacity = cap + (cap % 2)
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    # per-kernel profiling pass (outside the timed region), every HIP entry
+    # point bracketed by events, with the whole step on one stream (filter
+    # forwards in block order, weight-gradient reductions inline) so that no
+    # launch shares the GPU with another stream's work: stand-alone times
+    ahead, side = _fused._FILTER_AHEAD, _fused._TMM_SIDE
+    _fused._FILTER_AHEAD = _fused._TMM_SIDE = False
+    n_prof = 3
+    timer = _lib.LaunchTimer(None)
+    _lib.set_timer(timer)
+    for _ in range(n_prof):
+        step()
+    torch.cuda.synchronize()
+    _lib.set_timer(None)
+    _fused._FILTER_AHEAD, _fused._TMM_SIDE = ahead, side
+    warm = kernel_report(timer.summary(), E, P, N, B, timer.work())
+    per_step = {k: v["total_ms"] / n_prof for k, v in warm.items()}
+    dominant = max(per_step, key=per_step.get)
+
+    # timed region: only the dominant kernel's launches are bracketed (HIP
+    # events on the stream it runs on)
+    timer = _lib.LaunchTimer({dominant})
+    _lib.set_timer(timer)
+    ms, loss = _timed_steps(step, args.steps)
+    _lib.set_timer(None)
+    assert math.isfinite(float(loss.detach())), "non-finite loss"
+    if model.graph_capacity is not None:
+        flags = int(model.last_graph.flags.item())
+        assert flags == 0, f"radius graph overflowed its capacity (flags {flags})"
+        assert int(model.last_graph.rowptr[-1]) == E, "edge count changed"
+    dom = kernel_report(timer.summary(), E, P, N, B, timer.work())[dominant]
+    # where the eager step's time goes: the host's issue time of one step
+    # and the device time of a step queued ahead of the GPU
+    host_ms = _host_issue_ms(step)
+    dev_ms = _device_ms_per_step(step)
+    # the same step with the filter forwards in block order on one stream
+    _fused._FILTER_AHEAD = False
+    step()
+    noahead_ms, _ = _timed_steps(step, args.steps)
+    noahead_dev_ms = _device_ms_per_step(step)
+    _fused._FILTER_AHEAD = ahead
+    # the same step with the filter forward on the fp32 MFMA throughout
+    # (MLCG_FILTER_FP32_STRICT) instead of split-fp16 products, for comparison
+    model.strict_fp32_filters = True
+    for _ in range(2):
+        step()
+    strict_ms, _ = _timed_steps(step, args.steps)
+    model.strict_fp32_filters = False
+    return {"ms_per_step": ms, "E": E, "P": P, "N": N, "B": B, "dominant": dominant,
+            "strict_fp32_ms_per_step": strict_ms,
+            "host_issue_ms": host_ms, "device_ms": dev_ms,
+            "filter_ahead_off": {"ms_per_step": round(noahead_ms, 4),
+                                 "device_ms_per_step": round(noahead_dev_ms, 4)},
+            "dominant_row": dom, "kernels": warm, "loss": float(loss.detach()),
+            "step_kernel_ms": round(sum(per_step.values()), 4)}
+
+
+def captured_leg(args, E):
+    """The same config-2 training step recorded once as a HIP graph
+    (mlcg_amd.pl.CapturedTrainStep: capturable AdamW, warm-up and capture on
+    a side stream) and replayed: one host launch per step.  Every timed step
+    first loads its batch into the recorded inputs (device-to-device copies
+    of positions, forces, types, batch vector and frame sizes from a second
+    resident copy of the batch), as a training loop feeding new batches
+    would.  Fresh model and optimizer from the same seed as the eager leg."""
+    import torch
+
+    from mlcg_amd.pl import CapturedTrainStep
+
+    model, step, opt, data = _config2(args, capturable=True)
+    cap = int(E * 1.02) + 64
+    model.graph_capacity = cap + (cap % 2)
+    cs = CapturedTrainStep(lambda d: step(d), data, model, opt, warmup=3)
+    batch = data.clone()
+
+    def replay():
+        return cs.step(batch)
+
+    for _ in range(max(args.warmup, 1)):
+        replay()
+    ms, loss = _timed_steps(replay, args.steps)
+    dev_ms = _device_ms_per_step(replay)
+    loss = float(loss.detach())
     assert math.isfinite(loss), "non-finite loss in the captured step"
-    flags = int(model.last_graph.flags.item())
-    assert flags == 0, f"radius graph overflowed its capacity (flags {flags})"
+    cs.check()
     assert int(model.last_graph.rowptr[-1]) == E, "edge count changed"
-    return {"ms_per_step": round(ms, 4), "edges_per_s": E * N_BLOCKS / (ms * 1e-3),
-            "loss": loss,
-            "note": "same step as the headline (radius graph, energy, forces, double backward, "
-                    "AdamW), captured once as a HIP graph and replayed; the headline value is "
-                    "the eager step"}
+    return {"ms_per_step": ms, "device_ms_per_step": round(dev_ms, 4),
+            "edges_per_s": E * N_BLOCKS / (ms * 1e-3), "loss": loss}
 
 
 def gather_ceiling_leg(reps=10):
@@ -473,6 +520,60 @@ def gather_ceiling_leg(reps=10):
     return out
 
 
+def stream_leg(reps=5):
+    """The HBM ceiling of this part, measured with this library's streaming
+    kernels (mlcg_stream_read / mlcg_stream_copy: grid-stride loops, 16-byte
+    loads, `unroll` loads in flight per thread), caches evicted by a 1 GiB
+    read before every timed launch.  Sizes: 1 GiB (the asymptote) and the
+    byte counts of the config-2 gathers (~130 and ~250 MB) and of one node
+    tensor (9 MB), where launch ramp-up and tail are part of the time.  For
+    every size the best launch shape of the sweep is kept."""
+    import torch
+
+    from mlcg_amd import _lib
+
+    dev = torch.device("cuda:0")
+    flush = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+    partial = torch.empty(65536, dtype=torch.float32, device=dev)
+    sizes = {"1GiB": 1 << 30, "250MB": 250_000_000, "130MB": 130_000_000, "9MB": 9_175_040}
+    src = torch.ones((1 << 30) // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    for label, nbytes in sizes.items():
+        n = (nbytes // 16) * 4
+        best = {}
+        for kind in ("read", "copy"):
+            for groups in (512, 1024, 2048, 4096, 8192):
+                for unroll in (4, 8, 16):
+                    ts = []
+                    for _ in range(reps):
+                        flush.sum()
+                        torch.cuda.synchronize()
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        if kind == "read":
+                            _lib.call("mlcg_stream_read", src.data_ptr(), n, groups, unroll,
+                                      partial.data_ptr(), stream)
+                        else:
+                            _lib.call("mlcg_stream_copy", src.data_ptr(), dst.data_ptr(), n,
+                                      groups, unroll, stream)
+                        e1.record()
+                        torch.cuda.synchronize()
+                        ts.append(e0.elapsed_time(e1) * 1e-3)
+                    t = statistics.median(ts)
+                    moved = 4 * n * (1 if kind == "read" else 2)
+                    gbs = moved / t / 1e9
+                    if kind not in best or gbs > best[kind]["GB_per_s"]:
+                        best[kind] = {"GB_per_s": round(gbs, 1), "us": round(t * 1e6, 2),
+                                      "groups": groups, "unroll": unroll,
+                                      "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4)}
+        out[label] = best
+    del flush, src, dst
+    return out
+
+
 def radius_leg(reps=10):
     """Config 3 radius graph, inputs resident in HBM.  Figures: the exactly
     sized call end to end (sizing pass, one host synchronisation to size the
@@ -558,19 +659,30 @@ def fp16_leg(reps=5):
     gm = nn.GradientsOut(model).eval()
     b = synthetic.config4()
     data = b.to_torch(dev)
+    from mlcg_amd.nn import _fused
+
     with torch.no_grad():
         gm(data)
         torch.cuda.synchronize()
         E, P = model.last_graph.num_edges, model.last_graph.num_pairs
         t = []
-        timer = _lib.LaunchTimer({"mlcg_filter_fwd"})
         for _ in range(reps):
-            _lib.set_timer(timer)
+            torch.cuda.synchronize()
             t0 = time.perf_counter()
             gm(data)
             torch.cuda.synchronize()
             t.append(time.perf_counter() - t0)
-            _lib.set_timer(None)
+        # the filter kernel's stand-alone launch time: filter forwards in
+        # block order on one stream, bracketed by events
+        ahead = _fused._FILTER_AHEAD
+        _fused._FILTER_AHEAD = False
+        timer = _lib.LaunchTimer({"mlcg_filter_fwd"})
+        _lib.set_timer(timer)
+        for _ in range(2):
+            gm(data)
+        torch.cuda.synchronize()
+        _lib.set_timer(None)
+        _fused._FILTER_AHEAD = ahead
     s = statistics.median(t)
     n_l, tot = timer.summary()["mlcg_filter_fwd"]
     avg = tot / n_l
@@ -617,7 +729,11 @@ def md_leg(steps):
     sim.simulate()
     sps = sim.timed_steps / sim.timed_seconds
     # per-kernel device times of the force evaluation, eagerly, on the final state
+    from mlcg_amd.nn import _fused
+
     data = sim.final_data
+    ahead = _fused._FILTER_AHEAD
+    _fused._FILTER_AHEAD = False  # one stream: stand-alone launch times
     with torch.no_grad():
         model(data)
         torch.cuda.synchronize()
@@ -628,12 +744,14 @@ def md_leg(steps):
             model(data)
         torch.cuda.synchronize()
         _lib.set_timer(None)
+    _fused._FILTER_AHEAD = ahead
     g = schnet.last_graph
     N = data.pos.shape[0]
     E = int(g.rowptr[-1].item())
     P = int(g.pairptr[-1].item())
     summ = {k: (v[0] // reps, v[1] / reps) for k, v in timer.summary().items()}
-    rows = kernel_report(summ, E, P, N, sim.n_sims)
+    rows = kernel_report(summ, E, P, N, sim.n_sims,
+                         {k: v / reps for k, v in timer.work().items()})
     dom = max(rows, key=lambda k: rows[k]["total_ms"])
     d = rows[dom]
     roof = {k: d.get(k) for k in ("bound", "achieved", "peak", "unit", "frac")}
@@ -868,6 +986,17 @@ def main(argv=None):
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only_probes:
+        res = {}
+        if args.stream_probe:
+            res["stream"] = stream_leg()
+        if args.gather_probe:
+            res["gather_ceiling"] = gather_ceiling_leg()
+        print(json.dumps(res))
+        return 0
+    sp = stream_leg() if args.stream_probe else None
+    if sp:
+        print("[bench] stream probe " + json.dumps(sp), flush=True)
     g = gpu_leg(args)
     print(f"[bench] gpu leg done: {g['ms_per_step']:.3f} ms/step, E={g['E']}", flush=True)
     cg = None if args.no_capture else captured_leg(args, g["E"])
@@ -892,6 +1021,15 @@ def main(argv=None):
     if cpu_cfg:
         print("[bench] cpu configs 1, 3, 4, 5 done", flush=True)
 
+    # per-kernel tables go on their own lines before the result line, which
+    # stays short enough to be kept whole by a log tail
+    print("[bench] config2 kernels " + json.dumps(g["kernels"]), flush=True)
+    if md:
+        print("[bench] config5 kernels " + json.dumps(md.pop("kernels")), flush=True)
+        md.pop("prior_constants", None)
+    if cpu_cfg:
+        print("[bench] cpu baselines of configs 1, 3, 4, 5 " + json.dumps(cpu_cfg), flush=True)
+
     ms = g["ms_per_step"]
     value = g["E"] * N_BLOCKS / (ms * 1e-3)
     dom = g["dominant_row"]
@@ -900,6 +1038,9 @@ def main(argv=None):
                 "peak": dom.get("peak"), "unit": dom.get("unit"), "frac": dom.get("frac"),
                 "traffic": load_traffic(sym), "kernel": sym,
                 "avg_launch_us": dom["avg_us"], "launches": dom["launches"]}
+    kr = g["kernels"]
+    brief = {k: {kk: v[kk] for kk in ("avg_us", "frac") if kk in v}
+             for k, v in kr.items() if v["total_ms"] / 3 > 0.02}
     line = {
         "metric": "CFConv fwd+force+double-bwd edges/s",
         "value": value,
@@ -919,21 +1060,20 @@ def main(argv=None):
                    "frames": g["B"], "beads_per_frame": g["N"] // max(g["B"], 1),
                    "edges": g["E"], "pairs": g["P"], "blocks": N_BLOCKS},
         "frames_per_s": g["B"] / (ms * 1e-3),
-        "strict_fp32_filter_step": {
-            "ms_per_step": round(g["strict_fp32_ms_per_step"], 4),
-            "edges_per_s": g["E"] * N_BLOCKS / (g["strict_fp32_ms_per_step"] * 1e-3),
-            "note": "same step, filter forward on the fp32 MFMA (MLCG_FILTER_FP32_STRICT) "
-                    "instead of split-fp16 products; both meet the element-wise parity bar"},
+        "eager_step": {"host_issue_ms": round(g["host_issue_ms"], 4),
+                       "device_ms": round(g["device_ms"], 4),
+                       "filter_ahead_off": g["filter_ahead_off"]},
         "captured_step": cg,
-        "gather_ceiling": gc,
+        "strict_fp32_filter_step_ms": round(g["strict_fp32_ms_per_step"], 4),
         "roofline": roofline,
-        "kernels": g["kernels"],
+        "kernels_us_frac": brief,
         "step_kernel_ms": g["step_kernel_ms"],
         "radius_graph": rg,
         "fp16_config4": f16,
         "md_config5": md,
+        "gather_ceiling": gc,
+        "stream_ceiling": sp,
         "cpu_baseline": cpu,
-        "cpu_baselines_other_configs": cpu_cfg,
     }
     print(json.dumps(line))
     return 0

@@ -469,6 +469,20 @@ int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
                   float* out, float* colsum_a1, float* workspace,
                   int64_t workspace_floats, void* stream);
 
+/* `count` (1..4) independent mlcg_node_tmm reductions over the same number
+ * of rows in one launch pair: problems holds 6 pointers per reduction,
+ * {a1, b1, a2, b2, out, colsum_a1} (a2/b2 and colsum_a1 may be NULL), as in
+ * mlcg_node_tmm.  Each reduction splits its rows over about 256 / count
+ * workgroups, so each result is deterministic (run-to-run identical) though
+ * not bit-equal to a single mlcg_node_tmm call.  The weight-gradient
+ * reductions of one interaction block (lin, conv.lin2, conv.lin1 of
+ * schnet.py:259-261,343,347 through the double backward) are one batch.
+ * mlcg_node_tmm_batch_workspace_floats(rows, count) floats of workspace. */
+int64_t mlcg_node_tmm_batch_workspace_floats(int64_t rows, int count);
+int mlcg_node_tmm_batch(const void* const* problems, int count, int64_t rows,
+                        int features, int accumulate, float* workspace,
+                        int64_t workspace_floats, void* stream);
+
 /* out [num_types, 128] = for each type t the sum of the rows of x [rows, 128]
  * whose types[row] == t: the gradient of the bead-type embedding table
  * (schnet.py:132, `x = self.embedding_layer(data.atom_types)`, whose
@@ -605,6 +619,24 @@ int mlcg_philox_normals(uint64_t seed, int64_t step, int64_t n_nodes, float* out
 enum { MLCG_MATH_TANH = 0, MLCG_MATH_SIGMOID = 1, MLCG_MATH_SOFTPLUS = 2,
        MLCG_MATH_SINPI = 3, MLCG_MATH_COSPI = 4 };
 int mlcg_math_eval(int fn, const float* x, int64_t n, float* y, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* HBM ceiling probes                                                      */
+/* ---------------------------------------------------------------------- */
+
+/* Streaming read of n floats (n % 4 == 0, src 16-byte aligned) by `groups`
+ * 256-thread workgroups in a grid-stride loop with `unroll` (1, 4, 8, 16)
+ * 16-byte loads in flight per thread; partial[g] = sum of what workgroup g
+ * read.  No counterpart in the reference: it measures the HBM read ceiling
+ * that the memory-bound kernels above are compared with. */
+int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
+                     float* partial, void* stream);
+
+/* Streaming copy dst[i] = src[i] of n floats, the same launch shapes as
+ * mlcg_stream_read.  No counterpart in the reference: the read + write
+ * ceiling. */
+int mlcg_stream_copy(const float* src, float* dst, int64_t n, int groups,
+                     int unroll, void* stream);
 
 #ifdef __cplusplus
 }

@@ -84,6 +84,8 @@ _SIGNATURES = {
     "mlcg_out_rev2": [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P,
                       _P, _P, _P, _I64, _P],
     "mlcg_node_tmm_workspace_floats": [_I64],
+    "mlcg_node_tmm_batch_workspace_floats": [_I64, _I32],
+    "mlcg_node_tmm_batch": [_P, _I32, _I64, _I32, _I32, _P, _I64, _P],
     "mlcg_node_tmm": [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _I64, _P],
     "mlcg_type_sum_workspace_floats": [_I64, _I32],
     "mlcg_type_sum": [_P, _P, _I64, _I32, _I32, _P, _P, _P, _I64, _P],
@@ -95,10 +97,13 @@ _SIGNATURES = {
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
     "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
+    "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
+    "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_radius_workspace_bytes": _I64,
              "mlcg_filter_bwd_workspace_floats": _I64, "mlcg_node_tmm_workspace_floats": _I64,
+             "mlcg_node_tmm_batch_workspace_floats": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,
              "mlcg_type_sum_workspace_floats": _I64}
@@ -154,19 +159,24 @@ class LaunchTimer:
     device time of each launch can be read after a synchronisation.
 
     ``watch`` is a set of entry-point names, or None for every entry point.
+    A wrapper may pass the algorithmic work of a launch (bytes or FLOPs, as
+    the wrapper knows the shapes and the epilogue); ``work()`` sums it.
     """
 
     def __init__(self, watch=None):
         self.watch = None if watch is None else set(watch)
         self.events = {}
+        self.amounts = {}
 
     def wants(self, name: str) -> bool:
         return self.watch is None or name in self.watch
 
-    def record(self, name: str):
+    def record(self, name: str, work=None):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         self.events.setdefault(name, []).append((start, end))
+        if work is not None:
+            self.amounts[name] = self.amounts.get(name, 0) + work
         return start, end
 
     def summary(self):
@@ -174,8 +184,13 @@ class LaunchTimer:
         return {k: (len(v), sum(s.elapsed_time(e) for s, e in v))
                 for k, v in self.events.items()}
 
+    def work(self):
+        """{name: summed work of the launches whose wrapper reported it}."""
+        return dict(self.amounts)
+
 
 _timer: Optional[LaunchTimer] = None
+_fns = {}
 
 
 def set_timer(timer: Optional[LaunchTimer]) -> Optional[LaunchTimer]:
@@ -185,11 +200,14 @@ def set_timer(timer: Optional[LaunchTimer]) -> Optional[LaunchTimer]:
     return old
 
 
-def call(name: str, *args) -> None:
-    """Call an entry point and raise RuntimeError on a non-zero status."""
-    fn = getattr(load(), name)
+def call(name: str, *args, work=None) -> None:
+    """Call an entry point and raise RuntimeError on a non-zero status.
+    ``work`` (optional) is the launch's algorithmic work for a LaunchTimer."""
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
     if _timer is not None and _timer.wants(name):
-        start, end = _timer.record(name)
+        start, end = _timer.record(name, work)
         start.record()
         status = fn(*args)
         end.record()
@@ -208,9 +226,14 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return t.data_ptr()
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
 def stream_handle(device: Optional[torch.device] = None) -> int:
-    """hipStream_t of torch's current stream on `device`."""
-    return torch.cuda.current_stream(device).cuda_stream
+    """hipStream_t of torch's current stream on `device` (read without
+    building a torch Stream object)."""
+    idx = device.index if device is not None else None
+    return _raw_stream(torch.cuda.current_device() if idx is None else idx)
 
 
 def require_device(*tensors: torch.Tensor) -> None:

@@ -144,17 +144,19 @@ __device__ __forceinline__ void tmm_accumulate(const __bf16* ma, const __bf16* m
   }
 }
 
-// Workgroup g reduces the 32-row blocks [g B / G, (g+1) B / G) of the
+// Workgroup g of G reduces the 32-row blocks [g B / G, (g+1) B / G) of the
 // B = ceil(rows / 32) blocks: per block, each thread loads (the next block's
 // loads in flight during the products) and splits one 8 x 4 piece of one
 // matrix, and wave (rg, cg) = (w / 4, w % 4) accumulates output rows
 // 64 rg .. + 63 and columns 32 cg .. + 31.  Writes its partial [128, 128]
 // (+ the column sums of a1, added per thread in row order and over the four
 // row groups in order).
-__global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
-    const float* __restrict__ a1, const float* __restrict__ b1,
-    const float* __restrict__ a2, const float* __restrict__ b2, int64_t rows,
-    int want_colsum, float* __restrict__ partial) {
+__device__ __forceinline__ void tmm_body(const float* __restrict__ a1,
+                                         const float* __restrict__ b1,
+                                         const float* __restrict__ a2,
+                                         const float* __restrict__ b2, int64_t rows,
+                                         int want_colsum, float* __restrict__ o, int64_t g,
+                                         int64_t G) {
   __shared__ __align__(16) __bf16 lds[4 * kTmmMat];
   __shared__ float4 csum[4][kF / 4];
   const int w = threadIdx.x / MLCG_WAVE;
@@ -165,10 +167,9 @@ __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
   const int mat = threadIdx.x >> 7;  // the matrix this thread loads
   const float* src = mat == 0 ? a1 : mat == 1 ? b1 : mat == 2 ? a2 : b2;
   const bool loads = mat < 2 || two;
-  const int64_t G = gridDim.x;
   const int64_t nb = (rows + kTmmK - 1) / kTmmK;
-  const int64_t r_beg = kTmmK * (nb * blockIdx.x / G);
-  const int64_t r_stop = kTmmK * (nb * (blockIdx.x + 1) / G);
+  const int64_t r_beg = kTmmK * (nb * g / G);
+  const int64_t r_stop = kTmmK * (nb * (g + 1) / G);
   const int64_t r_end = r_stop < rows ? r_stop : rows;
   floatx4 acc[4][2];
 #pragma unroll
@@ -195,7 +196,6 @@ __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     if (two) tmm_accumulate(lds + 2 * kTmmMat, lds + 3 * kTmmMat, rg, cg, q, n, acc);
     __syncthreads();
   }
-  float* o = partial + (int64_t)blockIdx.x * kTmmPart;
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
@@ -209,25 +209,58 @@ __global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
     if (threadIdx.x < kF / 4) {
       float4 t = csum[0][threadIdx.x];
 #pragma unroll
-      for (int g = 1; g < 4; ++g) {
-        t.x += csum[g][threadIdx.x].x;
-        t.y += csum[g][threadIdx.x].y;
-        t.z += csum[g][threadIdx.x].z;
-        t.w += csum[g][threadIdx.x].w;
+      for (int gg = 1; gg < 4; ++gg) {
+        t.x += csum[gg][threadIdx.x].x;
+        t.y += csum[gg][threadIdx.x].y;
+        t.z += csum[gg][threadIdx.x].z;
+        t.w += csum[gg][threadIdx.x].w;
       }
       *reinterpret_cast<float4*>(o + kF * kF + 4 * threadIdx.x) = t;
     }
   }
 }
 
+__global__ __launch_bounds__(kTmmThreads) void node_tmm_kernel(
+    const float* __restrict__ a1, const float* __restrict__ b1,
+    const float* __restrict__ a2, const float* __restrict__ b2, int64_t rows,
+    int want_colsum, float* __restrict__ partial) {
+  tmm_body(a1, b1, a2, b2, rows, want_colsum, partial + (int64_t)blockIdx.x * kTmmPart,
+           blockIdx.x, gridDim.x);
+}
+
+// Up to kTmmMaxProblems independent reductions over the same number of rows
+// in one launch: problem blockIdx.y, its workgroup blockIdx.x of gridDim.x,
+// partials at problem * gridDim.x * kTmmPart.  Each problem's result is the
+// one node_tmm_kernel gives with the same group count, bit for bit.
+constexpr int kTmmMaxProblems = 4;
+struct TmmProblem {
+  const float* a1;
+  const float* b1;
+  const float* a2;
+  const float* b2;
+  float* out;
+  float* colsum;
+};
+struct TmmBatch {
+  TmmProblem p[kTmmMaxProblems];
+};
+
+__global__ __launch_bounds__(kTmmThreads) void node_tmm_batch_kernel(TmmBatch batch,
+                                                                     int64_t rows,
+                                                                     float* __restrict__ partial) {
+  const TmmProblem& pr = batch.p[blockIdx.y];
+  tmm_body(pr.a1, pr.b1, rows == 0 ? nullptr : pr.a2, pr.b2, rows, pr.colsum != nullptr ? 1 : 0,
+           partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kTmmPart, blockIdx.x,
+           gridDim.x);
+}
+
 // out (+)= sum of the `slices` partials (and colsum likewise).  A block
 // covers 64 outputs with 8 waves, wave g summing the partials s = g (mod 8)
 // (two interleaved accumulators); the 8 wave sums are combined in a fixed
 // order.
-__global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __restrict__ partial,
-                                                              int slices, int accumulate,
-                                                              float* __restrict__ out,
-                                                              float* __restrict__ colsum) {
+__device__ __forceinline__ void tmm_reduce_body(const float* __restrict__ partial, int slices,
+                                                int accumulate, float* __restrict__ out,
+                                                float* __restrict__ colsum) {
   __shared__ float part[8][64];
   const int o = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int j = blockIdx.x * 64 + o;
@@ -246,6 +279,23 @@ __global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __res
     float* dst = j < kF * kF ? out + j : colsum + (j - kF * kF);
     *dst = accumulate ? *dst + v : v;
   }
+}
+
+__global__ __launch_bounds__(512) void node_tmm_reduce_kernel(const float* __restrict__ partial,
+                                                              int slices, int accumulate,
+                                                              float* __restrict__ out,
+                                                              float* __restrict__ colsum) {
+  tmm_reduce_body(partial, slices, accumulate, out, colsum);
+}
+
+// The batch form: problem blockIdx.y; blocks past the 128 x 128 outputs of a
+// problem without column sums return at once.
+__global__ __launch_bounds__(512) void node_tmm_reduce_batch_kernel(
+    const float* __restrict__ partial, int slices, int accumulate, TmmBatch batch) {
+  const TmmProblem& pr = batch.p[blockIdx.y];
+  if (pr.colsum == nullptr && blockIdx.x * 64 >= kF * kF) return;
+  tmm_reduce_body(partial + (int64_t)blockIdx.y * slices * kTmmPart, slices, accumulate, pr.out,
+                  pr.colsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -985,6 +1035,51 @@ extern "C" int mlcg_node_tmm(const float* a1, const float* b1, const float* a2,
   const int outs = kF * kF + (colsum_a1 ? kF : 0);
   hipLaunchKernelGGL(node_tmm_reduce_kernel, dim3(outs / 64), dim3(512), 0, s, workspace, groups,
                      accumulate, out, colsum_a1);
+  return mlcg_launch_status();
+}
+
+// Workgroups per problem of the batch form: together about one per CU, but
+// at most 16 row blocks per workgroup while the count stays within
+// kTmmMaxGroups (the fp32 accumulation error grows with the rows each
+// workgroup sums; 16 blocks is what the single form reaches at ~128k rows).
+int tmm_batch_groups(int64_t rows, int count) {
+  const int64_t blocks = rows == 0 ? 1 : (rows + kTmmK - 1) / kTmmK;
+  int64_t want = kTmmMaxGroups / (count < 1 ? 1 : count);
+  const int64_t by_depth = (blocks + 15) / 16;
+  if (by_depth > want) want = by_depth < kTmmMaxGroups ? by_depth : kTmmMaxGroups;
+  return (int)(blocks < want ? blocks : want);
+}
+
+extern "C" int64_t mlcg_node_tmm_batch_workspace_floats(int64_t rows, int count) {
+  if (rows < 0 || count < 1 || count > kTmmMaxProblems) return -1;
+  return (int64_t)count * tmm_batch_groups(rows, count) * kTmmPart;
+}
+
+extern "C" int mlcg_node_tmm_batch(const void* const* problems, int count, int64_t rows,
+                                   int features, int accumulate, float* workspace,
+                                   int64_t workspace_floats, void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(problems && count >= 1 && count <= kTmmMaxProblems && rows >= 0 && workspace);
+  TmmBatch batch{};
+  for (int k = 0; k < count; ++k) {
+    const void* const* e = problems + 6 * k;
+    TmmProblem& pr = batch.p[k];
+    pr.a1 = static_cast<const float*>(e[0]);
+    pr.b1 = static_cast<const float*>(e[1]);
+    pr.a2 = static_cast<const float*>(e[2]);
+    pr.b2 = static_cast<const float*>(e[3]);
+    pr.out = static_cast<float*>(const_cast<void*>(e[4]));
+    pr.colsum = static_cast<float*>(const_cast<void*>(e[5]));
+    MLCG_REQUIRE(pr.out && (rows == 0 || (pr.a1 && pr.b1)));
+    MLCG_REQUIRE((pr.a2 == nullptr) == (pr.b2 == nullptr));
+  }
+  const int groups = tmm_batch_groups(rows, count);
+  MLCG_REQUIRE(workspace_floats >= (int64_t)count * groups * kTmmPart);
+  hipStream_t s = mlcg_stream(stream);
+  hipLaunchKernelGGL(node_tmm_batch_kernel, dim3((unsigned)groups, (unsigned)count),
+                     dim3(kTmmThreads), 0, s, batch, rows, workspace);
+  hipLaunchKernelGGL(node_tmm_reduce_batch_kernel, dim3((kF * kF + kF) / 64, (unsigned)count),
+                     dim3(512), 0, s, workspace, groups, accumulate, batch);
   return mlcg_launch_status();
 }
 

@@ -1,0 +1,96 @@
+// Streaming read and copy kernels: the HBM ceiling the memory-bound kernels
+// of this library are measured against (a STREAM-style probe on this part,
+// not part of the SchNet path).
+//
+// Each thread of a grid-stride loop keeps kUnroll 16-byte loads in flight:
+// an iteration of thread t starting at float4 i reads i + u G for u <
+// kUnroll (G threads in the grid), so consecutive lanes read consecutive
+// 16-byte chunks and every wave reads a whole 1 KiB run per load.  The read
+// kernel folds what it loads into one float per workgroup so that no load is
+// dead; the copy kernel writes every chunk back to the destination.
+#include "common.h"
+
+namespace {
+
+constexpr int kStreamThreads = 256;
+
+template <int kUnroll>
+__global__ __launch_bounds__(kStreamThreads) void stream_read_kernel(
+    const float4* __restrict__ src, int64_t n4, float* __restrict__ partial) {
+  const int64_t G = (int64_t)gridDim.x * kStreamThreads;
+  const int64_t t = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
+  float acc = 0.f;
+  int64_t i = t;
+  for (; i + (kUnroll - 1) * G < n4; i += kUnroll * G) {
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = src[i + u * G];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  }
+  for (; i < n4; i += G) {
+    const float4 v = src[i];
+    acc += (v.x + v.y) + (v.z + v.w);
+  }
+  __shared__ float part[kStreamThreads / MLCG_WAVE];
+  acc = mlcg_wave_sum(acc);
+  if (mlcg_lane() == 0) part[threadIdx.x / MLCG_WAVE] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+template <int kUnroll>
+__global__ __launch_bounds__(kStreamThreads) void stream_copy_kernel(
+    const float4* __restrict__ src, float4* __restrict__ dst, int64_t n4) {
+  const int64_t G = (int64_t)gridDim.x * kStreamThreads;
+  const int64_t t = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
+  int64_t i = t;
+  for (; i + (kUnroll - 1) * G < n4; i += kUnroll * G) {
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = src[i + u * G];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) dst[i + u * G] = v[u];
+  }
+  for (; i < n4; i += G) dst[i] = src[i];
+}
+
+}  // namespace
+
+extern "C" int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
+                                float* partial, void* stream) {
+  MLCG_REQUIRE(src && partial && n >= 0 && n % 4 == 0 && groups >= 1 && groups <= 65536);
+  MLCG_REQUIRE(unroll == 1 || unroll == 4 || unroll == 8 || unroll == 16);
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(src) % 16 == 0);
+  const auto s = mlcg_stream(stream);
+  const auto* s4 = reinterpret_cast<const float4*>(src);
+  if (unroll == 1)
+    stream_read_kernel<1><<<groups, kStreamThreads, 0, s>>>(s4, n / 4, partial);
+  else if (unroll == 4)
+    stream_read_kernel<4><<<groups, kStreamThreads, 0, s>>>(s4, n / 4, partial);
+  else if (unroll == 8)
+    stream_read_kernel<8><<<groups, kStreamThreads, 0, s>>>(s4, n / 4, partial);
+  else
+    stream_read_kernel<16><<<groups, kStreamThreads, 0, s>>>(s4, n / 4, partial);
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_stream_copy(const float* src, float* dst, int64_t n, int groups, int unroll,
+                                void* stream) {
+  MLCG_REQUIRE(src && dst && n >= 0 && n % 4 == 0 && groups >= 1 && groups <= 65536);
+  MLCG_REQUIRE(unroll == 1 || unroll == 4 || unroll == 8 || unroll == 16);
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+  const auto s = mlcg_stream(stream);
+  const auto* s4 = reinterpret_cast<const float4*>(src);
+  auto* d4 = reinterpret_cast<float4*>(dst);
+  if (unroll == 1)
+    stream_copy_kernel<1><<<groups, kStreamThreads, 0, s>>>(s4, d4, n / 4);
+  else if (unroll == 4)
+    stream_copy_kernel<4><<<groups, kStreamThreads, 0, s>>>(s4, d4, n / 4);
+  else if (unroll == 8)
+    stream_copy_kernel<8><<<groups, kStreamThreads, 0, s>>>(s4, d4, n / 4);
+  else
+    stream_copy_kernel<16><<<groups, kStreamThreads, 0, s>>>(s4, d4, n / 4);
+  return mlcg_launch_status();
+}

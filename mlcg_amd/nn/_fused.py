@@ -478,6 +478,9 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
 
 
 _SIDE_STREAMS = {}
+# Weight-gradient reductions of reverse2 on the side stream (False runs them
+# in order on the caller's stream; results are the same bit for bit).
+_TMM_SIDE = True
 
 
 class _SideStream:
@@ -499,6 +502,8 @@ class _SideStream:
         self.held = []
 
     def run(self, fn, *inputs):
+        if not _TMM_SIDE:
+            return fn()
         self.side.wait_stream(self.main)
         with torch.cuda.stream(self.side):
             out = fn()
@@ -510,6 +515,21 @@ class _SideStream:
         self.held.clear()
 
 
+def _node_tmm_batch(probs, rows, device):
+    """The weight-gradient reductions of probs [(a1, b1, a2, b2, colsum)] in
+    one batched launch when every operand is a contiguous [rows, 128] fp32
+    tensor, else one node_tmm call each (same results up to the split of the
+    rows over workgroups)."""
+    def ok(t):
+        return t is None or (t.dim() == 2 and t.shape[0] == rows
+                             and t.shape[1] == ops.NUM_FILTERS and t.dtype == torch.float32
+                             and t.is_contiguous())
+
+    if all(ok(t) for pr in probs for t in pr[:4]):
+        return ops.node_tmm_batch(probs, rows, device)
+    return [ops.node_tmm(a1, b1, a2, b2, colsum=cs) for a1, b1, a2, b2, cs in probs]
+
+
 def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     """reverse2 through the interaction blocks from the output network's
     adjoint xbar2; assembles the gradients in Params.flat() order."""
@@ -519,33 +539,35 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     g_blocks = [None] * len(P.blocks)
     g_basis = None
     side = _SideStream(st.pos.device)
-
-    def tmm(a1, b1, a2=None, b2=None, colsum=False):
-        return side.run(lambda: ops.node_tmm(a1, b1, a2, b2, colsum=colsum), a1, b1, a2, b2)
+    N = st.pos.shape[0]
 
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
+        xbar2_in = xbar2
         if tangent_on:
-            gA3, gc3 = tmm(xbar2, st.s[k], st.xbar_out[k], st.sdot[k], colsum=True)
             zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
                                           st.sbar1[k], st.zdot[k], bp.A2)
         else:
-            gA3, gc3 = tmm(xbar2, st.s[k], colsum=True)
             zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
                                           None, None, bp.A2)
-        if tangent_on:
-            gA2, gc2 = tmm(zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], colsum=True)
-        else:
-            gA2, gc2 = tmm(zbar2, st.agg[k], colsum=True)
         g1 = st.gagg1[k] if tangent_on else None
         yd = st.ydot[k] if tangent_on else None
         dd = st.ddot if tangent_on else None
         ybar2, _, _ = ops.cfconv_gather_rev2(gagg2, g1, st.y[k], yd, st.W[k], st.Wd[k], dd,
                                              graph, pair_adjoints=False)
-        if tangent_on and st.xdot_in[k] is not None:
-            gA1 = tmm(ybar2, st.x[k], st.ybar1[k], st.xdot_in[k])
+        # the block's three weight-gradient reductions (lin, conv.lin2 with
+        # their biases, conv.lin1), one batched launch on the side stream
+        if tangent_on:
+            probs = [(xbar2_in, st.s[k], st.xbar_out[k], st.sdot[k], True),
+                     (zbar2, st.agg[k], st.zbar1[k], st.aggdot[k], True),
+                     (ybar2, st.x[k], st.ybar1[k], st.xdot_in[k], False)
+                     if st.xdot_in[k] is not None else (ybar2, st.x[k], None, None, False)]
         else:
-            gA1 = tmm(ybar2, st.x[k])
+            probs = [(xbar2_in, st.s[k], None, None, True), (zbar2, st.agg[k], None, None, True),
+                     (ybar2, st.x[k], None, None, False)]
+        held = [t for pr in probs for t in pr[:4]]
+        (gA3, gc3), (gA2, gc2), gA1 = side.run(
+            lambda: _node_tmm_batch(probs, N, st.pos.device), *held)
         xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
         res = ops.filter_bwd_cfconv(st.pos, graph, st.filt, bp.W1, bp.b1, bp.W2, gagg2,
                                     st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable)

@@ -8,6 +8,7 @@ torch's caching allocator and launches on torch's current stream.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Optional, Tuple
 
@@ -19,9 +20,12 @@ from ._lib import call, ptr, require_device, stream_handle
 NUM_FILTERS = 128  # F fixed by the MFMA tiling of the filter kernels
 
 
-def _check(cond: bool, msg: str) -> None:
+def _check(cond: bool, msg) -> None:
+    """Raise RuntimeError(msg) unless cond; msg may be a zero-argument
+    callable, so that a message needing formatting costs nothing when the
+    check passes."""
     if not cond:
-        raise RuntimeError(msg)
+        raise RuntimeError(msg() if callable(msg) else msg)
 
 
 def _as_i64(t: torch.Tensor) -> torch.Tensor:
@@ -125,7 +129,7 @@ def _validate_exclusions(exclude_pair_xs, ptr_exclude_pair_xs, n: int, dev):
 
 def _validate_pos(pos: torch.Tensor) -> torch.Tensor:
     require_device(pos)
-    _check(pos.dim() == 2 and pos.shape[1] == 3, f"pos must be [N, 3], got {tuple(pos.shape)}")
+    _check(pos.dim() == 2 and pos.shape[1] == 3, lambda: f"pos must be [N, 3], got {tuple(pos.shape)}")
     _check(pos.dtype == torch.float32,
            f"the HIP radius graph and CFConv kernels take float32 positions, got {pos.dtype}")
     return pos.contiguous()
@@ -381,7 +385,7 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
     (act' and act'' from z and s = act(z)).  out0 is skipped for ACT/DACT
     when want_out0 is False."""
     require_device(x)
-    _check(_node_gemm_ok(x, W), f"node_gemm takes [N, {NUM_FILTERS}] float32 rows and a "
+    _check(_node_gemm_ok(x, W), lambda: f"node_gemm takes [N, {NUM_FILTERS}] float32 rows and a "
            f"[{NUM_FILTERS}, {NUM_FILTERS}] weight, got {tuple(x.shape)} / {tuple(W.shape)}")
     n = x.shape[0]
     dev = x.device
@@ -398,8 +402,22 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
         out1 = torch.empty_like(x)
     call("mlcg_node_gemm", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
          ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
-         ptr(out1), stream_handle(dev))
+         ptr(out1), stream_handle(dev),
+         work=_node_gemm_bytes(n, epilogue, act, (x, residual, out0, out1), s, z, e, f, 1))
     return out0, out1
+
+
+def _node_gemm_bytes(n, epilogue, act, tensors, s, z, e, f, n_weights):
+    """Algorithmic HBM bytes of one node-GEMM launch: every [n, 128] fp32
+    tensor the launch reads or writes once (the epilogue's z only for
+    activations other than tanh, whose derivatives come from s alone), the
+    weights and biases once."""
+    rows = [t for t in tensors if t is not None]
+    if epilogue in (NODE_DACT, NODE_DACT2):
+        rows += [t for t in (s, None if act == 0 else z) if t is not None]
+        if epilogue == NODE_DACT2:
+            rows += [t for t in (e, f) if t is not None]
+    return 4 * NUM_FILTERS * n * len(rows) + n_weights * 4 * (NUM_FILTERS + 1) * NUM_FILTERS
 
 
 def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bool = False,
@@ -417,7 +435,7 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
     _check(epilogue in (NODE_ACT, NODE_DACT, NODE_DACT2),
            "node_gemm2 takes an ACT, DACT or DACT2 first epilogue")
     _check(_node_gemm_ok(x, W) and _node_gemm_ok(x, W2),
-           f"node_gemm2 takes [N, {NUM_FILTERS}] float32 rows and two "
+           lambda: f"node_gemm2 takes [N, {NUM_FILTERS}] float32 rows and two "
            f"[{NUM_FILTERS}, {NUM_FILTERS}] weights, got {tuple(x.shape)} / "
            f"{tuple(W.shape)} / {tuple(W2.shape)}")
     n = x.shape[0]
@@ -438,7 +456,9 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
     out2 = torch.empty_like(x)
     call("mlcg_node_gemm2", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
          ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
-         ptr(out1), ptr(W2), ptr(bias2), ptr(residual2), ptr(out2), stream_handle(dev))
+         ptr(out1), ptr(W2), ptr(bias2), ptr(residual2), ptr(out2), stream_handle(dev),
+         work=_node_gemm_bytes(n, epilogue, act, (x, residual, out0, out1, residual2, out2),
+                               s, z, e, f, 2))
     return out0, out1, out2
 
 
@@ -463,6 +483,32 @@ def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = No
     if a2 is not None:
         out = out + tmm(a2, b2)
     return (out, a1.sum(0)) if colsum else out
+
+
+def node_tmm_batch(problems, rows: int, device) -> list:
+    """Several node_tmm reductions over `rows` rows in one launch pair
+    (mlcg_node_tmm_batch).  problems: list of (a1, b1, a2, b2, colsum) with
+    [rows, 128] fp32 contiguous tensors (a2, b2 may be None); returns, per
+    problem, the [128, 128] product and (when colsum) the column sums of a1,
+    as node_tmm does."""
+    count = len(problems)
+    _check(1 <= count <= 4, "node_tmm_batch takes 1 to 4 problems")
+    outs, flat = [], []
+    for a1, b1, a2, b2, colsum in problems:
+        for t in (a1, b1, a2, b2):
+            _check(t is None or (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()
+                                 and t.dim() == 2 and t.shape == (rows, NUM_FILTERS)),
+                   "node_tmm_batch operands must be contiguous [rows, 128] float32 on the GPU")
+        out = torch.empty(NUM_FILTERS, NUM_FILTERS, dtype=torch.float32, device=device)
+        cs = torch.empty(NUM_FILTERS, dtype=torch.float32, device=device) if colsum else None
+        outs.append((out, cs) if colsum else out)
+        flat += [ptr(a1), ptr(b1), ptr(a2), ptr(b2), ptr(out), ptr(cs)]
+    nws = int(_lib.load().mlcg_node_tmm_batch_workspace_floats(rows, count))
+    ws = torch.empty(nws, dtype=torch.float32, device=device)
+    arr = (ctypes.c_void_p * len(flat))(*flat)
+    call("mlcg_node_tmm_batch", arr, count, rows, NUM_FILTERS, 0, ptr(ws), nws,
+         stream_handle(device))
+    return outs
 
 
 def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
@@ -601,7 +647,7 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     stream allocates them on the stream that consumes them)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
-    _check(F == NUM_FILTERS, f"num_filters must be {NUM_FILTERS} for the HIP filter kernel")
+    _check(F == NUM_FILTERS, lambda: f"num_filters must be {NUM_FILTERS} for the HIP filter kernel")
     _check(tuple(W1.shape) == (F, spec.num_rbf) and tuple(W2.shape) == (F, F)
            and tuple(b1.shape) == (F,), "filter weights have unexpected shapes")
     cap = graph.pair_capacity
@@ -646,7 +692,7 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     _check(tuple(Wbar.shape) == (cap, F) and tuple(Wdbar.shape) == (cap, F),
            "Wbar / Wdbar must be [pair_capacity, F]")
     nws = int(_lib.load().mlcg_filter_bwd_workspace_floats(cap, K))
-    _check(nws > 0, f"num_rbf={K} is not supported by the filter backward")
+    _check(nws > 0, lambda: f"num_rbf={K} is not supported by the filter backward")
     ws = torch.empty(nws, dtype=torch.float32, device=dev)
     dW1 = torch.empty(F, K, dtype=torch.float32, device=dev)
     db1 = torch.empty(F, dtype=torch.float32, device=dev)
@@ -677,7 +723,7 @@ def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
     cap = graph.pair_capacity
     dev = pos.device
     nws = int(_lib.load().mlcg_filter_bwd_workspace_floats(cap, K))
-    _check(nws > 0, f"num_rbf={K} is not supported by the filter backward")
+    _check(nws > 0, lambda: f"num_rbf={K} is not supported by the filter backward")
     ws = torch.empty(nws, dtype=torch.float32, device=dev)
     dW1 = torch.empty(F, K, dtype=torch.float32, device=dev)
     db1 = torch.empty(F, dtype=torch.float32, device=dev)
@@ -707,7 +753,7 @@ def rbf_param_grad(dist: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: t
     _check(tuple(abar.shape) == (cap, NUM_FILTERS) and abar.shape == adbar.shape,
            "abar / adbar must be [pair_capacity, F]")
     nws = int(_lib.load().mlcg_rbf_param_grad_workspace_floats(cap, K))
-    _check(nws > 0, f"num_rbf={K} is not supported")
+    _check(nws > 0, lambda: f"num_rbf={K} is not supported")
     ws = torch.empty(nws, dtype=torch.float32, device=dev)
     accumulate = out is not None
     if out is None:

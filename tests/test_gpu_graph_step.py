@@ -71,3 +71,108 @@ def test_captured_training_step_matches_eager():
         assert torch.equal(le[k], lg[k]), k
         for a, c in zip(pe[k], pg[k]):
             assert torch.equal(a, c), k
+
+
+def _step_run(cfg, sd, b, ahead, tmm_side, n_steps=3, captured=False, capturable=False):
+    """Losses, forces and parameters after each of n_steps training steps
+    with the given stream arrangement (eager), or through CapturedTrainStep
+    (which needs the capturable AdamW)."""
+    from mlcg_amd import nn
+    from mlcg_amd.nn import _fused
+    from mlcg_amd.pl import CapturedTrainStep
+
+    saved = _fused._FILTER_AHEAD, _fused._TMM_SIDE
+    _fused._FILTER_AHEAD, _fused._TMM_SIDE = ahead, tmm_side
+    try:
+        model = make_model(cfg, sd).train()
+        data = b.to_torch("cuda")
+        g0 = model.build_graph(data)
+        cap = int(g0.num_edges * 1.05) + 64
+        model.graph_capacity = cap + (cap % 2)
+        gm = nn.GradientsOut(model)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True,
+                                capturable=captured or capturable)
+        forces = []
+
+        def step(d):
+            opt.zero_grad(set_to_none=True)
+            out = gm(d)
+            out.out.update(**out.out[model.name])
+            forces.append(out.out["forces"].detach().clone())
+            loss = nn.ForceMSE()(out)
+            loss.backward()
+            opt.step()
+            return loss
+
+        losses, params = [], []
+        if captured:
+            cs = CapturedTrainStep(step, data, model, opt, warmup=1)  # eager step 1
+            losses.append(None)
+            params.append(None)
+            batch = b.to_torch("cuda")  # a second resident copy, loaded each step
+            for _ in range(n_steps - 1):
+                loss = cs.step(batch)
+                torch.cuda.synchronize()
+                losses.append(loss.detach().clone())
+                params.append([p.detach().clone() for p in model.parameters()])
+            cs.check()
+        else:
+            for _ in range(n_steps):
+                losses.append(step(data).detach().clone())
+                params.append([p.detach().clone() for p in model.parameters()])
+        return losses, forces, params
+    finally:
+        _fused._FILTER_AHEAD, _fused._TMM_SIDE = saved
+
+
+def test_stream_arrangements_bit_identical():
+    """The filter forwards issued ahead on the side stream, and the
+    weight-gradient reductions on the side stream, change only where kernels
+    run, never what they compute: every arrangement gives the in-order
+    single-stream step's losses, forces and parameters bit for bit."""
+    from mlcg_amd import synthetic
+
+    print("stream arrangements, 3 blocks, 16 frames", flush=True)
+    cfg = make_cfg(num_blocks=3, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=32)
+    b = synthetic.config2(n_frames=16)
+    ref = _step_run(cfg, sd, b, ahead=False, tmm_side=False)
+    for ahead, side in ((True, False), (False, True), (True, True)):
+        got = _step_run(cfg, sd, b, ahead=ahead, tmm_side=side)
+        for k in range(3):
+            assert torch.equal(got[0][k], ref[0][k]), (ahead, side, k)
+            assert torch.equal(got[1][k], ref[1][k]), (ahead, side, k)
+            for a, c in zip(got[2][k], ref[2][k]):
+                assert torch.equal(a, c), (ahead, side, k)
+
+
+def test_captured_train_step_api_matches_eager():
+    """mlcg_amd.pl.CapturedTrainStep (one warm-up step, then replays that
+    each load a second resident copy of the batch) gives the eager steps'
+    losses and parameters bit for bit, with the filter forwards ahead on the
+    side stream inside the graph."""
+    from mlcg_amd import synthetic
+
+    print("CapturedTrainStep, 3 blocks, 16 frames", flush=True)
+    cfg = make_cfg(num_blocks=3, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=33)
+    b = synthetic.config2(n_frames=16)
+    ref = _step_run(cfg, sd, b, ahead=True, tmm_side=True, n_steps=4, capturable=True)
+    got = _step_run(cfg, sd, b, ahead=True, tmm_side=True, n_steps=4, captured=True)
+    for k in range(1, 4):
+        assert torch.equal(got[0][k], ref[0][k]), k
+        for a, c in zip(got[2][k], ref[2][k]):
+            assert torch.equal(a, c), k
+
+
+def test_captured_train_step_requires_capturable_optimizer():
+    from mlcg_amd import nn, synthetic
+    from mlcg_amd.pl import CapturedTrainStep
+
+    cfg = make_cfg(num_blocks=1, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=34)
+    model = make_model(cfg, sd).train()
+    data = synthetic.config2(n_frames=2).to_torch("cuda")
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    with pytest.raises(RuntimeError, match="capturable"):
+        CapturedTrainStep(lambda d: nn.GradientsOut(model)(d), data, model, opt)

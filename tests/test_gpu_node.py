@@ -56,6 +56,41 @@ def test_node_tmm(rows):
     check(cs, a1.double().sum(0), 1e-6, 'cs', atol_frac=1.0)
 
 
+@pytest.mark.parametrize("rows", [0, 1, 33, 1000, 17920, 128000])
+@pytest.mark.parametrize("count", [1, 3, 4])
+def test_node_tmm_batch(rows, count):
+    """Batched weight-gradient reductions (one launch pair for `count`
+    problems, with and without the second product and column sums) against
+    fp64 products, and run-to-run identical."""
+    from mlcg_amd import ops
+
+    print(f"node_tmm_batch rows={rows} count={count}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7 * rows + count)
+    probs, refs = [], []
+    for k in range(count):
+        a1, b1, a2, b2 = (torch.randn(rows, 128, device="cuda", generator=g) * (10.0 ** k)
+                          for _ in range(4))
+        two, cs = k % 2 == 0, k != 2
+        probs.append((a1, b1, a2 if two else None, b2 if two else None, cs))
+        r = a1.double().t().mm(b1.double())
+        if two:
+            r = r + a2.double().t().mm(b2.double())
+        refs.append((r, a1.double().sum(0) if cs else None))
+    got = ops.node_tmm_batch(probs, rows, torch.device("cuda"))
+    again = ops.node_tmm_batch(probs, rows, torch.device("cuda"))
+    for k, (pr, (r, rc)) in enumerate(zip(probs, refs)):
+        out, cs = got[k] if pr[4] else (got[k], None)
+        out2, cs2 = again[k] if pr[4] else (again[k], None)
+        assert torch.equal(out, out2)
+        if rows == 0:
+            assert float(out.abs().max()) == 0.0
+            continue
+        check(out, r, 1e-6, f"batch[{k}]", atol_frac=1.0)
+        if rc is not None:
+            assert torch.equal(cs, cs2)
+            check(cs, rc, 1e-6, f"colsum[{k}]", atol_frac=1.0)
+
+
 def _act64(z, act):
     if act == 0:
         return torch.tanh(z)
