@@ -279,7 +279,11 @@ int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij,
  * reductions run in one kernel (per-workgroup partial sums in `workspace`,
  * then a fixed-order reduction), so nothing per pair is written to memory.
  * `workspace` holds mlcg_filter_bwd_workspace_floats(max_pairs, num_rbf)
- * floats.  Replaces the autograd double backward through mlp.py:56-58 and
+ * floats.  num_rbf <= 64 runs on the fp16 MFMA with split operands (about
+ * 22 significant bits; activations and their derivatives must stay below
+ * 2^19 in magnitude, else bit 0 of mlcg_numerics_flags is set) unless
+ * fp32_strict != 0, which, like num_rbf > 64, runs every product on the fp32
+ * MFMA.  Replaces the autograd double backward through mlp.py:56-58 and
  * gaussian.py:98-102 (the parameter half of the create_graph=True backward
  * of gradients.py:216-222). */
 int64_t mlcg_filter_bwd_workspace_floats(int64_t max_pairs, int num_rbf);
@@ -293,7 +297,7 @@ int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij,
                     int num_filters, const float* Wbar, const float* Wdbar,
                     float* dW1, float* db1, float* dW2, float* abar_out,
                     float* adbar_out, float* workspace,
-                    int64_t workspace_floats, void* stream);
+                    int64_t workspace_floats, int fp32_strict, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* CFConv gather/scatter over the receiver CSR (rowptr, col, eid2pair)      */
@@ -361,7 +365,7 @@ int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
                            const float* ddot, float* dW1, float* db1,
                            float* dW2, float* abar_out, float* adbar_out,
                            float* workspace, int64_t workspace_floats,
-                           void* stream);
+                           int fp32_strict, void* stream);
 
 /* Gradients of trainable basis parameters from the first-layer pair
  * adjoints abar = dL/da, adbar = dL/da' [max_pairs, F] (a = W1 g + b1,
@@ -619,6 +623,20 @@ int mlcg_philox_normals(uint64_t seed, int64_t step, int64_t n_nodes, float* out
 enum { MLCG_MATH_TANH = 0, MLCG_MATH_SIGMOID = 1, MLCG_MATH_SOFTPLUS = 2,
        MLCG_MATH_SINPI = 3, MLCG_MATH_COSPI = 4 };
 int mlcg_math_eval(int fn, const float* x, int64_t n, float* y, void* stream);
+
+/* Numerics flags of the split-product (fp16 MFMA) kernels: writes the
+ * device's flag word to out[0] and, with clear != 0, clears it (both on the
+ * stream, no host synchronisation; capturable).  Bit 0: a filter backward
+ * (mlcg_filter_bwd, mlcg_filter_bwd_cfconv) met an activation value or
+ * derivative of magnitude 2^19 or more (or a non-finite one), past the range
+ * of its split operands, so its weight gradients may be non-finite.  Bit 1:
+ * a split filter kernel (forward or backward) met a weight of magnitude 65504
+ * (the fp16 maximum) or more, past what its fp16 weight planes hold.  The split filter forward
+ * needs no flag for large activations: tiles whose activations pass its 2^15
+ * bound are recomputed with an exact power-of-two scale.  No counterpart in the reference (its fp32
+ * products have no such bound); callers that must not return non-finite
+ * gradients silently read it after a training step. */
+int mlcg_numerics_flags(int* out, int clear, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* HBM ceiling probes                                                      */

@@ -59,10 +59,10 @@ _SIGNATURES = {
     "mlcg_filter_bwd_workspace_floats": [_I64, _I32],
     "mlcg_filter_bwd": [_P, _P, _I64, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32,
                         _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P,
-                        _P, _I64, _P],
+                        _P, _I64, _I32, _P],
     "mlcg_filter_bwd_cfconv": [_P, _P, _I64, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32,
                                _F32, _I32, _F32, _F32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P,
-                               _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+                               _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P],
     "mlcg_rbf_param_grad_workspace_floats": [_I64, _I32],
     "mlcg_rbf_param_grad": [_P, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32, _P, _I32,
                             _P, _P, _I32, _P, _P, _P, _I64, _P],
@@ -97,6 +97,7 @@ _SIGNATURES = {
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
     "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
+    "mlcg_numerics_flags": [_P, _I32, _P],
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
 }

@@ -652,6 +652,32 @@ __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, hal
   return acc;
 }
 
+// Numerics flags of the split-product kernels (one word per device, set with
+// a vector atomic OR, read and cleared by mlcg_numerics_flags):
+//   bit 0 -- the filter backward met an activation value |h| or derivative
+//            |h'| of 2^19 or more (or a non-finite one), past the range its
+//            split operands hold, so its weight gradients may be non-finite;
+//   bit 1 -- a filter weight (W1 or W2) of magnitude 65504 (the fp16
+//            maximum) or more, past what the weights' fp16 planes hold
+//            (forward and backward).
+// (The split forward needs no flag for large activations: a tile whose
+// values pass its bound is recomputed with a power-of-two scale, exactly.)
+__device__ unsigned mlcg_numerics_word;
+constexpr unsigned kFlagBwdRange = 1u;
+constexpr unsigned kFlagWeightRange = 2u;
+constexpr float kWeightBound = 65504.0f;
+
+__device__ __forceinline__ void raise_numerics_flag(unsigned bits) {
+  atomicOr(&mlcg_numerics_word, bits);
+}
+
+__global__ void numerics_flags_kernel(int* out, int clear) {
+  if (threadIdx.x == 0) {
+    out[0] = (int)mlcg_numerics_word;
+    if (clear) mlcg_numerics_word = 0u;
+  }
+}
+
 // Filter forward, fp32-accurate, on the fp16 MFMA.  The operand layouts are
 // those of filter_fwd_f16_kernel (see stage_f16) with K padded to two 32-wide
 // k blocks (K <= 64); W1 and W2 are staged as three planes each.  One wave per
@@ -664,6 +690,7 @@ __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, hal
 // Basis rows k >= K are evaluated with centre and width 0 (finite values)
 // and meet zero weights, so they add exact zeros.
 constexpr int kX3Blocks = 2;  // 32-wide k blocks of the first product
+constexpr int kRedoSlots = 8;  // tiles per wave recorded for the scaled pass
 
 template <int BASIS, int ACT>
 __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
@@ -737,8 +764,10 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
       m2 = fmaxf(m2, fabsf(w8[j]));
     }
   }
-  const float S1 = x3_scale(block_absmax(m1, red));
-  const float S2 = x3_scale(block_absmax(m2, red));
+  const float mw1 = block_absmax(m1, red), mw2 = block_absmax(m2, red);
+  const float S1 = x3_scale(mw1);
+  const float S2 = x3_scale(mw2);
+  if (threadIdx.x == 0 && !(fmaxf(mw1, mw2) < kWeightBound)) raise_numerics_flag(kFlagWeightRange);
   auto store_chunk = [](_Float16* plane, int plane_halfs, int c, const float* v, float S) {
     halfx8 h, hs, lo;
 #pragma unroll
@@ -795,6 +824,127 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
     ni = pi[p1];
     nj = pj[p1];
   }
+  // outputs of `tile` (lane's pair p, distance d) with the activations
+  // scaled by sig; true (wave-uniform) when an output of the tile is not
+  // finite
+  auto tile_body = [&](int64_t tile, float d, float sig, float inv_sig) -> bool {
+    const int64_t p = tile * 16 + (l & 15);
+    const bool valid = p < np;
+      float crbf, dcrbf, cc, dcc;
+      cut_eval(rp.rcut, d, crbf, dcrbf);
+      if (rp.same_cut) {  // uniform
+        cc = crbf;
+        dcc = dcrbf;
+      } else {
+        cut_eval(rp.ccut, d, cc, dcc);
+      }
+
+      // basis g, g' of the lane's pair, k = 32 s + 8 q + j, as split B parts
+      halfx8 gh[KS32], gl[KS32], gdh[KS32], gdl[KS32];
+#pragma unroll
+      for (int s = 0; s < KS32; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float g0, gd0, g1, gd1;
+          const int k = 32 * s + 8 * q + j;
+          rbf_eval_t<BASIS>(rp, true, bc[k], bw[k], d, crbf, dcrbf, g0, gd0);
+          rbf_eval_t<BASIS>(rp, true, bc[k + 1], bw[k + 1], d, crbf, dcrbf, g1, gd1);
+          halfx2 h, lo, hd, lod;
+          split2x2(g0, g1, S1, h, lo);
+          split2x2(gd0, gd1, S1, hd, lod);
+          gh[s][j] = h[0];
+          gh[s][j + 1] = h[1];
+          gl[s][j] = lo[0];
+          gl[s][j + 1] = lo[1];
+          gdh[s][j] = hd[0];
+          gdh[s][j + 1] = hd[1];
+          gdl[s][j] = lod[0];
+          gdl[s][j + 1] = lod[1];
+        }
+      // 1.-2. per feature tile t: a = W1 g, a' = W1 g' (times S1); then
+      // h = act(a + b1), h' = act'(a + b1) a', times sig, split for the second
+      // product.  The split holds |h sig|, |h' sig| below 65504 (the fp16
+      // maximum; hi_h S2 is never formed).  A larger value makes its fp16 hi
+      // part infinite, and through every row of W2 every output of its pair
+      // non-finite: one output of each pair is checked, and such a tile is
+      // done again with sig 2^6, 2^12, ... times smaller (exact, undone on the
+      // outputs).
+      halfx8 hh[kFT / 2], hl[kFT / 2], hdh[kFT / 2], hdl[kFT / 2];
+      auto features = [&](float sig) {
+#pragma unroll
+        for (int t = 0; t < kFT; ++t) {
+          floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < KS32; ++s) {
+            const int o = (t * KS32 + s) * MLCG_WAVE + l;
+            const halfx8 ah = w1v[o], ahs = w1v[n1v + o], al = w1v[2 * n1v + o];
+            a = mfma_x3(ah, ahs, al, gh[s], gl[s], a);
+            ad = mfma_x3(ah, ahs, al, gdh[s], gdl[s], ad);
+          }
+          const float4 bias = *reinterpret_cast<const float4*>(b1s + 16 * t + 4 * q);
+          const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            float s0, s1, e0, e1, unused;
+            act_t<ACT>(a[i] * inv1 + bv[i], s0, e0, unused);
+            act_t<ACT>(a[i + 1] * inv1 + bv[i + 1], s1, e1, unused);
+            float hd0 = e0 * (ad[i] * inv1), hd1 = e1 * (ad[i + 1] * inv1);
+            s0 *= sig;
+            s1 *= sig;
+            hd0 *= sig;
+            hd1 *= sig;
+            halfx2 h, lo, hd, lod;
+            split2x2(s0, s1, S2, h, lo);
+            split2x2(hd0, hd1, S2, hd, lod);
+            const int e = 4 * (t & 1) + i;
+            hh[t >> 1][e] = h[0];
+            hh[t >> 1][e + 1] = h[1];
+            hl[t >> 1][e] = lo[0];
+            hl[t >> 1][e + 1] = lo[1];
+            hdh[t >> 1][e] = hd[0];
+            hdh[t >> 1][e + 1] = hd[1];
+            hdl[t >> 1][e] = lod[0];
+            hdl[t >> 1][e + 1] = lod[1];
+          }
+        }
+      };
+      features(sig);
+      // 3. per output tile t: w = W2 h, w' = W2 h' (times S2 sig), enveloped
+      const float c2 = cc * (inv2 * inv_sig), dc2 = dcc * (inv2 * inv_sig);  // powers of two
+      bool bad = false;
+      float* wr = Wout + p * kF + 4 * q;
+      float* wdr = Wdout + p * kF + 4 * q;
+#pragma unroll
+      for (int t = 0; t < kFT; ++t) {
+        floatx4 w = {0.f, 0.f, 0.f, 0.f}, wd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kFT / 2; ++s) {
+          const int o = (t * (kFT / 2) + s) * MLCG_WAVE + l;
+          const halfx8 ah = w2v[o], ahs = w2v[n2v + o], al = w2v[2 * n2v + o];
+          w = mfma_x3(ah, ahs, al, hh[s], hl[s], w);
+          wd = mfma_x3(ah, ahs, al, hdh[s], hdl[s], wd);
+        }
+        if (t == 0) bad = valid && !(__builtin_isfinite(w[0]) && __builtin_isfinite(wd[0]));
+        if (valid) {
+          float4 o, od;
+          float* op = reinterpret_cast<float*>(&o);
+          float* odp = reinterpret_cast<float*>(&od);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            op[i] = w[i] * c2;
+            odp[i] = wd[i] * c2 + w[i] * dc2;
+          }
+          *reinterpret_cast<float4*>(wr + 16 * t) = o;
+          *reinterpret_cast<float4*>(wdr + 16 * t) = od;
+        }
+      }
+    if (valid && dist_out && q == 0) dist_out[p] = d;
+    return __builtin_amdgcn_ballot_w64(bad) != 0;
+  };
+  // tiles of this wave to do again with scaled activations (rare)
+  int* redo = reinterpret_cast<int*>(red + kWavesX3) +
+              __builtin_amdgcn_readfirstlane(threadIdx.x / MLCG_WAVE) * kRedoSlots;
+  int n_redo = 0;
   for (int64_t tile = wave; tile < tiles; tile += nwaves) {
     const int64_t p = tile * 16 + (l & 15);
     const bool valid = p < np;
@@ -810,100 +960,32 @@ __global__ __launch_bounds__(kThreadsX3) void filter_fwd_x3_kernel(
       ni = pi[p2];
       nj = pj[p2];
     }
-    float crbf, dcrbf, cc, dcc;
-    cut_eval(rp.rcut, d, crbf, dcrbf);
-    if (rp.same_cut) {  // uniform
-      cc = crbf;
-      dcc = dcrbf;
-    } else {
-      cut_eval(rp.ccut, d, cc, dcc);
+    if (tile_body(tile, d, 1.0f, 1.0f)) {  // rare: recorded, done again below
+      if (n_redo < kRedoSlots && l == 0) redo[n_redo] = (int)tile;
+      ++n_redo;
     }
-
-    // basis g, g' of the lane's pair, k = 32 s + 8 q + j, as split B parts
-    halfx8 gh[KS32], gl[KS32], gdh[KS32], gdl[KS32];
-#pragma unroll
-    for (int s = 0; s < KS32; ++s)
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        float g0, gd0, g1, gd1;
-        const int k = 32 * s + 8 * q + j;
-        rbf_eval_t<BASIS>(rp, true, bc[k], bw[k], d, crbf, dcrbf, g0, gd0);
-        rbf_eval_t<BASIS>(rp, true, bc[k + 1], bw[k + 1], d, crbf, dcrbf, g1, gd1);
-        halfx2 h, lo, hd, lod;
-        split2x2(g0, g1, S1, h, lo);
-        split2x2(gd0, gd1, S1, hd, lod);
-        gh[s][j] = h[0];
-        gh[s][j + 1] = h[1];
-        gl[s][j] = lo[0];
-        gl[s][j + 1] = lo[1];
-        gdh[s][j] = hd[0];
-        gdh[s][j + 1] = hd[1];
-        gdl[s][j] = lod[0];
-        gdl[s][j + 1] = lod[1];
-      }
-    // 1.-2. per feature tile t: a = W1 g, a' = W1 g' (times S1); then
-    // h = act(a + b1), h' = act'(a + b1) a', split for the second product
-    halfx8 hh[kFT / 2], hl[kFT / 2], hdh[kFT / 2], hdl[kFT / 2];
-#pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS32; ++s) {
-        const int o = (t * KS32 + s) * MLCG_WAVE + l;
-        const halfx8 ah = w1v[o], ahs = w1v[n1v + o], al = w1v[2 * n1v + o];
-        a = mfma_x3(ah, ahs, al, gh[s], gl[s], a);
-        ad = mfma_x3(ah, ahs, al, gdh[s], gdl[s], ad);
-      }
-      const float4 bias = *reinterpret_cast<const float4*>(b1s + 16 * t + 4 * q);
-      const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
-#pragma unroll
-      for (int i = 0; i < 4; i += 2) {
-        float s0, s1, e0, e1, unused;
-        act_t<ACT>(a[i] * inv1 + bv[i], s0, e0, unused);
-        act_t<ACT>(a[i + 1] * inv1 + bv[i + 1], s1, e1, unused);
-        const float hd0 = e0 * (ad[i] * inv1), hd1 = e1 * (ad[i + 1] * inv1);
-        halfx2 h, lo, hd, lod;
-        split2x2(s0, s1, S2, h, lo);
-        split2x2(hd0, hd1, S2, hd, lod);
-        const int e = 4 * (t & 1) + i;
-        hh[t >> 1][e] = h[0];
-        hh[t >> 1][e + 1] = h[1];
-        hl[t >> 1][e] = lo[0];
-        hl[t >> 1][e + 1] = lo[1];
-        hdh[t >> 1][e] = hd[0];
-        hdh[t >> 1][e + 1] = hd[1];
-        hdl[t >> 1][e] = lod[0];
-        hdl[t >> 1][e + 1] = lod[1];
-      }
+  }
+  // Tiles with an activation past the fp16 range (or a non-finite input,
+  // which no scale repairs) again, with sig = 2^-6, 2^-12, ..., 2^-30, after
+  // the main loop so that its registers are not shared with this path; when
+  // more tiles overflowed than the slots hold, every tile of the wave is
+  // checked again from sig = 1.
+  const bool redo_all = n_redo > kRedoSlots;
+  const int n_pass = redo_all ? (int)((tiles - wave + nwaves - 1) / nwaves) : n_redo;
+  for (int r = 0; r < n_pass; ++r) {
+    const int64_t tile =
+        redo_all ? wave + (int64_t)r * nwaves : (int64_t)__builtin_amdgcn_readfirstlane(redo[r]);
+    const int64_t p = pair_at(tile);
+    const int64_t i = pi[p], j = pj[p];
+    const float dx = pos[3 * j] - pos[3 * i], dy = pos[3 * j + 1] - pos[3 * i + 1],
+                dz = pos[3 * j + 2] - pos[3 * i + 2];
+    const float d = tile * 16 + (l & 15) < np ? sqrtf(dx * dx + dy * dy + dz * dz) : 1.0f;
+    float sig = redo_all ? 64.0f : 1.0f, inv_sig = redo_all ? 0.015625f : 1.0f;
+    for (int pass = 0; pass < 6; ++pass) {
+      sig *= 0.015625f;
+      inv_sig *= 64.0f;
+      if (!tile_body(tile, d, sig, inv_sig)) break;
     }
-    // 3. per output tile t: w = W2 h, w' = W2 h' (times S2), enveloped
-    const float c2 = cc * inv2, dc2 = dcc * inv2;  // 1 / S2 is a power of two
-    float* wr = Wout + p * kF + 4 * q;
-    float* wdr = Wdout + p * kF + 4 * q;
-#pragma unroll
-    for (int t = 0; t < kFT; ++t) {
-      floatx4 w = {0.f, 0.f, 0.f, 0.f}, wd = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < kFT / 2; ++s) {
-        const int o = (t * (kFT / 2) + s) * MLCG_WAVE + l;
-        const halfx8 ah = w2v[o], ahs = w2v[n2v + o], al = w2v[2 * n2v + o];
-        w = mfma_x3(ah, ahs, al, hh[s], hl[s], w);
-        wd = mfma_x3(ah, ahs, al, hdh[s], hdl[s], wd);
-      }
-      if (valid) {
-        float4 o, od;
-        float* op = reinterpret_cast<float*>(&o);
-        float* odp = reinterpret_cast<float*>(&od);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          op[i] = w[i] * c2;
-          odp[i] = wd[i] * c2 + w[i] * dc2;
-        }
-        *reinterpret_cast<float4*>(wr + 16 * t) = o;
-        *reinterpret_cast<float4*>(wdr + 16 * t) = od;
-      }
-    }
-    if (valid && dist_out && q == 0) dist_out[p] = d;
   }
 }
 
@@ -911,7 +993,7 @@ size_t fwd_x3_lds_bytes(int K) {
   if (K > 32 * kX3Blocks) return SIZE_MAX;  // the x3 kernel pads K to 64
   return sizeof(_Float16) * 3 *
              (kFT * kX3Blocks * MLCG_WAVE * 8 + kFT * (kFT / 2) * MLCG_WAVE * 8) +
-         sizeof(float) * (kF + 2 * kMaxK + kWavesX3);
+         sizeof(float) * (kF + 2 * kMaxK + kWavesX3) + sizeof(int) * kWavesX3 * kRedoSlots;
 }
 
 // ---------------------------------------------------------------------------
@@ -1169,8 +1251,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
         m2 = fmaxf(m2, fabsf(v2[r][j]));
       }
     }
-    S = x3_scale(block_absmax(m2, PMAX));
+    const float mw2 = block_absmax(m2, PMAX);
+    S = x3_scale(mw2);
     inv_S = 1.0f / S;
+    if (threadIdx.x == 0 && !(mw2 < kWeightBound)) raise_numerics_flag(kFlagWeightRange);
     halfx8* w2h = reinterpret_cast<halfx8*>(w2ts);
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
@@ -1195,16 +1279,19 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float w1f[KSMAX];
   halfx4 w1h[KSMAX / 4], w1l[KSMAX / 4];
   if constexpr (kX3) {
+    bool w1_big = false;
 #pragma unroll
     for (int b = 0; b < KSMAX / 4; ++b)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int k = 16 * b + 4 * q + j;
         const float v = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
+        w1_big = w1_big || !(fabsf(v) < kWeightBound);
         const f16split sp = split2(v, kS4);
         w1h[b][j] = sp.hi;
         w1l[b][j] = sp.lo;
       }
+    if (w1_big) raise_numerics_flag(kFlagWeightRange);
   } else {
 #pragma unroll
     for (int s = 0; s < KSMAX; ++s) {
@@ -1467,6 +1554,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
       act2[i] = d2 * ad[i];
       hv[i] = sv;
       hdv[i] = d1 * ad[i];
+    }
+    if constexpr (kX3) {
+      // h, h' enter step 4 as fp16 planes of h beta_h: past 2^19 they leave
+      // the planes' range -- report it (rare; the result is not repaired)
+      // (written so that a NaN counts as out of range)
+      bool out = false;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        out = out || !(fabsf(hv[i]) < 524288.0f) || !(fabsf(hdv[i]) < 524288.0f);
+      if (out) raise_numerics_flag(kFlagBwdRange);
     }
     if constexpr (kX3) {
       // h beta, h' beta as two fp16 planes (hi, lo S4) of [2][128 rows][16
@@ -1909,6 +2006,13 @@ bool valid_params(int basis, int K, int rk, int ck, int act, int F) {
 
 }  // namespace
 
+extern "C" int mlcg_numerics_flags(int* out, int clear, void* stream) {
+  MLCG_REQUIRE(out != nullptr);
+  hipLaunchKernelGGL(numerics_flags_kernel, dim3(1), dim3(64), 0, mlcg_stream(stream), out,
+                     clear);
+  return mlcg_launch_status();
+}
+
 extern "C" int mlcg_filter_fwd(const float* pos, const int32_t* pair_ij, int64_t pair_stride,
                                const int32_t* n_pairs_dev, int64_t max_pairs, int basis,
                                const float* centers, const float* widths, float alpha,
@@ -1995,7 +2099,8 @@ int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_str
                       float conv_lo, float conv_hi, int act, const float* W1, const float* b1,
                       const float* W2, int num_filters, const PairAdjoint& adj, bool nodes,
                       float* dW1, float* db1, float* dW2, float* abar_out, float* adbar_out,
-                      float* workspace, int64_t workspace_floats, void* stream) {
+                      float* workspace, int64_t workspace_floats, bool fp32_strict,
+                      void* stream) {
   if (!valid_params(basis, num_rbf, rbf_cut_kind, conv_cut_kind, act, num_filters))
     return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
@@ -2007,10 +2112,12 @@ int launch_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t pair_str
   RbfParams rp = make_params(basis, centers, widths, alpha, num_rbf, rbf_cut_kind, rbf_lo,
                              rbf_hi, conv_cut_kind, conv_lo, conv_hi, act);
   hipStream_t s = mlcg_stream(stream);
-  const size_t lds = sizeof(float) * bwd_lds_floats(num_rbf);
+  // the split (fp16 MFMA) form serves K <= 64 unless fp32 products are asked
+  // for; the fp32 form (KS = 32, rows up to 128) uses the wide LDS layout
+  const bool small_k = num_rbf <= 64 && !fp32_strict;
+  const size_t lds = sizeof(float) * bwd_lds_floats(small_k ? num_rbf : kMaxK);
   allow_lds_once();
   const int grid = max_pairs == 0 ? 1 : groups;
-  const bool small_k = num_rbf <= 64;
 #define MLCG_BWD_LAUNCH(KS, NODES, B, A)                                                      \
   hipLaunchKernelGGL((filter_bwd_fused_kernel<KS, NODES, B, A>), dim3(grid),                 \
                      dim3(kBwdThreads), lds, s, pos, pair_ij, pair_ij + pair_stride,         \
@@ -2049,13 +2156,14 @@ extern "C" int mlcg_filter_bwd(const float* pos, const int32_t* pair_ij, int64_t
                                int num_filters, const float* Wbar, const float* Wdbar,
                                float* dW1, float* db1, float* dW2, float* abar_out,
                                float* adbar_out, float* workspace, int64_t workspace_floats,
-                               void* stream) {
+                               int fp32_strict, void* stream) {
   MLCG_REQUIRE(max_pairs == 0 || (Wbar && Wdbar));
   PairAdjoint adj{Wbar, Wdbar, nullptr, nullptr, nullptr, nullptr, nullptr};
   return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, basis, centers,
                            widths, alpha, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind,
                            conv_lo, conv_hi, act, W1, b1, W2, num_filters, adj, false, dW1, db1,
-                           dW2, abar_out, adbar_out, workspace, workspace_floats, stream);
+                           dW2, abar_out, adbar_out, workspace, workspace_floats,
+                           fp32_strict != 0, stream);
 }
 
 extern "C" int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
@@ -2069,14 +2177,15 @@ extern "C" int mlcg_filter_bwd_cfconv(const float* pos, const int32_t* pair_ij,
                                       const float* gagg1, const float* ydot,
                                       const float* ddot, float* dW1, float* db1, float* dW2,
                                       float* abar_out, float* adbar_out, float* workspace,
-                                      int64_t workspace_floats, void* stream) {
+                                      int64_t workspace_floats, int fp32_strict, void* stream) {
   MLCG_REQUIRE(max_pairs == 0 || (gagg2 && y));
   MLCG_REQUIRE(!gagg1 || ddot);
   PairAdjoint adj{nullptr, nullptr, gagg2, y, gagg1, gagg1 ? ydot : nullptr, ddot};
   return launch_filter_bwd(pos, pair_ij, pair_stride, n_pairs_dev, max_pairs, basis, centers,
                            widths, alpha, num_rbf, rbf_cut_kind, rbf_lo, rbf_hi, conv_cut_kind,
                            conv_lo, conv_hi, act, W1, b1, W2, num_filters, adj, true, dW1, db1,
-                           dW2, abar_out, adbar_out, workspace, workspace_floats, stream);
+                           dW2, abar_out, adbar_out, workspace, workspace_floats,
+                           fp32_strict != 0, stream);
 }
 
 // ---------------------------------------------------------------------------

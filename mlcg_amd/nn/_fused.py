@@ -570,7 +570,8 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
             lambda: _node_tmm_batch(probs, N, st.pos.device), *held)
         xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
         res = ops.filter_bwd_cfconv(st.pos, graph, st.filt, bp.W1, bp.b1, bp.W2, gagg2,
-                                    st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable)
+                                    st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable,
+                                    strict_fp32=spec.strict_fp32)
         gW1, gb1, gW2 = res[:3]
         if spec.basis_trainable:
             # basis parameters are shared by all blocks: accumulate

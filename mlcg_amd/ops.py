@@ -671,6 +671,38 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
     return W, Wd, dist
 
 
+NUMERICS_BWD_RANGE = 1  # mlcg_numerics_flags bit 0
+NUMERICS_WEIGHT_RANGE = 2  # bit 1
+
+
+def numerics_flags(device=None, clear: bool = True) -> torch.Tensor:
+    """The split-product kernels' flag word on `device` as a one-element int32
+    device tensor (no host synchronisation), cleared afterwards by default.
+    Bit 0 (NUMERICS_BWD_RANGE): a filter backward met |h| or |h'| >= 2^19, so
+    its weight gradients may be non-finite.  Bit 1 (NUMERICS_WEIGHT_RANGE): a
+    split filter kernel met a weight >= 65504 (the fp16 maximum) in magnitude."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    call("mlcg_numerics_flags", ptr(out), int(clear), stream_handle(dev))
+    return out
+
+
+def check_numerics(device=None) -> None:
+    """Raise RuntimeError if a split-product kernel reported a value past its
+    range since the last check (one host synchronisation); clears the flags."""
+    v = int(numerics_flags(device, clear=True).item())
+    if v & NUMERICS_WEIGHT_RANGE:
+        raise RuntimeError(
+            "filter kernels: a filter weight reached 65504 (the fp16 maximum) or more in "
+            "magnitude, past the range of the split-fp16 products; filters and their gradients may be non-finite. "
+            "Use strict fp32 filters (model.strict_fp32_filters = True) for such models")
+    if v & NUMERICS_BWD_RANGE:
+        raise RuntimeError(
+            "filter backward: an activation value or derivative reached 2^19 or more, past "
+            "the range of the split-fp16 products; weight gradients may be non-finite. "
+            "Use strict fp32 filters (model.strict_fp32_filters = True) for such models")
+
+
 def _pair_adjoint_outputs(want: bool, cap: int, F: int, dev):
     if not want:
         return None, None
@@ -680,10 +712,12 @@ def _pair_adjoint_outputs(want: bool, cap: int, F: int, dev):
 
 def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.Tensor,
                b1: torch.Tensor, W2: torch.Tensor, Wbar: torch.Tensor,
-               Wdbar: torch.Tensor, pair_adjoints: bool = False):
+               Wdbar: torch.Tensor, pair_adjoints: bool = False, strict_fp32: bool = False):
     """Gradients (dW1 [F, K], db1 [F], dW2 [F, F]) of <Wbar, W> + <Wdbar, dW/dd>;
     with pair_adjoints also the first-layer pair adjoints (abar, adbar)
-    [P, F] that rbf_param_grad consumes."""
+    [P, F] that rbf_param_grad consumes.  strict_fp32 runs every product on
+    the fp32 MFMA instead of split-fp16 products (which hold activations and
+    derivatives below 2^19, see check_numerics)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     K = spec.num_rbf
@@ -703,7 +737,7 @@ def filter_bwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
          *spec.basis_args(), K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
          spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
          ptr(W2c), F, ptr(Wbar.contiguous()), ptr(Wdbar.contiguous()), ptr(dW1), ptr(db1),
-         ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, stream_handle(dev))
+         ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, int(strict_fp32), stream_handle(dev))
     if pair_adjoints:
         return dW1, db1, dW2, ab, adb
     return dW1, db1, dW2
@@ -713,10 +747,11 @@ def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
                       W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor,
                       gagg2: torch.Tensor, y: torch.Tensor, gagg1: Optional[torch.Tensor],
                       ydot: Optional[torch.Tensor],
-                      ddot: Optional[torch.Tensor], pair_adjoints: bool = False):
+                      ddot: Optional[torch.Tensor], pair_adjoints: bool = False,
+                      strict_fp32: bool = False):
     """filter_bwd with Wbar_p = g2_i y_j + g2_j y_i + g1_i yd_j + g1_j yd_i and
     Wdbar_p = dd_p (g1_i y_j + g1_j y_i) formed in the kernel from node arrays
-    (pair_adjoints as in filter_bwd)."""
+    (pair_adjoints and strict_fp32 as in filter_bwd)."""
     pos = _validate_pos(pos)
     F = W1.shape[0]
     K = spec.num_rbf
@@ -735,7 +770,8 @@ def filter_bwd_cfconv(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec,
          cap, *spec.basis_args(), K, spec.rbf_cut_kind, spec.rbf_lo, spec.rbf_hi,
          spec.conv_cut_kind, spec.conv_lo, spec.conv_hi, spec.act, ptr(W1c), ptr(b1c),
          ptr(W2c), F, ptr(c(gagg2)), ptr(c(y)), ptr(c(gagg1)), ptr(c(ydot)), ptr(ddot),
-         ptr(dW1), ptr(db1), ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, stream_handle(dev))
+         ptr(dW1), ptr(db1), ptr(dW2), ptr(ab), ptr(adb), ptr(ws), nws, int(strict_fp32),
+         stream_handle(dev))
     if pair_adjoints:
         return dW1, db1, dW2, ab, adb
     return dW1, db1, dW2
