@@ -254,10 +254,13 @@ __global__ __launch_bounds__(kCountThreads) void radius_count_kernel(
 // two interleaved status arrays -- block b's status of a launch with epoch e
 // at word 2 + 2b + (e & 1).  Every block reads the two header words first;
 // each launch clears the other array's words up to the larger of the two
-// block counts, and its last block advances the header after its look-back
-// (by then every block has published, so every block has read the header).
-// The next launch's array is therefore zero wherever it reads, with no
-// clearing launch in between.  The caller's overflow word is cleared by
+// block counts, and its last block advances the header after its look-back.
+// When no wait timed out, every block has published by then, hence read the
+// header, and the next launch's array is zero wherever it reads, with no
+// clearing launch in between.  After a timeout (bit 8) a block that had not
+// started yet may read the advanced header and publish into the next
+// launch's array: the flag makes every caller raise, and the host discards
+// the workspace when it reads bit 8 (ops.radius_flags_read).  The caller's overflow word is cleared by
 // block 0 before it publishes its prefix, and every block raises its bits
 // only after its own look-back has reached that prefix.
 enum { kModeRowptr = 0, kModeFill = 1, kModeFused = 2 };
@@ -824,7 +827,7 @@ __global__ __launch_bounds__(BlockWaves<kMode>::value * MLCG_WAVE) void radius_r
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       lookback(ws + 2 + (int)(ws_epoch & 1), t, agg_e, agg_p, le, lp, ov);
-      if (t == nblocks - 1 && lane == 0) {  // every block has read the header
+      if (t == nblocks - 1 && lane == 0) {  // see the workspace notes above
         st_status(ws + 1, (int64_t)ws_mark > nblocks ? ws_mark : (uint64_t)nblocks);
         st_status(ws, ws_epoch + 1);
       }

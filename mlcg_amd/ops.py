@@ -135,6 +135,34 @@ def _validate_pos(pos: torch.Tensor) -> torch.Tensor:
     return pos.contiguous()
 
 
+def radius_flags_read(overflow: int) -> None:
+    """Host-side bookkeeping for radius-graph flags read back from the device:
+    after bit 8 (a look-back wait hit its bound) the cached look-back
+    workspaces are discarded -- a block that had not started when the last
+    block advanced the workspace header may have published into the next
+    launch's status array -- so the next call starts from a zero-filled one.
+    Every caller that reads the flags calls this before raising."""
+    if overflow & 8:
+        _RADIUS_WS.clear()
+
+
+def radius_flags_message(overflow: int, capacity=None) -> str:
+    """What the radius-graph flag bits of `overflow` mean."""
+    parts = []
+    if overflow & 1:
+        parts.append("a row reached max_num_neighbors")
+    if overflow & 2:
+        parts.append("more edges than the capacity" +
+                     (f" {capacity}" if capacity is not None else ""))
+    if overflow & 4:
+        parts.append("the exclusion list is not symmetric")
+    if overflow & 8:
+        parts.append("a look-back wait of the radius kernel hit its bound")
+    if overflow & 16:
+        parts.append("more than 2^31 - 1 edges for the int32 CSR")
+    return "; ".join(parts) if parts else "none"
+
+
 def _check_radius_flags(overflow: int) -> None:
     """Raise for the radius graph's internal failure bits (8: a look-back wait
     hit its bound, 16: more than 2^31 - 1 edges for the int32 CSR)."""
@@ -255,9 +283,7 @@ def radius_graph(
             e_count, p_count, overflow = torch.cat([rowptr[n:], pairptr[n:], flags]).tolist()
         else:
             (e_count, overflow), p_count = torch.cat([rowptr[n:], flags]).tolist(), 0
-        if overflow & 8 and ws_key is not None:
-            # a block gave up waiting: the workspace's state is no longer known
-            _RADIUS_WS.pop(ws_key, None)
+        radius_flags_read(overflow)
         _check_radius_flags(overflow)
         if with_pairs and overflow & 1:
             raise RuntimeError(

@@ -121,13 +121,20 @@ class CapturedTrainStep:
 
     def check(self) -> None:
         """Raise if the radius graph of any step so far (warm-up steps and
-        replays) overflowed its edge capacity or max_num_neighbors (one host
-        synchronisation); the flags are cleared afterwards."""
+        replays) overflowed its edge capacity or max_num_neighbors, or a
+        split-fp16 filter kernel met a value past its range
+        (ops.check_numerics); one host synchronisation, the flags are cleared
+        afterwards."""
+        from .. import ops
+
+        ops.check_numerics(self.data.pos.device)
         flags = int(self.sticky.item())
         if flags:
             self.sticky.zero_()
-            raise RuntimeError(
-                f"radius graph of a captured step reported flags {flags} (bit 0: "
-                "max_num_neighbors reached, bit 1: more edges than the capacity "
-                f"{[m.graph_capacity for m in self.schnets]}); rebuild the "
-                "CapturedTrainStep with a larger capacity_factor")
+            ops.radius_flags_read(flags)
+            msg = ops.radius_flags_message(flags, [m.graph_capacity for m in self.schnets])
+            hint = ("rebuild the CapturedTrainStep with a larger capacity_factor or "
+                    "max_num_neighbors" if flags & 3 else
+                    "an internal failure of the radius kernel; rebuild the CapturedTrainStep")
+            raise RuntimeError(f"radius graph of a captured step reported flags {flags} "
+                               f"({msg}): {hint}")

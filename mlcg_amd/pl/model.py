@@ -62,6 +62,11 @@ class PLModel(torch.nn.Module):
 
     def on_train_epoch_end(self) -> None:
         detect_nan_parameters(self.model)
+        p = next(self.model.parameters(), None)
+        if p is not None and p.is_cuda:
+            from .. import ops
+
+            ops.check_numerics(p.device)  # split-fp16 range flags of the epoch
 
     def on_validation_epoch_end(self) -> torch.Tensor:
         """Mean over batches of the batch-size weighted validation loss per

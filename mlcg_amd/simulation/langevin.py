@@ -233,12 +233,17 @@ class LangevinSimulation:
         graph: `sticky` is the OR of every step's graph flags, accumulated on
         the device inside the (captured) step, so an overflow between two
         checks is not lost."""
+        from .. import ops
+
+        ops.check_numerics(self.device)
         v = int(sticky.item())
         if v:
+            ops.radius_flags_read(v)
+            hint = ("raise edge_capacity_factor or max_num_neighbors" if v & 3
+                    else "an internal failure of the radius kernel")
             raise RuntimeError(
-                f"radius graph overflow (flags={v}) in a step before step "
-                f"{self.current_step_for_check}: raise edge_capacity_factor or "
-                "max_num_neighbors")
+                f"radius graph overflow flags {v} ({ops.radius_flags_message(v)}) in a step before "
+                f"step {self.current_step_for_check}: {hint}")
 
     def simulate(self) -> np.ndarray:
         """Runs the BAOAB steps up to n_timesteps (from the checkpointed step

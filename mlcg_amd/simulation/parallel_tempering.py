@@ -14,9 +14,9 @@ configurations, rescaling the velocities by sqrt(beta_old / beta_new)
 beta_new keeps its kinetic temperature consistent with the new slot.  (The
 reference's code multiplies by sqrt(beta_new / beta_old) instead, lines
 484-497, which heats configurations moving to a colder slot; this module
-follows the docstring and equipartition; ``reference_velocity_scaling=True``
-applies the reference code's factor instead, for reproducing a reference run's
-ensemble.)  The forces travel with the configurations
+follows the docstring and equipartition, and warns once when the choice is
+left to the default; ``reference_velocity_scaling=True`` applies the reference
+code's factor instead, for reproducing a reference run's ensemble.)  The forces travel with the configurations
 (a force depends on the configuration only), so the next half-kick uses the
 force of the configuration it moves.  `acceptance_matrix[a, b]` counts the
 accepted (a < b) and rejected (a > b) exchanges between temperatures a and b.
@@ -26,7 +26,8 @@ The exchange runs on the host between steps, so it also works with
 
 from __future__ import annotations
 
-from typing import List, Tuple
+import warnings
+from typing import List, Optional, Tuple
 
 import numpy as np
 import torch
@@ -34,9 +35,12 @@ import torch
 from .langevin import LangevinSimulation
 
 
+_WARNED_SCALING = False
+
+
 class PTSimulation(LangevinSimulation):
-    def __init__(self, exchange_interval: int = 100, reference_velocity_scaling: bool = False,
-                 **kwargs):
+    def __init__(self, exchange_interval: int = 100,
+                 reference_velocity_scaling: Optional[bool] = None, **kwargs):
         super().__init__(**kwargs)
         if exchange_interval < 1:
             raise ValueError("exchange_interval must be positive")
@@ -44,7 +48,20 @@ class PTSimulation(LangevinSimulation):
         # False: a configuration moving from beta_old to beta_new has its
         # velocities scaled by sqrt(beta_old / beta_new) (the reference's
         # docstring, parallel_tempering.py:433-435); True: by
-        # sqrt(beta_new / beta_old), as the reference's code does (484-497)
+        # sqrt(beta_new / beta_old), as the reference's code does (484-497).
+        # Left unset, the docstring's factor is used and a warning says once
+        # per process that it differs from the reference code's.
+        if reference_velocity_scaling is None:
+            global _WARNED_SCALING
+            if not _WARNED_SCALING:
+                _WARNED_SCALING = True
+                warnings.warn(
+                    "PTSimulation rescales exchanged velocities by sqrt(beta_old / beta_new) "
+                    "(equipartition, as the reference's docstring states); the reference code "
+                    "applies sqrt(beta_new / beta_old). Pass reference_velocity_scaling=True to "
+                    "reproduce a reference run, or False to silence this warning.",
+                    stacklevel=2)
+            reference_velocity_scaling = False
         self.reference_velocity_scaling = bool(reference_velocity_scaling)
         self._hook = self.detect_and_exchange_replicas
         self._hook_interval = self.exchange_interval

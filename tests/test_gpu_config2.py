@@ -69,6 +69,13 @@ def _check(label, hip, ref, n_edges_ref=None):
     assert abs(loss - float(loss_r)) <= RTOL_EF * abs(float(loss_r))
     assert_close(E, E_r, RTOL_EF, scaled_atol(E_r, ATOL_EF), f"[{label}] energy")
     assert_close(F, F_r, RTOL_EF, scaled_atol(F_r, ATOL_EF), f"[{label}] forces")
+    # the literal reading of the bar (absolute term 1e-6, not 1e-6 max|ref|),
+    # reported beside the scaled one
+    for name, got, r in (("energy", E, E_r), ("forces", F, F_r)):
+        n_lit, n, _, _ = close_report(got, r, RTOL_EF, ATOL_EF)
+        print(f"[{label}] {name}: {n_lit}/{n} elements outside rtol 1e-5 + literal atol 1e-6 "
+              f"(0 outside the scaled bound atol = 1e-6 max|ref| = "
+              f"{scaled_atol(r, ATOL_EF):.3g})")
     worst = 0.0
     for k, gr in g_r.items():
         assert grads[k] is not None, k
@@ -99,6 +106,9 @@ def test_config2_32_frames_vs_oracle(strict):
         for name, got, r in (("F", r32[2], ref[2]), ("E", r32[1], ref[1])):
             print("reference fp32 arithmetic vs fp64,", name, close_report(
                 got, r, RTOL_EF, scaled_atol(r, ATOL_EF))[3])
+            n_lit, n, _, _ = close_report(got, r, RTOL_EF, ATOL_EF)
+            print(f"reference fp32 arithmetic vs fp64, {name}: {n_lit}/{n} elements outside "
+                  "rtol 1e-5 + literal atol 1e-6")
     _check("32 frames " + ("strict" if strict else "split"), _hip_step(sd, b, strict), ref,
            ei.shape[1])
 

@@ -15,7 +15,8 @@ import torch
 
 from oracle import radius as oracle_radius
 from oracle import schnet_ref as R
-from tests.helpers import check, check_calibrated, make_cfg, make_model, max_abs, rel_err
+from tests.helpers import (check, check_calibrated, close_report, make_cfg, make_model, max_abs,
+                           rel_err, scaled_atol)
 
 pytestmark = pytest.mark.gpu
 
@@ -209,10 +210,19 @@ def test_config1_cpu_reference_case():
     pos64, types, batch, ei = _oracle_inputs(b, 30.0)
     E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
                                           batch, ei, b.n_frames)
+    E32, F32 = R.schnet_energy_forces(sd, cfg, pos64.float(), types, batch, ei, b.n_frames)
     model = make_model(cfg, sd)
     data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
     check(data.out["SchNet"]["energy"], E_ref, 1e-5, 'data.out["SchNet"]["energy"]')
     check(data.out["SchNet"]["forces"], F_ref, 1e-5, 'data.out["SchNet"]["forces"]')
+    # the literal reading of the bar (absolute term 1e-6 rather than 1e-6 of
+    # the largest element), for the kernels and for the reference's own fp32
+    for name, got, r32, r in (("energy", data.out["SchNet"]["energy"], E32, E_ref),
+                              ("forces", data.out["SchNet"]["forces"], F32, F_ref)):
+        n_hip, n, _, _ = close_report(got, r, 1e-5, 1e-6)
+        n_ref, _, _, _ = close_report(r32, r, 1e-5, 1e-6)
+        print(f"config 1 {name}: {n_hip}/{n} elements outside rtol 1e-5 + literal atol 1e-6 "
+              f"(the reference's fp32 arithmetic: {n_ref}/{n})")
 
 
 def test_golden_fixture_hip():
@@ -273,7 +283,7 @@ def test_fp16_filters_config4_vs_oracle():
     with the pair terms it sums)."""
     from mlcg_amd import nn, synthetic
 
-    b = synthetic.config4(n_frames=3)
+    b = synthetic.config4(n_frames=16)
     cfg, sd, model = _config4_model()
     pos64, types, batch, ei = _oracle_inputs(b, 15.0)
     E_ref, F_ref = R.schnet_energy_forces(R.to_dtype(sd, torch.float64), cfg, pos64, types,
@@ -281,8 +291,16 @@ def test_fp16_filters_config4_vs_oracle():
     model.fp16_filters = True
     data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
     print("fp16 config4: edges", ei.shape[1])
-    check(data.out["SchNet"]["energy"], E_ref, 2e-3, "fp16 energy", atol_frac=1.0)
-    check(data.out["SchNet"]["forces"], F_ref, 2e-3, "fp16 forces", atol_frac=1.0)
+    E16, F16 = data.out["SchNet"]["energy"], data.out["SchNet"]["forces"]
+    check(E16, E_ref, 2e-3, "fp16 energy", atol_frac=1.0)
+    check(F16, F_ref, 2e-3, "fp16 forces", atol_frac=1.0)
+    # other readings of "2e-3 relative": norm-wise, and per element with the
+    # absolute term a tenth of the bound's (2e-4 of the largest component)
+    print(f"fp16 config4: norm-wise relative error: forces {rel_err(F16, F_ref):.3e}, "
+          f"energies {rel_err(E16, E_ref):.3e}")
+    n_el, n, _, _ = close_report(F16, F_ref, 2e-3, scaled_atol(F_ref, 2e-4))
+    print(f"fp16 config4 forces: {n_el}/{n} components outside 2e-3 |ref| + 2e-4 max|ref|")
+    assert rel_err(F16, F_ref) < 2e-3
     # and the fp32 path on the same frames meets the fp32 tolerance
     model.fp16_filters = False
     d32 = nn.GradientsOut(model).eval()(b.to_torch("cuda"))

@@ -315,3 +315,20 @@ def test_reference_operators_registered_with_fake_kernels():
         assert d.dtype == torch.float64 and d.shape[0] == ei.shape[1]
         xs, ptr = torch.ops.mlcg.exclusion_pair_to_ptr(torch.empty(2, 5, dtype=torch.int64), 7)
         assert tuple(xs.shape) == (5,) and tuple(ptr.shape) == (8,)
+
+
+def test_radius_flag_bookkeeping():
+    """Every bit of the radius graph's flag word is named, and a look-back
+    timeout (bit 8) discards the cached look-back workspaces so that the next
+    call starts from a zero-filled one (other bits keep them)."""
+    from mlcg_amd import ops
+
+    assert ops.radius_flags_message(0) == "none"
+    msg = ops.radius_flags_message(1 | 2 | 4 | 8 | 16, capacity=100)
+    for part in ("max_num_neighbors", "capacity 100", "not symmetric", "look-back", "2^31"):
+        assert part in msg, (part, msg)
+    ops._RADIUS_WS[(0, 1)] = "workspace"
+    ops.radius_flags_read(1 | 2 | 4 | 16)
+    assert (0, 1) in ops._RADIUS_WS
+    ops.radius_flags_read(8)
+    assert not ops._RADIUS_WS

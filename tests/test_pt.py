@@ -145,3 +145,23 @@ def test_pt_run_on_the_gpu():
     for r, b in enumerate(betas):
         ke = float((0.5 * m[r] * v[r] * v[r]).mean())
         assert ke == pytest.approx(0.5 / b, rel=0.1), r
+
+
+def test_default_velocity_scaling_warns_once():
+    """Left unset, the velocity factor is the docstring's (not the reference
+    code's) and a warning says so once per process; an explicit choice is
+    silent."""
+    import warnings
+
+    from mlcg_amd.simulation import parallel_tempering as ptm
+
+    ptm._WARNED_SCALING = False
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        a = PTSimulation(exchange_interval=5, n_timesteps=10, save_interval=10, device="cpu")
+        PTSimulation(exchange_interval=5, n_timesteps=10, save_interval=10, device="cpu")
+        PTSimulation(exchange_interval=5, reference_velocity_scaling=False, n_timesteps=10,
+                     save_interval=10, device="cpu")
+    msgs = [str(w.message) for w in rec if "reference_velocity_scaling" in str(w.message)]
+    assert len(msgs) == 1, msgs
+    assert a.reference_velocity_scaling is False
