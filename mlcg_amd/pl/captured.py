@@ -99,7 +99,8 @@ class CapturedTrainStep:
 
     def load(self, batch) -> None:
         """Copy batch's tensors into the recorded inputs (same keys, shapes
-        and dtypes), on the current stream."""
+        and dtypes), on the current stream, as one multi-tensor copy."""
+        dsts, srcs = [], []
         for k in self.fields:
             src = batch[k] if k in batch else None
             dst = self.data[k]
@@ -109,7 +110,10 @@ class CapturedTrainStep:
                     f"({tuple(dst.shape)}, {dst.dtype}); got "
                     f"{None if src is None else (tuple(src.shape), src.dtype)}")
             if src.data_ptr() != dst.data_ptr():
-                dst.copy_(src, non_blocking=True)
+                dsts.append(dst)
+                srcs.append(src if src.device == dst.device else src.to(dst.device))
+        if dsts:
+            torch._foreach_copy_(dsts, srcs, non_blocking=True)
 
     def step(self, batch=None) -> torch.Tensor:
         """One training step on batch (default: the recorded inputs as they
