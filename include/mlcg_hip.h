@@ -487,6 +487,15 @@ int mlcg_node_tmm_batch(const void* const* problems, int count, int64_t rows,
                         int features, int accumulate, float* workspace,
                         int64_t workspace_floats, void* stream);
 
+/* out [n, 128] = table[types[i]] for a [num_types, 128] fp32 table (16-byte
+ * aligned): the embedding lookup of schnet.py:132
+ * (`x = self.embedding_layer(data.atom_types)`, torch.nn.Embedding).  A type
+ * outside [0, num_types) gives a zero row and sets bit 2 of
+ * mlcg_numerics_flags (torch raises a device-side assertion there). */
+int mlcg_embedding_gather(const float* table, int num_types, int features,
+                          const int64_t* types, int64_t n, float* out,
+                          void* stream);
+
 /* out [num_types, 128] = for each type t the sum of the rows of x [rows, 128]
  * whose types[row] == t: the gradient of the bead-type embedding table
  * (schnet.py:132, `x = self.embedding_layer(data.atom_types)`, whose

@@ -98,6 +98,7 @@ _SIGNATURES = {
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
     "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
     "mlcg_numerics_flags": [_P, _I32, _P],
+    "mlcg_embedding_gather": [_P, _I32, _I32, _P, _I64, _P, _P],
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
 }

@@ -41,6 +41,11 @@ static inline unsigned mlcg_persistent_groups(int64_t work_groups, int per_cu) {
 
 __device__ __forceinline__ int mlcg_lane() { return threadIdx.x & (MLCG_WAVE - 1); }
 
+// Device address of the library's numerics flag word on the current device
+// (defined in filter.hip, read by mlcg_numerics_flags), or nullptr.
+unsigned* mlcg_numerics_word_ptr();
+constexpr unsigned kFlagTypeRange = 4u;  // bit 2: an atom type outside the table
+
 // Sum across the 64 lanes of a wave (butterfly through ds_swizzle/dpp via
 // __shfl_xor); every lane receives the total.
 __device__ __forceinline__ float mlcg_wave_sum(float v) {

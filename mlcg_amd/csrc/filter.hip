@@ -28,6 +28,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <mutex>
+
 namespace {
 
 #ifndef MLCG_FILTER_FWD_X3
@@ -659,7 +661,10 @@ __device__ __forceinline__ floatx4 mfma_x3(halfx8 ah, halfx8 ahs, halfx8 al, hal
 //            split operands hold, so its weight gradients may be non-finite;
 //   bit 1 -- a filter weight (W1 or W2) of magnitude 65504 (the fp16
 //            maximum) or more, past what the weights' fp16 planes hold
-//            (forward and backward).
+//            (forward and backward);
+//   bit 2 -- an atom type outside the embedding table (node.hip's
+//            embedding lookup, which finds the word through
+//            mlcg_numerics_word_ptr).
 // (The split forward needs no flag for large activations: a tile whose
 // values pass its bound is recomputed with a power-of-two scale, exactly.)
 __device__ unsigned mlcg_numerics_word;
@@ -670,6 +675,10 @@ constexpr float kWeightBound = 65504.0f;
 __device__ __forceinline__ void raise_numerics_flag(unsigned bits) {
   atomicOr(&mlcg_numerics_word, bits);
 }
+
+constexpr int kFlagDevices = 64;
+std::mutex g_flag_mutex;
+unsigned* g_flag_ptr[kFlagDevices] = {};
 
 __global__ void numerics_flags_kernel(int* out, int clear) {
   if (threadIdx.x == 0) {
@@ -2005,6 +2014,22 @@ bool valid_params(int basis, int K, int rk, int ck, int act, int F) {
 }
 
 }  // namespace
+
+// Device address of the numerics flag word on the current device (looked up
+// once per device with hipGetSymbolAddress; nullptr on failure), for the
+// kernels of other translation units that raise its bits.
+unsigned* mlcg_numerics_word_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFlagDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_flag_mutex);
+  if (g_flag_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(mlcg_numerics_word)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_flag_ptr[dev] = static_cast<unsigned*>(p);
+  }
+  return g_flag_ptr[dev];
+}
 
 extern "C" int mlcg_numerics_flags(int* out, int clear, void* stream) {
   MLCG_REQUIRE(out != nullptr);

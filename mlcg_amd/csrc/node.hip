@@ -746,6 +746,29 @@ void node_gemm2_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Embedding lookup: out[i][:] = table[types[i]][:] for [T, 128] fp32 tables
+// (schnet.py:132, `x = self.embedding_layer(data.atom_types)`): 32 lanes per
+// row, one float4 each, grid-stride.  A type outside [0, T) writes a zero row
+// and raises bit 2 of the numerics flag word (when its address is known).
+__global__ __launch_bounds__(256) void embedding_gather_kernel(
+    const float4* __restrict__ table, int T, const int64_t* __restrict__ types, int64_t n,
+    float4* __restrict__ out, unsigned* flags) {
+  const int64_t total = n * (kF / 4);
+  for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < total;
+       k += (int64_t)gridDim.x * 256) {
+    const int64_t r = k / (kF / 4);
+    const int c = (int)(k % (kF / 4));
+    const int64_t t = types[r];
+    float4 v{0.f, 0.f, 0.f, 0.f};
+    if (t >= 0 && t < T)
+      v = table[t * (kF / 4) + c];
+    else if (c == 0 && flags)
+      atomicOr(flags, kFlagTypeRange);
+    out[k] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // type_sum: out[t][:] = sum of the rows x[n][:] with types[n] == t, for
 // t < T <= 128 -- the gradient of an embedding table.  One workgroup per
 // type t walks the rows in chunks: its waves find the rows of type t
@@ -1080,6 +1103,22 @@ extern "C" int mlcg_node_tmm_batch(const void* const* problems, int count, int64
                      dim3(kTmmThreads), 0, s, batch, rows, workspace);
   hipLaunchKernelGGL(node_tmm_reduce_batch_kernel, dim3((kF * kF + kF) / 64, (unsigned)count),
                      dim3(512), 0, s, workspace, groups, accumulate, batch);
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_embedding_gather(const float* table, int num_types, int features,
+                                     const int64_t* types, int64_t n, float* out,
+                                     void* stream) {
+  if (features != kF) return MLCG_ERR_UNSUPPORTED;
+  MLCG_REQUIRE(n >= 0 && num_types >= 1);
+  if (n == 0) return MLCG_OK;
+  MLCG_REQUIRE(table && types && out);
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(table) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n * (kF / 4), 256), 16);
+  hipLaunchKernelGGL(embedding_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
+                     reinterpret_cast<const float4*>(table), num_types, types, n,
+                     reinterpret_cast<float4*>(out), mlcg_numerics_word_ptr());
   return mlcg_launch_status();
 }
 

@@ -283,7 +283,11 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     from."""
     st = State(pos=pos, types=types, graph=graph, filt=filter_spec(spec, P))
     ahead = _filters_ahead(spec, P, pos, graph, st.filt)
-    x = P.emb.index_select(0, types)
+    if (P.emb.dim() == 2 and P.emb.shape[1] == ops.NUM_FILTERS
+            and P.emb.dtype == torch.float32 and types.dtype == torch.int64):
+        x = ops.embedding_gather(P.emb.detach(), types)
+    else:
+        x = P.emb.index_select(0, types)
     for k, bp in enumerate(P.blocks):
         if k in ahead:
             W, Wd, done = ahead[k]

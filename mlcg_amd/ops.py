@@ -537,6 +537,22 @@ def node_tmm_batch(problems, rows: int, device) -> list:
     return outs
 
 
+def embedding_gather(table: torch.Tensor, types: torch.Tensor) -> torch.Tensor:
+    """table[types] for a [T, 128] fp32 table and int64 types (the embedding
+    lookup, mlcg_embedding_gather); a type outside [0, T) gives a zero row and
+    sets NUMERICS_TYPE_RANGE (check_numerics raises)."""
+    require_device(table, types)
+    _check(table.dim() == 2 and table.shape[1] == NUM_FILTERS and table.dtype == torch.float32,
+           "embedding_gather takes a [T, 128] float32 table")
+    _check(types.dtype == torch.int64 and types.dim() == 1, "types must be 1-D int64")
+    t = table.contiguous()
+    ty = types.contiguous()
+    out = torch.empty(ty.shape[0], NUM_FILTERS, dtype=torch.float32, device=table.device)
+    call("mlcg_embedding_gather", ptr(t), t.shape[0], NUM_FILTERS, ptr(ty), ty.shape[0],
+         ptr(out), stream_handle(table.device))
+    return out
+
+
 def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
              ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(out [num_types, 128], bad [1] int32): out[t] = sum of the rows of x
@@ -699,6 +715,7 @@ def filter_fwd(pos: torch.Tensor, graph: PairGraph, spec: FilterSpec, W1: torch.
 
 NUMERICS_BWD_RANGE = 1  # mlcg_numerics_flags bit 0
 NUMERICS_WEIGHT_RANGE = 2  # bit 1
+NUMERICS_TYPE_RANGE = 4  # bit 2
 
 
 def numerics_flags(device=None, clear: bool = True) -> torch.Tensor:
@@ -706,7 +723,8 @@ def numerics_flags(device=None, clear: bool = True) -> torch.Tensor:
     device tensor (no host synchronisation), cleared afterwards by default.
     Bit 0 (NUMERICS_BWD_RANGE): a filter backward met |h| or |h'| >= 2^19, so
     its weight gradients may be non-finite.  Bit 1 (NUMERICS_WEIGHT_RANGE): a
-    split filter kernel met a weight >= 65504 (the fp16 maximum) in magnitude."""
+    split filter kernel met a weight >= 65504 (the fp16 maximum) in magnitude.
+    Bit 2 (NUMERICS_TYPE_RANGE): embedding_gather met a type outside its table."""
     dev = torch.device("cuda") if device is None else torch.device(device)
     out = torch.empty(1, dtype=torch.int32, device=dev)
     call("mlcg_numerics_flags", ptr(out), int(clear), stream_handle(dev))
@@ -717,6 +735,9 @@ def check_numerics(device=None) -> None:
     """Raise RuntimeError if a split-product kernel reported a value past its
     range since the last check (one host synchronisation); clears the flags."""
     v = int(numerics_flags(device, clear=True).item())
+    if v & NUMERICS_TYPE_RANGE:
+        raise RuntimeError("embedding lookup: an atom type lies outside the embedding table "
+                           "(its row was set to zero)")
     if v & NUMERICS_WEIGHT_RANGE:
         raise RuntimeError(
             "filter kernels: a filter weight reached 65504 (the fp16 maximum) or more in "

@@ -282,3 +282,26 @@ def test_type_sum_flags_out_of_table_types():
     assert out[:, 0].tolist() == [2.0, 3.0, 2.0, 2.0]  # the type-9 row is skipped
     with pytest.raises(RuntimeError):
         ops.type_sum(x, types, 129)
+
+
+@pytest.mark.parametrize("rows", [1, 33, 17920, 128000])
+def test_embedding_gather(rows):
+    """The embedding lookup equals torch's index_select bit for bit; a type
+    outside the table gives a zero row and raises through check_numerics."""
+    from mlcg_amd import ops
+
+    print(f"embedding_gather rows={rows}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    table = torch.randn(100, 128, device="cuda", generator=g)
+    types = torch.randint(0, 100, (rows,), device="cuda", generator=g)
+    ops.numerics_flags(clear=True)
+    assert torch.equal(ops.embedding_gather(table, types), table.index_select(0, types))
+    ops.check_numerics()
+    bad = types.clone()
+    bad[rows // 2] = 100
+    out = ops.embedding_gather(table, bad)
+    assert float(out[rows // 2].abs().max()) == 0.0
+    keep = torch.arange(rows, device="cuda") != rows // 2
+    assert torch.equal(out[keep], table.index_select(0, types)[keep])
+    with pytest.raises(RuntimeError, match="embedding table"):
+        ops.check_numerics()
