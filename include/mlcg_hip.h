@@ -312,13 +312,15 @@ int mlcg_cfconv_gather(const float* src, const void* W, int w_f16,
                        int num_filters, float* out, void* stream);
 
 /* Force backward of one CFConv: ybar[i] = sum_j gagg[j] * W_ij and, per
- * pair p = {i < j}, dbar[p] += <Wd_p, gagg[i] * y[j] + gagg[j] * y[i]>.
+ * pair p = {i < j}, dbar[p] += <Wd_p, gagg[i] * y[j] + gagg[j] * y[i]>
+ * (accumulate != 0) or dbar[p] = ... (accumulate == 0: dbar need not be
+ * initialised; pairs past the graph's live count are left untouched).
  * Replaces the autograd backward of schnet.py:340-346. */
 int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const void* W,
                            const void* Wd, int w_f16, const int32_t* rowptr,
                            const int32_t* col, const int32_t* eid2pair,
                            int64_t n_nodes, int num_filters, float* ybar,
-                           float* dbar, void* stream);
+                           float* dbar, int accumulate, void* stream);
 
 /* Tangent (forward-mode) of the CFConv aggregation along a position
  * direction: out[i] = sum_j ydot[j] * W_ij + y[j] * Wd_ij * ddot_p.
@@ -391,10 +393,12 @@ int mlcg_rbf_param_grad(const float* dist, const int32_t* n_pairs_dev,
                         float* dwidths, float* workspace,
                         int64_t workspace_floats, void* stream);
 
-/* ddot[p] = rhat_p . (u[j] - u[i]), rhat_p = (pos[j] - pos[i]) / dist[p]. */
+/* ddot[p] = scale * rhat_p . (u[j] - u[i]), rhat_p = (pos[j] - pos[i]) /
+ * dist[p] (scale = -1 gives the tangent along -u exactly, without negating
+ * u first). */
 int mlcg_pair_ddot(const float* pos, const float* dist, const int32_t* pair_ij,
                    int64_t pair_stride, const int32_t* n_pairs_dev,
-                   int64_t max_pairs, const float* u, float* ddot,
+                   int64_t max_pairs, const float* u, float scale, float* ddot,
                    void* stream);
 
 /* forces[i] (+)= sum_{j in row i} dbar[p(i,j)] (pos[j] - pos[i]) / dist[p].
@@ -504,7 +508,8 @@ int mlcg_embedding_gather(const float* table, int num_types, int features,
  * (with many rows, G groups of row chunks per type whose partial sums are
  * added in group order), so the result is run-to-run identical.
  * num_types <= 128 (MLCG_ERR_UNSUPPORTED beyond); a type outside
- * [0, num_types) is skipped and sets *bad = 1 (bad is not cleared here).
+ * [0, num_types) is skipped and sets *bad = 1 (bad is not cleared here),
+ * or, with bad == NULL, bit 2 of the numerics flags (mlcg_numerics_flags).
  * mlcg_type_sum_workspace_floats gives the workspace the call needs: 0 up to
  * 24,576 rows or when one group per type fills the chip (workspace may then
  * be NULL), else 2 G num_types 128 floats. */
@@ -664,6 +669,15 @@ int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
  * ceiling. */
 int mlcg_stream_copy(const float* src, float* dst, int64_t n, int groups,
                      int unroll, void* stream);
+
+/* Device-to-device copies dsts[k][0 .. bytes[k]) = srcs[k][...] for
+ * k < count <= 8 (MLCG_ERR_UNSUPPORTED beyond) in one launch; every pointer
+ * 16-byte aligned, the ranges must not overlap.  The pointer and size arrays
+ * are host memory, read before the call returns.  No counterpart in the
+ * reference (its batches arrive through the data loader): it loads a new
+ * batch into the inputs of a training step recorded as a HIP graph. */
+int mlcg_copy_batch(const void* const* srcs, void* const* dsts,
+                    const int64_t* bytes, int count, void* stream);
 
 #ifdef __cplusplus
 }

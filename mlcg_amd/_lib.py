@@ -67,11 +67,12 @@ _SIGNATURES = {
     "mlcg_rbf_param_grad": [_P, _P, _I64, _I32, _P, _P, _F32, _I32, _I32, _F32, _F32, _P, _I32,
                             _P, _P, _I32, _P, _P, _P, _I64, _P],
     "mlcg_cfconv_gather": [_P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P],
-    "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
+    "mlcg_cfconv_gather_bwd": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _P, _P, _I32,
+                               _P],
     "mlcg_cfconv_gather_tangent": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_cfconv_gather_rev2": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P,
                                 _P, _P],
-    "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _P, _P],
+    "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _F32, _P, _P],
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
     "mlcg_node_gemm": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
@@ -101,6 +102,7 @@ _SIGNATURES = {
     "mlcg_embedding_gather": [_P, _I32, _I32, _P, _I64, _P, _P],
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
+    "mlcg_copy_batch": [_P, _P, _P, _I32, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_radius_workspace_bytes": _I64,

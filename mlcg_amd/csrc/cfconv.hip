@@ -175,7 +175,9 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
 }
 
 // ybar[i] = sum_j gagg[j] W_ij (all edges) and, on the upper edges (i < j)
-// that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i>.  The steps of
+// that own pair p, dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i> (dbar[p] = ...
+// with accumulate == 0, so the first of a model's blocks needs no zeroed
+// dbar).  The steps of
 // upper edges keep kUp steps (four loads per edge) in flight: its registers
 // set the kernel's occupancy, lower-edge steps included.
 template <int kUp>
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     const float* __restrict__ gagg, const float* __restrict__ y, const void* __restrict__ W,
     const void* __restrict__ Wd, int w_f16, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ col, const int32_t* __restrict__ eid2pair, int64_t n,
-    float* __restrict__ ybar, float* __restrict__ dbar) {
+    float* __restrict__ ybar, float* __restrict__ dbar, int accumulate) {
   const int lane = mlcg_lane();
   const int h = lane >> 5, m = lane & 31;
   const bool f16 = w_f16 != 0;
@@ -238,13 +240,21 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUp; ++u) part[u] = half_sum(part[u]);
-    // each pair has exactly one upper edge, so one add per address and launch:
-    // a returnless float atomic (performed in the L2) adds it without the
-    // dependent load of a read-modify-write holding up the next step
-    if (m == 0)
+    // each pair has exactly one upper edge, so one write per address and
+    // launch: a plain store, or a returnless float atomic (performed in the
+    // L2) that adds without the dependent load of a read-modify-write holding
+    // up the next step
+    if (m == 0) {
+      if (accumulate) {
 #pragma unroll
-      for (int u = 0; u < kUp; ++u)
-        if (up[u]) unsafeAtomicAdd(dbar + p[u], part[u]);
+        for (int u = 0; u < kUp; ++u)
+          if (up[u]) unsafeAtomicAdd(dbar + p[u], part[u]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < kUp; ++u)
+          if (up[u]) dbar[p[u]] = part[u];
+      }
+    }
   }
   MLCG_ROW_LOOP_END
   acc = combine_halves(acc, h);
@@ -379,7 +389,8 @@ __global__ __launch_bounds__(kThreads) void gather_rev2_kernel(
 __global__ void pair_ddot_kernel(const float* __restrict__ pos, const float* __restrict__ dist,
                                  const int32_t* __restrict__ pi, const int32_t* __restrict__ pj,
                                  const int32_t* __restrict__ n_pairs_dev, int64_t max_pairs,
-                                 const float* __restrict__ u, float* __restrict__ ddot) {
+                                 const float* __restrict__ u, float scale,
+                                 float* __restrict__ ddot) {
   int64_t np = *n_pairs_dev;
   if (np > max_pairs) np = max_pairs;
   for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < np;
@@ -389,7 +400,7 @@ __global__ void pair_ddot_kernel(const float* __restrict__ pos, const float* __r
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 3; ++c) acc += (pos[3 * j + c] - pos[3 * i + c]) * (u[3 * j + c] - u[3 * i + c]);
-    ddot[p] = acc * inv;
+    ddot[p] = (acc * inv) * scale;
   }
 }
 
@@ -540,7 +551,7 @@ extern "C" int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const v
                                       const void* Wd, int w_f16, const int32_t* rowptr,
                                       const int32_t* col, const int32_t* eid2pair,
                                       int64_t n_nodes, int num_filters, float* ybar,
-                                      float* dbar, void* stream) {
+                                      float* dbar, int accumulate, void* stream) {
   if (num_filters != kF) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(n_nodes >= 0);
   if (n_nodes == 0) return MLCG_OK;
@@ -552,11 +563,11 @@ extern "C" int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const v
   if (w_f16)
     hipLaunchKernelGGL(gather_bwd_kernel<2>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
                        mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
-                       n_nodes, ybar, dbar);
+                       n_nodes, ybar, dbar, accumulate);
   else
     hipLaunchKernelGGL(gather_bwd_kernel<kSteps>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
                        mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
-                       n_nodes, ybar, dbar);
+                       n_nodes, ybar, dbar, accumulate);
   return mlcg_launch_status();
 }
 
@@ -597,13 +608,14 @@ extern "C" int mlcg_cfconv_gather_rev2(const float* gagg2, const float* gagg1, c
 
 extern "C" int mlcg_pair_ddot(const float* pos, const float* dist, const int32_t* pair_ij,
                               int64_t pair_stride, const int32_t* n_pairs_dev,
-                              int64_t max_pairs, const float* u, float* ddot, void* stream) {
+                              int64_t max_pairs, const float* u, float scale, float* ddot,
+                              void* stream) {
   MLCG_REQUIRE(max_pairs >= 0 && pair_stride >= max_pairs);
   if (max_pairs == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && dist && pair_ij && n_pairs_dev && u && ddot);
   hipLaunchKernelGGL(pair_ddot_kernel, dim3(mlcg_persistent_groups(mlcg_div_up(max_pairs, 256), 8)),
                      dim3(256), 0, mlcg_stream(stream), pos, dist, pair_ij,
-                     pair_ij + pair_stride, n_pairs_dev, max_pairs, u, ddot);
+                     pair_ij + pair_stride, n_pairs_dev, max_pairs, u, scale, ddot);
   return mlcg_launch_status();
 }
 

@@ -795,6 +795,7 @@ __global__ __launch_bounds__(kTypeThreads) void type_sum_kernel(const float* __r
                                                                  int64_t rows, int T,
                                                                  float* __restrict__ out,
                                                                  int* __restrict__ bad,
+                                                                 unsigned* __restrict__ flags,
                                                                  float* __restrict__ partial) {
   __shared__ int list[kTypeChunk];  // the chunk's matches in ascending row order
   __shared__ int cnt[kTypeWaves];
@@ -818,8 +819,14 @@ __global__ __launch_bounds__(kTypeThreads) void type_sum_kernel(const float* __r
     int n = 0;
 #pragma unroll
     for (int i = 0; i < kTypeSteps; ++i) {
-      // an out-of-table type is flagged (by workgroup 0) and summed nowhere
-      if (t == 0 && base + MLCG_WAVE * i + l < rows && (tt[i] < 0 || tt[i] >= T)) bad[0] = 1;
+      // an out-of-table type is flagged (by workgroup 0: in bad, or without
+      // one in bit 2 of the numerics flags) and summed nowhere
+      if (t == 0 && base + MLCG_WAVE * i + l < rows && (tt[i] < 0 || tt[i] >= T)) {
+        if (bad)
+          bad[0] = 1;
+        else
+          atomicOr(flags, kFlagTypeRange);
+      }
       n += __popcll(__ballot(tt[i] == t));
     }
     if (l == 0) cnt[w] = n;
@@ -1115,10 +1122,12 @@ extern "C" int mlcg_embedding_gather(const float* table, int num_types, int feat
   MLCG_REQUIRE(table && types && out);
   MLCG_REQUIRE(reinterpret_cast<uintptr_t>(table) % 16 == 0 &&
                reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  unsigned* const flags = mlcg_numerics_word_ptr();
+  if (flags == nullptr) return MLCG_ERR_LAUNCH;  // the flag word's address is unknown
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n * (kF / 4), 256), 16);
   hipLaunchKernelGGL(embedding_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
                      reinterpret_cast<const float4*>(table), num_types, types, n,
-                     reinterpret_cast<float4*>(out), mlcg_numerics_word_ptr());
+                     reinterpret_cast<float4*>(out), flags);
   return mlcg_launch_status();
 }
 
@@ -1133,13 +1142,16 @@ extern "C" int mlcg_type_sum(const float* x, const int64_t* types, int64_t rows,
                              int64_t workspace_floats, void* stream) {
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   if (num_types > kTypeMax) return MLCG_ERR_UNSUPPORTED;
-  MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out && bad);
+  MLCG_REQUIRE(rows >= 0 && num_types >= 1 && out);
   MLCG_REQUIRE(rows == 0 || (x && types));
   const int G = type_groups(rows, num_types);
   const int64_t need = G == 1 ? 0 : (int64_t)2 * G * num_types * kF;
   MLCG_REQUIRE(workspace_floats >= need && (need == 0 || workspace));
+  unsigned* const flags = bad ? nullptr : mlcg_numerics_word_ptr();
+  if (bad == nullptr && flags == nullptr) return MLCG_ERR_LAUNCH;
   hipLaunchKernelGGL(type_sum_kernel, dim3((unsigned)num_types, (unsigned)G), dim3(kTypeThreads),
-                     0, mlcg_stream(stream), x, types, rows, num_types, out, bad, workspace);
+                     0, mlcg_stream(stream), x, types, rows, num_types, out, bad, flags,
+                     workspace);
   if (G > 1)
     hipLaunchKernelGGL(type_sum_combine_kernel, dim3((unsigned)num_types), dim3(kF), 0,
                        mlcg_stream(stream), workspace, G, num_types, out);

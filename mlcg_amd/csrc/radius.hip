@@ -563,12 +563,17 @@ __device__ __forceinline__ void emit_row_fast(uint64_t w, int nch, int st, int i
       *(int64_t*)(b1 + r * 8u) = (int64_t)j;
       if (kPairs) {
         *(int32_t*)(bc + r * 4u) = (int32_t)j;
+        // lower edges get pair 0 here and their pair from pair_reverse_kernel
+        // afterwards, so every edge of the CSR holds a valid pair id even
+        // when its pair fell past the pair capacity
+        int32_t pid = 0;
         if (__builtin_amdgcn_inverse_ballot_w64(um)) {
           const uint32_t rp = p + (uint32_t)lanes_below(um);
           *(int32_t*)(bpi + rp * 4u) = i;
           *(int32_t*)(bpj + rp * 4u) = (int32_t)j;
-          *(int32_t*)(be + r * 4u) = (int32_t)(p_base + rp);
+          pid = (int32_t)(p_base + rp);
         }
+        *(int32_t*)(be + r * 4u) = pid;
       }
     }
     e += (uint32_t)__popcll(m);
@@ -599,7 +604,10 @@ __device__ __forceinline__ void emit_chunk(uint64_t m, int jb, int i, int mnn, i
     if (e >= 0 && e < e_cap) {
       ei0[e] = i;
       ei1[e] = j;
-      if (kPairs) col[e] = j;
+      if (kPairs) {
+        col[e] = j;
+        eid2pair[e] = 0;  // a valid id until the edge's own pair is known
+      }
     } else {
       dropped = true;
     }

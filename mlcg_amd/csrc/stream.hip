@@ -55,7 +55,61 @@ __global__ __launch_bounds__(kStreamThreads) void stream_copy_kernel(
   for (; i < n4; i += G) dst[i] = src[i];
 }
 
+// One launch for a batch of device-to-device copies (a training batch's
+// tensors into the inputs of a recorded step): the jobs' 16-byte units are
+// numbered consecutively and a grid-stride loop copies them; the last unit of
+// a job whose size is not a multiple of 16 is copied byte by byte.
+constexpr int kCopyJobs = 8;
+struct CopyBatch {
+  const char* src[kCopyJobs];
+  char* dst[kCopyJobs];
+  int64_t bytes[kCopyJobs];
+  int64_t first[kCopyJobs + 1];  // first unit of each job; first[count] = total
+  int count;
+};
+
+__global__ __launch_bounds__(kStreamThreads) void copy_batch_kernel(CopyBatch b) {
+  const int64_t G = (int64_t)gridDim.x * kStreamThreads;
+  const int64_t total = b.first[b.count];
+  int k = 0;
+  for (int64_t u = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x; u < total; u += G) {
+    while (u >= b.first[k + 1]) ++k;  // units only grow along a thread's loop
+    const int64_t off = (u - b.first[k]) * 16;
+    const int64_t rem = b.bytes[k] - off;
+    if (rem >= 16) {
+      *reinterpret_cast<float4*>(b.dst[k] + off) =
+          *reinterpret_cast<const float4*>(b.src[k] + off);
+    } else {
+      for (int64_t c = 0; c < rem; ++c) b.dst[k][off + c] = b.src[k][off + c];
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int mlcg_copy_batch(const void* const* srcs, void* const* dsts, const int64_t* bytes,
+                               int count, void* stream) {
+  MLCG_REQUIRE(count >= 0 && srcs && dsts && bytes);
+  if (count > kCopyJobs) return MLCG_ERR_UNSUPPORTED;
+  CopyBatch b{};
+  b.count = count;
+  b.first[0] = 0;
+  for (int k = 0; k < count; ++k) {
+    MLCG_REQUIRE(bytes[k] >= 0 && (bytes[k] == 0 || (srcs[k] && dsts[k])));
+    MLCG_REQUIRE(reinterpret_cast<uintptr_t>(srcs[k]) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(dsts[k]) % 16 == 0);
+    b.src[k] = static_cast<const char*>(srcs[k]);
+    b.dst[k] = static_cast<char*>(dsts[k]);
+    b.bytes[k] = bytes[k];
+    b.first[k + 1] = b.first[k] + (bytes[k] + 15) / 16;
+  }
+  const int64_t total = b.first[count];
+  if (total == 0) return MLCG_OK;
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(total, kStreamThreads), 8);
+  hipLaunchKernelGGL(copy_batch_kernel, dim3(groups), dim3(kStreamThreads), 0,
+                     mlcg_stream(stream), b);
+  return mlcg_launch_status();
+}
 
 extern "C" int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
                                 float* partial, void* stream) {

@@ -282,12 +282,14 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     kernel also forms the adjoint a following reverse1(seed=rev_seed) starts
     from."""
     st = State(pos=pos, types=types, graph=graph, filt=filter_spec(spec, P))
-    ahead = _filters_ahead(spec, P, pos, graph, st.filt)
+    # the lookup goes first: the side stream's filter forwards then start
+    # with the first block's node products already queued behind it
     if (P.emb.dim() == 2 and P.emb.shape[1] == ops.NUM_FILTERS
             and P.emb.dtype == torch.float32 and types.dtype == torch.int64):
         x = ops.embedding_gather(P.emb.detach(), types)
     else:
         x = P.emb.index_select(0, types)
+    ahead = _filters_ahead(spec, P, pos, graph, st.filt)
     for k, bp in enumerate(P.blocks):
         if k in ahead:
             W, Wd, done = ahead[k]
@@ -363,8 +365,10 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
             zbar = hbar * d1
             hbar = zbar.mm(P.out_w[k])
         xbar = hbar
-    dbar = torch.zeros(graph.pair_capacity, dtype=torch.float32, device=st.pos.device)
     nb = len(P.blocks)
+    # the last block's gather stores dbar, the others add to it
+    dbar = (torch.empty if nb else torch.zeros)(graph.pair_capacity, dtype=torch.float32,
+                                                 device=st.pos.device)
     st.xbar_out = [None] * nb
     st.sbar1 = [None] * nb
     st.zbar1 = [None] * nb
@@ -374,7 +378,8 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
         bp = P.blocks[k]
         sbar, zbar, gagg = _lin_dact_lin(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True,
                                          bp.A2)
-        ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar)
+        ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar,
+                                     accumulate=(k != nb - 1))
         st.xbar_out[k] = xbar
         st.sbar1[k] = sbar
         st.zbar1[k] = zbar
@@ -386,12 +391,13 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     return ops.pair_forces(st.pos, st.dist, dbar, graph)
 
 
-def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor) -> None:
-    """Forward-mode sweep along position direction u.  The output network's
-    tangent odot lands in st.odot here, or -- with the fused output network
-    -- in the following reverse2(want_odot=True)."""
+def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor,
+            scale: float = 1.0) -> None:
+    """Forward-mode sweep along position direction scale * u.  The output
+    network's tangent odot lands in st.odot here, or -- with the fused output
+    network -- in the following reverse2(want_odot=True)."""
     graph = st.graph
-    st.ddot = ops.pair_ddot(st.pos, st.dist, graph, u)
+    st.ddot = ops.pair_ddot(st.pos, st.dist, graph, u, scale)
     xdot = None
     st.xdot_in, st.ydot, st.aggdot, st.zdot, st.sdot = [], [], [], [], []
     for k, bp in enumerate(P.blocks):
@@ -583,7 +589,8 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
                                          out=g_basis)
         g_blocks[k] = [gW1, gb1, gW2, gA1, gA2, gc2, gA3, gc3]
     if P.emb.shape[0] <= 128 and P.emb.shape[1] == 128 and st.types.dtype == torch.int64:
-        g_emb = ops.type_sum(xbar2, st.types, P.emb.shape[0])[0]  # fixed summation order
+        # fixed summation order; an out-of-table type raises a numerics flag
+        g_emb = ops.type_sum(xbar2, st.types, P.emb.shape[0], want_bad=False)[0]
     else:
         g_emb = torch.zeros_like(P.emb).index_add_(0, st.types, xbar2)
     side.join()
@@ -603,6 +610,25 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     return out
 
 
+_ONES: dict = {}
+
+
+def _ones(n: int, device: torch.device) -> torch.Tensor:
+    """A read-only float32 vector of n ones on device, made once per stream
+    (outside any stream capture, and filled on the stream that first uses it)
+    and then shared: the unit node seeds of the force path."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, n, torch.cuda.current_stream(device).cuda_stream)
+    t = _ONES.get(key)
+    if t is None:
+        t = torch.ones(n, dtype=torch.float32, device=device)
+        if not torch.cuda.is_current_stream_capturing():
+            # one made inside a capture holds its ones only once the graph
+            # has been replayed, so it is not kept for eager callers
+            _ONES[key] = t
+    return t
+
+
 def node_seed(frame_weights: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
     return frame_weights.to(torch.float32).index_select(0, batch).contiguous()
 
@@ -620,7 +646,7 @@ class EnergyForces(torch.autograd.Function):
     @staticmethod
     def forward(ctx, spec, pos, types, batch, graph, training, *flat):
         P = Params.unflat(spec, list(flat))
-        ones = torch.ones(pos.shape[0], dtype=torch.float32, device=pos.device)
+        ones = _ones(pos.shape[0], pos.device)
         E, st = forward(spec, P, pos, types, graph, save=True, rev_seed=ones)
         F = reverse1(spec, P, st, ones)
         if training:
@@ -638,8 +664,8 @@ class EnergyForces(torch.autograd.Function):
         tw = pw = None
         if Fbar is not None:
             # <Fbar, F> = <Fbar, -grad sum E> : tangent along u = -Fbar, seed 1
-            tangent(spec, P, st, -Fbar)
-            tw = torch.ones(st.pos.shape[0], dtype=torch.float32, device=st.pos.device)
+            tangent(spec, P, st, Fbar, scale=-1.0)
+            tw = _ones(st.pos.shape[0], st.pos.device)
         if Ebar is not None:
             pw = node_seed(Ebar, batch)
         if tw is None and pw is None:

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -180,14 +180,43 @@ def _check_radius_flags(overflow: int) -> None:
 _RADIUS_WS: dict = {}
 
 
+# Workspaces zero-filled ahead of a stream capture (reserve_radius_workspaces),
+# per device, handed to the radius-graph calls made inside it.
+_CAPTURE_WS: dict = {}
+
+
+def reserve_radius_workspaces(n: int, dev: torch.device, count: int) -> List[torch.Tensor]:
+    """Zero-filled look-back workspaces for `count` radius-graph calls over n
+    rows made inside the stream capture that follows on dev: those calls take
+    them (in order) instead of recording a zero fill that every replay of the
+    graph would run.  The caller keeps the list alive as long as the graph,
+    zeroes them again after a look-back timeout (flag 8), and ends the
+    reservation with release_radius_workspaces(dev) after the capture."""
+    words = max(1, _lib.load().mlcg_radius_workspace_bytes(n) // 8)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = [torch.zeros(words, dtype=torch.int64, device=dev) for _ in range(count)]
+    _CAPTURE_WS[index] = list(ws)
+    return ws
+
+
+def release_radius_workspaces(dev: torch.device) -> None:
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    _CAPTURE_WS.pop(index, None)
+
+
 def _radius_workspace(n: int, dev: torch.device) -> Tuple[torch.Tensor, Optional[tuple]]:
     """The workspace for n rows on the current stream, and its cache key
     (None for a fresh one).  Inside a stream capture the graph gets a
-    zero-filled workspace of its own (its replays may run on any stream)."""
+    workspace of its own (its replays may run on any stream): a reserved one
+    (reserve_radius_workspaces) or a zero-filled one."""
     words = max(1, _lib.load().mlcg_radius_workspace_bytes(n) // 8)
-    if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(words, dtype=torch.int64, device=dev), None
     index = dev.index if dev.index is not None else torch.cuda.current_device()
+    if torch.cuda.is_current_stream_capturing():
+        pool = _CAPTURE_WS.get(index, [])
+        for i, ws in enumerate(pool):
+            if ws.numel() >= words:
+                return pool.pop(i), None
+        return torch.zeros(words, dtype=torch.int64, device=dev), None
     key = (index, torch.cuda.current_stream(dev).cuda_stream)
     ws = _RADIUS_WS.get(key)
     if ws is None or ws.numel() < words:
@@ -304,8 +333,7 @@ def radius_graph(
     if with_pairs:
         col = torch.empty(e_cap, dtype=torch.int32, device=dev)
         pair_ij = torch.empty(2, p_cap, dtype=torch.int32, device=dev)
-        eid2pair = (torch.empty if capacity is None else torch.zeros)(
-            e_cap, dtype=torch.int32, device=dev)
+        eid2pair = torch.empty(e_cap, dtype=torch.int32, device=dev)
     if capacity is None:
         if f64:
             call("mlcg_radius_fill_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
@@ -537,6 +565,34 @@ def node_tmm_batch(problems, rows: int, device) -> list:
     return outs
 
 
+COPY_BATCH_MAX = 8  # jobs per mlcg_copy_batch launch
+
+
+def copy_batch(dsts, srcs) -> None:
+    """dst.copy_(src) for every pair, device to device on the current stream,
+    as one launch per eight pairs (mlcg_copy_batch).  Each pair: the same
+    device, dtype and shape, both contiguous and 16-byte aligned, not
+    overlapping; other pairs raise."""
+    _check(len(dsts) == len(srcs), "copy_batch takes as many destinations as sources")
+    if not dsts:
+        return
+    dev = dsts[0].device
+    for d, s_ in zip(dsts, srcs):
+        _check(d.is_cuda and s_.device == d.device == dev and d.dtype == s_.dtype
+               and d.shape == s_.shape and d.is_contiguous() and s_.is_contiguous()
+               and d.data_ptr() % 16 == 0 and s_.data_ptr() % 16 == 0,
+               lambda: f"copy_batch: {tuple(s_.shape)} {s_.dtype} on {s_.device} -> "
+                       f"{tuple(d.shape)} {d.dtype} on {d.device} needs one device, dtype "
+                       "and shape, contiguous 16-byte aligned tensors")
+    for k in range(0, len(dsts), COPY_BATCH_MAX):
+        dd, ss = dsts[k:k + COPY_BATCH_MAX], srcs[k:k + COPY_BATCH_MAX]
+        n = len(dd)
+        src_arr = (ctypes.c_void_p * n)(*[t.data_ptr() for t in ss])
+        dst_arr = (ctypes.c_void_p * n)(*[t.data_ptr() for t in dd])
+        nbytes = (ctypes.c_int64 * n)(*[t.numel() * t.element_size() for t in dd])
+        call("mlcg_copy_batch", src_arr, dst_arr, nbytes, n, stream_handle(dev))
+
+
 def embedding_gather(table: torch.Tensor, types: torch.Tensor) -> torch.Tensor:
     """table[types] for a [T, 128] fp32 table and int64 types (the embedding
     lookup, mlcg_embedding_gather); a type outside [0, T) gives a zero row and
@@ -553,11 +609,13 @@ def embedding_gather(table: torch.Tensor, types: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
-             ) -> Tuple[torch.Tensor, torch.Tensor]:
+def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int, want_bad: bool = True
+             ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """(out [num_types, 128], bad [1] int32): out[t] = sum of the rows of x
     whose type is t (the embedding-table gradient), summed in a fixed order
-    (mlcg_type_sum); bad[0] = 1 when a type lies outside [0, num_types)."""
+    (mlcg_type_sum); bad[0] = 1 when a type lies outside [0, num_types).
+    With want_bad=False bad is None and such a type raises bit 2 of the
+    numerics flags instead (check_numerics reports it)."""
     require_device(x, types)
     _check(x.dim() == 2 and x.shape[1] == NUM_FILTERS and x.dtype == torch.float32,
            f"type_sum takes [N, {NUM_FILTERS}] float32 rows")
@@ -566,7 +624,7 @@ def type_sum(x: torch.Tensor, types: torch.Tensor, num_types: int
     _check(1 <= num_types <= 128, "type_sum supports 1..128 types")
     x, types = x.contiguous(), types.contiguous()
     out = torch.empty(num_types, NUM_FILTERS, dtype=torch.float32, device=x.device)
-    bad = torch.zeros(1, dtype=torch.int32, device=x.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=x.device) if want_bad else None
     nws = int(_lib.load().mlcg_type_sum_workspace_floats(x.shape[0], num_types))
     ws = torch.empty(nws, dtype=torch.float32, device=x.device) if nws > 0 else None
     call("mlcg_type_sum", ptr(x), ptr(types), x.shape[0], NUM_FILTERS, num_types, ptr(out),
@@ -870,14 +928,16 @@ def cfconv_gather(src: torch.Tensor, W: torch.Tensor, graph: PairGraph) -> torch
 
 
 def cfconv_gather_bwd(gagg: torch.Tensor, y: torch.Tensor, W: torch.Tensor, Wd: torch.Tensor,
-                      graph: PairGraph, dbar: torch.Tensor) -> torch.Tensor:
-    """ybar = gather(gagg, W); dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i> (in place)."""
+                      graph: PairGraph, dbar: torch.Tensor, accumulate: bool = True
+                      ) -> torch.Tensor:
+    """ybar = gather(gagg, W); dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i> in
+    place (dbar[p] = ... with accumulate=False: dbar may be uninitialised)."""
     gagg = gagg.contiguous()
     ybar = torch.empty_like(gagg)
     wp, wf16 = _wptr(W)
     call("mlcg_cfconv_gather_bwd", ptr(gagg), ptr(y.contiguous()), wp, ptr(Wd), wf16,
          ptr(graph.rowptr), ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes,
-         gagg.shape[1], ptr(ybar), ptr(dbar), stream_handle(gagg.device))
+         gagg.shape[1], ptr(ybar), ptr(dbar), int(accumulate), stream_handle(gagg.device))
     return ybar
 
 
@@ -913,11 +973,12 @@ def cfconv_gather_rev2(gagg2: torch.Tensor, gagg1: Optional[torch.Tensor], y: to
 
 
 def pair_ddot(pos: torch.Tensor, dist: torch.Tensor, graph: PairGraph,
-              u: torch.Tensor) -> torch.Tensor:
+              u: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """ddot[p] = scale * rhat_p . (u[j] - u[i]) over the graph's pairs."""
     cap = graph.pair_capacity
     ddot = torch.empty(cap, dtype=torch.float32, device=pos.device)
     call("mlcg_pair_ddot", ptr(pos), ptr(dist), ptr(graph.pair_ij), cap,
-         ptr(graph.n_pairs_dev), cap, ptr(u.contiguous()), ptr(ddot),
+         ptr(graph.n_pairs_dev), cap, ptr(u.contiguous()), float(scale), ptr(ddot),
          stream_handle(pos.device))
     return ddot
 

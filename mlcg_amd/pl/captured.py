@@ -28,6 +28,7 @@ from typing import Callable, List, Optional
 
 import torch
 
+from .. import ops
 
 def _schnets(module: torch.nn.Module):
     from ..nn.schnet import SchNet
@@ -91,15 +92,23 @@ class CapturedTrainStep:
             for _ in range(max(int(warmup), 1)):
                 recorded(data)
         torch.cuda.current_stream(dev).wait_stream(self._side)
+        # the graph's radius-graph workspaces, zero-filled here once rather
+        # than by a fill recorded into (and rerun by) every replay
+        self._radius_ws = ops.reserve_radius_workspaces(data.pos.shape[0], dev,
+                                                        len(self.schnets))
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=self._side):
-            self.loss = recorded(data)
+        try:
+            with torch.cuda.graph(self.graph, stream=self._side):
+                self.loss = recorded(data)
+        finally:
+            ops.release_radius_workspaces(dev)
         torch.cuda.synchronize(dev)
 
     def load(self, batch) -> None:
         """Copy batch's tensors into the recorded inputs (same keys, shapes
-        and dtypes), on the current stream, as one multi-tensor copy."""
+        and dtypes), on the current stream, in one launch (ops.copy_batch)
+        when they are resident on the recorded device."""
         dsts, srcs = [], []
         for k in self.fields:
             src = batch[k] if k in batch else None
@@ -110,10 +119,17 @@ class CapturedTrainStep:
                     f"({tuple(dst.shape)}, {dst.dtype}); got "
                     f"{None if src is None else (tuple(src.shape), src.dtype)}")
             if src.data_ptr() != dst.data_ptr():
-                dsts.append(dst)
-                srcs.append(src if src.device == dst.device else src.to(dst.device))
+                if src.device != dst.device:  # host batches: one upload each
+                    src = src.to(dst.device, non_blocking=True)
+                src = src.contiguous()
+                if (dst.is_contiguous() and dst.data_ptr() % 16 == 0
+                        and src.data_ptr() % 16 == 0):
+                    dsts.append(dst)
+                    srcs.append(src)
+                else:  # a strided or unaligned recorded input
+                    dst.copy_(src, non_blocking=True)
         if dsts:
-            torch._foreach_copy_(dsts, srcs, non_blocking=True)
+            ops.copy_batch(dsts, srcs)
 
     def step(self, batch=None) -> torch.Tensor:
         """One training step on batch (default: the recorded inputs as they
@@ -129,13 +145,14 @@ class CapturedTrainStep:
         split-fp16 filter kernel met a value past its range
         (ops.check_numerics); one host synchronisation, the flags are cleared
         afterwards."""
-        from .. import ops
-
         ops.check_numerics(self.data.pos.device)
         flags = int(self.sticky.item())
         if flags:
             self.sticky.zero_()
             ops.radius_flags_read(flags)
+            if flags & 8:  # a look-back timed out: the graph's workspaces restart
+                for ws in self._radius_ws:
+                    ws.zero_()
             msg = ops.radius_flags_message(flags, [m.graph_capacity for m in self.schnets])
             hint = ("rebuild the CapturedTrainStep with a larger capacity_factor or "
                     "max_num_neighbors" if flags & 3 else

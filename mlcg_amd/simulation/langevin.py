@@ -239,6 +239,9 @@ class LangevinSimulation:
         v = int(sticky.item())
         if v:
             ops.radius_flags_read(v)
+            if v & 8:  # a look-back timed out: the captured step's workspaces restart
+                for ws in getattr(self, "_radius_ws", []):
+                    ws.zero_()
             hint = ("raise edge_capacity_factor or max_num_neighbors" if v & 3
                     else "an internal failure of the radius kernel")
             raise RuntimeError(
@@ -313,8 +316,16 @@ class LangevinSimulation:
                     torch.cuda.synchronize()
                     self._check_flags(sticky)
                     graph = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(graph):
-                        one_step()
+                    # the step's radius-graph workspaces, zero-filled once
+                    # here rather than by a fill every replay would rerun
+                    self._radius_ws = ops.reserve_radius_workspaces(
+                        x.shape[0], x.device, len(self._graph_flags()) or 1)
+                    torch.cuda.synchronize()
+                    try:
+                        with torch.cuda.graph(graph):
+                            one_step()
+                    finally:
+                        ops.release_radius_workspaces(x.device)
                     graph.replay()  # the captured step is step t
                 elif graph is not None:
                     graph.replay()

@@ -277,11 +277,47 @@ def test_type_sum_flags_out_of_table_types():
 
     x = torch.ones(10, 128, device="cuda")
     types = torch.tensor([0, 1, 2, 3, 9, 1, 1, 0, 2, 3], device="cuda")
+    ops.numerics_flags(clear=True)
     out, bad = ops.type_sum(x, types, 4)
     assert int(bad.item()) == 1
     assert out[:, 0].tolist() == [2.0, 3.0, 2.0, 2.0]  # the type-9 row is skipped
+    ops.check_numerics()  # reported in bad, not in the flags
+    out2, none = ops.type_sum(x, types, 4, want_bad=False)
+    assert none is None and torch.equal(out2, out)
+    with pytest.raises(RuntimeError, match="embedding table"):
+        ops.check_numerics()
+    assert ops.type_sum(x, types.clamp(max=3), 4, want_bad=False)[1] is None
+    ops.check_numerics()
     with pytest.raises(RuntimeError):
         ops.type_sum(x, types, 129)
+
+
+def test_copy_batch():
+    """One launch copies up to eight tensors (sizes not a multiple of 16
+    bytes included); more pairs take one launch per eight; mismatched pairs
+    raise before anything is launched."""
+    from mlcg_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(8)
+    srcs = [torch.randn(17920, 3, device="cuda", generator=g),
+            torch.randint(0, 9, (17920,), device="cuda", generator=g),
+            torch.randint(0, 9, (3,), device="cuda", generator=g),
+            torch.randn(5, device="cuda", generator=g),
+            torch.empty(0, device="cuda"),
+            torch.randint(0, 2 ** 30, (7, 5), dtype=torch.int32, device="cuda", generator=g),
+            torch.randn(1000, 128, device="cuda", generator=g).half(),
+            torch.randn(1, device="cuda", generator=g).double(),
+            torch.randn(33, 3, device="cuda", generator=g),
+            torch.randn(2, device="cuda", generator=g)]
+    for n in (1, 8, 10):
+        dsts = [torch.full_like(t, 7) for t in srcs[:n]]
+        ops.copy_batch(dsts, srcs[:n])
+        for d, t in zip(dsts, srcs[:n]):
+            assert torch.equal(d, t)
+    with pytest.raises(RuntimeError, match="copy_batch"):
+        ops.copy_batch([torch.empty(4, device="cuda")], [torch.empty(5, device="cuda")])
+    with pytest.raises(RuntimeError, match="copy_batch"):
+        ops.copy_batch([torch.empty(8, device="cuda")[1:5]], [torch.empty(4, device="cuda")])
 
 
 @pytest.mark.parametrize("rows", [1, 33, 17920, 128000])
