@@ -15,8 +15,9 @@ Metric: CFConv edges/s := E_directed * n_blocks / t_step (forward + force +
 double backward of every block per step), with the inputs resident in HBM.
 The headline step runs through mlcg_amd.pl.CapturedTrainStep: the whole step
 recorded once as a HIP graph, each timed step loading its batch into the
-recorded inputs (one multi-tensor device copy) and replaying the graph, so
-the figure does not depend on how fast the host issues ~140 launches.  The
+recorded inputs (one batched device copy, mlcg_copy_batch) and replaying the
+graph, so the figure does not depend on how fast the host issues ~140
+launches.  The
 same step issued eagerly from Python is timed beside it (`eager_step`, with
 the host's issue time per step and the device time of a step queued ahead).
 
@@ -83,6 +84,9 @@ def parse_args(argv=None):
                    help="run only the requested probes (no config legs)")
     p.add_argument("--no-capture", action="store_true",
                    help="skip the captured (HIP graph) config-2 step")
+    p.add_argument("--captured-only", action="store_true",
+                   help="run only the captured config-2 step (for kernel traces of the "
+                        "graph replays)")
     p.add_argument("--md-steps", type=int, default=200, help="MD steps of the config-5 leg")
     p.add_argument("--cpu-frames", type=int, default=32,
                    help="frames in the CPU baseline sample")
@@ -1004,6 +1008,13 @@ def main(argv=None):
             res["gather_ceiling"] = gather_ceiling_leg()
         print(json.dumps(res))
         return 0
+    if args.captured_only:
+        model, _, _, data = _config2(args)
+        E = model.build_graph(data).num_edges
+        del model, data
+        cg = captured_leg(args, E)
+        print(json.dumps({"captured_step": cg, "E": E}))
+        return 0
     sp = stream_leg() if args.stream_probe else None
     if sp:
         print("[bench] stream probe " + json.dumps(sp), flush=True)
@@ -1041,7 +1052,7 @@ def main(argv=None):
         print("[bench] cpu baselines of configs 1, 3, 4, 5 " + json.dumps(cpu_cfg), flush=True)
 
     # the headline: the training step through mlcg_amd.pl.CapturedTrainStep
-    # (one graph launch per step, its batch loaded by one multi-tensor copy),
+    # (one graph launch per step, its batch loaded by one mlcg_copy_batch),
     # whose time does not depend on the host's speed; the eager step (the same
     # kernels launched one by one from Python) is reported beside it
     eager_ms = g["ms_per_step"]

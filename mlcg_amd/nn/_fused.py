@@ -488,9 +488,13 @@ def reverse2(spec: FusedSpec, P: Params, st: State, tw: Optional[torch.Tensor],
 
 
 _SIDE_STREAMS = {}
-# Weight-gradient reductions of reverse2 on the side stream (False runs them
-# in order on the caller's stream; results are the same bit for bit).
-_TMM_SIDE = True
+# Weight-gradient reductions of reverse2 on the side stream (False, the
+# default, runs them in order on the caller's stream; results are the same bit
+# for bit).  Measured on config 2: in order, the eager step's device time is
+# 1 % lower (2.351 against 2.376 ms) and the captured step's 0.6 % higher
+# (2.353 against 2.338 ms), and no kernel shares the GPU with another stream's
+# work while the backward runs, so per-launch times are the kernels' own.
+_TMM_SIDE = os.environ.get("MLCG_TMM_SIDE", "0") == "1"
 
 
 class _SideStream:
