@@ -445,7 +445,7 @@ int mlcg_node_gemm(const float* x, int64_t rows, int features, const float* W,
                    int transpose_w, const float* bias, const float* residual,
                    int epilogue, int act, const float* z, const float* s,
                    const float* e, const float* f, float* out0, float* out1,
-                   void* stream);
+                   const void* w_image, void* stream);
 
 /* Two consecutive linears of the interaction block in one pass over the
  * rows: mlcg_node_gemm(x, W, ..., epilogue) as above (ACT, DACT or DACT2),
@@ -461,7 +461,25 @@ int mlcg_node_gemm2(const float* x, int64_t rows, int features, const float* W,
                     int epilogue, int act, const float* z, const float* s,
                     const float* e, const float* f, float* out0, float* out1,
                     const float* W2, const float* bias2, const float* residual2,
-                    float* out2, void* stream);
+                    float* out2, const void* w_image, const void* w2_image,
+                    void* stream);
+
+/* The split operand image of a [128, 128] node weight W for mlcg_node_gemm
+ * and mlcg_node_gemm2 (their w_image / w2_image arguments): the fp16 hi and
+ * lo planes of W^T (transpose_w = 0) or W (transpose_w != 0) in the order
+ * the kernels' MFMA fragments read them, mlcg_node_weight_image_bytes() =
+ * 65,536 bytes per weight.  Without an image every launch splits W itself
+ * (each workgroup, before its first row tile); with one, the launch reads the
+ * image instead and its results are the same bit for bit.  An image holds W
+ * as it was when the image was made: make the images again after every
+ * change of the weights (the fused SchNet makes them at the start of each
+ * forward, in one launch).  count <= 32 images go to images + k * 65,536
+ * (16-byte aligned); the weights and flags are host arrays read during the
+ * call.  No counterpart in the reference (its Linear layers keep fp32
+ * weights for the library GEMM). */
+int64_t mlcg_node_weight_image_bytes(void);
+int mlcg_node_weight_images(const float* const* weights, const int* transpose_w,
+                            int count, void* images, void* stream);
 
 /* out [128, 128] (+)= a1^T b1 (+ a2^T b2) for [rows, 128] inputs (a2/b2 may
  * be NULL) and, when colsum_a1 is non-NULL, colsum_a1 [128] (+)= the column

@@ -76,9 +76,11 @@ _SIGNATURES = {
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
     "mlcg_node_gemm": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
-                       _P],
+                       _P, _P],
     "mlcg_node_gemm2": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
-                        _P, _P, _P, _P, _P],
+                        _P, _P, _P, _P, _P, _P, _P],
+    "mlcg_node_weight_image_bytes": [],
+    "mlcg_node_weight_images": [_P, _P, _I32, _P, _P],
     "mlcg_out_forward": [_P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P,
                          _P],
     "mlcg_out_rev2_workspace_floats": [_I64, _I32],
@@ -110,7 +112,7 @@ _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_node_tmm_batch_workspace_floats": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,
-             "mlcg_type_sum_workspace_floats": _I64}
+             "mlcg_type_sum_workspace_floats": _I64, "mlcg_node_weight_image_bytes": _I64}
 
 STATUS = {
     0: "MLCG_OK",

@@ -464,6 +464,30 @@ __device__ __forceinline__ float4 gemm_epilogue(float4 y, int64_t r, int col, co
 constexpr int kWImg = 4 * 2 * (kF / 32) * MLCG_WAVE;  // halfx8 entries per plane
 constexpr int kWImgBytes = 2 * kWImg * 16;             // 64 KiB
 
+// The eight weights of image entry e (see above), from W as stored.
+__device__ __forceinline__ void gemm_w_entry(float (&wv)[8], const float* __restrict__ W,
+                                             bool xw, int e) {
+  const int l = e & 63, kb = (e >> 6) & 3, c = (e >> 8) & 1, cw = e >> 9;
+  const int q = l >> 4, col = 32 * cw + 16 * c + (l & 15);
+  if (xw) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[j] = W[(32 * kb + 8 * q + j) * kF + col];
+  } else {  // the eight k of an entry are contiguous in row `col` of W
+    const float4 v0 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q);
+    const float4 v1 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q + 4);
+    wv[0] = v0.x; wv[1] = v0.y; wv[2] = v0.z; wv[3] = v0.w;
+    wv[4] = v1.x; wv[5] = v1.y; wv[6] = v1.z; wv[7] = v1.w;
+  }
+}
+__device__ __forceinline__ void gemm_w_split(const float (&wv)[8], halfx8& h, halfx8& lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const f16split sp = split2(wv[j], kNodeS);
+    h[j] = sp.hi;
+    lo[j] = sp.lo;
+  }
+}
+
 template <int kRT, bool kXW>
 __device__ __forceinline__ void gemm_stage_w(halfx8* img, const float* __restrict__ W) {
   constexpr int kT = GemmShape<kRT>::kThreads;
@@ -476,29 +500,14 @@ __device__ __forceinline__ void gemm_stage_w(halfx8* img, const float* __restric
     for (int b = 0; b < kBatch; ++b) {
       const int e = threadIdx.x + (i0 + b) * kT;
       if (i0 + b >= kIt || (kWImg % kT != 0 && e >= kWImg)) break;
-      const int l = e & 63, kb = (e >> 6) & 3, c = (e >> 8) & 1, cw = e >> 9;
-      const int q = l >> 4, col = 32 * cw + 16 * c + (l & 15);
-      if (kXW) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) wv[b][j] = W[(32 * kb + 8 * q + j) * kF + col];
-      } else {  // the eight k of an entry are contiguous in row `col` of W
-        const float4 v0 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q);
-        const float4 v1 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q + 4);
-        wv[b][0] = v0.x; wv[b][1] = v0.y; wv[b][2] = v0.z; wv[b][3] = v0.w;
-        wv[b][4] = v1.x; wv[b][5] = v1.y; wv[b][6] = v1.z; wv[b][7] = v1.w;
-      }
+      gemm_w_entry(wv[b], W, kXW, e);
     }
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       const int e = threadIdx.x + (i0 + b) * kT;
       if (i0 + b >= kIt || (kWImg % kT != 0 && e >= kWImg)) break;
       halfx8 h, lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f16split sp = split2(wv[b][j], kNodeS);
-        h[j] = sp.hi;
-        lo[j] = sp.lo;
-      }
+      gemm_w_split(wv[b], h, lo);
       img[e] = h;
       img[kWImg + e] = lo;
     }
@@ -509,30 +518,15 @@ __device__ __forceinline__ void gemm_stage_w(halfx8* img, const float* __restric
 // node_gemm2, whose second weight leaves no registers for a staged copy).
 template <bool kXW>
 __device__ __forceinline__ void gemm_load_w(halfx8 (&bh)[2][kF / 32], halfx8 (&bl)[2][kF / 32],
-                                            const float* __restrict__ W, int cw, int q, int n) {
+                                            const float* __restrict__ W, int cw, int l) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int col = 32 * cw + 16 * c + n;
+  for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int kb = 0; kb < kF / 32; ++kb) {
       float wv[8];
-      if (kXW) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) wv[j] = W[(32 * kb + 8 * q + j) * kF + col];
-      } else {
-        const float4 v0 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q);
-        const float4 v1 = *reinterpret_cast<const float4*>(W + col * kF + 32 * kb + 8 * q + 4);
-        wv[0] = v0.x; wv[1] = v0.y; wv[2] = v0.z; wv[3] = v0.w;
-        wv[4] = v1.x; wv[5] = v1.y; wv[6] = v1.z; wv[7] = v1.w;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f16split sp = split2(wv[j], kNodeS);
-        bh[c][kb][j] = sp.hi;
-        bl[c][kb][j] = sp.lo;
-      }
+      gemm_w_entry(wv, W, kXW, ((cw * 2 + c) * (kF / 32) + kb) * MLCG_WAVE + l);
+      gemm_w_split(wv, bh[c][kb], bl[c][kb]);
     }
-  }
 }
 
 __device__ __forceinline__ void gemm_read_w(halfx8 (&bh)[2][kF / 32], halfx8 (&bl)[2][kF / 32],
@@ -545,6 +539,28 @@ __device__ __forceinline__ void gemm_read_w(halfx8 (&bh)[2][kF / 32], halfx8 (&b
       bh[c][kb] = img[e];
       bl[c][kb] = img[kWImg + e];
     }
+}
+
+// Split images of several weights in one launch (mlcg_node_weight_images):
+// job blockIdx.y, entries blockIdx.x * 256 + threadIdx.x, the same entries and
+// splits gemm_stage_w makes in LDS.
+constexpr int kWImgJobs = 32;
+struct WImgBatch {
+  const float* W[kWImgJobs];
+  halfx8* img[kWImgJobs];
+  int xw[kWImgJobs];
+};
+
+__global__ __launch_bounds__(256) void node_weight_image_kernel(WImgBatch b) {
+  const int job = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= kWImg) return;
+  float wv[8];
+  gemm_w_entry(wv, b.W[job], b.xw[job] != 0, e);
+  halfx8 h, lo;
+  gemm_w_split(wv, h, lo);
+  b.img[job][e] = h;
+  b.img[job][kWImg + e] = lo;
 }
 
 // The product of a staged tile (three planes in xs, row scales in rinv) and
@@ -589,7 +605,7 @@ __global__ __launch_bounds__(GemmShape<kRT>::kThreads) void node_gemm_kernel(
     const float* __restrict__ bias, const float* __restrict__ residual, int act,
     const float* __restrict__ zin, const float* __restrict__ sin_,
     const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
-    float* __restrict__ out1) {
+    float* __restrict__ out1, const halfx8* __restrict__ wimg) {
   using S = GemmShape<kRT>;
   constexpr int kXs = 2 * 3 * S::kPlane * 2, kRinv = 2 * S::kRows * 4;
   constexpr int kBytes = kXs + kRinv + S::kRows * kTRow * 4;
@@ -611,10 +627,14 @@ __global__ __launch_bounds__(GemmShape<kRT>::kThreads) void node_gemm_kernel(
   float4 pf[kGemmXPer];
   gemm_load_x<kRT>(pf, x, t, rows);
   halfx8 bh[2][kF / 32], bl[2][kF / 32];
-  gemm_stage_w<kRT, kXW>(reinterpret_cast<halfx8*>(smem), W);
-  __syncthreads();
-  gemm_read_w(bh, bl, reinterpret_cast<const halfx8*>(smem), cw, l);
-  __syncthreads();
+  if (wimg != nullptr) {  // uniform: the split image made ahead (mlcg_node_weight_images)
+    gemm_read_w(bh, bl, wimg, cw, l);
+  } else {
+    gemm_stage_w<kRT, kXW>(reinterpret_cast<halfx8*>(smem), W);
+    __syncthreads();
+    gemm_read_w(bh, bl, reinterpret_cast<const halfx8*>(smem), cw, l);
+    __syncthreads();
+  }
   gemm_stage_x3<kRT>(xs0, rinv0, pf);
   __syncthreads();
   int buf = 0;
@@ -668,7 +688,8 @@ void node_gemm2_kernel(
     const float* __restrict__ zin, const float* __restrict__ sin_,
     const float* __restrict__ ein, const float* __restrict__ fin, float* __restrict__ out0,
     float* __restrict__ out1, const float* __restrict__ W2, const float* __restrict__ bias2,
-    const float* __restrict__ residual2, float* __restrict__ out2) {
+    const float* __restrict__ residual2, float* __restrict__ out2,
+    const halfx8* __restrict__ wimg, const halfx8* __restrict__ w2img) {
   using S = GemmShape<kRT>;
   constexpr int kXs = 3 * 3 * S::kPlane * 2, kRinv = 3 * S::kRows * 4;
   __shared__ __align__(16) unsigned char smem[kXs + kRinv + 2 * S::kRows * kTRow * 4];
@@ -689,8 +710,14 @@ void node_gemm2_kernel(
   float4 pf[kGemmXPer];
   gemm_load_x<kRT>(pf, x, t, rows);
   halfx8 bh[2][kF / 32], bl[2][kF / 32], ch[2][kF / 32], cl[2][kF / 32];
-  gemm_load_w<kXW>(bh, bl, W, cw, q, n);
-  gemm_load_w<kXW>(ch, cl, W2, cw, q, n);
+  if (wimg != nullptr)
+    gemm_read_w(bh, bl, wimg, cw, l);
+  else
+    gemm_load_w<kXW>(bh, bl, W, cw, l);
+  if (w2img != nullptr)
+    gemm_read_w(ch, cl, w2img, cw, l);
+  else
+    gemm_load_w<kXW>(ch, cl, W2, cw, l);
   gemm_stage_x3<kRT>(xs0, rinv0, pf);
   __syncthreads();
   int buf = 0;
@@ -932,16 +959,16 @@ template <int MODE>
 void launch_node_gemm(bool xw, hipStream_t s, const float* x, int64_t rows,
                       const float* W, const float* bias, const float* residual, int act,
                       const float* z, const float* sv, const float* e, const float* f,
-                      float* out0, float* out1) {
+                      float* out0, float* out1, const halfx8* wimg) {
   constexpr int kRT = GemmRT<MODE>::value;
   const dim3 grid(mlcg_persistent_groups(gemm_tiles<kRT>(rows), 1));
   const dim3 block(GemmShape<kRT>::kThreads);
   if (xw)
     hipLaunchKernelGGL((node_gemm_kernel<MODE, true, kRT>), grid, block, 0, s, x, rows, W, bias,
-                       residual, act, z, sv, e, f, out0, out1);
+                       residual, act, z, sv, e, f, out0, out1, wimg);
   else
     hipLaunchKernelGGL((node_gemm_kernel<MODE, false, kRT>), grid, block, 0, s, x, rows, W, bias,
-                       residual, act, z, sv, e, f, out0, out1);
+                       residual, act, z, sv, e, f, out0, out1, wimg);
 }
 
 template <int MODE>
@@ -949,16 +976,19 @@ void launch_node_gemm2(bool xw, hipStream_t s, const float* x, int64_t rows,
                        const float* W, const float* bias, const float* residual, int act,
                        const float* z, const float* sv, const float* e, const float* f,
                        float* out0, float* out1, const float* W2, const float* bias2,
-                       const float* residual2, float* out2) {
+                       const float* residual2, float* out2, const halfx8* wimg,
+                       const halfx8* w2img) {
   constexpr int kRT = 1;  // both weights in registers: ~240 VGPRs, two workgroups per CU
   const dim3 grid(mlcg_persistent_groups(gemm_tiles<kRT>(rows), 2));
   const dim3 block(GemmShape<kRT>::kThreads);
   if (xw)
     hipLaunchKernelGGL((node_gemm2_kernel<MODE, true, kRT>), grid, block, 0, s, x, rows, W,
-                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2);
+                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2,
+                       wimg, w2img);
   else
     hipLaunchKernelGGL((node_gemm2_kernel<MODE, false, kRT>), grid, block, 0, s, x, rows, W,
-                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2);
+                       bias, residual, act, z, sv, e, f, out0, out1, W2, bias2, residual2, out2,
+                       wimg, w2img);
 }
 
 // Argument checks shared by mlcg_node_gemm and mlcg_node_gemm2.
@@ -986,28 +1016,30 @@ extern "C" int mlcg_node_gemm(const float* x, int64_t rows, int features, const 
                               int transpose_w, const float* bias, const float* residual,
                               int epilogue, int act, const float* z, const float* s,
                               const float* e, const float* f, float* out0, float* out1,
-                              void* stream) {
+                              const void* w_image, void* stream) {
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
   if (rc != MLCG_OK || rows == 0) return rc;
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(w_image) % 16 == 0);
   hipStream_t st = mlcg_stream(stream);
   const bool xw = transpose_w != 0;
+  const halfx8* wi = static_cast<const halfx8*>(w_image);
   switch (epilogue) {
     case MLCG_NODE_PLAIN:
       launch_node_gemm<MLCG_NODE_PLAIN>(xw, st, x, rows, W, bias, residual, act, z, s, e,
-                                        f, out0, out1);
+                                        f, out0, out1, wi);
       break;
     case MLCG_NODE_ACT:
       launch_node_gemm<MLCG_NODE_ACT>(xw, st, x, rows, W, bias, residual, act, z, s, e, f,
-                                      out0, out1);
+                                      out0, out1, wi);
       break;
     case MLCG_NODE_DACT:
       launch_node_gemm<MLCG_NODE_DACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
-                                       f, out0, out1);
+                                       f, out0, out1, wi);
       break;
     default:
       launch_node_gemm<MLCG_NODE_DACT2>(xw, st, x, rows, W, bias, residual, act, z, s, e,
-                                        f, out0, out1);
+                                        f, out0, out1, wi);
       break;
   }
   return mlcg_launch_status();
@@ -1018,28 +1050,54 @@ extern "C" int mlcg_node_gemm2(const float* x, int64_t rows, int features, const
                                int epilogue, int act, const float* z, const float* s,
                                const float* e, const float* f, float* out0, float* out1,
                                const float* W2, const float* bias2, const float* residual2,
-                               float* out2, void* stream) {
+                               float* out2, const void* w_image, const void* w2_image,
+                               void* stream) {
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(epilogue != MLCG_NODE_PLAIN);
   const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
   if (rc != MLCG_OK || rows == 0) return rc;
   MLCG_REQUIRE(W2 && out2);
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(w_image) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(w2_image) % 16 == 0);
   hipStream_t st = mlcg_stream(stream);
   const bool xw = transpose_w != 0;
+  const halfx8* wi = static_cast<const halfx8*>(w_image);
+  const halfx8* w2i = static_cast<const halfx8*>(w2_image);
   switch (epilogue) {
     case MLCG_NODE_ACT:
       launch_node_gemm2<MLCG_NODE_ACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
-                                       f, out0, out1, W2, bias2, residual2, out2);
+                                       f, out0, out1, W2, bias2, residual2, out2, wi, w2i);
       break;
     case MLCG_NODE_DACT:
       launch_node_gemm2<MLCG_NODE_DACT>(xw, st, x, rows, W, bias, residual, act, z, s, e,
-                                        f, out0, out1, W2, bias2, residual2, out2);
+                                        f, out0, out1, W2, bias2, residual2, out2, wi, w2i);
       break;
     default:
       launch_node_gemm2<MLCG_NODE_DACT2>(xw, st, x, rows, W, bias, residual, act, z, s,
-                                         e, f, out0, out1, W2, bias2, residual2, out2);
+                                         e, f, out0, out1, W2, bias2, residual2, out2, wi,
+                                         w2i);
       break;
   }
+  return mlcg_launch_status();
+}
+
+extern "C" int64_t mlcg_node_weight_image_bytes(void) { return kWImgBytes; }
+
+extern "C" int mlcg_node_weight_images(const float* const* weights, const int* transpose_w,
+                                       int count, void* images, void* stream) {
+  MLCG_REQUIRE(count >= 0 && (count == 0 || (weights && transpose_w && images)));
+  if (count > kWImgJobs) return MLCG_ERR_UNSUPPORTED;
+  if (count == 0) return MLCG_OK;
+  MLCG_REQUIRE(reinterpret_cast<uintptr_t>(images) % 16 == 0);
+  WImgBatch b{};
+  for (int k = 0; k < count; ++k) {
+    MLCG_REQUIRE(weights[k] != nullptr && reinterpret_cast<uintptr_t>(weights[k]) % 16 == 0);
+    b.W[k] = weights[k];
+    b.img[k] = reinterpret_cast<halfx8*>(static_cast<char*>(images) + (int64_t)k * kWImgBytes);
+    b.xw[k] = transpose_w[k] != 0;
+  }
+  hipLaunchKernelGGL(node_weight_image_kernel, dim3(kWImg / 256, (unsigned)count), dim3(256), 0,
+                     mlcg_stream(stream), b);
   return mlcg_launch_status();
 }
 

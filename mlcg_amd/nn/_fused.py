@@ -128,6 +128,8 @@ class State:
     z: List[torch.Tensor] = field(default_factory=list)
     s: List[torch.Tensor] = field(default_factory=list)
     xL: Optional[torch.Tensor] = None
+    # split images of the block weights, {(block, "A1" | "A2" | "A3", transpose)}
+    wimg: Optional[dict] = None
     oh: List[torch.Tensor] = field(default_factory=list)   # output-MLP layer inputs
     oz: List[torch.Tensor] = field(default_factory=list)   # output-MLP pre-activations
     os_: List[torch.Tensor] = field(default_factory=list)  # output-MLP activations
@@ -207,29 +209,32 @@ def _gemm2_ok(x, A, B):
     return ops._node_gemm_ok(x, A) and ops._node_gemm_ok(x, B)
 
 
-def _lin_act_lin(x, A, c, act, want_z, B, cb, residual):
-    """(z, s, s B^T + cb + residual) with (z, s) = _lin_act(x, A, c, act)."""
+def _lin_act_lin(x, A, c, act, want_z, B, cb, residual, imgs=(None, None)):
+    """(z, s, s B^T + cb + residual) with (z, s) = _lin_act(x, A, c, act);
+    imgs: the split images of A and B for this orientation (or None)."""
     if _gemm2_ok(x, A, B):
         return ops.node_gemm2(x, A, B, bias=c, epilogue=ops.NODE_ACT, act=act,
-                              want_out0=want_z, bias2=cb, residual2=residual)
+                              want_out0=want_z, bias2=cb, residual2=residual,
+                              w_image=imgs[0], w2_image=imgs[1])
     z, s = _lin_act(x, A, c, act, want_z)
     return z, s, ops.node_linear(s, B, bias=cb, residual=residual)
 
 
-def _lin_dact_lin(x, A, z, s, act, transpose, B, residual=None):
+def _lin_dact_lin(x, A, z, s, act, transpose, B, residual=None, imgs=(None, None)):
     """(y, v, v B^T [+ residual]) (v B with transpose), (y, v) = _lin_dact(...)."""
     if _gemm2_ok(x, A, B):
         return ops.node_gemm2(x, A, B, transpose=transpose, epilogue=ops.NODE_DACT, act=act,
-                              z=z, s=s, residual2=residual)
+                              z=z, s=s, residual2=residual, w_image=imgs[0],
+                              w2_image=imgs[1])
     y, v = _lin_dact(x, A, z, s, act, transpose)
     return y, v, ops.node_linear(v, B, transpose=transpose, residual=residual)
 
 
-def _lin_dact2_lin(x, A, z, s, act, e, f, B):
+def _lin_dact2_lin(x, A, z, s, act, e, f, B, imgs=(None, None)):
     """(v, v B) with v = _lin_dact2(x, A, z, s, act, e, f)."""
     if _gemm2_ok(x, A, B):
         v, _, out = ops.node_gemm2(x, A, B, transpose=True, epilogue=ops.NODE_DACT2, act=act,
-                                   z=z, s=s, e=e, f=f)
+                                   z=z, s=s, e=e, f=f, w_image=imgs[0], w2_image=imgs[1])
         return v, out
     v = _lin_dact2(x, A, z, s, act, e, f)
     return v, ops.node_linear(v, B, transpose=True)
@@ -275,6 +280,33 @@ def _filters_ahead(spec: FusedSpec, P: Params, pos: torch.Tensor, graph: ops.Pai
     return ahead
 
 
+# Split images of the block weights made once per forward (MLCG_NODE_IMAGES=0
+# lets every node GEMM launch split its weights itself; same results).
+_NODE_IMAGES = os.environ.get("MLCG_NODE_IMAGES", "1") != "0"
+_IMAGE_NAMES = ("A1", "A2", "A3")
+
+
+def _weight_images(P: Params, x: torch.Tensor, transposed: bool) -> Optional[dict]:
+    """{(block, name, transpose): image} of every block weight A1, A2, A3 in
+    the orientations the sweeps use (x A^T forward and tangent; x A in the
+    backward sweeps, when transposed), made in one launch from the weights
+    as they are now; None when a weight is not a [128, 128] fp32 tensor on
+    the GPU (those products split in the kernel or use the library GEMM)."""
+    if not (_NODE_IMAGES and x.is_cuda and P.blocks):
+        return None
+    if not all(ops._node_gemm_ok(x, getattr(bp, n)) for bp in P.blocks for n in _IMAGE_NAMES):
+        return None
+    keys = [(k, n, t) for k in range(len(P.blocks)) for n in _IMAGE_NAMES
+            for t in ((False, True) if transposed else (False,))]
+    imgs = ops.node_weight_images([getattr(P.blocks[k], n) for k, n, _ in keys],
+                                  [t for _, _, t in keys])
+    return {key: imgs[i] for i, key in enumerate(keys)}
+
+
+def _wi(st: "State", k: int, name: str, transpose: bool) -> Optional[torch.Tensor]:
+    return None if st.wimg is None else st.wimg.get((k, name, transpose))
+
+
 def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             graph: ops.PairGraph, save: bool = True,
             rev_seed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, State]:
@@ -290,6 +322,7 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
     else:
         x = P.emb.index_select(0, types)
     ahead = _filters_ahead(spec, P, pos, graph, st.filt)
+    st.wimg = _weight_images(P, x, transposed=save)
     for k, bp in enumerate(P.blocks):
         if k in ahead:
             W, Wd, done = ahead[k]
@@ -301,14 +334,15 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
             done = None
         if k == 0:
             st.dist = dist
-        y = ops.node_linear(x, bp.A1)
+        y = ops.node_linear(x, bp.A1, w_image=_wi(st, k, "A1", False))
         if done is not None:
             torch.cuda.current_stream(pos.device).wait_event(done)
         agg = ops.cfconv_gather(y, W, graph)
         # z itself is only read back by the shifted-softplus derivatives;
         # x_next = x + lin(act(z))
         z, s, x_next = _lin_act_lin(agg, bp.A2, bp.c2, spec.block_act,
-                                    save and spec.block_act != ACT_TANH, bp.A3, bp.c3, x)
+                                    save and spec.block_act != ACT_TANH, bp.A3, bp.c3, x,
+                                    imgs=(_wi(st, k, "A2", False), _wi(st, k, "A3", False)))
         st.W.append(W)
         st.Wd.append(Wd)
         if save:
@@ -377,7 +411,8 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     for k in range(nb - 1, -1, -1):
         bp = P.blocks[k]
         sbar, zbar, gagg = _lin_dact_lin(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True,
-                                         bp.A2)
+                                         bp.A2, imgs=(_wi(st, k, "A3", True),
+                                                      _wi(st, k, "A2", True)))
         ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar,
                                      accumulate=(k != nb - 1))
         st.xbar_out[k] = xbar
@@ -385,7 +420,8 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
         st.zbar1[k] = zbar
         st.gagg1[k] = gagg
         st.ybar1[k] = ybar
-        xbar = ops.node_linear(ybar, bp.A1, transpose=True, residual=xbar)
+        xbar = ops.node_linear(ybar, bp.A1, transpose=True, residual=xbar,
+                               w_image=_wi(st, k, "A1", True))
     if not need_forces:
         return None
     return ops.pair_forces(st.pos, st.dist, dbar, graph)
@@ -401,10 +437,13 @@ def tangent(spec: FusedSpec, P: Params, st: State, u: torch.Tensor,
     xdot = None
     st.xdot_in, st.ydot, st.aggdot, st.zdot, st.sdot = [], [], [], [], []
     for k, bp in enumerate(P.blocks):
-        ydot = None if xdot is None else ops.node_linear(xdot, bp.A1)
+        ydot = None if xdot is None else ops.node_linear(xdot, bp.A1,
+                                                         w_image=_wi(st, k, "A1", False))
         aggdot = ops.cfconv_gather_tangent(ydot, st.y[k], st.W[k], st.Wd[k], st.ddot, graph)
         zdot, sdot, xdot_next = _lin_dact_lin(aggdot, bp.A2, st.z[k], st.s[k], spec.block_act,
-                                              False, bp.A3, residual=xdot)
+                                              False, bp.A3, residual=xdot,
+                                              imgs=(_wi(st, k, "A2", False),
+                                                    _wi(st, k, "A3", False)))
         st.xdot_in.append(xdot)
         st.ydot.append(ydot)
         st.aggdot.append(aggdot)
@@ -558,12 +597,13 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
     for k in range(len(P.blocks) - 1, -1, -1):
         bp = P.blocks[k]
         xbar2_in = xbar2
+        imgs_t = (_wi(st, k, "A3", True), _wi(st, k, "A2", True))
         if tangent_on:
             zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
-                                          st.sbar1[k], st.zdot[k], bp.A2)
+                                          st.sbar1[k], st.zdot[k], bp.A2, imgs=imgs_t)
         else:
             zbar2, gagg2 = _lin_dact2_lin(xbar2, bp.A3, st.z[k], st.s[k], spec.block_act,
-                                          None, None, bp.A2)
+                                          None, None, bp.A2, imgs=imgs_t)
         g1 = st.gagg1[k] if tangent_on else None
         yd = st.ydot[k] if tangent_on else None
         dd = st.ddot if tangent_on else None
@@ -582,7 +622,8 @@ def _blocks_reverse2(spec, P, st, tw, xbar2, g_out_w, g_out_b):
         held = [t for pr in probs for t in pr[:4]]
         (gA3, gc3), (gA2, gc2), gA1 = side.run(
             lambda: _node_tmm_batch(probs, N, st.pos.device), *held)
-        xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2)
+        xbar2 = ops.node_linear(ybar2, bp.A1, transpose=True, residual=xbar2,
+                                w_image=_wi(st, k, "A1", True))
         res = ops.filter_bwd_cfconv(st.pos, graph, st.filt, bp.W1, bp.b1, bp.W2, gagg2,
                                     st.y[k], g1, yd, dd, pair_adjoints=spec.basis_trainable,
                                     strict_fp32=spec.strict_fp32)

@@ -395,14 +395,16 @@ def tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 # reduction kernel for F = 128)
 
 def node_linear(x: torch.Tensor, W: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                residual: Optional[torch.Tensor] = None, transpose: bool = False) -> torch.Tensor:
+                residual: Optional[torch.Tensor] = None, transpose: bool = False,
+                w_image: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x W^T (or x W with transpose=True) [+ bias] [+ residual]: the fused
-    node GEMM kernel for [N, 128] x [128, 128]; other shapes (the output
-    network) go to one library GEMM with the epilogue terms in addmm's beta
-    input."""
+    node GEMM kernel for [N, 128] x [128, 128] (w_image: W's split image for
+    this orientation, node_weight_images); other shapes (the output network)
+    go to one library GEMM with the epilogue terms in addmm's beta input."""
     require_device(x)
     if _node_gemm_ok(x, W):
-        return node_gemm(x, W, transpose=transpose, bias=bias, residual=residual)[0]
+        return node_gemm(x, W, transpose=transpose, bias=bias, residual=residual,
+                         w_image=w_image)[0]
     Wm = W if transpose else W.t()
     if residual is not None and bias is not None:
         return torch.addmm(residual + bias, x, Wm)
@@ -426,6 +428,7 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
               epilogue: int = NODE_PLAIN, act: int = 0, z: Optional[torch.Tensor] = None,
               s: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
               f: Optional[torch.Tensor] = None, want_out0: bool = True,
+              w_image: Optional[torch.Tensor] = None,
               ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """(out0, out1) of the fused node GEMM (mlcg_node_gemm) on [N, 128] fp32
     rows and a [128, 128] weight: y = x W^T (x W with transpose) [+ bias]
@@ -437,7 +440,9 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
         NODE_DACT2  out0 = y * act'(z) [+ e * act''(z) * f]
 
     (act' and act'' from z and s = act(z)).  out0 is skipped for ACT/DACT
-    when want_out0 is False."""
+    when want_out0 is False.  w_image: W's split image for this orientation
+    (node_weight_images, made after W's last change), read instead of
+    splitting W in the kernel; the results are the same bit for bit."""
     require_device(x)
     _check(_node_gemm_ok(x, W), lambda: f"node_gemm takes [N, {NUM_FILTERS}] float32 rows and a "
            f"[{NUM_FILTERS}, {NUM_FILTERS}] weight, got {tuple(x.shape)} / {tuple(W.shape)}")
@@ -454,9 +459,10 @@ def node_gemm(x: torch.Tensor, W: torch.Tensor, transpose: bool = False,
         out0 = torch.empty_like(x)
     if epilogue in (NODE_ACT, NODE_DACT):
         out1 = torch.empty_like(x)
+    _check_w_image(w_image, dev)
     call("mlcg_node_gemm", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
          ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
-         ptr(out1), stream_handle(dev),
+         ptr(out1), ptr(w_image), stream_handle(dev),
          work=_node_gemm_bytes(n, epilogue, act, (x, residual, out0, out1), s, z, e, f, 1))
     return out0, out1
 
@@ -480,11 +486,13 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
                s: Optional[torch.Tensor] = None, e: Optional[torch.Tensor] = None,
                f: Optional[torch.Tensor] = None, want_out0: bool = True,
                bias2: Optional[torch.Tensor] = None, residual2: Optional[torch.Tensor] = None,
+               w_image: Optional[torch.Tensor] = None, w2_image: Optional[torch.Tensor] = None,
                ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor], torch.Tensor]:
     """(out0, out1, out2): node_gemm(x, W, ...) with an ACT, DACT or DACT2
     epilogue followed, in the same kernel (mlcg_node_gemm2), by
     out2 = v W2^T (v W2 with transpose) [+ bias2] [+ residual2], v being out1
-    (ACT, DACT) or out0 (DACT2).  Bit-identical to the two node_gemm calls."""
+    (ACT, DACT) or out0 (DACT2).  Bit-identical to the two node_gemm calls.
+    w_image, w2_image: split images of W and W2 as in node_gemm."""
     require_device(x)
     _check(epilogue in (NODE_ACT, NODE_DACT, NODE_DACT2),
            "node_gemm2 takes an ACT, DACT or DACT2 first epilogue")
@@ -508,12 +516,50 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
     if epilogue in (NODE_ACT, NODE_DACT):
         out1 = torch.empty_like(x)
     out2 = torch.empty_like(x)
+    _check_w_image(w_image, dev)
+    _check_w_image(w2_image, dev)
     call("mlcg_node_gemm2", ptr(x), n, NUM_FILTERS, ptr(W), int(transpose), ptr(bias),
          ptr(residual), int(epilogue), int(act), ptr(z), ptr(s), ptr(e), ptr(f), ptr(out0),
-         ptr(out1), ptr(W2), ptr(bias2), ptr(residual2), ptr(out2), stream_handle(dev),
+         ptr(out1), ptr(W2), ptr(bias2), ptr(residual2), ptr(out2), ptr(w_image),
+         ptr(w2_image), stream_handle(dev),
          work=_node_gemm_bytes(n, epilogue, act, (x, residual, out0, out1, residual2, out2),
                                s, z, e, f, 2))
     return out0, out1, out2
+
+
+NODE_W_IMAGE_HALFS = 32768  # fp16 entries of one split weight image (64 KiB)
+
+
+def _check_w_image(img: Optional[torch.Tensor], dev) -> None:
+    _check(img is None or (img.dtype == torch.float16 and img.device == dev
+                           and img.numel() == NODE_W_IMAGE_HALFS and img.is_contiguous()
+                           and img.data_ptr() % 16 == 0),
+           lambda: f"a node weight image is a contiguous [{NODE_W_IMAGE_HALFS}] float16 tensor "
+                   f"on {dev} (node_weight_images)")
+
+
+def node_weight_images(weights, transposes) -> torch.Tensor:
+    """[count, NODE_W_IMAGE_HALFS] fp16: the split operand image of each
+    [128, 128] fp32 weight for node_gemm / node_gemm2 in the orientation given
+    by its transpose flag, all made in one launch (mlcg_node_weight_images,
+    at most 32 per launch).  Row k is the w_image argument for weights[k]."""
+    _check(len(weights) == len(transposes), "one transpose flag per weight")
+    n = len(weights)
+    _check(n >= 1, "node_weight_images needs at least one weight")
+    dev = weights[0].device
+    ws = []
+    for W in weights:
+        _check(W.is_cuda and W.device == dev and W.dtype == torch.float32
+               and tuple(W.shape) == (NUM_FILTERS, NUM_FILTERS),
+               lambda: f"node weights must be [{NUM_FILTERS}, {NUM_FILTERS}] float32 on {dev}")
+        ws.append(W.detach().contiguous())
+    out = torch.empty(n, NODE_W_IMAGE_HALFS, dtype=torch.float16, device=dev)
+    for k in range(0, n, 32):
+        m = min(32, n - k)
+        warr = (ctypes.c_void_p * m)(*[t.data_ptr() for t in ws[k:k + m]])
+        tarr = (ctypes.c_int * m)(*[int(bool(t)) for t in transposes[k:k + m]])
+        call("mlcg_node_weight_images", warr, tarr, m, ptr(out[k]), stream_handle(dev))
+    return out
 
 
 def node_tmm(a1: torch.Tensor, b1: torch.Tensor, a2: Optional[torch.Tensor] = None,

@@ -146,6 +146,32 @@ def test_stream_arrangements_bit_identical():
                 assert torch.equal(a, c), (ahead, side, k)
 
 
+def test_node_weight_images_step_bit_identical():
+    """Training steps whose node products read the per-forward split weight
+    images give the losses, forces and parameters of steps whose products
+    split the weights in every launch, bit for bit."""
+    from mlcg_amd import synthetic
+    from mlcg_amd.nn import _fused
+
+    print("weight images vs in-kernel splits, 3 blocks, 16 frames", flush=True)
+    cfg = make_cfg(num_blocks=3, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=35)
+    b = synthetic.config2(n_frames=16)
+    saved = _fused._NODE_IMAGES
+    try:
+        _fused._NODE_IMAGES = False
+        ref = _step_run(cfg, sd, b, ahead=True, tmm_side=False)
+        _fused._NODE_IMAGES = True
+        got = _step_run(cfg, sd, b, ahead=True, tmm_side=False)
+    finally:
+        _fused._NODE_IMAGES = saved
+    for k in range(3):
+        assert torch.equal(got[0][k], ref[0][k]), k
+        assert torch.equal(got[1][k], ref[1][k]), k
+        for a, c in zip(got[2][k], ref[2][k]):
+            assert torch.equal(a, c), k
+
+
 def test_captured_train_step_api_matches_eager():
     """mlcg_amd.pl.CapturedTrainStep (one warm-up step, then replays that
     each load a second resident copy of the batch) gives the eager steps'

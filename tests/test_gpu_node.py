@@ -213,6 +213,51 @@ def test_node_gemm2_matches_two_calls(rows, transpose, act):
         assert torch.equal(g2, ops.node_gemm(v0, W2, transpose=transpose)[0])
 
 
+@pytest.mark.parametrize("rows", [1, 17, 1000, 17920])
+@pytest.mark.parametrize("transpose", [False, True])
+def test_node_weight_images_bit_identical(rows, transpose):
+    """Products that read pre-split weight images (mlcg_node_weight_images)
+    equal those that split the weights in the kernel, bit for bit, for every
+    epilogue of node_gemm and node_gemm2; an image of the other orientation
+    gives a different product, so the orientation is part of the image; a
+    malformed image raises."""
+    from mlcg_amd import ops
+
+    print(f"weight images rows={rows} transpose={transpose}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows * 2 + int(transpose) + 7)
+    rnd = lambda *s: torch.randn(*s, device="cuda", generator=g)  # noqa: E731
+    x, r, z, e, f = (rnd(rows, 128) for _ in range(5))
+    s = torch.tanh(z)
+    W, W2 = rnd(128, 128) / 11, rnd(128, 128) * 3
+    b = rnd(128)
+    imgs = ops.node_weight_images([W, W2, W], [transpose, transpose, not transpose])
+    assert imgs.shape == (3, ops.NODE_W_IMAGE_HALFS) and imgs.dtype == torch.float16
+    wi, w2i, other = imgs[0], imgs[1], imgs[2]
+    kw = dict(transpose=transpose, act=0)
+    for ep, extra in ((ops.NODE_PLAIN, dict(bias=b, residual=r)),
+                      (ops.NODE_ACT, dict(bias=b)),
+                      (ops.NODE_DACT, dict(z=z, s=s)),
+                      (ops.NODE_DACT2, dict(z=z, s=s, e=e, f=f))):
+        ref = ops.node_gemm(x, W, epilogue=ep, **kw, **extra)
+        got = ops.node_gemm(x, W, epilogue=ep, w_image=wi, **kw, **extra)
+        for a_, c_ in zip(ref, got):
+            assert (a_ is None and c_ is None) or torch.equal(a_, c_), ep
+        if ep != ops.NODE_PLAIN:
+            ref2 = ops.node_gemm2(x, W, W2, epilogue=ep, residual2=r, **kw, **extra)
+            for images in ((wi, None), (None, w2i), (wi, w2i)):
+                got2 = ops.node_gemm2(x, W, W2, epilogue=ep, residual2=r, w_image=images[0],
+                                      w2_image=images[1], **kw, **extra)
+                for a_, c_ in zip(ref2, got2):
+                    assert (a_ is None and c_ is None) or torch.equal(a_, c_), (ep, images)
+    if rows >= 17:
+        wrong = ops.node_gemm(x, W, transpose=transpose, w_image=other)[0]
+        assert not torch.equal(wrong, ops.node_gemm(x, W, transpose=transpose)[0])
+    with pytest.raises(RuntimeError, match="image"):
+        ops.node_gemm(x, W, w_image=wi[:100])
+    with pytest.raises(RuntimeError, match="image"):
+        ops.node_gemm(x, W, w_image=wi.float())
+
+
 def test_node_gemm2_checks():
     from mlcg_amd import ops
 
