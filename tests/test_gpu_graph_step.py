@@ -191,6 +191,42 @@ def test_captured_train_step_api_matches_eager():
             assert torch.equal(a, c), k
 
 
+def test_captured_train_step_overflow_raises_at_check():
+    """A batch with more edges than the captured step's edge capacity does not
+    grow the graph: the replays run on the truncated graph (every kernel
+    stays inside its buffers) and check() raises naming the capacity; the
+    flags are cleared by the raising check."""
+    from mlcg_amd import nn, synthetic
+    from mlcg_amd.pl import CapturedTrainStep
+
+    print("CapturedTrainStep with half the needed edge capacity", flush=True)
+    cfg = make_cfg(num_blocks=2, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=36)
+    model = make_model(cfg, sd).train()
+    data = synthetic.config2(n_frames=4).to_torch("cuda")
+    gm = nn.GradientsOut(model)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True, capturable=True)
+
+    def step(d):
+        opt.zero_grad(set_to_none=True)
+        out = gm(d)
+        out.out.update(**out.out[model.name])
+        loss = nn.ForceMSE()(out)
+        loss.backward()
+        opt.step()
+        return loss
+
+    e_full = model.build_graph(data).num_edges
+    cs = CapturedTrainStep(step, data, model, opt, warmup=1, capacity_factor=0.5)
+    assert 0 < model.graph_capacity < e_full
+    cs.step(data)
+    cs.step(data)
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="more edges than the capacity"):
+        cs.check()
+    cs.check()  # cleared by the raising check
+
+
 def test_captured_train_step_requires_capturable_optimizer():
     from mlcg_amd import nn, synthetic
     from mlcg_amd.pl import CapturedTrainStep
