@@ -1059,6 +1059,7 @@ size_t fwd_x3_lds_bytes(int K) {
 //       of one row), and the B operand of step 1 (scalar); rows of 16 floats,
 //       float4 pair group c of row r stored at c ^ ((r >> 1) & 3).
 constexpr int kBwdWaves = 8;
+constexpr int kBwdXcds = 8;  // XCDs of the chip (workgroups dispatched round-robin)
 constexpr int kBwdThreads = kBwdWaves * MLCG_WAVE;
 
 __device__ __forceinline__ int tb_at(int pair, int g) { return pair * kF + ((g ^ (pair & 7)) << 2); }
@@ -1489,13 +1490,21 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     if (threadIdx.x < 64) PMAXu[threadIdx.x] = 0u;
     __syncthreads();
   }
+  // XCD-aware tile order: workgroups are dispatched round-robin over the
+  // XCDs, and the workgroups of one XCD take one contiguous range of tiles
+  // (strided among them), so the node rows of a frame's pairs are fetched
+  // into that XCD's L2 only, not into every XCD's (config 2: 269.5 -> 265 us).
+  const int nx = (int)gridDim.x < kBwdXcds ? (int)gridDim.x : kBwdXcds;
+  const int xcd = blockIdx.x % nx, wl = blockIdx.x / nx;
+  const int64_t stride = gridDim.x / nx + (xcd < (int)(gridDim.x % nx) ? 1 : 0);
+  const int64_t t_start = tiles * xcd / nx + wl, t_end = tiles * (xcd + 1) / nx;
   if (np > 0) {  // uniform across the workgroup
-    const int64_t p0 = clamp_pair(blockIdx.x);
+    const int64_t p0 = clamp_pair(t_start);
     const TileIn first = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, p0, pi[p0], pj[p0], fcol);
-    const int64_t p1 = clamp_pair((int64_t)blockIdx.x + gridDim.x);
+    const int64_t p1 = clamp_pair(t_start + stride);
     ni = pi[p1];
     nj = pj[p1];
-    const float vm0 = (int64_t)blockIdx.x * 16 + n < np ? 1.0f : 0.0f;
+    const float vm0 = t_start * 16 + n < np ? 1.0f : 0.0f;
     const BasisV bv0 = basis_eval(first);
     basis_store(bv0, 0);
     cc_cur = bv0.cc;
@@ -1507,15 +1516,15 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     pair_adjoints_store(pm0, pm1, 0);
   }
   __syncthreads();
-  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x, buf ^= 1) {
+  for (int64_t tile = t_start; tile < t_end; tile += stride, buf ^= 1) {
     float* GT = GT0 + buf * 2 * kRows * 16;
     const float vmask = tile * 16 + n < np ? 1.0f : 0.0f;
     // inputs of the next tile and indices of the one after it: consumed in
     // step 5 and one tile later
-    const int64_t pn = clamp_pair(tile + gridDim.x);
+    const int64_t pn = clamp_pair(tile + stride);
     const TileIn nxt = fetch_tile<kNodes>(pos, adj, ddp, g1p, ydp, pn, ni, nj, fcol);
     {
-      const int64_t pnn = clamp_pair(tile + 2 * (int64_t)gridDim.x);
+      const int64_t pnn = clamp_pair(tile + 2 * stride);
       ni = pi[pnn];
       nj = pj[pnn];
     }
@@ -1701,7 +1710,7 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     }
     // the next tile's pair adjoints from its node vectors (requested at the
     // start of this tile), early so that their registers are free for step 4
-    const float vm_nxt = (tile + gridDim.x) * 16 + n < np ? 1.0f : 0.0f;
+    const float vm_nxt = (tile + stride) * 16 + n < np ? 1.0f : 0.0f;
     float4 wb_nxt, wdb_nxt;
     tile_adjoint<kNodes>(nxt, tangent, has_yd, vm_nxt, wb_nxt, wdb_nxt);
     float abv[4], adbv[4];
