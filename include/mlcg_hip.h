@@ -688,6 +688,20 @@ int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
 int mlcg_stream_copy(const float* src, float* dst, int64_t n, int groups,
                      int unroll, void* stream);
 
+/* The force-matching loss (ForceMSE with reduction "mean",
+ * mlcg/nn/losses.py:130-181 -> torch.nn.functional.mse_loss):
+ * *loss = sum_k (x[k] - y[k])^2 / n over n >= 1 fp32 elements, summed per
+ * 64 Ki-element chunk and then over the chunks in a fixed order; `workspace`
+ * holds mlcg_mse_workspace_floats(n) floats (0 up to 65,536 elements: may be
+ * NULL).  mlcg_mse_mean_backward: grad_x[k] = (2/n) (x[k] - y[k]) g with g =
+ * *grad_loss (a device scalar), evaluated as torch's mse_loss backward does,
+ * so bit-identical to it. */
+int64_t mlcg_mse_workspace_floats(int64_t n);
+int mlcg_mse_mean(const float* x, const float* y, int64_t n, float* loss,
+                  float* workspace, int64_t workspace_floats, void* stream);
+int mlcg_mse_mean_backward(const float* x, const float* y, const float* grad_loss,
+                           int64_t n, float* grad_x, void* stream);
+
 /* Device-to-device copies dsts[k][0 .. bytes[k]) = srcs[k][...] for
  * k < count <= 8 (MLCG_ERR_UNSUPPORTED beyond) in one launch; every pointer
  * 16-byte aligned, the ranges must not overlap.  The pointer and size arrays

@@ -105,6 +105,9 @@ _SIGNATURES = {
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
     "mlcg_copy_batch": [_P, _P, _P, _I32, _P],
+    "mlcg_mse_workspace_floats": [_I64],
+    "mlcg_mse_mean": [_P, _P, _I64, _P, _P, _I64, _P],
+    "mlcg_mse_mean_backward": [_P, _P, _P, _I64, _P, _P],
 }
 _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_radius_workspace_bytes": _I64,
@@ -112,7 +115,8 @@ _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_node_tmm_batch_workspace_floats": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,
-             "mlcg_type_sum_workspace_floats": _I64, "mlcg_node_weight_image_bytes": _I64}
+             "mlcg_type_sum_workspace_floats": _I64, "mlcg_node_weight_image_bytes": _I64,
+             "mlcg_mse_workspace_floats": _I64}
 
 STATUS = {
     0: "MLCG_OK",

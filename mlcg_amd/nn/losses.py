@@ -8,6 +8,7 @@ import torch
 from torch.nn import functional as F
 from torch.nn.modules.loss import _Loss
 
+from .. import ops
 from ..data._keys import ENERGY_KEY, FORCE_KEY
 
 
@@ -46,6 +47,31 @@ class ForceRMSE(_Loss):
                                      reduction=self.reduction))
 
 
+class _MSEMean(torch.autograd.Function):
+    """mean((pred - ref)^2) on the HIP kernels (two launches per training step
+    instead of torch's five: square, mean, and the backward's zero fill,
+    product and seed); the gradient equals torch's mse_loss gradient bit for
+    bit, the loss agrees with it to rounding (fixed summation order)."""
+
+    @staticmethod
+    def forward(ctx, pred, ref):
+        ctx.save_for_backward(pred, ref)
+        return ops.mse_mean(pred, ref)
+
+    @staticmethod
+    def backward(ctx, grad):
+        pred, ref = ctx.saved_tensors
+        return ops.mse_mean_backward(pred, ref, grad), None
+
+
+def _mse(pred: torch.Tensor, ref: torch.Tensor, reduction: str) -> torch.Tensor:
+    """F.mse_loss, on the HIP kernels for the training step's case (mean of
+    contiguous fp32 GPU tensors, reference without gradient)."""
+    if reduction == "mean" and not ref.requires_grad and ops._mse_ok(pred, ref):
+        return _MSEMean.apply(pred, ref)
+    return F.mse_loss(pred, ref, reduction=reduction)
+
+
 class ForceMSE(_Loss):
     def __init__(self, force_kwd: str = FORCE_KEY, size_average=None, reduce=None,
                  reduction: str = "mean") -> None:
@@ -54,8 +80,7 @@ class ForceMSE(_Loss):
 
     def forward(self, data) -> torch.Tensor:
         _check(data, self.force_kwd)
-        return F.mse_loss(data.out[self.force_kwd], data[self.force_kwd],
-                          reduction=self.reduction)
+        return _mse(data.out[self.force_kwd], data[self.force_kwd], self.reduction)
 
 
 class EnergyMSE(_Loss):

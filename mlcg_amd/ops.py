@@ -639,6 +639,38 @@ def copy_batch(dsts, srcs) -> None:
         call("mlcg_copy_batch", src_arr, dst_arr, nbytes, n, stream_handle(dev))
 
 
+def _mse_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
+    return (x.is_cuda and y.device == x.device and x.dtype == torch.float32
+            and y.dtype == torch.float32 and x.shape == y.shape and x.numel() >= 1
+            and x.is_contiguous() and y.is_contiguous())
+
+
+def mse_mean(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """mean((x - y)^2) of two contiguous fp32 tensors of one shape on the GPU
+    as a 0-dim tensor (mlcg_mse_mean: fixed summation order)."""
+    require_device(x, y)
+    _check(_mse_ok(x, y), "mse_mean takes two contiguous float32 tensors of one shape on the "
+                          "same GPU")
+    n = x.numel()
+    loss = torch.empty((), dtype=torch.float32, device=x.device)
+    nws = int(_lib.load().mlcg_mse_workspace_floats(n))
+    ws = torch.empty(nws, dtype=torch.float32, device=x.device) if nws > 0 else None
+    call("mlcg_mse_mean", ptr(x), ptr(y), n, ptr(loss), ptr(ws), nws, stream_handle(x.device))
+    return loss
+
+
+def mse_mean_backward(x: torch.Tensor, y: torch.Tensor, grad: torch.Tensor) -> torch.Tensor:
+    """(2/n) (x - y) grad for the scalar upstream gradient `grad` (on the
+    device), as torch's mse_loss backward evaluates it (mlcg_mse_mean_backward)."""
+    require_device(x, y)
+    _check(_mse_ok(x, y), "mse_mean_backward takes the forward's two tensors")
+    g = grad.reshape(()).to(torch.float32).contiguous()
+    out = torch.empty_like(x)
+    call("mlcg_mse_mean_backward", ptr(x), ptr(y), ptr(g), x.numel(), ptr(out),
+         stream_handle(x.device))
+    return out
+
+
 def embedding_gather(table: torch.Tensor, types: torch.Tensor) -> torch.Tensor:
     """table[types] for a [T, 128] fp32 table and int64 types (the embedding
     lookup, mlcg_embedding_gather); a type outside [0, T) gives a zero row and
