@@ -3,10 +3,10 @@
 // "mean") and its gradient with respect to the prediction.
 //
 // Forward: each workgroup sums (x - y)^2 over one chunk of 64 Ki elements
-// (every thread a strided part, four loads in flight, then a fixed butterfly
-// over the wave and the waves in order); with one chunk the workgroup writes
-// the mean itself, otherwise its partial sum, which mse_final_kernel adds in
-// workgroup order.  Backward: grad_x = (norm (x - y)) g with norm = 2 / n as
+// (every thread a strided part, float4 loads eight in flight when the arrays
+// are 16-byte aligned, then a fixed butterfly over the wave and the waves in
+// order); with one chunk the workgroup writes the mean itself, otherwise
+// its partial sum, which mse_final_kernel adds in workgroup order.  Backward: grad_x = (norm (x - y)) g with norm = 2 / n as
 // a float, the same expression and order as torch's mse_loss backward, so
 // the gradient is the same bit for bit.
 #include "common.h"
@@ -16,25 +16,46 @@ namespace {
 constexpr int kMseThreads = 512;
 constexpr int64_t kMseChunk = 65536;  // elements per workgroup
 
+__device__ __forceinline__ float sq4(float4 a, float4 b) {
+  const float dx = a.x - b.x, dy = a.y - b.y, dz = a.z - b.z, dw = a.w - b.w;
+  return fmaf(dx, dx, dy * dy) + fmaf(dz, dz, dw * dw);
+}
+
+// vec4: x and y 16-byte aligned and the chunk a multiple of 4 elements, so
+// that each thread reads float4s (eight in flight): one workgroup then has
+// 64 KiB of loads outstanding instead of 8 KiB.
 __global__ __launch_bounds__(kMseThreads) void mse_partial_kernel(
-    const float* __restrict__ x, const float* __restrict__ y, int64_t n,
+    const float* __restrict__ x, const float* __restrict__ y, int64_t n, int vec4,
     float* __restrict__ partial, float* __restrict__ loss) {
   const int64_t base = (int64_t)blockIdx.x * kMseChunk;
   const int64_t end = base + kMseChunk < n ? base + kMseChunk : n;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int64_t k = base + threadIdx.x;
-  for (; k + 3 * kMseThreads < end; k += 4 * kMseThreads) {
-    float d[4];
+  constexpr int kU = 8;
+  float acc[kU] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t k = base;
+  if (vec4) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* y4 = reinterpret_cast<const float4*>(y);
+    const int64_t e4 = base / 4 + (end - base) / 4;
+    int64_t q = base / 4 + threadIdx.x;
+    for (; q + (kU - 1) * kMseThreads < e4; q += kU * kMseThreads) {
+      float4 a[kU], c[kU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) d[u] = x[k + u * kMseThreads] - y[k + u * kMseThreads];
+      for (int u = 0; u < kU; ++u) {
+        a[u] = x4[q + u * kMseThreads];
+        c[u] = y4[q + u * kMseThreads];
+      }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = fmaf(d[u], d[u], acc[u]);
+      for (int u = 0; u < kU; ++u) acc[u] += sq4(a[u], c[u]);
+    }
+    for (; q < e4; q += kMseThreads) acc[0] += sq4(x4[q], y4[q]);
+    k = 4 * e4;  // the chunk's last n mod 4 elements, if any, below
   }
-  for (; k < end; k += kMseThreads) {
+  for (k += threadIdx.x; k < end; k += kMseThreads) {
     const float d = x[k] - y[k];
-    acc[0] = fmaf(d, d, acc[0]);
+    acc[1] = fmaf(d, d, acc[1]);
   }
-  float s = mlcg_wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
+  float s = mlcg_wave_sum(((acc[0] + acc[1]) + (acc[2] + acc[3])) +
+                          ((acc[4] + acc[5]) + (acc[6] + acc[7])));
   __shared__ float part[kMseThreads / MLCG_WAVE];
   if (mlcg_lane() == 0) part[threadIdx.x / MLCG_WAVE] = s;
   __syncthreads();
@@ -86,8 +107,10 @@ extern "C" int mlcg_mse_mean(const float* x, const float* y, int64_t n, float* l
   const int groups = mse_groups(n);
   MLCG_REQUIRE(groups == 1 || (workspace && workspace_floats >= groups));
   hipStream_t s = mlcg_stream(stream);
+  const int vec4 = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 16 == 0;  // kMseChunk is a multiple of 4
   hipLaunchKernelGGL(mse_partial_kernel, dim3((unsigned)groups), dim3(kMseThreads), 0, s, x, y,
-                     n, workspace, loss);
+                     n, vec4, workspace, loss);
   if (groups > 1)
     hipLaunchKernelGGL(mse_final_kernel, dim3(1), dim3(MLCG_WAVE), 0, s, workspace, groups, n,
                        loss);

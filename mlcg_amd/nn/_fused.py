@@ -321,8 +321,10 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
         x = ops.embedding_gather(P.emb.detach(), types)
     else:
         x = P.emb.index_select(0, types)
-    ahead = _filters_ahead(spec, P, pos, graph, st.filt)
+    # the weight images before the side stream's filter forwards, which would
+    # otherwise hold every CU while this short launch waits for one
     st.wimg = _weight_images(P, x, transposed=save)
+    ahead = _filters_ahead(spec, P, pos, graph, st.filt)
     for k, bp in enumerate(P.blocks):
         if k in ahead:
             W, Wd, done = ahead[k]
