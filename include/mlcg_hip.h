@@ -702,6 +702,15 @@ int mlcg_mse_mean(const float* x, const float* y, int64_t n, float* loss,
 int mlcg_mse_mean_backward(const float* x, const float* y, const float* grad_loss,
                            int64_t n, float* grad_x, void* stream);
 
+/* out[k] = ((0 + a_0[k]) + a_1[k]) + ... for count <= 8 fp32 arrays of n
+ * elements (MLCG_ERR_UNSUPPORTED beyond): SumOut's running sum of its
+ * models' energies or forces (mlcg/nn/gradients.py SumOut.forward) in one
+ * launch, bit-identical to the sequence of adds it replaces.  The array of
+ * pointers is host memory, read during the call; out may alias none of the
+ * inputs. */
+int mlcg_sum_arrays(const float* const* arrays, int count, int64_t n, float* out,
+                    void* stream);
+
 /* Device-to-device copies dsts[k][0 .. bytes[k]) = srcs[k][...] for
  * k < count <= 8 (MLCG_ERR_UNSUPPORTED beyond) in one launch; every pointer
  * 16-byte aligned, the ranges must not overlap.  The pointer and size arrays

@@ -105,6 +105,7 @@ _SIGNATURES = {
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
     "mlcg_copy_batch": [_P, _P, _P, _I32, _P],
+    "mlcg_sum_arrays": [_P, _I32, _I64, _P, _P],
     "mlcg_mse_workspace_floats": [_I64],
     "mlcg_mse_mean": [_P, _P, _I64, _P, _P, _I64, _P],
     "mlcg_mse_mean_backward": [_P, _P, _P, _I64, _P, _P],

@@ -85,7 +85,43 @@ __global__ __launch_bounds__(kStreamThreads) void copy_batch_kernel(CopyBatch b)
   }
 }
 
+// out = ((0 + a_0) + a_1) + ... + a_{count-1} elementwise, the order in
+// which SumOut's running sum adds its models' outputs (mlcg/nn/gradients.py
+// SumOut), so the result is that loop's bit for bit, in one launch.
+constexpr int kSumMax = 8;
+struct SumBatch {
+  const float* a[kSumMax];
+  int count;
+};
+
+__global__ __launch_bounds__(kStreamThreads) void sum_arrays_kernel(SumBatch b, int64_t n,
+                                                                    float* __restrict__ out) {
+  const int64_t G = (int64_t)gridDim.x * kStreamThreads;
+  for (int64_t k = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x; k < n; k += G) {
+    float acc = 0.0f;
+    for (int m = 0; m < b.count; ++m) acc = acc + b.a[m][k];
+    out[k] = acc;
+  }
+}
+
 }  // namespace
+
+extern "C" int mlcg_sum_arrays(const float* const* arrays, int count, int64_t n, float* out,
+                               void* stream) {
+  MLCG_REQUIRE(count >= 1 && n >= 0 && arrays && (n == 0 || out));
+  if (count > kSumMax) return MLCG_ERR_UNSUPPORTED;
+  if (n == 0) return MLCG_OK;
+  SumBatch b{};
+  b.count = count;
+  for (int m = 0; m < count; ++m) {
+    MLCG_REQUIRE(arrays[m] != nullptr);
+    b.a[m] = arrays[m];
+  }
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n, kStreamThreads), 8);
+  hipLaunchKernelGGL(sum_arrays_kernel, dim3(groups), dim3(kStreamThreads), 0,
+                     mlcg_stream(stream), b, n, out);
+  return mlcg_launch_status();
+}
 
 extern "C" int mlcg_copy_batch(const void* const* srcs, void* const* dsts, const int64_t* bytes,
                                int count, void* stream) {

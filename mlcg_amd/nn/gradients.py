@@ -13,7 +13,22 @@ from typing import Any, List, Sequence
 
 import torch
 
+from .. import ops
 from ..data._keys import ENERGY_KEY, FORCE_KEY
+
+
+class _SumArrays(torch.autograd.Function):
+    """Sum of model outputs (ops.sum_arrays); the gradient reaches every input
+    unchanged, as through the adds it replaces."""
+
+    @staticmethod
+    def forward(ctx, *xs):
+        ctx.n = len(xs)
+        return ops.sum_arrays(list(xs))
+
+    @staticmethod
+    def backward(ctx, g):
+        return tuple(g for _ in range(ctx.n))
 
 
 class SumOut(torch.nn.Module):
@@ -27,6 +42,21 @@ class SumOut(torch.nn.Module):
         self.models = models
 
     def forward(self, data):
+        if self._outputs_independent():
+            # the models never read data.out[target]: run them, then add their
+            # outputs in the loop's order in one launch per target
+            for name in self.models.keys():
+                data = self.models[name](data)
+            for target in self.targets:
+                parts = [data.out[name][target] for name in self.models.keys()]
+                if ops.sum_arrays_ok(parts):
+                    data.out[target] = _SumArrays.apply(*parts)
+                else:
+                    acc = 0.00
+                    for p in parts:
+                        acc += p
+                    data.out[target] = acc
+            return data
         for target in self.targets:
             data.out[target] = 0.00
         for name in self.models.keys():
@@ -34,6 +64,12 @@ class SumOut(torch.nn.Module):
             for target in self.targets:
                 data.out[target] += data.out[name][target]
         return data
+
+    def _outputs_independent(self) -> bool:
+        """Every model is a GradientsOut that writes only data.out[its name]
+        (not one wrapping a SumOut, which writes data.out[target] itself)."""
+        return len(self.models) > 0 and all(
+            isinstance(m, GradientsOut) and m.name != "SumOut" for m in self.models.values())
 
     def neighbor_list(self, **kwargs):
         nl = {}

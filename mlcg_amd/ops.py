@@ -639,6 +639,31 @@ def copy_batch(dsts, srcs) -> None:
         call("mlcg_copy_batch", src_arr, dst_arr, nbytes, n, stream_handle(dev))
 
 
+SUM_ARRAYS_MAX = 8
+
+
+def sum_arrays_ok(xs) -> bool:
+    """Whether sum_arrays takes these tensors: 1..8 contiguous fp32 tensors of
+    one shape on one GPU."""
+    if not 1 <= len(xs) <= SUM_ARRAYS_MAX:
+        return False
+    x0 = xs[0]
+    return all(isinstance(t, torch.Tensor) and t.is_cuda and t.device == x0.device
+               and t.dtype == torch.float32 and t.shape == x0.shape and t.is_contiguous()
+               for t in xs)
+
+
+def sum_arrays(xs) -> torch.Tensor:
+    """((0 + xs[0]) + xs[1]) + ... elementwise in one launch (mlcg_sum_arrays),
+    bit-identical to adding them one by one in that order."""
+    _check(sum_arrays_ok(xs), "sum_arrays takes 1 to 8 contiguous float32 tensors of one "
+                              "shape on one GPU")
+    out = torch.empty_like(xs[0])
+    arr = (ctypes.c_void_p * len(xs))(*[t.data_ptr() for t in xs])
+    call("mlcg_sum_arrays", arr, len(xs), xs[0].numel(), ptr(out), stream_handle(out.device))
+    return out
+
+
 def _mse_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
     return (x.is_cuda and y.device == x.device and x.dtype == torch.float32
             and y.dtype == torch.float32 and x.shape == y.shape and x.numel() >= 1

@@ -161,8 +161,9 @@ def test_prior_modules_sumout_and_static():
                                              nlm["mapping_batch"].cpu(), 4, pp)
         check(e, E_ref, 1e-5, name)
         check(f, F_ref, 1e-5, name)
-    assert torch.allclose(out.out["energy"], total_E, atol=1e-5)
-    assert torch.allclose(out.out["forces"], total_F, atol=1e-5)
+    # the one-launch sum adds the parts in the loop's order: bit for bit
+    assert torch.equal(out.out["energy"], total_E)
+    assert torch.equal(out.out["forces"], total_F)
     # generic autograd route: forward energy, then grad wrt pos
     d2 = collate(confs).to("cuda")
     d2.pos.requires_grad_(True)
@@ -244,6 +245,40 @@ def test_langevin_thermostat_equipartition():
     m = sim.final_data.masses.double()
     ke_per_dof = float((0.5 * m[:, None] * v * v).mean())
     assert ke_per_dof == pytest.approx(0.5 / beta, rel=0.08)
+
+
+def test_sumout_one_launch_sum_matches_loop_with_gradients():
+    """SumOut over GradientsOut models adds their outputs in one launch: the
+    totals and, in training, every parameter gradient through the summed
+    forces equal those of the reference's running-sum loop bit for bit."""
+    from mlcg_amd import nn
+    from mlcg_amd.data.atomic_data import collate
+    from oracle import schnet_ref as R
+    from tests.helpers import make_cfg, make_model
+
+    bonds, _, _, _ = _stats_tables()
+    cfg = make_cfg(num_blocks=2, rc=20.0)
+    sd = R.random_state_dict(cfg, seed=41)
+    confs = _md_config()
+    runs = []
+    for fused in (True, False):
+        schnet = make_model(cfg, sd).train()
+        model = nn.SumOut(torch.nn.ModuleDict({
+            "SchNet": nn.GradientsOut(schnet),
+            "bonds": nn.GradientsOut(nn.HarmonicBonds(bonds))})).cuda().train()
+        if not fused:
+            model._outputs_independent = lambda: False
+        data = collate(confs).to("cuda")
+        out = model(data)
+        loss = (out.out["forces"] ** 2).mean() + out.out["energy"].sum()
+        loss.backward()
+        runs.append((out.out["energy"].detach(), out.out["forces"].detach(),
+                     [p.grad.clone() for p in schnet.parameters() if p.grad is not None]))
+    (e1, f1, g1), (e2, f2, g2) = runs
+    assert torch.equal(e1, e2) and torch.equal(f1, f2)
+    assert len(g1) == len(g2) and len(g1) > 0
+    for a, c in zip(g1, g2):
+        assert torch.equal(a, c)
 
 
 def test_radius_graph_capacity_mode():
