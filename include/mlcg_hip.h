@@ -595,7 +595,8 @@ int mlcg_prior_num_params(int kind, int n_degs);
 /* Per interaction m (index_mapping [order, mapping_stride] int64, bead
  * index_mapping[s][m] in slot s; params [M, n_params] float32):
  *   energy[m]            the interaction energy,
- *   slot_forces[m, s, :] the force -dU_m/dpos on the bead of slot s.
+ *   slot_forces[m, s, :] the force -dU_m/dpos on the bead of slot s
+ *                        (slot_forces may be NULL: energies only).
  * Replaces the forward of HarmonicBonds / HarmonicAngles
  * (src/mlcg/nn/prior/harmonic.py:90-120,199-298), Dihedral / FourierSeries
  * (src/mlcg/nn/prior/fourier_series.py:120-198,446-483) and Repulsion
@@ -615,6 +616,25 @@ int mlcg_prior_terms(int kind, int n_degs, const float* pos,
 int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
                              const int32_t* bead_slots, int64_t n_nodes,
                              int accumulate, float* forces, void* stream);
+
+/* Direct per-bead forces of an order-2 prior whose slot forces need only the
+ * two positions and one parameter (MLCG_PRIOR_REPULSION), without the slot
+ * force arrays: mlcg_prior_pair_records writes, for each position s of
+ * bead_slots (n_slots = 2 M), the record {partner bead | k << 31, params[m][0]}
+ * of slot 2m + k (records: n_slots x 2 int32; once per topology and parameter
+ * table), and mlcg_prior_repulsion_forces sets or adds forces[a] from the
+ * records of bead a over the same CSR bead_ptr.  The result is bit-identical
+ * to mlcg_prior_terms(MLCG_PRIOR_REPULSION) followed by
+ * mlcg_prior_gather_forces.  Replaces the autograd position gradient of
+ * Repulsion (src/mlcg/nn/prior/repulsion.py:136-140 under
+ * src/mlcg/nn/gradients.py:208-226). */
+int mlcg_prior_pair_records(const int64_t* index_mapping, int64_t mapping_stride,
+                            int64_t n_interactions, const float* params, int n_params,
+                            const int32_t* bead_slots, int64_t n_slots, void* records,
+                            void* stream);
+int mlcg_prior_repulsion_forces(const float* pos, const void* records,
+                                const int32_t* bead_ptr, int64_t n_nodes, int accumulate,
+                                float* forces, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Langevin BAOAB                                                          */

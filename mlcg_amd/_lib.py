@@ -96,6 +96,8 @@ _SIGNATURES = {
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
     "mlcg_prior_gather_forces": [_P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_prior_pair_records": [_P, _I64, _I64, _P, _I32, _P, _I64, _P, _P],
+    "mlcg_prior_repulsion_forces": [_P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_langevin_baoa": [_P, _P, _P, _P, _P, _I64, _F32, _F32, _F32, _U64, _P, _P, _P],
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],

@@ -16,6 +16,16 @@
 // ascending slot order, so the force reduction is deterministic and needs no
 // atomics.  Per-frame energies use the segmented sum of cfconv.hip.
 //
+// The repulsion prior gives every bead a few hundred slots, so its slot
+// forces (24 bytes per interaction written, 12 per slot read back) cost more
+// than the arithmetic.  Its forces also have a direct form: pair_records_kernel
+// lists, in the bead -> slot CSR order, each slot's partner bead, role (bead 0
+// or 1 of the interaction) and sigma (once per topology and parameter table),
+// and repulsion_forces_kernel evaluates each slot's force from the two
+// positions with the operations of prior_terms_kernel and adds them in
+// prior_gather_kernel's order, so the forces are the same bit for bit while
+// the terms kernel writes energies only.
+//
 // Torsion: with rij = pi - pj, rkj = pk - pj, rkl = pk - pl, m = rij x rkj,
 // n = rkj x rkl, the reference's atan2(-y, x) equals
 //   t = atan2(|rkj| (rij . n), m . n),
@@ -86,8 +96,10 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const double dUdr = 2.0 * k * dr;
       const D3 fi = scl(dUdr / r, d);  // force on bead 0; bead 1 gets -fi
       energy[m] = (float)(k * (dr * dr) + v0);
-      st3(slot_f, 2 * m, fi);
-      st3(slot_f, 2 * m + 1, scl(-1.0, fi));
+      if (slot_f) {
+        st3(slot_f, 2 * m, fi);
+        st3(slot_f, 2 * m + 1, scl(-1.0, fi));
+      }
     } else if (KIND == MLCG_PRIOR_REPULSION) {
       const V3 pi = ld3(pos, map[m]);
       const V3 pj = ld3(pos, map[stride + m]);
@@ -99,8 +111,10 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const float dUdr = -6.0f * e / r;
       const V3 fi = scl(dUdr / r, d);
       energy[m] = e;
-      st3(slot_f, 2 * m, fi);
-      st3(slot_f, 2 * m + 1, scl(-1.0f, fi));
+      if (slot_f) {
+        st3(slot_f, 2 * m, fi);
+        st3(slot_f, 2 * m + 1, scl(-1.0f, fi));
+      }
     } else if (KIND == MLCG_PRIOR_ANGLE) {
       // fp64 for the same reason as the bonds (k (cos t - x0)^2)
       const D3 p0 = ld3<double>(pos, map[m]);
@@ -117,9 +131,11 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const D3 dca = sub(scl(inv, b), scl(c / (na * na), a));
       const D3 dcb = sub(scl(inv, a), scl(c / (nb * nb), b));
       const D3 f0 = scl(-g, dca), f2 = scl(-g, dcb);
-      st3(slot_f, 3 * m, f0);
-      st3(slot_f, 3 * m + 1, scl(-1.0, add(f0, f2)));
-      st3(slot_f, 3 * m + 2, f2);
+      if (slot_f) {
+        st3(slot_f, 3 * m, f0);
+        st3(slot_f, 3 * m + 1, scl(-1.0, add(f0, f2)));
+        st3(slot_f, 3 * m + 2, f2);
+      }
     } else {  // MLCG_PRIOR_DIHEDRAL
       const V3 pi = ld3(pos, map[m]);
       const V3 pj = ld3(pos, map[stride + m]);
@@ -144,10 +160,12 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const float p = dot(rij, rkj) / rkj2, q = dot(rkl, rkj) / rkj2;
       const V3 sv = sub(scl(p, fi), scl(q, fl));
       const V3 fj = sub(fi, sv), fk = add(fl, sv);
-      st3(slot_f, 4 * m, fi);
-      st3(slot_f, 4 * m + 1, scl(-1.0f, fj));
-      st3(slot_f, 4 * m + 2, scl(-1.0f, fk));
-      st3(slot_f, 4 * m + 3, fl);
+      if (slot_f) {
+        st3(slot_f, 4 * m, fi);
+        st3(slot_f, 4 * m + 1, scl(-1.0f, fj));
+        st3(slot_f, 4 * m + 2, scl(-1.0f, fk));
+        st3(slot_f, 4 * m + 3, fl);
+      }
     }
   }
 }
@@ -184,6 +202,75 @@ __global__ __launch_bounds__(256) void prior_gather_kernel(
       fz += __shfl_xor(fz, o, kGatherLanes);
     }
     if (sub == 0) {
+      if (accumulate) {
+        forces[3 * a] += fx;
+        forces[3 * a + 1] += fy;
+        forces[3 * a + 2] += fz;
+      } else {
+        forces[3 * a] = fx;
+        forces[3 * a + 1] = fy;
+        forces[3 * a + 2] = fz;
+      }
+    }
+  }
+}
+
+// Bead-major records of an order-2 prior: position s of bead_slots (slot
+// 2m + k of interaction m) gets {partner bead | k << 31, params[m][0]}.
+__global__ __launch_bounds__(256) void pair_records_kernel(
+    const int64_t* __restrict__ map, int64_t stride, const float* __restrict__ params,
+    int n_params, const int32_t* __restrict__ bead_slots, int64_t n_slots,
+    int2* __restrict__ rec) {
+  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < n_slots;
+       s += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t slot = bead_slots[s];
+    const int64_t m = slot >> 1;
+    const int k = slot & 1;
+    const int64_t partner = map[(1 - k) * stride + m];
+    rec[s] = int2{(int)((uint32_t)partner | ((uint32_t)k << 31)), __float_as_int(params[m * n_params])};
+  }
+}
+
+// forces[a] (+)= the repulsion slot forces of bead a, each evaluated from the
+// positions as prior_terms_kernel<MLCG_PRIOR_REPULSION> does (bead 0 of the
+// interaction gets fi, bead 1 gets -fi) and added in prior_gather_kernel's
+// lane order and butterfly.  The products of the force are rounded on their
+// own (__fmul_rn), as when they were stored, before they are added.
+__global__ __launch_bounds__(256) void repulsion_forces_kernel(
+    const float* __restrict__ pos, const int2* __restrict__ rec,
+    const int32_t* __restrict__ bead_ptr, int64_t n, int accumulate, float* __restrict__ forces) {
+  const int lk = threadIdx.x % kGatherLanes;
+  const int64_t ngroups = (int64_t)gridDim.x * blockDim.x / kGatherLanes;
+  for (int64_t a = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kGatherLanes; a < n;
+       a += ngroups) {
+    float fx = 0.f, fy = 0.f, fz = 0.f;
+    const V3 pa = ld3(pos, a);
+    const int32_t s1 = bead_ptr[a + 1];
+    for (int32_t s = bead_ptr[a] + lk; s < s1; s += kGatherLanes) {
+      const int2 rc = rec[s];
+      const bool second = rc.x < 0;  // bit 31: the bead is bead 1 of the interaction
+      const V3 pb = ld3(pos, (int64_t)(rc.x & 0x7fffffff));
+      const V3 pi = second ? pb : pa, pj = second ? pa : pb;
+      const V3 d = sub(pj, pi);
+      const float r = sqrtf(dot(d, d));
+      const float sr = __int_as_float(rc.y) / r;
+      const float rr = sr * sr;
+      const float e = rr * rr * rr;
+      const float dUdr = -6.0f * e / r;
+      const float c = dUdr / r;
+      V3 f{__fmul_rn(c, d.x), __fmul_rn(c, d.y), __fmul_rn(c, d.z)};
+      if (second) f = V3{-f.x, -f.y, -f.z};
+      fx += f.x;
+      fy += f.y;
+      fz += f.z;
+    }
+#pragma unroll
+    for (int o = kGatherLanes / 2; o > 0; o >>= 1) {
+      fx += __shfl_xor(fx, o, kGatherLanes);
+      fy += __shfl_xor(fy, o, kGatherLanes);
+      fz += __shfl_xor(fz, o, kGatherLanes);
+    }
+    if (lk == 0) {
       if (accumulate) {
         forces[3 * a] += fx;
         forces[3 * a + 1] += fy;
@@ -240,7 +327,7 @@ extern "C" int mlcg_prior_terms(int kind, int n_degs, const float* pos,
   MLCG_REQUIRE(kind != MLCG_PRIOR_DIHEDRAL || (n_degs >= 1 && n_degs <= 64));
   MLCG_REQUIRE(n_params == params_of(kind, n_degs));
   if (n_interactions == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && index_mapping && params && energy && slot_forces);
+  MLCG_REQUIRE(pos && index_mapping && params && energy);
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_interactions, 256), 8);
   hipStream_t s = mlcg_stream(stream);
   switch (kind) {
@@ -278,5 +365,33 @@ extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t*
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes * kGatherLanes, 256), 8);
   hipLaunchKernelGGL(prior_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
                      slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces);
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_prior_pair_records(const int64_t* index_mapping, int64_t mapping_stride,
+                                       int64_t n_interactions, const float* params,
+                                       int n_params, const int32_t* bead_slots,
+                                       int64_t n_slots, void* records, void* stream) {
+  MLCG_REQUIRE(n_interactions >= 0 && mapping_stride >= n_interactions && n_params >= 1);
+  MLCG_REQUIRE(n_slots == 2 * n_interactions && n_interactions < (int64_t(1) << 30));
+  if (n_slots == 0) return MLCG_OK;
+  MLCG_REQUIRE(index_mapping && params && bead_slots && records);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_slots, 256), 8);
+  hipLaunchKernelGGL(pair_records_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
+                     index_mapping, mapping_stride, params, n_params, bead_slots, n_slots,
+                     reinterpret_cast<int2*>(records));
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_prior_repulsion_forces(const float* pos, const void* records,
+                                           const int32_t* bead_ptr, int64_t n_nodes,
+                                           int accumulate, float* forces, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31));
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && bead_ptr && forces);
+  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes * kGatherLanes, 256), 8);
+  hipLaunchKernelGGL(repulsion_forces_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
+                     pos, reinterpret_cast<const int2*>(records), bead_ptr, n_nodes, accumulate,
+                     forces);
   return mlcg_launch_status();
 }

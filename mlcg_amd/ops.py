@@ -1126,6 +1126,9 @@ class PriorGraph:
                     bead and ascending within a bead
     seg_ptr       : [B + 1] int64, interactions of frame b are
                     seg_ptr[b] : seg_ptr[b + 1] (mapping_batch is sorted)
+    pair_records  : (params, params version, [M * 2, 2] int32) -- the
+                    bead-major slot records of the direct repulsion forces,
+                    made for that parameter matrix (prior_pair_records)
     """
 
     index_mapping: torch.Tensor
@@ -1134,6 +1137,7 @@ class PriorGraph:
     seg_ptr: torch.Tensor
     num_nodes: int
     num_frames: int
+    pair_records: Optional[tuple] = None
 
     @property
     def num_interactions(self) -> int:
@@ -1188,15 +1192,46 @@ def prior_terms(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
     return energy, slot_f
 
 
+def prior_pair_records(graph: PriorGraph, params: torch.Tensor) -> torch.Tensor:
+    """[M * 2, 2] int32 bead-major records {partner | role << 31, sigma} of a
+    repulsion interaction list (mlcg_prior_pair_records), cached on the graph
+    for the parameter matrix they were made from (the same tensor at the same
+    version: the prior modules hand out one cached matrix per topology)."""
+    c = graph.pair_records
+    if c is not None and c[0] is params and c[1] == params._version:
+        return c[2]
+    M = graph.num_interactions
+    rec = torch.empty(2 * M, 2, dtype=torch.int32, device=params.device)
+    call("mlcg_prior_pair_records", ptr(graph.index_mapping), M, M, ptr(params),
+         params.shape[1], ptr(graph.bead_slots), 2 * M, ptr(rec), stream_handle(params.device))
+    graph.pair_records = (params, params._version, rec)
+    return rec
+
+
 def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
                         params: torch.Tensor, forces: Optional[torch.Tensor] = None):
     """Per-frame energies [B] and forces [N, 3] of one prior; with `forces`
-    given the forces are added to it in place."""
-    energy, slot_f = prior_terms(kind, n_degs, pos, graph, params)
-    E = segment_sum(energy, graph.seg_ptr)
+    given the forces are added to it in place.  The repulsion prior takes its
+    forces straight from the positions per bead (mlcg_prior_repulsion_forces,
+    the same values as the slot-force path) and writes energies only."""
     accumulate = forces is not None
     if forces is None:
         forces = torch.empty(graph.num_nodes, 3, dtype=torch.float32, device=pos.device)
+    if kind == PRIOR_KIND["repulsion"]:
+        pos = _validate_pos(pos)
+        M = graph.num_interactions
+        params = params.to(torch.float32).contiguous()
+        _check(tuple(params.shape) == (M, 1), f"params must be [{M}, 1], got {tuple(params.shape)}")
+        rec = prior_pair_records(graph, params)
+        energy = torch.empty(M, dtype=torch.float32, device=pos.device)
+        s = stream_handle(pos.device)
+        call("mlcg_prior_terms", kind, n_degs, ptr(pos), ptr(graph.index_mapping), M, M,
+             ptr(params), 1, ptr(energy), None, s)
+        call("mlcg_prior_repulsion_forces", ptr(pos), ptr(rec), ptr(graph.bead_ptr),
+             graph.num_nodes, int(accumulate), ptr(forces), s)
+        return segment_sum(energy, graph.seg_ptr), forces
+    energy, slot_f = prior_terms(kind, n_degs, pos, graph, params)
+    E = segment_sum(energy, graph.seg_ptr)
     call("mlcg_prior_gather_forces", ptr(slot_f), ptr(graph.bead_ptr), ptr(graph.bead_slots),
          graph.num_nodes, int(accumulate), ptr(forces), stream_handle(pos.device))
     return E, forces

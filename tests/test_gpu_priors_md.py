@@ -74,6 +74,43 @@ def test_prior_kernel_vs_oracle(kind):
     assert torch.allclose(F2, F + 1.0, rtol=1e-6, atol=1e-6)
 
 
+def test_repulsion_direct_forces_bit_identical_to_slot_forces():
+    """The repulsion prior's per-bead direct forces (mlcg_prior_pair_records +
+    mlcg_prior_repulsion_forces) equal the slot-force path (mlcg_prior_terms
+    with slot forces + mlcg_prior_gather_forces) bit for bit at config-5 size,
+    set and accumulate modes, and follow an in-place change of the parameter
+    matrix (the cached records are rebuilt for the new version)."""
+    from mlcg_amd import _lib, ops
+
+    n_frames, n = 100, 268
+    pos = _chain_batch(n_frames, n, seed=11).cuda()
+    mapping, mb = P.chain_topology(n_frames, n)["repulsion"]
+    M = mapping.shape[1]
+    g = ops.prior_graph(mapping.cuda(), mb.cuda(), pos.shape[0], n_frames)
+    gen = torch.Generator().manual_seed(4)
+    params = (3.5 + torch.rand(M, 1, generator=gen)).cuda()
+    kind = ops.PRIOR_KIND["repulsion"]
+
+    def slot_path(F0=None):
+        energy, slot_f = ops.prior_terms(kind, 0, pos, g, params)
+        out = torch.empty(n_frames * n, 3, device="cuda") if F0 is None else F0.clone()
+        _lib.call("mlcg_prior_gather_forces", _lib.ptr(slot_f), _lib.ptr(g.bead_ptr),
+                  _lib.ptr(g.bead_slots), g.num_nodes, int(F0 is not None), _lib.ptr(out),
+                  _lib.stream_handle(pos.device))
+        return ops.segment_sum(energy, g.seg_ptr), out
+
+    for rnd in range(2):
+        E_ref, F_ref = slot_path()
+        E, F = ops.prior_energy_forces(kind, 0, pos, g, params)
+        assert torch.equal(E, E_ref) and torch.equal(F, F_ref), rnd
+        F0 = torch.randn(n_frames * n, 3, device="cuda")
+        _, Fa_ref = slot_path(F0)
+        _, Fa = ops.prior_energy_forces(kind, 0, pos, g, params, forces=F0.clone())
+        assert torch.equal(Fa, Fa_ref), rnd
+        print("round", rnd, "max|F|", float(F.abs().max()))
+        params.mul_(1.05)  # new version: the records must be made again
+
+
 def _stats_tables():
     bonds = {(a, b): {"x_0": 3.8 + 0.01 * (a + b), "k": 100.0 - a} for a in range(1, 6)
              for b in range(1, 6)}
