@@ -617,24 +617,28 @@ int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
                              const int32_t* bead_slots, int64_t n_nodes,
                              int accumulate, float* forces, void* stream);
 
-/* Direct per-bead forces of an order-2 prior whose slot forces need only the
- * two positions and one parameter (MLCG_PRIOR_REPULSION), without the slot
- * force arrays: mlcg_prior_pair_records writes, for each position s of
- * bead_slots (n_slots = 2 M), the record {partner bead | k << 31, params[m][0]}
- * of slot 2m + k (records: n_slots x 2 int32; once per topology and parameter
- * table), and mlcg_prior_repulsion_forces sets or adds forces[a] from the
- * records of bead a over the same CSR bead_ptr.  The result is bit-identical
- * to mlcg_prior_terms(MLCG_PRIOR_REPULSION) followed by
- * mlcg_prior_gather_forces.  Replaces the autograd position gradient of
- * Repulsion (src/mlcg/nn/prior/repulsion.py:136-140 under
- * src/mlcg/nn/gradients.py:208-226). */
+/* The repulsion prior (MLCG_PRIOR_REPULSION) in one call, without slot force
+ * arrays: energy[m] of every interaction (as mlcg_prior_terms) and forces[a]
+ * set or added (accumulate != 0) per bead straight from the positions.
+ * mlcg_prior_pair_records fills `records` (mlcg_prior_pair_records_ints int32
+ * values; once per topology and parameter table): for each position s of
+ * bead_slots the record {partner bead | k << 31, params[m][0]} of slot 2m + k,
+ * followed by the bead windows the kernels stage in LDS (the range of beads
+ * that each block of 16 beads and each chunk of 1024 interactions touches).
+ * mlcg_prior_repulsion reads them over the same CSR bead_ptr.  Energies and
+ * forces are bit-identical to mlcg_prior_terms(MLCG_PRIOR_REPULSION) followed
+ * by mlcg_prior_gather_forces.  Replaces Repulsion.forward
+ * (src/mlcg/nn/prior/repulsion.py:111-140) with the autograd position
+ * gradient of src/mlcg/nn/gradients.py:208-226. */
+int64_t mlcg_prior_pair_records_ints(int64_t n_nodes, int64_t n_interactions);
 int mlcg_prior_pair_records(const int64_t* index_mapping, int64_t mapping_stride,
                             int64_t n_interactions, const float* params, int n_params,
-                            const int32_t* bead_slots, int64_t n_slots, void* records,
-                            void* stream);
-int mlcg_prior_repulsion_forces(const float* pos, const void* records,
-                                const int32_t* bead_ptr, int64_t n_nodes, int accumulate,
-                                float* forces, void* stream);
+                            const int32_t* bead_ptr, const int32_t* bead_slots,
+                            int64_t n_nodes, void* records, void* stream);
+int mlcg_prior_repulsion(const float* pos, int64_t n_nodes, const int64_t* index_mapping,
+                         int64_t mapping_stride, int64_t n_interactions, const float* params,
+                         const void* records, const int32_t* bead_ptr, float* energy,
+                         int accumulate, float* forces, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Langevin BAOAB                                                          */

@@ -96,8 +96,9 @@ _SIGNATURES = {
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
     "mlcg_prior_gather_forces": [_P, _P, _P, _I64, _I32, _P, _P],
-    "mlcg_prior_pair_records": [_P, _I64, _I64, _P, _I32, _P, _I64, _P, _P],
-    "mlcg_prior_repulsion_forces": [_P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_prior_pair_records_ints": [_I64, _I64],
+    "mlcg_prior_pair_records": [_P, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _P],
+    "mlcg_prior_repulsion": [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P],
     "mlcg_langevin_baoa": [_P, _P, _P, _P, _P, _I64, _F32, _F32, _F32, _U64, _P, _P, _P],
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
@@ -119,7 +120,7 @@ _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,
              "mlcg_type_sum_workspace_floats": _I64, "mlcg_node_weight_image_bytes": _I64,
-             "mlcg_mse_workspace_floats": _I64}
+             "mlcg_mse_workspace_floats": _I64, "mlcg_prior_pair_records_ints": _I64}
 
 STATUS = {
     0: "MLCG_OK",

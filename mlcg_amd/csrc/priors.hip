@@ -58,9 +58,12 @@ template <typename T>
 __device__ __forceinline__ V3T<T> scl(T s, V3T<T> a) {
   return V3T<T>{s * a.x, s * a.y, s * a.z};
 }
+// Fused multiply-adds in a fixed order: left to the compiler, the contraction
+// of a sum of products follows the surrounding code, and the repulsion forces
+// of prior_terms_kernel and repulsion_forces_kernel must round alike.
 template <typename T>
 __device__ __forceinline__ T dot(V3T<T> a, V3T<T> b) {
-  return a.x * b.x + a.y * b.y + a.z * b.z;
+  return fma(a.z, b.z, fma(a.y, b.y, a.x * b.x));
 }
 template <typename T>
 __device__ __forceinline__ V3T<T> cross(V3T<T> a, V3T<T> b) {
@@ -231,29 +234,121 @@ __global__ __launch_bounds__(256) void pair_records_kernel(
   }
 }
 
+// The repulsion kernels look up a random partner bead per slot; fetched from
+// the L2 these lookups (one request each) and not the bytes set their time,
+// so each workgroup stages the positions of the bead window its work touches
+// in LDS first.  Windows are computed with the records (once per topology):
+// for a force block of kRepBeads beads the range of the beads and all their
+// partners, for an energy chunk of kRepChunk interactions the range of their
+// beads.  A window wider than kRepWin beads is served from global memory.
+constexpr int kRepBeads = 256 / kGatherLanes;  // beads per force workgroup
+constexpr int kRepU = 4;                       // interactions per energy thread
+constexpr int kRepChunk = 256 * kRepU;         // interactions per energy workgroup
+constexpr int kRepWin = 1024;                  // LDS window, beads (16 KiB)
+
+__device__ __forceinline__ int2 block_minmax(int lo, int hi, int* red) {
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, __shfl_xor(lo, o, MLCG_WAVE));
+    hi = max(hi, __shfl_xor(hi, o, MLCG_WAVE));
+  }
+  const int w = threadIdx.x / MLCG_WAVE;
+  if (mlcg_lane() == 0) {
+    red[2 * w] = lo;
+    red[2 * w + 1] = hi;
+  }
+  __syncthreads();
+  lo = red[0];
+  hi = red[1];
+  for (int k = 1; k < (int)blockDim.x / MLCG_WAVE; ++k) {
+    lo = min(lo, red[2 * k]);
+    hi = max(hi, red[2 * k + 1]);
+  }
+  return int2{lo, hi + 1};
+}
+
+__global__ __launch_bounds__(256) void force_windows_kernel(const int2* __restrict__ rec,
+                                                            const int32_t* __restrict__ bead_ptr,
+                                                            int64_t n, int2* __restrict__ win) {
+  __shared__ int red[8];
+  const int64_t a0 = (int64_t)blockIdx.x * kRepBeads;
+  const int64_t a1 = min(a0 + kRepBeads, n);
+  int lo = (int)a0, hi = (int)(a1 - 1);
+  for (int32_t s = bead_ptr[a0] + threadIdx.x; s < bead_ptr[a1]; s += blockDim.x) {
+    const int b = rec[s].x & 0x7fffffff;
+    lo = min(lo, b);
+    hi = max(hi, b);
+  }
+  const int2 w = block_minmax(lo, hi, red);
+  if (threadIdx.x == 0) win[blockIdx.x] = w;
+}
+
+__global__ __launch_bounds__(256) void energy_windows_kernel(const int64_t* __restrict__ map,
+                                                             int64_t stride, int64_t M,
+                                                             int2* __restrict__ win) {
+  __shared__ int red[8];
+  int lo = INT_MAX, hi = -1;
+  for (int64_t m = (int64_t)blockIdx.x * kRepChunk + threadIdx.x;
+       m < min((int64_t)(blockIdx.x + 1) * kRepChunk, M); m += blockDim.x) {
+    const int bi = (int)map[m], bj = (int)map[stride + m];
+    lo = min(lo, min(bi, bj));
+    hi = max(hi, max(bi, bj));
+  }
+  const int2 w = block_minmax(lo, hi, red);
+  if (threadIdx.x == 0) win[blockIdx.x] = w;
+}
+
+// Window positions into LDS (4 floats a bead); false when the window is too
+// wide, and then nothing is staged.  Every thread of the workgroup calls it.
+__device__ __forceinline__ bool stage_window(const float* __restrict__ pos, int2 w, float4* P) {
+  const int cnt = w.y - w.x;
+  if (cnt > kRepWin || cnt <= 0) return false;
+  for (int k = threadIdx.x; k < cnt; k += blockDim.x) {
+    const int64_t b = (int64_t)w.x + k;
+    P[k] = float4{pos[3 * b], pos[3 * b + 1], pos[3 * b + 2], 0.f};
+  }
+  __syncthreads();
+  return true;
+}
+
+__device__ __forceinline__ V3 pos_at(const float* __restrict__ pos, const float4* P, bool staged,
+                                     int lo, int64_t b) {
+  if (staged) {
+    const float4 v = P[b - lo];
+    return V3{v.x, v.y, v.z};
+  }
+  return ld3(pos, b);
+}
+
 // forces[a] (+)= the repulsion slot forces of bead a, each evaluated from the
 // positions as prior_terms_kernel<MLCG_PRIOR_REPULSION> does (bead 0 of the
 // interaction gets fi, bead 1 gets -fi) and added in prior_gather_kernel's
 // lane order and butterfly.  The products of the force are rounded on their
 // own (__fmul_rn), as when they were stored, before they are added.
 __global__ __launch_bounds__(256) void repulsion_forces_kernel(
-    const float* __restrict__ pos, const int2* __restrict__ rec,
+    const float* __restrict__ pos, const int2* __restrict__ rec, const int2* __restrict__ win,
     const int32_t* __restrict__ bead_ptr, int64_t n, int accumulate, float* __restrict__ forces) {
+  __shared__ float4 P[kRepWin];
+  const int2 w = win[blockIdx.x];
+  const bool staged = stage_window(pos, w, P);
   const int lk = threadIdx.x % kGatherLanes;
-  const int64_t ngroups = (int64_t)gridDim.x * blockDim.x / kGatherLanes;
-  for (int64_t a = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kGatherLanes; a < n;
-       a += ngroups) {
-    float fx = 0.f, fy = 0.f, fz = 0.f;
-    const V3 pa = ld3(pos, a);
-    const int32_t s1 = bead_ptr[a + 1];
-    for (int32_t s = bead_ptr[a] + lk; s < s1; s += kGatherLanes) {
-      const int2 rc = rec[s];
-      const bool second = rc.x < 0;  // bit 31: the bead is bead 1 of the interaction
-      const V3 pb = ld3(pos, (int64_t)(rc.x & 0x7fffffff));
+  const int64_t a = (int64_t)blockIdx.x * kRepBeads + threadIdx.x / kGatherLanes;
+  if (a >= n) return;
+  float fx = 0.f, fy = 0.f, fz = 0.f;
+  const V3 pa = pos_at(pos, P, staged, w.x, a);
+  const int32_t s1 = bead_ptr[a + 1];
+  for (int32_t s = bead_ptr[a] + lk; s < s1; s += kRepU * kGatherLanes) {
+    int2 rc[kRepU];  // the records of kRepU slots requested together
+#pragma unroll
+    for (int u = 0; u < kRepU; ++u) rc[u] = rec[min(s + u * kGatherLanes, s1 - 1)];
+#pragma unroll
+    for (int u = 0; u < kRepU; ++u) {
+      if (s + u * kGatherLanes >= s1) break;
+      const bool second = rc[u].x < 0;  // bit 31: the bead is bead 1 of the interaction
+      const V3 pb = pos_at(pos, P, staged, w.x, rc[u].x & 0x7fffffff);
       const V3 pi = second ? pb : pa, pj = second ? pa : pb;
       const V3 d = sub(pj, pi);
       const float r = sqrtf(dot(d, d));
-      const float sr = __int_as_float(rc.y) / r;
+      const float sr = __int_as_float(rc[u].y) / r;
       const float rr = sr * sr;
       const float e = rr * rr * rr;
       const float dUdr = -6.0f * e / r;
@@ -264,23 +359,55 @@ __global__ __launch_bounds__(256) void repulsion_forces_kernel(
       fy += f.y;
       fz += f.z;
     }
+  }
+  // the 16 lanes of a bead are in one wave and active together
 #pragma unroll
-    for (int o = kGatherLanes / 2; o > 0; o >>= 1) {
-      fx += __shfl_xor(fx, o, kGatherLanes);
-      fy += __shfl_xor(fy, o, kGatherLanes);
-      fz += __shfl_xor(fz, o, kGatherLanes);
+  for (int o = kGatherLanes / 2; o > 0; o >>= 1) {
+    fx += __shfl_xor(fx, o, kGatherLanes);
+    fy += __shfl_xor(fy, o, kGatherLanes);
+    fz += __shfl_xor(fz, o, kGatherLanes);
+  }
+  if (lk == 0) {
+    if (accumulate) {
+      forces[3 * a] += fx;
+      forces[3 * a + 1] += fy;
+      forces[3 * a + 2] += fz;
+    } else {
+      forces[3 * a] = fx;
+      forces[3 * a + 1] = fy;
+      forces[3 * a + 2] = fz;
     }
-    if (lk == 0) {
-      if (accumulate) {
-        forces[3 * a] += fx;
-        forces[3 * a + 1] += fy;
-        forces[3 * a + 2] += fz;
-      } else {
-        forces[3 * a] = fx;
-        forces[3 * a + 1] = fy;
-        forces[3 * a + 2] = fz;
-      }
-    }
+  }
+}
+
+// Energies of the repulsion prior only (prior_terms_kernel's operations),
+// kRepU interactions per thread.
+__global__ __launch_bounds__(256) void repulsion_energy_kernel(
+    const float* __restrict__ pos, const int64_t* __restrict__ map, int64_t stride, int64_t M,
+    const float* __restrict__ params, const int2* __restrict__ win, float* __restrict__ energy) {
+  __shared__ float4 P[kRepWin];
+  const int2 w = win[blockIdx.x];
+  int64_t bi[kRepU], bj[kRepU];
+  float sg[kRepU];
+#pragma unroll
+  for (int u = 0; u < kRepU; ++u) {  // requested before the window is staged
+    const int64_t m = min((int64_t)blockIdx.x * kRepChunk + u * 256 + threadIdx.x, M - 1);
+    bi[u] = map[m];
+    bj[u] = map[stride + m];
+    sg[u] = params[m];
+  }
+  const bool staged = stage_window(pos, w, P);
+#pragma unroll
+  for (int u = 0; u < kRepU; ++u) {
+    const int64_t m = (int64_t)blockIdx.x * kRepChunk + u * 256 + threadIdx.x;
+    if (m >= M) break;
+    const V3 pi = pos_at(pos, P, staged, w.x, bi[u]);
+    const V3 pj = pos_at(pos, P, staged, w.x, bj[u]);
+    const V3 d = sub(pj, pi);
+    const float r = sqrtf(dot(d, d));
+    const float sr = sg[u] / r;
+    const float rr = sr * sr;
+    energy[m] = rr * rr * rr;
   }
 }
 
@@ -368,30 +495,62 @@ extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t*
   return mlcg_launch_status();
 }
 
+namespace {
+int64_t rep_force_blocks(int64_t n) { return (n + kRepBeads - 1) / kRepBeads; }
+int64_t rep_energy_chunks(int64_t M) { return (M + kRepChunk - 1) / kRepChunk; }
+}  // namespace
+
+extern "C" int64_t mlcg_prior_pair_records_ints(int64_t n_nodes, int64_t n_interactions) {
+  if (n_nodes < 0 || n_interactions < 0) return -1;
+  return 4 * n_interactions + 2 * rep_force_blocks(n_nodes) + 2 * rep_energy_chunks(n_interactions);
+}
+
 extern "C" int mlcg_prior_pair_records(const int64_t* index_mapping, int64_t mapping_stride,
                                        int64_t n_interactions, const float* params,
-                                       int n_params, const int32_t* bead_slots,
-                                       int64_t n_slots, void* records, void* stream) {
+                                       int n_params, const int32_t* bead_ptr,
+                                       const int32_t* bead_slots, int64_t n_nodes,
+                                       void* records, void* stream) {
   MLCG_REQUIRE(n_interactions >= 0 && mapping_stride >= n_interactions && n_params >= 1);
-  MLCG_REQUIRE(n_slots == 2 * n_interactions && n_interactions < (int64_t(1) << 30));
-  if (n_slots == 0) return MLCG_OK;
-  MLCG_REQUIRE(index_mapping && params && bead_slots && records);
-  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_slots, 256), 8);
-  hipLaunchKernelGGL(pair_records_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
-                     index_mapping, mapping_stride, params, n_params, bead_slots, n_slots,
-                     reinterpret_cast<int2*>(records));
+  MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31) && n_interactions < (int64_t(1) << 30));
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(bead_ptr && records);
+  MLCG_REQUIRE(n_interactions == 0 || (index_mapping && params && bead_slots));
+  hipStream_t s = mlcg_stream(stream);
+  int2* rec = reinterpret_cast<int2*>(records);
+  int2* fwin = rec + 2 * n_interactions;
+  int2* ewin = fwin + rep_force_blocks(n_nodes);
+  const int64_t n_slots = 2 * n_interactions;
+  if (n_slots > 0)
+    hipLaunchKernelGGL(pair_records_kernel, dim3(mlcg_persistent_groups(mlcg_div_up(n_slots, 256), 8)),
+                       dim3(256), 0, s, index_mapping, mapping_stride, params, n_params,
+                       bead_slots, n_slots, rec);
+  hipLaunchKernelGGL(force_windows_kernel, dim3((unsigned)rep_force_blocks(n_nodes)), dim3(256),
+                     0, s, rec, bead_ptr, n_nodes, fwin);
+  if (n_interactions > 0)
+    hipLaunchKernelGGL(energy_windows_kernel, dim3((unsigned)rep_energy_chunks(n_interactions)),
+                       dim3(256), 0, s, index_mapping, mapping_stride, n_interactions, ewin);
   return mlcg_launch_status();
 }
 
-extern "C" int mlcg_prior_repulsion_forces(const float* pos, const void* records,
-                                           const int32_t* bead_ptr, int64_t n_nodes,
-                                           int accumulate, float* forces, void* stream) {
+extern "C" int mlcg_prior_repulsion(const float* pos, int64_t n_nodes,
+                                    const int64_t* index_mapping, int64_t mapping_stride,
+                                    int64_t n_interactions, const float* params,
+                                    const void* records, const int32_t* bead_ptr, float* energy,
+                                    int accumulate, float* forces, void* stream) {
   MLCG_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 31));
+  MLCG_REQUIRE(n_interactions >= 0 && mapping_stride >= n_interactions);
   if (n_nodes == 0) return MLCG_OK;
-  MLCG_REQUIRE(pos && bead_ptr && forces);
-  const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes * kGatherLanes, 256), 8);
-  hipLaunchKernelGGL(repulsion_forces_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
-                     pos, reinterpret_cast<const int2*>(records), bead_ptr, n_nodes, accumulate,
-                     forces);
+  MLCG_REQUIRE(pos && bead_ptr && records && forces);
+  MLCG_REQUIRE(n_interactions == 0 || (index_mapping && params && energy));
+  hipStream_t s = mlcg_stream(stream);
+  const int2* rec = reinterpret_cast<const int2*>(records);
+  const int2* fwin = rec + 2 * n_interactions;
+  const int2* ewin = fwin + rep_force_blocks(n_nodes);
+  if (n_interactions > 0)
+    hipLaunchKernelGGL(repulsion_energy_kernel, dim3((unsigned)rep_energy_chunks(n_interactions)),
+                       dim3(256), 0, s, pos, index_mapping, mapping_stride, n_interactions,
+                       params, ewin, energy);
+  hipLaunchKernelGGL(repulsion_forces_kernel, dim3((unsigned)rep_force_blocks(n_nodes)),
+                     dim3(256), 0, s, pos, rec, fwin, bead_ptr, n_nodes, accumulate, forces);
   return mlcg_launch_status();
 }

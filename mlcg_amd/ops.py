@@ -1126,9 +1126,9 @@ class PriorGraph:
                     bead and ascending within a bead
     seg_ptr       : [B + 1] int64, interactions of frame b are
                     seg_ptr[b] : seg_ptr[b + 1] (mapping_batch is sorted)
-    pair_records  : (params, params version, [M * 2, 2] int32) -- the
-                    bead-major slot records of the direct repulsion forces,
-                    made for that parameter matrix (prior_pair_records)
+    pair_records  : (params, params version, int32 records) -- the bead-major
+                    slot records and bead windows of the direct repulsion
+                    path, made for that parameter matrix (prior_pair_records)
     """
 
     index_mapping: torch.Tensor
@@ -1193,17 +1193,20 @@ def prior_terms(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
 
 
 def prior_pair_records(graph: PriorGraph, params: torch.Tensor) -> torch.Tensor:
-    """[M * 2, 2] int32 bead-major records {partner | role << 31, sigma} of a
-    repulsion interaction list (mlcg_prior_pair_records), cached on the graph
-    for the parameter matrix they were made from (the same tensor at the same
-    version: the prior modules hand out one cached matrix per topology)."""
+    """int32 records of the direct repulsion path (mlcg_prior_pair_records:
+    bead-major {partner | role << 31, sigma} per slot and the bead windows the
+    kernels stage), cached on the graph for the parameter matrix they were
+    made from (the same tensor at the same version: the prior modules hand
+    out one cached matrix per topology)."""
     c = graph.pair_records
     if c is not None and c[0] is params and c[1] == params._version:
         return c[2]
-    M = graph.num_interactions
-    rec = torch.empty(2 * M, 2, dtype=torch.int32, device=params.device)
+    M, n = graph.num_interactions, graph.num_nodes
+    size = int(_lib.load().mlcg_prior_pair_records_ints(n, M))
+    rec = torch.empty(size, dtype=torch.int32, device=params.device)
     call("mlcg_prior_pair_records", ptr(graph.index_mapping), M, M, ptr(params),
-         params.shape[1], ptr(graph.bead_slots), 2 * M, ptr(rec), stream_handle(params.device))
+         params.shape[1], ptr(graph.bead_ptr), ptr(graph.bead_slots), n, ptr(rec),
+         stream_handle(params.device))
     graph.pair_records = (params, params._version, rec)
     return rec
 
@@ -1212,8 +1215,8 @@ def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorG
                         params: torch.Tensor, forces: Optional[torch.Tensor] = None):
     """Per-frame energies [B] and forces [N, 3] of one prior; with `forces`
     given the forces are added to it in place.  The repulsion prior takes its
-    forces straight from the positions per bead (mlcg_prior_repulsion_forces,
-    the same values as the slot-force path) and writes energies only."""
+    forces straight from the positions per bead (mlcg_prior_repulsion, the
+    same values as the slot-force path, without slot force arrays)."""
     accumulate = forces is not None
     if forces is None:
         forces = torch.empty(graph.num_nodes, 3, dtype=torch.float32, device=pos.device)
@@ -1222,13 +1225,13 @@ def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorG
         M = graph.num_interactions
         params = params.to(torch.float32).contiguous()
         _check(tuple(params.shape) == (M, 1), f"params must be [{M}, 1], got {tuple(params.shape)}")
+        _check(pos.shape[0] == graph.num_nodes,
+               "pos must hold the prior graph's num_nodes beads")
         rec = prior_pair_records(graph, params)
         energy = torch.empty(M, dtype=torch.float32, device=pos.device)
-        s = stream_handle(pos.device)
-        call("mlcg_prior_terms", kind, n_degs, ptr(pos), ptr(graph.index_mapping), M, M,
-             ptr(params), 1, ptr(energy), None, s)
-        call("mlcg_prior_repulsion_forces", ptr(pos), ptr(rec), ptr(graph.bead_ptr),
-             graph.num_nodes, int(accumulate), ptr(forces), s)
+        call("mlcg_prior_repulsion", ptr(pos), graph.num_nodes, ptr(graph.index_mapping), M, M,
+             ptr(params), ptr(rec), ptr(graph.bead_ptr), ptr(energy), int(accumulate),
+             ptr(forces), stream_handle(pos.device))
         return segment_sum(energy, graph.seg_ptr), forces
     energy, slot_f = prior_terms(kind, n_degs, pos, graph, params)
     E = segment_sum(energy, graph.seg_ptr)
