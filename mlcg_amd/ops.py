@@ -614,6 +614,14 @@ def node_tmm_batch(problems, rows: int, device) -> list:
 COPY_BATCH_MAX = 8  # jobs per mlcg_copy_batch launch
 
 
+def copy_batch_ok(dsts, srcs) -> bool:
+    """Whether copy_batch takes these pairs (see there)."""
+    return len(dsts) == len(srcs) and all(
+        d.is_cuda and s_.device == d.device and d.dtype == s_.dtype and d.shape == s_.shape
+        and d.is_contiguous() and s_.is_contiguous() and d.data_ptr() % 16 == 0
+        and s_.data_ptr() % 16 == 0 for d, s_ in zip(dsts, srcs))
+
+
 def copy_batch(dsts, srcs) -> None:
     """dst.copy_(src) for every pair, device to device on the current stream,
     as one launch per eight pairs (mlcg_copy_batch).  Each pair: the same

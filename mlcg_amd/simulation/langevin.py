@@ -293,8 +293,11 @@ class LangevinSimulation:
             data.pos = x
             e, f = self.calculate_potential_and_forces(data)
             or_flags()
-            F.copy_(f)
-            epot.copy_(e)
+            if ops.copy_batch_ok([F, epot], [f, e]):
+                ops.copy_batch([F, epot], [f, e])  # one launch for both
+            else:
+                F.copy_(f)
+                epot.copy_(e)
             ops.langevin_b(v, F, m, self.dt, step=step_ctr)
 
         graph = None
