@@ -213,6 +213,37 @@ int mlcg_radius_fill_f64(const double* pos, const int64_t* batch,
                          int64_t edge_stride, int64_t* edge_index,
                          int32_t* overflow, void* stream);
 
+/* The sizing pass (mlcg_radius_rowptr without pairptr) and the write pass
+ * (as mlcg_radius_fill_f64) for float16 / bfloat16 positions given as their
+ * raw 16-bit storage [N, 3]: every operation of the membership test is
+ * computed in float and rounded to the 16-bit type (round to nearest even),
+ * r*r in double rounded to float then to the 16-bit type, the comparison in
+ * float -- the arithmetic of the reference's Half / BFloat16 instantiations
+ * (radius.cu:117-141 under the dispatch of radius.cu:243-250).  Edge list
+ * only. */
+int mlcg_radius_rowptr_f16(const uint16_t* pos, const int64_t* batch,
+                           const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                           int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                           const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                           void* workspace, int32_t* overflow, void* stream);
+int mlcg_radius_rowptr_bf16(const uint16_t* pos, const int64_t* batch,
+                            const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                            int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                            const int64_t* ptr_exclude_pair_xs, int32_t* rowptr,
+                            void* workspace, int32_t* overflow, void* stream);
+int mlcg_radius_fill_f16(const uint16_t* pos, const int64_t* batch,
+                         const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                         int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                         const int64_t* ptr_exclude_pair_xs, const int32_t* rowptr,
+                         int64_t edge_capacity, int64_t edge_stride, int64_t* edge_index,
+                         int32_t* overflow, void* stream);
+int mlcg_radius_fill_bf16(const uint16_t* pos, const int64_t* batch,
+                          const int64_t* frame_ptr, int64_t n_nodes, double r, int loop,
+                          int64_t max_num_neighbors, const int64_t* exclude_pair_xs,
+                          const int64_t* ptr_exclude_pair_xs, const int32_t* rowptr,
+                          int64_t edge_capacity, int64_t edge_stride, int64_t* edge_index,
+                          int32_t* overflow, void* stream);
+
 /* HOST function (host pointers, no stream): the reference's
  * exclusion_pair_to_ptr (exclusion_pairs.cpp:7-62).  exc_pair_index is
  * [2, num_pairs] int64, row 0 = x (the excluded neighbour), row 1 = y (the

@@ -39,6 +39,12 @@ _SIGNATURES = {
     "mlcg_radius_count_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
     "mlcg_radius_fill_f64": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
                              _P, _P],
+    "mlcg_radius_fill_f16": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
+                             _P, _P],
+    "mlcg_radius_fill_bf16": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _I64, _I64, _P,
+                              _P, _P],
+    "mlcg_radius_rowptr_f16": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
+    "mlcg_radius_rowptr_bf16": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P],
     "mlcg_exclusion_pair_to_ptr": [_P, _I64, _I64, _P, _P],
     "mlcg_radius_workspace_bytes": [_I64],
     "mlcg_radius_rowptr": [_P, _P, _P, _I64, _F64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P],

@@ -34,12 +34,51 @@
 
 namespace {
 
-// Positions are float32 or float64 (T); the membership test runs in T, as
-// the reference's kernel runs it in its scalar type (radius.cu:243-250).
+// Positions are float32, float64, float16 or bfloat16 (T); the membership
+// test runs in T, as the reference's kernel runs it in its scalar type
+// (radius.cu:243-250).
 template <typename T>
 struct Vec3T {
   T x, y, z;
 };
+
+// float16 / bfloat16 positions: every operation is computed in float and
+// rounded to the storage type (round to nearest even), which is how the
+// reference's c10::Half / c10::BFloat16 instantiation of the kernel
+// evaluates `dist += (x - y) * (x - y)` and `dist < r` (each operator
+// converts to float, operates and converts back).  float carries more than
+// twice the significand bits of both types, so each operation equals the
+// native 16-bit one (the compiler emits those); products and sums are never
+// fused, as the reference rounds each of them.
+template <typename S>
+struct Narrow {
+  S v;
+  Narrow() = default;
+  __host__ __device__ Narrow(float f) : v(static_cast<S>(f)) {}
+  __host__ __device__ operator float() const { return static_cast<float>(v); }
+};
+template <typename S>
+__device__ __forceinline__ Narrow<S> operator-(Narrow<S> a, Narrow<S> b) {
+#pragma clang fp contract(off)
+  return Narrow<S>(static_cast<float>(a) - static_cast<float>(b));
+}
+template <typename S>
+__device__ __forceinline__ Narrow<S> operator+(Narrow<S> a, Narrow<S> b) {
+#pragma clang fp contract(off)
+  return Narrow<S>(static_cast<float>(a) + static_cast<float>(b));
+}
+template <typename S>
+__device__ __forceinline__ Narrow<S> operator*(Narrow<S> a, Narrow<S> b) {
+#pragma clang fp contract(off)
+  return Narrow<S>(static_cast<float>(a) * static_cast<float>(b));
+}
+template <typename S>
+__device__ __forceinline__ bool operator<(Narrow<S> a, Narrow<S> b) {
+  return static_cast<float>(a) < static_cast<float>(b);
+}
+using H16 = Narrow<_Float16>;
+using B16 = Narrow<__bf16>;
+static_assert(sizeof(H16) == 2 && sizeof(B16) == 2, "16-bit position storage");
 
 template <typename T>
 __device__ __forceinline__ Vec3T<T> load_pos(const T* __restrict__ pos, int64_t n) {
@@ -686,7 +725,7 @@ __global__ __launch_bounds__(BlockWaves<kMode>::value * MLCG_WAVE) void radius_r
       sp[k] = Pos4<T>{q[0], q[1], q[2], T(0)};
     }
     if (threadIdx.x == 0) {
-      const T inf = __builtin_huge_val();
+      const T inf = T(__builtin_huge_valf());
       sp[kStage] = Pos4<T>{inf, inf, inf, T(0)};
     }
   }
@@ -1419,6 +1458,38 @@ extern "C" int mlcg_radius_graph_f64(const double* pos, const int64_t* batch,
                             (int32_t*)nullptr, 0, 0, (int32_t*)nullptr, (int32_t*)nullptr,
                             workspace, overflow, stream);
 }
+
+// float16 / bfloat16 positions (raw 16-bit storage, [N, 3]): the sizing and
+// write passes of the exact edge list, as the _f64 forms (no pair map).
+#define MLCG_RADIUS_NARROW(SUFFIX, TYPE)                                                     \
+  extern "C" int mlcg_radius_rowptr_##SUFFIX(                                                \
+      const uint16_t* pos, const int64_t* batch, const int64_t* frame_ptr, int64_t n_nodes,  \
+      double r, int loop, int64_t max_num_neighbors, const int64_t* exclude_pair_xs,         \
+      const int64_t* ptr_exclude_pair_xs, int32_t* rowptr, void* workspace,                  \
+      int32_t* overflow, void* stream) {                                                     \
+    return launch_radius_rows(kModeRowptr, reinterpret_cast<const TYPE*>(pos), batch,        \
+                              frame_ptr, n_nodes, r, loop, max_num_neighbors,                \
+                              exclude_pair_xs, ptr_exclude_pair_xs, rowptr, (int32_t*)nullptr, \
+                              0, 0, (int64_t*)nullptr, (int32_t*)nullptr, 0, 0,              \
+                              (int32_t*)nullptr, (int32_t*)nullptr, workspace, overflow,     \
+                              stream);                                                       \
+  }                                                                                          \
+  extern "C" int mlcg_radius_fill_##SUFFIX(                                                  \
+      const uint16_t* pos, const int64_t* batch, const int64_t* frame_ptr, int64_t n_nodes,  \
+      double r, int loop, int64_t max_num_neighbors, const int64_t* exclude_pair_xs,         \
+      const int64_t* ptr_exclude_pair_xs, const int32_t* rowptr, int64_t edge_capacity,      \
+      int64_t edge_stride, int64_t* edge_index, int32_t* overflow, void* stream) {           \
+    return launch_radius_rows(kModeFill, reinterpret_cast<const TYPE*>(pos), batch,          \
+                              frame_ptr, n_nodes, r, loop, max_num_neighbors,                \
+                              exclude_pair_xs, ptr_exclude_pair_xs,                          \
+                              const_cast<int32_t*>(rowptr), (int32_t*)nullptr, edge_capacity, \
+                              edge_stride, edge_index, (int32_t*)nullptr, 0, 0,              \
+                              (int32_t*)nullptr, (int32_t*)nullptr, nullptr, overflow,       \
+                              stream);                                                       \
+  }
+MLCG_RADIUS_NARROW(f16, H16)
+MLCG_RADIUS_NARROW(bf16, B16)
+#undef MLCG_RADIUS_NARROW
 
 // Host-side conversion of an exclusion pair list to the per-row CSR the
 // kernels read (exclusion_pair_to_ptr, exclusion_pairs.cpp:7-62): pairs

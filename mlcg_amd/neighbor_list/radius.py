@@ -43,14 +43,16 @@ def radius_cuda(x: torch.Tensor, ptr_x: Optional[torch.Tensor], r: float,
     """(edge_index [2, E] int64, distance [E]) with the arguments of the
     reference's native operator ``mlcg::radius_cuda`` (radius.cu:197-307):
     frames given by ``ptr_x`` [B+1] (None = one frame), optional exclusion CSR.
-    Edges come out in canonical (centre, neighbour) order.  x is float32 or
-    float64, the membership test running in x's type as in the reference's
-    dispatch (radius.cu:243-250); float16/bfloat16 raise (the reference also
-    takes them)."""
+    Edges come out in canonical (centre, neighbour) order.  x is float32,
+    float64, float16 or bfloat16, the membership test running in x's type as
+    in the reference's dispatch (radius.cu:243-250); the distances are in x's
+    type (for the 16-bit types with every operation rounded to it, as the
+    reference's kernel computes sqrt(dist))."""
     require_device(x)
     _check_2d(x)
-    if x.dtype not in (torch.float32, torch.float64):
-        raise RuntimeError(f"radius_cuda takes float32 or float64 positions, got {x.dtype}")
+    if x.dtype not in _RADIUS_DTYPES:
+        raise RuntimeError(
+            f"radius_cuda takes float32, float64, float16 or bfloat16 positions, got {x.dtype}")
     n = x.shape[0]
     if ptr_x is None:
         ptr_x = torch.tensor([0, n], dtype=torch.int64, device=x.device)
@@ -65,7 +67,23 @@ def radius_cuda(x: torch.Tensor, ptr_x: Optional[torch.Tensor], r: float,
                          exclude_pair_xs=exclude_pair_xs,
                          ptr_exclude_pair_xs=ptr_exclude_pair_xs)
     ei = g.edge_index
-    return ei, (x.detach()[ei[0]] - x.detach()[ei[1]]).norm(dim=1)
+    return ei, _edge_distances(x.detach(), ei)
+
+
+_RADIUS_DTYPES = (torch.float32, torch.float64, torch.float16, torch.bfloat16)
+
+
+def _edge_distances(x: torch.Tensor, ei: torch.Tensor) -> torch.Tensor:
+    """|x_j - x_i| over the edges (i = ei[0], j = ei[1]).  For float16 and
+    bfloat16 it is the reference kernel's sequence in x's type, every
+    operation rounded (radius.cu:117-124): d = x_j - x_i, d2 = (dx^2 + dy^2) +
+    dz^2, sqrt(d2); torch evaluates each such elementwise operation in float
+    and rounds it, the c10 arithmetic."""
+    if x.dtype in (torch.float16, torch.bfloat16) and x.shape[1] == 3:
+        d = x[ei[1]] - x[ei[0]]
+        sq = d * d
+        return torch.sqrt((sq[:, 0] + sq[:, 1]) + sq[:, 2])
+    return (x[ei[0]] - x[ei[1]]).norm(dim=1)
 
 
 def _check_2d(x: torch.Tensor) -> None:
@@ -86,16 +104,15 @@ def radius_distance_fn(x: torch.Tensor, r: float, batch: Optional[torch.Tensor] 
     exs = eptr = None
     if exclude_pair_indices is not None:
         exs, eptr = ops.exclusion_pair_to_ptr(exclude_pair_indices, x.size(0))
-    # membership is decided in x's precision for float64 (the reference's
-    # scalar-type dispatch), in fp32 otherwise; the distances are computed in
-    # x's dtype so fp64 gradchecks stay exact
-    xm = x.detach() if x.dtype == torch.float64 else x.detach().float()
+    # membership is decided in x's own type (the reference's scalar-type
+    # dispatch, radius.cu:243-250); the distances are computed in x's dtype
+    # so fp64 gradchecks stay exact
+    xm = x.detach() if x.dtype in _RADIUS_DTYPES else x.detach().float()
     g = ops.radius_graph(xm, r, batch=batch, loop=loop,
                          max_num_neighbors=max_num_neighbors, n_frames=batch_size,
                          exclude_pair_xs=exs, ptr_exclude_pair_xs=eptr)
     ei = g.edge_index
-    d = (x.detach()[ei[0]] - x.detach()[ei[1]]).norm(dim=1)
-    return ei, d
+    return ei, _edge_distances(x.detach(), ei)
 
 
 class RadiusDistanceAGF(torch.autograd.Function):

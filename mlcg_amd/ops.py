@@ -245,7 +245,10 @@ def radius_graph(
     ``mlcg/neighbor_list/torch_impl.py:216-224``, with a deterministic
     canonical order (i ascending, then j ascending).  The membership test is
     ``d2 < fl32(r*r)`` with d2 = ((dx*dx + dy*dy) + dz*dz) in fp32, or in fp64
-    (``d2 < r*r``) for float64 positions (edge list only, no pair structures).
+    (``d2 < r*r``) for float64 positions, or for float16 / bfloat16 positions
+    with every operation rounded to the 16-bit type as the reference's
+    Half / BFloat16 kernels compute it (edge list only, no pair structures;
+    the 16-bit forms size their output exactly, without ``capacity``).
 
     with_pairs additionally builds the receiver CSR and pair map used by the
     CFConv kernels (it requires a symmetric graph, i.e. no binding
@@ -267,13 +270,18 @@ def radius_graph(
     exclusions must be symmetric (flag bit 2 otherwise).
     """
     f64 = pos.dtype == torch.float64
-    if f64:
-        # the membership test in double arithmetic (the reference dispatches
-        # on the scalar type, radius.cu:243-250); edge list only
+    narrow = pos.dtype in (torch.float16, torch.bfloat16)
+    sfx = {torch.float64: "_f64", torch.float16: "_f16", torch.bfloat16: "_bf16"}.get(
+        pos.dtype, "")
+    if f64 or narrow:
+        # the membership test in the positions' own arithmetic (the reference
+        # dispatches on the scalar type, radius.cu:243-250); edge list only
         require_device(pos)
         _check(pos.dim() == 2 and pos.shape[1] == 3,
                f"pos must be [N, 3], got {tuple(pos.shape)}")
         _check(not with_pairs, "the CFConv pair structures take float32 positions")
+        _check(not (narrow and capacity is not None),
+               "the fixed-capacity radius graph takes float32 or float64 positions")
         pos = pos.contiguous()
     else:
         pos = _validate_pos(pos)
@@ -305,9 +313,13 @@ def radius_graph(
     if capacity is None:
         # sizing pass (counts, block scan, look-back) -> rowptr / pairptr, then
         # one host sync to size the outputs (the reference syncs at radius.cu:288)
-        call("mlcg_radius_rowptr_f64" if f64 else "mlcg_radius_rowptr", ptr(pos), ptr(batch),
-             ptr(frame_ptr), n, float(r), int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr),
-             ptr(pairptr), ptr(ws), ptr(flags), s)
+        if narrow:
+            call(f"mlcg_radius_rowptr{sfx}", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+                 int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), ptr(ws), ptr(flags), s)
+        else:
+            call(f"mlcg_radius_rowptr{sfx}", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+                 int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), ptr(pairptr), ptr(ws),
+                 ptr(flags), s)
         if with_pairs:
             e_count, p_count, overflow = torch.cat([rowptr[n:], pairptr[n:], flags]).tolist()
         else:
@@ -335,8 +347,8 @@ def radius_graph(
         pair_ij = torch.empty(2, p_cap, dtype=torch.int32, device=dev)
         eid2pair = torch.empty(e_cap, dtype=torch.int32, device=dev)
     if capacity is None:
-        if f64:
-            call("mlcg_radius_fill_f64", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
+        if f64 or narrow:
+            call(f"mlcg_radius_fill{sfx}", ptr(pos), ptr(batch), ptr(frame_ptr), n, float(r),
                  int(loop), mnn, ptr(exs), ptr(eptr), ptr(rowptr), e_cap, e_cap,
                  ptr(edge_index), ptr(flags), s)
         else:

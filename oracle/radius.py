@@ -7,6 +7,11 @@ canonical (i asc, j asc) order.  Pinned by:
     (src/opt_radius/mlcg_opt_radius/utils.py:32-47, test_radius.py:66-104);
   * an independent numpy float32 restatement (tests/test_oracle_radius.py);
   * adversarial pairs placed exactly at d2 == fl32(r*r) and one ulp inside.
+float16 / bfloat16 positions (radius_graph_narrow) follow the reference's
+c10::Half / c10::BFloat16 arithmetic (every operation in float, rounded to
+the 16-bit type); their conversions are pinned against numpy's float16 and
+torch's bfloat16, and the search against per-operation numpy/torch
+restatements (tests/test_oracle_radius.py).
 """
 
 from __future__ import annotations
@@ -44,6 +49,14 @@ def _load():
         lib.oracle_radius_count_f64.restype = ctypes.c_int64
         lib.oracle_radius_fill_f64.argtypes = lib.oracle_radius_fill.argtypes
         lib.oracle_radius_fill_f64.restype = None
+        lib.oracle_radius_count_n16.argtypes = [ctypes.c_int] + lib.oracle_radius_count.argtypes
+        lib.oracle_radius_count_n16.restype = ctypes.c_int64
+        lib.oracle_radius_fill_n16.argtypes = [ctypes.c_int] + lib.oracle_radius_fill.argtypes
+        lib.oracle_radius_fill_n16.restype = None
+        lib.oracle_f32_to_narrow.argtypes = [ctypes.c_int, ctypes.c_float]
+        lib.oracle_f32_to_narrow.restype = ctypes.c_uint16
+        lib.oracle_narrow_to_f32.argtypes = [ctypes.c_int, ctypes.c_uint16]
+        lib.oracle_narrow_to_f32.restype = ctypes.c_float
         _lib = lib
     return _lib
 
@@ -105,4 +118,50 @@ def radius_graph(pos, r: float, batch=None, loop: bool = False, max_num_neighbor
     fill(pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
                            int(max_num_neighbors), ex_p, ep_p, ei[0].ctypes.data,
                            ei[1].ctypes.data)
+    return ei[:, :total].copy(), int(ovf.value)
+
+
+NARROW_KINDS = {"f16": 0, "bf16": 1}
+
+
+def narrow_round(kind: str, values) -> np.ndarray:
+    """float32 values rounded to the 16-bit type and back (the oracle's own
+    conversion, one value at a time: small arrays only)."""
+    lib = _load()
+    k = NARROW_KINDS[kind]
+    v = np.asarray(values, dtype=np.float32).ravel()
+    return np.array([lib.oracle_narrow_to_f32(k, lib.oracle_f32_to_narrow(k, float(x)))
+                     for x in v], dtype=np.float32)
+
+
+def radius_graph_narrow(bits, kind: str, r: float, batch=None, loop: bool = False,
+                        max_num_neighbors: int = 32, n_frames: int | None = None,
+                        exclude_pair_xs=None, ptr_exclude_pair_xs=None):
+    """radius_graph for float16 ("f16") or bfloat16 ("bf16") positions given as
+    their raw 16-bit patterns [N, 3] (uint16 / int16)."""
+    k = NARROW_KINDS[kind]
+    pos = np.ascontiguousarray(np.asarray(bits).view(np.uint16).reshape(-1, 3))
+    n = pos.shape[0]
+    if batch is None:
+        batch = np.zeros(n, dtype=np.int64)
+    ptr = frame_ptr_from_batch(batch, n_frames)
+    nb = ptr.shape[0] - 1
+    lib = _load()
+    exs = eptr = None
+    if exclude_pair_xs is not None:
+        exs = np.ascontiguousarray(np.asarray(exclude_pair_xs, dtype=np.int64))
+        if exs.size == 0:
+            exs = np.zeros(1, dtype=np.int64)
+        eptr = np.ascontiguousarray(np.asarray(ptr_exclude_pair_xs, dtype=np.int64))
+    ex_p = None if exs is None else exs.ctypes.data
+    ep_p = None if eptr is None else eptr.ctypes.data
+    deg = np.zeros(max(n, 1), dtype=np.int64)
+    ovf = ctypes.c_int(0)
+    total = lib.oracle_radius_count_n16(k, pos.ctypes.data, ptr.ctypes.data, nb, float(r),
+                                        int(loop), int(max_num_neighbors), ex_p, ep_p,
+                                        deg.ctypes.data, ctypes.addressof(ovf))
+    ei = np.zeros((2, max(total, 1)), dtype=np.int64)
+    lib.oracle_radius_fill_n16(k, pos.ctypes.data, ptr.ctypes.data, nb, float(r), int(loop),
+                               int(max_num_neighbors), ex_p, ep_p, ei[0].ctypes.data,
+                               ei[1].ctypes.data)
     return ei[:, :total].copy(), int(ovf.value)

@@ -321,8 +321,76 @@ def test_radius_cuda_float64_boundary():
     assert ei.cpu().tolist() == [[0, 1], [1, 0]] and d.dtype == torch.float64
     ei32, _ = radius_cuda(pos.float(), ptr, 1.0, 8, True)
     assert ei32.shape[1] == 0
-    with pytest.raises(RuntimeError, match="float32 or float64"):
-        radius_cuda(pos.half(), ptr, 1.0, 8, True)
+    with pytest.raises(RuntimeError, match="float32, float64, float16 or bfloat16"):
+        radius_cuda(pos.to(torch.int32), ptr, 1.0, 8, True)
+
+
+def _narrow(dt):
+    return torch.float16 if dt == "f16" else torch.bfloat16
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("loop,mnn,excl", [(False, 1000, False), (True, 1000, False),
+                                           (False, 6, False), (False, 1000, True)])
+def test_radius_narrow_positions_bit_exact(dt, loop, mnn, excl):
+    """float16 / bfloat16 positions (the reference's Half / BFloat16 dispatch,
+    radius.cu:243-250): the HIP search, every operation rounded to the 16-bit
+    type, equals the C oracle's bit for bit on 16 globule frames of 100 beads,
+    with self loops, a binding max_num_neighbors and exclusions; and the
+    16-bit membership differs from the float32 search of the same (widened)
+    positions, so the comparison is sensitive to the arithmetic."""
+    from mlcg_amd import ops, synthetic
+
+    rng = np.random.default_rng(500 + mnn + 7 * loop + 3 * excl)
+    pos32 = synthetic.globule(16, 100, 12.0, rng).reshape(-1, 3).astype(np.float32)
+    x = torch.from_numpy(pos32).to(_narrow(dt))
+    bits = x.view(torch.int16).numpy().view(np.uint16)
+    n = x.shape[0]
+    batch = np.repeat(np.arange(16), 100)
+    r = 9.7
+    kw_ref, kw = {}, {}
+    if excl:
+        exc = _exclusions(rng, n, 4 * n, batch)
+        xs_ref, yp_ref = oracle_radius.exclusion_pair_to_ptr(exc, n)
+        kw_ref = dict(exclude_pair_xs=xs_ref, ptr_exclude_pair_xs=yp_ref)
+        xs, yp = ops.exclusion_pair_to_ptr(torch.from_numpy(exc).cuda(), n)
+        kw = dict(exclude_pair_xs=xs, ptr_exclude_pair_xs=yp)
+    print(f"narrow {dt} loop={loop} mnn={mnn} excl={excl}", flush=True)
+    ref, _ = oracle_radius.radius_graph_narrow(bits, dt, r, batch, loop, mnn, **kw_ref)
+    g = ops.radius_graph(x.cuda(), r, batch=torch.from_numpy(batch).cuda(), loop=loop,
+                         max_num_neighbors=mnn, n_frames=16, **kw)
+    assert np.array_equal(g.edge_index.cpu().numpy(), ref)
+    if mnn == 1000 and not excl and not loop:
+        wide, _ = oracle_radius.radius_graph(x.float().numpy(), r, batch, loop, mnn)
+        assert not np.array_equal(wide, ref)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_radius_cuda_narrow_distances(dt):
+    """mlcg::radius_cuda on 16-bit positions: the oracle's edge list, and the
+    distances in x's type as the reference's kernel forms them (each
+    operation rounded to the 16-bit type, then sqrt), equal to a float32
+    computation rounded once within one 16-bit ulp."""
+    from mlcg_amd import library, synthetic
+
+    library.register()
+    rng = np.random.default_rng(77)
+    pos32 = synthetic.globule(4, 60, 9.0, rng).reshape(-1, 3).astype(np.float32)
+    x = torch.from_numpy(pos32).to(_narrow(dt)).cuda()
+    ptr = torch.tensor([0, 60, 120, 180, 240], device="cuda")
+    ei, d = torch.ops.mlcg.radius_cuda(x, ptr, 7.5, 64, True)
+    bits = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref, _ = oracle_radius.radius_graph_narrow(bits, dt, 7.5, np.repeat(np.arange(4), 60),
+                                               False, 64)
+    assert np.array_equal(ei.cpu().numpy(), ref) and d.dtype == x.dtype
+    xc = x.cpu()
+    diff = xc[ei[1].cpu()] - xc[ei[0].cpu()]
+    sq = diff * diff
+    want = torch.sqrt((sq[:, 0] + sq[:, 1]) + sq[:, 2])
+    assert torch.equal(d.cpu(), want)
+    once = (xc.float()[ei[1].cpu()] - xc.float()[ei[0].cpu()]).norm(dim=1)
+    ulp = 2.0 ** -10 if dt == "f16" else 2.0 ** -7
+    assert float(((d.cpu().float() - once).abs() / once).max()) < 4 * ulp
 
 
 def test_registered_operators_and_torch_compile():

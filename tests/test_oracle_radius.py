@@ -302,3 +302,141 @@ def test_oracle_f64_numpy_restatement():
             if (d[0] * d[0] + d[1] * d[1]) + d[2] * d[2] < r * r:
                 want.append((i, j))
     assert list(map(tuple, ei.T.tolist())) == want
+
+
+# --------------------------------------------------------------------------
+# float16 / bfloat16 positions (the reference's Half / BFloat16 dispatch,
+# radius.cu:243-250): c10 scalar arithmetic, every operation in float and
+# rounded to the 16-bit type.
+
+def test_oracle_f16_conversions_match_numpy():
+    """All 2^16 binary16 patterns widen like numpy's float16, and float32
+    values (random, exact ties, subnormal range, overflow) round like numpy's
+    float32 -> float16 cast (round to nearest even)."""
+    lib = oracle_radius._load()
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.oracle_narrow_to_f32(0, int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    rng = np.random.default_rng(3)
+    h = rng.integers(0, 0x7c00, 4000, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float32)
+    hi = (h + 1).view(np.float16).astype(np.float32)
+    ties = (lo.astype(np.float64) + hi.astype(np.float64)) / 2  # exact in float32
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * 10.0 ** rng.integers(-9, 5, 4000),
+        ties.astype(np.float32), -ties.astype(np.float32),
+        np.float32([0.0, -0.0, 65504.0, 65519.99, 65520.0, 7e4, 5.96e-8, 2.98e-8, 3e-8,
+                    6.1e-5, 6.09e-5, np.inf, -np.inf])])
+    got = np.array([lib.oracle_f32_to_narrow(0, float(v)) for v in vals], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_oracle_bf16_conversions_match_torch():
+    """bfloat16 widening is exact and the float32 -> bfloat16 rounding equals
+    torch's (round to nearest even), ties included."""
+    import torch
+
+    lib = oracle_radius._load()
+    rng = np.random.default_rng(4)
+    b = rng.integers(0, 0x7f80, 3000, dtype=np.uint16)
+    wide = (b.astype(np.uint32) << 16).view(np.float32)
+    got = np.array([lib.oracle_narrow_to_f32(1, int(x)) for x in b], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), wide.view(np.uint32))
+    nxt = ((b.astype(np.uint32) + 1) << 16).view(np.float32)
+    ties = ((wide.astype(np.float64) + nxt.astype(np.float64)) / 2).astype(np.float32)
+    vals = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 100.0, ties, -ties,
+                           np.float32([0.0, -0.0, 3.4e38, np.inf, -np.inf])])
+    got = np.array([lib.oracle_f32_to_narrow(1, float(v)) for v in vals], dtype=np.uint16)
+    want = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _narrow_restatement(d16, r, batch, loop):
+    """Edges of a per-operation 16-bit restatement: d16 computes (x_j - x_i)
+    squared and summed ((dx^2 + dy^2) + dz^2) in the 16-bit type, r2 is the
+    16-bit rounding of float32(r*r)."""
+    n = batch.shape[0]
+    want = []
+    for i in range(n):
+        d2, r2 = d16(i)
+        for j in range(n):
+            if batch[i] != batch[j] or (not loop and i == j):
+                continue
+            if d2[j] < r2:
+                want.append((i, j))
+    return want
+
+
+def test_oracle_f16_search_matches_numpy_float16():
+    """The float16 search equals numpy float16 arithmetic (numpy computes each
+    float16 operation in float32 and rounds, the c10 semantics) on random
+    frames, including self loops and a max_num_neighbors cap."""
+    rng = np.random.default_rng(21)
+    pos = (rng.random((80, 3)) * 6.0).astype(np.float16)
+    batch = np.repeat(np.arange(2), 40)
+    r = 2.1
+    r2 = np.float16(np.float32(r * r))
+
+    def d16(i):
+        d = pos - pos[i]  # float16 (x_j - x_i)
+        sq = d * d
+        return (sq[:, 0] + sq[:, 1]) + sq[:, 2], r2
+
+    for loop in (False, True):
+        ei, _ = oracle_radius.radius_graph_narrow(pos.view(np.uint16), "f16", r, batch, loop,
+                                                  1000)
+        assert list(map(tuple, ei.T.tolist())) == _narrow_restatement(d16, r, batch, loop)
+    ei, ovf = oracle_radius.radius_graph_narrow(pos.view(np.uint16), "f16", r, batch, False, 3)
+    full = _narrow_restatement(d16, r, batch, False)
+    capped = [e for e in full if sum(1 for f in full if f[0] == e[0] and f[1] <= e[1]) <= 3]
+    assert list(map(tuple, ei.T.tolist())) == capped and ovf == 1
+
+
+def test_oracle_bf16_search_matches_torch_bfloat16():
+    """The bfloat16 search equals torch's CPU bfloat16 arithmetic (each
+    operation in float, rounded to bfloat16) on random frames."""
+    import torch
+
+    rng = np.random.default_rng(22)
+    pos = torch.from_numpy(rng.random((70, 3)).astype(np.float32) * 6.0).to(torch.bfloat16)
+    batch = np.repeat(np.arange(2), 35)
+    r = 2.3
+    r2 = torch.tensor(np.float32(r * r)).to(torch.bfloat16).float().item()
+
+    def d16(i):
+        d = pos - pos[i]
+        sq = d * d
+        return ((sq[:, 0] + sq[:, 1]) + sq[:, 2]).float().numpy(), r2
+
+    bits = pos.view(torch.int16).numpy().view(np.uint16)
+    ei, _ = oracle_radius.radius_graph_narrow(bits, "bf16", r, batch, False, 1000)
+    assert list(map(tuple, ei.T.tolist())) == _narrow_restatement(d16, r, batch, False)
+
+
+def test_oracle_f16_boundary_in_half_precision():
+    """A pair whose float16 d2 equals the float16 r2 is outside (strict <);
+    moved one float16 ulp closer it is inside; a pair inside in float32 but
+    rounded onto r2 by the float16 subtraction is outside."""
+    r = 1.5
+    r2 = np.float16(np.float32(r * r))  # 2.25 exactly
+    x = np.float16(1.5)
+    pos = np.array([[0, 0, 0], [x, 0, 0]], dtype=np.float16)
+    ei, _ = oracle_radius.radius_graph_narrow(pos.view(np.uint16), "f16", r)
+    assert ei.shape[1] == 0 and float(np.float16(x * x)) == float(r2)
+    closer = np.nextafter(x, np.float16(0))
+    pos[1, 0] = closer
+    ei, _ = oracle_radius.radius_graph_narrow(pos.view(np.uint16), "f16", r)
+    assert ei.T.tolist() == [[0, 1], [1, 0]]
+    # exact difference 1.5 - 1e-4 (inside in float32) rounds to 1.5 in the
+    # float16 subtraction, so d2 lands on r2: outside
+    a, b = np.float16(1e-4), np.float16(1.5)
+    assert (np.float32(b) - np.float32(a)) ** 2 < np.float32(r * r)
+    assert b - a == np.float16(1.5)
+    pos = np.array([[a, 0, 0], [b, 0, 0]], dtype=np.float16)
+    ei, _ = oracle_radius.radius_graph_narrow(pos.view(np.uint16), "f16", r)
+    assert ei.shape[1] == 0
