@@ -65,6 +65,12 @@ def _edge_csr(edge_index: torch.Tensor, num_nodes: int, by_row: int) -> ops.Pair
                          num_nodes=num_nodes, num_edges=edge_index.shape[1], num_pairs=0)
 
 
+# PyG aggregation names of CFConv (MessagePassing(aggr=...), schnet.py:292-294)
+# that the CFConv kernels implement: "add" / "sum" on the fused path, "mean"
+# module by module (the HIP gather divided by each receiver's in-degree).
+_AGGR = ("add", "sum", "mean")
+
+
 class CFConv(torch.nn.Module):
     """Continuous-filter convolution (schnet.py:265-368).
 
@@ -76,9 +82,9 @@ class CFConv(torch.nn.Module):
                  in_channels: int = 128, out_channels: int = 128, num_filters: int = 128,
                  aggr: str = "add"):
         super().__init__()
-        if aggr != "add":
-            raise NotImplementedError(f"aggr={aggr!r}: only 'add' (the SchNet default) is "
-                                      "implemented by the CFConv kernels")
+        if aggr not in _AGGR:
+            raise NotImplementedError(f"aggr={aggr!r}: the CFConv kernels implement "
+                                      f"{', '.join(map(repr, _AGGR))}")
         self.aggr = aggr
         self.lin1 = torch.nn.Linear(in_channels, num_filters, bias=False)
         self.lin2 = torch.nn.Linear(num_filters, out_channels)
@@ -100,6 +106,11 @@ class CFConv(torch.nn.Module):
         fwd = _edge_csr(edge_index, n, by_row=1)
         bwd = _edge_csr(edge_index, n, by_row=0)
         agg = _EdgeGather.apply(y, W.float(), fwd, bwd, edge_index[0], edge_index[1])
+        if self.aggr == "mean":
+            # PyG's mean aggregation: the sum over a receiver's messages divided
+            # by their number, zero for a receiver without any
+            deg = (fwd.rowptr[1:] - fwd.rowptr[:-1]).clamp_min(1).to(agg.dtype)
+            agg = agg / deg.unsqueeze(1)
         return self.lin2(agg)
 
 
@@ -240,6 +251,8 @@ class SchNet(torch.nn.Module):
         filt_act = block_act = None
         for blk in self.interaction_blocks:
             if not isinstance(blk, InteractionBlock) or not isinstance(blk.conv, CFConv):
+                return None
+            if blk.conv.aggr not in ("add", "sum"):
                 return None
             fn = blk.conv.filter_network
             if not isinstance(fn, MLP):

@@ -19,6 +19,8 @@ Parity pins (besides the restatement itself):
                      the force loss with respect to the basis parameters
   schnet_energy   -- two-bead closed form; translation/rotation/permutation
                      invariance; sum_i F_i == 0 per frame
+  aggregate       -- per-receiver Python loops over the edge list ("add",
+                     "mean", a receiver without messages) on a small graph
   forces          -- central finite differences in fp64
   force_matching  -- torch.autograd.gradgradcheck-style finite differences
                      of the force loss with respect to parameters (fp64)
@@ -148,6 +150,7 @@ class SchNetConfig:
     act: str = "tanh"
     num_blocks: int = 3
     basis: str = "gaussian"        # "gaussian" | "expnormal"
+    aggr: str = "add"              # CFConv aggregation: "add" | "mean"
 
 
 BASIS_KEYS = {"gaussian": ("rbf_layer.offset", "rbf_layer.coeff"),
@@ -174,6 +177,19 @@ def _layers(sd, prefix: str) -> List[Dict[str, torch.Tensor]]:
     return out
 
 
+def aggregate(msg: torch.Tensor, index: torch.Tensor, n: int, aggr: str = "add") -> torch.Tensor:
+    """PyG's scatter of the messages onto their receivers (MessagePassing with
+    aggr="add" or "mean"): the sum, or the sum divided by the number of
+    messages, a receiver without messages getting zero."""
+    agg = torch.zeros(n, msg.shape[1], dtype=msg.dtype).index_add_(0, index, msg)
+    if aggr == "mean":
+        cnt = torch.bincount(index, minlength=n).clamp_min(1).to(msg.dtype)
+        agg = agg / cnt.unsqueeze(1)
+    elif aggr not in ("add", "sum"):
+        raise ValueError(f"aggr {aggr!r}")
+    return agg
+
+
 def schnet_energy(sd: Dict[str, torch.Tensor], cfg: SchNetConfig, pos: torch.Tensor,
                   atom_types: torch.Tensor, batch: torch.Tensor, edge_index: torch.Tensor,
                   n_frames: int) -> torch.Tensor:
@@ -191,7 +207,7 @@ def schnet_energy(sd: Dict[str, torch.Tensor], cfg: SchNetConfig, pos: torch.Ten
         W = mlp(rbf, _layers(sd, f"{p}.conv.filter_network"), act) * C.view(-1, 1)
         y = linear(x, sd[f"{p}.conv.lin1.weight"])
         msg = y.index_select(0, edge_index[0]) * W          # x_j * W (schnet.py:368)
-        agg = torch.zeros_like(y).index_add_(0, edge_index[1], msg)  # aggr="add"
+        agg = aggregate(msg, edge_index[1], y.shape[0], cfg.aggr)
         h = linear(agg, sd[f"{p}.conv.lin2.weight"], sd[f"{p}.conv.lin2.bias"])
         # InteractionBlock.forward (schnet.py:259-261), residual at 152-155
         v = linear(act(h), sd[f"{p}.lin.weight"], sd[f"{p}.lin.bias"])

@@ -7,10 +7,10 @@ from oracle import schnet_ref as R
 
 
 def make_cfg(num_blocks=3, num_rbf=50, rc=20.0, act="tanh", rbf_cut="cosine",
-             conv_cut="cosine", conv_lo=0.0, basis="gaussian"):
+             conv_cut="cosine", conv_lo=0.0, basis="gaussian", aggr="add"):
     return R.SchNetConfig(num_rbf=num_rbf, rbf_lo=0.0, rbf_hi=rc, rbf_cut=rbf_cut,
                           conv_cut=conv_cut, conv_lo=conv_lo, conv_hi=rc, act=act,
-                          num_blocks=num_blocks, basis=basis)
+                          num_blocks=num_blocks, basis=basis, aggr=aggr)
 
 
 def make_model(cfg, sd, out_widths=(64,), device="cuda", trainable_basis=False):
@@ -27,7 +27,8 @@ def make_model(cfg, sd, out_widths=(64,), device="cuda", trainable_basis=False):
         rbf = nn.ExpNormalBasis(rbf_cut, num_rbf=cfg.num_rbf, trainable=trainable_basis)
     m = nn.StandardSchNet(rbf, conv_cut, list(out_widths), hidden_channels=128,
                           embedding_size=sd["embedding_layer.weight"].shape[0],
-                          num_filters=128, num_interactions=cfg.num_blocks, activation=act)
+                          num_filters=128, num_interactions=cfg.num_blocks, activation=act,
+                          aggr=getattr(cfg, "aggr", "add"))
     m.load_state_dict(sd)
     return m.to(device)
 

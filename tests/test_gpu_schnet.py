@@ -465,3 +465,40 @@ def test_cosine_cutoff_with_lower_bound():
     assert abs(float(loss) - float(loss_ref)) <= 1e-5 * abs(float(loss_ref))
     for k, gr in g_ref.items():
         check(dict(model.named_parameters())[k].grad, gr, 1e-4, k)
+
+
+def test_mean_aggregation_vs_oracle():
+    """CFConv with aggr="mean" (PyG's mean: the HIP gather divided by each
+    receiver's in-degree, module by module) against the fp64 oracle's mean
+    aggregation: energies and forces at 1e-5, and the force-matching
+    parameter gradients (double backward through the module path) at 1e-4;
+    the mean model's energies differ from the add model's."""
+    from mlcg_amd import nn
+
+    cfg = make_cfg(num_blocks=2, rc=12.0, act="ssp", aggr="mean")
+    sd = R.random_state_dict(cfg, seed=17)
+    b = _small_batch()
+    pos64, types, batch, ei = _oracle_inputs(b, 12.0)
+    sd64 = R.to_dtype(sd, torch.float64)
+    E_ref, F_ref = R.schnet_energy_forces(sd64, cfg, pos64, types, batch, ei, b.n_frames)
+    model = make_model(cfg, sd)
+    assert model.fused_spec() is None
+    data = nn.GradientsOut(model).eval()(b.to_torch("cuda"))
+    check(data.out["SchNet"]["energy"], E_ref, 1e-5, "E mean")
+    check(data.out["SchNet"]["forces"], F_ref, 1e-5, "F mean")
+    E_add, _ = R.schnet_energy_forces(sd64, make_cfg(num_blocks=2, rc=12.0, act="ssp"), pos64,
+                                      types, batch, ei, b.n_frames)
+    assert float((E_add - E_ref).abs().max()) > 1e-3
+    fref64 = torch.from_numpy(b.forces).double()
+    loss_ref, _, _, g_ref = R.force_matching_grads(sd64, cfg, pos64, types, batch, ei,
+                                                   b.n_frames, fref64)
+    model = make_model(cfg, sd)
+    gm = nn.GradientsOut(model).train()
+    data = gm(b.to_torch("cuda"))
+    loss = torch.nn.functional.mse_loss(data.out["SchNet"]["forces"], data.forces)
+    loss.backward()
+    assert abs(float(loss) - float(loss_ref)) <= 1e-5 * abs(float(loss_ref))
+    grads = _param_grads(model)
+    for k, gr in g_ref.items():
+        assert grads[k] is not None, k
+        check(grads[k], gr, 1e-4, k)

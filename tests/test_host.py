@@ -194,6 +194,22 @@ def test_fused_spec_recognises_config2():
     assert m2.fused_spec() is None  # no kernel for ReLU: module-by-module path
 
 
+def test_cfconv_aggregations():
+    """CFConv takes PyG's "add" / "sum" (fused path) and "mean" (module by
+    module: the HIP gather divided by the in-degree); other aggregations
+    raise at construction."""
+    from mlcg_amd import nn
+
+    rbf = nn.GaussianBasis(nn.CosineCutoff(0.0, 20.0), num_rbf=50)
+    for aggr, fused in (("add", True), ("sum", True), ("mean", False)):
+        m = nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, 20.0), [64], num_interactions=2,
+                              embedding_size=21, aggr=aggr)
+        assert all(b.conv.aggr == aggr for b in m.interaction_blocks)
+        assert (m.fused_spec() is not None) == fused, aggr
+    with pytest.raises(NotImplementedError, match="aggr='max'"):
+        nn.StandardSchNet(rbf, nn.CosineCutoff(0.0, 20.0), [64], aggr="max")
+
+
 @pytest.mark.parametrize("trainable", [False, True])
 def test_fused_spec_basis_kinds(trainable):
     """Both bases, trainable or fixed, have a fused spec; its basis tensors

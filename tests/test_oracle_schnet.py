@@ -362,3 +362,26 @@ def test_chunked_force_matching_equals_whole_batch():
         assert torch.allclose(part[2], whole[2], rtol=1e-12, atol=1e-14)
         for k, v in whole[3].items():
             assert torch.allclose(part[3][k], v, rtol=1e-10, atol=1e-14), (chunk, k)
+
+
+@pytest.mark.parametrize("aggr", ["add", "mean"])
+def test_aggregate_matches_per_receiver_loops(aggr):
+    """The oracle's CFConv aggregation (PyG MessagePassing aggr="add" /
+    "mean") against explicit per-receiver loops over the edge list, with a
+    receiver that gets no message (zero in both) and repeated receivers."""
+    g = torch.Generator().manual_seed(5)
+    n, F = 7, 4
+    index = torch.tensor([0, 0, 3, 2, 3, 3, 6, 0, 2, 5])
+    msg = torch.randn(index.numel(), F, generator=g, dtype=torch.float64)
+    got = R.aggregate(msg, index, n, aggr)
+    for t in range(n):
+        rows = [msg[e] for e in range(index.numel()) if int(index[e]) == t]
+        want = torch.zeros(F, dtype=torch.float64)
+        for r in rows:
+            want = want + r
+        if aggr == "mean" and rows:
+            want = want / len(rows)
+        assert torch.allclose(got[t], want, rtol=0, atol=1e-15), t
+    assert torch.equal(got[1], torch.zeros(F, dtype=torch.float64))  # no messages
+    with pytest.raises(ValueError):
+        R.aggregate(msg, index, n, "max")
