@@ -447,6 +447,17 @@ int mlcg_segment_sum(const float* values, int64_t stride,
                      const int64_t* frame_ptr, int64_t n_frames, float* out,
                      void* stream);
 
+/* float64 forms for a model moved to double (the reference's simulations with
+ * dtype="double", src/mlcg/simulation/base.py:162,271): per-frame sums of a
+ * float64 vector (one workgroup per frame, fixed order), and the CFConv
+ * gather out[i] = sum_j src[j] * W[eid2pair[e]] over the receiver CSR for
+ * any feature count (each feature summed over the row in CSR order). */
+int mlcg_segment_sum_f64(const double* values, const int64_t* frame_ptr, int64_t n_frames,
+                         double* out, void* stream);
+int mlcg_cfconv_gather_f64(const double* src, const double* W, const int32_t* rowptr,
+                           const int32_t* col, const int32_t* eid2pair, int64_t n_nodes,
+                           int num_filters, double* out, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Node-level linears (F = H = 128) and their weight gradients             */
 /* ---------------------------------------------------------------------- */
@@ -648,6 +659,17 @@ int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
                              const int32_t* bead_slots, int64_t n_nodes,
                              int accumulate, float* forces, void* stream);
 
+/* mlcg_prior_terms / mlcg_prior_gather_forces for a model moved to double
+ * (positions, parameters, energies and forces float64; every kind evaluated
+ * in double). */
+int mlcg_prior_terms_f64(int kind, int n_degs, const double* pos,
+                         const int64_t* index_mapping, int64_t mapping_stride,
+                         int64_t n_interactions, const double* params, int n_params,
+                         double* energy, double* slot_forces, void* stream);
+int mlcg_prior_gather_forces_f64(const double* slot_forces, const int32_t* bead_ptr,
+                                 const int32_t* bead_slots, int64_t n_nodes, int accumulate,
+                                 double* forces, void* stream);
+
 /* The repulsion prior (MLCG_PRIOR_REPULSION) in one call, without slot force
  * arrays: energy[m] of every interaction (as mlcg_prior_terms) and forces[a]
  * set or added (accumulate != 0) per bead straight from the positions.
@@ -691,6 +713,18 @@ int mlcg_langevin_baoa(float* pos, float* vel, const float* forces,
  * advances *step_dev by one when step_dev is non-NULL. */
 int mlcg_langevin_b(float* vel, const float* forces, const float* masses,
                     int64_t n_nodes, float dt, int64_t* step_dev, void* stream);
+
+/* mlcg_langevin_baoa / mlcg_langevin_b for a simulation in double precision
+ * (LangevinSimulation with dtype="double", src/mlcg/simulation/base.py:162):
+ * every array float64; the noise is the same float Philox4x32-10 /
+ * Box-Muller stream, widened (explicit noise is float64). */
+int mlcg_langevin_baoa_f64(double* pos, double* vel, const double* forces,
+                           const double* masses, const double* beta_mass_ratio,
+                           int64_t n_nodes, double dt, double vscale, double noisescale,
+                           uint64_t seed, const int64_t* step_dev, const double* noise,
+                           void* stream);
+int mlcg_langevin_b_f64(double* vel, const double* forces, const double* masses,
+                        int64_t n_nodes, double dt, int64_t* step_dev, void* stream);
 
 /* The normals mlcg_langevin_baoa draws at `step`: out [N, 3].  Replaces the
  * torch.randn draw of langevin.py:129-134 (used by the statistics tests). */

@@ -80,6 +80,8 @@ _SIGNATURES = {
                                 _P, _P],
     "mlcg_pair_ddot": [_P, _P, _P, _I64, _P, _I64, _P, _F32, _P, _P],
     "mlcg_pair_forces": [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_segment_sum_f64": [_P, _P, _I64, _P, _P],
+    "mlcg_cfconv_gather_f64": [_P, _P, _P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_segment_sum": [_P, _I64, _P, _I64, _P, _P],
     "mlcg_node_gemm": [_P, _I64, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P,
                        _P, _P],
@@ -101,12 +103,16 @@ _SIGNATURES = {
     "mlcg_prior_order": [_I32],
     "mlcg_prior_num_params": [_I32, _I32],
     "mlcg_prior_terms": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
+    "mlcg_prior_terms_f64": [_I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P, _P, _P],
     "mlcg_prior_gather_forces": [_P, _P, _P, _I64, _I32, _P, _P],
+    "mlcg_prior_gather_forces_f64": [_P, _P, _P, _I64, _I32, _P, _P],
     "mlcg_prior_pair_records_ints": [_I64, _I64],
     "mlcg_prior_pair_records": [_P, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _P],
     "mlcg_prior_repulsion": [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P],
     "mlcg_langevin_baoa": [_P, _P, _P, _P, _P, _I64, _F32, _F32, _F32, _U64, _P, _P, _P],
+    "mlcg_langevin_baoa_f64": [_P, _P, _P, _P, _P, _I64, _F64, _F64, _F64, _U64, _P, _P, _P],
     "mlcg_langevin_b": [_P, _P, _P, _I64, _F32, _P, _P],
+    "mlcg_langevin_b_f64": [_P, _P, _P, _I64, _F64, _P, _P],
     "mlcg_philox_normals": [_U64, _I64, _I64, _P, _P],
     "mlcg_math_eval": [_I32, _P, _I64, _P, _P],
     "mlcg_numerics_flags": [_P, _I32, _P],

@@ -528,6 +528,51 @@ __global__ __launch_bounds__(kSegThreads) void segment_sum_kernel(
   }
 }
 
+// float64 models (the module path of a model moved to double, as the
+// reference's simulations do with dtype="double"): out[i] = sum_j src[j] W_p
+// for any feature count F, one wave per receiver row (XCD-aware as above),
+// lane l holding features l, l + 64, ...; each feature sums the row's edges in
+// CSR order (ascending neighbour), the CPU reference's order.
+__global__ __launch_bounds__(kThreads) void gather_f64_kernel(
+    const double* __restrict__ src, const double* __restrict__ W, int F,
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+    const int32_t* __restrict__ eid2pair, int64_t n, double* __restrict__ out) {
+  const int lane = mlcg_lane();
+  const int64_t i = xcd_row();
+  if (i >= n) return;
+  const int e0 = uniform(rowptr[i]), e1 = uniform(rowptr[i + 1]);
+  for (int f = lane; f < F; f += MLCG_WAVE) {
+    double acc = 0.0;
+    for (int e = e0; e < e1; ++e) {
+      const int64_t j = col[e], p = eid2pair[e];
+      acc += src[j * F + f] * W[p * F + f];
+    }
+    out[i * F + f] = acc;
+  }
+}
+
+// Per-segment sums of a float64 vector: one workgroup per segment, each
+// thread a strided part in order, then the waves' sums (fixed butterfly) in
+// wave order.
+__global__ __launch_bounds__(kSegThreads) void segment_sum_f64_kernel(
+    const double* __restrict__ v, const int64_t* __restrict__ ptr, int64_t nb,
+    double* __restrict__ out) {
+  __shared__ double part[kSegThreads / MLCG_WAVE];
+  for (int64_t b = blockIdx.x; b < nb; b += gridDim.x) {
+    double s = 0.0;
+    for (int64_t k = ptr[b] + threadIdx.x; k < ptr[b + 1]; k += kSegThreads) s += v[k];
+    for (int o = MLCG_WAVE / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, MLCG_WAVE);
+    if (mlcg_lane() == 0) part[threadIdx.x / MLCG_WAVE] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double t = 0.0;
+      for (int w = 0; w < kSegThreads / MLCG_WAVE; ++w) t += part[w];
+      out[b] = t;
+    }
+    __syncthreads();
+  }
+}
+
 // one wave per receiver row, kWaves rows per workgroup (see xcd_row)
 unsigned row_groups(int64_t n) { return mlcg_div_up(n, kWaves); }
 
@@ -640,5 +685,29 @@ extern "C" int mlcg_segment_sum(const float* values, int64_t stride, const int64
   hipLaunchKernelGGL(segment_sum_kernel, dim3(mlcg_persistent_groups(n_frames, 8)),
                      dim3(kSegThreads), 0, mlcg_stream(stream), values, stride, frame_ptr,
                      n_frames, out);
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_cfconv_gather_f64(const double* src, const double* W,
+                                      const int32_t* rowptr, const int32_t* col,
+                                      const int32_t* eid2pair, int64_t n_nodes, int num_filters,
+                                      double* out, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && num_filters >= 1);
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(src && W && rowptr && col && eid2pair && out);
+  hipLaunchKernelGGL(gather_f64_kernel, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
+                     mlcg_stream(stream), src, W, num_filters, rowptr, col, eid2pair, n_nodes,
+                     out);
+  return mlcg_launch_status();
+}
+
+extern "C" int mlcg_segment_sum_f64(const double* values, const int64_t* frame_ptr,
+                                    int64_t n_frames, double* out, void* stream) {
+  MLCG_REQUIRE(n_frames >= 0);
+  if (n_frames == 0) return MLCG_OK;
+  MLCG_REQUIRE(values && frame_ptr && out);
+  hipLaunchKernelGGL(segment_sum_f64_kernel, dim3(mlcg_persistent_groups(n_frames, 8)),
+                     dim3(kSegThreads), 0, mlcg_stream(stream), values, frame_ptr, n_frames,
+                     out);
   return mlcg_launch_status();
 }

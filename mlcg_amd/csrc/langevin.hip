@@ -62,43 +62,50 @@ __device__ __forceinline__ void normals3(uint64_t seed, int64_t bead, int64_t st
   n2 = rb * c;
 }
 
+// T: float, or double for a simulation in double precision (the noise is the
+// same float Philox/Box-Muller stream, widened).
+template <typename T>
 __global__ __launch_bounds__(256) void baoa_kernel(
-    float* __restrict__ x, float* __restrict__ v, const float* __restrict__ F,
-    const float* __restrict__ masses, const float* __restrict__ bmr, int64_t n, float half_dt,
-    float vscale, float noisescale, uint64_t seed, const int64_t* __restrict__ step_dev,
-    const float* __restrict__ noise) {
+    T* __restrict__ x, T* __restrict__ v, const T* __restrict__ F,
+    const T* __restrict__ masses, const T* __restrict__ bmr, int64_t n, T half_dt,
+    T vscale, T noisescale, uint64_t seed, const int64_t* __restrict__ step_dev,
+    const T* __restrict__ noise) {
   const int64_t step = step_dev ? *step_dev : 0;
   for (int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; a < n;
        a += (int64_t)gridDim.x * blockDim.x) {
-    const float m = masses[a];
-    const float sig = bmr[a];
-    float xi[3];
+    const T m = masses[a];
+    const T sig = bmr[a];
+    T xi[3];
     if (noise) {
       xi[0] = noise[3 * a];
       xi[1] = noise[3 * a + 1];
       xi[2] = noise[3 * a + 2];
     } else {
-      normals3(seed, a, step, xi[0], xi[1], xi[2]);
+      float n0, n1, n2;
+      normals3(seed, a, step, n0, n1, n2);
+      xi[0] = n0;
+      xi[1] = n1;
+      xi[2] = n2;
     }
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      float vv = v[3 * a + c] + half_dt * F[3 * a + c] / m;  // B
-      float xx = x[3 * a + c] + vv * half_dt;                  // A
-      vv = vv * vscale + noisescale * (sig * xi[c]);           // O
-      xx = xx + vv * half_dt;                                  // A
+      T vv = v[3 * a + c] + half_dt * F[3 * a + c] / m;  // B
+      T xx = x[3 * a + c] + vv * half_dt;                  // A
+      vv = vv * vscale + noisescale * (sig * xi[c]);       // O
+      xx = xx + vv * half_dt;                              // A
       v[3 * a + c] = vv;
       x[3 * a + c] = xx;
     }
   }
 }
 
-__global__ __launch_bounds__(256) void b_kernel(float* __restrict__ v,
-                                                const float* __restrict__ F,
-                                                const float* __restrict__ masses, int64_t n,
-                                                float half_dt, int64_t* __restrict__ step_dev) {
+template <typename T>
+__global__ __launch_bounds__(256) void b_kernel(T* __restrict__ v, const T* __restrict__ F,
+                                                const T* __restrict__ masses, int64_t n,
+                                                T half_dt, int64_t* __restrict__ step_dev) {
   for (int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; a < n;
        a += (int64_t)gridDim.x * blockDim.x) {
-    const float m = masses[a];
+    const T m = masses[a];
 #pragma unroll
     for (int c = 0; c < 3; ++c) v[3 * a + c] = v[3 * a + c] + half_dt * F[3 * a + c] / m;
   }
@@ -123,17 +130,46 @@ unsigned groups_for(int64_t n) { return mlcg_persistent_groups(mlcg_div_up(n, 25
 
 }  // namespace
 
+namespace {
+
+template <typename T>
+int launch_baoa(T* pos, T* vel, const T* forces, const T* masses, const T* beta_mass_ratio,
+                int64_t n_nodes, double dt, double vscale, double noisescale, uint64_t seed,
+                const int64_t* step_dev, const T* noise, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && dt > 0.0);
+  if (n_nodes == 0) return MLCG_OK;
+  MLCG_REQUIRE(pos && vel && forces && masses && beta_mass_ratio);
+  hipLaunchKernelGGL(baoa_kernel<T>, dim3(groups_for(n_nodes)), dim3(256), 0,
+                     mlcg_stream(stream), pos, vel, forces, masses, beta_mass_ratio, n_nodes,
+                     (T)(0.5 * dt), (T)vscale, (T)noisescale, seed, step_dev, noise);
+  return mlcg_launch_status();
+}
+
+template <typename T>
+int launch_b(T* vel, const T* forces, const T* masses, int64_t n_nodes, double dt,
+             int64_t* step_dev, void* stream) {
+  MLCG_REQUIRE(n_nodes >= 0 && dt > 0.0);
+  if (n_nodes == 0 && !step_dev) return MLCG_OK;
+  MLCG_REQUIRE(n_nodes == 0 || (vel && forces && masses));
+  hipLaunchKernelGGL(b_kernel<T>, dim3(groups_for(n_nodes)), dim3(256), 0, mlcg_stream(stream),
+                     vel, forces, masses, n_nodes, (T)(0.5 * dt), step_dev);
+  return mlcg_launch_status();
+}
+
+}  // namespace
+
 extern "C" int mlcg_langevin_baoa(float* pos, float* vel, const float* forces,
                                   const float* masses, const float* beta_mass_ratio,
                                   int64_t n_nodes, float dt, float vscale, float noisescale,
                                   uint64_t seed, const int64_t* step_dev, const float* noise,
                                   void* stream) {
+  // 0.5f * dt as before: the float form keeps its single-precision constants
   MLCG_REQUIRE(n_nodes >= 0 && dt > 0.0f);
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(pos && vel && forces && masses && beta_mass_ratio);
-  hipLaunchKernelGGL(baoa_kernel, dim3(groups_for(n_nodes)), dim3(256), 0, mlcg_stream(stream),
-                     pos, vel, forces, masses, beta_mass_ratio, n_nodes, 0.5f * dt, vscale,
-                     noisescale, seed, step_dev, noise);
+  hipLaunchKernelGGL(baoa_kernel<float>, dim3(groups_for(n_nodes)), dim3(256), 0,
+                     mlcg_stream(stream), pos, vel, forces, masses, beta_mass_ratio, n_nodes,
+                     0.5f * dt, vscale, noisescale, seed, step_dev, noise);
   return mlcg_launch_status();
 }
 
@@ -142,9 +178,25 @@ extern "C" int mlcg_langevin_b(float* vel, const float* forces, const float* mas
   MLCG_REQUIRE(n_nodes >= 0 && dt > 0.0f);
   if (n_nodes == 0 && !step_dev) return MLCG_OK;
   MLCG_REQUIRE(n_nodes == 0 || (vel && forces && masses));
-  hipLaunchKernelGGL(b_kernel, dim3(groups_for(n_nodes)), dim3(256), 0, mlcg_stream(stream),
-                     vel, forces, masses, n_nodes, 0.5f * dt, step_dev);
+  hipLaunchKernelGGL(b_kernel<float>, dim3(groups_for(n_nodes)), dim3(256), 0,
+                     mlcg_stream(stream), vel, forces, masses, n_nodes, 0.5f * dt, step_dev);
   return mlcg_launch_status();
+}
+
+extern "C" int mlcg_langevin_baoa_f64(double* pos, double* vel, const double* forces,
+                                      const double* masses, const double* beta_mass_ratio,
+                                      int64_t n_nodes, double dt, double vscale,
+                                      double noisescale, uint64_t seed,
+                                      const int64_t* step_dev, const double* noise,
+                                      void* stream) {
+  return launch_baoa(pos, vel, forces, masses, beta_mass_ratio, n_nodes, dt, vscale,
+                     noisescale, seed, step_dev, noise, stream);
+}
+
+extern "C" int mlcg_langevin_b_f64(double* vel, const double* forces, const double* masses,
+                                   int64_t n_nodes, double dt, int64_t* step_dev,
+                                   void* stream) {
+  return launch_b(vel, forces, masses, n_nodes, dt, step_dev, stream);
 }
 
 extern "C" int mlcg_philox_normals(uint64_t seed, int64_t step, int64_t n_nodes, float* out,

@@ -42,8 +42,8 @@ struct V3T {
 };
 using V3 = V3T<float>;
 using D3 = V3T<double>;
-template <typename T = float>
-__device__ __forceinline__ V3T<T> ld3(const float* __restrict__ p, int64_t i) {
+template <typename T = float, typename P>
+__device__ __forceinline__ V3T<T> ld3(const P* __restrict__ p, int64_t i) {
   return V3T<T>{(T)p[3 * i], (T)p[3 * i + 1], (T)p[3 * i + 2]};
 }
 template <typename T>
@@ -69,21 +69,32 @@ template <typename T>
 __device__ __forceinline__ V3T<T> cross(V3T<T> a, V3T<T> b) {
   return V3T<T>{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
 }
-template <typename T>
-__device__ __forceinline__ void st3(float* __restrict__ f, int64_t slot, V3T<T> v) {
-  f[3 * slot] = (float)v.x;
-  f[3 * slot + 1] = (float)v.y;
-  f[3 * slot + 2] = (float)v.z;
+template <typename S, typename T>
+__device__ __forceinline__ void st3(S* __restrict__ f, int64_t slot, V3T<T> v) {
+  f[3 * slot] = (S)v.x;
+  f[3 * slot + 1] = (S)v.y;
+  f[3 * slot + 2] = (S)v.z;
 }
+__device__ __forceinline__ void sin_cos(float x, float* s, float* c) { sincosf(x, s, c); }
+__device__ __forceinline__ void sin_cos(double x, double* s, double* c) { sincos(x, s, c); }
+__device__ __forceinline__ float sqrt_t(float x) { return sqrtf(x); }
+__device__ __forceinline__ double sqrt_t(double x) { return sqrt(x); }
+__device__ __forceinline__ float atan2_t(float y, float x) { return atan2f(y, x); }
+__device__ __forceinline__ double atan2_t(double y, double x) { return atan2(y, x); }
 
-template <int KIND>
+// S: the storage type of positions, parameters, energies and slot forces
+// (float, or double for a model moved to double).  Bonds and angles are
+// evaluated in double either way; the repulsion and the dihedrals in S.
+template <int KIND, typename S>
 __global__ __launch_bounds__(256) void prior_terms_kernel(
-    int n_degs, const float* __restrict__ pos, const int64_t* __restrict__ map,
-    int64_t stride, int64_t M, const float* __restrict__ params, int n_params,
-    float* __restrict__ energy, float* __restrict__ slot_f) {
+    int n_degs, const S* __restrict__ pos, const int64_t* __restrict__ map,
+    int64_t stride, int64_t M, const S* __restrict__ params, int n_params,
+    S* __restrict__ energy, S* __restrict__ slot_f) {
+  using C = S;  // compute type of the repulsion and the dihedrals
+  using VC = V3T<C>;
   for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M;
        m += (int64_t)gridDim.x * blockDim.x) {
-    const float* pr = params + m * n_params;
+    const S* pr = params + m * n_params;
     if (KIND == MLCG_PRIOR_BOND) {
       // Harmonic terms are evaluated in fp64 from the fp32 positions: the
       // force 2 k (r - x0) of a stiff bond (k = 100 at config 5) amplifies the
@@ -98,25 +109,25 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const double dr = r - x0;
       const double dUdr = 2.0 * k * dr;
       const D3 fi = scl(dUdr / r, d);  // force on bead 0; bead 1 gets -fi
-      energy[m] = (float)(k * (dr * dr) + v0);
+      energy[m] = (S)(k * (dr * dr) + v0);
       if (slot_f) {
         st3(slot_f, 2 * m, fi);
         st3(slot_f, 2 * m + 1, scl(-1.0, fi));
       }
     } else if (KIND == MLCG_PRIOR_REPULSION) {
-      const V3 pi = ld3(pos, map[m]);
-      const V3 pj = ld3(pos, map[stride + m]);
-      const V3 d = sub(pj, pi);
-      const float r = sqrtf(dot(d, d));
-      const float s = pr[0] / r;
-      const float rr = s * s;
-      const float e = rr * rr * rr;
-      const float dUdr = -6.0f * e / r;
-      const V3 fi = scl(dUdr / r, d);
+      const VC pi = ld3<C>(pos, map[m]);
+      const VC pj = ld3<C>(pos, map[stride + m]);
+      const VC d = sub(pj, pi);
+      const C r = sqrt_t(dot(d, d));
+      const C s = pr[0] / r;
+      const C rr = s * s;
+      const C e = rr * rr * rr;
+      const C dUdr = (C)-6.0 * e / r;
+      const VC fi = scl(dUdr / r, d);
       energy[m] = e;
       if (slot_f) {
         st3(slot_f, 2 * m, fi);
-        st3(slot_f, 2 * m + 1, scl(-1.0f, fi));
+        st3(slot_f, 2 * m + 1, scl((C)-1.0, fi));
       }
     } else if (KIND == MLCG_PRIOR_ANGLE) {
       // fp64 for the same reason as the bonds (k (cos t - x0)^2)
@@ -128,7 +139,7 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
       const double c = dot(a, b) / na / nb;
       const double x0 = pr[0], k = pr[1], v0 = pr[2];
       const double dc = c - x0;
-      energy[m] = (float)(k * (dc * dc) + v0);
+      energy[m] = (S)(k * (dc * dc) + v0);
       const double g = 2.0 * k * dc;  // dU/dcos
       const double inv = 1.0 / (na * nb);
       const D3 dca = sub(scl(inv, b), scl(c / (na * na), a));
@@ -140,33 +151,33 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
         st3(slot_f, 3 * m + 2, f2);
       }
     } else {  // MLCG_PRIOR_DIHEDRAL
-      const V3 pi = ld3(pos, map[m]);
-      const V3 pj = ld3(pos, map[stride + m]);
-      const V3 pk = ld3(pos, map[2 * stride + m]);
-      const V3 pl = ld3(pos, map[3 * stride + m]);
-      const V3 rij = sub(pi, pj), rkj = sub(pk, pj), rkl = sub(pk, pl);
-      const V3 mv = cross(rij, rkj), nv = cross(rkj, rkl);
-      const float rkj2 = dot(rkj, rkj);
-      const float nrkj = sqrtf(rkj2);
-      const float t = atan2f(nrkj * dot(rij, nv), dot(mv, nv));
-      float V = pr[0], dV = 0.0f;
+      const VC pi = ld3<C>(pos, map[m]);
+      const VC pj = ld3<C>(pos, map[stride + m]);
+      const VC pk = ld3<C>(pos, map[2 * stride + m]);
+      const VC pl = ld3<C>(pos, map[3 * stride + m]);
+      const VC rij = sub(pi, pj), rkj = sub(pk, pj), rkl = sub(pk, pl);
+      const VC mv = cross(rij, rkj), nv = cross(rkj, rkl);
+      const C rkj2 = dot(rkj, rkj);
+      const C nrkj = sqrt_t(rkj2);
+      const C t = atan2_t(nrkj * dot(rij, nv), dot(mv, nv));
+      C V = pr[0], dV = 0;
       for (int d = 1; d <= n_degs; ++d) {
-        float s, co;
-        sincosf((float)d * t, &s, &co);
-        const float k1 = pr[d], k2 = pr[n_degs + d];
-        V += k1 * s + k2 * co;
-        dV += (float)d * (k1 * co - k2 * s);
+        C sn, co;
+        sin_cos((C)d * t, &sn, &co);
+        const C k1 = pr[d], k2 = pr[n_degs + d];
+        V += k1 * sn + k2 * co;
+        dV += (C)d * (k1 * co - k2 * sn);
       }
       energy[m] = V;
-      const V3 fi = scl(-dV * nrkj / dot(mv, mv), mv);
-      const V3 fl = scl(dV * nrkj / dot(nv, nv), nv);
-      const float p = dot(rij, rkj) / rkj2, q = dot(rkl, rkj) / rkj2;
-      const V3 sv = sub(scl(p, fi), scl(q, fl));
-      const V3 fj = sub(fi, sv), fk = add(fl, sv);
+      const VC fi = scl(-dV * nrkj / dot(mv, mv), mv);
+      const VC fl = scl(dV * nrkj / dot(nv, nv), nv);
+      const C p = dot(rij, rkj) / rkj2, q = dot(rkl, rkj) / rkj2;
+      const VC sv = sub(scl(p, fi), scl(q, fl));
+      const VC fj = sub(fi, sv), fk = add(fl, sv);
       if (slot_f) {
         st3(slot_f, 4 * m, fi);
-        st3(slot_f, 4 * m + 1, scl(-1.0f, fj));
-        st3(slot_f, 4 * m + 2, scl(-1.0f, fk));
+        st3(slot_f, 4 * m + 1, scl((C)-1.0, fj));
+        st3(slot_f, 4 * m + 2, scl((C)-1.0, fk));
         st3(slot_f, 4 * m + 3, fl);
       }
     }
@@ -181,15 +192,16 @@ __global__ __launch_bounds__(256) void prior_terms_kernel(
 // dependent load at a time).
 constexpr int kGatherLanes = 16;
 
+template <typename S>
 __global__ __launch_bounds__(256) void prior_gather_kernel(
-    const float* __restrict__ slot_f, const int32_t* __restrict__ bead_ptr,
+    const S* __restrict__ slot_f, const int32_t* __restrict__ bead_ptr,
     const int32_t* __restrict__ bead_slots, int64_t n, int accumulate,
-    float* __restrict__ forces) {
+    S* __restrict__ forces) {
   const int sub = threadIdx.x % kGatherLanes;
   const int64_t ngroups = (int64_t)gridDim.x * blockDim.x / kGatherLanes;
   for (int64_t a = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kGatherLanes; a < n;
        a += ngroups) {
-    float fx = 0.f, fy = 0.f, fz = 0.f;
+    S fx = 0, fy = 0, fz = 0;
     const int32_t s1 = bead_ptr[a + 1];
     for (int32_t s = bead_ptr[a] + sub; s < s1; s += kGatherLanes) {
       const int64_t slot = bead_slots[s];
@@ -445,10 +457,12 @@ extern "C" int mlcg_prior_order(int kind) { return order_of(kind); }
 
 extern "C" int mlcg_prior_num_params(int kind, int n_degs) { return params_of(kind, n_degs); }
 
-extern "C" int mlcg_prior_terms(int kind, int n_degs, const float* pos,
-                                const int64_t* index_mapping, int64_t mapping_stride,
-                                int64_t n_interactions, const float* params, int n_params,
-                                float* energy, float* slot_forces, void* stream) {
+namespace {
+
+template <typename S>
+int launch_prior_terms(int kind, int n_degs, const S* pos, const int64_t* index_mapping,
+                       int64_t mapping_stride, int64_t n_interactions, const S* params,
+                       int n_params, S* energy, S* slot_forces, void* stream) {
   if (order_of(kind) == 0) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(n_interactions >= 0 && mapping_stride >= n_interactions);
   MLCG_REQUIRE(kind != MLCG_PRIOR_DIHEDRAL || (n_degs >= 1 && n_degs <= 64));
@@ -457,42 +471,72 @@ extern "C" int mlcg_prior_terms(int kind, int n_degs, const float* pos,
   MLCG_REQUIRE(pos && index_mapping && params && energy);
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_interactions, 256), 8);
   hipStream_t s = mlcg_stream(stream);
+#define MLCG_TERMS_LAUNCH(KIND)                                                              \
+  hipLaunchKernelGGL((prior_terms_kernel<KIND, S>), dim3(groups), dim3(256), 0, s, n_degs,  \
+                     pos, index_mapping, mapping_stride, n_interactions, params, n_params,  \
+                     energy, slot_forces)
   switch (kind) {
     case MLCG_PRIOR_BOND:
-      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_BOND>, dim3(groups), dim3(256), 0, s,
-                         n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
-                         n_params, energy, slot_forces);
+      MLCG_TERMS_LAUNCH(MLCG_PRIOR_BOND);
       break;
     case MLCG_PRIOR_ANGLE:
-      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_ANGLE>, dim3(groups), dim3(256), 0, s,
-                         n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
-                         n_params, energy, slot_forces);
+      MLCG_TERMS_LAUNCH(MLCG_PRIOR_ANGLE);
       break;
     case MLCG_PRIOR_DIHEDRAL:
-      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_DIHEDRAL>, dim3(groups), dim3(256), 0,
-                         s, n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
-                         n_params, energy, slot_forces);
+      MLCG_TERMS_LAUNCH(MLCG_PRIOR_DIHEDRAL);
       break;
     default:
-      hipLaunchKernelGGL(prior_terms_kernel<MLCG_PRIOR_REPULSION>, dim3(groups), dim3(256), 0,
-                         s, n_degs, pos, index_mapping, mapping_stride, n_interactions, params,
-                         n_params, energy, slot_forces);
+      MLCG_TERMS_LAUNCH(MLCG_PRIOR_REPULSION);
       break;
   }
+#undef MLCG_TERMS_LAUNCH
   return mlcg_launch_status();
 }
 
-extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
-                                        const int32_t* bead_slots, int64_t n_nodes,
-                                        int accumulate, float* forces, void* stream) {
+template <typename S>
+int launch_prior_gather(const S* slot_forces, const int32_t* bead_ptr,
+                        const int32_t* bead_slots, int64_t n_nodes, int accumulate, S* forces,
+                        void* stream) {
   MLCG_REQUIRE(n_nodes >= 0);
   if (n_nodes == 0) return MLCG_OK;
   MLCG_REQUIRE(bead_ptr && forces);
   MLCG_REQUIRE(slot_forces || bead_slots == nullptr);
   const unsigned groups = mlcg_persistent_groups(mlcg_div_up(n_nodes * kGatherLanes, 256), 8);
-  hipLaunchKernelGGL(prior_gather_kernel, dim3(groups), dim3(256), 0, mlcg_stream(stream),
+  hipLaunchKernelGGL(prior_gather_kernel<S>, dim3(groups), dim3(256), 0, mlcg_stream(stream),
                      slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces);
   return mlcg_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mlcg_prior_terms(int kind, int n_degs, const float* pos,
+                                const int64_t* index_mapping, int64_t mapping_stride,
+                                int64_t n_interactions, const float* params, int n_params,
+                                float* energy, float* slot_forces, void* stream) {
+  return launch_prior_terms(kind, n_degs, pos, index_mapping, mapping_stride, n_interactions,
+                            params, n_params, energy, slot_forces, stream);
+}
+
+extern "C" int mlcg_prior_terms_f64(int kind, int n_degs, const double* pos,
+                                    const int64_t* index_mapping, int64_t mapping_stride,
+                                    int64_t n_interactions, const double* params, int n_params,
+                                    double* energy, double* slot_forces, void* stream) {
+  return launch_prior_terms(kind, n_degs, pos, index_mapping, mapping_stride, n_interactions,
+                            params, n_params, energy, slot_forces, stream);
+}
+
+extern "C" int mlcg_prior_gather_forces(const float* slot_forces, const int32_t* bead_ptr,
+                                        const int32_t* bead_slots, int64_t n_nodes,
+                                        int accumulate, float* forces, void* stream) {
+  return launch_prior_gather(slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces,
+                             stream);
+}
+
+extern "C" int mlcg_prior_gather_forces_f64(const double* slot_forces, const int32_t* bead_ptr,
+                                            const int32_t* bead_slots, int64_t n_nodes,
+                                            int accumulate, double* forces, void* stream) {
+  return launch_prior_gather(slot_forces, bead_ptr, bead_slots, n_nodes, accumulate, forces,
+                             stream);
 }
 
 namespace {

@@ -45,6 +45,12 @@ class _PriorEnergy(torch.autograd.Function):
         return gpos, None, None, None, None, None
 
 
+def _pos_for_kernels(pos: torch.Tensor) -> torch.Tensor:
+    """float64 positions stay double (a model moved to double, the reference's
+    dtype="double" simulations); anything else runs in float32."""
+    return pos if pos.dtype == torch.float64 else pos.float()
+
+
 def _n_frames(data) -> int:
     if "n_atoms" in data:
         return int(data.n_atoms.numel())
@@ -115,7 +121,7 @@ class _Prior(torch.nn.Module):
     def forward(self, data):
         require_device(data.pos)
         g = self.prior_graph(data)
-        E = _PriorEnergy.apply(data.pos.float(), self.kind, self.n_degs, g,
+        E = _PriorEnergy.apply(_pos_for_kernels(data.pos), self.kind, self.n_degs, g,
                                self._params(data), self._batch(data))
         data.out[self.name] = {ENERGY_KEY: E}
         return data
@@ -126,7 +132,7 @@ class _Prior(torch.nn.Module):
         """(E [B], F [N, 3]); F is added into `forces` when given."""
         require_device(data.pos)
         g = self.prior_graph(data)
-        return ops.prior_energy_forces(self.kind, self.n_degs, data.pos.detach().float(), g,
+        return ops.prior_energy_forces(self.kind, self.n_degs, _pos_for_kernels(data.pos.detach()), g,
                                        self._params(data), forces=forces)
 
     def _types(self, data, order):

@@ -105,7 +105,9 @@ class CFConv(torch.nn.Module):
         n = x.shape[0]
         fwd = _edge_csr(edge_index, n, by_row=1)
         bwd = _edge_csr(edge_index, n, by_row=0)
-        agg = _EdgeGather.apply(y, W.float(), fwd, bwd, edge_index[0], edge_index[1])
+        # float64 models (moved to double) gather in double, others in float32
+        dt = torch.float64 if y.dtype == torch.float64 else torch.float32
+        agg = _EdgeGather.apply(y.to(dt), W.to(dt), fwd, bwd, edge_index[0], edge_index[1])
         if self.aggr == "mean":
             # PyG's mean aggregation: the sum over a receiver's messages divided
             # by their number, zero for a receiver without any
@@ -222,7 +224,7 @@ class SchNet(torch.nn.Module):
         bt = _basis_tensors(rbf)
         key = (bool(self.fp16_filters), bool(self.strict_fp32_filters), type(rbf),
                len(self.interaction_blocks),
-               bool(getattr(rbf, "trainable", False)))
+               bool(getattr(rbf, "trainable", False)), self._param_dtype())
         if bt is not None:
             # a float32 contiguous tensor is used in place; anything else is
             # converted, and the conversion is redone when the source changes
@@ -236,8 +238,14 @@ class SchNet(torch.nn.Module):
         self.__dict__["_spec_cache"] = (key, spec)
         return spec
 
+    def _param_dtype(self):
+        w = getattr(self.embedding_layer, "weight", None)
+        return None if w is None else w.dtype
+
     def _build_fused_spec(self) -> Optional[_fused.FusedSpec]:
         rbf = self.rbf_layer
+        if self._param_dtype() != torch.float32:
+            return None  # a model moved to double runs module by module in float64
         bt = _basis_tensors(rbf)
         if bt is None or bt[1].numel() != (bt[0].numel() if isinstance(rbf, ExpNormalBasis)
                                            else 1):
@@ -387,7 +395,8 @@ class _SegmentSum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, values, frame_ptr, batch):
         ctx.batch = batch
-        return ops.segment_sum(values.float(), frame_ptr)
+        return ops.segment_sum(values if values.dtype == torch.float64 else values.float(),
+                               frame_ptr)
 
     @staticmethod
     def backward(ctx, g):

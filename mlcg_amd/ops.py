@@ -1039,10 +1039,18 @@ def _wptr(W: torch.Tensor) -> Tuple[int, int]:
 
 
 def cfconv_gather(src: torch.Tensor, W: torch.Tensor, graph: PairGraph) -> torch.Tensor:
-    """out[i] = sum_j src[j] * W[p(i, j)]  (schnet.py:346,368)."""
+    """out[i] = sum_j src[j] * W[p(i, j)]  (schnet.py:346,368).  float64 src
+    and W (a model moved to double) take mlcg_cfconv_gather_f64, any width."""
     require_device(src, W)
     src = src.contiguous()
     out = torch.empty_like(src)
+    if src.dtype == torch.float64:
+        _check(W.dtype == torch.float64 and W.shape[1] == src.shape[1],
+               "a float64 gather takes float64 filters of the source's width")
+        call("mlcg_cfconv_gather_f64", ptr(src), ptr(W.contiguous()), ptr(graph.rowptr),
+             ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes, src.shape[1], ptr(out),
+             stream_handle(src.device))
+        return out
     wp, wf16 = _wptr(W)
     call("mlcg_cfconv_gather", ptr(src), wp, wf16, ptr(graph.rowptr), ptr(graph.col),
          ptr(graph.eid2pair), graph.num_nodes, src.shape[1], ptr(out),
@@ -1119,10 +1127,15 @@ def pair_forces(pos: torch.Tensor, dist: torch.Tensor, dbar: torch.Tensor,
 
 
 def segment_sum(values: torch.Tensor, frame_ptr: torch.Tensor) -> torch.Tensor:
-    """Per-frame sums of a [N] or [N, 1] float32 vector."""
+    """Per-frame sums of a [N] or [N, 1] float32 (or float64) vector."""
     require_device(values)
     v = values.contiguous().view(-1)
     nb = frame_ptr.numel() - 1
+    if v.dtype == torch.float64:
+        out = torch.empty(nb, dtype=torch.float64, device=values.device)
+        call("mlcg_segment_sum_f64", ptr(v), ptr(frame_ptr), nb, ptr(out),
+             stream_handle(values.device))
+        return out
     out = torch.empty(nb, dtype=torch.float32, device=values.device)
     call("mlcg_segment_sum", ptr(v), 1, ptr(frame_ptr), nb, ptr(out),
          stream_handle(values.device))
@@ -1197,19 +1210,29 @@ def prior_graph(index_mapping: torch.Tensor, mapping_batch: Optional[torch.Tenso
 
 def prior_terms(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorGraph,
                 params: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(energy [M], slot forces [M, order, 3]) of every interaction."""
-    pos = _validate_pos(pos)
+    """(energy [M], slot forces [M, order, 3]) of every interaction, in the
+    positions' type (float32, or float64 for a model moved to double)."""
+    f64 = pos.dtype == torch.float64
+    pos = _validate_pos_f64(pos) if f64 else _validate_pos(pos)
+    dt = pos.dtype
     M = graph.num_interactions
     order = PRIOR_ORDER[kind]
     n_params = int(_lib.load().mlcg_prior_num_params(kind, n_degs))
-    params = params.to(torch.float32).contiguous()
+    params = params.to(dt).contiguous()
     _check(tuple(params.shape) == (M, n_params),
            f"params must be [{M}, {n_params}], got {tuple(params.shape)}")
-    energy = torch.empty(M, dtype=torch.float32, device=pos.device)
-    slot_f = torch.empty(M, order, 3, dtype=torch.float32, device=pos.device)
-    call("mlcg_prior_terms", kind, n_degs, ptr(pos), ptr(graph.index_mapping), M, M,
-         ptr(params), n_params, ptr(energy), ptr(slot_f), stream_handle(pos.device))
+    energy = torch.empty(M, dtype=dt, device=pos.device)
+    slot_f = torch.empty(M, order, 3, dtype=dt, device=pos.device)
+    call("mlcg_prior_terms_f64" if f64 else "mlcg_prior_terms", kind, n_degs, ptr(pos),
+         ptr(graph.index_mapping), M, M, ptr(params), n_params, ptr(energy), ptr(slot_f),
+         stream_handle(pos.device))
     return energy, slot_f
+
+
+def _validate_pos_f64(pos: torch.Tensor) -> torch.Tensor:
+    require_device(pos)
+    _check(pos.dim() == 2 and pos.shape[1] == 3, lambda: f"pos must be [N, 3], got {tuple(pos.shape)}")
+    return pos.contiguous()
 
 
 def prior_pair_records(graph: PriorGraph, params: torch.Tensor) -> torch.Tensor:
@@ -1238,9 +1261,11 @@ def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorG
     forces straight from the positions per bead (mlcg_prior_repulsion, the
     same values as the slot-force path, without slot force arrays)."""
     accumulate = forces is not None
+    f64 = pos.dtype == torch.float64
     if forces is None:
-        forces = torch.empty(graph.num_nodes, 3, dtype=torch.float32, device=pos.device)
-    if kind == PRIOR_KIND["repulsion"]:
+        forces = torch.empty(graph.num_nodes, 3, dtype=pos.dtype if f64 else torch.float32,
+                             device=pos.device)
+    if kind == PRIOR_KIND["repulsion"] and not f64:
         pos = _validate_pos(pos)
         M = graph.num_interactions
         params = params.to(torch.float32).contiguous()
@@ -1255,8 +1280,10 @@ def prior_energy_forces(kind: int, n_degs: int, pos: torch.Tensor, graph: PriorG
         return segment_sum(energy, graph.seg_ptr), forces
     energy, slot_f = prior_terms(kind, n_degs, pos, graph, params)
     E = segment_sum(energy, graph.seg_ptr)
-    call("mlcg_prior_gather_forces", ptr(slot_f), ptr(graph.bead_ptr), ptr(graph.bead_slots),
-         graph.num_nodes, int(accumulate), ptr(forces), stream_handle(pos.device))
+    _check(forces.dtype == energy.dtype, "forces must have the positions' dtype")
+    call("mlcg_prior_gather_forces_f64" if f64 else "mlcg_prior_gather_forces", ptr(slot_f),
+         ptr(graph.bead_ptr), ptr(graph.bead_slots), graph.num_nodes, int(accumulate),
+         ptr(forces), stream_handle(pos.device))
     return E, forces
 
 
@@ -1268,23 +1295,24 @@ def langevin_baoa(pos: torch.Tensor, vel: torch.Tensor, forces: torch.Tensor,
                   vscale: float, noisescale: float, seed: int,
                   step: Optional[torch.Tensor] = None,
                   noise: Optional[torch.Tensor] = None) -> None:
-    """B, A, O, A sub-steps in place on pos and vel ([N, 3] float32)."""
+    """B, A, O, A sub-steps in place on pos and vel ([N, 3] float32, or all
+    float64 for a simulation in double precision)."""
     require_device(pos, vel, forces, masses, beta_mass_ratio)
+    dt_ = pos.dtype if pos.dtype == torch.float64 else torch.float32
     for t in (pos, vel, forces):
-        _check(t.dtype == torch.float32 and t.is_contiguous() and t.shape == pos.shape,
-               "pos, vel and forces must be contiguous float32 [N, 3]")
+        _check(t.dtype == dt_ and t.is_contiguous() and t.shape == pos.shape,
+               f"pos, vel and forces must be contiguous {dt_} [N, 3]")
     n = pos.shape[0]
     _check(masses.numel() == n and beta_mass_ratio.numel() == n,
            "masses and beta_mass_ratio must have one entry per bead")
     if noise is not None:
-        _check(noise.shape == pos.shape and noise.dtype == torch.float32,
-               "noise must be float32 [N, 3]")
+        _check(noise.shape == pos.shape and noise.dtype == dt_, f"noise must be {dt_} [N, 3]")
         noise = noise.contiguous()
     if step is not None:
         _check(step.dtype == torch.int64 and step.numel() == 1, "step must be one int64")
-    call("mlcg_langevin_baoa", ptr(pos), ptr(vel), ptr(forces),
-         ptr(masses.to(torch.float32).contiguous()),
-         ptr(beta_mass_ratio.to(torch.float32).contiguous()), n, float(dt), float(vscale),
+    call("mlcg_langevin_baoa_f64" if dt_ == torch.float64 else "mlcg_langevin_baoa", ptr(pos),
+         ptr(vel), ptr(forces), ptr(masses.to(dt_).contiguous()),
+         ptr(beta_mass_ratio.to(dt_).contiguous()), n, float(dt), float(vscale),
          float(noisescale), int(seed) & ((1 << 64) - 1), ptr(step), ptr(noise),
          stream_handle(pos.device))
 
@@ -1293,6 +1321,12 @@ def langevin_b(vel: torch.Tensor, forces: torch.Tensor, masses: torch.Tensor, dt
                step: Optional[torch.Tensor] = None) -> None:
     """Final B sub-step in place on vel; advances `step` by one."""
     require_device(vel, forces, masses)
+    if vel.dtype == torch.float64:
+        _check(forces.dtype == torch.float64, "forces must be float64 with float64 velocities")
+        call("mlcg_langevin_b_f64", ptr(vel), ptr(forces),
+             ptr(masses.to(torch.float64).contiguous()), vel.shape[0], float(dt), ptr(step),
+             stream_handle(vel.device))
+        return
     call("mlcg_langevin_b", ptr(vel), ptr(forces), ptr(masses.to(torch.float32).contiguous()),
          vel.shape[0], float(dt), ptr(step), stream_handle(vel.device))
 

@@ -68,8 +68,12 @@ class LangevinSimulation:
                  create_checkpoints: bool = False,
                  read_checkpoint_file: Union[str, bool, None] = None):
         assert friction > 0
-        if dtype != "single":
-            raise NotImplementedError("the HIP kernels integrate in single precision")
+        if dtype not in ("single", "double"):
+            raise ValueError(f"dtype must be 'single' or 'double', got {dtype!r}")
+        if dtype == "double" and capture:
+            # the float64 model runs module by module: its radius graph is sized
+            # on the host every step, which a captured graph cannot do
+            raise ValueError("capture=True needs dtype='single'")
         if n_timesteps % save_interval != 0:
             raise ValueError("n_timesteps must be a multiple of save_interval")
         self.friction = friction
@@ -78,7 +82,7 @@ class LangevinSimulation:
         self.save_interval = save_interval
         self.random_seed = 0 if random_seed is None else int(random_seed)
         self.device = torch.device(device)
-        self.dtype = torch.float32
+        self.dtype = torch.float64 if dtype == "double" else torch.float32
         self.save_forces = save_forces
         self.save_energies = save_energies
         self.capture = capture
@@ -113,7 +117,10 @@ class LangevinSimulation:
     def attach_model_and_configurations(self, model: torch.nn.Module,
                                         configurations: List[AtomicData],
                                         beta: Union[float, List[float]]):
-        self.model = model.eval().to(self.device)
+        # the whole model in the simulation's precision (base.py:271): in
+        # double, SchNet runs module by module in float64 (HIP gather, torch
+        # linears) and the priors and the integrator use their float64 kernels
+        self.model = model.eval().to(device=self.device, dtype=self.dtype)
         for p in self.model.parameters():
             p.requires_grad = False
         self._attach_configurations(configurations, beta)
@@ -147,6 +154,7 @@ class LangevinSimulation:
             g = torch.Generator().manual_seed(self.random_seed)
             data[VELOCITY_KEY] = sample_maxwell_boltzmann(
                 betas, data.masses.cpu(), generator=g).to(self.device, self.dtype)
+        data[VELOCITY_KEY] = data[VELOCITY_KEY].to(self.device, self.dtype).contiguous()
         self.beta_mass_ratio = torch.sqrt(1.0 / betas.to(self.device) / data.masses).contiguous()
         if self.read_checkpoint_file is not None:
             self._read_checkpoint(data)
@@ -207,7 +215,12 @@ class LangevinSimulation:
 
     # ------------------------------------------------------------------
     def calculate_potential_and_forces(self, data):
-        data = self.model(data)
+        # grad mode on, as the reference's loop runs: a model without a fused
+        # pass (a float64 model runs module by module) gets its forces from
+        # GradientsOut's autograd; the fused passes record nothing, since the
+        # parameters do not require gradients
+        with torch.enable_grad():
+            data = self.model(data)
         return data.out[ENERGY_KEY].detach(), data.out[FORCE_KEY].detach()
 
     def _set_capacity(self, data):
@@ -216,7 +229,7 @@ class LangevinSimulation:
         from ..nn.schnet import SchNet
 
         for m in self.model.modules():
-            if isinstance(m, SchNet) and m.graph_capacity is None:
+            if isinstance(m, SchNet) and m.graph_capacity is None and m.fused_spec() is not None:
                 g = m.build_graph(data)
                 cap = int(math.ceil(g.num_edges * self.edge_capacity_factor)) + 64
                 m.graph_capacity = cap + (cap % 2)

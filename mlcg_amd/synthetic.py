@@ -265,24 +265,40 @@ def config5_prior_models(n_types: int = 21):
 
     c = CONFIG5_PRIORS
     top = n_types - 1
-    bonds = nn.HarmonicBonds({(top, top): {"x_0": c["bonds"]["x_0"], "k": c["bonds"]["k"]}})
-    bonds.x_0.fill_(c["bonds"]["x_0"])
-    bonds.k.fill_(c["bonds"]["k"])
     cos0 = math.cos(math.radians(c["angles"]["theta_0_deg"]))
-    angles = nn.HarmonicAngles({(top,) * 3: {"x_0": cos0, "k": c["angles"]["k"]}})
-    angles.x_0.fill_(cos0)
-    angles.k.fill_(c["angles"]["k"])
     d = c["dihedrals"]
-    dih = nn.Dihedral({(top,) * 4: {"k1s": {f"k1_{i + 1}": v for i, v in enumerate(d["k1s"])},
-                                     "k2s": {f"k2_{i + 1}": v for i, v in enumerate(d["k2s"])},
-                                     "v_0": d["v_0"]}}, n_degs=3)
+    mods = {
+        "bonds": nn.HarmonicBonds({(top, top): {"x_0": c["bonds"]["x_0"],
+                                                "k": c["bonds"]["k"]}}),
+        "angles": nn.HarmonicAngles({(top,) * 3: {"x_0": cos0, "k": c["angles"]["k"]}}),
+        "dihedrals": nn.Dihedral(
+            {(top,) * 4: {"k1s": {f"k1_{i + 1}": v for i, v in enumerate(d["k1s"])},
+                          "k2s": {f"k2_{i + 1}": v for i, v in enumerate(d["k2s"])},
+                          "v_0": d["v_0"]}}, n_degs=3),
+        "repulsion": nn.Repulsion({(top, top): {"sigma": c["repulsion"]["sigma"]}}),
+    }
+    fill_config5_prior_constants(mods)
+    return mods
+
+
+def fill_config5_prior_constants(mods) -> None:
+    """Fills the type tables of the config-5 prior modules (as made by
+    config5_prior_models) with the CONFIG5_PRIORS constants, in the tables'
+    own dtype: after a move to float64 this makes them the exact decimal
+    constants rather than their float32 roundings."""
+    import math
+
+    c = CONFIG5_PRIORS
+    mods["bonds"].x_0.fill_(c["bonds"]["x_0"])
+    mods["bonds"].k.fill_(c["bonds"]["k"])
+    mods["angles"].x_0.fill_(math.cos(math.radians(c["angles"]["theta_0_deg"])))
+    mods["angles"].k.fill_(c["angles"]["k"])
+    d = c["dihedrals"]
     for i in range(3):
-        dih.k1s[i].fill_(d["k1s"][i])
-        dih.k2s[i].fill_(d["k2s"][i])
-    dih.v_0.fill_(d["v_0"])
-    rep = nn.Repulsion({(top, top): {"sigma": c["repulsion"]["sigma"]}})
-    rep.sigma.fill_(c["repulsion"]["sigma"])
-    return {"bonds": bonds, "angles": angles, "dihedrals": dih, "repulsion": rep}
+        mods["dihedrals"].k1s[i].fill_(d["k1s"][i])
+        mods["dihedrals"].k2s[i].fill_(d["k2s"][i])
+    mods["dihedrals"].v_0.fill_(d["v_0"])
+    mods["repulsion"].sigma.fill_(c["repulsion"]["sigma"])
 
 
 def config5_configurations(n_frames: int = 100, n_beads: int = 268):

@@ -47,8 +47,10 @@ def _model():
     return schnet, nn.SumOut(torch.nn.ModuleDict(models))
 
 
-def _oracle_force_fn(schnet, n_frames, types):
-    """Total force of the composite model at given positions, in fp64."""
+def _oracle_force_fn(schnet, n_frames, types, double_graph=False):
+    """Total force of the composite model at given positions, in fp64 (the
+    radius graph searched in float32 as the float32 model does, or in double
+    for a model moved to double)."""
     import math
 
     from mlcg_amd import synthetic
@@ -79,8 +81,8 @@ def _oracle_force_fn(schnet, n_frames, types):
     params["repulsion"] = {"sigma": full(M, c["repulsion"]["sigma"])}
 
     def forces(x64):
-        ei, ovf = oracle_radius.radius_graph(x64.float().numpy(), 20.0, batch.numpy(), False,
-                                             1000)
+        xg = x64.numpy() if double_graph else x64.float().numpy()
+        ei, ovf = oracle_radius.radius_graph(xg, 20.0, batch.numpy(), False, 1000)
         assert ovf == 0
         E, F = R.schnet_energy_forces(sd, cfg, x64, types, batch, torch.from_numpy(ei),
                                       n_frames)
@@ -166,3 +168,56 @@ def test_config5_full_size_captured_run():
     # the capture happens at step 3; steps 3..6 are replays
     np.testing.assert_allclose(xc[:, 2:], xe[:, 2:], rtol=1e-6, atol=1e-5)
     np.testing.assert_allclose(ec[:, 2:], ee[:, 2:], rtol=1e-5, atol=1e-4)
+
+
+def test_double_precision_composite_steps_vs_oracle():
+    """LangevinSimulation(dtype="double") (the reference moves the model to
+    double, base.py:162,271): SchNet module by module in float64 (HIP float64
+    gather and per-frame sums, torch linears), the four priors and BAOAB on
+    their float64 kernels, radius graph in double.  Against the fp64 oracles
+    chained as above (oracle radius graph searched in double) at rtol 1e-9 on
+    forces, energies, positions and velocities -- four orders tighter than a
+    float32 computation could meet."""
+    from mlcg_amd import ops, synthetic
+    from mlcg_amd.simulation import LangevinSimulation
+
+    n_frames, n_steps = 2, 4
+    c = synthetic.CONFIG5_PRIORS
+    schnet, model = _model()
+    confs = synthetic.config5_configurations(n_frames=n_frames, n_beads=N_BEADS)
+    beta = L.beta_of(c["temperature_K"])
+    sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"],
+                             n_timesteps=n_steps, save_interval=1, random_seed=SEED,
+                             dtype="double")
+    sim.attach_model_and_configurations(model, confs, beta)
+    assert all(p.dtype == torch.float64 for p in model.parameters())
+    assert schnet.fused_spec() is None
+    # the priors' tables hold float32 roundings of the constants until refilled
+    # in double (the oracle uses the exact constants)
+    synthetic.fill_config5_prior_constants(
+        {k: model.models[k].model for k in ("bonds", "angles", "dihedrals", "repulsion")})
+    states = []
+    sim._hook = lambda x, v, F, e: states.append(
+        tuple(t.detach().cpu().clone() for t in (x, v, F, e)))
+    sim._hook_interval = 1
+    sim.simulate()
+    assert len(states) == n_steps and all(t.dtype == torch.float64 for t in states[0])
+    types = torch.cat([d.atom_types for d in confs])
+    forces = _oracle_force_fn(schnet, n_frames, types, double_graph=True)
+    m = sim.initial_data.masses.double().cpu()
+    bmr = torch.sqrt(1.0 / (beta * m))
+    vscale, noisescale = L.constants(c["dt_ps"], c["friction_per_ps"])
+    N = m.numel()
+    oracle = [forces(s[0]) for s in states]
+    for k in range(n_steps):
+        _, _, F, epot = states[k]
+        check(F, oracle[k][1], 1e-9, f"double step {k} forces")
+        check(epot, oracle[k][0], 1e-9, f"double step {k} potential energies")
+    for k in range(n_steps - 1):
+        x, v, _, _ = states[k]
+        xn, vn, _, _ = states[k + 1]
+        xi = ops.philox_normals(SEED, k + 1, N, "cuda").double().cpu()
+        x1, v1 = L.baoa(x, v, oracle[k][1], m, bmr, c["dt_ps"], vscale, noisescale, xi)
+        v1 = L.b(v1, oracle[k + 1][1], m, c["dt_ps"])
+        check(xn, x1, 1e-9, f"double step {k + 1} positions")
+        check(vn, v1, 1e-9, f"double step {k + 1} velocities")

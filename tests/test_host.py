@@ -348,3 +348,16 @@ def test_radius_flag_bookkeeping():
     assert (0, 1) in ops._RADIUS_WS
     ops.radius_flags_read(8)
     assert not ops._RADIUS_WS
+
+
+def test_langevin_dtype_options():
+    """LangevinSimulation takes dtype "single" and "double" (base.py:162); a
+    double run is not captured; other dtypes raise."""
+    from mlcg_amd.simulation import LangevinSimulation
+
+    assert LangevinSimulation(dtype="single").dtype == torch.float32
+    assert LangevinSimulation(dtype="double").dtype == torch.float64
+    with pytest.raises(ValueError, match="capture"):
+        LangevinSimulation(dtype="double", capture=True)
+    with pytest.raises(ValueError, match="dtype"):
+        LangevinSimulation(dtype="half")
