@@ -2,9 +2,10 @@
 
 ``LangevinSimulation`` keeps the reference's constructor arguments that shape
 the dynamics (``friction``, ``dt``, ``n_timesteps``, ``save_interval``,
-``random_seed``, ``save_forces``, ``save_energies``, ``dtype``) and its
+``random_seed``, ``save_forces``, ``save_energies``, ``dtype``, ``compile``,
+``compile_mode``, ``force_compile``) and its
 ``attach_model_and_configurations(model, configurations, beta)`` /
-``simulate()`` entry points.  One timestep is
+``simulate()`` / ``compile_model(data)`` entry points.  One timestep is
 
     BAOA kernel (mlcg_langevin_baoa)  ->  model forces  ->  B kernel
 
@@ -66,7 +67,9 @@ class LangevinSimulation:
                  filename: Optional[str] = None, export_interval: Optional[int] = None,
                  log_interval: Optional[int] = None, log_type: str = "write",
                  create_checkpoints: bool = False,
-                 read_checkpoint_file: Union[str, bool, None] = None):
+                 read_checkpoint_file: Union[str, bool, None] = None,
+                 compile: bool = False, compile_mode: str = "default",
+                 force_compile: bool = False):
         assert friction > 0
         if dtype not in ("single", "double"):
             raise ValueError(f"dtype must be 'single' or 'double', got {dtype!r}")
@@ -74,6 +77,10 @@ class LangevinSimulation:
             # the float64 model runs module by module: its radius graph is sized
             # on the host every step, which a captured graph cannot do
             raise ValueError("capture=True needs dtype='single'")
+        if compile and capture:
+            # the captured step already replays the kernels without the host;
+            # torch.compile is for the eager loop
+            raise ValueError("compile=True and capture=True are exclusive")
         if n_timesteps % save_interval != 0:
             raise ValueError("n_timesteps must be a multiple of save_interval")
         self.friction = friction
@@ -109,6 +116,10 @@ class LangevinSimulation:
         self.create_checkpoints = create_checkpoints
         self.read_checkpoint_file = None if read_checkpoint_file is False else read_checkpoint_file
         self.current_timestep = 0  # files already written (restored from a checkpoint)
+        # torch.compile of the model at the start of simulate() (base.py:447-489)
+        self.compile = bool(compile)
+        self.compile_mode = compile_mode
+        self.force_compile = bool(force_compile)
         # hook run eagerly every `_hook_interval` steps on (x, v, F, potential)
         self._hook = None
         self._hook_interval = 0
@@ -223,6 +234,51 @@ class LangevinSimulation:
             data = self.model(data)
         return data.out[ENERGY_KEY].detach(), data.out[FORCE_KEY].detach()
 
+    def _run_and_check(self, data):
+        """One model call whose energies and forces must be finite
+        (base.py:434-445)."""
+        potential, forces = self.calculate_potential_and_forces(data)
+        if not bool(torch.isfinite(forces).all()):
+            raise RuntimeError("Invalid values detected in computed forces.")
+        if not bool(torch.isfinite(potential).all()):
+            raise RuntimeError("Invalid values detected in computed potential.")
+
+    def compile_model(self, data):
+        """With ``compile=True``: ``torch.compile(model, dynamic=True,
+        mode=compile_mode)`` (base.py:447-489).  A batch of one structure is
+        left eager unless ``force_compile``; if compiling or the first
+        compiled call fails, the model is compiled again with dynamo's
+        suppress_errors, so the failing parts run eagerly.  Either way the
+        model is run once and its outputs checked for non-finite values.
+
+        The fused SchNet and prior passes launch HIP kernels through ctypes,
+        so dynamo runs them as opaque calls (graph breaks); the compiler
+        works on the torch code around them."""
+        if self.compile:
+            if int(data.batch.max()) == 0 and not self.force_compile:
+                warnings.warn(
+                    "Compilation is allowed only when more than one structure is provided; "
+                    "the simulation runs in non-compiled mode (force_compile=True overrides "
+                    "this, with the risks of compiled scatter operations on one structure)")
+            else:
+                if int(data.batch.max()) == 0:
+                    warnings.warn("Forcing compilation with only one structure in the batch")
+                import logging
+                import torch._dynamo
+
+                torch._logging.set_logs(dynamo=logging.ERROR)
+                try:
+                    self.model = torch.compile(self.model, dynamic=True, mode=self.compile_mode)
+                    self._run_and_check(data)
+                    return
+                except Exception as e:  # the reference's fallback, base.py:467-486
+                    warnings.warn(f"torch.compile failed ({e}); compiling again with "
+                                  "torch._dynamo.config.suppress_errors = True")
+                    torch._dynamo.config.suppress_errors = True
+                    model = getattr(self.model, "_orig_mod", self.model)
+                    self.model = torch.compile(model, dynamic=True, mode=self.compile_mode)
+        self._run_and_check(data)
+
     def _set_capacity(self, data):
         """Fixed radius-graph capacities for every SchNet in the model (from
         the initial structure's edge count), so that no step synchronises."""
@@ -286,6 +342,7 @@ class LangevinSimulation:
                 sticky.bitwise_or_(fl)
 
         with torch.no_grad():
+            self.compile_model(data)
             e0, f0 = self.calculate_potential_and_forces(data)
             or_flags()
         F.copy_(f0)

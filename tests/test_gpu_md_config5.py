@@ -221,3 +221,46 @@ def test_double_precision_composite_steps_vs_oracle():
         v1 = L.b(v1, oracle[k + 1][1], m, c["dt_ps"])
         check(xn, x1, 1e-9, f"double step {k + 1} positions")
         check(vn, v1, 1e-9, f"double step {k + 1} velocities")
+
+
+def test_compiled_simulation_matches_eager():
+    """LangevinSimulation(compile=True): the model goes through
+    torch.compile(dynamic=True) with the default (inductor) backend at the
+    start of simulate(), as the reference's simulation does (base.py:447-489);
+    its energies, forces and trajectory equal the eager run's within the
+    reference's own compiled-vs-eager bar (rtol = atol = 1e-5,
+    tests/unit/simulation/test_compilation.py:264-269)."""
+    from mlcg_amd import synthetic
+    from mlcg_amd.simulation import LangevinSimulation
+
+    n_frames, n_steps = 4, 4
+    c = synthetic.CONFIG5_PRIORS
+    runs = []
+    for compile_flag in (False, True):
+        print(f"config-5 composite step, {n_frames} x {N_BEADS} beads, compile={compile_flag}",
+              flush=True)
+        _, model = _model()
+        sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"],
+                                 n_timesteps=n_steps, save_interval=1, random_seed=SEED,
+                                 save_energies=True, save_forces=True, compile=compile_flag)
+        sim.attach_model_and_configurations(
+            model, synthetic.config5_configurations(n_frames=n_frames, n_beads=N_BEADS),
+            L.beta_of(c["temperature_K"]))
+        import warnings
+
+        import torch._dynamo.utils
+
+        torch._dynamo.utils.counters.clear()
+        with warnings.catch_warnings(record=True) as caught:
+            warnings.simplefilter("always")
+            x = sim.simulate()
+        # compiled without the suppress_errors fallback
+        assert not any("torch.compile failed" in str(w.message) for w in caught)
+        assert isinstance(sim.model, torch._dynamo.eval_frame.OptimizedModule) == compile_flag
+        breaks = dict(torch._dynamo.utils.counters["graph_break"])
+        print(f"  graph breaks: {sum(breaks.values())} ({len(breaks)} reasons)", flush=True)
+        for reason in list(breaks)[:6]:
+            print("   ", reason.splitlines()[0][:150], flush=True)
+        runs.append((x, sim.simulated_potential, sim.simulated_forces))
+    for a, b, what in zip(runs[1], runs[0], ("positions", "energies", "forces")):
+        np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5, err_msg=what)

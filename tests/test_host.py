@@ -361,3 +361,78 @@ def test_langevin_dtype_options():
         LangevinSimulation(dtype="double", capture=True)
     with pytest.raises(ValueError, match="dtype"):
         LangevinSimulation(dtype="half")
+
+
+def test_simulation_compile_model_options(monkeypatch):
+    """compile_model follows the reference's control flow (base.py:447-489):
+    one structure stays eager with a warning unless force_compile; otherwise
+    torch.compile(model, dynamic=True, mode=compile_mode) and one checked
+    call; when the compiled call raises, dynamo's suppress_errors is set and
+    the model compiled again.  torch.compile is replaced by a recorder here
+    (the real compile of the HIP model runs in the GPU tests)."""
+    import warnings
+
+    import torch._dynamo
+
+    from mlcg_amd.data._keys import ENERGY_KEY, FORCE_KEY
+    from mlcg_amd.simulation import LangevinSimulation
+
+    class Toy(torch.nn.Module):
+        def forward(self, data):
+            data.out = {ENERGY_KEY: data.pos.sum().reshape(1), FORCE_KEY: -data.pos}
+            return data
+
+    class Data:
+        def __init__(self, n_frames):
+            self.pos = torch.ones(2 * n_frames, 3)
+            self.batch = torch.arange(n_frames).repeat_interleave(2)
+            self.out = {}
+
+    calls = []
+
+    def fake_compile(model, dynamic=None, mode=None):
+        calls.append((dynamic, mode))
+        if len(calls) == 1 and failing[0]:
+            class Broken(torch.nn.Module):
+                def __init__(self):
+                    super().__init__()
+                    self._orig_mod = model
+
+                def forward(self, data):
+                    raise RuntimeError("unsupported")
+            return Broken()
+        return model
+
+    monkeypatch.setattr(torch, "compile", fake_compile)
+    monkeypatch.setattr(torch._dynamo.config, "suppress_errors", False)
+    failing = [False]
+    with pytest.raises(ValueError):
+        LangevinSimulation(device="cpu", compile=True, capture=True)
+    sim = LangevinSimulation(device="cpu", compile=True, compile_mode="max-autotune")
+    sim.model = Toy()
+    with pytest.warns(UserWarning, match="more than one structure"):
+        sim.compile_model(Data(1))
+    assert calls == []
+    sim.compile_model(Data(2))
+    assert calls == [(True, "max-autotune")]
+    sim = LangevinSimulation(device="cpu", compile=True, force_compile=True)
+    sim.model = Toy()
+    calls.clear()
+    with pytest.warns(UserWarning, match="one structure"):
+        sim.compile_model(Data(1))
+    assert calls == [(True, "default")]
+    failing[0] = True
+    calls.clear()
+    sim = LangevinSimulation(device="cpu", compile=True)
+    sim.model = Toy()
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        sim.compile_model(Data(3))
+    assert any("suppress_errors" in str(x.message) for x in w)
+    assert len(calls) == 2 and torch._dynamo.config.suppress_errors
+    sim = LangevinSimulation(device="cpu")
+    sim.model = Toy()
+    d = Data(2)
+    d.pos[0, 0] = float("nan")
+    with pytest.raises(RuntimeError, match="forces"):
+        sim.compile_model(d)
