@@ -77,6 +77,8 @@ def parse_args(argv=None):
     p.add_argument("--no-md", action="store_true", help="skip the config-5 MD leg")
     p.add_argument("--gather-probe", action="store_true",
                    help="run the gather access-pattern probe (cold caches)")
+    p.add_argument("--mfma-probe", action="store_true",
+                   help="run the MFMA-loop probe (sustained matrix-core rate per shape)")
     p.add_argument("--stream-probe", action="store_true",
                    help="measure the HBM read / copy ceiling with the library's streaming "
                         "kernels")
@@ -585,6 +587,53 @@ def stream_leg(reps=5):
     return out
 
 
+MFMA_PEAKS = {  # published dense peaks of the part (TFLOP/s)
+    "f16_16x16x32": 2500.0, "f16_16x16x16": 2500.0, "f32_16x16x4": 157.3,
+    "bf16_16x16x32": 2500.0, "f16_32x32x16": 2500.0}
+
+
+def mfma_leg(reps=5):
+    """The sustained matrix-core rate of this part for each MFMA shape the
+    kernels use (mlcg_mfma_loop: 8 independent accumulator chains per wave on
+    register operands), for 1 to 4 workgroups of 4 waves per CU; the best
+    median of `reps` launches is kept per shape."""
+    import torch
+
+    from mlcg_amd import _lib
+
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {}
+    for kind, label in enumerate(MFMA_PEAKS):
+        fpw = int(lib.mlcg_mfma_loop_flops_per_wave_iter(kind))
+        best = None
+        for per_cu in (1, 2, 4):
+            groups = n_cu * per_cu
+            buf = torch.empty(groups * 256, dtype=torch.float32, device=dev)
+            iters = 4096 if kind != 2 else 1024
+            _lib.call("mlcg_mfma_loop", kind, iters, groups, buf.data_ptr(), stream)
+            ts = []
+            for _ in range(reps):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _lib.call("mlcg_mfma_loop", kind, iters, groups, buf.data_ptr(), stream)
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) * 1e-3)
+            assert bool(torch.isfinite(buf).all())
+            t = statistics.median(ts)
+            tf = groups * 4 * iters * fpw / t / 1e12
+            if best is None or tf > best["TFLOP_per_s"]:
+                best = {"TFLOP_per_s": round(tf, 1), "us": round(t * 1e6, 1),
+                        "groups_per_cu": per_cu, "iters": iters,
+                        "frac_of_peak": round(tf / MFMA_PEAKS[label], 4)}
+        out[label] = best
+    return out
+
+
 def radius_leg(reps=10):
     """Config 3 radius graph, inputs resident in HBM.  Figures: the exactly
     sized call end to end (sizing pass, one host synchronisation to size the
@@ -1006,6 +1055,8 @@ def main(argv=None):
             res["stream"] = stream_leg()
         if args.gather_probe:
             res["gather_ceiling"] = gather_ceiling_leg()
+        if args.mfma_probe:
+            res["mfma"] = mfma_leg()
         print(json.dumps(res))
         return 0
     if args.captured_only:

@@ -777,6 +777,18 @@ int mlcg_stream_read(const float* src, int64_t n, int groups, int unroll,
 int mlcg_stream_copy(const float* src, float* dst, int64_t n, int groups,
                      int unroll, void* stream);
 
+/* MFMA-loop probe: `groups` workgroups of 4 waves, each wave issuing `iters`
+ * iterations of 8 independent MFMAs of one shape on register operands;
+ * out[groups * 256] receives one float per thread (the accumulators' sum).
+ * kind: 0 v_mfma_f32_16x16x32_f16, 1 v_mfma_f32_16x16x16_f16,
+ * 2 v_mfma_f32_16x16x4_f32, 3 v_mfma_f32_16x16x32_bf16,
+ * 4 v_mfma_f32_32x32x16_f16.  No counterpart in the reference: the sustained
+ * matrix-core rate the MFMA-bound kernels are compared with. */
+int mlcg_mfma_loop(int kind, int64_t iters, int groups, float* out, void* stream);
+
+/* FLOP of one wave iteration of mlcg_mfma_loop for `kind` (-1 if unknown). */
+int64_t mlcg_mfma_loop_flops_per_wave_iter(int kind);
+
 /* The force-matching loss (ForceMSE with reduction "mean",
  * mlcg/nn/losses.py:130-181 -> torch.nn.functional.mse_loss):
  * *loss = sum_k (x[k] - y[k])^2 / n over n >= 1 fp32 elements, summed per

@@ -119,6 +119,8 @@ _SIGNATURES = {
     "mlcg_embedding_gather": [_P, _I32, _I32, _P, _I64, _P, _P],
     "mlcg_stream_read": [_P, _I64, _I32, _I32, _P, _P],
     "mlcg_stream_copy": [_P, _P, _I64, _I32, _I32, _P],
+    "mlcg_mfma_loop": [_I32, _I64, _I32, _P, _P],
+    "mlcg_mfma_loop_flops_per_wave_iter": [_I32],
     "mlcg_copy_batch": [_P, _P, _P, _I32, _P],
     "mlcg_sum_arrays": [_P, _I32, _I64, _P, _P],
     "mlcg_mse_workspace_floats": [_I64],
@@ -132,7 +134,8 @@ _RESTYPES = {"mlcg_version": _c.c_char_p, "mlcg_scan_workspace_ints": _I64,
              "mlcg_out_rev2_workspace_floats": _I64,
              "mlcg_rbf_param_grad_workspace_floats": _I64,
              "mlcg_type_sum_workspace_floats": _I64, "mlcg_node_weight_image_bytes": _I64,
-             "mlcg_mse_workspace_floats": _I64, "mlcg_prior_pair_records_ints": _I64}
+             "mlcg_mse_workspace_floats": _I64, "mlcg_prior_pair_records_ints": _I64,
+             "mlcg_mfma_loop_flops_per_wave_iter": _I64}
 
 STATUS = {
     0: "MLCG_OK",

@@ -1030,8 +1030,9 @@ size_t fwd_x3_lds_bytes(int K) {
 // fragment per k step) stays in registers; the W2^T A fragments of all eight
 // tiles are staged once in LDS.  Per tile:
 //   1. a, a' of feature tile w (v_mfma_f32_16x16x4f32, B operand g, g' from
-//      LDS; for K <= 64 three v_mfma_f32_16x16x16f16 per 16-wide k block of
-//      split operands, W1's two planes in registers);
+//      LDS; for K <= 64 three v_mfma_f32_16x16x32_f16 per 32-wide k block of
+//      split operands, W1's two planes in registers -- the 16x16x16 fp16
+//      shape sustains half the rate of the 16x16x32 one on gfx950);
 //   2. t, t', h, h' of its features, published in LDS;         -- barrier --
 //   3. hb, hb' of its tile (B operands = all 128 t features from LDS);
 //   4. dW2 rows of its tile += t^T h over the 16 pairs (the pair index is the
@@ -1238,8 +1239,10 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
   float* GT0 = kX3 ? HT + 2 * kF * 16 : AT + 2 * kF * 16;  // [2 bufs][2][kRows][16] g, g'
   // split path: GT0 holds the [row][pair] fp16 planes of g, g' (step 6); G1h
   // the pair-major planes (hi, hi S4, lo S4) of g beta_0, g' beta_1 for step
-  // 1, [3][2][16 pairs][64 k], 8-byte chunk c of pair n's row stored at c ^ n
-  // (one buffer: written in step 5 after the barrier that follows step 1)
+  // 1, [3][2][16 pairs][64 k], 16-byte chunk c of pair n's row stored at
+  // c ^ (n & 7) (one buffer: written in step 5 after the barrier that follows
+  // step 1).  With this permutation the step-1 reads (lane (q, n): chunk
+  // 4b + q of pair n) reach distinct banks in both 16-byte lane groups.
   _Float16* G1h = reinterpret_cast<_Float16*>(GT0 + 2 * 2 * kRows * 16);
   float* PMAX = GT0 + 2 * 2 * kRows * 16 + (kX3 ? 3 * 2 * 16 * 64 / 2 : 0);  // x3: [2][2][16] bits
   unsigned* PMAXu = reinterpret_cast<unsigned*>(PMAX);
@@ -1295,16 +1298,16 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
 
   // W1 fragment of feature tile w stays in registers: W1[16w + n][4s + q]
   // (fp32 path) or, on the split path, the two planes (hi, lo S4) of the
-  // v_mfma_f32_16x16x16f16 A fragments W1[16w + n][16b + 4q + j]
+  // v_mfma_f32_16x16x32_f16 A fragments W1[16w + n][32b + 8q + j]
   float w1f[KSMAX];
-  halfx4 w1h[KSMAX / 4], w1l[KSMAX / 4];
+  halfx8 w1h[KSMAX / 8], w1l[KSMAX / 8];
   if constexpr (kX3) {
     bool w1_big = false;
 #pragma unroll
-    for (int b = 0; b < KSMAX / 4; ++b)
+    for (int b = 0; b < KSMAX / 8; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = 16 * b + 4 * q + j;
+      for (int j = 0; j < 8; ++j) {
+        const int k = 32 * b + 8 * q + j;
         const float v = k < K ? W1[(16 * w + n) * K + k] : 0.0f;
         w1_big = w1_big || !(fabsf(v) < kWeightBound);
         const f16split sp = split2(v, kS4);
@@ -1430,8 +1433,9 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
           GTh[kRows * 16 + o] = bv.sh[e][1];
           GTh[2 * kRows * 16 + o] = bv.sl[e][0];
           GTh[3 * kRows * 16 + o] = bv.sl[e][1];
-          // step 1's copy (k = 4s + q: chunk s, element q)
-          const int o1 = n * 64 + 4 * (s ^ n) + q;
+          // step 1's copy (k = 4s + q: 16-byte chunk s / 2, element
+          // 4 (s & 1) + q)
+          const int o1 = n * 64 + 8 * ((s >> 1) ^ (n & 7)) + 4 * (s & 1) + q;
           G1h[o1] = bv.ch[e][0];
           G1h[1024 + o1] = bv.ch[e][1];
           G1h[2048 + o1] = bv.chs[e][0];
@@ -1533,22 +1537,22 @@ __global__ __launch_bounds__(kBwdThreads) void filter_bwd_fused_kernel(
     floatx4 a = {0.f, 0.f, 0.f, 0.f}, ad = {0.f, 0.f, 0.f, 0.f};
     floatx4 a_o = {0.f, 0.f, 0.f, 0.f}, ad_o = {0.f, 0.f, 0.f, 0.f};
     if constexpr (kX3) {
-      // 16-wide k blocks; B fragment = halfx4 of pair n, k = 16b + 4q .. + 3;
-      // slabs (plane, stream) of 256 halfx4: hi (0, 1), hi S (2, 3), lo S (4, 5)
-      const halfx4* g1v = reinterpret_cast<const halfx4*>(G1h);
+      // 32-wide k blocks; B fragment = halfx8 of pair n, k = 32b + 8q .. + 7;
+      // slabs (plane, stream) of 128 halfx8: hi (0, 1), hi S (2, 3), lo S (4, 5)
+      const halfx8* g1v = reinterpret_cast<const halfx8*>(G1h);
 #pragma unroll
-      for (int b = 0; b < KSMAX / 4; ++b) {
-        const int c = n * 16 + ((4 * b + q) ^ n);
-        const halfx4 h0 = g1v[c], s0 = g1v[512 + c], l0 = g1v[1024 + c];
-        const halfx4 h1 = g1v[256 + c], s1 = g1v[768 + c], l1 = g1v[1280 + c];
+      for (int b = 0; b < KSMAX / 8; ++b) {
+        const int c = n * 8 + ((4 * b + q) ^ (n & 7));
+        const halfx8 h0 = g1v[c], s0 = g1v[256 + c], l0 = g1v[512 + c];
+        const halfx8 h1 = g1v[128 + c], s1 = g1v[384 + c], l1 = g1v[640 + c];
         floatx4& A0 = (b & 1) ? a_o : a;
         floatx4& A1 = (b & 1) ? ad_o : ad;
-        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], s0, A0, 0, 0, 0);
-        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], s1, A1, 0, 0, 0);
-        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], l0, A0, 0, 0, 0);
-        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1h[b], l1, A1, 0, 0, 0);
-        A0 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1l[b], h0, A0, 0, 0, 0);
-        A1 = __builtin_amdgcn_mfma_f32_16x16x16f16(w1l[b], h1, A1, 0, 0, 0);
+        A0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1h[b], s0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1h[b], s1, A1, 0, 0, 0);
+        A0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1h[b], l0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1h[b], l1, A1, 0, 0, 0);
+        A0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1l[b], h0, A0, 0, 0, 0);
+        A1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1l[b], h1, A1, 0, 0, 0);
       }
       a = (a + a_o) * (1.0f / (kS4 * kBetaG0));
       ad = (ad + ad_o) * (1.0f / (kS4 * kBetaG1));
