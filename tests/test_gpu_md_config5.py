@@ -146,20 +146,30 @@ def test_config5_composite_steps_vs_oracle(capture):
 def test_config5_full_size_captured_run():
     """The full config-5 system (100 x 268 beads): a captured run stays
     finite, never overflows its radius-graph capacity (the simulation raises
-    otherwise), and its steps after the capture equal those of the eager run."""
-    from mlcg_amd import synthetic
+    otherwise), and its steps after the capture equal those of the eager run.
+    Three of its frames (0, 57, 99: each frame is an independent system) are
+    checked against the chained fp64 oracles as in the 4-frame test:
+    forces and potential energies at every replayed step, and the positions
+    and velocities of each replayed step from the state before it."""
+    from mlcg_amd import ops, synthetic
     from mlcg_amd.simulation import LangevinSimulation
 
     c = synthetic.CONFIG5_PRIORS
     trajs = []
+    states = []
+    schnet = None
     for capture in (False, True):
         print(f"config-5 full size, capture={capture}", flush=True)
-        _, model = _model()
+        schnet, model = _model()
         sim = LangevinSimulation(friction=c["friction_per_ps"], dt=c["dt_ps"], n_timesteps=6,
                                  save_interval=1, random_seed=SEED, capture=capture,
                                  save_energies=True, check_interval=1)
-        sim.attach_model_and_configurations(model, synthetic.config5_configurations(),
-                                            L.beta_of(c["temperature_K"]))
+        confs = synthetic.config5_configurations()
+        sim.attach_model_and_configurations(model, confs, L.beta_of(c["temperature_K"]))
+        if capture:
+            sim._hook = lambda x, v, F, e: states.append(
+                tuple(t.detach().double().cpu().clone() for t in (x, v, F, e)))
+            sim._hook_interval = 1
         x = sim.simulate()
         assert np.isfinite(x).all() and np.isfinite(sim.simulated_potential).all()
         trajs.append((x, sim.simulated_potential))
@@ -168,6 +178,31 @@ def test_config5_full_size_captured_run():
     # the capture happens at step 3; steps 3..6 are replays
     np.testing.assert_allclose(xc[:, 2:], xe[:, 2:], rtol=1e-6, atol=1e-5)
     np.testing.assert_allclose(ec[:, 2:], ee[:, 2:], rtol=1e-5, atol=1e-4)
+
+    assert len(states) == 6
+    beta = L.beta_of(c["temperature_K"])
+    m_all = sim.initial_data.masses.double().cpu()
+    vscale, noisescale = L.constants(c["dt_ps"], c["friction_per_ps"])
+    # the three frames are checked together, as one system of three frames
+    # (the element-wise bound's absolute term scales with that system's
+    # largest force, as in the 4-frame test above)
+    frames = (0, 57, 99)
+    idx = torch.cat([torch.arange(f * N_BEADS, (f + 1) * N_BEADS) for f in frames])
+    types_all = torch.cat([d.atom_types for d in confs])
+    forces = _oracle_force_fn(schnet, len(frames), types_all[idx])
+    m = m_all[idx]
+    bmr = torch.sqrt(1.0 / (beta * m))
+    oracle = {k: forces(states[k][0][idx]) for k in range(1, 6)}
+    for k in range(2, 6):  # steps 3..6: graph replays
+        _, _, F, epot = states[k]
+        check(F[idx], oracle[k][1], 1e-5, f"frames {frames} step {k} forces")
+        check(epot[list(frames)], oracle[k][0], 1e-5, f"frames {frames} step {k} energies")
+        x, v = (t[idx] for t in states[k - 1][:2])
+        xi = ops.philox_normals(SEED, k, m_all.numel(), "cuda").double().cpu()[idx]
+        x1, v1 = L.baoa(x, v, oracle[k - 1][1], m, bmr, c["dt_ps"], vscale, noisescale, xi)
+        v1 = L.b(v1, oracle[k][1], m, c["dt_ps"])
+        check(states[k][0][idx], x1, 1e-6, f"frames {frames} step {k} positions")
+        check(states[k][1][idx], v1, 1e-5, f"frames {frames} step {k} velocities")
 
 
 def test_double_precision_composite_steps_vs_oracle():
