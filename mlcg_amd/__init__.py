@@ -7,7 +7,9 @@ from . import library, ops
 from ._lib import available, version
 
 # torch.ops.mlcg.radius_cuda / exclusion_pair_to_ptr, as the reference's
-# extension registers them
+# extension registers them; and this library's own model operators, through
+# which torch.compile sees the fused energy/force passes
 library.register()
+library.register_model_ops()
 
 __all__ = ["ops", "available", "version"]

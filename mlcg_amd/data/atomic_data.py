@@ -49,7 +49,13 @@ class AtomicData:
 
     # attribute / item access -------------------------------------------------
     def __getattr__(self, name: str) -> Any:
-        store = object.__getattribute__(self, "_store")
+        # called only when the normal lookup fails; `_store` is an instance
+        # attribute, so reading it here does not recurse (except before it
+        # exists, while an instance is being copied or unpickled).  Plain
+        # attribute reads also keep the access traceable by torch.compile.
+        if name == "_store":
+            raise AttributeError(name)
+        store = self._store
         if name in store:
             return store[name]
         raise AttributeError(name)

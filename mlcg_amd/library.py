@@ -10,15 +10,132 @@ count is data-dependent: the fake implementation returns an unbacked size).
 
 If another library already defines the ``mlcg`` operators (the reference's own
 CUDA extension), nothing is registered.
+
+Two operators of this library's own (no counterpart in the reference) make the
+fused model visible to ``torch.compile`` (the reference's simulation compiles
+its model, simulation/base.py:447-489):
+
+  ``mlcg::direct_energy_forces``  energies [B] and forces [N, 3] of one model
+      wrapped by GradientsOut (a SchNet or a prior), found by the id of the
+      module, which GradientsOut registers;
+  ``mlcg::sum_arrays``  SumOut's sum of its models' outputs (mlcg_sum_arrays),
+      with the gradient passed to every input.
+
+Their fake implementations give the output shapes, so a compiled model
+holding them traces without graph breaks (``fullgraph=True``) and
+``mode="reduce-overhead"`` can capture the whole call.
 """
 
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import weakref
+from typing import List, Optional, Tuple
 
 import torch
 
 REGISTERED = False
+MODEL_OPS_REGISTERED = False
+
+# modules reachable from mlcg::direct_energy_forces, by id(module)
+_DIRECT_MODELS: "weakref.WeakValueDictionary[int, torch.nn.Module]" = weakref.WeakValueDictionary()
+
+
+def register_direct_model(module: torch.nn.Module) -> None:
+    """Makes `module` reachable from mlcg::direct_energy_forces as
+    id(module) (GradientsOut registers the model it wraps, also when it is
+    copied or unpickled)."""
+    _DIRECT_MODELS[id(module)] = module
+
+
+class _DirectData:
+    """The fields of a batch that the energy/force passes read: positions,
+    types, frame index and sizes, and the prior's interaction list."""
+
+    def __init__(self, pos, atom_types, batch, n_atoms, name, mapping, mapping_batch):
+        self.pos = pos
+        self.atom_types = atom_types
+        self.batch = batch
+        self.n_atoms = n_atoms
+        nl = {}
+        if mapping is not None:
+            nl["index_mapping"] = mapping
+            if mapping_batch is not None:
+                nl["mapping_batch"] = mapping_batch
+        self.neighbor_list = {name: nl}
+        self.out = {}
+
+    def __contains__(self, key: str) -> bool:
+        return key in ("pos", "atom_types", "batch", "n_atoms", "neighbor_list")
+
+
+def _energy_forces(model: torch.nn.Module, data: _DirectData):
+    """(E, F) of a SchNet or a prior: the fused pass when the model has one,
+    else the model's forward and the position gradient, as GradientsOut
+    computes them."""
+    from .data._keys import ENERGY_KEY
+    from .nn.prior import _Prior
+    from .nn.schnet import SchNet
+
+    if isinstance(model, _Prior) or (isinstance(model, SchNet) and model.fused_spec() is not None):
+        return model.energy_forces(data, create_graph=False)
+    with torch.enable_grad():
+        pos = data.pos.detach().requires_grad_(True)
+        data.pos = pos
+        data = model(data)
+        E = data.out[model.name][ENERGY_KEY]
+        (dE,) = torch.autograd.grad(E.sum(), pos)
+    return E.detach(), -dE
+
+
+def register_model_ops() -> None:
+    """Registers mlcg::direct_energy_forces and mlcg::sum_arrays (once)."""
+    global MODEL_OPS_REGISTERED
+    if MODEL_OPS_REGISTERED:
+        return
+
+    @torch.library.custom_op("mlcg::direct_energy_forces", mutates_args=())
+    def direct_energy_forces_op(pos: torch.Tensor, atom_types: torch.Tensor,
+                                batch: torch.Tensor, n_atoms: torch.Tensor,
+                                mapping: Optional[torch.Tensor],
+                                mapping_batch: Optional[torch.Tensor],
+                                model_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(E [n_frames], F [N, 3]) of the registered model id(model) ==
+        model_id on the batch (pos, atom_types, batch, n_atoms) and, for a
+        prior, its interaction list (mapping, mapping_batch)."""
+        model = _DIRECT_MODELS.get(model_id)
+        if model is None:
+            raise RuntimeError("mlcg::direct_energy_forces: no model registered under this id "
+                               "(GradientsOut registers the model it wraps)")
+        E, F = _energy_forces(model, _DirectData(pos, atom_types, batch, n_atoms, model.name,
+                                                 mapping, mapping_batch))
+        return E.contiguous(), F.contiguous()
+
+    @direct_energy_forces_op.register_fake
+    def _direct_fake(pos, atom_types, batch, n_atoms, mapping, mapping_batch, model_id):
+        if pos.dim() != 2 or pos.shape[1] != 3:
+            raise RuntimeError(f"pos must be [N, 3], got {tuple(pos.shape)}")
+        return pos.new_empty((n_atoms.shape[0],)), pos.new_empty(pos.shape)
+
+    @torch.library.custom_op("mlcg::sum_arrays", mutates_args=())
+    def sum_arrays_op(xs: List[torch.Tensor]) -> torch.Tensor:
+        """((0 + xs[0]) + xs[1]) + ... in one launch (1..8 contiguous float32
+        tensors of one shape on one GPU)."""
+        from . import ops
+
+        return ops.sum_arrays(list(xs))
+
+    @sum_arrays_op.register_fake
+    def _sum_fake(xs):
+        return torch.empty_like(xs[0])
+
+    def _sum_setup(ctx, inputs, output):
+        ctx.n = len(inputs[0])
+
+    def _sum_backward(ctx, g):
+        return [g] * ctx.n
+
+    sum_arrays_op.register_autograd(_sum_backward, setup_context=_sum_setup)
+    MODEL_OPS_REGISTERED = True
 
 
 def _already_defined(name: str) -> bool:

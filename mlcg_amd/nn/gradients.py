@@ -5,6 +5,11 @@ fused pass (``SchNet.energy_forces``) instead of an autograd replay; in
 training mode the result carries the hand-derived force-matching double
 backward.  Around a prior it takes the prior kernel's analytic forces.  Any other model goes through torch.autograd exactly like the
 reference (lines 208-228).
+
+Under torch.compile (outside training, float32 positions, a batch with
+``n_atoms``) the SchNet and prior passes are the custom operator
+``mlcg::direct_energy_forces`` and SumOut's sum ``mlcg::sum_arrays``: their
+fake implementations let dynamo trace the whole model as one graph.
 """
 
 from __future__ import annotations
@@ -13,7 +18,7 @@ from typing import Any, List, Sequence
 
 import torch
 
-from .. import ops
+from .. import library, ops
 from ..data._keys import ENERGY_KEY, FORCE_KEY
 
 
@@ -50,7 +55,10 @@ class SumOut(torch.nn.Module):
             for target in self.targets:
                 parts = [data.out[name][target] for name in self.models.keys()]
                 if ops.sum_arrays_ok(parts):
-                    data.out[target] = _SumArrays.apply(*parts)
+                    if torch.compiler.is_compiling():
+                        data.out[target] = torch.ops.mlcg.sum_arrays(parts)
+                    else:
+                        data.out[target] = _SumArrays.apply(*parts)
                 else:
                     acc = 0.00
                     for p in parts:
@@ -110,6 +118,12 @@ class GradientsOut(torch.nn.Module):
             self.targets = list(targets)
         assert any(k in GradientsOut._targets for k in self.targets), (
             f"targets={self.targets} should be any of {GradientsOut._targets}")
+        library.register_direct_model(model)
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        # a copied or unpickled wrapper holds a new model object
+        library.register_direct_model(self.model)
 
     def _direct_model(self):
         """The wrapped model when it computes energies and forces in one pass
@@ -126,7 +140,33 @@ class GradientsOut(torch.nn.Module):
             return m
         return None
 
+    def _compiled_route(self, data) -> bool:
+        """Whether a traced call goes through mlcg::direct_energy_forces
+        (decided from types and tensor metadata only, which dynamo evaluates
+        while tracing)."""
+        from .prior import _Prior
+        from .schnet import SchNet
+
+        return (FORCE_KEY in self.targets and not self.training
+                and isinstance(self.model, (SchNet, _Prior)) and "n_atoms" in data
+                and "batch" in data and data.pos.dtype == torch.float32
+                and data.pos.is_cuda)
+
     def forward(self, data):
+        if torch.compiler.is_compiling() and self._compiled_route(data):
+            from .prior import _Prior
+
+            mapping = mapping_batch = None
+            if isinstance(self.model, _Prior):
+                nl = data.neighbor_list[self.model.name]
+                mapping = nl["index_mapping"]
+                mapping_batch = nl.get("mapping_batch")
+            energy, forces = torch.ops.mlcg.direct_energy_forces(
+                data.pos.detach(), data.atom_types, data.batch, data.n_atoms, mapping,
+                mapping_batch, id(self.model))
+            data.out[self.name] = {ENERGY_KEY: energy, FORCE_KEY: forces}
+            data.pos = data.pos.detach()
+            return data
         direct = self._direct_model()
         if direct is not None:
             energy, forces = direct.energy_forces(data, create_graph=self.training)

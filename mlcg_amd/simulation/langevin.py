@@ -81,6 +81,15 @@ class LangevinSimulation:
             # the captured step already replays the kernels without the host;
             # torch.compile is for the eager loop
             raise ValueError("compile=True and capture=True are exclusive")
+        if compile and compile_mode in ("reduce-overhead", "max-autotune"):
+            # these modes record the model into CUDA graphs with torch's
+            # cudagraph trees, which reject the device caches the HIP passes
+            # build on first use (weight images, interaction structures)
+            raise ValueError(
+                f"compile_mode={compile_mode!r} records CUDA graphs through torch's cudagraph "
+                "trees, which do not hold this library's device caches: use capture=True (the "
+                "whole step as one HIP graph) or a mode without graphs ('default', "
+                "'max-autotune-no-cudagraphs')")
         if n_timesteps % save_interval != 0:
             raise ValueError("n_timesteps must be a multiple of save_interval")
         self.friction = friction

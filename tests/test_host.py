@@ -333,6 +333,43 @@ def test_reference_operators_registered_with_fake_kernels():
         assert tuple(xs.shape) == (5,) and tuple(ptr.shape) == (8,)
 
 
+def test_model_operators_fake_kernels_and_registry():
+    """mlcg::direct_energy_forces and mlcg::sum_arrays (the fused passes as
+    torch.compile sees them): the fake kernels give energies [n_frames] and
+    forces [N, 3] from the batch's n_atoms, and the sum's shape; GradientsOut
+    registers the model it wraps under id(model), again for a deep copy (which
+    holds a new model object), and an unregistered id is refused."""
+    import copy
+
+    import mlcg_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.fx.experimental.symbolic_shapes import ShapeEnv
+
+    from mlcg_amd import library, nn
+
+    with FakeTensorMode(shape_env=ShapeEnv()):
+        pos = torch.empty(12, 3)
+        types = torch.empty(12, dtype=torch.int64)
+        batch = torch.empty(12, dtype=torch.int64)
+        n_atoms = torch.empty(4, dtype=torch.int64)
+        E, F = torch.ops.mlcg.direct_energy_forces(pos, types, batch, n_atoms, None, None, 1)
+        assert tuple(E.shape) == (4,) and tuple(F.shape) == (12, 3)
+        assert E.dtype == F.dtype == torch.float32
+        S = torch.ops.mlcg.sum_arrays([pos, pos, pos])
+        assert tuple(S.shape) == (12, 3)
+
+    prior = nn.HarmonicBonds({(1, 2): {"x_0": 1.0, "k": 2.0}})
+    g = nn.GradientsOut(prior)
+    assert library._DIRECT_MODELS[id(prior)] is prior
+    g2 = copy.deepcopy(g)
+    assert g2.model is not prior and library._DIRECT_MODELS[id(g2.model)] is g2.model
+    unused = max(library._DIRECT_MODELS.keys()) + 8
+    with pytest.raises(RuntimeError, match="no model registered"):
+        torch.ops.mlcg.direct_energy_forces(torch.zeros(2, 3), torch.zeros(2, dtype=torch.int64),
+                                            torch.zeros(2, dtype=torch.int64),
+                                            torch.ones(1, dtype=torch.int64), None, None, unused)
+
+
 def test_radius_flag_bookkeeping():
     """Every bit of the radius graph's flag word is named, and a look-back
     timeout (bit 8) discards the cached look-back workspaces so that the next
@@ -408,13 +445,16 @@ def test_simulation_compile_model_options(monkeypatch):
     failing = [False]
     with pytest.raises(ValueError):
         LangevinSimulation(device="cpu", compile=True, capture=True)
-    sim = LangevinSimulation(device="cpu", compile=True, compile_mode="max-autotune")
+    for mode in ("reduce-overhead", "max-autotune"):
+        with pytest.raises(ValueError, match="capture=True"):
+            LangevinSimulation(device="cpu", compile=True, compile_mode=mode)
+    sim = LangevinSimulation(device="cpu", compile=True, compile_mode="max-autotune-no-cudagraphs")
     sim.model = Toy()
     with pytest.warns(UserWarning, match="more than one structure"):
         sim.compile_model(Data(1))
     assert calls == []
     sim.compile_model(Data(2))
-    assert calls == [(True, "max-autotune")]
+    assert calls == [(True, "max-autotune-no-cudagraphs")]
     sim = LangevinSimulation(device="cpu", compile=True, force_compile=True)
     sim.model = Toy()
     calls.clear()
