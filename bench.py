@@ -908,7 +908,8 @@ def cpu_leg(args):
 
 
 def cpu_configs_leg():
-    """CPU baselines of configs 1, 3, 4 and 5: the
+    """CPU baselines of configs 1, 3, 4 and 5 (the reference's own CPU-runnable
+    case, the radius-graph, fp16 and MD configurations): the
     oracle restatements in fp32 on the host cores, 2 warm-ups then the median
     of 5 (configs 1, 3, 4), and 20 steps reported per step (config 5).
     Configs 4 and 5 run on bounded samples (stated in each record)."""
