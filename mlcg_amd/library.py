@@ -68,6 +68,11 @@ class _DirectData:
         return key in ("pos", "atom_types", "batch", "n_atoms", "neighbor_list")
 
 
+_AUTOGRAD_KEYS = tuple(getattr(torch._C.DispatchKey, k) for k in (
+    "AutogradFunctionality", "AutogradOther", "AutogradCPU", "AutogradCUDA",
+    "AutogradNestedTensor") if hasattr(torch._C.DispatchKey, k))
+
+
 def _energy_forces(model: torch.nn.Module, data: _DirectData):
     """(E, F) of a SchNet or a prior: the fused pass when the model has one,
     else the model's forward and the position gradient, as GradientsOut
@@ -78,7 +83,14 @@ def _energy_forces(model: torch.nn.Module, data: _DirectData):
 
     if isinstance(model, _Prior) or (isinstance(model, SchNet) and model.fused_spec() is not None):
         return model.energy_forces(data, create_graph=False)
-    with torch.enable_grad():
+    # an operator's implementation runs with the autograd dispatch keys
+    # excluded; the module path takes its position gradient from autograd, so
+    # they are allowed again for this computation
+    exclude = torch._C._dispatch_tls_local_exclude_set()
+    for key in _AUTOGRAD_KEYS:
+        exclude = exclude.remove(key)
+    with torch._C._ForceDispatchKeyGuard(torch._C._dispatch_tls_local_include_set(), exclude), \
+            torch.enable_grad():
         pos = data.pos.detach().requires_grad_(True)
         data.pos = pos
         data = model(data)

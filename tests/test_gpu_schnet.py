@@ -502,3 +502,25 @@ def test_mean_aggregation_vs_oracle():
     for k, gr in g_ref.items():
         assert grads[k] is not None, k
         check(grads[k], gr, 1e-4, k)
+
+
+def test_compiled_module_path_schnet():
+    """A SchNet without a fused pass (mean aggregation) inside torch.compile
+    (fullgraph=True): mlcg::direct_energy_forces runs it module by module with
+    the position gradient taken inside the operator, as GradientsOut does
+    eagerly, so the compiled energies and forces equal the eager ones."""
+    import torch._dynamo
+
+    from mlcg_amd import nn
+
+    cfg = make_cfg(num_blocks=2, rc=12.0, act="ssp", aggr="mean")
+    sd = R.random_state_dict(cfg, seed=17)
+    b = _small_batch()
+    gm = nn.GradientsOut(make_model(cfg, sd)).eval()
+    ref = gm(b.to_torch("cuda"))
+    torch._dynamo.reset()
+    out = torch.compile(gm, fullgraph=True, dynamic=True)(b.to_torch("cuda"))
+    for key in ("energy", "forces"):
+        got, want = out.out["SchNet"][key], ref.out["SchNet"][key]
+        assert got.shape == want.shape
+        assert torch.allclose(got, want, rtol=1e-6, atol=1e-6), key
