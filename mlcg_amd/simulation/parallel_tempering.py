@@ -8,15 +8,13 @@ simulation slot r * n_indep + i holds configuration i at betas[r].  Every
 temperatures, alternating the pairs (0,1), (2,3), ... and (1,2), (3,4), ...,
 accepts a pair with the Metropolis probability
 min(1, exp((U_a - U_b)(beta_a - beta_b))), and swaps the two slots'
-configurations, rescaling the velocities by sqrt(beta_old / beta_new)
-(parallel_tempering.py:360-520), as the reference's docstring states it
-(parallel_tempering.py:433-435): a configuration moving from beta_old to
-beta_new keeps its kinetic temperature consistent with the new slot.  (The
-reference's code multiplies by sqrt(beta_new / beta_old) instead, lines
-484-497, which heats configurations moving to a colder slot; this module
-follows the docstring and equipartition, and warns once when the choice is
-left to the default; ``reference_velocity_scaling=True`` applies the reference
-code's factor instead, for reproducing a reference run's ensemble.)  The forces travel with the configurations
+configurations, rescaling the velocities by sqrt(beta_new / beta_old) as
+the reference's code does (parallel_tempering.py:360-520, the factor at
+484-497), so that a run reproduces a reference run.  The reference's
+docstring (433-435) states the inverse, sqrt(beta_old / beta_new), which
+keeps a moved configuration's kinetic temperature consistent with its new
+slot (equipartition); ``reference_velocity_scaling=False`` applies that
+factor instead.  The forces travel with the configurations
 (a force depends on the configuration only), so the next half-kick uses the
 force of the configuration it moves.  `acceptance_matrix[a, b]` counts the
 accepted (a < b) and rejected (a > b) exchanges between temperatures a and b.
@@ -26,8 +24,7 @@ The exchange runs on the host between steps, so it also works with
 
 from __future__ import annotations
 
-import warnings
-from typing import List, Optional, Tuple
+from typing import List, Tuple
 
 import numpy as np
 import torch
@@ -35,33 +32,17 @@ import torch
 from .langevin import LangevinSimulation
 
 
-_WARNED_SCALING = False
-
-
 class PTSimulation(LangevinSimulation):
     def __init__(self, exchange_interval: int = 100,
-                 reference_velocity_scaling: Optional[bool] = None, **kwargs):
+                 reference_velocity_scaling: bool = True, **kwargs):
         super().__init__(**kwargs)
         if exchange_interval < 1:
             raise ValueError("exchange_interval must be positive")
         self.exchange_interval = int(exchange_interval)
-        # False: a configuration moving from beta_old to beta_new has its
-        # velocities scaled by sqrt(beta_old / beta_new) (the reference's
-        # docstring, parallel_tempering.py:433-435); True: by
-        # sqrt(beta_new / beta_old), as the reference's code does (484-497).
-        # Left unset, the docstring's factor is used and a warning says once
-        # per process that it differs from the reference code's.
-        if reference_velocity_scaling is None:
-            global _WARNED_SCALING
-            if not _WARNED_SCALING:
-                _WARNED_SCALING = True
-                warnings.warn(
-                    "PTSimulation rescales exchanged velocities by sqrt(beta_old / beta_new) "
-                    "(equipartition, as the reference's docstring states); the reference code "
-                    "applies sqrt(beta_new / beta_old). Pass reference_velocity_scaling=True to "
-                    "reproduce a reference run, or False to silence this warning.",
-                    stacklevel=2)
-            reference_velocity_scaling = False
+        # True (the default): a configuration moving from beta_old to beta_new
+        # has its velocities scaled by sqrt(beta_new / beta_old), as the
+        # reference's code does (484-497); False: by sqrt(beta_old / beta_new),
+        # the factor the reference's docstring states (433-435)
         self.reference_velocity_scaling = bool(reference_velocity_scaling)
         self._hook = self.detect_and_exchange_replicas
         self._hook_interval = self.exchange_interval
@@ -116,9 +97,9 @@ class PTSimulation(LangevinSimulation):
 
     def _perform_exchange(self, x, v, F, potential, pair_a, pair_b) -> None:
         """Swaps the configurations of the approved slot pairs in place,
-        velocities rescaled by sqrt(beta_old / beta_new), or by the reference
-        code's sqrt(beta_new / beta_old) with reference_velocity_scaling
-        (parallel_tempering.py:442-520)."""
+        velocities rescaled by the reference code's sqrt(beta_new / beta_old)
+        (parallel_tempering.py:442-520), or by sqrt(beta_old / beta_new) with
+        reference_velocity_scaling=False."""
         if len(pair_a) == 0:
             return
         dev = x.device
@@ -127,8 +108,8 @@ class PTSimulation(LangevinSimulation):
         s = self.n_sims
         x3, v3, f3 = (t.view(s, self.n_atoms, 3) for t in (x, v, F))
         beta = self.beta.to(dev)
-        # b's configuration moves into slot a: v sqrt(beta_b / beta_a), and back
-        # (the reference code's inverse factor when asked for)
+        # b's configuration moves into slot a: v sqrt(beta_a / beta_b) (the
+        # reference code's factor), or v sqrt(beta_b / beta_a) when asked for
         ratio = beta[a] / beta[b] if self.reference_velocity_scaling else beta[b] / beta[a]
         scale_ba = torch.sqrt(ratio).view(-1, 1, 1).to(v.dtype)
         xa, va, fa, ua = x3[a].clone(), v3[a].clone(), f3[a].clone(), potential[a].clone()

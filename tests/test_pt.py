@@ -65,9 +65,10 @@ def test_metropolis_rule_and_velocity_rescaling():
     u = torch.tensor([5.0, 1.0])
     sim.detect_and_exchange_replicas(x, v, f, u)
     assert sim.acceptance_matrix[0, 1] == 1
-    # the hot configuration entering the cold slot slows by sqrt(1/2)
-    torch.testing.assert_close(v.view(2, 3, 3)[0], v0.view(2, 3, 3)[1] * math.sqrt(0.5))
-    torch.testing.assert_close(v.view(2, 3, 3)[1], v0.view(2, 3, 3)[0] * math.sqrt(2.0))
+    # the reference code's factor (the default): the hot configuration
+    # entering the cold slot is scaled by sqrt(beta_cold / beta_hot) = sqrt(2)
+    torch.testing.assert_close(v.view(2, 3, 3)[0], v0.view(2, 3, 3)[1] * math.sqrt(2.0))
+    torch.testing.assert_close(v.view(2, 3, 3)[1], v0.view(2, 3, 3)[0] * math.sqrt(0.5))
     # a huge penalty: never accepted
     u = torch.tensor([0.0, 1e4])
     before = x.clone()
@@ -79,10 +80,10 @@ def test_metropolis_rule_and_velocity_rescaling():
 
 def test_reference_velocity_scaling_option():
     """reference_velocity_scaling=True applies the factor of the reference's
-    code (parallel_tempering.py:484-497): the configuration entering slot a
-    from slot b is scaled by sqrt(beta_a / beta_b); the default follows the
-    reference's docstring, sqrt(beta_b / beta_a).  Positions and forces move
-    the same way in both."""
+    code (parallel_tempering.py:484-497, the default): the configuration
+    entering slot a from slot b is scaled by sqrt(beta_a / beta_b); False
+    follows the reference's docstring, sqrt(beta_b / beta_a).  Positions and
+    forces move the same way in both."""
     for ref_scaling, factor_into_cold in ((False, math.sqrt(0.5)), (True, math.sqrt(2.0))):
         sim = _sim([2.0, 1.0], n_indep=1)
         sim.reference_velocity_scaling = ref_scaling
@@ -133,8 +134,10 @@ def test_pt_run_on_the_gpu():
             c.neighbor_list.pop(k)
     model = nn.SumOut(torch.nn.ModuleDict({"bonds": nn.GradientsOut(nn.HarmonicBonds(bonds))}))
     betas = [L.beta_of(300.0), L.beta_of(350.0), L.beta_of(400.0)]
+    # the docstring's factor, which keeps equipartition across exchanges
     sim = PTSimulation(exchange_interval=50, friction=10.0, dt=0.004, n_timesteps=3000,
-                       save_interval=1000, random_seed=4, capture=True)
+                       save_interval=1000, random_seed=4, capture=True,
+                       reference_velocity_scaling=False)
     sim.attach_model_and_configurations(model, confs, betas)
     out = sim.simulate()
     assert np.isfinite(out).all()
@@ -147,21 +150,16 @@ def test_pt_run_on_the_gpu():
         assert ke == pytest.approx(0.5 / b, rel=0.1), r
 
 
-def test_default_velocity_scaling_warns_once():
-    """Left unset, the velocity factor is the docstring's (not the reference
-    code's) and a warning says so once per process; an explicit choice is
-    silent."""
+def test_default_velocity_scaling_is_the_reference_codes():
+    """Left unset, the velocity factor is the reference code's
+    sqrt(beta_new / beta_old) (parallel_tempering.py:484-497), with no warning;
+    reference_velocity_scaling=False selects the docstring's factor."""
     import warnings
 
-    from mlcg_amd.simulation import parallel_tempering as ptm
-
-    ptm._WARNED_SCALING = False
     with warnings.catch_warnings(record=True) as rec:
         warnings.simplefilter("always")
         a = PTSimulation(exchange_interval=5, n_timesteps=10, save_interval=10, device="cpu")
-        PTSimulation(exchange_interval=5, n_timesteps=10, save_interval=10, device="cpu")
-        PTSimulation(exchange_interval=5, reference_velocity_scaling=False, n_timesteps=10,
-                     save_interval=10, device="cpu")
-    msgs = [str(w.message) for w in rec if "reference_velocity_scaling" in str(w.message)]
-    assert len(msgs) == 1, msgs
-    assert a.reference_velocity_scaling is False
+        b = PTSimulation(exchange_interval=5, reference_velocity_scaling=False, n_timesteps=10,
+                         save_interval=10, device="cpu")
+    assert not [w for w in rec if "velocity" in str(w.message)]
+    assert a.reference_velocity_scaling is True and b.reference_velocity_scaling is False
