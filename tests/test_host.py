@@ -370,6 +370,18 @@ def test_model_operators_fake_kernels_and_registry():
                                             torch.ones(1, dtype=torch.int64), None, None, unused)
 
 
+def test_mfma_probe_flop_counts():
+    """The MFMA-loop probe's FLOP count per wave iteration (host-side, no
+    GPU): 8 chains of 2·M·N·K for each shape, -1 for an unknown kind."""
+    from mlcg_amd import _lib
+
+    lib = _lib.load()
+    shapes = {0: (16, 16, 32), 1: (16, 16, 16), 2: (16, 16, 4), 3: (16, 16, 32), 4: (32, 32, 16)}
+    for kind, (m, n, k) in shapes.items():
+        assert lib.mlcg_mfma_loop_flops_per_wave_iter(kind) == 8 * 2 * m * n * k
+    assert lib.mlcg_mfma_loop_flops_per_wave_iter(5) == -1
+
+
 def test_radius_flag_bookkeeping():
     """Every bit of the radius graph's flag word is named, and a look-back
     timeout (bit 8) discards the cached look-back workspaces so that the next
