@@ -346,6 +346,8 @@ int mlcg_cfconv_gather(const float* src, const void* W, int w_f16,
  * pair p = {i < j}, dbar[p] += <Wd_p, gagg[i] * y[j] + gagg[j] * y[i]>
  * (accumulate != 0) or dbar[p] = ... (accumulate == 0: dbar need not be
  * initialised; pairs past the graph's live count are left untouched).
+ * ybar == NULL: dbar only (no filter row W is read; the same dbar values
+ * bit for bit), for a block whose input does not depend on the positions.
  * Replaces the autograd backward of schnet.py:340-346. */
 int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const void* W,
                            const void* Wd, int w_f16, const int32_t* rowptr,

@@ -180,7 +180,25 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
 // dbar).  The steps of
 // upper edges keep kUp steps (four loads per edge) in flight: its registers
 // set the kernel's occupancy, lower-edge steps included.
-template <int kUp>
+// <Wd, gi yj + gj yi> of one lane's four features, in a fixed fma order
+// (the backend would otherwise contract the products differently in each
+// instantiation of the kernel, and the two gather_bwd forms must agree).
+__device__ __forceinline__ float dbar_term(float4 wd, float4 gi, float4 yj, float4 gj,
+                                           float4 yi) {
+  const float tx = __builtin_fmaf(gi.x, yj.x, __fmul_rn(gj.x, yi.x));
+  const float ty = __builtin_fmaf(gi.y, yj.y, __fmul_rn(gj.y, yi.y));
+  const float tz = __builtin_fmaf(gi.z, yj.z, __fmul_rn(gj.z, yi.z));
+  const float tw = __builtin_fmaf(gi.w, yj.w, __fmul_rn(gj.w, yi.w));
+  return __builtin_fmaf(wd.w, tw, __builtin_fmaf(wd.z, tz,
+                                                 __builtin_fmaf(wd.y, ty, __fmul_rn(wd.x, tx))));
+}
+
+// kYbar = false: dbar only (no ybar): the lower edges, which add to ybar
+// alone, are skipped, and the upper edges load no filter rows W; their dbar
+// terms are formed by the same code, so they equal the full kernel's bit for
+// bit.  (A model's first block needs no ybar on the force sweep: its input
+// is the embedding, which does not depend on the positions.)
+template <int kUp, bool kYbar>
 __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     const float* __restrict__ gagg, const float* __restrict__ y, const void* __restrict__ W,
     const void* __restrict__ Wd, int w_f16, const int32_t* __restrict__ rowptr,
@@ -198,20 +216,24 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
   // steps before the first step that holds an upper edge: gather only
   const int lo_steps_end = split & ~1;
   int k = 0;
-  for (; k + 2 * kSteps <= lo_steps_end; k += 2 * kSteps) {
-    float4 g[kSteps], w[kSteps];
+  if constexpr (kYbar) {
+    for (; k + 2 * kSteps <= lo_steps_end; k += 2 * kSteps) {
+      float4 g[kSteps], w[kSteps];
 #pragma unroll
-    for (int u = 0; u < kSteps; ++u) {
-      const Edge e = edge_at(k + 2 * u, h, cn, my_col, my_pair, 0.f);
-      g[u] = ld4(gagg, e.j, m);
-      w[u] = ldw4(W, f16, e.p, m);
+      for (int u = 0; u < kSteps; ++u) {
+        const Edge e = edge_at(k + 2 * u, h, cn, my_col, my_pair, 0.f);
+        g[u] = ld4(gagg, e.j, m);
+        w[u] = ldw4(W, f16, e.p, m);
+      }
+#pragma unroll
+      for (int u = 0; u < kSteps; ++u) fma4(acc, g[u], w[u]);
     }
-#pragma unroll
-    for (int u = 0; u < kSteps; ++u) fma4(acc, g[u], w[u]);
-  }
-  for (; k < lo_steps_end; k += 2) {
-    const Edge e = edge_at(k, h, cn, my_col, my_pair, 0.f);
-    fma4(acc, ld4(gagg, e.j, m), ldw4(W, f16, e.p, m));
+    for (; k < lo_steps_end; k += 2) {
+      const Edge e = edge_at(k, h, cn, my_col, my_pair, 0.f);
+      fma4(acc, ld4(gagg, e.j, m), ldw4(W, f16, e.p, m));
+    }
+  } else {
+    k = lo_steps_end;
   }
   // remaining steps: gather, plus the distance adjoint on upper edges
   for (; k < cn; k += 2 * kUp) {
@@ -225,18 +247,16 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
       ok[u] = k + 2 * u < cn && ke < cn;
       up[u] = ok[u] && ke >= split;
       p[u] = e.p;
-      g[u] = ok[u] ? ld4(gagg, e.j, m) : f4zero();
-      w[u] = ok[u] ? ldw4(W, f16, e.p, m) : f4zero();
+      g[u] = (kYbar ? ok[u] : up[u]) ? ld4(gagg, e.j, m) : f4zero();
+      w[u] = kYbar && ok[u] ? ldw4(W, f16, e.p, m) : f4zero();
       yj[u] = up[u] ? ld4(y, e.j, m) : f4zero();
       wd[u] = up[u] ? ldw4(Wd, f16, e.p, m) : f4zero();
     }
     float part[kUp];
 #pragma unroll
     for (int u = 0; u < kUp; ++u) {
-      fma4(acc, g[u], w[u]);
-      const float4 t{gi.x * yj[u].x + g[u].x * yi.x, gi.y * yj[u].y + g[u].y * yi.y,
-                     gi.z * yj[u].z + g[u].z * yi.z, gi.w * yj[u].w + g[u].w * yi.w};
-      part[u] = dot4(wd[u], t);
+      if constexpr (kYbar) fma4(acc, g[u], w[u]);
+      part[u] = dbar_term(wd[u], gi, yj[u], g[u], yi);
     }
 #pragma unroll
     for (int u = 0; u < kUp; ++u) part[u] = half_sum(part[u]);
@@ -257,8 +277,10 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     }
   }
   MLCG_ROW_LOOP_END
-  acc = combine_halves(acc, h);
-  if (h == 0) st4(ybar, i, m, acc);
+  if constexpr (kYbar) {
+    acc = combine_halves(acc, h);
+    if (h == 0) st4(ybar, i, m, acc);
+  }
 }
 
 // out[i] = sum_j ydot[j] W_ij + y[j] Wd_ij ddot_p (ydot may be null).
@@ -600,19 +622,28 @@ extern "C" int mlcg_cfconv_gather_bwd(const float* gagg, const float* y, const v
   if (num_filters != kF) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(n_nodes >= 0);
   if (n_nodes == 0) return MLCG_OK;
-  MLCG_REQUIRE(gagg && y && W && Wd && rowptr && col && eid2pair && ybar && dbar);
+  MLCG_REQUIRE(gagg && y && W && Wd && rowptr && col && eid2pair && dbar);
   // upper steps in flight: 4 with fp32 filter rows (104 VGPRs, 4 waves per
   // SIMD; config 2, 24 edges a row: 48 us against 54 with 2), 2 with fp16
   // rows (68 VGPRs, 7 waves per SIMD; config 4, 47 edges a row: 0.61 ms
-  // against 0.89 with 4)
-  if (w_f16)
-    hipLaunchKernelGGL(gather_bwd_kernel<2>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
-                       mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
-                       n_nodes, ybar, dbar, accumulate);
-  else
-    hipLaunchKernelGGL(gather_bwd_kernel<kSteps>, dim3(row_groups(n_nodes)), dim3(kThreads), 0,
-                       mlcg_stream(stream), gagg, y, W, Wd, w_f16, rowptr, col, eid2pair,
-                       n_nodes, ybar, dbar, accumulate);
+  // against 0.89 with 4); ybar == NULL: dbar only
+  const dim3 grid(row_groups(n_nodes)), block(kThreads);
+  const auto s = mlcg_stream(stream);
+  if (w_f16) {
+    if (ybar)
+      hipLaunchKernelGGL((gather_bwd_kernel<2, true>), grid, block, 0, s, gagg, y, W, Wd, w_f16,
+                         rowptr, col, eid2pair, n_nodes, ybar, dbar, accumulate);
+    else
+      hipLaunchKernelGGL((gather_bwd_kernel<2, false>), grid, block, 0, s, gagg, y, W, Wd, w_f16,
+                         rowptr, col, eid2pair, n_nodes, ybar, dbar, accumulate);
+  } else {
+    if (ybar)
+      hipLaunchKernelGGL((gather_bwd_kernel<kSteps, true>), grid, block, 0, s, gagg, y, W, Wd,
+                         w_f16, rowptr, col, eid2pair, n_nodes, ybar, dbar, accumulate);
+    else
+      hipLaunchKernelGGL((gather_bwd_kernel<kSteps, false>), grid, block, 0, s, gagg, y, W, Wd,
+                         w_f16, rowptr, col, eid2pair, n_nodes, ybar, dbar, accumulate);
+  }
   return mlcg_launch_status();
 }
 

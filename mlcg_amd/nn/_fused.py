@@ -415,15 +415,20 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
         sbar, zbar, gagg = _lin_dact_lin(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True,
                                          bp.A2, imgs=(_wi(st, k, "A3", True),
                                                       _wi(st, k, "A2", True)))
+        # the first block's input is the embedding, which does not depend on
+        # the positions: its ybar (and the adjoint of its input) enter neither
+        # the forces nor the second sweep (whose first block has no input
+        # tangent), so only its distance adjoints are formed
         ybar = ops.cfconv_gather_bwd(gagg, st.y[k], st.W[k], st.Wd[k], graph, dbar,
-                                     accumulate=(k != nb - 1))
+                                     accumulate=(k != nb - 1), want_ybar=(k != 0))
         st.xbar_out[k] = xbar
         st.sbar1[k] = sbar
         st.zbar1[k] = zbar
         st.gagg1[k] = gagg
         st.ybar1[k] = ybar
-        xbar = ops.node_linear(ybar, bp.A1, transpose=True, residual=xbar,
-                               w_image=_wi(st, k, "A1", True))
+        if k != 0:
+            xbar = ops.node_linear(ybar, bp.A1, transpose=True, residual=xbar,
+                                   w_image=_wi(st, k, "A1", True))
     if not need_forces:
         return None
     return ops.pair_forces(st.pos, st.dist, dbar, graph)

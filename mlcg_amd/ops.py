@@ -1059,12 +1059,13 @@ def cfconv_gather(src: torch.Tensor, W: torch.Tensor, graph: PairGraph) -> torch
 
 
 def cfconv_gather_bwd(gagg: torch.Tensor, y: torch.Tensor, W: torch.Tensor, Wd: torch.Tensor,
-                      graph: PairGraph, dbar: torch.Tensor, accumulate: bool = True
-                      ) -> torch.Tensor:
+                      graph: PairGraph, dbar: torch.Tensor, accumulate: bool = True,
+                      want_ybar: bool = True) -> Optional[torch.Tensor]:
     """ybar = gather(gagg, W); dbar[p] += <Wd_p, gagg_i y_j + gagg_j y_i> in
-    place (dbar[p] = ... with accumulate=False: dbar may be uninitialised)."""
+    place (dbar[p] = ... with accumulate=False: dbar may be uninitialised).
+    want_ybar=False: dbar only (the same values), returns None."""
     gagg = gagg.contiguous()
-    ybar = torch.empty_like(gagg)
+    ybar = torch.empty_like(gagg) if want_ybar else None
     wp, wf16 = _wptr(W)
     call("mlcg_cfconv_gather_bwd", ptr(gagg), ptr(y.contiguous()), wp, ptr(Wd), wf16,
          ptr(graph.rowptr), ptr(graph.col), ptr(graph.eid2pair), graph.num_nodes,

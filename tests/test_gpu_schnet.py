@@ -527,3 +527,31 @@ def test_compiled_module_path_schnet():
         got, want = out.out["SchNet"][key], ref.out["SchNet"][key]
         assert got.shape == want.shape
         assert torch.allclose(got, want, rtol=1e-6, atol=1e-6), key
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["fp32_rows", "fp16_rows"])
+def test_gather_bwd_dbar_only_bit_identical(f16):
+    """mlcg_cfconv_gather_bwd without ybar (the first block of the force
+    sweep, whose input does not depend on the positions) gives the full
+    kernel's distance adjoints bit for bit, stored and accumulated."""
+    from mlcg_amd import ops
+
+    cfg, sd, b, pos, g, spec, bp = _filter_setup(n_frames=8)
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    N, P = pos.shape[0], g.pair_capacity
+    gagg = torch.randn(N, 128, generator=gen).cuda()
+    y = torch.randn(N, 128, generator=gen).cuda()
+    W = torch.randn(P, 128, generator=gen).cuda()
+    Wd = torch.randn(P, 128, generator=gen).cuda()
+    if f16:
+        W, Wd = W.half(), Wd.half()
+    base = torch.randn(P, generator=gen).cuda()
+    for accumulate in (False, True):
+        d_full, d_only = base.clone(), base.clone()
+        ybar = ops.cfconv_gather_bwd(gagg, y, W, Wd, g, d_full, accumulate=accumulate)
+        none = ops.cfconv_gather_bwd(gagg, y, W, Wd, g, d_only, accumulate=accumulate,
+                                     want_ybar=False)
+        torch.cuda.synchronize()
+        assert none is None and ybar is not None
+        n = int(g.num_pairs) if hasattr(g, "num_pairs") else P
+        assert torch.equal(d_only[:n], d_full[:n]), accumulate
