@@ -437,7 +437,7 @@ __device__ __forceinline__ float4 gemm_epilogue(float4 y, int64_t r, int col, co
     if (MODE == MLCG_NODE_DACT) {
       if (out0) st4(out0 + o, y);
       const float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
-      st4(out1 + o, v);
+      if (out1) st4(out1 + o, v);  // node_gemm2 may keep v to itself
       return v;
     } else {  // MLCG_NODE_DACT2
       float4 v{y.x * d1.x, y.y * d1.y, y.z * d1.z, y.w * d1.w};
@@ -994,7 +994,7 @@ void launch_node_gemm2(bool xw, hipStream_t s, const float* x, int64_t rows,
 // Argument checks shared by mlcg_node_gemm and mlcg_node_gemm2.
 int check_node_gemm(const float* x, int64_t rows, const float* W, int epilogue, int act,
                     const float* z, const float* s, const float* e, const float* f,
-                    const float* out0, const float* out1) {
+                    const float* out0, const float* out1, bool out1_optional = false) {
   MLCG_REQUIRE(rows >= 0 && (act == MLCG_ACT_TANH || act == MLCG_ACT_SSP));
   MLCG_REQUIRE((e == nullptr) == (f == nullptr));
   MLCG_REQUIRE(epilogue >= MLCG_NODE_PLAIN && epilogue <= MLCG_NODE_DACT2);
@@ -1002,7 +1002,9 @@ int check_node_gemm(const float* x, int64_t rows, const float* W, int epilogue, 
   switch (epilogue) {
     case MLCG_NODE_PLAIN: MLCG_REQUIRE(out0 != nullptr); break;
     case MLCG_NODE_ACT: MLCG_REQUIRE(out1 != nullptr); break;
-    case MLCG_NODE_DACT: MLCG_REQUIRE(out1 && s && (z || act == MLCG_ACT_TANH)); break;
+    case MLCG_NODE_DACT:
+      MLCG_REQUIRE((out1 || out1_optional) && s && (z || act == MLCG_ACT_TANH));
+      break;
     case MLCG_NODE_DACT2: MLCG_REQUIRE(out0 && s && (z || act == MLCG_ACT_TANH)); break;
     default: break;
   }
@@ -1054,7 +1056,9 @@ extern "C" int mlcg_node_gemm2(const float* x, int64_t rows, int features, const
                                void* stream) {
   if (features != kF) return MLCG_ERR_UNSUPPORTED;
   MLCG_REQUIRE(epilogue != MLCG_NODE_PLAIN);
-  const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1);
+  // the DACT form's v (out1) feeds the second product from registers, so a
+  // caller that needs only out2 may pass out1 = NULL
+  const int rc = check_node_gemm(x, rows, W, epilogue, act, z, s, e, f, out0, out1, true);
   if (rc != MLCG_OK || rows == 0) return rc;
   MLCG_REQUIRE(W2 && out2);
   MLCG_REQUIRE(reinterpret_cast<uintptr_t>(w_image) % 16 == 0 &&

@@ -220,12 +220,14 @@ def _lin_act_lin(x, A, c, act, want_z, B, cb, residual, imgs=(None, None)):
     return z, s, ops.node_linear(s, B, bias=cb, residual=residual)
 
 
-def _lin_dact_lin(x, A, z, s, act, transpose, B, residual=None, imgs=(None, None)):
-    """(y, v, v B^T [+ residual]) (v B with transpose), (y, v) = _lin_dact(...)."""
+def _lin_dact_lin(x, A, z, s, act, transpose, B, residual=None, imgs=(None, None),
+                  keep: bool = True):
+    """(y, v, v B^T [+ residual]) (v B with transpose), (y, v) = _lin_dact(...);
+    keep=False: y and v may be None (not written) when the fused kernel runs."""
     if _gemm2_ok(x, A, B):
         return ops.node_gemm2(x, A, B, transpose=transpose, epilogue=ops.NODE_DACT, act=act,
                               z=z, s=s, residual2=residual, w_image=imgs[0],
-                              w2_image=imgs[1])
+                              w2_image=imgs[1], want_out0=keep, want_out1=keep)
     y, v = _lin_dact(x, A, z, s, act, transpose)
     return y, v, ops.node_linear(v, B, transpose=transpose, residual=residual)
 
@@ -381,7 +383,7 @@ def forward(spec: FusedSpec, P: Params, pos: torch.Tensor, types: torch.Tensor,
 
 
 def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
-             need_forces: bool = True) -> Optional[torch.Tensor]:
+             need_forces: bool = True, keep_adjoints: bool = True) -> Optional[torch.Tensor]:
     """First-order reverse seeded with d(objective)/d o_n = seed[n]; returns
     the forces -d/dpos (sum_n seed_n o_n) and saves the adjoints."""
     graph = st.graph
@@ -412,9 +414,12 @@ def reverse1(spec: FusedSpec, P: Params, st: State, seed: torch.Tensor,
     st.ybar1 = [None] * nb
     for k in range(nb - 1, -1, -1):
         bp = P.blocks[k]
+        # sbar, zbar feed only the second sweep: without keep_adjoints (energies
+        # and forces alone) the fused kernel does not write them
         sbar, zbar, gagg = _lin_dact_lin(xbar, bp.A3, st.z[k], st.s[k], spec.block_act, True,
                                          bp.A2, imgs=(_wi(st, k, "A3", True),
-                                                      _wi(st, k, "A2", True)))
+                                                      _wi(st, k, "A2", True)),
+                                         keep=keep_adjoints)
         # the first block's input is the embedding, which does not depend on
         # the positions: its ybar (and the adjoint of its input) enter neither
         # the forces nor the second sweep (whose first block has no input
@@ -700,7 +705,7 @@ class EnergyForces(torch.autograd.Function):
         P = Params.unflat(spec, list(flat))
         ones = _ones(pos.shape[0], pos.device)
         E, st = forward(spec, P, pos, types, graph, save=True, rev_seed=ones)
-        F = reverse1(spec, P, st, ones)
+        F = reverse1(spec, P, st, ones, keep_adjoints=bool(training))
         if training:
             ctx.spec, ctx.P, ctx.st, ctx.batch = spec, P, st, batch
         ctx.set_materialize_grads(False)

@@ -499,12 +499,14 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
                f: Optional[torch.Tensor] = None, want_out0: bool = True,
                bias2: Optional[torch.Tensor] = None, residual2: Optional[torch.Tensor] = None,
                w_image: Optional[torch.Tensor] = None, w2_image: Optional[torch.Tensor] = None,
+               want_out1: bool = True,
                ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor], torch.Tensor]:
     """(out0, out1, out2): node_gemm(x, W, ...) with an ACT, DACT or DACT2
     epilogue followed, in the same kernel (mlcg_node_gemm2), by
     out2 = v W2^T (v W2 with transpose) [+ bias2] [+ residual2], v being out1
     (ACT, DACT) or out0 (DACT2).  Bit-identical to the two node_gemm calls.
-    w_image, w2_image: split images of W and W2 as in node_gemm."""
+    w_image, w2_image: split images of W and W2 as in node_gemm.  With the
+    DACT epilogue, want_out1=False leaves v (out1) unwritten (None)."""
     require_device(x)
     _check(epilogue in (NODE_ACT, NODE_DACT, NODE_DACT2),
            "node_gemm2 takes an ACT, DACT or DACT2 first epilogue")
@@ -525,7 +527,7 @@ def node_gemm2(x: torch.Tensor, W: torch.Tensor, W2: torch.Tensor, transpose: bo
     out0 = out1 = None
     if epilogue == NODE_DACT2 or want_out0:
         out0 = torch.empty_like(x)
-    if epilogue in (NODE_ACT, NODE_DACT):
+    if epilogue == NODE_ACT or (epilogue == NODE_DACT and want_out1):
         out1 = torch.empty_like(x)
     out2 = torch.empty_like(x)
     _check_w_image(w_image, dev)
